@@ -1,0 +1,265 @@
+/*
+ * libttrl_hip: the C ABI of the MI355X (gfx950) learner-update path.
+ *
+ * A drop-in for the ttnn device calls that tt-rl's engine makes from Python.
+ * Every function returns TTRL_OK (0) or a negative TTRL_E* code and leaves a
+ * thread-local message for ttrl_last_error().  Pointers are device pointers
+ * unless the name says host; all float data is IEEE fp32, row-major.  Every
+ * kernel entry point only enqueues work on the context's stream, so a
+ * sequence of them can be recorded into one graph between
+ * ttrl_capture_begin and ttrl_capture_end.  Nothing here allocates device
+ * memory except ttrl_alloc (and ttrl_init, which reserves the stream-ordered
+ * split-K workspace).
+ *
+ * Each declaration names the reference interface it replaces (paths are
+ * relative to the tt-rl repository).
+ */
+#ifndef TTRL_HIP_H
+#define TTRL_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTRL_ABI_VERSION 1
+
+#define TTRL_OK 0
+#define TTRL_EINVAL (-1) /* bad argument or shape: the reference raises ValueError */
+#define TTRL_EHIP (-2)   /* HIP runtime error */
+#define TTRL_ENOMEM (-3)
+#define TTRL_ESTATE (-4) /* call not allowed in the current state (e.g. host read during capture) */
+
+typedef struct ttrl_ctx ttrl_ctx;
+typedef struct ttrl_graph ttrl_graph;
+
+/* ------------------------------------------------------------ context --- */
+
+/* Message of the last failed call on this thread. */
+const char* ttrl_last_error(void);
+int ttrl_version(void);
+int ttrl_device_count(int* out);
+/* Open a device and its stream; replaces acquire() (ttrl/engine/device/acquire.py:56). */
+int ttrl_init(int device, ttrl_ctx** out);
+/* Close; replaces the device close in ttrl/engine/device/acquire.py:56-140. */
+int ttrl_shutdown(ttrl_ctx* ctx);
+/* Wait for the stream; replaces ttnn.synchronize_device (ttrl/engine/step/core.py:135-141). */
+int ttrl_sync(ttrl_ctx* ctx);
+/* The context's hipStream_t, as an opaque handle. */
+void* ttrl_stream(ttrl_ctx* ctx);
+
+/* ------------------------------------------------------------- memory --- */
+/* Fixed-address device buffers (ttrl/engine/tensor/arena.py:21-87): blocks
+ * come from slab pools and are reused only by later allocations of the same
+ * pool, in stream order, so buffers recorded into a graph keep their
+ * addresses for the graph's lifetime.  Pool 0 is the default pool. */
+int ttrl_pool_create(ttrl_ctx* ctx, int* pool);
+int ttrl_pool_release(ttrl_ctx* ctx, int pool);
+int ttrl_pool_use(ttrl_ctx* ctx, int pool, int* previous);
+int ttrl_pool_stats(ttrl_ctx* ctx, int pool, size_t* reserved, size_t* live);
+int ttrl_alloc(ttrl_ctx* ctx, size_t bytes, void** out);
+int ttrl_free(ttrl_ctx* ctx, void* ptr);
+
+/* Host<->device copies; replace to_device/to_host/restore_in_place
+ * (ttrl/engine/tensor/transfer.py:11-51) and InputBinder.load
+ * (ttrl/engine/step/inputs.py:28-85).  Both refuse to run during capture. */
+int ttrl_h2d(ttrl_ctx* ctx, void* dst, const void* host_src, size_t bytes);
+int ttrl_d2h(ttrl_ctx* ctx, void* host_dst, const void* src, size_t bytes);
+/* Device copy on the stream; replaces copy_in_place (ttrl/engine/tensor/arena.py:32). */
+int ttrl_d2d(ttrl_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Fill with a kernel (never a memset node); replaces ttnn.full_like / zeros. */
+int ttrl_fill_f32(ttrl_ctx* ctx, float* dst, float value, long n);
+int ttrl_fill_i32(ttrl_ctx* ctx, int* dst, int value, long n);
+
+/* ------------------------------------------------------------- graphs --- */
+/* Replace ttnn trace capture/replay (ttrl/engine/trace.py:56-126). */
+int ttrl_capture_begin(ttrl_ctx* ctx);
+int ttrl_capture_end(ttrl_ctx* ctx, ttrl_graph** out);
+/* Leave capture after a failure (ttrl/engine/trace.py:39-53). */
+int ttrl_capture_abort(ttrl_ctx* ctx);
+int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g);
+int ttrl_graph_launch_n(ttrl_ctx* ctx, ttrl_graph* g, int n);
+int ttrl_graph_nodes(ttrl_graph* g, size_t* out);
+int ttrl_graph_destroy(ttrl_graph* g);
+
+/* Stream timer (events on the context's stream). */
+int ttrl_timer_start(ttrl_ctx* ctx);
+int ttrl_timer_stop(ttrl_ctx* ctx, float* ms);
+
+/* ------------------------------------------------------ dense layers --- */
+
+/* C[M][N] = alpha * op(A) op(B) + beta * C, op(X) = X or X^T.  Replaces the
+ * HiFi4 ttnn.matmul and its transposed backward products
+ * (ttrl/engine/ops/matmul.py:42-86). */
+int ttrl_matmul(ttrl_ctx* ctx, int M, int N, int K, const float* A, long lda, int trans_a, const float* B,
+                long ldb, int trans_b, float* C, long ldc, float alpha, float beta);
+
+/* A linear layer y = x @ W + b with W stored (in, out) (ttrl/engine/layers.py:22-61),
+ * optionally fused with ReLU (ttrl/engine/ops/unary.py:25-37) or a column clamp
+ * (ttrl/nets/heads.py:65-93).  Extensions used by the SAC nets:
+ *   groups     independent problems with element strides g* (twin critics),
+ *   x2/k1      input columns k >= k1 come from x2: concat(s, a) folded into the
+ *              load (ttrl/engine/ops/shape.py:10-48, ttrl/nets/fusion.py:36-71),
+ *   W2/b2/n1   output columns n >= n1 use a second weight (N - n1 wide): the
+ *              mean and log_std heads in one launch (ttrl/nets/heads.py:65-93).
+ * Backward: dZ = dy * [ymask > 0] when ymask is given (relu_bw), then
+ * dW = x^T dZ with db = column sums of dZ folded in as an implicit ones row
+ * (ttrl/engine/ops/broadcast.py:11-30), and dx = dZ W^T restricted to input
+ * columns [dx_col0, dx_col0 + dx_cols) when dx_cols > 0.  beta_* = 1
+ * accumulates into existing gradients (ttrl/engine/autograd.py:106-114). */
+typedef struct ttrl_linear_desc {
+  int M, K, N;
+  int groups;
+  const float* x;
+  long ldx, gx;
+  const float* x2;
+  long ldx2, gx2;
+  int k1;
+  const float* W;
+  long gW;
+  const float* b;
+  long gb;
+  const float* W2;
+  const float* b2;
+  int n1;
+  float* y;
+  long gy;
+  int relu;
+  int clamp_col;
+  float lo, hi;
+  const float* ymask;
+  const float* dy;
+  float* dW;
+  float* db;
+  float* dW2;
+  float* db2;
+  float* dx;
+  long lddx, gdx;
+  int dx_col0, dx_cols;
+  float beta_w, beta_x;
+} ttrl_linear_desc;
+
+int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* desc);
+int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* desc);
+
+/* ------------------------------------------------------- convolution --- */
+
+#define TTRL_LAYOUT_NHWC_F32 0 /* [B][H][W][C] fp32 activations */
+#define TTRL_LAYOUT_NCHW_U8 1  /* [B][C][H][W] uint8 frames */
+
+/* Geometry of ConvGeometry (ttrl/engine/conv/geometry.py:94-199), square kernel. */
+typedef struct ttrl_conv_geom {
+  int batch, in_c, in_h, in_w, out_c, kernel, stride, padding;
+  int in_layout;
+} ttrl_conv_geom;
+
+/* (size + 2p - k)/s + 1, refusing ragged geometry (ttrl/engine/conv/geometry.py:107-119). */
+int ttrl_conv_out_size(int size, int kernel, int stride, int padding, int* out);
+
+/* y[B][OH][OW][O] = x_scale * conv(x, W) + b (+ReLU).  W is the master
+ * Wt[k][O], k = (kh, kw, c) for NHWC inputs and (c, kh, kw) for NCHW uint8
+ * inputs.  Replaces ttnn.conv2d + bias add with the input-scale fold
+ * (ttrl/engine/conv/forward.py:160-205, ttrl/engine/conv/module.py:257-263). */
+int ttrl_conv2d_forward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, const float* wt,
+                        const float* bias, float* y, float x_scale, int relu);
+/* dWt = x_scale * sum over pixels of patch^T dZ, db = column sums of dZ,
+ * dZ = dy * [ymask > 0].  Replaces weight_grad + dw_to_prepared
+ * (ttrl/engine/conv/backward.py:45-78, ttrl/engine/conv/transform.py:232-254)
+ * and the conv bias-gradient sum (ttrl/engine/ops/broadcast.py:11-30). */
+int ttrl_conv2d_backward_weight(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale,
+                                const float* dy, const float* ymask, float* dwt, float* db, float beta);
+/* dx = x_scale * conv_transpose(dZ, W) for fp32 NHWC inputs.  Replaces
+ * input_grad / transpose_weight / conv_transpose2d
+ * (ttrl/engine/conv/backward.py:33-42, ttrl/engine/conv/transform.py:71-129). */
+int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const float* dy, const float* ymask,
+                               const float* wt, float* dx, float x_scale, float beta);
+
+/* ---------------------------------------------------------- loss heads --- */
+
+/* The DQN update head of update_loss (ttrl/algos/dqn/losses.py:77-140):
+ * pred = gather_onehot(q, actions_onehot); a* = argmax q_next_select (first
+ * index wins); y = r + discounts*(1 - done)*q_next_value[a*]; loss =
+ * mean(w * huber(pred - y, delta)); mean_q = mean(pred); td_abs = |pred - y|;
+ * dq = dloss/dq.  is_weights, mean_q, td_abs, next_actions, td_target may be
+ * NULL.  Pass q_next_select = q_next_value for vanilla DQN. */
+int ttrl_dqn_loss(ttrl_ctx* ctx, int B, int A, const float* q, const float* q_next_select,
+                  const float* q_next_value, const float* actions_onehot, const float* rewards, const float* dones,
+                  const float* discounts, const float* is_weights, float delta, float* loss, float* mean_q,
+                  float* td_abs, float* dq, float* next_actions, float* td_target);
+
+/* SquashedGaussian.sample (ttrl/algos/sac/policy.py:30-40) over head rows
+ * [mean | log_std] ([B][2d], log_std already clamped): action =
+ * centre + half_width * tanh(mean + exp(log_std)*noise), logp with the stable
+ * softplus correction (ttrl/algos/gaussian.py:55-117) minus log_det. */
+int ttrl_sac_sample(ttrl_ctx* ctx, int B, int d, const float* head, const float* noise, const float* centre,
+                    const float* half_width, float log_det, float* action, float* logp, float* u_out);
+/* Its backward to d_head ([B][2d]), given dL/daction (g_action0 + g_action1,
+ * either may be NULL) and dL/dlogp per row; the log_std clamp passes
+ * gradient strictly inside (log_std_min, log_std_max) (ttrl/engine/ops/select.py:26-29). */
+int ttrl_sac_sample_backward(ttrl_ctx* ctx, int B, int d, const float* head, const float* noise, const float* u,
+                             const float* half_width, const float* g_action0, const float* g_action1,
+                             const float* g_logp, float log_std_min, float log_std_max, float* d_head, float beta);
+/* critic_loss (ttrl/algos/sac/losses.py:46-76) for two critics: q and
+ * q_next_target are [2][B]; writes loss, q_target[B], dq [2][B],
+ * td_abs (priority_errors, losses.py:30-43; may be NULL) and alpha = exp(log_alpha). */
+int ttrl_sac_critic_loss(ttrl_ctx* ctx, int B, const float* q, const float* q_next_target, const float* logp_next,
+                         const float* log_alpha, const float* rewards, const float* dones, const float* discounts,
+                         const float* is_weights, float* loss, float* q_target, float* dq, float* td_abs,
+                         float* alpha_out);
+/* actor_loss and alpha_loss (ttrl/algos/sac/losses.py:79-94): q is [2][B] at
+ * the reparameterised action; writes both losses, dq [2][B], dL/dlogp per
+ * row and dL_alpha/dlog_alpha. */
+int ttrl_sac_actor_loss(ttrl_ctx* ctx, int B, const float* q, const float* logp, const float* log_alpha,
+                        float target_entropy, int learn_alpha, float* actor_loss, float* alpha_loss, float* dq,
+                        float* g_logp, float* d_log_alpha);
+
+/* ----------------------------------------------------------- optimizer --- */
+
+/* One Adam update over a flat range (ttrl/engine/optim/adam.py:93-134 with
+ * ttrl/engine/optim/scalars.py:13-27): m_s and v_s hold S = m/(1-b1) and
+ * V = v/(1-b2); *step (device int) is the update count before the call and
+ * is incremented by it; grad_sq (may be NULL) receives sum(g^2)
+ * (ttrl/algos/grads.py:46-60), added to its value when accumulate_grad_sq. */
+int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n, int* step, float lr,
+                   float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq);
+/* sum(x^2) into *out (grad_sq_device, ttrl/algos/grads.py:46-60). */
+int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate);
+/* dst = (1 - tau) * dst + tau * src (ttrl/algos/sac/targets.py:45-52). */
+int ttrl_polyak(ttrl_ctx* ctx, float* dst, const float* src, long n, float tau);
+
+/* ------------------------------------------------------ elementwise ops --- */
+
+enum {
+  TTRL_U_RELU = 0, TTRL_U_ABS, TTRL_U_SIGN, TTRL_U_SQUARE, TTRL_U_EXP, TTRL_U_LOG, TTRL_U_TANH,
+  TTRL_U_SIGMOID, TTRL_U_SQRT, TTRL_U_NEG, TTRL_U_ADD_S, TTRL_U_MUL_S, TTRL_U_RSUB_S, TTRL_U_DIV_S,
+  TTRL_U_EQZ, TTRL_U_GTZ, TTRL_U_ISFINITE, TTRL_U_COUNT
+};
+enum { TTRL_B_ADD = 0, TTRL_B_SUB, TTRL_B_MUL, TTRL_B_DIV, TTRL_B_RELU_BW, TTRL_B_MAX, TTRL_B_MIN, TTRL_B_EQ,
+       TTRL_B_COUNT };
+enum { TTRL_R_SUM = 0, TTRL_R_MAX, TTRL_R_ARGMAX, TTRL_R_COUNT };
+
+/* y = f(a) elementwise, with a scalar operand for the *_S ops; replaces the
+ * unary ttnn ops and scalar spellings (ttrl/engine/ops/unary.py:21-150,
+ * ttrl/engine/ops/elementwise.py:15-148). */
+int ttrl_unary(ttrl_ctx* ctx, int op, const float* a, float* y, long n, float scalar);
+/* y = a op b over a contiguous output of rank ndim <= 6; operands are read
+ * through element strides (0 broadcasts).  Replaces the binary ttnn ops and
+ * relu_bw (ttrl/engine/ops/elementwise.py:15-148, ttrl/engine/ops/unary.py:34). */
+int ttrl_binary(ttrl_ctx* ctx, int op, const float* a, const float* b, float* y, int ndim, const long* shape,
+                const long* stride_a, const long* stride_b);
+/* y[strided] = a[strided]: concat, split, slice and repeat
+ * (ttrl/engine/ops/shape.py:10-151, ttrl/engine/ops/broadcast.py:33-54). */
+int ttrl_copy_strided(ttrl_ctx* ctx, const float* a, float* y, int ndim, const long* shape, const long* stride_a,
+                      const long* stride_y);
+/* Sum, max or argmax (first index, as fp32) of the middle axis of an
+ * [outer][dim][inner] view (ttrl/engine/ops/reduce.py:12-99). */
+int ttrl_reduce(ttrl_ctx* ctx, int op, const float* a, float* y, long outer, long dim, long inner);
+/* y[b][c] = (c - indices[b] == 0) (ttrl/engine/ops/functional.py:112-123). */
+int ttrl_one_hot(ttrl_ctx* ctx, const float* indices, float* y, long batch, int num_classes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTRL_HIP_H */

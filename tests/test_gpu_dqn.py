@@ -1,0 +1,108 @@
+"""Full DQN learner update on the GPU against the float64 oracle
+(config: batch 32, 4x84x84 uint8 frames, 6 actions, double DQN, n-step 3,
+prioritized weights, Huber delta 1, Adam lr 6.25e-5 eps 1.5e-4).
+
+Tolerances: rel 1e-4 on Q-values, loss, mean_q, td_abs and Adam-updated
+parameters (max abs error over each tensor relative to its max |value|);
+exact next actions wherever the top-two Q gap is decisive; ReLU gates
+adopted from the device only where float64 puts the pre-activation within
+1e-4 of the tensor's RMS of zero."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests._dqn_helpers import build_learner, qnet_to_oracle
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-4
+
+
+def _rel(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def _device_gates(learner, frames):
+    from ttrl_amd.engine import layers
+    from ttrl_amd.engine.autograd import Tensor, no_grad
+    from ttrl_amd.engine.tensor import to_device
+
+    layers.RECORD = []
+    try:
+        with no_grad():
+            q = learner.online(Tensor(to_device(frames, learner.device, np.uint8)))
+        recs = [r.numpy() for r in layers.RECORD]
+    finally:
+        layers.RECORD = None
+    names = ["conv0", "conv1", "conv2", "fc0"]
+    gates = {}
+    for name, r in zip(names, recs):
+        if r.ndim == 4:
+            b = frames.shape[0]
+            r = r.reshape(b, -1, r.shape[-1])
+        gates[name] = r > 0
+    return q.numpy(), gates
+
+
+@pytest.mark.parametrize("step_mode", ["graph", "eager"])
+def test_dqn_update_matches_oracle(device, step_mode):
+    from oracle.dqn import dqn_update
+    from oracle.nets import qnet_forward
+    from ttrl_amd.workloads import dqn_batch
+
+    learner, online, target = build_learner(device, seed=0, step_mode=step_mode)
+    batch = dqn_batch(11, batch=32)
+    q_dev, gates = _device_gates(learner, batch["obs"])
+    onet, tnet = qnet_to_oracle(online), qnet_to_oracle(target)
+    # reshape NHWC conv gates to the oracle's (B, OH, OW, C)
+    _, acts = qnet_forward(onet, batch["obs"])
+    for i in range(3):
+        gates[f"conv{i}"] = gates[f"conv{i}"].reshape(acts[i][1].shape)
+    q_next_dev, _ = _device_gates(learner, batch["next_obs"])
+    ref = dqn_update(onet, tnet, batch, double=True, delta=1.0, lr=6.25e-5, eps=1.5e-4, gates=gates,
+                     device_next_actions=np.argmax(q_next_dev, 1))
+    assert _rel(q_dev, ref["q"]) < REL
+    assert sum(ref["gate_stats"].decided_mismatch.values()) == 0
+    m = learner.update(batch)
+    assert abs(m["loss"] - ref["loss"]) <= REL * abs(ref["loss"])
+    assert abs(m["mean_q"] - ref["mean_q"]) <= REL * abs(ref["mean_q"])
+    assert _rel(m["td_abs"], ref["td_abs"]) < REL
+    assert abs(m["grad_norm"] - ref["grad_norm"]) <= REL * ref["grad_norm"]
+    new = learner.online.state_dict()
+    for (k, got), want in zip(new.items(), ref["new_params"]):
+        assert _rel(np.asarray(got).reshape(want.shape), want) < REL, k
+    learner.close()
+
+
+def test_dqn_graph_replays_are_deterministic(device):
+    """Two learners from the same state, same batches: bit-identical params
+    after 3 graph replays (the reference's replay-determinism tests)."""
+    from ttrl_amd.workloads import dqn_batch
+
+    outs = []
+    for _ in range(2):
+        learner, _, _ = build_learner(device, seed=3, step_mode="graph")
+        for k in range(3):
+            learner.update(dqn_batch(100 + k))
+        outs.append(learner.online.state_dict())
+        learner.close()
+    for k in outs[0]:
+        assert np.array_equal(outs[0][k], outs[1][k]), k
+
+
+def test_dqn_graph_and_eager_agree(device):
+    from ttrl_amd.workloads import dqn_batch
+
+    res = {}
+    for mode in ("graph", "eager"):
+        learner, _, _ = build_learner(device, seed=4, step_mode=mode)
+        ms = [learner.update(dqn_batch(200 + k)) for k in range(3)]
+        res[mode] = (ms, learner.online.state_dict())
+        learner.close()
+    for a, b in zip(res["graph"][0], res["eager"][0]):
+        assert a["loss"] == b["loss"]
+    for k in res["graph"][1]:
+        assert np.array_equal(res["graph"][1][k], res["eager"][1][k]), k

@@ -1,0 +1,194 @@
+// Optimizer-side kernels over flat parameter arenas: the fused Adam step
+// with a device-resident update counter and the sum of squared gradients,
+// a standalone sum of squares, the Polyak blend and a fill kernel.
+//
+// Reference semantics:
+//   Adam (S = m/(1-b1), V = v/(1-b2) storage, fused scalars)
+//                          ttrl/engine/optim/adam.py:93-134, ttrl/engine/optim/scalars.py:13-27
+//   grad_sq_device         ttrl/algos/grads.py:46-60
+//   Polyak blend           ttrl/algos/sac/targets.py:45-52
+//
+// The Adam scalars depend on the update count t.  The count lives on the
+// device, so one captured graph replays correctly for every t: the update
+// kernel reads t_old and uses t = t_old + 1, and the finishing kernel (one
+// block, after every update block has run) stores t and the reduced
+// sum of squares.  All reductions are fixed-order.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace ttrl {
+
+constexpr int kOptThreads = 256;
+constexpr int kOptMaxBlocks = 1024;
+
+float* ctx_workspace(ttrl_ctx* ctx, long* floats);
+
+__global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, const float* __restrict__ g,
+                                                      float* __restrict__ S, float* __restrict__ V, long n,
+                                                      const int* __restrict__ step, float lr, float b1, float b2,
+                                                      float eps, float wd, float* __restrict__ partials) {
+  __shared__ float sc[2];
+  __shared__ float red[kOptThreads / 64];
+  if (threadIdx.x == 0) {
+    const int t = *step + 1;
+    const double bc1 = 1.0 - pow(double(b1), double(t));
+    const double bc2 = 1.0 - pow(double(b2), double(t));
+    const double c = sqrt((1.0 - double(b2)) / bc2);
+    sc[0] = float(double(lr) * (1.0 - double(b1)) / bc1 / c);
+    sc[1] = float(double(eps) / c);
+  }
+  __syncthreads();
+  const float alpha_t = sc[0], eps_t = sc[1];
+  float gsq = 0.f;
+  const long n4 = n / 4;
+  const long stride = long(gridDim.x) * kOptThreads;
+  for (long i = blockIdx.x * long(kOptThreads) + threadIdx.x; i < n4; i += stride) {
+    f32x4 pv = reinterpret_cast<f32x4*>(p)[i];
+    const f32x4 gv = reinterpret_cast<const f32x4*>(g)[i];
+    f32x4 sv = reinterpret_cast<f32x4*>(S)[i];
+    f32x4 vv = reinterpret_cast<f32x4*>(V)[i];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float graw = gv[q];
+      gsq += graw * graw;
+      const float gg = wd != 0.f ? graw + wd * pv[q] : graw;
+      vv[q] = gg * gg + b2 * vv[q];
+      sv[q] = gg + b1 * sv[q];
+      const float upd = (sv[q] / (sqrtf(vv[q]) + eps_t)) * alpha_t;
+      pv[q] = pv[q] - upd;
+    }
+    reinterpret_cast<f32x4*>(p)[i] = pv;
+    reinterpret_cast<f32x4*>(S)[i] = sv;
+    reinterpret_cast<f32x4*>(V)[i] = vv;
+  }
+  // Tail (n % 4) handled by block 0.
+  if (blockIdx.x == 0) {
+    for (long i = n4 * 4 + threadIdx.x; i < n; i += kOptThreads) {
+      const float graw = g[i];
+      gsq += graw * graw;
+      const float gg = wd != 0.f ? graw + wd * p[i] : graw;
+      V[i] = gg * gg + b2 * V[i];
+      S[i] = gg + b1 * S[i];
+      p[i] = p[i] - (S[i] / (sqrtf(V[i]) + eps_t)) * alpha_t;
+    }
+  }
+  const float tot = block_sum<kOptThreads>(gsq, red);
+  if (threadIdx.x == 0) partials[blockIdx.x] = tot;
+}
+
+__global__ __launch_bounds__(kOptThreads) void k_finish(const float* __restrict__ partials, int nparts,
+                                                        int* __restrict__ step, float* __restrict__ out,
+                                                        int accumulate) {
+  __shared__ float red[kOptThreads / 64];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += partials[i];
+  const float tot = block_sum<kOptThreads>(s, red);
+  if (threadIdx.x == 0) {
+    if (out) *out = accumulate ? *out + tot : tot;
+    if (step) *step = *step + 1;
+  }
+}
+
+__global__ __launch_bounds__(kOptThreads) void k_sumsq(const float* __restrict__ x, long n,
+                                                       float* __restrict__ partials) {
+  __shared__ float red[kOptThreads / 64];
+  float s = 0.f;
+  const long stride = long(gridDim.x) * kOptThreads;
+  for (long i = blockIdx.x * long(kOptThreads) + threadIdx.x; i < n; i += stride) {
+    const float v = x[i];
+    s += v * v;
+  }
+  const float tot = block_sum<kOptThreads>(s, red);
+  if (threadIdx.x == 0) partials[blockIdx.x] = tot;
+}
+
+__global__ __launch_bounds__(kOptThreads) void k_polyak(float* __restrict__ dst, const float* __restrict__ src,
+                                                        long n, float keep, float tau) {
+  const long stride = long(gridDim.x) * kOptThreads;
+  for (long i = blockIdx.x * long(kOptThreads) + threadIdx.x; i < n; i += stride) {
+    dst[i] = dst[i] * keep + src[i] * tau;
+  }
+}
+
+__global__ __launch_bounds__(kOptThreads) void k_fill(float* __restrict__ p, long n, float v) {
+  const long stride = long(gridDim.x) * kOptThreads;
+  for (long i = blockIdx.x * long(kOptThreads) + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+__global__ void k_fill_i32(int* __restrict__ p, long n, int v) {
+  for (long i = blockIdx.x * long(blockDim.x) + threadIdx.x; i < n; i += long(gridDim.x) * blockDim.x) p[i] = v;
+}
+
+inline unsigned grid_for(long n, long per_thread = 1) {
+  long b = (n / per_thread + kOptThreads - 1) / kOptThreads;
+  if (b < 1) b = 1;
+  if (b > kOptMaxBlocks) b = kOptMaxBlocks;
+  return unsigned(b);
+}
+
+}  // namespace ttrl
+
+using namespace ttrl;
+
+extern "C" {
+
+int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n, int* step, float lr,
+                   float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq) {
+  TTRL_REQUIRE(ctx && p && g && m_s && v_s && step, "ttrl_adam_step: null argument");
+  TTRL_REQUIRE(n > 0, "ttrl_adam_step: empty parameter range");
+  TTRL_REQUIRE(lr > 0.f && eps > 0.f && beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f &&
+                   weight_decay >= 0.f,
+               "ttrl_adam_step: bad hyper-parameters");
+  TTRL_REQUIRE(((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
+                 reinterpret_cast<uintptr_t>(m_s) | reinterpret_cast<uintptr_t>(v_s)) & 15) == 0,
+               "ttrl_adam_step: buffers must be 16-byte aligned");
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  const unsigned blocks = grid_for(n, 4);
+  TTRL_REQUIRE(wsf >= long(blocks), "ttrl_adam_step: workspace too small");
+  hipStream_t st = stream_of(ctx);
+  hipLaunchKernelGGL(k_adam, dim3(blocks), dim3(kOptThreads), 0, st, p, g, m_s, v_s, n, step, lr, beta1, beta2,
+                     eps, weight_decay, ws);
+  hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
+                     accumulate_grad_sq);
+  return check_launch("ttrl_adam_step");
+}
+
+int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate) {
+  TTRL_REQUIRE(ctx && x && out, "ttrl_sum_squares: null argument");
+  TTRL_REQUIRE(n >= 0, "ttrl_sum_squares: negative length");
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  const unsigned blocks = grid_for(n > 0 ? n : 1, 4);
+  hipStream_t st = stream_of(ctx);
+  hipLaunchKernelGGL(k_sumsq, dim3(blocks), dim3(kOptThreads), 0, st, x, n, ws);
+  hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), (int*)nullptr, out,
+                     accumulate);
+  return check_launch("ttrl_sum_squares");
+}
+
+int ttrl_polyak(ttrl_ctx* ctx, float* dst, const float* src, long n, float tau) {
+  TTRL_REQUIRE(ctx && dst && src, "ttrl_polyak: null argument");
+  TTRL_REQUIRE(tau >= 0.f && tau <= 1.f, "ttrl_polyak: tau must be in [0, 1]");
+  if (n <= 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_polyak, dim3(grid_for(n)), dim3(kOptThreads), 0, stream_of(ctx), dst, src, n, 1.f - tau,
+                     tau);
+  return check_launch("ttrl_polyak");
+}
+
+int ttrl_fill_f32(ttrl_ctx* ctx, float* dst, float value, long n) {
+  TTRL_REQUIRE(ctx && (dst || n == 0), "ttrl_fill_f32: null argument");
+  if (n <= 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_fill, dim3(grid_for(n)), dim3(kOptThreads), 0, stream_of(ctx), dst, n, value);
+  return check_launch("ttrl_fill_f32");
+}
+
+int ttrl_fill_i32(ttrl_ctx* ctx, int* dst, int value, long n) {
+  TTRL_REQUIRE(ctx && (dst || n == 0), "ttrl_fill_i32: null argument");
+  if (n <= 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(n)), dim3(kOptThreads), 0, stream_of(ctx), dst, n, value);
+  return check_launch("ttrl_fill_i32");
+}
+
+}  // extern "C"

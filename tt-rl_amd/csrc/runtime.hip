@@ -1,0 +1,445 @@
+// Host runtime of libttrl_hip: device context, stream, slab-pool device
+// allocator, host<->device transfers, fill, hipGraph capture and replay,
+// stream timers.  Every entry point returns 0 or a negative TTRL_E* code and
+// leaves a thread-local message for ttrl_last_error().
+//
+// Replaces the ttnn device plumbing the reference drives from Python:
+//   device open/close            ttrl/engine/device/acquire.py:56-140
+//   fixed-address buffers        ttrl/engine/tensor/arena.py:21-87
+//   host<->device copies         ttrl/engine/tensor/transfer.py:11-51
+//   trace capture / replay       ttrl/engine/trace.py:56-126
+#include "common.hpp"
+
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+constexpr size_t kAlign = 256;
+constexpr size_t kSlabBytes = size_t(64) << 20;
+constexpr size_t kWorkspaceBytes = size_t(64) << 20;
+
+struct Pool {
+  std::vector<std::pair<char*, size_t>> slabs;
+  char* cursor = nullptr;
+  size_t left = 0;
+  std::unordered_map<size_t, std::vector<char*>> free_lists;
+  size_t reserved = 0;
+  size_t live = 0;
+  bool retired = false;
+  bool in_use = false;
+};
+
+struct Block {
+  size_t size;
+  int pool;
+};
+
+}  // namespace
+
+struct ttrl_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::vector<Pool> pools;
+  int current_pool = 0;
+  std::unordered_map<void*, Block> blocks;
+  bool capturing = false;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  float* ws = nullptr;  // stream-ordered scratch of split-K GEMMs and reductions
+  long ws_floats = 0;
+};
+
+struct ttrl_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  size_t nodes = 0;
+};
+
+namespace ttrl {
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_error(hipError_t e, const char* what) {
+  return set_error(TTRL_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), int(e));
+}
+
+hipStream_t stream_of(ttrl_ctx* ctx) { return ctx->stream; }
+
+float* ctx_workspace(ttrl_ctx* ctx, long* floats) {
+  if (floats) *floats = ctx->ws_floats;
+  return ctx->ws;
+}
+
+int check_launch(const char* name) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_error(e, name);
+  return TTRL_OK;
+}
+
+}  // namespace ttrl
+
+using namespace ttrl;
+
+namespace {
+
+int pool_grow(Pool& p, size_t need) {
+  size_t bytes = need > kSlabBytes ? need : kSlabBytes;
+  void* ptr = nullptr;
+  hipError_t e = hipMalloc(&ptr, bytes);
+  if (e != hipSuccess) return hip_error(e, "hipMalloc (pool slab)");
+  p.slabs.emplace_back(static_cast<char*>(ptr), bytes);
+  p.cursor = static_cast<char*>(ptr);
+  p.left = bytes;
+  p.reserved += bytes;
+  return TTRL_OK;
+}
+
+void pool_free_slabs(Pool& p) {
+  for (auto& s : p.slabs) (void)hipFree(s.first);
+  p.slabs.clear();
+  p.free_lists.clear();
+  p.cursor = nullptr;
+  p.left = 0;
+  p.reserved = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ttrl_last_error(void) { return g_last_error.c_str(); }
+
+int ttrl_version(void) { return TTRL_ABI_VERSION; }
+
+int ttrl_device_count(int* out) {
+  if (!out) return set_error(TTRL_EINVAL, "ttrl_device_count: null out");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *out = 0;
+    return hip_error(e, "hipGetDeviceCount");
+  }
+  *out = n;
+  return TTRL_OK;
+}
+
+int ttrl_init(int device, ttrl_ctx** out) {
+  if (!out) return set_error(TTRL_EINVAL, "ttrl_init: null out");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n)
+    return set_error(TTRL_EINVAL, "ttrl_init: device %d out of range (%d visible)", device, n);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_error(e, "hipSetDevice");
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_error(e, "hipGetDeviceProperties");
+  if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+    return set_error(TTRL_EINVAL, "ttrl_init: device %d is %s; this library is built for gfx950 only",
+                     device, prop.gcnArchName);
+  auto* ctx = new ttrl_ctx();
+  ctx->device = device;
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_error(e, "hipStreamCreate");
+  }
+  (void)hipEventCreate(&ctx->t0);
+  (void)hipEventCreate(&ctx->t1);
+  // Split-K partial tiles and reduction partials are written and consumed
+  // by consecutive kernels on this one stream, so one fixed buffer serves
+  // every launch and every captured graph of the context.
+  void* ws = nullptr;
+  e = hipMalloc(&ws, kWorkspaceBytes);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_error(e, "hipMalloc (workspace)");
+  }
+  ctx->ws = static_cast<float*>(ws);
+  ctx->ws_floats = long(kWorkspaceBytes / sizeof(float));
+  ctx->pools.emplace_back();  // pool 0: the default pool
+  ctx->pools[0].in_use = true;
+  *out = ctx;
+  return TTRL_OK;
+}
+
+int ttrl_shutdown(ttrl_ctx* ctx) {
+  if (!ctx) return TTRL_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (auto& p : ctx->pools) pool_free_slabs(p);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->t0) (void)hipEventDestroy(ctx->t0);
+  if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return TTRL_OK;
+}
+
+int ttrl_sync(ttrl_ctx* ctx) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_sync: null ctx");
+  if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_sync: the stream is capturing a graph");
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+  return TTRL_OK;
+}
+
+void* ttrl_stream(ttrl_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+// ---------------------------------------------------------------- pools ---
+
+int ttrl_pool_create(ttrl_ctx* ctx, int* pool) {
+  if (!ctx || !pool) return set_error(TTRL_EINVAL, "ttrl_pool_create: null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  for (size_t i = 1; i < ctx->pools.size(); ++i) {
+    if (!ctx->pools[i].in_use) {
+      ctx->pools[i] = Pool();
+      ctx->pools[i].in_use = true;
+      *pool = int(i);
+      return TTRL_OK;
+    }
+  }
+  ctx->pools.emplace_back();
+  ctx->pools.back().in_use = true;
+  *pool = int(ctx->pools.size() - 1);
+  return TTRL_OK;
+}
+
+int ttrl_pool_release(ttrl_ctx* ctx, int pool) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_pool_release: null ctx");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  if (pool <= 0 || pool >= int(ctx->pools.size()) || !ctx->pools[pool].in_use)
+    return set_error(TTRL_EINVAL, "ttrl_pool_release: bad pool %d", pool);
+  if (ctx->current_pool == pool) ctx->current_pool = 0;
+  Pool& p = ctx->pools[pool];
+  if (p.live == 0) {
+    (void)hipStreamSynchronize(ctx->stream);
+    pool_free_slabs(p);
+    p.in_use = false;
+  } else {
+    p.retired = true;  // slabs go back when the last live block is freed
+  }
+  return TTRL_OK;
+}
+
+int ttrl_pool_use(ttrl_ctx* ctx, int pool, int* previous) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_pool_use: null ctx");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  if (pool < 0 || pool >= int(ctx->pools.size()) || !ctx->pools[pool].in_use || ctx->pools[pool].retired)
+    return set_error(TTRL_EINVAL, "ttrl_pool_use: bad pool %d", pool);
+  if (previous) *previous = ctx->current_pool;
+  ctx->current_pool = pool;
+  return TTRL_OK;
+}
+
+int ttrl_pool_stats(ttrl_ctx* ctx, int pool, size_t* reserved, size_t* live) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_pool_stats: null ctx");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  if (pool < 0 || pool >= int(ctx->pools.size()))
+    return set_error(TTRL_EINVAL, "ttrl_pool_stats: bad pool %d", pool);
+  if (reserved) *reserved = ctx->pools[pool].reserved;
+  if (live) *live = ctx->pools[pool].live;
+  return TTRL_OK;
+}
+
+int ttrl_alloc(ttrl_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return set_error(TTRL_EINVAL, "ttrl_alloc: null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  size_t size = ((bytes ? bytes : 1) + kAlign - 1) / kAlign * kAlign;
+  int pid = ctx->current_pool;
+  Pool& p = ctx->pools[pid];
+  char* ptr = nullptr;
+  auto it = p.free_lists.find(size);
+  if (it != p.free_lists.end() && !it->second.empty()) {
+    ptr = it->second.back();
+    it->second.pop_back();
+  } else {
+    if (p.left < size) {
+      int rc = pool_grow(p, size);
+      if (rc) return rc;
+    }
+    ptr = p.cursor;
+    p.cursor += size;
+    p.left -= size;
+  }
+  p.live += size;
+  ctx->blocks[ptr] = Block{size, pid};
+  *out = ptr;
+  return TTRL_OK;
+}
+
+int ttrl_free(ttrl_ctx* ctx, void* ptr) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_free: null ctx");
+  if (!ptr) return TTRL_OK;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  auto it = ctx->blocks.find(ptr);
+  if (it == ctx->blocks.end()) return set_error(TTRL_EINVAL, "ttrl_free: %p was not allocated here", ptr);
+  Block b = it->second;
+  ctx->blocks.erase(it);
+  Pool& p = ctx->pools[b.pool];
+  p.live -= b.size;
+  p.free_lists[b.size].push_back(static_cast<char*>(ptr));
+  if (p.retired && p.live == 0) {
+    (void)hipStreamSynchronize(ctx->stream);
+    pool_free_slabs(p);
+    p.retired = false;
+    p.in_use = false;
+  }
+  return TTRL_OK;
+}
+
+// ------------------------------------------------------------ transfers ---
+
+int ttrl_h2d(ttrl_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return set_error(TTRL_EINVAL, "ttrl_h2d: null argument");
+  if (ctx->capturing)
+    return set_error(TTRL_ESTATE,
+                     "ttrl_h2d: host-to-device writes are not allowed while a graph is being captured; "
+                     "load inputs before the capture or between replays");
+  if (!bytes) return TTRL_OK;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D");
+  e = hipStreamSynchronize(ctx->stream);  // the host buffer may be reused as soon as we return
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize after H2D");
+  return TTRL_OK;
+}
+
+int ttrl_d2h(ttrl_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return set_error(TTRL_EINVAL, "ttrl_d2h: null argument");
+  if (ctx->capturing)
+    return set_error(TTRL_ESTATE,
+                     "ttrl_d2h: reads to host are not supported during graph capture; "
+                     "read metrics after the replay");
+  if (!bytes) return TTRL_OK;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync D2H");
+  e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize after D2H");
+  return TTRL_OK;
+}
+
+int ttrl_d2d(ttrl_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return set_error(TTRL_EINVAL, "ttrl_d2d: null argument");
+  if (!bytes) return TTRL_OK;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync D2D");
+  return TTRL_OK;
+}
+
+// --------------------------------------------------------------- graphs ---
+
+int ttrl_capture_begin(ttrl_ctx* ctx) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_capture_begin: null ctx");
+  if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_capture_begin: already capturing");
+  hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) return hip_error(e, "hipStreamBeginCapture");
+  ctx->capturing = true;
+  return TTRL_OK;
+}
+
+int ttrl_capture_end(ttrl_ctx* ctx, ttrl_graph** out) {
+  if (!ctx || !out) return set_error(TTRL_EINVAL, "ttrl_capture_end: null argument");
+  if (!ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_capture_end: not capturing");
+  ctx->capturing = false;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+  if (e != hipSuccess) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return hip_error(e, "hipStreamEndCapture");
+  }
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return hip_error(e, "hipGraphInstantiate");
+  }
+  auto* g = new ttrl_graph();
+  g->graph = graph;
+  g->exec = exec;
+  size_t n = 0;
+  if (hipGraphGetNodes(graph, nullptr, &n) == hipSuccess) g->nodes = n;
+  *out = g;
+  return TTRL_OK;
+}
+
+int ttrl_capture_abort(ttrl_ctx* ctx) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_capture_abort: null ctx");
+  if (!ctx->capturing) return TTRL_OK;
+  ctx->capturing = false;
+  hipGraph_t graph = nullptr;
+  (void)hipStreamEndCapture(ctx->stream, &graph);
+  if (graph) (void)hipGraphDestroy(graph);
+  (void)hipGetLastError();
+  return TTRL_OK;
+}
+
+int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g) {
+  if (!ctx || !g || !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_launch: null argument");
+  if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_launch: the stream is capturing");
+  hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipGraphLaunch");
+  return TTRL_OK;
+}
+
+int ttrl_graph_launch_n(ttrl_ctx* ctx, ttrl_graph* g, int n) {
+  if (!ctx || !g || !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_launch_n: null argument");
+  if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_launch_n: the stream is capturing");
+  for (int i = 0; i < n; ++i) {
+    hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipGraphLaunch");
+  }
+  return TTRL_OK;
+}
+
+int ttrl_graph_nodes(ttrl_graph* g, size_t* out) {
+  if (!g || !out) return set_error(TTRL_EINVAL, "ttrl_graph_nodes: null argument");
+  *out = g->nodes;
+  return TTRL_OK;
+}
+
+int ttrl_graph_destroy(ttrl_graph* g) {
+  if (!g) return TTRL_OK;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
+  return TTRL_OK;
+}
+
+// --------------------------------------------------------------- timing ---
+
+int ttrl_timer_start(ttrl_ctx* ctx) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_timer_start: null ctx");
+  hipError_t e = hipEventRecord(ctx->t0, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+  return TTRL_OK;
+}
+
+int ttrl_timer_stop(ttrl_ctx* ctx, float* ms) {
+  if (!ctx || !ms) return set_error(TTRL_EINVAL, "ttrl_timer_stop: null argument");
+  hipError_t e = hipEventRecord(ctx->t1, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+  e = hipEventSynchronize(ctx->t1);
+  if (e != hipSuccess) return hip_error(e, "hipEventSynchronize");
+  e = hipEventElapsedTime(ms, ctx->t0, ctx->t1);
+  if (e != hipSuccess) return hip_error(e, "hipEventElapsedTime");
+  return TTRL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,169 @@
+"""ctypes binding of libttrl_hip.so (the C ABI declared in include/ttrl_hip.h).
+
+The library is the only compute path: importing this module does not load it,
+`lib()` does, and it raises if the shared object is missing rather than
+falling back to any host implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libttrl_hip.so"
+
+TTRL_OK = 0
+TTRL_EINVAL = -1
+TTRL_EHIP = -2
+TTRL_ENOMEM = -3
+TTRL_ESTATE = -4
+
+LAYOUT_NHWC_F32 = 0
+LAYOUT_NCHW_U8 = 1
+
+# unary / binary / reduce op codes (enum order in ttrl_hip.h)
+U_OPS = ["relu", "abs", "sign", "square", "exp", "log", "tanh", "sigmoid", "sqrt", "neg",
+         "add_s", "mul_s", "rsub_s", "div_s", "eqz", "gtz", "isfinite"]
+U = {name: i for i, name in enumerate(U_OPS)}
+B_OPS = ["add", "sub", "mul", "div", "relu_bw", "max", "min", "eq"]
+BOP = {name: i for i, name in enumerate(B_OPS)}
+R = {"sum": 0, "max": 1, "argmax": 2}
+
+
+class LinearDesc(C.Structure):
+    """Mirror of ttrl_linear_desc."""
+
+    _fields_ = [
+        ("M", C.c_int), ("K", C.c_int), ("N", C.c_int), ("groups", C.c_int),
+        ("x", C.c_void_p), ("ldx", C.c_long), ("gx", C.c_long),
+        ("x2", C.c_void_p), ("ldx2", C.c_long), ("gx2", C.c_long), ("k1", C.c_int),
+        ("W", C.c_void_p), ("gW", C.c_long),
+        ("b", C.c_void_p), ("gb", C.c_long),
+        ("W2", C.c_void_p), ("b2", C.c_void_p), ("n1", C.c_int),
+        ("y", C.c_void_p), ("gy", C.c_long),
+        ("relu", C.c_int), ("clamp_col", C.c_int), ("lo", C.c_float), ("hi", C.c_float),
+        ("ymask", C.c_void_p), ("dy", C.c_void_p),
+        ("dW", C.c_void_p), ("db", C.c_void_p), ("dW2", C.c_void_p), ("db2", C.c_void_p),
+        ("dx", C.c_void_p), ("lddx", C.c_long), ("gdx", C.c_long),
+        ("dx_col0", C.c_int), ("dx_cols", C.c_int),
+        ("beta_w", C.c_float), ("beta_x", C.c_float),
+    ]
+
+
+class ConvGeom(C.Structure):
+    """Mirror of ttrl_conv_geom."""
+
+    _fields_ = [(name, C.c_int) for name in (
+        "batch", "in_c", "in_h", "in_w", "out_c", "kernel", "stride", "padding", "in_layout")]
+
+
+P = C.c_void_p
+I = C.c_int
+L = C.c_long
+F = C.c_float
+SZ = C.c_size_t
+
+#: name -> (argtypes, restype); every entry point of ttrl_hip.h.
+SIGNATURES = {
+    "ttrl_last_error": ([], C.c_char_p),
+    "ttrl_version": ([], I),
+    "ttrl_device_count": ([C.POINTER(I)], I),
+    "ttrl_init": ([I, C.POINTER(P)], I),
+    "ttrl_shutdown": ([P], I),
+    "ttrl_sync": ([P], I),
+    "ttrl_stream": ([P], P),
+    "ttrl_pool_create": ([P, C.POINTER(I)], I),
+    "ttrl_pool_release": ([P, I], I),
+    "ttrl_pool_use": ([P, I, C.POINTER(I)], I),
+    "ttrl_pool_stats": ([P, I, C.POINTER(SZ), C.POINTER(SZ)], I),
+    "ttrl_alloc": ([P, SZ, C.POINTER(P)], I),
+    "ttrl_free": ([P, P], I),
+    "ttrl_h2d": ([P, P, P, SZ], I),
+    "ttrl_d2h": ([P, P, P, SZ], I),
+    "ttrl_d2d": ([P, P, P, SZ], I),
+    "ttrl_fill_f32": ([P, P, F, L], I),
+    "ttrl_fill_i32": ([P, P, I, L], I),
+    "ttrl_capture_begin": ([P], I),
+    "ttrl_capture_end": ([P, C.POINTER(P)], I),
+    "ttrl_capture_abort": ([P], I),
+    "ttrl_graph_launch": ([P, P], I),
+    "ttrl_graph_launch_n": ([P, P, I], I),
+    "ttrl_graph_nodes": ([P, C.POINTER(SZ)], I),
+    "ttrl_graph_destroy": ([P], I),
+    "ttrl_timer_start": ([P], I),
+    "ttrl_timer_stop": ([P, C.POINTER(F)], I),
+    "ttrl_matmul": ([P, I, I, I, P, L, I, P, L, I, P, L, F, F], I),
+    "ttrl_linear_forward": ([P, C.POINTER(LinearDesc)], I),
+    "ttrl_linear_backward": ([P, C.POINTER(LinearDesc)], I),
+    "ttrl_conv_out_size": ([I, I, I, I, C.POINTER(I)], I),
+    "ttrl_conv2d_forward": ([P, C.POINTER(ConvGeom), P, P, P, P, F, I], I),
+    "ttrl_conv2d_backward_weight": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, F], I),
+    "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, F, F], I),
+    "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
+    "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
+    "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),
+    "ttrl_sac_critic_loss": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),
+    "ttrl_sac_actor_loss": ([P, I, P, P, P, F, I, P, P, P, P, P], I),
+    "ttrl_adam_step": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
+    "ttrl_sum_squares": ([P, P, L, P, I], I),
+    "ttrl_polyak": ([P, P, P, L, F], I),
+    "ttrl_unary": ([P, I, P, P, L, F], I),
+    "ttrl_binary": ([P, I, P, P, P, I, C.POINTER(L), C.POINTER(L), C.POINTER(L)], I),
+    "ttrl_copy_strided": ([P, P, P, I, C.POINTER(L), C.POINTER(L), C.POINTER(L)], I),
+    "ttrl_reduce": ([P, I, P, P, L, L, L], I),
+    "ttrl_one_hot": ([P, P, P, L, I], I),
+}
+
+_LIB = None
+
+
+class TTRLError(RuntimeError):
+    """A libttrl_hip call failed; `code` is the TTRL_E* status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def load(path: Path | str | None = None) -> C.CDLL:
+    """Open the shared library without touching any device."""
+    target = Path(path) if path else LIB_PATH
+    if not target.exists():
+        raise RuntimeError(
+            f"libttrl_hip.so is not built ({target} missing). Run __graft_entry__.build() or "
+            f"`python -m ttrl_amd._build` with tt-rl_amd on sys.path; there is no host fallback."
+        )
+    dll = C.CDLL(str(target), mode=os.RTLD_LOCAL if hasattr(os, "RTLD_LOCAL") else 0)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(dll, name)
+        fn.argtypes = args
+        fn.restype = res
+    return dll
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        _LIB = load()
+    return _LIB
+
+
+def check(rc: int, what: str = "") -> None:
+    """Raise the reference's exception type for a failed call."""
+    if rc == TTRL_OK:
+        return
+    msg = lib().ttrl_last_error().decode(errors="replace")
+    text = f"{what}: {msg}" if what else msg
+    if rc == TTRL_EINVAL:
+        raise ValueError(text)
+    raise TTRLError(rc, text)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def longs(values) -> C.Array:
+    values = [int(v) for v in values]
+    return (L * len(values))(*values)

@@ -1,0 +1,189 @@
+"""The DQN learner update (ttrl/algos/dqn/losses.py:44-140,
+ttrl/algos/dqn/agent.py:151-214).
+
+`step_inputs` names the bound buffers one update reads; `update_loss` is the
+update body: online forward with tape, target and online forwards on s'
+without tape, the fused TD/Huber head, backward, metrics.  `DQNLearner` owns
+the networks, the Adam optimizer and the TrainStep; `update(batch)` loads
+one replay batch and runs one gradient step (the body of the reference's
+`_gradient_step` after sampling).
+
+Image observations are bound as uint8 NCHW frames, the layout the
+environment produces, so an update uploads 1 byte per pixel and no host
+transpose; the first convolution reads them directly.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from ttrl_amd.algos.grads import grad_sq_device
+from ttrl_amd.engine.autograd import Tensor, no_grad
+from ttrl_amd.engine.ops.fused import dqn_td_loss
+from ttrl_amd.engine.optim import Adam
+from ttrl_amd.engine.step import TrainStep
+from ttrl_amd.nets.build import build_q_net
+
+__all__ = ["DQNConfig", "DQNLearner", "leaf_key", "step_inputs", "update_loss"]
+
+
+@dataclass(frozen=True)
+class DQNConfig:
+    """The learner-side fields of ttrl/algos/dqn/config.py:19-151, plus the
+    Adam epsilon, which the reference leaves at the engine default 1e-8."""
+
+    lr: float = 1e-4
+    adam_eps: float = 1e-8
+    gamma: float = 0.99
+    n_step: int = 3
+    batch_size: int = 32
+    double: bool = True
+    huber_delta: float = 1.0
+    target_sync_interval: int = 8000
+    prioritized: bool = True
+    step_mode: str = "graph"
+    encoder: str = "auto"
+
+    def __post_init__(self):
+        if self.lr <= 0 or self.adam_eps <= 0:
+            raise ValueError("DQNConfig: lr and adam_eps must be > 0")
+        if self.batch_size < 1:
+            raise ValueError(f"DQNConfig: batch_size must be >= 1, got {self.batch_size}")
+        if self.huber_delta <= 0:
+            raise ValueError(f"DQNConfig: huber_delta must be > 0, got {self.huber_delta}")
+        if self.target_sync_interval < 1:
+            raise ValueError("DQNConfig: target_sync_interval must be >= 1")
+
+
+def leaf_key(which: str, leaf: str) -> str:
+    return f"{which}.{leaf}"
+
+
+def _obs_buffer(spec, device, batch):
+    if spec.kind == "image":
+        return Tensor.from_numpy(np.zeros((batch,) + tuple(spec.shape), np.uint8), device, dtype=np.uint8)
+    return Tensor.from_numpy(np.zeros((batch, spec.size), np.float32), device)
+
+
+def step_inputs(obs_spec, device, *, batch: int, num_actions: int, mask_n: int = 0,
+                prioritized: bool = False) -> dict:
+    """The fixed device buffers one update reads, allocated once."""
+    if mask_n:
+        raise ValueError("step_inputs: legal-action masks are not supported by this learner")
+
+    def zeros(*shape):
+        return Tensor.from_numpy(np.zeros(shape, np.float32), device)
+
+    inputs = {
+        "rewards": zeros(batch, 1),
+        "dones": zeros(batch, 1),
+        "discounts": zeros(batch, 1),
+        "actions_onehot": zeros(batch, num_actions),
+        leaf_key("obs", obs_spec.name): _obs_buffer(obs_spec, device, batch),
+        leaf_key("next_obs", obs_spec.name): _obs_buffer(obs_spec, device, batch),
+    }
+    if prioritized:
+        inputs["is_weights"] = Tensor.from_numpy(np.ones((batch, 1), np.float32), device)
+    return inputs
+
+
+def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_n: int = 0, double: bool = True,
+                huber_delta: float = 1.0, prioritized: bool = False, grad_sq: bool = True) -> dict:
+    """One DQN update body: Huber loss against the n-step double-Q target,
+    backward, metrics.  Reads only `inputs`; no host reads (capturable)."""
+    (leaf,) = tuple(leaves)
+    obs = inputs[leaf_key("obs", leaf)]
+    next_obs = inputs[leaf_key("next_obs", leaf)]
+    q = online(obs)
+    with no_grad():
+        next_target_q = target(next_obs)
+        selector = online(next_obs) if double else next_target_q
+    loss, extra = dqn_td_loss(q, selector, next_target_q, inputs["actions_onehot"], inputs["rewards"],
+                              inputs["dones"], inputs["discounts"],
+                              inputs["is_weights"] if prioritized else None, huber_delta)
+    loss.backward()
+    metrics = {"loss": loss, "mean_q": extra["mean_q"]}
+    if prioritized:
+        metrics["td_abs"] = extra["td_abs"]
+    if grad_sq:
+        total = grad_sq_device(online.parameters())
+        if total is not None:
+            metrics["grad_sq"] = Tensor(total)
+    return metrics
+
+
+class DQNLearner:
+    """Online and target Q networks, Adam, and one captured update."""
+
+    def __init__(self, obs_spec, action_spec, device, *, cfg: DQNConfig = DQNConfig(), seed: int | None = None,
+                 online_state: dict | None = None, target_state: dict | None = None):
+        if action_spec.kind != "discrete":
+            raise ValueError(f"DQN supports discrete actions only, got {action_spec.kind!r}")
+        self.obs_spec = obs_spec
+        self.action_spec = action_spec
+        self.device = device
+        self.cfg = cfg
+        self.num_actions = int(action_spec.n)
+        if seed is not None:
+            np.random.seed(seed)
+        self.online = build_q_net(obs_spec, action_spec, device, batch=cfg.batch_size, encoder=cfg.encoder)
+        self.target = build_q_net(obs_spec, action_spec, device, batch=cfg.batch_size, encoder=cfg.encoder)
+        if online_state is not None:
+            self.online.load_state_dict(online_state)
+        self.target.copy_from(self.online)
+        if target_state is not None:
+            self.target.load_state_dict(target_state)
+        self.optimizer = Adam(list(self.online.parameters()), lr=cfg.lr, eps=cfg.adam_eps)
+        self.inputs = step_inputs(obs_spec, device, batch=cfg.batch_size, num_actions=self.num_actions,
+                                  prioritized=cfg.prioritized)
+        self.step = TrainStep(self._step_fn, self.inputs, device, optimizer=self.optimizer, mode=cfg.step_mode)
+        self.update_count = 0
+
+    def _step_fn(self, inputs: dict) -> dict:
+        metrics = update_loss(self.online, self.target, inputs, leaves=(self.obs_spec.name,),
+                              num_actions=self.num_actions, double=self.cfg.double,
+                              huber_delta=self.cfg.huber_delta, prioritized=self.cfg.prioritized, grad_sq=False)
+        # Adam reduces sum(g^2) over the same gradients in its own launch.
+        metrics["grad_sq"] = Tensor(self.optimizer.grad_sq)
+        return metrics
+
+    def load_batch(self, batch: dict) -> None:
+        """Upload one replay batch into the bound buffers."""
+        leaf = self.obs_spec.name
+        step = self.step
+        step.load_input(leaf_key("obs", leaf), batch["obs"])
+        step.load_input(leaf_key("next_obs", leaf), batch["next_obs"])
+        B = self.cfg.batch_size
+        step.load_input("rewards", np.asarray(batch["rewards"], np.float32).reshape(B, 1))
+        step.load_input("dones", np.asarray(batch["dones"], np.float32).reshape(B, 1))
+        step.load_input("discounts", np.asarray(batch["discounts"], np.float32).reshape(B, 1))
+        onehot = np.zeros((B, self.num_actions), np.float32)
+        onehot[np.arange(B), np.asarray(batch["actions"]).reshape(-1).astype(np.int64)] = 1.0
+        step.load_input("actions_onehot", onehot)
+        if self.cfg.prioritized:
+            w = batch.get("is_weights")
+            step.load_input("is_weights", np.ones((B, 1), np.float32) if w is None
+                            else np.asarray(w, np.float32).reshape(B, 1))
+
+    def update(self, batch: dict | None = None) -> dict:
+        """One gradient step; returns the reference's metric keys."""
+        if batch is not None:
+            self.load_batch(batch)
+        out = self.step.run()
+        self.update_count += 1
+        if self.update_count % self.cfg.target_sync_interval == 0:
+            self.target.copy_from(self.online)
+        grad_sq = float(np.asarray(out.get("grad_sq", 0.0)).reshape(-1)[0])
+        metrics = {
+            "loss": float(np.asarray(out["loss"]).reshape(-1)[0]),
+            "mean_q": float(np.asarray(out["mean_q"]).reshape(-1)[0]),
+            "grad_norm": float(np.sqrt(max(grad_sq, 0.0))),
+        }
+        if "td_abs" in out:
+            metrics["td_abs"] = np.asarray(out["td_abs"]).reshape(-1)
+        return metrics
+
+    def close(self) -> None:
+        self.step.close()

@@ -1,0 +1,256 @@
+"""Reverse-mode autograd tape over device arrays.
+
+Same contract as the reference tape (ttrl/engine/autograd.py:30-271): a
+`Tensor` node holds `data`, `requires_grad`, `grad`, a `_backward(grad)`
+closure and its `_parents`; `backward()` seeds 1.0 on a scalar, walks an
+iterative post-order DFS once, accumulates fp32 gradients, and releases the
+tape in a `finally`.  It refuses a non-scalar root, a second pass and a root
+with no tape, with the reference's messages.
+
+Two MI355X-side additions, invisible to callers:
+* a gradient may be written by a kernel straight into its final buffer:
+  `_grad_target()` hands out (buffer, beta) so a fused backward accumulates
+  in its epilogue instead of through a separate add, and parameters built
+  inside a `ParamArena` own a fixed gradient slot;
+* the seed is flagged as exactly 1.0, so a fused loss backward skips the
+  multiply by its upstream gradient.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from ttrl_amd.engine.tensor import DeviceArray, ParamArena, to_device, to_host
+
+__all__ = ["Tensor", "backward", "no_grad", "is_grad_enabled"]
+
+_GRAD_ENABLED = True
+
+
+def is_grad_enabled() -> bool:
+    return _GRAD_ENABLED
+
+
+class no_grad:
+    """Ops built inside record no tape (ttrl/engine/autograd.py:30-44)."""
+
+    def __enter__(self):
+        global _GRAD_ENABLED
+        self._prev = _GRAD_ENABLED
+        _GRAD_ENABLED = False
+        return self
+
+    def __exit__(self, *exc):
+        global _GRAD_ENABLED
+        _GRAD_ENABLED = self._prev
+        return False
+
+
+def _no_backward(grad):
+    return None
+
+
+class Tensor:
+    """A node in the autograd graph, backed by a `DeviceArray`."""
+
+    __slots__ = ("data", "requires_grad", "grad", "_backward", "_parents", "_op", "_backward_done",
+                 "_grad_slot", "_grad_owned", "_arena", "__weakref__")
+
+    def __init__(self, data, requires_grad: bool = False, _parents=(), _op: str = ""):
+        self.data = data
+        self.requires_grad = requires_grad
+        self.grad = None
+        self._backward = _no_backward
+        self._parents = tuple(_parents)
+        self._op = _op
+        self._backward_done = False
+        self._grad_slot = None
+        self._grad_owned = False
+        self._arena = None
+
+    # -- construction ------------------------------------------------------
+
+    @staticmethod
+    def from_numpy(array, device, *, requires_grad=False, dtype=np.float32, layout=None) -> "Tensor":
+        arr = np.asarray(array)
+        t = Tensor(to_device(arr, device, dtype), requires_grad)
+        arena = ParamArena.current()
+        if requires_grad and arena is not None and t.data.dtype == np.float32:
+            arena.register(t)
+        return t
+
+    def numpy(self) -> np.ndarray:
+        return to_host(self.data)
+
+    # -- introspection -----------------------------------------------------
+
+    @property
+    def shape(self):
+        return tuple(self.data.shape)
+
+    @property
+    def device(self):
+        return self.data.dev
+
+    @property
+    def dtype(self):
+        return self.data.dtype
+
+    def __repr__(self):
+        return f"Tensor(shape={self.shape}, op={self._op or 'leaf'}, grad={self.requires_grad})"
+
+    # -- gradient plumbing -------------------------------------------------
+
+    def _accumulate(self, grad: DeviceArray):
+        """grad += g (ttrl/engine/autograd.py:106-114)."""
+        from ttrl_amd.engine.ops import _kernels as K
+
+        if grad.shape != self.shape:
+            grad = grad.reshape(self.shape)
+        if self.grad is None:
+            if self._grad_slot is not None:
+                self._grad_slot.copy_from(grad)
+                self.grad = self._grad_slot
+                self._grad_owned = True
+            else:
+                self.grad = grad
+                self._grad_owned = False
+            return
+        if self._grad_owned:
+            K.binary_into("add", self.grad, grad, self.grad)
+        else:
+            out = K.binary("add", self.grad, grad)
+            self.grad = out
+            self._grad_owned = True
+
+    def _grad_target(self):
+        """(buffer, beta) a kernel writes this tensor's gradient into.
+
+        beta is 0.0 for the first contribution (overwrite) and 1.0 after
+        (accumulate).  The buffer is exclusively this tensor's.
+        """
+        if self.grad is None:
+            buf = self._grad_slot if self._grad_slot is not None else DeviceArray(self.device, self.shape)
+            self.grad = buf
+            self._grad_owned = True
+            return buf, 0.0
+        if not self._grad_owned:
+            own = self._grad_slot if self._grad_slot is not None else DeviceArray(self.device, self.shape)
+            own.copy_from(self.grad)
+            self.grad = own
+            self._grad_owned = True
+        return self.grad, 1.0
+
+    def zero_grad(self):
+        self.grad = None
+        self._grad_owned = False
+
+    def detach(self) -> "Tensor":
+        return Tensor(self.data, requires_grad=False)
+
+    def backward(self):
+        if not self.requires_grad:
+            raise RuntimeError(
+                "backward() called on a Tensor that requires no gradient; it "
+                "carries no tape (a leaf, a detached node, or built inside "
+                "no_grad()), so this call would silently produce no parameter "
+                "gradients at all."
+            )
+        if self._backward_done:
+            raise RuntimeError(
+                "backward() called a second time on the same graph; this tape "
+                "does not keep saved activations alive for a second pass "
+                "(no retain_graph). Build a fresh forward pass instead."
+            )
+        topo: list[Tensor] = []
+        seen: set[int] = set()
+        stack: list[tuple[Tensor, bool]] = [(self, False)]
+        while stack:
+            node, expanded = stack.pop()
+            if expanded:
+                topo.append(node)
+                continue
+            if id(node) in seen:
+                continue
+            seen.add(id(node))
+            stack.append((node, True))
+            for parent in node._parents:
+                if id(parent) not in seen:
+                    stack.append((parent, False))
+        numel = 1
+        for dim in self.shape:
+            numel *= dim
+        if numel != 1:
+            raise RuntimeError(
+                f"backward() called on a non-scalar Tensor with shape {self.shape} "
+                f"(numel={numel}); there is no `gradient=` kwarg to seed a "
+                "non-scalar backward pass, so reduce to a scalar first."
+            )
+        seed = DeviceArray(self.device, self.shape)
+        seed.fill(1.0)
+        self.grad = seed
+        self._grad_owned = True
+        try:
+            for node in reversed(topo):
+                grad = node.grad
+                if grad is not None:
+                    if node._backward_done and node is not self:
+                        raise RuntimeError(
+                            "backward() reached a node whose tape was already "
+                            "consumed by a previous backward() call on a graph "
+                            "sharing this subgraph; reusing a consumed subgraph "
+                            "is not supported (no retain_graph)."
+                        )
+                    node._backward(grad)
+        finally:
+            for node in topo:
+                if node._op:
+                    node._backward_done = True
+                node._backward = _no_backward
+                node._parents = ()
+
+    # -- operators ---------------------------------------------------------
+
+    def __add__(self, other):
+        from ttrl_amd.engine.ops.elementwise import add
+        return add(self, other)
+
+    __radd__ = __add__
+
+    def __mul__(self, other):
+        from ttrl_amd.engine.ops.elementwise import mul
+        return mul(self, other)
+
+    __rmul__ = __mul__
+
+    def __sub__(self, other):
+        from ttrl_amd.engine.ops.elementwise import sub
+        return sub(self, other)
+
+    def __rsub__(self, other):
+        from ttrl_amd.engine.ops.elementwise import sub
+        return sub(other, self)
+
+    def __neg__(self):
+        from ttrl_amd.engine.ops.elementwise import mul
+        return mul(self, -1.0)
+
+    def __truediv__(self, other):
+        from ttrl_amd.engine.ops.elementwise import div
+        return div(self, other)
+
+
+def backward(tensor: Tensor) -> None:
+    tensor.backward()
+
+
+def _is_scalar(x) -> bool:
+    return not isinstance(x, Tensor) and not hasattr(x, "shape")
+
+
+def _needs(*tensors) -> bool:
+    return _GRAD_ENABLED and any(isinstance(t, Tensor) and t.requires_grad for t in tensors)
+
+
+def _detached(data) -> Tensor:
+    return Tensor(data, requires_grad=False)

@@ -1,0 +1,126 @@
+"""Device handle: one HIP context and stream per opened GPU.
+
+Replaces `acquire` (ttrl/engine/device/acquire.py:56) and the chip scoping
+around it.  A `Device` owns a context from libttrl_hip; every kernel it
+launches runs on that context's single stream, so ordering between ops,
+copies and graph replays is stream order.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from contextlib import contextmanager
+
+from ttrl_amd import _lib
+
+__all__ = ["Device", "acquire", "device_count", "NoDeviceAvailable"]
+
+
+class NoDeviceAvailable(RuntimeError):
+    """No gfx950 device is visible to this process."""
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    rc = _lib.lib().ttrl_device_count(C.byref(n))
+    if rc != _lib.TTRL_OK:
+        return 0
+    return int(n.value)
+
+
+class Device:
+    """An open GPU: context, stream, allocation pools."""
+
+    def __init__(self, index: int = 0):
+        self.index = int(index)
+        handle = C.c_void_p()
+        rc = _lib.lib().ttrl_init(self.index, C.byref(handle))
+        if rc != _lib.TTRL_OK:
+            msg = _lib.lib().ttrl_last_error().decode(errors="replace")
+            raise NoDeviceAvailable(f"cannot open device {self.index}: {msg}")
+        self.ctx = handle
+        self._lock = threading.RLock()
+        self.closed = False
+        self._pool_stack = [0]
+
+    # -- plumbing ----------------------------------------------------------
+
+    def call(self, name: str, *args) -> None:
+        if self.closed:
+            raise RuntimeError("device is closed")
+        _lib.check(getattr(_lib.lib(), name)(self.ctx, *args), name)
+
+    def synchronize(self) -> None:
+        self.call("ttrl_sync")
+
+    @property
+    def capturing(self) -> bool:
+        return getattr(self, "_capturing", False)
+
+    # -- memory ------------------------------------------------------------
+
+    def alloc(self, nbytes: int) -> int:
+        ptr = C.c_void_p()
+        self.call("ttrl_alloc", C.c_size_t(max(1, int(nbytes))), C.byref(ptr))
+        return int(ptr.value)
+
+    def free(self, ptr: int) -> None:
+        if self.closed or not ptr:
+            return
+        _lib.lib().ttrl_free(self.ctx, C.c_void_p(ptr))
+
+    def create_pool(self) -> int:
+        pid = C.c_int(0)
+        self.call("ttrl_pool_create", C.byref(pid))
+        return int(pid.value)
+
+    def release_pool(self, pool: int) -> None:
+        if self.closed:
+            return
+        self.call("ttrl_pool_release", int(pool))
+
+    @contextmanager
+    def use_pool(self, pool: int):
+        """Allocations inside the block come from `pool`."""
+        prev = C.c_int(0)
+        self.call("ttrl_pool_use", int(pool), C.byref(prev))
+        try:
+            yield
+        finally:
+            if not self.closed:
+                self.call("ttrl_pool_use", int(prev.value), None)
+
+    def pool_stats(self, pool: int = 0) -> tuple[int, int]:
+        reserved, live = C.c_size_t(0), C.c_size_t(0)
+        self.call("ttrl_pool_stats", int(pool), C.byref(reserved), C.byref(live))
+        return int(reserved.value), int(live.value)
+
+    # -- lifecycle ---------------------------------------------------------
+
+    def close(self) -> None:
+        if self.closed:
+            return
+        _lib.lib().ttrl_shutdown(self.ctx)
+        self.closed = True
+
+    def __enter__(self) -> "Device":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def __repr__(self) -> str:
+        return f"Device({self.index}{', closed' if self.closed else ''})"
+
+
+_DEFAULT: dict[int, Device] = {}
+
+
+def acquire(index: int = 0) -> Device:
+    """The process-wide Device for GPU `index`, opened on first use."""
+    dev = _DEFAULT.get(index)
+    if dev is None or dev.closed:
+        dev = Device(index)
+        _DEFAULT[index] = dev
+    return dev

@@ -1,0 +1,153 @@
+"""Fused layer and loss ops: one tape node per layer (GEMM + bias + ReLU in
+one kernel, masked-ReLU backward and the bias gradient inside the
+weight-gradient GEMM) and one per loss head.
+
+`linear` computes exactly `relu(matmul(x, W) + b)` of
+ttrl/engine/layers.py:57-61 and ttrl/engine/ops/unary.py:25-37; its backward
+gives the same gradients as the reference's matmul / add / relu_bw chain
+(ttrl/engine/ops/matmul.py:71-84, ttrl/engine/ops/broadcast.py:11-30).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+from ttrl_amd import _lib
+from ttrl_amd.engine.autograd import Tensor, _detached, _needs
+from ttrl_amd.engine.tensor import DeviceArray
+
+__all__ = ["linear", "dqn_td_loss", "grad_targets"]
+
+
+def _p(arr) -> int | None:
+    return None if arr is None else arr.ptr
+
+
+def grad_targets(*tensors):
+    """(buffer, beta) per tensor that requires grad (None otherwise), with a
+    common beta.  A mixed first/accumulated set is brought to beta=1 by
+    zero-filling the fresh buffers."""
+    out = []
+    for t in tensors:
+        if t is None or not t.requires_grad:
+            out.append(None)
+            continue
+        out.append(list(t._grad_target()))
+    betas = {o[1] for o in out if o is not None}
+    if len(betas) > 1:
+        for o in out:
+            if o is not None and o[1] == 0.0:
+                o[0].fill(0.0)
+                o[1] = 1.0
+    beta = 1.0 if 1.0 in betas else 0.0
+    return [None if o is None else o[0] for o in out], beta
+
+
+def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None, *, relu: bool = False) -> Tensor:
+    """y = x @ W + b (+ ReLU) as one MFMA launch; W stored (in, out)."""
+    if len(x.shape) != 2 or len(weight.shape) != 2:
+        raise ValueError(f"linear: expected (M, K) @ (K, N), got {x.shape} @ {weight.shape}")
+    M, K = (int(d) for d in x.shape)
+    K2, N = (int(d) for d in weight.shape)
+    if K != K2:
+        raise ValueError(f"linear: input has {K} features, weight expects {K2}")
+    if bias is not None and bias.data.numel != N:
+        raise ValueError(f"linear: bias has {bias.data.numel} elements, expected {N}")
+    dev = x.device
+    y = DeviceArray(dev, (M, N))
+    d = _lib.LinearDesc()
+    d.M, d.K, d.N, d.groups = M, K, N, 1
+    d.x, d.ldx = x.data.ptr, K
+    d.W = weight.data.ptr
+    d.b = _p(bias.data if bias is not None else None)
+    d.y = y.ptr
+    d.relu = int(relu)
+    dev.call("ttrl_linear_forward", C.byref(d))
+    if not _needs(x, weight, bias):
+        return _detached(y)
+    parents = (x, weight) + ((bias,) if bias is not None else ())
+    out = Tensor(y, True, parents, "linear_relu" if relu else "linear")
+    x_data, w_data = x.data, weight.data
+
+    def _backward(grad):
+        (dw, db), beta_w = grad_targets(weight, bias)
+        (dx,), beta_x = grad_targets(x)
+        if dw is None and db is not None:
+            # Bias-only gradient: a column sum of dZ.
+            from ttrl_amd.engine.ops import _kernels as Kk
+            g = Kk.binary("relu_bw", grad, y) if relu else grad
+            s = Kk.reduce_dim("sum", g, 0, keepdim=True)
+            if beta_w:
+                Kk.binary_into("add", db, s.reshape(db.shape), db)
+            else:
+                db.copy_from(s.reshape(db.shape))
+            db_ = None
+        else:
+            db_ = db
+        b = _lib.LinearDesc()
+        b.M, b.K, b.N, b.groups = M, K, N, 1
+        b.x, b.ldx = x_data.ptr, K
+        b.W = w_data.ptr
+        b.dy = grad.ptr
+        b.ymask = y.ptr if relu else None
+        b.dW = _p(dw)
+        b.db = _p(db_) if dw is not None else None
+        b.dx = _p(dx)
+        b.lddx = K
+        b.beta_w, b.beta_x = beta_w, beta_x
+        if dw is not None or dx is not None:
+            dev.call("ttrl_linear_backward", C.byref(b))
+
+    out._backward = _backward
+    return out
+
+
+def dqn_td_loss(q: Tensor, q_next_select: Tensor, q_next_value: Tensor, actions_onehot: Tensor,
+                rewards: Tensor, dones: Tensor, discounts: Tensor, is_weights: Tensor | None,
+                delta: float):
+    """The DQN update head as one kernel (ttrl/algos/dqn/losses.py:96-129).
+
+    -> (loss, metrics) where loss is a (1, 1) tape node differentiable in `q`
+    and metrics holds detached `mean_q`, `td_abs` (B, 1), `td_target` (B, 1)
+    and `next_actions` (B, 1, float indices).
+    """
+    B, A = (int(d) for d in q.shape)
+    for name, t, shape in (("q_next_select", q_next_select, (B, A)), ("q_next_value", q_next_value, (B, A)),
+                           ("actions_onehot", actions_onehot, (B, A))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"dqn_td_loss: {name} has shape {t.shape}, expected {shape}")
+    for name, t in (("rewards", rewards), ("dones", dones), ("discounts", discounts), ("is_weights", is_weights)):
+        if t is not None and t.data.numel != B:
+            raise ValueError(f"dqn_td_loss: {name} has {t.data.numel} elements, expected {B}")
+    if not delta > 0.0:
+        raise ValueError(f"dqn_td_loss: huber delta must be > 0, got {delta}")
+    dev = q.device
+    loss = DeviceArray(dev, (1, 1))
+    mean_q = DeviceArray(dev, (1, 1))
+    td_abs = DeviceArray(dev, (B, 1))
+    td_target = DeviceArray(dev, (B, 1))
+    next_act = DeviceArray(dev, (B, 1))
+    dq = DeviceArray(dev, (B, A))
+    dev.call("ttrl_dqn_loss", B, A, q.data.vp, q_next_select.data.vp, q_next_value.data.vp,
+             actions_onehot.data.vp, rewards.data.vp, dones.data.vp, discounts.data.vp,
+             None if is_weights is None else is_weights.data.vp, C.c_float(delta), loss.vp, mean_q.vp,
+             td_abs.vp, dq.vp, next_act.vp, td_target.vp)
+    metrics = {
+        "mean_q": Tensor(mean_q), "td_abs": Tensor(td_abs), "td_target": Tensor(td_target),
+        "next_actions": Tensor(next_act),
+    }
+    if not _needs(q):
+        return _detached(loss), metrics
+    out = Tensor(loss, True, (q,), "dqn_td_loss")
+
+    def _backward(grad):
+        if not q.requires_grad:
+            return
+        if grad.unit:
+            q._accumulate(dq)
+        else:
+            from ttrl_amd.engine.ops import _kernels as Kk
+            q._accumulate(Kk.binary("mul", dq, grad.reshape((1, 1))))
+
+    out._backward = _backward
+    return out, metrics

@@ -1,0 +1,209 @@
+"""Adam over fp32 parameters, updated in place (ttrl/engine/optim/adam.py:25-134).
+
+Stores S = m/(1-b1) and V = v/(1-b2) like the reference, so the fused
+bias-correction scalars (ttrl/engine/optim/scalars.py:13-27) apply unchanged
+and checkpoints carry canonical m and v (ttrl/engine/optim/checkpoint.py:15-104).
+
+One kernel updates a whole parameter arena (every tensor of a network built
+inside one `ParamArena`), reading the update count from a device counter so
+that a captured graph containing the step replays correctly for every t.
+The same launch reduces sum(g^2) into `grad_sq` (ttrl/algos/grads.py:46-60).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+
+from ttrl_amd.engine.tensor import DeviceArray, MASTER_DTYPE, arena_of, zeros
+
+__all__ = ["Adam", "Optimizer", "adam_fused_scalars"]
+
+
+def adam_fused_scalars(lr: float, b1: float, b2: float, eps: float, t: int) -> tuple[float, float]:
+    """(alpha_t, eps_t) of the composed Adam tail for update number t."""
+    if t < 1:
+        raise ValueError(f"adam_fused_scalars: t must be >= 1, got {t}")
+    bc1 = 1 - b1 ** t
+    bc2 = 1 - b2 ** t
+    c = math.sqrt((1 - b2) / bc2)
+    return lr * (1 - b1) / bc1 / c, eps / c
+
+
+class Optimizer:
+    def __init__(self, params):
+        self.params = list(params)
+
+    def zero_grad(self) -> None:
+        for p in self.params:
+            p.zero_grad()
+
+
+class Adam(Optimizer):
+    """Adam over fp32 parameters, updated in place."""
+
+    def __init__(self, params, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0):
+        super().__init__(params)
+        if not self.params:
+            raise ValueError("Adam: params is empty, so there is nothing to optimize")
+        if lr <= 0:
+            raise ValueError(f"Adam: lr must be > 0, got {lr}")
+        b1, b2 = betas
+        if not (0.0 <= b1 < 1.0 and 0.0 <= b2 < 1.0):
+            raise ValueError(f"Adam: betas must be in [0, 1), got {betas}")
+        if eps <= 0:
+            raise ValueError(f"Adam: eps must be > 0, got {eps}")
+        if weight_decay < 0:
+            raise ValueError(f"Adam: weight_decay must be >= 0, got {weight_decay}")
+        wrong = [i for i, p in enumerate(self.params) if p.data.dtype != MASTER_DTYPE]
+        if wrong:
+            raise ValueError(f"Adam: parameters must be float32; parameters {wrong} are not")
+        self.lr = float(lr)
+        self.b1, self.b2 = float(b1), float(b2)
+        self.eps = float(eps)
+        self.weight_decay = float(weight_decay)
+        self.t = 0
+        self.steps = [0] * len(self.params)
+        dev = self.params[0].device
+        self.device = dev
+        self.arena = arena_of(self.params)
+        n = len(self.params)
+        # counters[i]: update count of parameter i; counters[n]: of the arena launch.
+        self._counters = DeviceArray(dev, (n + 1,), np.int32)
+        self._counters.fill(0)
+        self._arena_t = 0
+        self.grad_sq = zeros(dev, (1, 1))
+        if self.arena is not None:
+            self._m_flat = zeros(dev, (self.arena.numel,))
+            self._v_flat = zeros(dev, (self.arena.numel,))
+            self.m = [self._m_flat.view(off, p.shape) for p, off in zip(self.params, self.arena.offsets)]
+            self.v = [self._v_flat.view(off, p.shape) for p, off in zip(self.params, self.arena.offsets)]
+        else:
+            self.m = [zeros(dev, p.shape) for p in self.params]
+            self.v = [zeros(dev, p.shape) for p in self.params]
+
+    @property
+    def _m_scale(self) -> float:
+        return 1 - self.b1
+
+    @property
+    def _v_scale(self) -> float:
+        return 1 - self.b2
+
+    def _counter(self, i: int) -> C.c_void_p:
+        return C.c_void_p(self._counters.ptr + 4 * i)
+
+    def step(self) -> None:
+        """One update of every parameter that holds a gradient.
+
+        Inside a graph capture nothing executes, so the host counters are
+        advanced by `_replayed()` when the graph runs instead of here.
+        """
+        capturing = self.device.capturing
+        if not capturing:
+            self.t += 1
+        have = [p.grad is not None for p in self.params]
+        dev = self.device
+        args = (C.c_float(self.lr), C.c_float(self.b1), C.c_float(self.b2), C.c_float(self.eps),
+                C.c_float(self.weight_decay))
+        counts_in_sync = all(s == self._arena_t for s in self.steps)
+        if self.arena is not None and all(have) and counts_in_sync:
+            for p in self.params:
+                if p.grad is not p._grad_slot:
+                    p._grad_slot.copy_from(p.grad)
+                    p.grad = p._grad_slot
+                    p._grad_owned = True
+            a = self.arena
+            dev.call("ttrl_adam_step", a.data.vp, a.grad.vp, self._m_flat.vp, self._v_flat.vp,
+                     C.c_long(a.numel), self._counter(len(self.params)), *args, self.grad_sq.vp, 0)
+            if not capturing:
+                self._arena_t += 1
+                self.steps = [s + 1 for s in self.steps]
+            return
+        if dev.capturing:
+            raise RuntimeError(
+                "Adam.step inside a captured graph needs every parameter of one arena to hold a "
+                "gradient; step this optimizer outside the capture instead."
+            )
+        self._counters.upload(np.asarray(self.steps + [self._arena_t], np.int32))
+        first = True
+        for i, p in enumerate(self.params):
+            if p.grad is None:
+                continue
+            g = p.grad
+            if p.data.numel % 4 or (p.data.ptr | g.ptr | self.m[i].ptr | self.v[i].ptr) % 16:
+                # the kernel needs 16-byte aligned float4 ranges: stage through aligned copies
+                g = _aligned_copy(g)
+            self._step_one(i, p, g, args, accumulate=not first)
+            first = False
+            self.steps[i] += 1
+
+    def _step_one(self, i, p, g, args, accumulate):
+        dev = self.device
+        pd, m, v = p.data, self.m[i], self.v[i]
+        staged = [_aligned_copy(x) if (x.ptr % 16) else x for x in (pd, m, v)]
+        dev.call("ttrl_adam_step", staged[0].vp, g.vp, staged[1].vp, staged[2].vp, C.c_long(pd.numel),
+                 self._counter(i), *args, self.grad_sq.vp, int(accumulate))
+        for orig, st in zip((pd, m, v), staged):
+            if st is not orig:
+                orig.copy_from(st)
+
+    def _replayed(self, have_grads=None) -> None:
+        """Host bookkeeping after a graph replay that ran one step."""
+        self.t += 1
+        self._arena_t += 1
+        self.steps = [s + 1 for s in self.steps]
+
+    # -- checkpointing -----------------------------------------------------
+
+    def state_dict(self) -> dict:
+        return {
+            "t": self.t,
+            "steps": list(self.steps),
+            "lr": self.lr,
+            "betas": (self.b1, self.b2),
+            "eps": self.eps,
+            "weight_decay": self.weight_decay,
+            "m": [m.numpy() * self._m_scale for m in self.m],
+            "v": [v.numpy() * self._v_scale for v in self.v],
+        }
+
+    def load_state_dict(self, state: dict, device=None) -> None:
+        if len(state["m"]) != len(self.m) or len(state["v"]) != len(self.v):
+            raise ValueError(
+                f"Adam.load_state_dict: checkpoint has {len(state['m'])} m and {len(state['v'])} v buffers, "
+                f"expected {len(self.m)} of each for this optimizer's parameter list."
+            )
+        for key, buffers in (("m", self.m), ("v", self.v)):
+            for i, (arr, buf) in enumerate(zip(state[key], buffers)):
+                got = tuple(np.asarray(arr).shape)
+                if got != tuple(buf.shape):
+                    raise ValueError(
+                        f"Adam.load_state_dict: {key}[{i}] has shape {got}, which does not match its "
+                        f"parameter's shape {tuple(buf.shape)}."
+                    )
+        t = int(state["t"])
+        steps = [int(s) for s in state.get("steps", [t] * len(self.params))]
+        self.lr = float(state.get("lr", self.lr))
+        self.b1, self.b2 = (float(x) for x in state.get("betas", (self.b1, self.b2)))
+        self.eps = float(state.get("eps", self.eps))
+        self.weight_decay = float(state.get("weight_decay", self.weight_decay))
+        for arr, buf in zip(state["m"], self.m):
+            buf.upload(np.asarray(arr, np.float64) / self._m_scale)
+        for arr, buf in zip(state["v"], self.v):
+            buf.upload(np.asarray(arr, np.float64) / self._v_scale)
+        self.t = t
+        self.steps = steps
+        self._arena_t = steps[0] if steps and all(s == steps[0] for s in steps) else -1
+        self._counters.upload(np.asarray(self.steps + [max(self._arena_t, 0)], np.int32))
+
+
+def _aligned_copy(x: DeviceArray) -> DeviceArray:
+    n = x.numel
+    padded = DeviceArray(x.dev, (((n + 3) // 4) * 4,))
+    padded.fill(0.0)
+    padded.view(0, x.shape).copy_from(x)
+    out = padded.view(0, x.shape)
+    return out

@@ -1,0 +1,107 @@
+"""Output heads (ttrl/nets/heads.py:25-116).  GaussianHead clamps log_std to
+[-20, 2]; `forward` composes Linear + clamp like the reference, and
+`forward_packed` computes both heads in one launch with the clamp in the
+epilogue, returning [mean | log_std] rows for the fused squashed sample."""
+
+from __future__ import annotations
+
+import ctypes as C
+
+from ttrl_amd import _lib
+from ttrl_amd.engine.autograd import Tensor, _detached, _needs
+from ttrl_amd.engine.layers import Linear
+from ttrl_amd.engine.nn import Module, ModuleDict
+from ttrl_amd.engine.ops import clamp
+from ttrl_amd.engine.ops.fused import grad_targets
+from ttrl_amd.engine.tensor import DeviceArray
+
+LOG_STD_MIN = -20.0
+LOG_STD_MAX = 2.0
+
+
+class QHead(Module):
+    def __init__(self, in_features: int, n_actions: int, device):
+        self.q = Linear(in_features, n_actions, device)
+        self.n_actions = int(n_actions)
+
+    def forward(self, x):
+        return self.q(x)
+
+
+class CategoricalHead(Module):
+    def __init__(self, in_features: int, n_actions: int, device):
+        self.logits = Linear(in_features, n_actions, device)
+        self.n_actions = int(n_actions)
+
+    def forward(self, x):
+        return self.logits(x)
+
+
+class ValueHead(Module):
+    def __init__(self, in_features: int, device):
+        self.value = Linear(in_features, 1, device)
+
+    def forward(self, x):
+        return self.value(x)
+
+
+class GaussianHead(Module):
+    def __init__(self, in_features: int, action_dim: int, device, *, log_std_min: float = LOG_STD_MIN,
+                 log_std_max: float = LOG_STD_MAX):
+        if log_std_min >= log_std_max:
+            raise ValueError(
+                f"GaussianHead: log_std_min must be < log_std_max, got {log_std_min} and {log_std_max}"
+            )
+        self.action_dim = int(action_dim)
+        self.log_std_min = float(log_std_min)
+        self.log_std_max = float(log_std_max)
+        self.heads = ModuleDict({
+            "mean": Linear(in_features, self.action_dim, device),
+            "log_std": Linear(in_features, self.action_dim, device),
+        })
+
+    def forward(self, x):
+        mean = self.heads["mean"](x)
+        log_std = clamp(self.heads["log_std"](x), self.log_std_min, self.log_std_max)
+        return mean, log_std
+
+    def forward_packed(self, x: Tensor) -> Tensor:
+        """(B, 2d) rows [mean | clamp(log_std)] from one launch.  Its backward
+        expects the log_std columns' gradient already masked to the open clamp
+        interval, which the fused squashed-sample backward provides."""
+        lm, ls = self.heads["mean"], self.heads["log_std"]
+        M, K = (int(d) for d in x.shape)
+        d = self.action_dim
+        dev = x.device
+        y = DeviceArray(dev, (M, 2 * d))
+        desc = _lib.LinearDesc()
+        desc.M, desc.K, desc.N, desc.groups = M, K, 2 * d, 1
+        desc.x, desc.ldx = x.data.ptr, K
+        desc.W, desc.b = lm.weight.data.ptr, lm.bias.data.ptr
+        desc.W2, desc.b2, desc.n1 = ls.weight.data.ptr, ls.bias.data.ptr, d
+        desc.y = y.ptr
+        desc.clamp_col, desc.lo, desc.hi = d, self.log_std_min, self.log_std_max
+        dev.call("ttrl_linear_forward", C.byref(desc))
+        params = (lm.weight, lm.bias, ls.weight, ls.bias)
+        if not _needs(x, *params):
+            return _detached(y)
+        out = Tensor(y, True, (x,) + params, "gaussian_head")
+        x_data = x.data
+
+        def _backward(grad):
+            (dwm, dbm, dws, dbs), beta_w = grad_targets(*params)
+            (dx,), beta_x = grad_targets(x)
+            b = _lib.LinearDesc()
+            b.M, b.K, b.N, b.groups = M, K, 2 * d, 1
+            b.x, b.ldx = x_data.ptr, K
+            b.W, b.W2, b.n1 = lm.weight.data.ptr, ls.weight.data.ptr, d
+            b.dy = grad.ptr
+            if dwm is not None:
+                b.dW, b.db, b.dW2, b.db2 = dwm.ptr, dbm.ptr, dws.ptr, dbs.ptr
+            b.dx = None if dx is None else dx.ptr
+            b.lddx = K
+            b.beta_w, b.beta_x = beta_w, beta_x
+            dev.call("ttrl_linear_backward", C.byref(b))
+
+        out._backward = _backward
+        return out

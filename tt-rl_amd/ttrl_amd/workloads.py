@@ -1,0 +1,92 @@
+"""Seeded synthetic inputs and initial weights for the learner-update
+workloads (uint8 Atari-shaped frames for DQN, Hopper-shaped vectors for SAC).
+
+No data is downloaded: every array is drawn from numpy's default_rng with
+the given seed, with the distributions of the benchmark configurations:
+  DQN  frames uint8 uniform 0..255, actions uniform in [0, A), rewards in
+       {-1, 0, 1} w.p. 0.05 / 0.9 / 0.05, done ~ Bernoulli(0.01), discounts
+       gamma**n_step, importance weights uniform in (0.4, 1];
+  SAC  observations and actions N(0, 1) (actions clipped to [-1, 1]),
+       rewards N(0, 1), done ~ Bernoulli(0.001), reparameterisation noise
+       N(0, 1).
+Weights are He-uniform U(+-sqrt(6/fan_in)) with biases U(+-1/sqrt(fan_in)).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = ["dqn_batch", "sac_batch", "he_uniform_qnet_state", "he_uniform_sac_state"]
+
+
+def dqn_batch(seed: int, batch: int = 32, num_actions: int = 6, frame_shape=(4, 84, 84), gamma: float = 0.99,
+              n_step: int = 3, prioritized: bool = True, discounts=None) -> dict:
+    rng = np.random.default_rng(seed)
+    out = {
+        "obs": rng.integers(0, 256, (batch,) + tuple(frame_shape), dtype=np.uint8),
+        "next_obs": rng.integers(0, 256, (batch,) + tuple(frame_shape), dtype=np.uint8),
+        "actions": rng.integers(0, num_actions, batch).astype(np.int64),
+        "rewards": rng.choice(np.array([-1.0, 0.0, 1.0], np.float32), batch, p=[0.05, 0.9, 0.05]),
+        "dones": (rng.random(batch) < 0.01).astype(np.float32),
+        "discounts": (np.full(batch, gamma ** n_step, np.float32) if discounts is None
+                      else np.asarray(discounts, np.float32)),
+    }
+    if prioritized:
+        out["is_weights"] = (1.0 - 0.6 * rng.random(batch)).astype(np.float32)  # (0.4, 1]
+    return out
+
+
+def sac_batch(seed: int, batch: int = 256, obs_dim: int = 11, act_dim: int = 3, gamma: float = 0.99) -> dict:
+    rng = np.random.default_rng(seed)
+    return {
+        "obs": rng.standard_normal((batch, obs_dim)).astype(np.float32),
+        "next_obs": rng.standard_normal((batch, obs_dim)).astype(np.float32),
+        "actions": np.clip(rng.standard_normal((batch, act_dim)), -1.0, 1.0).astype(np.float32),
+        "rewards": rng.standard_normal(batch).astype(np.float32),
+        "dones": (rng.random(batch) < 0.001).astype(np.float32),
+        "discounts": np.full(batch, gamma, np.float32),
+        "noise": rng.standard_normal((batch, act_dim)).astype(np.float32),
+        "next_noise": rng.standard_normal((batch, act_dim)).astype(np.float32),
+    }
+
+
+def _he(rng, shape, fan_in):
+    bound = np.sqrt(6.0 / fan_in)
+    return rng.uniform(-bound, bound, shape).astype(np.float32)
+
+
+def _bias(rng, n, fan_in):
+    bound = 1.0 / np.sqrt(fan_in)
+    return rng.uniform(-bound, bound, n).astype(np.float32)
+
+
+def he_uniform_qnet_state(net, seed: int) -> dict:
+    """A state_dict for `net` (a built Q network) with He-uniform weights."""
+    rng = np.random.default_rng(seed)
+    state = {}
+    ref = net.state_dict()
+    keys = list(ref)
+    for k in keys:
+        shape = ref[k].shape
+        if k.endswith("weight"):
+            fan_in = int(np.prod(shape[1:])) if len(shape) == 4 else int(shape[0])
+            state[k] = _he(rng, shape, fan_in)
+            last_fan = fan_in
+        else:
+            state[k] = _bias(rng, int(np.prod(shape)), last_fan).reshape(shape)
+    return state
+
+
+def he_uniform_sac_state(module, seed: int) -> dict:
+    """He-uniform weights for any module of Linear layers (W stored (in, out))."""
+    rng = np.random.default_rng(seed)
+    state = {}
+    ref = module.state_dict()
+    last_fan = 1
+    for k, v in ref.items():
+        if k.endswith("weight"):
+            last_fan = int(v.shape[0])
+            state[k] = _he(rng, v.shape, last_fan)
+        else:
+            state[k] = _bias(rng, int(np.prod(v.shape)), last_fan).reshape(v.shape)
+    return state
