@@ -1,0 +1,60 @@
+"""Shared set-up of SAC parity tests."""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def _pairs(state: dict):
+    items = list(state.items())
+    return [(np.asarray(items[i][1], np.float64), np.asarray(items[i + 1][1], np.float64).reshape(-1))
+            for i in range(0, len(items), 2)]
+
+
+def sac_to_oracle(policy_state: dict, critics_state: dict, targets_state: dict, log_alpha: float):
+    from oracle.sac import SacParams
+
+    pol = _pairs(policy_state)
+    crit = _pairs(critics_state)
+    targ = _pairs(targets_state)
+    n = len(crit) // 2
+    return SacParams(trunk=pol[:-2], mean=pol[-2], log_std=pol[-1], critics=[crit[:n], crit[n:]],
+                     targets=[targ[:n], targ[n:]], log_alpha=float(log_alpha))
+
+
+def build_sac(device, *, seed=0, step_mode="graph", batch=256):
+    from ttrl_amd.algos.sac import SACConfig, SACLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_sac_state
+
+    cfg = SACConfig(batch_size=batch, step_mode=step_mode)
+    learner = SACLearner(ObsSpec.vector(11), ActionSpec.continuous(3), device, cfg=cfg, seed=seed)
+    pol = he_uniform_sac_state(learner.nets.policy, seed + 10)
+    crit = he_uniform_sac_state(learner.nets.critics, seed + 20)
+    learner.nets.policy.load_state_dict(pol)
+    learner.nets.critics.load_state_dict(crit)
+    learner.nets.targets.load_state_dict(crit)
+    return learner, pol, crit
+
+
+def record_gates(records, B):
+    """Device ReLU outputs in execution order -> oracle gate names."""
+    names = []
+    out = {}
+    it = iter(records)
+
+    def twin(prefix, suffix=""):
+        for layer in range(2):
+            y = next(it).numpy().reshape(2, B, -1)
+            out[f"{prefix}0{suffix}.{layer}"] = y[0] > 0
+            out[f"{prefix}1{suffix}.{layer}"] = y[1] > 0
+
+    for layer in range(2):
+        out[f"policy_next.{layer}"] = next(it).numpy() > 0
+    twin("target")
+    twin("critic")
+    for layer in range(2):
+        out[f"policy.{layer}"] = next(it).numpy() > 0
+    twin("critic", "_pi")
+    del names
+    return out

@@ -1,0 +1,463 @@
+"""The SAC learner update (ttrl/algos/sac/losses.py:25-94, step.py:28-130,
+targets.py:21-96, agent.py:175-238).
+
+One update, in the reference's order: critic region (soft target under
+no_grad, twin-critic loss, backward), critic Adam, actor region (reading the
+just-updated critics: reparameterised sample, actor loss, temperature loss,
+backwards), policy and temperature Adam, Polyak blend of the targets.  In
+"graph" mode the whole update, optimizers and blend included, is one
+hipGraph; in "eager" mode the same kernels run one by one.
+
+Fused pieces:
+* `TwinQ` runs both critics of a `build_sac_nets` critic list as one grouped
+  launch per layer (they live in one parameter arena at a fixed stride), with
+  concat(s, a) folded into the first layer's loads;
+* `squashed_sample` (ttrl_amd.algos.gaussian) is one kernel forward and one
+  backward;
+* the critic loss and the actor + temperature losses are one kernel each.
+The critic weight gradients that the reference computes in the actor region
+and then discards (its RegionOptimizers zero them) are not computed: the
+critics enter the actor region with their parameters frozen.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ttrl_amd import _lib
+from ttrl_amd.algos.gaussian import ActionScale, squashed_sample
+from ttrl_amd.engine.autograd import Tensor, _needs, no_grad
+from ttrl_amd.engine import layers as layers_mod
+from ttrl_amd.engine.layers import Linear, ReLU
+from ttrl_amd.engine.ops import _kernels as K
+from ttrl_amd.engine.ops.fused import grad_targets
+from ttrl_amd.engine.optim import Adam
+from ttrl_amd.engine.tensor import DeviceArray, ParamArena
+from ttrl_amd.engine.trace import capture
+from ttrl_amd.nets.build import build_sac_nets
+from ttrl_amd.nets.heads import GaussianHead
+
+__all__ = ["SACConfig", "SACLearner", "TwinQ", "sac_critic_loss", "sac_actor_losses"]
+
+
+@dataclass(frozen=True)
+class SACConfig:
+    """Learner-side fields of ttrl/algos/sac/config.py:15-183."""
+
+    lr: float = 3e-4
+    adam_eps: float = 1e-8
+    gamma: float = 0.99
+    tau: float = 0.005
+    batch_size: int = 256
+    learn_alpha: bool = True
+    init_log_alpha: float = 0.0
+    target_entropy: float | None = None
+    prioritized: bool = False
+    step_mode: str = "graph"
+    critic_hidden: tuple = (256, 256)
+    policy_hidden: tuple = (256, 256)
+
+    def __post_init__(self):
+        if self.lr <= 0 or self.adam_eps <= 0:
+            raise ValueError("SACConfig: lr and adam_eps must be > 0")
+        if not 0.0 <= self.tau <= 1.0:
+            raise ValueError(f"SACConfig: tau must be in [0, 1], got {self.tau}")
+        if self.step_mode not in ("eager", "graph"):
+            raise ValueError(f"SACConfig: step_mode must be 'eager' or 'graph', got {self.step_mode!r}")
+
+
+# --------------------------------------------------------------- twin Q ---
+
+class TwinQ:
+    """Both critics of a critic list as grouped launches.
+
+    Each critic must be concat(s, a) -> [Linear -> ReLU]* -> Linear(1) with
+    its parameters at a fixed stride from the first critic's in one arena,
+    which is how `build_sac_nets` lays them out.
+    """
+
+    def __init__(self, critics):
+        crit = list(critics)
+        if len(crit) != 2:
+            raise ValueError(f"TwinQ: expected two critics, got {len(crit)}")
+        self.layers = []
+        for c in crit:
+            seq = list(c.head.layers)
+            lins = []
+            for i, layer in enumerate(seq):
+                if isinstance(layer, Linear):
+                    lins.append(layer)
+                elif isinstance(layer, ReLU):
+                    continue
+                elif hasattr(layer, "value") and isinstance(layer.value, Linear):
+                    lins.append(layer.value)
+                else:
+                    raise ValueError(f"TwinQ: unsupported critic layer {type(layer).__name__}")
+            if len(c.encoder.tower) != 0:
+                raise ValueError("TwinQ: the critic's observation tower must be the identity encoder")
+            self.layers.append(lins)
+        a, b = self.layers
+        if len(a) != len(b):
+            raise ValueError("TwinQ: the two critics differ in depth")
+        info0 = a[0].weight._arena
+        if info0 is None:
+            raise ValueError("TwinQ: critics must be built inside one ParamArena")
+        stride = b[0].weight._arena[1] - info0[1]
+        for la, lb in zip(a, b):
+            for pa, pb in ((la.weight, lb.weight), (la.bias, lb.bias)):
+                if pa._arena is None or pb._arena is None or pa._arena[0] is not pb._arena[0]:
+                    raise ValueError("TwinQ: critics must share one ParamArena")
+                if pb._arena[1] - pa._arena[1] != stride or tuple(pa.shape) != tuple(pb.shape):
+                    raise ValueError("TwinQ: critic parameters are not at a fixed stride")
+        self.stride = stride
+        self.obs_dim = a[0].in_features - crit[0].encoder.action_width
+        self.act_dim = crit[0].encoder.action_width
+
+    def params(self):
+        out = []
+        for lins in self.layers:
+            for lin in lins:
+                out += [lin.weight, lin.bias]
+        return out
+
+    def forward(self, obs: Tensor | None = None, action: Tensor | None = None, *, obs_action: Tensor | None = None,
+                train_params: bool = True) -> Tensor:
+        """Q of both critics, (2, B, 1).  Pass a dense concat(s, a) as
+        `obs_action` (required when training the critics) or `obs` and
+        `action` separately."""
+        lins = self.layers[0]
+        if obs_action is not None:
+            x, x2 = obs_action, None
+        else:
+            x, x2 = obs, action
+        B = int(x.shape[0])
+        dev = x.device
+        S = self.stride
+        acts = []
+        h = None
+        nl = len(lins)
+        for j, lin in enumerate(lins):
+            N = lin.out_features
+            y = DeviceArray(dev, (2, B, N))
+            d = _lib.LinearDesc()
+            d.M, d.K, d.N, d.groups = B, lin.in_features, N, 2
+            if j == 0:
+                d.x, d.ldx, d.gx = x.data.ptr, int(x.shape[1]), 0
+                if x2 is not None:
+                    d.x2, d.ldx2, d.gx2, d.k1 = x2.data.ptr, int(x2.shape[1]), 0, int(x.shape[1])
+            else:
+                d.x, d.ldx, d.gx = h.ptr, lins[j - 1].out_features, B * lins[j - 1].out_features
+            d.W, d.gW = lin.weight.data.ptr, S
+            d.b, d.gb = lin.bias.data.ptr, S
+            d.y, d.gy = y.ptr, B * N
+            d.relu = int(j < nl - 1)
+            dev.call("ttrl_linear_forward", C.byref(d))
+            if d.relu and layers_mod.RECORD is not None:
+                layers_mod.RECORD.append(y)
+            acts.append(y)
+            h = y
+        params = self.params() if train_params else []
+        inputs = [t for t in (x, x2) if t is not None]
+        if not _needs(*inputs, *params):
+            return Tensor(h)
+        out = Tensor(h, True, tuple(inputs) + tuple(params), "twin_q")
+        want_action = x2 is not None and x2.requires_grad
+        first_in = x.data
+
+        def _backward(grad):
+            g = grad
+            for j in range(nl - 1, -1, -1):
+                lin = lins[j]
+                N, Kin = lin.out_features, lin.in_features
+                d = _lib.LinearDesc()
+                d.M, d.K, d.N, d.groups = B, Kin, N, 2
+                d.W, d.gW = lin.weight.data.ptr, S
+                d.dy, d.gy = g.ptr, B * N
+                d.ymask = acts[j].ptr if j < nl - 1 else None
+                if params:
+                    c0, c1 = self.layers[0][j], self.layers[1][j]
+                    (dw0, db0, dw1, db1), beta = grad_targets(c0.weight, c0.bias, c1.weight, c1.bias)
+                    if dw1.ptr - dw0.ptr != 4 * S or db1.ptr - db0.ptr != 4 * S:
+                        raise RuntimeError("TwinQ: critic gradients are not in the arena's gradient slots")
+                    if j == 0 and x2 is not None:
+                        raise ValueError("TwinQ: training the critics needs a dense obs_action input")
+                    xin = first_in if j == 0 else acts[j - 1]
+                    d.x, d.ldx = xin.ptr, Kin
+                    d.gx = 0 if j == 0 else B * Kin
+                    d.dW, d.db, d.gb = dw0.ptr, db0.ptr, S
+                    d.beta_w = beta
+                if j > 0:
+                    dx = DeviceArray(dev, (2, B, Kin))
+                    d.dx, d.lddx, d.gdx = dx.ptr, Kin, B * Kin
+                elif want_action:
+                    dx = DeviceArray(dev, (2, B, self.act_dim))
+                    d.dx, d.lddx, d.gdx = dx.ptr, self.act_dim, B * self.act_dim
+                    d.dx_col0, d.dx_cols = self.obs_dim, self.act_dim
+                else:
+                    dx = None
+                if d.dW or d.dx:
+                    dev.call("ttrl_linear_backward", C.byref(d))
+                g = dx
+            if want_action and g is not None:
+                g0 = g.view(0, (B, self.act_dim))
+                g1 = g.view(B * self.act_dim, (B, self.act_dim))
+                if hasattr(x2, "_accept_pair"):
+                    x2._accept_pair(g0, g1)
+                else:
+                    x2._accumulate(K.binary("add", g0, g1))
+
+        out._backward = _backward
+        return out
+
+
+# ---------------------------------------------------------------- losses ---
+
+def sac_critic_loss(q: Tensor, q_next_target: Tensor, logp_next: Tensor, log_alpha: Tensor, rewards: Tensor,
+                    dones: Tensor, discounts: Tensor, is_weights: Tensor | None = None):
+    """critic_loss of ttrl/algos/sac/losses.py:46-76 as one kernel.
+
+    -> (loss (1, 1) differentiable in q, metrics {q_target, td_abs, alpha})."""
+    B = int(q.shape[1])
+    dev = q.device
+    loss = DeviceArray(dev, (1, 1))
+    q_target = DeviceArray(dev, (B, 1))
+    dq = DeviceArray(dev, (2, B, 1))
+    td_abs = DeviceArray(dev, (B, 1))
+    alpha = DeviceArray(dev, (1, 1))
+    dev.call("ttrl_sac_critic_loss", B, q.data.vp, q_next_target.data.vp, logp_next.data.vp, log_alpha.data.vp,
+             rewards.data.vp, dones.data.vp, discounts.data.vp, None if is_weights is None else is_weights.data.vp,
+             loss.vp, q_target.vp, dq.vp, td_abs.vp, alpha.vp)
+    metrics = {"q_target": Tensor(q_target), "td_abs": Tensor(td_abs), "alpha": Tensor(alpha)}
+    if not _needs(q):
+        return Tensor(loss), metrics
+    out = Tensor(loss, True, (q,), "sac_critic_loss")
+
+    def _backward(grad):
+        q._accumulate(dq if grad.unit else K.binary("mul", dq, grad.reshape((1, 1, 1))))
+
+    out._backward = _backward
+    return out, metrics
+
+
+def sac_actor_losses(q_pi: Tensor, logp: Tensor, log_alpha: Tensor, target_entropy: float,
+                     learn_alpha: bool = True):
+    """actor_loss and alpha_loss (ttrl/algos/sac/losses.py:79-94) as one
+    kernel.  -> (actor_loss, alpha_loss | None), each (1, 1)."""
+    B = int(q_pi.shape[1])
+    dev = q_pi.device
+    la = DeviceArray(dev, (1, 1))
+    lalpha = DeviceArray(dev, (1, 1))
+    dq = DeviceArray(dev, (2, B, 1))
+    g_logp = DeviceArray(dev, (B, 1))
+    d_log_alpha = DeviceArray(dev, (1, 1))
+    dev.call("ttrl_sac_actor_loss", B, q_pi.data.vp, logp.data.vp, log_alpha.data.vp, C.c_float(target_entropy),
+             int(learn_alpha), la.vp, lalpha.vp, dq.vp, g_logp.vp, d_log_alpha.vp)
+    actor = Tensor(la)
+    if _needs(q_pi, logp):
+        actor = Tensor(la, True, (q_pi, logp), "sac_actor_loss")
+
+        def _backward(grad):
+            scale = None if grad.unit else grad.reshape((1, 1, 1))
+            if q_pi.requires_grad:
+                q_pi._accumulate(dq if scale is None else K.binary("mul", dq, scale))
+            if logp.requires_grad:
+                logp._accumulate(g_logp if scale is None else K.binary("mul", g_logp, scale.reshape((1, 1))))
+
+        actor._backward = _backward
+    alpha_loss = None
+    if learn_alpha:
+        alpha_loss = Tensor(lalpha)
+        if _needs(log_alpha):
+            alpha_loss = Tensor(lalpha, True, (log_alpha,), "sac_alpha_loss")
+
+            def _backward_alpha(grad):
+                log_alpha._accumulate(d_log_alpha if grad.unit else K.binary("mul", d_log_alpha, grad))
+
+            alpha_loss._backward = _backward_alpha
+    return actor, alpha_loss
+
+
+# --------------------------------------------------------------- learner ---
+
+def policy_packed(policy, obs: Tensor) -> Tensor:
+    """Policy forward to packed [mean | clamp(log_std)] rows."""
+    head = policy.head
+    if not isinstance(head, GaussianHead):
+        raise ValueError("SAC needs a GaussianHead policy")
+    return head.forward_packed(policy.encoder(obs))
+
+
+class _BatchBuffers:
+    """Bound device buffers of one SAC batch (allocated once, written in place)."""
+
+    def __init__(self, device, B, obs_dim, act_dim, prioritized):
+        def z(*shape):
+            return Tensor.from_numpy(np.zeros(shape, np.float32), device)
+
+        self.tensors = {
+            "obs": z(B, obs_dim), "next_obs": z(B, obs_dim), "actions": z(B, act_dim),
+            "obs_actions": z(B, obs_dim + act_dim), "rewards": z(B, 1), "dones": z(B, 1), "discounts": z(B, 1),
+            "noise": z(B, act_dim), "next_noise": z(B, act_dim),
+        }
+        if prioritized:
+            self.tensors["is_weights"] = Tensor.from_numpy(np.ones((B, 1), np.float32), device)
+        self.B = B
+
+    def __getitem__(self, key):
+        return self.tensors[key]
+
+    def load(self, name, array):
+        t = self.tensors[name]
+        t.data.upload(np.asarray(array, np.float32).reshape(t.shape))
+
+    def load_batch(self, batch: dict):
+        B = self.B
+        for name in ("obs", "next_obs", "actions", "noise", "next_noise"):
+            self.load(name, batch[name])
+        for name in ("rewards", "dones", "discounts"):
+            self.load(name, np.asarray(batch[name], np.float32).reshape(B, 1))
+        self.load("obs_actions", np.concatenate([np.asarray(batch["obs"], np.float32).reshape(B, -1),
+                                                 np.asarray(batch["actions"], np.float32).reshape(B, -1)], 1))
+        if "is_weights" in self.tensors:
+            w = batch.get("is_weights")
+            self.load("is_weights", np.ones((B, 1), np.float32) if w is None else w)
+
+
+class SACLearner:
+    """Policy, twin critics, targets, log_alpha, three Adams, one update."""
+
+    def __init__(self, obs_spec, action_spec, device, *, cfg: SACConfig = SACConfig(), seed: int | None = None):
+        if action_spec.kind != "continuous":
+            raise ValueError(f"SAC supports continuous actions only, got {action_spec.kind!r}")
+        self.cfg = cfg
+        self.device = device
+        self.obs_spec, self.action_spec = obs_spec, action_spec
+        if seed is not None:
+            np.random.seed(seed)
+        self.nets = build_sac_nets(obs_spec, action_spec, device, batch=cfg.batch_size,
+                                   critic_hidden=cfg.critic_hidden, encoder_kwargs={"hidden": cfg.policy_hidden})
+        with ParamArena(device, "log_alpha") as aa:
+            self.log_alpha = Tensor.from_numpy(np.full((1, 1), cfg.init_log_alpha, np.float32), device,
+                                               requires_grad=True)
+        self.alpha_arena = aa
+        self.target_entropy = (-float(action_spec.dim) if cfg.target_entropy is None else float(cfg.target_entropy))
+        self.scale = ActionScale(action_spec, device)
+        self.actor_opt = Adam(self.nets.policy_parameters(), lr=cfg.lr, eps=cfg.adam_eps)
+        self.critic_opt = Adam(self.nets.critic_parameters(), lr=cfg.lr, eps=cfg.adam_eps)
+        self.alpha_opt = Adam([self.log_alpha], lr=cfg.lr, eps=cfg.adam_eps)
+        self.twin = TwinQ(self.nets.critics)
+        self.twin_targets = TwinQ(self.nets.targets)
+        self.batch = _BatchBuffers(device, cfg.batch_size, obs_spec.size, action_spec.dim, cfg.prioritized)
+        self._graph = None
+        self._graph_metrics = None
+        self._pool = None
+        self.update_count = 0
+
+    # -- one update ----------------------------------------------------------
+
+    def _critic_region(self) -> dict:
+        b = self.batch
+        with no_grad():
+            head_n = policy_packed(self.nets.policy, b["next_obs"])
+            a_next, logp_next = squashed_sample(head_n, b["next_noise"], self.scale)
+            q_next = self.twin_targets.forward(b["next_obs"], a_next)
+        q = self.twin.forward(obs_action=b["obs_actions"])
+        loss, m = sac_critic_loss(q, q_next, logp_next, self.log_alpha, b["rewards"], b["dones"], b["discounts"],
+                                  b["is_weights"] if self.cfg.prioritized else None)
+        loss.backward()
+        out = {"critic_loss": loss, "alpha": m["alpha"], "q_target": m["q_target"]}
+        if self.cfg.prioritized:
+            out["td_abs"] = m["td_abs"]
+        return out
+
+    def _actor_region(self) -> dict:
+        b = self.batch
+        head = policy_packed(self.nets.policy, b["obs"])
+        action, logp = squashed_sample(head, b["noise"], self.scale)
+        q_pi = self.twin.forward(b["obs"], action, train_params=False)
+        actor, dual = sac_actor_losses(q_pi, logp, self.log_alpha, self.target_entropy, self.cfg.learn_alpha)
+        actor.backward()
+        out = {"actor_loss": actor, "logp": Tensor(logp.data)}
+        if dual is not None:
+            dual.backward()
+            out["alpha_loss"] = dual
+        return out
+
+    def _body(self) -> dict:
+        self.critic_opt.zero_grad()
+        self.actor_opt.zero_grad()
+        self.alpha_opt.zero_grad()
+        critic = self._critic_region()
+        self.critic_opt.step()
+        actor = self._actor_region()
+        self.actor_opt.step()
+        if self.cfg.learn_alpha:
+            self.alpha_opt.step()
+        self.device.call("ttrl_polyak", self.nets.targets.arena.data.vp, self.nets.critics.arena.data.vp,
+                         C.c_long(self.nets.targets.arena.numel), C.c_float(self.cfg.tau))
+        metrics = dict(critic)
+        metrics.update(actor)
+        metrics["critic_grad_sq"] = Tensor(self.critic_opt.grad_sq)
+        metrics["actor_grad_sq"] = Tensor(self.actor_opt.grad_sq)
+        return metrics
+
+    def _run(self) -> dict:
+        if self.cfg.step_mode == "eager":
+            return self._body()
+        dev = self.device
+        if self._graph is None:
+            # First update runs eagerly (warming the pool), then the body is
+            # captured; later updates replay it.
+            self._pool = dev.create_pool()
+            with dev.use_pool(self._pool):
+                metrics = self._body()
+                dev.synchronize()
+                self._graph, self._graph_metrics = capture(dev, self._body)
+            return metrics
+        self.replay()
+        return self._graph_metrics
+
+    def replay(self) -> None:
+        self._graph.replay()
+        for opt in (self.critic_opt, self.actor_opt) + ((self.alpha_opt,) if self.cfg.learn_alpha else ()):
+            opt._replayed()
+
+    def update(self, batch: dict | None = None) -> dict:
+        if batch is not None:
+            self.batch.load_batch(batch)
+        out = self._run()
+        self.update_count += 1
+        return self.summarize({k: v.numpy() if isinstance(v, Tensor) else v for k, v in out.items()})
+
+    def summarize(self, m: dict) -> dict:
+        """The reference's metric keys (ttrl/algos/sac/step.py:115-130)."""
+        def s(v):
+            return float(np.asarray(v).reshape(-1)[0])
+
+        out = {
+            "critic_loss": s(m["critic_loss"]),
+            "actor_loss": s(m["actor_loss"]),
+            "alpha_loss": s(m["alpha_loss"]) if self.cfg.learn_alpha else 0.0,
+            "alpha": s(m["alpha"]),
+            "entropy": float(-np.mean(np.asarray(m["logp"], np.float64))),
+            "mean_q_target": float(np.mean(np.asarray(m["q_target"], np.float64))),
+            "critic_grad_norm": float(np.sqrt(max(s(m["critic_grad_sq"]), 0.0))),
+            "actor_grad_norm": float(np.sqrt(max(s(m["actor_grad_sq"]), 0.0))),
+        }
+        out["q_target"] = np.asarray(m["q_target"]).reshape(-1)
+        out["logp"] = np.asarray(m["logp"]).reshape(-1)
+        if "td_abs" in m:
+            out["td_abs"] = np.asarray(m["td_abs"]).reshape(-1)
+        return out
+
+    def close(self) -> None:
+        if self._graph is not None:
+            self._graph.close()
+            self._graph = None
+            self._graph_metrics = None
+        if self._pool is not None and not self.device.closed:
+            self.device.release_pool(self._pool)
+            self._pool = None
