@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Learner-update throughput on one MI355X: DQN updates/s at batch 32 (the
+headline value) and SAC updates/s at batch 256, with roofline fractions and
+a CPU baseline timed on this machine's host cores.
+
+One step = one full learner update (forward, backward, Adam; for SAC also
+the temperature step and the Polyak blend) replayed as one hipGraph, on a
+fresh synthetic batch: a ring of distinct batches is resident in HBM and each
+step first copies the next one into the graph's bound input block (one
+device copy), so no step re-reads the previous step's inputs and no host
+transfer is timed.  Weights are seeded He-uniform; data is synthetic
+(uint8 Atari-shaped frames, Hopper-shaped vectors).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "tt-rl_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import numpy as np  # noqa: E402
+
+PEAK_FP32_MFMA = 157.3e12
+PEAK_HBM = 8.0e12
+
+# Multiply-accumulates per sample of the Nature CNN at 4x84x84 (conv1..3, fc1, fc2).
+NATURE_MACS = (20 * 20 * 32 * 4 * 64, 9 * 9 * 64 * 32 * 16, 7 * 7 * 64 * 64 * 9, 3136 * 512, 512 * 6)
+
+
+def dqn_update_flops(batch: int = 32) -> float:
+    """3 forwards + weight gradients of all layers + input gradients of all but conv1."""
+    fwd = sum(NATURE_MACS)
+    return 2.0 * batch * (3 * fwd + fwd + (fwd - NATURE_MACS[0]))
+
+
+def sac_update_flops(batch: int = 256) -> float:
+    pol = 11 * 256 + 256 * 256 + 2 * 256 * 3
+    crit = 14 * 256 + 256 * 256 + 256
+    crit_dw, crit_dx = crit, 256 * 256 + 256 + 3 * 256
+    critic_region = pol + 2 * crit + 2 * crit + 2 * (crit_dw + 256 * 256 + 256)
+    actor_region = pol + 2 * crit + 2 * crit_dx + pol + (pol - 11 * 256)
+    return 2.0 * batch * (critic_region + actor_region)
+
+
+def _ring(dev, block, fill, n):
+    from ttrl_amd.engine.tensor import DeviceArray
+
+    ring = []
+    for r in range(n):
+        fill(r)
+        slot = DeviceArray(dev, block.shape, np.uint8)
+        slot.copy_from(block)
+        ring.append(slot)
+    dev.synchronize()
+    return ring
+
+
+def _time_steps(dev, step, ring, block, steps, warmup):
+    for i in range(warmup):
+        block.copy_from(ring[i % len(ring)])
+        step()
+    dev.synchronize()
+    dev.call("ttrl_timer_start")
+    t0 = time.perf_counter()
+    for i in range(steps):
+        block.copy_from(ring[i % len(ring)])
+        step()
+    ms = C.c_float(0.0)
+    dev.call("ttrl_timer_stop", C.byref(ms))
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, ms.value / 1e3
+
+
+def bench_dqn(dev, steps, warmup, ring_n, mode="graph"):
+    from ttrl_amd.algos.dqn import DQNConfig, DQNLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import dqn_batch, he_uniform_qnet_state
+
+    cfg = DQNConfig(lr=6.25e-5, adam_eps=1.5e-4, batch_size=32, step_mode=mode, prioritized=True)
+    learner = DQNLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(6), dev, cfg=cfg, seed=0)
+    learner.online.load_state_dict(he_uniform_qnet_state(learner.online, 1))
+    learner.target.copy_from(learner.online)
+    block = learner.inputs["_block"]
+    ring = _ring(dev, block, lambda r: learner.load_batch(dqn_batch(1000 + r)), ring_n)
+    learner.update()  # captures the graph and runs the first update
+    step = learner.step.replay if mode == "graph" else learner.step.run
+    wall, gpu = _time_steps(dev, step, ring, block, steps, warmup)
+    nodes = learner.step._trace.nodes if mode == "graph" else 0
+    return learner, wall, gpu, nodes
+
+
+def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
+    from ttrl_amd.algos.sac import SACConfig, SACLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_sac_state, sac_batch
+
+    learner = SACLearner(ObsSpec.vector(11), ActionSpec.continuous(3), dev, cfg=SACConfig(batch_size=256, step_mode=mode), seed=0)
+    learner.nets.policy.load_state_dict(he_uniform_sac_state(learner.nets.policy, 2))
+    crit = he_uniform_sac_state(learner.nets.critics, 3)
+    learner.nets.critics.load_state_dict(crit)
+    learner.nets.targets.load_state_dict(crit)
+    block = learner.batch.block
+    ring = _ring(dev, block, lambda r: learner.batch.load_batch(sac_batch(2000 + r)), ring_n)
+    learner.update()  # eager first update
+    learner.update()  # captured graph, first replay
+    step = learner.replay if mode == "graph" else learner._run
+    wall, gpu = _time_steps(dev, step, ring, block, steps, warmup)
+    return learner, wall, gpu, (learner._graph.nodes if mode == "graph" else 0)
+
+
+def dominant_kernel(dev, learner, reps=200):
+    """The fc1 weight-gradient GEMM of the DQN update ([3136+1] x 512 from a
+    batch-32 reduction, bias gradient folded in), timed alone on the
+    library's stream with HIP events.  Algorithmic HBM bytes per launch:
+    read x (32x3136) and dZ, mask (32x512), write dW+db (3137x512)."""
+    from ttrl_amd import _lib
+    from ttrl_amd.engine.tensor import DeviceArray
+
+    fc1 = learner.online.encoder.layers[7]
+    M, K, N = 32, 3136, 512
+    x = DeviceArray(dev, (M, K))
+    x.fill(0.5)
+    dy = DeviceArray(dev, (M, N))
+    dy.fill(0.25)
+    dw = DeviceArray(dev, (K, N))
+    db = DeviceArray(dev, (N,))
+    d = _lib.LinearDesc()
+    d.M, d.K, d.N, d.groups = M, K, N, 1
+    d.x, d.ldx, d.W, d.dy, d.ymask = x.ptr, K, fc1.weight.data.ptr, dy.ptr, dy.ptr
+    d.dW, d.db = dw.ptr, db.ptr
+    for _ in range(10):
+        dev.call("ttrl_linear_backward", C.byref(d))
+    dev.synchronize()
+    ms = C.c_float(0.0)
+    dev.call("ttrl_timer_start")
+    for _ in range(reps):
+        dev.call("ttrl_linear_backward", C.byref(d))
+    dev.call("ttrl_timer_stop", C.byref(ms))
+    sec = ms.value / 1e3 / reps
+    algo_bytes = 4 * (M * K + 2 * M * N + (K + 1) * N)
+    return {"name": "linear_backward dW (fc1 3136x512, batch 32)", "seconds": sec, "bytes": algo_bytes,
+            "flops": 2.0 * M * (K + 1) * N}
+
+
+def cpu_baseline(seconds: float):
+    """The float64 numpy oracle of the same DQN update, on this host."""
+    from oracle.dqn import dqn_update
+    from oracle.nets import QNet
+    from ttrl_amd.workloads import dqn_batch
+
+    rng = np.random.default_rng(0)
+
+    def he(shape, fan):
+        b = np.sqrt(6.0 / fan)
+        return rng.uniform(-b, b, shape)
+
+    net = QNet([(he((32, 4, 8, 8), 256), he((32,), 256), 4, 0), (he((64, 32, 4, 4), 512), he((64,), 512), 2, 0),
+                (he((64, 64, 3, 3), 576), he((64,), 576), 1, 0)],
+               [(he((3136, 512), 3136), he((512,), 3136)), (he((512, 6), 512), he((6,), 512))])
+    target = net.copy()
+    batches = [dqn_batch(3000 + i) for i in range(4)]
+    dqn_update(net, target, batches[0])  # warm caches
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n < 2:
+        dqn_update(net, target, batches[n % 4])
+        n += 1
+    dt = time.perf_counter() - t0
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+    return {"value": n / dt, "unit": "DQN updates/s", "cores": min(threads, cores), "kind": "port",
+            "sample": f"{n} DQN updates (batch 32, 4x84x84 uint8) of the float64 numpy oracle in {dt:.1f} s",
+            "cpu": platform.processor() or platform.machine()}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--ring", type=int, default=32, help="distinct resident batches cycled through")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
+                    help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path; "
+              "replicas would shard as independent learners with a periodic parameter all-reduce.",
+              file=sys.stderr)
+        return 2
+    from ttrl_amd.engine.device import acquire
+
+    dev = acquire(0)
+    dqn, wall, gpu, nodes = bench_dqn(dev, args.steps, args.warmup, args.ring, args.mode)
+    value = args.steps / wall
+    flops = dqn_update_flops(32)
+    sac, swall, sgpu, snodes = bench_sac(dev, args.steps, args.warmup, args.ring, args.mode)
+    sac_value = args.steps / swall
+    sflops = sac_update_flops(256)
+    dom = dominant_kernel(dev, dqn)
+    achieved = dom["bytes"] / dom["seconds"]
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": "DQN updates/s @bs32, SAC updates/s @bs256 on 1 MI355X; % of roofline",
+        "value": round(value, 2),
+        "unit": "DQN updates/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded uint8 frames, resident in HBM, fresh batch per step)",
+        "mode": args.mode,
+        "config": {"workload": "DQN learner update: double DQN, n-step 3, PER weights, Nature-CNN 4x84x84 -> 6, "
+                               "Huber 1, Adam lr 6.25e-5 eps 1.5e-4", "batch": 32, "graph_nodes": nodes},
+        "update_roofline": {"flops_per_update": flops, "achieved_tflops": flops * value / 1e12,
+                            "frac": flops * value / PEAK_FP32_MFMA, "gpu_ms_per_step": gpu / args.steps * 1e3},
+        "sac": {"value": round(sac_value, 2), "unit": "SAC updates/s", "batch": 256,
+                "ms_per_step": round(swall / args.steps * 1e3, 5), "gpu_ms_per_step": sgpu / args.steps * 1e3,
+                "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA},
+        "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
+                     "avg_us": dom["seconds"] * 1e6},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    dqn.close()
+    sac.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

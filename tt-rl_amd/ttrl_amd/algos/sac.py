@@ -35,7 +35,7 @@ from ttrl_amd.engine.layers import Linear, ReLU
 from ttrl_amd.engine.ops import _kernels as K
 from ttrl_amd.engine.ops.fused import grad_targets
 from ttrl_amd.engine.optim import Adam
-from ttrl_amd.engine.tensor import DeviceArray, ParamArena
+from ttrl_amd.engine.tensor import DeviceArray, ParamArena, bound_block
 from ttrl_amd.engine.trace import capture
 from ttrl_amd.nets.build import build_sac_nets
 from ttrl_amd.nets.heads import GaussianHead
@@ -291,19 +291,20 @@ def policy_packed(policy, obs: Tensor) -> Tensor:
 
 
 class _BatchBuffers:
-    """Bound device buffers of one SAC batch (allocated once, written in place)."""
+    """Bound device buffers of one SAC batch, back to back in one block
+    (`block`), allocated once and written in place."""
 
     def __init__(self, device, B, obs_dim, act_dim, prioritized):
         def z(*shape):
-            return Tensor.from_numpy(np.zeros(shape, np.float32), device)
+            return np.zeros(shape, np.float32)
 
-        self.tensors = {
-            "obs": z(B, obs_dim), "next_obs": z(B, obs_dim), "actions": z(B, act_dim),
-            "obs_actions": z(B, obs_dim + act_dim), "rewards": z(B, 1), "dones": z(B, 1), "discounts": z(B, 1),
-            "noise": z(B, act_dim), "next_noise": z(B, act_dim),
-        }
+        specs = [("obs", z(B, obs_dim)), ("next_obs", z(B, obs_dim)), ("actions", z(B, act_dim)),
+                 ("obs_actions", z(B, obs_dim + act_dim)), ("rewards", z(B, 1)), ("dones", z(B, 1)),
+                 ("discounts", z(B, 1)), ("noise", z(B, act_dim)), ("next_noise", z(B, act_dim))]
         if prioritized:
-            self.tensors["is_weights"] = Tensor.from_numpy(np.ones((B, 1), np.float32), device)
+            specs.append(("is_weights", np.ones((B, 1), np.float32)))
+        arrays, self.block = bound_block(device, specs)
+        self.tensors = {name: Tensor(arr) for name, arr in arrays.items()}
         self.B = B
 
     def __getitem__(self, key):

@@ -22,7 +22,7 @@ import numpy as np
 from ttrl_amd.engine.device import Device
 
 __all__ = [
-    "DeviceArray", "MASTER_DTYPE", "ParamArena", "copy_in_place", "copy_tensor_in_place",
+    "DeviceArray", "MASTER_DTYPE", "ParamArena", "bound_block", "copy_in_place", "copy_tensor_in_place",
     "restore_in_place", "to_device", "to_host", "zeros",
 ]
 
@@ -160,6 +160,28 @@ def zeros(dev: Device, shape, dtype=np.float32) -> DeviceArray:
     else:
         out.fill(0)
     return out
+
+
+def bound_block(device: Device, specs):
+    """Input buffers laid out back to back in one allocation.
+
+    `specs` is a sequence of (name, host_array); each buffer starts on a
+    256-byte boundary.  Returns ({name: DeviceArray}, whole block as uint8),
+    so one device copy refreshes every input of a step.
+    """
+    layout, offset = [], 0
+    for name, arr in specs:
+        arr = np.ascontiguousarray(arr)
+        layout.append((name, arr, offset))
+        offset += int(math.ceil(max(arr.nbytes, 1) / 256.0)) * 256
+    block = _Block(device, max(offset, 256))
+    whole = DeviceArray(device, (max(offset, 256),), np.uint8, block=block)
+    out = {}
+    for name, arr, off in layout:
+        view = DeviceArray(device, arr.shape, arr.dtype, block=block, offset=off)
+        view.upload(arr)
+        out[name] = view
+    return out, whole
 
 
 def to_device(array, device: Device, dtype=np.float32, layout=None) -> DeviceArray:
