@@ -141,6 +141,12 @@ typedef struct ttrl_linear_desc {
 } ttrl_linear_desc;
 
 int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* desc);
+/* `groups` (<= 4) independent y[g] = x[g] @ W[g] + b[g] (+ReLU), each [M][K] @ [K][N],
+ * from pointer tables (b may be NULL): several networks' same-shaped layers in
+ * one launch, e.g. the online and target Q networks of one DQN update
+ * (ttrl/algos/dqn/losses.py:96-103).  No reference counterpart as one call. */
+int ttrl_linear_forward_multi(ttrl_ctx* ctx, int M, int K, int N, int groups, const float* const* x,
+                              const float* const* W, const float* const* b, float* const* y, int relu);
 int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* desc);
 
 /* ------------------------------------------------------- convolution --- */
@@ -163,6 +169,11 @@ int ttrl_conv_out_size(int size, int kernel, int stride, int padding, int* out);
  * (ttrl/engine/conv/forward.py:160-205, ttrl/engine/conv/module.py:257-263). */
 int ttrl_conv2d_forward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, const float* wt,
                         const float* bias, float* y, float x_scale, int relu);
+/* The same convolution geometry over `groups` (<= 4) input/weight/bias/output
+ * pointer tables in one launch (the online and target towers of a DQN update). */
+int ttrl_conv2d_forward_multi(ttrl_ctx* ctx, const ttrl_conv_geom* geom, int groups, const void* const* x,
+                              const float* const* wt, const float* const* bias, float* const* y, float x_scale,
+                              int relu);
 /* dWt = x_scale * sum over pixels of patch^T dZ, db = column sums of dZ,
  * dZ = dy * [ymask > 0].  Replaces weight_grad + dw_to_prepared
  * (ttrl/engine/conv/backward.py:45-78, ttrl/engine/conv/transform.py:232-254)

@@ -14,50 +14,60 @@ namespace ttrl {
 
 GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, int force_cfg, int force_splits) {
   static const int order[] = {T128x64, T64x128, T64x64, T128x32, T64x32, T32x64, T32x32};
-  GemmPlan p{T32x32, 32, 32, 1, 0};
   const int mfit = ((M + 31) / 32) * 32, nfit = ((N + 31) / 32) * 32;
-  bool chosen = false;
-  if (force_cfg >= 0) {
-    p.cfg = force_cfg;
-    chosen = true;
+  int cfg = -1;
+  if (force_cfg >= 0 && force_cfg < kNumCfg) {
+    cfg = force_cfg;
   } else {
-    for (int cfg : order) {
-      int bm, bn;
-      tile_dims(cfg, bm, bn);
-      if (bm > mfit || bn > nfit) continue;
-      const long tiles = long(ceil_div(M, bm)) * ceil_div(N, bn) * groups;
-      if (tiles >= 192) {
-        p.cfg = cfg;
-        chosen = true;
+    for (int c : order) {
+      const TileDims t = tile_dims(c);
+      if (t.bm > mfit || t.bn > nfit) continue;
+      const long tiles = long(ceil_div(M, t.bm)) * ceil_div(N, t.bn) * groups;
+      if (tiles >= 240) {
+        cfg = c;
         break;
       }
     }
-    if (!chosen) p.cfg = (nfit >= 64 && mfit <= 32) ? T32x64 : T32x32;
+    if (cfg < 0) cfg = (nfit >= 64 && mfit <= 32) ? T32x64 : T32x32;
   }
-  tile_dims(p.cfg, p.bm, p.bn);
-  const long tiles = long(ceil_div(M, p.bm)) * ceil_div(N, p.bn) * groups;
+  const TileDims t = tile_dims(cfg);
+  GemmPlan p{cfg, t.bm, t.bn, t.tbk, 1, t.tbk};
+  const long tiles = long(ceil_div(M, t.bm)) * ceil_div(N, t.bn) * groups;
+  const int stages = (K + t.tbk - 1) / t.tbk;  // LDS stages of the whole reduction
   int splits = 1;
   if (force_splits > 0) {
     splits = force_splits;
-  } else if (tiles < 128 && K >= 8 * TBK) {
-    splits = int((256 + tiles - 1) / tiles);
-    const int max_by_k = K / (4 * TBK);
-    if (splits > max_by_k) splits = max_by_k;
-    if (splits < 1) splits = 1;
+  } else if (stages > 1 && tiles < 160) {
+    // Too few workgroups to cover the chip: split K until ~480 are in flight.
+    const long want = (480 + tiles - 1) / tiles;
+    splits = int(want < stages ? want : stages);
+  } else if (stages > 4) {
+    // Enough workgroups, but long serial reductions: cap them at 4 stages.
+    splits = (stages + 3) / 4;
   }
   while (splits > 1 && long(splits) * groups * M * N > ws_floats) --splits;
-  int chunk = (K + splits - 1) / splits;
-  chunk = ((chunk + TBK - 1) / TBK) * TBK;
-  if (chunk <= 0) chunk = TBK;
-  p.splits = (K + chunk - 1) / chunk;
+  if (splits < 1) splits = 1;
+  const int stages_per = (stages + splits - 1) / splits;
+  p.kchunk = stages_per * t.tbk;
+  p.splits = (K + p.kchunk - 1) / p.kchunk;
   if (p.splits < 1) p.splits = 1;
-  p.kchunk = chunk;
   return p;
 }
 
 namespace {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <class T>
+inline void groups_of(T* (&dst)[kMaxGroups], T* base, long stride, int groups) {
+  fill_groups(dst, base, stride, groups);
+}
+
+inline bool all_aligned(const float* const (&p)[kMaxGroups], int groups) {
+  for (int g = 0; g < groups; ++g)
+    if (p[g] && !aligned16(p[g])) return false;
+  return true;
+}
 
 }  // namespace
 }  // namespace ttrl
@@ -73,151 +83,194 @@ int ttrl_matmul(ttrl_ctx* ctx, int M, int N, int K, const float* A, long lda, in
   EpStore ep;
   ep.M = M;
   ep.N = N;
-  ep.C = C;
+  ep.C[0] = C;
   ep.ldc = ldc;
-  ep.alpha = alpha;
+  ep.alpha = K == 0 ? 0.f : alpha;  // an empty reduction still defines C = beta*C
   ep.beta = beta;
-  if (K == 0) {
-    // An empty reduction still defines C = beta*C.
-    ep.alpha = 0.f;
-  }
-  const bool va = aligned16(A) && lda % 4 == 0, vb = aligned16(B) && ldb % 4 == 0;
   const int Kr = K > 0 ? K : 1;
   if (!ta && !tb) {
-    LdRowK la; la.p = A; la.ld = lda; la.rows = M; la.K = K; la.vec = va;
-    LdColK lb; lb.p = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec = vb;
+    LdRowK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
+    LdColK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
     return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   } else if (!ta && tb) {
-    LdRowK la; la.p = A; la.ld = lda; la.rows = M; la.K = K; la.vec = va;
-    LdRowK lb; lb.p = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec = vb;
+    LdRowK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
+    LdRowK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
     return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   } else if (ta && !tb) {
-    LdColK la; la.p = A; la.ld = lda; la.rows = M; la.K = K; la.vec = va;
-    LdColK lb; lb.p = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec = vb;
+    LdColK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
+    LdColK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
     return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   } else {
-    LdColK la; la.p = A; la.ld = lda; la.rows = M; la.K = K; la.vec = va;
-    LdRowK lb; lb.p = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec = vb;
+    LdColK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
+    LdRowK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
     return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   }
+}
+
+// Forward of `groups` linear layers given per-group pointer tables.
+static int linear_forward_tables(ttrl_ctx* ctx, int M, int K, int N, int groups, const float* const (&x)[kMaxGroups],
+                                 long ldx, const float* const (&x2)[kMaxGroups], long ldx2, int k1,
+                                 const float* const (&W)[kMaxGroups], const float* const (&b)[kMaxGroups],
+                                 const float* const (&W2)[kMaxGroups], const float* const (&b2)[kMaxGroups], int n1,
+                                 float* const (&y)[kMaxGroups], int relu, int clamp_col, float lo, float hi,
+                                 const char* name) {
+  const bool split_w = W2[0] != nullptr;
+  EpStore ep;
+  ep.M = M;
+  ep.N = N;
+  ep.ldc = N;
+  for (int g = 0; g < kMaxGroups; ++g) {
+    ep.C[g] = y[g];
+    ep.bias[g] = b[g];
+    if (split_w) {
+      ep.Cc[g] = y[g] ? y[g] + n1 : nullptr;  // same row-major [M][N] output, rebased column
+      ep.bias2[g] = b2[g];
+    }
+  }
+  if (split_w) {
+    ep.csplit = n1;
+    ep.ldcc = N;
+  }
+  ep.relu = relu;
+  ep.clamp_col = clamp_col > 0 ? clamp_col : (1 << 30);
+  ep.lo = lo;
+  ep.hi = hi;
+
+  LdColK lb;  // B(k, n) = W[k][n]
+  lb.ld = split_w ? n1 : N;
+  lb.rows = N;
+  lb.K = K;
+  for (int g = 0; g < kMaxGroups; ++g) {
+    lb.p[g] = W[g];
+    lb.p2[g] = W2[g];
+  }
+  lb.vec_ok(all_aligned(W, groups));
+  if (split_w) {
+    lb.ld2 = N - n1;
+    lb.split = n1;
+  }
+  if (x2[0]) {
+    LdRowKCat la;
+    for (int g = 0; g < kMaxGroups; ++g) {
+      la.p1[g] = x[g];
+      la.p2[g] = x2[g];
+    }
+    la.ld1 = ldx;
+    la.ld2 = ldx2;
+    la.rows = M;
+    la.k1 = k1;
+    la.K = K;
+    return run_gemm(ctx, la, lb, ep, M, N, K, groups, name);
+  }
+  LdRowK la;
+  for (int g = 0; g < kMaxGroups; ++g) la.p[g] = x[g];
+  la.ld = ldx;
+  la.rows = M;
+  la.K = K;
+  la.vec_ok(all_aligned(x, groups));
+  return run_gemm(ctx, la, lb, ep, M, N, K, groups, name);
 }
 
 int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
   TTRL_REQUIRE(ctx && d, "ttrl_linear_forward: null argument");
   TTRL_REQUIRE(d->x && d->W && d->y, "ttrl_linear_forward: x, W and y are required");
-  TTRL_REQUIRE(d->M >= 0 && d->K > 0 && d->N > 0 && d->groups >= 1, "ttrl_linear_forward: bad extents");
+  TTRL_REQUIRE(d->M >= 0 && d->K > 0 && d->N > 0 && d->groups >= 1 && d->groups <= kMaxGroups,
+               "ttrl_linear_forward: bad extents");
   const int n1 = d->W2 ? d->n1 : d->N;
   TTRL_REQUIRE(n1 > 0 && n1 <= d->N, "ttrl_linear_forward: n1 out of range");
   const int k1 = d->x2 ? d->k1 : d->K;
   TTRL_REQUIRE(k1 > 0 && k1 <= d->K, "ttrl_linear_forward: k1 out of range");
+  const float* x[kMaxGroups];
+  const float* x2[kMaxGroups];
+  const float* W[kMaxGroups];
+  const float* b[kMaxGroups];
+  const float* W2[kMaxGroups];
+  const float* b2[kMaxGroups];
+  float* y[kMaxGroups];
+  groups_of(x, d->x, d->gx, d->groups);
+  groups_of(x2, d->x2, d->gx2, d->groups);
+  groups_of(W, d->W, d->gW, d->groups);
+  groups_of(b, d->b, d->gb, d->groups);
+  groups_of(W2, d->W2, d->gW, d->groups);
+  groups_of(b2, d->b2, d->gb, d->groups);
+  groups_of(y, d->y, d->gy, d->groups);
+  return linear_forward_tables(ctx, d->M, d->K, d->N, d->groups, x, d->ldx, x2, d->ldx2, k1, W, b, W2, b2, n1, y,
+                               d->relu, d->clamp_col, d->lo, d->hi, "ttrl_linear_forward");
+}
 
-  EpStore ep;
-  ep.M = d->M;
-  ep.N = d->N;
-  ep.C = d->y;
-  ep.ldc = d->N;
-  ep.gC = d->gy;
-  ep.bias = d->b;
-  ep.gb = d->gb;
-  if (d->W2) {
-    ep.csplit = n1;
-    ep.Cc = d->y + n1;  // same row-major [M][N] output, rebased column
-    ep.ldcc = d->N;
-    ep.gCc = d->gy;
-    ep.bias2 = d->b2;
-    ep.gb2 = d->gb;
+int ttrl_linear_forward_multi(ttrl_ctx* ctx, int M, int K, int N, int groups, const float* const* x,
+                              const float* const* W, const float* const* b, float* const* y, int relu) {
+  TTRL_REQUIRE(ctx && x && W && y, "ttrl_linear_forward_multi: null argument");
+  TTRL_REQUIRE(M >= 0 && K > 0 && N > 0 && groups >= 1 && groups <= kMaxGroups,
+               "ttrl_linear_forward_multi: bad extents (at most %d groups)", kMaxGroups);
+  const float* xt[kMaxGroups] = {};
+  const float* none[kMaxGroups] = {};
+  const float* Wt[kMaxGroups] = {};
+  const float* bt[kMaxGroups] = {};
+  float* yt[kMaxGroups] = {};
+  for (int g = 0; g < groups; ++g) {
+    TTRL_REQUIRE(x[g] && W[g] && y[g], "ttrl_linear_forward_multi: null pointer in group %d", g);
+    xt[g] = x[g];
+    Wt[g] = W[g];
+    bt[g] = b ? b[g] : nullptr;
+    yt[g] = y[g];
   }
-  ep.relu = d->relu;
-  ep.clamp_col = d->clamp_col > 0 ? d->clamp_col : (1 << 30);
-  ep.lo = d->lo;
-  ep.hi = d->hi;
-
-  LdColK lb;  // B(k, n) = W[k][n]
-  lb.p = d->W;
-  lb.ld = n1;
-  lb.gs = d->gW;
-  lb.rows = d->N;
-  lb.K = d->K;
-  lb.vec = aligned16(d->W) && n1 % 4 == 0 && d->gW % 4 == 0;
-  if (d->W2) {
-    lb.p2 = d->W2;
-    lb.ld2 = d->N - n1;
-    lb.split = n1;
-  }
-  if (d->x2) {
-    LdRowKCat la;
-    la.p1 = d->x;
-    la.ld1 = d->ldx;
-    la.gs1 = d->gx;
-    la.p2 = d->x2;
-    la.ld2 = d->ldx2;
-    la.gs2 = d->gx2;
-    la.rows = d->M;
-    la.k1 = k1;
-    la.K = d->K;
-    return run_gemm(ctx, la, lb, ep, d->M, d->N, d->K, d->groups, "ttrl_linear_forward");
-  }
-  LdRowK la;
-  la.p = d->x;
-  la.ld = d->ldx;
-  la.gs = d->gx;
-  la.rows = d->M;
-  la.K = d->K;
-  la.vec = aligned16(d->x) && d->ldx % 4 == 0 && d->gx % 4 == 0;
-  return run_gemm(ctx, la, lb, ep, d->M, d->N, d->K, d->groups, "ttrl_linear_forward");
+  return linear_forward_tables(ctx, M, K, N, groups, xt, K, none, 0, K, Wt, bt, none, none, N, yt, relu, 0, 0.f,
+                               0.f, "ttrl_linear_forward_multi");
 }
 
 int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
   TTRL_REQUIRE(ctx && d, "ttrl_linear_backward: null argument");
   TTRL_REQUIRE(d->dy && d->W, "ttrl_linear_backward: dy and W are required");
-  TTRL_REQUIRE(d->M >= 0 && d->K > 0 && d->N > 0 && d->groups >= 1, "ttrl_linear_backward: bad extents");
+  TTRL_REQUIRE(d->M >= 0 && d->K > 0 && d->N > 0 && d->groups >= 1 && d->groups <= kMaxGroups,
+               "ttrl_linear_backward: bad extents");
+  const int G = d->groups;
   const int n1 = d->W2 ? d->n1 : d->N;
   TTRL_REQUIRE(n1 > 0 && n1 <= d->N, "ttrl_linear_backward: n1 out of range");
-  const bool dyvec = aligned16(d->dy) && d->N % 4 == 0 && d->gy % 4 == 0 &&
-                     (!d->ymask || aligned16(d->ymask));
+  const float* dy[kMaxGroups];
+  const float* ym[kMaxGroups];
+  groups_of(dy, d->dy, d->gy, G);
+  groups_of(ym, d->ymask, d->gy, G);
+  const bool dyal = all_aligned(dy, G) && all_aligned(ym, G);
 
   if (d->dW) {
     TTRL_REQUIRE(d->x && !d->x2, "ttrl_linear_backward: dW needs a single dense input x");
     TTRL_REQUIRE(!d->W2 || d->dW2, "ttrl_linear_backward: a split weight needs dW2");
     // dW_aug[k][n] = sum_m xaug[m][k] dZ[m][n], xaug = [x | 1]; row K is db.
     const bool with_b = d->db != nullptr;
+    TTRL_REQUIRE(!with_b || !d->W2 || d->db2, "ttrl_linear_backward: a split bias needs db2");
     LdColK la;  // A(r=k_in, k=m) = x[m][k_in]
-    la.p = d->x;
+    groups_of(la.p, d->x, d->gx, G);
     la.ld = d->ldx;
-    la.gs = d->gx;
     la.rows = with_b ? d->K + 1 : d->K;
     la.K = d->M;
     la.real_rows = d->K;
     la.ones = with_b;
-    la.vec = aligned16(d->x) && d->ldx % 4 == 0 && d->gx % 4 == 0;
+    la.vec_ok(all_aligned(la.p, G));
     LdColK lb;  // B(r=n, k=m) = dZ[m][n]
-    lb.p = d->dy;
+    for (int g = 0; g < kMaxGroups; ++g) {
+      lb.p[g] = dy[g];
+      lb.mask[g] = ym[g];
+    }
     lb.ld = d->N;
-    lb.gs = d->gy;
     lb.rows = d->N;
     lb.K = d->M;
-    lb.mask = d->ymask;
-    lb.vec = dyvec;
+    lb.vec_ok(dyal);
     EpStore ep;
     ep.M = la.rows;
     ep.N = d->N;
-    ep.C = d->dW;
+    groups_of(ep.C, d->dW, d->gW, G);
     ep.ldc = n1;
-    ep.gC = d->gW;
     ep.rsplit = d->K;
-    ep.Cr = d->db;
-    ep.gCr = d->gb;
+    groups_of(ep.Cr, d->db, d->gb, G);
     ep.beta = d->beta_w;
     if (d->W2) {
       ep.csplit = n1;
-      ep.Cc = d->dW2;
+      groups_of(ep.Cc, d->dW2, d->gW, G);
       ep.ldcc = d->N - n1;
-      ep.gCc = d->gW;
-      ep.Crc = d->db2;
-      ep.gCrc = d->gb;
-      TTRL_REQUIRE(!with_b || d->db2, "ttrl_linear_backward: a split bias needs db2");
+      groups_of(ep.Crc, d->db2, d->gb, G);
     }
-    int rc = run_gemm(ctx, la, lb, ep, la.rows, d->N, d->M > 0 ? d->M : 1, d->groups, "ttrl_linear_backward dW");
+    int rc = run_gemm(ctx, la, lb, ep, la.rows, d->N, d->M > 0 ? d->M : 1, G, "ttrl_linear_backward dW");
     if (rc) return rc;
   }
   if (d->dx) {
@@ -225,33 +278,38 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
     const int nc = d->dx_cols > 0 ? d->dx_cols : d->K;
     TTRL_REQUIRE(c0 >= 0 && c0 + nc <= d->K, "ttrl_linear_backward: dx column range out of bounds");
     LdRowK la;  // A(m, k=n) = dZ[m][n]
-    la.p = d->dy;
+    for (int g = 0; g < kMaxGroups; ++g) {
+      la.p[g] = dy[g];
+      la.mask[g] = ym[g];
+    }
     la.ld = d->N;
-    la.gs = d->gy;
     la.rows = d->M;
     la.K = d->N;
-    la.mask = d->ymask;
-    la.vec = dyvec;
+    la.vec_ok(dyal);
     EpStore ep;
     ep.M = d->M;
     ep.N = nc;
-    ep.C = d->dx;
+    groups_of(ep.C, d->dx, d->gdx, G);
     ep.ldc = d->lddx > 0 ? d->lddx : nc;
-    ep.gC = d->gdx;
     ep.beta = d->beta_x;
     if (d->W2) {
-      // B(r=k_in, k=n): n < n1 from W[k_in][n], else W2[k_in][n-n1].
-      LdRowK2 lb{d->W + long(c0) * n1, d->W2 + long(c0) * (d->N - n1), n1, d->N - n1, d->gW, nc, n1, d->N};
-      return run_gemm(ctx, la, lb, ep, d->M, nc, d->N, d->groups, "ttrl_linear_backward dx");
+      LdRowK2 lb;  // B(r=k_in, k=n): n < n1 from W[k_in][n], else W2[k_in][n-n1]
+      groups_of(lb.p1, d->W ? d->W + long(c0) * n1 : nullptr, d->gW, G);
+      groups_of(lb.p2, d->W2 + long(c0) * (d->N - n1), d->gW, G);
+      lb.ld1 = n1;
+      lb.ld2 = d->N - n1;
+      lb.rows = nc;
+      lb.k1 = n1;
+      lb.K = d->N;
+      return run_gemm(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx");
     }
     LdRowK lb;  // B(r=k_in, k=n) = W[k_in][n]
-    lb.p = d->W + long(c0) * d->N;
+    groups_of(lb.p, d->W + long(c0) * d->N, d->gW, G);
     lb.ld = d->N;
-    lb.gs = d->gW;
     lb.rows = nc;
     lb.K = d->N;
-    lb.vec = aligned16(lb.p) && d->N % 4 == 0 && d->gW % 4 == 0;
-    return run_gemm(ctx, la, lb, ep, d->M, nc, d->N, d->groups, "ttrl_linear_backward dx");
+    lb.vec_ok(all_aligned(lb.p, G));
+    return run_gemm(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx");
   }
   return TTRL_OK;
 }

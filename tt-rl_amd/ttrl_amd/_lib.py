@@ -96,8 +96,11 @@ SIGNATURES = {
     "ttrl_matmul": ([P, I, I, I, P, L, I, P, L, I, P, L, F, F], I),
     "ttrl_linear_forward": ([P, C.POINTER(LinearDesc)], I),
     "ttrl_linear_backward": ([P, C.POINTER(LinearDesc)], I),
+    "ttrl_linear_forward_multi": ([P, I, I, I, I, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P), I], I),
     "ttrl_conv_out_size": ([I, I, I, I, C.POINTER(I)], I),
     "ttrl_conv2d_forward": ([P, C.POINTER(ConvGeom), P, P, P, P, F, I], I),
+    "ttrl_conv2d_forward_multi": ([P, C.POINTER(ConvGeom), I, C.POINTER(P), C.POINTER(P), C.POINTER(P),
+                                   C.POINTER(P), F, I], I),
     "ttrl_conv2d_backward_weight": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, F], I),
     "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, F, F], I),
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
@@ -162,6 +165,12 @@ def check(rc: int, what: str = "") -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args), name)
+
+
+def ptrs(values) -> C.Array:
+    """A C array of void pointers (None for NULL)."""
+    values = [None if v is None else int(v) for v in values]
+    return (P * len(values))(*values)
 
 
 def longs(values) -> C.Array:

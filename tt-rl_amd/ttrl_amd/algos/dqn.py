@@ -17,14 +17,19 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import ctypes as C
+
 import numpy as np
 
+from ttrl_amd import _lib
 from ttrl_amd.algos.grads import grad_sq_device
 from ttrl_amd.engine.autograd import Tensor, no_grad
-from ttrl_amd.engine.ops.fused import dqn_td_loss
+from ttrl_amd.engine.conv import Conv2d
+from ttrl_amd.engine.layers import Linear, ReLU
+from ttrl_amd.engine.ops.fused import dqn_td_loss, linear_node
 from ttrl_amd.engine.optim import Adam
 from ttrl_amd.engine.step import TrainStep
-from ttrl_amd.engine.tensor import bound_block
+from ttrl_amd.engine.tensor import DeviceArray, bound_block
 from ttrl_amd.nets.build import build_q_net
 
 __all__ = ["DQNConfig", "DQNLearner", "leaf_key", "step_inputs", "update_loss"]
@@ -89,17 +94,91 @@ def step_inputs(obs_spec, device, *, batch: int, num_actions: int, mask_n: int =
     return inputs
 
 
+def _lockstep_layers(nets):
+    """Encoder layers + Q head of same-structured EncoderHead Q networks, or None."""
+    try:
+        stacks = [list(n.encoder.layers) + [n.head.q] for n in nets]
+    except AttributeError:
+        return None
+    first = stacks[0]
+    for st in stacks[1:]:
+        if len(st) != len(first) or any(type(a) is not type(b) for a, b in zip(st, first)):
+            return None
+    return stacks
+
+
+def q_forward_multi(nets, inputs, tape_group: int | None = 0):
+    """Q values of several same-shaped Q networks, one launch per layer.
+
+    `nets[g]` is applied to `inputs[g]`; the evaluations share each layer's
+    launch (per-group weight and activation pointers).  Only group
+    `tape_group` records a tape (the online network on s); every other group
+    is a constant of the step, as under no_grad in the reference.
+    """
+    stacks = _lockstep_layers(nets)
+    if stacks is None:
+        raise ValueError("q_forward_multi: the networks do not share one layer structure")
+    G = len(nets)
+    if G > 4:
+        raise ValueError("q_forward_multi: at most 4 networks per launch")
+    xs = list(inputs)
+    dev = xs[0].device
+    layers0 = stacks[0]
+    i = 0
+    while i < len(layers0):
+        layer = layers0[i]
+        fuse = i + 1 < len(layers0) and isinstance(layers0[i + 1], ReLU)
+        group = [st[i] for st in stacks]
+        if isinstance(layer, Conv2d):
+            batch = layer._check_input(xs[0])
+            for x, conv in zip(xs, group):
+                conv._check_input(x)
+            ys = [conv.out_array(dev) for conv in group]
+            dev.call("ttrl_conv2d_forward_multi", C.byref(layer._c_geom(batch)), G,
+                     _lib.ptrs(x.data.ptr for x in xs), _lib.ptrs(c.weight.data.ptr for c in group),
+                     _lib.ptrs(None if c.bias is None else c.bias.data.ptr for c in group),
+                     _lib.ptrs(y.ptr for y in ys), C.c_float(layer.input_scale), int(fuse))
+            xs = [group[g].node(xs[g], ys[g], fuse) if g == tape_group else Tensor(ys[g]) for g in range(G)]
+        elif isinstance(layer, Linear):
+            M, K = (int(d) for d in xs[0].shape)
+            N = layer.out_features
+            weights = [lin.effective_weight() for lin in group]
+            ys = [DeviceArray(dev, (M, N)) for _ in range(G)]
+            dev.call("ttrl_linear_forward_multi", M, K, N, G, _lib.ptrs(x.data.ptr for x in xs),
+                     _lib.ptrs(w.data.ptr for w in weights),
+                     _lib.ptrs(None if lin.bias is None else lin.bias.data.ptr for lin in group),
+                     _lib.ptrs(y.ptr for y in ys), int(fuse))
+            xs = [linear_node(xs[g], weights[g], group[g].bias, ys[g], relu=fuse) if g == tape_group
+                  else Tensor(ys[g]) for g in range(G)]
+        else:
+            xs = [group[g](xs[g]) for g in range(G)]  # Flatten: a view; only the taped group records
+            fuse = False
+        i += 2 if fuse else 1
+    return xs
+
+
 def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_n: int = 0, double: bool = True,
                 huber_delta: float = 1.0, prioritized: bool = False, grad_sq: bool = True) -> dict:
     """One DQN update body: Huber loss against the n-step double-Q target,
-    backward, metrics.  Reads only `inputs`; no host reads (capturable)."""
+    backward, metrics.  Reads only `inputs`; no host reads (capturable).
+
+    The online forward on s (with tape), the online forward on s' and the
+    target forward on s' (both constants of the step) run as one grouped
+    launch per layer."""
     (leaf,) = tuple(leaves)
     obs = inputs[leaf_key("obs", leaf)]
     next_obs = inputs[leaf_key("next_obs", leaf)]
-    q = online(obs)
-    with no_grad():
-        next_target_q = target(next_obs)
-        selector = online(next_obs) if double else next_target_q
+    if _lockstep_layers([online, target]) is not None:
+        if double:
+            q, selector, next_target_q = q_forward_multi([online, online, target], [obs, next_obs, next_obs])
+        else:
+            q, next_target_q = q_forward_multi([online, target], [obs, next_obs])
+            selector = next_target_q
+    else:
+        q = online(obs)
+        with no_grad():
+            next_target_q = target(next_obs)
+            selector = online(next_obs) if double else next_target_q
     loss, extra = dqn_td_loss(q, selector, next_target_q, inputs["actions_onehot"], inputs["rewards"],
                               inputs["dones"], inputs["discounts"],
                               inputs["is_weights"] if prioritized else None, huber_delta)

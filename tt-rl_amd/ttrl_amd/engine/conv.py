@@ -213,7 +213,8 @@ class Conv2d(Module):
     def forward(self, x: Tensor) -> Tensor:
         return self.forward_fused(x, relu=False)
 
-    def forward_fused(self, x: Tensor, relu: bool) -> Tensor:
+    def _check_input(self, x: Tensor) -> int:
+        """The activation batch, after validating dtype and geometry."""
         g = self.geom
         want_dtype = np.uint8 if self.input_layout == "nchw_u8" else np.float32
         if x.data.dtype != want_dtype:
@@ -231,20 +232,33 @@ class Conv2d(Module):
                 f"conv2d: activation holds batch {batch} but this layer's geometry {g} requires "
                 f"{g.batch}; build the layer for this batch or use at_batch()."
             )
+        return batch
+
+    def out_array(self, dev) -> DeviceArray:
+        g = self.geom
+        return DeviceArray(dev, (1, 1, g.batch * g.out_h * g.out_w, g.out_channels))
+
+    def forward_fused(self, x: Tensor, relu: bool) -> Tensor:
+        batch = self._check_input(x)
         cg = self._c_geom(batch)
         dev = x.device
-        rows = batch * g.out_h * g.out_w
-        y = DeviceArray(dev, (1, 1, rows, g.out_channels))
+        y = self.out_array(dev)
         bias = self.bias
         dev.call("ttrl_conv2d_forward", C.byref(cg), x.data.vp, self.weight.data.vp,
                  None if bias is None else bias.data.vp, y.vp, C.c_float(self.input_scale), int(relu))
-        weight = self.weight
+        return self.node(x, y, relu)
+
+    def node(self, x: Tensor, y: DeviceArray, relu: bool) -> Tensor:
+        """The tape node of this layer's output `y` = conv(x) (+ReLU), computed elsewhere."""
+        weight, bias = self.weight, self.bias
         needs = is_grad_enabled() and (x.requires_grad or weight.requires_grad or
                                        (bias is not None and bias.requires_grad))
         parents = (x, weight) + ((bias,) if bias is not None else ())
         out = Tensor(y, needs, parents if needs else (), "conv2d_relu" if relu else "conv2d")
         if not needs:
             return out
+        cg = self._c_geom(self.geom.batch)
+        dev = x.device
         x_data, w_data = x.data, weight.data
         scale = self.input_scale
         layer_has_dx = self.needs_input_grad
@@ -257,30 +271,25 @@ class Conv2d(Module):
                     "Rebuild the layer with needs_input_grad=True, or detach "
                     "the activation it is given."
                 )
+            mask = y.vp if relu else None
             (dw, db), beta_w = grad_targets(weight, bias)
-            if dw is not None or db is not None:
-                if dw is None:
-                    dw_tmp = DeviceArray(dev, w_data.shape)
-                    beta_use = 0.0
-                    dw_ptr = dw_tmp.vp
-                    if db is not None and beta_w:
-                        # keep a mixed request simple: compute both fresh, then add the bias part
-                        db_tmp = DeviceArray(dev, db.shape)
-                        dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale),
-                                 grad.vp, y.vp if relu else None, dw_ptr, db_tmp.vp, C.c_float(0.0))
-                        from ttrl_amd.engine.ops import _kernels as Kk
-                        Kk.binary_into("add", db, db_tmp, db)
-                    else:
-                        dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale),
-                                 grad.vp, y.vp if relu else None, dw_ptr, None if db is None else db.vp,
-                                 C.c_float(beta_use))
+            if dw is not None:
+                dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp, mask,
+                         dw.vp, None if db is None else db.vp, C.c_float(beta_w))
+            elif db is not None:
+                dw_tmp = DeviceArray(dev, w_data.shape)
+                db_tmp = DeviceArray(dev, db.shape)
+                dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp, mask,
+                         dw_tmp.vp, db_tmp.vp, C.c_float(0.0))
+                from ttrl_amd.engine.ops import _kernels as Kk
+                if beta_w:
+                    Kk.binary_into("add", db, db_tmp, db)
                 else:
-                    dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp,
-                             y.vp if relu else None, dw.vp, None if db is None else db.vp, C.c_float(beta_w))
+                    db.copy_from(db_tmp)
             if x.requires_grad:
                 (dx,), beta_x = grad_targets(x)
-                dev.call("ttrl_conv2d_backward_input", C.byref(cg), grad.vp, y.vp if relu else None, w_data.vp,
-                         dx.vp, C.c_float(scale), C.c_float(beta_x))
+                dev.call("ttrl_conv2d_backward_input", C.byref(cg), grad.vp, mask, w_data.vp, dx.vp,
+                         C.c_float(scale), C.c_float(beta_x))
 
         out._backward = _backward
         return out

@@ -16,7 +16,7 @@ from ttrl_amd import _lib
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs
 from ttrl_amd.engine.tensor import DeviceArray
 
-__all__ = ["linear", "dqn_td_loss", "grad_targets"]
+__all__ = ["linear", "linear_node", "dqn_td_loss", "grad_targets"]
 
 
 def _p(arr) -> int | None:
@@ -63,8 +63,16 @@ def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None, *, relu: bool 
     d.y = y.ptr
     d.relu = int(relu)
     dev.call("ttrl_linear_forward", C.byref(d))
+    return linear_node(x, weight, bias, y, relu=relu)
+
+
+def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, *, relu: bool) -> Tensor:
+    """The tape node of y = x @ W + b (+ReLU), with y computed elsewhere."""
     if not _needs(x, weight, bias):
         return _detached(y)
+    M, K = (int(dim) for dim in x.shape)
+    N = int(weight.shape[1])
+    dev = x.device
     parents = (x, weight) + ((bias,) if bias is not None else ())
     out = Tensor(y, True, parents, "linear_relu" if relu else "linear")
     x_data, w_data = x.data, weight.data
