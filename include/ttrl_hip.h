@@ -106,8 +106,11 @@ int ttrl_matmul(ttrl_ctx* ctx, int M, int N, int K, const float* A, long lda, in
  * Backward: dZ = dy * [ymask > 0] when ymask is given (relu_bw), then
  * dW = x^T dZ with db = column sums of dZ folded in as an implicit ones row
  * (ttrl/engine/ops/broadcast.py:11-30), and dx = dZ W^T restricted to input
- * columns [dx_col0, dx_col0 + dx_cols) when dx_cols > 0.  beta_* = 1
- * accumulates into existing gradients (ttrl/engine/autograd.py:106-114). */
+ * columns [dx_col0, dx_col0 + dx_cols) when dx_cols > 0.  dxmask, laid out
+ * like dx, multiplies dx by [dxmask > 0] as it is written: the relu_bw of
+ * the layer below applied in this epilogue, so that layer's backward needs
+ * no ymask.  beta_* = 1 accumulates into existing gradients
+ * (ttrl/engine/autograd.py:106-114). */
 typedef struct ttrl_linear_desc {
   int M, K, N;
   int groups;
@@ -138,6 +141,7 @@ typedef struct ttrl_linear_desc {
   long lddx, gdx;
   int dx_col0, dx_cols;
   float beta_w, beta_x;
+  const float* dxmask;
 } ttrl_linear_desc;
 
 int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* desc);
@@ -180,11 +184,13 @@ int ttrl_conv2d_forward_multi(ttrl_ctx* ctx, const ttrl_conv_geom* geom, int gro
  * and the conv bias-gradient sum (ttrl/engine/ops/broadcast.py:11-30). */
 int ttrl_conv2d_backward_weight(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale,
                                 const float* dy, const float* ymask, float* dwt, float* db, float beta);
-/* dx = x_scale * conv_transpose(dZ, W) for fp32 NHWC inputs.  Replaces
+/* dx = x_scale * conv_transpose(dZ, W) for fp32 NHWC inputs, times
+ * [xmask > 0] when xmask (laid out like dx: the ReLU output that fed this
+ * layer) is given, so the layer below needs no ymask.  Replaces
  * input_grad / transpose_weight / conv_transpose2d
  * (ttrl/engine/conv/backward.py:33-42, ttrl/engine/conv/transform.py:71-129). */
 int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const float* dy, const float* ymask,
-                               const float* wt, float* dx, float x_scale, float beta);
+                               const float* wt, float* dx, const float* xmask, float x_scale, float beta);
 
 /* ---------------------------------------------------------- loss heads --- */
 

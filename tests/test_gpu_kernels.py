@@ -64,6 +64,16 @@ def test_linear_forward_backward(device):
     assert _rel(dW_.numpy(), x.T.astype(np.float64) @ dz) < 1e-5
     assert _rel(db_.numpy(), dz.sum(0)) < 1e-5
     assert _rel(dx_.numpy(), dz @ W.T.astype(np.float64)) < 1e-5
+    # The gate of the layer below applied as dx is written (dxmask), with the
+    # already-gated dZ passed in and no ymask: same dW, dx * [x > 0].
+    dzd = _dev_arr(device, dz.astype(np.float32))
+    f = _lib.LinearDesc()
+    f.M, f.K, f.N, f.groups = M, K, N, 1
+    f.x, f.ldx, f.W, f.dy, f.dxmask = xd.ptr, K, Wd.ptr, dzd.ptr, xd.ptr
+    dx2 = DeviceArray(device, (M, K))
+    f.dx, f.lddx = dx2.ptr, K
+    device.call("ttrl_linear_backward", C.byref(f))
+    assert _rel(dx2.numpy(), (dz @ W.T.astype(np.float64)) * (x > 0)) < 1e-5
 
 
 @pytest.mark.parametrize("case", [
@@ -117,9 +127,15 @@ def test_conv_forward_and_gradients(device, case):
     assert _rel(db_.numpy(), db_ref) < 2e-5
     if not u8:
         dx_ = DeviceArray(device, (B, H, W, Cc))
-        device.call("ttrl_conv2d_backward_input", C.byref(g), dyd.vp, y.vp, wd.vp, dx_.vp, C.c_float(1.0),
+        device.call("ttrl_conv2d_backward_input", C.byref(g), dyd.vp, y.vp, wd.vp, dx_.vp, None, C.c_float(1.0),
                     C.c_float(0.0))
         assert _rel(dx_.numpy(), dx_ref) < 2e-5
+        # Pre-gated dZ, no ymask, and the input's own ReLU gate fused into the write.
+        dzd = _dev_arr(device, dz.astype(np.float32))
+        dx2 = DeviceArray(device, (B, H, W, Cc))
+        device.call("ttrl_conv2d_backward_input", C.byref(g), dzd.vp, None, wd.vp, dx2.vp, xd.vp, C.c_float(1.0),
+                    C.c_float(0.0))
+        assert _rel(dx2.numpy(), dx_ref * (x_nhwc > 0)) < 2e-5
 
 
 def test_adam_step_matches_fused_oracle_over_steps(device):

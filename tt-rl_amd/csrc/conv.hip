@@ -29,11 +29,15 @@
 
 namespace ttrl {
 
+// Tile shapes each convolution GEMM may use (each one is a separate kernel).
+constexpr unsigned kConvFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32) | cfg_bit(T64x64);
+constexpr unsigned kConvDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64);
+constexpr unsigned kConvDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32);
 
 struct ConvGeo {
   int B, C, H, W, O, KH, KW, S, P, OH, OW, u8;
   int M;                           // B * OH * OW
-  FDiv d_ohow, d_ow, d_c, d_kw, d_khkw, d_o, d_tw;
+  FDiv d_ohow, d_ow, d_c, d_kw, d_khkw, d_o, d_tw, d_s;
   int TH, TW;                      // taps per class along h and w: ceil(K / S)
   // The input gradient's residue classes cls0 .. cls0+3 (one launch), by group.
   int cls0;
@@ -63,96 +67,140 @@ struct ConvGeo {
   }
 };
 
-// Patch elements of output pixel m at patch index k (zero outside the image).
-struct ConvPatch {
-  ConvGeo g;
-  const void* x[kMaxGroups];
+// Patch element (m, k) of the input: element offset, or -1 outside the image.
+__device__ inline long patch_index(const ConvGeo& g, int m, int k) {
+  if (m >= g.M || k >= g.kp()) return -1;
+  int b, oh, ow, c, kh, kw;
+  g.split_m(m, b, oh, ow);
+  g.split_k(k, c, kh, kw);
+  const int ih = oh * g.S + kh - g.P, iw = ow * g.S + kw - g.P;
+  if (ih < 0 || ih >= g.H || iw < 0 || iw >= g.W) return -1;
+  if (g.u8) return ((long(b) * g.C + c) * g.H + ih) * g.W + iw;
+  return ((long(b) * g.H + ih) * g.W + iw) * g.C + c;
+}
 
-  // Element index of (m, k) in the input, or -1 outside the image.
-  __device__ inline long index(int m, int k) const {
-    if (m >= g.M || k >= g.kp()) return -1;
-    int b, oh, ow, c, kh, kw;
-    g.split_m(m, b, oh, ow);
-    g.split_k(k, c, kh, kw);
-    const int ih = oh * g.S + kh - g.P, iw = ow * g.S + kw - g.P;
-    if (ih < 0 || ih >= g.H || iw < 0 || iw >= g.W) return -1;
-    if (g.u8) return ((long(b) * g.C + c) * g.H + ih) * g.W + iw;
-    return ((long(b) * g.H + ih) * g.W + iw) * g.C + c;
-  }
-  // Issue the loads of patch indices k..k+3 (k % 4 == 0) of pixel m.
-  __device__ inline void issue4(int m, int k, int grp, Fetch4& f) const {
-    f.m = f32x4{1.f, 1.f, 1.f, 1.f};
-    if (m < g.M && k < g.kp()) {
-      int b, oh, ow, c, kh, kw;
-      g.split_m(m, b, oh, ow);
-      g.split_k(k, c, kh, kw);
-      const int ih = oh * g.S + kh - g.P, iw = ow * g.S + kw - g.P;
-      if (g.u8) {
-        // k..k+3 are kw..kw+3 of one kernel row when KW % 4 == 0.
-        if ((g.KW & 3) == 0 && ((g.W & 3) == 0) && ((iw & 3) == 0) && k + 3 < g.kp()) {
-          const bool in = ih >= 0 && ih < g.H && iw >= 0 && iw + 3 < g.W;
-          const long i = in ? ((long(b) * g.C + c) * g.H + ih) * g.W + iw : 0;
-          f.v.x = __uint_as_float(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(x[grp]) + i));
-          f.ok = in ? (0xFu | kU8Word) : 0u;
-          return;
-        }
-      } else if ((g.C & 3) == 0 && k + 3 < g.kp()) {
-        // k..k+3 are channels c..c+3 of one tap.
-        const bool in = ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
-        const long i = in ? ((long(b) * g.H + ih) * g.W + iw) * g.C + c : 0;
-        f.v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x[grp]) + i);
-        f.ok = in ? 0xFu : 0u;
-        return;
-      }
-    }
-    f.ok = g.u8 ? kU8Each : 0u;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const long idx = index(m, k + j);
-      const long i = idx < 0 ? 0 : idx;
-      if (g.u8) f.v[j] = __uint_as_float(uint32_t(static_cast<const uint8_t*>(x[grp])[i]));
-      else f.v[j] = static_cast<const float*>(x[grp])[i];
-      f.ok |= uint32_t(idx >= 0) << j;
-    }
-  }
+// One patch element, any layout (the general path).
+__device__ inline float patch_elem(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int m, int k) {
+  const long idx = patch_index(g, m, k);
+  if (g.u8) return __uint_as_float(ld_u8(rs, idx < 0 ? kOob : uint32_t(idx)));
+  return ld_f1(rs, idx < 0 ? kOob : uint32_t(idx) * 4u);
+}
+
+// How four consecutive patch indices k..k+3 (k % 4 == 0) lie in memory.
+enum PatchMode {
+  kPatchNhwcVec = 0,  // fp32 NHWC, C % 4 == 0: four channels of one tap, one 16-byte load
+  kPatchU8Word = 1,   // uint8 NCHW, KW, W, S, P multiples of 4: four kw of one row, one aligned word
+  kPatchGeneral = 2,  // element by element
 };
+
+__host__ inline int patch_mode(const ConvGeo& g, bool aligned) {
+  if (!g.u8 && g.C % 4 == 0 && aligned) return kPatchNhwcVec;
+  if (g.u8 && g.KW % 4 == 0 && g.W % 4 == 0 && g.S % 4 == 0 && g.P % 4 == 0 && aligned) return kPatchU8Word;
+  return kPatchGeneral;
+}
+
+// Output pixel m as an input position: element offset of (b, ih0, iw0) and
+// ih0 = oh*S - P, iw0 = ow*S - P (ih0 far below zero for m past the end).
+struct PixelPos {
+  int base, ih0, iw0;
+};
+__device__ inline PixelPos pixel_pos(const ConvGeo& g, int m) {
+  if (m >= g.M) return PixelPos{0, -(1 << 28), 0};
+  int b, oh, ow;
+  g.split_m(m, b, oh, ow);
+  const int ih0 = oh * g.S - g.P, iw0 = ow * g.S - g.P;
+  const int base = g.u8 ? (b * g.C * g.H + ih0) * g.W + iw0 : ((b * g.H + ih0) * g.W + iw0) * g.C;
+  return PixelPos{base, ih0, iw0};
+}
+
+// Patch chunk k..k+3 as a tap: element offset relative to the pixel base
+// and (kh, kw) of its first element.
+struct TapPos {
+  int off, kh, kw;
+  bool v;  // k < C*KH*KW
+};
+__device__ inline TapPos tap_pos(const ConvGeo& g, int k) {
+  if (k >= g.kp()) return TapPos{0, 0, 0, false};
+  int c, kh, kw;
+  g.split_k(k, c, kh, kw);
+  const int off = g.u8 ? (c * g.H + kh) * g.W + kw : (kh * g.W + kw) * g.C + c;
+  return TapPos{off, kh, kw, true};
+}
+
+// Starts the load of patch chunk (pixel, tap) in the given mode.
+__device__ inline void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int mode, const PixelPos& px,
+                                   const TapPos& tp, Fetch4& f) {
+  const int ih = px.ih0 + tp.kh, iw = px.iw0 + tp.kw;
+  const bool hv = tp.v && ih >= 0 && ih < g.H;
+  if (mode == kPatchNhwcVec) {
+    const bool in = hv && iw >= 0 && iw < g.W;
+    f.v = ld_f4(rs, in ? uint32_t(px.base + tp.off) * 4u : kOob);
+  } else {  // kPatchU8Word
+    const bool in = hv && iw >= 0 && iw + 3 < g.W;
+    f.v.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, in ? uint32_t(px.base + tp.off) : kOob, 0, 0));
+  }
+}
 
 // Forward A operand: A(m, k) = patch(m, k).
 struct LdConvFwd {
   static constexpr bool KCONTIG = true;
-  ConvPatch p;
-  __device__ inline bool masked(int) const { return false; }
-  __device__ inline void issue(int r, int k, int grp, Fetch4& f) const { p.issue4(r, k, grp, f); }
+  ConvGeo g;
+  const void* x[kMaxGroups];
+  uint32_t xbytes;
+  int mode;
+  struct Row { PixelPos px; };  // the general mode keeps the pixel index in px.base
+  struct Kp { TapPos tp; int k; };
+  __device__ inline int fmt() const {
+    return mode == kPatchU8Word ? kU8Word : (mode == kPatchGeneral && g.u8 ? kU8Each : kF32);
+  }
+  __device__ inline __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
+  __device__ inline Row row(int m, int) const {
+    return mode == kPatchGeneral ? Row{PixelPos{m, 0, 0}} : Row{pixel_pos(g, m)};
+  }
+  __device__ inline Kp kpos(int k, int) const { return Kp{mode == kPatchGeneral ? TapPos{} : tap_pos(g, k), k}; }
+  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
+    if (mode != kPatchGeneral) {
+      patch_issue(rs, g, mode, r.px, kp.tp, f);
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, g, r.px.base, kp.k + j);
+  }
 };
 
 // Weight-gradient A operand: A(r = k, k = m) = patch(m, r), with the ones row
 // at r == kp when the bias gradient is wanted.
 struct LdConvPatchT {
   static constexpr bool KCONTIG = false;
-  ConvPatch p;
+  ConvGeo g;
+  const void* x[kMaxGroups];
+  uint32_t xbytes;
+  int mode;
   int ones;
-  __device__ inline bool masked(int) const { return false; }
-  __device__ inline void issue(int r, int m, int grp, Fetch4& f) const {
-    const int kp = p.g.kp();
-    if (r + 3 < kp) {
-      p.issue4(m, r, grp, f);
+  struct Row { TapPos tp; int r; bool whole; };
+  __device__ inline int fmt() const {
+    return mode == kPatchU8Word ? kU8Word : (g.u8 ? kU8Each : kF32);
+  }
+  __device__ inline __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
+  __device__ inline Row row(int r, int) const {
+    const bool whole = mode != kPatchGeneral && r + 3 < g.kp();
+    return Row{whole ? tap_pos(g, r) : TapPos{}, r, whole};
+  }
+  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, int m, Fetch4& f) const {
+    if (r.whole) {
+      patch_issue(rs, g, mode, pixel_pos(g, m), r.tp, f);
       return;
     }
-    // The tail chunk: patch rows, then the ones row, then nothing.
-    f.m = f32x4{1.f, 1.f, 1.f, 1.f};
-    f.ok = 0;
-    const bool mv = m < p.g.M;
+    // The general path and the tail chunk: patch rows, then the ones row.
+    const int kp = g.kp();
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int rr = r + j;
+      const int rr = r.r + j;
       if (rr < kp) {
-        const long idx = mv ? p.index(m, rr) : -1;
-        const long i = idx < 0 ? 0 : idx;
-        f.v[j] = p.g.u8 ? float(static_cast<const uint8_t*>(p.x[grp])[i]) : static_cast<const float*>(p.x[grp])[i];
-        f.ok |= uint32_t(idx >= 0) << j;
+        f.v[j] = patch_elem(rs, g, m, rr);
       } else {
-        f.v[j] = (ones && rr == kp) ? 1.f : 0.f;
-        f.ok |= uint32_t(mv) << j;
+        const float one = (ones && rr == kp && m < g.M) ? 1.f : 0.f;
+        f.v[j] = g.u8 ? __uint_as_float(uint32_t(one)) : one;
       }
     }
   }
@@ -160,51 +208,55 @@ struct LdConvPatchT {
 
 // Input-gradient A operand of class `cls`: A(r, k = (jh, jw, o)) = dZ at the
 // output pixel that tap (kh, kw) = (ch + s*jh, cw + s*jw) connects to input
-// pixel r; dZ = dY * [Y > 0] when a mask is given.
+// pixel r: oh = ohc(r) - jh, ow = owc(r) - jw with ohc = (ih + p - ch) / s.
 struct LdConvDxA {
   static constexpr bool KCONTIG = true;
   ConvGeo g;
   const float* dy;
-  const float* ymask;
-  // dZ element index, or -1 when the tap or the output pixel falls outside.
-  __device__ inline long index(int r, int k, int grp) const {
-    const int cls = g.cls0 + grp;
-    const int rows = g.B * g.nh[grp] * g.nw[grp];
-    if (r >= rows || k >= g.TH * g.TW * g.O) return -1;
+  uint32_t dybytes;
+  struct Row { int base, ohc, owc; };  // base = element offset of dZ(b, ohc, owc, 0)
+  struct Kp { int off, jh, jw; bool v; int k, ch, cw; };
+  __device__ inline int fmt() const { return kF32; }
+  __device__ inline __amdgpu_buffer_rsrc_t res(int) const { return make_res(dy, dybytes); }
+  __device__ inline int cls(int grp) const { return g.cls0 + grp; }
+  __device__ inline Row row(int r, int grp) const {
+    if (r >= g.B * g.nh[grp] * g.nw[grp]) return Row{0, -(1 << 28), 0};
     const int b = g.d_nhnw[grp].div(r);
     const int rem = r - b * g.nh[grp] * g.nw[grp];
     const int i = g.d_nw[grp].div(rem), j = rem - i * g.nw[grp];
-    const int ch = cls / g.S, cw = cls - ch * g.S;
-    const int ih = g.ih0[grp] + g.S * i, iw = g.iw0[grp] + g.S * j;
+    const int c = cls(grp), ch = c / g.S, cw = c - ch * g.S;
+    const int ohc = g.d_s.div(g.ih0[grp] + g.S * i + g.P - ch);
+    const int owc = g.d_s.div(g.iw0[grp] + g.S * j + g.P - cw);
+    return Row{((b * g.OH + ohc) * g.OW + owc) * g.O, ohc, owc};
+  }
+  __device__ inline Kp kpos(int k, int grp) const {
+    const int c = cls(grp), ch = c / g.S, cw = c - ch * g.S;
+    if (k >= g.TH * g.TW * g.O) return Kp{0, 0, 0, false, k, ch, cw};
     const int jt = g.d_o.div(k), o = k - jt * g.O;
     const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
-    const int kh = ch + g.S * jh, kw = cw + g.S * jw;
-    if (kh >= g.KH || kw >= g.KW) return -1;
-    const int th = ih + g.P - kh, tw = iw + g.P - kw;
-    if (th < 0 || tw < 0) return -1;
-    const int oh = th / g.S, ow = tw / g.S;
-    if (oh >= g.OH || ow >= g.OW) return -1;
-    return ((long(b) * g.OH + oh) * g.OW + ow) * g.O + o;
+    const bool v = ch + g.S * jh < g.KH && cw + g.S * jw < g.KW;
+    return Kp{o - (jh * g.OW + jw) * g.O, jh, jw, v, k, ch, cw};
   }
-  __device__ inline bool masked(int) const { return ymask != nullptr; }
-  __device__ inline void issue(int r, int k, int grp, Fetch4& f) const {
-    if ((g.O & 3) == 0) {
-      // k % 4 == 0 and O % 4 == 0: the four k share one tap and output pixel.
-      const long idx = index(r, k, grp);
-      const long i = idx < 0 ? 0 : idx;
-      f.v = *reinterpret_cast<const f32x4*>(dy + i);
-      if (ymask) f.m = *reinterpret_cast<const f32x4*>(ymask + i);
-      f.ok = idx >= 0 ? 0xFu : 0u;
+  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
+    if ((g.O & 3) == 0) {  // the four k share one tap and output pixel
+      const int oh = r.ohc - kp.jh, ow = r.owc - kp.jw;
+      const bool in = kp.v && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
+      f.v = ld_f4(rs, in ? uint32_t(r.base + kp.off) * 4u : kOob);
       return;
     }
-    f.ok = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const long idx = index(r, k + j, grp);
-      const long i = idx < 0 ? 0 : idx;
-      f.v[j] = dy[i];
-      f.m[j] = ymask ? ymask[i] : 1.f;
-      f.ok |= uint32_t(idx >= 0) << j;
+      const int k = kp.k + j;
+      bool in = k < g.TH * g.TW * g.O;
+      int off = 0;
+      if (in) {
+        const int jt = g.d_o.div(k), o = k - jt * g.O;
+        const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
+        const int oh = r.ohc - jh, ow = r.owc - jw;
+        in = kp.ch + g.S * jh < g.KH && kp.cw + g.S * jw < g.KW && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
+        off = r.base - (jh * g.OW + jw) * g.O + o;
+      }
+      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kOob);
     }
   }
 };
@@ -215,38 +267,49 @@ struct LdConvDxB {
   static constexpr bool KCONTIG = true;
   ConvGeo g;
   const float* wt;
-  __device__ inline long index(int c, int k, int grp) const {
-    const int cls = g.cls0 + grp;
-    if (c >= g.C || k >= g.TH * g.TW * g.O) return -1;
-    const int ch = cls / g.S, cw = cls - ch * g.S;
+  uint32_t wbytes;
+  struct Row { int off; bool v; };
+  struct Kp { int off; bool v; int k, ch, cw; };
+  __device__ inline int fmt() const { return kF32; }
+  __device__ inline __amdgpu_buffer_rsrc_t res(int) const { return make_res(wt, wbytes); }
+  __device__ inline Row row(int c, int) const { return Row{c * g.O, c < g.C}; }
+  __device__ inline Kp kpos(int k, int grp) const {
+    const int c = g.cls0 + grp, ch = c / g.S, cw = c - ch * g.S;
+    if (k >= g.TH * g.TW * g.O) return Kp{0, false, k, ch, cw};
     const int jt = g.d_o.div(k), o = k - jt * g.O;
     const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
     const int kh = ch + g.S * jh, kw = cw + g.S * jw;
-    if (kh >= g.KH || kw >= g.KW) return -1;
-    return ((long(kh) * g.KW + kw) * g.C + c) * g.O + o;
+    const bool v = kh < g.KH && kw < g.KW;
+    return Kp{(kh * g.KW + kw) * g.C * g.O + o, v, k, ch, cw};
   }
-  __device__ inline bool masked(int) const { return false; }
-  __device__ inline void issue(int c, int k, int grp, Fetch4& f) const {
+  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
     if ((g.O & 3) == 0) {
-      const long idx = index(c, k, grp);
-      f.v = *reinterpret_cast<const f32x4*>(wt + (idx < 0 ? 0 : idx));
-      f.ok = idx >= 0 ? 0xFu : 0u;
+      f.v = ld_f4(rs, (r.v && kp.v) ? uint32_t(r.off + kp.off) * 4u : kOob);
       return;
     }
-    f.ok = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const long idx = index(c, k + j, grp);
-      f.v[j] = wt[idx < 0 ? 0 : idx];
-      f.ok |= uint32_t(idx >= 0) << j;
+      const int k = kp.k + j;
+      bool in = r.v && k < g.TH * g.TW * g.O;
+      int off = 0;
+      if (in) {
+        const int jt = g.d_o.div(k), o = k - jt * g.O;
+        const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
+        const int kh = kp.ch + g.S * jh, kw = kp.cw + g.S * jw;
+        in = kh < g.KH && kw < g.KW;
+        off = r.off + (kh * g.KW + kw) * g.C * g.O + o;
+      }
+      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kOob);
     }
   }
 };
 
-// Input-gradient epilogue: class row r -> NHWC input pixel.
+// Input-gradient epilogue: class row r -> NHWC input pixel, times
+// [xmask > 0] when the input was a ReLU output.
 struct EpConvDx {
   ConvGeo g;
   float* dx;
+  const float* xmask;
   float alpha, beta;
   __device__ inline int rows(int grp) const { return g.B * g.nh[grp] * g.nw[grp]; }
   __device__ inline void store(int r, int c, float acc, int grp) const {
@@ -255,8 +318,10 @@ struct EpConvDx {
     const int rem = r - b * g.nh[grp] * g.nw[grp];
     const int i = g.d_nw[grp].div(rem), j = rem - i * g.nw[grp];
     const int ih = g.ih0[grp] + g.S * i, iw = g.iw0[grp] + g.S * j;
-    float* dst = dx + ((long(b) * g.H + ih) * g.W + iw) * g.C + c;
+    const long idx = ((long(b) * g.H + ih) * g.W + iw) * g.C + c;
+    float* dst = dx + idx;
     float v = alpha * acc;
+    if (xmask && !(xmask[idx] > 0.f)) v = 0.f;
     if (beta != 0.f) v += beta * *dst;
     *dst = v;
   }
@@ -308,8 +373,10 @@ int make_geo(const ttrl_conv_geom* s, ConvGeo& g) {
   g.OW = span_w / s->stride + 1;
   g.u8 = s->in_layout == TTRL_LAYOUT_NCHW_U8 ? 1 : 0;
   g.M = g.B * g.OH * g.OW;
-  const long bigs[] = {long(g.B) * g.OH * g.OW, long(g.B) * g.H * g.W * g.C, long(g.C) * g.KH * g.KW * g.O};
-  for (long v : bigs) TTRL_REQUIRE(v < (1L << 31), "conv: extent %ld exceeds 2^31", v);
+  // Buffer loads address operands with 32-bit byte offsets.
+  const long bigs[] = {long(g.B) * g.OH * g.OW * g.O * 4, long(g.B) * g.H * g.W * g.C * (g.u8 ? 1 : 4),
+                       long(g.C) * g.KH * g.KW * g.O * 4};
+  for (long v : bigs) TTRL_REQUIRE(v < (1L << 31), "conv: an operand of %ld bytes exceeds 2^31", v);
   g.d_ohow.set(g.OH * g.OW);
   g.d_ow.set(g.OW);
   g.d_c.set(g.C);
@@ -319,19 +386,28 @@ int make_geo(const ttrl_conv_geom* s, ConvGeo& g) {
   g.TH = (g.KH + g.S - 1) / g.S;
   g.TW = (g.KW + g.S - 1) / g.S;
   g.d_tw.set(g.TW);
+  g.d_s.set(g.S);
   set_classes(g, 0);
   return TTRL_OK;
+}
+
+inline uint32_t input_bytes(const ConvGeo& g) { return uint32_t(long(g.B) * g.H * g.W * g.C * (g.u8 ? 1 : 4)); }
+
+inline bool input_aligned(const ConvGeo& g, const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & (g.u8 ? 3 : 15)) == 0;
 }
 
 int conv_forward(ttrl_ctx* ctx, const ConvGeo& g, int groups, const void* const* x, const float* const* wt,
                  const float* const* bias, float* const* y, float x_scale, int relu, const char* name) {
   const int K = g.C * g.KH * g.KW;
-  LdConvFwd la{ConvPatch{g, {}}};
+  LdConvFwd la{g, {}, input_bytes(g), kPatchGeneral};
   LdColK lb;  // B(k, n=o) = Wt[k][o]
   EpStore ep;
+  bool xal = true;
   for (int i = 0; i < groups; ++i) {
     TTRL_REQUIRE(x[i] && wt[i] && y[i], "%s: null pointer in group %d", name, i);
-    la.p.x[i] = x[i];
+    xal = xal && input_aligned(g, x[i]);
+    la.x[i] = x[i];
     lb.p[i] = wt[i];
     ep.C[i] = y[i];
     ep.bias[i] = bias ? bias[i] : nullptr;
@@ -342,12 +418,13 @@ int conv_forward(ttrl_ctx* ctx, const ConvGeo& g, int groups, const void* const*
   bool al = true;
   for (int i = 0; i < groups; ++i) al = al && (reinterpret_cast<uintptr_t>(wt[i]) & 15) == 0;
   lb.vec_ok(al);
+  la.mode = patch_mode(g, xal);
   ep.M = g.M;
   ep.N = g.O;
   ep.ldc = g.O;
   ep.alpha = x_scale;
   ep.relu = relu;
-  return run_gemm(ctx, la, lb, ep, g.M, g.O, K, groups, name);
+  return run_gemm<kConvFwdCfgs>(ctx, la, lb, ep, g.M, g.O, K, groups, name);
 }
 
 }  // namespace
@@ -399,14 +476,18 @@ int ttrl_conv2d_backward_weight(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const
   int rc = make_geo(geom, g);
   if (rc) return rc;
   const int Kp = g.C * g.KH * g.KW;
-  LdConvPatchT la{ConvPatch{g, {x}}, db ? 1 : 0};
+  long reserved = 0;
+  if (ymask) {
+    dy = relu_mask_into_workspace(ctx, dy, ymask, long(g.M) * g.O, 0, 1, &reserved, &rc);
+    if (rc) return rc;
+  }
+  LdConvPatchT la{g, {x}, input_bytes(g), patch_mode(g, input_aligned(g, x)), db ? 1 : 0};
   LdColK lb;  // B(r=o, k=m) = dZ[m][o]
   lb.p[0] = dy;
-  lb.mask[0] = ymask;
   lb.ld = g.O;
   lb.rows = g.O;
   lb.K = g.M;
-  lb.vec_ok(((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(ymask)) & 15) == 0);
+  lb.vec_ok((reinterpret_cast<uintptr_t>(dy) & 15) == 0);
   EpStore ep;
   ep.M = db ? Kp + 1 : Kp;
   ep.N = g.O;
@@ -417,16 +498,21 @@ int ttrl_conv2d_backward_weight(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const
   ep.alpha = x_scale;  // d/dW of conv(s*x, W) = s * dW(x, dY); the bias row is unscaled
   ep.alpha_r = 1.f;
   ep.beta = beta;
-  return run_gemm(ctx, la, lb, ep, ep.M, g.O, g.M, 1, "ttrl_conv2d_backward_weight");
+  return run_gemm<kConvDwCfgs>(ctx, la, lb, ep, ep.M, g.O, g.M, 1, "ttrl_conv2d_backward_weight", reserved);
 }
 
 int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const float* dy, const float* ymask,
-                               const float* wt, float* dx, float x_scale, float beta) {
+                               const float* wt, float* dx, const float* xmask, float x_scale, float beta) {
   TTRL_REQUIRE(ctx && dy && wt && dx, "ttrl_conv2d_backward_input: null argument");
   ConvGeo g;
   int rc = make_geo(geom, g);
   if (rc) return rc;
   TTRL_REQUIRE(!g.u8, "ttrl_conv2d_backward_input: a uint8 frame input has no gradient");
+  long reserved = 0;
+  if (ymask) {
+    dy = relu_mask_into_workspace(ctx, dy, ymask, long(g.M) * g.O, 0, 1, &reserved, &rc);
+    if (rc) return rc;
+  }
   const int Kd = g.TH * g.TW * g.O;
   const int classes = g.S * g.S;
   // One launch covers up to kMaxGroups residue classes; the largest class
@@ -435,10 +521,10 @@ int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const 
   for (int c0 = 0; c0 < classes; c0 += kMaxGroups) {
     const int n = std::min(kMaxGroups, classes - c0);
     set_classes(g, c0);
-    LdConvDxA la{g, dy, ymask};
-    LdConvDxB lb{g, wt};
-    EpConvDx ep{g, dx, x_scale, beta};
-    rc = run_gemm(ctx, la, lb, ep, Mmax, g.C, Kd, n, "ttrl_conv2d_backward_input");
+    LdConvDxA la{g, dy, uint32_t(long(g.M) * g.O * 4)};
+    LdConvDxB lb{g, wt, uint32_t(long(g.C) * g.KH * g.KW * g.O * 4)};
+    EpConvDx ep{g, dx, xmask, x_scale, beta};
+    rc = run_gemm<kConvDxCfgs>(ctx, la, lb, ep, Mmax, g.C, Kd, n, "ttrl_conv2d_backward_input", reserved);
     if (rc) return rc;
   }
   return TTRL_OK;

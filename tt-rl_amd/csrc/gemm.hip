@@ -10,51 +10,77 @@
 //   log_std clamp         ttrl/nets/heads.py:65-93, ttrl/engine/ops/select.py:52-63
 #include "tile_gemm.hpp"
 
+#include <algorithm>
+#include <cmath>
+
 namespace ttrl {
 
-GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, int force_cfg, int force_splits) {
-  static const int order[] = {T128x64, T64x128, T64x64, T128x32, T64x32, T32x64, T32x32};
-  const int mfit = ((M + 31) / 32) * 32, nfit = ((N + 31) / 32) * 32;
-  int cfg = -1;
-  if (force_cfg >= 0 && force_cfg < kNumCfg) {
-    cfg = force_cfg;
-  } else {
-    for (int c : order) {
-      const TileDims t = tile_dims(c);
-      if (t.bm > mfit || t.bn > nfit) continue;
-      const long tiles = long(ceil_div(M, t.bm)) * ceil_div(N, t.bn) * groups;
-      if (tiles >= 240) {
-        cfg = c;
-        break;
+GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, unsigned allowed) {
+  // Cost model in shader cycles, per candidate tile and split-K factor:
+  //   rounds * (latency + stages_per_block * blocks_per_cu * max(mfma, fetch))
+  //   + a reduction pass when K is split,
+  // with mfma = 32 cycles per 16x16x4 MFMA of one wavefront (the FP32 MFMA
+  // issue interval), fetch = stage bytes at 64 B/cycle per CU, and the
+  // workgroups a CU holds limited by LDS (160 KiB) and registers (two).
+  constexpr double kLatency = 2500.0, kReduceFixed = 4000.0, kCus = 256.0;
+  GemmPlan best{T32x32, 32, 32, 256, 1, 256};
+  double best_t = 1e300;
+  for (int c = 0; c < kNumCfg; ++c) {
+    if (!(allowed & (1u << c))) continue;
+    const TileDims t = tile_dims(c);
+    const long tiles = long(ceil_div(M, t.bm)) * ceil_div(N, t.bn) * groups;
+    const int stages = std::max(1, (K + t.tbk - 1) / t.tbk);
+    const double lds = 4.0 * (t.bm + t.bn) * (t.tbk + 4);
+    const double bpc = std::max(1.0, std::min(2.0, std::floor(160.0 * 1024.0 / lds)));
+    const double mfma = double(t.bm / t.wgm / 16) * (t.bn / t.wgn / 16) * (t.tbk / 4) * 32.0;
+    const double fetch = 4.0 * (t.bm + t.bn) * t.tbk / 64.0;
+    const int smax = std::max(1, stages);
+    for (int sp = 1; sp <= smax; ++sp) {
+      const int spb = (stages + sp - 1) / sp;
+      const int real = (stages + spb - 1) / spb;  // splits that own a stage
+      if (real != sp) continue;
+      if (sp > 1 && long(sp) * groups * M * N > ws_floats) break;
+      const double blocks = double(tiles) * sp;
+      const double per_cu = std::min(bpc, std::ceil(blocks / kCus));
+      const double rounds = std::ceil(blocks / (kCus * bpc));
+      double tt = rounds * (kLatency + spb * per_cu * std::max(mfma, fetch));
+      if (sp > 1) tt += kReduceFixed + double(groups) * M * N * sp * 4.0 / (kCus * 32.0);
+      if (tt < best_t) {
+        best_t = tt;
+        best = GemmPlan{c, t.bm, t.bn, t.tbk, sp, spb * t.tbk};
       }
     }
-    if (cfg < 0) cfg = (nfit >= 64 && mfit <= 32) ? T32x64 : T32x32;
   }
-  const TileDims t = tile_dims(cfg);
-  GemmPlan p{cfg, t.bm, t.bn, t.tbk, 1, t.tbk};
-  const long tiles = long(ceil_div(M, t.bm)) * ceil_div(N, t.bn) * groups;
-  const int stages = (K + t.tbk - 1) / t.tbk;  // LDS stages of the whole reduction
-  int splits = 1;
-  if (force_splits > 0) {
-    splits = force_splits;
-  } else if (stages > 1 && tiles < 160) {
-    // Too few workgroups to cover the chip: split K until ~480 are in flight.
-    const long want = (480 + tiles - 1) / tiles;
-    splits = int(want < stages ? want : stages);
-  } else if (stages > 4) {
-    // Enough workgroups, but long serial reductions: cap them at 4 stages.
-    splits = (stages + 3) / 4;
-  }
-  while (splits > 1 && long(splits) * groups * M * N > ws_floats) --splits;
-  if (splits < 1) splits = 1;
-  const int stages_per = (stages + splits - 1) / splits;
-  p.kchunk = stages_per * t.tbk;
-  p.splits = (K + p.kchunk - 1) / p.kchunk;
-  if (p.splits < 1) p.splits = 1;
-  return p;
+  return best;
 }
 
+const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const float* mask, long n, long gs,
+                                      int groups, long* reserved, int* rc);
+
 namespace {
+
+constexpr unsigned kMatmulCfgs = cfg_bit(T32x32) | cfg_bit(T64x64) | cfg_bit(T128x64);
+constexpr unsigned kLinFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64);
+constexpr unsigned kLinDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
+                                cfg_bit(T128x64);
+constexpr unsigned kLinDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64);
+
+__global__ __launch_bounds__(256) void k_relu_mask(float* dst, const float* src, const float* mask, long n, long gs,
+                                                   int groups) {
+  const long total = n * groups;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += long(gridDim.x) * 256) {
+    const long g = i / n, j = i - g * n;
+    const long s = g * gs + j;
+    dst[i] = mask[s] > 0.f ? src[s] : 0.f;
+  }
+}
+
+// Buffer loads address an operand with 32-bit byte offsets.
+inline bool fits(const LdRowK& l) { return l.bytes() < (1L << 31); }
+inline bool fits(const LdColK& l) { return l.bytes() < (1L << 31) && l.bytes2() < (1L << 31); }
+inline bool fits(const LdRowKCat& l) { return l.bytes1() < (1L << 31) && l.bytes2() < (1L << 31); }
+#define TTRL_FITS(la, lb, name) \
+  TTRL_REQUIRE(fits(la) && fits(lb), "%s: an operand of 2^31 bytes or more is not supported", name)
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -70,6 +96,26 @@ inline bool all_aligned(const float* const (&p)[kMaxGroups], int groups) {
 }
 
 }  // namespace
+
+const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const float* mask, long n, long gs,
+                                      int groups, long* reserved, int* rc) {
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  const long need = (n * groups + 63) / 64 * 64;
+  if (need + *reserved > wsf / 2) {
+    *rc = set_error(TTRL_ENOMEM, "relu mask: %ld floats exceed half of the %ld-float workspace", need, wsf);
+    return nullptr;
+  }
+  float* dst = ws + wsf - *reserved - need;
+  *reserved += need;
+  const long total = n * groups;
+  unsigned blocks = unsigned(std::min<long>(4096, (total + 255) / 256));
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(k_relu_mask, dim3(blocks), dim3(256), 0, stream_of(ctx), dst, src, mask, n, gs, groups);
+  *rc = check_launch("relu mask");
+  return dst;
+}
+
 }  // namespace ttrl
 
 using namespace ttrl;
@@ -91,19 +137,23 @@ int ttrl_matmul(ttrl_ctx* ctx, int M, int N, int K, const float* A, long lda, in
   if (!ta && !tb) {
     LdRowK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
     LdColK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
-    return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
+    TTRL_FITS(la, lb, "ttrl_matmul");
+    return run_gemm<kMatmulCfgs>(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   } else if (!ta && tb) {
     LdRowK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
     LdRowK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
-    return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
+    TTRL_FITS(la, lb, "ttrl_matmul");
+    return run_gemm<kMatmulCfgs>(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   } else if (ta && !tb) {
     LdColK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
     LdColK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
-    return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
+    TTRL_FITS(la, lb, "ttrl_matmul");
+    return run_gemm<kMatmulCfgs>(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   } else {
     LdColK la; la.p[0] = A; la.ld = lda; la.rows = M; la.K = K; la.vec_ok(aligned16(A));
     LdRowK lb; lb.p[0] = B; lb.ld = ldb; lb.rows = N; lb.K = K; lb.vec_ok(aligned16(B));
-    return run_gemm(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
+    TTRL_FITS(la, lb, "ttrl_matmul");
+    return run_gemm<kMatmulCfgs>(ctx, la, lb, ep, M, N, Kr, 1, "ttrl_matmul");
   }
 }
 
@@ -160,7 +210,8 @@ static int linear_forward_tables(ttrl_ctx* ctx, int M, int K, int N, int groups,
     la.rows = M;
     la.k1 = k1;
     la.K = K;
-    return run_gemm(ctx, la, lb, ep, M, N, K, groups, name);
+    TTRL_FITS(la, lb, name);
+    return run_gemm<kLinFwdCfgs>(ctx, la, lb, ep, M, N, K, groups, name);
   }
   LdRowK la;
   for (int g = 0; g < kMaxGroups; ++g) la.p[g] = x[g];
@@ -168,7 +219,8 @@ static int linear_forward_tables(ttrl_ctx* ctx, int M, int K, int N, int groups,
   la.rows = M;
   la.K = K;
   la.vec_ok(all_aligned(x, groups));
-  return run_gemm(ctx, la, lb, ep, M, N, K, groups, name);
+  TTRL_FITS(la, lb, name);
+    return run_gemm<kLinFwdCfgs>(ctx, la, lb, ep, M, N, K, groups, name);
 }
 
 int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
@@ -228,10 +280,17 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
   const int n1 = d->W2 ? d->n1 : d->N;
   TTRL_REQUIRE(n1 > 0 && n1 <= d->N, "ttrl_linear_backward: n1 out of range");
   const float* dy[kMaxGroups];
-  const float* ym[kMaxGroups];
   groups_of(dy, d->dy, d->gy, G);
-  groups_of(ym, d->ymask, d->gy, G);
-  const bool dyal = all_aligned(dy, G) && all_aligned(ym, G);
+  long reserved = 0;
+  if (d->ymask) {
+    // dZ = dy * [ymask > 0] once, densely, for both products below.
+    int rc = TTRL_OK;
+    const long n = long(d->M) * d->N;
+    const float* dz = relu_mask_into_workspace(ctx, d->dy, d->ymask, n, d->gy, G, &reserved, &rc);
+    if (rc) return rc;
+    groups_of(dy, dz, n, G);
+  }
+  const bool dyal = all_aligned(dy, G);
 
   if (d->dW) {
     TTRL_REQUIRE(d->x && !d->x2, "ttrl_linear_backward: dW needs a single dense input x");
@@ -248,10 +307,7 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
     la.ones = with_b;
     la.vec_ok(all_aligned(la.p, G));
     LdColK lb;  // B(r=n, k=m) = dZ[m][n]
-    for (int g = 0; g < kMaxGroups; ++g) {
-      lb.p[g] = dy[g];
-      lb.mask[g] = ym[g];
-    }
+    for (int g = 0; g < kMaxGroups; ++g) lb.p[g] = dy[g];
     lb.ld = d->N;
     lb.rows = d->N;
     lb.K = d->M;
@@ -270,7 +326,9 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
       ep.ldcc = d->N - n1;
       groups_of(ep.Crc, d->db2, d->gb, G);
     }
-    int rc = run_gemm(ctx, la, lb, ep, la.rows, d->N, d->M > 0 ? d->M : 1, G, "ttrl_linear_backward dW");
+    TTRL_FITS(la, lb, "ttrl_linear_backward");
+    int rc = run_gemm<kLinDwCfgs>(ctx, la, lb, ep, la.rows, d->N, d->M > 0 ? d->M : 1, G, "ttrl_linear_backward dW",
+                                  reserved);
     if (rc) return rc;
   }
   if (d->dx) {
@@ -278,10 +336,7 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
     const int nc = d->dx_cols > 0 ? d->dx_cols : d->K;
     TTRL_REQUIRE(c0 >= 0 && c0 + nc <= d->K, "ttrl_linear_backward: dx column range out of bounds");
     LdRowK la;  // A(m, k=n) = dZ[m][n]
-    for (int g = 0; g < kMaxGroups; ++g) {
-      la.p[g] = dy[g];
-      la.mask[g] = ym[g];
-    }
+    for (int g = 0; g < kMaxGroups; ++g) la.p[g] = dy[g];
     la.ld = d->N;
     la.rows = d->M;
     la.K = d->N;
@@ -290,10 +345,11 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
     ep.M = d->M;
     ep.N = nc;
     groups_of(ep.C, d->dx, d->gdx, G);
+    groups_of(ep.mask, d->dxmask, d->gdx, G);
     ep.ldc = d->lddx > 0 ? d->lddx : nc;
     ep.beta = d->beta_x;
     if (d->W2) {
-      LdRowK2 lb;  // B(r=k_in, k=n): n < n1 from W[k_in][n], else W2[k_in][n-n1]
+      LdRowKCat lb;  // B(r=k_in, k=n): n < n1 from W[k_in][n], else W2[k_in][n-n1]
       groups_of(lb.p1, d->W ? d->W + long(c0) * n1 : nullptr, d->gW, G);
       groups_of(lb.p2, d->W2 + long(c0) * (d->N - n1), d->gW, G);
       lb.ld1 = n1;
@@ -301,7 +357,8 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
       lb.rows = nc;
       lb.k1 = n1;
       lb.K = d->N;
-      return run_gemm(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx");
+      TTRL_FITS(la, lb, "ttrl_linear_backward");
+      return run_gemm<kLinDxCfgs>(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx", reserved);
     }
     LdRowK lb;  // B(r=k_in, k=n) = W[k_in][n]
     groups_of(lb.p, d->W + long(c0) * d->N, d->gW, G);
@@ -309,7 +366,8 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
     lb.rows = nc;
     lb.K = d->N;
     lb.vec_ok(all_aligned(lb.p, G));
-    return run_gemm(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx");
+    TTRL_FITS(la, lb, "ttrl_linear_backward");
+    return run_gemm<kLinDxCfgs>(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx", reserved);
   }
   return TTRL_OK;
 }

@@ -30,6 +30,8 @@
 
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace ttrl {
 
 constexpr int kMaxGroups = 4;
@@ -55,81 +57,93 @@ struct FDiv {
 
 // ------------------------------------------------------------- loaders ---
 //
-// Loaders work in two phases so that a workgroup's loads are all in flight
-// before any of them is waited on: issue() computes the addresses (clamped
-// into the operand, so every load is legal) and starts the loads into a
-// Fetch4, recording which of the four elements are real; resolve() runs
-// after every issue() of the stage and applies those predicates and the
-// ReLU mask.  Issue paths never read a loaded value.
+// Operands are read with buffer loads: a 32-bit byte offset into a buffer
+// resource whose range covers the operand, so an offset past the range
+// (kOob) reads zero.  Out-of-operand elements (ragged M, N, K; image
+// borders) are given kOob instead of being clamped and masked.
+//
+// Loads are issued in two phases so that all of a stage's loads are in
+// flight before any is waited on: issue() starts loads into a Fetch4 and
+// never reads a loaded value; write_tile() converts and stores to LDS.
+//
+// A KCONTIG loader returns four consecutive k of one row.  The kernel
+// arranges that every fetch of a thread has the same k offset within the
+// stage, so the loader splits its address into a per-row part (Row,
+// computed once per workgroup) and a per-k part (Kp, once per stage).  Any
+// other loader returns four consecutive rows at one k; then every fetch of a
+// thread covers the same four rows (Row, once per workgroup) and the k part
+// is computed per fetch.
 
-struct Fetch4 {
-  f32x4 v;
-  f32x4 m;      // mask values (1.0 where an element is not masked)
-  uint32_t ok;  // bit j: element j lies inside the operand; kU8Word, kU8Each: v holds bytes
-};
+constexpr uint32_t kOob = 0x80000000u;
+constexpr int kBufFlags = 0x00020000;  // gfx9 buffer resource word 3: raw 32-bit dwords
 
-constexpr uint32_t kU8Word = 0x10u;  // v.x carries four uint8 values packed in one word
-constexpr uint32_t kU8Each = 0x20u;  // each element carries one uint8 value as integer bits
-
-__device__ inline f32x4 resolve4(const Fetch4& f, bool masked) {
-  f32x4 v = f.v;
-  if (f.ok & kU8Word) {
-    const uint32_t w = __float_as_uint(f.v.x);
-    v = f32x4{float(w & 0xffu), float((w >> 8) & 0xffu), float((w >> 16) & 0xffu), float(w >> 24)};
-  } else if (f.ok & kU8Each) {
-    v = f32x4{float(__float_as_uint(f.v.x)), float(__float_as_uint(f.v.y)), float(__float_as_uint(f.v.z)),
-              float(__float_as_uint(f.v.w))};
-  }
-  v.x = ((f.ok & 1u) && (!masked || f.m.x > 0.f)) ? v.x : 0.f;
-  v.y = ((f.ok & 2u) && (!masked || f.m.y > 0.f)) ? v.y : 0.f;
-  v.z = ((f.ok & 4u) && (!masked || f.m.z > 0.f)) ? v.z : 0.f;
-  v.w = ((f.ok & 8u) && (!masked || f.m.w > 0.f)) ? v.w : 0.f;
-  return v;
+__device__ inline __amdgpu_buffer_rsrc_t make_res(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                           kBufFlags);
+}
+__device__ inline f32x4 ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ inline float ld_f1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ inline uint32_t ld_u8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return uint32_t(__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0));
 }
 
-// v(r, k) = p[g][r*ld + k] * [mask[g](r, k) > 0]; k contiguous.
+// Element formats a loader leaves in Fetch4::v.
+enum FetchFmt { kF32 = 0, kU8Word = 1, kU8Each = 2 };
+
+struct Fetch4 {
+  f32x4 v;  // kF32: four floats; kU8Word: four bytes packed in v.x; kU8Each: one byte per element (bits)
+};
+
+__device__ inline f32x4 resolve4(const Fetch4& f, int fmt) {
+  if (fmt == kU8Word) {
+    const uint32_t w = __float_as_uint(f.v.x);
+    return f32x4{float(w & 0xffu), float((w >> 8) & 0xffu), float((w >> 16) & 0xffu), float(w >> 24)};
+  }
+  if (fmt == kU8Each)
+    return f32x4{float(__float_as_uint(f.v.x)), float(__float_as_uint(f.v.y)), float(__float_as_uint(f.v.z)),
+                 float(__float_as_uint(f.v.w))};
+  return f.v;
+}
+
+// v(r, k) = p[g][r*ld + k]; k contiguous.  Offsets are 32-bit: the host
+// refuses operands of 2^31 bytes or more.
 struct LdRowK {
   static constexpr bool KCONTIG = true;
   const float* p[kMaxGroups] = {};
-  const float* mask[kMaxGroups] = {};  // same indexing as p
   long ld = 0;
   int rows = 0, K = 0;
-  bool vec = false;  // p[g], mask[g] 16-byte aligned and ld, K multiples of 4 (set by vec_ok)
+  bool vec = false;  // p[g] 16-byte aligned and ld, K multiples of 4 (set by vec_ok)
 
   __host__ void vec_ok(bool aligned) { vec = aligned && ld % 4 == 0 && K % 4 == 0; }
-  __device__ inline bool masked(int g) const { return mask[g] != nullptr; }
-  __device__ inline void issue(int r, int k, int g, Fetch4& f) const {
-    const bool rv = r < rows;
-    const float* base = p[g];
-    const float* mb = mask[g];
-    if (vec) {  // uniform: K % 4 == 0, so k < K covers all four
-      const bool in = rv && k < K;
-      const long i = in ? long(r) * ld + k : 0;
-      f.v = *reinterpret_cast<const f32x4*>(base + i);
-      if (mb) f.m = *reinterpret_cast<const f32x4*>(mb + i);
-      f.ok = in ? 0xFu : 0u;
+  __host__ __device__ long bytes() const { return rows > 0 ? ((long(rows) - 1) * ld + K) * 4 : 0; }
+  struct Row { uint32_t off; };
+  struct Kp { int k; };
+  __device__ inline int fmt() const { return kF32; }
+  __device__ inline __amdgpu_buffer_rsrc_t res(int g) const { return make_res(p[g], uint32_t(bytes())); }
+  __device__ inline Row row(int r, int) const { return Row{r < rows ? uint32_t(r * ld) * 4u : kOob}; }
+  __device__ inline Kp kpos(int k, int) const { return Kp{k}; }
+  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
+    if (vec) {  // K % 4 == 0: k < K covers all four
+      f.v = ld_f4(rs, (r.off != kOob && kp.k < K) ? r.off + uint32_t(kp.k) * 4u : kOob);
       return;
     }
-    f.ok = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool vj = rv && k + j < K;
-      const long i = vj ? long(r) * ld + k + j : 0;
-      f.v[j] = base[i];
-      if (mb) f.m[j] = mb[i];
-      f.ok |= uint32_t(vj) << j;
-    }
+    for (int j = 0; j < 4; ++j)
+      f.v[j] = ld_f1(rs, (r.off != kOob && kp.k + j < K) ? r.off + uint32_t(kp.k + j) * 4u : kOob);
   }
 };
 
-// v(r, k) = p[g][k*ld + r] * [mask > 0]; r contiguous.  Row `real_rows` reads
-// 1.0 when `ones` is set (the implicit ones row of a bias gradient); rows >=
-// `split` read p2[g][k*ld2 + r - split] (a second weight matrix beside the
-// first along the output axis).
+// v(r, k) = p[g][k*ld + r]; r contiguous.  Row `real_rows` reads 1.0 when
+// `ones` is set (the implicit ones row of a bias gradient); rows >= `split`
+// read p2[g][k*ld2 + r - split] (a second weight matrix beside the first
+// along the output axis).
 struct LdColK {
   static constexpr bool KCONTIG = false;
   const float* p[kMaxGroups] = {};
-  const float* mask[kMaxGroups] = {};
   const float* p2[kMaxGroups] = {};
   long ld = 0, ld2 = 0;
   int rows = 0, K = 0;
@@ -141,40 +155,45 @@ struct LdColK {
   // Vector loads need aligned bases and ld % 4 == 0; a 4-row chunk that
   // straddles `rows`, `real_rows` or `split` takes the element path.
   __host__ void vec_ok(bool aligned) { vec = aligned && ld % 4 == 0; }
-  __device__ inline bool masked(int g) const { return mask[g] != nullptr; }
-  __device__ inline void issue(int r, int k, int g, Fetch4& f) const {
+  __host__ __device__ long bytes() const {
+    int rr = rows < real_rows ? rows : real_rows;
+    rr = rr < split ? rr : split;
+    return (K > 0 && rr > 0) ? ((long(K) - 1) * ld + rr) * 4 : 0;
+  }
+  __host__ __device__ long bytes2() const { return (K > 0 && rows > split) ? ((long(K) - 1) * ld2 + (rows - split)) * 4 : 0; }
+  struct Row { int r; bool whole; };
+  struct Res { __amdgpu_buffer_rsrc_t a, b; };
+  __device__ inline int fmt() const { return kF32; }
+  __device__ inline Res res(int g) const {
+    return Res{make_res(p[g], uint32_t(bytes())), make_res(p2[g] ? p2[g] : p[g], uint32_t(bytes2()))};
+  }
+  __device__ inline Row row(int r, int) const {
+    return Row{r, vec && r + 3 < real_rows && r + 3 < split && r + 3 < rows};
+  }
+  __device__ inline void issue(const Res& rs, const Row& r, int k, Fetch4& f) const {
     const bool kv = k < K;
-    const float* base = p[g];
-    const float* mb = mask[g];
-    if (vec && r + 3 < real_rows && r + 3 < split && r + 3 < rows) {
-      const long i = kv ? long(k) * ld + r : 0;
-      f.v = *reinterpret_cast<const f32x4*>(base + i);
-      if (mb) f.m = *reinterpret_cast<const f32x4*>(mb + i);
-      f.ok = kv ? 0xFu : 0u;
+    if (r.whole) {
+      f.v = ld_f4(rs.a, kv ? uint32_t(k * ld + r.r) * 4u : kOob);
       return;
     }
-    f.ok = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int rr = r + j;
+      const int rr = r.r + j;
       const bool in = kv && rr < rows;
-      f.m[j] = 1.f;
       if (in && rr >= real_rows) {
         f.v[j] = (ones && rr == real_rows) ? 1.f : 0.f;
       } else if (in && rr >= split) {
-        f.v[j] = p2[g][long(k) * ld2 + (rr - split)];
+        f.v[j] = ld_f1(rs.b, uint32_t(k * ld2 + (rr - split)) * 4u);
       } else {
-        const long i = in ? long(k) * ld + rr : 0;
-        f.v[j] = base[i];
-        if (mb) f.m[j] = mb[i];
+        f.v[j] = ld_f1(rs.a, in ? uint32_t(k * ld + rr) * 4u : kOob);
       }
-      f.ok |= uint32_t(in) << j;
     }
   }
 };
 
 // Concatenation along k of two row-major operands: k < k1 reads p1[g][r*ld1+k],
-// k >= k1 reads p2[g][r*ld2 + k-k1] (the SAC critic's concat(s, a) input).
+// k >= k1 reads p2[g][r*ld2 + k-k1] (the SAC critic's concat(s, a) input;
+// also the transposed view of two weight matrices side by side).
 struct LdRowKCat {
   static constexpr bool KCONTIG = true;
   const float* p1[kMaxGroups] = {};
@@ -182,46 +201,25 @@ struct LdRowKCat {
   long ld1 = 0, ld2 = 0;
   int rows = 0, k1 = 0, K = 0;
 
-  __device__ inline bool masked(int) const { return false; }
-  __device__ inline void issue(int r, int k, int g, Fetch4& f) const {
-    f.ok = 0;
-    const bool rv = r < rows;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kk = k + j;
-      const bool vj = rv && kk < K;
-      const bool first = kk < k1;
-      const float* base = first ? p1[g] : p2[g];
-      const long i = !vj ? 0 : (first ? long(r) * ld1 + kk : long(r) * ld2 + (kk - k1));
-      f.v[j] = base[i];
-      f.ok |= uint32_t(vj) << j;
-    }
+  __host__ __device__ long bytes1() const { return rows > 0 ? ((long(rows) - 1) * ld1 + k1) * 4 : 0; }
+  __host__ __device__ long bytes2() const { return rows > 0 && K > k1 ? ((long(rows) - 1) * ld2 + (K - k1)) * 4 : 0; }
+  struct Row { int r; };
+  struct Kp { int k; };
+  struct Res { __amdgpu_buffer_rsrc_t a, b; };
+  __device__ inline int fmt() const { return kF32; }
+  __device__ inline Res res(int g) const {
+    return Res{make_res(p1[g], uint32_t(bytes1())), make_res(p2[g] ? p2[g] : p1[g], uint32_t(bytes2()))};
   }
-};
-
-// Concatenation along k of two row-major matrices: k < k1 reads p1[g][r*ld1 + k],
-// k >= k1 reads p2[g][r*ld2 + k-k1] (the transposed view of two weight
-// matrices side by side along the output axis).
-struct LdRowK2 {
-  static constexpr bool KCONTIG = true;
-  const float* p1[kMaxGroups] = {};
-  const float* p2[kMaxGroups] = {};
-  long ld1 = 0, ld2 = 0;
-  int rows = 0, k1 = 0, K = 0;
-
-  __device__ inline bool masked(int) const { return false; }
-  __device__ inline void issue(int r, int k, int g, Fetch4& f) const {
-    f.ok = 0;
-    const bool rv = r < rows;
+  __device__ inline Row row(int r, int) const { return Row{r}; }
+  __device__ inline Kp kpos(int k, int) const { return Kp{k}; }
+  __device__ inline void issue(const Res& rs, const Row& r, const Kp& kp, Fetch4& f) const {
+    const bool rv = r.r < rows;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int kk = k + j;
+      const int kk = kp.k + j;
       const bool vj = rv && kk < K;
-      const bool first = kk < k1;
-      const float* base = first ? p1[g] : p2[g];
-      const long i = !vj ? 0 : (first ? long(r) * ld1 + kk : long(r) * ld2 + (kk - k1));
-      f.v[j] = base[i];
-      f.ok |= uint32_t(vj) << j;
+      if (kk < k1) f.v[j] = ld_f1(rs.a, vj ? uint32_t(r.r * ld1 + kk) * 4u : kOob);
+      else f.v[j] = ld_f1(rs.b, vj ? uint32_t(r.r * ld2 + (kk - k1)) * 4u : kOob);
     }
   }
 };
@@ -230,7 +228,9 @@ struct LdRowK2 {
 
 // Element (m, n) of group g goes to one of four row-major blocks: rows
 // >= rsplit and columns >= csplit address the tail blocks with their index
-// rebased to 0.  v = alpha*acc (+ bias) (relu | clamp) (+ beta*old).
+// rebased to 0.  v = alpha*acc (+ bias) (relu | clamp) (* [mask > 0])
+// (+ beta*old); the mask (the ReLU output of the layer whose gradient this
+// is) applies to the leading block and is indexed like it.
 struct EpStore {
   int M = 0, N = 0;
   float* C[kMaxGroups] = {};    long ldc = 0;
@@ -245,6 +245,7 @@ struct EpStore {
   int relu = 0;
   int clamp_col = 1 << 30;                        // cols >= clamp_col clamp to [lo, hi]
   float lo = 0.f, hi = 0.f;
+  const float* mask[kMaxGroups] = {};
 
   __device__ inline int rows(int) const { return M; }
   __device__ inline void store(int m, int n, float acc, int g) const {
@@ -257,6 +258,7 @@ struct EpStore {
     if (ct && bias2[g]) v += bias2[g][nn];
     if (relu) v = v > 0.f ? v : 0.f;
     if (n >= clamp_col) v = fminf(fmaxf(v, lo), hi);
+    if (!rt && !ct && mask[g] && !(mask[g][long(mm) * ldc + nn] > 0.f)) v = 0.f;
     float* dst;
     if (!rt && !ct) dst = C[g] + long(mm) * ldc + nn;
     else if (rt && !ct) dst = Cr[g] + long(mm) * ldc + nn;
@@ -276,33 +278,70 @@ struct TileLds {
   static constexpr int SIZE = KCONTIG ? ROWS * LD : TBK * LD;
 };
 
+// One operand stage: CH float4 chunks per LDS row, PER chunks per thread.
+// Chunk i = tid + j*NT of a thread sits at LDS row i / CH, column i % CH;
+// NT % CH == 0, so the column is tid % CH for every j.
 template <int ROWS, int TBK, int NT, class L>
-__device__ inline void stage_tile(float* T, const L& ld, int r0, int k0, int g, int tid) {
+struct Stage {
+  static constexpr int CH = L::KCONTIG ? TBK / 4 : ROWS / 4;
+  static constexpr int TOTAL = (L::KCONTIG ? ROWS : TBK) * CH;
+  static constexpr int PER = (TOTAL + NT - 1) / NT;
+  static_assert(NT % CH == 0, "a thread's chunks must share one column");
+  __device__ static constexpr bool live(int j, int tid) { return TOTAL % NT == 0 || tid + j * NT < TOTAL; }
+};
+
+// The per-workgroup part of a thread's fetch addresses: one Row per fetch
+// for a KCONTIG loader (its rows differ), one shared Row otherwise.
+template <class L, int PER, bool KC = L::KCONTIG>
+struct Cursor;
+template <class L, int PER>
+struct Cursor<L, PER, true> {
+  typename L::Row r[PER];
+};
+template <class L, int PER>
+struct Cursor<L, PER, false> {
+  typename L::Row r;
+};
+
+template <int ROWS, int TBK, int NT, class L, int PER>
+__device__ inline void make_cursor(Cursor<L, PER>& c, const L& ld, int r0, int g, int tid) {
+  using S = Stage<ROWS, TBK, NT, L>;
+  if constexpr (L::KCONTIG) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) c.r[j] = ld.row(r0 + (tid + j * NT) / S::CH, g);
+  } else {
+    c.r = ld.row(r0 + (tid % S::CH) * 4, g);
+  }
+}
+
+// Starts every load of one operand stage (no value is read here).
+template <int ROWS, int TBK, int NT, class L, int PER, class R>
+__device__ inline void issue_tile(Fetch4 (&f)[PER], const L& ld, const R& rs, const Cursor<L, PER>& c, int k0, int g,
+                                  int tid) {
+  using S = Stage<ROWS, TBK, NT, L>;
+  if constexpr (L::KCONTIG) {
+    const auto kp = ld.kpos(k0 + (tid % S::CH) * 4, g);
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (S::live(j, tid)) ld.issue(rs, c.r[j], kp, f[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (S::live(j, tid)) ld.issue(rs, c.r, k0 + (tid + j * NT) / S::CH, f[j]);
+  }
+}
+
+// Converts the fetched values and writes them to the LDS tile.
+template <int ROWS, int TBK, int NT, class L, int PER>
+__device__ inline void write_tile(float* T, const Fetch4 (&f)[PER], int fmt, int tid) {
+  using S = Stage<ROWS, TBK, NT, L>;
   using Lds = TileLds<ROWS, TBK, L::KCONTIG>;
-  constexpr int CH = L::KCONTIG ? TBK / 4 : ROWS / 4;  // float4 chunks per LDS row
-  constexpr int TOTAL = (L::KCONTIG ? ROWS : TBK) * CH;
-  constexpr int PER = (TOTAL + NT - 1) / NT;
-  constexpr int BATCH = PER < 8 ? PER : 8;  // fetches in flight per thread
-  const bool masked = ld.masked(g);
 #pragma unroll
-  for (int j0 = 0; j0 < PER; j0 += BATCH) {
-    Fetch4 f[BATCH];
-#pragma unroll
-    for (int j = 0; j < BATCH; ++j) {
-      const int i = tid + (j0 + j) * NT;
-      if (j0 + j < PER && i < TOTAL) {
-        const int a = i / CH, b = (i - a * CH) * 4;
-        if constexpr (L::KCONTIG) ld.issue(r0 + a, k0 + b, g, f[j]);
-        else ld.issue(r0 + b, k0 + a, g, f[j]);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < BATCH; ++j) {
-      const int i = tid + (j0 + j) * NT;
-      if (j0 + j < PER && i < TOTAL) {
-        const int a = i / CH, b = (i - a * CH) * 4;
-        *reinterpret_cast<f32x4*>(T + a * Lds::LD + b) = resolve4(f[j], masked);
-      }
+  for (int j = 0; j < PER; ++j) {
+    const int i = tid + j * NT;
+    if (S::live(j, tid)) {
+      const int a = i / S::CH, b = (i - a * S::CH) * 4;
+      *reinterpret_cast<f32x4*>(T + a * Lds::LD + b) = resolve4(f[j], fmt);
     }
   }
 }
@@ -319,7 +358,11 @@ __device__ inline f32x4 lds_frag(const float* T, int row, int kk) {
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int TBK, bool PARTIAL, class LA, class LB, class EP>
+// Software pipeline over LDS stages: the loads of stage s+1 are issued into
+// registers before the MFMAs of stage s run, so global-memory latency is
+// paid once per workgroup rather than once per stage; both operands' loads
+// of a stage are in flight together.
+template <int BM, int BN, int WGM, int WGN, int TBK, class LA, class LB, class EP>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, float* ws, int M, int N, int K,
                                                          int kchunk, int splits) {
   constexpr int NT = 64 * WGM * WGN;
@@ -329,6 +372,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
   static_assert(TBK % 16 == 0, "TBK must be a multiple of 16");
   using LdsA = TileLds<BM, TBK, LA::KCONTIG>;
   using LdsB = TileLds<BN, TBK, LB::KCONTIG>;
+  constexpr int PA = Stage<BM, TBK, NT, LA>::PER;
+  constexpr int PB = Stage<BN, TBK, NT, LB>::PER;
   __shared__ __attribute__((aligned(16))) float As[LdsA::SIZE];
   __shared__ __attribute__((aligned(16))) float Bs[LdsB::SIZE];
 
@@ -346,13 +391,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const auto ra = la.res(g);
+  const auto rb = lb.res(g);
+  Cursor<LA, PA> ca;
+  Cursor<LB, PB> cb;
+  make_cursor<BM, TBK, NT>(ca, la, m0, g, tid);
+  make_cursor<BN, TBK, NT>(cb, lb, n0, g, tid);
+  const int fa_fmt = la.fmt(), fb_fmt = lb.fmt();
+
+  Fetch4 fa[PA], fb[PB];
+  issue_tile<BM, TBK, NT>(fa, la, ra, ca, kbeg, g, tid);
+  issue_tile<BN, TBK, NT>(fb, lb, rb, cb, kbeg, g, tid);
+
   const int lr = lane & 15, lk = (lane >> 4) * 4;
   for (int k0 = kbeg; k0 < kend; k0 += TBK) {
-    if (k0 != kbeg) __syncthreads();
-    stage_tile<BM, TBK, NT>(As, la, m0, k0, g, tid);
-    stage_tile<BN, TBK, NT>(Bs, lb, n0, k0, g, tid);
+    if (k0 != kbeg) __syncthreads();  // the previous stage's LDS reads are done
+    write_tile<BM, TBK, NT, LA>(As, fa, fa_fmt, tid);
+    write_tile<BN, TBK, NT, LB>(Bs, fb, fb_fmt, tid);
     __syncthreads();
-    const int kspan = min(TBK, kend - k0);  // multiple of 4 is not required: zero padded
+    if (k0 + TBK < kend) {
+      issue_tile<BM, TBK, NT>(fa, la, ra, ca, k0 + TBK, g, tid);
+      issue_tile<BN, TBK, NT>(fb, lb, rb, cb, k0 + TBK, g, tid);
+    }
+    const int kspan = min(TBK, kend - k0);  // zero padded past K
 #pragma unroll 2
     for (int kb = 0; kb < kspan; kb += 16) {
       f32x4 a[FM], b[FN];
@@ -381,7 +442,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
         const int n = n0 + wn * WTN + j * 16 + lr;
-        if constexpr (PARTIAL) {
+        if (splits > 1) {
           if (m < M && n < N) ws[((long(g) * splits + split) * M + m) * N + n] = acc[i][j][r];
         } else {
           ep.store(m, n, acc[i][j][r], g);
@@ -389,7 +450,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
       }
 }
 
-// Sums split-K partials in split order and applies the epilogue.
+// Sums split-K partials in split order and applies the epilogue.  Eight
+// partials are loaded before any is added, so a long split list costs a
+// few memory round trips rather than one per split.
 template <class EP>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, int M, int N, int splits,
                                                        int groups, FDiv dmn, FDiv dn) {
@@ -400,9 +463,17 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
     const int mn = i - g * MN;
     const int m = dn.div(mn), n = mn - m * N;
     if (m >= ep.rows(g)) continue;
-    float s = 0.f;
     const float* p = ws + long(g) * splits * MN + mn;
-    for (int sp = 0; sp < splits; ++sp) s += p[long(sp) * MN];
+    float s = 0.f;
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = p[long(sp + j) * MN];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; sp < splits; ++sp) s += p[long(sp) * MN];
     ep.store(m, n, s, g);
   }
 }
@@ -411,18 +482,18 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
 enum TileCfg { T32x32 = 0, T64x32 = 1, T32x64 = 2, T64x64 = 3, T128x32 = 4, T128x64 = 5, T64x128 = 6, kNumCfg = 7 };
 
 struct TileDims {
-  int bm, bn, tbk;
+  int bm, bn, tbk, wgm, wgn;
 };
 
 inline TileDims tile_dims(int cfg) {
   switch (cfg) {
-    case T32x32: return {32, 32, 256};
-    case T64x32: return {64, 32, 128};
-    case T32x64: return {32, 64, 128};
-    case T64x64: return {64, 64, 128};
-    case T128x32: return {128, 32, 128};
-    case T128x64: return {128, 64, 64};
-    default: return {64, 128, 64};
+    case T32x32: return {32, 32, 256, 2, 2};
+    case T64x32: return {64, 32, 128, 2, 2};
+    case T32x64: return {32, 64, 128, 2, 2};
+    case T64x64: return {64, 64, 128, 2, 2};
+    case T128x32: return {128, 32, 128, 4, 1};
+    case T128x64: return {128, 64, 64, 2, 2};
+    default: return {64, 128, 64, 2, 2};
   }
 }
 
@@ -430,24 +501,28 @@ struct GemmPlan {
   int cfg, bm, bn, tbk, splits, kchunk;
 };
 
-// Chooses a tile and a split-K factor: enough workgroups to cover the 256
-// CUs, each split a whole number of LDS stages, within `ws_floats` of
-// workspace.
-GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, int force_cfg = -1, int force_splits = 0);
+// Chooses a tile among `allowed` (bit per TileCfg) and a split-K factor
+// that minimise a cycle estimate, each split a whole number of LDS stages,
+// within `ws_floats` of workspace.
+GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, unsigned allowed);
 
 // Workspace owned by the context (stream-ordered scratch for split-K).
 float* ctx_workspace(ttrl_ctx* ctx, long* floats);
+
+// dZ = src * [mask > 0] for `groups` blocks of n elements (element stride gs
+// between blocks), written densely to the top of the context workspace
+// (block g at offset g*n).  Adds the floats it occupies to *reserved, which
+// the caller passes on to run_gemm; *rc receives the status.
+const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const float* mask, long n, long gs,
+                                      int groups, long* reserved, int* rc);
 
 template <int BM, int BN, int WGM, int WGN, int TBK, class LA, class LB, class EP>
 inline void launch_cfg(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
                        const GemmPlan& p, hipStream_t st) {
   dim3 grid(ceil_div(M, BM), ceil_div(N, BN), unsigned(groups * p.splits));
-  if (p.splits == 1) {
-    hipLaunchKernelGGL((k_gemm<BM, BN, WGM, WGN, TBK, false, LA, LB, EP>), grid, dim3(64 * WGM * WGN), 0, st, la,
-                       lb, ep, ws, M, N, K, p.kchunk, 1);
-  } else {
-    hipLaunchKernelGGL((k_gemm<BM, BN, WGM, WGN, TBK, true, LA, LB, EP>), grid, dim3(64 * WGM * WGN), 0, st, la,
-                       lb, ep, ws, M, N, K, p.kchunk, p.splits);
+  hipLaunchKernelGGL((k_gemm<BM, BN, WGM, WGN, TBK, LA, LB, EP>), grid, dim3(64 * WGM * WGN), 0, st, la, lb, ep, ws,
+                     M, N, K, p.kchunk, p.splits);
+  if (p.splits > 1) {
     const long total = long(groups) * M * N;
     unsigned blocks = unsigned(total / 256 + 1);
     if (blocks > 4096) blocks = 4096;
@@ -459,24 +534,31 @@ inline void launch_cfg(const LA& la, const LB& lb, const EP& ep, float* ws, int 
   }
 }
 
-template <class LA, class LB, class EP>
+constexpr unsigned cfg_bit(int c) { return 1u << c; }
+constexpr unsigned kCfgAll = (1u << kNumCfg) - 1;
+
+// Plans and launches one GEMM.  ALLOWED restricts the tile shapes a call
+// site instantiates (each is a separate kernel); `ws_reserved` floats at the
+// top of the context workspace are in use by the caller.
+template <unsigned ALLOWED, class LA, class LB, class EP>
 inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int M, int N, int K, int groups,
-                    const char* name, int force_cfg = -1, int force_splits = 0) {
+                    const char* name, long ws_reserved = 0) {
+  static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
   if (M <= 0 || N <= 0 || groups <= 0) return TTRL_OK;
   if (groups > kMaxGroups) return set_error(TTRL_EINVAL, "%s: at most %d groups", name, kMaxGroups);
   if (long(groups) * M * N >= (1L << 31)) return set_error(TTRL_EINVAL, "%s: output too large", name);
   long wsf = 0;
   float* ws = ctx_workspace(ctx, &wsf);
-  GemmPlan p = plan_gemm(M, N, K, groups, wsf, force_cfg, force_splits);
+  GemmPlan p = plan_gemm(M, N, K, groups, wsf - ws_reserved, ALLOWED);
   hipStream_t st = stream_of(ctx);
   switch (p.cfg) {
-    case T32x32: launch_cfg<32, 32, 2, 2, 256>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T64x32: launch_cfg<64, 32, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T32x64: launch_cfg<32, 64, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T64x64: launch_cfg<64, 64, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T128x32: launch_cfg<128, 32, 4, 1, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T128x64: launch_cfg<128, 64, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    default: launch_cfg<64, 128, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    case T32x32: if constexpr ((ALLOWED & cfg_bit(T32x32)) != 0) launch_cfg<32, 32, 2, 2, 256>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    case T64x32: if constexpr ((ALLOWED & cfg_bit(T64x32)) != 0) launch_cfg<64, 32, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    case T32x64: if constexpr ((ALLOWED & cfg_bit(T32x64)) != 0) launch_cfg<32, 64, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    case T64x64: if constexpr ((ALLOWED & cfg_bit(T64x64)) != 0) launch_cfg<64, 64, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    case T128x32: if constexpr ((ALLOWED & cfg_bit(T128x32)) != 0) launch_cfg<128, 32, 4, 1, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    case T128x64: if constexpr ((ALLOWED & cfg_bit(T128x64)) != 0) launch_cfg<128, 64, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    default: if constexpr ((ALLOWED & cfg_bit(T64x128)) != 0) launch_cfg<64, 128, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
   }
   return check_launch(name);
 }

@@ -48,6 +48,7 @@ class LinearDesc(C.Structure):
         ("dx", C.c_void_p), ("lddx", C.c_long), ("gdx", C.c_long),
         ("dx_col0", C.c_int), ("dx_cols", C.c_int),
         ("beta_w", C.c_float), ("beta_x", C.c_float),
+        ("dxmask", C.c_void_p),
     ]
 
 
@@ -102,7 +103,7 @@ SIGNATURES = {
     "ttrl_conv2d_forward_multi": ([P, C.POINTER(ConvGeom), I, C.POINTER(P), C.POINTER(P), C.POINTER(P),
                                    C.POINTER(P), F, I], I),
     "ttrl_conv2d_backward_weight": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, F], I),
-    "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, F, F], I),
+    "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, P, F, F], I),
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
     "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),

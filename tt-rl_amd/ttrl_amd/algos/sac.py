@@ -175,8 +175,7 @@ class TwinQ:
                 d = _lib.LinearDesc()
                 d.M, d.K, d.N, d.groups = B, Kin, N, 2
                 d.W, d.gW = lin.weight.data.ptr, S
-                d.dy, d.gy = g.ptr, B * N
-                d.ymask = acts[j].ptr if j < nl - 1 else None
+                d.dy, d.gy = g.ptr, B * N  # hidden-layer dy arrives gated by the layer above
                 if params:
                     c0, c1 = self.layers[0][j], self.layers[1][j]
                     (dw0, db0, dw1, db1), beta = grad_targets(c0.weight, c0.bias, c1.weight, c1.bias)
@@ -192,6 +191,7 @@ class TwinQ:
                 if j > 0:
                     dx = DeviceArray(dev, (2, B, Kin))
                     d.dx, d.lddx, d.gdx = dx.ptr, Kin, B * Kin
+                    d.dxmask = acts[j - 1].ptr  # relu_bw of layer j-1, applied as dx is written
                 elif want_action:
                     dx = DeviceArray(dev, (2, B, self.act_dim))
                     d.dx, d.lddx, d.gdx = dx.ptr, self.act_dim, B * self.act_dim

@@ -46,6 +46,19 @@ class no_grad:
         return False
 
 
+#: Ops whose output is a ReLU output (their backward applies relu_bw).
+RELU_OPS = frozenset({"linear_relu", "conv2d_relu"})
+
+
+def relu_mask(t: "Tensor"):
+    """The array whose positive entries gate t's gradient when t is a ReLU
+    output (possibly through reshapes, which share its buffer), else None."""
+    s = t
+    while s._op == "reshape" and s._parents:
+        s = s._parents[0]
+    return t.data if s._op in RELU_OPS else None
+
+
 def _no_backward(grad):
     return None
 
@@ -54,7 +67,7 @@ class Tensor:
     """A node in the autograd graph, backed by a `DeviceArray`."""
 
     __slots__ = ("data", "requires_grad", "grad", "_backward", "_parents", "_op", "_backward_done",
-                 "_grad_slot", "_grad_owned", "_arena", "__weakref__")
+                 "_grad_slot", "_grad_owned", "_arena", "_grad_masked", "__weakref__")
 
     def __init__(self, data, requires_grad: bool = False, _parents=(), _op: str = ""):
         self.data = data
@@ -67,6 +80,11 @@ class Tensor:
         self._grad_slot = None
         self._grad_owned = False
         self._arena = None
+        # True while every contribution to `grad` was already multiplied by
+        # [data > 0]: a consumer applied this node's ReLU backward in its own
+        # epilogue, so this node's backward must not apply it again (it would
+        # be harmless, but it costs a pass).
+        self._grad_masked = False
 
     # -- construction ------------------------------------------------------
 
@@ -101,10 +119,12 @@ class Tensor:
 
     # -- gradient plumbing -------------------------------------------------
 
-    def _accumulate(self, grad: DeviceArray):
-        """grad += g (ttrl/engine/autograd.py:106-114)."""
+    def _accumulate(self, grad: DeviceArray, masked: bool = False):
+        """grad += g (ttrl/engine/autograd.py:106-114); `masked` says g was
+        already multiplied by this node's ReLU gate."""
         from ttrl_amd.engine.ops import _kernels as K
 
+        self._grad_masked = masked and (self.grad is None or self._grad_masked)
         if grad.shape != self.shape:
             grad = grad.reshape(self.shape)
         if self.grad is None:
@@ -141,9 +161,15 @@ class Tensor:
             self._grad_owned = True
         return self.grad, 1.0
 
+    def _note_write(self, beta: float, masked: bool):
+        """Record a kernel's write into the buffer `_grad_target` handed out
+        (beta 0 overwrote, 1 accumulated), `masked` as for `_accumulate`."""
+        self._grad_masked = masked and (beta == 0.0 or self._grad_masked)
+
     def zero_grad(self):
         self.grad = None
         self._grad_owned = False
+        self._grad_masked = False
 
     def detach(self) -> "Tensor":
         return Tensor(self.data, requires_grad=False)

@@ -22,7 +22,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ttrl_amd import _lib
-from ttrl_amd.engine.autograd import Tensor, is_grad_enabled
+from ttrl_amd.engine.autograd import Tensor, is_grad_enabled, relu_mask
 from ttrl_amd.engine.nn import Module
 from ttrl_amd.engine.ops.fused import grad_targets
 from ttrl_amd.engine.tensor import DeviceArray
@@ -271,7 +271,7 @@ class Conv2d(Module):
                     "Rebuild the layer with needs_input_grad=True, or detach "
                     "the activation it is given."
                 )
-            mask = y.vp if relu else None
+            mask = y.vp if relu and not out._grad_masked else None
             (dw, db), beta_w = grad_targets(weight, bias)
             if dw is not None:
                 dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp, mask,
@@ -288,8 +288,10 @@ class Conv2d(Module):
                     db.copy_from(db_tmp)
             if x.requires_grad:
                 (dx,), beta_x = grad_targets(x)
+                xmask = relu_mask(x)
                 dev.call("ttrl_conv2d_backward_input", C.byref(cg), grad.vp, mask, w_data.vp, dx.vp,
-                         C.c_float(scale), C.c_float(beta_x))
+                         None if xmask is None else xmask.vp, C.c_float(scale), C.c_float(beta_x))
+                x._note_write(beta_x, xmask is not None)
 
         out._backward = _backward
         return out

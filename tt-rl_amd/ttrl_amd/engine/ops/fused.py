@@ -13,7 +13,7 @@ from __future__ import annotations
 import ctypes as C
 
 from ttrl_amd import _lib
-from ttrl_amd.engine.autograd import Tensor, _detached, _needs
+from ttrl_amd.engine.autograd import Tensor, _detached, _needs, relu_mask
 from ttrl_amd.engine.tensor import DeviceArray
 
 __all__ = ["linear", "linear_node", "dqn_td_loss", "grad_targets"]
@@ -80,10 +80,12 @@ def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, 
     def _backward(grad):
         (dw, db), beta_w = grad_targets(weight, bias)
         (dx,), beta_x = grad_targets(x)
+        gate = relu and not out._grad_masked  # relu_bw still to apply to grad
+        xmask = relu_mask(x) if dx is not None else None
         if dw is None and db is not None:
             # Bias-only gradient: a column sum of dZ.
             from ttrl_amd.engine.ops import _kernels as Kk
-            g = Kk.binary("relu_bw", grad, y) if relu else grad
+            g = Kk.binary("relu_bw", grad, y) if gate else grad
             s = Kk.reduce_dim("sum", g, 0, keepdim=True)
             if beta_w:
                 Kk.binary_into("add", db, s.reshape(db.shape), db)
@@ -97,7 +99,8 @@ def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, 
         b.x, b.ldx = x_data.ptr, K
         b.W = w_data.ptr
         b.dy = grad.ptr
-        b.ymask = y.ptr if relu else None
+        b.ymask = y.ptr if gate else None
+        b.dxmask = xmask.ptr if xmask is not None else None
         b.dW = _p(dw)
         b.db = _p(db_) if dw is not None else None
         b.dx = _p(dx)
@@ -105,6 +108,8 @@ def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, 
         b.beta_w, b.beta_x = beta_w, beta_x
         if dw is not None or dx is not None:
             dev.call("ttrl_linear_backward", C.byref(b))
+        if dx is not None:
+            x._note_write(beta_x, xmask is not None)
 
     out._backward = _backward
     return out

@@ -58,7 +58,7 @@ def reshape(a: Tensor, shape) -> Tensor:
 
     def _backward(grad):
         if a.requires_grad:
-            a._accumulate(grad.reshape(in_shape))
+            a._accumulate(grad.reshape(in_shape), masked=out._grad_masked)
 
     out._backward = _backward
     return out
