@@ -245,6 +245,39 @@ int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accu
 /* dst = (1 - tau) * dst + tau * src (ttrl/algos/sac/targets.py:45-52). */
 int ttrl_polyak(ttrl_ctx* ctx, float* dst, const float* src, long n, float tau);
 
+/* ---------------------------------------------------------------- PPO --- */
+
+/* GAE-lambda over a [T][N] rollout (time-major, one column per env lane),
+ * recursing t = T-1 .. 0 with last_values [N] as the value after the last
+ * step: delta = r + gamma*V'*(1-done) - V; A = delta + gamma*lam*(1-done)*A';
+ * A *= valid (a padding slot cuts the chain; valid may be NULL for all ones);
+ * returns = A + V.  Products round as the reference's float32 recursion does.
+ * Replaces RolloutBuffer.compute_gae (ttrl/buffers/rollout.py:195-226). */
+int ttrl_gae(ttrl_ctx* ctx, int T, int N, const float* rewards, const float* values, const float* dones,
+             const float* valid, const float* last_values, double gamma, double lam, float* advantages,
+             float* returns);
+/* out = (a - mean) / (std + eps) over the n entries with valid > 0 (population
+ * std; valid NULL = all), 0 elsewhere; stats (nullable) receives {mean, std}.
+ * The minibatch advantage normalisation of ttrl/buffers/rollout.py:269-270. */
+int ttrl_normalize_advantages(ttrl_ctx* ctx, const float* adv, const float* valid, long n, float eps, float* out,
+                              float* stats);
+/* The PPO objective of one minibatch (ttrl/algos/ppo/loss.py:42-83) with the
+ * categorical head's log-prob and entropy (ttrl/algos/ppo/policy.py:64-76,
+ * ttrl/engine/ops/functional.py:160-178): logits [B][A], actions [B] (int32),
+ * per-row old_logp, advantages, returns, old_values, values [B]; valid [B]
+ * (nullable) selects the masked mean (masked_mean, loss.py:27-39).
+ * out4 = {loss, policy_loss, value_loss, entropy}; new_logp [B];
+ * dlogits [B][A] and dvalues [B] = d loss / d logits, d loss / d values. */
+int ttrl_ppo_loss(ttrl_ctx* ctx, int B, int A, const float* logits, const int* actions, const float* old_logp,
+                  const float* advantages, const float* returns, const float* old_values, const float* values,
+                  const float* valid, float clip_eps, float value_clip_eps, float value_coef, float entropy_coef,
+                  float* out4, float* new_logp, float* dlogits, float* dvalues);
+/* Global L2 clip of one flat gradient arena, on the device (no host read):
+ * norm = sqrt(sum g^2); if norm > max_norm, g *= max_norm / (norm + 1e-6).
+ * *norm_out (nullable) receives the norm before clipping; sq_scratch is one
+ * float.  Replaces clip_grad_norm (ttrl/algos/grads.py:13-43). */
+int ttrl_clip_grad_norm(ttrl_ctx* ctx, float* g, long n, float max_norm, float* sq_scratch, float* norm_out);
+
 /* ------------------------------------------------------ elementwise ops --- */
 
 enum {

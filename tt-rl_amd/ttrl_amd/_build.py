@@ -20,7 +20,7 @@ LIB_DIR = PKG_DIR / "lib"
 OBJ_DIR = PKG_DIR.parent / "_build"
 LIB_PATH = LIB_DIR / "libttrl_hip.so"
 
-SOURCES = ("runtime.hip", "gemm.hip", "conv.hip", "eltwise.hip", "heads.hip", "optim.hip")
+SOURCES = ("runtime.hip", "gemm.hip", "conv.hip", "eltwise.hip", "heads.hip", "optim.hip", "ppo.hip")
 
 ARCH = "gfx950"
 

@@ -112,6 +112,10 @@ SIGNATURES = {
     "ttrl_adam_step": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
     "ttrl_sum_squares": ([P, P, L, P, I], I),
     "ttrl_polyak": ([P, P, P, L, F], I),
+    "ttrl_gae": ([P, I, I, P, P, P, P, P, C.c_double, C.c_double, P, P], I),
+    "ttrl_normalize_advantages": ([P, P, P, L, F, P, P], I),
+    "ttrl_ppo_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, F, F, F, P, P, P, P], I),
+    "ttrl_clip_grad_norm": ([P, P, L, F, P, P], I),
     "ttrl_unary": ([P, I, P, P, L, F], I),
     "ttrl_binary": ([P, I, P, P, P, I, C.POINTER(L), C.POINTER(L), C.POINTER(L)], I),
     "ttrl_copy_strided": ([P, P, P, I, C.POINTER(L), C.POINTER(L), C.POINTER(L)], I),
