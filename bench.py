@@ -123,37 +123,64 @@ def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
 
 
 def dominant_kernel(dev, learner, reps=200):
-    """The fc1 weight-gradient GEMM of the DQN update ([3136+1] x 512 from a
-    batch-32 reduction, bias gradient folded in), timed alone on the
-    library's stream with HIP events.  Algorithmic HBM bytes per launch:
-    read x (32x3136) and dZ, mask (32x512), write dW+db (3137x512)."""
+    """The longest kernel of the DQN update: the conv1 forward of the three
+    Q evaluations in one launch (online(s), online(s'), target(s'); uint8
+    4x84x84 frames at batch 32 -> 32 x 20 x 20 x 32, bias + ReLU), timed
+    alone on the library's stream with HIP events over `reps` launches.
+    Algorithmic work per launch: 3 x 2 x 12800 x 32 x 256 FLOPs; HBM bytes:
+    two frame batches, two weight sets, three outputs."""
     from ttrl_amd import _lib
     from ttrl_amd.engine.tensor import DeviceArray
 
-    fc1 = learner.online.encoder.layers[7]
-    M, K, N = 32, 3136, 512
-    x = DeviceArray(dev, (M, K))
-    x.fill(0.5)
-    dy = DeviceArray(dev, (M, N))
-    dy.fill(0.25)
-    dw = DeviceArray(dev, (K, N))
-    db = DeviceArray(dev, (N,))
-    d = _lib.LinearDesc()
-    d.M, d.K, d.N, d.groups = M, K, N, 1
-    d.x, d.ldx, d.W, d.dy, d.ymask = x.ptr, K, fc1.weight.data.ptr, dy.ptr, dy.ptr
-    d.dW, d.db = dw.ptr, db.ptr
+    B, Cin, H, W, O, k, s = 32, 4, 84, 84, 32, 8, 4
+    OH = (H - k) // s + 1
+    frames = [DeviceArray(dev, (B, Cin, H, W), np.uint8) for _ in range(2)]
+    rng = np.random.default_rng(5)
+    for f in frames:
+        f.upload(rng.integers(0, 256, (B, Cin, H, W), dtype=np.uint8))
+    conv1 = [learner.online.encoder.layers[0], learner.target.encoder.layers[0]]
+    ys = [DeviceArray(dev, (B, OH, OH, O)) for _ in range(3)]
+    xs = [frames[0], frames[1], frames[1]]
+    nets = [conv1[0], conv1[0], conv1[1]]
+    geom = _lib.ConvGeom(B, Cin, H, W, O, k, s, 0, _lib.LAYOUT_NCHW_U8)
+    xp = _lib.ptrs([x.ptr for x in xs])
+    wp = _lib.ptrs([n.weight.data.ptr for n in nets])
+    bp = _lib.ptrs([n.bias.data.ptr for n in nets])
+    yp = _lib.ptrs([y.ptr for y in ys])
+
+    def launch():
+        dev.call("ttrl_conv2d_forward_multi", C.byref(geom), 3, xp, wp, bp, yp, C.c_float(1.0 / 255.0), 1)
+
     for _ in range(10):
-        dev.call("ttrl_linear_backward", C.byref(d))
+        launch()
     dev.synchronize()
     ms = C.c_float(0.0)
     dev.call("ttrl_timer_start")
     for _ in range(reps):
-        dev.call("ttrl_linear_backward", C.byref(d))
+        launch()
     dev.call("ttrl_timer_stop", C.byref(ms))
     sec = ms.value / 1e3 / reps
-    algo_bytes = 4 * (M * K + 2 * M * N + (K + 1) * N)
-    return {"name": "linear_backward dW (fc1 3136x512, batch 32)", "seconds": sec, "bytes": algo_bytes,
-            "flops": 2.0 * M * (K + 1) * N}
+    M = B * OH * OH
+    flops = 3 * 2.0 * M * O * Cin * k * k
+    algo_bytes = 2 * B * Cin * H * W + 2 * 4 * (Cin * k * k + 1) * O + 3 * 4 * M * O
+    return {"name": "conv2d_forward_multi: Nature-CNN conv1, 3 x (32x4x84x84 uint8 -> 32x20x20x32)",
+            "seconds": sec, "bytes": algo_bytes, "flops": flops}
+
+
+def pcie_inclusive(dev, learner, n=100):
+    """Updates/s when every update starts from a host batch (numpy arrays in
+    pageable memory): the host-to-device copy of the batch is inside the loop."""
+    from ttrl_amd.workloads import dqn_batch
+
+    batches = [dqn_batch(4000 + i) for i in range(8)]
+    for i in range(5):
+        learner.update(batches[i % 8])
+    dev.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        learner.update(batches[i % 8])
+    dev.synchronize()
+    return n / (time.perf_counter() - t0)
 
 
 def cpu_baseline(seconds: float):
@@ -215,7 +242,8 @@ def main() -> int:
     sac_value = args.steps / swall
     sflops = sac_update_flops(256)
     dom = dominant_kernel(dev, dqn)
-    achieved = dom["bytes"] / dom["seconds"]
+    achieved = dom["flops"] / dom["seconds"]
+    host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "DQN updates/s @bs32, SAC updates/s @bs256 on 1 MI355X; % of roofline",
@@ -238,9 +266,12 @@ def main() -> int:
         "sac": {"value": round(sac_value, 2), "unit": "SAC updates/s", "batch": 256,
                 "ms_per_step": round(swall / args.steps * 1e3, 5), "gpu_ms_per_step": sgpu / args.steps * 1e3,
                 "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA},
-        "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
-                     "avg_us": dom["seconds"] * 1e6},
+        "roofline": {"bound": "mfma", "kernel": dom["name"], "achieved": achieved / 1e12,
+                     "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
+                     "traffic": None, "algorithmic_bytes": dom["bytes"], "avg_us": dom["seconds"] * 1e6},
+        "pcie_inclusive": None if host_rate is None else {
+            "value": round(host_rate, 2), "unit": "DQN updates/s",
+            "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
