@@ -82,8 +82,8 @@ __device__ inline long patch_index(const ConvGeo& g, int m, int k) {
 // One patch element, any layout (the general path).
 __device__ inline float patch_elem(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int m, int k) {
   const long idx = patch_index(g, m, k);
-  if (g.u8) return __uint_as_float(ld_u8(rs, idx < 0 ? kOob : uint32_t(idx)));
-  return ld_f1(rs, idx < 0 ? kOob : uint32_t(idx) * 4u);
+  if (g.u8) return __uint_as_float(ld_u8(rs, idx < 0 ? kBad : uint32_t(idx)));
+  return ld_f1(rs, idx < 0 ? kBad : uint32_t(idx) * 4u);
 }
 
 // How four consecutive patch indices k..k+3 (k % 4 == 0) lie in memory.
@@ -99,46 +99,48 @@ __host__ inline int patch_mode(const ConvGeo& g, bool aligned) {
   return kPatchGeneral;
 }
 
-// Output pixel m as an input position: element offset of (b, ih0, iw0) and
-// ih0 = oh*S - P, iw0 = ow*S - P (ih0 far below zero for m past the end).
+// Output pixel m as an input position: byte offset of (b, ih0, iw0) and
+// ih0 = oh*S - P, iw0 = ow*S - P; a pixel past the end gets kBad and an ih0
+// far below zero.  Without padding every tap of a real pixel is inside the
+// image, so the byte offset alone carries validity.
 struct PixelPos {
-  int base, ih0, iw0;
+  uint32_t base;
+  int ih0, iw0;
 };
 __device__ inline PixelPos pixel_pos(const ConvGeo& g, int m) {
-  if (m >= g.M) return PixelPos{0, -(1 << 28), 0};
+  if (m >= g.M) return PixelPos{kBad, -(1 << 28), 0};
   int b, oh, ow;
   g.split_m(m, b, oh, ow);
   const int ih0 = oh * g.S - g.P, iw0 = ow * g.S - g.P;
-  const int base = g.u8 ? (b * g.C * g.H + ih0) * g.W + iw0 : ((b * g.H + ih0) * g.W + iw0) * g.C;
-  return PixelPos{base, ih0, iw0};
+  const int e = g.u8 ? (b * g.C * g.H + ih0) * g.W + iw0 : ((b * g.H + ih0) * g.W + iw0) * g.C;
+  return PixelPos{uint32_t(e) * (g.u8 ? 1u : 4u), ih0, iw0};
 }
 
-// Patch chunk k..k+3 as a tap: element offset relative to the pixel base
-// and (kh, kw) of its first element.
+// Patch chunk k..k+3 as a tap: byte offset relative to the pixel base and
+// (kh, kw) of its first element; kBad past the patch.
 struct TapPos {
-  int off, kh, kw;
-  bool v;  // k < C*KH*KW
+  uint32_t off;
+  int kh, kw;
 };
 __device__ inline TapPos tap_pos(const ConvGeo& g, int k) {
-  if (k >= g.kp()) return TapPos{0, 0, 0, false};
+  if (k >= g.kp()) return TapPos{kBad, 0, 0};
   int c, kh, kw;
   g.split_k(k, c, kh, kw);
-  const int off = g.u8 ? (c * g.H + kh) * g.W + kw : (kh * g.W + kw) * g.C + c;
-  return TapPos{off, kh, kw, true};
+  const int e = g.u8 ? (c * g.H + kh) * g.W + kw : (kh * g.W + kw) * g.C + c;
+  return TapPos{uint32_t(e) * (g.u8 ? 1u : 4u), kh, kw};
 }
 
 // Starts the load of patch chunk (pixel, tap) in the given mode.
 __device__ inline void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int mode, const PixelPos& px,
                                    const TapPos& tp, Fetch4& f) {
-  const int ih = px.ih0 + tp.kh, iw = px.iw0 + tp.kw;
-  const bool hv = tp.v && ih >= 0 && ih < g.H;
-  if (mode == kPatchNhwcVec) {
-    const bool in = hv && iw >= 0 && iw < g.W;
-    f.v = ld_f4(rs, in ? uint32_t(px.base + tp.off) * 4u : kOob);
-  } else {  // kPatchU8Word
-    const bool in = hv && iw >= 0 && iw + 3 < g.W;
-    f.v.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, in ? uint32_t(px.base + tp.off) : kOob, 0, 0));
+  uint32_t off = px.base + tp.off;
+  if (g.P != 0) {  // borders: the tap may fall outside the image
+    const int ih = px.ih0 + tp.kh, iw = px.iw0 + tp.kw;
+    const int wlast = mode == kPatchU8Word ? iw + 3 : iw;
+    if (ih < 0 || ih >= g.H || iw < 0 || wlast >= g.W) off = kBad;
   }
+  if (mode == kPatchNhwcVec) f.v = ld_f4(rs, off);
+  else f.v.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
 }
 
 // Forward A operand: A(m, k) = patch(m, k).
@@ -155,7 +157,7 @@ struct LdConvFwd {
   }
   __device__ inline __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
   __device__ inline Row row(int m, int) const {
-    return mode == kPatchGeneral ? Row{PixelPos{m, 0, 0}} : Row{pixel_pos(g, m)};
+    return mode == kPatchGeneral ? Row{PixelPos{uint32_t(m), 0, 0}} : Row{pixel_pos(g, m)};
   }
   __device__ inline Kp kpos(int k, int) const { return Kp{mode == kPatchGeneral ? TapPos{} : tap_pos(g, k), k}; }
   __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
@@ -164,7 +166,7 @@ struct LdConvFwd {
       return;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, g, r.px.base, kp.k + j);
+    for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, g, int(r.px.base), kp.k + j);
   }
 };
 
@@ -178,6 +180,7 @@ struct LdConvPatchT {
   int mode;
   int ones;
   struct Row { TapPos tp; int r; bool whole; };
+  struct Ks { int m; };
   __device__ inline int fmt() const {
     return mode == kPatchU8Word ? kU8Word : (g.u8 ? kU8Each : kF32);
   }
@@ -186,7 +189,9 @@ struct LdConvPatchT {
     const bool whole = mode != kPatchGeneral && r + 3 < g.kp();
     return Row{whole ? tap_pos(g, r) : TapPos{}, r, whole};
   }
-  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, int m, Fetch4& f) const {
+  __device__ inline Ks kstage(const Row&, int m, int) const { return Ks{m}; }
+  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Ks& ks, int dm, Fetch4& f) const {
+    const int m = ks.m + dm;
     if (r.whole) {
       patch_issue(rs, g, mode, pixel_pos(g, m), r.tp, f);
       return;
@@ -241,7 +246,7 @@ struct LdConvDxA {
     if ((g.O & 3) == 0) {  // the four k share one tap and output pixel
       const int oh = r.ohc - kp.jh, ow = r.owc - kp.jw;
       const bool in = kp.v && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
-      f.v = ld_f4(rs, in ? uint32_t(r.base + kp.off) * 4u : kOob);
+      f.v = ld_f4(rs, in ? uint32_t(r.base + kp.off) * 4u : kBad);
       return;
     }
 #pragma unroll
@@ -256,7 +261,7 @@ struct LdConvDxA {
         in = kp.ch + g.S * jh < g.KH && kp.cw + g.S * jw < g.KW && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
         off = r.base - (jh * g.OW + jw) * g.O + o;
       }
-      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kOob);
+      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kBad);
     }
   }
 };
@@ -268,38 +273,38 @@ struct LdConvDxB {
   ConvGeo g;
   const float* wt;
   uint32_t wbytes;
-  struct Row { int off; bool v; };
-  struct Kp { int off; bool v; int k, ch, cw; };
+  struct Row { uint32_t off; int c; };  // byte offset of Wt[(0,0,c)][0], kBad past C
+  struct Kp { uint32_t off; int k, ch, cw; };
   __device__ inline int fmt() const { return kF32; }
   __device__ inline __amdgpu_buffer_rsrc_t res(int) const { return make_res(wt, wbytes); }
-  __device__ inline Row row(int c, int) const { return Row{c * g.O, c < g.C}; }
+  __device__ inline Row row(int c, int) const { return Row{c < g.C ? uint32_t(c * g.O) * 4u : kBad, c}; }
   __device__ inline Kp kpos(int k, int grp) const {
     const int c = g.cls0 + grp, ch = c / g.S, cw = c - ch * g.S;
-    if (k >= g.TH * g.TW * g.O) return Kp{0, false, k, ch, cw};
+    if (k >= g.TH * g.TW * g.O) return Kp{kBad, k, ch, cw};
     const int jt = g.d_o.div(k), o = k - jt * g.O;
     const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
     const int kh = ch + g.S * jh, kw = cw + g.S * jw;
     const bool v = kh < g.KH && kw < g.KW;
-    return Kp{(kh * g.KW + kw) * g.C * g.O + o, v, k, ch, cw};
+    return Kp{v ? uint32_t((kh * g.KW + kw) * g.C * g.O + o) * 4u : kBad, k, ch, cw};
   }
   __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
     if ((g.O & 3) == 0) {
-      f.v = ld_f4(rs, (r.v && kp.v) ? uint32_t(r.off + kp.off) * 4u : kOob);
+      f.v = ld_f4(rs, r.off + kp.off);
       return;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = kp.k + j;
-      bool in = r.v && k < g.TH * g.TW * g.O;
+      bool in = r.c < g.C && k < g.TH * g.TW * g.O;
       int off = 0;
       if (in) {
         const int jt = g.d_o.div(k), o = k - jt * g.O;
         const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
         const int kh = kp.ch + g.S * jh, kw = kp.cw + g.S * jw;
         in = kh < g.KH && kw < g.KW;
-        off = r.off + (kh * g.KW + kw) * g.C * g.O + o;
+        off = (r.c + (kh * g.KW + kw) * g.C) * g.O + o;
       }
-      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kOob);
+      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kBad);
     }
   }
 };
@@ -312,18 +317,32 @@ struct EpConvDx {
   const float* xmask;
   float alpha, beta;
   __device__ inline int rows(int grp) const { return g.B * g.nh[grp] * g.nw[grp]; }
-  __device__ inline void store(int r, int c, float acc, int grp) const {
-    if (r >= rows(grp) || c >= g.C) return;
+  __host__ long tune_span() const { return long(g.B) * g.H * g.W * g.C + 64; }
+  __host__ EpConvDx tune_copy(float* sink) const {
+    EpConvDx e = *this;
+    e.dx = sink;
+    e.beta = 0.f;
+    return e;
+  }
+  __device__ inline EpAux aux(int r, int c, int grp) const {
+    EpAux x{nullptr, 0.f, 1.f, 0.f};
+    if (r >= rows(grp) || c >= g.C) return x;
     const int b = g.d_nhnw[grp].div(r);
     const int rem = r - b * g.nh[grp] * g.nw[grp];
     const int i = g.d_nw[grp].div(rem), j = rem - i * g.nw[grp];
     const int ih = g.ih0[grp] + g.S * i, iw = g.iw0[grp] + g.S * j;
     const long idx = ((long(b) * g.H + ih) * g.W + iw) * g.C + c;
-    float* dst = dx + idx;
+    x.dst = dx + idx;
+    if (xmask) x.keep = xmask[idx];
+    if (beta != 0.f) x.old = *x.dst;
+    return x;
+  }
+  __device__ inline void store(int, int, float acc, const EpAux& x) const {
+    if (!x.dst) return;
     float v = alpha * acc;
-    if (xmask && !(xmask[idx] > 0.f)) v = 0.f;
-    if (beta != 0.f) v += beta * *dst;
-    *dst = v;
+    if (!(x.keep > 0.f)) v = 0.f;
+    if (beta != 0.f) v += beta * x.old;
+    *x.dst = v;
   }
 };
 
@@ -373,10 +392,10 @@ int make_geo(const ttrl_conv_geom* s, ConvGeo& g) {
   g.OW = span_w / s->stride + 1;
   g.u8 = s->in_layout == TTRL_LAYOUT_NCHW_U8 ? 1 : 0;
   g.M = g.B * g.OH * g.OW;
-  // Buffer loads address operands with 32-bit byte offsets.
+  // Buffer loads address operands with 32-bit byte offsets below 2^30.
   const long bigs[] = {long(g.B) * g.OH * g.OW * g.O * 4, long(g.B) * g.H * g.W * g.C * (g.u8 ? 1 : 4),
                        long(g.C) * g.KH * g.KW * g.O * 4};
-  for (long v : bigs) TTRL_REQUIRE(v < (1L << 31), "conv: an operand of %ld bytes exceeds 2^31", v);
+  for (long v : bigs) TTRL_REQUIRE(v < kMaxOperandBytes, "conv: an operand of %ld bytes exceeds 2^30", v);
   g.d_ohow.set(g.OH * g.OW);
   g.d_ow.set(g.OW);
   g.d_c.set(g.C);

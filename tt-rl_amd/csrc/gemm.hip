@@ -12,19 +12,27 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <vector>
 
 namespace ttrl {
 
-GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, unsigned allowed) {
-  // Cost model in shader cycles, per candidate tile and split-K factor:
-  //   rounds * (latency + stages_per_block * blocks_per_cu * max(mfma, fetch))
-  //   + a reduction pass when K is split,
-  // with mfma = 32 cycles per 16x16x4 MFMA of one wavefront (the FP32 MFMA
-  // issue interval), fetch = stage bytes at 64 B/cycle per CU, and the
-  // workgroups a CU holds limited by LDS (160 KiB) and registers (two).
+namespace {
+
+struct Costed {
+  double t;
+  GemmPlan p;
+};
+
+// Every (tile, split) the cost model admits, with its estimate in cycles:
+//   rounds * (latency + stages_per_block * blocks_per_cu * max(mfma, fetch))
+//   + a reduction pass when K is split,
+// with mfma = 32 cycles per 16x16x4 MFMA of one wavefront (the FP32 MFMA
+// issue interval), fetch = stage bytes at 64 B/cycle per CU, and the
+// workgroups a CU holds limited by LDS (160 KiB) and registers (two).
+std::vector<Costed> costed_plans(int M, int N, int K, int groups, long ws_floats, unsigned allowed) {
   constexpr double kLatency = 2500.0, kReduceFixed = 4000.0, kCus = 256.0;
-  GemmPlan best{T32x32, 32, 32, 256, 1, 256};
-  double best_t = 1e300;
+  std::vector<Costed> out;
   for (int c = 0; c < kNumCfg; ++c) {
     if (!(allowed & (1u << c))) continue;
     const TileDims t = tile_dims(c);
@@ -34,8 +42,7 @@ GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, unsigned all
     const double bpc = std::max(1.0, std::min(2.0, std::floor(160.0 * 1024.0 / lds)));
     const double mfma = double(t.bm / t.wgm / 16) * (t.bn / t.wgn / 16) * (t.tbk / 4) * 32.0;
     const double fetch = 4.0 * (t.bm + t.bn) * t.tbk / 64.0;
-    const int smax = std::max(1, stages);
-    for (int sp = 1; sp <= smax; ++sp) {
+    for (int sp = 1; sp <= stages; ++sp) {
       const int spb = (stages + sp - 1) / sp;
       const int real = (stages + spb - 1) / spb;  // splits that own a stage
       if (real != sp) continue;
@@ -45,13 +52,54 @@ GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, unsigned all
       const double rounds = std::ceil(blocks / (kCus * bpc));
       double tt = rounds * (kLatency + spb * per_cu * std::max(mfma, fetch));
       if (sp > 1) tt += kReduceFixed + double(groups) * M * N * sp * 4.0 / (kCus * 32.0);
-      if (tt < best_t) {
-        best_t = tt;
-        best = GemmPlan{c, t.bm, t.bn, t.tbk, sp, spb * t.tbk};
-      }
+      out.push_back(Costed{tt, GemmPlan{c, t.bm, t.bn, t.tbk, sp, spb * t.tbk}});
     }
   }
-  return best;
+  std::stable_sort(out.begin(), out.end(), [](const Costed& a, const Costed& b) { return a.t < b.t; });
+  return out;
+}
+
+}  // namespace
+
+GemmPlan plan_gemm(int M, int N, int K, int groups, long ws_floats, unsigned allowed) {
+  const std::vector<Costed> all = costed_plans(M, N, K, groups, ws_floats, allowed);
+  return all.empty() ? GemmPlan{T32x32, 32, 32, 256, 1, 256} : all.front().p;
+}
+
+std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_floats, unsigned allowed,
+                                      int max_n) {
+  const std::vector<Costed> all = costed_plans(M, N, K, groups, ws_floats, allowed);
+  std::vector<GemmPlan> out;
+  // the model's best split of every tile shape, then the next best overall
+  for (int c = 0; c < kNumCfg; ++c)
+    for (const Costed& x : all)
+      if (x.p.cfg == c) {
+        out.push_back(x.p);
+        break;
+      }
+  for (const Costed& x : all) {
+    if (int(out.size()) >= max_n) break;
+    bool seen = false;
+    for (const GemmPlan& q : out) seen = seen || (q.cfg == x.p.cfg && q.splits == x.p.splits);
+    if (!seen) out.push_back(x.p);
+  }
+  return out;
+}
+
+bool gemm_tuning_log() {
+  static const bool on = [] {
+    const char* v = std::getenv("TTRL_GEMM_TUNE_LOG");
+    return v && v[0] == '1';
+  }();
+  return on;
+}
+
+bool gemm_tuning_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("TTRL_GEMM_TUNE");
+    return !(v && v[0] == '0');
+  }();
+  return on;
 }
 
 const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const float* mask, long n, long gs,
@@ -76,11 +124,11 @@ __global__ __launch_bounds__(256) void k_relu_mask(float* dst, const float* src,
 }
 
 // Buffer loads address an operand with 32-bit byte offsets.
-inline bool fits(const LdRowK& l) { return l.bytes() < (1L << 31); }
-inline bool fits(const LdColK& l) { return l.bytes() < (1L << 31) && l.bytes2() < (1L << 31); }
-inline bool fits(const LdRowKCat& l) { return l.bytes1() < (1L << 31) && l.bytes2() < (1L << 31); }
+inline bool fits(const LdRowK& l) { return l.bytes() < kMaxOperandBytes; }
+inline bool fits(const LdColK& l) { return l.bytes() < kMaxOperandBytes && l.bytes2() < kMaxOperandBytes; }
+inline bool fits(const LdRowKCat& l) { return l.bytes1() < kMaxOperandBytes && l.bytes2() < kMaxOperandBytes; }
 #define TTRL_FITS(la, lb, name) \
-  TTRL_REQUIRE(fits(la) && fits(lb), "%s: an operand of 2^31 bytes or more is not supported", name)
+  TTRL_REQUIRE(fits(la) && fits(lb), "%s: an operand of 2^30 bytes or more is not supported", name)
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -194,11 +242,11 @@ static int linear_forward_tables(ttrl_ctx* ctx, int M, int K, int N, int groups,
     lb.p[g] = W[g];
     lb.p2[g] = W2[g];
   }
-  lb.vec_ok(all_aligned(W, groups));
   if (split_w) {
     lb.ld2 = N - n1;
     lb.split = n1;
   }
+  lb.vec_ok(all_aligned(W, groups));
   if (x2[0]) {
     LdRowKCat la;
     for (int g = 0; g < kMaxGroups; ++g) {

@@ -9,6 +9,7 @@
 //   host<->device copies         ttrl/engine/tensor/transfer.py:11-51
 //   trace capture / replay       ttrl/engine/trace.py:56-126
 #include "common.hpp"
+#include "tile_gemm.hpp"
 
 #include <cstdarg>
 #include <cstdio>
@@ -54,6 +55,11 @@ struct ttrl_ctx {
   hipEvent_t t0 = nullptr, t1 = nullptr;
   float* ws = nullptr;  // stream-ordered scratch of split-K GEMMs and reductions
   long ws_floats = 0;
+  // GEMM plans chosen by timing candidates on this device, by call signature.
+  std::unordered_map<std::string, ttrl::GemmPlan> plans;
+  float* tune_out = nullptr;  // output sink of candidate runs
+  size_t tune_bytes = 0;
+  hipEvent_t tune0 = nullptr, tune1 = nullptr;
 };
 
 struct ttrl_graph {
@@ -83,6 +89,34 @@ hipStream_t stream_of(ttrl_ctx* ctx) { return ctx->stream; }
 float* ctx_workspace(ttrl_ctx* ctx, long* floats) {
   if (floats) *floats = ctx->ws_floats;
   return ctx->ws;
+}
+
+bool ctx_capturing(ttrl_ctx* ctx) { return ctx->capturing; }
+
+const GemmPlan* ctx_plan_find(ttrl_ctx* ctx, const std::string& key) {
+  auto it = ctx->plans.find(key);
+  return it == ctx->plans.end() ? nullptr : &it->second;
+}
+
+void ctx_plan_store(ttrl_ctx* ctx, const std::string& key, const GemmPlan& p) { ctx->plans[key] = p; }
+
+float* ctx_tune_sink(ttrl_ctx* ctx, size_t bytes) {
+  if (bytes > ctx->tune_bytes) {
+    if (ctx->tune_out) hipFree(ctx->tune_out);
+    ctx->tune_out = nullptr;
+    ctx->tune_bytes = 0;
+    if (hipMalloc(&ctx->tune_out, bytes) != hipSuccess) return nullptr;
+    ctx->tune_bytes = bytes;
+  }
+  return ctx->tune_out;
+}
+
+bool ctx_tune_events(ttrl_ctx* ctx, hipEvent_t* a, hipEvent_t* b) {
+  if (!ctx->tune0 && hipEventCreate(&ctx->tune0) != hipSuccess) return false;
+  if (!ctx->tune1 && hipEventCreate(&ctx->tune1) != hipSuccess) return false;
+  *a = ctx->tune0;
+  *b = ctx->tune1;
+  return true;
 }
 
 int check_launch(const char* name) {
@@ -186,6 +220,9 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   for (auto& p : ctx->pools) pool_free_slabs(p);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->tune_out) (void)hipFree(ctx->tune_out);
+  if (ctx->tune0) (void)hipEventDestroy(ctx->tune0);
+  if (ctx->tune1) (void)hipEventDestroy(ctx->tune1);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
   (void)hipStreamDestroy(ctx->stream);

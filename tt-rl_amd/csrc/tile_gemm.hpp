@@ -31,6 +31,9 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdio>
+#include <string>
+#include <vector>
 
 namespace ttrl {
 
@@ -58,9 +61,12 @@ struct FDiv {
 // ------------------------------------------------------------- loaders ---
 //
 // Operands are read with buffer loads: a 32-bit byte offset into a buffer
-// resource whose range covers the operand, so an offset past the range
-// (kOob) reads zero.  Out-of-operand elements (ragged M, N, K; image
-// borders) are given kOob instead of being clamped and masked.
+// resource whose range covers the operand exactly, so an offset past the
+// range reads zero.  Operands are under 2^30 bytes (the host refuses larger
+// ones), and an out-of-operand element (ragged M, N, K; image borders) gets
+// an offset of at least kBad = 2^30: the sum of any valid offset and kBad,
+// or of two kBad, stays in [2^30, 2^32), out of range, so validity folds
+// into one addition instead of per-element predicates.
 //
 // Loads are issued in two phases so that all of a stage's loads are in
 // flight before any is waited on: issue() starts loads into a Fetch4 and
@@ -69,12 +75,19 @@ struct FDiv {
 // A KCONTIG loader returns four consecutive k of one row.  The kernel
 // arranges that every fetch of a thread has the same k offset within the
 // stage, so the loader splits its address into a per-row part (Row,
-// computed once per workgroup) and a per-k part (Kp, once per stage).  Any
-// other loader returns four consecutive rows at one k; then every fetch of a
-// thread covers the same four rows (Row, once per workgroup) and the k part
-// is computed per fetch.
+// computed once per workgroup) and a per-k part (Kp, once per stage): one
+// addition per fetch.  Any other loader returns four consecutive rows at one
+// k; every fetch of a thread covers the same four rows (Row), its first k
+// gives a per-stage base (Ks) and fetch j sits j*NT/CH k-rows further on,
+// a uniform stride.
 
-constexpr uint32_t kOob = 0x80000000u;
+constexpr uint32_t kBad = 0x40000000u;
+
+// Element paths whose source buffer differs from lane to lane read through
+// plain pointers (a buffer resource chosen per lane would serialise the
+// wavefront); an element outside the operand reads one of these instead.
+__device__ const float g_zero_one[2] = {0.f, 1.f};
+constexpr long kMaxOperandBytes = 1L << 30;
 constexpr int kBufFlags = 0x00020000;  // gfx9 buffer resource word 3: raw 32-bit dwords
 
 __device__ inline __amdgpu_buffer_rsrc_t make_res(const void* p, uint32_t bytes) {
@@ -109,8 +122,7 @@ __device__ inline f32x4 resolve4(const Fetch4& f, int fmt) {
   return f.v;
 }
 
-// v(r, k) = p[g][r*ld + k]; k contiguous.  Offsets are 32-bit: the host
-// refuses operands of 2^31 bytes or more.
+// v(r, k) = p[g][r*ld + k]; k contiguous.
 struct LdRowK {
   static constexpr bool KCONTIG = true;
   const float* p[kMaxGroups] = {};
@@ -121,26 +133,26 @@ struct LdRowK {
   __host__ void vec_ok(bool aligned) { vec = aligned && ld % 4 == 0 && K % 4 == 0; }
   __host__ __device__ long bytes() const { return rows > 0 ? ((long(rows) - 1) * ld + K) * 4 : 0; }
   struct Row { uint32_t off; };
-  struct Kp { int k; };
+  struct Kp { uint32_t add; int k; };
   __device__ inline int fmt() const { return kF32; }
   __device__ inline __amdgpu_buffer_rsrc_t res(int g) const { return make_res(p[g], uint32_t(bytes())); }
-  __device__ inline Row row(int r, int) const { return Row{r < rows ? uint32_t(r * ld) * 4u : kOob}; }
-  __device__ inline Kp kpos(int k, int) const { return Kp{k}; }
+  __device__ inline Row row(int r, int) const { return Row{r < rows ? uint32_t(r * ld) * 4u : kBad}; }
+  __device__ inline Kp kpos(int k, int) const { return Kp{k < K ? uint32_t(k) * 4u : kBad, k}; }
   __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
     if (vec) {  // K % 4 == 0: k < K covers all four
-      f.v = ld_f4(rs, (r.off != kOob && kp.k < K) ? r.off + uint32_t(kp.k) * 4u : kOob);
+      f.v = ld_f4(rs, r.off + kp.add);
       return;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      f.v[j] = ld_f1(rs, (r.off != kOob && kp.k + j < K) ? r.off + uint32_t(kp.k + j) * 4u : kOob);
+    for (int j = 0; j < 4; ++j) f.v[j] = ld_f1(rs, r.off + (kp.k + j < K ? uint32_t(kp.k + j) * 4u : kBad));
   }
 };
 
 // v(r, k) = p[g][k*ld + r]; r contiguous.  Row `real_rows` reads 1.0 when
 // `ones` is set (the implicit ones row of a bias gradient); rows >= `split`
 // read p2[g][k*ld2 + r - split] (a second weight matrix beside the first
-// along the output axis).
+// along the output axis).  With ld >= the real rows, every k >= K lies past
+// the resource's range, so the vector path needs no k check.
 struct LdColK {
   static constexpr bool KCONTIG = false;
   const float* p[kMaxGroups] = {};
@@ -154,39 +166,52 @@ struct LdColK {
 
   // Vector loads need aligned bases and ld % 4 == 0; a 4-row chunk that
   // straddles `rows`, `real_rows` or `split` takes the element path.
-  __host__ void vec_ok(bool aligned) { vec = aligned && ld % 4 == 0; }
-  __host__ __device__ long bytes() const {
+  __host__ void vec_ok(bool aligned) { vec = aligned && ld % 4 == 0 && ld >= real_dense(); }
+  __host__ __device__ int real_dense() const {
     int rr = rows < real_rows ? rows : real_rows;
-    rr = rr < split ? rr : split;
+    return rr < split ? rr : split;
+  }
+  __host__ __device__ long bytes() const {
+    const int rr = real_dense();
     return (K > 0 && rr > 0) ? ((long(K) - 1) * ld + rr) * 4 : 0;
   }
-  __host__ __device__ long bytes2() const { return (K > 0 && rows > split) ? ((long(K) - 1) * ld2 + (rows - split)) * 4 : 0; }
-  struct Row { int r; bool whole; };
-  struct Res { __amdgpu_buffer_rsrc_t a, b; };
+  __host__ __device__ long bytes2() const {
+    return (K > 0 && rows > split) ? ((long(K) - 1) * ld2 + (rows - split)) * 4 : 0;
+  }
+  // mode 0: four real rows, one vector load; 1: no row inside, zeros; 2: element by element.
+  struct Row { uint32_t off; int r; int mode; };
+  struct Ks { uint32_t base; int k; };
+  struct Res { __amdgpu_buffer_rsrc_t a; int g; };
+  __device__ static inline int g_of(const Res& rs) { return rs.g; }
   __device__ inline int fmt() const { return kF32; }
-  __device__ inline Res res(int g) const {
-    return Res{make_res(p[g], uint32_t(bytes())), make_res(p2[g] ? p2[g] : p[g], uint32_t(bytes2()))};
-  }
+  __device__ inline Res res(int g) const { return Res{make_res(p[g], uint32_t(bytes())), g}; }
   __device__ inline Row row(int r, int) const {
-    return Row{r, vec && r + 3 < real_rows && r + 3 < split && r + 3 < rows};
+    const bool whole = vec && r + 3 < real_rows && r + 3 < split && r + 3 < rows;
+    return Row{uint32_t(r) * 4u, r, whole ? 0 : (r >= rows ? 1 : 2)};
   }
-  __device__ inline void issue(const Res& rs, const Row& r, int k, Fetch4& f) const {
-    const bool kv = k < K;
-    if (r.whole) {
-      f.v = ld_f4(rs.a, kv ? uint32_t(k * ld + r.r) * 4u : kOob);
+  __device__ inline Ks kstage(const Row& r, int k, int) const { return Ks{uint32_t(k * ld) * 4u + r.off, k}; }
+  __device__ inline void issue(const Res& rs, const Row& r, const Ks& ks, int dk, Fetch4& f) const {
+    if (r.mode == 0) {
+      f.v = ld_f4(rs.a, ks.base + uint32_t(dk * ld) * 4u);
       return;
     }
+    if (r.mode == 1) {
+      f.v = f32x4{0.f, 0.f, 0.f, 0.f};
+      return;
+    }
+    const int k = ks.k + dk;
+    const bool kv = k < K;
+    const float* base = p[g_of(rs)];
+    const float* base2 = p2[g_of(rs)];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int rr = r.r + j;
       const bool in = kv && rr < rows;
-      if (in && rr >= real_rows) {
-        f.v[j] = (ones && rr == real_rows) ? 1.f : 0.f;
-      } else if (in && rr >= split) {
-        f.v[j] = ld_f1(rs.b, uint32_t(k * ld2 + (rr - split)) * 4u);
-      } else {
-        f.v[j] = ld_f1(rs.a, in ? uint32_t(k * ld + rr) * 4u : kOob);
-      }
+      const float* src = &g_zero_one[0];
+      if (in && rr >= real_rows) src = &g_zero_one[(ones && rr == real_rows) ? 1 : 0];
+      else if (in && rr >= split) src = base2 + (long(k) * ld2 + (rr - split));
+      else if (in) src = base + (long(k) * ld + rr);
+      f.v[j] = *src;
     }
   }
 };
@@ -202,24 +227,23 @@ struct LdRowKCat {
   int rows = 0, k1 = 0, K = 0;
 
   __host__ __device__ long bytes1() const { return rows > 0 ? ((long(rows) - 1) * ld1 + k1) * 4 : 0; }
-  __host__ __device__ long bytes2() const { return rows > 0 && K > k1 ? ((long(rows) - 1) * ld2 + (K - k1)) * 4 : 0; }
+  __host__ __device__ long bytes2() const {
+    return rows > 0 && K > k1 ? ((long(rows) - 1) * ld2 + (K - k1)) * 4 : 0;
+  }
   struct Row { int r; };
   struct Kp { int k; };
-  struct Res { __amdgpu_buffer_rsrc_t a, b; };
   __device__ inline int fmt() const { return kF32; }
-  __device__ inline Res res(int g) const {
-    return Res{make_res(p1[g], uint32_t(bytes1())), make_res(p2[g] ? p2[g] : p1[g], uint32_t(bytes2()))};
-  }
+  __device__ inline int res(int g) const { return g; }
   __device__ inline Row row(int r, int) const { return Row{r}; }
   __device__ inline Kp kpos(int k, int) const { return Kp{k}; }
-  __device__ inline void issue(const Res& rs, const Row& r, const Kp& kp, Fetch4& f) const {
+  __device__ inline void issue(int g, const Row& r, const Kp& kp, Fetch4& f) const {
     const bool rv = r.r < rows;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kk = kp.k + j;
-      const bool vj = rv && kk < K;
-      if (kk < k1) f.v[j] = ld_f1(rs.a, vj ? uint32_t(r.r * ld1 + kk) * 4u : kOob);
-      else f.v[j] = ld_f1(rs.b, vj ? uint32_t(r.r * ld2 + (kk - k1)) * 4u : kOob);
+      const float* src = &g_zero_one[0];
+      if (rv && kk < K) src = kk < k1 ? p1[g] + (long(r.r) * ld1 + kk) : p2[g] + (long(r.r) * ld2 + (kk - k1));
+      f.v[j] = *src;
     }
   }
 };
@@ -231,6 +255,11 @@ struct LdRowKCat {
 // rebased to 0.  v = alpha*acc (+ bias) (relu | clamp) (* [mask > 0])
 // (+ beta*old); the mask (the ReLU output of the layer whose gradient this
 // is) applies to the leading block and is indexed like it.
+struct EpAux {
+  float* dst;
+  float add, keep, old;
+};
+
 struct EpStore {
   int M = 0, N = 0;
   float* C[kMaxGroups] = {};    long ldc = 0;
@@ -248,24 +277,46 @@ struct EpStore {
   const float* mask[kMaxGroups] = {};
 
   __device__ inline int rows(int) const { return M; }
-  __device__ inline void store(int m, int n, float acc, int g) const {
-    if (m >= M || n >= N) return;
+  // A copy that writes every element into `sink` (at least tune_span()
+  // floats) and reads nothing old: timing a candidate plan must not disturb
+  // the real output.
+  __host__ long tune_span() const {
+    const long ld = ldc > ldcc ? ldc : ldcc;
+    return long(M) * (ld > 0 ? ld : N) + N + 64;
+  }
+  __host__ EpStore tune_copy(float* sink) const {
+    EpStore e = *this;
+    for (int g = 0; g < kMaxGroups; ++g) e.C[g] = e.Cr[g] = e.Cc[g] = e.Crc[g] = sink;
+    e.beta = 0.f;
+    return e;
+  }
+  // Everything element (m, n) reads besides the accumulator: its address, the
+  // bias, the mask and (beta != 0) the old value.  The kernel issues these
+  // loads for a batch of elements before it stores any of them.
+  __device__ inline EpAux aux(int m, int n, int g) const {
+    EpAux x{nullptr, 0.f, 1.f, 0.f};
+    if (m >= M || n >= N) return x;
     const bool rt = m >= rsplit, ct = n >= csplit;
     const int mm = rt ? m - rsplit : m;
     const int nn = ct ? n - csplit : n;
-    float v = (rt ? alpha_r : alpha) * acc;
-    if (!ct && bias[g]) v += bias[g][nn];
-    if (ct && bias2[g]) v += bias2[g][nn];
+    if (!ct && bias[g]) x.add = bias[g][nn];
+    if (ct && bias2[g]) x.add = bias2[g][nn];
+    if (!rt && !ct && mask[g]) x.keep = mask[g][long(mm) * ldc + nn];
+    if (!rt && !ct) x.dst = C[g] + long(mm) * ldc + nn;
+    else if (rt && !ct) x.dst = Cr[g] + long(mm) * ldc + nn;
+    else if (!rt && ct) x.dst = Cc[g] + long(mm) * ldcc + nn;
+    else x.dst = Crc[g] + long(mm) * ldcc + nn;
+    if (beta != 0.f) x.old = *x.dst;
+    return x;
+  }
+  __device__ inline void store(int m, int n, float acc, const EpAux& x) const {
+    if (!x.dst) return;
+    float v = (m >= rsplit ? alpha_r : alpha) * acc + x.add;
     if (relu) v = v > 0.f ? v : 0.f;
     if (n >= clamp_col) v = fminf(fmaxf(v, lo), hi);
-    if (!rt && !ct && mask[g] && !(mask[g][long(mm) * ldc + nn] > 0.f)) v = 0.f;
-    float* dst;
-    if (!rt && !ct) dst = C[g] + long(mm) * ldc + nn;
-    else if (rt && !ct) dst = Cr[g] + long(mm) * ldc + nn;
-    else if (!rt && ct) dst = Cc[g] + long(mm) * ldcc + nn;
-    else dst = Crc[g] + long(mm) * ldcc + nn;
-    if (beta != 0.f) v += beta * *dst;
-    *dst = v;
+    if (!(x.keep > 0.f)) v = 0.f;
+    if (beta != 0.f) v += beta * x.old;
+    *x.dst = v;
   }
 };
 
@@ -325,9 +376,11 @@ __device__ inline void issue_tile(Fetch4 (&f)[PER], const L& ld, const R& rs, co
     for (int j = 0; j < PER; ++j)
       if (S::live(j, tid)) ld.issue(rs, c.r[j], kp, f[j]);
   } else {
+    constexpr int KSTEP = NT / S::CH;  // k-rows between a thread's consecutive fetches
+    const auto ks = ld.kstage(c.r, k0 + tid / S::CH, g);
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-      if (S::live(j, tid)) ld.issue(rs, c.r, k0 + (tid + j * NT) / S::CH, f[j]);
+      if (S::live(j, tid)) ld.issue(rs, c.r, ks, j * KSTEP, f[j]);
   }
 }
 
@@ -434,20 +487,31 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
   }
 
   // Fragment (i, j) register r holds C(row 4*(lane/16) + r, col lane%16).
+  // Each row of fragments first issues every load its elements need
+  // (bias, mask, old value), then stores.
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < FM; ++i) {
+    const int mb = m0 + wm * WTM + i * 16 + (lane >> 4) * 4;
+    if (splits > 1) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = mb + r, n = n0 + wn * WTN + j * 16 + lr;
+          if (m < M && n < N) ws[((long(g) * splits + split) * M + m) * N + n] = acc[i][j][r];
+        }
+      continue;
+    }
+    EpAux x[FN][4];
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
-        const int n = n0 + wn * WTN + j * 16 + lr;
-        if (splits > 1) {
-          if (m < M && n < N) ws[((long(g) * splits + split) * M + m) * N + n] = acc[i][j][r];
-        } else {
-          ep.store(m, n, acc[i][j][r], g);
-        }
-      }
+      for (int r = 0; r < 4; ++r) x[j][r] = ep.aux(mb + r, n0 + wn * WTN + j * 16 + lr, g);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ep.store(mb + r, n0 + wn * WTN + j * 16 + lr, acc[i][j][r], x[j][r]);
+  }
 }
 
 // Sums split-K partials in split order and applies the epilogue.  Eight
@@ -474,7 +538,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
       for (int j = 0; j < 8; ++j) s += v[j];
     }
     for (; sp < splits; ++sp) s += p[long(sp) * MN];
-    ep.store(m, n, s, g);
+    ep.store(m, n, s, ep.aux(m, n, g));
   }
 }
 
@@ -537,20 +601,19 @@ inline void launch_cfg(const LA& la, const LB& lb, const EP& ep, float* ws, int 
 constexpr unsigned cfg_bit(int c) { return 1u << c; }
 constexpr unsigned kCfgAll = (1u << kNumCfg) - 1;
 
-// Plans and launches one GEMM.  ALLOWED restricts the tile shapes a call
-// site instantiates (each is a separate kernel); `ws_reserved` floats at the
-// top of the context workspace are in use by the caller.
+// Plan cache and tuning resources of the context (runtime.hip).
+bool ctx_capturing(ttrl_ctx* ctx);
+const GemmPlan* ctx_plan_find(ttrl_ctx* ctx, const std::string& key);
+void ctx_plan_store(ttrl_ctx* ctx, const std::string& key, const GemmPlan& p);
+float* ctx_tune_sink(ttrl_ctx* ctx, size_t bytes);
+bool ctx_tune_events(ttrl_ctx* ctx, hipEvent_t* a, hipEvent_t* b);
+std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_floats, unsigned allowed, int max_n);
+bool gemm_tuning_enabled();
+bool gemm_tuning_log();  // TTRL_GEMM_TUNE_LOG=1: print each tuned signature's candidates to stderr
+
 template <unsigned ALLOWED, class LA, class LB, class EP>
-inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int M, int N, int K, int groups,
-                    const char* name, long ws_reserved = 0) {
-  static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
-  if (M <= 0 || N <= 0 || groups <= 0) return TTRL_OK;
-  if (groups > kMaxGroups) return set_error(TTRL_EINVAL, "%s: at most %d groups", name, kMaxGroups);
-  if (long(groups) * M * N >= (1L << 31)) return set_error(TTRL_EINVAL, "%s: output too large", name);
-  long wsf = 0;
-  float* ws = ctx_workspace(ctx, &wsf);
-  GemmPlan p = plan_gemm(M, N, K, groups, wsf - ws_reserved, ALLOWED);
-  hipStream_t st = stream_of(ctx);
+inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
+                           const GemmPlan& p, hipStream_t st) {
   switch (p.cfg) {
     case T32x32: if constexpr ((ALLOWED & cfg_bit(T32x32)) != 0) launch_cfg<32, 32, 2, 2, 256>(la, lb, ep, ws, M, N, K, groups, p, st); break;
     case T64x32: if constexpr ((ALLOWED & cfg_bit(T64x32)) != 0) launch_cfg<64, 32, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
@@ -560,6 +623,73 @@ inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int
     case T128x64: if constexpr ((ALLOWED & cfg_bit(T128x64)) != 0) launch_cfg<128, 64, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
     default: if constexpr ((ALLOWED & cfg_bit(T64x128)) != 0) launch_cfg<64, 128, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
   }
+}
+
+// Times the model's leading candidates on the real operands, writing into a
+// sink instead of the output; returns the fastest (the model's first choice
+// if timing is unavailable).
+template <unsigned ALLOWED, class LA, class LB, class EP>
+inline GemmPlan tune_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, float* ws, long ws_limit, int M,
+                          int N, int K, int groups, hipStream_t st) {
+  const std::vector<GemmPlan> cands = plan_candidates(M, N, K, groups, ws_limit, ALLOWED, 10);
+  hipEvent_t e0, e1;
+  float* sink = ctx_tune_sink(ctx, size_t(ep.tune_span()) * sizeof(float));
+  if (cands.empty() || !sink || !ctx_tune_events(ctx, &e0, &e1)) return plan_gemm(M, N, K, groups, ws_limit, ALLOWED);
+  const EP tep = ep.tune_copy(sink);
+  GemmPlan best = cands.front();
+  float best_ms = 1e30f;
+  for (const GemmPlan& c : cands) {
+    launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);  // warm
+    if (hipEventRecord(e0, st) != hipSuccess) break;
+    for (int r = 0; r < 3; ++r) launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);
+    if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) break;
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) break;
+    if (gemm_tuning_log())
+      fprintf(stderr, "[ttrl gemm tune] M=%d N=%d K=%d G=%d  %dx%d tbk%d splits=%d  %.2f us\n", M, N, K, groups, c.bm,
+              c.bn, c.tbk, c.splits, ms * 1e3f / 3.f);
+    if (ms < best_ms) {
+      best_ms = ms;
+      best = c;
+    }
+  }
+  (void)hipGetLastError();
+  return best;
+}
+
+// Plans and launches one GEMM.  ALLOWED restricts the tile shapes a call
+// site instantiates (each is a separate kernel); `ws_reserved` floats at the
+// top of the context workspace are in use by the caller.  The first call of
+// a signature (kernel types and extents) outside graph capture times the
+// model's leading candidates and keeps the fastest for the context; a call
+// during capture uses the kept plan, or the model's, and keeps that.  Every
+// later call of the signature in the context runs the same plan, so eager
+// runs and graph replays sum split-K partials in the same order.
+template <unsigned ALLOWED, class LA, class LB, class EP>
+inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int M, int N, int K, int groups,
+                    const char* name, long ws_reserved = 0) {
+  static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
+  if (M <= 0 || N <= 0 || groups <= 0) return TTRL_OK;
+  if (groups > kMaxGroups) return set_error(TTRL_EINVAL, "%s: at most %d groups", name, kMaxGroups);
+  if (long(groups) * M * N >= (1L << 31)) return set_error(TTRL_EINVAL, "%s: output too large", name);
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  const long ws_limit = wsf - ws_reserved;
+  hipStream_t st = stream_of(ctx);
+  char keybuf[96];
+  snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%ld", M, N, K, groups, ws_limit);
+  const std::string key = std::string(__PRETTY_FUNCTION__) + keybuf;
+  GemmPlan p;
+  if (const GemmPlan* hit = ctx_plan_find(ctx, key)) {
+    p = *hit;
+  } else {
+    if (!ctx_capturing(ctx) && gemm_tuning_enabled())
+      p = tune_gemm<ALLOWED>(ctx, la, lb, ep, ws, ws_limit, M, N, K, groups, st);
+    else
+      p = plan_gemm(M, N, K, groups, ws_limit, ALLOWED);
+    ctx_plan_store(ctx, key, p);
+  }
+  launch_allowed<ALLOWED>(la, lb, ep, ws, M, N, K, groups, p, st);
   return check_launch(name);
 }
 
