@@ -25,26 +25,18 @@ def _rel(got, ref):
     return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
-def _device_gates(learner, frames):
+def _update_recording(learner, batch):
+    """Run one update while recording every layer's grouped outputs; returns
+    (metrics, records of the last pass): the device's own activations of
+    this update, so the oracle adopts exactly the gates the update used."""
     from ttrl_amd.engine import layers
-    from ttrl_amd.engine.autograd import Tensor, no_grad
-    from ttrl_amd.engine.tensor import to_device
-
     layers.RECORD = []
     try:
-        with no_grad():
-            q = learner.online(Tensor(to_device(frames, learner.device, np.uint8)))
-        recs = [r.numpy() for r in layers.RECORD]
+        m = learner.update(batch)
+        recs = [[y.numpy() for y in ys] for ys in layers.RECORD[-5:]]
     finally:
         layers.RECORD = None
-    names = ["conv0", "conv1", "conv2", "fc0"]
-    gates = {}
-    for name, r in zip(names, recs):
-        if r.ndim == 4:
-            b = frames.shape[0]
-            r = r.reshape(b, -1, r.shape[-1])
-        gates[name] = r > 0
-    return q.numpy(), gates
+    return m, recs
 
 
 @pytest.mark.parametrize("step_mode", ["graph", "eager"])
@@ -55,18 +47,20 @@ def test_dqn_update_matches_oracle(device, step_mode):
 
     learner, online, target = build_learner(device, seed=0, step_mode=step_mode)
     batch = dqn_batch(11, batch=32)
-    q_dev, gates = _device_gates(learner, batch["obs"])
     onet, tnet = qnet_to_oracle(online), qnet_to_oracle(target)
-    # reshape NHWC conv gates to the oracle's (B, OH, OW, C)
+    m, recs = _update_recording(learner, batch)
+    # recs: conv1, conv2, conv3, fc1 (ReLU outputs) and the Q layer, each over
+    # the groups [online(s), online(s'), target(s')]
     _, acts = qnet_forward(onet, batch["obs"])
-    for i in range(3):
-        gates[f"conv{i}"] = gates[f"conv{i}"].reshape(acts[i][1].shape)
-    q_next_dev, _ = _device_gates(learner, batch["next_obs"])
+    gates = {}
+    for i, name in enumerate(("conv0", "conv1", "conv2", "fc0")):
+        r = recs[i][0]
+        gates[name] = (r > 0).reshape(acts[i][1].shape)
+    q_dev, q_next_dev = recs[4][0], recs[4][1]
     ref = dqn_update(onet, tnet, batch, double=True, delta=1.0, lr=6.25e-5, eps=1.5e-4, gates=gates,
                      device_next_actions=np.argmax(q_next_dev, 1))
     assert _rel(q_dev, ref["q"]) < REL
     assert sum(ref["gate_stats"].decided_mismatch.values()) == 0
-    m = learner.update(batch)
     assert abs(m["loss"] - ref["loss"]) <= REL * abs(ref["loss"])
     assert abs(m["mean_q"] - ref["mean_q"]) <= REL * abs(ref["mean_q"])
     assert _rel(m["td_abs"], ref["td_abs"]) < REL

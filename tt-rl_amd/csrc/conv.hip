@@ -30,9 +30,12 @@
 namespace ttrl {
 
 // Tile shapes each convolution GEMM may use (each one is a separate kernel).
-constexpr unsigned kConvFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32) | cfg_bit(T64x64);
-constexpr unsigned kConvDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64);
-constexpr unsigned kConvDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32);
+constexpr unsigned kConvFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32) | cfg_bit(T64x64) |
+                                  cfg_bit(T32x32K2) | cfg_bit(T64x32K2) | cfg_bit(T64x64K2);
+constexpr unsigned kConvDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
+                                 cfg_bit(T32x32K2) | cfg_bit(T32x32K4) | cfg_bit(T32x64K2);
+constexpr unsigned kConvDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32) | cfg_bit(T32x32K2) |
+                                 cfg_bit(T64x32K2);
 
 struct ConvGeo {
   int B, C, H, W, O, KH, KW, S, P, OH, OW, u8;

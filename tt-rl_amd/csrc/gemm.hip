@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <vector>
 
@@ -40,7 +41,7 @@ std::vector<Costed> costed_plans(int M, int N, int K, int groups, long ws_floats
     const int stages = std::max(1, (K + t.tbk - 1) / t.tbk);
     const double lds = 4.0 * (t.bm + t.bn) * (t.tbk + 4);
     const double bpc = std::max(1.0, std::min(2.0, std::floor(160.0 * 1024.0 / lds)));
-    const double mfma = double(t.bm / t.wgm / 16) * (t.bn / t.wgn / 16) * (t.tbk / 4) * 32.0;
+    const double mfma = double(t.bm / t.wgm / 16) * (t.bn / t.wgn / 16) * (t.tbk / 4 / t.wgk) * 32.0;
     const double fetch = 4.0 * (t.bm + t.bn) * t.tbk / 64.0;
     for (int sp = 1; sp <= stages; ++sp) {
       const int spb = (stages + sp - 1) / sp;
@@ -86,6 +87,25 @@ std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_f
   return out;
 }
 
+bool gemm_forced(unsigned allowed, int M, int N, int K, int groups, long ws_floats, GemmPlan* out) {
+  const char* v = std::getenv("TTRL_GEMM_FORCE");
+  if (!v || !*v) return false;
+  int cfg = -1, splits = 0;
+  if (std::sscanf(v, "%d:%d", &cfg, &splits) < 1 || cfg < 0 || cfg >= kNumCfg || !(allowed & (1u << cfg)))
+    return false;
+  const TileDims t = tile_dims(cfg);
+  const int stages = std::max(1, (K + t.tbk - 1) / t.tbk);
+  GemmPlan p = plan_gemm(M, N, K, groups, ws_floats, 1u << cfg);
+  if (splits > 0) {
+    const int sp = std::min(splits, stages);
+    const int spb = (stages + sp - 1) / sp;
+    p = GemmPlan{cfg, t.bm, t.bn, t.tbk, (stages + spb - 1) / spb, spb * t.tbk};
+    if (p.splits > 1 && long(p.splits) * groups * M * N > ws_floats) p = plan_gemm(M, N, K, groups, ws_floats, 1u << cfg);
+  }
+  *out = p;
+  return true;
+}
+
 bool gemm_tuning_log() {
   static const bool on = [] {
     const char* v = std::getenv("TTRL_GEMM_TUNE_LOG");
@@ -107,11 +127,12 @@ const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const flo
 
 namespace {
 
-constexpr unsigned kMatmulCfgs = cfg_bit(T32x32) | cfg_bit(T64x64) | cfg_bit(T128x64);
-constexpr unsigned kLinFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64);
+constexpr unsigned kMatmulCfgs = cfg_bit(T32x32) | cfg_bit(T64x64) | cfg_bit(T128x64) | cfg_bit(T32x32K4);
+constexpr unsigned kSmallK = cfg_bit(T32x32K2) | cfg_bit(T32x32K4) | cfg_bit(T64x32K2) | cfg_bit(T32x64K2);
+constexpr unsigned kLinFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) | kSmallK;
 constexpr unsigned kLinDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
-                                cfg_bit(T128x64);
-constexpr unsigned kLinDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64);
+                                cfg_bit(T128x64) | kSmallK | cfg_bit(T64x64K2);
+constexpr unsigned kLinDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) | kSmallK;
 
 __global__ __launch_bounds__(256) void k_relu_mask(float* dst, const float* src, const float* mask, long n, long gs,
                                                    int groups) {

@@ -415,10 +415,15 @@ __device__ inline f32x4 lds_frag(const float* T, int row, int kk) {
 // registers before the MFMAs of stage s run, so global-memory latency is
 // paid once per workgroup rather than once per stage; both operands' loads
 // of a stage are in flight together.
-template <int BM, int BN, int WGM, int WGN, int TBK, class LA, class LB, class EP>
-__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, float* ws, int M, int N, int K,
-                                                         int kchunk, int splits) {
-  constexpr int NT = 64 * WGM * WGN;
+// WGK > 1 splits each LDS stage's k-blocks over WGK groups of wavefronts
+// (interleaved, k-block b to group b % WGK); their partial accumulators are
+// summed through LDS in group order before the epilogue, so a workgroup's
+// MFMA chain, fetch count per thread and LDS traffic per wavefront shrink by
+// WGK at the same tile size.
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA, class LB, class EP>
+__global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP ep, float* ws, int M, int N, int K,
+                                                               int kchunk, int splits) {
+  constexpr int NT = 64 * WGM * WGN * WGK;
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
   static_assert(FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "bad tile");
@@ -431,7 +436,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
   __shared__ __attribute__((aligned(16))) float Bs[LdsB::SIZE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave % WGM, wn = wave / WGM;
+  const int wk = wave / (WGM * WGN), wmn = wave - wk * (WGM * WGN);
+  const int wm = wmn % WGM, wn = wmn / WGM;
   const int g = blockIdx.z / splits, split = blockIdx.z - g * splits;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
   if (m0 >= ep.rows(g)) return;  // uniform per block: ragged residue classes
@@ -468,7 +474,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
     }
     const int kspan = min(TBK, kend - k0);  // zero padded past K
 #pragma unroll 2
-    for (int kb = 0; kb < kspan; kb += 16) {
+    for (int kb = wk * 16; kb < kspan; kb += 16 * WGK) {
       f32x4 a[FM], b[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i) a[i] = lds_frag<BM, TBK, LA::KCONTIG>(As, wm * WTM + i * 16 + lr, kb + lk);
@@ -487,6 +493,35 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(LA la, LB lb, EP ep, fl
   }
 
   // Fragment (i, j) register r holds C(row 4*(lane/16) + r, col lane%16).
+  if constexpr (WGK > 1) {
+    static_assert((WGK - 1) * BM * BN <= LdsA::SIZE, "k-group reduction must fit in the A tile");
+    float* red = As;
+    __syncthreads();  // every wavefront is done reading the tiles
+    if (wk > 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = wm * WTM + i * 16 + (lane >> 4) * 4 + r, col = wn * WTN + j * 16 + lr;
+            red[((wk - 1) * BM + row) * BN + col] = acc[i][j][r];
+          }
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int q = 0; q < WGK - 1; ++q)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = wm * WTM + i * 16 + (lane >> 4) * 4 + r, col = wn * WTN + j * 16 + lr;
+            acc[i][j][r] += red[(q * BM + row) * BN + col];
+          }
+  }
   // Each row of fragments first issues every load its elements need
   // (bias, mask, old value), then stores.
 #pragma unroll
@@ -543,21 +578,30 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
 }
 
 // Tile shapes: BM x BN output tile, TBK reduction slice per LDS stage.
-enum TileCfg { T32x32 = 0, T64x32 = 1, T32x64 = 2, T64x64 = 3, T128x32 = 4, T128x64 = 5, T64x128 = 6, kNumCfg = 7 };
+// K2 / K4: the same tile with 2 or 4 wavefront groups along k (8 or 16 wavefronts).
+enum TileCfg {
+  T32x32 = 0, T64x32 = 1, T32x64 = 2, T64x64 = 3, T128x32 = 4, T128x64 = 5, T64x128 = 6,
+  T32x32K2 = 7, T32x32K4 = 8, T64x32K2 = 9, T32x64K2 = 10, T64x64K2 = 11, kNumCfg = 12
+};
 
 struct TileDims {
-  int bm, bn, tbk, wgm, wgn;
+  int bm, bn, tbk, wgm, wgn, wgk;
 };
 
 inline TileDims tile_dims(int cfg) {
   switch (cfg) {
-    case T32x32: return {32, 32, 256, 2, 2};
-    case T64x32: return {64, 32, 128, 2, 2};
-    case T32x64: return {32, 64, 128, 2, 2};
-    case T64x64: return {64, 64, 128, 2, 2};
-    case T128x32: return {128, 32, 128, 4, 1};
-    case T128x64: return {128, 64, 64, 2, 2};
-    default: return {64, 128, 64, 2, 2};
+    case T32x32: return {32, 32, 256, 2, 2, 1};
+    case T64x32: return {64, 32, 128, 2, 2, 1};
+    case T32x64: return {32, 64, 128, 2, 2, 1};
+    case T64x64: return {64, 64, 128, 2, 2, 1};
+    case T128x32: return {128, 32, 128, 4, 1, 1};
+    case T128x64: return {128, 64, 64, 2, 2, 1};
+    case T64x128: return {64, 128, 64, 2, 2, 1};
+    case T32x32K2: return {32, 32, 256, 2, 2, 2};
+    case T32x32K4: return {32, 32, 256, 2, 2, 4};
+    case T64x32K2: return {64, 32, 128, 2, 2, 2};
+    case T32x64K2: return {32, 64, 128, 2, 2, 2};
+    default: return {64, 64, 128, 2, 2, 2};
   }
 }
 
@@ -580,12 +624,12 @@ float* ctx_workspace(ttrl_ctx* ctx, long* floats);
 const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const float* mask, long n, long gs,
                                       int groups, long* reserved, int* rc);
 
-template <int BM, int BN, int WGM, int WGN, int TBK, class LA, class LB, class EP>
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA, class LB, class EP>
 inline void launch_cfg(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
                        const GemmPlan& p, hipStream_t st) {
   dim3 grid(ceil_div(M, BM), ceil_div(N, BN), unsigned(groups * p.splits));
-  hipLaunchKernelGGL((k_gemm<BM, BN, WGM, WGN, TBK, LA, LB, EP>), grid, dim3(64 * WGM * WGN), 0, st, la, lb, ep, ws,
-                     M, N, K, p.kchunk, p.splits);
+  hipLaunchKernelGGL((k_gemm<BM, BN, WGM, WGN, WGK, TBK, LA, LB, EP>), grid, dim3(64 * WGM * WGN * WGK), 0, st, la,
+                     lb, ep, ws, M, N, K, p.kchunk, p.splits);
   if (p.splits > 1) {
     const long total = long(groups) * M * N;
     unsigned blocks = unsigned(total / 256 + 1);
@@ -610,19 +654,34 @@ bool ctx_tune_events(ttrl_ctx* ctx, hipEvent_t* a, hipEvent_t* b);
 std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_floats, unsigned allowed, int max_n);
 bool gemm_tuning_enabled();
 bool gemm_tuning_log();  // TTRL_GEMM_TUNE_LOG=1: print each tuned signature's candidates to stderr
+// TTRL_GEMM_FORCE="cfg[:splits]" (read on every call, for tests): run that
+// tile shape wherever a call site allows it, bypassing the plan cache.
+bool gemm_forced(unsigned allowed, int M, int N, int K, int groups, long ws_floats, GemmPlan* out);
 
 template <unsigned ALLOWED, class LA, class LB, class EP>
 inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
                            const GemmPlan& p, hipStream_t st) {
+#define TTRL_CFG(C, BM, BN, WGM, WGN, WGK, TBK)                                                          \
+  case C:                                                                                               \
+    if constexpr ((ALLOWED & cfg_bit(C)) != 0)                                                          \
+      launch_cfg<BM, BN, WGM, WGN, WGK, TBK>(la, lb, ep, ws, M, N, K, groups, p, st);                   \
+    break;
   switch (p.cfg) {
-    case T32x32: if constexpr ((ALLOWED & cfg_bit(T32x32)) != 0) launch_cfg<32, 32, 2, 2, 256>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T64x32: if constexpr ((ALLOWED & cfg_bit(T64x32)) != 0) launch_cfg<64, 32, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T32x64: if constexpr ((ALLOWED & cfg_bit(T32x64)) != 0) launch_cfg<32, 64, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T64x64: if constexpr ((ALLOWED & cfg_bit(T64x64)) != 0) launch_cfg<64, 64, 2, 2, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T128x32: if constexpr ((ALLOWED & cfg_bit(T128x32)) != 0) launch_cfg<128, 32, 4, 1, 128>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    case T128x64: if constexpr ((ALLOWED & cfg_bit(T128x64)) != 0) launch_cfg<128, 64, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
-    default: if constexpr ((ALLOWED & cfg_bit(T64x128)) != 0) launch_cfg<64, 128, 2, 2, 64>(la, lb, ep, ws, M, N, K, groups, p, st); break;
+    TTRL_CFG(T32x32, 32, 32, 2, 2, 1, 256)
+    TTRL_CFG(T64x32, 64, 32, 2, 2, 1, 128)
+    TTRL_CFG(T32x64, 32, 64, 2, 2, 1, 128)
+    TTRL_CFG(T64x64, 64, 64, 2, 2, 1, 128)
+    TTRL_CFG(T128x32, 128, 32, 4, 1, 1, 128)
+    TTRL_CFG(T128x64, 128, 64, 2, 2, 1, 64)
+    TTRL_CFG(T64x128, 64, 128, 2, 2, 1, 64)
+    TTRL_CFG(T32x32K2, 32, 32, 2, 2, 2, 256)
+    TTRL_CFG(T32x32K4, 32, 32, 2, 2, 4, 256)
+    TTRL_CFG(T64x32K2, 64, 32, 2, 2, 2, 128)
+    TTRL_CFG(T32x64K2, 32, 64, 2, 2, 2, 128)
+    TTRL_CFG(T64x64K2, 64, 64, 2, 2, 2, 128)
+    default: break;
   }
+#undef TTRL_CFG
 }
 
 // Times the model's leading candidates on the real operands, writing into a
@@ -680,6 +739,10 @@ inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int
   snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%ld", M, N, K, groups, ws_limit);
   const std::string key = std::string(__PRETTY_FUNCTION__) + keybuf;
   GemmPlan p;
+  if (gemm_forced(ALLOWED, M, N, K, groups, ws_limit, &p)) {
+    launch_allowed<ALLOWED>(la, lb, ep, ws, M, N, K, groups, p, st);
+    return check_launch(name);
+  }
   if (const GemmPlan* hit = ctx_plan_find(ctx, key)) {
     p = *hit;
   } else {

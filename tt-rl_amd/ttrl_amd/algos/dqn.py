@@ -25,6 +25,7 @@ from ttrl_amd import _lib
 from ttrl_amd.algos.grads import grad_sq_device
 from ttrl_amd.engine.autograd import Tensor, no_grad
 from ttrl_amd.engine.conv import Conv2d
+from ttrl_amd.engine import layers as layers_mod
 from ttrl_amd.engine.layers import Linear, ReLU
 from ttrl_amd.engine.ops.fused import dqn_td_loss, linear_node
 from ttrl_amd.engine.optim import Adam
@@ -138,6 +139,8 @@ def q_forward_multi(nets, inputs, tape_group: int | None = 0):
                      _lib.ptrs(x.data.ptr for x in xs), _lib.ptrs(c.weight.data.ptr for c in group),
                      _lib.ptrs(None if c.bias is None else c.bias.data.ptr for c in group),
                      _lib.ptrs(y.ptr for y in ys), C.c_float(layer.input_scale), int(fuse))
+            if layers_mod.RECORD is not None:  # every group's output of this layer, in launch order
+                layers_mod.RECORD.append(list(ys))
             xs = [group[g].node(xs[g], ys[g], fuse) if g == tape_group else Tensor(ys[g]) for g in range(G)]
         elif isinstance(layer, Linear):
             M, K = (int(d) for d in xs[0].shape)
@@ -148,6 +151,8 @@ def q_forward_multi(nets, inputs, tape_group: int | None = 0):
                      _lib.ptrs(w.data.ptr for w in weights),
                      _lib.ptrs(None if lin.bias is None else lin.bias.data.ptr for lin in group),
                      _lib.ptrs(y.ptr for y in ys), int(fuse))
+            if layers_mod.RECORD is not None:
+                layers_mod.RECORD.append(list(ys))
             xs = [linear_node(xs[g], weights[g], group[g].bias, ys[g], relu=fuse) if g == tape_group
                   else Tensor(ys[g]) for g in range(G)]
         else:
