@@ -47,9 +47,9 @@ struct ConvGeo {
   int ih0[kMaxGroups], iw0[kMaxGroups], nh[kMaxGroups], nw[kMaxGroups];
   FDiv d_nhnw[kMaxGroups], d_nw[kMaxGroups];
 
-  __device__ inline int kp() const { return C * KH * KW; }
+  __device__ __forceinline__ int kp() const { return C * KH * KW; }
   // (c, kh, kw) of patch index k, in this layer's k order.
-  __device__ inline void split_k(int k, int& c, int& kh, int& kw) const {
+  __device__ __forceinline__ void split_k(int k, int& c, int& kh, int& kw) const {
     if (u8) {
       c = d_khkw.div(k);
       const int t = k - c * KH * KW;
@@ -62,7 +62,7 @@ struct ConvGeo {
       kw = tap - kh * KW;
     }
   }
-  __device__ inline void split_m(int m, int& b, int& oh, int& ow) const {
+  __device__ __forceinline__ void split_m(int m, int& b, int& oh, int& ow) const {
     b = d_ohow.div(m);
     const int rem = m - b * OH * OW;
     oh = d_ow.div(rem);
@@ -71,7 +71,7 @@ struct ConvGeo {
 };
 
 // Patch element (m, k) of the input: element offset, or -1 outside the image.
-__device__ inline long patch_index(const ConvGeo& g, int m, int k) {
+__device__ __forceinline__ long patch_index(const ConvGeo& g, int m, int k) {
   if (m >= g.M || k >= g.kp()) return -1;
   int b, oh, ow, c, kh, kw;
   g.split_m(m, b, oh, ow);
@@ -83,7 +83,7 @@ __device__ inline long patch_index(const ConvGeo& g, int m, int k) {
 }
 
 // One patch element, any layout (the general path).
-__device__ inline float patch_elem(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int m, int k) {
+__device__ __forceinline__ float patch_elem(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int m, int k) {
   const long idx = patch_index(g, m, k);
   if (g.u8) return __uint_as_float(ld_u8(rs, idx < 0 ? kBad : uint32_t(idx)));
   return ld_f1(rs, idx < 0 ? kBad : uint32_t(idx) * 4u);
@@ -110,7 +110,7 @@ struct PixelPos {
   uint32_t base;
   int ih0, iw0;
 };
-__device__ inline PixelPos pixel_pos(const ConvGeo& g, int m) {
+__device__ __forceinline__ PixelPos pixel_pos(const ConvGeo& g, int m) {
   if (m >= g.M) return PixelPos{kBad, -(1 << 28), 0};
   int b, oh, ow;
   g.split_m(m, b, oh, ow);
@@ -125,7 +125,7 @@ struct TapPos {
   uint32_t off;
   int kh, kw;
 };
-__device__ inline TapPos tap_pos(const ConvGeo& g, int k) {
+__device__ __forceinline__ TapPos tap_pos(const ConvGeo& g, int k) {
   if (k >= g.kp()) return TapPos{kBad, 0, 0};
   int c, kh, kw;
   g.split_k(k, c, kh, kw);
@@ -134,7 +134,7 @@ __device__ inline TapPos tap_pos(const ConvGeo& g, int k) {
 }
 
 // Starts the load of patch chunk (pixel, tap) in the given mode.
-__device__ inline void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int mode, const PixelPos& px,
+__device__ __forceinline__ void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int mode, const PixelPos& px,
                                    const TapPos& tp, Fetch4& f) {
   uint32_t off = px.base + tp.off;
   if (g.P != 0) {  // borders: the tap may fall outside the image
@@ -155,15 +155,15 @@ struct LdConvFwd {
   int mode;
   struct Row { PixelPos px; };  // the general mode keeps the pixel index in px.base
   struct Kp { TapPos tp; int k; };
-  __device__ inline int fmt() const {
+  __device__ __forceinline__ int fmt() const {
     return mode == kPatchU8Word ? kU8Word : (mode == kPatchGeneral && g.u8 ? kU8Each : kF32);
   }
-  __device__ inline __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
-  __device__ inline Row row(int m, int) const {
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
+  __device__ __forceinline__ Row row(int m, int) const {
     return mode == kPatchGeneral ? Row{PixelPos{uint32_t(m), 0, 0}} : Row{pixel_pos(g, m)};
   }
-  __device__ inline Kp kpos(int k, int) const { return Kp{mode == kPatchGeneral ? TapPos{} : tap_pos(g, k), k}; }
-  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
+  __device__ __forceinline__ Kp kpos(int k, int) const { return Kp{mode == kPatchGeneral ? TapPos{} : tap_pos(g, k), k}; }
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
     if (mode != kPatchGeneral) {
       patch_issue(rs, g, mode, r.px, kp.tp, f);
       return;
@@ -184,16 +184,16 @@ struct LdConvPatchT {
   int ones;
   struct Row { TapPos tp; int r; bool whole; };
   struct Ks { int m; };
-  __device__ inline int fmt() const {
+  __device__ __forceinline__ int fmt() const {
     return mode == kPatchU8Word ? kU8Word : (g.u8 ? kU8Each : kF32);
   }
-  __device__ inline __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
-  __device__ inline Row row(int r, int) const {
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
+  __device__ __forceinline__ Row row(int r, int) const {
     const bool whole = mode != kPatchGeneral && r + 3 < g.kp();
     return Row{whole ? tap_pos(g, r) : TapPos{}, r, whole};
   }
-  __device__ inline Ks kstage(const Row&, int m, int) const { return Ks{m}; }
-  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Ks& ks, int dm, Fetch4& f) const {
+  __device__ __forceinline__ Ks kstage(const Row&, int m, int) const { return Ks{m}; }
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Ks& ks, int dm, Fetch4& f) const {
     const int m = ks.m + dm;
     if (r.whole) {
       patch_issue(rs, g, mode, pixel_pos(g, m), r.tp, f);
@@ -224,10 +224,10 @@ struct LdConvDxA {
   uint32_t dybytes;
   struct Row { int base, ohc, owc; };  // base = element offset of dZ(b, ohc, owc, 0)
   struct Kp { int off, jh, jw; bool v; int k, ch, cw; };
-  __device__ inline int fmt() const { return kF32; }
-  __device__ inline __amdgpu_buffer_rsrc_t res(int) const { return make_res(dy, dybytes); }
-  __device__ inline int cls(int grp) const { return g.cls0 + grp; }
-  __device__ inline Row row(int r, int grp) const {
+  __device__ __forceinline__ int fmt() const { return kF32; }
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int) const { return make_res(dy, dybytes); }
+  __device__ __forceinline__ int cls(int grp) const { return g.cls0 + grp; }
+  __device__ __forceinline__ Row row(int r, int grp) const {
     if (r >= g.B * g.nh[grp] * g.nw[grp]) return Row{0, -(1 << 28), 0};
     const int b = g.d_nhnw[grp].div(r);
     const int rem = r - b * g.nh[grp] * g.nw[grp];
@@ -237,7 +237,7 @@ struct LdConvDxA {
     const int owc = g.d_s.div(g.iw0[grp] + g.S * j + g.P - cw);
     return Row{((b * g.OH + ohc) * g.OW + owc) * g.O, ohc, owc};
   }
-  __device__ inline Kp kpos(int k, int grp) const {
+  __device__ __forceinline__ Kp kpos(int k, int grp) const {
     const int c = cls(grp), ch = c / g.S, cw = c - ch * g.S;
     if (k >= g.TH * g.TW * g.O) return Kp{0, 0, 0, false, k, ch, cw};
     const int jt = g.d_o.div(k), o = k - jt * g.O;
@@ -245,7 +245,7 @@ struct LdConvDxA {
     const bool v = ch + g.S * jh < g.KH && cw + g.S * jw < g.KW;
     return Kp{o - (jh * g.OW + jw) * g.O, jh, jw, v, k, ch, cw};
   }
-  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
     if ((g.O & 3) == 0) {  // the four k share one tap and output pixel
       const int oh = r.ohc - kp.jh, ow = r.owc - kp.jw;
       const bool in = kp.v && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
@@ -278,10 +278,10 @@ struct LdConvDxB {
   uint32_t wbytes;
   struct Row { uint32_t off; int c; };  // byte offset of Wt[(0,0,c)][0], kBad past C
   struct Kp { uint32_t off; int k, ch, cw; };
-  __device__ inline int fmt() const { return kF32; }
-  __device__ inline __amdgpu_buffer_rsrc_t res(int) const { return make_res(wt, wbytes); }
-  __device__ inline Row row(int c, int) const { return Row{c < g.C ? uint32_t(c * g.O) * 4u : kBad, c}; }
-  __device__ inline Kp kpos(int k, int grp) const {
+  __device__ __forceinline__ int fmt() const { return kF32; }
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int) const { return make_res(wt, wbytes); }
+  __device__ __forceinline__ Row row(int c, int) const { return Row{c < g.C ? uint32_t(c * g.O) * 4u : kBad, c}; }
+  __device__ __forceinline__ Kp kpos(int k, int grp) const {
     const int c = g.cls0 + grp, ch = c / g.S, cw = c - ch * g.S;
     if (k >= g.TH * g.TW * g.O) return Kp{kBad, k, ch, cw};
     const int jt = g.d_o.div(k), o = k - jt * g.O;
@@ -290,7 +290,7 @@ struct LdConvDxB {
     const bool v = kh < g.KH && kw < g.KW;
     return Kp{v ? uint32_t((kh * g.KW + kw) * g.C * g.O + o) * 4u : kBad, k, ch, cw};
   }
-  __device__ inline void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
     if ((g.O & 3) == 0) {
       f.v = ld_f4(rs, r.off + kp.off);
       return;
@@ -319,7 +319,7 @@ struct EpConvDx {
   float* dx;
   const float* xmask;
   float alpha, beta;
-  __device__ inline int rows(int grp) const { return g.B * g.nh[grp] * g.nw[grp]; }
+  __device__ __forceinline__ int rows(int grp) const { return g.B * g.nh[grp] * g.nw[grp]; }
   __host__ long tune_span() const { return long(g.B) * g.H * g.W * g.C + 64; }
   __host__ EpConvDx tune_copy(float* sink) const {
     EpConvDx e = *this;
@@ -327,25 +327,40 @@ struct EpConvDx {
     e.beta = 0.f;
     return e;
   }
-  __device__ inline EpAux aux(int r, int c, int grp) const {
-    EpAux x{nullptr, 0.f, 1.f, 0.f};
-    if (r >= rows(grp) || c >= g.C) return x;
-    const int b = g.d_nhnw[grp].div(r);
-    const int rem = r - b * g.nh[grp] * g.nw[grp];
-    const int i = g.d_nw[grp].div(rem), j = rem - i * g.nw[grp];
-    const int ih = g.ih0[grp] + g.S * i, iw = g.iw0[grp] + g.S * j;
-    const long idx = ((long(b) * g.H + ih) * g.W + iw) * g.C + c;
-    x.dst = dx + idx;
-    if (xmask) x.keep = xmask[idx];
-    if (beta != 0.f) x.old = *x.dst;
-    return x;
-  }
-  __device__ inline void store(int, int, float acc, const EpAux& x) const {
-    if (!x.dst) return;
-    float v = alpha * acc;
-    if (!(x.keep > 0.f)) v = 0.f;
-    if (beta != 0.f) v += beta * x.old;
-    *x.dst = v;
+  // One residue class's epilogue with its tables bound.
+  struct Bound {
+    int rows, C, H, W, S, nw, ih0, iw0;
+    FDiv d_nhnw, d_nw;
+    float* dx;
+    const float* xmask;
+    float alpha, beta;
+    __device__ __forceinline__ EpAux aux(int r, int c) const {
+      EpAux x{nullptr, 0.f, 1.f, 0.f};
+      if (r >= rows || c >= C) return x;
+      const int b = d_nhnw.div(r);
+      const int rem = r - b * d_nhnw.d;
+      const int i = d_nw.div(rem), j = rem - i * nw;
+      const int ih = ih0 + S * i, iw = iw0 + S * j;
+      const long idx = ((long(b) * H + ih) * W + iw) * C + c;
+      x.dst = dx + idx;
+      if (xmask) x.keep = gload(xmask + idx);
+      if (beta != 0.f) x.old = gload(x.dst);
+      return x;
+    }
+    __device__ __forceinline__ void store(int, int, float acc, const EpAux& x) const {
+      if (!x.dst) return;
+      float v = alpha * acc;
+      if (!(x.keep > 0.f)) v = 0.f;
+      if (beta != 0.f) v += beta * x.old;
+      *x.dst = v;
+    }
+  };
+  __device__ __forceinline__ Bound bind(int grp) const {
+    float* d = dx;
+    const float* xm = xmask;
+    pin(d, xm);
+    return Bound{rows(grp), g.C, g.H, g.W, g.S, g.nw[grp], g.ih0[grp], g.iw0[grp], g.d_nhnw[grp], g.d_nw[grp],
+                 d, xm, alpha, beta};
   }
 };
 
