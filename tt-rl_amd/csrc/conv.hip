@@ -327,40 +327,41 @@ struct EpConvDx {
     e.beta = 0.f;
     return e;
   }
-  // One residue class's epilogue with its tables bound.
+  // One residue class's epilogue with its tables bound: buffer loads and
+  // stores, an element outside the class reading zero and storing nothing.
   struct Bound {
     int rows, C, H, W, S, nw, ih0, iw0;
     FDiv d_nhnw, d_nw;
-    float* dx;
-    const float* xmask;
+    __amdgpu_buffer_rsrc_t rdx, rxm, rold;  // rxm, rold empty when absent (read zero)
+    bool has_xm;
     float alpha, beta;
     __device__ __forceinline__ EpAux aux(int r, int c) const {
-      EpAux x{nullptr, 0.f, 1.f, 0.f};
-      if (r >= rows || c >= C) return x;
+      EpAux x{nullptr, 0.f, 1.f, 0.f, kBad};
       const int b = d_nhnw.div(r);
       const int rem = r - b * d_nhnw.d;
       const int i = d_nw.div(rem), j = rem - i * nw;
       const int ih = ih0 + S * i, iw = iw0 + S * j;
-      const long idx = ((long(b) * H + ih) * W + iw) * C + c;
-      x.dst = dx + idx;
-      if (xmask) x.keep = gload(xmask + idx);
-      if (beta != 0.f) x.old = gload(x.dst);
+      x.off = (r < rows && c < C) ? uint32_t(((b * H + ih) * W + iw) * C + c) * 4u : kBad;
+      x.keep = ld_f1(rxm, x.off);
+      x.old = ld_f1(rold, x.off);
       return x;
     }
     __device__ __forceinline__ void store(int, int, float acc, const EpAux& x) const {
-      if (!x.dst) return;
       float v = alpha * acc;
-      if (!(x.keep > 0.f)) v = 0.f;
-      if (beta != 0.f) v += beta * x.old;
-      *x.dst = v;
+      if (has_xm && !(x.keep > 0.f)) v = 0.f;
+      v += beta * x.old;
+      st_f1(rdx, x.off, v);
     }
   };
-  __device__ __forceinline__ Bound bind(int grp) const {
+  template <class F>
+  __device__ __forceinline__ void with_bound(int grp, F&& f) const {
     float* d = dx;
     const float* xm = xmask;
     pin(d, xm);
-    return Bound{rows(grp), g.C, g.H, g.W, g.S, g.nw[grp], g.ih0[grp], g.iw0[grp], g.d_nhnw[grp], g.d_nw[grp],
-                 d, xm, alpha, beta};
+    const uint32_t bytes = uint32_t(long(g.B) * g.H * g.W * g.C * 4);
+    f(Bound{rows(grp), g.C, g.H, g.W, g.S, g.nw[grp], g.ih0[grp], g.iw0[grp], g.d_nhnw[grp], g.d_nw[grp],
+            make_res(d, bytes), make_res(xm, xm ? bytes : 0u), make_res(d, beta != 0.f ? bytes : 0u), xm != nullptr,
+            alpha, beta});
   }
 };
 

@@ -292,9 +292,14 @@ struct LdRowKCat {
 // (+ beta*old); the mask (the ReLU output of the layer whose gradient this
 // is) applies to the leading block and is indexed like it.
 struct EpAux {
-  float* dst;
+  float* dst;  // pointer path
   float add, keep, old;
+  uint32_t off;  // buffer path: byte offset, kBad for an element outside the output
 };
+
+__device__ __forceinline__ void st_f1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+}
 
 struct EpStore {
   int M = 0, N = 0;
@@ -331,7 +336,46 @@ struct EpStore {
   // the bias, the mask and, when beta != 0, the old value) comes from aux();
   // the kernel issues these loads for a batch of elements before it stores
   // any of them.
-  struct Bound {
+  // One group's epilogue, its pointers bound in scalar registers, in one
+  // of two forms chosen once per workgroup.  Everything element (m, n) reads
+  // besides the accumulator (the bias, the mask and, when beta != 0, the old
+  // value) comes from aux(); the kernel issues these loads for a batch of
+  // elements before it stores any of them.
+  //
+  // Fast: one output block (no row or column tail) under 2^30 bytes, read
+  // and written with buffer instructions.  An out-of-range offset reads zero
+  // and drops the store, so an element needs no branch, and the loads of a
+  // batch are all in flight before the first store waits on them.
+  // The three reads are unconditional: an absent bias, mask or old value
+  // (beta == 0) has an empty resource and reads zero without a memory access.
+  struct Fast {
+    int M, N;
+    uint32_t ldc;
+    float alpha, beta;
+    int relu, clamp_col;
+    float lo, hi;
+    bool has_mask;
+    __amdgpu_buffer_rsrc_t rc, rb, rm, ro;
+
+    __device__ __forceinline__ EpAux aux(int m, int n) const {
+      EpAux x{nullptr, 0.f, 1.f, 0.f, kBad};
+      x.off = (m < M && n < N) ? (uint32_t(m) * ldc + uint32_t(n)) * 4u : kBad;
+      x.add = ld_f1(rb, uint32_t(n) * 4u);
+      x.keep = ld_f1(rm, x.off);
+      x.old = ld_f1(ro, x.off);
+      return x;
+    }
+    __device__ __forceinline__ void store(int, int n, float acc, const EpAux& x) const {
+      float v = alpha * acc + x.add;
+      if (relu) v = v > 0.f ? v : 0.f;
+      if (n >= clamp_col) v = fminf(fmaxf(v, lo), hi);
+      if (has_mask && !(x.keep > 0.f)) v = 0.f;
+      v += beta * x.old;
+      st_f1(rc, x.off, v);
+    }
+  };
+  // General: row and column tails in separate blocks, through pointers.
+  struct Split {
     int M, N;
     float* C;
     float* Cr;
@@ -347,7 +391,7 @@ struct EpStore {
     const float* mask;
 
     __device__ __forceinline__ EpAux aux(int m, int n) const {
-      EpAux x{nullptr, 0.f, 1.f, 0.f};
+      EpAux x{nullptr, 0.f, 1.f, 0.f, kBad};
       if (m >= M || n >= N) return x;
       const bool rt = m >= rsplit, ct = n >= csplit;
       const int mm = rt ? m - rsplit : m;
@@ -374,7 +418,9 @@ struct EpStore {
       *x.dst = v;
     }
   };
-  __device__ __forceinline__ Bound bind(int g) const {
+  // Calls f with group g's bound epilogue.
+  template <class F>
+  __device__ __forceinline__ void with_bound(int g, F&& f) const {
     float* c0 = C[g];
     float* c1 = Cr[g];
     float* c2 = Cc[g];
@@ -383,8 +429,16 @@ struct EpStore {
     const float* b1 = bias2[g];
     const float* mk = mask[g];
     asm volatile("" : "+s"(c0), "+s"(c1), "+s"(c2), "+s"(c3), "+s"(b0), "+s"(b1), "+s"(mk));
-    return Bound{M, N, c0, c1, c2, c3, ldc, ldcc, rsplit, csplit, alpha, beta, alpha_r, b0, b1, relu, clamp_col, lo, hi,
-                 mk};
+    const long cb = M > 0 ? (long(M - 1) * ldc + N) * 4 : 0;
+    if (rsplit >= M && csplit >= N && cb < kMaxOperandBytes) {
+      const uint32_t cbytes = uint32_t(cb);
+      f(Fast{M, N, uint32_t(ldc), alpha, beta, relu, clamp_col, lo, hi, mk != nullptr, make_res(c0, cbytes),
+             make_res(b0, b0 ? uint32_t(N) * 4u : 0u), make_res(mk, mk ? cbytes : 0u),
+             make_res(c0, beta != 0.f ? cbytes : 0u)});
+    } else {
+      f(Split{M, N, c0, c1, c2, c3, ldc, ldcc, rsplit, csplit, alpha, beta, alpha_r, b0, b1, relu, clamp_col, lo, hi,
+              mk});
+    }
   }
 };
 
@@ -669,11 +723,10 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
   }
   // Each row of fragments first issues every load its elements need
   // (bias, mask, old value), then stores.
-  const auto eb = ep.bind(g);
+  if (splits > 1) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int mb = m0 + wm * WTM + i * 16 + (lane >> 4) * 4;
-    if (splits > 1) {
+    for (int i = 0; i < FM; ++i) {
+      const int mb = m0 + wm * WTM + i * 16 + (lane >> 4) * 4;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -681,18 +734,24 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
           const int m = mb + r, n = n0 + wn * WTN + j * 16 + lr;
           if (m < M && n < N) ws[((long(g) * splits + split) * M + m) * N + n] = acc[i][j][r];
         }
-      continue;
     }
-    EpAux x[FN][4];
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[j][r] = eb.aux(mb + r, n0 + wn * WTN + j * 16 + lr);
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) eb.store(mb + r, n0 + wn * WTN + j * 16 + lr, acc[i][j][r], x[j][r]);
+    return;
   }
+  ep.with_bound(g, [&](const auto& eb) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int mb = m0 + wm * WTM + i * 16 + (lane >> 4) * 4;
+      EpAux x[FN][4];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[j][r] = eb.aux(mb + r, n0 + wn * WTN + j * 16 + lr);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) eb.store(mb + r, n0 + wn * WTN + j * 16 + lr, acc[i][j][r], x[j][r]);
+    }
+  });
 }
 
 // Sums split-K partials in split order and applies the epilogue; group
@@ -703,24 +762,25 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
   const int g = blockIdx.y;
   const int MN = M * N;
   const int rows = ep.rows(g);
-  const auto eb = ep.bind(g);
   const float* wg = ws + long(g) * splits * MN;
-  for (int mn = blockIdx.x * 256 + threadIdx.x; mn < MN; mn += gridDim.x * 256) {
-    const int m = dn.div(mn), n = mn - m * N;
-    if (m >= rows) continue;
-    const float* p = wg + mn;
-    float s = 0.f;
-    int sp = 0;
-    for (; sp + 8 <= splits; sp += 8) {
-      float v[8];
+  ep.with_bound(g, [&](const auto& eb) {
+    for (int mn = blockIdx.x * 256 + threadIdx.x; mn < MN; mn += gridDim.x * 256) {
+      const int m = dn.div(mn), n = mn - m * N;
+      if (m >= rows) continue;
+      const float* p = wg + mn;
+      float s = 0.f;
+      int sp = 0;
+      for (; sp + 8 <= splits; sp += 8) {
+        float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = gload(p + long(sp + j) * MN);
+        for (int j = 0; j < 8; ++j) v[j] = gload(p + long(sp + j) * MN);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s += v[j];
+        for (int j = 0; j < 8; ++j) s += v[j];
+      }
+      for (; sp < splits; ++sp) s += gload(p + long(sp) * MN);
+      eb.store(m, n, s, eb.aux(m, n));
     }
-    for (; sp < splits; ++sp) s += gload(p + long(sp) * MN);
-    eb.store(m, n, s, eb.aux(m, n));
-  }
+  });
 }
 
 // Tile shapes: BM x BN output tile, TBK reduction slice per LDS stage.
