@@ -46,33 +46,40 @@ struct ConvGeo {
   int cls0;
   int ih0[kMaxGroups], iw0[kMaxGroups], nh[kMaxGroups], nw[kMaxGroups];
   FDiv d_nhnw[kMaxGroups], d_nw[kMaxGroups];
+};
 
-  __device__ __forceinline__ int kp() const { return C * KH * KW; }
-  // (c, kh, kw) of patch index k, in this layer's k order.
-  __device__ __forceinline__ void split_k(int k, int& c, int& kh, int& kw) const {
-    if (u8) {
-      c = d_khkw.div(k);
-      const int t = k - c * KH * KW;
-      kh = d_kw.div(t);
-      kw = t - kh * KW;
-    } else {
-      const int tap = d_c.div(k);
-      c = k - tap * C;
-      kh = d_kw.div(tap);
-      kw = tap - kh * KW;
-    }
-  }
+// The forward / weight-gradient view of a layer on the device: extents and
+// the divisions that split a pixel index m into (b, oh, ow) and a patch
+// index k into (c, kh, kw), 23 words pinned in scalar registers.
+struct ConvCore {
+  int M, S, P, H, W, C, u8, kp, KW, ohow, OW;
+  FDiv dm1, dm2;  // m / (OH*OW), then / OW
+  FDiv dk1, dk2;  // k / (KH*KW) (uint8 NCHW: c first) or k / C (NHWC: tap first), then / KW
+
   __device__ __forceinline__ void split_m(int m, int& b, int& oh, int& ow) const {
-    b = d_ohow.div(m);
-    const int rem = m - b * OH * OW;
-    oh = d_ow.div(rem);
+    b = dm1.div(m);
+    const int rem = m - b * ohow;
+    oh = dm2.div(rem);
     ow = rem - oh * OW;
+  }
+  __device__ __forceinline__ void split_k(int k, int& c, int& kh, int& kw) const {
+    const int first = dk1.div(k);
+    const int rest = k - first * dk1.d;
+    const int tap = u8 ? rest : first;
+    c = u8 ? first : rest;
+    kh = dk2.div(tap);
+    kw = tap - kh * KW;
   }
 };
 
+__device__ __forceinline__ ConvCore conv_core(const ConvGeo& g) {
+  return ConvCore{g.M, g.S, g.P, g.H, g.W, g.C, g.u8, g.C * g.KH * g.KW, g.KW, g.OH * g.OW, g.OW,
+                  g.d_ohow, g.d_ow, g.u8 ? g.d_khkw : g.d_c, g.d_kw};
+}
+
 // Patch element (m, k) of the input: element offset, or -1 outside the image.
-__device__ __forceinline__ long patch_index(const ConvGeo& g, int m, int k) {
-  if (m >= g.M || k >= g.kp()) return -1;
+__device__ __forceinline__ long patch_index(const ConvCore& g, int m, int k) {
+  if (m >= g.M || k >= g.kp) return -1;
   int b, oh, ow, c, kh, kw;
   g.split_m(m, b, oh, ow);
   g.split_k(k, c, kh, kw);
@@ -83,7 +90,7 @@ __device__ __forceinline__ long patch_index(const ConvGeo& g, int m, int k) {
 }
 
 // One patch element, any layout (the general path).
-__device__ __forceinline__ float patch_elem(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int m, int k) {
+__device__ __forceinline__ float patch_elem(__amdgpu_buffer_rsrc_t rs, const ConvCore& g, int m, int k) {
   const long idx = patch_index(g, m, k);
   if (g.u8) return __uint_as_float(ld_u8(rs, idx < 0 ? kBad : uint32_t(idx)));
   return ld_f1(rs, idx < 0 ? kBad : uint32_t(idx) * 4u);
@@ -110,7 +117,7 @@ struct PixelPos {
   uint32_t base;
   int ih0, iw0;
 };
-__device__ __forceinline__ PixelPos pixel_pos(const ConvGeo& g, int m) {
+__device__ __forceinline__ PixelPos pixel_pos(const ConvCore& g, int m) {
   if (m >= g.M) return PixelPos{kBad, -(1 << 28), 0};
   int b, oh, ow;
   g.split_m(m, b, oh, ow);
@@ -125,8 +132,8 @@ struct TapPos {
   uint32_t off;
   int kh, kw;
 };
-__device__ __forceinline__ TapPos tap_pos(const ConvGeo& g, int k) {
-  if (k >= g.kp()) return TapPos{kBad, 0, 0};
+__device__ __forceinline__ TapPos tap_pos(const ConvCore& g, int k) {
+  if (k >= g.kp) return TapPos{kBad, 0, 0};
   int c, kh, kw;
   g.split_k(k, c, kh, kw);
   const int e = g.u8 ? (c * g.H + kh) * g.W + kw : (kh * g.W + kw) * g.C + c;
@@ -134,8 +141,8 @@ __device__ __forceinline__ TapPos tap_pos(const ConvGeo& g, int k) {
 }
 
 // Starts the load of patch chunk (pixel, tap) in the given mode.
-__device__ __forceinline__ void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvGeo& g, int mode, const PixelPos& px,
-                                   const TapPos& tp, Fetch4& f) {
+__device__ __forceinline__ void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvCore& g, int mode, const PixelPos& px,
+                                            const TapPos& tp, Fetch4& f) {
   uint32_t off = px.base + tp.off;
   if (g.P != 0) {  // borders: the tap may fall outside the image
     const int ih = px.ih0 + tp.kh, iw = px.iw0 + tp.kw;
@@ -148,69 +155,98 @@ __device__ __forceinline__ void patch_issue(__amdgpu_buffer_rsrc_t rs, const Con
 
 // Forward A operand: A(m, k) = patch(m, k).
 struct LdConvFwd {
-  static constexpr bool KCONTIG = true;
   ConvGeo g;
   const void* x[kMaxGroups];
   uint32_t xbytes;
   int mode;
-  struct Row { PixelPos px; };  // the general mode keeps the pixel index in px.base
-  struct Kp { TapPos tp; int k; };
-  __device__ __forceinline__ int fmt() const {
-    return mode == kPatchU8Word ? kU8Word : (mode == kPatchGeneral && g.u8 ? kU8Each : kF32);
-  }
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
-  __device__ __forceinline__ Row row(int m, int) const {
-    return mode == kPatchGeneral ? Row{PixelPos{uint32_t(m), 0, 0}} : Row{pixel_pos(g, m)};
-  }
-  __device__ __forceinline__ Kp kpos(int k, int) const { return Kp{mode == kPatchGeneral ? TapPos{} : tap_pos(g, k), k}; }
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
-    if (mode != kPatchGeneral) {
-      patch_issue(rs, g, mode, r.px, kp.tp, f);
-      return;
+
+  struct Params {
+    ConvCore g;
+    const void* x;
+    uint32_t xbytes;
+    int mode;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = true;
+    Params q;
+    __amdgpu_buffer_rsrc_t rs;
+    struct Row { PixelPos px; };  // the general mode keeps the pixel index in px.base
+    struct Kp { TapPos tp; int k; };
+    __device__ __forceinline__ int fmt() const {
+      return q.mode == kPatchU8Word ? kU8Word : (q.mode == kPatchGeneral && q.g.u8 ? kU8Each : kF32);
     }
+    __device__ __forceinline__ Row row(int m) const {
+      return q.mode == kPatchGeneral ? Row{PixelPos{uint32_t(m), 0, 0}} : Row{pixel_pos(q.g, m)};
+    }
+    __device__ __forceinline__ Kp kpos(int k) const {
+      return Kp{q.mode == kPatchGeneral ? TapPos{} : tap_pos(q.g, k), k};
+    }
+    __device__ __forceinline__ void issue(const Row& r, const Kp& kp, Fetch4& f) const {
+      if (q.mode != kPatchGeneral) {
+        patch_issue(rs, q.g, q.mode, r.px, kp.tp, f);
+        return;
+      }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, g, int(r.px.base), kp.k + j);
+      for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, q.g, int(r.px.base), kp.k + j);
+    }
+  };
+  __device__ __forceinline__ Live live(int grp) const {
+    const Params q = pin_pod(Params{conv_core(g), x[grp], xbytes, mode});
+    return Live{q, make_res(q.x, q.xbytes)};
   }
 };
 
 // Weight-gradient A operand: A(r = k, k = m) = patch(m, r), with the ones row
 // at r == kp when the bias gradient is wanted.
 struct LdConvPatchT {
-  static constexpr bool KCONTIG = false;
   ConvGeo g;
   const void* x[kMaxGroups];
   uint32_t xbytes;
   int mode;
   int ones;
-  struct Row { TapPos tp; int r; bool whole; };
-  struct Ks { int m; };
-  __device__ __forceinline__ int fmt() const {
-    return mode == kPatchU8Word ? kU8Word : (g.u8 ? kU8Each : kF32);
-  }
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int grp) const { return make_res(x[grp], xbytes); }
-  __device__ __forceinline__ Row row(int r, int) const {
-    const bool whole = mode != kPatchGeneral && r + 3 < g.kp();
-    return Row{whole ? tap_pos(g, r) : TapPos{}, r, whole};
-  }
-  __device__ __forceinline__ Ks kstage(const Row&, int m, int) const { return Ks{m}; }
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Ks& ks, int dm, Fetch4& f) const {
-    const int m = ks.m + dm;
-    if (r.whole) {
-      patch_issue(rs, g, mode, pixel_pos(g, m), r.tp, f);
-      return;
+
+  struct Params {
+    ConvCore g;
+    const void* x;
+    uint32_t xbytes;
+    int mode, ones;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = false;
+    Params q;
+    __amdgpu_buffer_rsrc_t rs;
+    struct Row { TapPos tp; int r; bool whole; };
+    struct Ks { int m; };
+    __device__ __forceinline__ int fmt() const {
+      return q.mode == kPatchU8Word ? kU8Word : (q.g.u8 ? kU8Each : kF32);
     }
-    // The general path and the tail chunk: patch rows, then the ones row.
-    const int kp = g.kp();
+    __device__ __forceinline__ Row row(int r) const {
+      const bool whole = q.mode != kPatchGeneral && r + 3 < q.g.kp;
+      return Row{whole ? tap_pos(q.g, r) : TapPos{}, r, whole};
+    }
+    __device__ __forceinline__ Ks kstage(const Row&, int m) const { return Ks{m}; }
+    __device__ __forceinline__ void issue(const Row& r, const Ks& ks, int dm, Fetch4& f) const {
+      const int m = ks.m + dm;
+      if (r.whole) {
+        patch_issue(rs, q.g, q.mode, pixel_pos(q.g, m), r.tp, f);
+        return;
+      }
+      // The general path and the tail chunk: patch rows, then the ones row.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int rr = r.r + j;
-      if (rr < kp) {
-        f.v[j] = patch_elem(rs, g, m, rr);
-      } else {
-        const float one = (ones && rr == kp && m < g.M) ? 1.f : 0.f;
-        f.v[j] = g.u8 ? __uint_as_float(uint32_t(one)) : one;
+      for (int j = 0; j < 4; ++j) {
+        const int rr = r.r + j;
+        if (rr < q.g.kp) {
+          f.v[j] = patch_elem(rs, q.g, m, rr);
+        } else {
+          const float one = (q.ones && rr == q.g.kp && m < q.g.M) ? 1.f : 0.f;
+          f.v[j] = q.g.u8 ? __uint_as_float(uint32_t(one)) : one;
+        }
       }
     }
+  };
+  __device__ __forceinline__ Live live(int grp) const {
+    const Params q = pin_pod(Params{conv_core(g), x[grp], xbytes, mode, ones});
+    return Live{q, make_res(q.x, q.xbytes)};
   }
 };
 
@@ -218,97 +254,131 @@ struct LdConvPatchT {
 // output pixel that tap (kh, kw) = (ch + s*jh, cw + s*jw) connects to input
 // pixel r: oh = ohc(r) - jh, ow = owc(r) - jw with ohc = (ih + p - ch) / s.
 struct LdConvDxA {
-  static constexpr bool KCONTIG = true;
   ConvGeo g;
   const float* dy;
   uint32_t dybytes;
-  struct Row { int base, ohc, owc; };  // base = element offset of dZ(b, ohc, owc, 0)
-  struct Kp { int off, jh, jw; bool v; int k, ch, cw; };
-  __device__ __forceinline__ int fmt() const { return kF32; }
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int) const { return make_res(dy, dybytes); }
-  __device__ __forceinline__ int cls(int grp) const { return g.cls0 + grp; }
-  __device__ __forceinline__ Row row(int r, int grp) const {
-    if (r >= g.B * g.nh[grp] * g.nw[grp]) return Row{0, -(1 << 28), 0};
-    const int b = g.d_nhnw[grp].div(r);
-    const int rem = r - b * g.nh[grp] * g.nw[grp];
-    const int i = g.d_nw[grp].div(rem), j = rem - i * g.nw[grp];
-    const int c = cls(grp), ch = c / g.S, cw = c - ch * g.S;
-    const int ohc = g.d_s.div(g.ih0[grp] + g.S * i + g.P - ch);
-    const int owc = g.d_s.div(g.iw0[grp] + g.S * j + g.P - cw);
-    return Row{((b * g.OH + ohc) * g.OW + owc) * g.O, ohc, owc};
-  }
-  __device__ __forceinline__ Kp kpos(int k, int grp) const {
-    const int c = cls(grp), ch = c / g.S, cw = c - ch * g.S;
-    if (k >= g.TH * g.TW * g.O) return Kp{0, 0, 0, false, k, ch, cw};
-    const int jt = g.d_o.div(k), o = k - jt * g.O;
-    const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
-    const bool v = ch + g.S * jh < g.KH && cw + g.S * jw < g.KW;
-    return Kp{o - (jh * g.OW + jw) * g.O, jh, jw, v, k, ch, cw};
-  }
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
-    if ((g.O & 3) == 0) {  // the four k share one tap and output pixel
-      const int oh = r.ohc - kp.jh, ow = r.owc - kp.jw;
-      const bool in = kp.v && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
-      f.v = ld_f4(rs, in ? uint32_t(r.base + kp.off) * 4u : kBad);
-      return;
+
+  struct Params {
+    const float* dy;
+    uint32_t bytes;
+    int rows, nw;
+    FDiv d_nhnw, d_nw;
+    int ch, cw, ihp, iwp, S;  // ihp = ih0 + P - ch: ohc = (ihp + S*i) / S
+    FDiv d_s;
+    int OH, OW, O, kmax;  // kmax = TH*TW*O
+    FDiv d_o, d_tw;
+    int TW, KH, KW;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = true;
+    Params q;
+    __amdgpu_buffer_rsrc_t rs;
+    struct Row { int base, ohc, owc; };  // base = element offset of dZ(b, ohc, owc, 0)
+    struct Kp { int off, jh, jw; bool v; int k; };
+    __device__ __forceinline__ int fmt() const { return kF32; }
+    __device__ __forceinline__ Row row(int r) const {
+      if (r >= q.rows) return Row{0, -(1 << 28), 0};
+      const int b = q.d_nhnw.div(r);
+      const int rem = r - b * q.d_nhnw.d;
+      const int i = q.d_nw.div(rem), j = rem - i * q.nw;
+      const int ohc = q.d_s.div(q.ihp + q.S * i);
+      const int owc = q.d_s.div(q.iwp + q.S * j);
+      return Row{((b * q.OH + ohc) * q.OW + owc) * q.O, ohc, owc};
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kp.k + j;
-      bool in = k < g.TH * g.TW * g.O;
-      int off = 0;
-      if (in) {
-        const int jt = g.d_o.div(k), o = k - jt * g.O;
-        const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
-        const int oh = r.ohc - jh, ow = r.owc - jw;
-        in = kp.ch + g.S * jh < g.KH && kp.cw + g.S * jw < g.KW && oh >= 0 && oh < g.OH && ow >= 0 && ow < g.OW;
-        off = r.base - (jh * g.OW + jw) * g.O + o;
+    __device__ __forceinline__ Kp kpos(int k) const {
+      if (k >= q.kmax) return Kp{0, 0, 0, false, k};
+      const int jt = q.d_o.div(k), o = k - jt * q.O;
+      const int jh = q.d_tw.div(jt), jw = jt - jh * q.TW;
+      const bool v = q.ch + q.S * jh < q.KH && q.cw + q.S * jw < q.KW;
+      return Kp{o - (jh * q.OW + jw) * q.O, jh, jw, v, k};
+    }
+    __device__ __forceinline__ void issue(const Row& r, const Kp& kp, Fetch4& f) const {
+      if ((q.O & 3) == 0) {  // the four k share one tap and output pixel
+        const int oh = r.ohc - kp.jh, ow = r.owc - kp.jw;
+        const bool in = kp.v && oh >= 0 && oh < q.OH && ow >= 0 && ow < q.OW;
+        f.v = ld_f4(rs, in ? uint32_t(r.base + kp.off) * 4u : kBad);
+        return;
       }
-      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kBad);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = kp.k + j;
+        bool in = k < q.kmax;
+        int off = 0;
+        if (in) {
+          const int jt = q.d_o.div(k), o = k - jt * q.O;
+          const int jh = q.d_tw.div(jt), jw = jt - jh * q.TW;
+          const int oh = r.ohc - jh, ow = r.owc - jw;
+          in = q.ch + q.S * jh < q.KH && q.cw + q.S * jw < q.KW && oh >= 0 && oh < q.OH && ow >= 0 && ow < q.OW;
+          off = r.base - (jh * q.OW + jw) * q.O + o;
+        }
+        f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kBad);
+      }
     }
+  };
+  __device__ __forceinline__ Live live(int grp) const {
+    const int c = g.cls0 + grp, ch = c / g.S, cw = c - ch * g.S;
+    const Params q = pin_pod(Params{dy, dybytes, g.B * g.nh[grp] * g.nw[grp], g.nw[grp], g.d_nhnw[grp], g.d_nw[grp],
+                                    ch, cw, g.ih0[grp] + g.P - ch, g.iw0[grp] + g.P - cw, g.S, g.d_s, g.OH, g.OW,
+                                    g.O, g.TH * g.TW * g.O, g.d_o, g.d_tw, g.TW, g.KH, g.KW});
+    return Live{q, make_res(q.dy, q.bytes)};
   }
 };
 
 // Input-gradient B operand of class `cls`: B(k = (jh, jw, o), n = c) =
 // Wt[(kh, kw, c)][o]; stored here as rows n, k contiguous.
 struct LdConvDxB {
-  static constexpr bool KCONTIG = true;
   ConvGeo g;
   const float* wt;
   uint32_t wbytes;
-  struct Row { uint32_t off; int c; };  // byte offset of Wt[(0,0,c)][0], kBad past C
-  struct Kp { uint32_t off; int k, ch, cw; };
-  __device__ __forceinline__ int fmt() const { return kF32; }
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int) const { return make_res(wt, wbytes); }
-  __device__ __forceinline__ Row row(int c, int) const { return Row{c < g.C ? uint32_t(c * g.O) * 4u : kBad, c}; }
-  __device__ __forceinline__ Kp kpos(int k, int grp) const {
-    const int c = g.cls0 + grp, ch = c / g.S, cw = c - ch * g.S;
-    if (k >= g.TH * g.TW * g.O) return Kp{kBad, k, ch, cw};
-    const int jt = g.d_o.div(k), o = k - jt * g.O;
-    const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
-    const int kh = ch + g.S * jh, kw = cw + g.S * jw;
-    const bool v = kh < g.KH && kw < g.KW;
-    return Kp{v ? uint32_t((kh * g.KW + kw) * g.C * g.O + o) * 4u : kBad, k, ch, cw};
-  }
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
-    if ((g.O & 3) == 0) {
-      f.v = ld_f4(rs, r.off + kp.off);
-      return;
+
+  struct Params {
+    const float* wt;
+    uint32_t bytes;
+    int C, O, ch, cw, S, KH, KW, kmax, TW;
+    FDiv d_o, d_tw;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = true;
+    Params q;
+    __amdgpu_buffer_rsrc_t rs;
+    struct Row { uint32_t off; int c; };  // byte offset of Wt[(0,0,c)][0], kBad past C
+    struct Kp { uint32_t off; int k; };
+    __device__ __forceinline__ int fmt() const { return kF32; }
+    __device__ __forceinline__ Row row(int c) const { return Row{c < q.C ? uint32_t(c * q.O) * 4u : kBad, c}; }
+    __device__ __forceinline__ Kp kpos(int k) const {
+      if (k >= q.kmax) return Kp{kBad, k};
+      const int jt = q.d_o.div(k), o = k - jt * q.O;
+      const int jh = q.d_tw.div(jt), jw = jt - jh * q.TW;
+      const int kh = q.ch + q.S * jh, kw = q.cw + q.S * jw;
+      const bool v = kh < q.KH && kw < q.KW;
+      return Kp{v ? uint32_t((kh * q.KW + kw) * q.C * q.O + o) * 4u : kBad, k};
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kp.k + j;
-      bool in = r.c < g.C && k < g.TH * g.TW * g.O;
-      int off = 0;
-      if (in) {
-        const int jt = g.d_o.div(k), o = k - jt * g.O;
-        const int jh = g.d_tw.div(jt), jw = jt - jh * g.TW;
-        const int kh = kp.ch + g.S * jh, kw = kp.cw + g.S * jw;
-        in = kh < g.KH && kw < g.KW;
-        off = (r.c + (kh * g.KW + kw) * g.C) * g.O + o;
+    __device__ __forceinline__ void issue(const Row& r, const Kp& kp, Fetch4& f) const {
+      if ((q.O & 3) == 0) {
+        f.v = ld_f4(rs, r.off + kp.off);
+        return;
       }
-      f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kBad);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = kp.k + j;
+        bool in = r.c < q.C && k < q.kmax;
+        int off = 0;
+        if (in) {
+          const int jt = q.d_o.div(k), o = k - jt * q.O;
+          const int jh = q.d_tw.div(jt), jw = jt - jh * q.TW;
+          const int kh = q.ch + q.S * jh, kw = q.cw + q.S * jw;
+          in = kh < q.KH && kw < q.KW;
+          off = (r.c + (kh * q.KW + kw) * q.C) * q.O + o;
+        }
+        f.v[j] = ld_f1(rs, in ? uint32_t(off) * 4u : kBad);
+      }
     }
+  };
+  __device__ __forceinline__ Live live(int grp) const {
+    const int c = g.cls0 + grp, ch = c / g.S, cw = c - ch * g.S;
+    const Params q = pin_pod(Params{wt, wbytes, g.C, g.O, ch, cw, g.S, g.KH, g.KW, g.TH * g.TW * g.O, g.TW, g.d_o,
+                                    g.d_tw});
+    return Live{q, make_res(q.wt, q.bytes)};
   }
 };
 
@@ -353,15 +423,21 @@ struct EpConvDx {
       st_f1(rdx, x.off, v);
     }
   };
+  struct Params {
+    float* dx;
+    const float* xm;
+    uint32_t bytes;
+    int rows, C, H, W, S, nw, ih0, iw0;
+    FDiv d_nhnw, d_nw;
+    float alpha, beta;
+  };
   template <class F>
   __device__ __forceinline__ void with_bound(int grp, F&& f) const {
-    float* d = dx;
-    const float* xm = xmask;
-    pin(d, xm);
-    const uint32_t bytes = uint32_t(long(g.B) * g.H * g.W * g.C * 4);
-    f(Bound{rows(grp), g.C, g.H, g.W, g.S, g.nw[grp], g.ih0[grp], g.iw0[grp], g.d_nhnw[grp], g.d_nw[grp],
-            make_res(d, bytes), make_res(xm, xm ? bytes : 0u), make_res(d, beta != 0.f ? bytes : 0u), xm != nullptr,
-            alpha, beta});
+    const Params q = pin_pod(Params{dx, xmask, uint32_t(long(g.B) * g.H * g.W * g.C * 4), rows(grp), g.C, g.H, g.W,
+                                    g.S, g.nw[grp], g.ih0[grp], g.iw0[grp], g.d_nhnw[grp], g.d_nw[grp], alpha, beta});
+    f(Bound{q.rows, q.C, q.H, q.W, q.S, q.nw, q.ih0, q.iw0, q.d_nhnw, q.d_nw, make_res(q.dx, q.bytes),
+            make_res(q.xm, q.xm ? q.bytes : 0u), make_res(q.dx, q.beta != 0.f ? q.bytes : 0u), q.xm != nullptr,
+            q.alpha, q.beta});
   }
 };
 

@@ -106,6 +106,42 @@ template <class T, class U>
 __device__ __forceinline__ void pin(T*& a, U*& b) {
   asm volatile("" : "+s"(a), "+s"(b));
 }
+
+// A copy of a plain struct of wave-uniform words (at most 32), every word
+// materialised in scalar registers by one asm statement: the values are
+// read once, together, and the compiler cannot re-read them from memory.
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+template <class T>
+__device__ __forceinline__ T pin_pod(const T& src) {
+  static_assert(sizeof(T) % 4 == 0 && sizeof(T) <= 128, "pin_pod: at most 32 words");
+  constexpr int N = int(sizeof(T) / 4);
+  uint32_t w[32] = {};
+  __builtin_memcpy(w, &src, sizeof(T));
+  u32x8 c0, c1, c2, c3;
+  // readfirstlane: words the compiler computed on the vector unit (uniform
+  // by construction) move to scalar registers.
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    c0[i] = __builtin_amdgcn_readfirstlane(w[i]);
+    c1[i] = __builtin_amdgcn_readfirstlane(w[8 + i]);
+    c2[i] = __builtin_amdgcn_readfirstlane(w[16 + i]);
+    c3[i] = __builtin_amdgcn_readfirstlane(w[24 + i]);
+  }
+  if constexpr (N <= 8) asm volatile("" : "+s"(c0));
+  else if constexpr (N <= 16) asm volatile("" : "+s"(c0), "+s"(c1));
+  else if constexpr (N <= 24) asm volatile("" : "+s"(c0), "+s"(c1), "+s"(c2));
+  else asm volatile("" : "+s"(c0), "+s"(c1), "+s"(c2), "+s"(c3));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w[i] = c0[i];
+    w[8 + i] = c1[i];
+    w[16 + i] = c2[i];
+    w[24 + i] = c3[i];
+  }
+  T out;
+  __builtin_memcpy(&out, w, sizeof(T));
+  return out;
+}
 constexpr int kBufFlags = 0x00020000;  // gfx9 buffer resource word 3: raw 32-bit dwords
 
 // The base and size are wave-uniform by construction; reading them through
@@ -148,9 +184,15 @@ __device__ __forceinline__ f32x4 resolve4(const Fetch4& f, int fmt) {
   return f.v;
 }
 
+// Each loader is a host-side description (per-group pointer tables and
+// extents, passed as a kernel argument) and a device-side Live view of one
+// group: the parameters its device code reads, loaded together and pinned
+// in scalar registers by live(g) before any load is issued.  Reading kernel
+// arguments where they are used instead makes the compiler reload them in
+// every branch, each reload a scalar-cache round trip the wavefront waits on.
+
 // v(r, k) = p[g][r*ld + k]; k contiguous.
 struct LdRowK {
-  static constexpr bool KCONTIG = true;
   const float* p[kMaxGroups] = {};
   long ld = 0;
   int rows = 0, K = 0;
@@ -158,19 +200,33 @@ struct LdRowK {
 
   __host__ void vec_ok(bool aligned) { vec = aligned && ld % 4 == 0 && K % 4 == 0; }
   __host__ __device__ long bytes() const { return rows > 0 ? ((long(rows) - 1) * ld + K) * 4 : 0; }
-  struct Row { uint32_t off; };
-  struct Kp { uint32_t add; int k; };
-  __device__ __forceinline__ int fmt() const { return kF32; }
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t res(int g) const { return make_res(p[g], uint32_t(bytes())); }
-  __device__ __forceinline__ Row row(int r, int) const { return Row{r < rows ? uint32_t(r * ld) * 4u : kBad}; }
-  __device__ __forceinline__ Kp kpos(int k, int) const { return Kp{k < K ? uint32_t(k) * 4u : kBad, k}; }
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, const Row& r, const Kp& kp, Fetch4& f) const {
-    if (vec) {  // K % 4 == 0: k < K covers all four
-      f.v = ld_f4(rs, r.off + kp.add);
-      return;
-    }
+
+  struct Params {
+    const float* p;
+    uint32_t bytes;
+    int ld, rows, K, vec;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = true;
+    Params q;
+    __amdgpu_buffer_rsrc_t rs;
+    struct Row { uint32_t off; };
+    struct Kp { uint32_t add; int k; };
+    __device__ __forceinline__ int fmt() const { return kF32; }
+    __device__ __forceinline__ Row row(int r) const { return Row{r < q.rows ? uint32_t(r * q.ld) * 4u : kBad}; }
+    __device__ __forceinline__ Kp kpos(int k) const { return Kp{k < q.K ? uint32_t(k) * 4u : kBad, k}; }
+    __device__ __forceinline__ void issue(const Row& r, const Kp& kp, Fetch4& f) const {
+      if (q.vec) {  // K % 4 == 0: k < K covers all four
+        f.v = ld_f4(rs, r.off + kp.add);
+        return;
+      }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.v[j] = ld_f1(rs, r.off + (kp.k + j < K ? uint32_t(kp.k + j) * 4u : kBad));
+      for (int j = 0; j < 4; ++j) f.v[j] = ld_f1(rs, r.off + (kp.k + j < q.K ? uint32_t(kp.k + j) * 4u : kBad));
+    }
+  };
+  __device__ __forceinline__ Live live(int g) const {
+    const Params q = pin_pod(Params{p[g], uint32_t(bytes()), int(ld), rows, K, vec ? 1 : 0});
+    return Live{q, make_res(q.p, q.bytes)};
   }
 };
 
@@ -180,7 +236,6 @@ struct LdRowK {
 // along the output axis).  With ld >= the real rows, every k >= K lies past
 // the resource's range, so the vector path needs no k check.
 struct LdColK {
-  static constexpr bool KCONTIG = false;
   const float* p[kMaxGroups] = {};
   const float* p2[kMaxGroups] = {};
   long ld = 0, ld2 = 0;
@@ -204,45 +259,53 @@ struct LdColK {
   __host__ __device__ long bytes2() const {
     return (K > 0 && rows > split) ? ((long(K) - 1) * ld2 + (rows - split)) * 4 : 0;
   }
-  // mode 0: four real rows, one vector load; 1: no row inside, zeros; 2: element by element.
-  struct Row { uint32_t off; int r; int mode; };
-  struct Ks { uint32_t base; int k; };
-  struct Res { __amdgpu_buffer_rsrc_t a; const float* base; const float* base2; };
-  __device__ __forceinline__ int fmt() const { return kF32; }
-  __device__ __forceinline__ Res res(int g) const {
-    const float* a = p[g];
-    const float* b = p2[g];
-    pin(a, b);
-    return Res{make_res(a, uint32_t(bytes())), a, b};
-  }
-  __device__ __forceinline__ Row row(int r, int) const {
-    const bool whole = vec && r + 3 < real_rows && r + 3 < split && r + 3 < rows;
-    return Row{uint32_t(r) * 4u, r, whole ? 0 : (r >= rows ? 1 : 2)};
-  }
-  __device__ __forceinline__ Ks kstage(const Row& r, int k, int) const { return Ks{uint32_t(k * ld) * 4u + r.off, k}; }
-  __device__ __forceinline__ void issue(const Res& rs, const Row& r, const Ks& ks, int dk, Fetch4& f) const {
-    if (r.mode == 0) {
-      f.v = ld_f4(rs.a, ks.base + uint32_t(dk * ld) * 4u);
-      return;
+
+  struct Params {
+    const float* base;
+    const float* base2;
+    uint32_t bytes;
+    int ld, ld2, rows, K, vec, real_rows, ones, split;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = false;
+    Params q;
+    __amdgpu_buffer_rsrc_t rs;
+    // mode 0: four real rows, one vector load; 1: no row inside, zeros; 2: element by element.
+    struct Row { uint32_t off; int r; int mode; };
+    struct Ks { uint32_t base; int k; };
+    __device__ __forceinline__ int fmt() const { return kF32; }
+    __device__ __forceinline__ Row row(int r) const {
+      const bool whole = q.vec && r + 3 < q.real_rows && r + 3 < q.split && r + 3 < q.rows;
+      return Row{uint32_t(r) * 4u, r, whole ? 0 : (r >= q.rows ? 1 : 2)};
     }
-    if (r.mode == 1) {
-      f.v = f32x4{0.f, 0.f, 0.f, 0.f};
-      return;
-    }
-    const int k = ks.k + dk;
-    const bool kv = k < K;
-    const float* base = rs.base;
-    const float* base2 = rs.base2;
+    __device__ __forceinline__ Ks kstage(const Row& r, int k) const { return Ks{uint32_t(k * q.ld) * 4u + r.off, k}; }
+    __device__ __forceinline__ void issue(const Row& r, const Ks& ks, int dk, Fetch4& f) const {
+      if (r.mode == 0) {
+        f.v = ld_f4(rs, ks.base + uint32_t(dk * q.ld) * 4u);
+        return;
+      }
+      if (r.mode == 1) {
+        f.v = f32x4{0.f, 0.f, 0.f, 0.f};
+        return;
+      }
+      const int k = ks.k + dk;
+      const bool kv = k < q.K;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int rr = r.r + j;
-      const bool in = kv && rr < rows;
-      const float* src = &g_zero_one[0];
-      if (in && rr >= real_rows) src = &g_zero_one[(ones && rr == real_rows) ? 1 : 0];
-      else if (in && rr >= split) src = base2 + (long(k) * ld2 + (rr - split));
-      else if (in) src = base + (long(k) * ld + rr);
-      f.v[j] = gload(src);
+      for (int j = 0; j < 4; ++j) {
+        const int rr = r.r + j;
+        const bool in = kv && rr < q.rows;
+        const float* src = &g_zero_one[0];
+        if (in && rr >= q.real_rows) src = &g_zero_one[(q.ones && rr == q.real_rows) ? 1 : 0];
+        else if (in && rr >= q.split) src = q.base2 + (long(k) * q.ld2 + (rr - q.split));
+        else if (in) src = q.base + (long(k) * q.ld + rr);
+        f.v[j] = gload(src);
+      }
     }
+  };
+  __device__ __forceinline__ Live live(int g) const {
+    const Params q = pin_pod(Params{p[g], p2[g], uint32_t(bytes()), int(ld), int(ld2), rows, K, vec ? 1 : 0,
+                                    real_rows, ones ? 1 : 0, split});
+    return Live{q, make_res(q.base, q.bytes)};
   }
 };
 
@@ -250,7 +313,6 @@ struct LdColK {
 // k >= k1 reads p2[g][r*ld2 + k-k1] (the SAC critic's concat(s, a) input;
 // also the transposed view of two weight matrices side by side).
 struct LdRowKCat {
-  static constexpr bool KCONTIG = true;
   const float* p1[kMaxGroups] = {};
   const float* p2[kMaxGroups] = {};
   long ld1 = 0, ld2 = 0;
@@ -260,27 +322,34 @@ struct LdRowKCat {
   __host__ __device__ long bytes2() const {
     return rows > 0 && K > k1 ? ((long(rows) - 1) * ld2 + (K - k1)) * 4 : 0;
   }
-  struct Row { int r; };
-  struct Kp { int k; };
-  struct Res { const float* a; const float* b; };
-  __device__ __forceinline__ int fmt() const { return kF32; }
-  __device__ __forceinline__ Res res(int g) const {
-    const float* a = p1[g];
-    const float* b = p2[g];
-    pin(a, b);
-    return Res{a, b};
-  }
-  __device__ __forceinline__ Row row(int r, int) const { return Row{r}; }
-  __device__ __forceinline__ Kp kpos(int k, int) const { return Kp{k}; }
-  __device__ __forceinline__ void issue(const Res& rs, const Row& r, const Kp& kp, Fetch4& f) const {
-    const bool rv = r.r < rows;
+
+  struct Params {
+    const float* a;
+    const float* b;
+    int ld1, ld2, rows, k1, K;
+  };
+  struct Live {
+    static constexpr bool KCONTIG = true;
+    Params q;
+    struct Row { int r; };
+    struct Kp { int k; };
+    __device__ __forceinline__ int fmt() const { return kF32; }
+    __device__ __forceinline__ Row row(int r) const { return Row{r}; }
+    __device__ __forceinline__ Kp kpos(int k) const { return Kp{k}; }
+    __device__ __forceinline__ void issue(const Row& r, const Kp& kp, Fetch4& f) const {
+      const bool rv = r.r < q.rows;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kk = kp.k + j;
-      const float* src = &g_zero_one[0];
-      if (rv && kk < K) src = kk < k1 ? rs.a + (long(r.r) * ld1 + kk) : rs.b + (long(r.r) * ld2 + (kk - k1));
-      f.v[j] = gload(src);
+      for (int j = 0; j < 4; ++j) {
+        const int kk = kp.k + j;
+        const float* src = &g_zero_one[0];
+        if (rv && kk < q.K)
+          src = kk < q.k1 ? q.a + (long(r.r) * q.ld1 + kk) : q.b + (long(r.r) * q.ld2 + (kk - q.k1));
+        f.v[j] = gload(src);
+      }
     }
+  };
+  __device__ __forceinline__ Live live(int g) const {
+    return Live{pin_pod(Params{p1[g], p2[g], int(ld1), int(ld2), rows, k1, K})};
   }
 };
 
@@ -418,26 +487,34 @@ struct EpStore {
       *x.dst = v;
     }
   };
-  // Calls f with group g's bound epilogue.
+  // Calls f with group g's bound epilogue (its parameters pinned, as for
+  // the loaders).
+  struct Params {
+    float* c0;
+    float* c1;
+    float* c2;
+    float* c3;
+    const float* b0;
+    const float* b1;
+    const float* mk;
+    int M, N, ldc, ldcc, rsplit, csplit;
+    float alpha, beta, alpha_r;
+    int relu, clamp_col;
+    float lo, hi;
+  };
   template <class F>
   __device__ __forceinline__ void with_bound(int g, F&& f) const {
-    float* c0 = C[g];
-    float* c1 = Cr[g];
-    float* c2 = Cc[g];
-    float* c3 = Crc[g];
-    const float* b0 = bias[g];
-    const float* b1 = bias2[g];
-    const float* mk = mask[g];
-    asm volatile("" : "+s"(c0), "+s"(c1), "+s"(c2), "+s"(c3), "+s"(b0), "+s"(b1), "+s"(mk));
-    const long cb = M > 0 ? (long(M - 1) * ldc + N) * 4 : 0;
-    if (rsplit >= M && csplit >= N && cb < kMaxOperandBytes) {
+    const Params q = pin_pod(Params{C[g], Cr[g], Cc[g], Crc[g], bias[g], bias2[g], mask[g], M, N, int(ldc), int(ldcc),
+                                    rsplit, csplit, alpha, beta, alpha_r, relu, clamp_col, lo, hi});
+    const long cb = q.M > 0 ? (long(q.M - 1) * q.ldc + q.N) * 4 : 0;
+    if (q.rsplit >= q.M && q.csplit >= q.N && cb < kMaxOperandBytes) {
       const uint32_t cbytes = uint32_t(cb);
-      f(Fast{M, N, uint32_t(ldc), alpha, beta, relu, clamp_col, lo, hi, mk != nullptr, make_res(c0, cbytes),
-             make_res(b0, b0 ? uint32_t(N) * 4u : 0u), make_res(mk, mk ? cbytes : 0u),
-             make_res(c0, beta != 0.f ? cbytes : 0u)});
+      f(Fast{q.M, q.N, uint32_t(q.ldc), q.alpha, q.beta, q.relu, q.clamp_col, q.lo, q.hi, q.mk != nullptr,
+             make_res(q.c0, cbytes), make_res(q.b0, q.b0 ? uint32_t(q.N) * 4u : 0u),
+             make_res(q.mk, q.mk ? cbytes : 0u), make_res(q.c0, q.beta != 0.f ? cbytes : 0u)});
     } else {
-      f(Split{M, N, c0, c1, c2, c3, ldc, ldcc, rsplit, csplit, alpha, beta, alpha_r, b0, b1, relu, clamp_col, lo, hi,
-              mk});
+      f(Split{q.M, q.N, q.c0, q.c1, q.c2, q.c3, q.ldc, q.ldcc, q.rsplit, q.csplit, q.alpha, q.beta, q.alpha_r, q.b0,
+              q.b1, q.relu, q.clamp_col, q.lo, q.hi, q.mk});
     }
   }
 };
@@ -477,32 +554,31 @@ struct Cursor<L, PER, false> {
 };
 
 template <int ROWS, int TBK, int NT, class L, int PER>
-__device__ __forceinline__ void make_cursor(Cursor<L, PER>& c, const L& ld, int r0, int g, int tid) {
+__device__ __forceinline__ void make_cursor(Cursor<L, PER>& c, const L& ld, int r0, int tid) {
   using S = Stage<ROWS, TBK, NT, L>;
   if constexpr (L::KCONTIG) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) c.r[j] = ld.row(r0 + (tid + j * NT) / S::CH, g);
+    for (int j = 0; j < PER; ++j) c.r[j] = ld.row(r0 + (tid + j * NT) / S::CH);
   } else {
-    c.r = ld.row(r0 + (tid % S::CH) * 4, g);
+    c.r = ld.row(r0 + (tid % S::CH) * 4);
   }
 }
 
 // Starts every load of one operand stage (no value is read here).
-template <int ROWS, int TBK, int NT, class L, int PER, class R>
-__device__ __forceinline__ void issue_tile(Fetch4 (&f)[PER], const L& ld, const R& rs, const Cursor<L, PER>& c, int k0, int g,
-                                  int tid) {
+template <int ROWS, int TBK, int NT, class L, int PER>
+__device__ __forceinline__ void issue_tile(Fetch4 (&f)[PER], const L& ld, const Cursor<L, PER>& c, int k0, int tid) {
   using S = Stage<ROWS, TBK, NT, L>;
   if constexpr (L::KCONTIG) {
-    const auto kp = ld.kpos(k0 + (tid % S::CH) * 4, g);
+    const auto kp = ld.kpos(k0 + (tid % S::CH) * 4);
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-      if (S::live(j, tid)) ld.issue(rs, c.r[j], kp, f[j]);
+      if (S::live(j, tid)) ld.issue(c.r[j], kp, f[j]);
   } else {
     constexpr int KSTEP = NT / S::CH;  // k-rows between a thread's consecutive fetches
-    const auto ks = ld.kstage(c.r, k0 + tid / S::CH, g);
+    const auto ks = ld.kstage(c.r, k0 + tid / S::CH);
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-      if (S::live(j, tid)) ld.issue(rs, c.r, ks, j * KSTEP, f[j]);
+      if (S::live(j, tid)) ld.issue(c.r, ks, j * KSTEP, f[j]);
   }
 }
 
@@ -638,10 +714,12 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
   constexpr int FM = WTM / 16, FN = WTN / 16;
   static_assert(FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "bad tile");
   static_assert(TBK % 16 == 0, "TBK must be a multiple of 16");
-  using LdsA = TileLds<BM, TBK, LA::KCONTIG>;
-  using LdsB = TileLds<BN, TBK, LB::KCONTIG>;
-  constexpr int PA = Stage<BM, TBK, NT, LA>::PER;
-  constexpr int PB = Stage<BN, TBK, NT, LB>::PER;
+  using VA = typename LA::Live;
+  using VB = typename LB::Live;
+  using LdsA = TileLds<BM, TBK, VA::KCONTIG>;
+  using LdsB = TileLds<BN, TBK, VB::KCONTIG>;
+  constexpr int PA = Stage<BM, TBK, NT, VA>::PER;
+  constexpr int PB = Stage<BN, TBK, NT, VB>::PER;
   __shared__ __attribute__((aligned(16))) float As[LdsA::SIZE];
   __shared__ __attribute__((aligned(16))) float Bs[LdsB::SIZE];
 
@@ -661,33 +739,33 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const auto ra = la.res(g);
-  const auto rb = lb.res(g);
-  Cursor<LA, PA> ca;
-  Cursor<LB, PB> cb;
-  make_cursor<BM, TBK, NT>(ca, la, m0, g, tid);
-  make_cursor<BN, TBK, NT>(cb, lb, n0, g, tid);
-  const int fa_fmt = la.fmt(), fb_fmt = lb.fmt();
+  const VA va = la.live(g);
+  const VB vb = lb.live(g);
+  Cursor<VA, PA> ca;
+  Cursor<VB, PB> cb;
+  make_cursor<BM, TBK, NT>(ca, va, m0, tid);
+  make_cursor<BN, TBK, NT>(cb, vb, n0, tid);
+  const int fa_fmt = va.fmt(), fb_fmt = vb.fmt();
 
   Fetch4 fa[PA], fb[PB];
-  issue_tile<BM, TBK, NT>(fa, la, ra, ca, kbeg, g, tid);
-  issue_tile<BN, TBK, NT>(fb, lb, rb, cb, kbeg, g, tid);
+  issue_tile<BM, TBK, NT>(fa, va, ca, kbeg, tid);
+  issue_tile<BN, TBK, NT>(fb, vb, cb, kbeg, tid);
 
   const int lr = lane & 15, lk = (lane >> 4) * 4;
   for (int k0 = kbeg; k0 < kend; k0 += TBK) {
     if (k0 != kbeg) __syncthreads();  // the previous stage's LDS reads are done
-    write_tile<BM, TBK, NT, LA>(As, fa, fa_fmt, tid);
-    write_tile<BN, TBK, NT, LB>(Bs, fb, fb_fmt, tid);
+    write_tile<BM, TBK, NT, VA>(As, fa, fa_fmt, tid);
+    write_tile<BN, TBK, NT, VB>(Bs, fb, fb_fmt, tid);
     __syncthreads();
     if (k0 + TBK < kend) {
-      issue_tile<BM, TBK, NT>(fa, la, ra, ca, k0 + TBK, g, tid);
-      issue_tile<BN, TBK, NT>(fb, lb, rb, cb, k0 + TBK, g, tid);
+      issue_tile<BM, TBK, NT>(fa, va, ca, k0 + TBK, tid);
+      issue_tile<BN, TBK, NT>(fb, vb, cb, k0 + TBK, tid);
     }
     const int kspan = min(TBK, kend - k0);  // zero padded past K
     if (kspan == TBK)
-      mma_stage_full<BM, BN, TBK, WGK, LA::KCONTIG, LB::KCONTIG>(acc, As, Bs, wm * WTM + lr, wn * WTN + lr, wk, lk);
+      mma_stage_full<BM, BN, TBK, WGK, VA::KCONTIG, VB::KCONTIG>(acc, As, Bs, wm * WTM + lr, wn * WTN + lr, wk, lk);
     else
-      mma_stage_part<BM, BN, TBK, WGK, LA::KCONTIG, LB::KCONTIG>(acc, As, Bs, wm * WTM + lr, wn * WTN + lr, wk, lk,
+      mma_stage_part<BM, BN, TBK, WGK, VA::KCONTIG, VB::KCONTIG>(acc, As, Bs, wm * WTM + lr, wn * WTN + lr, wk, lk,
                                                                   kspan);
   }
 
