@@ -23,6 +23,8 @@
 //
 // Index arithmetic uses multiply-high division by the layer's constant
 // extents (FDiv), precomputed on the host.
+#pragma once
+
 #include "tile_gemm.hpp"
 
 #include <algorithm>
@@ -36,6 +38,8 @@ constexpr unsigned kConvDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32
                                  cfg_bit(T32x32K2) | cfg_bit(T32x32K4) | cfg_bit(T32x64K2);
 constexpr unsigned kConvDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T128x32) | cfg_bit(T32x32K2) |
                                  cfg_bit(T64x32K2);
+// The element-by-element patch path (padding, odd channel counts) only.
+constexpr unsigned kConvGeneralCfgs = cfg_bit(T32x32) | cfg_bit(T64x32);
 
 struct ConvGeo {
   int B, C, H, W, O, KH, KW, S, P, OH, OW, u8;
@@ -98,138 +102,128 @@ __device__ __forceinline__ float patch_elem(__amdgpu_buffer_rsrc_t rs, const Con
 
 // How four consecutive patch indices k..k+3 (k % 4 == 0) lie in memory.
 enum PatchMode {
-  kPatchNhwcVec = 0,  // fp32 NHWC, C % 4 == 0: four channels of one tap, one 16-byte load
-  kPatchU8Word = 1,   // uint8 NCHW, KW, W, S, P multiples of 4: four kw of one row, one aligned word
-  kPatchGeneral = 2,  // element by element
+  kPatchNhwcVec = 0,  // fp32 NHWC, C % 4 == 0, no padding: four channels of one tap, one 16-byte load
+  kPatchU8Word = 1,   // uint8 NCHW, KW, W, S multiples of 4, no padding: four kw of one row, one aligned word
+  kPatchGeneral = 2,  // element by element, any geometry
 };
 
 __host__ inline int patch_mode(const ConvGeo& g, bool aligned) {
-  if (!g.u8 && g.C % 4 == 0 && aligned) return kPatchNhwcVec;
-  if (g.u8 && g.KW % 4 == 0 && g.W % 4 == 0 && g.S % 4 == 0 && g.P % 4 == 0 && aligned) return kPatchU8Word;
+  if (g.P == 0 && !g.u8 && g.C % 4 == 0 && aligned) return kPatchNhwcVec;
+  if (g.P == 0 && g.u8 && g.KW % 4 == 0 && g.W % 4 == 0 && g.S % 4 == 0 && aligned) return kPatchU8Word;
   return kPatchGeneral;
 }
 
-// Output pixel m as an input position: byte offset of (b, ih0, iw0) and
-// ih0 = oh*S - P, iw0 = ow*S - P; a pixel past the end gets kBad and an ih0
-// far below zero.  Without padding every tap of a real pixel is inside the
-// image, so the byte offset alone carries validity.
-struct PixelPos {
-  uint32_t base;
-  int ih0, iw0;
-};
-__device__ __forceinline__ PixelPos pixel_pos(const ConvCore& g, int m) {
-  if (m >= g.M) return PixelPos{kBad, -(1 << 28), 0};
+// Vector modes (no padding).  pixel_base: byte offset of output pixel m's
+// first tap, (b, oh*S, ow*S); kBad past the last pixel.  tap_off: byte
+// offset of patch chunk k..k+3 relative to it; kBad past the patch.  Their
+// sum is in range exactly when both are valid.
+__device__ __forceinline__ uint32_t pixel_base(const ConvCore& g, int m) {
+  if (m >= g.M) return kBad;
   int b, oh, ow;
   g.split_m(m, b, oh, ow);
-  const int ih0 = oh * g.S - g.P, iw0 = ow * g.S - g.P;
+  const int ih0 = oh * g.S, iw0 = ow * g.S;
   const int e = g.u8 ? (b * g.C * g.H + ih0) * g.W + iw0 : ((b * g.H + ih0) * g.W + iw0) * g.C;
-  return PixelPos{uint32_t(e) * (g.u8 ? 1u : 4u), ih0, iw0};
+  return uint32_t(e) * (g.u8 ? 1u : 4u);
 }
-
-// Patch chunk k..k+3 as a tap: byte offset relative to the pixel base and
-// (kh, kw) of its first element; kBad past the patch.
-struct TapPos {
-  uint32_t off;
-  int kh, kw;
-};
-__device__ __forceinline__ TapPos tap_pos(const ConvCore& g, int k) {
-  if (k >= g.kp) return TapPos{kBad, 0, 0};
+__device__ __forceinline__ uint32_t tap_off(const ConvCore& g, int k) {
+  if (k >= g.kp) return kBad;
   int c, kh, kw;
   g.split_k(k, c, kh, kw);
   const int e = g.u8 ? (c * g.H + kh) * g.W + kw : (kh * g.W + kw) * g.C + c;
-  return TapPos{uint32_t(e) * (g.u8 ? 1u : 4u), kh, kw};
+  return uint32_t(e) * (g.u8 ? 1u : 4u);
 }
 
-// Starts the load of patch chunk (pixel, tap) in the given mode.
-__device__ __forceinline__ void patch_issue(__amdgpu_buffer_rsrc_t rs, const ConvCore& g, int mode, const PixelPos& px,
-                                            const TapPos& tp, Fetch4& f) {
-  uint32_t off = px.base + tp.off;
-  if (g.P != 0) {  // borders: the tap may fall outside the image
-    const int ih = px.ih0 + tp.kh, iw = px.iw0 + tp.kw;
-    const int wlast = mode == kPatchU8Word ? iw + 3 : iw;
-    if (ih < 0 || ih >= g.H || iw < 0 || wlast >= g.W) off = kBad;
-  }
-  if (mode == kPatchNhwcVec) f.v = ld_f4(rs, off);
-  else f.v.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
-}
-
-// Forward A operand: A(m, k) = patch(m, k).
+// Forward A operand: A(m, k) = patch(m, k).  MODE is how four consecutive
+// patch indices lie in memory (PatchMode); the vector modes assume no
+// padding, so a real pixel's taps are all inside the image and the byte
+// offset alone carries validity.
+template <int MODE>
 struct LdConvFwd {
   ConvGeo g;
   const void* x[kMaxGroups];
   uint32_t xbytes;
-  int mode;
 
   struct Params {
     ConvCore g;
     const void* x;
     uint32_t xbytes;
-    int mode;
   };
   struct Live {
     static constexpr bool KCONTIG = true;
     Params q;
     __amdgpu_buffer_rsrc_t rs;
-    struct Row { PixelPos px; };  // the general mode keeps the pixel index in px.base
-    struct Kp { TapPos tp; int k; };
+    struct Row { uint32_t base; };  // vector modes: byte offset of the pixel's first tap; general: m
+    struct Kp { uint32_t off; int k; };
     __device__ __forceinline__ int fmt() const {
-      return q.mode == kPatchU8Word ? kU8Word : (q.mode == kPatchGeneral && q.g.u8 ? kU8Each : kF32);
+      if constexpr (MODE == kPatchU8Word) return kU8Word;
+      else if constexpr (MODE == kPatchNhwcVec) return kF32;
+      else return q.g.u8 ? kU8Each : kF32;
     }
     __device__ __forceinline__ Row row(int m) const {
-      return q.mode == kPatchGeneral ? Row{PixelPos{uint32_t(m), 0, 0}} : Row{pixel_pos(q.g, m)};
+      if constexpr (MODE == kPatchGeneral) return Row{uint32_t(m)};
+      else return Row{pixel_base(q.g, m)};
     }
     __device__ __forceinline__ Kp kpos(int k) const {
-      return Kp{q.mode == kPatchGeneral ? TapPos{} : tap_pos(q.g, k), k};
+      if constexpr (MODE == kPatchGeneral) return Kp{0u, k};
+      else return Kp{tap_off(q.g, k), k};
     }
     __device__ __forceinline__ void issue(const Row& r, const Kp& kp, Fetch4& f) const {
-      if (q.mode != kPatchGeneral) {
-        patch_issue(rs, q.g, q.mode, r.px, kp.tp, f);
-        return;
-      }
+      if constexpr (MODE == kPatchNhwcVec) {
+        f.v = ld_f4(rs, r.base + kp.off);
+      } else if constexpr (MODE == kPatchU8Word) {
+        f.v.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, r.base + kp.off, 0, 0));
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, q.g, int(r.px.base), kp.k + j);
+        for (int j = 0; j < 4; ++j) f.v[j] = patch_elem(rs, q.g, int(r.base), kp.k + j);
+      }
     }
   };
   __device__ __forceinline__ Live live(int grp) const {
-    const Params q = pin_pod(Params{conv_core(g), x[grp], xbytes, mode});
+    const Params q = pin_pod(Params{conv_core(g), x[grp], xbytes});
     return Live{q, make_res(q.x, q.xbytes)};
   }
 };
 
 // Weight-gradient A operand: A(r = k, k = m) = patch(m, r), with the ones row
-// at r == kp when the bias gradient is wanted.
+// at r == kp when the bias gradient is wanted.  MODE as for LdConvFwd; the
+// chunk that holds the ones row goes element by element in every mode.
+template <int MODE>
 struct LdConvPatchT {
   ConvGeo g;
   const void* x[kMaxGroups];
   uint32_t xbytes;
-  int mode;
   int ones;
 
   struct Params {
     ConvCore g;
     const void* x;
     uint32_t xbytes;
-    int mode, ones;
+    int ones;
   };
   struct Live {
     static constexpr bool KCONTIG = false;
     Params q;
     __amdgpu_buffer_rsrc_t rs;
-    struct Row { TapPos tp; int r; bool whole; };
+    struct Row { uint32_t tap; int r; bool whole; };
     struct Ks { int m; };
     __device__ __forceinline__ int fmt() const {
-      return q.mode == kPatchU8Word ? kU8Word : (q.g.u8 ? kU8Each : kF32);
+      if constexpr (MODE == kPatchU8Word) return kU8Word;
+      else return q.g.u8 ? kU8Each : kF32;
     }
     __device__ __forceinline__ Row row(int r) const {
-      const bool whole = q.mode != kPatchGeneral && r + 3 < q.g.kp;
-      return Row{whole ? tap_pos(q.g, r) : TapPos{}, r, whole};
+      const bool whole = MODE != kPatchGeneral && r + 3 < q.g.kp;
+      return Row{whole ? tap_off(q.g, r) : 0u, r, whole};
     }
     __device__ __forceinline__ Ks kstage(const Row&, int m) const { return Ks{m}; }
     __device__ __forceinline__ void issue(const Row& r, const Ks& ks, int dm, Fetch4& f) const {
       const int m = ks.m + dm;
-      if (r.whole) {
-        patch_issue(rs, q.g, q.mode, pixel_pos(q.g, m), r.tp, f);
-        return;
+      if constexpr (MODE != kPatchGeneral) {
+        if (r.whole) {
+          const uint32_t off = pixel_base(q.g, m) + r.tap;
+          if constexpr (MODE == kPatchNhwcVec) f.v = ld_f4(rs, off);
+          else f.v.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+          return;
+        }
       }
       // The general path and the tail chunk: patch rows, then the ones row.
 #pragma unroll
@@ -245,7 +239,7 @@ struct LdConvPatchT {
     }
   };
   __device__ __forceinline__ Live live(int grp) const {
-    const Params q = pin_pod(Params{conv_core(g), x[grp], xbytes, mode, ones});
+    const Params q = pin_pod(Params{conv_core(g), x[grp], xbytes, ones});
     return Live{q, make_res(q.x, q.xbytes)};
   }
 };
@@ -441,10 +435,9 @@ struct EpConvDx {
   }
 };
 
-namespace {
 
 // Residue-class tables of classes cls0 .. cls0+kMaxGroups-1 (empty past S*S).
-void set_classes(ConvGeo& g, int cls0) {
+inline void set_classes(ConvGeo& g, int cls0) {
   g.cls0 = cls0;
   for (int grp = 0; grp < kMaxGroups; ++grp) {
     const int cls = cls0 + grp;
@@ -462,7 +455,7 @@ void set_classes(ConvGeo& g, int cls0) {
   }
 }
 
-int make_geo(const ttrl_conv_geom* s, ConvGeo& g) {
+inline int make_geo(const ttrl_conv_geom* s, ConvGeo& g) {
   TTRL_REQUIRE(s, "conv: null geometry");
   TTRL_REQUIRE(s->batch > 0 && s->in_c > 0 && s->in_h > 0 && s->in_w > 0 && s->out_c > 0 && s->kernel > 0 &&
                    s->stride > 0 && s->padding >= 0,
@@ -511,137 +504,4 @@ inline bool input_aligned(const ConvGeo& g, const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & (g.u8 ? 3 : 15)) == 0;
 }
 
-int conv_forward(ttrl_ctx* ctx, const ConvGeo& g, int groups, const void* const* x, const float* const* wt,
-                 const float* const* bias, float* const* y, float x_scale, int relu, const char* name) {
-  const int K = g.C * g.KH * g.KW;
-  LdConvFwd la{g, {}, input_bytes(g), kPatchGeneral};
-  LdColK lb;  // B(k, n=o) = Wt[k][o]
-  EpStore ep;
-  bool xal = true;
-  for (int i = 0; i < groups; ++i) {
-    TTRL_REQUIRE(x[i] && wt[i] && y[i], "%s: null pointer in group %d", name, i);
-    xal = xal && input_aligned(g, x[i]);
-    la.x[i] = x[i];
-    lb.p[i] = wt[i];
-    ep.C[i] = y[i];
-    ep.bias[i] = bias ? bias[i] : nullptr;
-  }
-  lb.ld = g.O;
-  lb.rows = g.O;
-  lb.K = K;
-  bool al = true;
-  for (int i = 0; i < groups; ++i) al = al && (reinterpret_cast<uintptr_t>(wt[i]) & 15) == 0;
-  lb.vec_ok(al);
-  la.mode = patch_mode(g, xal);
-  ep.M = g.M;
-  ep.N = g.O;
-  ep.ldc = g.O;
-  ep.alpha = x_scale;
-  ep.relu = relu;
-  return run_gemm<kConvFwdCfgs>(ctx, la, lb, ep, g.M, g.O, K, groups, name);
-}
-
-}  // namespace
 }  // namespace ttrl
-
-using namespace ttrl;
-
-extern "C" {
-
-int ttrl_conv_out_size(int size, int kernel, int stride, int padding, int* out) {
-  TTRL_REQUIRE(out, "ttrl_conv_out_size: null out");
-  TTRL_REQUIRE(kernel > 0 && stride > 0 && padding >= 0 && size > 0, "ttrl_conv_out_size: bad arguments");
-  const int span = size + 2 * padding - kernel;
-  TTRL_REQUIRE(span >= 0, "ttrl_conv_out_size: kernel %d larger than padded size %d", kernel, size + 2 * padding);
-  TTRL_REQUIRE(span % stride == 0, "ttrl_conv_out_size: ragged geometry (size %d, kernel %d, stride %d, padding %d)",
-               size, kernel, stride, padding);
-  *out = span / stride + 1;
-  return TTRL_OK;
-}
-
-int ttrl_conv2d_forward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, const float* wt,
-                        const float* bias, float* y, float x_scale, int relu) {
-  TTRL_REQUIRE(ctx && x && wt && y, "ttrl_conv2d_forward: null argument");
-  ConvGeo g;
-  int rc = make_geo(geom, g);
-  if (rc) return rc;
-  const void* xs[1] = {x};
-  const float* ws[1] = {wt};
-  const float* bs[1] = {bias};
-  float* ys[1] = {y};
-  return conv_forward(ctx, g, 1, xs, ws, bs, ys, x_scale, relu, "ttrl_conv2d_forward");
-}
-
-int ttrl_conv2d_forward_multi(ttrl_ctx* ctx, const ttrl_conv_geom* geom, int groups, const void* const* x,
-                              const float* const* wt, const float* const* bias, float* const* y, float x_scale,
-                              int relu) {
-  TTRL_REQUIRE(ctx && x && wt && y, "ttrl_conv2d_forward_multi: null argument");
-  TTRL_REQUIRE(groups >= 1 && groups <= kMaxGroups, "ttrl_conv2d_forward_multi: 1..%d groups", kMaxGroups);
-  ConvGeo g;
-  int rc = make_geo(geom, g);
-  if (rc) return rc;
-  return conv_forward(ctx, g, groups, x, wt, bias, y, x_scale, relu, "ttrl_conv2d_forward_multi");
-}
-
-int ttrl_conv2d_backward_weight(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale,
-                                const float* dy, const float* ymask, float* dwt, float* db, float beta) {
-  TTRL_REQUIRE(ctx && x && dy && dwt, "ttrl_conv2d_backward_weight: null argument");
-  ConvGeo g;
-  int rc = make_geo(geom, g);
-  if (rc) return rc;
-  const int Kp = g.C * g.KH * g.KW;
-  long reserved = 0;
-  if (ymask) {
-    dy = relu_mask_into_workspace(ctx, dy, ymask, long(g.M) * g.O, 0, 1, &reserved, &rc);
-    if (rc) return rc;
-  }
-  LdConvPatchT la{g, {x}, input_bytes(g), patch_mode(g, input_aligned(g, x)), db ? 1 : 0};
-  LdColK lb;  // B(r=o, k=m) = dZ[m][o]
-  lb.p[0] = dy;
-  lb.ld = g.O;
-  lb.rows = g.O;
-  lb.K = g.M;
-  lb.vec_ok((reinterpret_cast<uintptr_t>(dy) & 15) == 0);
-  EpStore ep;
-  ep.M = db ? Kp + 1 : Kp;
-  ep.N = g.O;
-  ep.C[0] = dwt;
-  ep.ldc = g.O;
-  ep.rsplit = Kp;
-  ep.Cr[0] = db;
-  ep.alpha = x_scale;  // d/dW of conv(s*x, W) = s * dW(x, dY); the bias row is unscaled
-  ep.alpha_r = 1.f;
-  ep.beta = beta;
-  return run_gemm<kConvDwCfgs>(ctx, la, lb, ep, ep.M, g.O, g.M, 1, "ttrl_conv2d_backward_weight", reserved);
-}
-
-int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const float* dy, const float* ymask,
-                               const float* wt, float* dx, const float* xmask, float x_scale, float beta) {
-  TTRL_REQUIRE(ctx && dy && wt && dx, "ttrl_conv2d_backward_input: null argument");
-  ConvGeo g;
-  int rc = make_geo(geom, g);
-  if (rc) return rc;
-  TTRL_REQUIRE(!g.u8, "ttrl_conv2d_backward_input: a uint8 frame input has no gradient");
-  long reserved = 0;
-  if (ymask) {
-    dy = relu_mask_into_workspace(ctx, dy, ymask, long(g.M) * g.O, 0, 1, &reserved, &rc);
-    if (rc) return rc;
-  }
-  const int Kd = g.TH * g.TW * g.O;
-  const int classes = g.S * g.S;
-  // One launch covers up to kMaxGroups residue classes; the largest class
-  // (ih0 = iw0 = 0) has ceil(H/S) * ceil(W/S) pixels per image.
-  const int Mmax = g.B * ((g.H + g.S - 1) / g.S) * ((g.W + g.S - 1) / g.S);
-  for (int c0 = 0; c0 < classes; c0 += kMaxGroups) {
-    const int n = std::min(kMaxGroups, classes - c0);
-    set_classes(g, c0);
-    LdConvDxA la{g, dy, uint32_t(long(g.M) * g.O * 4)};
-    LdConvDxB lb{g, wt, uint32_t(long(g.C) * g.KH * g.KW * g.O * 4)};
-    EpConvDx ep{g, dx, xmask, x_scale, beta};
-    rc = run_gemm<kConvDxCfgs>(ctx, la, lb, ep, Mmax, g.C, Kd, n, "ttrl_conv2d_backward_input", reserved);
-    if (rc) return rc;
-  }
-  return TTRL_OK;
-}
-
-}  // extern "C"
