@@ -1,25 +1,29 @@
 // FP32 MFMA tile GEMM core for gfx950: C[g](m, n) = sum_k A[g](m, k) * B[g](k, n).
 //
-// Work decomposition.  A workgroup of WGM x WGN wavefronts (64 lanes each)
-// owns a BM x BN output tile; each wavefront owns a (BM/WGM) x (BN/WGN)
-// sub-tile built from 16x16 v_mfma_f32_16x16x4f32 fragments.  The reduction
-// is staged through LDS in slices of TBK (up to 256): at the batch sizes of
-// a learner update most workgroups own a single slice, so every global load
-// of the workgroup is in flight at once and the load latency is paid once.
+// Work decomposition.  A workgroup of WGM x WGN wavefronts (64 lanes each),
+// times WGK groups along k, owns a BM x BN output tile; each wavefront owns
+// a (BM/WGM) x (BN/WGN) sub-tile built from 16x16 v_mfma_f32_16x16x4f32
+// fragments.  The reduction is staged through LDS in slices of TBK (up to
+// 256), the next slice's global loads in flight while the current one's
+// MFMAs run.  At the batch sizes of a learner update most workgroups own
+// one or two slices, so a kernel's time is one workgroup's latency chain;
+// the code below is arranged to keep that chain short.
 //
 // MFMA operand order.  Lane l of step s supplies A(row l%16, k = 4*(l/16)+s)
 // and B(k = 4*(l/16)+s, col l%16): a fixed permutation of each 16-wide
 // k-block shared by both operands, so the block is summed exactly once.
 //
 // Operands come from loader objects, so one core serves dense matrices in
-// either storage order, implicit-GEMM convolution patches, masked ReLU
-// gradients and the implicit ones row that folds a bias gradient into a
-// weight-gradient GEMM.  A KCONTIG loader returns four consecutive k of one
-// row and is staged row-major ([rows][TBK+4], one 128-bit LDS read feeds four
-// MFMAs); any other loader returns four consecutive rows at one k and is
-// staged k-major ([TBK][rows+4], 128-bit LDS stores, 32-bit reads), so
-// neither layout takes bank conflicts on its stores.  Loaders bounds-check
-// and return zeros outside the operand, so ragged M, N and K need no padding.
+// either storage order, implicit-GEMM convolution patches and the implicit
+// ones row that folds a bias gradient into a weight-gradient GEMM.  A
+// KCONTIG loader returns four consecutive k of one row and is staged
+// row-major ([rows][TBK+4], one 128-bit LDS read feeds four MFMAs); any
+// other loader returns four consecutive rows at one k and is staged k-major
+// ([TBK][rows+4], 128-bit LDS stores, 32-bit reads), so neither layout takes
+// bank conflicts on its stores.  Loaders bounds-check and return zeros
+// outside the operand, so ragged M, N and K need no padding.  Epilogues
+// apply bias, ReLU, clamp, a ReLU gate of the consuming layer's input, a
+// scale and beta-accumulation as the tile is stored.
 //
 // blockIdx.z = group * splits + split: groups are independent problems
 // (per-group pointer tables: twin critics, online/target networks,
