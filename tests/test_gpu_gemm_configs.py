@@ -1,6 +1,7 @@
 """Every tile shape of the GEMM core (forced through TTRL_GEMM_FORCE, with and
 without split-K) on ragged linear and convolution problems of each loader
-kind, against float64.  A shape a call site does not instantiate falls back
+kind, against float64, alone and as paired launches (a layer's dW and dX in
+one kernel: linear backward and ttrl_conv2d_backward).  A shape a call site does not instantiate falls back
 to its normal plan, which is checked the same way.  Tolerance: rel 2e-5 of
 each output's scale (fp32 accumulation over at most a few thousand terms)."""
 
@@ -99,3 +100,10 @@ def test_conv_each_tile(device, monkeypatch, cfg, splits, u8):
         device.call("ttrl_conv2d_backward_input", C.byref(g), dzd.vp, None, wd.vp, dx.vp, None, C.c_float(1.0),
                     C.c_float(0.0))
         assert _rel(dx.numpy(), dx_ref) < 2e-5
+        # both gradients in one paired launch
+        dw2, db2, dx2 = DeviceArray(device, wt.shape), DeviceArray(device, (O,)), DeviceArray(device, (B, H, W, Cc))
+        device.call("ttrl_conv2d_backward", C.byref(g), xd.vp, C.c_float(scale), dzd.vp, None, wd.vp, dw2.vp, db2.vp,
+                    C.c_float(0.0), dx2.vp, None, C.c_float(0.0))
+        assert _rel(master_to_oihw(dw2.numpy(), w.shape, layout), dw_ref) < 2e-5
+        assert _rel(db2.numpy(), db_ref) < 2e-5
+        assert _rel(dx2.numpy(), dx_ref) < 2e-5

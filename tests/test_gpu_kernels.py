@@ -136,6 +136,16 @@ def test_conv_forward_and_gradients(device, case):
         device.call("ttrl_conv2d_backward_input", C.byref(g), dzd.vp, None, wd.vp, dx2.vp, xd.vp, C.c_float(1.0),
                     C.c_float(0.0))
         assert _rel(dx2.numpy(), dx_ref * (x_nhwc > 0)) < 2e-5
+        # Both gradients in one call (a paired launch), with the output's and
+        # the input's ReLU gates and beta accumulation into preset buffers.
+        dw3, db3, dx3 = DeviceArray(device, wt.shape), DeviceArray(device, (O,)), DeviceArray(device, (B, H, W, Cc))
+        for t in (dw3, db3, dx3):
+            t.fill(0.5)
+        device.call("ttrl_conv2d_backward", C.byref(g), xd.vp, C.c_float(scale), dyd.vp, y.vp, wd.vp, dw3.vp, db3.vp,
+                    C.c_float(1.0), dx3.vp, xd.vp, C.c_float(2.0))
+        assert _rel(master_to_oihw(dw3.numpy(), w.shape, layout) - 0.5, dw_ref) < 2e-5
+        assert _rel(db3.numpy() - 0.5, db_ref) < 2e-5
+        assert _rel(dx3.numpy() - 1.0, dx_ref * (x_nhwc > 0)) < 2e-5
 
 
 def test_adam_step_matches_fused_oracle_over_steps(device):

@@ -504,4 +504,54 @@ inline bool input_aligned(const ConvGeo& g, const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & (g.u8 ? 3 : 15)) == 0;
 }
 
+// The weight-gradient GEMM of a layer: dWt_aug[r][o] = x_scale * sum_m
+// patch(m, r) dZ[m][o], row kp (when db is wanted) the bias gradient.
+template <int MODE>
+struct ConvDwProblem {
+  LdConvPatchT<MODE> la;
+  LdColK lb;
+  EpStore ep;
+  GemmDims q;
+};
+template <int MODE>
+inline ConvDwProblem<MODE> conv_dw_problem(const ConvGeo& g, const void* x, float x_scale, const float* dy, float* dwt,
+                                           float* db, float beta) {
+  const int Kp = g.C * g.KH * g.KW;
+  ConvDwProblem<MODE> p{LdConvPatchT<MODE>{g, {x}, input_bytes(g), db ? 1 : 0}, LdColK{}, EpStore{}, GemmDims{}};
+  p.lb.p[0] = dy;  // B(r=o, k=m) = dZ[m][o]
+  p.lb.ld = g.O;
+  p.lb.rows = g.O;
+  p.lb.K = g.M;
+  p.lb.vec_ok((reinterpret_cast<uintptr_t>(dy) & 15) == 0);
+  p.ep.M = db ? Kp + 1 : Kp;
+  p.ep.N = g.O;
+  p.ep.C[0] = dwt;
+  p.ep.ldc = g.O;
+  p.ep.rsplit = Kp;
+  p.ep.Cr[0] = db;
+  p.ep.alpha = x_scale;  // d/dW of conv(s*x, W) = s * dW(x, dY); the bias row is unscaled
+  p.ep.alpha_r = 1.f;
+  p.ep.beta = beta;
+  p.q = GemmDims{p.ep.M, g.O, g.M, 1};
+  return p;
+}
+
+// The input-gradient GEMM of residue classes c0 .. c0+n-1 (n <= kMaxGroups).
+struct ConvDxProblem {
+  LdConvDxA la;
+  LdConvDxB lb;
+  EpConvDx ep;
+  GemmDims q;
+};
+inline ConvDxProblem conv_dx_problem(ConvGeo g, int c0, const float* dy, const float* wt, float* dx,
+                                     const float* xmask, float x_scale, float beta) {
+  const int n = std::min(kMaxGroups, g.S * g.S - c0);
+  set_classes(g, c0);
+  // The largest class (ih0 = iw0 = 0) has ceil(H/S) * ceil(W/S) pixels per image.
+  const int Mmax = g.B * ((g.H + g.S - 1) / g.S) * ((g.W + g.S - 1) / g.S);
+  return ConvDxProblem{LdConvDxA{g, dy, uint32_t(long(g.M) * g.O * 4)},
+                       LdConvDxB{g, wt, uint32_t(long(g.C) * g.KH * g.KW * g.O * 4)},
+                       EpConvDx{g, dx, xmask, x_scale, beta}, GemmDims{Mmax, g.C, g.TH * g.TW * g.O, n}};
+}
+
 }  // namespace ttrl

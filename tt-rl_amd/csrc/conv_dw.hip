@@ -9,25 +9,8 @@ namespace {
 template <int MODE, unsigned CFGS>
 int conv_backward_weight_mode(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
                               float* dwt, float* db, float beta, long reserved) {
-  const int Kp = g.C * g.KH * g.KW;
-  LdConvPatchT<MODE> la{g, {x}, input_bytes(g), db ? 1 : 0};
-  LdColK lb;  // B(r=o, k=m) = dZ[m][o]
-  lb.p[0] = dy;
-  lb.ld = g.O;
-  lb.rows = g.O;
-  lb.K = g.M;
-  lb.vec_ok((reinterpret_cast<uintptr_t>(dy) & 15) == 0);
-  EpStore ep;
-  ep.M = db ? Kp + 1 : Kp;
-  ep.N = g.O;
-  ep.C[0] = dwt;
-  ep.ldc = g.O;
-  ep.rsplit = Kp;
-  ep.Cr[0] = db;
-  ep.alpha = x_scale;  // d/dW of conv(s*x, W) = s * dW(x, dY); the bias row is unscaled
-  ep.alpha_r = 1.f;
-  ep.beta = beta;
-  return run_gemm<CFGS>(ctx, la, lb, ep, ep.M, g.O, g.M, 1, "ttrl_conv2d_backward_weight", reserved);
+  const ConvDwProblem<MODE> p = conv_dw_problem<MODE>(g, x, x_scale, dy, dwt, db, beta);
+  return run_gemm<CFGS>(ctx, p.la, p.lb, p.ep, p.q.M, p.q.N, p.q.K, 1, "ttrl_conv2d_backward_weight", reserved);
 }
 
 }  // namespace

@@ -21,18 +21,10 @@ int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const 
     dy = relu_mask_into_workspace(ctx, dy, ymask, long(g.M) * g.O, 0, 1, &reserved, &rc);
     if (rc) return rc;
   }
-  const int Kd = g.TH * g.TW * g.O;
-  const int classes = g.S * g.S;
-  // One launch covers up to kMaxGroups residue classes; the largest class
-  // (ih0 = iw0 = 0) has ceil(H/S) * ceil(W/S) pixels per image.
-  const int Mmax = g.B * ((g.H + g.S - 1) / g.S) * ((g.W + g.S - 1) / g.S);
-  for (int c0 = 0; c0 < classes; c0 += kMaxGroups) {
-    const int n = std::min(kMaxGroups, classes - c0);
-    set_classes(g, c0);
-    LdConvDxA la{g, dy, uint32_t(long(g.M) * g.O * 4)};
-    LdConvDxB lb{g, wt, uint32_t(long(g.C) * g.KH * g.KW * g.O * 4)};
-    EpConvDx ep{g, dx, xmask, x_scale, beta};
-    rc = run_gemm<kConvDxCfgs>(ctx, la, lb, ep, Mmax, g.C, Kd, n, "ttrl_conv2d_backward_input", reserved);
+  for (int c0 = 0; c0 < g.S * g.S; c0 += kMaxGroups) {
+    const ConvDxProblem p = conv_dx_problem(g, c0, dy, wt, dx, xmask, x_scale, beta);
+    rc = run_gemm<kConvDxCfgs>(ctx, p.la, p.lb, p.ep, p.q.M, p.q.N, p.q.K, p.q.groups, "ttrl_conv2d_backward_input",
+                               reserved);
     if (rc) return rc;
   }
   return TTRL_OK;

@@ -133,6 +133,9 @@ constexpr unsigned kLinFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32
 constexpr unsigned kLinDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
                                 cfg_bit(T128x64) | kSmallK | cfg_bit(T64x64K2);
 constexpr unsigned kLinDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) | kSmallK;
+// A layer's dW and dx in one launch (k_gemm_pair): one tile shape for both.
+constexpr unsigned kLinPairCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T32x32K2) |
+                                  cfg_bit(T64x32K2);
 
 __global__ __launch_bounds__(256) void k_relu_mask(float* dst, const float* src, const float* mask, long n, long gs,
                                                    int groups) {
@@ -361,84 +364,94 @@ int ttrl_linear_backward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
   }
   const bool dyal = all_aligned(dy, G);
 
+  // dW_aug[k][n] = sum_m xaug[m][k] dZ[m][n], xaug = [x | 1]; row K is db.
+  LdColK wa;  // A(r=k_in, k=m) = x[m][k_in]
+  LdColK wb;  // B(r=n, k=m) = dZ[m][n]
+  EpStore wep;
+  GemmDims wq{0, 0, 0, G};
   if (d->dW) {
     TTRL_REQUIRE(d->x && !d->x2, "ttrl_linear_backward: dW needs a single dense input x");
     TTRL_REQUIRE(!d->W2 || d->dW2, "ttrl_linear_backward: a split weight needs dW2");
-    // dW_aug[k][n] = sum_m xaug[m][k] dZ[m][n], xaug = [x | 1]; row K is db.
     const bool with_b = d->db != nullptr;
     TTRL_REQUIRE(!with_b || !d->W2 || d->db2, "ttrl_linear_backward: a split bias needs db2");
-    LdColK la;  // A(r=k_in, k=m) = x[m][k_in]
-    groups_of(la.p, d->x, d->gx, G);
-    la.ld = d->ldx;
-    la.rows = with_b ? d->K + 1 : d->K;
-    la.K = d->M;
-    la.real_rows = d->K;
-    la.ones = with_b;
-    la.vec_ok(all_aligned(la.p, G));
-    LdColK lb;  // B(r=n, k=m) = dZ[m][n]
-    for (int g = 0; g < kMaxGroups; ++g) lb.p[g] = dy[g];
-    lb.ld = d->N;
-    lb.rows = d->N;
-    lb.K = d->M;
-    lb.vec_ok(dyal);
-    EpStore ep;
-    ep.M = la.rows;
-    ep.N = d->N;
-    groups_of(ep.C, d->dW, d->gW, G);
-    ep.ldc = n1;
-    ep.rsplit = d->K;
-    groups_of(ep.Cr, d->db, d->gb, G);
-    ep.beta = d->beta_w;
+    groups_of(wa.p, d->x, d->gx, G);
+    wa.ld = d->ldx;
+    wa.rows = with_b ? d->K + 1 : d->K;
+    wa.K = d->M;
+    wa.real_rows = d->K;
+    wa.ones = with_b;
+    wa.vec_ok(all_aligned(wa.p, G));
+    for (int g = 0; g < kMaxGroups; ++g) wb.p[g] = dy[g];
+    wb.ld = d->N;
+    wb.rows = d->N;
+    wb.K = d->M;
+    wb.vec_ok(dyal);
+    wep.M = wa.rows;
+    wep.N = d->N;
+    groups_of(wep.C, d->dW, d->gW, G);
+    wep.ldc = n1;
+    wep.rsplit = d->K;
+    groups_of(wep.Cr, d->db, d->gb, G);
+    wep.beta = d->beta_w;
     if (d->W2) {
-      ep.csplit = n1;
-      groups_of(ep.Cc, d->dW2, d->gW, G);
-      ep.ldcc = d->N - n1;
-      groups_of(ep.Crc, d->db2, d->gb, G);
+      wep.csplit = n1;
+      groups_of(wep.Cc, d->dW2, d->gW, G);
+      wep.ldcc = d->N - n1;
+      groups_of(wep.Crc, d->db2, d->gb, G);
     }
-    TTRL_FITS(la, lb, "ttrl_linear_backward");
-    int rc = run_gemm<kLinDwCfgs>(ctx, la, lb, ep, la.rows, d->N, d->M > 0 ? d->M : 1, G, "ttrl_linear_backward dW",
-                                  reserved);
-    if (rc) return rc;
+    TTRL_FITS(wa, wb, "ttrl_linear_backward");
+    wq = GemmDims{wa.rows, d->N, d->M > 0 ? d->M : 1, G};
   }
-  if (d->dx) {
-    const int c0 = d->dx_cols > 0 ? d->dx_col0 : 0;
-    const int nc = d->dx_cols > 0 ? d->dx_cols : d->K;
-    TTRL_REQUIRE(c0 >= 0 && c0 + nc <= d->K, "ttrl_linear_backward: dx column range out of bounds");
-    LdRowK la;  // A(m, k=n) = dZ[m][n]
-    for (int g = 0; g < kMaxGroups; ++g) la.p[g] = dy[g];
-    la.ld = d->N;
-    la.rows = d->M;
-    la.K = d->N;
-    la.vec_ok(dyal);
-    EpStore ep;
-    ep.M = d->M;
-    ep.N = nc;
-    groups_of(ep.C, d->dx, d->gdx, G);
-    groups_of(ep.mask, d->dxmask, d->gdx, G);
-    ep.ldc = d->lddx > 0 ? d->lddx : nc;
-    ep.beta = d->beta_x;
-    if (d->W2) {
-      LdRowKCat lb;  // B(r=k_in, k=n): n < n1 from W[k_in][n], else W2[k_in][n-n1]
-      groups_of(lb.p1, d->W ? d->W + long(c0) * n1 : nullptr, d->gW, G);
-      groups_of(lb.p2, d->W2 + long(c0) * (d->N - n1), d->gW, G);
-      lb.ld1 = n1;
-      lb.ld2 = d->N - n1;
-      lb.rows = nc;
-      lb.k1 = n1;
-      lb.K = d->N;
-      TTRL_FITS(la, lb, "ttrl_linear_backward");
-      return run_gemm<kLinDxCfgs>(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx", reserved);
+  if (!d->dx)
+    return d->dW ? run_gemm<kLinDwCfgs>(ctx, wa, wb, wep, wq.M, wq.N, wq.K, G, "ttrl_linear_backward dW", reserved)
+                 : TTRL_OK;
+
+  const int c0 = d->dx_cols > 0 ? d->dx_col0 : 0;
+  const int nc = d->dx_cols > 0 ? d->dx_cols : d->K;
+  TTRL_REQUIRE(c0 >= 0 && c0 + nc <= d->K, "ttrl_linear_backward: dx column range out of bounds");
+  LdRowK xa;  // A(m, k=n) = dZ[m][n]
+  for (int g = 0; g < kMaxGroups; ++g) xa.p[g] = dy[g];
+  xa.ld = d->N;
+  xa.rows = d->M;
+  xa.K = d->N;
+  xa.vec_ok(dyal);
+  EpStore xep;
+  xep.M = d->M;
+  xep.N = nc;
+  groups_of(xep.C, d->dx, d->gdx, G);
+  groups_of(xep.mask, d->dxmask, d->gdx, G);
+  xep.ldc = d->lddx > 0 ? d->lddx : nc;
+  xep.beta = d->beta_x;
+  const GemmDims xq{d->M, nc, d->N, G};
+  // dW and dx are independent given dZ: one paired launch when both are wanted.
+  auto finish = [&](const auto& xb) -> int {
+    TTRL_FITS(xa, xb, "ttrl_linear_backward");
+    if (d->dW && d->M > 0)
+      return run_gemm_pair<kLinPairCfgs>(ctx, wa, wb, wep, wq, xa, xb, xep, xq, "ttrl_linear_backward", reserved);
+    if (d->dW) {
+      const int rc = run_gemm<kLinDwCfgs>(ctx, wa, wb, wep, wq.M, wq.N, wq.K, G, "ttrl_linear_backward dW", reserved);
+      if (rc) return rc;
     }
-    LdRowK lb;  // B(r=k_in, k=n) = W[k_in][n]
-    groups_of(lb.p, d->W + long(c0) * d->N, d->gW, G);
-    lb.ld = d->N;
-    lb.rows = nc;
-    lb.K = d->N;
-    lb.vec_ok(all_aligned(lb.p, G));
-    TTRL_FITS(la, lb, "ttrl_linear_backward");
-    return run_gemm<kLinDxCfgs>(ctx, la, lb, ep, d->M, nc, d->N, G, "ttrl_linear_backward dx", reserved);
+    return run_gemm<kLinDxCfgs>(ctx, xa, xb, xep, d->M, nc, d->N, G, "ttrl_linear_backward dx", reserved);
+  };
+  if (d->W2) {
+    LdRowKCat xb;  // B(r=k_in, k=n): n < n1 from W[k_in][n], else W2[k_in][n-n1]
+    groups_of(xb.p1, d->W ? d->W + long(c0) * n1 : nullptr, d->gW, G);
+    groups_of(xb.p2, d->W2 + long(c0) * (d->N - n1), d->gW, G);
+    xb.ld1 = n1;
+    xb.ld2 = d->N - n1;
+    xb.rows = nc;
+    xb.k1 = n1;
+    xb.K = d->N;
+    return finish(xb);
   }
-  return TTRL_OK;
+  LdRowK xb;  // B(r=k_in, k=n) = W[k_in][n]
+  groups_of(xb.p, d->W + long(c0) * d->N, d->gW, G);
+  xb.ld = d->N;
+  xb.rows = nc;
+  xb.K = d->N;
+  xb.vec_ok(all_aligned(xb.p, G));
+  return finish(xb);
 }
 
 }  // extern "C"

@@ -37,6 +37,8 @@
 #include <algorithm>
 #include <cstdio>
 #include <string>
+#include <type_traits>
+#include <utility>
 #include <vector>
 
 namespace ttrl {
@@ -710,9 +712,19 @@ __device__ __forceinline__ void warm_kernargs() {
 // summed through LDS in group order before the epilogue, so a workgroup's
 // MFMA chain, fetch count per thread and LDS traffic per wavefront shrink by
 // WGK at the same tile size.
+// LDS floats of one tile shape's A and B stages.
+template <int BM, int BN, int TBK, class LA, class LB>
+struct TileShared {
+  static constexpr int A = TileLds<BM, TBK, LA::Live::KCONTIG>::SIZE;
+  static constexpr int B = TileLds<BN, TBK, LB::Live::KCONTIG>::SIZE;
+  static constexpr int SIZE = A + B;
+};
+
+// One workgroup's output tile (bx, by) of problem bz = group * splits +
+// split, its stages in As and Bs.
 template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA, class LB, class EP>
-__global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP ep, float* ws, int M, int N, int K,
-                                                               int kchunk, int splits) {
+__device__ __forceinline__ void gemm_tile(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K,
+                                          int kchunk, int splits, int bx, int by, int bz, float* As, float* Bs) {
   constexpr int NT = 64 * WGM * WGN * WGK;
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -724,15 +736,12 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
   using LdsB = TileLds<BN, TBK, VB::KCONTIG>;
   constexpr int PA = Stage<BM, TBK, NT, VA>::PER;
   constexpr int PB = Stage<BN, TBK, NT, VB>::PER;
-  __shared__ __attribute__((aligned(16))) float As[LdsA::SIZE];
-  __shared__ __attribute__((aligned(16))) float Bs[LdsB::SIZE];
 
-  warm_kernargs<int(sizeof(LA) + sizeof(LB) + sizeof(EP) + sizeof(float*) + 5 * sizeof(int))>();
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wk = wave / (WGM * WGN), wmn = wave - wk * (WGM * WGN);
   const int wm = wmn % WGM, wn = wmn / WGM;
-  const int g = blockIdx.z / splits, split = blockIdx.z - g * splits;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int g = bz / splits, split = bz - g * splits;
+  const int m0 = bx * BM, n0 = by * BN;
   if (m0 >= ep.rows(g)) return;  // uniform per block: ragged residue classes
   const int kbeg = split * kchunk;
   const int kend = min(K, kbeg + kchunk);
@@ -834,6 +843,49 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
         for (int r = 0; r < 4; ++r) eb.store(mb + r, n0 + wn * WTN + j * 16 + lr, acc[i][j][r], x[j][r]);
     }
   });
+}
+
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA, class LB, class EP>
+__global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP ep, float* ws, int M, int N, int K,
+                                                               int kchunk, int splits) {
+  using S = TileShared<BM, BN, TBK, LA, LB>;
+  __shared__ __attribute__((aligned(16))) float lds[S::SIZE];
+  warm_kernargs<int(sizeof(LA) + sizeof(LB) + sizeof(EP) + sizeof(float*) + 5 * sizeof(int))>();
+  gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la, lb, ep, ws, M, N, K, kchunk, splits, blockIdx.x, blockIdx.y, blockIdx.z,
+                                        lds, lds + S::A);
+}
+
+// Extents and grid of one problem of a paired launch.
+struct PairDims {
+  int M, N, K, kchunk, splits, gx, gy, blocks;
+  long ws_off;  // its split-K partials start here in the workspace
+};
+
+// Two independent GEMMs of one tile shape in one launch (a layer's weight
+// and input gradients): workgroups [0, d1.blocks) run the first, the rest
+// the second, so the two fill the device together instead of one after the
+// other.  LDS is the larger of the two problems' stages.
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA1, class LB1, class EP1, class LA2, class LB2,
+          class EP2>
+__global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm_pair(LA1 la1, LB1 lb1, EP1 ep1, LA2 la2, LB2 lb2,
+                                                                    EP2 ep2, float* ws, PairDims d1, PairDims d2) {
+  using S1 = TileShared<BM, BN, TBK, LA1, LB1>;
+  using S2 = TileShared<BM, BN, TBK, LA2, LB2>;
+  constexpr int SIZE = S1::SIZE > S2::SIZE ? S1::SIZE : S2::SIZE;
+  __shared__ __attribute__((aligned(16))) float lds[SIZE];
+  warm_kernargs<int(sizeof(LA1) + sizeof(LB1) + sizeof(EP1) + sizeof(LA2) + sizeof(LB2) + sizeof(EP2) +
+                    sizeof(float*) + 2 * sizeof(PairDims))>();
+  int b = blockIdx.x;
+  if (b < d1.blocks) {
+    const int bx = b % d1.gx, byz = b / d1.gx;
+    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la1, lb1, ep1, ws + d1.ws_off, d1.M, d1.N, d1.K, d1.kchunk, d1.splits, bx,
+                                          byz % d1.gy, byz / d1.gy, lds, lds + S1::A);
+  } else {
+    b -= d1.blocks;
+    const int bx = b % d2.gx, byz = b / d2.gx;
+    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la2, lb2, ep2, ws + d2.ws_off, d2.M, d2.N, d2.K, d2.kchunk, d2.splits, bx,
+                                          byz % d2.gy, byz / d2.gy, lds, lds + S2::A);
+  }
 }
 
 // Sums split-K partials in split order and applies the epilogue; group
@@ -944,15 +996,19 @@ bool gemm_tuning_log();  // TTRL_GEMM_TUNE_LOG=1: print each tuned signature's c
 // tile shape wherever a call site allows it, bypassing the plan cache.
 bool gemm_forced(unsigned allowed, int M, int N, int K, int groups, long ws_floats, GemmPlan* out);
 
-template <unsigned ALLOWED, class LA, class LB, class EP>
-inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
-                           const GemmPlan& p, hipStream_t st) {
-#define TTRL_CFG(C, BM, BN, WGM, WGN, WGK, TBK)                                                          \
-  case C:                                                                                               \
-    if constexpr ((ALLOWED & cfg_bit(C)) != 0)                                                          \
-      launch_cfg<BM, BN, WGM, WGN, WGK, TBK>(la, lb, ep, ws, M, N, K, groups, p, st);                   \
+template <int BM_, int BN_, int WGM_, int WGN_, int WGK_, int TBK_>
+struct CfgTag {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, WGK = WGK_, TBK = TBK_;
+};
+
+// Calls f(CfgTag<...>{}) for tile shape `cfg` if ALLOWED instantiates it.
+template <unsigned ALLOWED, class F>
+inline void dispatch_cfg(int cfg, F&& f) {
+#define TTRL_CFG(C, BM, BN, WGM, WGN, WGK, TBK)                                        \
+  case C:                                                                             \
+    if constexpr ((ALLOWED & cfg_bit(C)) != 0) f(CfgTag<BM, BN, WGM, WGN, WGK, TBK>{}); \
     break;
-  switch (p.cfg) {
+  switch (cfg) {
     TTRL_CFG(T32x32, 32, 32, 2, 2, 1, 256)
     TTRL_CFG(T64x32, 64, 32, 2, 2, 1, 128)
     TTRL_CFG(T32x64, 32, 64, 2, 2, 1, 128)
@@ -968,6 +1024,15 @@ inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, 
     default: break;
   }
 #undef TTRL_CFG
+}
+
+template <unsigned ALLOWED, class LA, class LB, class EP>
+inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
+                           const GemmPlan& p, hipStream_t st) {
+  dispatch_cfg<ALLOWED>(p.cfg, [&](auto c) {
+    using C = decltype(c);
+    launch_cfg<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK>(la, lb, ep, ws, M, N, K, groups, p, st);
+  });
 }
 
 // Times the model's leading candidates on the real operands, writing into a
@@ -1039,6 +1104,127 @@ inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int
     ctx_plan_store(ctx, key, p);
   }
   launch_allowed<ALLOWED>(la, lb, ep, ws, M, N, K, groups, p, st);
+  return check_launch(name);
+}
+
+// ---------------------------------------------------------- pairs -------
+
+struct GemmDims {
+  int M, N, K, groups;
+};
+
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA1, class LB1, class EP1, class LA2, class LB2,
+          class EP2>
+inline void launch_pair_cfg(const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1, const GemmPlan& p1,
+                            const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const GemmPlan& p2,
+                            float* ws, hipStream_t st) {
+  const int gx1 = int(ceil_div(q1.M, BM)), gy1 = int(ceil_div(q1.N, BN));
+  const int gx2 = int(ceil_div(q2.M, BM)), gy2 = int(ceil_div(q2.N, BN));
+  const long part1 = p1.splits > 1 ? (long(p1.splits) * q1.groups * q1.M * q1.N + 63) / 64 * 64 : 0;
+  const PairDims d1{q1.M, q1.N, q1.K, p1.kchunk, p1.splits, gx1, gy1, gx1 * gy1 * q1.groups * p1.splits, 0};
+  const PairDims d2{q2.M, q2.N, q2.K, p2.kchunk, p2.splits, gx2, gy2, gx2 * gy2 * q2.groups * p2.splits, part1};
+  hipLaunchKernelGGL((k_gemm_pair<BM, BN, WGM, WGN, WGK, TBK, LA1, LB1, EP1, LA2, LB2, EP2>),
+                     dim3(unsigned(d1.blocks + d2.blocks)), dim3(64 * WGM * WGN * WGK), 0, st, la1, lb1, ep1, la2, lb2,
+                     ep2, ws, d1, d2);
+  auto reduce = [&](const auto& ep, const GemmDims& q, const GemmPlan& p, float* w) {
+    if (p.splits <= 1) return;
+    unsigned blocks = unsigned(long(q.M) * q.N / 256 + 1);
+    if (blocks > 2048) blocks = 2048;
+    FDiv dn;
+    dn.set(q.N);
+    using E = std::decay_t<decltype(ep)>;
+    hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(blocks, unsigned(q.groups)), dim3(256), 0, st, w, ep, q.M, q.N,
+                       p.splits, dn);
+  };
+  reduce(ep1, q1, p1, ws);
+  reduce(ep2, q2, p2, ws + part1);
+}
+
+template <unsigned ALLOWED, class LA1, class LB1, class EP1, class LA2, class LB2, class EP2>
+inline void launch_pair(const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1, const GemmPlan& p1,
+                        const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const GemmPlan& p2,
+                        float* ws, hipStream_t st) {
+  dispatch_cfg<ALLOWED>(p1.cfg, [&](auto c) {
+    using C = decltype(c);
+    launch_pair_cfg<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws,
+                                                                  st);
+  });
+}
+
+// Two independent GEMMs in one launch of one tile shape (k_gemm_pair),
+// planned together: the first eager call of a signature times, for each
+// allowed tile shape, the cost model's split of each problem, and keeps the
+// fastest pair for the context (as run_gemm does for one GEMM).  The two
+// problems' split-K partials share the workspace below `ws_reserved`.
+template <unsigned ALLOWED, class LA1, class LB1, class EP1, class LA2, class LB2, class EP2>
+inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1,
+                         const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const char* name,
+                         long ws_reserved = 0) {
+  static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
+  for (const GemmDims* q : {&q1, &q2}) {
+    if (q->M <= 0 || q->N <= 0 || q->groups <= 0 || q->groups > kMaxGroups || long(q->groups) * q->M * q->N >= (1L << 31))
+      return set_error(TTRL_EINVAL, "%s: bad extents", name);
+  }
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  const long half = (wsf - ws_reserved) / 2 / 64 * 64;
+  hipStream_t st = stream_of(ctx);
+  char keybuf[160];
+  snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%d|%d|%d|%d|%ld", q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K,
+           q2.groups, half);
+  const std::string key = std::string(__PRETTY_FUNCTION__) + keybuf;
+  GemmPlan p1, p2;
+  if (gemm_forced(ALLOWED, q1.M, q1.N, q1.K, q1.groups, half, &p1) &&
+      gemm_forced(ALLOWED, q2.M, q2.N, q2.K, q2.groups, half, &p2)) {
+    launch_pair<ALLOWED>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws, st);
+    return check_launch(name);
+  }
+  const std::string key2 = key + "#2";
+  const GemmPlan* h1 = ctx_plan_find(ctx, key);
+  const GemmPlan* h2 = ctx_plan_find(ctx, key2);
+  if (h1 && h2) {
+    p1 = *h1;
+    p2 = *h2;
+  } else {
+    std::vector<std::pair<GemmPlan, GemmPlan>> cands;
+    for (int c = 0; c < kNumCfg; ++c)
+      if (ALLOWED & cfg_bit(c))
+        cands.emplace_back(plan_gemm(q1.M, q1.N, q1.K, q1.groups, half, cfg_bit(c)),
+                           plan_gemm(q2.M, q2.N, q2.K, q2.groups, half, cfg_bit(c)));
+    p1 = cands.front().first;
+    p2 = cands.front().second;
+    hipEvent_t e0, e1;
+    const long span1 = ep1.tune_span();
+    float* sink = nullptr;
+    if (!ctx_capturing(ctx) && gemm_tuning_enabled() && cands.size() > 1 &&
+        (sink = ctx_tune_sink(ctx, size_t(span1 + ep2.tune_span()) * sizeof(float))) != nullptr &&
+        ctx_tune_events(ctx, &e0, &e1)) {
+      const EP1 t1 = ep1.tune_copy(sink);
+      const EP2 t2 = ep2.tune_copy(sink + span1);
+      float best_ms = 1e30f;
+      for (const auto& c : cands) {
+        launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st);  // warm
+        if (hipEventRecord(e0, st) != hipSuccess) break;
+        for (int r = 0; r < 3; ++r) launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st);
+        if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) break;
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) break;
+        if (gemm_tuning_log())
+          fprintf(stderr, "[ttrl gemm tune pair] %dx%dx%d(G%d) + %dx%dx%d(G%d)  %dx%d tbk%d splits=%d,%d  %.2f us\n",
+                  q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K, q2.groups, c.first.bm, c.first.bn, c.first.tbk,
+                  c.first.splits, c.second.splits, ms * 1e3f / 3.f);
+        if (ms < best_ms) {
+          best_ms = ms;
+          p1 = c.first;
+          p2 = c.second;
+        }
+      }
+      (void)hipGetLastError();
+    }
+    ctx_plan_store(ctx, key, p1);
+    ctx_plan_store(ctx, key2, p2);
+  }
+  launch_pair<ALLOWED>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws, st);
   return check_launch(name);
 }
 

@@ -104,6 +104,7 @@ SIGNATURES = {
                                    C.POINTER(P), F, I], I),
     "ttrl_conv2d_backward_weight": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, F], I),
     "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, P, F, F], I),
+    "ttrl_conv2d_backward": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, P, F, P, P, F], I),
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
     "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),

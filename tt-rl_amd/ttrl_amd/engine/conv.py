@@ -273,6 +273,15 @@ class Conv2d(Module):
                 )
             mask = y.vp if relu and not out._grad_masked else None
             (dw, db), beta_w = grad_targets(weight, bias)
+            if dw is not None and x.requires_grad:
+                # both gradients in one call: the two GEMMs share a launch
+                (dx,), beta_x = grad_targets(x)
+                xmask = relu_mask(x)
+                dev.call("ttrl_conv2d_backward", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp, mask, w_data.vp,
+                         dw.vp, None if db is None else db.vp, C.c_float(beta_w), dx.vp,
+                         None if xmask is None else xmask.vp, C.c_float(beta_x))
+                x._note_write(beta_x, xmask is not None)
+                return
             if dw is not None:
                 dev.call("ttrl_conv2d_backward_weight", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp, mask,
                          dw.vp, None if db is None else db.vp, C.c_float(beta_w))
