@@ -14,7 +14,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-N_CFG = 12
+N_CFG = 15
 CASES = [(c, s) for c in range(N_CFG) for s in (0, 3)]
 
 

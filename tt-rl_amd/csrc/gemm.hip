@@ -130,12 +130,14 @@ namespace {
 constexpr unsigned kMatmulCfgs = cfg_bit(T32x32) | cfg_bit(T64x64) | cfg_bit(T128x64) | cfg_bit(T32x32K4);
 constexpr unsigned kSmallK = cfg_bit(T32x32K2) | cfg_bit(T32x32K4) | cfg_bit(T64x32K2) | cfg_bit(T32x64K2);
 constexpr unsigned kLinFwdCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) | kSmallK;
+constexpr unsigned kShallow = cfg_bit(T32x32S) | cfg_bit(T64x64S) | cfg_bit(T128x64S);
 constexpr unsigned kLinDwCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
-                                cfg_bit(T128x64) | kSmallK | cfg_bit(T64x64K2);
-constexpr unsigned kLinDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) | kSmallK;
+                                cfg_bit(T128x64) | kSmallK | cfg_bit(T64x64K2) | kShallow;
+constexpr unsigned kLinDxCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) | kSmallK |
+                                cfg_bit(T32x32S);
 // A layer's dW and dx in one launch (k_gemm_pair): one tile shape for both.
 constexpr unsigned kLinPairCfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T32x32K2) |
-                                  cfg_bit(T64x32K2);
+                                  cfg_bit(T64x32K2) | cfg_bit(T32x32S) | cfg_bit(T64x64S);
 
 __global__ __launch_bounds__(256) void k_relu_mask(float* dst, const float* src, const float* mask, long n, long gs,
                                                    int groups) {

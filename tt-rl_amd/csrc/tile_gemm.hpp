@@ -919,9 +919,12 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
 
 // Tile shapes: BM x BN output tile, TBK reduction slice per LDS stage.
 // K2 / K4: the same tile with 2 or 4 wavefront groups along k (8 or 16 wavefronts).
+// S: a 32-deep stage for small K (the batch dimension of a weight gradient):
+// a deeper stage would fetch and store zeros past K.
 enum TileCfg {
   T32x32 = 0, T64x32 = 1, T32x64 = 2, T64x64 = 3, T128x32 = 4, T128x64 = 5, T64x128 = 6,
-  T32x32K2 = 7, T32x32K4 = 8, T64x32K2 = 9, T32x64K2 = 10, T64x64K2 = 11, kNumCfg = 12
+  T32x32K2 = 7, T32x32K4 = 8, T64x32K2 = 9, T32x64K2 = 10, T64x64K2 = 11,
+  T32x32S = 12, T64x64S = 13, T128x64S = 14, kNumCfg = 15
 };
 
 struct TileDims {
@@ -941,6 +944,9 @@ inline TileDims tile_dims(int cfg) {
     case T32x32K4: return {32, 32, 256, 2, 2, 4};
     case T64x32K2: return {64, 32, 128, 2, 2, 2};
     case T32x64K2: return {32, 64, 128, 2, 2, 2};
+    case T32x32S: return {32, 32, 32, 2, 2, 1};
+    case T64x64S: return {64, 64, 32, 2, 2, 1};
+    case T128x64S: return {128, 64, 32, 2, 2, 1};
     default: return {64, 64, 128, 2, 2, 2};
   }
 }
@@ -1021,6 +1027,9 @@ inline void dispatch_cfg(int cfg, F&& f) {
     TTRL_CFG(T64x32K2, 64, 32, 2, 2, 2, 128)
     TTRL_CFG(T32x64K2, 32, 64, 2, 2, 2, 128)
     TTRL_CFG(T64x64K2, 64, 64, 2, 2, 2, 128)
+    TTRL_CFG(T32x32S, 32, 32, 2, 2, 1, 32)
+    TTRL_CFG(T64x64S, 64, 64, 2, 2, 1, 32)
+    TTRL_CFG(T128x64S, 128, 64, 2, 2, 1, 32)
     default: break;
   }
 #undef TTRL_CFG
