@@ -212,6 +212,17 @@ int ttrl_dqn_loss(ttrl_ctx* ctx, int B, int A, const float* q, const float* q_ne
                   const float* q_next_value, const float* actions_onehot, const float* rewards, const float* dones,
                   const float* discounts, const float* is_weights, float delta, float* loss, float* mean_q,
                   float* td_abs, float* dq, float* next_actions, float* td_target);
+/* The Q head's last linear layer (ttrl/nets/heads.py QHead: q = h @ W + b,
+ * ttrl/engine/layers.py:22-61) for `groups` feature sets in one launch,
+ * followed by ttrl_dqn_loss on the results: group 0 = online(s) gives q,
+ * group 1 selects a*, group groups-1 values it (3 groups: double DQN with
+ * online(s'), target(s'); 2 groups: vanilla, the target both selects and
+ * values).  h[g] is [B][K], W[g] is [K][A] (in, out), bias[g] may be NULL or
+ * bias itself NULL; q_out[g] receives [B][A].  A <= 32. */
+int ttrl_dqn_head(ttrl_ctx* ctx, int B, int K, int A, int groups, const float* const* h, const float* const* W,
+                  const float* const* bias, float* const* q_out, const float* actions_onehot, const float* rewards,
+                  const float* dones, const float* discounts, const float* is_weights, float delta, float* loss,
+                  float* mean_q, float* td_abs, float* dq, float* next_actions, float* td_target);
 
 /* SquashedGaussian.sample (ttrl/algos/sac/policy.py:30-40) over head rows
  * [mean | log_std] ([B][2d], log_std already clamped): action =

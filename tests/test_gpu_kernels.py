@@ -202,3 +202,61 @@ def test_dqn_loss_head_matches_oracle(device):
     dq[np.arange(B), actions] = w / B * np.clip(e, -1, 1)
     assert np.max(np.abs(outs["dq"].numpy() - dq)) < 1e-7
     assert _rel(outs["td"].numpy(), np.abs(e)) < 1e-6
+
+
+@pytest.mark.parametrize("groups,B,K,A", [(3, 32, 512, 6), (2, 32, 512, 6), (3, 7, 100, 18), (3, 130, 64, 4),
+                                           (3, 32, 512, 12)])
+def test_dqn_head_fused_matches_linear_then_loss(device, groups, B, K, A):
+    """ttrl_dqn_head (last linear layer x groups + DQN loss, one launch)
+    against float64: q per group, then the loss head on those q (group 1
+    selects, the last group values).  Tolerance: q rel 2e-6 (fp32 dot of
+    K terms), loss / dq / targets through the oracle rel 1e-5; argmax
+    adopted from the device where the top-two gap is under 1e-5."""
+    from oracle.dqn import huber
+    from ttrl_amd import _lib
+    from ttrl_amd.engine.tensor import DeviceArray
+    rng = np.random.default_rng(groups * 1000 + B + K + A)
+    hs = [np.maximum(rng.standard_normal((B, K)), 0).astype(np.float32) for _ in range(groups)]
+    Ws = [(rng.standard_normal((K, A)) / np.sqrt(K)).astype(np.float32) for _ in range(groups)]
+    bs = [(0.1 * rng.standard_normal(A)).astype(np.float32) for _ in range(groups)]
+    actions = rng.integers(0, A, B)
+    onehot = np.eye(A, dtype=np.float32)[actions]
+    r = rng.choice([-1.0, 0.0, 1.0], B, p=[0.1, 0.8, 0.1]).astype(np.float32)
+    d = (rng.random(B) < 0.2).astype(np.float32)
+    disc = np.full(B, 0.99 ** 3, np.float32)
+    w = rng.uniform(0.4, 1.0, B).astype(np.float32)
+    hd = [_dev_arr(device, h) for h in hs]
+    Wd = [_dev_arr(device, W) for W in Ws]
+    bd = [_dev_arr(device, b) for b in bs]
+    qd = [DeviceArray(device, (B, A)) for _ in range(groups)]
+    outs = {k: DeviceArray(device, s) for k, s in
+            (("loss", (1,)), ("mq", (1,)), ("td", (B,)), ("dq", (B, A)), ("na", (B,)), ("y", (B,)))}
+    ins = [_dev_arr(device, v) for v in (onehot, r, d, disc, w)]
+    # Twice: the batch means are finished by the last workgroup through a
+    # device counter that each launch must leave at zero for the next.
+    for rep in range(2):
+        for o in outs.values():
+            o.fill(-7.0)
+        device.call("ttrl_dqn_head", B, K, A, groups, _lib.ptrs(x.ptr for x in hd), _lib.ptrs(x.ptr for x in Wd),
+                    _lib.ptrs(x.ptr for x in bd), _lib.ptrs(x.ptr for x in qd), *[v.vp for v in ins], C.c_float(1.0),
+                    outs["loss"].vp, outs["mq"].vp, outs["td"].vp, outs["dq"].vp, outs["na"].vp, outs["y"].vp)
+    q64 = [h.astype(np.float64) @ W + b for h, W, b in zip(hs, Ws, bs)]
+    for g in range(groups):
+        assert _rel(qd[g].numpy(), q64[g]) < 2e-6
+    sel, val = q64[1], q64[groups - 1]
+    a_star = np.argmax(sel, 1)
+    top2 = np.sort(sel, 1)[:, -2:]
+    close = (top2[:, 1] - top2[:, 0]) < 1e-5
+    a_dev = outs["na"].numpy().astype(int)
+    assert np.array_equal(a_dev[~close], a_star[~close])
+    a_star = np.where(close, a_dev, a_star)
+    y = r + disc * (1 - d) * val[np.arange(B), a_star]
+    pred = q64[0][np.arange(B), actions]
+    e = pred - y
+    ref_loss = np.mean(w * huber(e, 1.0))
+    assert abs(outs["loss"].numpy()[0] - ref_loss) < 1e-5 * max(1.0, abs(ref_loss))
+    assert abs(outs["mq"].numpy()[0] - pred.mean()) < 1e-5 * max(1.0, abs(pred.mean()))
+    assert _rel(outs["y"].numpy(), y) < 1e-5
+    dq = np.zeros((B, A))
+    dq[np.arange(B), actions] = w / B * np.clip(e, -1, 1)
+    assert np.max(np.abs(outs["dq"].numpy() - dq)) < 1e-5 * max(1e-3, np.abs(dq).max())

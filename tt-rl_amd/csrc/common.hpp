@@ -14,6 +14,12 @@ namespace ttrl {
 int set_error(int code, const char* fmt, ...);
 int hip_error(hipError_t e, const char* what);
 hipStream_t stream_of(ttrl_ctx* ctx);
+// Device words zeroed when the context opens, for kernels whose last
+// workgroup finishes a reduction: kSyncCounters counters (each kernel that
+// uses one leaves it at zero), then float partials (kSyncPartials).
+constexpr int kSyncCounters = 64, kSyncPartials = 2 * 1024;
+constexpr int kSyncDqnHead = 0;  // counter of ttrl_dqn_head
+unsigned* ctx_sync_words(ttrl_ctx* ctx);
 // Converts a pending launch error into a status code.
 int check_launch(const char* name);
 

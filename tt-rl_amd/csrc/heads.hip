@@ -33,6 +33,47 @@ __device__ inline float softplus_f(float x) { return relu_f(x) + logf(expf(-fabs
 // the gradient goes to b iff a > b.
 __device__ inline float min_relu(float a, float b) { return a - relu_f(a - b); }
 
+// One sample of the DQN head: Q(s, a) of the taken action, the double-DQN
+// target from the selection row `sb` and the valuation row `vb`, Huber,
+// the per-sample outputs and dL/dQ for row b.  Returns (w * huber, pred).
+struct DqnRow {
+  float h, pred;
+};
+__device__ inline DqnRow dqn_row_v(int b, int A, const float* qb, const float* sb, const float* vb, const float* ob,
+                                   float reward, float done, float discount, float w, bool has_w, float delta,
+                                   float invB, float* td_abs, float* next_act, float* td_target, float* dqb) {
+  float pred = 0.f;
+  for (int a = 0; a < A; ++a) pred += qb[a] * ob[a];
+  int best = 0;
+  float bv = sb[0];
+  for (int a = 1; a < A; ++a)
+    if (sb[a] > bv) {
+      bv = sb[a];
+      best = a;
+    }
+  const float nv = vb[best];
+  const float y = reward + (nv * (1.f - done)) * discount;
+  const float e = pred - y;
+  const float ae = fabsf(e);
+  const float quad = ae - relu_f(ae - delta);
+  const float lin = ae - quad;
+  const float h = (quad * quad) * 0.5f + lin * delta;
+  if (td_abs) td_abs[b] = ae;
+  if (next_act) next_act[b] = float(best);
+  if (td_target) td_target[b] = y;
+  const float clip = fminf(fmaxf(e, -delta), delta);
+  const float gscale = (has_w ? w * invB : invB) * clip;
+  for (int a = 0; a < A; ++a) dqb[a] = ob[a] * gscale;
+  return DqnRow{has_w ? h * w : h, pred};
+}
+__device__ inline DqnRow dqn_row(int b, int A, const float* qb, const float* sb, const float* vb, const float* ob,
+                                 const float* rewards, const float* dones, const float* discounts,
+                                 const float* weights, float delta, float invB, float* td_abs, float* next_act,
+                                 float* td_target, float* dqb) {
+  return dqn_row_v(b, A, qb, sb, vb, ob, rewards[b], dones[b], discounts[b], weights ? weights[b] : 1.f,
+                   weights != nullptr, delta, invB, td_abs, next_act, td_target, dqb);
+}
+
 __global__ __launch_bounds__(kHeadThreads) void k_dqn_loss(
     int B, int A, const float* __restrict__ q, const float* __restrict__ qsel, const float* __restrict__ qval,
     const float* __restrict__ onehot, const float* __restrict__ rewards, const float* __restrict__ dones,
@@ -43,40 +84,188 @@ __global__ __launch_bounds__(kHeadThreads) void k_dqn_loss(
   const float invB = 1.f / float(B);
   float sum_h = 0.f, sum_p = 0.f;
   for (int b = threadIdx.x; b < B; b += kHeadThreads) {
-    const float* qb = q + long(b) * A;
-    const float* ob = onehot + long(b) * A;
-    float pred = 0.f;
-    for (int a = 0; a < A; ++a) pred += qb[a] * ob[a];
-    const float* sb = qsel + long(b) * A;
-    int best = 0;
-    float bv = sb[0];
-    for (int a = 1; a < A; ++a)
-      if (sb[a] > bv) {
-        bv = sb[a];
-        best = a;
-      }
-    const float nv = qval[long(b) * A + best];
-    const float y = rewards[b] + (nv * (1.f - dones[b])) * discounts[b];
-    const float e = pred - y;
-    const float ae = fabsf(e);
-    const float quad = ae - relu_f(ae - delta);
-    const float lin = ae - quad;
-    const float h = (quad * quad) * 0.5f + lin * delta;
-    const float w = weights ? weights[b] : 1.f;
-    sum_h += weights ? h * w : h;
-    sum_p += pred;
-    if (td_abs) td_abs[b] = ae;
-    if (next_act) next_act[b] = float(best);
-    if (td_target) td_target[b] = y;
-    const float clip = fminf(fmaxf(e, -delta), delta);
-    const float gscale = (weights ? w * invB : invB) * clip;
-    for (int a = 0; a < A; ++a) dq[long(b) * A + a] = ob[a] * gscale;
+    const long o = long(b) * A;
+    const DqnRow r = dqn_row(b, A, q + o, qsel + o, qval + o, onehot + o, rewards, dones, discounts, weights, delta,
+                             invB, td_abs, next_act, td_target, dq + o);
+    sum_h += r.h;
+    sum_p += r.pred;
   }
   const float th = block_sum<kHeadThreads>(sum_h, red);
   const float tp = block_sum<kHeadThreads>(sum_p, red);
   if (threadIdx.x == 0) {
     *loss = th * invB;
     if (mean_q) *mean_q = tp * invB;
+  }
+}
+
+// The Q head's last linear layer for the online(s), online(s') and
+// target(s') features (groups 0, 1, 2; two groups for vanilla DQN, where the
+// target both selects and values), then the DQN head above, in one launch.
+// Workgroup j owns samples [j*RB, (j+1)*RB) of every group: per group, W is
+// staged in LDS as [K][AP] rows padded with zeros to AP (8, 16 or 32)
+// actions, so a lane's k-slice reads whole 16-byte chunks with no
+// per-action branch; a wavefront owns one sample row, its lanes split the
+// K-sum, and a butterfly sums the lanes.  Each sample's target, Huber term
+// and dL/dQ need only its own row, so the workgroups never wait on each
+// other; the batch means are summed from per-workgroup partials, in
+// workgroup order, by the workgroup that finishes last (a device-scope
+// counter, reset by that workgroup for the next launch).
+// Range-checked loads: an offset past `bytes` reads zero.  The base and
+// size are wave-uniform; readfirstlane keeps the resource in scalar
+// registers (one in vector registers would loop over the lanes per load).
+__device__ inline __amdgpu_buffer_rsrc_t head_res(const float* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<float*>((uint64_t(hi) << 32) | lo), static_cast<short>(0),
+                                           static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)), 0x00020000);
+}
+__device__ inline float head_ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+constexpr int kDqnHeadThreads = 1024;
+constexpr int kDqnHeadMaxA = 32;
+constexpr int kDqnHeadLds = 128 * 1024;  // dynamic LDS (gfx950: 160 KiB per workgroup)
+constexpr int kDqnHeadMaxBlocks = 1024;
+struct DqnHeadGroups {
+  const float* h[3];
+  const float* W[3];
+  const float* b[3];
+  float* q[3];
+};
+template <int AP>
+__global__ __launch_bounds__(kDqnHeadThreads) void k_dqn_head(
+    int B, int K, int A, int G, int RB, DqnHeadGroups p, const float* __restrict__ onehot,
+    const float* __restrict__ rewards, const float* __restrict__ dones, const float* __restrict__ discounts,
+    const float* __restrict__ weights, float delta, float* __restrict__ loss, float* __restrict__ mean_q,
+    float* __restrict__ td_abs, float* __restrict__ dq, float* __restrict__ next_act, float* __restrict__ td_target,
+    unsigned* __restrict__ counter, float* __restrict__ partials) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* Ws = lds;                     // [G][K][AP]
+  float* qs = lds + long(G) * K * AP;  // [G][RB][A]
+  __shared__ float red[kDqnHeadThreads / 64];
+  __shared__ bool last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b0 = blockIdx.x * RB;
+  const int nrows = min(RB, B - b0);
+  constexpr int KU = 8;  // loads per lane in flight together
+  // Wavefront (g, i) owns sample b0 + i of group g; its first K-slice of h
+  // is in flight while the workgroup stages every group's W.
+  const int g = wave / RB, i = wave - g * RB;
+  const bool owner = g < G && i < nrows;
+  const __amdgpu_buffer_rsrc_t rh =
+      head_res(owner ? p.h[g] + long(b0 + i) * K : p.h[0], owner ? uint32_t(K) * 4u : 0u);
+  float hv[KU];
+#pragma unroll
+  for (int u = 0; u < KU; ++u) hv[u] = head_ld(rh, uint32_t(u * 64 + lane) * 4u);  // zero past K
+  // The batch inputs of the samples this workgroup finishes, also early.
+  const int mine = b0 + int(threadIdx.x);
+  const bool fin = int(threadIdx.x) < nrows;
+  const float r_in = fin ? rewards[mine] : 0.f, d_in = fin ? dones[mine] : 0.f;
+  const float disc_in = fin ? discounts[mine] : 0.f, w_in = (fin && weights) ? weights[mine] : 1.f;
+  // Every group's W at once, staged in chunks of kDqnHeadThreads * SU
+  // words per group with all groups' loads in flight before any store.
+  constexpr int SU = 4;
+  const int per_group = K * AP;
+  for (int t0 = 0; t0 < per_group; t0 += kDqnHeadThreads * SU) {
+    float v[3][SU];
+#pragma unroll
+    for (int gg = 0; gg < 3; ++gg) {
+      const __amdgpu_buffer_rsrc_t rw = head_res(p.W[gg < G ? gg : 0], gg < G ? uint32_t(K) * uint32_t(A) * 4u : 0u);
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int t = t0 + u * kDqnHeadThreads + threadIdx.x;
+        const int k = t / AP, a = t - k * AP;
+        v[gg][u] = head_ld(rw, (a < A && t < per_group) ? (uint32_t(k) * uint32_t(A) + uint32_t(a)) * 4u : 0x40000000u);
+      }
+    }
+#pragma unroll
+    for (int gg = 0; gg < 3; ++gg) {
+      if (gg >= G) break;
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int t = t0 + u * kDqnHeadThreads + threadIdx.x;
+        if (t < per_group) Ws[gg * per_group + t] = v[gg][u];
+      }
+    }
+  }
+  __syncthreads();
+  if (owner) {
+    const float* Wg = Ws + long(g) * K * AP;
+    float acc[AP];
+#pragma unroll
+    for (int a = 0; a < AP; ++a) acc[a] = 0.f;
+    for (int k0 = 0; k0 < K; k0 += 64 * KU) {
+      if (k0 > 0) {
+#pragma unroll
+        for (int u = 0; u < KU; ++u) hv[u] = head_ld(rh, uint32_t(k0 + u * 64 + lane) * 4u);
+      }
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const int k = min(k0 + u * 64 + lane, K - 1);  // a real row of Ws; hv is zero past K
+        const float4* wr = reinterpret_cast<const float4*>(Wg + k * AP);
+#pragma unroll
+        for (int c = 0; c < AP / 4; ++c) {
+          const float4 w4 = wr[c];
+          acc[4 * c + 0] = fmaf(hv[u], w4.x, acc[4 * c + 0]);
+          acc[4 * c + 1] = fmaf(hv[u], w4.y, acc[4 * c + 1]);
+          acc[4 * c + 2] = fmaf(hv[u], w4.z, acc[4 * c + 2]);
+          acc[4 * c + 3] = fmaf(hv[u], w4.w, acc[4 * c + 3]);
+        }
+      }
+    }
+    // Butterfly over the lanes, the AP sums interleaved level by level.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+      for (int a = 0; a < AP; ++a) acc[a] += __shfl_xor(acc[a], off, 64);
+    }
+    if (lane < A) {
+      float v = acc[0];
+#pragma unroll
+      for (int a = 1; a < AP; ++a) v = lane == a ? acc[a] : v;
+      if (p.b[g]) v += p.b[g][lane];
+      qs[(g * RB + i) * A + lane] = v;
+      p.q[g][long(b0 + i) * A + lane] = v;
+    }
+  }
+  __syncthreads();
+  const float invB = 1.f / float(B);
+  float sum_h = 0.f, sum_p = 0.f;
+  if (fin) {
+    const int i = threadIdx.x, b = mine;
+    const long o = long(b) * A;
+    const DqnRow r = dqn_row_v(b, A, qs + i * A, qs + (RB + i) * A, qs + ((G - 1) * RB + i) * A, onehot + o, r_in,
+                               d_in, disc_in, w_in, weights != nullptr, delta, invB, td_abs, next_act, td_target,
+                               dq + o);
+    sum_h = r.h;
+    sum_p = r.pred;
+  }
+  // The workgroup's samples are all in wavefront 0 (nrows <= 16).
+  float th = sum_h, tp = sum_p;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    th += __shfl_xor(th, off, 64);
+    tp += __shfl_xor(tp, off, 64);
+  }
+  if (threadIdx.x == 0) {
+    partials[2 * blockIdx.x] = th;
+    partials[2 * blockIdx.x + 1] = tp;
+    __threadfence();  // the partials are visible device-wide before the count
+    last = atomicAdd(counter, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (last && threadIdx.x == 0) {
+    __threadfence();
+    float sh = 0.f, sp = 0.f;
+    for (unsigned j = 0; j < gridDim.x; ++j) {  // workgroup order: the same sum on every run
+      sh += __hip_atomic_load(&partials[2 * j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sp += __hip_atomic_load(&partials[2 * j + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *loss = sh * invB;
+    if (mean_q) *mean_q = sp * invB;
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -227,6 +416,49 @@ int ttrl_dqn_loss(ttrl_ctx* ctx, int B, int A, const float* q, const float* q_ne
                      q_next_value, actions_onehot, rewards, dones, discounts, is_weights, delta, loss, mean_q, td_abs,
                      dq, next_actions, td_target);
   return check_launch("ttrl_dqn_loss");
+}
+
+int ttrl_dqn_head(ttrl_ctx* ctx, int B, int K, int A, int groups, const float* const* h, const float* const* W,
+                  const float* const* bias, float* const* q_out, const float* actions_onehot, const float* rewards,
+                  const float* dones, const float* discounts, const float* is_weights, float delta, float* loss,
+                  float* mean_q, float* td_abs, float* dq, float* next_actions, float* td_target) {
+  TTRL_REQUIRE(ctx && h && W && q_out && actions_onehot && rewards && dones && discounts && loss && dq,
+               "ttrl_dqn_head: null argument");
+  TTRL_REQUIRE(groups == 2 || groups == 3, "ttrl_dqn_head: 2 (vanilla) or 3 (double) groups, got %d", groups);
+  TTRL_REQUIRE(B > 0 && K > 0 && A > 0, "ttrl_dqn_head: empty extents");
+  TTRL_REQUIRE(A <= kDqnHeadMaxA, "ttrl_dqn_head: at most %d actions", kDqnHeadMaxA);
+  TTRL_REQUIRE(delta > 0.f, "ttrl_dqn_head: huber delta must be > 0");
+  const int ap = A <= 8 ? 8 : (A <= 16 ? 16 : 32);
+  const int rb = (kDqnHeadThreads / 64) / groups;  // sample rows per workgroup: one wavefront per (group, row)
+  const int blocks = (B + rb - 1) / rb;
+  const size_t lds = (size_t(groups) * K * ap + size_t(groups) * rb * A) * sizeof(float);
+  TTRL_REQUIRE(lds <= size_t(kDqnHeadLds), "ttrl_dqn_head: %d groups of K=%d x %d actions exceed the %d-byte LDS",
+               groups, K, A, kDqnHeadLds);
+  TTRL_REQUIRE(blocks <= kDqnHeadMaxBlocks, "ttrl_dqn_head: batch %d needs more than %d workgroups", B,
+               kDqnHeadMaxBlocks);
+  DqnHeadGroups p{};
+  for (int g = 0; g < groups; ++g) {
+    TTRL_REQUIRE(h[g] && W[g] && q_out[g], "ttrl_dqn_head: null pointer in group %d", g);
+    p.h[g] = h[g];
+    p.W[g] = W[g];
+    p.b[g] = bias ? bias[g] : nullptr;
+    p.q[g] = q_out[g];
+  }
+  unsigned* counter = ctx_sync_words(ctx);
+  float* partials = reinterpret_cast<float*>(counter + kSyncCounters);
+  auto launch = [&](auto kernel) -> int {
+    // Above 64 KiB of LDS a kernel needs the larger limit set once.
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kDqnHeadLds);
+    if (attr != hipSuccess && lds > size_t(64 * 1024)) return hip_error(attr, "ttrl_dqn_head: LDS limit");
+    hipLaunchKernelGGL(kernel, dim3(unsigned(blocks)), dim3(kDqnHeadThreads), lds, stream_of(ctx), B, K, A, groups,
+                       rb, p, actions_onehot, rewards, dones, discounts, is_weights, delta, loss, mean_q, td_abs, dq,
+                       next_actions, td_target, counter + kSyncDqnHead, partials);
+    return check_launch("ttrl_dqn_head");
+  };
+  if (ap == 8) return launch(k_dqn_head<8>);
+  if (ap == 16) return launch(k_dqn_head<16>);
+  return launch(k_dqn_head<32>);
 }
 
 int ttrl_sac_sample(ttrl_ctx* ctx, int B, int d, const float* head, const float* noise, const float* centre,

@@ -55,6 +55,7 @@ struct ttrl_ctx {
   hipEvent_t t0 = nullptr, t1 = nullptr;
   float* ws = nullptr;  // stream-ordered scratch of split-K GEMMs and reductions
   long ws_floats = 0;
+  unsigned* sync = nullptr;  // zeroed counters and partials (ctx_sync_words)
   // GEMM plans chosen by timing candidates on this device, by call signature.
   std::unordered_map<std::string, ttrl::GemmPlan> plans;
   float* tune_out = nullptr;  // output sink of candidate runs
@@ -85,6 +86,8 @@ int hip_error(hipError_t e, const char* what) {
 }
 
 hipStream_t stream_of(ttrl_ctx* ctx) { return ctx->stream; }
+
+unsigned* ctx_sync_words(ttrl_ctx* ctx) { return ctx->sync; }
 
 float* ctx_workspace(ttrl_ctx* ctx, long* floats) {
   if (floats) *floats = ctx->ws_floats;
@@ -208,6 +211,18 @@ int ttrl_init(int device, ttrl_ctx** out) {
   }
   ctx->ws = static_cast<float*>(ws);
   ctx->ws_floats = long(kWorkspaceBytes / sizeof(float));
+  const size_t sync_bytes = sizeof(unsigned) * (kSyncCounters + kSyncPartials);
+  void* sync = nullptr;
+  e = hipMalloc(&sync, sync_bytes);
+  if (e == hipSuccess) e = hipMemset(sync, 0, sync_bytes);
+  if (e != hipSuccess) {
+    if (sync) (void)hipFree(sync);
+    (void)hipFree(ws);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_error(e, "hipMalloc (sync words)");
+  }
+  ctx->sync = static_cast<unsigned*>(sync);
   ctx->pools.emplace_back();  // pool 0: the default pool
   ctx->pools[0].in_use = true;
   *out = ctx;
@@ -220,6 +235,7 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   for (auto& p : ctx->pools) pool_free_slabs(p);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->sync) (void)hipFree(ctx->sync);
   if (ctx->tune_out) (void)hipFree(ctx->tune_out);
   if (ctx->tune0) (void)hipEventDestroy(ctx->tune0);
   if (ctx->tune1) (void)hipEventDestroy(ctx->tune1);

@@ -1044,6 +1044,24 @@ inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, 
   });
 }
 
+// Best of three rounds of three back-to-back runs of `run` (milliseconds
+// for three runs), -1 if an event call fails.  The minimum over rounds
+// discards rounds slowed by clock ramps or other work on the device.
+template <class F>
+inline float time_best_of(hipEvent_t e0, hipEvent_t e1, hipStream_t st, F&& run) {
+  float best = -1.f;
+  for (int round = 0; round < 3; ++round) {
+    if (hipEventRecord(e0, st) != hipSuccess) return -1.f;
+    for (int r = 0; r < 3; ++r) run();
+    float ms = 0.f;
+    if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+      return -1.f;
+    if (best < 0.f || ms < best) best = ms;
+  }
+  return best;
+}
+
 // Times the model's leading candidates on the real operands, writing into a
 // sink instead of the output; returns the fastest (the model's first choice
 // if timing is unavailable).
@@ -1059,11 +1077,8 @@ inline GemmPlan tune_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& e
   float best_ms = 1e30f;
   for (const GemmPlan& c : cands) {
     launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);  // warm
-    if (hipEventRecord(e0, st) != hipSuccess) break;
-    for (int r = 0; r < 3; ++r) launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);
-    if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) break;
-    float ms = 0.f;
-    if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) break;
+    const float ms = time_best_of(e0, e1, st, [&] { launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st); });
+    if (ms < 0.f) break;
     if (gemm_tuning_log())
       fprintf(stderr, "[ttrl gemm tune] M=%d N=%d K=%d G=%d  %dx%d tbk%d splits=%d  %.2f us\n", M, N, K, groups, c.bm,
               c.bn, c.tbk, c.splits, ms * 1e3f / 3.f);
@@ -1213,11 +1228,9 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
       float best_ms = 1e30f;
       for (const auto& c : cands) {
         launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st);  // warm
-        if (hipEventRecord(e0, st) != hipSuccess) break;
-        for (int r = 0; r < 3; ++r) launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st);
-        if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) break;
-        float ms = 0.f;
-        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) break;
+        const float ms = time_best_of(
+            e0, e1, st, [&] { launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st); });
+        if (ms < 0.f) break;
         if (gemm_tuning_log())
           fprintf(stderr, "[ttrl gemm tune pair] %dx%dx%d(G%d) + %dx%dx%d(G%d)  %dx%d tbk%d splits=%d,%d  %.2f us\n",
                   q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K, q2.groups, c.first.bm, c.first.bn, c.first.tbk,

@@ -106,6 +106,7 @@ SIGNATURES = {
     "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, P, F, F], I),
     "ttrl_conv2d_backward": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, P, F, P, P, F], I),
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
+    "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
     "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),
     "ttrl_sac_critic_loss": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),

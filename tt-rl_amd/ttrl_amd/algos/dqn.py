@@ -27,7 +27,7 @@ from ttrl_amd.engine.autograd import Tensor, no_grad
 from ttrl_amd.engine.conv import Conv2d
 from ttrl_amd.engine import layers as layers_mod
 from ttrl_amd.engine.layers import Linear, ReLU
-from ttrl_amd.engine.ops.fused import dqn_td_loss, linear_node
+from ttrl_amd.engine.ops.fused import dqn_head_td_loss, dqn_td_loss, linear_node
 from ttrl_amd.engine.optim import Adam
 from ttrl_amd.engine.step import TrainStep
 from ttrl_amd.engine.tensor import DeviceArray, bound_block
@@ -108,13 +108,15 @@ def _lockstep_layers(nets):
     return stacks
 
 
-def q_forward_multi(nets, inputs, tape_group: int | None = 0):
+def q_forward_multi(nets, inputs, tape_group: int | None = 0, *, skip_last: bool = False):
     """Q values of several same-shaped Q networks, one launch per layer.
 
     `nets[g]` is applied to `inputs[g]`; the evaluations share each layer's
     launch (per-group weight and activation pointers).  Only group
     `tape_group` records a tape (the online network on s); every other group
-    is a constant of the step, as under no_grad in the reference.
+    is a constant of the step, as under no_grad in the reference.  With
+    `skip_last` the Q head's last layer is not applied: the features it
+    would consume are returned.
     """
     stacks = _lockstep_layers(nets)
     if stacks is None:
@@ -124,7 +126,7 @@ def q_forward_multi(nets, inputs, tape_group: int | None = 0):
         raise ValueError("q_forward_multi: at most 4 networks per launch")
     xs = list(inputs)
     dev = xs[0].device
-    layers0 = stacks[0]
+    layers0 = stacks[0][:-1] if skip_last else stacks[0]
     i = 0
     while i < len(layers0):
         layer = layers0[i]
@@ -173,11 +175,24 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
     (leaf,) = tuple(leaves)
     obs = inputs[leaf_key("obs", leaf)]
     next_obs = inputs[leaf_key("next_obs", leaf)]
-    if _lockstep_layers([online, target]) is not None:
+    stacks = _lockstep_layers([online, target])
+    nets = [online, online, target] if double else [online, target]
+    feeds = [obs, next_obs, next_obs] if double else [obs, next_obs]
+    if stacks is not None and _fused_head_fits(stacks[0], obs, len(nets)):
+        # The Q head's last layer and the loss in one launch.
+        features = q_forward_multi(nets, feeds, skip_last=True)
+        heads = [_lockstep_layers([n])[0][-1] for n in nets]
+        loss, extra, qs = dqn_head_td_loss(features, heads, inputs["actions_onehot"], inputs["rewards"],
+                                           inputs["dones"], inputs["discounts"],
+                                           inputs["is_weights"] if prioritized else None, huber_delta)
+        if layers_mod.RECORD is not None:
+            layers_mod.RECORD.append(list(qs))
+        return _finish_update(online, loss, extra, prioritized, grad_sq)
+    if stacks is not None:
         if double:
-            q, selector, next_target_q = q_forward_multi([online, online, target], [obs, next_obs, next_obs])
+            q, selector, next_target_q = q_forward_multi(nets, feeds)
         else:
-            q, next_target_q = q_forward_multi([online, target], [obs, next_obs])
+            q, next_target_q = q_forward_multi(nets, feeds)
             selector = next_target_q
     else:
         q = online(obs)
@@ -187,6 +202,23 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
     loss, extra = dqn_td_loss(q, selector, next_target_q, inputs["actions_onehot"], inputs["rewards"],
                               inputs["dones"], inputs["discounts"],
                               inputs["is_weights"] if prioritized else None, huber_delta)
+    return _finish_update(online, loss, extra, prioritized, grad_sq)
+
+
+def _fused_head_fits(layers, obs, groups: int) -> bool:
+    """The fused Q head (ttrl_dqn_head) applies to a last Linear layer with
+    at most 32 actions whose weights for every group, padded to 8/16/32
+    actions, fit a workgroup's 128 KiB of LDS."""
+    head = layers[-1]
+    A = head.out_features if isinstance(head, Linear) else 0
+    if not 0 < A <= 32:
+        return False
+    ap = 8 if A <= 8 else (16 if A <= 16 else 32)
+    rows = 16 // groups
+    return groups * (head.in_features * ap + rows * A) * 4 <= 128 * 1024
+
+
+def _finish_update(online, loss, extra, prioritized: bool, grad_sq: bool) -> dict:
     loss.backward()
     metrics = {"loss": loss, "mean_q": extra["mean_q"]}
     if prioritized:

@@ -47,6 +47,10 @@ class no_grad:
 
 
 #: Ops whose output is a ReLU output (their backward applies relu_bw).
+# Fused loss nodes whose backward, given a gradient marked `unit`, reads only
+# the mark (dQ etc. are already scaled for a unit seed); backward() seeds
+# them without filling the seed buffer.
+UNIT_SEED_OPS = frozenset({"dqn_td_loss", "sac_critic_loss", "sac_actor_loss", "sac_alpha_loss", "ppo_objective"})
 RELU_OPS = frozenset({"linear_relu", "conv2d_relu"})
 
 
@@ -213,7 +217,10 @@ class Tensor:
                 "non-scalar backward pass, so reduce to a scalar first."
             )
         seed = DeviceArray(self.device, self.shape)
-        seed.fill(1.0)
+        if self._op in UNIT_SEED_OPS:
+            seed.unit = True  # the root's backward reads only the flag: no fill launch
+        else:
+            seed.fill(1.0)
         self.grad = seed
         self._grad_owned = True
         try:

@@ -135,16 +135,21 @@ def dqn_td_loss(q: Tensor, q_next_select: Tensor, q_next_value: Tensor, actions_
     if not delta > 0.0:
         raise ValueError(f"dqn_td_loss: huber delta must be > 0, got {delta}")
     dev = q.device
-    loss = DeviceArray(dev, (1, 1))
-    mean_q = DeviceArray(dev, (1, 1))
-    td_abs = DeviceArray(dev, (B, 1))
-    td_target = DeviceArray(dev, (B, 1))
-    next_act = DeviceArray(dev, (B, 1))
-    dq = DeviceArray(dev, (B, A))
+    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A)
     dev.call("ttrl_dqn_loss", B, A, q.data.vp, q_next_select.data.vp, q_next_value.data.vp,
              actions_onehot.data.vp, rewards.data.vp, dones.data.vp, discounts.data.vp,
              None if is_weights is None else is_weights.data.vp, C.c_float(delta), loss.vp, mean_q.vp,
              td_abs.vp, dq.vp, next_act.vp, td_target.vp)
+    return _dqn_loss_node(q, loss, mean_q, td_abs, td_target, next_act, dq)
+
+
+def _dqn_outputs(dev, B: int, A: int):
+    return (DeviceArray(dev, (1, 1)), DeviceArray(dev, (1, 1)), DeviceArray(dev, (B, 1)), DeviceArray(dev, (B, 1)),
+            DeviceArray(dev, (B, 1)), DeviceArray(dev, (B, A)))
+
+
+def _dqn_loss_node(q: Tensor, loss, mean_q, td_abs, td_target, next_act, dq):
+    """The loss tape node over q, its dL/dq already computed for a unit seed."""
     metrics = {
         "mean_q": Tensor(mean_q), "td_abs": Tensor(td_abs), "td_target": Tensor(td_target),
         "next_actions": Tensor(next_act),
@@ -164,3 +169,41 @@ def dqn_td_loss(q: Tensor, q_next_select: Tensor, q_next_value: Tensor, actions_
 
     out._backward = _backward
     return out, metrics
+
+
+def dqn_head_td_loss(features, heads, actions_onehot: Tensor, rewards: Tensor, dones: Tensor, discounts: Tensor,
+                     is_weights: Tensor | None, delta: float):
+    """The Q head's last linear layer over 2 or 3 feature sets and the DQN
+    loss in one launch (ttrl_dqn_head): features[0] = online(s) (taped),
+    features[1] = online(s') selecting a* (double) or target(s'),
+    features[-1] = target(s') valuing it; heads[g] the matching Linear.
+    -> (loss, metrics, q_arrays) with the same loss node and metrics as
+    dqn_td_loss on the three Q tensors; q of group 0 is a linear tape node,
+    so the backward is the layer's usual weight / input gradient."""
+    G = len(features)
+    if G not in (2, 3) or len(heads) != G:
+        raise ValueError(f"dqn_head_td_loss: 2 or 3 feature sets and heads, got {G} and {len(heads)}")
+    B, K = (int(d) for d in features[0].shape)
+    A = int(heads[0].out_features)
+    for f, h in zip(features, heads):
+        if tuple(f.shape) != (B, K) or int(h.in_features) != K or int(h.out_features) != A:
+            raise ValueError("dqn_head_td_loss: feature sets and heads must share (B, K) and (K, A)")
+    if tuple(actions_onehot.shape) != (B, A):
+        raise ValueError(f"dqn_head_td_loss: actions_onehot has shape {actions_onehot.shape}, expected {(B, A)}")
+    for name, t in (("rewards", rewards), ("dones", dones), ("discounts", discounts), ("is_weights", is_weights)):
+        if t is not None and t.data.numel != B:
+            raise ValueError(f"dqn_head_td_loss: {name} has {t.data.numel} elements, expected {B}")
+    if not delta > 0.0:
+        raise ValueError(f"dqn_head_td_loss: huber delta must be > 0, got {delta}")
+    dev = features[0].device
+    weights = [h.effective_weight() for h in heads]
+    qs = [DeviceArray(dev, (B, A)) for _ in range(G)]
+    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A)
+    dev.call("ttrl_dqn_head", B, K, A, G, _lib.ptrs(f.data.ptr for f in features), _lib.ptrs(w.data.ptr for w in weights),
+             _lib.ptrs(None if h.bias is None else h.bias.data.ptr for h in heads), _lib.ptrs(q.ptr for q in qs),
+             actions_onehot.data.vp, rewards.data.vp, dones.data.vp, discounts.data.vp,
+             None if is_weights is None else is_weights.data.vp, C.c_float(delta), loss.vp, mean_q.vp, td_abs.vp,
+             dq.vp, next_act.vp, td_target.vp)
+    q0 = linear_node(features[0], weights[0], heads[0].bias, qs[0], relu=False)
+    out, metrics = _dqn_loss_node(q0, loss, mean_q, td_abs, td_target, next_act, dq)
+    return out, metrics, qs
