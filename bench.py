@@ -34,6 +34,11 @@ for _p in (ROOT, ROOT / "tt-rl_amd"):
 import numpy as np  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12
+# HBM bytes per launch of the dominant kernel (conv1 forward x 3): rocprofv3
+# FETCH_SIZE 1713.5 KiB x 2.000 + WRITE_SIZE 4800.0 KiB x 1.000, the factors
+# being what the same counters read for a 256 MiB device-to-device copy
+# (131083.5 and 262144.0 KiB); profiles/conv1_forward_traffic_counters.md.
+CONV1_FWD_TRAFFIC_BYTES = 8424135
 PEAK_HBM = 8.0e12
 
 # Multiply-accumulates per sample of the Nature CNN at 4x84x84 (conv1..3, fc1, fc2).
@@ -226,6 +231,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
                     help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run five device-to-device copies of MIB MiB (the reference for scaling a "
+                         "profiler's FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path; "
@@ -268,13 +276,22 @@ def main() -> int:
                 "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA},
         "roofline": {"bound": "mfma", "kernel": dom["name"], "achieved": achieved / 1e12,
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
-                     "traffic": None, "algorithmic_bytes": dom["bytes"], "avg_us": dom["seconds"] * 1e6},
+                     "traffic": CONV1_FWD_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],
+                     "avg_us": dom["seconds"] * 1e6},
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    if args.copy_calibration > 0:
+        from ttrl_amd.engine.tensor import DeviceArray
+        n = args.copy_calibration * (1 << 20) // 4
+        src, dst = DeviceArray(dev, (n,)), DeviceArray(dev, (n,))
+        src.fill(1.0)
+        for _ in range(5):
+            dst.copy_from(src)
+        dev.synchronize()
     dqn.close()
     sac.close()
     return 0
