@@ -188,6 +188,62 @@ def pcie_inclusive(dev, learner, n=100):
     return n / (time.perf_counter() - t0)
 
 
+def bench_act(dev, dqn, sac, steps=500, lanes_dqn=(1, 8, 16, 32), lanes_sac=(1, 16, 256)):
+    """Acting steps/s of the learners' acting networks: one step = host
+    observations (pageable numpy) -> device -> captured forward + fused
+    head-and-decision kernel -> actions back on the host (DQN: greedy
+    actions before the host epsilon draw; SAC: squashed-Gaussian actions at
+    host-drawn noise).  At 32 lanes the DQN step is the batch-32 Q-network
+    forward of the deploy path, plus the upload and the action read."""
+    out = {"dqn": [], "sac": []}
+    rng = np.random.default_rng(17)
+    for lanes in lanes_dqn:
+        frames = [rng.integers(0, 256, (lanes, 4, 84, 84), dtype=np.uint8) for _ in range(8)]
+        for i in range(20):
+            dqn._acting.decide(frames[i % 8])
+        t0 = time.perf_counter()
+        for i in range(steps):
+            dqn._acting.decide(frames[i % 8])
+        dt = time.perf_counter() - t0
+        out["dqn"].append({"lanes": lanes, "steps_per_s": round(steps / dt, 1), "us_per_step": round(dt / steps * 1e6, 2)})
+    for lanes in lanes_sac:
+        obs = [rng.standard_normal((lanes, 11)).astype(np.float32) for _ in range(8)]
+        noise = [rng.standard_normal((lanes, 3)).astype(np.float32) for _ in range(8)]
+        for i in range(20):
+            sac._acting.decide(obs[i % 8], noise=noise[i % 8])
+        t0 = time.perf_counter()
+        for i in range(steps):
+            sac._acting.decide(obs[i % 8], noise=noise[i % 8])
+        dt = time.perf_counter() - t0
+        out["sac"].append({"lanes": lanes, "steps_per_s": round(steps / dt, 1), "us_per_step": round(dt / steps * 1e6, 2)})
+    return out
+
+
+def cpu_deploy_forward(seconds: float):
+    """The oracle's restatement of the numpy deploy forward (batch 32,
+    4x84x84 uint8 frames scaled by 1/255), forwards/s on this host."""
+    from oracle.nets import QNet, qnet_forward
+
+    rng = np.random.default_rng(1)
+
+    def he(shape, fan):
+        b = np.sqrt(6.0 / fan)
+        return rng.uniform(-b, b, shape)
+
+    net = QNet([(he((32, 4, 8, 8), 256), he((32,), 256), 4, 0), (he((64, 32, 4, 4), 512), he((64,), 512), 2, 0),
+                (he((64, 64, 3, 3), 576), he((64,), 576), 1, 0)],
+               [(he((3136, 512), 3136), he((512,), 3136)), (he((512, 6), 512), he((6,), 512))])
+    frames = rng.integers(0, 256, (32, 4, 84, 84), dtype=np.uint8)
+    qnet_forward(net, frames)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n < 2:
+        qnet_forward(net, frames)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 2), "unit": "DQN forwards/s (batch 32)", "kind": "port",
+            "sample": f"{n} float64 forwards in {dt:.1f} s"}
+
+
 def cpu_baseline(seconds: float):
     """The float64 numpy oracle of the same DQN update, on this host."""
     from oracle.dqn import dqn_update
@@ -229,6 +285,7 @@ def main() -> int:
     ap.add_argument("--ring", type=int, default=32, help="distinct resident batches cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--act-steps", type=int, default=500, help="acting steps timed per lane count (0: skip)")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
                     help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -252,7 +309,10 @@ def main() -> int:
     dom = dominant_kernel(dev, dqn)
     achieved = dom["flops"] / dom["seconds"]
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
+    act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    if act is not None and not args.no_cpu_baseline:
+        act["cpu_deploy_forward"] = cpu_deploy_forward(min(5.0, args.cpu_seconds))
     line = {
         "metric": "DQN updates/s @bs32, SAC updates/s @bs256 on 1 MI355X; % of roofline",
         "value": round(value, 2),
@@ -281,6 +341,7 @@ def main() -> int:
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},
+        "act": act,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -80,6 +80,15 @@ int ttrl_capture_end(ttrl_ctx* ctx, ttrl_graph** out);
 int ttrl_capture_abort(ttrl_ctx* ctx);
 int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g);
 int ttrl_graph_launch_n(ttrl_ctx* ctx, ttrl_graph* g, int n);
+/* One acting step as one host call: copy in_bytes of host memory into the
+ * bound device block in_dev, replay g (skipped when NULL), copy out_bytes of
+ * out_dev back to host memory, and wait.  Both copies go through one pinned
+ * staging buffer the context owns and grows on demand.  Replaces the acting
+ * round trip of ttrl/nets/acting.py:164-169 (ObsViews.load, the eager
+ * forward) and the action read of ttrl/algos/dqn/agent.py:107-109 and
+ * ttrl/algos/sac/agent.py:118-121. */
+int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_host, size_t in_bytes,
+                    void* out_host, const void* out_dev, size_t out_bytes);
 int ttrl_graph_nodes(ttrl_graph* g, size_t* out);
 int ttrl_graph_destroy(ttrl_graph* g);
 
@@ -326,6 +335,28 @@ int ttrl_copy_strided(ttrl_ctx* ctx, const float* a, float* y, int ndim, const l
 int ttrl_reduce(ttrl_ctx* ctx, int op, const float* a, float* y, long outer, long dim, long inner);
 /* y[b][c] = (c - indices[b] == 0) (ttrl/engine/ops/functional.py:112-123). */
 int ttrl_one_hot(ttrl_ctx* ctx, const float* indices, float* y, long batch, int num_classes);
+
+/* ---- acting step -------------------------------------------------------- */
+
+/* Greedy action of a Q network's last linear layer, fused: q = h W + bias
+ * ([B][K] x [K][A], W in the (in, out) layout of ttrl/engine/layers.py:43-47;
+ * bias may be NULL, q_out may be NULL) and actions[b] = the first index of
+ * the row maximum, as int32.  Replaces the acting forward's QHead matmul and
+ * argmax_dim_detached (ttrl/algos/dqn/agent.py:107-109,
+ * ttrl/engine/ops/reduce.py:82-99).  A <= 32. */
+int ttrl_q_act(ttrl_ctx* ctx, int B, int K, int A, const float* h, const float* W, const float* bias, float* q_out,
+               int* actions);
+/* Squashed-Gaussian action of a GaussianHead, fused: mean = h W_mean +
+ * b_mean, log_std = clamp(h W_log_std + b_log_std, min, max)
+ * (ttrl/nets/heads.py:65-93); stochastic: u = mean + exp(log_std) * noise,
+ * action = centre + half_width * tanh(u), logp = squashed_logp(u) - log_det;
+ * deterministic: action = centre + half_width * tanh(mean), logp = 0
+ * (ttrl/algos/sac/policy.py:42-59, ttrl/algos/gaussian.py:106-167).
+ * head_out ([B][2d] = [mean | clamped log_std]) may be NULL.  d <= 16. */
+int ttrl_gaussian_act(ttrl_ctx* ctx, int B, int K, int d, const float* h, const float* W_mean, const float* b_mean,
+                      const float* W_log_std, const float* b_log_std, float log_std_min, float log_std_max,
+                      const float* noise, const float* centre, const float* half_width, float log_det,
+                      int deterministic, float* head_out, float* action, float* logp);
 
 #ifdef __cplusplus
 }

@@ -11,8 +11,10 @@
 #include "common.hpp"
 #include "tile_gemm.hpp"
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -61,6 +63,9 @@ struct ttrl_ctx {
   float* tune_out = nullptr;  // output sink of candidate runs
   size_t tune_bytes = 0;
   hipEvent_t tune0 = nullptr, tune1 = nullptr;
+  // Pinned host staging of ttrl_graph_step: inputs first, outputs after.
+  unsigned char* pinned = nullptr;
+  size_t pinned_bytes = 0;
 };
 
 struct ttrl_graph {
@@ -241,6 +246,7 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   if (ctx->tune1) (void)hipEventDestroy(ctx->tune1);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+  if (ctx->pinned) (void)hipHostFree(ctx->pinned);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return TTRL_OK;
@@ -448,6 +454,45 @@ int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g) {
   if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_launch: the stream is capturing");
   hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
   if (e != hipSuccess) return hip_error(e, "hipGraphLaunch");
+  return TTRL_OK;
+}
+
+int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_host, size_t in_bytes,
+                    void* out_host, const void* out_dev, size_t out_bytes) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_graph_step: null ctx");
+  if ((in_bytes && (!in_dev || !in_host)) || (out_bytes && (!out_dev || !out_host)))
+    return set_error(TTRL_EINVAL, "ttrl_graph_step: null buffer with a nonzero size");
+  if (g && !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_step: destroyed graph");
+  if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_step: the stream is capturing");
+  const size_t out_at = (in_bytes + 255) & ~size_t(255);
+  const size_t need = out_at + out_bytes;
+  if (need > ctx->pinned_bytes) {
+    // Grow only: the previous step has been waited for, so nothing reads the old staging.
+    size_t cap = std::max(need, ctx->pinned_bytes * 2);
+    unsigned char* p = nullptr;
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), cap, hipHostMallocDefault);
+    if (e != hipSuccess) return hip_error(e, "hipHostMalloc (graph step staging)");
+    if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+    ctx->pinned = p;
+    ctx->pinned_bytes = cap;
+  }
+  hipError_t e;
+  if (in_bytes) {
+    std::memcpy(ctx->pinned, in_host, in_bytes);
+    e = hipMemcpyAsync(in_dev, ctx->pinned, in_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (graph step)");
+  }
+  if (g) {
+    e = hipGraphLaunch(g->exec, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipGraphLaunch (graph step)");
+  }
+  if (out_bytes) {
+    e = hipMemcpyAsync(ctx->pinned + out_at, out_dev, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync D2H (graph step)");
+  }
+  e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize (graph step)");
+  if (out_bytes) std::memcpy(out_host, ctx->pinned + out_at, out_bytes);
   return TTRL_OK;
 }
 

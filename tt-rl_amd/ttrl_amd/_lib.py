@@ -90,6 +90,7 @@ SIGNATURES = {
     "ttrl_capture_abort": ([P], I),
     "ttrl_graph_launch": ([P, P], I),
     "ttrl_graph_launch_n": ([P, P, I], I),
+    "ttrl_graph_step": ([P, P, P, P, SZ, P, P, SZ], I),
     "ttrl_graph_nodes": ([P, C.POINTER(SZ)], I),
     "ttrl_graph_destroy": ([P], I),
     "ttrl_timer_start": ([P], I),
@@ -108,6 +109,8 @@ SIGNATURES = {
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
+    "ttrl_q_act": ([P, I, I, I, P, P, P, P, P], I),
+    "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),
     "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),
     "ttrl_sac_critic_loss": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),
     "ttrl_sac_actor_loss": ([P, I, P, P, P, F, I, P, P, P, P, P], I),

@@ -31,6 +31,7 @@ from ttrl_amd.engine.ops.fused import dqn_head_td_loss, dqn_td_loss, linear_node
 from ttrl_amd.engine.optim import Adam
 from ttrl_amd.engine.step import TrainStep
 from ttrl_amd.engine.tensor import DeviceArray, bound_block
+from ttrl_amd.nets.acting import ActingNet, GreedyDecision
 from ttrl_amd.nets.build import build_q_net
 
 __all__ = ["DQNConfig", "DQNLearner", "leaf_key", "step_inputs", "update_loss"]
@@ -52,6 +53,11 @@ class DQNConfig:
     prioritized: bool = True
     step_mode: str = "graph"
     encoder: str = "auto"
+    eps_start: float = 1.0
+    eps_end: float = 0.01
+    eps_decay_frames: int = 1_000_000
+    eval_epsilon: float = 0.05
+    act_mode: str = "graph"
 
     def __post_init__(self):
         if self.lr <= 0 or self.adam_eps <= 0:
@@ -62,6 +68,13 @@ class DQNConfig:
             raise ValueError(f"DQNConfig: huber_delta must be > 0, got {self.huber_delta}")
         if self.target_sync_interval < 1:
             raise ValueError("DQNConfig: target_sync_interval must be >= 1")
+        if not 0.0 <= self.eps_end <= self.eps_start <= 1.0:
+            raise ValueError(f"DQNConfig: the epsilon schedule must satisfy 0 <= eps_end <= eps_start <= 1, "
+                             f"got eps_start={self.eps_start}, eps_end={self.eps_end}")
+        if self.eps_decay_frames < 1:
+            raise ValueError(f"DQNConfig: eps_decay_frames must be >= 1, got {self.eps_decay_frames}")
+        if not 0.0 <= self.eval_epsilon <= 1.0:
+            raise ValueError(f"DQNConfig: eval_epsilon must be in [0, 1], got {self.eval_epsilon}")
 
 
 def leaf_key(which: str, leaf: str) -> str:
@@ -231,10 +244,11 @@ def _finish_update(online, loss, extra, prioritized: bool, grad_sq: bool) -> dic
 
 
 class DQNLearner:
-    """Online and target Q networks, Adam, and one captured update."""
+    """Online and target Q networks, Adam, one captured update, and the
+    acting step either side of it (ttrl/algos/dqn/agent.py:89-119)."""
 
     def __init__(self, obs_spec, action_spec, device, *, cfg: DQNConfig = DQNConfig(), seed: int | None = None,
-                 online_state: dict | None = None, target_state: dict | None = None):
+                 online_state: dict | None = None, target_state: dict | None = None, n_envs: int = 1):
         if action_spec.kind != "discrete":
             raise ValueError(f"DQN supports discrete actions only, got {action_spec.kind!r}")
         self.obs_spec = obs_spec
@@ -256,6 +270,37 @@ class DQNLearner:
                                   prioritized=cfg.prioritized)
         self.step = TrainStep(self._step_fn, self.inputs, device, optimizer=self.optimizer, mode=cfg.step_mode)
         self.update_count = 0
+        self.n_envs = int(n_envs)
+        self._acting = ActingNet(self.online, obs_spec, device, width=cfg.batch_size, lanes=self.n_envs,
+                                 decision=GreedyDecision(), mode=cfg.act_mode)
+        self.frame_count = 0
+        self._rng = np.random.default_rng(seed)
+        # A separate stream for evaluation acting, so evaluation does not
+        # perturb the training exploration trajectory.
+        self._eval_rng = np.random.default_rng(seed).spawn(1)[0]
+
+    # -- acting ------------------------------------------------------------
+
+    def epsilon(self) -> float:
+        cfg = self.cfg
+        frac = min(1.0, self.frame_count / cfg.eps_decay_frames)
+        return cfg.eps_start + frac * (cfg.eps_end - cfg.eps_start)
+
+    def act(self, obs, *, deterministic: bool = False, episode_starts=None) -> np.ndarray:
+        """One action per lane: epsilon-greedy over the online network's
+        greedy action, the random draws made on the host in the reference's
+        order (ttrl/algos/dqn/agent.py:97-119).  `episode_starts` is part of
+        the acting contract for a policy with memory; this one has none."""
+        eps = self.cfg.eval_epsilon if deterministic else self.epsilon()
+        rng = self._eval_rng if deterministic else self._rng
+        greedy = self._acting.decide(obs)["actions"]
+        batch = greedy.shape[0]
+        draws = rng.random(batch)
+        random_actions = rng.integers(0, self.num_actions, size=batch)
+        actions = np.where(draws < eps, random_actions, greedy).astype(np.int64)
+        if not deterministic:
+            self.frame_count += batch
+        return actions
 
     def _step_fn(self, inputs: dict) -> dict:
         metrics = update_loss(self.online, self.target, inputs, leaves=(self.obs_spec.name,),
@@ -302,4 +347,7 @@ class DQNLearner:
         return metrics
 
     def close(self) -> None:
-        self.step.close()
+        try:
+            self._acting.close()
+        finally:
+            self.step.close()

@@ -29,6 +29,7 @@ import numpy as np
 
 from ttrl_amd import _lib
 from ttrl_amd.algos.gaussian import ActionScale, squashed_sample
+from ttrl_amd.nets.acting import ActingNet, SquashedDecision
 from ttrl_amd.engine.autograd import Tensor, _needs, no_grad
 from ttrl_amd.engine import layers as layers_mod
 from ttrl_amd.engine.layers import Linear, ReLU
@@ -59,6 +60,7 @@ class SACConfig:
     step_mode: str = "graph"
     critic_hidden: tuple = (256, 256)
     policy_hidden: tuple = (256, 256)
+    act_mode: str = "graph"
 
     def __post_init__(self):
         if self.lr <= 0 or self.adam_eps <= 0:
@@ -328,9 +330,11 @@ class _BatchBuffers:
 
 
 class SACLearner:
-    """Policy, twin critics, targets, log_alpha, three Adams, one update."""
+    """Policy, twin critics, targets, log_alpha, three Adams, one update, and
+    the acting step (ttrl/algos/sac/agent.py:95-125)."""
 
-    def __init__(self, obs_spec, action_spec, device, *, cfg: SACConfig = SACConfig(), seed: int | None = None):
+    def __init__(self, obs_spec, action_spec, device, *, cfg: SACConfig = SACConfig(), seed: int | None = None,
+                 n_envs: int = 1):
         if action_spec.kind != "continuous":
             raise ValueError(f"SAC supports continuous actions only, got {action_spec.kind!r}")
         self.cfg = cfg
@@ -356,6 +360,29 @@ class SACLearner:
         self._graph_metrics = None
         self._pool = None
         self.update_count = 0
+        self.n_envs = int(n_envs)
+        self._acting = ActingNet(self.nets.policy, obs_spec, device, width=cfg.batch_size, lanes=self.n_envs,
+                                 decision=SquashedDecision(self.scale), mode=cfg.act_mode)
+        self.frame_count = 0
+        self._rng = np.random.default_rng(seed)
+        self._eval_rng = np.random.default_rng(seed).spawn(1)[0]
+
+    # -- acting --------------------------------------------------------------
+
+    def act(self, obs, *, deterministic: bool = False, episode_starts=None) -> np.ndarray:
+        """One action per lane from the squashed-Gaussian policy; the noise
+        is drawn on the host from the same stream and in the same shape as
+        the reference's sample (ttrl/algos/sac/agent.py:111-125,
+        ttrl/algos/sac/policy.py:42-59), the sample itself on the device.
+        `deterministic` takes tanh of the mean."""
+        lanes = int(np.asarray(obs).shape[0])
+        noise = None
+        if not deterministic:
+            noise = self._rng.standard_normal((lanes, self.action_spec.dim))
+        out = self._acting.decide(obs, noise=noise, deterministic=deterministic)
+        if not deterministic:
+            self.frame_count += lanes
+        return out["action"]
 
     # -- one update ----------------------------------------------------------
 
@@ -455,6 +482,7 @@ class SACLearner:
         return out
 
     def close(self) -> None:
+        self._acting.close()
         if self._graph is not None:
             self._graph.close()
             self._graph = None
