@@ -127,6 +127,48 @@ def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
     return learner, wall, gpu, (learner._graph.nodes if mode == "graph" else 0)
 
 
+def ppo_step_flops(batch: int = 256, actions: int = 18) -> float:
+    """One PPO minibatch step on the shared Nature-CNN actor-critic:
+    forward, weight gradients of every layer, input gradients of all but conv1."""
+    fwd = sum(NATURE_MACS[:-1]) + 512 * (actions + 1)
+    return 2.0 * batch * (2 * fwd + (fwd - NATURE_MACS[0]))
+
+
+def bench_ppo(dev, updates=5, mode="graph"):
+    """PPO updates over one resident rollout of 8 envs x 128 steps (1024
+    uint8 4x84x84 frames): GAE, normalisation and 4 epochs x 4 minibatches
+    of 256, each minibatch step one replay of the captured step graph."""
+    from ttrl_amd.algos.ppo import PPOConfig, PPOLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_qnet_state, ppo_rollout
+
+    cfg = PPOConfig(minibatch_size=256, epochs=4, n_steps=128, step_mode=mode)
+    learner = PPOLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(18), dev, cfg=cfg, seed=0)
+    learner.net.load_state_dict(he_uniform_qnet_state(learner.net, 4))
+    rollout = ppo_rollout(5000, 128, 8, 18)
+    steps = learner.load_rollout(rollout)
+    learner.run_update(steps)  # captures the step graph
+    dev.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(updates):
+        learner.run_update(steps)
+    dev.synchronize()
+    dt = (time.perf_counter() - t0) / updates
+    t1 = time.perf_counter()
+    learner.update(rollout)
+    host_dt = time.perf_counter() - t1
+    flops = ppo_step_flops(256, 18)
+    out = {"unit": "PPO minibatch steps/s", "value": round(steps / dt, 2), "batch": 256, "steps_per_update": steps,
+           "ms_per_update": round(dt * 1e3, 3), "ms_per_step": round(dt / steps * 1e3, 4),
+           "flops_per_step": flops, "roofline_frac": flops * steps / dt / PEAK_FP32_MFMA,
+           "ms_per_update_with_upload": round(host_dt * 1e3, 3),
+           "workload": "PPO update: 8 envs x 128 steps of uint8 4x84x84, GAE 0.99/0.95, 4 epochs x 4 minibatches "
+                       "of 256, Nature-CNN -> 512 -> {18, 1}, clip 0.1, vclip 0.1, vf 0.5, ent 0.01, "
+                       "grad clip 0.5, Adam 2.5e-4"}
+    learner.close()
+    return out
+
+
 def dominant_kernel(dev, learner, reps=200):
     """The longest kernel of the DQN update: the conv1 forward of the three
     Q evaluations in one launch (online(s), online(s'), target(s'); uint8
@@ -286,6 +328,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--act-steps", type=int, default=500, help="acting steps timed per lane count (0: skip)")
+    ap.add_argument("--ppo-updates", type=int, default=5, help="PPO updates timed (0: skip)")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
                     help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -308,6 +351,7 @@ def main() -> int:
     sflops = sac_update_flops(256)
     dom = dominant_kernel(dev, dqn)
     achieved = dom["flops"] / dom["seconds"]
+    ppo = bench_ppo(dev, args.ppo_updates, args.mode) if args.ppo_updates > 0 else None
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
@@ -341,6 +385,7 @@ def main() -> int:
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},
+        "ppo": ppo,
         "act": act,
         "cpu_baseline": cpu,
     }

@@ -300,6 +300,28 @@ int ttrl_ppo_loss(ttrl_ctx* ctx, int B, int A, const float* logits, const int* a
                   const float* advantages, const float* returns, const float* old_values, const float* values,
                   const float* valid, float clip_eps, float value_clip_eps, float value_coef, float entropy_coef,
                   float* out4, float* new_logp, float* dlogits, float* dvalues);
+/* ttrl_ppo_loss over the packed rows of the fused policy-and-value head:
+ * head [B][A+1] holds the logits in columns 0..A-1 and the value in column A,
+ * dhead is laid out the same; out5 = {loss, policy_loss, value_loss, entropy,
+ * approx_kl}, approx_kl = mean(expm1(r) - r) with r = new_logp - old_logp
+ * (ttrl/algos/ppo/learn.py:101-112). */
+int ttrl_ppo_loss_packed(ttrl_ctx* ctx, int B, int A, const float* head, const int* actions, const float* old_logp,
+                         const float* advantages, const float* returns, const float* old_values, const float* valid,
+                         float clip_eps, float value_clip_eps, float value_coef, float entropy_coef, float* out5,
+                         float* new_logp, float* dhead);
+/* Minibatch assembly by index from a resident flattened rollout
+ * (RolloutBuffer.minibatches, ttrl/buffers/rollout.py:239-282): for each of
+ * nsrc (<= 8) sources, dst[s] row i = src[s] row idx[c * stride + i], rows of
+ * row_bytes[s] bytes (a multiple of 4; 16-byte rows move as 16-byte units),
+ * i < n, c = *counter (counter NULL: c = 0).  Table slots past idx_len and
+ * indices outside [0, rows) are skipped. */
+int ttrl_gather_rows(ttrl_ctx* ctx, int n, int nsrc, const void* const* src, void* const* dst, const long* row_bytes,
+                     long rows, const int* idx, long idx_len, const int* counter, int stride);
+/* End of one replayed minibatch step: ring[c][0..n) = metrics when
+ * 0 <= c < slots, then *counter = c + 1 (the per-minibatch metric reads of
+ * ttrl/algos/ppo/learn.py:94-112, kept on the device for one read per
+ * update). */
+int ttrl_step_end(ttrl_ctx* ctx, int* counter, const float* metrics, int n, float* ring, int slots);
 /* Global L2 clip of one flat gradient arena, on the device (no host read):
  * norm = sqrt(sum g^2); if norm > max_norm, g *= max_norm / (norm + 1e-6).
  * *norm_out (nullable) receives the norm before clipping; sq_scratch is one

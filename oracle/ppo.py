@@ -16,6 +16,15 @@ ppo_objective        ttrl/algos/ppo/loss.py:27-83 with the categorical head's
                      tie to the first operand and vanish at clamp bounds
 clip_grad_norm       ttrl/algos/grads.py:13-43 (float64 norm, scale
                      max_norm / (norm + 1e-6) when norm > max_norm)
+minibatch_indices    RolloutBuffer.minibatches' shuffle (ttrl/buffers/rollout.py:239-282):
+                     valid rows only, one rng.permutation per epoch, trailing
+                     partial minibatch dropped
+ppo_update           ttrl/algos/ppo/learn.py:46-112 on a shared-trunk
+                     actor-critic whose two heads are one Linear of width A+1
+                     ([logits | value], ttrl/nets/models.py:65-71): GAE,
+                     normalisation, then per minibatch forward, objective,
+                     backward, clip_grad_norm, Adam (oracle.adam.fused_step),
+                     approx_kl = mean(expm1(r) - r)
 
 Forward values and the analytic gradients d loss / d logits, d loss / d
 values are float64.  Test infrastructure only.
@@ -24,6 +33,9 @@ values are float64.  Test infrastructure only.
 from __future__ import annotations
 
 import numpy as np
+
+from oracle import adam
+from oracle.nets import qnet_backward, qnet_forward
 
 
 def gae(rewards, values, dones, last_values, gamma: float, lam: float, valid=None):
@@ -125,3 +137,88 @@ def clip_grad_norm(g, max_norm: float):
     if total > max_norm:
         g = g * np.float32(max_norm / (total + 1e-6))
     return g, total
+
+
+def minibatch_indices(valid, minibatch_size: int, epochs: int, rng) -> list:
+    """Flat (time-major) row indices of every minibatch of one update."""
+    keep = np.flatnonzero(np.asarray(valid).reshape(-1) > 0.0)
+    total = int(keep.size)
+    n_full = total // minibatch_size
+    if n_full == 0:
+        raise ValueError("minibatch_indices: fewer valid rows than one minibatch")
+    out = []
+    for _ in range(epochs):
+        perm = rng.permutation(total)
+        for start in range(0, n_full * minibatch_size, minibatch_size):
+            out.append(keep[perm[start:start + minibatch_size]])
+    return out
+
+
+def ppo_minibatch_step(net, S: list, V: list, t: int, mb: dict, *, clip_eps: float = 0.1,
+                       value_clip_eps: float = 0.1, value_coef: float = 0.5, entropy_coef: float = 0.01,
+                       max_grad_norm: float = 0.5, lr: float = 2.5e-4, adam_eps: float = 1e-8,
+                       betas=(0.9, 0.999), gates=None, stats=None) -> dict:
+    """One minibatch step (ttrl/algos/ppo/learn.py:74-112) from parameters
+    `net` and Adam state S, V (stored form) with update count t (>= 1).
+    mb: obs, actions, old_logp, advantages, returns, values of the rows;
+    gates: device ReLU gates adopted inside the kink band (oracle.nets.gate).
+    -> dict(net, S, V, metrics, grads (clipped))."""
+    out, acts = qnet_forward(net, mb["obs"], gates=gates, stats=stats)
+    A = out.shape[1] - 1
+    old_logp = np.asarray(mb["old_logp"], np.float64).reshape(-1)
+    o = ppo_objective(out[:, :A], mb["actions"], old_logp, mb["advantages"], mb["returns"], mb["values"],
+                      out[:, A], clip_eps=clip_eps, value_clip_eps=value_clip_eps, value_coef=value_coef,
+                      entropy_coef=entropy_coef)
+    dout = np.concatenate([o["dlogits"], o["dvalues"][:, None]], axis=1)
+    grads = qnet_backward(net, acts, dout)
+    norm = float(np.sqrt(sum(np.sum(g * g) for g in grads)))
+    if norm > max_grad_norm:
+        grads = [g * (max_grad_norm / (norm + 1e-6)) for g in grads]
+    logratio = o["new_logp"] - old_logp
+    params, S2, V2 = [], [], []
+    for p, g, s_, v_ in zip(net.flat(), grads, S, V):
+        p2, s2, v2 = adam.fused_step(p, g, s_, v_, t, lr, betas[0], betas[1], adam_eps)
+        params.append(p2)
+        S2.append(s2)
+        V2.append(v2)
+    metrics = dict(loss=o["loss"], policy_loss=o["policy_loss"], value_loss=o["value_loss"], entropy=o["entropy"],
+                   approx_kl=float(np.mean(np.expm1(logratio) - logratio)), grad_norm=norm)
+    return dict(net=net.with_flat(params), S=S2, V=V2, metrics=metrics, grads=grads)
+
+
+def ppo_update(net, rollout: dict, *, rng, minibatch_size: int, epochs: int, gamma: float = 0.99,
+               lam: float = 0.95, normalize_adv: bool = True, keep_grads: bool = False, **step_cfg) -> dict:
+    """-> dict(net, steps=[per-step metrics], advantages, returns, batches[,
+    grads]).  `net` is an oracle.nets.QNet whose last layer has A + 1
+    outputs; batches[t] holds step t's minibatch rows, grads[t] its clipped
+    gradients (with keep_grads); step_cfg goes to ppo_minibatch_step."""
+    rewards = np.asarray(rollout["rewards"], np.float32)
+    T, N = rewards.shape
+    valid = rollout.get("valid")
+    valid = np.ones((T, N), np.float32) if valid is None else np.asarray(valid, np.float32)
+    adv, ret = gae(rewards, rollout["values"], rollout["dones"], rollout["last_values"], gamma, lam, valid)
+    if normalize_adv:
+        adv_n, _, _ = normalize_advantages(adv, valid)
+    else:
+        adv_n = adv.astype(np.float64)
+    flat = dict(obs=np.asarray(rollout["obs"]).reshape((T * N,) + np.shape(rollout["obs"])[2:]),
+                actions=np.asarray(rollout["actions"]).reshape(-1),
+                old_logp=np.asarray(rollout["logp"], np.float64).reshape(-1),
+                advantages=np.asarray(adv_n, np.float64).reshape(-1),
+                returns=np.asarray(ret, np.float64).reshape(-1),
+                values=np.asarray(rollout["values"], np.float64).reshape(-1))
+    S = [np.zeros(np.shape(p)) for p in net.flat()]
+    V = [np.zeros(np.shape(p)) for p in net.flat()]
+    steps, kept, batches = [], [], []
+    for t, idx in enumerate(minibatch_indices(valid, minibatch_size, epochs, rng), start=1):
+        mb = {k: v[idx] for k, v in flat.items()}
+        r = ppo_minibatch_step(net, S, V, t, mb, **step_cfg)
+        net, S, V = r["net"], r["S"], r["V"]
+        steps.append(r["metrics"])
+        batches.append(mb)
+        if keep_grads:
+            kept.append(r["grads"])
+    out = dict(net=net, steps=steps, advantages=adv, returns=ret, batches=batches)
+    if keep_grads:
+        out["grads"] = kept
+    return out

@@ -115,3 +115,22 @@ def test_folded_convolutions_are_refused():
 
     with pytest.raises(ValueError, match="fold=2"):
         check_encoder_layout(Net())
+
+
+def test_a_shared_trunk_checkpoints_once():
+    """One self-serialising module in two slots appears once in the state
+    (ttrl/engine/nn/discovery.py:128-139), as a shared actor-critic trunk."""
+    import numpy as np
+    from ttrl_amd.engine.nn import Module, ModuleDict
+
+    class Leaf(Module):
+        def state_dict(self):
+            return {"w": np.ones(2)}
+
+    class Net(Module):
+        def __init__(self):
+            trunk = Leaf()
+            self.encoders = ModuleDict({"actor": trunk, "critic": trunk})
+            self.head = Leaf()
+
+    assert list(Net().state_dict()) == ["encoders.actor.w", "head.w"]

@@ -130,6 +130,9 @@ __global__ __launch_bounds__(kRedThreads) void k_adv_normalize(const float* __re
 struct PpoCfg {
   int B, A;
   float clip, vclip, vcoef, ecoef;
+  int ldz;   // row stride of logits / dlogits
+  int ldv;   // element stride of values / dvalues
+  int kl;    // also write out[4] = approx_kl = mean(expm1(r) - r), r = new_logp - old_logp
 };
 
 // The PPO objective for one minibatch in one workgroup: per row the
@@ -152,9 +155,9 @@ __global__ __launch_bounds__(kRedThreads) void k_ppo_loss(
   const float total = tree_sum<kRedThreads>(wsum, sh);  // sum_all(valid)
   const float inv = 1.f / total;
 
-  float s_pol = 0.f, s_val = 0.f, s_ent = 0.f;
+  float s_pol = 0.f, s_val = 0.f, s_ent = 0.f, s_kl = 0.f;
   for (int i = threadIdx.x; i < B; i += kRedThreads) {
-    const float* z = logits + long(i) * A;
+    const float* z = logits + long(i) * cfg.ldz;
     const float w = valid ? valid[i] : 1.f;
     float mx = z[0];
     for (int j = 1; j < A; ++j) mx = fmaxf(mx, z[j]);
@@ -174,7 +177,9 @@ __global__ __launch_bounds__(kRedThreads) void k_ppo_loss(
     new_logp[i] = lp;
 
     // clipped surrogate
-    const float r = expf(lp - old_logp[i]);
+    const float lr = lp - old_logp[i];
+    s_kl += expm1f(lr) - lr;  // Schulman's k3 estimator (ttrl/algos/ppo/learn.py:101-104)
+    const float r = expf(lr);
     const float lo = 1.f - cfg.clip, hi = 1.f + cfg.clip;
     const float rc = fminf(fmaxf(r, lo), hi);
     const float Ad = adv[i];
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(kRedThreads) void k_ppo_loss(
     const float dsurr_dr = take_u ? Ad : dclamp * Ad;
 
     // clipped value error
-    const float v = value[i], ov = old_value[i], R = returns[i];
+    const float v = value[long(i) * cfg.ldv], ov = old_value[i], R = returns[i];
     const float dv = v - ov;
     const float dvc = fminf(fmaxf(dv, -cfg.vclip), cfg.vclip);
     const float eu = v - R, ec = (ov + dvc) - R;
@@ -202,22 +207,24 @@ __global__ __launch_bounds__(kRedThreads) void k_ppo_loss(
     // d loss / d logits: -(w/total) dsurr/dr * r * (onehot - p) + ecoef (w/total) p (logp + H)
     const float gp = act_in ? -w * inv * dsurr_dr * r : 0.f;
     const float ge = cfg.ecoef * w * inv;
-    float* dz = dlogits + long(i) * A;
+    float* dz = dlogits + long(i) * cfg.ldz;
     for (int j = 0; j < A; ++j) {
       const float l = (z[j] - mx) - lse;
       const float p = expf(l);
       dz[j] = gp * ((j == a ? 1.f : 0.f) - p) + ge * p * (l + H);
     }
-    dvalue[i] = cfg.vcoef * 0.5f * w * inv * dq_dv;
+    dvalue[long(i) * cfg.ldv] = cfg.vcoef * 0.5f * w * inv * dq_dv;
   }
   const float pol = -tree_sum<kRedThreads>(s_pol, sh) * inv;
   const float val = 0.5f * tree_sum<kRedThreads>(s_val, sh) * inv;
   const float ent = tree_sum<kRedThreads>(s_ent, sh) * inv;
+  const float kl = cfg.kl ? tree_sum<kRedThreads>(s_kl, sh) / float(B) : 0.f;
   if (threadIdx.x == 0) {
     out[0] = (pol + val * cfg.vcoef) + ent * -cfg.ecoef;
     out[1] = pol;
     out[2] = val;
     out[3] = ent;
+    if (cfg.kl) out[4] = kl;
   }
 }
 
@@ -269,10 +276,25 @@ int ttrl_ppo_loss(ttrl_ctx* ctx, int B, int A, const float* logits, const int* a
                "ttrl_ppo_loss: null argument");
   TTRL_REQUIRE(B > 0 && A > 0, "ttrl_ppo_loss: B and A must be positive (got %d, %d)", B, A);
   TTRL_REQUIRE(clip_eps > 0.f && value_clip_eps > 0.f, "ttrl_ppo_loss: clip ranges must be positive");
-  PpoCfg cfg{B, A, clip_eps, value_clip_eps, value_coef, entropy_coef};
+  PpoCfg cfg{B, A, clip_eps, value_clip_eps, value_coef, entropy_coef, A, 1, 0};
   hipLaunchKernelGGL(k_ppo_loss, dim3(1), dim3(kRedThreads), 0, stream_of(ctx), cfg, logits, actions, old_logp,
                      advantages, returns, old_values, values, valid, out4, new_logp, dlogits, dvalues);
   return check_launch("ttrl_ppo_loss");
+}
+
+int ttrl_ppo_loss_packed(ttrl_ctx* ctx, int B, int A, const float* head, const int* actions, const float* old_logp,
+                         const float* advantages, const float* returns, const float* old_values, const float* valid,
+                         float clip_eps, float value_clip_eps, float value_coef, float entropy_coef, float* out5,
+                         float* new_logp, float* dhead) {
+  TTRL_REQUIRE(ctx && head && actions && old_logp && advantages && returns && old_values && out5 && new_logp &&
+                   dhead,
+               "ttrl_ppo_loss_packed: null argument");
+  TTRL_REQUIRE(B > 0 && A > 0, "ttrl_ppo_loss_packed: B and A must be positive (got %d, %d)", B, A);
+  TTRL_REQUIRE(clip_eps > 0.f && value_clip_eps > 0.f, "ttrl_ppo_loss_packed: clip ranges must be positive");
+  PpoCfg cfg{B, A, clip_eps, value_clip_eps, value_coef, entropy_coef, A + 1, A + 1, 1};
+  hipLaunchKernelGGL(k_ppo_loss, dim3(1), dim3(kRedThreads), 0, stream_of(ctx), cfg, head, actions, old_logp,
+                     advantages, returns, old_values, head + A, valid, out5, new_logp, dhead, dhead + A);
+  return check_launch("ttrl_ppo_loss_packed");
 }
 
 int ttrl_clip_grad_norm(ttrl_ctx* ctx, float* g, long n, float max_norm, float* sq_scratch, float* norm_out) {

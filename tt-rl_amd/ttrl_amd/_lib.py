@@ -119,6 +119,9 @@ SIGNATURES = {
     "ttrl_polyak": ([P, P, P, L, F], I),
     "ttrl_gae": ([P, I, I, P, P, P, P, P, C.c_double, C.c_double, P, P], I),
     "ttrl_normalize_advantages": ([P, P, P, L, F, P, P], I),
+    "ttrl_ppo_loss_packed": ([P, I, I, P, P, P, P, P, P, P, F, F, F, F, P, P, P], I),
+    "ttrl_gather_rows": ([P, I, I, P, P, P, C.c_long, P, C.c_long, P, I], I),
+    "ttrl_step_end": ([P, P, P, I, P, I], I),
     "ttrl_ppo_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, F, F, F, P, P, P, P], I),
     "ttrl_clip_grad_norm": ([P, P, L, F, P, P], I),
     "ttrl_unary": ([P, I, P, P, L, F], I),

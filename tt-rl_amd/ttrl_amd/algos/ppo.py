@@ -23,11 +23,14 @@ from dataclasses import dataclass
 
 import numpy as np
 
+from ttrl_amd import _lib
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs
-from ttrl_amd.engine.tensor import DeviceArray, arena_of, to_device
+from ttrl_amd.engine.optim import Adam
+from ttrl_amd.engine.tensor import DeviceArray, arena_of, bound_block, to_device
+from ttrl_amd.engine.trace import capture
 
-__all__ = ["PPOLossConfig", "compute_gae", "normalize_advantages", "objective", "clip_grad_norm",
-           "clip_grad_norm_device"]
+__all__ = ["PPOConfig", "PPOLearner", "PPOLossConfig", "compute_gae", "normalize_advantages", "objective",
+           "objective_packed", "clip_grad_norm", "clip_grad_norm_device"]
 
 
 def _dev(x, device, dtype=np.float32) -> DeviceArray:
@@ -148,6 +151,35 @@ def objective(policy_out: Tensor, value: Tensor, batch, cfg: PPOLossConfig, vali
     return loss, parts, Tensor(new_logp)
 
 
+def objective_packed(head: Tensor, mb: dict, cfg, out5: DeviceArray, new_logp: DeviceArray) -> Tensor:
+    """The objective over the fused head's packed [logits | value] rows, as
+    one tape node (ttrl/algos/ppo/loss.py:42-83).  `mb` holds the minibatch's
+    device arrays `actions` (int32), `old_logp`, `advantages`, `returns`,
+    `values`; out5 receives {loss, policy_loss, value_loss, entropy,
+    approx_kl} and new_logp the rows' log-probs.  The loss is the (1, 1)
+    view out5[0]."""
+    dev = head.device
+    B, N = (int(d) for d in head.shape)
+    A = N - 1
+    dhead = DeviceArray(dev, (B, N))
+    dev.call("ttrl_ppo_loss_packed", B, A, head.data.vp, mb["actions"].vp, mb["old_logp"].vp,
+             mb["advantages"].vp, mb["returns"].vp, mb["values"].vp, None, C.c_float(cfg.clip_eps),
+             C.c_float(cfg.value_clip_eps), C.c_float(cfg.value_coef), C.c_float(cfg.entropy_coef), out5.vp,
+             new_logp.vp, dhead.vp)
+    loss_arr = out5.view(0, (1, 1))
+    if not _needs(head):
+        return _detached(loss_arr)
+    loss = Tensor(loss_arr, True, (head,), "ppo_objective")
+
+    def _backward(grad):
+        from ttrl_amd.engine.ops import _kernels as K
+
+        head._accumulate(dhead if grad.unit else K.binary("mul", dhead, grad.reshape((1, 1))))
+
+    loss._backward = _backward
+    return loss
+
+
 def clip_grad_norm_device(grad: DeviceArray, max_norm: float) -> DeviceArray:
     """Clip one flat gradient buffer in place; -> the norm before clipping,
     as a (1,) device array (readable after the update)."""
@@ -173,3 +205,279 @@ def clip_grad_norm(params, max_norm: float) -> float:
         raise RuntimeError("clip_grad_norm: every parameter of the arena needs this step's gradient")
     norm = clip_grad_norm_device(arena.grad, max_norm)
     return float(norm.numpy()[0])
+
+
+# ------------------------------------------------------------ the learner ---
+
+@dataclass(frozen=True)
+class PPOConfig:
+    """Learner-side fields of ttrl/algos/ppo/config.py:67-120, plus the Adam
+    epsilon (the engine default 1e-8, ttrl/algos/ppo/agent.py:81)."""
+
+    lr: float = 2.5e-4
+    adam_eps: float = 1e-8
+    gamma: float = 0.99
+    lam: float = 0.95
+    n_steps: int = 128
+    minibatch_size: int = 32
+    epochs: int = 4
+    clip_eps: float = 0.1
+    value_clip_eps: float = 0.1
+    value_coef: float = 0.5
+    entropy_coef: float = 0.01
+    max_grad_norm: float = 0.5
+    normalize_adv: bool = True
+    anneal_lr: bool = False
+    total_frames: int | None = None
+    step_mode: str = "graph"
+    encoder: str = "auto"
+
+    def __post_init__(self):
+        if self.lr <= 0 or self.adam_eps <= 0:
+            raise ValueError("PPOConfig: lr and adam_eps must be > 0")
+        if not 0.0 < self.gamma <= 1.0 or not 0.0 <= self.lam <= 1.0:
+            raise ValueError(f"PPOConfig: need 0 < gamma <= 1 and 0 <= lam <= 1, got {self.gamma}, {self.lam}")
+        if self.n_steps < 1 or self.minibatch_size < 1 or self.epochs < 1:
+            raise ValueError("PPOConfig: n_steps, minibatch_size and epochs must be >= 1")
+        if not (self.clip_eps > 0 and self.value_clip_eps > 0 and self.max_grad_norm > 0):
+            raise ValueError("PPOConfig: clip_eps, value_clip_eps and max_grad_norm must be > 0")
+        if self.step_mode not in ("eager", "graph"):
+            raise ValueError(f"PPOConfig: step_mode must be 'eager' or 'graph', got {self.step_mode!r}")
+        if self.anneal_lr and not self.total_frames:
+            raise ValueError("PPOConfig: anneal_lr needs total_frames")
+        if self.anneal_lr and self.step_mode == "graph":
+            raise ValueError("PPOConfig: the learning rate is a constant of the captured minibatch step; "
+                             "anneal_lr needs step_mode='eager'")
+
+
+class _Resident:
+    """One rollout of T x N transitions resident in HBM, flattened time-major
+    (row t * N + n, the reference's reshape order), with the shuffled index
+    table of every minibatch of one update and the per-step metric ring."""
+
+    def __init__(self, device, obs_spec, T: int, N: int, cfg: PPOConfig):
+        rows = T * N
+        self.T, self.N, self.rows = T, N, rows
+        mb = cfg.minibatch_size
+        self.table_len = cfg.epochs * (rows // mb) * mb
+        if obs_spec.kind == "image":
+            frames = np.zeros((rows,) + tuple(obs_spec.shape), np.uint8)
+        else:
+            frames = np.zeros((rows, obs_spec.size), np.float32)
+        z = np.zeros(rows, np.float32)
+        specs = [("obs", frames), ("actions", np.zeros(rows, np.int32)), ("logp", z), ("values", z),
+                 ("rewards", z), ("dones", z), ("valid", z), ("last_values", np.zeros(N, np.float32)),
+                 ("idx", np.zeros(max(self.table_len, 1), np.int32))]
+        self.host, self.block = bound_block(device, specs)
+        self.image = np.zeros(self.block.nbytes, np.uint8)
+        self.advantages = DeviceArray(device, (rows,))
+        self.returns = DeviceArray(device, (rows,))
+        self.adv_norm = DeviceArray(device, (rows,))
+        self.slots = cfg.epochs * (rows // mb)
+        self.ring = DeviceArray(device, (max(self.slots, 1), len(PPOLearner.METRICS)))
+
+    def stage(self, name: str, array) -> None:
+        view = self.host[name]
+        arr = np.ascontiguousarray(array, dtype=view.dtype)
+        if arr.size != view.numel:
+            raise ValueError(f"PPO rollout field {name!r}: {arr.shape} does not fit {view.shape}")
+        off = view.offset - self.block.offset
+        self.image[off:off + arr.nbytes] = arr.reshape(-1).view(np.uint8)
+
+
+class PPOLearner:
+    """The PPO update (ttrl/algos/ppo/learn.py:46-112) on a shared-trunk
+    actor-critic (ttrl/nets/build.py:95-117).
+
+    `update(rollout)` uploads one rollout (time-major [T, N] fields plus the
+    frames) into a resident HBM block in one copy, runs GAE and the advantage
+    normalisation on the device, and then every minibatch step of every
+    epoch: gather by index from the resident rollout, trunk forward, the
+    fused [logits | value] head, the fused objective, backward, global-norm
+    clip, Adam, and the step's metrics into a device ring.  In graph mode the
+    minibatch step is one captured graph replayed epochs x minibatches times
+    back to back (a device counter selects the minibatch); the metrics are
+    read once per update.  The shuffles are the reference's: one
+    `rng.permutation` of the valid rows per epoch from a generator seeded
+    with `seed`, trailing partial minibatch dropped.
+    """
+
+    METRICS = ("loss", "policy_loss", "value_loss", "entropy", "approx_kl", "grad_norm")
+
+    def __init__(self, obs_spec, action_spec, device, *, cfg: PPOConfig = PPOConfig(), seed: int | None = None):
+        from ttrl_amd.nets.build import build_actor_critic
+
+        if action_spec.kind != "discrete":
+            raise ValueError(f"PPOLearner supports discrete actions only, got {action_spec.kind!r}")
+        self.cfg = cfg
+        self.device = device
+        self.obs_spec, self.action_spec = obs_spec, action_spec
+        if seed is not None:
+            np.random.seed(seed)
+        self.net = build_actor_critic(obs_spec, action_spec, device, batch=cfg.minibatch_size,
+                                      encoder=cfg.encoder)
+        self.params = list(self.net.parameters())
+        self.optimizer = Adam(self.params, lr=cfg.lr, eps=cfg.adam_eps)
+        self._rng = np.random.default_rng(seed)
+        self.frame_count = 0
+        self.update_count = 0
+        mb = cfg.minibatch_size
+        if obs_spec.kind == "image":
+            obs = np.zeros((mb,) + tuple(obs_spec.shape), np.uint8)
+        else:
+            obs = np.zeros((mb, obs_spec.size), np.float32)
+        z = np.zeros(mb, np.float32)
+        self.mb, self.mb_block = bound_block(device, [
+            ("obs", obs), ("actions", np.zeros(mb, np.int32)), ("old_logp", z), ("advantages", z),
+            ("returns", z), ("values", z)])
+        self._counter = DeviceArray(device, (1,), np.int32)
+        self._metrics = DeviceArray(device, (len(self.METRICS),))
+        self._sq = DeviceArray(device, (1,))
+        self._new_logp = DeviceArray(device, (mb, 1))
+        self._res: _Resident | None = None
+        self._graph = None
+        self._pool = None
+
+    # -- one minibatch step --------------------------------------------------
+
+    def _gather(self) -> None:
+        r, mb = self._res, self.mb
+        pairs = [(r.host["obs"], mb["obs"]), (r.host["actions"], mb["actions"]), (r.host["logp"], mb["old_logp"]),
+                 (r.adv_norm, mb["advantages"]), (r.returns, mb["returns"]), (r.host["values"], mb["values"])]
+        row_bytes = (C.c_long * len(pairs))(*[d.nbytes // self.cfg.minibatch_size for _s, d in pairs])
+        self.device.call("ttrl_gather_rows", self.cfg.minibatch_size, len(pairs), _lib.ptrs(s.ptr for s, _ in pairs),
+                         _lib.ptrs(d.ptr for _, d in pairs), row_bytes, C.c_long(r.rows), r.host["idx"].vp,
+                         C.c_long(r.table_len), self._counter.vp, self.cfg.minibatch_size)
+
+    def _forward_backward(self) -> None:
+        from ttrl_amd.nets.heads import policy_value_packed
+
+        self._gather()
+        net = self.net
+        features = net.encoders["actor"](Tensor(self.mb["obs"]))
+        head = policy_value_packed(net.heads["policy"], net.heads["value"], features)
+        loss = objective_packed(head, self.mb, self.cfg, self._metrics.view(0, (5,)), self._new_logp)
+        loss.backward()
+
+    def _step(self) -> None:
+        dev = self.device
+        self._forward_backward()
+        grad = self.optimizer.arena_grads()
+        dev.call("ttrl_clip_grad_norm", grad.vp, C.c_long(grad.numel), C.c_float(self.cfg.max_grad_norm),
+                 self._sq.vp, C.c_void_p(self._metrics.ptr + 4 * 5))
+        self.optimizer.step()
+        r = self._res
+        dev.call("ttrl_step_end", self._counter.vp, self._metrics.vp, len(self.METRICS), r.ring.vp, r.slots)
+
+    def _capture(self) -> None:
+        dev = self.device
+        self._pool = dev.create_pool()
+        with dev.use_pool(self._pool):
+            self.optimizer.zero_grad()
+            self._forward_backward()  # warm-up: tunes plans and fills the pool; no parameter changes
+            self.optimizer.zero_grad()
+            dev.synchronize()
+            self._graph, _ = capture(dev, self._step)
+
+    def _release_graph(self) -> None:
+        if self._graph is not None:
+            self._graph.close()
+            self._graph = None
+        if self._pool is not None and not self.device.closed:
+            self.device.release_pool(self._pool)
+        self._pool = None
+
+    # -- one update ----------------------------------------------------------
+
+    def _resident(self, T: int, N: int) -> _Resident:
+        r = self._res
+        if r is None or (r.T, r.N) != (T, N):
+            self._release_graph()
+            self._res = r = _Resident(self.device, self.obs_spec, T, N, self.cfg)
+        return r
+
+    def load_rollout(self, rollout: dict) -> int:
+        """Upload one rollout and its minibatch index table; -> minibatch
+        steps this update will run.  Fields (time-major): obs [T, N, ...],
+        actions, rewards, dones, values, logp [T, N], last_values [N]
+        (the critic's value after the last step), optional valid [T, N]."""
+        rewards = np.asarray(rollout["rewards"], np.float32)
+        if rewards.ndim != 2:
+            raise ValueError(f"PPOLearner: rollout fields must be time-major [T, N], got rewards {rewards.shape}")
+        T, N = rewards.shape
+        r = self._resident(T, N)
+        cfg = self.cfg
+        valid = rollout.get("valid")
+        valid = np.ones((T, N), np.float32) if valid is None else np.asarray(valid, np.float32).reshape(T, N)
+        keep = np.flatnonzero(valid.reshape(-1) > 0.0)
+        total = int(keep.size)
+        mb = cfg.minibatch_size
+        n_full = total // mb
+        if n_full == 0:
+            raise ValueError(f"PPOLearner: {total} valid transitions but minibatch_size={mb}, which would yield "
+                             f"zero minibatches (n_steps={T}, n_envs={N}). Lower minibatch_size or collect a "
+                             f"longer rollout.")
+        table = np.zeros(max(r.table_len, 1), np.int32)
+        for e in range(cfg.epochs):
+            perm = self._rng.permutation(total)
+            table[e * n_full * mb:(e + 1) * n_full * mb] = keep[perm[:n_full * mb]]
+        r.stage("obs", np.asarray(rollout["obs"]).reshape((T * N,) + r.host["obs"].shape[1:]))
+        r.stage("actions", np.asarray(rollout["actions"]).reshape(-1).astype(np.int32))
+        for name, key in (("logp", "logp"), ("values", "values"), ("rewards", "rewards"), ("dones", "dones")):
+            r.stage(name, np.asarray(rollout[key], np.float32).reshape(-1))
+        r.stage("valid", valid.reshape(-1))
+        r.stage("last_values", np.asarray(rollout["last_values"], np.float32).reshape(-1))
+        r.stage("idx", table)
+        r.block.upload(r.image)
+        return cfg.epochs * n_full
+
+    def begin_update(self) -> None:
+        """GAE and the advantage normalisation over the resident rollout,
+        and the step counter back to the first minibatch (no host transfer)."""
+        cfg, r, dev = self.cfg, self._res, self.device
+        h = r.host
+        dev.call("ttrl_gae", r.T, r.N, h["rewards"].vp, h["values"].vp, h["dones"].vp, h["valid"].vp,
+                 h["last_values"].vp, C.c_double(cfg.gamma), C.c_double(cfg.lam), r.advantages.vp, r.returns.vp)
+        if cfg.normalize_adv:
+            dev.call("ttrl_normalize_advantages", r.advantages.vp, h["valid"].vp, C.c_long(r.rows),
+                     C.c_float(1e-8), r.adv_norm.vp, None)
+        else:
+            r.adv_norm.copy_from(r.advantages)
+        self._counter.fill(0)
+        if cfg.step_mode == "graph" and self._graph is None:
+            self._capture()
+
+    def run_steps(self, n: int) -> None:
+        """The next n minibatch steps of the current update."""
+        if self.cfg.step_mode == "graph":
+            self._graph.replay_n(n)
+            for _ in range(n):
+                self.optimizer._replayed()
+        else:
+            for _ in range(n):
+                self.optimizer.zero_grad()
+                self._step()
+
+    def run_update(self, steps: int) -> None:
+        """GAE, normalisation and `steps` minibatch steps over the resident
+        rollout (no host transfer)."""
+        self.begin_update()
+        self.run_steps(steps)
+
+    def update(self, rollout: dict) -> dict:
+        """One rollout's update; -> the reference's metric keys averaged over
+        the minibatch steps, plus lr and minibatches."""
+        cfg = self.cfg
+        if cfg.anneal_lr:
+            self.optimizer.lr = cfg.lr * max(0.0, 1.0 - self.frame_count / cfg.total_frames)
+        steps = self.load_rollout(rollout)
+        self.run_update(steps)
+        ring = self._res.ring.numpy()[:steps].astype(np.float64)
+        self.update_count += 1
+        out = {k: float(np.mean(ring[:, i])) for i, k in enumerate(self.METRICS)}
+        out["lr"] = self.optimizer.lr
+        out["minibatches"] = float(steps)
+        return out
+
+    def close(self) -> None:
+        self._release_graph()

@@ -49,6 +49,11 @@ def _slots_from(prefix: str, value, seen: set):
         return []
     if isinstance(value, Module):
         if _serialises_own_state(value):
+            # One module in two slots (a shared trunk) checkpoints once
+            # (ttrl/engine/nn/discovery.py:128-139).
+            if id(value) in seen:
+                return []
+            seen.add(id(value))
             return [(prefix, value)]
         out = []
         for name, child in value._slot_sources():

@@ -140,6 +140,20 @@ class Adam(Optimizer):
             first = False
             self.steps[i] += 1
 
+    def arena_grads(self) -> DeviceArray:
+        """The arena's flat gradient, after moving every parameter's gradient
+        into its slot there (what a global-norm clip reads before the step)."""
+        if self.arena is None:
+            raise ValueError("Adam.arena_grads: the parameters are not one ParamArena's")
+        for p in self.params:
+            if p.grad is None:
+                raise RuntimeError("Adam.arena_grads: every parameter needs this step's gradient")
+            if p.grad is not p._grad_slot:
+                p._grad_slot.copy_from(p.grad)
+                p.grad = p._grad_slot
+                p._grad_owned = True
+        return self.arena.grad
+
     def _step_one(self, i, p, g, args, accumulate):
         dev = self.device
         pd, m, v = p.data, self.m[i], self.v[i]

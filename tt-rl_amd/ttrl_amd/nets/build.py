@@ -14,10 +14,10 @@ from ttrl_amd.engine.layers import Linear, ReLU, Sequential
 from ttrl_amd.engine.nn import ModuleList
 from ttrl_amd.engine.tensor import ParamArena
 from ttrl_amd.nets.encoders import identity_encoder, image_encoder, vector_encoder
-from ttrl_amd.nets.heads import GaussianHead, QHead, ValueHead
-from ttrl_amd.nets.models import ConcatEncoder, ContinuousCritic, EncoderHead, SacNets
+from ttrl_amd.nets.heads import CategoricalHead, GaussianHead, QHead, ValueHead
+from ttrl_amd.nets.models import ActorCritic, ConcatEncoder, ContinuousCritic, EncoderHead, SacNets
 
-__all__ = ["build_encoder", "build_q_net", "build_sac_nets"]
+__all__ = ["build_actor_critic", "build_encoder", "build_q_net", "build_sac_nets"]
 
 
 def build_encoder(obs_spec, device, *, batch: int, name: str = "auto", role: str = "actor", **kwargs):
@@ -42,6 +42,22 @@ def build_q_net(obs_spec, action_spec, device, *, batch: int, encoder: str = "au
     with ParamArena(device, "q_net") as arena:
         tower = build_encoder(obs_spec, device, batch=batch, name=encoder, **encoder_kwargs)
         net = EncoderHead(tower, QHead(tower.out_features, action_spec.width, device))
+    net.arena = arena
+    return net
+
+
+def build_actor_critic(obs_spec, action_spec, device, *, batch: int, encoder: str = "auto",
+                       **encoder_kwargs) -> ActorCritic:
+    """Shared trunk + categorical policy head + value head, for PPO
+    (ttrl/nets/build.py:95-117, discrete actions; every observation field
+    belongs to the actor here, so one trunk fills both slots)."""
+    if action_spec.kind != "discrete":
+        raise ValueError(f"build_actor_critic supports discrete actions only, got {action_spec.kind!r}")
+    with ParamArena(device, "actor_critic") as arena:
+        trunk = build_encoder(obs_spec, device, batch=batch, name=encoder, **encoder_kwargs)
+        policy = CategoricalHead(trunk.out_features, action_spec.width, device)
+        value = ValueHead(trunk.out_features, device)
+        net = ActorCritic(trunk, trunk, policy, value)
     net.arena = arena
     return net
 

@@ -69,39 +69,56 @@ class GaussianHead(Module):
         """(B, 2d) rows [mean | clamp(log_std)] from one launch.  Its backward
         expects the log_std columns' gradient already masked to the open clamp
         interval, which the fused squashed-sample backward provides."""
-        lm, ls = self.heads["mean"], self.heads["log_std"]
-        M, K = (int(d) for d in x.shape)
-        d = self.action_dim
-        dev = x.device
-        y = DeviceArray(dev, (M, 2 * d))
-        desc = _lib.LinearDesc()
-        desc.M, desc.K, desc.N, desc.groups = M, K, 2 * d, 1
-        desc.x, desc.ldx = x.data.ptr, K
-        desc.W, desc.b = lm.weight.data.ptr, lm.bias.data.ptr
-        desc.W2, desc.b2, desc.n1 = ls.weight.data.ptr, ls.bias.data.ptr, d
-        desc.y = y.ptr
-        desc.clamp_col, desc.lo, desc.hi = d, self.log_std_min, self.log_std_max
-        dev.call("ttrl_linear_forward", C.byref(desc))
-        params = (lm.weight, lm.bias, ls.weight, ls.bias)
-        if not _needs(x, *params):
-            return _detached(y)
-        out = Tensor(y, True, (x,) + params, "gaussian_head")
-        x_data = x.data
+        return packed_linear_pair(self.heads["mean"], self.heads["log_std"], x,
+                                  clamp=(self.log_std_min, self.log_std_max), op="gaussian_head")
 
-        def _backward(grad):
-            (dwm, dbm, dws, dbs), beta_w = grad_targets(*params)
-            (dx,), beta_x = grad_targets(x)
-            b = _lib.LinearDesc()
-            b.M, b.K, b.N, b.groups = M, K, 2 * d, 1
-            b.x, b.ldx = x_data.ptr, K
-            b.W, b.W2, b.n1 = lm.weight.data.ptr, ls.weight.data.ptr, d
-            b.dy = grad.ptr
-            if dwm is not None:
-                b.dW, b.db, b.dW2, b.db2 = dwm.ptr, dbm.ptr, dws.ptr, dbs.ptr
-            b.dx = None if dx is None else dx.ptr
-            b.lddx = K
-            b.beta_w, b.beta_x = beta_w, beta_x
-            dev.call("ttrl_linear_backward", C.byref(b))
 
-        out._backward = _backward
-        return out
+def policy_value_packed(policy: CategoricalHead, value: ValueHead, x: Tensor) -> Tensor:
+    """(B, A + 1) rows [logits | value] of a shared-trunk actor-critic's two
+    heads (ttrl/nets/models.py:65-71) from one launch."""
+    return packed_linear_pair(policy.logits, value.value, x, op="policy_value_head")
+
+
+def packed_linear_pair(first: Linear, second: Linear, x: Tensor, *, clamp=None, op: str) -> Tensor:
+    """(B, n1 + n2) rows [x W1 + b1 | x W2 + b2] of two Linear layers over one
+    input, from one launch; `clamp` = (lo, hi) clamps the second block in the
+    epilogue.  Backward: both layers' dW and db and dx in one launch."""
+    M, K = (int(d) for d in x.shape)
+    n1 = first.out_features
+    N = n1 + second.out_features
+    dev = x.device
+    y = DeviceArray(dev, (M, N))
+    desc = _lib.LinearDesc()
+    desc.M, desc.K, desc.N, desc.groups = M, K, N, 1
+    desc.x, desc.ldx = x.data.ptr, K
+    desc.W, desc.b = first.weight.data.ptr, None if first.bias is None else first.bias.data.ptr
+    desc.W2, desc.b2, desc.n1 = second.weight.data.ptr, None if second.bias is None else second.bias.data.ptr, n1
+    desc.y = y.ptr
+    if clamp is not None:
+        desc.clamp_col, desc.lo, desc.hi = n1, float(clamp[0]), float(clamp[1])
+    dev.call("ttrl_linear_forward", C.byref(desc))
+    params = tuple(t for t in (first.weight, first.bias, second.weight, second.bias) if t is not None)
+    if not _needs(x, *params):
+        return _detached(y)
+    if first.bias is None or second.bias is None:
+        raise ValueError(f"{op}: the fused backward needs both layers to have a bias")
+    out = Tensor(y, True, (x,) + params, op)
+    x_data = x.data
+
+    def _backward(grad):
+        (dw1, db1, dw2, db2), beta_w = grad_targets(*params)
+        (dx,), beta_x = grad_targets(x)
+        b = _lib.LinearDesc()
+        b.M, b.K, b.N, b.groups = M, K, N, 1
+        b.x, b.ldx = x_data.ptr, K
+        b.W, b.W2, b.n1 = first.weight.data.ptr, second.weight.data.ptr, n1
+        b.dy = grad.ptr
+        if dw1 is not None:
+            b.dW, b.db, b.dW2, b.db2 = dw1.ptr, db1.ptr, dw2.ptr, db2.ptr
+        b.dx = None if dx is None else dx.ptr
+        b.lddx = K
+        b.beta_w, b.beta_x = beta_w, beta_x
+        dev.call("ttrl_linear_backward", C.byref(b))
+
+    out._backward = _backward
+    return out

@@ -4,7 +4,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-from ttrl_amd.engine.nn import Module, ModuleList
+from ttrl_amd.engine.nn import Module, ModuleDict, ModuleList
 from ttrl_amd.engine.ops import concat
 
 
@@ -25,6 +25,28 @@ class EncoderHead(Module):
 
     def forward(self, obs):
         return self.head(self.encoder(_actor(obs)))
+
+
+class ActorCritic(Module):
+    """Actor trunk, critic trunk, policy head, value head
+    (ttrl/nets/models.py:42-71).  Parameters are named `encoders.actor.*`
+    and `heads.policy.*`; one trunk in both slots is the shared-trunk case,
+    run once, whose gradient is the sum of the two heads'.
+    `forward(obs) -> (policy_out, value)`."""
+
+    def __init__(self, actor, critic, policy, value):
+        self.encoders = ModuleDict({"actor": actor, "critic": critic})
+        self.heads = ModuleDict({"policy": policy, "value": value})
+
+    @property
+    def shared_trunk(self) -> bool:
+        return self.encoders["actor"] is self.encoders["critic"]
+
+    def forward(self, obs):
+        actor, critic = self.encoders["actor"], self.encoders["critic"]
+        features = actor(_actor(obs))
+        critic_features = features if critic is actor else critic(_critic(obs))
+        return self.heads["policy"](features), self.heads["value"](critic_features)
 
 
 class ConcatEncoder(Module):

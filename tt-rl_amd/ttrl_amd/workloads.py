@@ -50,6 +50,29 @@ def sac_batch(seed: int, batch: int = 256, obs_dim: int = 11, act_dim: int = 3, 
     }
 
 
+def ppo_rollout(seed: int, n_steps: int = 128, n_envs: int = 8, num_actions: int = 18,
+                frame_shape=(4, 84, 84)) -> dict:
+    """One synthetic PPO rollout, time-major [T, N]: uint8 frames uniform
+    0..255, actions uniform, rewards in {-1, 0, 1} w.p. 0.05/0.9/0.05,
+    dones Bernoulli(0.01), values and last values N(0, 1), and the behaviour
+    policy's log-probs of the actions under random logits."""
+    rng = np.random.default_rng(seed)
+    T, N = n_steps, n_envs
+    logits = rng.standard_normal((T, N, num_actions))
+    actions = rng.integers(0, num_actions, (T, N))
+    lse = np.log(np.exp(logits - logits.max(-1, keepdims=True)).sum(-1)) + logits.max(-1)
+    logp = np.take_along_axis(logits, actions[..., None], -1)[..., 0] - lse
+    return {
+        "obs": rng.integers(0, 256, (T, N) + tuple(frame_shape), dtype=np.uint8),
+        "actions": actions,
+        "rewards": rng.choice(np.array([-1.0, 0.0, 1.0], np.float32), (T, N), p=[0.05, 0.9, 0.05]),
+        "dones": (rng.random((T, N)) < 0.01).astype(np.float32),
+        "values": rng.standard_normal((T, N)).astype(np.float32),
+        "logp": logp.astype(np.float32),
+        "last_values": rng.standard_normal(N).astype(np.float32),
+    }
+
+
 def _he(rng, shape, fan_in):
     bound = np.sqrt(6.0 / fan_in)
     return rng.uniform(-bound, bound, shape).astype(np.float32)
