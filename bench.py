@@ -169,6 +169,82 @@ def bench_ppo(dev, updates=5, mode="graph"):
     return out
 
 
+def bench_replay(dev, reps=200, cpu=True):
+    """One batch of 32 sampled from the GPU-resident replay of 8 lanes of
+    uint8 4x84x84 frames (n-step 3), assembled into a learner's input
+    buffers: prioritized at 1M transitions (28 GB of frames in HBM), uniform
+    at 100k.  Times the whole sample call (host generator draws, the lane-sum
+    read of a prioritized draw, the uploads, the pick, the IS weights, the
+    n-step assembly)."""
+    import gc
+
+    from ttrl_amd.buffers import PriorityConfig, ReplayBuffer
+    from ttrl_amd.engine.tensor import DeviceArray
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+
+    spec, lanes, batch = ObsSpec.image((4, 84, 84)), 8, 32
+    rng = np.random.default_rng(7)
+    steps_per_call = 512
+    frames = rng.integers(0, 256, (steps_per_call, lanes, 4, 84, 84), dtype=np.uint8)
+    out = {}
+    sink = {"obs": DeviceArray(dev, (batch, 4, 84, 84), np.uint8), "next_obs": DeviceArray(dev, (batch, 4, 84, 84),
+            np.uint8), "actions_onehot": DeviceArray(dev, (batch, 6)), "rewards": DeviceArray(dev, (batch, 1)),
+            "dones": DeviceArray(dev, (batch, 1)), "discounts": DeviceArray(dev, (batch, 1)),
+            "weights": DeviceArray(dev, (batch, 1))}
+    for name, capacity, prio in (("prioritized", 1_000_000, PriorityConfig()), ("uniform", 100_000, None)):
+        buf = ReplayBuffer(spec, ActionSpec.discrete(6), dev, capacity=capacity, n_envs=lanes, n_step=3,
+                           gamma=0.99, seed=0, priority=prio)
+        t0 = time.perf_counter()
+        for _ in range(buf.per_lane_capacity // steps_per_call + 1):
+            buf.add_steps(frames, rng.integers(0, 6, (steps_per_call, lanes)),
+                          rng.standard_normal((steps_per_call, lanes)).astype(np.float32),
+                          np.zeros((steps_per_call, lanes), bool))
+        if prio is not None:
+            cols = np.arange(buf.per_lane_capacity)
+            for lane in range(lanes):
+                for c0 in range(0, cols.size, 1024):
+                    cc = cols[c0:c0 + 1024]
+                    buf.update_priorities(np.full(cc.size, lane), cc, rng.exponential(1.0, cc.size))
+        dev.synchronize()
+        fill_s = time.perf_counter() - t0
+        beta = 0.4 if prio is not None else None
+        for _ in range(10):
+            buf.sample(batch, beta=beta, out=sink)
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            buf.sample(batch, beta=beta, out=sink)
+        dev.synchronize()
+        us = (time.perf_counter() - t0) / reps * 1e6
+        out[name] = {"capacity": buf.capacity, "us_per_sample": round(us, 2), "fill_seconds": round(fill_s, 2)}
+        del buf
+        gc.collect()
+    if cpu:
+        out["cpu_prioritized_draw"] = cpu_replay_draw(1_000_000, lanes, batch)
+    return out
+
+
+def cpu_replay_draw(capacity, lanes, batch, seconds=3.0):
+    """The oracle's restatement of the reference's host prioritized draw
+    (per-lane cumsum + searchsorted over float64 priorities) and n-step
+    assembly, at the same capacity, with one-byte observations so the time is
+    the draw's."""
+    from oracle.replay import ReplayOracle
+
+    o = ReplayOracle((1,), np.uint8, capacity=capacity, n_envs=lanes, n_step=3, seed=0, alpha=0.6)
+    o.pos[:] = 0
+    o.full[:] = True
+    o.weight[:] = (np.random.default_rng(1).exponential(1.0, o.weight.shape) + 1e-6) ** 0.6
+    o.sample(batch, beta=0.4)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n < 3:
+        o.sample(batch, beta=0.4)
+        n += 1
+    ms = (time.perf_counter() - t0) / n * 1e3
+    return {"capacity": o.cols * lanes, "ms_per_sample": round(ms, 3), "kind": "port",
+            "sample": f"{n} prioritized draws of {batch} from the float64 numpy oracle"}
+
+
 def dominant_kernel(dev, learner, reps=200):
     """The longest kernel of the DQN update: the conv1 forward of the three
     Q evaluations in one launch (online(s), online(s'), target(s'); uint8
@@ -329,6 +405,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--act-steps", type=int, default=500, help="acting steps timed per lane count (0: skip)")
     ap.add_argument("--ppo-updates", type=int, default=5, help="PPO updates timed (0: skip)")
+    ap.add_argument("--replay-reps", type=int, default=200, help="replay samples timed (0: skip)")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
                     help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -352,6 +429,7 @@ def main() -> int:
     dom = dominant_kernel(dev, dqn)
     achieved = dom["flops"] / dom["seconds"]
     ppo = bench_ppo(dev, args.ppo_updates, args.mode) if args.ppo_updates > 0 else None
+    replay = bench_replay(dev, args.replay_reps, not args.no_cpu_baseline) if args.replay_reps > 0 else None
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
@@ -386,6 +464,7 @@ def main() -> int:
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},
         "ppo": ppo,
+        "replay": replay,
         "act": act,
         "cpu_baseline": cpu,
     }

@@ -380,6 +380,78 @@ int ttrl_gaussian_act(ttrl_ctx* ctx, int B, int K, int d, const float* h, const 
                       const float* noise, const float* centre, const float* half_width, float log_det,
                       int deterministic, float* head_out, float* action, float* logp);
 
+/* ---- GPU-resident replay -------------------------------------------------- */
+
+/* One replay ring in device memory (ttrl/buffers/replay.py:62-129): per lane
+ * `cols` columns; column i holds the state its action was taken from.  One
+ * observation leaf of obs_bytes bytes (a multiple of 4).  final_slot[l][c]
+ * names the row of final_obs holding the episode-final observation of an
+ * ending column (the boundary table of ttrl/buffers/boundaries.py), or -1.
+ * weight (NULL for a uniform ring) holds (p + epsilon) ** alpha per column
+ * and *max_priority the largest raw priority seen, both float64
+ * (ttrl/buffers/sampling.py:111-133). */
+typedef struct ttrl_replay_ring {
+  int lanes, cols;
+  long obs_bytes;
+  unsigned char* obs;        /* [lanes][cols][obs_bytes] */
+  int* actions;              /* [lanes][cols] */
+  float* rewards;            /* [lanes][cols] */
+  unsigned char* dones;      /* [lanes][cols] terminated */
+  unsigned char* ends;       /* [lanes][cols] terminated or truncated */
+  int* final_slot;           /* [lanes][cols] */
+  unsigned char* final_obs;  /* [final_rows][obs_bytes] */
+  int final_rows;
+  double* weight;            /* [lanes][cols] or NULL */
+  double* max_priority;      /* device scalar or NULL */
+  double alpha, epsilon;
+} ttrl_replay_ring;
+
+/* Write n transitions, entry e into (lane[e], col[e]): obs row e of obs
+ * ([n][obs_bytes]), action, reward, terminated and ended flags, and for an
+ * ending entry (final_row[e] >= 0) row e of final_obs into that boundary
+ * row; a prioritized ring gives the column the weight (max priority + eps)
+ * ** alpha.  Replaces ReplayBuffer._write_slot (ttrl/buffers/replay.py:178-199)
+ * and PrioritySampler.on_write (ttrl/buffers/sampling.py:130-133).  All
+ * arrays are device arrays. */
+int ttrl_replay_write(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
+                      const int* action, const float* reward, const unsigned char* terminated,
+                      const unsigned char* ended, const int* final_row, const void* obs, const void* final_obs);
+/* Per-lane sums of the priority weights over each lane's sampleable run
+ * (start[l], count[l] in ring order), as chunk sums of `chunk` run positions
+ * ([lanes][max_chunks]) and their ordered totals sums[lanes]
+ * (PrioritySampler.draw's lane sums, ttrl/buffers/sampling.py:135-166). */
+int ttrl_replay_lane_sums(ttrl_ctx* ctx, const ttrl_replay_ring* ring, const int* start, const int* count, int chunk,
+                          int max_chunks, double* chunk_sums, double* sums);
+/* For sample b in lane[b] with uniform u[b]: the run position where the
+ * cumulative weight first exceeds u[b] * sums[lane] (searchsorted 'right',
+ * capped at the run's end, ttrl/buffers/sampling.py:216-222); writes the
+ * ring column and that column's weight. */
+int ttrl_replay_priority_pick(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const double* u,
+                              const int* start, const int* count, int chunk, int max_chunks,
+                              const double* chunk_sums, const double* sums, int* cols_out, double* picked_weight);
+/* Importance-sampling weights (N * P) ** -beta over the batch maximum, P =
+ * picked weight / sum of the lane sums, N = total_count sampleable
+ * transitions (ttrl/buffers/sampling.py:225-236), as float32. */
+int ttrl_replay_is_weights(ttrl_ctx* ctx, int n, const double* picked_weight, const double* sums, int lanes,
+                           long total_count, double beta, float* weights_out);
+/* The batch rows of the transitions at (lane[b], col[b]): the n-step return
+ * in float64 cast to float32, terminated flag and gamma ** steps
+ * (ttrl/buffers/indexing.py:94-131), the observation and the successor (the
+ * next column, or the boundary row of an ending column), the action as an
+ * index and/or one-hot row (ttrl/buffers/replaybatch.py:15-76).  Output
+ * pointers may be a learner's bound input buffers. */
+int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
+                         int n_step, double gamma, void* obs_out, void* next_obs_out, float* actions_onehot,
+                         int num_actions, int* actions_out, float* rewards_out, float* dones_out,
+                         float* discounts_out);
+/* weight[lane[b]][col[b]] = (|priorities[b]| + eps) ** alpha, the last of
+ * duplicate columns winning, and *max_priority = max(*max_priority,
+ * max |priorities|) (PrioritySampler.update, ttrl/buffers/sampling.py:168-193).
+ * priorities is a device array, e.g. the TD errors an update left on the
+ * device. */
+int ttrl_replay_update_priorities(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
+                                  const float* priorities);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,17 @@ class LinearDesc(C.Structure):
     ]
 
 
+class ReplayRing(C.Structure):
+    """Mirror of ttrl_replay_ring."""
+
+    _fields_ = [
+        ("lanes", C.c_int), ("cols", C.c_int), ("obs_bytes", C.c_long),
+        ("obs", C.c_void_p), ("actions", C.c_void_p), ("rewards", C.c_void_p), ("dones", C.c_void_p),
+        ("ends", C.c_void_p), ("final_slot", C.c_void_p), ("final_obs", C.c_void_p), ("final_rows", C.c_int),
+        ("weight", C.c_void_p), ("max_priority", C.c_void_p), ("alpha", C.c_double), ("epsilon", C.c_double),
+    ]
+
+
 class ConvGeom(C.Structure):
     """Mirror of ttrl_conv_geom."""
 
@@ -110,6 +121,12 @@ SIGNATURES = {
     "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
     "ttrl_q_act": ([P, I, I, I, P, P, P, P, P], I),
+    "ttrl_replay_write": ([P, C.POINTER(ReplayRing), I, P, P, P, P, P, P, P, P, P], I),
+    "ttrl_replay_lane_sums": ([P, C.POINTER(ReplayRing), P, P, I, I, P, P], I),
+    "ttrl_replay_priority_pick": ([P, C.POINTER(ReplayRing), I, P, P, P, P, I, I, P, P, P, P], I),
+    "ttrl_replay_is_weights": ([P, I, P, P, I, C.c_long, C.c_double, P], I),
+    "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P], I),
+    "ttrl_replay_update_priorities": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),
     "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),
     "ttrl_sac_critic_loss": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),

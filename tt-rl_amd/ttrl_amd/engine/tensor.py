@@ -27,7 +27,7 @@ __all__ = [
 ]
 
 MASTER_DTYPE = np.float32
-_DTYPES = (np.dtype(np.float32), np.dtype(np.uint8), np.dtype(np.int32))
+_DTYPES = (np.dtype(np.float32), np.dtype(np.uint8), np.dtype(np.int32), np.dtype(np.float64))
 
 #: Parameters start on 256-byte boundaries inside an arena, so weight rows,
 #: vector loads and the Adam kernel's float4 accesses stay aligned.
