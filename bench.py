@@ -324,6 +324,19 @@ def bench_act(dev, dqn, sac, steps=500, lanes_dqn=(1, 8, 16, 32), lanes_sac=(1, 
             dqn._acting.decide(frames[i % 8])
         dt = time.perf_counter() - t0
         out["dqn"].append({"lanes": lanes, "steps_per_s": round(steps / dt, 1), "us_per_step": round(dt / steps * 1e6, 2)})
+    # Config 1 on the GPU: the batch-32 Q-network forward with its frames
+    # resident in HBM (the acting graph at 32 lanes replayed back to back,
+    # no host copies): forwards/s against the FP32 MFMA roofline.
+    fw = dqn._acting._views[32].graphs[False]
+    fw.replay_n(50)
+    dev.synchronize()
+    t0 = time.perf_counter()
+    fw.replay_n(steps * 4)
+    dev.synchronize()
+    dt = (time.perf_counter() - t0) / (steps * 4)
+    flops = 2.0 * 32 * sum(NATURE_MACS)
+    out["dqn_forward_bs32"] = {"forwards_per_s": round(1.0 / dt, 1), "us_per_forward": round(dt * 1e6, 2),
+                               "flops": flops, "roofline_frac": flops / dt / PEAK_FP32_MFMA}
     for lanes in lanes_sac:
         obs = [rng.standard_normal((lanes, 11)).astype(np.float32) for _ in range(8)]
         noise = [rng.standard_normal((lanes, 3)).astype(np.float32) for _ in range(8)]

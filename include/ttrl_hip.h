@@ -380,6 +380,27 @@ int ttrl_gaussian_act(ttrl_ctx* ctx, int B, int K, int d, const float* h, const 
                       const float* noise, const float* centre, const float* half_width, float log_det,
                       int deterministic, float* head_out, float* action, float* logp);
 
+/* ---- GRU unroll ------------------------------------------------------------ */
+
+/* One timestep of a GRU (GRUCell, ttrl/engine/recurrent.py:39-110; gate order
+ * reset, update, candidate): gi and gh are the [B][3H] projections x W_ih +
+ * b_ih and hin W_hh + b_hh; writes hout = (1 - z) * n + z * hin and, when
+ * hin_next is given, hin_next = hout * (1 - done_next) (done_next [B] may be
+ * NULL: no reset), the state entering the next step (GRU.forward's
+ * apply_done_mask, ttrl/engine/recurrent.py:144-168). */
+int ttrl_gru_step(ttrl_ctx* ctx, int B, int H, const float* gi, const float* gh, const float* hin, float* hout,
+                  const float* done_next, float* hin_next);
+/* out = h * (1 - done) per row (done NULL: a copy): the reset of the initial
+ * state (apply_done_mask, ttrl/engine/ops/functional.py:40-46). */
+int ttrl_gru_mask(ttrl_ctx* ctx, int B, int H, const float* h, const float* done, float* out);
+/* Backward of ttrl_gru_step: with dh = dout + (1 - done_next) * dhin_next
+ * (either term may be NULL), writes the gate gradients dgi, dgh ([B][3H])
+ * and dhin = z * dh, the direct part of the gradient of hin (a GEMM adds
+ * dgh W_hh^T). */
+int ttrl_gru_step_backward(ttrl_ctx* ctx, int B, int H, const float* gi, const float* gh, const float* hin,
+                           const float* dout, const float* dhin_next, const float* done_next, float* dgi, float* dgh,
+                           float* dhin);
+
 /* ---- GPU-resident replay -------------------------------------------------- */
 
 /* One replay ring in device memory (ttrl/buffers/replay.py:62-129): per lane

@@ -121,6 +121,9 @@ SIGNATURES = {
     "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
     "ttrl_q_act": ([P, I, I, I, P, P, P, P, P], I),
+    "ttrl_gru_step": ([P, I, I, P, P, P, P, P, P], I),
+    "ttrl_gru_mask": ([P, I, I, P, P, P], I),
+    "ttrl_gru_step_backward": ([P, I, I, P, P, P, P, P, P, P, P, P], I),
     "ttrl_replay_write": ([P, C.POINTER(ReplayRing), I, P, P, P, P, P, P, P, P, P], I),
     "ttrl_replay_lane_sums": ([P, C.POINTER(ReplayRing), P, P, I, I, P, P], I),
     "ttrl_replay_priority_pick": ([P, C.POINTER(ReplayRing), I, P, P, P, P, I, I, P, P, P, P], I),

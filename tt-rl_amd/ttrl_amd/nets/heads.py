@@ -119,6 +119,8 @@ def packed_linear_pair(first: Linear, second: Linear, x: Tensor, *, clamp=None, 
         b.lddx = K
         b.beta_w, b.beta_x = beta_w, beta_x
         dev.call("ttrl_linear_backward", C.byref(b))
+        if dx is not None:
+            x._note_write(beta_x, False)
 
     out._backward = _backward
     return out
