@@ -19,6 +19,14 @@ clip_grad_norm       ttrl/algos/grads.py:13-43 (float64 norm, scale
 minibatch_indices    RolloutBuffer.minibatches' shuffle (ttrl/buffers/rollout.py:239-282):
                      valid rows only, one rng.permutation per epoch, trailing
                      partial minibatch dropped
+sequence_minibatches ttrl/buffers/seqbatch.py:40-120: whole sequences over
+                     (chunk, lane), one permutation per epoch, rows
+                     time-major (t * n_seq + sequence)
+recurrent_ppo_step   ttrl/algos/ppo/recurrent.py:190-225 with
+                     ttrl/nets/recurrent.py:49-196: trunk, ReLU, GRU unroll
+                     from h0 with the episode-start mask, packed heads, the
+                     objective's masked mean over valid slots, backward, clip,
+                     Adam
 ppo_update           ttrl/algos/ppo/learn.py:46-112 on a shared-trunk
                      actor-critic whose two heads are one Linear of width A+1
                      ([logits | value], ttrl/nets/models.py:65-71): GAE,
@@ -35,7 +43,8 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import adam
-from oracle.nets import qnet_backward, qnet_forward
+from oracle.gru import gru_backward, gru_forward
+from oracle.nets import KINK_BAND, qnet_backward, qnet_forward
 
 
 def gae(rewards, values, dones, last_values, gamma: float, lam: float, valid=None):
@@ -222,3 +231,115 @@ def ppo_update(net, rollout: dict, *, rng, minibatch_size: int, epochs: int, gam
     if keep_grads:
         out["grads"] = kept
     return out
+
+
+def sequence_minibatches(T: int, N: int, seq_len: int, minibatch_size: int, epochs: int, rng) -> list:
+    """-> [(rows (seq_len * n_seq,), h0 rows (n_seq,))] of flat time-major
+    rollout indices (row t * N + lane) per minibatch, in the reference's
+    shuffle order."""
+    S = minibatch_size // seq_len
+    total = (T // seq_len) * N
+    n_full = total // S
+    if n_full == 0:
+        raise ValueError("sequence_minibatches: fewer sequences than one minibatch")
+    out = []
+    steps = np.arange(seq_len)
+    for _ in range(epochs):
+        perm = rng.permutation(total)
+        for start in range(0, n_full * S, S):
+            ids = perm[start:start + S]
+            ch, ln = ids // N, ids % N
+            rows = (ch[None, :] * seq_len + steps[:, None]) * N + ln[None, :]
+            out.append((rows.reshape(-1), ch * N + ln))
+    return out
+
+
+def _relu_gate(z, gates, name):
+    m = z > 0
+    if gates is not None and name in gates:
+        rms = np.sqrt(np.mean(z * z)) if z.size else 0.0
+        near = np.abs(z) <= KINK_BAND * rms
+        m = np.where(near, np.asarray(gates[name], bool).reshape(z.shape), m)
+    return m.astype(np.float64)
+
+
+def recurrent_ppo_step(params: dict, S: list, V: list, t: int, mb: dict, *, seq_len: int, clip_eps: float = 0.1,
+                       value_clip_eps: float = 0.1, value_coef: float = 0.5, entropy_coef: float = 0.01,
+                       max_grad_norm: float = 0.5, lr: float = 2.5e-4, adam_eps: float = 1e-8,
+                       betas=(0.9, 0.999), gates=None) -> dict:
+    """One recurrent minibatch step from parameters
+    params = dict(trunk=QNet(convs, [fc1]), gru=(W_ih, W_hh, b_ih, b_hh),
+    head=(W [H, A + 1], b)) and Adam state S, V (flat in the order trunk,
+    gru, head) with update count t.  mb: obs, actions, old_logp, advantages,
+    returns, values, valid (rows), starts (rows), h0 (n_seq, H).
+    -> dict(params, S, V, metrics, grads)."""
+    trunk, (W_ih, W_hh, b_ih, b_hh), (Wh, bh) = params["trunk"], params["gru"], params["head"]
+    z1, acts = qnet_forward(trunk, mb["obs"], gates=gates)
+    m1 = _relu_gate(z1, gates, "fc0")
+    feat = z1 * m1
+    rows, F = feat.shape
+    n_seq = rows // seq_len
+    H = W_hh.shape[0]
+    starts = np.asarray(mb["starts"], np.float64).reshape(seq_len, n_seq)
+    outs, cache = gru_forward(W_ih, W_hh, b_ih, b_hh, feat.reshape(seq_len, n_seq, F), mb["h0"], starts)
+    state = outs.reshape(rows, H)
+    out = state @ Wh + bh.reshape(1, -1)
+    A = out.shape[1] - 1
+    valid = np.asarray(mb["valid"], np.float64).reshape(-1)
+    keep = valid > 0
+    old_logp = np.where(keep, np.asarray(mb["old_logp"], np.float64).reshape(-1), 0.0)
+    o = ppo_objective(out[:, :A], mb["actions"], old_logp, np.where(keep, mb["advantages"], 0.0),
+                      np.where(keep, mb["returns"], 0.0), mb["values"], out[:, A], valid, clip_eps=clip_eps,
+                      value_clip_eps=value_clip_eps, value_coef=value_coef, entropy_coef=entropy_coef)
+    dout = np.concatenate([o["dlogits"], o["dvalues"][:, None]], axis=1)
+    dWh, dbh = state.T @ dout, dout.sum(axis=0)
+    dstate = dout @ Wh.T
+    dseq, _dh0, dW_ih, dW_hh, db_ih, db_hh = gru_backward(cache, dstate.reshape(seq_len, n_seq, H))
+    dfeat = dseq.reshape(rows, F) * m1
+    grads = qnet_backward(trunk, acts, dfeat) + [dW_ih, dW_hh, db_ih, db_hh, dWh, dbh]
+    norm = float(np.sqrt(sum(np.sum(g * g) for g in grads)))
+    if norm > max_grad_norm:
+        grads = [g * (max_grad_norm / (norm + 1e-6)) for g in grads]
+    flat = trunk.flat() + [W_ih, W_hh, b_ih, b_hh, Wh, bh]
+    new, S2, V2 = [], [], []
+    for p, g, s_, v_ in zip(flat, grads, S, V):
+        p2, s2, v2 = adam.fused_step(p, g, s_, v_, t, lr, betas[0], betas[1], adam_eps)
+        new.append(p2)
+        S2.append(s2)
+        V2.append(v2)
+    nt = len(trunk.flat())
+    logratio = o["new_logp"] - old_logp
+    metrics = dict(loss=o["loss"], policy_loss=o["policy_loss"], value_loss=o["value_loss"], entropy=o["entropy"],
+                   approx_kl=float(np.mean(np.expm1(logratio) - logratio)), grad_norm=norm)
+    return dict(params=dict(trunk=trunk.with_flat(new[:nt]), gru=tuple(new[nt:nt + 4]), head=tuple(new[nt + 4:])),
+                S=S2, V=V2, metrics=metrics, grads=grads)
+
+
+def recurrent_ppo_update(params: dict, rollout: dict, *, rng, minibatch_size: int, epochs: int, seq_len: int,
+                         gamma: float = 0.99, lam: float = 0.95, **step_cfg) -> dict:
+    """-> dict(params, steps, batches): the whole recurrent update."""
+    rewards = np.asarray(rollout["rewards"], np.float32)
+    T, N = rewards.shape
+    valid = rollout.get("valid")
+    valid = np.ones((T, N), np.float32) if valid is None else np.asarray(valid, np.float32)
+    adv, ret = gae(rewards, rollout["values"], rollout["dones"], rollout["last_values"], gamma, lam, valid)
+    adv_n, _, _ = normalize_advantages(adv, valid)
+    flat = dict(obs=np.asarray(rollout["obs"]).reshape((T * N,) + np.shape(rollout["obs"])[2:]),
+                actions=np.asarray(rollout["actions"]).reshape(-1),
+                old_logp=np.asarray(rollout["logp"], np.float64).reshape(-1),
+                advantages=np.asarray(adv_n, np.float64).reshape(-1), returns=np.asarray(ret, np.float64).reshape(-1),
+                values=np.asarray(rollout["values"], np.float64).reshape(-1), valid=valid.reshape(-1),
+                starts=np.asarray(rollout["starts"], np.float64).reshape(-1))
+    hidden = np.asarray(rollout["hidden"], np.float64).reshape(-1, np.shape(rollout["hidden"])[-1])
+    flat_params = params["trunk"].flat() + list(params["gru"]) + list(params["head"])
+    S = [np.zeros(np.shape(p)) for p in flat_params]
+    V = [np.zeros(np.shape(p)) for p in flat_params]
+    steps, batches = [], []
+    for t, (rows, h0_rows) in enumerate(sequence_minibatches(T, N, seq_len, minibatch_size, epochs, rng), start=1):
+        mb = {k: v[rows] for k, v in flat.items()}
+        mb["h0"] = hidden[h0_rows]
+        r = recurrent_ppo_step(params, S, V, t, mb, seq_len=seq_len, **step_cfg)
+        params, S, V = r["params"], r["S"], r["V"]
+        steps.append(r["metrics"])
+        batches.append(mb)
+    return dict(params=params, steps=steps, batches=batches)

@@ -129,3 +129,122 @@ def test_ppo_update_oracle_matches_torch(max_grad_norm):
     assert all(clipped) if max_grad_norm < 1 else not any(clipped)
     for got, want in zip(res["net"].flat(), want_params):
         assert np.allclose(got, want, rtol=1e-9, atol=1e-12)
+
+
+def test_sequence_minibatches_follow_the_reference_rule():
+    """Whole sequences over (chunk, lane), one permutation per epoch, rows
+    time-major (ttrl/buffers/seqbatch.py:52-76, ttrl/buffers/sequences.py:121-155)."""
+    from oracle.ppo import sequence_minibatches
+
+    T, N, L, mb = 8, 3, 4, 8
+    got = sequence_minibatches(T, N, L, mb, 2, np.random.default_rng(1))
+    rng = np.random.default_rng(1)
+    total, S = (T // L) * N, mb // L
+    k = 0
+    for _ in range(2):
+        perm = rng.permutation(total)
+        for start in range(0, (total // S) * S, S):
+            ids = perm[start:start + S]
+            rows, h0 = got[k]
+            k += 1
+            for s, i in enumerate(ids):
+                chunk, lane = divmod(int(i), N)
+                assert h0[s] == chunk * N + lane
+                for t in range(L):
+                    assert rows[t * S + s] == (chunk * L + t) * N + lane  # one lane, consecutive steps
+    assert k == len(got) == 2 * (total // S)
+
+
+def test_recurrent_ppo_oracle_matches_torch():
+    import torch
+
+    from oracle.ppo import gae, normalize_advantages, recurrent_ppo_update, sequence_minibatches
+
+    torch.set_default_dtype(torch.float64)
+    rng = np.random.default_rng(21)
+    A, T, N, L, Hd, mb = 4, 8, 2, 4, 6, 8
+    base = _small_net(rng, 16 - 1)  # convs and fc1 (72 -> 16); the head below replaces its last layer
+    from oracle.nets import QNet
+    trunk = QNet(base.convs, [base.fcs[0]], base.scale)
+    u = lambda *s: rng.uniform(-0.4, 0.4, s)
+    gru = (u(16, 3 * Hd), u(Hd, 3 * Hd), u(3 * Hd), u(3 * Hd))
+    head = (u(Hd, A + 1), u(A + 1))
+    rollout = {
+        "obs": rng.integers(0, 256, (T, N, 4, 12, 12), dtype=np.uint8),
+        "actions": rng.integers(0, A, (T, N)),
+        "rewards": rng.choice([-1.0, 0.0, 1.0], (T, N)).astype(np.float32),
+        "dones": (rng.random((T, N)) < 0.2).astype(np.float32),
+        "values": rng.standard_normal((T, N)).astype(np.float32),
+        "logp": np.log(rng.uniform(0.1, 0.5, (T, N))).astype(np.float32),
+        "last_values": rng.standard_normal(N).astype(np.float32),
+        "valid": np.ones((T, N), np.float32),
+        "starts": (rng.random((T, N)) < 0.25).astype(np.float32),
+        "hidden": rng.standard_normal((T // L, N, Hd)).astype(np.float32),
+    }
+    rollout["valid"][3, 1] = 0.0
+    cfg = dict(lr=1e-3, adam_eps=1e-8, clip_eps=0.1, value_clip_eps=0.1, value_coef=0.5, entropy_coef=0.01,
+               max_grad_norm=0.05)
+    res = recurrent_ppo_update(dict(trunk=trunk, gru=gru, head=head), rollout, rng=np.random.default_rng(5),
+                               minibatch_size=mb, epochs=2, seq_len=L, **cfg)
+
+    params = [torch.tensor(p, requires_grad=True) for p in trunk.flat() + list(gru) + list(head)]
+    opt = torch.optim.Adam(params, lr=cfg["lr"], eps=cfg["adam_eps"])
+    adv, ret = gae(rollout["rewards"], rollout["values"], rollout["dones"], rollout["last_values"], 0.99, 0.95,
+                   rollout["valid"])
+    adv_n, _, _ = normalize_advantages(adv, rollout["valid"])
+    flat_obs = rollout["obs"].reshape(T * N, 4, 12, 12)
+    hid = rollout["hidden"].reshape(-1, Hd)
+    for step, (rows, h0_rows) in enumerate(sequence_minibatches(T, N, L, mb, 2, np.random.default_rng(5))):
+        w1, b1, w2, b2, f1, fb1, Wi, Wr, bi, br, Wo, bo = params
+        x = torch.tensor(flat_obs[rows], dtype=torch.float64) / 255.0
+        h = torch.relu(torch.nn.functional.conv2d(x, w1, b1, stride=2))
+        h = torch.relu(torch.nn.functional.conv2d(h, w2, b2, stride=1))
+        feat = torch.relu(h.permute(0, 2, 3, 1).reshape(len(rows), -1) @ f1 + fb1)
+        S = mb // L
+        seq = feat.reshape(L, S, -1)
+        starts = torch.tensor(rollout["starts"].reshape(-1)[rows], dtype=torch.float64).reshape(L, S, 1)
+        st = torch.tensor(hid[h0_rows])
+        outs = []
+        for t in range(L):
+            st = st * (1 - starts[t])
+            gi, gh = seq[t] @ Wi + bi, st @ Wr + br
+            r = torch.sigmoid(gi[:, :Hd] + gh[:, :Hd])
+            z = torch.sigmoid(gi[:, Hd:2 * Hd] + gh[:, Hd:2 * Hd])
+            n = torch.tanh(gi[:, 2 * Hd:] + r * gh[:, 2 * Hd:])
+            st = (1 - z) * n + z * st
+            outs.append(st)
+        out = torch.stack(outs).reshape(L * S, Hd) @ Wo + bo
+        logits, value = out[:, :A], out[:, A]
+        valid = torch.tensor(rollout["valid"].reshape(-1)[rows], dtype=torch.float64)
+        keep = valid > 0
+        old = torch.where(keep, torch.tensor(rollout["logp"].reshape(-1)[rows], dtype=torch.float64), 0.0)
+        a_ = torch.tensor(adv_n.reshape(-1)[rows])
+        R = torch.tensor(np.asarray(ret, np.float64).reshape(-1)[rows])
+        a_, R = torch.where(keep, a_, 0.0), torch.where(keep, R, 0.0)
+        ov = torch.tensor(rollout["values"].reshape(-1)[rows], dtype=torch.float64)
+        logp_all = torch.log_softmax(logits, dim=-1)
+        new_logp = logp_all.gather(1, torch.tensor(rollout["actions"].reshape(-1)[rows])[:, None])[:, 0]
+        ratio = torch.exp(new_logp - old)
+        surr = torch.minimum(ratio * a_, torch.clamp(ratio, 0.9, 1.1) * a_)
+        total = valid.sum()
+        pol = -(surr * valid).sum() / total
+        clipped = ov + torch.clamp(value - ov, -0.1, 0.1)
+        vl = 0.5 * (torch.maximum((value - R) ** 2, (clipped - R) ** 2) * valid).sum() / total
+        ent = ((-(logp_all.exp() * logp_all).sum(1)) * valid).sum() / total
+        loss = pol + 0.5 * vl - 0.01 * ent
+        opt.zero_grad()
+        loss.backward()
+        norm = float(torch.sqrt(sum((p.grad ** 2).sum() for p in params)))
+        if norm > cfg["max_grad_norm"]:
+            for p in params:
+                p.grad *= cfg["max_grad_norm"] / (norm + 1e-6)
+        opt.step()
+        got = res["steps"][step]
+        assert got["loss"] == pytest.approx(loss.item(), rel=1e-9, abs=1e-12)
+        assert got["grad_norm"] == pytest.approx(norm, rel=1e-9)
+        lr_ = new_logp.detach().numpy() - old.numpy()
+        assert got["approx_kl"] == pytest.approx(float(np.mean(np.expm1(lr_) - lr_)), rel=1e-9, abs=1e-12)
+    want = [p.detach().numpy() for p in params]
+    flat = res["params"]["trunk"].flat() + list(res["params"]["gru"]) + list(res["params"]["head"])
+    for g, w in zip(flat, want):
+        assert np.allclose(g, w, rtol=1e-9, atol=1e-12)

@@ -159,6 +159,24 @@ __global__ __launch_bounds__(kRedThreads) void k_ppo_loss(
   for (int i = threadIdx.x; i < B; i += kRedThreads) {
     const float* z = logits + long(i) * cfg.ldz;
     const float w = valid ? valid[i] : 1.f;
+    if (!(w > 0.f)) {
+      // An excluded slot (autoreset padding of a recurrent minibatch): no
+      // loss term and no gradient; its old log-prob counts as 0 in the
+      // approximate KL, as the reference zeroes the field before the
+      // forward (ttrl/algos/ppo/recurrent.py:214-224).
+      float mx = z[0];
+      for (int j = 1; j < A; ++j) mx = fmaxf(mx, z[j]);
+      float se = 0.f;
+      for (int j = 0; j < A; ++j) se += expf(z[j] - mx);
+      const int a = actions[i];
+      const float lp = (a >= 0 && a < A) ? (z[a] - mx) - logf(se) : 0.f;
+      new_logp[i] = lp;
+      s_kl += expm1f(lp) - lp;
+      float* dz0 = dlogits + long(i) * cfg.ldz;
+      for (int j = 0; j < A; ++j) dz0[j] = 0.f;
+      dvalue[long(i) * cfg.ldv] = 0.f;
+      continue;
+    }
     float mx = z[0];
     for (int j = 1; j < A; ++j) mx = fmaxf(mx, z[j]);
     float se = 0.f;

@@ -151,7 +151,8 @@ def objective(policy_out: Tensor, value: Tensor, batch, cfg: PPOLossConfig, vali
     return loss, parts, Tensor(new_logp)
 
 
-def objective_packed(head: Tensor, mb: dict, cfg, out5: DeviceArray, new_logp: DeviceArray) -> Tensor:
+def objective_packed(head: Tensor, mb: dict, cfg, out5: DeviceArray, new_logp: DeviceArray,
+                     valid: DeviceArray | None = None) -> Tensor:
     """The objective over the fused head's packed [logits | value] rows, as
     one tape node (ttrl/algos/ppo/loss.py:42-83).  `mb` holds the minibatch's
     device arrays `actions` (int32), `old_logp`, `advantages`, `returns`,
@@ -163,7 +164,8 @@ def objective_packed(head: Tensor, mb: dict, cfg, out5: DeviceArray, new_logp: D
     A = N - 1
     dhead = DeviceArray(dev, (B, N))
     dev.call("ttrl_ppo_loss_packed", B, A, head.data.vp, mb["actions"].vp, mb["old_logp"].vp,
-             mb["advantages"].vp, mb["returns"].vp, mb["values"].vp, None, C.c_float(cfg.clip_eps),
+             mb["advantages"].vp, mb["returns"].vp, mb["values"].vp, None if valid is None else valid.vp,
+             C.c_float(cfg.clip_eps),
              C.c_float(cfg.value_clip_eps), C.c_float(cfg.value_coef), C.c_float(cfg.entropy_coef), out5.vp,
              new_logp.vp, dhead.vp)
     loss_arr = out5.view(0, (1, 1))
@@ -210,6 +212,20 @@ def clip_grad_norm(params, max_norm: float) -> float:
 # ------------------------------------------------------------ the learner ---
 
 @dataclass(frozen=True)
+class RecurrentConfig:
+    """The memory's settings (ttrl/algos/ppo/config.py:21-65)."""
+
+    hidden_size: int = 128
+    seq_len: int = 16
+
+    def __post_init__(self):
+        if self.hidden_size < 1:
+            raise ValueError(f"RecurrentConfig: hidden_size must be >= 1, got {self.hidden_size}")
+        if self.seq_len < 2:
+            raise ValueError(f"RecurrentConfig: seq_len must be >= 2, got {self.seq_len}")
+
+
+@dataclass(frozen=True)
 class PPOConfig:
     """Learner-side fields of ttrl/algos/ppo/config.py:67-120, plus the Adam
     epsilon (the engine default 1e-8, ttrl/algos/ppo/agent.py:81)."""
@@ -231,10 +247,15 @@ class PPOConfig:
     total_frames: int | None = None
     step_mode: str = "graph"
     encoder: str = "auto"
+    recurrent: RecurrentConfig | None = None
 
     def __post_init__(self):
         if self.lr <= 0 or self.adam_eps <= 0:
             raise ValueError("PPOConfig: lr and adam_eps must be > 0")
+        if self.recurrent is not None and self.minibatch_size % self.recurrent.seq_len:
+            raise ValueError(f"PPOConfig: minibatch_size={self.minibatch_size} is not a multiple of "
+                             f"seq_len={self.recurrent.seq_len}; a recurrent minibatch is a whole number of "
+                             f"sequences")
         if not 0.0 < self.gamma <= 1.0 or not 0.0 <= self.lam <= 1.0:
             raise ValueError(f"PPOConfig: need 0 < gamma <= 1 and 0 <= lam <= 1, got {self.gamma}, {self.lam}")
         if self.n_steps < 1 or self.minibatch_size < 1 or self.epochs < 1:
@@ -255,11 +276,12 @@ class _Resident:
     (row t * N + n, the reference's reshape order), with the shuffled index
     table of every minibatch of one update and the per-step metric ring."""
 
-    def __init__(self, device, obs_spec, T: int, N: int, cfg: PPOConfig):
+    def __init__(self, device, obs_spec, T: int, N: int, cfg: PPOConfig, extra=(), steps_per_epoch=None):
         rows = T * N
         self.T, self.N, self.rows = T, N, rows
         mb = cfg.minibatch_size
-        self.table_len = cfg.epochs * (rows // mb) * mb
+        per_epoch = rows // mb if steps_per_epoch is None else steps_per_epoch
+        self.table_len = cfg.epochs * per_epoch * mb
         if obs_spec.kind == "image":
             frames = np.zeros((rows,) + tuple(obs_spec.shape), np.uint8)
         else:
@@ -267,13 +289,13 @@ class _Resident:
         z = np.zeros(rows, np.float32)
         specs = [("obs", frames), ("actions", np.zeros(rows, np.int32)), ("logp", z), ("values", z),
                  ("rewards", z), ("dones", z), ("valid", z), ("last_values", np.zeros(N, np.float32)),
-                 ("idx", np.zeros(max(self.table_len, 1), np.int32))]
+                 ("idx", np.zeros(max(self.table_len, 1), np.int32))] + list(extra)
         self.host, self.block = bound_block(device, specs)
         self.image = np.zeros(self.block.nbytes, np.uint8)
         self.advantages = DeviceArray(device, (rows,))
         self.returns = DeviceArray(device, (rows,))
         self.adv_norm = DeviceArray(device, (rows,))
-        self.slots = cfg.epochs * (rows // mb)
+        self.slots = cfg.epochs * per_epoch
         self.ring = DeviceArray(device, (max(self.slots, 1), len(PPOLearner.METRICS)))
 
     def stage(self, name: str, array) -> None:
@@ -305,8 +327,6 @@ class PPOLearner:
     METRICS = ("loss", "policy_loss", "value_loss", "entropy", "approx_kl", "grad_norm")
 
     def __init__(self, obs_spec, action_spec, device, *, cfg: PPOConfig = PPOConfig(), seed: int | None = None):
-        from ttrl_amd.nets.build import build_actor_critic
-
         if action_spec.kind != "discrete":
             raise ValueError(f"PPOLearner supports discrete actions only, got {action_spec.kind!r}")
         self.cfg = cfg
@@ -314,8 +334,7 @@ class PPOLearner:
         self.obs_spec, self.action_spec = obs_spec, action_spec
         if seed is not None:
             np.random.seed(seed)
-        self.net = build_actor_critic(obs_spec, action_spec, device, batch=cfg.minibatch_size,
-                                      encoder=cfg.encoder)
+        self.net = self._build_net()
         self.params = list(self.net.parameters())
         self.optimizer = Adam(self.params, lr=cfg.lr, eps=cfg.adam_eps)
         self._rng = np.random.default_rng(seed)
@@ -329,7 +348,7 @@ class PPOLearner:
         z = np.zeros(mb, np.float32)
         self.mb, self.mb_block = bound_block(device, [
             ("obs", obs), ("actions", np.zeros(mb, np.int32)), ("old_logp", z), ("advantages", z),
-            ("returns", z), ("values", z)])
+            ("returns", z), ("values", z)] + self._mb_extra())
         self._counter = DeviceArray(device, (1,), np.int32)
         self._metrics = DeviceArray(device, (len(self.METRICS),))
         self._sq = DeviceArray(device, (1,))
@@ -337,6 +356,17 @@ class PPOLearner:
         self._res: _Resident | None = None
         self._graph = None
         self._pool = None
+
+    def _build_net(self):
+        from ttrl_amd.nets.build import build_actor_critic
+
+        if self.cfg.recurrent is not None:
+            raise ValueError("PPOLearner: a recurrent config needs RecurrentPPOLearner")
+        return build_actor_critic(self.obs_spec, self.action_spec, self.device, batch=self.cfg.minibatch_size,
+                                  encoder=self.cfg.encoder)
+
+    def _mb_extra(self) -> list:
+        return []
 
     # -- one minibatch step --------------------------------------------------
 
@@ -481,3 +511,132 @@ class PPOLearner:
 
     def close(self) -> None:
         self._release_graph()
+
+
+class RecurrentPPOLearner(PPOLearner):
+    """The recurrent PPO update (ttrl/algos/ppo/learn.py:74-90,
+    ttrl/algos/ppo/recurrent.py:190-225, ttrl/buffers/seqbatch.py:40-120) on
+    a shared trunk with a GRU memory (ttrl/nets/recurrent.py).
+
+    The rollout additionally carries `starts` [T, N] (1 where the step opens
+    an episode: the state entering it is reset) and `hidden` [T / seq_len,
+    N, hidden_size] (the unmasked state entering each sequence's first step).
+    A minibatch is `minibatch_size / seq_len` whole sequences, shuffled as
+    units over (chunk, lane) with one permutation per epoch; rows are
+    time-major (t * n_seq + sequence).  The loss reduces over valid slots;
+    the advantages are normalised over the valid slots of the rollout.  The
+    step graph gathers the rows and the sequences' initial states by index
+    from the resident rollout, runs trunk, unroll and both heads, the
+    objective, backward, clip and Adam.
+    """
+
+    def __init__(self, obs_spec, action_spec, device, *, cfg: PPOConfig, seed: int | None = None):
+        if cfg.recurrent is None:
+            raise ValueError("RecurrentPPOLearner needs cfg.recurrent")
+        self.seq_len = cfg.recurrent.seq_len
+        self.hidden_size = cfg.recurrent.hidden_size
+        self.n_seq = cfg.minibatch_size // self.seq_len
+        super().__init__(obs_spec, action_spec, device, cfg=cfg, seed=seed)
+        self._h0 = Tensor(self.mb["h0"])
+        self._starts = Tensor(self.mb["starts"])
+
+    def _build_net(self):
+        from ttrl_amd.nets.recurrent import build_recurrent_actor_critic
+
+        return build_recurrent_actor_critic(self.obs_spec, self.action_spec, self.device,
+                                            batch=self.cfg.minibatch_size, hidden_size=self.hidden_size,
+                                            encoder=self.cfg.encoder)
+
+    def _mb_extra(self) -> list:
+        mb = self.cfg.minibatch_size
+        return [("valid", np.zeros(mb, np.float32)), ("starts", np.zeros((self.seq_len, self.n_seq, 1), np.float32)),
+                ("h0", np.zeros((self.n_seq, self.hidden_size), np.float32))]
+
+    def _resident(self, T: int, N: int) -> _Resident:
+        r = self._res
+        if r is None or (r.T, r.N) != (T, N):
+            if T % self.seq_len:
+                raise ValueError(f"RecurrentPPOLearner: n_steps={T} is not a multiple of seq_len={self.seq_len}")
+            self._release_graph()
+            chunks = T // self.seq_len
+            per_epoch = (chunks * N) // self.n_seq
+            extra = [("starts", np.zeros(T * N, np.float32)),
+                     ("hidden", np.zeros((chunks * N, self.hidden_size), np.float32)),
+                     ("idx_h0", np.zeros(max(self.cfg.epochs * per_epoch * self.n_seq, 1), np.int32))]
+            self._res = r = _Resident(self.device, self.obs_spec, T, N, self.cfg, extra, per_epoch)
+            r.h0_len = self.cfg.epochs * per_epoch * self.n_seq
+        return r
+
+    def load_rollout(self, rollout: dict) -> int:
+        rewards = np.asarray(rollout["rewards"], np.float32)
+        if rewards.ndim != 2:
+            raise ValueError(f"RecurrentPPOLearner: rollout fields must be time-major [T, N], got {rewards.shape}")
+        T, N = rewards.shape
+        r = self._resident(T, N)
+        cfg, L, S = self.cfg, self.seq_len, self.n_seq
+        chunks = T // L
+        total = chunks * N
+        n_full = total // S
+        if n_full == 0:
+            raise ValueError(f"RecurrentPPOLearner: the rollout holds {total} sequences of {L} steps and a "
+                             f"minibatch of {cfg.minibatch_size} rows wants {S} of them, which would yield zero "
+                             f"minibatches. Lower minibatch_size or seq_len, or collect a longer rollout.")
+        valid = rollout.get("valid")
+        valid = np.ones((T, N), np.float32) if valid is None else np.asarray(valid, np.float32).reshape(T, N)
+        if not (valid > 0).any():
+            raise ValueError("RecurrentPPOLearner: the rollout holds no valid transitions")
+        hidden = np.asarray(rollout["hidden"], np.float32)
+        if hidden.shape != (chunks, N, self.hidden_size):
+            raise ValueError(f"RecurrentPPOLearner: hidden must be ({chunks}, {N}, {self.hidden_size}), "
+                             f"got {hidden.shape}")
+        rows_t = np.zeros(max(r.table_len, 1), np.int32)
+        h0_t = np.zeros(max(r.h0_len, 1), np.int32)
+        steps = np.arange(L)
+        k = 0
+        for _ in range(cfg.epochs):
+            perm = self._rng.permutation(total)
+            for start in range(0, n_full * S, S):
+                ids = perm[start:start + S]
+                ch, ln = ids // N, ids % N
+                # time-major rows: (t, s) -> flat rollout row (ch_s * L + t) * N + ln_s
+                rows = (ch[None, :] * L + steps[:, None]) * N + ln[None, :]
+                rows_t[k * S * L:(k + 1) * S * L] = rows.reshape(-1)
+                h0_t[k * S:(k + 1) * S] = ch * N + ln
+                k += 1
+        batch_valid = valid.reshape(-1)[rows_t[:k * S * L].reshape(k, S * L)]
+        if not np.all(batch_valid.sum(axis=1) > 0):
+            raise ValueError("RecurrentPPOLearner: a sequence minibatch holds no valid transitions")
+        r.stage("obs", np.asarray(rollout["obs"]).reshape((T * N,) + r.host["obs"].shape[1:]))
+        r.stage("actions", np.asarray(rollout["actions"]).reshape(-1).astype(np.int32))
+        for name in ("logp", "values", "rewards", "dones"):
+            r.stage(name, np.asarray(rollout[name], np.float32).reshape(-1))
+        r.stage("valid", valid.reshape(-1))
+        r.stage("starts", np.asarray(rollout["starts"], np.float32).reshape(-1))
+        r.stage("hidden", hidden.reshape(chunks * N, self.hidden_size))
+        r.stage("last_values", np.asarray(rollout["last_values"], np.float32).reshape(-1))
+        r.stage("idx", rows_t)
+        r.stage("idx_h0", h0_t)
+        r.block.upload(r.image)
+        return k
+
+    def _gather(self) -> None:
+        r, mb, dev = self._res, self.mb, self.device
+        n = self.cfg.minibatch_size
+        pairs = [(r.host["obs"], mb["obs"]), (r.host["actions"], mb["actions"]), (r.host["logp"], mb["old_logp"]),
+                 (r.adv_norm, mb["advantages"]), (r.returns, mb["returns"]), (r.host["values"], mb["values"]),
+                 (r.host["valid"], mb["valid"]), (r.host["starts"], mb["starts"])]
+        row_bytes = (C.c_long * len(pairs))(*[d.nbytes // n for _s, d in pairs])
+        dev.call("ttrl_gather_rows", n, len(pairs), _lib.ptrs(s.ptr for s, _ in pairs),
+                 _lib.ptrs(d.ptr for _, d in pairs), row_bytes, C.c_long(r.rows), r.host["idx"].vp,
+                 C.c_long(r.table_len), self._counter.vp, n)
+        h_rows = r.host["hidden"].shape[0]
+        hb = (C.c_long * 1)(self.hidden_size * 4)
+        dev.call("ttrl_gather_rows", self.n_seq, 1, _lib.ptrs([r.host["hidden"].ptr]), _lib.ptrs([mb["h0"].ptr]), hb,
+                 C.c_long(h_rows), r.host["idx_h0"].vp, C.c_long(r.h0_len), self._counter.vp, self.n_seq)
+
+    def _forward_backward(self) -> None:
+        self._gather()
+        head = self.net.forward_packed(Tensor(self.mb["obs"]), self._h0, self._starts, seq_len=self.seq_len)
+        loss = objective_packed(head, self.mb, self.cfg, self._metrics.view(0, (5,)), self._new_logp,
+                                valid=self.mb["valid"])
+        loss.backward()

@@ -73,6 +73,22 @@ def ppo_rollout(seed: int, n_steps: int = 128, n_envs: int = 8, num_actions: int
     }
 
 
+def recurrent_ppo_rollout(seed: int, n_steps: int = 128, n_envs: int = 16, num_actions: int = 18,
+                          seq_len: int = 32, hidden_size: int = 512, frame_shape=(4, 84, 84)) -> dict:
+    """ppo_rollout plus what a recurrent update reads: `starts` [T, N] (the
+    previous step's done shifted by one, the first row from Bernoulli(0.01)
+    carried flags) and `hidden` [T / seq_len, N, hidden] states entering each
+    sequence, N(0, 0.5)."""
+    out = ppo_rollout(seed, n_steps, n_envs, num_actions, frame_shape)
+    rng = np.random.default_rng(seed + 1)
+    starts = np.zeros((n_steps, n_envs), np.float32)
+    starts[0] = (rng.random(n_envs) < 0.01).astype(np.float32)
+    starts[1:] = out["dones"][:-1]
+    out["starts"] = starts
+    out["hidden"] = (0.5 * rng.standard_normal((n_steps // seq_len, n_envs, hidden_size))).astype(np.float32)
+    return out
+
+
 def _he(rng, shape, fan_in):
     bound = np.sqrt(6.0 / fan_in)
     return rng.uniform(-bound, bound, shape).astype(np.float32)
