@@ -245,6 +245,48 @@ def cpu_replay_draw(capacity, lanes, batch, seconds=3.0):
             "sample": f"{n} prioritized draws of {batch} from the float64 numpy oracle"}
 
 
+def rppo_step_flops(rows=512, hidden=512, features=512, actions=18) -> float:
+    """One recurrent PPO minibatch step: the Nature-CNN trunk's forward,
+    weight and input gradients (no input gradient at conv1), the GRU's input
+    projection, recurrent GEMMs and their gradients over all timesteps, and
+    both heads."""
+    trunk = sum(NATURE_MACS[:4])
+    per_row = 2 * trunk + (trunk - NATURE_MACS[0])
+    per_row += 3 * hidden * (3 * features + 3 * hidden) + 3 * hidden * (actions + 1)
+    return 2.0 * rows * per_row
+
+
+def bench_rppo(dev, updates=3, mode="graph"):
+    """Recurrent PPO updates over one resident rollout of 16 envs x 128 steps
+    of uint8 4x84x84 frames: sequences of 32, GRU hidden 512, 4 epochs x 4
+    minibatches of 512 rows (16 sequences), 18 actions."""
+    from ttrl_amd.algos.ppo import PPOConfig, RecurrentConfig, RecurrentPPOLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_qnet_state, recurrent_ppo_rollout
+
+    cfg = PPOConfig(minibatch_size=512, epochs=4, n_steps=128, step_mode=mode,
+                    recurrent=RecurrentConfig(hidden_size=512, seq_len=32))
+    learner = RecurrentPPOLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(18), dev, cfg=cfg, seed=0)
+    learner.net.load_state_dict(he_uniform_qnet_state(learner.net, 6))
+    rollout = recurrent_ppo_rollout(6000, 128, 16, 18, 32, 512)
+    steps = learner.load_rollout(rollout)
+    learner.run_update(steps)
+    dev.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(updates):
+        learner.run_update(steps)
+    dev.synchronize()
+    dt = (time.perf_counter() - t0) / updates
+    flops = rppo_step_flops()
+    out = {"unit": "recurrent PPO minibatch steps/s", "value": round(steps / dt, 2), "rows": 512,
+           "steps_per_update": steps, "ms_per_update": round(dt * 1e3, 3), "ms_per_step": round(dt / steps * 1e3, 4),
+           "flops_per_step": flops, "roofline_frac": flops * steps / dt / PEAK_FP32_MFMA,
+           "workload": "recurrent PPO update: 16 envs x 128 steps of uint8 4x84x84, sequences of 32, "
+                       "Nature-CNN -> 512 -> GRU(512) -> {18, 1}, 4 epochs x 4 minibatches of 16 sequences"}
+    learner.close()
+    return out
+
+
 def dominant_kernel(dev, learner, reps=200):
     """The longest kernel of the DQN update: the conv1 forward of the three
     Q evaluations in one launch (online(s), online(s'), target(s'); uint8
@@ -442,6 +484,7 @@ def main() -> int:
     dom = dominant_kernel(dev, dqn)
     achieved = dom["flops"] / dom["seconds"]
     ppo = bench_ppo(dev, args.ppo_updates, args.mode) if args.ppo_updates > 0 else None
+    rppo = bench_rppo(dev, max(1, args.ppo_updates // 2), args.mode) if args.ppo_updates > 0 else None
     replay = bench_replay(dev, args.replay_reps, not args.no_cpu_baseline) if args.replay_reps > 0 else None
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
@@ -477,6 +520,7 @@ def main() -> int:
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},
         "ppo": ppo,
+        "recurrent_ppo": rppo,
         "replay": replay,
         "act": act,
         "cpu_baseline": cpu,
