@@ -205,7 +205,7 @@ def test_dqn_loss_head_matches_oracle(device):
 
 
 @pytest.mark.parametrize("groups,B,K,A", [(3, 32, 512, 6), (2, 32, 512, 6), (3, 7, 100, 18), (3, 130, 64, 4),
-                                           (3, 32, 512, 12)])
+                                           (3, 32, 512, 12), (3, 64, 700, 5), (2, 200, 256, 32)])
 def test_dqn_head_fused_matches_linear_then_loss(device, groups, B, K, A):
     """ttrl_dqn_head (last linear layer x groups + DQN loss, one launch)
     against float64: q per group, then the loss head on those q (group 1
@@ -232,8 +232,9 @@ def test_dqn_head_fused_matches_linear_then_loss(device, groups, B, K, A):
     outs = {k: DeviceArray(device, s) for k, s in
             (("loss", (1,)), ("mq", (1,)), ("td", (B,)), ("dq", (B, A)), ("na", (B,)), ("y", (B,)))}
     ins = [_dev_arr(device, v) for v in (onehot, r, d, disc, w)]
-    # Twice: the batch means are finished by the last workgroup through a
-    # device counter that each launch must leave at zero for the next.
+    # Twice: above 64 samples the batch means are finished by the last
+    # workgroup through a device counter that each launch must leave at zero
+    # for the next.
     for rep in range(2):
         for o in outs.values():
             o.fill(-7.0)

@@ -101,15 +101,20 @@ __global__ __launch_bounds__(kHeadThreads) void k_dqn_loss(
 // The Q head's last linear layer for the online(s), online(s') and
 // target(s') features (groups 0, 1, 2; two groups for vanilla DQN, where the
 // target both selects and values), then the DQN head above, in one launch.
-// Workgroup j owns samples [j*RB, (j+1)*RB) of every group: per group, W is
-// staged in LDS as [K][AP] rows padded with zeros to AP (8, 16 or 32)
-// actions, so a lane's k-slice reads whole 16-byte chunks with no
-// per-action branch; a wavefront owns one sample row, its lanes split the
-// K-sum, and a butterfly sums the lanes.  Each sample's target, Huber term
-// and dL/dQ need only its own row, so the workgroups never wait on each
-// other; the batch means are summed from per-workgroup partials, in
-// workgroup order, by the workgroup that finishes last (a device-scope
-// counter, reset by that workgroup for the next launch).
+// Workgroup j owns samples [j*RB, (j+1)*RB) of every group (RB <= 64): per
+// group, W is staged in LDS as [K][AP] rows padded with zeros to AP (8, 16
+// or 32) actions, so a lane's k-slice reads whole 16-byte chunks with no
+// per-action branch.  The wavefronts are split evenly over the groups; a
+// wavefront owns every WPG-th sample row of its group and takes RU rows at
+// a time (RU * AP = 32 sums) with all their loads in flight together, its
+// lanes split the K-sum, and a reduce-scatter over the lanes finishes the
+// 32 sums in 32 exchanges.  Each sample's target, Huber term
+// and dL/dQ need only its own row; the batch means are a butterfly over
+// wavefront 0, which holds the workgroup's samples.  A batch of at most 64
+// is one workgroup and writes the means directly; a larger batch sums the
+// per-workgroup partials, in workgroup order, in the workgroup that
+// finishes last (a device-scope counter, reset by that workgroup for the
+// next launch).
 // Range-checked loads: an offset past `bytes` reads zero.  The base and
 // size are wave-uniform; readfirstlane keeps the resource in scalar
 // registers (one in vector registers would loop over the lanes per load).
@@ -124,8 +129,23 @@ __device__ inline float head_ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
+// One level of a reduce-scatter over the lanes: lanes l and l ^ O swap
+// halves of their first 2 HALF sums, each keeping the upper half if l & O,
+// and add.  Compile-time offsets keep every index static.
+template <int O, int HALF>
+__device__ __forceinline__ void scatter_level(float* acc, int lane) {
+  const bool up = (lane & O) != 0;
+#pragma unroll
+  for (int t = 0; t < HALF; ++t) {
+    const float keep = up ? acc[t + HALF] : acc[t];
+    const float send = up ? acc[t] : acc[t + HALF];
+    acc[t] = keep + __shfl_xor(send, O, 64);
+  }
+}
+
 constexpr int kDqnHeadThreads = 1024;
 constexpr int kDqnHeadMaxA = 32;
+constexpr int kDqnHeadRows = 64;         // samples per workgroup (wavefront 0 finishes them)
 constexpr int kDqnHeadLds = 128 * 1024;  // dynamic LDS (gfx950: 160 KiB per workgroup)
 constexpr int kDqnHeadMaxBlocks = 1024;
 struct DqnHeadGroups {
@@ -144,21 +164,31 @@ __global__ __launch_bounds__(kDqnHeadThreads) void k_dqn_head(
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float* Ws = lds;                     // [G][K][AP]
   float* qs = lds + long(G) * K * AP;  // [G][RB][A]
-  __shared__ float red[kDqnHeadThreads / 64];
-  __shared__ bool last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int KU = 8;                                      // k-loads per lane and row in flight together
+  constexpr int RU = AP <= 8 ? 4 : (AP <= 16 ? 2 : 1);     // rows in flight together (RU * AP accumulators)
+  // The wavefront index and everything derived from it are scalar: a
+  // per-lane index would fetch p.h[g] with a vector load whose wait also
+  // waits for every row load issued before it.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b0 = blockIdx.x * RB;
   const int nrows = min(RB, B - b0);
-  constexpr int KU = 8;  // loads per lane in flight together
-  // Wavefront (g, i) owns sample b0 + i of group g; its first K-slice of h
-  // is in flight while the workgroup stages every group's W.
-  const int g = wave / RB, i = wave - g * RB;
-  const bool owner = g < G && i < nrows;
-  const __amdgpu_buffer_rsrc_t rh =
-      head_res(owner ? p.h[g] + long(b0 + i) * K : p.h[0], owner ? uint32_t(K) * 4u : 0u);
-  float hv[KU];
+  // Wavefront (g, j) owns rows j, j + WPG, j + 2 WPG, ... of group g.
+  const int WPG = (kDqnHeadThreads / 64) / G;
+  const int g = wave / WPG, j = wave - g * WPG;
+  const int my_rows = g < G && j < nrows ? (nrows - j + WPG - 1) / WPG : 0;
+  const float* hg = g == 0 ? p.h[0] : (g == 1 ? p.h[1] : p.h[2]);  // read only for g < G
+  const float* bg = g == 0 ? p.b[0] : (g == 1 ? p.b[1] : p.b[2]);
+  float* qg = g == 0 ? p.q[0] : (g == 1 ? p.q[1] : p.q[2]);
+  auto row_res = [&](int r) {  // the r-th row of this wavefront; none past my_rows
+    const bool ok = r < my_rows;
+    return head_res(ok ? hg + long(b0 + j + r * WPG) * K : p.h[0], ok ? uint32_t(K) * 4u : 0u);
+  };
+  // The first rows' first K-slice is in flight while the workgroup stages W.
+  float hv[RU][KU];
 #pragma unroll
-  for (int u = 0; u < KU; ++u) hv[u] = head_ld(rh, uint32_t(u * 64 + lane) * 4u);  // zero past K
+  for (int u = 0; u < RU; ++u)
+#pragma unroll
+    for (int uu = 0; uu < KU; ++uu) hv[u][uu] = head_ld(row_res(u), uint32_t(uu * 64 + lane) * 4u);  // zero past K
   // The batch inputs of the samples this workgroup finishes, also early.
   const int mine = b0 + int(threadIdx.x);
   const bool fin = int(threadIdx.x) < nrows;
@@ -191,43 +221,57 @@ __global__ __launch_bounds__(kDqnHeadThreads) void k_dqn_head(
     }
   }
   __syncthreads();
-  if (owner) {
-    const float* Wg = Ws + long(g) * K * AP;
-    float acc[AP];
+  const float* Wg = Ws + long(g < G ? g : 0) * K * AP;
+  static_assert(RU * AP == 32, "the lane reduction scatters 32 sums over 32 lanes");
+  // After the lane reduction lane l (and l + 32) holds sum number
+  // bitrev5(l & 31): each level's upper partner keeps the upper half.
+  const int vi = ((lane & 1) << 4) | ((lane & 2) << 2) | (lane & 4) | ((lane & 8) >> 2) | ((lane & 16) >> 4);
+  const int vu = vi / AP, va = vi - vu * AP;
+  for (int r0 = 0; r0 < my_rows; r0 += RU) {  // wave-uniform
+    float acc[RU * AP];  // [row][action]
 #pragma unroll
-    for (int a = 0; a < AP; ++a) acc[a] = 0.f;
+    for (int t = 0; t < RU * AP; ++t) acc[t] = 0.f;
     for (int k0 = 0; k0 < K; k0 += 64 * KU) {
-      if (k0 > 0) {
+      if (r0 > 0 || k0 > 0) {
 #pragma unroll
-        for (int u = 0; u < KU; ++u) hv[u] = head_ld(rh, uint32_t(k0 + u * 64 + lane) * 4u);
+        for (int u = 0; u < RU; ++u)
+#pragma unroll
+          for (int uu = 0; uu < KU; ++uu) hv[u][uu] = head_ld(row_res(r0 + u), uint32_t(k0 + uu * 64 + lane) * 4u);
       }
 #pragma unroll
-      for (int u = 0; u < KU; ++u) {
-        const int k = min(k0 + u * 64 + lane, K - 1);  // a real row of Ws; hv is zero past K
+      for (int uu = 0; uu < KU; ++uu) {
+        const int k = min(k0 + uu * 64 + lane, K - 1);  // a real row of Ws; hv is zero past K
         const float4* wr = reinterpret_cast<const float4*>(Wg + k * AP);
 #pragma unroll
         for (int c = 0; c < AP / 4; ++c) {
           const float4 w4 = wr[c];
-          acc[4 * c + 0] = fmaf(hv[u], w4.x, acc[4 * c + 0]);
-          acc[4 * c + 1] = fmaf(hv[u], w4.y, acc[4 * c + 1]);
-          acc[4 * c + 2] = fmaf(hv[u], w4.z, acc[4 * c + 2]);
-          acc[4 * c + 3] = fmaf(hv[u], w4.w, acc[4 * c + 3]);
+#pragma unroll
+          for (int u = 0; u < RU; ++u) {
+            float* au = acc + u * AP + 4 * c;
+            au[0] = fmaf(hv[u][uu], w4.x, au[0]);
+            au[1] = fmaf(hv[u][uu], w4.y, au[1]);
+            au[2] = fmaf(hv[u][uu], w4.z, au[2]);
+            au[3] = fmaf(hv[u][uu], w4.w, au[3]);
+          }
         }
       }
     }
-    // Butterfly over the lanes, the AP sums interleaved level by level.
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-      for (int a = 0; a < AP; ++a) acc[a] += __shfl_xor(acc[a], off, 64);
-    }
-    if (lane < A) {
-      float v = acc[0];
-#pragma unroll
-      for (int a = 1; a < AP; ++a) v = lane == a ? acc[a] : v;
-      if (p.b[g]) v += p.b[g][lane];
-      qs[(g * RB + i) * A + lane] = v;
-      p.q[g][long(b0 + i) * A + lane] = v;
+    // Reduce-scatter over the lanes: at offset o a lane keeps half of the
+    // sums it holds (the upper half if lane & o) and adds its partner's
+    // copy of that half, so five levels exchange 16 + 8 + 4 + 2 + 1 values
+    // and leave each lane one sum over its half-wave; the last exchange adds
+    // the other half-wave.
+    scatter_level<1, 16>(acc, lane);
+    scatter_level<2, 8>(acc, lane);
+    scatter_level<4, 4>(acc, lane);
+    scatter_level<8, 2>(acc, lane);
+    scatter_level<16, 1>(acc, lane);
+    float v = acc[0] + __shfl_xor(acc[0], 32, 64);
+    if (lane < 32 && va < A && r0 + vu < my_rows) {
+      const int i = j + (r0 + vu) * WPG;
+      if (bg) v += bg[va];
+      qs[(g * RB + i) * A + va] = v;
+      qg[long(b0 + i) * A + va] = v;
     }
   }
   __syncthreads();
@@ -242,30 +286,35 @@ __global__ __launch_bounds__(kDqnHeadThreads) void k_dqn_head(
     sum_h = r.h;
     sum_p = r.pred;
   }
-  // The workgroup's samples are all in wavefront 0 (nrows <= 16).
+  if (wave != 0) return;  // the workgroup's samples are all in wavefront 0 (nrows <= 64)
   float th = sum_h, tp = sum_p;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     th += __shfl_xor(th, off, 64);
     tp += __shfl_xor(tp, off, 64);
   }
+  if (gridDim.x == 1) {
+    if (threadIdx.x == 0) {
+      *loss = th * invB;
+      if (mean_q) *mean_q = tp * invB;
+    }
+    return;
+  }
   if (threadIdx.x == 0) {
     partials[2 * blockIdx.x] = th;
     partials[2 * blockIdx.x + 1] = tp;
     __threadfence();  // the partials are visible device-wide before the count
-    last = atomicAdd(counter, 1u) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (last && threadIdx.x == 0) {
-    __threadfence();
-    float sh = 0.f, sp = 0.f;
-    for (unsigned j = 0; j < gridDim.x; ++j) {  // workgroup order: the same sum on every run
-      sh += __hip_atomic_load(&partials[2 * j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sp += __hip_atomic_load(&partials[2 * j + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (atomicAdd(counter, 1u) == gridDim.x - 1) {
+      __threadfence();
+      float sh = 0.f, sp = 0.f;
+      for (unsigned jj = 0; jj < gridDim.x; ++jj) {  // workgroup order: the same sum on every run
+        sh += __hip_atomic_load(&partials[2 * jj], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sp += __hip_atomic_load(&partials[2 * jj + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      *loss = sh * invB;
+      if (mean_q) *mean_q = sp * invB;
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    *loss = sh * invB;
-    if (mean_q) *mean_q = sp * invB;
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -429,7 +478,7 @@ int ttrl_dqn_head(ttrl_ctx* ctx, int B, int K, int A, int groups, const float* c
   TTRL_REQUIRE(A <= kDqnHeadMaxA, "ttrl_dqn_head: at most %d actions", kDqnHeadMaxA);
   TTRL_REQUIRE(delta > 0.f, "ttrl_dqn_head: huber delta must be > 0");
   const int ap = A <= 8 ? 8 : (A <= 16 ? 16 : 32);
-  const int rb = (kDqnHeadThreads / 64) / groups;  // sample rows per workgroup: one wavefront per (group, row)
+  const int rb = B < kDqnHeadRows ? B : kDqnHeadRows;  // sample rows per workgroup
   const int blocks = (B + rb - 1) / rb;
   const size_t lds = (size_t(groups) * K * ap + size_t(groups) * rb * A) * sizeof(float);
   TTRL_REQUIRE(lds <= size_t(kDqnHeadLds), "ttrl_dqn_head: %d groups of K=%d x %d actions exceed the %d-byte LDS",
