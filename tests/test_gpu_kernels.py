@@ -148,11 +148,13 @@ def test_conv_forward_and_gradients(device, case):
         assert _rel(dx3.numpy() - 1.0, dx_ref * (x_nhwc > 0)) < 2e-5
 
 
-def test_adam_step_matches_fused_oracle_over_steps(device):
+@pytest.mark.parametrize("n", [10007, 2_200_003])
+def test_adam_step_matches_fused_oracle_over_steps(device, n):
+    """A ragged tail (n % 4), a partial last workgroup, and (2.2M) more
+    than one pass of the grid per thread."""
     from oracle import adam as oadam
     from ttrl_amd.engine.tensor import DeviceArray
     rng = np.random.default_rng(3)
-    n = 10007
     p = rng.uniform(-1, 1, n).astype(np.float32)
     pd = _dev_arr(device, p)
     S, V = DeviceArray(device, (n,)), DeviceArray(device, (n,))

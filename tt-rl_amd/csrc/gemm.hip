@@ -87,20 +87,27 @@ std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_f
   return out;
 }
 
+bool plan_with_splits(int cfg, int M, int N, int K, int groups, long ws_floats, int splits, GemmPlan* out) {
+  const TileDims t = tile_dims(cfg);
+  const int stages = std::max(1, (K + t.tbk - 1) / t.tbk);
+  const int sp = std::max(1, std::min(splits, stages));
+  const int spb = (stages + sp - 1) / sp;
+  const GemmPlan p{cfg, t.bm, t.bn, t.tbk, (stages + spb - 1) / spb, spb * t.tbk};
+  if (p.splits > 1 && long(p.splits) * groups * M * N > ws_floats) return false;
+  *out = p;
+  return true;
+}
+
 bool gemm_forced(unsigned allowed, int M, int N, int K, int groups, long ws_floats, GemmPlan* out) {
   const char* v = std::getenv("TTRL_GEMM_FORCE");
   if (!v || !*v) return false;
   int cfg = -1, splits = 0;
   if (std::sscanf(v, "%d:%d", &cfg, &splits) < 1 || cfg < 0 || cfg >= kNumCfg || !(allowed & (1u << cfg)))
     return false;
-  const TileDims t = tile_dims(cfg);
-  const int stages = std::max(1, (K + t.tbk - 1) / t.tbk);
   GemmPlan p = plan_gemm(M, N, K, groups, ws_floats, 1u << cfg);
   if (splits > 0) {
-    const int sp = std::min(splits, stages);
-    const int spb = (stages + sp - 1) / sp;
-    p = GemmPlan{cfg, t.bm, t.bn, t.tbk, (stages + spb - 1) / spb, spb * t.tbk};
-    if (p.splits > 1 && long(p.splits) * groups * M * N > ws_floats) p = plan_gemm(M, N, K, groups, ws_floats, 1u << cfg);
+    GemmPlan q;
+    if (plan_with_splits(cfg, M, N, K, groups, ws_floats, splits, &q)) p = q;
   }
   *out = p;
   return true;

@@ -996,6 +996,9 @@ void ctx_plan_store(ttrl_ctx* ctx, const std::string& key, const GemmPlan& p);
 float* ctx_tune_sink(ttrl_ctx* ctx, size_t bytes);
 bool ctx_tune_events(ttrl_ctx* ctx, hipEvent_t* a, hipEvent_t* b);
 std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_floats, unsigned allowed, int max_n);
+// Tile shape `cfg` with K split `splits` ways (fewer if K has fewer LDS
+// stages); false if the partials would not fit in `ws_floats`.
+bool plan_with_splits(int cfg, int M, int N, int K, int groups, long ws_floats, int splits, GemmPlan* out);
 bool gemm_tuning_enabled();
 bool gemm_tuning_log();  // TTRL_GEMM_TUNE_LOG=1: print each tuned signature's candidates to stderr
 // TTRL_GEMM_FORCE="cfg[:splits]" (read on every call, for tests): run that
@@ -1210,11 +1213,26 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
     p1 = *h1;
     p2 = *h2;
   } else {
+    // Per tile shape: the cost model's split of each problem, then each
+    // problem split 2 to 16 ways with the other at the model's split (the
+    // model prices a long K loop of a small problem below its latency).
     std::vector<std::pair<GemmPlan, GemmPlan>> cands;
-    for (int c = 0; c < kNumCfg; ++c)
-      if (ALLOWED & cfg_bit(c))
-        cands.emplace_back(plan_gemm(q1.M, q1.N, q1.K, q1.groups, half, cfg_bit(c)),
-                           plan_gemm(q2.M, q2.N, q2.K, q2.groups, half, cfg_bit(c)));
+    for (int c = 0; c < kNumCfg; ++c) {
+      if (!(ALLOWED & cfg_bit(c))) continue;
+      const GemmPlan b1 = plan_gemm(q1.M, q1.N, q1.K, q1.groups, half, cfg_bit(c));
+      const GemmPlan b2 = plan_gemm(q2.M, q2.N, q2.K, q2.groups, half, cfg_bit(c));
+      auto add = [&](const GemmPlan& a, const GemmPlan& b) {
+        for (const auto& e : cands)
+          if (e.first.cfg == a.cfg && e.first.splits == a.splits && e.second.splits == b.splits) return;
+        cands.emplace_back(a, b);
+      };
+      add(b1, b2);
+      for (int sp : {2, 4, 8, 16}) {
+        GemmPlan v;
+        if (plan_with_splits(c, q1.M, q1.N, q1.K, q1.groups, half, sp, &v)) add(v, b2);
+        if (plan_with_splits(c, q2.M, q2.N, q2.K, q2.groups, half, sp, &v)) add(b1, v);
+      }
+    }
     p1 = cands.front().first;
     p2 = cands.front().second;
     hipEvent_t e0, e1;
