@@ -889,10 +889,12 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm_pair(LA1 la1, LB1
 }
 
 // Sums split-K partials in split order and applies the epilogue; group
-// blockIdx.y.  Eight partials are loaded before any is added, so a long
-// split list costs a few memory round trips rather than one per split.
+// blockIdx.y.  Up to 32 partials are loaded before any is added (indices
+// past the last split re-read it and are not added), so a split list of up
+// to 32 costs one memory round trip.
 template <class EP>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, int M, int N, int splits, FDiv dn) {
+  constexpr int RB = 32;
   const int g = blockIdx.y;
   const int MN = M * N;
   const int rows = ep.rows(g);
@@ -903,15 +905,14 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* ws, EP ep, i
       if (m >= rows) continue;
       const float* p = wg + mn;
       float s = 0.f;
-      int sp = 0;
-      for (; sp + 8 <= splits; sp += 8) {
-        float v[8];
+      for (int sp = 0; sp < splits; sp += RB) {
+        float v[RB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = gload(p + long(sp + j) * MN);
+        for (int j = 0; j < RB; ++j) v[j] = gload(p + long(min(sp + j, splits - 1)) * MN);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += v[j];
+        for (int j = 0; j < RB; ++j)
+          if (sp + j < splits) s += v[j];
       }
-      for (; sp < splits; ++sp) s += gload(p + long(sp) * MN);
       eb.store(m, n, s, eb.aux(m, n));
     }
   });
