@@ -1,0 +1,110 @@
+"""Learner state through a checkpoint file on the GPU: a learner restored
+from another's L1 file (into its own already-captured update graph) holds
+the same parameters, canonical Adam moments, counters and sampling RNG, and
+its next update is bit-identical to the original's (same kernels and plans
+in one process, as the graph-replay determinism tests rely on).  The
+weights-only marker, the config check and a reference-style config record
+follow ttrl/algos/checkpoint.py:72-129."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests._dqn_helpers import build_learner
+from tests._sac_helpers import build_sac
+
+pytestmark = pytest.mark.gpu
+
+
+def _same_tree(a, b, path=""):
+    if isinstance(a, dict):
+        assert set(a) == set(b), path
+        for k in a:
+            _same_tree(a[k], b[k], f"{path}.{k}")
+    elif isinstance(a, (list, tuple)):
+        assert len(a) == len(b), path
+        for i, (x, y) in enumerate(zip(a, b)):
+            _same_tree(x, y, f"{path}.{i}")
+    elif isinstance(a, np.ndarray):
+        if a.dtype == np.float64:  # canonical m / v: S * scale then / scale
+            assert np.allclose(a, b, rtol=1e-12, atol=0), path
+        else:
+            assert np.array_equal(a, np.asarray(b)), path
+    else:
+        assert a == b, path
+
+
+def test_dqn_state_round_trips_through_a_file(device, tmp_path):
+    from ttrl_amd import checkpoint as ck
+    from ttrl_amd.workloads import dqn_batch
+
+    a, _, _ = build_learner(device, seed=5)
+    b, _, _ = build_learner(device, seed=6)
+    try:
+        for k in range(2):
+            a.update(dqn_batch(300 + k))
+        a.act(np.random.default_rng(0).integers(0, 256, (1, 4, 84, 84), dtype=np.uint8))
+        b.update(dqn_batch(999))  # b's graph is captured before the restore
+        path = str(tmp_path / "dqn.npz")
+        ck.save_checkpoint(path, agent_state=a.state_dict(), obs_spec=a.obs_spec, action_spec=a.action_spec,
+                           level=ck.L1, config=a.cfg, frame=a.frame_count)
+        loaded = ck.load_checkpoint(path)
+        assert loaded["config"] == a.cfg and loaded["frame"] == a.frame_count
+        b.load_state_dict(loaded["agent_state"])
+        _same_tree(a.state_dict(), b.state_dict())
+        ma, mb = a.update(dqn_batch(302)), b.update(dqn_batch(302))
+        assert ma["loss"] == mb["loss"] and ma["mean_q"] == mb["mean_q"]
+        for k, v in a.online.state_dict().items():
+            assert np.array_equal(v, b.online.state_dict()[k]), k
+        assert a.update_count == b.update_count
+        assert a._rng.random() == b._rng.random()
+
+        weights = a.state_dict(weights_only=True)
+        assert weights["weights_only"] is True and "optimizer" not in weights
+        with pytest.raises(ValueError, match="parameters only"):
+            b.load_state_dict(weights)
+        b.load_state_dict(weights, weights_only=True)
+
+        foreign = a.state_dict()
+        foreign["config"] = ck.StoredDataclass("ttrl.algos.dqn.config:DQNConfig", {"double": True})
+        b.load_state_dict(foreign)  # a reference config is carried, the weights are checked by shape
+        other = a.state_dict()
+        other["config"] = type(a.cfg)(lr=1e-3)
+        with pytest.raises(ValueError, match="configuration differs"):
+            b.load_state_dict(other)
+        broken = a.state_dict()
+        del broken["optimizer"]
+        with pytest.raises(ValueError, match="missing"):
+            b.load_state_dict(broken)
+    finally:
+        a.close()
+        b.close()
+
+
+def test_sac_state_round_trips_through_a_file(device, tmp_path):
+    from ttrl_amd import checkpoint as ck
+    from ttrl_amd.workloads import sac_batch
+
+    a, _, _ = build_sac(device, seed=7)
+    b, _, _ = build_sac(device, seed=8)
+    try:
+        for k in range(2):
+            a.update(sac_batch(70 + k))
+        b.update(sac_batch(99))
+        b.update(sac_batch(98))  # b's update graph is captured before the restore
+        path = str(tmp_path / "sac.npz")
+        ck.save_checkpoint(path, agent_state=a.state_dict(), obs_spec=a.obs_spec, action_spec=a.action_spec,
+                           level=ck.L0)
+        loaded = ck.load_checkpoint(path)
+        assert loaded["level"] == ck.L0 and loaded["action_spec"].dim == 3
+        b.load_state_dict(loaded["agent_state"])
+        _same_tree(a.state_dict(), b.state_dict())
+        ma, mb = a.update(sac_batch(72)), b.update(sac_batch(72))
+        assert ma["critic_loss"] == mb["critic_loss"] and ma["actor_loss"] == mb["actor_loss"]
+        for k, v in a.nets.state_dict().items():
+            assert np.array_equal(v, b.nets.state_dict()[k]), k
+        assert np.array_equal(a.log_alpha.numpy(), b.log_alpha.numpy())
+    finally:
+        a.close()
+        b.close()

@@ -23,6 +23,7 @@ import numpy as np
 
 from ttrl_amd import _lib
 from ttrl_amd.algos.grads import grad_sq_device
+from ttrl_amd.algos.state import assemble, validate
 from ttrl_amd.engine.autograd import Tensor, no_grad
 from ttrl_amd.engine.conv import Conv2d
 from ttrl_amd.engine import layers as layers_mod
@@ -278,6 +279,34 @@ class DQNLearner:
         # A separate stream for evaluation acting, so evaluation does not
         # perturb the training exploration trajectory.
         self._eval_rng = np.random.default_rng(seed).spawn(1)[0]
+
+    # -- state -------------------------------------------------------------
+
+    _WEIGHT_KEYS = ("online", "target")
+    _RUN_KEYS = ("optimizer", "frame_count", "update_count", "rng_state")
+
+    def state_dict(self, *, weights_only: bool = False) -> dict:
+        """The reference agent's state tree (ttrl/algos/dqn/agent.py:225-238)
+        for the parts a learner holds; the agent loop's autoreset phase and
+        update clock are not part of it."""
+        return assemble(self.cfg, {"online": self.online.state_dict(), "target": self.target.state_dict()},
+                        {"optimizer": self.optimizer.state_dict(), "frame_count": self.frame_count,
+                         "update_count": self.update_count, "rng_state": self._rng.bit_generator.state},
+                        weights_only=weights_only)
+
+    def load_state_dict(self, state: dict, *, weights_only: bool = False) -> None:
+        """In place, so a captured update keeps its buffers
+        (ttrl/algos/dqn/agent.py:240-253)."""
+        load_run = validate(state, algo="DQN", config=self.cfg, weight_keys=self._WEIGHT_KEYS,
+                            run_keys=self._RUN_KEYS, weights_only=weights_only)
+        self.online.load_state_dict(state["online"])
+        self.target.load_state_dict(state["target"])
+        if not load_run:
+            return
+        self.optimizer.load_state_dict(state["optimizer"])
+        self.frame_count = int(state["frame_count"])
+        self.update_count = int(state["update_count"])
+        self._rng.bit_generator.state = state["rng_state"]
 
     # -- acting ------------------------------------------------------------
 

@@ -29,6 +29,7 @@ import numpy as np
 
 from ttrl_amd import _lib
 from ttrl_amd.algos.gaussian import ActionScale, squashed_sample
+from ttrl_amd.algos.state import assemble, validate
 from ttrl_amd.nets.acting import ActingNet, SquashedDecision
 from ttrl_amd.engine.autograd import Tensor, _needs, no_grad
 from ttrl_amd.engine import layers as layers_mod
@@ -366,6 +367,40 @@ class SACLearner:
         self.frame_count = 0
         self._rng = np.random.default_rng(seed)
         self._eval_rng = np.random.default_rng(seed).spawn(1)[0]
+
+    # -- state ---------------------------------------------------------------
+
+    _WEIGHT_KEYS = ("nets", "log_alpha")
+    _RUN_KEYS = ("actor_opt", "critic_opt", "alpha_opt", "frame_count", "update_count", "rng_state")
+
+    def state_dict(self, *, weights_only: bool = False) -> dict:
+        """The reference agent's state tree (ttrl/algos/sac/agent.py:249-264)
+        for the parts a learner holds; the agent loop's autoreset phase and
+        update clock are not part of it."""
+        return assemble(self.cfg, {"nets": self.nets.state_dict(), "log_alpha": self.log_alpha.numpy()},
+                        {"actor_opt": self.actor_opt.state_dict(), "critic_opt": self.critic_opt.state_dict(),
+                         "alpha_opt": self.alpha_opt.state_dict(), "frame_count": self.frame_count,
+                         "update_count": self.update_count, "rng_state": self._rng.bit_generator.state},
+                        weights_only=weights_only)
+
+    def load_state_dict(self, state: dict, *, weights_only: bool = False) -> None:
+        """In place, so the captured update keeps its buffers
+        (ttrl/algos/sac/agent.py:266-282)."""
+        load_run = validate(state, algo="SAC", config=self.cfg, weight_keys=self._WEIGHT_KEYS,
+                            run_keys=self._RUN_KEYS, weights_only=weights_only)
+        log_alpha = np.asarray(state["log_alpha"], np.float32)
+        if log_alpha.size != 1:
+            raise ValueError(f"SAC.load_state_dict: log_alpha must hold one value, got shape {log_alpha.shape}")
+        self.nets.load_state_dict(state["nets"])
+        self.log_alpha.data.upload(log_alpha.reshape(tuple(self.log_alpha.shape)))
+        if not load_run:
+            return
+        self.actor_opt.load_state_dict(state["actor_opt"])
+        self.critic_opt.load_state_dict(state["critic_opt"])
+        self.alpha_opt.load_state_dict(state["alpha_opt"])
+        self.frame_count = int(state["frame_count"])
+        self.update_count = int(state["update_count"])
+        self._rng.bit_generator.state = state["rng_state"]
 
     # -- acting --------------------------------------------------------------
 

@@ -1,0 +1,63 @@
+"""A learner's state tree: a WEIGHTS half (parameters and their lagged
+copies) and a RUN half (optimizer moments, counters, the sampling RNG), with
+the reference's marker for a weights-only state and its loading rules
+(ttrl/algos/checkpoint.py:31-129).
+
+The config is compared when it is one of this package's configs.  A config
+read from a reference checkpoint (a `StoredDataclass` of a `ttrl.` class) is
+carried, not compared: the weights it came with are checked against this
+learner's networks by name and shape instead.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+from ttrl_amd.checkpoint import StoredDataclass
+
+__all__ = ["CONFIG_KEY", "WEIGHTS_ONLY_KEY", "assemble", "validate"]
+
+WEIGHTS_ONLY_KEY = "weights_only"
+CONFIG_KEY = "config"
+
+
+def assemble(config, weights: dict, run: dict, *, weights_only: bool) -> dict:
+    """One state dict from its two halves (ttrl/algos/checkpoint.py:31-39)."""
+    state = dict(weights)
+    state[CONFIG_KEY] = config
+    if weights_only:
+        state[WEIGHTS_ONLY_KEY] = True
+        return state
+    state.update(run)
+    return state
+
+
+def _config_diff(saved, current) -> str:
+    if not (dataclasses.is_dataclass(saved) and type(saved) is type(current)):
+        return f"checkpoint holds {saved!r}; this learner has {current!r}"
+    names = [f.name for f in dataclasses.fields(saved) if getattr(saved, f.name) != getattr(current, f.name)]
+    was = ", ".join(f"{n}={getattr(saved, n)!r}" for n in names)
+    now = ", ".join(f"{n}={getattr(current, n)!r}" for n in names)
+    return f"{len(names)} field(s) differ: checkpoint was written with {was}; this learner has {now}"
+
+
+def validate(state: dict, *, algo: str, config, weight_keys: tuple, run_keys: tuple, weights_only: bool) -> bool:
+    """Check `state` against what `algo` needs; True when its run half is to
+    be loaded (ttrl/algos/checkpoint.py:72-129)."""
+    carries_weights_only = bool(state.get(WEIGHTS_ONLY_KEY, False))
+    if carries_weights_only and not weights_only:
+        raise ValueError(f"{algo}.load_state_dict: this state carries parameters only (written with "
+                         f"state_dict(weights_only=True)) and none of {list(run_keys)}; continuing from it would "
+                         f"restart the optimizer moments and counters. Pass weights_only=True to load the "
+                         f"parameters on purpose.")
+    required = tuple(weight_keys) + (CONFIG_KEY,)
+    if not (carries_weights_only or weights_only):
+        required += tuple(run_keys)
+    missing = [key for key in required if key not in state]
+    if missing:
+        raise ValueError(f"{algo}.load_state_dict: state is missing {missing}.")
+    saved = state[CONFIG_KEY]
+    if not isinstance(saved, StoredDataclass) and saved != config:
+        raise ValueError(f"{algo}.load_state_dict: this learner's configuration differs from the state's. "
+                         f"{_config_diff(saved, config)}.")
+    return not (carries_weights_only or weights_only)

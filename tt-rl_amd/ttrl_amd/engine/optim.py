@@ -180,8 +180,10 @@ class Adam(Optimizer):
             "betas": (self.b1, self.b2),
             "eps": self.eps,
             "weight_decay": self.weight_decay,
-            "m": [m.numpy() * self._m_scale for m in self.m],
-            "v": [v.numpy() * self._v_scale for v in self.v],
+            # Canonical m and v in float64: S * scale / scale then returns the
+            # stored float32 S exactly, so a restore resumes bit for bit.
+            "m": [m.numpy().astype(np.float64) * self._m_scale for m in self.m],
+            "v": [v.numpy().astype(np.float64) * self._v_scale for v in self.v],
         }
 
     def load_state_dict(self, state: dict, device=None) -> None:
