@@ -108,3 +108,35 @@ def test_sac_state_round_trips_through_a_file(device, tmp_path):
     finally:
         a.close()
         b.close()
+
+
+def test_ppo_state_round_trips_through_a_file(device, tmp_path):
+    from ttrl_amd import checkpoint as ck
+    from ttrl_amd.algos.ppo import PPOConfig, PPOLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_qnet_state, ppo_rollout
+
+    cfg = PPOConfig(minibatch_size=64, epochs=2, n_steps=32)
+    learners = []
+    for seed in (11, 12):
+        lr = PPOLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(6), device, cfg=cfg, seed=seed)
+        lr.net.load_state_dict(he_uniform_qnet_state(lr.net, seed + 1))
+        learners.append(lr)
+    a, b = learners
+    try:
+        a.update(ppo_rollout(20, 32, 4, 6))
+        b.update(ppo_rollout(21, 32, 4, 6))  # b's minibatch graph is captured before the restore
+        path = str(tmp_path / "ppo.npz")
+        ck.save_checkpoint(path, agent_state=a.state_dict(), obs_spec=a.obs_spec, action_spec=a.action_spec,
+                           level=ck.L1, config=a.cfg, frame=a.frame_count)
+        b.load_state_dict(ck.load_checkpoint(path)["agent_state"])
+        _same_tree(a.state_dict(), b.state_dict())
+        rollout = ppo_rollout(22, 32, 4, 6)
+        ma, mb = a.update(rollout), b.update(rollout)
+        for k in PPOLearner.METRICS:
+            assert ma[k] == mb[k], k
+        for k, v in a.net.state_dict().items():
+            assert np.array_equal(v, b.net.state_dict()[k]), k
+    finally:
+        a.close()
+        b.close()

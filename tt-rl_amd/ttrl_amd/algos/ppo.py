@@ -24,6 +24,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ttrl_amd import _lib
+from ttrl_amd.algos.state import assemble, validate
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs
 from ttrl_amd.engine.optim import Adam
 from ttrl_amd.engine.tensor import DeviceArray, arena_of, bound_block, to_device
@@ -508,6 +509,33 @@ class PPOLearner:
         out["lr"] = self.optimizer.lr
         out["minibatches"] = float(steps)
         return out
+
+    # -- state -------------------------------------------------------------
+
+    _WEIGHT_KEYS = ("net",)
+    _RUN_KEYS = ("optimizer", "frame_count", "update_count", "rng_state")
+
+    def state_dict(self, *, weights_only: bool = False) -> dict:
+        """The reference agent's state tree (ttrl/algos/ppo/state.py:25-46)
+        for the parts a learner holds; the agent loop's autoreset phase and
+        partial rollout are not part of it."""
+        return assemble(self.cfg, {"net": self.net.state_dict()},
+                        {"optimizer": self.optimizer.state_dict(), "frame_count": self.frame_count,
+                         "update_count": self.update_count, "rng_state": self._rng.bit_generator.state},
+                        weights_only=weights_only)
+
+    def load_state_dict(self, state: dict, *, weights_only: bool = False) -> None:
+        """In place, so a captured minibatch step keeps its buffers
+        (ttrl/algos/ppo/state.py:49-72)."""
+        load_run = validate(state, algo="PPO", config=self.cfg, weight_keys=self._WEIGHT_KEYS,
+                            run_keys=self._RUN_KEYS, weights_only=weights_only)
+        self.net.load_state_dict(state["net"])
+        if not load_run:
+            return
+        self.optimizer.load_state_dict(state["optimizer"])
+        self.frame_count = int(state["frame_count"])
+        self.update_count = int(state["update_count"])
+        self._rng.bit_generator.state = state["rng_state"]
 
     def close(self) -> None:
         self._release_graph()
