@@ -143,3 +143,39 @@ def test_write_is_atomic_and_leaves_no_temp_files(tmp_path):
     _save(tmp_path / "c.npz", agent_state={"w": np.ones(2, np.float32)})
     assert [p.name for p in tmp_path.iterdir()] == ["c.npz"]
     assert np.array_equal(ck.load_checkpoint(path)["agent_state"]["w"], np.ones(2, np.float32))
+
+
+def _reference_trunk(prefix):
+    # The reference exporter's pattern for an actor tower's Linear/conv
+    # weights (ttrl/deploy/policies.py:61-66).
+    import re
+    return re.compile(rf"^{re.escape(prefix)}towers\.(?P<leaf>[^.]+)\.layers\.(?P<index>\d+)\.weight$")
+
+
+@pytest.mark.parametrize("towers,prefix,ours", [
+    ("TOWERS_DQN", "encoder.", ["encoder.layers.0.weight", "encoder.layers.7.weight", "encoder.layers.7.bias",
+                                "head.q.weight"]),
+    ("TOWERS_SAC", "policy.encoder.", ["policy.encoder.layers.0.weight", "policy.encoder.layers.2.bias",
+                                       "policy.head.heads.mean.weight", "critics.0.head.layers.0.weight",
+                                       "critics.1.encoder.tower.layers.0.weight",
+                                       "targets.1.encoder.tower.layers.0.bias"]),
+    ("TOWERS_PPO", "encoders.actor.", ["encoders.actor.layers.0.weight", "encoders.actor.layers.7.weight",
+                                       "heads.policy.logits.weight", "heads.value.value.weight",
+                                       "memories.actor.cell.weight_ih"]),
+])
+def test_state_keys_take_the_reference_names_and_come_back(towers, prefix, ours):
+    from ttrl_amd.algos import state as st
+    table = getattr(st, towers)
+    state = {k: i for i, k in enumerate(ours)}
+    ref = st.to_reference_keys(state, table, "obs")
+    trunk = _reference_trunk(prefix)
+    for k in ours:
+        if k.startswith(prefix) and k.endswith(".weight"):
+            moved = next(r for r, v in ref.items() if v == state[k])
+            m = trunk.match(moved)
+            assert m and m["leaf"] == "obs" and m["index"] == k.split(".")[-2], moved
+    assert "critics.1.encoder.encoder.towers.obs.layers.0.weight" in ref or towers != "TOWERS_SAC"
+    assert st.from_reference_keys(ref, table, "obs") == state
+    for k in ("head.q.weight", "policy.head.heads.mean.weight", "heads.policy.logits.weight"):
+        if k in state:
+            assert k in ref  # heads already carry the reference's names

@@ -51,6 +51,12 @@ def test_dqn_state_round_trips_through_a_file(device, tmp_path):
                            level=ck.L1, config=a.cfg, frame=a.frame_count)
         loaded = ck.load_checkpoint(path)
         assert loaded["config"] == a.cfg and loaded["frame"] == a.frame_count
+        # the names the reference's exporter reads (ttrl/deploy/policies.py:91-97)
+        assert {"encoder.towers.obs.layers.0.weight", "encoder.towers.obs.layers.7.weight",
+                "head.q.weight"} <= set(loaded["agent_state"]["online"])
+        online = loaded["agent_state"]["online"]
+        assert online["encoder.towers.obs.layers.0.weight"].shape == (32, 4, 8, 8)  # logical OIHW
+        assert online["encoder.towers.obs.layers.7.weight"].shape == (3136, 512)  # (in, out)
         b.load_state_dict(loaded["agent_state"])
         _same_tree(a.state_dict(), b.state_dict())
         ma, mb = a.update(dqn_batch(302)), b.update(dqn_batch(302))
@@ -98,6 +104,8 @@ def test_sac_state_round_trips_through_a_file(device, tmp_path):
                            level=ck.L0)
         loaded = ck.load_checkpoint(path)
         assert loaded["level"] == ck.L0 and loaded["action_spec"].dim == 3
+        assert {"policy.encoder.towers.obs.layers.0.weight", "policy.head.heads.mean.weight",
+                "critics.0.head.layers.0.weight"} <= set(loaded["agent_state"]["nets"])  # policies.py:69-77
         b.load_state_dict(loaded["agent_state"])
         _same_tree(a.state_dict(), b.state_dict())
         ma, mb = a.update(sac_batch(72)), b.update(sac_batch(72))
@@ -129,7 +137,10 @@ def test_ppo_state_round_trips_through_a_file(device, tmp_path):
         path = str(tmp_path / "ppo.npz")
         ck.save_checkpoint(path, agent_state=a.state_dict(), obs_spec=a.obs_spec, action_spec=a.action_spec,
                            level=ck.L1, config=a.cfg, frame=a.frame_count)
-        b.load_state_dict(ck.load_checkpoint(path)["agent_state"])
+        agent_state = ck.load_checkpoint(path)["agent_state"]
+        assert {"encoders.actor.towers.obs.layers.0.weight",
+                "heads.policy.logits.weight"} <= set(agent_state["net"])  # policies.py:78-90
+        b.load_state_dict(agent_state)
         _same_tree(a.state_dict(), b.state_dict())
         rollout = ppo_rollout(22, 32, 4, 6)
         ma, mb = a.update(rollout), b.update(rollout)

@@ -23,7 +23,7 @@ import numpy as np
 
 from ttrl_amd import _lib
 from ttrl_amd.algos.grads import grad_sq_device
-from ttrl_amd.algos.state import assemble, validate
+from ttrl_amd.algos.state import TOWERS_DQN, assemble, from_reference_keys, to_reference_keys, validate
 from ttrl_amd.engine.autograd import Tensor, no_grad
 from ttrl_amd.engine.conv import Conv2d
 from ttrl_amd.engine import layers as layers_mod
@@ -289,7 +289,9 @@ class DQNLearner:
         """The reference agent's state tree (ttrl/algos/dqn/agent.py:225-238)
         for the parts a learner holds; the agent loop's autoreset phase and
         update clock are not part of it."""
-        return assemble(self.cfg, {"online": self.online.state_dict(), "target": self.target.state_dict()},
+        leaf = self.obs_spec.name
+        return assemble(self.cfg, {"online": to_reference_keys(self.online.state_dict(), TOWERS_DQN, leaf),
+                                   "target": to_reference_keys(self.target.state_dict(), TOWERS_DQN, leaf)},
                         {"optimizer": self.optimizer.state_dict(), "frame_count": self.frame_count,
                          "update_count": self.update_count, "rng_state": self._rng.bit_generator.state},
                         weights_only=weights_only)
@@ -299,8 +301,9 @@ class DQNLearner:
         (ttrl/algos/dqn/agent.py:240-253)."""
         load_run = validate(state, algo="DQN", config=self.cfg, weight_keys=self._WEIGHT_KEYS,
                             run_keys=self._RUN_KEYS, weights_only=weights_only)
-        self.online.load_state_dict(state["online"])
-        self.target.load_state_dict(state["target"])
+        leaf = self.obs_spec.name
+        self.online.load_state_dict(from_reference_keys(state["online"], TOWERS_DQN, leaf))
+        self.target.load_state_dict(from_reference_keys(state["target"], TOWERS_DQN, leaf))
         if not load_run:
             return
         self.optimizer.load_state_dict(state["optimizer"])

@@ -24,7 +24,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ttrl_amd import _lib
-from ttrl_amd.algos.state import assemble, validate
+from ttrl_amd.algos.state import TOWERS_PPO, assemble, from_reference_keys, to_reference_keys, validate
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs
 from ttrl_amd.engine.optim import Adam
 from ttrl_amd.engine.tensor import DeviceArray, arena_of, bound_block, to_device
@@ -519,7 +519,7 @@ class PPOLearner:
         """The reference agent's state tree (ttrl/algos/ppo/state.py:25-46)
         for the parts a learner holds; the agent loop's autoreset phase and
         partial rollout are not part of it."""
-        return assemble(self.cfg, {"net": self.net.state_dict()},
+        return assemble(self.cfg, {"net": to_reference_keys(self.net.state_dict(), TOWERS_PPO, self.obs_spec.name)},
                         {"optimizer": self.optimizer.state_dict(), "frame_count": self.frame_count,
                          "update_count": self.update_count, "rng_state": self._rng.bit_generator.state},
                         weights_only=weights_only)
@@ -529,7 +529,7 @@ class PPOLearner:
         (ttrl/algos/ppo/state.py:49-72)."""
         load_run = validate(state, algo="PPO", config=self.cfg, weight_keys=self._WEIGHT_KEYS,
                             run_keys=self._RUN_KEYS, weights_only=weights_only)
-        self.net.load_state_dict(state["net"])
+        self.net.load_state_dict(from_reference_keys(state["net"], TOWERS_PPO, self.obs_spec.name))
         if not load_run:
             return
         self.optimizer.load_state_dict(state["optimizer"])

@@ -29,7 +29,7 @@ import numpy as np
 
 from ttrl_amd import _lib
 from ttrl_amd.algos.gaussian import ActionScale, squashed_sample
-from ttrl_amd.algos.state import assemble, validate
+from ttrl_amd.algos.state import TOWERS_SAC, assemble, from_reference_keys, to_reference_keys, validate
 from ttrl_amd.nets.acting import ActingNet, SquashedDecision
 from ttrl_amd.engine.autograd import Tensor, _needs, no_grad
 from ttrl_amd.engine import layers as layers_mod
@@ -377,7 +377,8 @@ class SACLearner:
         """The reference agent's state tree (ttrl/algos/sac/agent.py:249-264)
         for the parts a learner holds; the agent loop's autoreset phase and
         update clock are not part of it."""
-        return assemble(self.cfg, {"nets": self.nets.state_dict(), "log_alpha": self.log_alpha.numpy()},
+        nets = to_reference_keys(self.nets.state_dict(), TOWERS_SAC, self.obs_spec.name)
+        return assemble(self.cfg, {"nets": nets, "log_alpha": self.log_alpha.numpy()},
                         {"actor_opt": self.actor_opt.state_dict(), "critic_opt": self.critic_opt.state_dict(),
                          "alpha_opt": self.alpha_opt.state_dict(), "frame_count": self.frame_count,
                          "update_count": self.update_count, "rng_state": self._rng.bit_generator.state},
@@ -391,7 +392,7 @@ class SACLearner:
         log_alpha = np.asarray(state["log_alpha"], np.float32)
         if log_alpha.size != 1:
             raise ValueError(f"SAC.load_state_dict: log_alpha must hold one value, got shape {log_alpha.shape}")
-        self.nets.load_state_dict(state["nets"])
+        self.nets.load_state_dict(from_reference_keys(state["nets"], TOWERS_SAC, self.obs_spec.name))
         self.log_alpha.data.upload(log_alpha.reshape(tuple(self.log_alpha.shape)))
         if not load_run:
             return

@@ -12,13 +12,57 @@ learner's networks by name and shape instead.
 from __future__ import annotations
 
 import dataclasses
+import re
 
 from ttrl_amd.checkpoint import StoredDataclass
 
-__all__ = ["CONFIG_KEY", "WEIGHTS_ONLY_KEY", "assemble", "validate"]
+__all__ = ["CONFIG_KEY", "WEIGHTS_ONLY_KEY", "TOWERS_DQN", "TOWERS_PPO", "TOWERS_SAC", "assemble",
+           "from_reference_keys", "to_reference_keys", "validate"]
 
 WEIGHTS_ONLY_KEY = "weights_only"
 CONFIG_KEY = "config"
+
+
+# Where a network's per-observation towers sit, as (name here, name in the
+# reference) templates whose `{field}`s stand for one name segment each.  The
+# reference hangs each observation leaf's tower under `<encoder>.towers.<leaf>.`
+# (ttrl/nets/multi.py:53-85) and names a critic's concat encoder's tower
+# `encoder` (ttrl/nets/fusion.py:60-72); the networks here hold the one
+# leaf's tower directly.
+TOWERS_DQN = (("encoder", "encoder"),)
+TOWERS_SAC = (("policy.encoder", "policy.encoder"), ("{net}.{i}.encoder.tower", "{net}.{i}.encoder.encoder"))
+TOWERS_PPO = (("encoders.{role}", "encoders.{role}"),)
+
+
+def _template(t: str, tail: str) -> re.Pattern:
+    parts = re.split(r"\{(\w+)\}", t)
+    rx = "".join(re.escape(p) if i % 2 == 0 else f"(?P<{p}>[^.]+)" for i, p in enumerate(parts))
+    return re.compile(f"^{rx}{re.escape(tail)}")
+
+
+def _rename(state: dict, towers, leaf: str, *, to_reference: bool) -> dict:
+    out = {}
+    for key, value in state.items():
+        for here, there in towers:
+            src, dst = (here, there) if to_reference else (there, here)
+            m = _template(src, "." if to_reference else f".towers.{leaf}.").match(key)
+            if m:
+                head = dst.format(**m.groupdict())
+                key = (f"{head}.towers.{leaf}." if to_reference else f"{head}.") + key[m.end():]
+                break
+        out[key] = value
+    return out
+
+
+def to_reference_keys(state: dict, towers, leaf: str) -> dict:
+    """A network state dict under the reference's parameter names."""
+    return _rename(state, towers, leaf, to_reference=True)
+
+
+def from_reference_keys(state: dict, towers, leaf: str) -> dict:
+    """The inverse of `to_reference_keys`; names it does not know pass
+    through, so the network's own load names them."""
+    return _rename(state, towers, leaf, to_reference=False)
 
 
 def assemble(config, weights: dict, run: dict, *, weights_only: bool) -> dict:
