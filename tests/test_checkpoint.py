@@ -71,6 +71,9 @@ def test_unknown_or_missing_fields_of_own_dataclasses_are_named(tmp_path):
     meta["agent_state"]["config"]["fields"]["renamed_field"] = 1
     with pytest.raises(ck.CheckpointFieldError, match="renamed_field"):
         ck.join(meta["agent_state"], arrays, file=path)
+    for bad in ("ttrl_amd.no_such_module:X", "ttrl_amd.algos.dqn:NoSuchClass", "ttrl_amd.algos.dqn:DQNLearner.act"):
+        with pytest.raises(ck.CheckpointFieldError, match="not a dataclass"):
+            ck.join({"__dataclass__": bad, "fields": {}}, arrays, file=path)
 
 
 def test_format_marker_and_unreadable_files_are_refused(tmp_path):

@@ -35,7 +35,7 @@ import numpy as np
 
 from ttrl_amd.spaces import ActionSpec, ObsSpec
 
-__all__ = ["FORMAT", "L0", "L1", "LEVELS", "StoredDataclass", "CheckpointFieldError", "split", "join",
+__all__ = ["FORMAT", "L0", "L1", "LEVELS", "StoredDataclass", "CheckpointFieldError", "atomic_write", "split", "join",
            "save_checkpoint", "load_checkpoint", "read_meta", "obs_spec_to_json", "obs_spec_from_json",
            "action_spec_to_json", "action_spec_from_json"]
 
@@ -122,15 +122,17 @@ def _rebuild(path: str, fields: dict, *, file: str):
     if not path.startswith(TYPE_ROOT) or path.count(":") != 1:
         return StoredDataclass(path, fields)
     module_name, qualname = path.split(":")
-    module = sys.modules.get(module_name)
-    if module is None:  # a module of this package, never one outside it
-        module = importlib.import_module(module_name)
-    cls = module
+    cls = sys.modules.get(module_name)
+    if cls is None:  # a module of this package, never one outside it
+        try:
+            cls = importlib.import_module(module_name)
+        except ImportError:
+            cls = None
     for part in qualname.split("."):
-        cls = getattr(cls, part, None)
-        if cls is None:
-            raise CheckpointFieldError(f"checkpoint at {file!r} names the type {path!r}, which this build does not "
-                                       f"define.")
+        cls = getattr(cls, part, None) if cls is not None else None
+    if not (isinstance(cls, type) and dataclasses.is_dataclass(cls)):
+        raise CheckpointFieldError(f"checkpoint at {file!r} names the type {path!r}, which is not a dataclass this "
+                                   f"build defines.")
     declared = {f.name: f for f in dataclasses.fields(cls)}
     unknown = sorted(k for k in fields if k not in declared)
     if unknown:
@@ -200,7 +202,7 @@ def _json_default(obj: Any) -> Any:
 
 # ------------------------------------------------------------------ files --
 
-def _atomic_write(path: str, data: bytes) -> None:
+def atomic_write(path: str, data: bytes) -> None:
     """Temp file beside the destination, fsync, rename: a reader sees the old
     file or the whole new one (ttrl/train/checkpoint/atomic.py:24-37)."""
     directory = os.path.dirname(os.path.abspath(path)) or "."
@@ -259,7 +261,7 @@ def save_checkpoint(path: str, *, agent_state: dict, obs_spec: ObsSpec, action_s
     payload[_META] = np.frombuffer(json.dumps(meta, default=_json_default).encode("utf-8"), dtype=np.uint8)
     buf = io.BytesIO()
     np.savez(buf, **payload)
-    _atomic_write(path, buf.getvalue())
+    atomic_write(path, buf.getvalue())
 
 
 def read_meta(path: str) -> tuple[dict, dict]:

@@ -26,7 +26,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ttrl_amd.checkpoint import StoredDataclass, _atomic_write, load_checkpoint
+from ttrl_amd.checkpoint import StoredDataclass, atomic_write, load_checkpoint
 from ttrl_amd.nets.towers import NATURE_CNN
 from ttrl_amd.spaces import ActionSpec, ObsSpec
 
@@ -205,7 +205,7 @@ def export_policy(checkpoint_path: str, out_path: str) -> str:
     payload[META_KEY] = np.frombuffer(json.dumps(meta).encode("utf-8"), dtype=np.uint8)
     buf = io.BytesIO()
     np.savez(buf, **payload)
-    _atomic_write(out_path, buf.getvalue())
+    atomic_write(out_path, buf.getvalue())
     return out_path
 
 
