@@ -151,3 +151,47 @@ def test_ppo_state_round_trips_through_a_file(device, tmp_path):
     finally:
         a.close()
         b.close()
+
+
+def test_recurrent_ppo_state_round_trips_through_a_file(device, tmp_path):
+    """The GRU memories keep the reference's names (`memories.<role>.cell.*`)
+    while the conv tower moves under `encoders.<role>.towers.obs`."""
+    from ttrl_amd import checkpoint as ck
+    from ttrl_amd.algos.ppo import PPOConfig, RecurrentConfig, RecurrentPPOLearner
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_qnet_state, recurrent_ppo_rollout
+
+    T, N, L, Hd, mb, A = 16, 4, 8, 32, 16, 6
+    cfg = PPOConfig(minibatch_size=mb, epochs=2, n_steps=T, recurrent=RecurrentConfig(hidden_size=Hd, seq_len=L))
+    learners = []
+    for seed in (51, 52):
+        lr = RecurrentPPOLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(A), device, cfg=cfg, seed=seed)
+        lr.net.load_state_dict(he_uniform_qnet_state(lr.net, seed + 1))
+        learners.append(lr)
+    a, b = learners
+    try:
+        a.update(recurrent_ppo_rollout(60, T, N, A, L, Hd))
+        b.update(recurrent_ppo_rollout(61, T, N, A, L, Hd))
+        path = str(tmp_path / "rppo.npz")
+        ck.save_checkpoint(path, agent_state=a.state_dict(), obs_spec=a.obs_spec, action_spec=a.action_spec,
+                           level=ck.L1, config=a.cfg, frame=a.frame_count)
+        agent_state = ck.load_checkpoint(path)["agent_state"]
+        names = set(agent_state["net"])
+        assert "encoders.actor.towers.obs.layers.0.weight" in names
+        assert any(k.startswith("memories.actor.cell.") for k in names) and not any("towers" in k and "memories" in k
+                                                                                  for k in names)
+        b.load_state_dict(agent_state)
+        _same_tree(a.state_dict(), b.state_dict())
+        rollout = recurrent_ppo_rollout(62, T, N, A, L, Hd)
+        ma, mb_ = a.update(rollout), b.update(rollout)
+        for k in RecurrentPPOLearner.METRICS:
+            assert ma[k] == mb_[k], k
+        for k, v in a.net.state_dict().items():
+            assert np.array_equal(v, b.net.state_dict()[k]), k
+        with pytest.raises(ValueError, match="configuration differs"):
+            other = a.state_dict()
+            other["config"] = PPOConfig()
+            b.load_state_dict(other)
+    finally:
+        a.close()
+        b.close()
