@@ -2,8 +2,10 @@
 (config: batch 32, 4x84x84 uint8 frames, 6 actions, double DQN, n-step 3,
 prioritized weights, Huber delta 1, Adam lr 6.25e-5 eps 1.5e-4).
 
-Tolerances: rel 1e-4 on Q-values, loss, mean_q, td_abs and Adam-updated
-parameters (max abs error over each tensor relative to its max |value|);
+Tolerances: rel 1e-4 on Q-values, loss, mean_q, td_abs, every gradient
+tensor, Adam-updated parameters (max abs error over each tensor relative to
+its max |value|) and Adam deltas p1 - p0 (relative to the largest delta,
+plus the float32 spacing of the parameter);
 exact next actions wherever the top-two Q gap is decisive; ReLU gates
 adopted from the device only where float64 puts the pre-activation within
 1e-4 of the tensor's RMS of zero."""
@@ -14,6 +16,7 @@ import numpy as np
 import pytest
 
 from tests._dqn_helpers import build_learner, qnet_to_oracle
+from tests._grads import check_deltas, check_grads, grad_state
 
 pytestmark = pytest.mark.gpu
 
@@ -65,9 +68,17 @@ def test_dqn_update_matches_oracle(device, step_mode):
     assert abs(m["mean_q"] - ref["mean_q"]) <= REL * abs(ref["mean_q"])
     assert _rel(m["td_abs"], ref["td_abs"]) < REL
     assert abs(m["grad_norm"] - ref["grad_norm"]) <= REL * ref["grad_norm"]
+    # every gradient tensor, each at rel 1e-4 of its own scale (the
+    # reference checks every parameter gradient by name,
+    # tests/hardware/test_algos_dqn_parity.py:147-152)
+    check_grads(grad_state(learner.online), ref["grads"], REL, "dqn")
     new = learner.online.state_dict()
     for (k, got), want in zip(new.items(), ref["new_params"]):
         assert _rel(np.asarray(got).reshape(want.shape), want) < REL, k
+    # the Adam step itself: p1 - p0 against the oracle's delta at rel 1e-4 of
+    # the delta's scale (lr = 6.25e-5, eps = 1.5e-4: the delta is lr*g/(|g|+eps),
+    # linear in g wherever |g| is below eps)
+    check_deltas(list(online.values()), list(new.values()), ref["new_params"], REL, "dqn")
     learner.close()
 
 

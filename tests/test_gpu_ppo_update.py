@@ -132,14 +132,17 @@ def _flat_like_oracle(state_or_list):
     return body + [np.concatenate([pw, vw], axis=1), np.concatenate([pb.reshape(-1), vb.reshape(-1)])]
 
 
-def test_ppo_minibatch_steps_at_256_match_oracle_step_by_step(device):
+@pytest.mark.parametrize("mode,epochs", [("eager", 1), ("graph", 4)])
+def test_ppo_minibatch_steps_at_256_match_oracle_step_by_step(device, mode, epochs):
     """The Atari PPO shape (8 envs x 128 steps, minibatches of 256, 18
     actions), compared step by step: before every step the oracle takes the
     device's parameters and Adam moments, so each step's arithmetic is
-    checked from an identical state (one epoch of four steps).  The steps run
-    eagerly so each records its ReLU outputs; the oracle adopts the device's
-    gate only where its float64 pre-activation is within 1e-4 of the
-    tensor's RMS of zero (oracle.nets.gate)."""
+    checked from an identical state.  Eager: one epoch of four steps, each
+    recording its ReLU outputs as it runs.  Graph: the whole update, 4 epochs
+    x 4 minibatches, as 16 replays of the captured step; the ReLU outputs are
+    read after each replay from the buffers the capture recorded.  The oracle
+    adopts the device's gate only where its float64 pre-activation is within
+    1e-4 of the tensor's RMS of zero (oracle.nets.gate)."""
     from ttrl_amd.engine import layers as layers_mod
     from oracle.ppo import ppo_minibatch_step, ppo_update
     from ttrl_amd.algos.ppo import PPOConfig, PPOLearner
@@ -147,27 +150,41 @@ def test_ppo_minibatch_steps_at_256_match_oracle_step_by_step(device):
     from ttrl_amd.workloads import he_uniform_qnet_state, ppo_rollout
 
     T, N, mb, A, seed = 128, 8, 256, 18, 31
-    cfg = PPOConfig(minibatch_size=mb, epochs=1, n_steps=T, step_mode="eager")
+    cfg = PPOConfig(minibatch_size=mb, epochs=epochs, n_steps=T, step_mode=mode)
     learner = PPOLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(A), device, cfg=cfg, seed=seed)
     try:
         state = he_uniform_qnet_state(learner.net, seed + 1)
         learner.net.load_state_dict(state)
         rollout = ppo_rollout(seed + 2, T, N, A)
         steps = learner.load_rollout(rollout)
-        assert steps == 4
+        assert steps == 4 * epochs
         # The oracle's own pass, only for its minibatch rows and advantages.
-        ref = ppo_update(_to_oracle(state), rollout, rng=np.random.default_rng(seed), minibatch_size=mb, epochs=1,
-                         lr=cfg.lr, adam_eps=cfg.adam_eps, max_grad_norm=cfg.max_grad_norm)
-        learner.begin_update()
+        ref = ppo_update(_to_oracle(state), rollout, rng=np.random.default_rng(seed), minibatch_size=mb,
+                         epochs=epochs, lr=cfg.lr, adam_eps=cfg.adam_eps, max_grad_norm=cfg.max_grad_norm)
+        captured = None
+        if mode == "graph":
+            layers_mod.RECORD = []
+            try:
+                learner.begin_update()  # warm-up pass, then the capture: the last four records are the graph's
+                captured = list(layers_mod.RECORD[-4:])
+            finally:
+                layers_mod.RECORD = None
+            assert learner._graph is not None
+        else:
+            learner.begin_update()
         for t in range(steps):
             params0 = _to_oracle(learner.net.state_dict())
             S0, V0 = _adam_state(learner)
-            layers_mod.RECORD = []
-            try:
+            if captured is not None:
                 learner.run_steps(1)
-                recs = [y.numpy() for y in layers_mod.RECORD[-4:]]
-            finally:
-                layers_mod.RECORD = None
+                recs = [y.numpy() for y in captured]
+            else:
+                layers_mod.RECORD = []
+                try:
+                    learner.run_steps(1)
+                    recs = [y.numpy() for y in layers_mod.RECORD[-4:]]
+                finally:
+                    layers_mod.RECORD = None
             shapes = [(mb, 20, 20, 32), (mb, 9, 9, 64), (mb, 7, 7, 64), (mb, 512)]
             gates = {n: y.reshape(sh) > 0 for n, y, sh in zip(("conv0", "conv1", "conv2", "fc0"), recs, shapes)}
             got_metrics = learner._res.ring.numpy()[t]

@@ -5,7 +5,9 @@ Gaussian, learned temperature with target entropy -3, three Adams at lr 3e-4,
 Polyak tau 0.005).
 
 Tolerance rel 1e-4 (max abs error over a tensor relative to its max |value|)
-on losses, q_target, logp, gradient norms and every updated parameter; ReLU
+on losses, q_target, logp, gradient norms, every gradient tensor of the
+policy and both critics, the temperature gradient and every updated
+parameter; ReLU
 gates adopted from the device only inside the 1e-4 RMS band; Adam with
 eps 1e-8 turns a gradient of either sign into a step of size lr, so updated
 parameters whose oracle gradient lies below the fp32 resolution of its
@@ -17,6 +19,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from tests._grads import check_grads, grad_of, grad_state
 from tests._sac_helpers import build_sac, record_gates, sac_to_oracle
 
 pytestmark = pytest.mark.gpu
@@ -65,6 +68,13 @@ def test_sac_update_matches_oracle(device, step_mode):
         assert abs(m[key] - ref[key]) <= REL * max(abs(ref[key]), 1e-6), (key, m[key], ref[key])
     assert _rel(m["q_target"], ref["q_target"]) < REL
     assert _rel(m["logp"], ref["logp"]) < REL
+    # every gradient tensor at rel 1e-4 of its own scale: the policy's from
+    # the actor region, the critics' from the critic region (the actor region
+    # leaves the critic gradients alone), and d alpha_loss / d log_alpha
+    check_grads(grad_state(learner.nets.policy), ref["policy_grads"], REL, "policy")
+    check_grads(grad_state(learner.nets.critics), ref["critic_grads"], REL, "critics")
+    g_alpha = float(grad_of(learner.log_alpha).reshape(-1)[0])
+    assert abs(g_alpha - ref["d_log_alpha"]) <= REL * max(abs(ref["d_log_alpha"]), 1e-6)
     lr = 3e-4
     _check_params(learner.nets.policy.state_dict(), ref["new_policy"], ref["policy_grads"], lr, "policy")
     crit_flat = [x for c in ref["new_critics"] for pair in c for x in pair]
