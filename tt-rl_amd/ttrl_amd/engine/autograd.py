@@ -2,10 +2,11 @@
 
 Same contract as the reference tape (ttrl/engine/autograd.py:30-271): a
 `Tensor` node holds `data`, `requires_grad`, `grad`, a `_backward(grad)`
-closure and its `_parents`; `backward()` seeds 1.0 on a scalar, walks an
-iterative post-order DFS once, accumulates fp32 gradients, and releases the
-tape in a `finally`.  It refuses a non-scalar root, a second pass and a root
-with no tape, with the reference's messages.
+closure and its `_parents`; `backward()` seeds 1.0 on a scalar, runs every
+closure once, each after all of its node's gradient has accumulated (in
+fp32), and releases the tape afterwards even on failure.  It refuses a
+non-scalar root, a second pass and a root with no tape, with the
+reference's messages (its tests match them).
 
 Two MI355X-side additions, invisible to callers:
 * a gradient may be written by a kernel straight into its final buffer:
@@ -179,6 +180,14 @@ class Tensor:
         return Tensor(self.data, requires_grad=False)
 
     def backward(self):
+        """Run every recorded backward closure once, from this scalar root.
+
+        Order: a node runs only after every node that consumes it has run
+        (all of its gradient contributions have arrived).  Each reachable
+        node's count of reachable consumers is taken in one sweep; the walk
+        then pops ready nodes from a stack and releases a parent when its
+        count reaches zero.  The tape is torn down in a `finally`, so saved
+        activations go whether the walk finished or raised."""
         if not self.requires_grad:
             raise RuntimeError(
                 "backward() called on a Tensor that requires no gradient; it "
@@ -192,30 +201,14 @@ class Tensor:
                 "does not keep saved activations alive for a second pass "
                 "(no retain_graph). Build a fresh forward pass instead."
             )
-        topo: list[Tensor] = []
-        seen: set[int] = set()
-        stack: list[tuple[Tensor, bool]] = [(self, False)]
-        while stack:
-            node, expanded = stack.pop()
-            if expanded:
-                topo.append(node)
-                continue
-            if id(node) in seen:
-                continue
-            seen.add(id(node))
-            stack.append((node, True))
-            for parent in node._parents:
-                if id(parent) not in seen:
-                    stack.append((parent, False))
-        numel = 1
-        for dim in self.shape:
-            numel *= dim
+        numel = int(np.prod(self.shape, dtype=np.int64))
         if numel != 1:
             raise RuntimeError(
                 f"backward() called on a non-scalar Tensor with shape {self.shape} "
                 f"(numel={numel}); there is no `gradient=` kwarg to seed a "
                 "non-scalar backward pass, so reduce to a scalar first."
             )
+        order = _consumers_first(self)
         seed = DeviceArray(self.device, self.shape)
         if self._op in UNIT_SEED_OPS:
             seed.unit = True  # the root's backward reads only the flag: no fill launch
@@ -224,53 +217,77 @@ class Tensor:
         self.grad = seed
         self._grad_owned = True
         try:
-            for node in reversed(topo):
-                grad = node.grad
-                if grad is not None:
-                    if node._backward_done and node is not self:
-                        raise RuntimeError(
-                            "backward() reached a node whose tape was already "
-                            "consumed by a previous backward() call on a graph "
-                            "sharing this subgraph; reusing a consumed subgraph "
-                            "is not supported (no retain_graph)."
-                        )
-                    node._backward(grad)
+            for node in order:
+                if node.grad is None:
+                    continue
+                if node._backward_done and node is not self:
+                    raise RuntimeError(
+                        "backward() reached a node whose tape was already "
+                        "consumed by a previous backward() call on a graph "
+                        "sharing this subgraph; reusing a consumed subgraph "
+                        "is not supported (no retain_graph)."
+                    )
+                node._backward(node.grad)
         finally:
-            for node in topo:
-                if node._op:
-                    node._backward_done = True
+            for node in order:
+                # Leaves begin the next step's graph: only op nodes are spent.
+                node._backward_done = node._backward_done or bool(node._op)
                 node._backward = _no_backward
                 node._parents = ()
 
-    # -- operators ---------------------------------------------------------
 
-    def __add__(self, other):
-        from ttrl_amd.engine.ops.elementwise import add
-        return add(self, other)
+def _consumers_first(root: Tensor) -> list:
+    """Nodes reachable from `root`, each after all of its reachable consumers."""
+    pending: dict[int, int] = {}
+    frontier, reached = [root], {id(root)}
+    while frontier:
+        for parent in frontier.pop()._parents:
+            key = id(parent)
+            pending[key] = pending.get(key, 0) + 1
+            if key not in reached:
+                reached.add(key)
+                frontier.append(parent)
+    order, ready = [], [root]
+    while ready:
+        node = ready.pop()
+        order.append(node)
+        for parent in node._parents:
+            key = id(parent)
+            pending[key] -= 1
+            if pending[key] == 0:
+                ready.append(parent)
+    return order
 
-    __radd__ = __add__
 
-    def __mul__(self, other):
-        from ttrl_amd.engine.ops.elementwise import mul
-        return mul(self, other)
+# Python operators -> (op name in ttrl_amd.engine.ops.elementwise, operands swapped)
+_OPERATORS = {
+    "__add__": ("add", False), "__radd__": ("add", True),
+    "__sub__": ("sub", False), "__rsub__": ("sub", True),
+    "__mul__": ("mul", False), "__rmul__": ("mul", True),
+    "__truediv__": ("div", False),
+}
 
-    __rmul__ = __mul__
 
-    def __sub__(self, other):
-        from ttrl_amd.engine.ops.elementwise import sub
-        return sub(self, other)
+def _operator(op_name: str, swapped: bool):
+    def method(self, other):
+        from ttrl_amd.engine.ops import elementwise
 
-    def __rsub__(self, other):
-        from ttrl_amd.engine.ops.elementwise import sub
-        return sub(other, self)
+        fn = getattr(elementwise, op_name)
+        return fn(other, self) if swapped else fn(self, other)
 
-    def __neg__(self):
-        from ttrl_amd.engine.ops.elementwise import mul
-        return mul(self, -1.0)
+    method.__name__ = op_name
+    return method
 
-    def __truediv__(self, other):
-        from ttrl_amd.engine.ops.elementwise import div
-        return div(self, other)
+
+def _negate(self):
+    from ttrl_amd.engine.ops.elementwise import mul
+
+    return mul(self, -1.0)
+
+
+for _dunder, (_op_name, _swapped) in _OPERATORS.items():
+    setattr(Tensor, _dunder, _operator(_op_name, _swapped))
+Tensor.__neg__ = _negate
 
 
 def backward(tensor: Tensor) -> None:

@@ -1,152 +1,127 @@
 """Binary elementwise arithmetic: add, sub, mul, div
-(ttrl/engine/ops/elementwise.py:15-148).  A python-scalar operand goes to the
-kernel as an argument; tensor operands broadcast, and the backward sums the
-gradient back over every broadcast axis."""
+(ttrl/engine/ops/elementwise.py:15-148).
+
+Every op is one entry of `_OPS`; `_arith` builds the node for any of them.
+
+* Tensor (op) Tensor: the broadcast kernel of the entry, and a backward made
+  of the entry's two partials, each folded back onto its operand's shape
+  (`sum_to_shape`).
+* Tensor (op) scalar, scalar (op) Tensor: the scalar travels as a kernel
+  argument, so the op is an affine map of the tensor operand, y = t + c,
+  y = c - t, y = t * c or y = t / c; its backward is the same map's slope
+  applied to the upstream gradient (`_SLOPE`).  No scalar is ever
+  materialised as a device tensor.
+"""
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import numpy as np
+
 from ttrl_amd.engine.autograd import Tensor, _detached, _is_scalar, _needs
 from ttrl_amd.engine.ops import _kernels as K
-from ttrl_amd.engine.ops.broadcast import _reduce_broadcast_grad
+from ttrl_amd.engine.ops.broadcast import sum_to_shape
+
+__all__ = ["add", "sub", "mul", "div"]
+
+# d y / d t of each affine kernel y = f(t; c), applied to an upstream gradient.
+_SLOPE: dict[str, Callable] = {
+    "add_s": lambda g, c: g,
+    "rsub_s": lambda g, c: K.unary("neg", g),
+    "mul_s": lambda g, c: K.unary("mul_s", g, c),
+    "div_s": lambda g, c: K.unary("div_s", g, c),
+}
 
 
-def _as_tensor(x, like: Tensor) -> Tensor:
-    if isinstance(x, Tensor):
-        return x
-    return Tensor(K.full_like(like.data, float(x)), requires_grad=False)
+@dataclass(frozen=True)
+class _Op:
+    name: str
+    kernel: str
+    # tensor (op) c  ->  (affine kernel, its constant)
+    with_rhs: Callable[[float], tuple]
+    # c (op) tensor  ->  (affine kernel, its constant), None if unsupported
+    with_lhs: Optional[Callable[[float], tuple]]
+    # partials of y = a (op) b, each (g, a, b, y) -> contribution at the output shape
+    d_lhs: Callable
+    d_rhs: Callable
 
 
-def add(a: Tensor, b) -> Tensor:
-    if _is_scalar(b):
-        y = K.unary("add_s", a.data, float(b))
-        if not _needs(a):
-            return _detached(y)
-        out = Tensor(y, True, (a,), "add")
+_OPS = {
+    "add": _Op("add", "add", lambda c: ("add_s", c), lambda c: ("add_s", c),
+               lambda g, a, b, y: g, lambda g, a, b, y: g),
+    "sub": _Op("sub", "sub", lambda c: ("add_s", -c), lambda c: ("rsub_s", c),
+               lambda g, a, b, y: g, lambda g, a, b, y: K.unary("neg", g)),
+    "mul": _Op("mul", "mul", lambda c: ("mul_s", c), lambda c: ("mul_s", c),
+               lambda g, a, b, y: K.binary("mul", g, b), lambda g, a, b, y: K.binary("mul", g, a)),
+    # y = a / b: dy/da = 1/b, dy/db = -y/b
+    "div": _Op("div", "div", lambda c: ("div_s", c), None,
+               lambda g, a, b, y: K.binary("div", g, b),
+               lambda g, a, b, y: K.binary("mul", g, K.unary("neg", K.binary("div", y, b)))),
+}
 
-        def _backward_scalar(grad):
-            if a.requires_grad:
-                a._accumulate(grad)
 
-        out._backward = _backward_scalar
-        return out
-    b = _as_tensor(b, a)
-    y = K.binary("add", a.data, b.data)
-    if not _needs(a, b):
+def _number(x) -> bool:
+    """A python number, or a numpy scalar / 0-d array (read as its value)."""
+    return _is_scalar(x) or (isinstance(x, (np.generic, np.ndarray)) and np.ndim(x) == 0)
+
+
+def _affine(op: _Op, t: Tensor, kernel: str, c: float) -> Tensor:
+    y = K.unary(kernel, t.data, c)
+    if not _needs(t):
         return _detached(y)
-    out = Tensor(y, True, (a, b), "add")
+    out = Tensor(y, True, (t,), op.name)
+    slope = _SLOPE[kernel]
 
     def _backward(grad):
-        if a.requires_grad:
-            a._accumulate(_reduce_broadcast_grad(grad, a.shape))
-        if b.requires_grad:
-            b._accumulate(_reduce_broadcast_grad(grad, b.shape))
+        t._accumulate(slope(grad, c))
 
     out._backward = _backward
     return out
+
+
+def _arith(name: str, a, b) -> Tensor:
+    op = _OPS[name]
+    a_is_t, b_is_t = isinstance(a, Tensor), isinstance(b, Tensor)
+    if a_is_t and _number(b):
+        kernel, c = op.with_rhs(float(b))
+        return _affine(op, a, kernel, c)
+    if b_is_t and _number(a):
+        if op.with_lhs is None:
+            raise TypeError(f"{name}: a python number on the left of a Tensor is not supported; "
+                            f"got {type(a).__name__} {name} Tensor")
+        kernel, c = op.with_lhs(float(a))
+        return _affine(op, b, kernel, c)
+    if not (a_is_t and b_is_t):
+        raise TypeError(f"{name}: operands must be Tensors, or one Tensor and one python number; "
+                        f"got {type(a).__name__} and {type(b).__name__}")
+    y = K.binary(op.kernel, a.data, b.data)
+    if not _needs(a, b):
+        return _detached(y)
+    out = Tensor(y, True, (a, b), name)
+    a_data, b_data = a.data, b.data
+
+    def _backward(grad):
+        for t, partial in ((a, op.d_lhs), (b, op.d_rhs)):
+            if t.requires_grad:
+                t._accumulate(sum_to_shape(partial(grad, a_data, b_data, y), t.shape))
+
+    out._backward = _backward
+    return out
+
+
+def add(a, b) -> Tensor:
+    return _arith("add", a, b)
 
 
 def sub(a, b) -> Tensor:
-    if isinstance(a, Tensor) and _is_scalar(b):
-        y = K.unary("add_s", a.data, -float(b))
-        if not _needs(a):
-            return _detached(y)
-        out = Tensor(y, True, (a,), "sub")
-
-        def _backward_scalar(grad):
-            if a.requires_grad:
-                a._accumulate(grad)
-
-        out._backward = _backward_scalar
-        return out
-    if isinstance(b, Tensor) and _is_scalar(a):
-        y = K.unary("rsub_s", b.data, float(a))
-        if not _needs(b):
-            return _detached(y)
-        out = Tensor(y, True, (b,), "sub")
-
-        def _backward_rscalar(grad):
-            if b.requires_grad:
-                b._accumulate(K.unary("neg", grad))
-
-        out._backward = _backward_rscalar
-        return out
-    if not isinstance(a, Tensor) or not isinstance(b, Tensor):
-        raise TypeError(f"sub expects Tensor operands or one scalar, got {type(a)} and {type(b)}")
-    y = K.binary("sub", a.data, b.data)
-    if not _needs(a, b):
-        return _detached(y)
-    out = Tensor(y, True, (a, b), "sub")
-
-    def _backward(grad):
-        if a.requires_grad:
-            a._accumulate(_reduce_broadcast_grad(grad, a.shape))
-        if b.requires_grad:
-            b._accumulate(_reduce_broadcast_grad(K.unary("neg", grad), b.shape))
-
-    out._backward = _backward
-    return out
+    return _arith("sub", a, b)
 
 
-def mul(a: Tensor, b) -> Tensor:
-    if _is_scalar(b):
-        s = float(b)
-        y = K.unary("mul_s", a.data, s)
-        if not _needs(a):
-            return _detached(y)
-        out = Tensor(y, True, (a,), "mul")
-
-        def _backward_scalar(grad):
-            if a.requires_grad:
-                a._accumulate(K.unary("mul_s", grad, s))
-
-        out._backward = _backward_scalar
-        return out
-    b = _as_tensor(b, a)
-    y = K.binary("mul", a.data, b.data)
-    if not _needs(a, b):
-        return _detached(y)
-    out = Tensor(y, True, (a, b), "mul")
-    a_data, b_data = a.data, b.data
-
-    def _backward(grad):
-        if a.requires_grad:
-            a._accumulate(_reduce_broadcast_grad(K.binary("mul", grad, b_data), a.shape))
-        if b.requires_grad:
-            b._accumulate(_reduce_broadcast_grad(K.binary("mul", grad, a_data), b.shape))
-
-    out._backward = _backward
-    return out
+def mul(a, b) -> Tensor:
+    return _arith("mul", a, b)
 
 
-def div(a: Tensor, b) -> Tensor:
-    if _is_scalar(b):
-        s = float(b)
-        y = K.unary("div_s", a.data, s)
-        if not _needs(a):
-            return _detached(y)
-        out = Tensor(y, True, (a,), "div")
-
-        def _backward_scalar(grad):
-            if a.requires_grad:
-                a._accumulate(K.unary("div_s", grad, s))
-
-        out._backward = _backward_scalar
-        return out
-    b = _as_tensor(b, a)
-    y = K.binary("div", a.data, b.data)
-    if not _needs(a, b):
-        return _detached(y)
-    out = Tensor(y, True, (a, b), "div")
-    a_data, b_data = a.data, b.data
-
-    def _backward(grad):
-        if a.requires_grad:
-            a._accumulate(_reduce_broadcast_grad(K.binary("div", grad, b_data), a.shape))
-        if b.requires_grad:
-            # d/db (a/b) = -a/b^2
-            q = K.binary("div", a_data, K.binary("mul", b_data, b_data))
-            gb = K.binary("mul", grad, K.unary("neg", q))
-            b._accumulate(_reduce_broadcast_grad(gb, b.shape))
-
-    out._backward = _backward
-    return out
+def div(a, b) -> Tensor:
+    return _arith("div", a, b)

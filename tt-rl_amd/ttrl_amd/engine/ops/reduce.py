@@ -4,7 +4,7 @@ from __future__ import annotations
 
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs
 from ttrl_amd.engine.ops import _kernels as K
-from ttrl_amd.engine.ops.broadcast import _broadcast_grad_to
+from ttrl_amd.engine.ops.broadcast import expand_to
 from ttrl_amd.engine.ops.elementwise import mul
 
 
@@ -18,7 +18,7 @@ def sum_all(a: Tensor) -> Tensor:
 
     def _backward(grad):
         if a.requires_grad:
-            a._accumulate(_broadcast_grad_to(grad.reshape((1,) * len(like.shape)), like))
+            a._accumulate(expand_to(grad.reshape((1,) * len(like.shape)), like.shape))
 
     out._backward = _backward
     return out
@@ -44,7 +44,7 @@ def sum_dim(a: Tensor, dim: int, keepdim: bool = True) -> Tensor:
             return
         if not keepdim:
             grad = grad.reshape(tuple(like.shape[:d]) + (1,) + tuple(like.shape[d + 1:]))
-        a._accumulate(_broadcast_grad_to(grad, like))
+        a._accumulate(expand_to(grad, like.shape))
 
     out._backward = _backward
     return out
