@@ -182,3 +182,33 @@ def test_state_keys_take_the_reference_names_and_come_back(towers, prefix, ours)
     for k in ("head.q.weight", "policy.head.heads.mean.weight", "heads.policy.logits.weight"):
         if k in state:
             assert k in ref  # heads already carry the reference's names
+
+
+def test_validate_compares_a_reference_config_field_by_field():
+    """A reference-written config (a StoredDataclass) is compared on every
+    field that maps onto this learner's config; dispatch-only and unmapped
+    fields are carried (ttrl/algos/checkpoint.py:107-115 refuses any change)."""
+    from ttrl_amd.algos.dqn import DQNConfig
+    from ttrl_amd.algos.state import validate
+    from ttrl_amd.checkpoint import StoredDataclass
+
+    cfg = DQNConfig(lr=6.25e-5, gamma=0.99, n_step=3, prioritized=True)
+    base = {"online": {}, "target": {}, "optimizer": {}, "frame_count": 0, "update_count": 0, "rng_state": {}}
+
+    def state(fields):
+        out = dict(base)
+        out["config"] = StoredDataclass("ttrl.algos.dqn.config:DQNConfig", fields)
+        return out
+
+    kw = dict(algo="DQN", config=cfg, weight_keys=("online", "target"),
+              run_keys=("optimizer", "frame_count", "update_count", "rng_state"))
+    ok = {"gamma": 0.99, "n_step": 3, "lr": 6.25e-5, "double": True, "step_mode": "traced_fwd_bwd",
+          "buffer_capacity": 100000, "priority": {"alpha": 0.6}, "encoder_kwargs": {}}
+    assert validate(state(ok), weights_only=False, **kw) is True
+    for field, value in (("gamma", 0.9), ("n_step", 1), ("lr", 1e-3), ("double", False),
+                         ("target_sync_interval", 1), ("priority", None), ("batch_size", 64)):
+        with pytest.raises(ValueError, match="configuration differs") as e:
+            validate(state(dict(ok, **{field: value})), weights_only=False, **kw)
+        assert field in str(e.value)
+        with pytest.raises(ValueError, match="configuration differs"):
+            validate(state(dict(ok, **{field: value})), weights_only=True, **kw)

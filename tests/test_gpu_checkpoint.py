@@ -73,8 +73,17 @@ def test_dqn_state_round_trips_through_a_file(device, tmp_path):
         b.load_state_dict(weights, weights_only=True)
 
         foreign = a.state_dict()
-        foreign["config"] = ck.StoredDataclass("ttrl.algos.dqn.config:DQNConfig", {"double": True})
-        b.load_state_dict(foreign)  # a reference config is carried, the weights are checked by shape
+        # a reference config whose mapped fields agree loads (its dispatch mode and
+        # its unmapped fields are carried); one that differs in a mapped field does not
+        foreign["config"] = ck.StoredDataclass("ttrl.algos.dqn.config:DQNConfig", {
+            "double": True, "gamma": a.cfg.gamma, "lr": a.cfg.lr, "step_mode": "traced_fwd_bwd",
+            "train_freq": 4, "priority": {"alpha": 0.6}})
+        b.load_state_dict(foreign)
+        for field, value in (("gamma", 0.5), ("n_step", 5), ("target_sync_interval", 10), ("priority", None)):
+            changed = a.state_dict()
+            changed["config"] = ck.StoredDataclass("ttrl.algos.dqn.config:DQNConfig", {"double": True, field: value})
+            with pytest.raises(ValueError, match="configuration differs"):
+                b.load_state_dict(changed)
         other = a.state_dict()
         other["config"] = type(a.cfg)(lr=1e-3)
         with pytest.raises(ValueError, match="configuration differs"):

@@ -3,10 +3,14 @@ copies) and a RUN half (optimizer moments, counters, the sampling RNG), with
 the reference's marker for a weights-only state and its loading rules
 (ttrl/algos/checkpoint.py:31-129).
 
-The config is compared when it is one of this package's configs.  A config
-read from a reference checkpoint (a `StoredDataclass` of a `ttrl.` class) is
-carried, not compared: the weights it came with are checked against this
-learner's networks by name and shape instead.
+The config is compared as the reference compares it (any difference
+refuses the load, ttrl/algos/checkpoint.py:107-115).  A config read from a
+reference checkpoint (a `StoredDataclass` of a `ttrl.` class) is compared
+field by field wherever a stored field maps onto a field of this learner's
+config: the same name, or the reference's `priority` record against this
+config's `prioritized` flag.  Fields that only choose how a step is
+dispatched (`step_mode`, `act_mode`) are not compared, and stored fields
+with no counterpart here are carried.
 """
 
 from __future__ import annotations
@@ -85,6 +89,40 @@ def _config_diff(saved, current) -> str:
     return f"{len(names)} field(s) differ: checkpoint was written with {was}; this learner has {now}"
 
 
+# Fields that choose how an update is dispatched, not what it computes.
+_DISPATCH_ONLY = frozenset({"step_mode", "act_mode"})
+
+
+def _plain(value):
+    """A stored value in comparable form (JSON lists back to tuples)."""
+    if isinstance(value, (list, tuple)):
+        return tuple(_plain(v) for v in value)
+    return value
+
+
+def _foreign_diff(saved: StoredDataclass, current) -> list:
+    """[(field, stored, current)] of mapped fields whose values differ."""
+    if not dataclasses.is_dataclass(current):
+        return []
+    mine = {f.name: getattr(current, f.name) for f in dataclasses.fields(current)}
+    out = []
+    for name, stored in saved.fields.items():
+        if name in _DISPATCH_ONLY:
+            continue
+        if name == "priority" and "prioritized" in mine:
+            if (stored is not None) != bool(mine["prioritized"]):
+                out.append(("priority", stored, mine["prioritized"]))
+            continue
+        if name not in mine or isinstance(stored, (dict, StoredDataclass)):
+            continue
+        have = mine[name]
+        if dataclasses.is_dataclass(have) or isinstance(have, dict):
+            continue
+        if _plain(stored) != _plain(have):
+            out.append((name, stored, have))
+    return out
+
+
 def validate(state: dict, *, algo: str, config, weight_keys: tuple, run_keys: tuple, weights_only: bool) -> bool:
     """Check `state` against what `algo` needs; True when its run half is to
     be loaded (ttrl/algos/checkpoint.py:72-129)."""
@@ -101,7 +139,15 @@ def validate(state: dict, *, algo: str, config, weight_keys: tuple, run_keys: tu
     if missing:
         raise ValueError(f"{algo}.load_state_dict: state is missing {missing}.")
     saved = state[CONFIG_KEY]
-    if not isinstance(saved, StoredDataclass) and saved != config:
+    if isinstance(saved, StoredDataclass):
+        diff = _foreign_diff(saved, config)
+        if diff:
+            was = ", ".join(f"{n}={a!r}" for n, a, _ in diff)
+            now = ", ".join(f"{n}={b!r}" for n, _, b in diff)
+            raise ValueError(f"{algo}.load_state_dict: this learner's configuration differs from the state's "
+                             f"({saved.path}): {len(diff)} field(s) differ: the state was written with {was}; this "
+                             f"learner has {now}. Loading would change the algorithm mid-run.")
+    elif saved != config:
         raise ValueError(f"{algo}.load_state_dict: this learner's configuration differs from the state's. "
                          f"{_config_diff(saved, config)}.")
     return not (carries_weights_only or weights_only)
