@@ -472,6 +472,11 @@ int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, con
  * device. */
 int ttrl_replay_update_priorities(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
                                   const float* priorities);
+/* The same update from float64 priorities (host values, whose
+ * (|p| + eps) ** alpha the reference computes in float64,
+ * ttrl/buffers/sampling.py:180-193). */
+int ttrl_replay_update_priorities_f64(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane,
+                                      const int* col, const double* priorities);
 
 #ifdef __cplusplus
 }

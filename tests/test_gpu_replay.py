@@ -104,10 +104,11 @@ def test_prioritized_batches_and_updates_match_the_oracle(device):
         got = buf.sample(64, beta=0.4 + 0.1 * round_)
         want = orc.sample(64, beta=0.4 + 0.1 * round_)
         _same(got.host(), want)
-        td = rng.uniform(0.0, 5.0, 64).astype(np.float32)
+        td = rng.uniform(0.0, 5.0, 64)
         if round_ % 2:
-            buf.update_priorities(want["lanes"], want["cols"], td)
+            buf.update_priorities(want["lanes"], want["cols"], td)  # float64 end to end
         else:
+            td = td.astype(np.float32)  # TD errors an update left on the device
             dev_td = DeviceArray(device, (64,), np.float32)
             dev_td.upload(td)
             buf.update_priorities_device(got, dev_td)
@@ -120,6 +121,13 @@ def test_prioritized_batches_and_updates_match_the_oracle(device):
         buf.sample(8)
     with pytest.raises(ValueError, match="NaN or infinite"):
         buf.update_priorities([0], [0], [np.nan])
+    # a non-finite TD error from the device path is caught by the next draw
+    got = buf.sample(8, beta=0.5)
+    bad = DeviceArray(device, (8,), np.float32)
+    bad.upload(np.array([1.0, np.nan, 2.0, 3.0, 1.0, 1.0, 1.0, 1.0], np.float32))
+    buf.update_priorities_device(got, bad)
+    with pytest.raises(ValueError, match="NaN or infinite"):
+        buf.sample(8, beta=0.5)
 
 
 def test_a_batch_lands_in_the_learner_inputs(device):

@@ -311,9 +311,12 @@ __global__ __launch_bounds__(kReplayThreads) void k_replay_assemble(
   if (succ) copy_row(next_out + long(b) * r.obs_bytes, succ, r.obs_bytes);
 }
 
+// The priorities arrive as float32 (TD errors an update left on the device)
+// or float64 (host priorities, kept in the reference's float64).
+template <typename P>
 __global__ __launch_bounds__(kReplayThreads) void k_replay_priorities(Ring r, int n, const int* __restrict__ lane,
                                                                       const int* __restrict__ col,
-                                                                      const float* __restrict__ prio) {
+                                                                      const P* __restrict__ prio) {
   __shared__ double red[kReplayThreads];
   double mx = 0.0;
   for (int b = threadIdx.x; b < n; b += kReplayThreads) {
@@ -424,16 +427,34 @@ int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, con
   return check_launch("ttrl_replay_assemble");
 }
 
+}  // extern "C"
+
+namespace {
+
+template <typename P>
+int update_priorities(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
+                      const P* priorities, const char* name) {
+  int rc = check_ring(ring, name);
+  if (rc) return rc;
+  TTRL_REQUIRE(ctx && ring->weight && ring->max_priority && lane && col && priorities, "%s: null argument", name);
+  if (n <= 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_replay_priorities<P>, dim3(1), dim3(kReplayThreads), 0, stream_of(ctx), ring_of(ring), n,
+                     lane, col, priorities);
+  return check_launch(name);
+}
+
+}  // namespace
+
+extern "C" {
+
 int ttrl_replay_update_priorities(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
                                   const float* priorities) {
-  int rc = check_ring(ring, "ttrl_replay_update_priorities");
-  if (rc) return rc;
-  TTRL_REQUIRE(ctx && ring->weight && ring->max_priority && lane && col && priorities,
-               "ttrl_replay_update_priorities: null argument");
-  if (n <= 0) return TTRL_OK;
-  hipLaunchKernelGGL(k_replay_priorities, dim3(1), dim3(kReplayThreads), 0, stream_of(ctx), ring_of(ring), n, lane,
-                     col, priorities);
-  return check_launch("ttrl_replay_update_priorities");
+  return update_priorities(ctx, ring, n, lane, col, priorities, "ttrl_replay_update_priorities");
+}
+
+int ttrl_replay_update_priorities_f64(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane,
+                                      const int* col, const double* priorities) {
+  return update_priorities(ctx, ring, n, lane, col, priorities, "ttrl_replay_update_priorities_f64");
 }
 
 }  // extern "C"

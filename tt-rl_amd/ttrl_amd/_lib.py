@@ -130,6 +130,7 @@ SIGNATURES = {
     "ttrl_replay_is_weights": ([P, I, P, P, I, C.c_long, C.c_double, P], I),
     "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P], I),
     "ttrl_replay_update_priorities": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
+    "ttrl_replay_update_priorities_f64": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),
     "ttrl_sac_sample_backward": ([P, I, I, P, P, P, P, P, P, P, F, F, P, F], I),
     "ttrl_sac_critic_loss": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),

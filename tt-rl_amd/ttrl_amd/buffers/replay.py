@@ -366,6 +366,11 @@ class ReplayBuffer:
             dev.call("ttrl_replay_lane_sums", C.byref(self._ring), d["start"].vp, d["count"].vp, PICK_CHUNK,
                      self._max_chunks, self._csum.vp, self._sums.vp)
             sums = self._sums.numpy()
+            if not np.all(np.isfinite(sums)):
+                # A non-finite TD error written by update_priorities_device
+                # (the host path refuses it on entry) poisons its lane's sum.
+                raise ValueError("ReplayBuffer.sample: a priority is NaN or infinite (written by a device "
+                                 "priority update since the last sample)")
             if sums.sum() <= 0.0:
                 raise RuntimeError(f"replay: {total} transitions are sampleable but every priority in the "
                                    f"sampleable runs is zero")
@@ -439,10 +444,10 @@ class ReplayBuffer:
         self._draw_put("lanes", lanes)
         self._draw_put("cols", cols)
         self._draw.upload(self._draw_host)
-        prio = DeviceArray(self.device, (n,), np.float32)
-        prio.upload(p.astype(np.float32))
+        prio = DeviceArray(self.device, (n,), np.float64)  # float64 end to end, as the reference
+        prio.upload(p)
         d = self._draw_in
-        self.device.call("ttrl_replay_update_priorities", C.byref(self._ring), n, d["lanes"].vp, d["cols"].vp,
+        self.device.call("ttrl_replay_update_priorities_f64", C.byref(self._ring), n, d["lanes"].vp, d["cols"].vp,
                          prio.vp)
 
     def update_priorities_device(self, batch: DeviceBatch, priorities: DeviceArray) -> None:
