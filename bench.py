@@ -100,7 +100,7 @@ def bench_dqn(dev, steps, warmup, ring_n, mode="graph"):
     learner.online.load_state_dict(he_uniform_qnet_state(learner.online, 1))
     learner.target.copy_from(learner.online)
     block = learner.inputs["_block"]
-    ring = _ring(dev, block, lambda r: learner.load_batch(dqn_batch(1000 + r)), ring_n)
+    ring = _ring(dev, block, lambda r: (learner.load_batch(dqn_batch(1000 + r)), learner.step.flush_inputs()), ring_n)
     learner.update()  # captures the graph and runs the first update
     step = learner.step.replay if mode == "graph" else learner.step.run
     wall, gpu = _time_steps(dev, step, ring, block, steps, warmup)
@@ -119,7 +119,7 @@ def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
     learner.nets.critics.load_state_dict(crit)
     learner.nets.targets.load_state_dict(crit)
     block = learner.batch.block
-    ring = _ring(dev, block, lambda r: learner.batch.load_batch(sac_batch(2000 + r)), ring_n)
+    ring = _ring(dev, block, lambda r: (learner.batch.load_batch(sac_batch(2000 + r)), learner.batch.flush()), ring_n)
     learner.update()  # eager first update
     learner.update()  # captured graph, first replay
     step = learner.replay if mode == "graph" else learner._run

@@ -89,6 +89,14 @@ int ttrl_graph_launch_n(ttrl_ctx* ctx, ttrl_graph* g, int n);
  * ttrl/algos/sac/agent.py:118-121. */
 int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_host, size_t in_bytes,
                     void* out_host, const void* out_dev, size_t out_bytes);
+/* Pinned host memory owned by the context (freed by ttrl_host_free or at
+ * shutdown).  When both host buffers of ttrl_graph_step lie in such blocks
+ * the step copies from and to them directly: one H2D, the replay, one D2H
+ * and one wait.  Replaces the wide-row staging buffer of InputBinder
+ * (ttrl/engine/step/inputs.py:28-102) and the packed metric read of
+ * read_metrics (ttrl/engine/step/metrics.py:22-30). */
+int ttrl_host_alloc(ttrl_ctx* ctx, size_t bytes, void** out);
+int ttrl_host_free(ttrl_ctx* ctx, void* ptr);
 int ttrl_graph_nodes(ttrl_graph* g, size_t* out);
 int ttrl_graph_destroy(ttrl_graph* g);
 

@@ -66,6 +66,8 @@ struct ttrl_ctx {
   // Pinned host staging of ttrl_graph_step: inputs first, outputs after.
   unsigned char* pinned = nullptr;
   size_t pinned_bytes = 0;
+  // Pinned host blocks handed out by ttrl_host_alloc (base -> bytes).
+  std::unordered_map<void*, size_t> host_blocks;
 };
 
 struct ttrl_graph {
@@ -247,6 +249,7 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
   if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+  for (auto& hb : ctx->host_blocks) (void)hipHostFree(hb.first);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return TTRL_OK;
@@ -457,6 +460,49 @@ int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g) {
   return TTRL_OK;
 }
 
+int ttrl_host_alloc(ttrl_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return set_error(TTRL_EINVAL, "ttrl_host_alloc: null argument");
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
+  if (e != hipSuccess) return hip_error(e, "hipHostMalloc (ttrl_host_alloc)");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  ctx->host_blocks[p] = bytes ? bytes : 1;
+  *out = p;
+  return TTRL_OK;
+}
+
+int ttrl_host_free(ttrl_ctx* ctx, void* ptr) {
+  if (!ctx) return set_error(TTRL_EINVAL, "ttrl_host_free: null ctx");
+  if (!ptr) return TTRL_OK;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  auto it = ctx->host_blocks.find(ptr);
+  if (it == ctx->host_blocks.end()) return set_error(TTRL_EINVAL, "ttrl_host_free: %p was not allocated here", ptr);
+  // A copy from or to the block may still be queued on the stream.
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipHostFree(ptr);
+  ctx->host_blocks.erase(it);
+  return TTRL_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// True when [p, p + bytes) lies inside one block of ttrl_host_alloc.
+bool in_host_block(ttrl_ctx* ctx, const void* p, size_t bytes) {
+  const char* c = static_cast<const char*>(p);
+  std::lock_guard<std::mutex> g(ctx->mu);
+  for (auto& hb : ctx->host_blocks) {
+    const char* base = static_cast<const char*>(hb.first);
+    if (c >= base && c + bytes <= base + hb.second) return true;
+  }
+  return false;
+}
+
+}  // namespace
+
+extern "C" {
+
 int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_host, size_t in_bytes,
                     void* out_host, const void* out_dev, size_t out_bytes) {
   if (!ctx) return set_error(TTRL_EINVAL, "ttrl_graph_step: null ctx");
@@ -464,6 +510,24 @@ int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_h
     return set_error(TTRL_EINVAL, "ttrl_graph_step: null buffer with a nonzero size");
   if (g && !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_step: destroyed graph");
   if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_step: the stream is capturing");
+  // Host buffers from ttrl_host_alloc are pinned already: the copies read
+  // and write them in place, with no staging pass.
+  const bool in_pinned = in_bytes && in_host_block(ctx, in_host, in_bytes);
+  const bool out_pinned = out_bytes && in_host_block(ctx, out_host, out_bytes);
+  if (in_pinned && out_pinned) {
+    hipError_t e;
+    e = hipMemcpyAsync(in_dev, in_host, in_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (graph step)");
+    if (g) {
+      e = hipGraphLaunch(g->exec, ctx->stream);
+      if (e != hipSuccess) return hip_error(e, "hipGraphLaunch (graph step)");
+    }
+    e = hipMemcpyAsync(out_host, out_dev, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync D2H (graph step)");
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize (graph step)");
+    return TTRL_OK;
+  }
   const size_t out_at = (in_bytes + 255) & ~size_t(255);
   const size_t need = out_at + out_bytes;
   if (need > ctx->pinned_bytes) {

@@ -102,6 +102,8 @@ SIGNATURES = {
     "ttrl_graph_launch": ([P, P], I),
     "ttrl_graph_launch_n": ([P, P, I], I),
     "ttrl_graph_step": ([P, P, P, P, SZ, P, P, SZ], I),
+    "ttrl_host_alloc": ([P, SZ, C.POINTER(P)], I),
+    "ttrl_host_free": ([P, P], I),
     "ttrl_graph_nodes": ([P, C.POINTER(SZ)], I),
     "ttrl_graph_destroy": ([P], I),
     "ttrl_timer_start": ([P], I),

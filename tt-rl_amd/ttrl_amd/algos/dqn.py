@@ -179,13 +179,15 @@ def q_forward_multi(nets, inputs, tape_group: int | None = 0, *, skip_last: bool
 
 
 def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_n: int = 0, double: bool = True,
-                huber_delta: float = 1.0, prioritized: bool = False, grad_sq: bool = True) -> dict:
+                huber_delta: float = 1.0, prioritized: bool = False, grad_sq: bool = True,
+                metrics_out: dict | None = None) -> dict:
     """One DQN update body: Huber loss against the n-step double-Q target,
     backward, metrics.  Reads only `inputs`; no host reads (capturable).
 
     The online forward on s (with tape), the online forward on s' and the
     target forward on s' (both constants of the step) run as one grouped
-    launch per layer."""
+    launch per layer.  `metrics_out` may name the device arrays `loss`,
+    `mean_q` and `td_abs` are written to."""
     (leaf,) = tuple(leaves)
     obs = inputs[leaf_key("obs", leaf)]
     next_obs = inputs[leaf_key("next_obs", leaf)]
@@ -198,7 +200,8 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
         heads = [_lockstep_layers([n])[0][-1] for n in nets]
         loss, extra, qs = dqn_head_td_loss(features, heads, inputs["actions_onehot"], inputs["rewards"],
                                            inputs["dones"], inputs["discounts"],
-                                           inputs["is_weights"] if prioritized else None, huber_delta)
+                                           inputs["is_weights"] if prioritized else None, huber_delta,
+                                           out=metrics_out)
         if layers_mod.RECORD is not None:
             layers_mod.RECORD.append(list(qs))
         return _finish_update(online, loss, extra, prioritized, grad_sq)
@@ -215,7 +218,7 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
             selector = online(next_obs) if double else next_target_q
     loss, extra = dqn_td_loss(q, selector, next_target_q, inputs["actions_onehot"], inputs["rewards"],
                               inputs["dones"], inputs["discounts"],
-                              inputs["is_weights"] if prioritized else None, huber_delta)
+                              inputs["is_weights"] if prioritized else None, huber_delta, out=metrics_out)
     return _finish_update(online, loss, extra, prioritized, grad_sq)
 
 
@@ -267,6 +270,14 @@ class DQNLearner:
         if target_state is not None:
             self.target.load_state_dict(target_state)
         self.optimizer = Adam(list(self.online.parameters()), lr=cfg.lr, eps=cfg.adam_eps)
+        # Every metric of an update in one device block, read back with one
+        # copy: [loss, mean_q, grad_sq, -, td_abs[B]].
+        B = cfg.batch_size
+        self._metric_block = DeviceArray(device, (4 + B,))
+        self._metric_block.fill(0.0)
+        self._metrics_out = {"loss": self._metric_block.view(0, (1, 1)), "mean_q": self._metric_block.view(1, (1, 1)),
+                             "td_abs": self._metric_block.view(4, (B, 1))}
+        self.optimizer.grad_sq = self._metric_block.view(2, (1, 1))
         self.inputs = step_inputs(obs_spec, device, batch=cfg.batch_size, num_actions=self.num_actions,
                                   prioritized=cfg.prioritized)
         self.step = TrainStep(self._step_fn, self.inputs, device, optimizer=self.optimizer, mode=cfg.step_mode)
@@ -337,13 +348,15 @@ class DQNLearner:
     def _step_fn(self, inputs: dict) -> dict:
         metrics = update_loss(self.online, self.target, inputs, leaves=(self.obs_spec.name,),
                               num_actions=self.num_actions, double=self.cfg.double,
-                              huber_delta=self.cfg.huber_delta, prioritized=self.cfg.prioritized, grad_sq=False)
+                              huber_delta=self.cfg.huber_delta, prioritized=self.cfg.prioritized, grad_sq=False,
+                              metrics_out=self._metrics_out)
         # Adam reduces sum(g^2) over the same gradients in its own launch.
         metrics["grad_sq"] = Tensor(self.optimizer.grad_sq)
         return metrics
 
     def load_batch(self, batch: dict) -> None:
-        """Upload one replay batch into the bound buffers."""
+        """Stage one replay batch for the bound buffers (written into the
+        step's pinned host image; the next update sends it with one copy)."""
         leaf = self.obs_spec.name
         step = self.step
         step.load_input(leaf_key("obs", leaf), batch["obs"])

@@ -112,9 +112,10 @@ class _HubOutput(Tensor):
 
 
 def squashed_sample(head: Tensor, noise: Tensor, scale: ActionScale, log_std_min: float = -20.0,
-                    log_std_max: float = 2.0):
+                    log_std_max: float = 2.0, logp_out: DeviceArray | None = None):
     """One-kernel reparameterised sample from packed [mean | log_std] rows
-    (log_std already clamped).  -> (action (B, d), logp (B, 1))."""
+    (log_std already clamped).  -> (action (B, d), logp (B, 1)).  `logp_out`
+    may give the (B, 1) array the log-probabilities are written to."""
     B, two_d = (int(s) for s in head.shape)
     d = two_d // 2
     if two_d != 2 * d or tuple(noise.shape) != (B, d):
@@ -124,7 +125,9 @@ def squashed_sample(head: Tensor, noise: Tensor, scale: ActionScale, log_std_min
         raise ValueError("squashed_sample needs the device-resident bounds; construct ActionScale with a device")
     centre, half = scale._centre.data, scale._scale.data
     action = DeviceArray(dev, (B, d))
-    logp = DeviceArray(dev, (B, 1))
+    if logp_out is not None and (logp_out.numel != B or logp_out.dtype != np.float32):
+        raise ValueError(f"squashed_sample: logp_out must hold {B} float32 values")
+    logp = DeviceArray(dev, (B, 1)) if logp_out is None else logp_out.reshape((B, 1))
     u = DeviceArray(dev, (B, d))
     dev.call("ttrl_sac_sample", B, d, head.data.vp, noise.data.vp, centre.vp, half.vp, C.c_float(scale.log_det),
              action.vp, logp.vp, u.vp)

@@ -37,6 +37,7 @@ from ttrl_amd.engine.layers import Linear, ReLU
 from ttrl_amd.engine.ops import _kernels as K
 from ttrl_amd.engine.ops.fused import grad_targets
 from ttrl_amd.engine.optim import Adam
+from ttrl_amd.engine.step import InputBinder, MetricReader
 from ttrl_amd.engine.tensor import DeviceArray, ParamArena, bound_block
 from ttrl_amd.engine.trace import capture
 from ttrl_amd.nets.build import build_sac_nets
@@ -218,18 +219,29 @@ class TwinQ:
 
 # ---------------------------------------------------------------- losses ---
 
+def _out_array(out: dict | None, name: str, dev, shape) -> DeviceArray:
+    """out[name] reshaped to `shape` when the caller supplies it, else a new array."""
+    a = (out or {}).get(name)
+    if a is None:
+        return DeviceArray(dev, shape)
+    if a.numel != int(np.prod(shape)) or a.dtype != np.float32:
+        raise ValueError(f"SAC loss: out[{name!r}] must hold {int(np.prod(shape))} float32 values")
+    return a.reshape(shape)
+
+
 def sac_critic_loss(q: Tensor, q_next_target: Tensor, logp_next: Tensor, log_alpha: Tensor, rewards: Tensor,
-                    dones: Tensor, discounts: Tensor, is_weights: Tensor | None = None):
+                    dones: Tensor, discounts: Tensor, is_weights: Tensor | None = None, out: dict | None = None):
     """critic_loss of ttrl/algos/sac/losses.py:46-76 as one kernel.
 
-    -> (loss (1, 1) differentiable in q, metrics {q_target, td_abs, alpha})."""
+    -> (loss (1, 1) differentiable in q, metrics {q_target, td_abs, alpha}).
+    `out` may supply the arrays loss, q_target, td_abs and alpha go to."""
     B = int(q.shape[1])
     dev = q.device
-    loss = DeviceArray(dev, (1, 1))
-    q_target = DeviceArray(dev, (B, 1))
+    loss = _out_array(out, "loss", dev, (1, 1))
+    q_target = _out_array(out, "q_target", dev, (B, 1))
     dq = DeviceArray(dev, (2, B, 1))
-    td_abs = DeviceArray(dev, (B, 1))
-    alpha = DeviceArray(dev, (1, 1))
+    td_abs = _out_array(out, "td_abs", dev, (B, 1))
+    alpha = _out_array(out, "alpha", dev, (1, 1))
     dev.call("ttrl_sac_critic_loss", B, q.data.vp, q_next_target.data.vp, logp_next.data.vp, log_alpha.data.vp,
              rewards.data.vp, dones.data.vp, discounts.data.vp, None if is_weights is None else is_weights.data.vp,
              loss.vp, q_target.vp, dq.vp, td_abs.vp, alpha.vp)
@@ -246,13 +258,14 @@ def sac_critic_loss(q: Tensor, q_next_target: Tensor, logp_next: Tensor, log_alp
 
 
 def sac_actor_losses(q_pi: Tensor, logp: Tensor, log_alpha: Tensor, target_entropy: float,
-                     learn_alpha: bool = True):
+                     learn_alpha: bool = True, out: dict | None = None):
     """actor_loss and alpha_loss (ttrl/algos/sac/losses.py:79-94) as one
-    kernel.  -> (actor_loss, alpha_loss | None), each (1, 1)."""
+    kernel.  -> (actor_loss, alpha_loss | None), each (1, 1).  `out` may
+    supply the arrays actor_loss and alpha_loss go to."""
     B = int(q_pi.shape[1])
     dev = q_pi.device
-    la = DeviceArray(dev, (1, 1))
-    lalpha = DeviceArray(dev, (1, 1))
+    la = _out_array(out, "actor_loss", dev, (1, 1))
+    lalpha = _out_array(out, "alpha_loss", dev, (1, 1))
     dq = DeviceArray(dev, (2, B, 1))
     g_logp = DeviceArray(dev, (B, 1))
     d_log_alpha = DeviceArray(dev, (1, 1))
@@ -309,13 +322,21 @@ class _BatchBuffers:
         arrays, self.block = bound_block(device, specs)
         self.tensors = {name: Tensor(arr) for name, arr in arrays.items()}
         self.B = B
+        # staged in a pinned image of the block, sent as one copy per update
+        self.binder = InputBinder(device, dict(self.tensors, _block=self.block))
 
     def __getitem__(self, key):
         return self.tensors[key]
 
     def load(self, name, array):
-        t = self.tensors[name]
-        t.data.upload(np.asarray(array, np.float32).reshape(t.shape))
+        self.binder.load(name, np.asarray(array, np.float32))
+
+    def flush(self):
+        """Send what was loaded since the last update (one copy for a batch)."""
+        self.binder.flush()
+
+    def close(self):
+        self.binder.close()
 
     def load_batch(self, batch: dict):
         B = self.B
@@ -357,6 +378,20 @@ class SACLearner:
         self.twin = TwinQ(self.nets.critics)
         self.twin_targets = TwinQ(self.nets.targets)
         self.batch = _BatchBuffers(device, cfg.batch_size, obs_spec.size, action_spec.dim, cfg.prioritized)
+        # Every metric of an update in one device block, read back with one copy:
+        # [critic_loss, alpha, actor_loss, alpha_loss, critic_grad_sq, actor_grad_sq, -, -,
+        #  q_target[B], logp[B], td_abs[B]].
+        B = cfg.batch_size
+        blk = DeviceArray(device, (8 + 3 * B,))
+        blk.fill(0.0)
+        self._metric_block = blk
+        self._critic_out = {"loss": blk.view(0, (1, 1)), "alpha": blk.view(1, (1, 1)),
+                            "q_target": blk.view(8, (B, 1)), "td_abs": blk.view(8 + 2 * B, (B, 1))}
+        self._actor_out = {"actor_loss": blk.view(2, (1, 1)), "alpha_loss": blk.view(3, (1, 1))}
+        self._logp_out = blk.view(8 + B, (B, 1))
+        self.critic_opt.grad_sq = blk.view(4, (1, 1))
+        self.actor_opt.grad_sq = blk.view(5, (1, 1))
+        self._reader = MetricReader(device)
         self._graph = None
         self._graph_metrics = None
         self._pool = None
@@ -430,7 +465,7 @@ class SACLearner:
             q_next = self.twin_targets.forward(b["next_obs"], a_next)
         q = self.twin.forward(obs_action=b["obs_actions"])
         loss, m = sac_critic_loss(q, q_next, logp_next, self.log_alpha, b["rewards"], b["dones"], b["discounts"],
-                                  b["is_weights"] if self.cfg.prioritized else None)
+                                  b["is_weights"] if self.cfg.prioritized else None, out=self._critic_out)
         loss.backward()
         out = {"critic_loss": loss, "alpha": m["alpha"], "q_target": m["q_target"]}
         if self.cfg.prioritized:
@@ -440,9 +475,10 @@ class SACLearner:
     def _actor_region(self) -> dict:
         b = self.batch
         head = policy_packed(self.nets.policy, b["obs"])
-        action, logp = squashed_sample(head, b["noise"], self.scale)
+        action, logp = squashed_sample(head, b["noise"], self.scale, logp_out=self._logp_out)
         q_pi = self.twin.forward(b["obs"], action, train_params=False)
-        actor, dual = sac_actor_losses(q_pi, logp, self.log_alpha, self.target_entropy, self.cfg.learn_alpha)
+        actor, dual = sac_actor_losses(q_pi, logp, self.log_alpha, self.target_entropy, self.cfg.learn_alpha,
+                                       out=self._actor_out)
         actor.backward()
         out = {"actor_loss": actor, "logp": Tensor(logp.data)}
         if dual is not None:
@@ -469,23 +505,46 @@ class SACLearner:
         return metrics
 
     def _run(self) -> dict:
+        """One update; -> its metrics, read from the device."""
+        binder = self.batch.binder
         if self.cfg.step_mode == "eager":
-            return self._body()
+            binder.flush()
+            metrics = self._body()
+            self._reader.bind(metrics)
+            return self._reader.read(metrics)
         dev = self.device
         if self._graph is None:
             # First update runs eagerly (warming the pool), then the body is
             # captured; later updates replay it.
+            binder.flush()
             self._pool = dev.create_pool()
             with dev.use_pool(self._pool):
                 metrics = self._body()
                 dev.synchronize()
                 self._graph, self._graph_metrics = capture(dev, self._body)
-            return metrics
-        self.replay()
-        return self._graph_metrics
+            self._reader.bind(self._graph_metrics)
+            return self._reader.read(metrics)
+        span = self._reader.span
+        sent = binder.take_single_range() if span is not None else None
+        if sent is None:
+            self.replay()
+            return self._reader.read(self._graph_metrics)
+        # One call: the batch in, the replay, the metric block out, one wait.
+        b, e = sent
+        ptr, n, _ = span
+        dev.call("ttrl_graph_step", self._graph._graph, C.c_void_p(binder.block.ptr + b),
+                 C.c_void_p(binder.image.ptr + b), C.c_size_t(e - b), C.c_void_p(self._reader.image.ptr),
+                 C.c_void_p(ptr), C.c_size_t(n))
+        self._replayed()
+        return self._reader._unpack(self._graph_metrics)
 
     def replay(self) -> None:
+        """Launch the captured update without reading metrics (benchmark loop)."""
+        self.batch.flush()
         self._graph.replay()
+        self._replayed()
+
+    def _replayed(self) -> None:
         for opt in (self.critic_opt, self.actor_opt) + ((self.alpha_opt,) if self.cfg.learn_alpha else ()):
             opt._replayed()
 
@@ -494,7 +553,7 @@ class SACLearner:
             self.batch.load_batch(batch)
         out = self._run()
         self.update_count += 1
-        return self.summarize({k: v.numpy() if isinstance(v, Tensor) else v for k, v in out.items()})
+        return self.summarize(out)
 
     def summarize(self, m: dict) -> dict:
         """The reference's metric keys (ttrl/algos/sac/step.py:115-130)."""
@@ -519,6 +578,8 @@ class SACLearner:
 
     def close(self) -> None:
         self._acting.close()
+        self.batch.close()
+        self._reader.close()
         if self._graph is not None:
             self._graph.close()
             self._graph = None

@@ -14,7 +14,7 @@ from contextlib import contextmanager
 
 from ttrl_amd import _lib
 
-__all__ = ["Device", "acquire", "device_count", "NoDeviceAvailable"]
+__all__ = ["Device", "HostBlock", "acquire", "device_count", "NoDeviceAvailable"]
 
 
 class NoDeviceAvailable(RuntimeError):
@@ -70,6 +70,10 @@ class Device:
             return
         _lib.lib().ttrl_free(self.ctx, C.c_void_p(ptr))
 
+    def host_block(self, nbytes: int) -> "HostBlock":
+        """Pinned host memory owned by this context (see `HostBlock`)."""
+        return HostBlock(self, nbytes)
+
     def create_pool(self) -> int:
         pid = C.c_int(0)
         self.call("ttrl_pool_create", C.byref(pid))
@@ -112,6 +116,42 @@ class Device:
 
     def __repr__(self) -> str:
         return f"Device({self.index}{', closed' if self.closed else ''})"
+
+
+class HostBlock:
+    """Pinned host memory from the device context (ttrl_host_alloc).
+
+    `array` is a uint8 numpy view of it.  Copies between it and device memory
+    read and write it in place (no staging pass), which makes it the host
+    image of a bound input block or a metrics block.  The block owns the
+    memory: views of `array` must not outlive it."""
+
+    def __init__(self, dev: Device, nbytes: int):
+        import numpy as np
+
+        self.dev = dev
+        self.nbytes = max(1, int(nbytes))
+        ptr = C.c_void_p()
+        dev.call("ttrl_host_alloc", C.c_size_t(self.nbytes), C.byref(ptr))
+        self.ptr = int(ptr.value)
+        self.array = np.frombuffer((C.c_uint8 * self.nbytes).from_address(self.ptr), dtype=np.uint8)
+
+    def view(self, offset: int, shape, dtype):
+        """A typed numpy view `offset` bytes into the block."""
+        import numpy as np
+
+        return np.ndarray(shape, dtype=dtype, buffer=self.array, offset=int(offset))
+
+    def close(self) -> None:
+        ptr, self.ptr = self.ptr, 0
+        if ptr and not self.dev.closed:
+            _lib.lib().ttrl_host_free(self.dev.ctx, C.c_void_p(ptr))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 _DEFAULT: dict[int, Device] = {}

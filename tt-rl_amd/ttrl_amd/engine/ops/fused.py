@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import ctypes as C
 
+import numpy as np
+
 from ttrl_amd import _lib
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs, relu_mask
 from ttrl_amd.engine.tensor import DeviceArray
@@ -117,12 +119,14 @@ def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, 
 
 def dqn_td_loss(q: Tensor, q_next_select: Tensor, q_next_value: Tensor, actions_onehot: Tensor,
                 rewards: Tensor, dones: Tensor, discounts: Tensor, is_weights: Tensor | None,
-                delta: float):
+                delta: float, out: dict | None = None):
     """The DQN update head as one kernel (ttrl/algos/dqn/losses.py:96-129).
 
     -> (loss, metrics) where loss is a (1, 1) tape node differentiable in `q`
     and metrics holds detached `mean_q`, `td_abs` (B, 1), `td_target` (B, 1)
-    and `next_actions` (B, 1, float indices).
+    and `next_actions` (B, 1, float indices).  `out` may supply the arrays
+    `loss`, `mean_q` and `td_abs` are written to (views of one packed metrics
+    block, read back with one copy).
     """
     B, A = (int(d) for d in q.shape)
     for name, t, shape in (("q_next_select", q_next_select, (B, A)), ("q_next_value", q_next_value, (B, A)),
@@ -135,7 +139,7 @@ def dqn_td_loss(q: Tensor, q_next_select: Tensor, q_next_value: Tensor, actions_
     if not delta > 0.0:
         raise ValueError(f"dqn_td_loss: huber delta must be > 0, got {delta}")
     dev = q.device
-    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A)
+    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A, out)
     dev.call("ttrl_dqn_loss", B, A, q.data.vp, q_next_select.data.vp, q_next_value.data.vp,
              actions_onehot.data.vp, rewards.data.vp, dones.data.vp, discounts.data.vp,
              None if is_weights is None else is_weights.data.vp, C.c_float(delta), loss.vp, mean_q.vp,
@@ -143,8 +147,20 @@ def dqn_td_loss(q: Tensor, q_next_select: Tensor, q_next_value: Tensor, actions_
     return _dqn_loss_node(q, loss, mean_q, td_abs, td_target, next_act, dq)
 
 
-def _dqn_outputs(dev, B: int, A: int):
-    return (DeviceArray(dev, (1, 1)), DeviceArray(dev, (1, 1)), DeviceArray(dev, (B, 1)), DeviceArray(dev, (B, 1)),
+def _dqn_outputs(dev, B: int, A: int, out: dict | None = None):
+    """loss, mean_q, td_abs (caller-supplied when `out` names them),
+    td_target, next_actions, dq."""
+    out = out or {}
+
+    def given(name, shape):
+        a = out.get(name)
+        if a is None:
+            return DeviceArray(dev, shape)
+        if a.numel != int(np.prod(shape)) or a.dtype != np.float32:
+            raise ValueError(f"DQN loss: out[{name!r}] must hold {int(np.prod(shape))} float32 values")
+        return a.reshape(shape)
+
+    return (given("loss", (1, 1)), given("mean_q", (1, 1)), given("td_abs", (B, 1)), DeviceArray(dev, (B, 1)),
             DeviceArray(dev, (B, 1)), DeviceArray(dev, (B, A)))
 
 
@@ -172,7 +188,7 @@ def _dqn_loss_node(q: Tensor, loss, mean_q, td_abs, td_target, next_act, dq):
 
 
 def dqn_head_td_loss(features, heads, actions_onehot: Tensor, rewards: Tensor, dones: Tensor, discounts: Tensor,
-                     is_weights: Tensor | None, delta: float):
+                     is_weights: Tensor | None, delta: float, out: dict | None = None):
     """The Q head's last linear layer over 2 or 3 feature sets and the DQN
     loss in one launch (ttrl_dqn_head): features[0] = online(s) (taped),
     features[1] = online(s') selecting a* (double) or target(s'),
@@ -198,7 +214,7 @@ def dqn_head_td_loss(features, heads, actions_onehot: Tensor, rewards: Tensor, d
     dev = features[0].device
     weights = [h.effective_weight() for h in heads]
     qs = [DeviceArray(dev, (B, A)) for _ in range(G)]
-    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A)
+    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A, out)
     dev.call("ttrl_dqn_head", B, K, A, G, _lib.ptrs(f.data.ptr for f in features), _lib.ptrs(w.data.ptr for w in weights),
              _lib.ptrs(None if h.bias is None else h.bias.data.ptr for h in heads), _lib.ptrs(q.ptr for q in qs),
              actions_onehot.data.vp, rewards.data.vp, dones.data.vp, discounts.data.vp,

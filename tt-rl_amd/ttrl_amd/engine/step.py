@@ -22,12 +22,15 @@ from __future__ import annotations
 
 from typing import Callable
 
+import ctypes as C
+
 import numpy as np
 
 from ttrl_amd.engine.autograd import Tensor
+from ttrl_amd.engine.tensor import DeviceArray
 from ttrl_amd.engine.trace import capture
 
-__all__ = ["MODES", "StepFn", "TrainStep", "read_metrics", "InputBinder"]
+__all__ = ["MODES", "StepFn", "TrainStep", "read_metrics", "InputBinder", "MetricReader"]
 
 StepFn = Callable[[dict], dict]
 
@@ -35,24 +38,135 @@ MODES = ("eager", "traced_fwd_bwd", "graph")
 
 
 class InputBinder:
-    """Copies fresh host data into bound input buffers, never rebinding them."""
+    """Writes fresh host data into the bound input buffers, never rebinding
+    them (ttrl/engine/step/inputs.py:16-102).
+
+    Inputs that are views of one bound block (`inputs["_block"]`, laid out
+    by `bound_block`) are staged in a pinned host image of that block:
+    `load` writes into the image only, and `flush` sends every range loaded
+    since the last flush, adjacent ranges coalesced, so a full batch is one
+    host-to-device copy.  Ranges not loaded are never sent, so device-side
+    writes into the block (a replay draw assembling a batch in place) are
+    not overwritten by stale host data.  Other inputs upload directly."""
 
     def __init__(self, device, inputs: dict):
         self.device = device
         self.inputs = inputs
+        self.block = inputs.get("_block")
+        self.image = None
+        self._views: dict = {}
+        self._ranges: dict = {}
+        self._dirty: set = set()
+        if self.block is not None and isinstance(self.block, DeviceArray):
+            self.image = device.host_block(self.block.nbytes)
+            for name, t in inputs.items():
+                d = getattr(t, "data", None)
+                if name.startswith("_") or not isinstance(d, DeviceArray) or not d.same_storage(self.block):
+                    continue
+                off = d.offset - self.block.offset
+                self._views[name] = self.image.view(off, d.shape, d.dtype)
+                self._ranges[name] = (off, off + d.nbytes)
 
     def load(self, name: str, array) -> None:
         t = self.inputs[name]
         arr = np.asarray(array)
-        want = t.data.dtype
-        if arr.dtype != want:
-            arr = arr.astype(want)
         if arr.size != t.data.numel:
             raise ValueError(f"load_input({name!r}): {arr.shape} does not fit the bound buffer {t.shape}")
-        t.data.upload(arr)
+        view = self._views.get(name)
+        if view is None:
+            t.data.upload(arr.astype(t.data.dtype, copy=False))
+            return
+        np.copyto(view, arr.reshape(view.shape), casting="unsafe")
+        self._dirty.add(name)
+
+    def pending(self) -> list:
+        """[(begin, end)] byte ranges of the block loaded since the last
+        flush, adjacent or overlapping ranges merged."""
+        spans = sorted(self._ranges[n] for n in self._dirty)
+        out: list = []
+        for b, e in spans:
+            if out and b <= out[-1][1] + 256:  # bound_block aligns inputs to 256 bytes
+                out[-1] = (out[-1][0], max(out[-1][1], e))
+            else:
+                out.append((b, e))
+        return out
+
+    def flush(self) -> None:
+        for b, e in self.pending():
+            self.device.call("ttrl_h2d", C.c_void_p(self.block.ptr + b), C.c_void_p(self.image.ptr + b),
+                             C.c_size_t(e - b))
+        self._dirty.clear()
+
+    def take_single_range(self):
+        """The one pending range (begin, end) when exactly one is pending,
+        clearing it (the caller sends it), else None."""
+        spans = self.pending()
+        if len(spans) != 1:
+            return None
+        self._dirty.clear()
+        return spans[0]
 
     def close(self) -> None:
-        pass
+        if self.image is not None:
+            self.image.close()
+            self.image = None
+            self._views.clear()
+
+
+class MetricReader:
+    """Reads a step's metrics (ttrl/engine/step/metrics.py:22-112).
+
+    When every tensor metric is a view of one device allocation, one copy of
+    the span covering them lands in a pinned host image and each metric is
+    sliced out of it; otherwise each tensor is read on its own."""
+
+    def __init__(self, device):
+        self.device = device
+        self.image = None
+        self.span = None  # (device ptr, nbytes, {name: (offset, shape, dtype)})
+
+    def bind(self, metrics: dict | None):
+        self.span = None
+        tensors = {k: v.data for k, v in (metrics or {}).items() if isinstance(v, Tensor)}
+        if not tensors:
+            return
+        arrays = list(tensors.values())
+        block = arrays[0].block
+        if any(a.block is not block for a in arrays):
+            return
+        lo = min(a.ptr for a in arrays)
+        hi = max(a.ptr + a.nbytes for a in arrays)
+        if self.image is None or self.image.nbytes < hi - lo:
+            if self.image is not None:
+                self.image.close()
+            self.image = self.device.host_block(hi - lo)
+        self.span = (lo, hi - lo, {k: (a.ptr - lo, a.shape, a.dtype) for k, a in tensors.items()})
+
+    def _unpack(self, metrics: dict) -> dict:
+        ptr, n, layout = self.span
+        out = {}
+        for k, v in metrics.items():
+            if k in layout:
+                off, shape, dtype = layout[k]
+                out[k] = self.image.view(off, shape, dtype).copy()
+            else:
+                out[k] = v
+        return out
+
+    def read(self, metrics: dict | None) -> dict:
+        if not metrics:
+            return {}
+        if self.span is None:
+            return read_metrics(metrics)
+        ptr, n, _ = self.span
+        self.device.call("ttrl_d2h", C.c_void_p(self.image.ptr), C.c_void_p(ptr), C.c_size_t(n))
+        return self._unpack(metrics)
+
+    def close(self) -> None:
+        if self.image is not None:
+            self.image.close()
+            self.image = None
+        self.span = None
 
 
 def read_metrics(metrics: dict | None) -> dict:
@@ -76,6 +190,7 @@ class TrainStep:
         self.mode = mode
         self.cfg = cfg
         self._binder = InputBinder(device, inputs)
+        self._reader = MetricReader(device)
         self._trace = None
         self._trace_metrics: dict | None = None
         self._captured_grads: list = []
@@ -84,22 +199,32 @@ class TrainStep:
     def load_input(self, name: str, array) -> None:
         self._binder.load(name, array)
 
+    def flush_inputs(self) -> None:
+        """Send staged inputs now (the next run would send them anyway)."""
+        self._binder.flush()
+
     def run(self) -> dict:
         if self.mode == "eager":
             return self._run_eager()
         return self._run_graph()
 
     def _run_eager(self) -> dict:
+        self._binder.flush()
         if self.optimizer is not None:
             self.optimizer.zero_grad()
         metrics = self.step_fn(self.inputs)
         if self.optimizer is not None:
             self.optimizer.step()
-        return read_metrics(metrics)
+        self._reader.bind(metrics)
+        return self._reader.read(metrics)
 
     def replay(self) -> None:
         """Launch the captured step without reading metrics (benchmark loop)."""
+        self._binder.flush()
         self._trace.replay()
+        self._after_replay()
+
+    def _after_replay(self) -> None:
         self._rebind_grads()
         if self.optimizer is not None:
             if self.mode == "graph":
@@ -109,10 +234,23 @@ class TrainStep:
 
     def _run_graph(self) -> dict:
         if self._trace is None:
+            self._binder.flush()
             self._capture()
-        else:
+            self._reader.bind(self._trace_metrics)
+            return self._reader.read(self._trace_metrics)
+        span = self._reader.span
+        sent = self._binder.take_single_range() if (span is not None and self.mode == "graph") else None
+        if sent is None:
             self.replay()
-        return read_metrics(self._trace_metrics)
+            return self._reader.read(self._trace_metrics)
+        # One call: the loaded input range in, the replay, the metric span out, one wait.
+        b, e = sent
+        blk, img = self._binder.block, self._binder.image
+        ptr, n, _ = span
+        self.device.call("ttrl_graph_step", self._trace._graph, C.c_void_p(blk.ptr + b), C.c_void_p(img.ptr + b),
+                         C.c_size_t(e - b), C.c_void_p(self._reader.image.ptr), C.c_void_p(ptr), C.c_size_t(n))
+        self._after_replay()
+        return self._reader._unpack(self._trace_metrics)
 
     def _body(self, with_optimizer: bool):
         metrics = self.step_fn(self.inputs)
@@ -155,6 +293,7 @@ class TrainStep:
                 trace.close()
         finally:
             self._binder.close()
+            self._reader.close()
             if self._pool is not None and not self.device.closed:
                 self.device.release_pool(self._pool)
             self._pool = None
