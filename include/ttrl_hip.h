@@ -100,6 +100,19 @@ int ttrl_host_free(ttrl_ctx* ctx, void* ptr);
 int ttrl_graph_nodes(ttrl_graph* g, size_t* out);
 int ttrl_graph_destroy(ttrl_graph* g);
 
+/* The context's table of GEMM plans (tile shape and K split per call
+ * signature), as text: one "cfg bm bn tbk splits kchunk<TAB>signature" line
+ * per entry, sorted.  A plan is otherwise chosen by timing candidates at the
+ * first call of a signature, which can differ between processes and with it
+ * the split-K summation order; importing a saved table makes a second
+ * process run the same plans and produce the same bits.  With buf NULL,
+ * *len receives the size.  Imported plans are checked against each call's
+ * extents before use (an invalid one is re-planned).  No reference
+ * counterpart: ttnn's program cache (ttrl/engine/step/core.py:44-141) holds
+ * compiled kernels, not tuning choices. */
+int ttrl_plans_export(ttrl_ctx* ctx, char* buf, size_t cap, size_t* len);
+int ttrl_plans_import(ttrl_ctx* ctx, const char* text, int* count);
+
 /* Stream timer (events on the context's stream). */
 int ttrl_timer_start(ttrl_ctx* ctx);
 int ttrl_timer_stop(ttrl_ctx* ctx, float* ms);
@@ -433,18 +446,23 @@ typedef struct ttrl_replay_ring {
   double* weight;            /* [lanes][cols] or NULL */
   double* max_priority;      /* device scalar or NULL */
   double alpha, epsilon;
+  float* action_vec;         /* [lanes][cols][action_dim] continuous actions, or NULL (index actions) */
+  int action_dim;            /* 1..64 when action_vec is set */
 } ttrl_replay_ring;
 
 /* Write n transitions, entry e into (lane[e], col[e]): obs row e of obs
- * ([n][obs_bytes]), action, reward, terminated and ended flags, and for an
+ * ([n][obs_bytes]), the action (action[e], or row e of action_vec
+ * ([n][action_dim]) for a ring with vector actions, the continuous actions
+ * of SAC's replay), reward, terminated and ended flags, and for an
  * ending entry (final_row[e] >= 0) row e of final_obs into that boundary
  * row; a prioritized ring gives the column the weight (max priority + eps)
  * ** alpha.  Replaces ReplayBuffer._write_slot (ttrl/buffers/replay.py:178-199)
  * and PrioritySampler.on_write (ttrl/buffers/sampling.py:130-133).  All
  * arrays are device arrays. */
 int ttrl_replay_write(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
-                      const int* action, const float* reward, const unsigned char* terminated,
-                      const unsigned char* ended, const int* final_row, const void* obs, const void* final_obs);
+                      const int* action, const float* action_vec, const float* reward,
+                      const unsigned char* terminated, const unsigned char* ended, const int* final_row,
+                      const void* obs, const void* final_obs);
 /* Per-lane sums of the priority weights over each lane's sampleable run
  * (start[l], count[l] in ring order), as chunk sums of `chunk` run positions
  * ([lanes][max_chunks]) and their ordered totals sums[lanes]
@@ -467,12 +485,13 @@ int ttrl_replay_is_weights(ttrl_ctx* ctx, int n, const double* picked_weight, co
  * in float64 cast to float32, terminated flag and gamma ** steps
  * (ttrl/buffers/indexing.py:94-131), the observation and the successor (the
  * next column, or the boundary row of an ending column), the action as an
- * index and/or one-hot row (ttrl/buffers/replaybatch.py:15-76).  Output
- * pointers may be a learner's bound input buffers. */
+ * index and/or one-hot row, or as a [n][action_dim] row of a ring with
+ * vector actions (ttrl/buffers/replaybatch.py:15-76).  Output pointers may
+ * be a learner's bound input buffers. */
 int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
                          int n_step, double gamma, void* obs_out, void* next_obs_out, float* actions_onehot,
-                         int num_actions, int* actions_out, float* rewards_out, float* dones_out,
-                         float* discounts_out);
+                         int num_actions, int* actions_out, float* action_vec_out, float* rewards_out,
+                         float* dones_out, float* discounts_out);
 /* weight[lane[b]][col[b]] = (|priorities[b]| + eps) ** alpha, the last of
  * duplicate columns winning, and *max_priority = max(*max_priority,
  * max |priorities|) (PrioritySampler.update, ttrl/buffers/sampling.py:168-193).

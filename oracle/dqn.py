@@ -46,8 +46,10 @@ def huber(e: np.ndarray, delta: float) -> np.ndarray:
 
 def dqn_update(online: QNet, target: QNet, batch: dict, *, double: bool = True, delta: float = 1.0,
                lr: float = 6.25e-5, eps: float = 1.5e-4, betas=(0.9, 0.999), gates=None,
-               device_next_actions=None, prioritized: bool = True) -> dict:
-    """One update from fresh optimizer state; every array float64."""
+               device_next_actions=None, prioritized: bool = True, adam_state=None, t: int = 1) -> dict:
+    """One update; every array float64.  The Adam step starts from
+    `adam_state` = (S list, V list) in the online parameters' order at update
+    count `t` (1-based), or from zero moments at t = 1."""
     stats = GateStats()
     obs, nxt = batch["obs"], batch["next_obs"]
     actions = np.asarray(batch["actions"]).reshape(-1).astype(np.int64)
@@ -72,14 +74,18 @@ def dqn_update(online: QNet, target: QNet, batch: dict, *, double: bool = True, 
     grads = qnet_backward(online, acts, dq)
     grad_sq = float(sum(np.sum(g * g) for g in grads))
     b1, b2 = betas
-    new = []
-    for p, g in zip(online.flat(), grads):
-        p1, _, _ = adam.fused_step(p, g, np.zeros_like(g), np.zeros_like(g), 1, lr, b1, b2, eps)
+    new, new_S, new_V = [], [], []
+    for i, (p, g) in enumerate(zip(online.flat(), grads)):
+        S0 = np.zeros_like(g) if adam_state is None else np.asarray(adam_state[0][i], np.float64).reshape(g.shape)
+        V0 = np.zeros_like(g) if adam_state is None else np.asarray(adam_state[1][i], np.float64).reshape(g.shape)
+        p1, S1, V1 = adam.fused_step(p, g, S0, V0, t, lr, b1, b2, eps)
         new.append(p1)
+        new_S.append(S1)
+        new_V.append(V1)
     return {
         "q": q, "pred": pred, "q_online_next": q_online_next, "q_target_next": q_target_next,
         "next_actions": a_star, "td_target": y, "loss": loss, "mean_q": float(np.mean(pred)),
         "td_abs": np.abs(e), "dq": dq, "grads": grads, "grad_sq": grad_sq,
-        "grad_norm": float(np.sqrt(grad_sq)), "new_params": new, "gate_stats": stats,
+        "grad_norm": float(np.sqrt(grad_sq)), "new_params": new, "new_S": new_S, "new_V": new_V, "gate_stats": stats,
         "argmax_adopted": adopted,
     }

@@ -34,14 +34,16 @@ import numpy as np
 
 class ReplayOracle:
     def __init__(self, obs_shape, obs_dtype, *, capacity: int, n_envs: int = 1, n_step: int = 1,
-                 gamma: float = 0.99, seed=None, alpha: float | None = None, epsilon: float = 1e-6):
+                 gamma: float = 0.99, seed=None, alpha: float | None = None, epsilon: float = 1e-6,
+                 action_dim: int = 0):
         per_lane = -(-int(capacity) // int(n_envs))
         if per_lane <= n_step + 1:
             raise ValueError("ReplayOracle: a lane must hold more than n_step + 1 columns")
         self.n_envs, self.cols, self.n_step, self.gamma = int(n_envs), per_lane, int(n_step), float(gamma)
         L, C = self.n_envs, per_lane
         self.obs = np.zeros((L, C) + tuple(obs_shape), obs_dtype)
-        self.actions = np.zeros((L, C), np.int64)
+        # index actions, or float32 rows of action_dim for continuous actions
+        self.actions = np.zeros((L, C, action_dim), np.float32) if action_dim else np.zeros((L, C), np.int64)
         self.rewards = np.zeros((L, C), np.float32)
         self.dones = np.zeros((L, C), bool)
         self.ends = np.zeros((L, C), bool)

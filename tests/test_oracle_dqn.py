@@ -128,3 +128,29 @@ def test_huber_gradient_closed_form():
     (quad * quad * 0.5 + (ae - quad)).sum().backward()
     np.testing.assert_allclose(et.grad.numpy(), np.clip(e, -1, 1))
     np.testing.assert_allclose(huber(e, 1.0), np.where(np.abs(e) <= 1, 0.5 * e * e, np.abs(e) - 0.5))
+
+
+def test_three_chained_updates_match_torch_adam():
+    """Threading the oracle's Adam state (S, V, t) through three updates
+    equals torch.optim.Adam (eps 1.5e-4) driving the torch reproduction:
+    pins dqn_update's adam_state / t path, which steps from a learner's
+    saved moments."""
+    net, target = _net(10), _net(11)
+    lr, eps = 6.25e-5, 1.5e-4
+    params = [torch.tensor(a, requires_grad=True) for a in net.flat()]
+    opt = torch.optim.Adam(params, lr=lr, betas=(0.9, 0.999), eps=eps)
+    state, cur = None, net
+    for step in range(1, 4):
+        batch = _batch(20 + step)
+        ref = dqn_update(cur, target, batch, lr=lr, eps=eps, adam_state=state, t=step)
+        opt.zero_grad()
+        tnet = net.with_flat([p.detach().numpy().copy() for p in params])
+        loss, grads, _, _ = _torch_update(tnet, target, batch)
+        assert ref["loss"] == pytest.approx(loss, rel=1e-12)
+        for p, g in zip(params, grads):
+            p.grad = torch.tensor(g)
+        opt.step()
+        for got, want in zip(ref["new_params"], params):
+            np.testing.assert_allclose(got.reshape(want.shape), want.detach().numpy(), rtol=1e-12, atol=1e-15)
+        state = (ref["new_S"], ref["new_V"])
+        cur = net.with_flat(ref["new_params"])

@@ -98,6 +98,17 @@ bool plan_with_splits(int cfg, int M, int N, int K, int groups, long ws_floats, 
   return true;
 }
 
+bool plan_valid(const GemmPlan& p, int M, int N, int K, int groups, long ws_floats, unsigned allowed) {
+  if (p.cfg < 0 || p.cfg >= kNumCfg || !(allowed & (1u << p.cfg))) return false;
+  const TileDims t = tile_dims(p.cfg);
+  if (p.bm != t.bm || p.bn != t.bn || p.tbk != t.tbk) return false;
+  if (p.splits < 1 || p.kchunk < t.tbk || p.kchunk % t.tbk) return false;
+  const int stages = std::max(1, (K + t.tbk - 1) / t.tbk);
+  const int spb = p.kchunk / t.tbk;
+  if (p.splits != (stages + spb - 1) / spb) return false;  // the splits exactly cover K
+  return p.splits == 1 || long(p.splits) * groups * M * N <= ws_floats;
+}
+
 bool gemm_forced(unsigned allowed, int M, int N, int K, int groups, long ws_floats, GemmPlan* out) {
   const char* v = std::getenv("TTRL_GEMM_FORCE");
   if (!v || !*v) return false;

@@ -50,12 +50,15 @@ struct Ring {
   double* weight;
   double* max_priority;
   double alpha, epsilon;
+  float* action_vec;
+  int action_dim;
 };
 
 Ring ring_of(const ttrl_replay_ring* r) {
   return Ring{r->lanes,      r->cols,       r->obs_bytes,  r->obs,        r->actions,
               r->rewards,    r->dones,      r->ends,       r->final_slot, r->final_obs,
-              r->final_rows, r->weight,     r->max_priority, r->alpha,    r->epsilon};
+              r->final_rows, r->weight,     r->max_priority, r->alpha,    r->epsilon,
+              r->action_vec, r->action_vec ? r->action_dim : 0};
 }
 
 // Copy one row of `bytes` bytes with the whole block, 16-byte units when the
@@ -76,6 +79,7 @@ __device__ __forceinline__ void copy_row(unsigned char* dst, const unsigned char
 __global__ __launch_bounds__(kReplayThreads) void k_replay_write(Ring r, int n, const int* __restrict__ lane,
                                                                  const int* __restrict__ col,
                                                                  const int* __restrict__ action,
+                                                                 const float* __restrict__ action_vec,
                                                                  const float* __restrict__ reward,
                                                                  const unsigned char* __restrict__ term,
                                                                  const unsigned char* __restrict__ end,
@@ -90,8 +94,10 @@ __global__ __launch_bounds__(kReplayThreads) void k_replay_write(Ring r, int n, 
   copy_row(r.obs + at * r.obs_bytes, obs + long(e) * r.obs_bytes, r.obs_bytes);
   const bool has_final = f >= 0 && f < r.final_rows;
   if (has_final) copy_row(r.final_obs + long(f) * r.obs_bytes, fin + long(e) * r.obs_bytes, r.obs_bytes);
+  for (int i = threadIdx.x; i < r.action_dim; i += blockDim.x)
+    r.action_vec[at * r.action_dim + i] = action_vec[long(e) * r.action_dim + i];
   if (threadIdx.x == 0) {
-    r.actions[at] = action[e];
+    r.actions[at] = action ? action[e] : 0;
     r.rewards[at] = reward[e];
     r.dones[at] = term[e];
     r.ends[at] = end[e];
@@ -256,8 +262,8 @@ __global__ __launch_bounds__(kReplayThreads) void k_replay_is_weights(int n, con
 __global__ __launch_bounds__(kReplayThreads) void k_replay_assemble(
     Ring r, int n, const int* __restrict__ lane, const int* __restrict__ col, int n_step, double gamma,
     unsigned char* __restrict__ obs_out, unsigned char* __restrict__ next_out, float* __restrict__ onehot, int A,
-    int* __restrict__ actions_out, float* __restrict__ rewards_out, float* __restrict__ dones_out,
-    float* __restrict__ discounts_out) {
+    int* __restrict__ actions_out, float* __restrict__ action_vec_out, float* __restrict__ rewards_out,
+    float* __restrict__ dones_out, float* __restrict__ discounts_out) {
   __shared__ int s_end, s_ok;
   const int b = blockIdx.x;
   if (b >= n) return;
@@ -298,6 +304,9 @@ __global__ __launch_bounds__(kReplayThreads) void k_replay_assemble(
   __syncthreads();
   if (!s_ok) return;
   const long row = long(l) * r.cols;
+  if (action_vec_out)
+    for (int i = threadIdx.x; i < r.action_dim; i += blockDim.x)
+      action_vec_out[long(b) * r.action_dim + i] = r.action_vec[(row + c) * r.action_dim + i];
   copy_row(obs_out + long(b) * r.obs_bytes, r.obs + (row + c) * r.obs_bytes, r.obs_bytes);
   const int e = s_end;
   const unsigned char* succ;
@@ -342,6 +351,8 @@ int check_ring(const ttrl_replay_ring* r, const char* name) {
   TTRL_REQUIRE(r->lanes > 0 && r->cols > 0 && r->obs_bytes > 0 && r->obs_bytes % 4 == 0,
                "%s: bad ring extents (lanes %d, cols %d, obs_bytes %ld)", name, r->lanes, r->cols, r->obs_bytes);
   TTRL_REQUIRE(r->final_rows >= 0 && (r->final_rows == 0 || r->final_obs), "%s: bad boundary pool", name);
+  TTRL_REQUIRE(!r->action_vec || (r->action_dim > 0 && r->action_dim <= 64), "%s: action_dim %d outside [1, 64]",
+               name, r->action_dim);
   return TTRL_OK;
 }
 
@@ -353,16 +364,20 @@ using namespace ttrl;
 extern "C" {
 
 int ttrl_replay_write(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
-                      const int* action, const float* reward, const unsigned char* terminated,
-                      const unsigned char* ended, const int* final_row, const void* obs, const void* final_obs) {
+                      const int* action, const float* action_vec, const float* reward,
+                      const unsigned char* terminated, const unsigned char* ended, const int* final_row,
+                      const void* obs, const void* final_obs) {
   int rc = check_ring(ring, "ttrl_replay_write");
   if (rc) return rc;
-  TTRL_REQUIRE(ctx && lane && col && action && reward && terminated && ended && final_row && obs,
+  TTRL_REQUIRE(ctx && lane && col && reward && terminated && ended && final_row && obs,
                "ttrl_replay_write: null argument");
+  TTRL_REQUIRE(ring->action_vec ? (action_vec != nullptr) : (action != nullptr),
+               "ttrl_replay_write: a ring with %s actions needs the %s action array",
+               ring->action_vec ? "vector" : "index", ring->action_vec ? "vector" : "index");
   TTRL_REQUIRE(!ring->weight || (ring->max_priority && ring->alpha >= 0.0), "ttrl_replay_write: bad priorities");
   if (n <= 0) return TTRL_OK;
   hipLaunchKernelGGL(k_replay_write, dim3(unsigned(n)), dim3(kReplayThreads), 0, stream_of(ctx), ring_of(ring), n,
-                     lane, col, action, reward, terminated, ended, final_row,
+                     lane, col, action, action_vec, reward, terminated, ended, final_row,
                      static_cast<const unsigned char*>(obs), static_cast<const unsigned char*>(final_obs));
   return check_launch("ttrl_replay_write");
 }
@@ -411,8 +426,8 @@ int ttrl_replay_is_weights(ttrl_ctx* ctx, int n, const double* picked_weight, co
 
 int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, const int* lane, const int* col,
                          int n_step, double gamma, void* obs_out, void* next_obs_out, float* actions_onehot,
-                         int num_actions, int* actions_out, float* rewards_out, float* dones_out,
-                         float* discounts_out) {
+                         int num_actions, int* actions_out, float* action_vec_out, float* rewards_out,
+                         float* dones_out, float* discounts_out) {
   int rc = check_ring(ring, "ttrl_replay_assemble");
   if (rc) return rc;
   TTRL_REQUIRE(ctx && lane && col && obs_out && next_obs_out && rewards_out && dones_out && discounts_out,
@@ -423,7 +438,7 @@ int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, con
   hipLaunchKernelGGL(k_replay_assemble, dim3(unsigned(n)), dim3(kReplayThreads), 0, stream_of(ctx), ring_of(ring), n,
                      lane, col, n_step, gamma, static_cast<unsigned char*>(obs_out),
                      static_cast<unsigned char*>(next_obs_out), actions_onehot, num_actions, actions_out,
-                     rewards_out, dones_out, discounts_out);
+                     ring->action_vec ? action_vec_out : nullptr, rewards_out, dones_out, discounts_out);
   return check_launch("ttrl_replay_assemble");
 }
 

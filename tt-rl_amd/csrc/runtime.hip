@@ -584,6 +584,52 @@ int ttrl_graph_destroy(ttrl_graph* g) {
   return TTRL_OK;
 }
 
+// ---------------------------------------------------------------- plans ---
+
+int ttrl_plans_export(ttrl_ctx* ctx, char* buf, size_t cap, size_t* len) {
+  if (!ctx || !len) return set_error(TTRL_EINVAL, "ttrl_plans_export: null argument");
+  std::vector<std::pair<std::string, GemmPlan>> rows(ctx->plans.begin(), ctx->plans.end());
+  std::sort(rows.begin(), rows.end(), [](const auto& a, const auto& b) { return a.first < b.first; });
+  std::string text;
+  char head[96];
+  for (const auto& r : rows) {
+    const GemmPlan& p = r.second;
+    snprintf(head, sizeof(head), "%d %d %d %d %d %d\t", p.cfg, p.bm, p.bn, p.tbk, p.splits, p.kchunk);
+    text += head;
+    text += r.first;
+    text += '\n';
+  }
+  *len = text.size();
+  if (buf) {
+    if (cap < text.size() + 1) return set_error(TTRL_EINVAL, "ttrl_plans_export: %zu bytes needed", text.size() + 1);
+    std::memcpy(buf, text.c_str(), text.size() + 1);
+  }
+  return TTRL_OK;
+}
+
+int ttrl_plans_import(ttrl_ctx* ctx, const char* text, int* count) {
+  if (!ctx || !text) return set_error(TTRL_EINVAL, "ttrl_plans_import: null argument");
+  int n = 0;
+  const char* line = text;
+  while (*line) {
+    const char* end = std::strchr(line, '\n');
+    const size_t size = end ? size_t(end - line) : std::strlen(line);
+    const std::string row(line, size);
+    const size_t tab = row.find('\t');
+    GemmPlan p;
+    if (tab != std::string::npos && tab + 1 < row.size() &&
+        std::sscanf(row.c_str(), "%d %d %d %d %d %d", &p.cfg, &p.bm, &p.bn, &p.tbk, &p.splits, &p.kchunk) == 6) {
+      // A plan is checked against its call's extents when it is used.
+      ctx->plans[row.substr(tab + 1)] = p;
+      ++n;
+    }
+    if (!end) break;
+    line = end + 1;
+  }
+  if (count) *count = n;
+  return TTRL_OK;
+}
+
 // --------------------------------------------------------------- timing ---
 
 int ttrl_timer_start(ttrl_ctx* ctx) {

@@ -1000,6 +1000,10 @@ std::vector<GemmPlan> plan_candidates(int M, int N, int K, int groups, long ws_f
 // Tile shape `cfg` with K split `splits` ways (fewer if K has fewer LDS
 // stages); false if the partials would not fit in `ws_floats`.
 bool plan_with_splits(int cfg, int M, int N, int K, int groups, long ws_floats, int splits, GemmPlan* out);
+// True when `p` is a plan of an allowed tile shape whose splits exactly cover
+// K and whose partials fit `ws_floats`: checked on every plan taken from the
+// context's table, which may have been imported from a file.
+bool plan_valid(const GemmPlan& p, int M, int N, int K, int groups, long ws_floats, unsigned allowed);
 bool gemm_tuning_enabled();
 bool gemm_tuning_log();  // TTRL_GEMM_TUNE_LOG=1: print each tuned signature's candidates to stderr
 // TTRL_GEMM_FORCE="cfg[:splits]" (read on every call, for tests): run that
@@ -1122,7 +1126,8 @@ inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int
     launch_allowed<ALLOWED>(la, lb, ep, ws, M, N, K, groups, p, st);
     return check_launch(name);
   }
-  if (const GemmPlan* hit = ctx_plan_find(ctx, key)) {
+  const GemmPlan* hit = ctx_plan_find(ctx, key);
+  if (hit && plan_valid(*hit, M, N, K, groups, ws_limit, ALLOWED)) {
     p = *hit;
   } else {
     if (!ctx_capturing(ctx) && gemm_tuning_enabled())
@@ -1210,7 +1215,8 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
   const std::string key2 = key + "#2";
   const GemmPlan* h1 = ctx_plan_find(ctx, key);
   const GemmPlan* h2 = ctx_plan_find(ctx, key2);
-  if (h1 && h2) {
+  if (h1 && h2 && h1->cfg == h2->cfg && plan_valid(*h1, q1.M, q1.N, q1.K, q1.groups, half, ALLOWED) &&
+      plan_valid(*h2, q2.M, q2.N, q2.K, q2.groups, half, ALLOWED)) {
     p1 = *h1;
     p2 = *h2;
   } else {

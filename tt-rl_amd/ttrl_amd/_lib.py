@@ -60,6 +60,7 @@ class ReplayRing(C.Structure):
         ("obs", C.c_void_p), ("actions", C.c_void_p), ("rewards", C.c_void_p), ("dones", C.c_void_p),
         ("ends", C.c_void_p), ("final_slot", C.c_void_p), ("final_obs", C.c_void_p), ("final_rows", C.c_int),
         ("weight", C.c_void_p), ("max_priority", C.c_void_p), ("alpha", C.c_double), ("epsilon", C.c_double),
+        ("action_vec", C.c_void_p), ("action_dim", C.c_int),
     ]
 
 
@@ -106,6 +107,8 @@ SIGNATURES = {
     "ttrl_host_free": ([P, P], I),
     "ttrl_graph_nodes": ([P, C.POINTER(SZ)], I),
     "ttrl_graph_destroy": ([P], I),
+    "ttrl_plans_export": ([P, C.c_char_p, SZ, C.POINTER(SZ)], I),
+    "ttrl_plans_import": ([P, C.c_char_p, C.POINTER(I)], I),
     "ttrl_timer_start": ([P], I),
     "ttrl_timer_stop": ([P, C.POINTER(F)], I),
     "ttrl_matmul": ([P, I, I, I, P, L, I, P, L, I, P, L, F, F], I),
@@ -126,11 +129,11 @@ SIGNATURES = {
     "ttrl_gru_step": ([P, I, I, P, P, P, P, P, P], I),
     "ttrl_gru_mask": ([P, I, I, P, P, P], I),
     "ttrl_gru_step_backward": ([P, I, I, P, P, P, P, P, P, P, P, P], I),
-    "ttrl_replay_write": ([P, C.POINTER(ReplayRing), I, P, P, P, P, P, P, P, P, P], I),
+    "ttrl_replay_write": ([P, C.POINTER(ReplayRing), I, P, P, P, P, P, P, P, P, P, P], I),
     "ttrl_replay_lane_sums": ([P, C.POINTER(ReplayRing), P, P, I, I, P, P], I),
     "ttrl_replay_priority_pick": ([P, C.POINTER(ReplayRing), I, P, P, P, P, I, I, P, P, P, P], I),
     "ttrl_replay_is_weights": ([P, I, P, P, I, C.c_long, C.c_double, P], I),
-    "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P], I),
+    "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P, P], I),
     "ttrl_replay_update_priorities": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_replay_update_priorities_f64": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),

@@ -24,6 +24,7 @@ import numpy as np
 from ttrl_amd import _lib
 from ttrl_amd.algos.grads import grad_sq_device
 from ttrl_amd.algos.state import TOWERS_DQN, assemble, from_reference_keys, to_reference_keys, validate
+from ttrl_amd.buffers.replay import PriorityConfig
 from ttrl_amd.engine.autograd import Tensor, no_grad
 from ttrl_amd.engine.conv import Conv2d
 from ttrl_amd.engine import layers as layers_mod
@@ -59,6 +60,11 @@ class DQNConfig:
     eps_decay_frames: int = 1_000_000
     eval_epsilon: float = 0.05
     act_mode: str = "graph"
+    # the agent's replay and update clock (DQNAgent)
+    buffer_capacity: int = 100_000
+    train_freq: int = 4
+    learning_starts: int = 1_000
+    priority: PriorityConfig | None = None
 
     def __post_init__(self):
         if self.lr <= 0 or self.adam_eps <= 0:
@@ -76,6 +82,17 @@ class DQNConfig:
             raise ValueError(f"DQNConfig: eps_decay_frames must be >= 1, got {self.eps_decay_frames}")
         if not 0.0 <= self.eval_epsilon <= 1.0:
             raise ValueError(f"DQNConfig: eval_epsilon must be in [0, 1], got {self.eval_epsilon}")
+        if self.buffer_capacity < 1 or self.train_freq < 1 or self.learning_starts < 0:
+            raise ValueError("DQNConfig: buffer_capacity and train_freq must be >= 1, learning_starts >= 0")
+        if self.priority is not None and not self.prioritized:
+            raise ValueError("DQNConfig: a priority config needs prioritized=True (the update reads IS weights)")
+
+    def replay_priority(self) -> PriorityConfig | None:
+        """The agent's replay prioritisation: `priority`, or the default
+        settings when only `prioritized` is set."""
+        if not self.prioritized:
+            return None
+        return self.priority if self.priority is not None else PriorityConfig()
 
 
 def leaf_key(which: str, leaf: str) -> str:

@@ -30,6 +30,7 @@ import numpy as np
 from ttrl_amd import _lib
 from ttrl_amd.algos.gaussian import ActionScale, squashed_sample
 from ttrl_amd.algos.state import TOWERS_SAC, assemble, from_reference_keys, to_reference_keys, validate
+from ttrl_amd.buffers.replay import PriorityConfig
 from ttrl_amd.nets.acting import ActingNet, SquashedDecision
 from ttrl_amd.engine.autograd import Tensor, _needs, no_grad
 from ttrl_amd.engine import layers as layers_mod
@@ -63,14 +64,29 @@ class SACConfig:
     critic_hidden: tuple = (256, 256)
     policy_hidden: tuple = (256, 256)
     act_mode: str = "graph"
+    # the agent's replay and update clock (SACAgent)
+    n_step: int = 1
+    buffer_capacity: int = 100_000
+    train_freq: int = 1
+    learning_starts: int = 1_000
+    priority: PriorityConfig | None = None
 
     def __post_init__(self):
         if self.lr <= 0 or self.adam_eps <= 0:
             raise ValueError("SACConfig: lr and adam_eps must be > 0")
+        if self.n_step < 1 or self.buffer_capacity < 1 or self.train_freq < 1 or self.learning_starts < 0:
+            raise ValueError("SACConfig: n_step, buffer_capacity and train_freq must be >= 1, learning_starts >= 0")
+        if self.priority is not None and not self.prioritized:
+            raise ValueError("SACConfig: a priority config needs prioritized=True (the critic loss reads IS weights)")
         if not 0.0 <= self.tau <= 1.0:
             raise ValueError(f"SACConfig: tau must be in [0, 1], got {self.tau}")
         if self.step_mode not in ("eager", "graph"):
             raise ValueError(f"SACConfig: step_mode must be 'eager' or 'graph', got {self.step_mode!r}")
+
+    def replay_priority(self) -> PriorityConfig | None:
+        if not self.prioritized:
+            return None
+        return self.priority if self.priority is not None else PriorityConfig()
 
 
 # --------------------------------------------------------------- twin Q ---

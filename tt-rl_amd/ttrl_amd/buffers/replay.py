@@ -108,8 +108,10 @@ class ReplayBuffer:
                 f"ReplayBuffer: capacity {capacity} split across {n_envs} lanes gives {per_lane} columns per "
                 f"lane, but one transition reads n_step + 1 = {n_step + 1} columns of its own lane, so a lane "
                 f"that short has no sampleable transition. Raise capacity or lower n_envs.")
-        if action_spec.kind != "discrete":
-            raise ValueError("ReplayBuffer: this buffer stores discrete actions")
+        if action_spec.kind not in ("discrete", "continuous"):
+            raise ValueError(f"ReplayBuffer: unsupported action kind {action_spec.kind!r}")
+        # discrete actions are stored as indices, continuous ones as float32 rows
+        self.action_dim = int(action_spec.dim) if action_spec.kind == "continuous" else 0
         self.obs_spec, self.action_spec, self.device = obs_spec, action_spec, device
         self.n_envs, self.per_lane_capacity = int(n_envs), per_lane
         self.capacity = per_lane * self.n_envs
@@ -124,6 +126,7 @@ class ReplayBuffer:
         cells = L * Cc
         self._obs = DeviceArray(dev, (cells * self.obs_bytes,), np.uint8)
         self._actions = DeviceArray(dev, (cells,), np.int32)
+        self._action_vec = DeviceArray(dev, (cells * self.action_dim,), np.float32) if self.action_dim else None
         self._rewards = DeviceArray(dev, (cells,), np.float32)
         self._flags = DeviceArray(dev, (2 * cells,), np.uint8)  # dones | ends
         self._final_slot = DeviceArray(dev, (cells,), np.int32)
@@ -144,16 +147,13 @@ class ReplayBuffer:
             self._flags.ptr + cells, self._final_slot.ptr, self._final_obs.ptr, rows,
             None if self._weight is None else self._weight.ptr,
             None if self._max_priority is None else self._max_priority.ptr,
-            0.0 if priority is None else float(priority.alpha), 1e-6 if priority is None else float(priority.epsilon))
+            0.0 if priority is None else float(priority.alpha), 1e-6 if priority is None else float(priority.epsilon),
+            None if self._action_vec is None else self._action_vec.ptr, self.action_dim)
         self._pos = np.zeros(L, np.int64)
         self._full = np.zeros(L, bool)
         self._rng = np.random.default_rng(seed)
         # Staging of one vector-env step's writes, and of one draw.
-        self._stage_in, self._stage = bound_block(dev, [
-            ("lane", np.zeros(L, np.int32)), ("col", np.zeros(L, np.int32)), ("action", np.zeros(L, np.int32)),
-            ("reward", np.zeros(L, np.float32)), ("term", np.zeros(L, np.uint8)), ("end", np.zeros(L, np.uint8)),
-            ("frow", np.zeros(L, np.int32)), ("obs", np.zeros(L * self.obs_bytes, np.uint8)),
-            ("final", np.zeros(L * self.obs_bytes, np.uint8))])
+        self._stage_in, self._stage = bound_block(dev, self._stage_specs(L, True))
         self._stage_host = np.zeros(self._stage.nbytes, np.uint8)
         self.max_batch = int(max_batch)
         self._max_chunks = -(-Cc // PICK_CHUNK)
@@ -238,8 +238,15 @@ class ReplayBuffer:
             stage, block = self._staging(n, with_final)
             host = np.zeros(block.nbytes, np.uint8)
         host[:] = 0
+        if self.action_dim:
+            acts = np.asarray(actions, np.float32).reshape(n, self.action_dim)
+        else:
+            acts = np.asarray(actions).reshape(-1)
+            if acts.dtype.kind == "f" and np.any(acts != np.floor(acts)):
+                raise ValueError("ReplayBuffer: a discrete action must be a whole number")
+            acts = acts.astype(np.int32)
         fields = [("lane", lanes.astype(np.int32)), ("col", cols.astype(np.int32)),
-                  ("action", np.asarray(actions, np.int32)), ("reward", np.asarray(rewards, np.float32)),
+                  ("action", acts), ("reward", np.asarray(rewards, np.float32)),
                   ("term", np.asarray(term, np.uint8)), ("end", ended.astype(np.uint8)), ("frow", frow),
                   ("obs", obs)]
         if with_final:
@@ -251,18 +258,24 @@ class ReplayBuffer:
             host[off:off + a.nbytes] = a
         block.upload(host)
         final = stage["final"] if "final" in stage else stage["obs"]  # read only for rows with a boundary
+        vec = bool(self.action_dim)
         self.device.call("ttrl_replay_write", C.byref(self._ring), n, stage["lane"].vp, stage["col"].vp,
-                         stage["action"].vp, stage["reward"].vp, stage["term"].vp, stage["end"].vp,
-                         stage["frow"].vp, stage["obs"].vp, final.vp)
+                         None if vec else stage["action"].vp, stage["action"].vp if vec else None,
+                         stage["reward"].vp, stage["term"].vp, stage["end"].vp, stage["frow"].vp, stage["obs"].vp,
+                         final.vp)
         self._pos, self._full = pos, full
 
-    def _staging(self, n: int, with_final: bool):
-        specs = [("lane", np.zeros(n, np.int32)), ("col", np.zeros(n, np.int32)), ("action", np.zeros(n, np.int32)),
+    def _stage_specs(self, n: int, with_final: bool):
+        action = np.zeros((n, self.action_dim), np.float32) if self.action_dim else np.zeros(n, np.int32)
+        specs = [("lane", np.zeros(n, np.int32)), ("col", np.zeros(n, np.int32)), ("action", action),
                  ("reward", np.zeros(n, np.float32)), ("term", np.zeros(n, np.uint8)), ("end", np.zeros(n, np.uint8)),
                  ("frow", np.zeros(n, np.int32)), ("obs", np.zeros(n * self.obs_bytes, np.uint8))]
         if with_final:
             specs.append(("final", np.zeros(n * self.obs_bytes, np.uint8)))
-        return bound_block(self.device, specs)
+        return specs
+
+    def _staging(self, n: int, with_final: bool):
+        return bound_block(self.device, self._stage_specs(n, with_final))
 
     def add_steps(self, obs, actions, rewards, terminated, truncated=None, final_obs=None) -> None:
         """T vector-env steps at once, every argument [T, n_envs, ...]: the
@@ -296,6 +309,30 @@ class ReplayBuffer:
         rows = self._obs_rows(np.asarray(obs)[None], 1, "add")
         fin = None if final_obs is None else self._obs_rows(np.asarray(final_obs)[None], 1, "add")
         self._write(np.array([lane]), rows, [action], [reward], [bool(terminated)], [ended], fin)
+
+    def add_lanes(self, lanes, obs, actions, rewards, terminated, truncated=None, final_obs=None) -> None:
+        """One transition into each of `lanes` (distinct), in one upload and
+        one launch: the lanes of a vector-env step that are real transitions
+        (ttrl/algos/offpolicy.py:37-58 writes them one `add` at a time).
+        Arguments are lane-major over `lanes`; final_obs rows are read for
+        the entries that ended."""
+        lanes = np.asarray(lanes, np.int64).reshape(-1)
+        n = lanes.size
+        if n == 0:
+            return
+        if np.unique(lanes).size != n or lanes.min() < 0 or lanes.max() >= self.n_envs:
+            raise ValueError(f"ReplayBuffer.add_lanes: lanes must be distinct and in [0, {self.n_envs}), "
+                             f"got {lanes.tolist()}")
+        rows = self._obs_rows(np.asarray(obs).reshape((n,) + self.obs_shape), n, "add_lanes")
+        term = np.asarray(terminated, bool).reshape(n)
+        trunc = np.zeros(n, bool) if truncated is None else np.asarray(truncated, bool).reshape(n)
+        ended = term | trunc
+        fin = None
+        if ended.any():
+            if final_obs is None:
+                raise ValueError("ReplayBuffer.add_lanes: some lanes ended but final_obs is None")
+            fin = np.asarray(final_obs, self.obs_dtype).reshape((n,) + self.obs_shape)
+        self._write(lanes, rows, actions, np.asarray(rewards).reshape(-1), term, ended, fin)
 
     def add_batch(self, obs, actions, rewards, terminated, truncated=None, final_obs=None) -> None:
         """One vector-env step, the leading axis of every argument the lane
@@ -394,7 +431,7 @@ class ReplayBuffer:
 
     def _assemble(self, n: int, out: dict | None, weights) -> DeviceBatch:
         dev, out = self.device, dict(out or {})
-        A = int(self.action_spec.n)
+        A = int(self.action_spec.n) if not self.action_dim else 0
 
         def dst(name, shape, dtype=np.float32):
             a = out.get(name)
@@ -408,13 +445,18 @@ class ReplayBuffer:
         obs = dst("obs", (n,) + self.obs_shape, self.obs_dtype)
         nxt = dst("next_obs", (n,) + self.obs_shape, self.obs_dtype)
         onehot = out.get("actions_onehot")
-        if onehot is not None:
-            onehot = dst("actions_onehot", (n, A))
-        actions = DeviceArray(dev, (n,), np.int32)
+        if self.action_dim:
+            onehot = None
+            actions = dst("actions", (n, self.action_dim))
+        else:
+            if onehot is not None:
+                onehot = dst("actions_onehot", (n, A))
+            actions = DeviceArray(dev, (n,), np.int32)
         rewards, dones, discounts = (dst(k, (n, 1)) for k in ("rewards", "dones", "discounts"))
         d = self._draw_in
         dev.call("ttrl_replay_assemble", C.byref(self._ring), n, d["lanes"].vp, d["cols"].vp, self.n_step,
-                 C.c_double(self.gamma), obs.vp, nxt.vp, None if onehot is None else onehot.vp, A, actions.vp,
+                 C.c_double(self.gamma), obs.vp, nxt.vp, None if onehot is None else onehot.vp, A,
+                 None if self.action_dim else actions.vp, actions.vp if self.action_dim else None,
                  rewards.vp, dones.vp, discounts.vp)
         self._last = n
         return DeviceBatch(obs, nxt, actions, rewards, dones, discounts, weights, d["lanes"].view(0, (n,)),

@@ -9,12 +9,20 @@ copies and graph replays is stream order.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import threading
 from contextlib import contextmanager
+from pathlib import Path
 
 from ttrl_amd import _lib
 
 __all__ = ["Device", "HostBlock", "acquire", "device_count", "NoDeviceAvailable"]
+
+
+#: GEMM plans tuned on gfx950 for this package's learner workloads, loaded
+#: into every context at open (TTRL_PLANS=<path> loads another file instead,
+#: TTRL_PLANS=none none), so processes run the same plans and agree bit for bit.
+PLAN_FILE = Path(__file__).resolve().parents[1] / "plans" / "gfx950.tsv"
 
 
 class NoDeviceAvailable(RuntimeError):
@@ -43,6 +51,11 @@ class Device:
         self._lock = threading.RLock()
         self.closed = False
         self._pool_stack = [0]
+        plans = os.environ.get("TTRL_PLANS", "")
+        if plans.lower() != "none":
+            path = Path(plans) if plans else PLAN_FILE
+            if path.is_file():
+                self.load_plans(path)
 
     # -- plumbing ----------------------------------------------------------
 
@@ -57,6 +70,28 @@ class Device:
     @property
     def capturing(self) -> bool:
         return getattr(self, "_capturing", False)
+
+    # -- GEMM plans --------------------------------------------------------
+
+    def export_plans(self) -> str:
+        """The context's GEMM plan table as text (ttrl_plans_export)."""
+        n = C.c_size_t(0)
+        self.call("ttrl_plans_export", None, C.c_size_t(0), C.byref(n))
+        buf = C.create_string_buffer(int(n.value) + 1)
+        self.call("ttrl_plans_export", buf, C.c_size_t(len(buf)), C.byref(n))
+        return buf.value.decode()
+
+    def import_plans(self, text: str) -> int:
+        """Add plans to the table; later calls of those signatures run them."""
+        count = C.c_int(0)
+        self.call("ttrl_plans_import", text.encode(), C.byref(count))
+        return int(count.value)
+
+    def save_plans(self, path) -> None:
+        Path(path).write_text(self.export_plans())
+
+    def load_plans(self, path) -> int:
+        return self.import_plans(Path(path).read_text())
 
     # -- memory ------------------------------------------------------------
 
