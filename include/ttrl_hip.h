@@ -289,6 +289,19 @@ int ttrl_sac_actor_loss(ttrl_ctx* ctx, int B, const float* q, const float* logp,
  * (ttrl/algos/grads.py:46-60), added to its value when accumulate_grad_sq. */
 int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n, int* step, float lr,
                    float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq);
+/* ttrl_adam_step with the same kernels and results, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops): no context
+ * and no allocation of any kind.  It enqueues on `stream` (a hipStream_t;
+ * NULL is the default stream) and keeps its per-workgroup sums of squared
+ * gradients in a static device array of 1024 floats (4 KiB, one per
+ * workgroup of the launch, which never exceeds 1024) that each GPU holds
+ * until the process ends; every n > 0 fits.  Calls on one GPU share that
+ * array: calls that can overlap (different streams, no ordering between
+ * them) race and must not be issued.  The first call on a device resolves
+ * the array's address for that device.  No counterpart in the reference. */
+int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, float* v_s, long n, int* step,
+                          float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                          int accumulate_grad_sq);
 /* sum(x^2) into *out (grad_sq_device, ttrl/algos/grads.py:46-60). */
 int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate);
 /* dst = (1 - tau) * dst + tau * src (ttrl/algos/sac/targets.py:45-52). */

@@ -16,6 +16,8 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <cstdint>
+#include <mutex>
 
 namespace ttrl {
 
@@ -127,6 +129,50 @@ inline unsigned grid_for(long n, long per_thread = 1) {
   return unsigned(b);
 }
 
+// Scratch of the allocation-free Adam step: one partial sum of squared
+// gradients per workgroup of k_adam.  A launch uses at most kOptMaxBlocks
+// workgroups, so this bounds nothing about n.  Each GPU holds its own copy;
+// host code reaches it only through the address hipGetSymbolAddress gives
+// for the current device (static_scratch_for), never through the name.
+constexpr int kStaticScratchFloats = kOptMaxBlocks;
+__device__ __align__(256) float scratch[kStaticScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, resolved once per
+// device (with that device current) and kept.
+int static_scratch_for(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDevice (ttrl_adam_step_static)");
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(TTRL_EINVAL, "ttrl_adam_step_static: device %d beyond the %d supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_error(e, "hipGetSymbolAddress (ttrl_adam_step_static scratch)");
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return TTRL_OK;
+}
+
+int check_adam_args(const float* p, const float* g, const float* m_s, const float* v_s, long n, const int* step,
+                    float lr, float beta1, float beta2, float eps, float weight_decay, const char* name) {
+  TTRL_REQUIRE(p && g && m_s && v_s && step, "%s: null argument", name);
+  TTRL_REQUIRE(n > 0, "%s: empty parameter range", name);
+  TTRL_REQUIRE(lr > 0.f && eps > 0.f && beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f &&
+                   weight_decay >= 0.f,
+               "%s: bad hyper-parameters", name);
+  TTRL_REQUIRE(((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
+                 reinterpret_cast<uintptr_t>(m_s) | reinterpret_cast<uintptr_t>(v_s)) & 15) == 0,
+               "%s: buffers must be 16-byte aligned", name);
+  return TTRL_OK;
+}
+
 }  // namespace ttrl
 
 using namespace ttrl;
@@ -135,14 +181,9 @@ extern "C" {
 
 int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n, int* step, float lr,
                    float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq) {
-  TTRL_REQUIRE(ctx && p && g && m_s && v_s && step, "ttrl_adam_step: null argument");
-  TTRL_REQUIRE(n > 0, "ttrl_adam_step: empty parameter range");
-  TTRL_REQUIRE(lr > 0.f && eps > 0.f && beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f &&
-                   weight_decay >= 0.f,
-               "ttrl_adam_step: bad hyper-parameters");
-  TTRL_REQUIRE(((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
-                 reinterpret_cast<uintptr_t>(m_s) | reinterpret_cast<uintptr_t>(v_s)) & 15) == 0,
-               "ttrl_adam_step: buffers must be 16-byte aligned");
+  TTRL_REQUIRE(ctx, "ttrl_adam_step: null ctx");
+  int rc = check_adam_args(p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, "ttrl_adam_step");
+  if (rc) return rc;
   long wsf = 0;
   float* ws = ctx_workspace(ctx, &wsf);
   const unsigned blocks = grid_for(n, 4);
@@ -153,6 +194,28 @@ int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v
   hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
                      accumulate_grad_sq);
   return check_launch("ttrl_adam_step");
+}
+
+int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, float* v_s, long n, int* step,
+                          float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                          int accumulate_grad_sq) {
+  int rc = check_adam_args(p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, "ttrl_adam_step_static");
+  if (rc) return rc;
+  const unsigned blocks = grid_for(n, 4);
+  TTRL_REQUIRE(blocks <= unsigned(kStaticScratchFloats),
+               "ttrl_adam_step_static: %u workgroups exceed the %d partial sums of the static scratch", blocks,
+               kStaticScratchFloats);
+  float* partials = nullptr;
+  rc = static_scratch_for(&partials);
+  if (rc) return rc;
+  // Every workgroup writes its own partial before k_finish reads them, so
+  // nothing in the scratch needs clearing between calls.
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_adam, dim3(blocks), dim3(kOptThreads), 0, st, p, g, m_s, v_s, n, step, lr, beta1, beta2,
+                     eps, weight_decay, partials);
+  hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, partials, int(blocks), step, grad_sq,
+                     accumulate_grad_sq);
+  return check_launch("ttrl_adam_step_static");
 }
 
 int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate) {

@@ -141,6 +141,7 @@ SIGNATURES = {
     "ttrl_sac_critic_loss": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),
     "ttrl_sac_actor_loss": ([P, I, P, P, P, F, I, P, P, P, P, P], I),
     "ttrl_adam_step": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
+    "ttrl_adam_step_static": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
     "ttrl_sum_squares": ([P, P, L, P, I], I),
     "ttrl_polyak": ([P, P, P, L, F], I),
     "ttrl_gae": ([P, I, I, P, P, P, P, P, C.c_double, C.c_double, P, P], I),
