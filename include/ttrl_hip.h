@@ -254,6 +254,45 @@ int ttrl_dqn_head(ttrl_ctx* ctx, int B, int K, int A, int groups, const float* c
                   const float* dones, const float* discounts, const float* is_weights, float delta, float* loss,
                   float* mean_q, float* td_abs, float* dq, float* next_actions, float* td_target);
 
+/* A DQN Q network's last two layers over 2 or 3 feature sets, the DQN loss
+ * and the head's backward (ttrl/algos/dqn/losses.py:77-140 over the Nature
+ * CNN's Linear(K, F) -> ReLU -> QHead Linear(F, A), ttrl/nets/encoders.py,
+ * ttrl/nets/heads.py): h[g] = relu(x[g] W1[g] + b1[g]) ([B][F]); q[g] =
+ * h[g] W2[g] + b2[g] ([B][A]); the loss and metrics of ttrl_dqn_loss with q[0]
+ * = online(s), q[1] selecting a* and q[groups-1] valuing it; dq = dloss/dq[0];
+ * dh = dq W2[0]^T * [h[0] > 0], the gradient entering the first layer's
+ * backward; dW2 = h[0]^T dq and db2 = column sums of dq, the second layer's
+ * gradients (added to their values when beta_w = 1).  b1, b2, is_weights,
+ * mean_q, td_abs, next_actions, td_target and db2 may be NULL.  B <= 1024,
+ * F <= 2048, A <= 32. */
+typedef struct ttrl_dqn_tail_desc {
+  int B, K, F, A, groups;
+  const float* x[3];
+  const float* W1[3];
+  const float* b1[3];
+  float* h[3];
+  const float* W2[3];
+  const float* b2[3];
+  float* q[3];
+  const float* actions_onehot;
+  const float* rewards;
+  const float* dones;
+  const float* discounts;
+  const float* is_weights;
+  float delta;
+  float* loss;
+  float* mean_q;
+  float* td_abs;
+  float* dq;
+  float* next_actions;
+  float* td_target;
+  float* dh;
+  float* dW2;
+  float* db2;
+  float beta_w;
+} ttrl_dqn_tail_desc;
+int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* desc);
+
 /* SquashedGaussian.sample (ttrl/algos/sac/policy.py:30-40) over head rows
  * [mean | log_std] ([B][2d], log_std already clamped): action =
  * centre + half_width * tanh(mean + exp(log_std)*noise), logp with the stable

@@ -19,6 +19,7 @@ hipStream_t stream_of(ttrl_ctx* ctx);
 // uses one leaves it at zero), then float partials (kSyncPartials).
 constexpr int kSyncCounters = 64, kSyncPartials = 2 * 1024;
 constexpr int kSyncDqnHead = 0;  // counter of ttrl_dqn_head
+constexpr int kSyncDqnTail = 1;  // counter of ttrl_dqn_tail
 unsigned* ctx_sync_words(ttrl_ctx* ctx);
 // Converts a pending launch error into a status code.
 int check_launch(const char* name);

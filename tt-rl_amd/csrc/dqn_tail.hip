@@ -1,0 +1,415 @@
+// The last two layers of the DQN update's Q networks, the loss and the
+// head's backward in two launches (ttrl/algos/dqn/losses.py:77-140 over
+// ttrl/nets/encoders.py's Linear(3136, 512) -> ReLU -> QHead Linear(512, A)).
+//
+// Launch 1, the first linear layer of every feature set, a GEMM on the
+// MFMA core planned like any other; when its plan splits K the partial
+// tiles stay in the workspace (run_gemm_deferred).
+//
+// Launch 2, k_dqn_tail, one workgroup per sample b:
+//   h_g[b]  = relu(sum of the split partials in split order + b1_g)   (what
+//             k_splitk_reduce would write; read back when K was not split)
+//   q_g[b]  = h_g[b] W2_g + b2_g                 fixed-order block sums
+//   the DQN row of sample b (dqn_row.hpp): a* from group 1, valued by group
+//             G-1, Huber, IS weight, td_abs, dL/dq
+//   dh[b]   = (dq[b] W2_0^T) * [h_0[b] > 0]      the gradient entering the
+//             first layer's backward, already through its ReLU
+// and the workgroup that finishes last (a device-scope counter, reset by it)
+// sums, in sample order, the batch loss and mean Q and the second layer's
+// weight and bias gradients dW2 = h_0^T dq, db2 = column sums of dq.
+//
+// This replaces a split-K reduce, the Q-head-and-loss kernel and the second
+// layer's backward launch: three graph nodes become one.
+#include "dqn_row.hpp"
+#include "tile_gemm.hpp"
+
+#include <cmath>
+
+namespace ttrl {
+namespace {
+
+constexpr int kTailThreads = 256;
+constexpr int kTailMaxF = 2048;  // first-layer outputs per feature set held in LDS
+constexpr int kTailMaxA = 32;
+constexpr int kTailMaxB = kSyncPartials / 2;  // two partial sums per sample in the sync words
+constexpr int kTailChunk = 32;                // samples per pass of the weight-gradient sum
+constexpr int kTailItems = 8;                 // first-layer outputs per thread per pass
+static_assert(kSyncPartials + kTailChunk * kTailMaxA <= 3 * kTailMaxF, "the last workgroup's staging fits hs");
+
+constexpr unsigned kFc1Cfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
+                              cfg_bit(T32x32K2) | cfg_bit(T32x32K4) | cfg_bit(T64x32K2) | cfg_bit(T32x64K2);
+
+struct TailArgs {
+  int B, F, A, G, splits;  // splits 0: h holds the first layer's outputs already
+  const float* part;       // [G][splits][B][F]
+  float* h[3];
+  const float* b1[3];
+  const float* W2[3];
+  const float* b2[3];
+  float* q[3];
+  const float* onehot;
+  const float* rewards;
+  const float* dones;
+  const float* discounts;
+  const float* weights;
+  float delta;
+  float* loss;
+  float* mean_q;
+  float* td_abs;
+  float* dq;
+  float* next_act;
+  float* td_target;
+  float* dh;
+  float* dW2;
+  float* db2;
+  float beta_w;
+  unsigned* counter;
+  float* partials;
+};
+
+// Every phase issues all of its loads before it uses one: the kernel is a
+// chain of memory round trips, one workgroup per sample, so the number of
+// trips, not the arithmetic, sets its duration.  The inner loops carry no
+// per-action or per-row branch (a guarded load or LDS read becomes a basic
+// block of its own, with a wait of its own): action columns run to AP with
+// clamped indexes or zero padding, and the extra accumulators are dropped.
+// Sum of v over the 64 lanes of a wavefront, the same in every lane, without
+// LDS: within each quad xor-1 and xor-2 swaps (quad_perm), then the mirror of
+// each half-row of 8 and of each row of 16 (row_half_mirror, row_mirror)
+// leave every lane of a row of 16 holding that row's sum; the four row sums
+// are added in row order.  A fixed association, so the same bits every run.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  const int i = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
+template <int AP>
+__global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
+  __shared__ float hs[3 * kTailMaxF];  // the sample's first-layer outputs; the last workgroup's staging
+  __shared__ float red[kTailThreads / 64][3 * AP];
+  __shared__ float qrow[3 * kTailMaxA];
+  __shared__ float dqrow[kTailMaxA];
+  __shared__ float onehot[kTailMaxA];
+  __shared__ float scal[4];  // reward, done, discount, importance weight
+  __shared__ int last;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int F = t.F, A = t.A, G = t.G, S = t.splits, B = t.B;
+
+  // 0. the sample's action, reward, done, discount and weight, in flight
+  // with the first layer's loads
+  if (tid < A) onehot[tid] = t.onehot[long(b) * A + tid];
+  if (tid >= A && tid < AP) dqrow[tid] = 0.f;  // dq's padding columns, read by phase 4
+  if (tid == kTailMaxA) scal[0] = t.rewards[b];
+  if (tid == kTailMaxA + 1) scal[1] = t.dones[b];
+  if (tid == kTailMaxA + 2) scal[2] = t.discounts[b];
+  if (tid == kTailMaxA + 3) scal[3] = t.weights ? t.weights[b] : 1.f;
+
+  // 1. the first layer's outputs of sample b, every feature set: item
+  // k = g * F + n, kTailItems items per thread per pass
+  const int items = G * F;
+  const long stride = long(B) * F;  // one split's partial tile
+  // a lane's feature set is its own: pointers picked by compares, not by a
+  // per-lane index into the argument arrays (a vector load of the pointer)
+  auto pick = [](int g, auto p0, auto p1, auto p2) { return g == 0 ? p0 : (g == 1 ? p1 : p2); };
+  for (int k0 = 0; k0 < items; k0 += kTailItems * kTailThreads) {
+    if (S == 0) {
+      for (int u = 0; u < kTailItems; ++u) {
+        const int k = k0 + u * kTailThreads + tid;
+        if (k >= items) break;
+        const int g = k / F, n = k - g * F;
+        hs[k] = pick(g, t.h[0], t.h[1], t.h[2])[long(b) * F + n];
+      }
+      continue;
+    }
+    float v[kTailItems][8], bias[kTailItems];
+#pragma unroll
+    for (int u = 0; u < kTailItems; ++u) {
+      const int k = min(k0 + u * kTailThreads + tid, items - 1);  // a clamped lane's loads are dropped
+      const int g = k / F, n = k - g * F;
+      const float* p = t.part + (long(g) * S * B + b) * F + n;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[u][j] = p[min(j, S - 1) * stride];
+      const float* bg = pick(g, t.b1[0], t.b1[1], t.b1[2]);
+      bias[u] = bg ? bg[n] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kTailItems; ++u) {
+      const int k = k0 + u * kTailThreads + tid;
+      if (k >= items) break;
+      const int g = k / F, n = k - g * F;
+      float sum = 0.f;  // split order from zero, as k_splitk_reduce sums
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum += j < S ? v[u][j] : 0.f;
+      const float* p = t.part + (long(g) * S * B + b) * F + n;
+      for (int j = 8; j < S; ++j) sum += p[j * stride];
+      const float h = relu_f(sum + bias[u]);
+      pick(g, t.h[0], t.h[1], t.h[2])[long(b) * F + n] = h;
+      hs[k] = h;
+    }
+  }
+  __syncthreads();
+
+  // 2. q_g = h_g W2_g + b2_g: per-thread partial dot products over its
+  // features, a DPP sum over each wavefront, then the wavefronts in order
+  float acc[3][AP];
+#pragma unroll
+  for (int g = 0; g < 3; ++g)
+#pragma unroll
+    for (int a = 0; a < AP; ++a) acc[g][a] = 0.f;
+  for (int n = tid; n < F; n += kTailThreads) {
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+      if (g < G) {
+        const float hv = hs[g * F + n];
+        const float* w = t.W2[g] + long(n) * A;
+#pragma unroll
+        for (int a = 0; a < AP; ++a) acc[g][a] = fmaf(hv, w[min(a, A - 1)], acc[g][a]);
+      }
+  }
+#pragma unroll
+  for (int g = 0; g < 3; ++g)
+#pragma unroll
+    for (int a = 0; a < AP; ++a) {
+      if (g >= G || a >= A) continue;  // uniform
+      const float v = wave_sum(acc[g][a]);
+      if (lane == 0) red[wave][g * AP + a] = v;
+    }
+  __syncthreads();
+  if (tid < 3 * AP) {
+    const int g = tid / AP, a = tid - g * AP;
+    if (g < G && a < A) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kTailThreads / 64; ++w) v += red[w][tid];
+      if (t.b2[g]) v += t.b2[g][a];
+      qrow[g * A + a] = v;
+      t.q[g][long(b) * A + a] = v;
+    }
+  }
+  __syncthreads();
+
+  // 3. the DQN row of sample b
+  if (tid == 0) {
+    const DqnRow r = dqn_row_v(b, A, qrow, qrow + A, qrow + (G - 1) * A, onehot, scal[0], scal[1], scal[2], scal[3],
+                               t.weights != nullptr, t.delta, 1.f / float(B), t.td_abs, t.next_act, t.td_target,
+                               dqrow);
+    t.partials[2 * b] = r.h;
+    t.partials[2 * b + 1] = r.pred;
+  }
+  __syncthreads();
+  if (tid < A) t.dq[long(b) * A + tid] = dqrow[tid];
+
+  // 4. dh = dq W2_0^T through the first layer's ReLU
+  for (int n = tid; n < F; n += kTailThreads) {
+    const float* w = t.W2[0] + long(n) * A;
+    float s = 0.f;
+#pragma unroll
+    for (int a = 0; a < AP; ++a) s = fmaf(dqrow[a], w[min(a, A - 1)], s);  // dqrow is zero past A
+    t.dh[long(b) * F + n] = hs[n] > 0.f ? s : 0.f;
+  }
+
+  // 5. the last workgroup to finish sums the batch
+  __threadfence();  // this workgroup's rows, dq and partials, visible device-wide before the count
+  __syncthreads();
+  if (tid == 0) last = atomicAdd(t.counter, 1u) == unsigned(gridDim.x - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // acquire: every workgroup's writes are visible to the loads below
+
+  float* part = hs;                   // 2 B per-sample loss terms and predictions
+  float* dqs = hs + kSyncPartials;    // a chunk of dq rows
+  for (int e = tid; e < 2 * B; e += kTailThreads) part[e] = t.partials[e];
+
+  // dW2 = h_0^T dq, two features per thread per pass; dq staged in LDS a
+  // chunk of samples at a time as [kTailChunk][AP] rows, zero past the batch
+  // and past A.  A chunk's h_0 and dq loads are all issued before the barrier
+  // that waits for them: one memory round trip per pass and chunk.
+  constexpr int DQV = (kTailChunk * AP + kTailThreads - 1) / kTailThreads;
+  const float* h0 = t.h[0];
+  float gb = 0.f;
+  for (int n0 = 0; n0 < F; n0 += 2 * kTailThreads) {  // uniform trip counts: the barriers below
+    int nn[2], nc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      nn[i] = n0 + i * kTailThreads + tid;
+      nc[i] = min(nn[i], F - 1);
+    }
+    float gw[2][AP];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int a = 0; a < AP; ++a) gw[i][a] = 0.f;
+    for (int j0 = 0; j0 < B; j0 += kTailChunk) {
+      const int rows = min(kTailChunk, B - j0);
+      float hv[2][kTailChunk], dqv[DQV];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < kTailChunk; ++j) hv[i][j] = h0[long(j0 + min(j, rows - 1)) * F + nc[i]];
+#pragma unroll
+      for (int u = 0; u < DQV; ++u) {
+        const int e = u * kTailThreads + tid, j = e / AP, a = e - j * AP;
+        dqv[u] = t.dq[long(j0 + min(j, rows - 1)) * A + min(a, A - 1)];
+        dqv[u] = j < rows && a < A ? dqv[u] : 0.f;
+      }
+      __syncthreads();  // the previous chunk's readers of dqs are done
+#pragma unroll
+      for (int u = 0; u < DQV; ++u) {
+        const int e = u * kTailThreads + tid;
+        if (e < kTailChunk * AP) dqs[e] = dqv[u];
+      }
+      __syncthreads();
+      if (n0 == 0 && tid < A)
+        for (int j = 0; j < rows; ++j) gb += dqs[j * AP + tid];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < kTailChunk; ++j) hv[i][j] = j < rows ? hv[i][j] : 0.f;
+#pragma unroll
+      for (int j = 0; j < kTailChunk; ++j)
+#pragma unroll
+        for (int a = 0; a < AP; ++a) {
+          const float d = dqs[j * AP + a];
+          gw[0][a] = fmaf(hv[0][j], d, gw[0][a]);
+          gw[1][a] = fmaf(hv[1][j], d, gw[1][a]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (nn[i] < F)
+#pragma unroll
+        for (int a = 0; a < AP; ++a)
+          if (a < A) {
+            float* o = t.dW2 + long(nn[i]) * A + a;
+            *o = t.beta_w != 0.f ? gw[i][a] + t.beta_w * *o : gw[i][a];
+          }
+  }
+  if (t.db2 && tid < A) t.db2[tid] = t.beta_w != 0.f ? gb + t.beta_w * t.db2[tid] : gb;
+  __syncthreads();
+  if (tid == 0) {
+    const float invB = 1.f / float(B);
+    float sh = 0.f, sp = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < B; ++j) {  // sample order: the same sum on every run
+      sh += part[2 * j];
+      sp += part[2 * j + 1];
+    }
+    *t.loss = sh * invB;
+    if (t.mean_q) *t.mean_q = sp * invB;
+    __hip_atomic_store(t.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace ttrl
+
+using namespace ttrl;
+
+extern "C" {
+
+int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* d) {
+  TTRL_REQUIRE(ctx && d, "ttrl_dqn_tail: null argument");
+  const int B = d->B, K = d->K, F = d->F, A = d->A, G = d->groups;
+  TTRL_REQUIRE(G == 2 || G == 3, "ttrl_dqn_tail: 2 (vanilla) or 3 (double) feature sets, got %d", G);
+  TTRL_REQUIRE(B > 0 && B <= kTailMaxB, "ttrl_dqn_tail: batch %d outside [1, %d]", B, kTailMaxB);
+  TTRL_REQUIRE(K > 0 && F > 0 && F <= kTailMaxF, "ttrl_dqn_tail: %d hidden units outside [1, %d]", F, kTailMaxF);
+  TTRL_REQUIRE(A > 0 && A <= kTailMaxA, "ttrl_dqn_tail: %d actions outside [1, %d]", A, kTailMaxA);
+  TTRL_REQUIRE(d->delta > 0.f, "ttrl_dqn_tail: huber delta must be > 0");
+  TTRL_REQUIRE(d->actions_onehot && d->rewards && d->dones && d->discounts && d->loss && d->dq && d->dh && d->dW2,
+               "ttrl_dqn_tail: null argument");
+  TTRL_REQUIRE(long(B) * K * 4 < kMaxOperandBytes && long(K) * F * 4 < kMaxOperandBytes,
+               "ttrl_dqn_tail: an operand of 2^30 bytes or more is not supported");
+  bool al = true;
+  for (int g = 0; g < G; ++g) {
+    TTRL_REQUIRE(d->x[g] && d->W1[g] && d->h[g] && d->W2[g] && d->q[g], "ttrl_dqn_tail: null pointer in set %d", g);
+    al = al && aligned16(d->x[g]);
+  }
+  bool wal = true;
+  for (int g = 0; g < G; ++g) wal = wal && aligned16(d->W1[g]);
+
+  // the first layer, h = relu(x W1 + b1)
+  EpStore ep;
+  ep.M = B;
+  ep.N = F;
+  ep.ldc = F;
+  ep.relu = 1;
+  LdColK lb;  // B(k, n) = W1[k][n]
+  lb.ld = F;
+  lb.rows = F;
+  lb.K = K;
+  LdRowK la;  // A(m, k) = x[m][k]
+  la.ld = K;
+  la.rows = B;
+  la.K = K;
+  for (int g = 0; g < G; ++g) {
+    ep.C[g] = d->h[g];
+    ep.bias[g] = d->b1[g];
+    lb.p[g] = d->W1[g];
+    la.p[g] = d->x[g];
+  }
+  lb.vec_ok(wal);
+  la.vec_ok(al);
+  GemmPlan plan;
+  int rc = run_gemm_deferred<kFc1Cfgs>(ctx, la, lb, ep, B, F, K, G, "ttrl_dqn_tail", &plan);
+  if (rc) return rc;
+
+  TailArgs t{};
+  t.B = B;
+  t.F = F;
+  t.A = A;
+  t.G = G;
+  t.splits = plan.splits > 1 ? plan.splits : 0;
+  long wsf = 0;
+  t.part = ctx_workspace(ctx, &wsf);
+  for (int g = 0; g < 3; ++g) {
+    const int s = g < G ? g : 0;
+    t.h[g] = d->h[s];
+    t.b1[g] = d->b1[s];
+    t.W2[g] = d->W2[s];
+    t.b2[g] = d->b2[s];
+    t.q[g] = d->q[s];
+  }
+  t.onehot = d->actions_onehot;
+  t.rewards = d->rewards;
+  t.dones = d->dones;
+  t.discounts = d->discounts;
+  t.weights = d->is_weights;
+  t.delta = d->delta;
+  t.loss = d->loss;
+  t.mean_q = d->mean_q;
+  t.td_abs = d->td_abs;
+  t.dq = d->dq;
+  t.next_act = d->next_actions;
+  t.td_target = d->td_target;
+  t.dh = d->dh;
+  t.dW2 = d->dW2;
+  t.db2 = d->db2;
+  t.beta_w = d->beta_w;
+  unsigned* words = ctx_sync_words(ctx);
+  t.counter = words + kSyncDqnTail;
+  t.partials = reinterpret_cast<float*>(words + kSyncCounters);
+  const int ap = A <= 8 ? 8 : (A <= 16 ? 16 : 32);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(unsigned(B)), dim3(kTailThreads), 0, stream_of(ctx), t);
+    return check_launch("ttrl_dqn_tail");
+  };
+  if (ap == 8) return launch(k_dqn_tail<8>);
+  if (ap == 16) return launch(k_dqn_tail<16>);
+  return launch(k_dqn_tail<32>);
+}
+
+}  // extern "C"

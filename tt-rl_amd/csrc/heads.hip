@@ -15,6 +15,7 @@
 // sample and log-density in its stable forms, its backward, the twin-critic
 // soft target and loss, and the actor and temperature losses.
 #include "common.hpp"
+#include "dqn_row.hpp"
 
 #include <cmath>
 
@@ -24,55 +25,12 @@ constexpr int kHeadThreads = 256;
 constexpr float kLog2 = 0.69314718055994530942f;
 constexpr float kLog2Pi = 1.83787706640934548356f;
 
-__device__ inline float relu_f(float x) { return x > 0.f ? x : 0.f; }
-
 // softplus(x) = relu(x) + log(1 + exp(-|x|))  (ttrl/algos/gaussian.py:55-62)
 __device__ inline float softplus_f(float x) { return relu_f(x) + logf(expf(-fabsf(x)) + 1.f); }
 
 // min(a, b) through the relu identity a - relu(a - b) (ttrl/engine/ops/select.py:39-47):
 // the gradient goes to b iff a > b.
 __device__ inline float min_relu(float a, float b) { return a - relu_f(a - b); }
-
-// One sample of the DQN head: Q(s, a) of the taken action, the double-DQN
-// target from the selection row `sb` and the valuation row `vb`, Huber,
-// the per-sample outputs and dL/dQ for row b.  Returns (w * huber, pred).
-struct DqnRow {
-  float h, pred;
-};
-__device__ inline DqnRow dqn_row_v(int b, int A, const float* qb, const float* sb, const float* vb, const float* ob,
-                                   float reward, float done, float discount, float w, bool has_w, float delta,
-                                   float invB, float* td_abs, float* next_act, float* td_target, float* dqb) {
-  float pred = 0.f;
-  for (int a = 0; a < A; ++a) pred += qb[a] * ob[a];
-  int best = 0;
-  float bv = sb[0];
-  for (int a = 1; a < A; ++a)
-    if (sb[a] > bv) {
-      bv = sb[a];
-      best = a;
-    }
-  const float nv = vb[best];
-  const float y = reward + (nv * (1.f - done)) * discount;
-  const float e = pred - y;
-  const float ae = fabsf(e);
-  const float quad = ae - relu_f(ae - delta);
-  const float lin = ae - quad;
-  const float h = (quad * quad) * 0.5f + lin * delta;
-  if (td_abs) td_abs[b] = ae;
-  if (next_act) next_act[b] = float(best);
-  if (td_target) td_target[b] = y;
-  const float clip = fminf(fmaxf(e, -delta), delta);
-  const float gscale = (has_w ? w * invB : invB) * clip;
-  for (int a = 0; a < A; ++a) dqb[a] = ob[a] * gscale;
-  return DqnRow{has_w ? h * w : h, pred};
-}
-__device__ inline DqnRow dqn_row(int b, int A, const float* qb, const float* sb, const float* vb, const float* ob,
-                                 const float* rewards, const float* dones, const float* discounts,
-                                 const float* weights, float delta, float invB, float* td_abs, float* next_act,
-                                 float* td_target, float* dqb) {
-  return dqn_row_v(b, A, qb, sb, vb, ob, rewards[b], dones[b], discounts[b], weights ? weights[b] : 1.f,
-                   weights != nullptr, delta, invB, td_abs, next_act, td_target, dqb);
-}
 
 __global__ __launch_bounds__(kHeadThreads) void k_dqn_loss(
     int B, int A, const float* __restrict__ q, const float* __restrict__ qsel, const float* __restrict__ qval,

@@ -1140,6 +1140,47 @@ inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int
   return check_launch(name);
 }
 
+// run_gemm without the split-K reduction, for a consumer kernel that sums
+// the partials itself: when the plan splits K, k_gemm leaves partial tiles
+// at the start of the workspace as [groups][splits][M][N] floats, to be
+// summed in split order from 0.f (as k_splitk_reduce does) and passed
+// through the epilogue by that consumer; with one split the epilogue runs in
+// the GEMM.  *plan receives the plan that ran.
+template <unsigned ALLOWED, class LA, class LB, class EP>
+inline int run_gemm_deferred(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int M, int N, int K,
+                             int groups, const char* name, GemmPlan* plan) {
+  static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
+  if (M <= 0 || N <= 0 || groups <= 0) return set_error(TTRL_EINVAL, "%s: empty GEMM", name);
+  if (groups > kMaxGroups) return set_error(TTRL_EINVAL, "%s: at most %d groups", name, kMaxGroups);
+  if (long(groups) * M * N >= (1L << 31)) return set_error(TTRL_EINVAL, "%s: output too large", name);
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  hipStream_t st = stream_of(ctx);
+  char keybuf[96];
+  snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%ld", M, N, K, groups, wsf);
+  const std::string key = std::string(__PRETTY_FUNCTION__) + keybuf;
+  GemmPlan p;
+  const GemmPlan* hit = ctx_plan_find(ctx, key);
+  if (gemm_forced(ALLOWED, M, N, K, groups, wsf, &p)) {
+  } else if (hit && plan_valid(*hit, M, N, K, groups, wsf, ALLOWED)) {
+    p = *hit;
+  } else {
+    if (!ctx_capturing(ctx) && gemm_tuning_enabled())
+      p = tune_gemm<ALLOWED>(ctx, la, lb, ep, ws, wsf, M, N, K, groups, st);
+    else
+      p = plan_gemm(M, N, K, groups, wsf, ALLOWED);
+    ctx_plan_store(ctx, key, p);
+  }
+  dispatch_cfg<ALLOWED>(p.cfg, [&](auto c) {
+    using C = decltype(c);
+    dim3 grid(ceil_div(M, C::BM), ceil_div(N, C::BN), unsigned(groups * p.splits));
+    hipLaunchKernelGGL((k_gemm<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK, LA, LB, EP>), grid,
+                       dim3(64 * C::WGM * C::WGN * C::WGK), 0, st, la, lb, ep, ws, M, N, K, p.kchunk, p.splits);
+  });
+  *plan = p;
+  return check_launch(name);
+}
+
 // ---------------------------------------------------------- pairs -------
 
 struct GemmDims {

@@ -52,6 +52,21 @@ class LinearDesc(C.Structure):
     ]
 
 
+class DqnTailDesc(C.Structure):
+    """Mirror of ttrl_dqn_tail_desc."""
+
+    _fields_ = [
+        ("B", C.c_int), ("K", C.c_int), ("F", C.c_int), ("A", C.c_int), ("groups", C.c_int),
+        ("x", C.c_void_p * 3), ("W1", C.c_void_p * 3), ("b1", C.c_void_p * 3), ("h", C.c_void_p * 3),
+        ("W2", C.c_void_p * 3), ("b2", C.c_void_p * 3), ("q", C.c_void_p * 3),
+        ("actions_onehot", C.c_void_p), ("rewards", C.c_void_p), ("dones", C.c_void_p),
+        ("discounts", C.c_void_p), ("is_weights", C.c_void_p), ("delta", C.c_float),
+        ("loss", C.c_void_p), ("mean_q", C.c_void_p), ("td_abs", C.c_void_p), ("dq", C.c_void_p),
+        ("next_actions", C.c_void_p), ("td_target", C.c_void_p), ("dh", C.c_void_p), ("dW2", C.c_void_p),
+        ("db2", C.c_void_p), ("beta_w", C.c_float),
+    ]
+
+
 class ReplayRing(C.Structure):
     """Mirror of ttrl_replay_ring."""
 
@@ -124,6 +139,7 @@ SIGNATURES = {
     "ttrl_conv2d_backward": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, P, F, P, P, F], I),
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
+    "ttrl_dqn_tail": ([P, C.POINTER(DqnTailDesc)], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
     "ttrl_q_act": ([P, I, I, I, P, P, P, P, P], I),
     "ttrl_gru_step": ([P, I, I, P, P, P, P, P, P], I),

@@ -29,7 +29,7 @@ from ttrl_amd.engine.autograd import Tensor, no_grad
 from ttrl_amd.engine.conv import Conv2d
 from ttrl_amd.engine import layers as layers_mod
 from ttrl_amd.engine.layers import Linear, ReLU
-from ttrl_amd.engine.ops.fused import dqn_head_td_loss, dqn_td_loss, linear_node
+from ttrl_amd.engine.ops.fused import dqn_head_td_loss, dqn_tail_td_loss, dqn_td_loss, linear_node
 from ttrl_amd.engine.optim import Adam
 from ttrl_amd.engine.step import TrainStep
 from ttrl_amd.engine.tensor import DeviceArray, bound_block
@@ -139,15 +139,15 @@ def _lockstep_layers(nets):
     return stacks
 
 
-def q_forward_multi(nets, inputs, tape_group: int | None = 0, *, skip_last: bool = False):
+def q_forward_multi(nets, inputs, tape_group: int | None = 0, *, skip_last: int = 0):
     """Q values of several same-shaped Q networks, one launch per layer.
 
     `nets[g]` is applied to `inputs[g]`; the evaluations share each layer's
     launch (per-group weight and activation pointers).  Only group
     `tape_group` records a tape (the online network on s); every other group
-    is a constant of the step, as under no_grad in the reference.  With
-    `skip_last` the Q head's last layer is not applied: the features it
-    would consume are returned.
+    is a constant of the step, as under no_grad in the reference.  The last
+    `skip_last` layers (a ReLU counting as one) are not applied: the
+    features they would consume are returned.
     """
     stacks = _lockstep_layers(nets)
     if stacks is None:
@@ -157,7 +157,7 @@ def q_forward_multi(nets, inputs, tape_group: int | None = 0, *, skip_last: bool
         raise ValueError("q_forward_multi: at most 4 networks per launch")
     xs = list(inputs)
     dev = xs[0].device
-    layers0 = stacks[0][:-1] if skip_last else stacks[0]
+    layers0 = stacks[0][:len(stacks[0]) - int(skip_last)]
     i = 0
     while i < len(layers0):
         layer = layers0[i]
@@ -211,9 +211,21 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
     stacks = _lockstep_layers([online, target])
     nets = [online, online, target] if double else [online, target]
     feeds = [obs, next_obs, next_obs] if double else [obs, next_obs]
+    if stacks is not None and _fused_tail_fits(stacks[0], obs):
+        # The last two layers, the loss and the head's backward in one GEMM and one kernel.
+        features = q_forward_multi(nets, feeds, skip_last=3)
+        tails = [_lockstep_layers([n])[0][-3:] for n in nets]
+        loss, extra, hs, qs = dqn_tail_td_loss(features, [t[0] for t in tails], [t[2] for t in tails],
+                                               inputs["actions_onehot"], inputs["rewards"], inputs["dones"],
+                                               inputs["discounts"], inputs["is_weights"] if prioritized else None,
+                                               huber_delta, out=metrics_out)
+        if layers_mod.RECORD is not None:  # the first layer's outputs, then the Q values, of every group
+            layers_mod.RECORD.append(list(hs))
+            layers_mod.RECORD.append(list(qs))
+        return _finish_update(online, loss, extra, prioritized, grad_sq)
     if stacks is not None and _fused_head_fits(stacks[0], obs, len(nets)):
         # The Q head's last layer and the loss in one launch.
-        features = q_forward_multi(nets, feeds, skip_last=True)
+        features = q_forward_multi(nets, feeds, skip_last=1)
         heads = [_lockstep_layers([n])[0][-1] for n in nets]
         loss, extra, qs = dqn_head_td_loss(features, heads, inputs["actions_onehot"], inputs["rewards"],
                                            inputs["dones"], inputs["discounts"],
@@ -237,6 +249,21 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
                               inputs["dones"], inputs["discounts"],
                               inputs["is_weights"] if prioritized else None, huber_delta, out=metrics_out)
     return _finish_update(online, loss, extra, prioritized, grad_sq)
+
+
+def _fused_tail_fits(layers, obs) -> bool:
+    """ttrl_dqn_tail applies to Q networks ending Linear -> ReLU -> Linear
+    (at most 2048 hidden units, 32 actions) at a batch of at most 1024,
+    the last layer's weight its own parameter."""
+    if len(layers) < 3:
+        return False
+    fc1, act, fc2 = layers[-3:]
+    if not (isinstance(fc1, Linear) and isinstance(act, ReLU) and isinstance(fc2, Linear)):
+        return False
+    if fc2.effective_weight() is not fc2.weight or not fc2.weight.requires_grad:
+        return False
+    return (int(fc1.out_features) <= 2048 and 0 < int(fc2.out_features) <= 32 and
+            int(obs.shape[0]) <= 1024)
 
 
 def _fused_head_fits(layers, obs, groups: int) -> bool:

@@ -18,7 +18,7 @@ from ttrl_amd import _lib
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs, relu_mask
 from ttrl_amd.engine.tensor import DeviceArray
 
-__all__ = ["linear", "linear_node", "dqn_td_loss", "grad_targets"]
+__all__ = ["linear", "linear_node", "dqn_td_loss", "dqn_head_td_loss", "dqn_tail_td_loss", "grad_targets"]
 
 
 def _p(arr) -> int | None:
@@ -223,3 +223,80 @@ def dqn_head_td_loss(features, heads, actions_onehot: Tensor, rewards: Tensor, d
     q0 = linear_node(features[0], weights[0], heads[0].bias, qs[0], relu=False)
     out, metrics = _dqn_loss_node(q0, loss, mean_q, td_abs, td_target, next_act, dq)
     return out, metrics, qs
+
+
+def dqn_tail_td_loss(features, fc1s, fc2s, actions_onehot: Tensor, rewards: Tensor, dones: Tensor,
+                     discounts: Tensor, is_weights: Tensor | None, delta: float, out: dict | None = None):
+    """A Q network's last two layers (Linear -> ReLU -> Linear) over 2 or 3
+    feature sets, the DQN loss and the second layer's backward, as one GEMM
+    and one kernel (ttrl_dqn_tail): features[0] = online(s) (taped),
+    features[1] selects a*, features[-1] values it; fc1s[g] / fc2s[g] the
+    matching layers.
+
+    -> (loss, metrics, hs, qs): the loss node and metrics of dqn_td_loss, the
+    first layer's outputs and the Q values of every set.  The second layer's
+    weight and bias gradients are produced with the loss (they depend on the
+    loss alone), so they are written into those parameters' gradients here;
+    the loss node's backward hands the first layer's ReLU node its already
+    gated gradient.  The loss must be the root of the backward pass."""
+    G = len(features)
+    if G not in (2, 3) or len(fc1s) != G or len(fc2s) != G:
+        raise ValueError(f"dqn_tail_td_loss: 2 or 3 feature sets and layer pairs, got {G}")
+    B, K = (int(d) for d in features[0].shape)
+    F, A = int(fc1s[0].out_features), int(fc2s[0].out_features)
+    for x, l1, l2 in zip(features, fc1s, fc2s):
+        if tuple(x.shape) != (B, K) or (int(l1.in_features), int(l1.out_features)) != (K, F) or \
+                (int(l2.in_features), int(l2.out_features)) != (F, A):
+            raise ValueError("dqn_tail_td_loss: feature sets and layers must share their shapes")
+    if tuple(actions_onehot.shape) != (B, A):
+        raise ValueError(f"dqn_tail_td_loss: actions_onehot has shape {actions_onehot.shape}, expected {(B, A)}")
+    for name, t in (("rewards", rewards), ("dones", dones), ("discounts", discounts), ("is_weights", is_weights)):
+        if t is not None and t.data.numel != B:
+            raise ValueError(f"dqn_tail_td_loss: {name} has {t.data.numel} elements, expected {B}")
+    if not delta > 0.0:
+        raise ValueError(f"dqn_tail_td_loss: huber delta must be > 0, got {delta}")
+    head = fc2s[0]
+    if head.effective_weight() is not head.weight:
+        raise ValueError("dqn_tail_td_loss: the second layer's weight must be its parameter (no scale)")
+    dev = features[0].device
+    w1 = [l.effective_weight() for l in fc1s]
+    hs = [DeviceArray(dev, (B, F)) for _ in range(G)]
+    qs = [DeviceArray(dev, (B, A)) for _ in range(G)]
+    loss, mean_q, td_abs, td_target, next_act, dq = _dqn_outputs(dev, B, A, out)
+    dh = DeviceArray(dev, (B, F))
+    (dw2, db2), beta_w = grad_targets(head.weight, head.bias)
+    if dw2 is None:
+        raise ValueError("dqn_tail_td_loss: the second layer's weight must require a gradient")
+    d = _lib.DqnTailDesc()
+    d.B, d.K, d.F, d.A, d.groups = B, K, F, A, G
+    for g in range(G):
+        d.x[g] = features[g].data.ptr
+        d.W1[g] = w1[g].data.ptr
+        d.b1[g] = _p(None if fc1s[g].bias is None else fc1s[g].bias.data)
+        d.h[g] = hs[g].ptr
+        d.W2[g] = fc2s[g].weight.data.ptr
+        d.b2[g] = _p(None if fc2s[g].bias is None else fc2s[g].bias.data)
+        d.q[g] = qs[g].ptr
+    d.actions_onehot = actions_onehot.data.ptr
+    d.rewards, d.dones, d.discounts = rewards.data.ptr, dones.data.ptr, discounts.data.ptr
+    d.is_weights = _p(None if is_weights is None else is_weights.data)
+    d.delta = float(delta)
+    d.loss, d.mean_q, d.td_abs, d.dq = loss.ptr, mean_q.ptr, td_abs.ptr, dq.ptr
+    d.next_actions, d.td_target = next_act.ptr, td_target.ptr
+    d.dh, d.dW2, d.db2, d.beta_w = dh.ptr, dw2.ptr, _p(db2), beta_w
+    dev.call("ttrl_dqn_tail", C.byref(d))
+    h0 = linear_node(features[0], w1[0], fc1s[0].bias, hs[0], relu=True)
+    metrics = {"mean_q": Tensor(mean_q), "td_abs": Tensor(td_abs), "td_target": Tensor(td_target),
+               "next_actions": Tensor(next_act)}
+    if not _needs(h0):
+        return _detached(loss), metrics, hs, qs
+    node = Tensor(loss, True, (h0,), "dqn_td_loss")
+
+    def _backward(grad):
+        if not grad.unit:
+            raise RuntimeError("dqn_tail_td_loss: the fused loss produces the head's gradients for a unit seed; "
+                               "call backward() on the loss itself")
+        h0._accumulate(dh, masked=True)
+
+    node._backward = _backward
+    return node, metrics, hs, qs
