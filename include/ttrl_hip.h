@@ -172,6 +172,14 @@ typedef struct ttrl_linear_desc {
   int dx_col0, dx_cols;
   float beta_w, beta_x;
   const float* dxmask;
+  /* Forward only: per-group pointers (g < groups) in place of base + g *
+   * stride where non-NULL, for groups whose buffers sit at no common stride
+   * (the online and the target critics of one SAC update live in two
+   * parameter arenas). */
+  const float* xg[4];
+  const float* x2g[4];
+  const float* Wg[4];
+  const float* bg[4];
 } ttrl_linear_desc;
 
 int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* desc);
@@ -341,6 +349,43 @@ int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v
 int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, float* v_s, long n, int* step,
                           float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
                           int accumulate_grad_sq);
+/* Deferred Adam steps, for an update that steps several optimizers (the
+ * SAC critic, then actor and temperature, then the Polyak blend,
+ * ttrl/algos/sac/agent.py:229-236) in fewer launches.
+ * ttrl_adam_step_deferred is ttrl_adam_step without its finish: *step is
+ * read, not stored, and the per-workgroup partial sums of g^2 go to partial
+ * slot `slot` (0 <= slot < 8) of the context, which keeps them until
+ * ttrl_adam_finish_slots.  ttrl_adam_multi runs up to 4 deferred ranges and
+ * a Polyak blend dst = (1 - tau) dst + tau src (ttrl/algos/sac/targets.py:45-52;
+ * polyak_n may be 0) in one launch.  ttrl_adam_finish_slots finishes up to 8
+ * deferred steps in one launch: the partials of each slot (a range of n
+ * parameters) summed into *grad_sq (added when accumulate; grad_sq may be
+ * NULL) and *step incremented.  Each range gives the same bits as
+ * ttrl_adam_step (ttrl/engine/optim/adam.py:93-134), grad_sq included.  A
+ * slot must not be reused between its step and its finish. */
+typedef struct ttrl_adam_range {
+  float* p;
+  const float* g;
+  float* m_s;
+  float* v_s;
+  long n;
+  const int* step;
+  float lr, beta1, beta2, eps, weight_decay;
+  int slot;
+} ttrl_adam_range;
+typedef struct ttrl_adam_finish {
+  int slot;
+  long n;
+  int* step;
+  float* grad_sq;
+  int accumulate;
+} ttrl_adam_finish;
+int ttrl_adam_step_deferred(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n,
+                            const int* step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                            int slot);
+int ttrl_adam_multi(ttrl_ctx* ctx, int nranges, const ttrl_adam_range* ranges, float* polyak_dst,
+                    const float* polyak_src, long polyak_n, float tau);
+int ttrl_adam_finish_slots(ttrl_ctx* ctx, int n, const ttrl_adam_finish* finishes);
 /* sum(x^2) into *out (grad_sq_device, ttrl/algos/grads.py:46-60). */
 int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate);
 /* dst = (1 - tau) * dst + tau * src (ttrl/algos/sac/targets.py:45-52). */

@@ -38,23 +38,22 @@ def build_sac(device, *, seed=0, step_mode="graph", batch=256):
 
 
 def record_gates(records, B):
-    """Device ReLU outputs in execution order -> oracle gate names."""
-    names = []
+    """Device ReLU outputs in execution order -> oracle gate names: the
+    policy over [obs; next_obs] (one record per layer), the target critics
+    and the critics as four groups (target 0, target 1, critic 0, critic 1),
+    then the critics on the actor's actions."""
     out = {}
     it = iter(records)
-
-    def twin(prefix, suffix=""):
-        for layer in range(2):
-            y = next(it).numpy().reshape(2, B, -1)
-            out[f"{prefix}0{suffix}.{layer}"] = y[0] > 0
-            out[f"{prefix}1{suffix}.{layer}"] = y[1] > 0
-
     for layer in range(2):
-        out[f"policy_next.{layer}"] = next(it).numpy() > 0
-    twin("target")
-    twin("critic")
+        y = next(it).numpy().reshape(2, B, -1)
+        out[f"policy.{layer}"] = y[0] > 0
+        out[f"policy_next.{layer}"] = y[1] > 0
     for layer in range(2):
-        out[f"policy.{layer}"] = next(it).numpy() > 0
-    twin("critic", "_pi")
-    del names
+        y = next(it).numpy().reshape(4, B, -1)
+        for g, name in enumerate(("target0", "target1", "critic0", "critic1")):
+            out[f"{name}.{layer}"] = y[g] > 0
+    for layer in range(2):
+        y = next(it).numpy().reshape(2, B, -1)
+        out[f"critic0_pi.{layer}"] = y[0] > 0
+        out[f"critic1_pi.{layer}"] = y[1] > 0
     return out

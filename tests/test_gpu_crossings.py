@@ -96,6 +96,7 @@ def test_sac_update_from_a_host_batch_is_one_call(device):
             assert m["critic_loss"] == float(blk[0]) and m["alpha"] == float(blk[1])
             assert m["actor_loss"] == float(blk[2]) and m["alpha_loss"] == float(blk[3])
             assert np.array_equal(m["q_target"], blk[8:8 + B])
-            assert np.array_equal(m["logp"], blk[8 + B:8 + 2 * B])
+            # td_abs at 8 + B, then the log-probabilities of obs (the metric) and next_obs
+            assert np.array_equal(m["logp"], blk[8 + 2 * B:8 + 3 * B])
     finally:
         learner.close()

@@ -21,6 +21,10 @@ constexpr int kSyncCounters = 64, kSyncPartials = 2 * 1024;
 constexpr int kSyncDqnHead = 0;  // counter of ttrl_dqn_head
 constexpr int kSyncDqnTail = 1;  // counter of ttrl_dqn_tail
 unsigned* ctx_sync_words(ttrl_ctx* ctx);
+// Partial sums of deferred Adam steps: kAdamSlots slots of kAdamSlotFloats,
+// each kept from its step to its finish (ttrl_adam_finish_slots).
+constexpr int kAdamSlots = 8, kAdamSlotFloats = 1024;
+float* ctx_adam_partials(ttrl_ctx* ctx);
 // Converts a pending launch error into a status code.
 int check_launch(const char* name);
 

@@ -338,6 +338,12 @@ int ttrl_linear_forward(ttrl_ctx* ctx, const ttrl_linear_desc* d) {
   groups_of(W2, d->W2, d->gW, d->groups);
   groups_of(b2, d->b2, d->gb, d->groups);
   groups_of(y, d->y, d->gy, d->groups);
+  for (int g = 0; g < d->groups; ++g) {
+    if (d->xg[g]) x[g] = d->xg[g];
+    if (d->x2g[g]) x2[g] = d->x2g[g];
+    if (d->Wg[g]) W[g] = d->Wg[g];
+    if (d->bg[g]) b[g] = d->bg[g];
+  }
   return linear_forward_tables(ctx, d->M, d->K, d->N, d->groups, x, d->ldx, x2, d->ldx2, k1, W, b, W2, b2, n1, y,
                                d->relu, d->clamp_col, d->lo, d->hi, "ttrl_linear_forward");
 }

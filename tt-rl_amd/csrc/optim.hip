@@ -26,10 +26,14 @@ constexpr int kOptMaxBlocks = 1024;
 
 float* ctx_workspace(ttrl_ctx* ctx, long* floats);
 
-__global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, const float* __restrict__ g,
-                                                      float* __restrict__ S, float* __restrict__ V, long n,
-                                                      const int* __restrict__ step, float lr, float b1, float b2,
-                                                      float eps, float wd, float* __restrict__ partials) {
+// Block `blk` of `nblk` of one Adam update: its grid-stride share of the
+// range and its partial sum of g^2 into partials[blk].  The same code serves
+// a single-range launch and a range of a multi-range launch, so both give
+// the same bits.
+__device__ __forceinline__ void adam_block(float* __restrict__ p, const float* __restrict__ g,
+                                           float* __restrict__ S, float* __restrict__ V, long n,
+                                           const int* __restrict__ step, float lr, float b1, float b2, float eps,
+                                           float wd, float* __restrict__ partials, int blk, int nblk) {
   __shared__ float sc[2];
   __shared__ float red[kOptThreads / 64];
   if (threadIdx.x == 0) {
@@ -44,8 +48,8 @@ __global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, con
   const float alpha_t = sc[0], eps_t = sc[1];
   float gsq = 0.f;
   const long n4 = n / 4;
-  const long stride = long(gridDim.x) * kOptThreads;
-  for (long i = blockIdx.x * long(kOptThreads) + threadIdx.x; i < n4; i += stride) {
+  const long stride = long(nblk) * kOptThreads;
+  for (long i = blk * long(kOptThreads) + threadIdx.x; i < n4; i += stride) {
     f32x4 pv = reinterpret_cast<f32x4*>(p)[i];
     const f32x4 gv = reinterpret_cast<const f32x4*>(g)[i];
     f32x4 sv = reinterpret_cast<f32x4*>(S)[i];
@@ -65,7 +69,7 @@ __global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, con
     reinterpret_cast<f32x4*>(V)[i] = vv;
   }
   // Tail (n % 4) handled by block 0.
-  if (blockIdx.x == 0) {
+  if (blk == 0) {
     for (long i = n4 * 4 + threadIdx.x; i < n; i += kOptThreads) {
       const float graw = g[i];
       gsq += graw * graw;
@@ -76,7 +80,76 @@ __global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, con
     }
   }
   const float tot = block_sum<kOptThreads>(gsq, red);
-  if (threadIdx.x == 0) partials[blockIdx.x] = tot;
+  if (threadIdx.x == 0) partials[blk] = tot;
+}
+
+__global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, const float* __restrict__ g,
+                                                      float* __restrict__ S, float* __restrict__ V, long n,
+                                                      const int* __restrict__ step, float lr, float b1, float b2,
+                                                      float eps, float wd, float* __restrict__ partials) {
+  adam_block(p, g, S, V, n, step, lr, b1, b2, eps, wd, partials, int(blockIdx.x), int(gridDim.x));
+}
+
+// Up to kMultiRanges deferred Adam ranges and a Polyak blend in one launch:
+// blocks [r.block0, r.block0 + r.blocks) run range r (r.blocks = the grid a
+// single-range launch of it uses), the rest the blend.
+constexpr int kMultiRanges = 4;
+struct AdamRange {
+  float* p;
+  const float* g;
+  float* S;
+  float* V;
+  long n;
+  const int* step;
+  float lr, b1, b2, eps, wd;
+  float* partials;
+  int block0, blocks;
+};
+struct AdamMulti {
+  AdamRange r[kMultiRanges];
+  int nr;
+  float* pd;
+  const float* ps;
+  long pn;
+  float keep, tau;
+  int pblock0, pblocks;
+};
+__global__ __launch_bounds__(kOptThreads) void k_adam_multi(AdamMulti a) {
+  const int b = int(blockIdx.x);
+#pragma unroll
+  for (int i = 0; i < kMultiRanges; ++i) {
+    if (i >= a.nr) break;
+    const AdamRange& r = a.r[i];
+    if (b >= r.block0 && b < r.block0 + r.blocks) {
+      adam_block(r.p, r.g, r.S, r.V, r.n, r.step, r.lr, r.b1, r.b2, r.eps, r.wd, r.partials, b - r.block0,
+                 r.blocks);
+      return;
+    }
+  }
+  const long stride = long(a.pblocks) * kOptThreads;
+  for (long i = (b - a.pblock0) * long(kOptThreads) + threadIdx.x; i < a.pn; i += stride)
+    a.pd[i] = a.pd[i] * a.keep + a.ps[i] * a.tau;
+}
+
+// The finishes of up to kAdamSlots deferred steps, one block each: the
+// partials of slot f.slot[b] summed as k_finish sums them.
+struct FinishSlots {
+  const float* parts[kAdamSlots];
+  int count[kAdamSlots];
+  int* step[kAdamSlots];
+  float* out[kAdamSlots];
+  int accumulate[kAdamSlots];
+};
+__global__ __launch_bounds__(kOptThreads) void k_finish_slots(FinishSlots f) {
+  __shared__ float red[kOptThreads / 64];
+  const int b = int(blockIdx.x);
+  float s = 0.f;
+  for (int i = threadIdx.x; i < f.count[b]; i += kOptThreads) s += f.parts[b][i];
+  const float tot = block_sum<kOptThreads>(s, red);
+  if (threadIdx.x == 0) {
+    if (f.out[b]) *f.out[b] = f.accumulate[b] ? *f.out[b] + tot : tot;
+    *f.step[b] = *f.step[b] + 1;
+  }
 }
 
 __global__ __launch_bounds__(kOptThreads) void k_finish(const float* __restrict__ partials, int nparts,
@@ -216,6 +289,77 @@ int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, fl
   hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, partials, int(blocks), step, grad_sq,
                      accumulate_grad_sq);
   return check_launch("ttrl_adam_step_static");
+}
+
+int ttrl_adam_step_deferred(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n,
+                            const int* step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                            int slot) {
+  TTRL_REQUIRE(ctx, "ttrl_adam_step_deferred: null ctx");
+  int rc = check_adam_args(p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, "ttrl_adam_step_deferred");
+  if (rc) return rc;
+  TTRL_REQUIRE(slot >= 0 && slot < kAdamSlots, "ttrl_adam_step_deferred: slot %d outside [0, %d)", slot,
+               kAdamSlots);
+  static_assert(kAdamSlotFloats >= kOptMaxBlocks, "a slot holds one launch's partials");
+  hipLaunchKernelGGL(k_adam, dim3(grid_for(n, 4)), dim3(kOptThreads), 0, stream_of(ctx), p, g, m_s, v_s, n, step,
+                     lr, beta1, beta2, eps, weight_decay, ctx_adam_partials(ctx) + long(slot) * kAdamSlotFloats);
+  return check_launch("ttrl_adam_step_deferred");
+}
+
+int ttrl_adam_multi(ttrl_ctx* ctx, int nranges, const ttrl_adam_range* ranges, float* polyak_dst,
+                    const float* polyak_src, long polyak_n, float tau) {
+  TTRL_REQUIRE(ctx, "ttrl_adam_multi: null ctx");
+  TTRL_REQUIRE(nranges >= 0 && nranges <= kMultiRanges && (nranges == 0 || ranges),
+               "ttrl_adam_multi: %d ranges outside [0, %d]", nranges, kMultiRanges);
+  TTRL_REQUIRE(polyak_n >= 0 && (polyak_n == 0 || (polyak_dst && polyak_src)),
+               "ttrl_adam_multi: null Polyak buffer");
+  TTRL_REQUIRE(tau >= 0.f && tau <= 1.f, "ttrl_adam_multi: tau must be in [0, 1]");
+  AdamMulti a{};
+  a.nr = nranges;
+  int blocks = 0;
+  bool slot_used[kAdamSlots] = {};
+  for (int i = 0; i < nranges; ++i) {
+    const ttrl_adam_range& r = ranges[i];
+    int rc = check_adam_args(r.p, r.g, r.m_s, r.v_s, r.n, r.step, r.lr, r.beta1, r.beta2, r.eps, r.weight_decay,
+                             "ttrl_adam_multi");
+    if (rc) return rc;
+    TTRL_REQUIRE(r.slot >= 0 && r.slot < kAdamSlots && !slot_used[r.slot],
+                 "ttrl_adam_multi: range %d: slot %d outside [0, %d) or taken twice", i, r.slot, kAdamSlots);
+    slot_used[r.slot] = true;
+    const int nb = int(grid_for(r.n, 4));
+    a.r[i] = AdamRange{r.p, r.g, r.m_s, r.v_s, r.n, r.step, r.lr, r.beta1, r.beta2, r.eps, r.weight_decay,
+                       ctx_adam_partials(ctx) + long(r.slot) * kAdamSlotFloats, blocks, nb};
+    blocks += nb;
+  }
+  a.pd = polyak_dst;
+  a.ps = polyak_src;
+  a.pn = polyak_n;
+  a.keep = 1.f - tau;
+  a.tau = tau;
+  a.pblock0 = blocks;
+  a.pblocks = polyak_n > 0 ? int(grid_for(polyak_n)) : 0;
+  blocks += a.pblocks;
+  if (blocks == 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_adam_multi, dim3(unsigned(blocks)), dim3(kOptThreads), 0, stream_of(ctx), a);
+  return check_launch("ttrl_adam_multi");
+}
+
+int ttrl_adam_finish_slots(ttrl_ctx* ctx, int n, const ttrl_adam_finish* f) {
+  TTRL_REQUIRE(ctx && (n == 0 || f), "ttrl_adam_finish_slots: null argument");
+  TTRL_REQUIRE(n >= 0 && n <= kAdamSlots, "ttrl_adam_finish_slots: %d finishes outside [0, %d]", n, kAdamSlots);
+  if (n == 0) return TTRL_OK;
+  FinishSlots fs{};
+  for (int i = 0; i < n; ++i) {
+    TTRL_REQUIRE(f[i].slot >= 0 && f[i].slot < kAdamSlots, "ttrl_adam_finish_slots: slot %d outside [0, %d)",
+                 f[i].slot, kAdamSlots);
+    TTRL_REQUIRE(f[i].n > 0 && f[i].step, "ttrl_adam_finish_slots: finish %d: empty range or null step", i);
+    fs.parts[i] = ctx_adam_partials(ctx) + long(f[i].slot) * kAdamSlotFloats;
+    fs.count[i] = int(grid_for(f[i].n, 4));
+    fs.step[i] = f[i].step;
+    fs.out[i] = f[i].grad_sq;
+    fs.accumulate[i] = f[i].accumulate;
+  }
+  hipLaunchKernelGGL(k_finish_slots, dim3(unsigned(n)), dim3(kOptThreads), 0, stream_of(ctx), fs);
+  return check_launch("ttrl_adam_finish_slots");
 }
 
 int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate) {

@@ -58,6 +58,7 @@ struct ttrl_ctx {
   float* ws = nullptr;  // stream-ordered scratch of split-K GEMMs and reductions
   long ws_floats = 0;
   unsigned* sync = nullptr;  // zeroed counters and partials (ctx_sync_words)
+  float* adam_parts = nullptr;  // ctx_adam_partials
   // GEMM plans chosen by timing candidates on this device, by call signature.
   std::unordered_map<std::string, ttrl::GemmPlan> plans;
   float* tune_out = nullptr;  // output sink of candidate runs
@@ -95,6 +96,8 @@ int hip_error(hipError_t e, const char* what) {
 hipStream_t stream_of(ttrl_ctx* ctx) { return ctx->stream; }
 
 unsigned* ctx_sync_words(ttrl_ctx* ctx) { return ctx->sync; }
+
+float* ctx_adam_partials(ttrl_ctx* ctx) { return ctx->adam_parts; }
 
 float* ctx_workspace(ttrl_ctx* ctx, long* floats) {
   if (floats) *floats = ctx->ws_floats;
@@ -230,6 +233,16 @@ int ttrl_init(int device, ttrl_ctx** out) {
     return hip_error(e, "hipMalloc (sync words)");
   }
   ctx->sync = static_cast<unsigned*>(sync);
+  void* parts = nullptr;
+  e = hipMalloc(&parts, sizeof(float) * kAdamSlots * kAdamSlotFloats);
+  if (e != hipSuccess) {
+    (void)hipFree(sync);
+    (void)hipFree(ws);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_error(e, "hipMalloc (Adam partial slots)");
+  }
+  ctx->adam_parts = static_cast<float*>(parts);
   ctx->pools.emplace_back();  // pool 0: the default pool
   ctx->pools[0].in_use = true;
   *out = ctx;
@@ -243,6 +256,7 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   for (auto& p : ctx->pools) pool_free_slabs(p);
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->sync) (void)hipFree(ctx->sync);
+  if (ctx->adam_parts) (void)hipFree(ctx->adam_parts);
   if (ctx->tune_out) (void)hipFree(ctx->tune_out);
   if (ctx->tune0) (void)hipEventDestroy(ctx->tune0);
   if (ctx->tune1) (void)hipEventDestroy(ctx->tune1);

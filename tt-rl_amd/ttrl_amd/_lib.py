@@ -49,7 +49,25 @@ class LinearDesc(C.Structure):
         ("dx_col0", C.c_int), ("dx_cols", C.c_int),
         ("beta_w", C.c_float), ("beta_x", C.c_float),
         ("dxmask", C.c_void_p),
+        ("xg", C.c_void_p * 4), ("x2g", C.c_void_p * 4), ("Wg", C.c_void_p * 4), ("bg", C.c_void_p * 4),
     ]
+
+
+class AdamRange(C.Structure):
+    """Mirror of ttrl_adam_range."""
+
+    _fields_ = [
+        ("p", C.c_void_p), ("g", C.c_void_p), ("m_s", C.c_void_p), ("v_s", C.c_void_p), ("n", C.c_long),
+        ("step", C.c_void_p), ("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+        ("weight_decay", C.c_float), ("slot", C.c_int),
+    ]
+
+
+class AdamFinish(C.Structure):
+    """Mirror of ttrl_adam_finish."""
+
+    _fields_ = [("slot", C.c_int), ("n", C.c_long), ("step", C.c_void_p), ("grad_sq", C.c_void_p),
+                ("accumulate", C.c_int)]
 
 
 class DqnTailDesc(C.Structure):
@@ -158,6 +176,9 @@ SIGNATURES = {
     "ttrl_sac_actor_loss": ([P, I, P, P, P, F, I, P, P, P, P, P], I),
     "ttrl_adam_step": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
     "ttrl_adam_step_static": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
+    "ttrl_adam_step_deferred": ([P, P, P, P, P, L, P, F, F, F, F, F, I], I),
+    "ttrl_adam_multi": ([P, I, C.POINTER(AdamRange), P, P, L, F], I),
+    "ttrl_adam_finish_slots": ([P, I, C.POINTER(AdamFinish)], I),
     "ttrl_sum_squares": ([P, P, L, P, I], I),
     "ttrl_polyak": ([P, P, P, L, F], I),
     "ttrl_gae": ([P, I, I, P, P, P, P, P, C.c_double, C.c_double, P, P], I),

@@ -111,28 +111,32 @@ class _HubOutput(Tensor):
         self._hub.grad[self._key].extend((g0, g1))
 
 
-def squashed_sample(head: Tensor, noise: Tensor, scale: ActionScale, log_std_min: float = -20.0,
-                    log_std_max: float = 2.0, logp_out: DeviceArray | None = None):
-    """One-kernel reparameterised sample from packed [mean | log_std] rows
-    (log_std already clamped).  -> (action (B, d), logp (B, 1)).  `logp_out`
-    may give the (B, 1) array the log-probabilities are written to."""
-    B, two_d = (int(s) for s in head.shape)
+def _sample_launch(head: DeviceArray, noise: DeviceArray, scale: ActionScale, action: DeviceArray,
+                   logp: DeviceArray) -> DeviceArray:
+    """ttrl_sac_sample over every row of `head`; -> u, the pre-squash sample."""
+    rows, two_d = (int(s) for s in head.shape)
     d = two_d // 2
-    if two_d != 2 * d or tuple(noise.shape) != (B, d):
+    if two_d != 2 * d or tuple(noise.shape) != (rows, d):
         raise ValueError(f"squashed_sample: head {head.shape} and noise {noise.shape} disagree")
-    dev = head.device
     if scale._centre is None:
         raise ValueError("squashed_sample needs the device-resident bounds; construct ActionScale with a device")
-    centre, half = scale._centre.data, scale._scale.data
-    action = DeviceArray(dev, (B, d))
-    if logp_out is not None and (logp_out.numel != B or logp_out.dtype != np.float32):
-        raise ValueError(f"squashed_sample: logp_out must hold {B} float32 values")
-    logp = DeviceArray(dev, (B, 1)) if logp_out is None else logp_out.reshape((B, 1))
-    u = DeviceArray(dev, (B, d))
-    dev.call("ttrl_sac_sample", B, d, head.data.vp, noise.data.vp, centre.vp, half.vp, C.c_float(scale.log_det),
-             action.vp, logp.vp, u.vp)
-    if not _needs(head):
-        return Tensor(action), Tensor(logp)
+    if logp.numel != rows or logp.dtype != np.float32 or action.numel != rows * d:
+        raise ValueError(f"squashed_sample: outputs must hold {rows} rows")
+    dev = head.dev
+    u = DeviceArray(dev, (rows, d))
+    dev.call("ttrl_sac_sample", rows, d, head.vp, noise.vp, scale._centre.data.vp, scale._scale.data.vp,
+             C.c_float(scale.log_det), action.vp, logp.vp, u.vp)
+    return u
+
+
+def _sample_tape(head: Tensor, noise: DeviceArray, u: DeviceArray, action: DeviceArray, logp: DeviceArray,
+                 scale: ActionScale, log_std_min: float, log_std_max: float):
+    """The tape of one sample launch's rows: (action, logp) tensors whose
+    backward is one ttrl_sac_sample_backward into `head`."""
+    B, two_d = (int(s) for s in head.shape)
+    d = two_d // 2
+    dev = head.device
+    half = scale._scale.data
     hub = Tensor(None, True, (head,), "squashed_sample")
     hub.grad = None
     outs = []
@@ -142,7 +146,7 @@ def squashed_sample(head: Tensor, noise: Tensor, scale: ActionScale, log_std_min
         t._key = key
         outs.append(t)
     parts = {"action": [], "logp": []}
-    head_data, noise_data = head.data, noise.data
+    head_data = head.data
 
     def _arm(grad_holder=parts):
         hub.grad = grad_holder
@@ -159,10 +163,51 @@ def squashed_sample(head: Tensor, noise: Tensor, scale: ActionScale, log_std_min
         while len(gl) > 1:
             gl = [K.binary("add", gl[0], gl[1])] + gl[2:]
         dh = DeviceArray(dev, (B, 2 * d))
-        dev.call("ttrl_sac_sample_backward", B, d, head_data.vp, noise_data.vp, u.vp, half.vp,
+        dev.call("ttrl_sac_sample_backward", B, d, head_data.vp, noise.vp, u.vp, half.vp,
                  ga[0].vp if ga else None, ga[1].vp if len(ga) > 1 else None, gl[0].vp if gl else None,
                  C.c_float(log_std_min), C.c_float(log_std_max), dh.vp, C.c_float(0.0))
         head._accumulate(dh)
 
     hub._backward = _backward
     return outs[0], outs[1]
+
+
+def squashed_sample(head: Tensor, noise: Tensor, scale: ActionScale, log_std_min: float = -20.0,
+                    log_std_max: float = 2.0, logp_out: DeviceArray | None = None):
+    """One-kernel reparameterised sample from packed [mean | log_std] rows
+    (log_std already clamped).  -> (action (B, d), logp (B, 1)).  `logp_out`
+    may give the (B, 1) array the log-probabilities are written to."""
+    B, two_d = (int(s) for s in head.shape)
+    dev = head.device
+    action = DeviceArray(dev, (B, two_d // 2))
+    if logp_out is not None and (logp_out.numel != B or logp_out.dtype != np.float32):
+        raise ValueError(f"squashed_sample: logp_out must hold {B} float32 values")
+    logp = DeviceArray(dev, (B, 1)) if logp_out is None else logp_out.reshape((B, 1))
+    u = _sample_launch(head.data, noise.data, scale, action, logp)
+    if not _needs(head):
+        return Tensor(action), Tensor(logp)
+    return _sample_tape(head, noise.data, u, action, logp, scale, log_std_min, log_std_max)
+
+
+def squashed_sample_rows(head: Tensor, head_all: DeviceArray, noise_all: DeviceArray, scale: ActionScale,
+                         logp_all: DeviceArray, log_std_min: float = -20.0, log_std_max: float = 2.0):
+    """squashed_sample over every row of `head_all` in one launch, the tape
+    over its first B rows (`head`, a tape node whose data views them).
+    -> (action, logp) tensors of the first B rows and (action, logp) arrays
+    of the rest; `logp_all` receives every row's log-probability."""
+    B = int(head.shape[0])
+    rows, two_d = (int(s) for s in head_all.shape)
+    d = two_d // 2
+    if head.data.ptr != head_all.ptr or rows <= B:
+        raise ValueError("squashed_sample_rows: head must view the leading rows of head_all")
+    dev = head_all.dev
+    action_all = DeviceArray(dev, (rows, d))
+    u = _sample_launch(head_all, noise_all, scale, action_all, logp_all.reshape((rows, 1)))
+    action = action_all.view(0, (B, d))
+    logp = logp_all.view(0, (B, 1))
+    rest = (action_all.view(B * d, (rows - B, d)), logp_all.view(B, (rows - B, 1)))
+    if not _needs(head):
+        return Tensor(action), Tensor(logp), rest
+    a, lp = _sample_tape(head, noise_all.view(0, (B, d)), u.view(0, (B, d)), action, logp, scale, log_std_min,
+                         log_std_max)
+    return a, lp, rest

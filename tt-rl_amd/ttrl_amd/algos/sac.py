@@ -28,7 +28,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ttrl_amd import _lib
-from ttrl_amd.algos.gaussian import ActionScale, squashed_sample
+from ttrl_amd.algos.gaussian import ActionScale, squashed_sample, squashed_sample_rows
 from ttrl_amd.algos.state import TOWERS_SAC, assemble, from_reference_keys, to_reference_keys, validate
 from ttrl_amd.buffers.replay import PriorityConfig
 from ttrl_amd.nets.acting import ActingNet, SquashedDecision
@@ -36,13 +36,13 @@ from ttrl_amd.engine.autograd import Tensor, _needs, no_grad
 from ttrl_amd.engine import layers as layers_mod
 from ttrl_amd.engine.layers import Linear, ReLU
 from ttrl_amd.engine.ops import _kernels as K
-from ttrl_amd.engine.ops.fused import grad_targets
-from ttrl_amd.engine.optim import Adam
+from ttrl_amd.engine.ops.fused import grad_targets, linear_node
+from ttrl_amd.engine.optim import Adam, adam_multi, finish_steps
 from ttrl_amd.engine.step import InputBinder, MetricReader
 from ttrl_amd.engine.tensor import DeviceArray, ParamArena, bound_block
 from ttrl_amd.engine.trace import capture
 from ttrl_amd.nets.build import build_sac_nets
-from ttrl_amd.nets.heads import GaussianHead
+from ttrl_amd.nets.heads import GaussianHead, packed_linear_pair_rows
 
 __all__ = ["SACConfig", "SACLearner", "TwinQ", "sac_critic_loss", "sac_actor_losses"]
 
@@ -143,35 +143,36 @@ class TwinQ:
                 out += [lin.weight, lin.bias]
         return out
 
-    def forward(self, obs: Tensor | None = None, action: Tensor | None = None, *, obs_action: Tensor | None = None,
-                train_params: bool = True) -> Tensor:
-        """Q of both critics, (2, B, 1).  Pass a dense concat(s, a) as
-        `obs_action` (required when training the critics) or `obs` and
-        `action` separately."""
-        lins = self.layers[0]
-        if obs_action is not None:
-            x, x2 = obs_action, None
-        else:
-            x, x2 = obs, action
-        B = int(x.shape[0])
-        dev = x.device
-        S = self.stride
+    def _run_layers(self, dev, B: int, sets, first: dict) -> list:
+        """Every layer of len(sets) critics (sets[g]: critic g's Linear
+        layers, all of one shape) in one launch per layer; the first layer
+        reads concat(first["x"][g], first["x2"][g]).  -> each layer's output,
+        (G, B, N)."""
+        G = len(sets)
         acts = []
         h = None
-        nl = len(lins)
-        for j, lin in enumerate(lins):
+        nl = len(sets[0])
+        for j in range(nl):
+            lin = sets[0][j]
             N = lin.out_features
-            y = DeviceArray(dev, (2, B, N))
+            y = DeviceArray(dev, (G, B, N))
             d = _lib.LinearDesc()
-            d.M, d.K, d.N, d.groups = B, lin.in_features, N, 2
+            d.M, d.K, d.N, d.groups = B, lin.in_features, N, G
             if j == 0:
-                d.x, d.ldx, d.gx = x.data.ptr, int(x.shape[1]), 0
+                d.x, d.ldx = first["x"][0], first["ldx"]
+                x2 = first.get("x2")
                 if x2 is not None:
-                    d.x2, d.ldx2, d.gx2, d.k1 = x2.data.ptr, int(x2.shape[1]), 0, int(x.shape[1])
+                    d.x2, d.ldx2, d.k1 = x2[0], first["ldx2"], first["k1"]
+                for g in range(G):
+                    d.xg[g] = first["x"][g]
+                    if x2 is not None:
+                        d.x2g[g] = x2[g]
             else:
-                d.x, d.ldx, d.gx = h.ptr, lins[j - 1].out_features, B * lins[j - 1].out_features
-            d.W, d.gW = lin.weight.data.ptr, S
-            d.b, d.gb = lin.bias.data.ptr, S
+                prev = sets[0][j - 1].out_features
+                d.x, d.ldx, d.gx = h.ptr, prev, B * prev
+            d.W, d.b = lin.weight.data.ptr, lin.bias.data.ptr
+            for g in range(G):
+                d.Wg[g], d.bg[g] = sets[g][j].weight.data.ptr, sets[g][j].bias.data.ptr
             d.y, d.gy = y.ptr, B * N
             d.relu = int(j < nl - 1)
             dev.call("ttrl_linear_forward", C.byref(d))
@@ -179,6 +180,49 @@ class TwinQ:
                 layers_mod.RECORD.append(y)
             acts.append(y)
             h = y
+        return acts
+
+    def forward(self, obs: Tensor | None = None, action: Tensor | None = None, *, obs_action: Tensor | None = None,
+                train_params: bool = True) -> Tensor:
+        """Q of both critics, (2, B, 1).  Pass a dense concat(s, a) as
+        `obs_action` (required when training the critics) or `obs` and
+        `action` separately."""
+        if obs_action is not None:
+            x, x2 = obs_action, None
+        else:
+            x, x2 = obs, action
+        B = int(x.shape[0])
+        first = {"x": [x.data.ptr] * 2, "ldx": int(x.shape[1])}
+        if x2 is not None:
+            first.update(x2=[x2.data.ptr] * 2, ldx2=int(x2.shape[1]), k1=int(x.shape[1]))
+        acts = self._run_layers(x.device, B, self.layers, first)
+        return self._tape(x, x2, acts, train_params)
+
+    def forward_with_targets(self, targets: "TwinQ", next_obs: Tensor, next_action: DeviceArray, obs: Tensor,
+                             action: Tensor, obs_action: Tensor):
+        """The target critics on (s', a') and these critics on (s, a), four
+        groups of one launch per layer.  -> (q (2, B, 1) on the tape, its
+        first-layer weight gradient read from the dense `obs_action`;
+        q_next (2, B, 1) off the tape)."""
+        B = int(obs.shape[0])
+        if tuple(int(d) for d in next_action.shape) != (B, self.act_dim):
+            raise ValueError(f"TwinQ: next_action must be ({B}, {self.act_dim})")
+        first = {"x": [next_obs.data.ptr] * 2 + [obs.data.ptr] * 2, "ldx": self.obs_dim,
+                 "x2": [next_action.ptr] * 2 + [action.data.ptr] * 2, "ldx2": self.act_dim, "k1": self.obs_dim}
+        acts = self._run_layers(obs.device, B, list(targets.layers) + list(self.layers), first)
+        online = [a.view(2 * B * int(a.shape[2]), (2, B, int(a.shape[2]))) for a in acts]
+        q_next = Tensor(acts[-1].view(0, (2, B, 1)))
+        return self._tape(obs_action, None, online, True), q_next
+
+    def _tape(self, x: Tensor, x2: Tensor | None, acts: list, train_params: bool) -> Tensor:
+        """The tape node of both critics' outputs acts[-1] (acts: each
+        layer's (2, B, N) output), from input x (and x2 after it)."""
+        lins = self.layers[0]
+        B = int(x.shape[0])
+        dev = x.device
+        S = self.stride
+        nl = len(lins)
+        h = acts[-1]
         params = self.params() if train_params else []
         inputs = [t for t in (x, x2) if t is not None]
         if not _needs(*inputs, *params):
@@ -322,6 +366,49 @@ def policy_packed(policy, obs: Tensor) -> Tensor:
     return head.forward_packed(policy.encoder(obs))
 
 
+def _linear_relu_pairs(encoder):
+    """The encoder's layers as (linear, ReLU) pairs, else None."""
+    items = list(getattr(encoder, "layers", ()))
+    if not items or len(items) % 2:
+        return None
+    pairs = list(zip(items[0::2], items[1::2]))
+    for lin, act in pairs:
+        if not (isinstance(lin, Linear) and isinstance(act, ReLU)):
+            return None
+    return [lin for lin, _ in pairs]
+
+
+def policy_rows(policy, obs_all: DeviceArray, B: int):
+    """The policy over every row of obs_all, one launch per layer, with the
+    tape over its first B rows (the actor's observations; the rest are the
+    soft target's next observations, constants of the update).
+    -> (packed head rows on the tape (B, 2d), packed head of every row)."""
+    head = policy.head
+    lins = _linear_relu_pairs(policy.encoder)
+    if not isinstance(head, GaussianHead) or lins is None:
+        raise ValueError("policy_rows: needs an MLP encoder of Linear -> ReLU pairs and a GaussianHead")
+    rows = int(obs_all.shape[0])
+    dev = obs_all.dev
+    x_all = obs_all
+    x = Tensor(obs_all.view(0, (B, int(obs_all.shape[1]))))
+    for lin in lins:
+        w = lin.effective_weight()
+        N = lin.out_features
+        y_all = DeviceArray(dev, (rows, N))
+        d = _lib.LinearDesc()
+        d.M, d.K, d.N, d.groups = rows, lin.in_features, N, 1
+        d.x, d.ldx = x_all.ptr, lin.in_features
+        d.W, d.b = w.data.ptr, None if lin.bias is None else lin.bias.data.ptr
+        d.y, d.relu = y_all.ptr, 1
+        dev.call("ttrl_linear_forward", C.byref(d))
+        if layers_mod.RECORD is not None:
+            layers_mod.RECORD.append(y_all)
+        x = linear_node(x, w, lin.bias, y_all.view(0, (B, N)), relu=True)
+        x_all = y_all
+    return packed_linear_pair_rows(head.heads["mean"], head.heads["log_std"], x, x_all,
+                                   clamp=(head.log_std_min, head.log_std_max), op="gaussian_head")
+
+
 class _BatchBuffers:
     """Bound device buffers of one SAC batch, back to back in one block
     (`block`), allocated once and written in place."""
@@ -330,12 +417,19 @@ class _BatchBuffers:
         def z(*shape):
             return np.zeros(shape, np.float32)
 
-        specs = [("obs", z(B, obs_dim)), ("next_obs", z(B, obs_dim)), ("actions", z(B, act_dim)),
+        # obs and next_obs (and the two noises) back to back, so the policy
+        # runs over both in one launch per layer
+        specs = [("obs_pair", z(2 * B, obs_dim)), ("actions", z(B, act_dim)),
                  ("obs_actions", z(B, obs_dim + act_dim)), ("rewards", z(B, 1)), ("dones", z(B, 1)),
-                 ("discounts", z(B, 1)), ("noise", z(B, act_dim)), ("next_noise", z(B, act_dim))]
+                 ("discounts", z(B, 1)), ("noise_pair", z(2 * B, act_dim))]
         if prioritized:
             specs.append(("is_weights", np.ones((B, 1), np.float32)))
         arrays, self.block = bound_block(device, specs)
+        self.obs_pair, self.noise_pair = arrays["obs_pair"], arrays["noise_pair"]
+        arrays["obs"] = self.obs_pair.view(0, (B, obs_dim))
+        arrays["next_obs"] = self.obs_pair.view(B * obs_dim, (B, obs_dim))
+        arrays["noise"] = self.noise_pair.view(0, (B, act_dim))
+        arrays["next_noise"] = self.noise_pair.view(B * act_dim, (B, act_dim))
         self.tensors = {name: Tensor(arr) for name, arr in arrays.items()}
         self.B = B
         # staged in a pinned image of the block, sent as one copy per update
@@ -398,13 +492,18 @@ class SACLearner:
         # [critic_loss, alpha, actor_loss, alpha_loss, critic_grad_sq, actor_grad_sq, -, -,
         #  q_target[B], logp[B], td_abs[B]].
         B = cfg.batch_size
-        blk = DeviceArray(device, (8 + 3 * B,))
+        # scalars, q_target, td_abs, then the sample's log-probabilities of
+        # obs (the logp metric) and next_obs back to back
+        blk = DeviceArray(device, (8 + 4 * B,))
         blk.fill(0.0)
         self._metric_block = blk
         self._critic_out = {"loss": blk.view(0, (1, 1)), "alpha": blk.view(1, (1, 1)),
-                            "q_target": blk.view(8, (B, 1)), "td_abs": blk.view(8 + 2 * B, (B, 1))}
+                            "q_target": blk.view(8, (B, 1)), "td_abs": blk.view(8 + B, (B, 1))}
         self._actor_out = {"actor_loss": blk.view(2, (1, 1)), "alpha_loss": blk.view(3, (1, 1))}
-        self._logp_out = blk.view(8 + B, (B, 1))
+        self._logp_all = blk.view(8 + 2 * B, (2 * B, 1))
+        self._logp_out = blk.view(8 + 2 * B, (B, 1))
+        self._stacked = isinstance(self.nets.policy.head, GaussianHead) and \
+            _linear_relu_pairs(self.nets.policy.encoder) is not None
         self.critic_opt.grad_sq = blk.view(4, (1, 1))
         self.actor_opt.grad_sq = blk.view(5, (1, 1))
         self._reader = MetricReader(device)
@@ -473,13 +572,30 @@ class SACLearner:
 
     # -- one update ----------------------------------------------------------
 
-    def _critic_region(self) -> dict:
+    def _policy_both(self):
+        """The policy and its sample over [obs; next_obs], one launch each
+        layer and one sample launch, the tape over the obs rows: the critic
+        step leaves the policy unchanged, so the actor's forward can run with
+        the soft target's.  -> (action, logp) on the tape, (a_next, logp_next)."""
         b = self.batch
-        with no_grad():
-            head_n = policy_packed(self.nets.policy, b["next_obs"])
-            a_next, logp_next = squashed_sample(head_n, b["next_noise"], self.scale)
-            q_next = self.twin_targets.forward(b["next_obs"], a_next)
-        q = self.twin.forward(obs_action=b["obs_actions"])
+        head, head_all = policy_rows(self.nets.policy, b.obs_pair, b.B)
+        action, logp, (a_next, logp_next) = squashed_sample_rows(head, head_all, b.noise_pair, self.scale,
+                                                                 self._logp_all)
+        return (action, logp), (a_next, Tensor(logp_next))
+
+    def _critic_region(self, nxt=None) -> dict:
+        b = self.batch
+        if nxt is not None:
+            # the target critics on (s', a') and the critics on (s, a): one launch per layer
+            a_next, logp_next = nxt
+            q, q_next = self.twin.forward_with_targets(self.twin_targets, b["next_obs"], a_next, b["obs"],
+                                                       b["actions"], b["obs_actions"])
+        else:
+            with no_grad():
+                head_n = policy_packed(self.nets.policy, b["next_obs"])
+                a_next, logp_next = squashed_sample(head_n, b["next_noise"], self.scale)
+                q_next = self.twin_targets.forward(b["next_obs"], a_next)
+            q = self.twin.forward(obs_action=b["obs_actions"])
         loss, m = sac_critic_loss(q, q_next, logp_next, self.log_alpha, b["rewards"], b["dones"], b["discounts"],
                                   b["is_weights"] if self.cfg.prioritized else None, out=self._critic_out)
         loss.backward()
@@ -488,10 +604,13 @@ class SACLearner:
             out["td_abs"] = m["td_abs"]
         return out
 
-    def _actor_region(self) -> dict:
+    def _actor_region(self, sampled=None) -> dict:
         b = self.batch
-        head = policy_packed(self.nets.policy, b["obs"])
-        action, logp = squashed_sample(head, b["noise"], self.scale, logp_out=self._logp_out)
+        if sampled is not None:
+            action, logp = sampled
+        else:
+            head = policy_packed(self.nets.policy, b["obs"])
+            action, logp = squashed_sample(head, b["noise"], self.scale, logp_out=self._logp_out)
         q_pi = self.twin.forward(b["obs"], action, train_params=False)
         actor, dual = sac_actor_losses(q_pi, logp, self.log_alpha, self.target_entropy, self.cfg.learn_alpha,
                                        out=self._actor_out)
@@ -506,14 +625,22 @@ class SACLearner:
         self.critic_opt.zero_grad()
         self.actor_opt.zero_grad()
         self.alpha_opt.zero_grad()
-        critic = self._critic_region()
-        self.critic_opt.step()
-        actor = self._actor_region()
-        self.actor_opt.step()
-        if self.cfg.learn_alpha:
-            self.alpha_opt.step()
-        self.device.call("ttrl_polyak", self.nets.targets.arena.data.vp, self.nets.critics.arena.data.vp,
-                         C.c_long(self.nets.targets.arena.numel), C.c_float(self.cfg.tau))
+        # The reference's order (ttrl/algos/sac/agent.py:229-236): critic step, actor
+        # and temperature steps, Polyak blend.  The critic's finish waits for the
+        # others so all three finish in one launch; actor, temperature and blend
+        # share one launch (disjoint buffers, the blend reading the stepped critic).
+        if self._stacked:
+            sampled, nxt = self._policy_both()
+            critic = self._critic_region(nxt)
+        else:
+            sampled = None
+            critic = self._critic_region()
+        self.critic_opt.step_deferred(0)
+        actor = self._actor_region(sampled)
+        stepped = [(self.actor_opt, 1)] + ([(self.alpha_opt, 2)] if self.cfg.learn_alpha else [])
+        adam_multi(self.device, stepped,
+                   polyak=(self.nets.targets.arena.data, self.nets.critics.arena.data, self.cfg.tau))
+        finish_steps(self.device, [(self.critic_opt, 0)] + stepped)
         metrics = dict(critic)
         metrics.update(actor)
         metrics["critic_grad_sq"] = Tensor(self.critic_opt.grad_sq)

@@ -8,6 +8,11 @@ One kernel updates a whole parameter arena (every tensor of a network built
 inside one `ParamArena`), reading the update count from a device counter so
 that a captured graph containing the step replays correctly for every t.
 The same launch reduces sum(g^2) into `grad_sq` (ttrl/algos/grads.py:46-60).
+
+Several optimizers stepped in one update (SAC's critic, actor and
+temperature) can defer their finishes: `step_deferred` or one `adam_multi`
+launch for several arenas (with the Polyak blend), then one `finish_steps`
+launch that stores every update count and sum(g^2).
 """
 
 from __future__ import annotations
@@ -17,9 +22,10 @@ import math
 
 import numpy as np
 
+from ttrl_amd import _lib
 from ttrl_amd.engine.tensor import DeviceArray, MASTER_DTYPE, arena_of, zeros
 
-__all__ = ["Adam", "Optimizer", "adam_fused_scalars"]
+__all__ = ["Adam", "Optimizer", "adam_fused_scalars", "adam_multi", "finish_steps"]
 
 
 def adam_fused_scalars(lr: float, b1: float, b2: float, eps: float, t: int) -> tuple[float, float]:
@@ -140,6 +146,55 @@ class Adam(Optimizer):
             first = False
             self.steps[i] += 1
 
+    # -- deferred steps ------------------------------------------------------
+
+    def _hyper(self) -> tuple:
+        return (C.c_float(self.lr), C.c_float(self.b1), C.c_float(self.b2), C.c_float(self.eps),
+                C.c_float(self.weight_decay))
+
+    def _arena_ready(self, who: str) -> None:
+        """The arena launch's preconditions; moves every gradient into its slot."""
+        if self.arena is None:
+            raise ValueError(f"Adam.{who}: the parameters must be exactly one ParamArena's")
+        missing = [i for i, p in enumerate(self.params) if p.grad is None]
+        if missing:
+            raise RuntimeError(f"Adam.{who}: parameters {missing} hold no gradient for this step")
+        if any(st != self._arena_t for st in self.steps):
+            raise RuntimeError(f"Adam.{who}: the parameters' update counts differ; use step()")
+        for p in self.params:
+            if p.grad is not p._grad_slot:
+                p._grad_slot.copy_from(p.grad)
+                p.grad = p._grad_slot
+                p._grad_owned = True
+
+    def step_deferred(self, slot: int) -> None:
+        """The arena's update with its finish left to `finish_steps`: the
+        update count is read, not stored, and the partial sums of g^2 wait in
+        the device context's partial slot `slot` (0-7)."""
+        self._arena_ready("step_deferred")
+        a = self.arena
+        self.device.call("ttrl_adam_step_deferred", a.data.vp, a.grad.vp, self._m_flat.vp, self._v_flat.vp,
+                         C.c_long(a.numel), self._counter(len(self.params)), *self._hyper(), int(slot))
+
+    def deferred_range(self, slot: int) -> "_lib.AdamRange":
+        """This arena's update as one range of `adam_multi`."""
+        self._arena_ready("deferred_range")
+        a = self.arena
+        return _lib.AdamRange(a.data.ptr, a.grad.ptr, self._m_flat.ptr, self._v_flat.ptr, a.numel,
+                              self._counter(len(self.params)).value, self.lr, self.b1, self.b2, self.eps,
+                              self.weight_decay, int(slot))
+
+    def _finish_desc(self, slot: int) -> "_lib.AdamFinish":
+        return _lib.AdamFinish(int(slot), self.arena.numel, self._counter(len(self.params)).value,
+                               self.grad_sq.ptr, 0)
+
+    def _finished(self) -> None:
+        """Host counters after a finished step (a capture advances them at replay)."""
+        if not self.device.capturing:
+            self.t += 1
+            self._arena_t += 1
+            self.steps = [st + 1 for st in self.steps]
+
     def arena_grads(self) -> DeviceArray:
         """The arena's flat gradient, after moving every parameter's gradient
         into its slot there (what a global-norm clip reads before the step)."""
@@ -223,3 +278,29 @@ def _aligned_copy(x: DeviceArray) -> DeviceArray:
     padded.view(0, x.shape).copy_from(x)
     out = padded.view(0, x.shape)
     return out
+
+
+def adam_multi(device, ranges, polyak=None) -> None:
+    """One launch: the deferred updates `ranges` ([(optimizer, slot)], at
+    most four) and, with polyak=(dst, src, tau) (DeviceArrays of one
+    length), dst = (1 - tau) dst + tau src (ttrl/algos/sac/targets.py:45-52)."""
+    descs = [opt.deferred_range(slot) for opt, slot in ranges]
+    arr = (_lib.AdamRange * max(1, len(descs)))(*descs)
+    if polyak is not None:
+        dst, src, tau = polyak
+        if dst.numel != src.numel:
+            raise ValueError(f"adam_multi: Polyak buffers differ in length ({dst.numel} vs {src.numel})")
+        pd, ps, pn = dst.vp, src.vp, dst.numel
+    else:
+        pd, ps, pn, tau = None, None, 0, 0.0
+    device.call("ttrl_adam_multi", len(descs), arr, pd, ps, C.c_long(pn), C.c_float(tau))
+
+
+def finish_steps(device, steps) -> None:
+    """Finishes deferred steps ([(optimizer, slot)]) in one launch: each
+    optimizer's sum(g^2) into its `grad_sq` and its update count stored."""
+    descs = [opt._finish_desc(slot) for opt, slot in steps]
+    arr = (_lib.AdamFinish * max(1, len(descs)))(*descs)
+    device.call("ttrl_adam_finish_slots", len(descs), arr)
+    for opt, _ in steps:
+        opt._finished()

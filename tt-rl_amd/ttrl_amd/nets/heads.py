@@ -79,24 +79,30 @@ def policy_value_packed(policy: CategoricalHead, value: ValueHead, x: Tensor) ->
     return packed_linear_pair(policy.logits, value.value, x, op="policy_value_head")
 
 
-def packed_linear_pair(first: Linear, second: Linear, x: Tensor, *, clamp=None, op: str) -> Tensor:
-    """(B, n1 + n2) rows [x W1 + b1 | x W2 + b2] of two Linear layers over one
-    input, from one launch; `clamp` = (lo, hi) clamps the second block in the
-    epilogue.  Backward: both layers' dW and db and dx in one launch."""
+def _packed_launch(first: Linear, second: Linear, x: DeviceArray, clamp) -> DeviceArray:
+    """(M, n1 + n2) rows [x W1 + b1 | x W2 + b2] over every row of x, one launch."""
     M, K = (int(d) for d in x.shape)
     n1 = first.out_features
     N = n1 + second.out_features
-    dev = x.device
-    y = DeviceArray(dev, (M, N))
+    y = DeviceArray(x.dev, (M, N))
     desc = _lib.LinearDesc()
     desc.M, desc.K, desc.N, desc.groups = M, K, N, 1
-    desc.x, desc.ldx = x.data.ptr, K
+    desc.x, desc.ldx = x.ptr, K
     desc.W, desc.b = first.weight.data.ptr, None if first.bias is None else first.bias.data.ptr
     desc.W2, desc.b2, desc.n1 = second.weight.data.ptr, None if second.bias is None else second.bias.data.ptr, n1
     desc.y = y.ptr
     if clamp is not None:
         desc.clamp_col, desc.lo, desc.hi = n1, float(clamp[0]), float(clamp[1])
-    dev.call("ttrl_linear_forward", C.byref(desc))
+    x.dev.call("ttrl_linear_forward", C.byref(desc))
+    return y
+
+
+def _packed_tape(first: Linear, second: Linear, x: Tensor, y: DeviceArray, op: str) -> Tensor:
+    """The tape node of a packed pair's rows: y (x's rows) computed elsewhere."""
+    M, K = (int(d) for d in x.shape)
+    n1 = first.out_features
+    N = n1 + second.out_features
+    dev = x.device
     params = tuple(t for t in (first.weight, first.bias, second.weight, second.bias) if t is not None)
     if not _needs(x, *params):
         return _detached(y)
@@ -124,3 +130,22 @@ def packed_linear_pair(first: Linear, second: Linear, x: Tensor, *, clamp=None, 
 
     out._backward = _backward
     return out
+
+
+def packed_linear_pair(first: Linear, second: Linear, x: Tensor, *, clamp=None, op: str) -> Tensor:
+    """(B, n1 + n2) rows [x W1 + b1 | x W2 + b2] of two Linear layers over one
+    input, from one launch; `clamp` = (lo, hi) clamps the second block in the
+    epilogue.  Backward: both layers' dW and db and dx in one launch."""
+    return _packed_tape(first, second, x, _packed_launch(first, second, x.data, clamp), op)
+
+
+def packed_linear_pair_rows(first: Linear, second: Linear, x: Tensor, x_all: DeviceArray, *, clamp=None,
+                            op: str):
+    """packed_linear_pair over every row of x_all in one launch, the tape over
+    its leading rows (x, whose data views them).  -> (tape node, y_all)."""
+    B = int(x.shape[0])
+    if x.data.ptr != x_all.ptr or int(x_all.shape[0]) < B:
+        raise ValueError(f"{op}: x must view the leading rows of x_all")
+    y_all = _packed_launch(first, second, x_all, clamp)
+    N = int(y_all.shape[1])
+    return _packed_tape(first, second, x, y_all.view(0, (B, N)), op), y_all
