@@ -328,7 +328,11 @@ def sac_actor_losses(q_pi: Tensor, logp: Tensor, log_alpha: Tensor, target_entro
     lalpha = _out_array(out, "alpha_loss", dev, (1, 1))
     dq = DeviceArray(dev, (2, B, 1))
     g_logp = DeviceArray(dev, (B, 1))
-    d_log_alpha = DeviceArray(dev, (1, 1))
+    # d alpha_loss / d log_alpha straight into log_alpha's gradient slot when
+    # nothing else holds a gradient there yet: the backward then only claims it
+    ahead = (log_alpha._grad_slot if learn_alpha and log_alpha.requires_grad and log_alpha.grad is None
+             else None)
+    d_log_alpha = ahead.reshape((1, 1)) if ahead is not None else DeviceArray(dev, (1, 1))
     dev.call("ttrl_sac_actor_loss", B, q_pi.data.vp, logp.data.vp, log_alpha.data.vp, C.c_float(target_entropy),
              int(learn_alpha), la.vp, lalpha.vp, dq.vp, g_logp.vp, d_log_alpha.vp)
     actor = Tensor(la)
@@ -350,6 +354,14 @@ def sac_actor_losses(q_pi: Tensor, logp: Tensor, log_alpha: Tensor, target_entro
             alpha_loss = Tensor(lalpha, True, (log_alpha,), "sac_alpha_loss")
 
             def _backward_alpha(grad):
+                if ahead is not None:
+                    if log_alpha.grad is not None:
+                        raise RuntimeError("sac_actor_losses: log_alpha received a gradient between the loss, "
+                                           "which wrote its own into the gradient slot, and this backward")
+                    log_alpha.grad, log_alpha._grad_owned = ahead, True
+                    if not grad.unit:
+                        K.binary_into("mul", ahead, grad.reshape(tuple(ahead.shape)), ahead)
+                    return
                 log_alpha._accumulate(d_log_alpha if grad.unit else K.binary("mul", d_log_alpha, grad))
 
             alpha_loss._backward = _backward_alpha

@@ -8,7 +8,7 @@ from __future__ import annotations
 import ctypes as C
 
 from ttrl_amd import _lib
-from ttrl_amd.engine.autograd import Tensor, _detached, _needs
+from ttrl_amd.engine.autograd import Tensor, _detached, _needs, relu_mask
 from ttrl_amd.engine.layers import Linear
 from ttrl_amd.engine.nn import Module, ModuleDict
 from ttrl_amd.engine.ops import clamp
@@ -114,6 +114,9 @@ def _packed_tape(first: Linear, second: Linear, x: Tensor, y: DeviceArray, op: s
     def _backward(grad):
         (dw1, db1, dw2, db2), beta_w = grad_targets(*params)
         (dx,), beta_x = grad_targets(x)
+        # x a ReLU output: its gate applied as dx is written, so the layer
+        # below takes the gradient without a masking pass of its own
+        xmask = relu_mask(x) if dx is not None else None
         b = _lib.LinearDesc()
         b.M, b.K, b.N, b.groups = M, K, N, 1
         b.x, b.ldx = x_data.ptr, K
@@ -122,11 +125,12 @@ def _packed_tape(first: Linear, second: Linear, x: Tensor, y: DeviceArray, op: s
         if dw1 is not None:
             b.dW, b.db, b.dW2, b.db2 = dw1.ptr, db1.ptr, dw2.ptr, db2.ptr
         b.dx = None if dx is None else dx.ptr
+        b.dxmask = None if xmask is None else xmask.ptr
         b.lddx = K
         b.beta_w, b.beta_x = beta_w, beta_x
         dev.call("ttrl_linear_backward", C.byref(b))
         if dx is not None:
-            x._note_write(beta_x, False)
+            x._note_write(beta_x, xmask is not None)
 
     out._backward = _backward
     return out
