@@ -38,7 +38,7 @@ PEAK_FP32_MFMA = 157.3e12
 # FETCH_SIZE 1713.5 KiB x 2.000 + WRITE_SIZE 4800.0 KiB x 1.000, the factors
 # being what the same counters read for a 256 MiB device-to-device copy
 # (131083.5 and 262144.0 KiB); profiles/conv1_forward_traffic_counters.md.
-CONV1_FWD_TRAFFIC_BYTES = 8424135
+DQN_TAIL_TRAFFIC_BYTES = None  # HBM bytes per ttrl_dqn_tail call, from counters (set below once measured)
 PEAK_HBM = 8.0e12
 
 # Multiply-accumulates per sample of the Nature CNN at 4x84x84 (conv1..3, fc1, fc2).
@@ -288,33 +288,54 @@ def bench_rppo(dev, updates=3, mode="graph"):
 
 
 def dominant_kernel(dev, learner, reps=200):
-    """The longest kernel of the DQN update: the conv1 forward of the three
-    Q evaluations in one launch (online(s), online(s'), target(s'); uint8
-    4x84x84 frames at batch 32 -> 32 x 20 x 20 x 32, bias + ReLU), timed
-    alone on the library's stream with HIP events over `reps` launches.
-    Algorithmic work per launch: 3 x 2 x 12800 x 32 x 256 FLOPs; HBM bytes:
-    two frame batches, two weight sets, three outputs."""
+    """The DQN update's longest entry point, ttrl_dqn_tail, at the update's
+    shapes on the learner's weights: the first linear layer 3136 -> 512 of the
+    three Q evaluations (online(s), online(s'), target(s')) as one split-K
+    GEMM launch, then one kernel for the split sums, the Q head 512 -> 6, the
+    double-DQN Huber loss and the second layer's backward.  Timed alone on
+    the library's stream with HIP events over `reps` calls.
+    Algorithmic work per call: 3 x 2 x 32 x 3136 x 512 FLOPs in the GEMM,
+    3 x 2 x 32 x 512 x 6 in the head, 2 x 32 x 512 x 6 each for dh and dW2;
+    HBM bytes: the three feature batches, the two distinct first-layer
+    weight sets (online, target) and biases, the three 32 x 512 outputs, dh."""
     from ttrl_amd import _lib
+    from ttrl_amd.algos.dqn import _lockstep_layers
     from ttrl_amd.engine.tensor import DeviceArray
 
-    B, Cin, H, W, O, k, s = 32, 4, 84, 84, 32, 8, 4
-    OH = (H - k) // s + 1
-    frames = [DeviceArray(dev, (B, Cin, H, W), np.uint8) for _ in range(2)]
+    B, K, F, A = 32, 3136, 512, 6
     rng = np.random.default_rng(5)
-    for f in frames:
-        f.upload(rng.integers(0, 256, (B, Cin, H, W), dtype=np.uint8))
-    conv1 = [learner.online.encoder.layers[0], learner.target.encoder.layers[0]]
-    ys = [DeviceArray(dev, (B, OH, OH, O)) for _ in range(3)]
-    xs = [frames[0], frames[1], frames[1]]
-    nets = [conv1[0], conv1[0], conv1[1]]
-    geom = _lib.ConvGeom(B, Cin, H, W, O, k, s, 0, _lib.LAYOUT_NCHW_U8)
-    xp = _lib.ptrs([x.ptr for x in xs])
-    wp = _lib.ptrs([n.weight.data.ptr for n in nets])
-    bp = _lib.ptrs([n.bias.data.ptr for n in nets])
-    yp = _lib.ptrs([y.ptr for y in ys])
+
+    def arr(shape, values=None):
+        a = DeviceArray(dev, shape)
+        a.upload((rng.standard_normal(shape) if values is None else values).astype(np.float32))
+        return a
+
+    online = _lockstep_layers([learner.online])[0][-3:]
+    target = _lockstep_layers([learner.target])[0][-3:]
+    sets = [online, online, target]
+    feats = [arr((B, K), np.maximum(rng.standard_normal((B, K)), 0.0)) for _ in range(3)]
+    hs = [DeviceArray(dev, (B, F)) for _ in range(3)]
+    qs = [DeviceArray(dev, (B, A)) for _ in range(3)]
+    onehot = np.zeros((B, A), np.float32)
+    onehot[np.arange(B), rng.integers(0, A, B)] = 1.0
+    keep = [arr((B, A), onehot), arr((B, 1)), arr((B, 1), (rng.random((B, 1)) < 0.1).astype(np.float32)),
+            arr((B, 1), np.full((B, 1), 0.99 ** 3)), arr((B, 1), rng.random((B, 1)))]
+    outs = {n: DeviceArray(dev, shape) for n, shape in (("loss", (1, 1)), ("mean_q", (1, 1)), ("td_abs", (B, 1)),
+                                                          ("dq", (B, A)), ("next", (B, 1)), ("y", (B, 1)),
+                                                          ("dh", (B, F)), ("dw2", (F, A)), ("db2", (1, A)))}
+    d = _lib.DqnTailDesc()
+    d.B, d.K, d.F, d.A, d.groups = B, K, F, A, 3
+    for g, (fc1, _, fc2) in enumerate(sets):
+        d.x[g], d.W1[g], d.b1[g] = feats[g].ptr, fc1.weight.data.ptr, fc1.bias.data.ptr
+        d.h[g], d.W2[g], d.b2[g], d.q[g] = hs[g].ptr, fc2.weight.data.ptr, fc2.bias.data.ptr, qs[g].ptr
+    d.actions_onehot, d.rewards, d.dones, d.discounts, d.is_weights = (k.ptr for k in keep)
+    d.delta = 1.0
+    d.loss, d.mean_q, d.td_abs, d.dq = outs["loss"].ptr, outs["mean_q"].ptr, outs["td_abs"].ptr, outs["dq"].ptr
+    d.next_actions, d.td_target, d.dh = outs["next"].ptr, outs["y"].ptr, outs["dh"].ptr
+    d.dW2, d.db2, d.beta_w = outs["dw2"].ptr, outs["db2"].ptr, 0.0
 
     def launch():
-        dev.call("ttrl_conv2d_forward_multi", C.byref(geom), 3, xp, wp, bp, yp, C.c_float(1.0 / 255.0), 1)
+        dev.call("ttrl_dqn_tail", C.byref(d))
 
     for _ in range(10):
         launch()
@@ -325,10 +346,11 @@ def dominant_kernel(dev, learner, reps=200):
         launch()
     dev.call("ttrl_timer_stop", C.byref(ms))
     sec = ms.value / 1e3 / reps
-    M = B * OH * OH
-    flops = 3 * 2.0 * M * O * Cin * k * k
-    algo_bytes = 2 * B * Cin * H * W + 2 * 4 * (Cin * k * k + 1) * O + 3 * 4 * M * O
-    return {"name": "conv2d_forward_multi: Nature-CNN conv1, 3 x (32x4x84x84 uint8 -> 32x20x20x32)",
+    flops = 3 * 2.0 * B * K * F + 3 * 2.0 * B * F * A + 2 * 2.0 * B * F * A
+    algo_bytes = 4 * (3 * B * K + 2 * (K * F + F) + 3 * B * F + B * F)
+    return {"name": "ttrl_dqn_tail: fc1 3 x (32x3136 @ 3136x512) split-K GEMM + k_dqn_tail (split sums, Q head "
+                    "512->6, double-DQN Huber loss, fc2 backward), batch 32",
+            "kernels": ["k_gemm<32,64,2,2,1,128,LdRowK,LdColK,EpStore> (deferred split-K)", "k_dqn_tail<8>"],
             "seconds": sec, "bytes": algo_bytes, "flops": flops}
 
 
@@ -512,10 +534,10 @@ def main() -> int:
         "sac": {"value": round(sac_value, 2), "unit": "SAC updates/s", "batch": 256,
                 "ms_per_step": round(swall / args.steps * 1e3, 5), "gpu_ms_per_step": sgpu / args.steps * 1e3,
                 "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA},
-        "roofline": {"bound": "mfma", "kernel": dom["name"], "achieved": achieved / 1e12,
+        "roofline": {"bound": "mfma", "kernel": dom["name"], "kernels": dom["kernels"], "achieved": achieved / 1e12,
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
-                     "traffic": CONV1_FWD_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],
-                     "avg_us": dom["seconds"] * 1e6},
+                     "traffic": DQN_TAIL_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],
+                     "hbm_frac": dom["bytes"] / dom["seconds"] / PEAK_HBM, "avg_us": dom["seconds"] * 1e6},
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},

@@ -1052,6 +1052,11 @@ inline void launch_allowed(const LA& la, const LB& lb, const EP& ep, float* ws, 
   });
 }
 
+// A split-K plan's reduce is one more launch, which back-to-back timing
+// outside a graph prices below what a node of a replayed graph costs; the
+// tuners charge it this much per run, so a split must win by more.
+constexpr float kReduceLaunchMs = 1.0e-3f;
+
 // Best of three rounds of three back-to-back runs of `run` (milliseconds
 // for three runs), -1 if an event call fails.  The minimum over rounds
 // discards rounds slowed by clock ramps or other work on the device.
@@ -1070,12 +1075,25 @@ inline float time_best_of(hipEvent_t e0, hipEvent_t e1, hipStream_t st, F&& run)
   return best;
 }
 
+// k_gemm alone: with a split plan the partial tiles stay in the workspace.
+template <unsigned ALLOWED, class LA, class LB, class EP>
+inline void launch_gemm_only(const LA& la, const LB& lb, const EP& ep, float* ws, int M, int N, int K, int groups,
+                             const GemmPlan& p, hipStream_t st) {
+  dispatch_cfg<ALLOWED>(p.cfg, [&](auto c) {
+    using C = decltype(c);
+    dim3 grid(ceil_div(M, C::BM), ceil_div(N, C::BN), unsigned(groups * p.splits));
+    hipLaunchKernelGGL((k_gemm<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK, LA, LB, EP>), grid,
+                       dim3(64 * C::WGM * C::WGN * C::WGK), 0, st, la, lb, ep, ws, M, N, K, p.kchunk, p.splits);
+  });
+}
+
 // Times the model's leading candidates on the real operands, writing into a
 // sink instead of the output; returns the fastest (the model's first choice
-// if timing is unavailable).
+// if timing is unavailable).  `reduce` false times k_gemm alone, for a
+// consumer that sums the split partials itself.
 template <unsigned ALLOWED, class LA, class LB, class EP>
 inline GemmPlan tune_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, float* ws, long ws_limit, int M,
-                          int N, int K, int groups, hipStream_t st) {
+                          int N, int K, int groups, hipStream_t st, bool reduce = true) {
   const std::vector<GemmPlan> cands = plan_candidates(M, N, K, groups, ws_limit, ALLOWED, 10);
   hipEvent_t e0, e1;
   float* sink = ctx_tune_sink(ctx, size_t(ep.tune_span()) * sizeof(float));
@@ -1084,14 +1102,21 @@ inline GemmPlan tune_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& e
   GemmPlan best = cands.front();
   float best_ms = 1e30f;
   for (const GemmPlan& c : cands) {
-    launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);  // warm
-    const float ms = time_best_of(e0, e1, st, [&] { launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st); });
+    auto run = [&] {
+      if (reduce)
+        launch_allowed<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);
+      else
+        launch_gemm_only<ALLOWED>(la, lb, tep, ws, M, N, K, groups, c, st);
+    };
+    run();  // warm
+    const float ms = time_best_of(e0, e1, st, run);
     if (ms < 0.f) break;
     if (gemm_tuning_log())
       fprintf(stderr, "[ttrl gemm tune] M=%d N=%d K=%d G=%d  %dx%d tbk%d splits=%d  %.2f us\n", M, N, K, groups, c.bm,
               c.bn, c.tbk, c.splits, ms * 1e3f / 3.f);
-    if (ms < best_ms) {
-      best_ms = ms;
+    const float cost = ms + (reduce && c.splits > 1 ? 3.f * kReduceLaunchMs : 0.f);
+    if (cost < best_ms) {
+      best_ms = cost;
       best = c;
     }
   }
@@ -1166,17 +1191,12 @@ inline int run_gemm_deferred(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP
     p = *hit;
   } else {
     if (!ctx_capturing(ctx) && gemm_tuning_enabled())
-      p = tune_gemm<ALLOWED>(ctx, la, lb, ep, ws, wsf, M, N, K, groups, st);
+      p = tune_gemm<ALLOWED>(ctx, la, lb, ep, ws, wsf, M, N, K, groups, st, false);
     else
       p = plan_gemm(M, N, K, groups, wsf, ALLOWED);
     ctx_plan_store(ctx, key, p);
   }
-  dispatch_cfg<ALLOWED>(p.cfg, [&](auto c) {
-    using C = decltype(c);
-    dim3 grid(ceil_div(M, C::BM), ceil_div(N, C::BN), unsigned(groups * p.splits));
-    hipLaunchKernelGGL((k_gemm<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK, LA, LB, EP>), grid,
-                       dim3(64 * C::WGM * C::WGN * C::WGK), 0, st, la, lb, ep, ws, M, N, K, p.kchunk, p.splits);
-  });
+  launch_gemm_only<ALLOWED>(la, lb, ep, ws, M, N, K, groups, p, st);
   *plan = p;
   return check_launch(name);
 }
@@ -1301,8 +1321,9 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
           fprintf(stderr, "[ttrl gemm tune pair] %dx%dx%d(G%d) + %dx%dx%d(G%d)  %dx%d tbk%d splits=%d,%d  %.2f us\n",
                   q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K, q2.groups, c.first.bm, c.first.bn, c.first.tbk,
                   c.first.splits, c.second.splits, ms * 1e3f / 3.f);
-        if (ms < best_ms) {
-          best_ms = ms;
+        const float cost = ms + 3.f * kReduceLaunchMs * float(int(c.first.splits > 1) + int(c.second.splits > 1));
+        if (cost < best_ms) {
+          best_ms = cost;
           p1 = c.first;
           p2 = c.second;
         }
