@@ -34,11 +34,11 @@ for _p in (ROOT, ROOT / "tt-rl_amd"):
 import numpy as np  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12
-# HBM bytes per launch of the dominant kernel (conv1 forward x 3): rocprofv3
-# FETCH_SIZE 1713.5 KiB x 2.000 + WRITE_SIZE 4800.0 KiB x 1.000, the factors
-# being what the same counters read for a 256 MiB device-to-device copy
-# (131083.5 and 262144.0 KiB); profiles/conv1_forward_traffic_counters.md.
-DQN_TAIL_TRAFFIC_BYTES = None  # HBM bytes per ttrl_dqn_tail call, from counters (set below once measured)
+# HBM bytes per ttrl_dqn_tail call (fc1 GEMM + k_dqn_tail at batch 32): rocprofv3
+# FETCH_SIZE (11108.0 + 1172.4) KiB x 2.000 + WRITE_SIZE (1728.0 + 279.1) KiB x 1.000,
+# the factors being what the same counters read for a 256 MiB device-to-device
+# copy (131083.5 and 262144.0 KiB); profiles/dqn_tail_roofline_and_traffic.md.
+DQN_TAIL_TRAFFIC_BYTES = 27203426
 PEAK_HBM = 8.0e12
 
 # Multiply-accumulates per sample of the Nature CNN at 4x84x84 (conv1..3, fc1, fc2).
@@ -350,7 +350,8 @@ def dominant_kernel(dev, learner, reps=200):
     algo_bytes = 4 * (3 * B * K + 2 * (K * F + F) + 3 * B * F + B * F)
     return {"name": "ttrl_dqn_tail: fc1 3 x (32x3136 @ 3136x512) split-K GEMM + k_dqn_tail (split sums, Q head "
                     "512->6, double-DQN Huber loss, fc2 backward), batch 32",
-            "kernels": ["k_gemm<32,64,2,2,1,128,LdRowK,LdColK,EpStore> (deferred split-K)", "k_dqn_tail<8>"],
+            "kernels": ["k_gemm<..., LdRowK, LdColK, EpStore> (tile and split from the plan table, partials left "
+                        "for the tail)", "k_dqn_tail<8>"],
             "seconds": sec, "bytes": algo_bytes, "flops": flops}
 
 
