@@ -415,62 +415,124 @@ def bench_act(dev, dqn, sac, steps=500, lanes_dqn=(1, 8, 16, 32), lanes_sac=(1, 
     return out
 
 
-def cpu_deploy_forward(seconds: float):
-    """The oracle's restatement of the numpy deploy forward (batch 32,
-    4x84x84 uint8 frames scaled by 1/255), forwards/s on this host."""
-    from oracle.nets import QNet, qnet_forward
+def _he(rng, shape, fan, dtype):
+    b = np.sqrt(6.0 / fan)
+    return rng.uniform(-b, b, shape).astype(dtype)
 
-    rng = np.random.default_rng(1)
 
-    def he(shape, fan):
-        b = np.sqrt(6.0 / fan)
-        return rng.uniform(-b, b, shape)
+def _cpu_worker(spec: str) -> int:
+    """One CPU measurement in this process, whose BLAS thread count the
+    parent set in the environment: spec "kind,dtype,seconds", kind dqn (the
+    oracle's DQN update, batch 32), sac (the oracle's SAC update, batch 256)
+    or deploy (the oracle's restatement of the reference's numpy deploy
+    forward, batch 32 frames).  Prints one JSON line."""
+    import oracle
+    from oracle import deploy
+    from oracle.dqn import dqn_update
+    from oracle.nets import QNet
+    from oracle.sac import SacParams, sac_update
+    from ttrl_amd.workloads import dqn_batch, sac_batch
 
-    net = QNet([(he((32, 4, 8, 8), 256), he((32,), 256), 4, 0), (he((64, 32, 4, 4), 512), he((64,), 512), 2, 0),
-                (he((64, 64, 3, 3), 576), he((64,), 576), 1, 0)],
-               [(he((3136, 512), 3136), he((512,), 3136)), (he((512, 6), 512), he((6,), 512))])
-    frames = rng.integers(0, 256, (32, 4, 84, 84), dtype=np.uint8)
-    qnet_forward(net, frames)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds or n < 2:
-        qnet_forward(net, frames)
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 2), "unit": "DQN forwards/s (batch 32)", "kind": "port",
-            "sample": f"{n} float64 forwards in {dt:.1f} s"}
+    kind, dname, seconds = spec.split(",")
+    dt = np.float32 if dname == "f32" else np.float64
+    rng = np.random.default_rng(0)
+    if kind == "dqn":
+        net = QNet([(_he(rng, (32, 4, 8, 8), 256, dt), _he(rng, (32,), 256, dt), 4, 0),
+                    (_he(rng, (64, 32, 4, 4), 512, dt), _he(rng, (64,), 512, dt), 2, 0),
+                    (_he(rng, (64, 64, 3, 3), 576, dt), _he(rng, (64,), 576, dt), 1, 0)],
+                   [(_he(rng, (3136, 512), 3136, dt), _he(rng, (512,), 3136, dt)),
+                    (_he(rng, (512, 6), 512, dt), _he(rng, (6,), 512, dt))])
+        target = net.copy()
+        batches = [dqn_batch(3000 + i) for i in range(4)]
+        step = lambda i: dqn_update(net, target, batches[i % 4])  # noqa: E731
+    elif kind == "sac":
+        def mlp(dims):
+            return [(_he(rng, (a, b), a, dt), _he(rng, (b,), a, dt)) for a, b in zip(dims[:-1], dims[1:])]
+        crit = [mlp((14, 256, 256, 1)) for _ in range(2)]
+        P = SacParams(trunk=mlp((11, 256, 256)), mean=mlp((256, 3))[0], log_std=mlp((256, 3))[0], critics=crit,
+                      targets=[[(w.copy(), b.copy()) for w, b in c] for c in crit], log_alpha=0.0)
+        batches = [sac_batch(4000 + i) for i in range(4)]
+        step = lambda i: sac_update(P, batches[i % 4])  # noqa: E731
+    else:
+        meta = {"obs_shape": [4, 84, 84], "trunk_layers": 1,
+                "conv": [{"stride": 4, "padding": 0}, {"stride": 2, "padding": 0}, {"stride": 1, "padding": 0}]}
+        arrays = {"conv.0.weight": _he(rng, (32, 4, 8, 8), 256, dt), "conv.0.bias": _he(rng, (32,), 256, dt),
+                  "conv.1.weight": _he(rng, (64, 32, 4, 4), 512, dt), "conv.1.bias": _he(rng, (64,), 512, dt),
+                  "conv.2.weight": _he(rng, (64, 64, 3, 3), 576, dt), "conv.2.bias": _he(rng, (64,), 576, dt),
+                  "trunk.0.weight": _he(rng, (3136, 512), 3136, dt), "trunk.0.bias": _he(rng, (512,), 3136, dt),
+                  "head.weight": _he(rng, (512, 6), 512, dt), "head.bias": _he(rng, (6,), 512, dt)}
+        frames = rng.integers(0, 256, (32, 4, 84, 84), dtype=np.uint8)
+        step = lambda i: deploy.head_rows(meta, arrays, frames)  # noqa: E731
+    with oracle.precision(dt):
+        step(0)  # warm caches and the BLAS pool
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < float(seconds) or n < 2:
+            step(n)
+            n += 1
+        dt_s = time.perf_counter() - t0
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [{k: i.get(k) for k in ("internal_api", "version", "num_threads")} for i in threadpool_info()
+                if i.get("user_api") == "blas"]
+    except ImportError:
+        blas = []
+    print(json.dumps({"n": n, "seconds": dt_s, "rate": n / dt_s, "blas_runtime": blas}), flush=True)
+    return 0
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _numpy_blas() -> dict:
+    try:
+        deps = np.show_config(mode="dicts")["Build Dependencies"]
+        return {k: deps[k].get("name") + " " + str(deps[k].get("version")) for k in ("blas", "lapack") if k in deps}
+    except Exception:  # the layout of show_config's dict is not a stable API
+        return {}
 
 
 def cpu_baseline(seconds: float):
-    """The float64 numpy oracle of the same DQN update, on this host."""
-    from oracle.dqn import dqn_update
-    from oracle.nets import QNet
-    from ttrl_amd.workloads import dqn_batch
+    """The float64 numpy oracle of the same updates on this host, and the same
+    arithmetic in float32 (the GPU path's type): the DQN update, the SAC
+    update and the deploy forward, each on every core this process may use
+    (threads capped by OMP_NUM_THREADS) and on one, each case in a child
+    process so its BLAS starts with that thread count.  `value` is the DQN
+    update in float32 on all those cores."""
+    import subprocess
 
-    rng = np.random.default_rng(0)
-
-    def he(shape, fan):
-        b = np.sqrt(6.0 / fan)
-        return rng.uniform(-b, b, shape)
-
-    net = QNet([(he((32, 4, 8, 8), 256), he((32,), 256), 4, 0), (he((64, 32, 4, 4), 512), he((64,), 512), 2, 0),
-                (he((64, 64, 3, 3), 576), he((64,), 576), 1, 0)],
-               [(he((3136, 512), 3136), he((512,), 3136)), (he((512, 6), 512), he((6,), 512))])
-    target = net.copy()
-    batches = [dqn_batch(3000 + i) for i in range(4)]
-    dqn_update(net, target, batches[0])  # warm caches
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds or n < 2:
-        dqn_update(net, target, batches[n % 4])
-        n += 1
-    dt = time.perf_counter() - t0
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
-    return {"value": n / dt, "unit": "DQN updates/s", "cores": min(threads, cores), "kind": "port",
-            "sample": f"{n} DQN updates (batch 32, 4x84x84 uint8) of the float64 numpy oracle in {dt:.1f} s",
-            "cpu": platform.processor() or platform.machine()}
+    threads = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    runs = []
+    for kind, secs, unit in (("dqn", seconds / 2, "DQN updates/s"), ("sac", seconds / 4, "SAC updates/s"),
+                             ("deploy", seconds / 4, "DQN forwards/s (batch 32)")):
+        for dname in ("f32", "f64"):
+            for t in (threads, 1):
+                env = dict(os.environ)
+                for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS", "BLIS_NUM_THREADS"):
+                    env[var] = str(t)
+                proc = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-worker",
+                                       f"{kind},{dname},{secs}"], env=env, capture_output=True, text=True,
+                                      timeout=600)
+                if proc.returncode != 0:
+                    raise RuntimeError(f"cpu baseline worker {kind},{dname},{t} failed:\n{proc.stderr[-2000:]}")
+                out = json.loads(proc.stdout.strip().splitlines()[-1])
+                runs.append({"workload": kind, "dtype": dname, "threads": t, "value": round(out["rate"], 3),
+                             "unit": unit, "sample": f"{out['n']} in {out['seconds']:.1f} s",
+                             "blas_runtime": out["blas_runtime"]})
+    head = next(r for r in runs if r["workload"] == "dqn" and r["dtype"] == "f32" and r["threads"] == threads)
+    return {"value": head["value"], "unit": "DQN updates/s", "cores": threads, "kind": "port",
+            "sample": f"{head['sample']}: DQN updates (batch 32, 4x84x84 uint8) of the numpy oracle in float32",
+            "cpu": _cpu_model(), "logical_cpus": cores, "numpy_blas": _numpy_blas(), "runs": runs}
 
 
 def main() -> int:
@@ -486,10 +548,13 @@ def main() -> int:
     ap.add_argument("--replay-reps", type=int, default=200, help="replay samples timed (0: skip)")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
                     help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
+    ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run five device-to-device copies of MIB MiB (the reference for scaling a "
                          "profiler's FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
+    if args.cpu_worker:
+        return _cpu_worker(args.cpu_worker)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path; "
               "replicas would shard as independent learners with a periodic parameter all-reduce.",
@@ -512,8 +577,8 @@ def main() -> int:
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
-    if act is not None and not args.no_cpu_baseline:
-        act["cpu_deploy_forward"] = cpu_deploy_forward(min(5.0, args.cpu_seconds))
+    if act is not None and cpu is not None:
+        act["cpu_deploy_forward"] = [r for r in cpu["runs"] if r["workload"] == "deploy"]
     line = {
         "metric": "DQN updates/s @bs32, SAC updates/s @bs256 on 1 MI355X; % of roofline",
         "value": round(value, 2),

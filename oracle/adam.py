@@ -12,6 +12,8 @@ import math
 
 import numpy as np
 
+from oracle import fa, float_type
+
 
 def fused_scalars(lr, b1, b2, eps, t):
     if t < 1:
@@ -24,21 +26,21 @@ def fused_scalars(lr, b1, b2, eps, t):
 
 def fused_step(p, g, S, V, t, lr, b1=0.9, b2=0.999, eps=1e-8, weight_decay=0.0):
     """One update in the stored form; returns (p, S, V) as float64."""
-    p = np.asarray(p, np.float64)
-    g = np.asarray(g, np.float64)
+    p = fa(p)
+    g = fa(g)
     if weight_decay:
         g = g + weight_decay * p
-    V = g * g + b2 * np.asarray(V, np.float64)
-    S = g + b1 * np.asarray(S, np.float64)
+    V = g * g + b2 * fa(V)
+    S = g + b1 * fa(S)
     alpha_t, eps_t = fused_scalars(lr, b1, b2, eps, t)
     return p - alpha_t * S / (np.sqrt(V) + eps_t), S, V
 
 
 def textbook_step(p, g, m, v, t, lr, b1=0.9, b2=0.999, eps=1e-8):
-    p = np.asarray(p, np.float64)
-    g = np.asarray(g, np.float64)
-    m = b1 * np.asarray(m, np.float64) + (1 - b1) * g
-    v = b2 * np.asarray(v, np.float64) + (1 - b2) * g * g
+    p = fa(p)
+    g = fa(g)
+    m = b1 * fa(m) + (1 - b1) * g
+    v = b2 * fa(v) + (1 - b2) * g * g
     mhat = m / (1 - b1 ** t)
     vhat = v / (1 - b2 ** t)
     return p - lr * mhat / (np.sqrt(vhat) + eps), m, v

@@ -9,6 +9,8 @@ from __future__ import annotations
 
 import numpy as np
 
+from oracle import fa, float_type
+
 
 def out_size(size: int, kernel: int, stride: int, padding: int = 0) -> int:
     """(size + 2p - k)/s + 1, refusing ragged geometry (ttrl/engine/conv/geometry.py:107-119)."""
@@ -27,24 +29,24 @@ def _windows(x: np.ndarray, k: int, s: int, p: int) -> np.ndarray:
 
 def forward(x: np.ndarray, w: np.ndarray, b: np.ndarray | None, stride: int, padding: int = 0) -> np.ndarray:
     """y[n,i,j,o] = sum_{c,p,q} x[n, i*s+p, j*s+q, c] w[o,c,p,q] + b[o]; x NHWC, w OIHW."""
-    x = np.asarray(x, np.float64)
-    w = np.asarray(w, np.float64)
+    x = fa(x)
+    w = fa(w)
     o, _, k, _ = w.shape
     win = _windows(x, k, stride, padding)
     n, oh, ow = win.shape[:3]
     cols = win.reshape(n * oh * ow, -1)
     y = cols @ w.reshape(o, -1).T
     if b is not None:
-        y = y + np.asarray(b, np.float64).reshape(-1)
+        y = y + fa(b).reshape(-1)
     return y.reshape(n, oh, ow, o)
 
 
 def backward(x: np.ndarray, w: np.ndarray, dy: np.ndarray, stride: int, padding: int = 0,
              need_dx: bool = True):
     """(dx NHWC | None, dw OIHW, db (O,)) for y = forward(x, w, b)."""
-    x = np.asarray(x, np.float64)
-    w = np.asarray(w, np.float64)
-    dy = np.asarray(dy, np.float64)
+    x = fa(x)
+    w = fa(w)
+    dy = fa(dy)
     o, c, k, _ = w.shape
     win = _windows(x, k, stride, padding)  # (n, oh, ow, c, k, k)
     dw = np.einsum("nijckl,nijo->ockl", win, dy, optimize=True)
@@ -53,7 +55,7 @@ def backward(x: np.ndarray, w: np.ndarray, dy: np.ndarray, stride: int, padding:
     if need_dx:
         n, h, wd, _ = x.shape
         oh, ow = dy.shape[1], dy.shape[2]
-        dxp = np.zeros((n, h + 2 * padding, wd + 2 * padding, c))
+        dxp = np.zeros((n, h + 2 * padding, wd + 2 * padding, c), float_type())
         # contribution of every output pixel to its input window
         contrib = np.einsum("nijo,ockl->nijklc", dy, w, optimize=True)
         for p in range(k):

@@ -17,6 +17,8 @@ import json
 
 import numpy as np
 
+from oracle import fa, float_type
+
 __all__ = ["read", "head_rows", "actions"]
 
 
@@ -46,15 +48,15 @@ def head_rows(meta: dict, arrays: dict, obs: np.ndarray) -> np.ndarray:
     """The head's raw rows for a batch of raw observations
     (ttrl/deploy/artifact.py:188-203, ttrl/deploy/conv.py:22-29)."""
     shape = tuple(int(d) for d in meta["obs_shape"])
-    hidden = np.asarray(obs, np.float64).reshape((-1,) + shape)
+    hidden = fa(obs).reshape((-1,) + shape)
     if meta["conv"]:
-        stages = [(arrays[f"conv.{i}.weight"].astype(np.float64), arrays[f"conv.{i}.bias"].astype(np.float64),
+        stages = [(arrays[f"conv.{i}.weight"].astype(float_type(), copy=False), arrays[f"conv.{i}.bias"].astype(float_type(), copy=False),
                    int(g["stride"]), int(g["padding"])) for i, g in enumerate(meta["conv"])]
         hidden = _conv_features(hidden, stages)
     for i in range(int(meta["trunk_layers"])):
-        hidden = np.maximum(hidden @ arrays[f"trunk.{i}.weight"].astype(np.float64)
-                            + arrays[f"trunk.{i}.bias"].astype(np.float64), 0.0)
-    return hidden @ arrays["head.weight"].astype(np.float64) + arrays["head.bias"].astype(np.float64)
+        hidden = np.maximum(hidden @ arrays[f"trunk.{i}.weight"].astype(float_type(), copy=False)
+                            + arrays[f"trunk.{i}.bias"].astype(float_type(), copy=False), 0.0)
+    return hidden @ arrays["head.weight"].astype(float_type(), copy=False) + arrays["head.bias"].astype(float_type(), copy=False)
 
 
 def actions(meta: dict, arrays: dict, obs: np.ndarray) -> np.ndarray:
@@ -64,8 +66,8 @@ def actions(meta: dict, arrays: dict, obs: np.ndarray) -> np.ndarray:
     kind = meta["action_map"]
     if kind == "argmax":
         return np.argmax(row, axis=-1).astype(np.int64)
-    low = arrays["action_low"].astype(np.float64)
-    high = arrays["action_high"].astype(np.float64)
+    low = arrays["action_low"].astype(float_type(), copy=False)
+    high = arrays["action_high"].astype(float_type(), copy=False)
     if kind == "tanh_bounds":
         return (high + low) * 0.5 + (high - low) * 0.5 * np.tanh(row)
     if kind == "clip_bounds":

@@ -14,7 +14,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle import adam
+from oracle import adam, fa, float_type
 from oracle.nets import GateStats, QNet, qnet_backward, qnet_forward
 
 ARGMAX_BAND = 1e-4
@@ -61,23 +61,23 @@ def dqn_update(online: QNet, target: QNet, batch: dict, *, double: bool = True, 
     sel = q_online_next if double else q_target_next
     a_star, adopted = select_actions(sel, device_next_actions)
     nv = q_target_next[np.arange(B), a_star]
-    rewards = np.asarray(batch["rewards"], np.float64).reshape(-1)
-    dones = np.asarray(batch["dones"], np.float64).reshape(-1)
-    discounts = np.asarray(batch["discounts"], np.float64).reshape(-1)
+    rewards = fa(batch["rewards"]).reshape(-1)
+    dones = fa(batch["dones"]).reshape(-1)
+    discounts = fa(batch["discounts"]).reshape(-1)
     y = rewards + discounts * (1.0 - dones) * nv
     pred = q[np.arange(B), actions]
     e = pred - y
-    w = np.asarray(batch["is_weights"], np.float64).reshape(-1) if prioritized else np.ones(B)
+    w = fa(batch["is_weights"]).reshape(-1) if prioritized else np.ones(B, float_type())
     loss = float(np.mean(w * huber(e, delta)))
-    dq = np.zeros((B, A))
+    dq = np.zeros((B, A), float_type())
     dq[np.arange(B), actions] = w / B * np.clip(e, -delta, delta)
     grads = qnet_backward(online, acts, dq)
     grad_sq = float(sum(np.sum(g * g) for g in grads))
     b1, b2 = betas
     new, new_S, new_V = [], [], []
     for i, (p, g) in enumerate(zip(online.flat(), grads)):
-        S0 = np.zeros_like(g) if adam_state is None else np.asarray(adam_state[0][i], np.float64).reshape(g.shape)
-        V0 = np.zeros_like(g) if adam_state is None else np.asarray(adam_state[1][i], np.float64).reshape(g.shape)
+        S0 = np.zeros_like(g) if adam_state is None else fa(adam_state[0][i]).reshape(g.shape)
+        V0 = np.zeros_like(g) if adam_state is None else fa(adam_state[1][i]).reshape(g.shape)
         p1, S1, V1 = adam.fused_step(p, g, S0, V0, t, lr, b1, b2, eps)
         new.append(p1)
         new_S.append(S1)

@@ -9,6 +9,8 @@ import math
 
 import numpy as np
 
+from oracle import fa, float_type
+
 LOG_2PI = math.log(2.0 * math.pi)
 LOG_2 = math.log(2.0)
 
@@ -19,10 +21,10 @@ def softplus(x):
 
 def sample(mean, log_std, noise, centre=0.0, half_width=1.0, log_det=0.0):
     """-> (action, logp (B,), u)."""
-    mean = np.asarray(mean, np.float64)
-    log_std = np.asarray(log_std, np.float64)
+    mean = fa(mean)
+    log_std = fa(log_std)
     sigma = np.exp(log_std)
-    u = mean + sigma * np.asarray(noise, np.float64)
+    u = mean + sigma * fa(noise)
     z = (u - mean) / sigma
     d = mean.shape[-1]
     normal = np.sum(-0.5 * z * z - log_std, axis=-1) - 0.5 * d * LOG_2PI
@@ -34,15 +36,15 @@ def sample(mean, log_std, noise, centre=0.0, half_width=1.0, log_det=0.0):
 def sample_backward(mean, log_std, noise, g_action, g_logp, half_width=1.0):
     """dL/dmean, dL/dlog_std (before any clamp mask) for upstream
     dL/daction (B, d) and dL/dlogp (B,)."""
-    mean = np.asarray(mean, np.float64)
-    log_std = np.asarray(log_std, np.float64)
+    mean = fa(mean)
+    log_std = fa(log_std)
     sigma = np.exp(log_std)
-    eps = np.asarray(noise, np.float64)
+    eps = fa(noise)
     u = mean + sigma * eps
     z = (u - mean) / sigma
     t = np.tanh(u)
-    glp = np.asarray(g_logp, np.float64).reshape(-1, 1)
-    gu = np.asarray(g_action, np.float64) * half_width * (1.0 - t * t) + glp * (2.0 * t - z / sigma)
+    glp = fa(g_logp).reshape(-1, 1)
+    gu = fa(g_action) * half_width * (1.0 - t * t) + glp * (2.0 * t - z / sigma)
     gmean = gu + glp * (z / sigma)
     gls = gu * sigma * eps + glp * (z * z - 1.0)
     return gmean, gls

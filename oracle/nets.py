@@ -22,7 +22,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from oracle import conv
+from oracle import conv, fa, float_type
 
 KINK_BAND = 1e-4
 
@@ -73,7 +73,7 @@ class QNet:
 
 def qnet_forward(net: QNet, frames: np.ndarray, *, gates=None, stats=None, prefix: str = ""):
     """-> (q (B, A), acts); acts holds (input, pre-activation, gate) per layer."""
-    x = np.asarray(frames, np.float64)
+    x = fa(frames)
     h = x.transpose(0, 2, 3, 1) * net.scale
     acts = []
     for i, (w, b, s, p) in enumerate(net.convs):
@@ -97,7 +97,7 @@ def qnet_forward(net: QNet, frames: np.ndarray, *, gates=None, stats=None, prefi
 
 def qnet_backward(net: QNet, acts, dq: np.ndarray) -> list:
     """Gradients in `QNet.flat()` order for upstream dL/dq."""
-    g = np.asarray(dq, np.float64)
+    g = fa(dq)
     nconv = len(net.convs)
     fc_grads = []
     for j in range(len(net.fcs) - 1, -1, -1):
@@ -130,7 +130,7 @@ def qnet_backward(net: QNet, acts, dq: np.ndarray) -> list:
 
 def mlp_forward(layers: list, x: np.ndarray, *, relu_last: bool = False, gates=None, stats=None, prefix=""):
     """Linear (+ReLU on all but the last unless relu_last) -> (out, acts)."""
-    h = np.asarray(x, np.float64)
+    h = fa(x)
     acts = []
     last = len(layers) - 1
     for j, (w, b) in enumerate(layers):
@@ -147,7 +147,7 @@ def mlp_forward(layers: list, x: np.ndarray, *, relu_last: bool = False, gates=N
 
 def mlp_backward(layers: list, acts, dout: np.ndarray, *, need_dx: bool = False):
     """-> ([(dW, db) per layer], dx | None)."""
-    g = np.asarray(dout, np.float64)
+    g = fa(dout)
     grads = []
     for j in range(len(layers) - 1, -1, -1):
         h_in, _, m = acts[j]

@@ -21,7 +21,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from oracle import adam, gaussian
+from oracle import adam, gaussian, fa, float_type
 from oracle.nets import GateStats, mlp_backward, mlp_forward
 
 LOG_STD_MIN = -20.0
@@ -60,7 +60,7 @@ def policy_forward(P: SacParams, obs, *, gates=None, stats=None, prefix="policy.
 
 
 def critic_forward(layers, obs, action, *, gates=None, stats=None, prefix=""):
-    x = np.concatenate([np.asarray(obs, np.float64), np.asarray(action, np.float64)], axis=1)
+    x = np.concatenate([fa(obs), fa(action)], axis=1)
     return mlp_forward(layers, x, gates=gates, stats=stats, prefix=prefix)
 
 
@@ -76,15 +76,15 @@ def sac_update(P: SacParams, batch: dict, *, lr: float = 3e-4, eps: float = 1e-8
                tau: float = 0.005, target_entropy: float | None = None, learn_alpha: bool = True,
                prioritized: bool = False, gates=None) -> dict:
     stats = GateStats()
-    obs = np.asarray(batch["obs"], np.float64)
-    nxt = np.asarray(batch["next_obs"], np.float64)
-    act = np.asarray(batch["actions"], np.float64)
+    obs = fa(batch["obs"])
+    nxt = fa(batch["next_obs"])
+    act = fa(batch["actions"])
     B, d = act.shape
     H = -float(d) if target_entropy is None else float(target_entropy)
-    r = np.asarray(batch["rewards"], np.float64).reshape(-1)
-    done = np.asarray(batch["dones"], np.float64).reshape(-1)
-    disc = np.asarray(batch["discounts"], np.float64).reshape(-1)
-    w = np.asarray(batch["is_weights"], np.float64).reshape(-1) if prioritized else np.ones(B)
+    r = fa(batch["rewards"]).reshape(-1)
+    done = fa(batch["dones"]).reshape(-1)
+    disc = fa(batch["discounts"]).reshape(-1)
+    w = fa(batch["is_weights"]).reshape(-1) if prioritized else np.ones(B, float_type())
     alpha = float(np.exp(P.log_alpha))
 
     # ---- critic region
@@ -127,7 +127,7 @@ def sac_update(P: SacParams, batch: dict, *, lr: float = 3e-4, eps: float = 1e-8
     for i, c in enumerate(new_critics):
         _, dx = mlp_backward(c, cachea[i], dq[i].reshape(-1, 1), need_dx=True)
         g_action += dx[:, obs_dim:]
-    g_logp = np.full(B, alpha / B)
+    g_logp = np.full(B, alpha / B, float_type())
     gmean, gls = gaussian.sample_backward(mean, ls, batch["noise"], g_action, g_logp)
     gls = gls * ((raw > LOG_STD_MIN) & (raw < LOG_STD_MAX))
     dW_mean, db_mean = h.T @ gmean, gmean.sum(0)

@@ -525,19 +525,23 @@ int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_h
   if (g && !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_step: destroyed graph");
   if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_step: the stream is capturing");
   // Host buffers from ttrl_host_alloc are pinned already: the copies read
-  // and write them in place, with no staging pass.
-  const bool in_pinned = in_bytes && in_host_block(ctx, in_host, in_bytes);
-  const bool out_pinned = out_bytes && in_host_block(ctx, out_host, out_bytes);
+  // and write them in place, with no staging pass (an empty side needs none).
+  const bool in_pinned = in_bytes == 0 || in_host_block(ctx, in_host, in_bytes);
+  const bool out_pinned = out_bytes == 0 || in_host_block(ctx, out_host, out_bytes);
   if (in_pinned && out_pinned) {
     hipError_t e;
-    e = hipMemcpyAsync(in_dev, in_host, in_bytes, hipMemcpyHostToDevice, ctx->stream);
-    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (graph step)");
+    if (in_bytes) {
+      e = hipMemcpyAsync(in_dev, in_host, in_bytes, hipMemcpyHostToDevice, ctx->stream);
+      if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (graph step)");
+    }
     if (g) {
       e = hipGraphLaunch(g->exec, ctx->stream);
       if (e != hipSuccess) return hip_error(e, "hipGraphLaunch (graph step)");
     }
-    e = hipMemcpyAsync(out_host, out_dev, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
-    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync D2H (graph step)");
+    if (out_bytes) {
+      e = hipMemcpyAsync(out_host, out_dev, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
+      if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync D2H (graph step)");
+    }
     e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize (graph step)");
     return TTRL_OK;

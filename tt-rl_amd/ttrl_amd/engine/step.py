@@ -98,9 +98,12 @@ class InputBinder:
         self._dirty.clear()
 
     def take_single_range(self):
-        """The one pending range (begin, end) when exactly one is pending,
-        clearing it (the caller sends it), else None."""
+        """The one pending range (begin, end) when at most one is pending
+        ((0, 0) when none is), clearing
+        it (the caller sends it), else None."""
         spans = self.pending()
+        if not spans:
+            return (0, 0)
         if len(spans) != 1:
             return None
         self._dirty.clear()
