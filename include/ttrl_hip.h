@@ -238,6 +238,54 @@ int ttrl_conv2d_backward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* 
                          const float* ymask, const float* wt, float* dwt, float* db, float beta_w, float* dx,
                          const float* xmask, float beta_x);
 
+/* Gradient sources: a parameter's gradient that an earlier launch left
+ * unreduced, formed by the optimizer step that consumes it
+ * (ttrl_adam_step_sources) or by ttrl_grad_sources_materialize.  The
+ * gradient is a [rows][cols] row-major block at dw and, when db is not
+ * NULL, cols bias entries at db.
+ *   TTRL_GRAD_SPLITS: split-K partial sums part[splits][rows (+1)][cols]
+ *     (the extra row is the bias's): dw[r][c] = scale * sum_s part[s][r][c],
+ *     db[c] = bias_scale * sum_s part[s][rows][c], summed in split order from
+ *     zero, as the weight-gradient launch itself would.
+ *   TTRL_GRAD_OUTER: dw[r][c] = sum_b u[b][r] * v[b][c] and
+ *     db[c] = sum_b v[b][c], b = 0 .. batch-1 in order from zero (a linear
+ *     layer's gradients from its input rows u[batch][rows] and output
+ *     gradient rows v[batch][cols]).
+ *   TTRL_GRAD_NONE: nothing pending (the launch wrote dw and db itself). */
+#define TTRL_GRAD_NONE 0
+#define TTRL_GRAD_SPLITS 1
+#define TTRL_GRAD_OUTER 2
+typedef struct ttrl_grad_source {
+  int kind;
+  int rows, cols;
+  float* dw;
+  float* db;
+  const float* part; /* TTRL_GRAD_SPLITS */
+  int splits;
+  float scale, bias_scale;
+  const float* u; /* TTRL_GRAD_OUTER */
+  const float* v;
+  int batch;
+} ttrl_grad_source;
+/* ttrl_conv2d_backward with the weight gradient's split-K sum left to the
+ * optimizer step (ttrl/engine/conv/backward.py:33-78): when the planned
+ * launch splits the weight-gradient GEMM, its partials stay in gradient
+ * bank `bank` (0 <= bank < 4, 4 MiB each, owned by the context) and *out
+ * describes them (TTRL_GRAD_SPLITS); otherwise dwt and db are written and
+ * out->kind is TTRL_GRAD_NONE.  The weight gradient is not accumulated
+ * (beta_w = 0).  A bank's partials live until the next deferred call that
+ * names the same bank. */
+int ttrl_conv2d_backward_deferred(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale,
+                                  const float* dy, const float* ymask, const float* wt, float* dwt, float* db,
+                                  float* dx, const float* xmask, float beta_x, int bank, ttrl_grad_source* out);
+/* ttrl_conv2d_backward_weight with the same deferral (beta = 0). */
+int ttrl_conv2d_backward_weight_deferred(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale,
+                                         const float* dy, const float* ymask, float* dwt, float* db, int bank,
+                                         ttrl_grad_source* out);
+/* Writes the gradients `n` sources describe (<= 8), with the bits the
+ * optimizer step that consumes them would form. */
+int ttrl_grad_sources_materialize(ttrl_ctx* ctx, int n, const ttrl_grad_source* sources);
+
 /* ---------------------------------------------------------- loss heads --- */
 
 /* The DQN update head of update_loss (ttrl/algos/dqn/losses.py:77-140):
@@ -271,8 +319,14 @@ int ttrl_dqn_head(ttrl_ctx* ctx, int B, int K, int A, int groups, const float* c
  * dh = dq W2[0]^T * [h[0] > 0], the gradient entering the first layer's
  * backward; dW2 = h[0]^T dq and db2 = column sums of dq, the second layer's
  * gradients (added to their values when beta_w = 1).  b1, b2, is_weights,
- * mean_q, td_abs, next_actions, td_target and db2 may be NULL.  B <= 1024,
- * F <= 2048, A <= 32. */
+ * mean_q, td_abs, next_actions, td_target and db2 may be NULL.  dW2 NULL
+ * leaves the second layer's gradients to the caller (an outer-product
+ * gradient source over h[0] and dq).  loss_terms not NULL defers the batch
+ * sums as well: sample b's weighted Huber term and prediction go to
+ * loss_terms[2b] and loss_terms[2b + 1], loss and mean_q are not written
+ * (the caller sums the terms in sample order and scales by 1/B), and dW2
+ * must be NULL; the launch then needs no cross-workgroup step.
+ * B <= 1024, F <= 2048, A <= 32. */
 typedef struct ttrl_dqn_tail_desc {
   int B, K, F, A, groups;
   const float* x[3];
@@ -298,6 +352,7 @@ typedef struct ttrl_dqn_tail_desc {
   float* dW2;
   float* db2;
   float beta_w;
+  float* loss_terms;
 } ttrl_dqn_tail_desc;
 int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* desc);
 
@@ -386,6 +441,41 @@ int ttrl_adam_step_deferred(ttrl_ctx* ctx, float* p, const float* g, float* m_s,
 int ttrl_adam_multi(ttrl_ctx* ctx, int nranges, const ttrl_adam_range* ranges, float* polyak_dst,
                     const float* polyak_src, long polyak_n, float tau);
 int ttrl_adam_finish_slots(ttrl_ctx* ctx, int n, const ttrl_adam_finish* finishes);
+/* ttrl_adam_step over an arena whose gradients include up to 8 gradient
+ * sources (ranges of g that earlier launches left unreduced): the step forms
+ * each source's gradient, writes it into g, and updates those parameters
+ * with it, so an update needs no separate reduction launch per source
+ * (ttrl/engine/optim/adam.py:93-134 over the gradients of
+ * ttrl/engine/conv/backward.py:45-78 and ttrl/engine/layers.py:22-61).  The
+ * finishing launch also forms up to 4 ordered sums dst = scale * sum over
+ * i < n of src[i * stride], in order from zero (an update's batch means,
+ * ttrl/algos/dqn/losses.py:120-140).  Each source's dw (and db) must lie in
+ * [g, g + n), 16-byte aligned, rows * cols a multiple of 4; a splits
+ * source needs cols % 4 == 0. */
+typedef struct ttrl_ordered_sum {
+  const float* src;
+  int n, stride;
+  float scale;
+  float* dst;
+} ttrl_ordered_sum;
+typedef struct ttrl_adam_sources_desc {
+  float* p;
+  float* g;
+  float* m_s;
+  float* v_s;
+  long n;
+  int* step;
+  float lr, beta1, beta2, eps, weight_decay;
+  float* grad_sq;
+  int accumulate_grad_sq;
+  int nsources;
+  const ttrl_grad_source* sources;
+  int nsums;
+  const ttrl_ordered_sum* sums;
+} ttrl_adam_sources_desc;
+int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* desc);
+/* The ordered sums of ttrl_adam_step_sources without a step (up to 4). */
+int ttrl_ordered_sums(ttrl_ctx* ctx, int n, const ttrl_ordered_sum* sums);
 /* sum(x^2) into *out (grad_sq_device, ttrl/algos/grads.py:46-60). */
 int ttrl_sum_squares(ttrl_ctx* ctx, const float* x, long n, float* out, int accumulate);
 /* dst = (1 - tau) * dst + tau * src (ttrl/algos/sac/targets.py:45-52). */

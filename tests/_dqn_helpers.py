@@ -31,14 +31,15 @@ def oracle_to_state(net, keys) -> dict:
     return {k: v for k, v in zip(keys, flat)}
 
 
-def build_learner(device, *, seed=0, step_mode="graph", double=True, batch=32):
+def build_learner(device, *, seed=0, step_mode="graph", double=True, batch=32, defer_grads=True):
     from ttrl_amd.algos.dqn import DQNConfig, DQNLearner
     from ttrl_amd.spaces import ActionSpec, ObsSpec
     from ttrl_amd.workloads import he_uniform_qnet_state
 
     cfg = DQNConfig(lr=6.25e-5, adam_eps=1.5e-4, batch_size=batch, step_mode=step_mode, double=double,
                     prioritized=True)
-    learner = DQNLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(6), device, cfg=cfg, seed=seed)
+    learner = DQNLearner(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(6), device, cfg=cfg, seed=seed,
+                         defer_grads=defer_grads)
     online = he_uniform_qnet_state(learner.online, seed + 100)
     learner.online.load_state_dict(online)
     rng = np.random.default_rng(seed + 200)

@@ -42,13 +42,16 @@ def _update_recording(learner, batch):
     return m, recs
 
 
-@pytest.mark.parametrize("step_mode", ["graph", "eager"])
-def test_dqn_update_matches_oracle(device, step_mode):
+@pytest.mark.parametrize("step_mode,defer", [("graph", True), ("eager", True), ("graph", False)])
+def test_dqn_update_matches_oracle(device, step_mode, defer):
+    """defer: the weight-gradient reductions, the Q head's gradients and the
+    batch means formed by the Adam launch (gradient sources) rather than by
+    launches of their own."""
     from oracle.dqn import dqn_update
     from oracle.nets import qnet_forward
     from ttrl_amd.workloads import dqn_batch
 
-    learner, online, target = build_learner(device, seed=0, step_mode=step_mode)
+    learner, online, target = build_learner(device, seed=0, step_mode=step_mode, defer_grads=defer)
     batch = dqn_batch(11, batch=32)
     onet, tnet = qnet_to_oracle(online), qnet_to_oracle(target)
     m, recs = _update_recording(learner, batch)

@@ -25,12 +25,51 @@ unsigned* ctx_sync_words(ttrl_ctx* ctx);
 // each kept from its step to its finish (ttrl_adam_finish_slots).
 constexpr int kAdamSlots = 8, kAdamSlotFloats = 1024;
 float* ctx_adam_partials(ttrl_ctx* ctx);
+// Gradient banks: split-K partials of weight gradients whose sum an
+// optimizer step forms later (ttrl_conv2d_backward_deferred); a bank's
+// contents live until the next deferred launch that names it.
+constexpr int kGradBanks = 4;
+constexpr long kGradBankFloats = 1L << 20;
+float* ctx_grad_bank(ttrl_ctx* ctx, int bank);
 // Converts a pending launch error into a status code.
 int check_launch(const char* name);
 
 inline unsigned ceil_div(long a, long b) { return unsigned((a + b - 1) / b); }
 
+// Division by a runtime-constant positive divisor d with a multiply-high:
+// q = (umulhi(n, m) + n) >> s, m = floor(2^32 (2^s - d) / d) + 1, s = ceil(log2 d)
+// (exact for 0 <= n < 2^31).
+struct FDiv {
+  uint32_t m = 0, s = 0;
+  int d = 1;
+  __host__ void set(int divisor) {
+    d = divisor;
+    s = 0;
+    while ((1u << s) < uint32_t(divisor)) ++s;
+    const uint64_t two32 = uint64_t(1) << 32;
+    m = uint32_t((two32 * ((uint64_t(1) << s) - uint64_t(divisor))) / uint64_t(divisor) + 1);
+  }
+  __device__ __forceinline__ int div(int n) const {
+    const uint32_t hi = __umulhi(uint32_t(n), m);
+    return int((uint64_t(hi) + uint32_t(n)) >> s);
+  }
+};
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Touches every 64-byte line of the first BYTES bytes of the kernel's
+// argument segment with independent scalar loads and waits for them once,
+// so the argument reads that follow hit the scalar cache instead of taking
+// one memory round trip per line, one after another.
+template <int BYTES>
+__device__ __forceinline__ void warm_kernargs() {
+  typedef __attribute__((address_space(4))) const uint32_t kword;
+  kword* ka = (kword*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t t = 0;
+#pragma unroll
+  for (int o = 0; o < BYTES / 4; o += 16) t ^= ka[o];
+  asm volatile("" ::"s"(t));
+}
 
 // Deterministic (fixed-order) reduction of one float per thread over a
 // block of NT threads.  Wavefronts of 64 fold with DPP-free shuffles, then

@@ -536,6 +536,27 @@ inline ConvDwProblem<MODE> conv_dw_problem(const ConvGeo& g, const void* x, floa
   return p;
 }
 
+// The gradient source of a weight-gradient launch that ran `plan` with its
+// partials in `part`: split partials when the plan split K (the epilogue's
+// alpha = x_scale for the weight rows, 1 for the bias row), nothing pending
+// otherwise.
+inline ttrl_grad_source conv_dw_source(const ConvGeo& g, float x_scale, float* dwt, float* db, const float* part,
+                                       const GemmPlan& plan) {
+  ttrl_grad_source s{};
+  s.rows = g.C * g.KH * g.KW;
+  s.cols = g.O;
+  s.dw = dwt;
+  s.db = db;
+  if (plan.splits > 1) {
+    s.kind = TTRL_GRAD_SPLITS;
+    s.part = part;
+    s.splits = plan.splits;
+    s.scale = x_scale;
+    s.bias_scale = 1.f;
+  }
+  return s;
+}
+
 // The input-gradient GEMM of residue classes c0 .. c0+n-1 (n <= kMaxGroups).
 struct ConvDxProblem {
   LdConvDxA la;

@@ -15,8 +15,11 @@
 //   dh[b]   = (dq[b] W2_0^T) * [h_0[b] > 0]      the gradient entering the
 //             first layer's backward, already through its ReLU
 // and the workgroup that finishes last (a device-scope counter, reset by it)
-// sums, in sample order, the batch loss and mean Q and the second layer's
-// weight and bias gradients dW2 = h_0^T dq, db2 = column sums of dq.
+// sums, in sample order, the batch loss and mean Q and, when the caller asks
+// for them here, the second layer's weight and bias gradients
+// dW2 = h_0^T dq, db2 = column sums of dq.  A caller that leaves dW2 out
+// forms it later from h_0 and dq (an outer-product gradient source of the
+// optimizer step), off this kernel's serial last phase.
 //
 // This replaces a split-K reduce, the Q-head-and-loss kernel and the second
 // layer's backward launch: three graph nodes become one.
@@ -34,6 +37,7 @@ constexpr int kTailMaxA = 32;
 constexpr int kTailMaxB = kSyncPartials / 2;  // two partial sums per sample in the sync words
 constexpr int kTailChunk = 32;                // samples per pass of the weight-gradient sum
 constexpr int kTailItems = 8;                 // first-layer outputs per thread per pass
+constexpr int kTailSplits = 16;               // split partials of an output loaded in one batch, at most
 static_assert(kSyncPartials + kTailChunk * kTailMaxA <= 3 * kTailMaxF, "the last workgroup's staging fits hs");
 
 constexpr unsigned kFc1Cfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
@@ -41,6 +45,7 @@ constexpr unsigned kFc1Cfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64
 
 struct TailArgs {
   int B, F, A, G, splits;  // splits 0: h holds the first layer's outputs already
+  FDiv fdiv;               // division by F
   const float* part;       // [G][splits][B][F]
   float* h[3];
   const float* b1[3];
@@ -65,6 +70,7 @@ struct TailArgs {
   float beta_w;
   unsigned* counter;
   float* partials;
+  float* loss_terms;  // not null: per-sample terms for the caller, no batch phase
 };
 
 // Every phase issues all of its loads before it uses one: the kernel is a
@@ -95,29 +101,39 @@ __device__ __forceinline__ float wave_sum(float v) {
   return ((r0 + r1) + r2) + r3;
 }
 
+// NPRE: features per thread whose second-layer weights are fetched before
+// the first layer's sums (registers they occupy: NPRE * 3 * AP).
 template <int AP>
+constexpr int tail_prefetch() { return AP <= 16 ? 2 : 1; }
+
+template <int AP, int SP>
 __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
+  constexpr int NPRE = tail_prefetch<AP>();
   __shared__ float hs[3 * kTailMaxF];  // the sample's first-layer outputs; the last workgroup's staging
   __shared__ float red[kTailThreads / 64][3 * AP];
-  __shared__ float qrow[3 * kTailMaxA];
-  __shared__ float dqrow[kTailMaxA];
-  __shared__ float onehot[kTailMaxA];
-  __shared__ float scal[4];  // reward, done, discount, importance weight
+  __shared__ float qrow[3 * AP];
+  __shared__ float dqrow[AP];
   __shared__ int last;
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int F = t.F, A = t.A, G = t.G, S = t.splits, B = t.B;
 
-  // 0. the sample's action, reward, done, discount and weight, in flight
-  // with the first layer's loads
-  if (tid < A) onehot[tid] = t.onehot[long(b) * A + tid];
-  if (tid >= A && tid < AP) dqrow[tid] = 0.f;  // dq's padding columns, read by phase 4
-  if (tid == kTailMaxA) scal[0] = t.rewards[b];
-  if (tid == kTailMaxA + 1) scal[1] = t.dones[b];
-  if (tid == kTailMaxA + 2) scal[2] = t.discounts[b];
-  if (tid == kTailMaxA + 3) scal[3] = t.weights ? t.weights[b] : 1.f;
-
+  // 0. the second layer's weights of this thread's first NPRE features in
+  // every set, in flight with the first layer's loads
+  float w2p[NPRE][3][AP];
+#pragma unroll
+  for (int i = 0; i < NPRE; ++i) {
+    const int n = min(tid + i * kTailThreads, F - 1);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const float* w = t.W2[g] + long(n) * A;
+#pragma unroll
+      for (int a = 0; a < AP; ++a) w2p[i][g][a] = w[min(a, A - 1)];
+    }
+  }
   // 1. the first layer's outputs of sample b, every feature set: item
-  // k = g * F + n, kTailItems items per thread per pass
+  // k = g * F + n, kTailItems items per thread per pass, every split of an
+  // item loaded in one batch (SP of them, indexes past the last split
+  // re-reading it and not added)
   const int items = G * F;
   const long stride = long(B) * F;  // one split's partial tile
   // a lane's feature set is its own: pointers picked by compares, not by a
@@ -128,19 +144,19 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
       for (int u = 0; u < kTailItems; ++u) {
         const int k = k0 + u * kTailThreads + tid;
         if (k >= items) break;
-        const int g = k / F, n = k - g * F;
+        const int g = t.fdiv.div(k), n = k - g * F;
         hs[k] = pick(g, t.h[0], t.h[1], t.h[2])[long(b) * F + n];
       }
       continue;
     }
-    float v[kTailItems][8], bias[kTailItems];
+    float v[kTailItems][SP], bias[kTailItems];
 #pragma unroll
     for (int u = 0; u < kTailItems; ++u) {
       const int k = min(k0 + u * kTailThreads + tid, items - 1);  // a clamped lane's loads are dropped
-      const int g = k / F, n = k - g * F;
+      const int g = t.fdiv.div(k), n = k - g * F;
       const float* p = t.part + (long(g) * S * B + b) * F + n;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[u][j] = p[min(j, S - 1) * stride];
+      for (int j = 0; j < SP; ++j) v[u][j] = p[min(j, S - 1) * stride];
       const float* bg = pick(g, t.b1[0], t.b1[1], t.b1[2]);
       bias[u] = bg ? bg[n] : 0.f;
     }
@@ -148,27 +164,47 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
     for (int u = 0; u < kTailItems; ++u) {
       const int k = k0 + u * kTailThreads + tid;
       if (k >= items) break;
-      const int g = k / F, n = k - g * F;
+      const int g = t.fdiv.div(k), n = k - g * F;
       float sum = 0.f;  // split order from zero, as k_splitk_reduce sums
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sum += j < S ? v[u][j] : 0.f;
+      for (int j = 0; j < SP; ++j) sum += j < S ? v[u][j] : 0.f;
       const float* p = t.part + (long(g) * S * B + b) * F + n;
-      for (int j = 8; j < S; ++j) sum += p[j * stride];
+      for (int j = SP; j < S; ++j) sum += p[j * stride];
       const float h = relu_f(sum + bias[u]);
       pick(g, t.h[0], t.h[1], t.h[2])[long(b) * F + n] = h;
       hs[k] = h;
     }
   }
+  // the sample's action row and scalars (uniform loads), in flight through
+  // the next phase
+  float oh[AP];
+#pragma unroll
+  for (int a = 0; a < AP; ++a) oh[a] = t.onehot[long(b) * A + min(a, A - 1)];
+  const float reward = t.rewards[b], done = t.dones[b], discount = t.discounts[b];
+  const float weight = t.weights ? t.weights[b] : 1.f;
   __syncthreads();
 
   // 2. q_g = h_g W2_g + b2_g: per-thread partial dot products over its
-  // features, a DPP sum over each wavefront, then the wavefronts in order
+  // features in increasing order, a DPP sum over each wavefront, then the
+  // wavefronts in order
   float acc[3][AP];
 #pragma unroll
   for (int g = 0; g < 3; ++g)
 #pragma unroll
     for (int a = 0; a < AP; ++a) acc[g][a] = 0.f;
-  for (int n = tid; n < F; n += kTailThreads) {
+#pragma unroll
+  for (int i = 0; i < NPRE; ++i) {
+    const int n = tid + i * kTailThreads;
+    if (n < F) {
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        const float hv = hs[g * F + n];
+#pragma unroll
+        for (int a = 0; a < AP; ++a) acc[g][a] = fmaf(hv, w2p[i][g][a], acc[g][a]);
+      }
+    }
+  }
+  for (int n = tid + NPRE * kTailThreads; n < F; n += kTailThreads) {
 #pragma unroll
     for (int g = 0; g < 3; ++g)
       if (g < G) {
@@ -189,38 +225,61 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
   __syncthreads();
   if (tid < 3 * AP) {
     const int g = tid / AP, a = tid - g * AP;
+    float v = 0.f;
     if (g < G && a < A) {
-      float v = 0.f;
 #pragma unroll
       for (int w = 0; w < kTailThreads / 64; ++w) v += red[w][tid];
       if (t.b2[g]) v += t.b2[g][a];
-      qrow[g * A + a] = v;
       t.q[g][long(b) * A + a] = v;
     }
+    qrow[tid] = v;
   }
   __syncthreads();
 
-  // 3. the DQN row of sample b
+  // 3. the DQN row of sample b, from registers
   if (tid == 0) {
-    const DqnRow r = dqn_row_v(b, A, qrow, qrow + A, qrow + (G - 1) * A, onehot, scal[0], scal[1], scal[2], scal[3],
-                               t.weights != nullptr, t.delta, 1.f / float(B), t.td_abs, t.next_act, t.td_target,
-                               dqrow);
-    t.partials[2 * b] = r.h;
-    t.partials[2 * b + 1] = r.pred;
+    float q0[AP], qs[AP], qv[AP], dq[AP];
+#pragma unroll
+    for (int a = 0; a < AP; ++a) {
+      q0[a] = qrow[a];
+      qs[a] = qrow[AP + a];
+      qv[a] = qrow[(G - 1) * AP + a];
+    }
+    const DqnRow r = dqn_row_r<AP>(b, A, q0, qs, qv, oh, reward, done, discount, weight, t.weights != nullptr,
+                                   t.delta, 1.f / float(B), t.td_abs, t.next_act, t.td_target, dq);
+#pragma unroll
+    for (int a = 0; a < AP; ++a) dqrow[a] = dq[a];
+    float* terms = t.loss_terms ? t.loss_terms : t.partials;
+    terms[2 * b] = r.h;
+    terms[2 * b + 1] = r.pred;
   }
   __syncthreads();
   if (tid < A) t.dq[long(b) * A + tid] = dqrow[tid];
 
   // 4. dh = dq W2_0^T through the first layer's ReLU
-  for (int n = tid; n < F; n += kTailThreads) {
+  float dqr[AP];
+#pragma unroll
+  for (int a = 0; a < AP; ++a) dqr[a] = dqrow[a];  // zero past A
+#pragma unroll
+  for (int i = 0; i < NPRE; ++i) {
+    const int n = tid + i * kTailThreads;
+    if (n < F) {
+      float s = 0.f;
+#pragma unroll
+      for (int a = 0; a < AP; ++a) s = fmaf(dqr[a], w2p[i][0][a], s);
+      t.dh[long(b) * F + n] = hs[n] > 0.f ? s : 0.f;
+    }
+  }
+  for (int n = tid + NPRE * kTailThreads; n < F; n += kTailThreads) {
     const float* w = t.W2[0] + long(n) * A;
     float s = 0.f;
 #pragma unroll
-    for (int a = 0; a < AP; ++a) s = fmaf(dqrow[a], w[min(a, A - 1)], s);  // dqrow is zero past A
+    for (int a = 0; a < AP; ++a) s = fmaf(dqr[a], w[min(a, A - 1)], s);
     t.dh[long(b) * F + n] = hs[n] > 0.f ? s : 0.f;
   }
 
-  // 5. the last workgroup to finish sums the batch
+  // 5. the last workgroup to finish sums the batch (unless the caller does)
+  if (t.loss_terms) return;
   __threadfence();  // this workgroup's rows, dq and partials, visible device-wide before the count
   __syncthreads();
   if (tid == 0) last = atomicAdd(t.counter, 1u) == unsigned(gridDim.x - 1);
@@ -232,14 +291,16 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
   float* dqs = hs + kSyncPartials;    // a chunk of dq rows
   for (int e = tid; e < 2 * B; e += kTailThreads) part[e] = t.partials[e];
 
-  // dW2 = h_0^T dq, two features per thread per pass; dq staged in LDS a
-  // chunk of samples at a time as [kTailChunk][AP] rows, zero past the batch
-  // and past A.  A chunk's h_0 and dq loads are all issued before the barrier
-  // that waits for them: one memory round trip per pass and chunk.
+  // dW2 = h_0^T dq (when asked for), two features per thread per pass; dq
+  // staged in LDS a chunk of samples at a time as [kTailChunk][AP] rows, zero
+  // past the batch and past A.  A chunk's h_0 and dq loads are all issued
+  // before the barrier that waits for them: one memory round trip per pass
+  // and chunk.
   constexpr int DQV = (kTailChunk * AP + kTailThreads - 1) / kTailThreads;
   const float* h0 = t.h[0];
   float gb = 0.f;
-  for (int n0 = 0; n0 < F; n0 += 2 * kTailThreads) {  // uniform trip counts: the barriers below
+  const int fw = t.dW2 ? F : 0;  // uniform: no pass when the caller forms dW2
+  for (int n0 = 0; n0 < fw; n0 += 2 * kTailThreads) {  // uniform trip counts: the barriers below
     int nn[2], nc[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -329,8 +390,12 @@ int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* d) {
   TTRL_REQUIRE(K > 0 && F > 0 && F <= kTailMaxF, "ttrl_dqn_tail: %d hidden units outside [1, %d]", F, kTailMaxF);
   TTRL_REQUIRE(A > 0 && A <= kTailMaxA, "ttrl_dqn_tail: %d actions outside [1, %d]", A, kTailMaxA);
   TTRL_REQUIRE(d->delta > 0.f, "ttrl_dqn_tail: huber delta must be > 0");
-  TTRL_REQUIRE(d->actions_onehot && d->rewards && d->dones && d->discounts && d->loss && d->dq && d->dh && d->dW2,
+  TTRL_REQUIRE(d->actions_onehot && d->rewards && d->dones && d->discounts && d->dq && d->dh,
                "ttrl_dqn_tail: null argument");
+  TTRL_REQUIRE(d->dW2 || !d->db2, "ttrl_dqn_tail: a bias gradient without the weight gradient");
+  TTRL_REQUIRE(d->loss || d->loss_terms, "ttrl_dqn_tail: neither loss nor loss_terms given");
+  TTRL_REQUIRE(!d->loss_terms || !d->dW2,
+               "ttrl_dqn_tail: with loss_terms the second layer's gradients are the caller's (dW2 must be NULL)");
   TTRL_REQUIRE(long(B) * K * 4 < kMaxOperandBytes && long(K) * F * 4 < kMaxOperandBytes,
                "ttrl_dqn_tail: an operand of 2^30 bytes or more is not supported");
   bool al = true;
@@ -373,6 +438,7 @@ int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* d) {
   t.A = A;
   t.G = G;
   t.splits = plan.splits > 1 ? plan.splits : 0;
+  t.fdiv.set(F);
   long wsf = 0;
   t.part = ctx_workspace(ctx, &wsf);
   for (int g = 0; g < 3; ++g) {
@@ -402,14 +468,16 @@ int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* d) {
   unsigned* words = ctx_sync_words(ctx);
   t.counter = words + kSyncDqnTail;
   t.partials = reinterpret_cast<float*>(words + kSyncCounters);
+  t.loss_terms = d->loss_terms;
   const int ap = A <= 8 ? 8 : (A <= 16 ? 16 : 32);
+  const bool wide = t.splits > 8;  // up to kTailSplits partials per output in one batch
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(unsigned(B)), dim3(kTailThreads), 0, stream_of(ctx), t);
     return check_launch("ttrl_dqn_tail");
   };
-  if (ap == 8) return launch(k_dqn_tail<8>);
-  if (ap == 16) return launch(k_dqn_tail<16>);
-  return launch(k_dqn_tail<32>);
+  if (ap == 8) return wide ? launch(k_dqn_tail<8, kTailSplits>) : launch(k_dqn_tail<8, 8>);
+  if (ap == 16) return wide ? launch(k_dqn_tail<16, kTailSplits>) : launch(k_dqn_tail<16, 8>);
+  return wide ? launch(k_dqn_tail<32, kTailSplits>) : launch(k_dqn_tail<32, 8>);
 }
 
 }  // extern "C"

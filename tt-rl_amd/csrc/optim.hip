@@ -15,9 +15,12 @@
 // sum of squares.  All reductions are fixed-order.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 namespace ttrl {
 
@@ -26,16 +29,11 @@ constexpr int kOptMaxBlocks = 1024;
 
 float* ctx_workspace(ttrl_ctx* ctx, long* floats);
 
-// Block `blk` of `nblk` of one Adam update: its grid-stride share of the
-// range and its partial sum of g^2 into partials[blk].  The same code serves
-// a single-range launch and a range of a multi-range launch, so both give
-// the same bits.
-__device__ __forceinline__ void adam_block(float* __restrict__ p, const float* __restrict__ g,
-                                           float* __restrict__ S, float* __restrict__ V, long n,
-                                           const int* __restrict__ step, float lr, float b1, float b2, float eps,
-                                           float wd, float* __restrict__ partials, int blk, int nblk) {
+// The step's fused scalars (alpha_t, eps_t) from the update count *step + 1,
+// computed once per workgroup.
+__device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float lr, float b1, float b2, float eps,
+                                             float* alpha_t, float* eps_t) {
   __shared__ float sc[2];
-  __shared__ float red[kOptThreads / 64];
   if (threadIdx.x == 0) {
     const int t = *step + 1;
     const double bc1 = 1.0 - pow(double(b1), double(t));
@@ -45,29 +43,96 @@ __device__ __forceinline__ void adam_block(float* __restrict__ p, const float* _
     sc[1] = float(double(eps) / c);
   }
   __syncthreads();
-  const float alpha_t = sc[0], eps_t = sc[1];
+  *alpha_t = sc[0];
+  *eps_t = sc[1];
+}
+
+// The update of four consecutive parameters with gradient gv; g^2 is added
+// to gsq element by element in order.
+__device__ __forceinline__ void adam4(f32x4& pv, const f32x4& gv, f32x4& sv, f32x4& vv, float b1, float b2, float wd,
+                                      float eps_t, float alpha_t, float& gsq) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float graw = gv[q];
+    gsq += graw * graw;
+    const float gg = wd != 0.f ? graw + wd * pv[q] : graw;
+    vv[q] = gg * gg + b2 * vv[q];
+    sv[q] = gg + b1 * sv[q];
+    const float upd = (sv[q] / (sqrtf(vv[q]) + eps_t)) * alpha_t;
+    pv[q] = pv[q] - upd;
+  }
+}
+
+// The update of float4s first, first + step, ... below end whose skip(i)
+// is false, g^2 added to gsq in that order.  The next float4's loads are in
+// flight while one is computed, and the first float4's are issued before
+// the step's scalars are formed (thread 0's double-precision powers), so
+// those latencies overlap.  Every thread of the workgroup calls it (the
+// scalars' barrier); alpha_t and eps_t receive the scalars.
+template <class Skip>
+__device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ S,
+                                          float* __restrict__ V, long first, long end, long step,
+                                          const int* __restrict__ stepc, float lr, float b1, float b2, float eps,
+                                          float wd, float& gsq, float* alpha_t, float* eps_t, Skip skip) {
+  f32x4* P = reinterpret_cast<f32x4*>(p);
+  const f32x4* G = reinterpret_cast<const f32x4*>(g);
+  f32x4* Sv = reinterpret_cast<f32x4*>(S);
+  f32x4* Vv = reinterpret_cast<f32x4*>(V);
+  long i = first;
+  bool have = i < end;
+  f32x4 pv = {}, gv = {}, sv = {}, vv = {};
+  if (have) {
+    pv = P[i];
+    gv = G[i];
+    sv = Sv[i];
+    vv = Vv[i];
+  }
+  adam_scalars(stepc, lr, b1, b2, eps, alpha_t, eps_t);
+  const float at = *alpha_t, et = *eps_t;
+  while (have) {
+    const long j = i + step;
+    const bool more = j < end;
+    f32x4 pn = {}, gn = {}, sn = {}, vn = {};
+    if (more) {
+      pn = P[j];
+      gn = G[j];
+      sn = Sv[j];
+      vn = Vv[j];
+    }
+    if (!skip(i)) {
+      adam4(pv, gv, sv, vv, b1, b2, wd, et, at, gsq);
+      P[i] = pv;
+      Sv[i] = sv;
+      Vv[i] = vv;
+    }
+    i = j;
+    have = more;
+    pv = pn;
+    gv = gn;
+    sv = sn;
+    vv = vn;
+  }
+}
+
+struct NoSkip {
+  __device__ bool operator()(long) const { return false; }
+};
+
+// Block `blk` of `nblk` of one Adam update: its grid-stride share of the
+// range and its partial sum of g^2 into partials[blk].  The same code serves
+// a single-range launch and a range of a multi-range launch, so both give
+// the same bits.
+__device__ __forceinline__ void adam_block(float* __restrict__ p, const float* __restrict__ g,
+                                           float* __restrict__ S, float* __restrict__ V, long n,
+                                           const int* __restrict__ step, float lr, float b1, float b2, float eps,
+                                           float wd, float* __restrict__ partials, int blk, int nblk) {
+  __shared__ float red[kOptThreads / 64];
+  float alpha_t, eps_t;
   float gsq = 0.f;
   const long n4 = n / 4;
   const long stride = long(nblk) * kOptThreads;
-  for (long i = blk * long(kOptThreads) + threadIdx.x; i < n4; i += stride) {
-    f32x4 pv = reinterpret_cast<f32x4*>(p)[i];
-    const f32x4 gv = reinterpret_cast<const f32x4*>(g)[i];
-    f32x4 sv = reinterpret_cast<f32x4*>(S)[i];
-    f32x4 vv = reinterpret_cast<f32x4*>(V)[i];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float graw = gv[q];
-      gsq += graw * graw;
-      const float gg = wd != 0.f ? graw + wd * pv[q] : graw;
-      vv[q] = gg * gg + b2 * vv[q];
-      sv[q] = gg + b1 * sv[q];
-      const float upd = (sv[q] / (sqrtf(vv[q]) + eps_t)) * alpha_t;
-      pv[q] = pv[q] - upd;
-    }
-    reinterpret_cast<f32x4*>(p)[i] = pv;
-    reinterpret_cast<f32x4*>(S)[i] = sv;
-    reinterpret_cast<f32x4*>(V)[i] = vv;
-  }
+  adam_loop(p, g, S, V, blk * long(kOptThreads) + threadIdx.x, n4, stride, step, lr, b1, b2, eps, wd, gsq, &alpha_t,
+            &eps_t, NoSkip{});
   // Tail (n % 4) handled by block 0.
   if (blk == 0) {
     for (long i = n4 * 4 + threadIdx.x; i < n; i += kOptThreads) {
@@ -165,6 +230,334 @@ __global__ __launch_bounds__(kOptThreads) void k_finish(const float* __restrict_
   }
 }
 
+// ----------------------------------------------------- gradient sources ---
+//
+// A source's gradient is formed a float4 at a time: float4 q < nw4 covers
+// elements 4q .. 4q+3 of its [rows][cols] weight block, the next nb4 its
+// bias (elements past cols are the arena's padding: zero).  Each element is
+// summed in the order its unreduced launch would have used, so the step
+// writes the same bits that launch's own reduction would have.
+constexpr int kMaxGradSources = 8;
+constexpr int kMaxOrderedSums = 4;
+constexpr int kSplitBatch = 16;  // split partials of a float4 in flight together
+constexpr int kOuterBatch = 8;   // batch rows of an outer-product float4 in flight together (general path)
+constexpr int kOuterRows = 8;    // batch rows in flight together (staged path)
+constexpr int kOuterLds = 2048;  // v floats an outer-product source stages in LDS
+constexpr int kSumLds = 1024;    // terms of an ordered sum staged in LDS
+
+struct GradSrc {
+  int kind, rows, cols, splits, batch;
+  float scale, bias_scale;
+  float* gw;       // where the weight block's gradient is written
+  float* gb;       // the bias's (null: none)
+  long w4, b4;     // the same places as float4 indexes of the arena (Adam only)
+  int nw4, nb4;
+  const float* part;
+  long sstride;    // floats per split
+  const float* u;
+  const float* v;
+  FDiv dc;         // division by cols
+  int block0, blocks;
+};
+
+__device__ __forceinline__ f32x4 source_grad(const GradSrc& s, int q, bool* bias, int* qq) {
+  *bias = q >= s.nw4;
+  *qq = *bias ? q - s.nw4 : q;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (s.kind == TTRL_GRAD_SPLITS) {
+    const float* base = s.part + (*bias ? long(s.rows) * s.cols : 0L) + 4L * *qq;
+    for (int s0 = 0; s0 < s.splits; s0 += kSplitBatch) {
+      f32x4 v[kSplitBatch];
+#pragma unroll
+      for (int j = 0; j < kSplitBatch; ++j)
+        v[j] = *reinterpret_cast<const f32x4*>(base + long(min(s0 + j, s.splits - 1)) * s.sstride);
+#pragma unroll
+      for (int j = 0; j < kSplitBatch; ++j)
+        if (s0 + j < s.splits) {  // uniform
+          acc.x += v[j].x;
+          acc.y += v[j].y;
+          acc.z += v[j].z;
+          acc.w += v[j].w;
+        }
+    }
+    // the weight-gradient epilogue's alpha * acc + 0 (bias row: bias_scale)
+    const float sc = *bias ? s.bias_scale : s.scale;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = fmaf(sc, acc[c], 0.f);
+    return acc;
+  }
+  // outer product: element e of the weight block is (r, c) = divmod(e, cols)
+  int r[4], c[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * *qq + j;
+    r[j] = *bias ? 0 : s.dc.div(e);
+    c[j] = *bias ? min(e, s.cols - 1) : e - r[j] * s.cols;
+  }
+  for (int b0 = 0; b0 < s.batch; b0 += kOuterBatch) {
+    float uu[kOuterBatch][4], vv[kOuterBatch][4];
+#pragma unroll
+    for (int i = 0; i < kOuterBatch; ++i) {
+      const long bb = min(b0 + i, s.batch - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uu[i][j] = s.u[bb * s.rows + r[j]];
+        vv[i][j] = s.v[bb * s.cols + c[j]];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kOuterBatch; ++i)
+      if (b0 + i < s.batch)  // uniform
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = fmaf(*bias ? 1.f : uu[i][j], vv[i][j], acc[j]);
+  }
+  if (*bias)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = 4 * *qq + j < s.cols ? acc[j] : 0.f;
+  return acc;
+}
+
+// True when an outer-product source's workgroups stage v ([batch][cols])
+// in LDS: then a float4 of the weight block spans at most two rows of u
+// (cols >= 4), both loaded for kOuterRows batch rows at a time.
+__device__ __forceinline__ bool outer_staged(const GradSrc& s) {
+  return s.kind == TTRL_GRAD_OUTER && s.cols >= 4 && s.batch * s.cols <= kOuterLds;
+}
+__device__ __forceinline__ void stage_outer(const GradSrc& s, float* vs) {
+  for (int i = threadIdx.x; i < s.batch * s.cols; i += kOptThreads) vs[i] = s.v[i];
+  __syncthreads();
+}
+// source_grad of a staged outer-product source: the same sums in the same
+// order (b from zero, fmaf(u, v, acc); the bias adds v).
+__device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const float* vs, int q, bool* bias, int* qq) {
+  *bias = q >= s.nw4;
+  *qq = *bias ? q - s.nw4 : q;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (*bias) {
+    int c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = min(4 * *qq + j, s.cols - 1);
+    for (int b = 0; b < s.batch; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = fmaf(1.f, vs[b * s.cols + c[j]], acc[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = 4 * *qq + j < s.cols ? acc[j] : 0.f;
+    return acc;
+  }
+  const int e0 = 4 * *qq, r0 = s.dc.div(e0);
+  const int r1 = min(r0 + 1, s.rows - 1);
+  int c[4];
+  bool second[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int cj = e0 + j - r0 * s.cols;  // < 2 cols: the float4 spans rows r0 and r0 + 1 at most
+    second[j] = cj >= s.cols;
+    c[j] = second[j] ? cj - s.cols : cj;
+  }
+  for (int b0 = 0; b0 < s.batch; b0 += kOuterRows) {
+    float ua[kOuterRows], ub[kOuterRows];
+#pragma unroll
+    for (int i = 0; i < kOuterRows; ++i) {
+      const long bb = min(b0 + i, s.batch - 1);
+      ua[i] = s.u[bb * s.rows + r0];
+      ub[i] = s.u[bb * s.rows + r1];
+    }
+#pragma unroll
+    for (int i = 0; i < kOuterRows; ++i)
+      if (b0 + i < s.batch) {  // uniform
+        const float* vr = vs + (b0 + i) * s.cols;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = fmaf(second[j] ? ub[i] : ua[i], vr[c[j]], acc[j]);
+      }
+  }
+  return acc;
+}
+
+struct AdamSrcArgs {
+  float* p;
+  float* g;
+  float* S;
+  float* V;
+  long n;
+  const int* step;
+  float lr, b1, b2, eps, wd;
+  float* partials;
+  int nsrc;
+  GradSrc src[kMaxGradSources];
+  int plain0, plain_blocks;
+  long chunk4;  // float4s per plain workgroup (a contiguous chunk)
+  int nholes;   // the sources' float4 ranges [lo, hi), which plain workgroups skip
+  long hole_lo[2 * kMaxGradSources], hole_hi[2 * kMaxGradSources];
+};
+
+// Blocks [0, plain0) form the sources' gradients (source k owns blocks
+// [block0, block0 + blocks)) and update their parameters; the rest update
+// contiguous chunks of chunk4 float4s, skipping the sources' ranges (a chunk
+// that meets none, the usual case, checks nothing per float4).  Block b's
+// partial sum of g^2 goes to partials[b].
+__global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_adam_src(AdamSrcArgs a) {
+  __shared__ float red[kOptThreads / 64];
+  warm_kernargs<int(sizeof(AdamSrcArgs))>();
+  const int blk = int(blockIdx.x);
+  float alpha_t, eps_t;
+  float gsq = 0.f;
+  f32x4* P = reinterpret_cast<f32x4*>(a.p);
+  f32x4* Gd = reinterpret_cast<f32x4*>(a.g);
+  f32x4* Sv = reinterpret_cast<f32x4*>(a.S);
+  f32x4* Vv = reinterpret_cast<f32x4*>(a.V);
+  if (blk < a.plain0) {
+    int k = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGradSources; ++i)
+      if (i < a.nsrc && blk >= a.src[i].block0) k = i;
+    const GradSrc& s = a.src[k];
+    __shared__ float vs[kOuterLds];
+    const bool staged = outer_staged(s);  // uniform over the workgroup
+    const int nq = s.nw4 + s.nb4;
+    const int step = s.blocks * kOptThreads;
+    int q = (blk - s.block0) * kOptThreads + int(threadIdx.x);
+    // the first float4's parameters and moments in flight while the
+    // gradient's operands are staged and the scalars formed
+    auto where = [&](int qv) { return qv >= s.nw4 ? s.b4 + (qv - s.nw4) : s.w4 + qv; };
+    f32x4 pv = {}, sv = {}, vv = {};
+    if (q < nq) {
+      const long i = where(q);
+      pv = P[i];
+      sv = Sv[i];
+      vv = Vv[i];
+    }
+    if (staged) stage_outer(s, vs);
+    adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+    for (bool first = true; q < nq; q += step, first = false) {
+      bool bias;
+      int qq;
+      const f32x4 gv = staged ? outer_grad_staged(s, vs, q, &bias, &qq) : source_grad(s, q, &bias, &qq);
+      const long i = (bias ? s.b4 : s.w4) + qq;
+      if (!first) {
+        pv = P[i];
+        sv = Sv[i];
+        vv = Vv[i];
+      }
+      Gd[i] = gv;
+      adam4(pv, gv, sv, vv, a.b1, a.b2, a.wd, eps_t, alpha_t, gsq);
+      P[i] = pv;
+      Sv[i] = sv;
+      Vv[i] = vv;
+    }
+  } else {
+    const long n4 = a.n / 4;
+    const long c0 = long(blk - a.plain0) * a.chunk4, c1 = min(n4, c0 + a.chunk4);
+    bool touch = false;  // uniform: does this chunk meet a source's range?
+    for (int h = 0; h < a.nholes; ++h) touch = touch || (a.hole_lo[h] < c1 && a.hole_hi[h] > c0);
+    if (!touch) {
+      adam_loop(a.p, a.g, a.S, a.V, c0 + threadIdx.x, c1, kOptThreads, a.step, a.lr, a.b1, a.b2, a.eps, a.wd, gsq,
+                &alpha_t, &eps_t, NoSkip{});
+    } else {
+      adam_loop(a.p, a.g, a.S, a.V, c0 + threadIdx.x, c1, kOptThreads, a.step, a.lr, a.b1, a.b2, a.eps, a.wd, gsq,
+                &alpha_t, &eps_t, [&](long i) {
+                  bool in = false;
+                  for (int h = 0; h < a.nholes; ++h) in = in || (i >= a.hole_lo[h] && i < a.hole_hi[h]);
+                  return in;
+                });
+    }
+    // Tail (n % 4) handled by the first plain block; no source reaches it.
+    if (blk == a.plain0) {
+      for (long i = n4 * 4 + threadIdx.x; i < a.n; i += kOptThreads) {
+        const float graw = a.g[i];
+        gsq += graw * graw;
+        const float gg = a.wd != 0.f ? graw + a.wd * a.p[i] : graw;
+        a.V[i] = gg * gg + a.b2 * a.V[i];
+        a.S[i] = gg + a.b1 * a.S[i];
+        a.p[i] = a.p[i] - (a.S[i] / (sqrtf(a.V[i]) + eps_t)) * alpha_t;
+      }
+    }
+  }
+  const float tot = block_sum<kOptThreads>(gsq, red);
+  if (threadIdx.x == 0) a.partials[blk] = tot;
+}
+
+// Writes the sources' gradients only (no step).
+struct SrcSet {
+  int nsrc;
+  GradSrc src[kMaxGradSources];
+};
+__global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
+  warm_kernargs<int(sizeof(SrcSet))>();
+  const int blk = int(blockIdx.x);
+  int k = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGradSources; ++i)
+    if (i < a.nsrc && blk >= a.src[i].block0) k = i;
+  const GradSrc& s = a.src[k];
+  __shared__ float vs[kOuterLds];
+  const bool staged = outer_staged(s);
+  if (staged) stage_outer(s, vs);
+  const int nq = s.nw4 + s.nb4;
+  for (int q = (blk - s.block0) * kOptThreads + int(threadIdx.x); q < nq; q += s.blocks * kOptThreads) {
+    bool bias;
+    int qq;
+    const f32x4 gv = staged ? outer_grad_staged(s, vs, q, &bias, &qq) : source_grad(s, q, &bias, &qq);
+    if (!bias) {
+      reinterpret_cast<f32x4*>(s.gw)[qq] = gv;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (4 * qq + j < s.cols) s.gb[4 * qq + j] = gv[j];
+    }
+  }
+}
+
+// Ordered sums dst = scale * sum_{i<n} src[i*stride], one thread each.
+struct OrderedSums {
+  const float* src[kMaxOrderedSums];
+  int n[kMaxOrderedSums], stride[kMaxOrderedSums];
+  float scale[kMaxOrderedSums];
+  float* dst[kMaxOrderedSums];
+  int count;
+};
+// Every term of a sum of at most kSumLds terms is staged in LDS (one memory
+// round trip for all of them, overlapping the caller's own loads), then,
+// after a barrier of the caller's, one thread adds them in order.
+__device__ __forceinline__ void stage_sums(const OrderedSums& s, float (*terms)[kSumLds]) {
+#pragma unroll
+  for (int k = 0; k < kMaxOrderedSums; ++k)
+    if (k < s.count && s.n[k] <= kSumLds)
+      for (int i = threadIdx.x; i < s.n[k]; i += kOptThreads) terms[k][i] = s.src[k][long(i) * s.stride[k]];
+}
+__device__ __forceinline__ void ordered_sums(const OrderedSums& s, const float (*terms)[kSumLds]) {
+  const int k = int(threadIdx.x);
+  if (k >= s.count || k >= kMaxOrderedSums) return;
+  const float* src = s.src[k];
+  const int n = s.n[k], st = s.stride[k];
+  float t = 0.f;
+  if (n <= kSumLds) {
+    for (int i = 0; i < n; ++i) t += terms[k][i];  // in order: the same sum on every run
+  } else {
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) t += src[long(i) * st];
+  }
+  *s.dst[k] = t * s.scale[k];
+}
+
+// k_finish, and the ordered sums, their terms staged while the partials
+// are read (block_sum's barriers order the staging before the sums).
+__global__ __launch_bounds__(kOptThreads) void k_finish_sums(const float* __restrict__ partials, int nparts,
+                                                             int* __restrict__ step, float* __restrict__ out,
+                                                             int accumulate, OrderedSums sums) {
+  __shared__ float red[kOptThreads / 64];
+  __shared__ float terms[kMaxOrderedSums][kSumLds];
+  warm_kernargs<int(sizeof(OrderedSums) + 40)>();
+  stage_sums(sums, terms);
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += partials[i];
+  const float tot = block_sum<kOptThreads>(s, red);
+  if (threadIdx.x == 0) {
+    if (out) *out = accumulate ? *out + tot : tot;
+    if (step) *step = *step + 1;
+  }
+  ordered_sums(sums, terms);
+}
+
 __global__ __launch_bounds__(kOptThreads) void k_sumsq(const float* __restrict__ x, long n,
                                                        float* __restrict__ partials) {
   __shared__ float red[kOptThreads / 64];
@@ -246,11 +639,172 @@ int check_adam_args(const float* p, const float* g, const float* m_s, const floa
   return TTRL_OK;
 }
 
+inline bool inside(const float* x, long count, const float* base, long n) {
+  return x >= base && x + count <= base + n;
+}
+inline bool aligned16(const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; }
+
+// Checks sources[0 .. n) and fills their device form; blocks are laid out
+// from block 0.  With an arena (g, gn), each written range must lie inside
+// it, and ranges of different sources must not overlap.  Sources of kind
+// TTRL_GRAD_NONE are skipped.  *blocks receives the blocks they use.
+int make_sources(int n, const ttrl_grad_source* srcs, const float* g, long gn, GradSrc* out, int* count, int* blocks,
+                 const char* name) {
+  TTRL_REQUIRE(n >= 0 && n <= kMaxGradSources && (n == 0 || srcs), "%s: %d sources outside [0, %d]", name, n,
+               kMaxGradSources);
+  int c = 0, b = 0;
+  std::vector<std::pair<const float*, const float*>> spans;
+  for (int i = 0; i < n; ++i) {
+    const ttrl_grad_source& s = srcs[i];
+    if (s.kind == TTRL_GRAD_NONE) continue;
+    TTRL_REQUIRE(s.kind == TTRL_GRAD_SPLITS || s.kind == TTRL_GRAD_OUTER, "%s: source %d: unknown kind %d", name, i,
+                 s.kind);
+    TTRL_REQUIRE(s.rows > 0 && s.cols > 0 && (long(s.rows) * s.cols) % 4 == 0 && long(s.rows) * s.cols < (1L << 30),
+                 "%s: source %d: a %dx%d block (rows * cols must be a positive multiple of 4)", name, i, s.rows,
+                 s.cols);
+    TTRL_REQUIRE(s.dw && aligned16(s.dw) && (!s.db || aligned16(s.db)),
+                 "%s: source %d: gradient destinations must be 16-byte aligned", name, i);
+    const long wn = long(s.rows) * s.cols, bn = s.db ? (s.cols + 3) / 4 * 4 : 0;
+    if (g) {
+      TTRL_REQUIRE(inside(s.dw, wn, g, gn) && (!s.db || inside(s.db, bn, g, gn)),
+                   "%s: source %d: gradient outside the arena", name, i);
+    }
+    spans.emplace_back(s.dw, s.dw + wn);
+    if (s.db) spans.emplace_back(s.db, s.db + bn);
+    GradSrc d{};
+    d.kind = s.kind;
+    d.rows = s.rows;
+    d.cols = s.cols;
+    d.gw = s.dw;
+    d.gb = s.db;
+    d.w4 = g ? (s.dw - g) / 4 : 0;
+    d.b4 = g && s.db ? (s.db - g) / 4 : -1;
+    d.nw4 = int(wn / 4);
+    d.nb4 = int(bn / 4);
+    d.dc.set(s.cols);
+    if (s.kind == TTRL_GRAD_SPLITS) {
+      TTRL_REQUIRE(s.part && aligned16(s.part) && s.splits >= 1 && s.cols % 4 == 0,
+                   "%s: source %d: split partials need a 16-byte aligned buffer, splits >= 1 and cols %% 4 == 0",
+                   name, i);
+      d.part = s.part;
+      d.splits = s.splits;
+      d.sstride = (long(s.rows) + (s.db ? 1 : 0)) * s.cols;
+      d.scale = s.scale;
+      d.bias_scale = s.bias_scale;
+    } else {
+      TTRL_REQUIRE(s.u && s.v && s.batch >= 1, "%s: source %d: an outer product needs u, v and batch >= 1", name, i);
+      d.u = s.u;
+      d.v = s.v;
+      d.batch = s.batch;
+    }
+    d.block0 = b;
+    d.blocks = int(ceil_div(long(d.nw4) + d.nb4, kOptThreads));
+    b += d.blocks;
+    out[c++] = d;
+  }
+  std::sort(spans.begin(), spans.end());
+  for (size_t i = 1; i < spans.size(); ++i)
+    TTRL_REQUIRE(spans[i].first >= spans[i - 1].second, "%s: two sources write the same gradient", name);
+  *count = c;
+  *blocks = b;
+  return TTRL_OK;
+}
+
+int make_sums(int n, const ttrl_ordered_sum* sums, OrderedSums* out, const char* name) {
+  TTRL_REQUIRE(n >= 0 && n <= kMaxOrderedSums && (n == 0 || sums), "%s: %d ordered sums outside [0, %d]", name, n,
+               kMaxOrderedSums);
+  *out = OrderedSums{};
+  for (int i = 0; i < n; ++i) {
+    TTRL_REQUIRE(sums[i].src && sums[i].dst && sums[i].n >= 1 && sums[i].stride >= 1,
+                 "%s: ordered sum %d: null buffer, empty or bad stride", name, i);
+    for (int j = 0; j < i; ++j)
+      TTRL_REQUIRE(sums[j].dst != sums[i].dst, "%s: ordered sums %d and %d write the same value", name, j, i);
+    out->src[i] = sums[i].src;
+    out->n[i] = sums[i].n;
+    out->stride[i] = sums[i].stride;
+    out->scale[i] = sums[i].scale;
+    out->dst[i] = sums[i].dst;
+  }
+  out->count = n;
+  return TTRL_OK;
+}
+
 }  // namespace ttrl
 
 using namespace ttrl;
 
 extern "C" {
+
+int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* d) {
+  TTRL_REQUIRE(ctx && d, "ttrl_adam_step_sources: null argument");
+  int rc = check_adam_args(d->p, d->g, d->m_s, d->v_s, d->n, d->step, d->lr, d->beta1, d->beta2, d->eps,
+                           d->weight_decay, "ttrl_adam_step_sources");
+  if (rc) return rc;
+  AdamSrcArgs a{};
+  int srcblocks = 0;
+  rc = make_sources(d->nsources, d->sources, d->g, d->n, a.src, &a.nsrc, &srcblocks, "ttrl_adam_step_sources");
+  if (rc) return rc;
+  OrderedSums sums;
+  rc = make_sums(d->nsums, d->sums, &sums, "ttrl_adam_step_sources");
+  if (rc) return rc;
+  a.p = d->p;
+  a.g = d->g;
+  a.S = d->m_s;
+  a.V = d->v_s;
+  a.n = d->n;
+  a.step = d->step;
+  a.lr = d->lr;
+  a.b1 = d->beta1;
+  a.b2 = d->beta2;
+  a.eps = d->eps;
+  a.wd = d->weight_decay;
+  a.plain0 = srcblocks;
+  // the plain part takes what the source workgroups leave of a launch's
+  // kOptMaxBlocks, so the whole grid is resident at once
+  a.plain_blocks = std::max(1, std::min(int(grid_for(d->n, 4)), kOptMaxBlocks - srcblocks));
+  const long n4 = d->n / 4;
+  a.chunk4 = std::max(1L, (n4 + a.plain_blocks - 1) / a.plain_blocks);
+  a.nholes = 0;
+  for (int k = 0; k < a.nsrc; ++k) {
+    a.hole_lo[a.nholes] = a.src[k].w4;
+    a.hole_hi[a.nholes++] = a.src[k].w4 + a.src[k].nw4;
+    if (a.src[k].nb4 > 0) {
+      a.hole_lo[a.nholes] = a.src[k].b4;
+      a.hole_hi[a.nholes++] = a.src[k].b4 + a.src[k].nb4;
+    }
+  }
+  const int blocks = a.plain0 + a.plain_blocks;
+  long wsf = 0;
+  a.partials = ctx_workspace(ctx, &wsf);
+  TTRL_REQUIRE(wsf >= long(blocks), "ttrl_adam_step_sources: workspace too small");
+  hipStream_t st = stream_of(ctx);
+  hipLaunchKernelGGL(k_adam_src, dim3(unsigned(blocks)), dim3(kOptThreads), 0, st, a);
+  hipLaunchKernelGGL(k_finish_sums, dim3(1), dim3(kOptThreads), 0, st, a.partials, blocks, d->step, d->grad_sq,
+                     d->accumulate_grad_sq, sums);
+  return check_launch("ttrl_adam_step_sources");
+}
+
+int ttrl_grad_sources_materialize(ttrl_ctx* ctx, int n, const ttrl_grad_source* sources) {
+  TTRL_REQUIRE(ctx, "ttrl_grad_sources_materialize: null ctx");
+  SrcSet a{};
+  int blocks = 0;
+  int rc = make_sources(n, sources, nullptr, 0, a.src, &a.nsrc, &blocks, "ttrl_grad_sources_materialize");
+  if (rc) return rc;
+  if (blocks == 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_sources_write, dim3(unsigned(blocks)), dim3(kOptThreads), 0, stream_of(ctx), a);
+  return check_launch("ttrl_grad_sources_materialize");
+}
+
+int ttrl_ordered_sums(ttrl_ctx* ctx, int n, const ttrl_ordered_sum* sums) {
+  TTRL_REQUIRE(ctx, "ttrl_ordered_sums: null ctx");
+  OrderedSums s;
+  int rc = make_sums(n, sums, &s, "ttrl_ordered_sums");
+  if (rc) return rc;
+  if (n == 0) return TTRL_OK;
+  hipLaunchKernelGGL(k_finish_sums, dim3(1), dim3(kOptThreads), 0, stream_of(ctx), (const float*)nullptr, 0,
+                     (int*)nullptr, (float*)nullptr, 0, s);
+  return check_launch("ttrl_ordered_sums");
+}
 
 int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n, int* step, float lr,
                    float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq) {

@@ -59,6 +59,7 @@ struct ttrl_ctx {
   long ws_floats = 0;
   unsigned* sync = nullptr;  // zeroed counters and partials (ctx_sync_words)
   float* adam_parts = nullptr;  // ctx_adam_partials
+  float* grad_banks = nullptr;  // ctx_grad_bank
   // GEMM plans chosen by timing candidates on this device, by call signature.
   std::unordered_map<std::string, ttrl::GemmPlan> plans;
   float* tune_out = nullptr;  // output sink of candidate runs
@@ -98,6 +99,7 @@ hipStream_t stream_of(ttrl_ctx* ctx) { return ctx->stream; }
 unsigned* ctx_sync_words(ttrl_ctx* ctx) { return ctx->sync; }
 
 float* ctx_adam_partials(ttrl_ctx* ctx) { return ctx->adam_parts; }
+float* ctx_grad_bank(ttrl_ctx* ctx, int bank) { return ctx->grad_banks + long(bank) * kGradBankFloats; }
 
 float* ctx_workspace(ttrl_ctx* ctx, long* floats) {
   if (floats) *floats = ctx->ws_floats;
@@ -243,6 +245,17 @@ int ttrl_init(int device, ttrl_ctx** out) {
     return hip_error(e, "hipMalloc (Adam partial slots)");
   }
   ctx->adam_parts = static_cast<float*>(parts);
+  void* banks = nullptr;
+  e = hipMalloc(&banks, sizeof(float) * kGradBanks * kGradBankFloats);
+  if (e != hipSuccess) {
+    (void)hipFree(parts);
+    (void)hipFree(sync);
+    (void)hipFree(ws);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_error(e, "hipMalloc (gradient banks)");
+  }
+  ctx->grad_banks = static_cast<float*>(banks);
   ctx->pools.emplace_back();  // pool 0: the default pool
   ctx->pools[0].in_use = true;
   *out = ctx;
@@ -257,6 +270,7 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->sync) (void)hipFree(ctx->sync);
   if (ctx->adam_parts) (void)hipFree(ctx->adam_parts);
+  if (ctx->grad_banks) (void)hipFree(ctx->grad_banks);
   if (ctx->tune_out) (void)hipFree(ctx->tune_out);
   if (ctx->tune0) (void)hipEventDestroy(ctx->tune0);
   if (ctx->tune1) (void)hipEventDestroy(ctx->tune1);

@@ -45,25 +45,6 @@ namespace ttrl {
 
 constexpr int kMaxGroups = 4;
 
-// Division by a runtime-constant positive divisor d with a multiply-high:
-// q = (umulhi(n, m) + n) >> s, m = floor(2^32 (2^s - d) / d) + 1, s = ceil(log2 d)
-// (exact for 0 <= n < 2^31).
-struct FDiv {
-  uint32_t m = 0, s = 0;
-  int d = 1;
-  __host__ void set(int divisor) {
-    d = divisor;
-    s = 0;
-    while ((1u << s) < uint32_t(divisor)) ++s;
-    const uint64_t two32 = uint64_t(1) << 32;
-    m = uint32_t((two32 * ((uint64_t(1) << s) - uint64_t(divisor))) / uint64_t(divisor) + 1);
-  }
-  __device__ __forceinline__ int div(int n) const {
-    const uint32_t hi = __umulhi(uint32_t(n), m);
-    return int((uint64_t(hi) + uint32_t(n)) >> s);
-  }
-};
-
 // ------------------------------------------------------------- loaders ---
 //
 // Operands are read with buffer loads: a 32-bit byte offset into a buffer
@@ -689,20 +670,6 @@ __device__ __forceinline__ void mma_stage_part(f32x4 (&acc)[FM][FN], const float
   }
 }
 
-// Touches every 64-byte line of the first BYTES bytes of the kernel's
-// argument segment with independent scalar loads and waits for them once,
-// so the argument reads that follow hit the scalar cache instead of taking
-// one memory round trip per line, one after another.
-template <int BYTES>
-__device__ __forceinline__ void warm_kernargs() {
-  typedef __attribute__((address_space(4))) const uint32_t kword;
-  kword* ka = (kword*)__builtin_amdgcn_kernarg_segment_ptr();
-  uint32_t t = 0;
-#pragma unroll
-  for (int o = 0; o < BYTES / 4; o += 16) t ^= ka[o];
-  asm volatile("" ::"s"(t));
-}
-
 // Software pipeline over LDS stages: the loads of stage s+1 are issued into
 // registers before the MFMAs of stage s run, so global-memory latency is
 // paid once per workgroup rather than once per stage; both operands' loads
@@ -858,32 +825,33 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm(LA la, LB lb, EP 
 // Extents and grid of one problem of a paired launch.
 struct PairDims {
   int M, N, K, kchunk, splits, gx, gy, blocks;
-  long ws_off;  // its split-K partials start here in the workspace
 };
 
 // Two independent GEMMs of one tile shape in one launch (a layer's weight
 // and input gradients): workgroups [0, d1.blocks) run the first, the rest
 // the second, so the two fill the device together instead of one after the
-// other.  LDS is the larger of the two problems' stages.
+// other.  LDS is the larger of the two problems' stages.  Each problem's
+// split-K partials go to its own buffer (ws1, ws2).
 template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA1, class LB1, class EP1, class LA2, class LB2,
           class EP2>
 __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm_pair(LA1 la1, LB1 lb1, EP1 ep1, LA2 la2, LB2 lb2,
-                                                                    EP2 ep2, float* ws, PairDims d1, PairDims d2) {
+                                                                    EP2 ep2, float* ws1, float* ws2, PairDims d1,
+                                                                    PairDims d2) {
   using S1 = TileShared<BM, BN, TBK, LA1, LB1>;
   using S2 = TileShared<BM, BN, TBK, LA2, LB2>;
   constexpr int SIZE = S1::SIZE > S2::SIZE ? S1::SIZE : S2::SIZE;
   __shared__ __attribute__((aligned(16))) float lds[SIZE];
   warm_kernargs<int(sizeof(LA1) + sizeof(LB1) + sizeof(EP1) + sizeof(LA2) + sizeof(LB2) + sizeof(EP2) +
-                    sizeof(float*) + 2 * sizeof(PairDims))>();
+                    2 * sizeof(float*) + 2 * sizeof(PairDims))>();
   int b = blockIdx.x;
   if (b < d1.blocks) {
     const int bx = b % d1.gx, byz = b / d1.gx;
-    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la1, lb1, ep1, ws + d1.ws_off, d1.M, d1.N, d1.K, d1.kchunk, d1.splits, bx,
+    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la1, lb1, ep1, ws1, d1.M, d1.N, d1.K, d1.kchunk, d1.splits, bx,
                                           byz % d1.gy, byz / d1.gy, lds, lds + S1::A);
   } else {
     b -= d1.blocks;
     const int bx = b % d2.gx, byz = b / d2.gx;
-    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la2, lb2, ep2, ws + d2.ws_off, d2.M, d2.N, d2.K, d2.kchunk, d2.splits, bx,
+    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la2, lb2, ep2, ws2, d2.M, d2.N, d2.K, d2.kchunk, d2.splits, bx,
                                           byz % d2.gy, byz / d2.gy, lds, lds + S2::A);
   }
 }
@@ -1170,16 +1138,18 @@ inline int run_gemm(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int
 // at the start of the workspace as [groups][splits][M][N] floats, to be
 // summed in split order from 0.f (as k_splitk_reduce does) and passed
 // through the epilogue by that consumer; with one split the epilogue runs in
-// the GEMM.  *plan receives the plan that ran.
+// the GEMM.  *plan receives the plan that ran.  `part` (room for
+// part_floats) replaces the workspace as the partials' home when given.
 template <unsigned ALLOWED, class LA, class LB, class EP>
 inline int run_gemm_deferred(ttrl_ctx* ctx, const LA& la, const LB& lb, const EP& ep, int M, int N, int K,
-                             int groups, const char* name, GemmPlan* plan) {
+                             int groups, const char* name, GemmPlan* plan, float* part = nullptr,
+                             long part_floats = 0) {
   static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
   if (M <= 0 || N <= 0 || groups <= 0) return set_error(TTRL_EINVAL, "%s: empty GEMM", name);
   if (groups > kMaxGroups) return set_error(TTRL_EINVAL, "%s: at most %d groups", name, kMaxGroups);
   if (long(groups) * M * N >= (1L << 31)) return set_error(TTRL_EINVAL, "%s: output too large", name);
-  long wsf = 0;
-  float* ws = ctx_workspace(ctx, &wsf);
+  long wsf = part_floats;
+  float* ws = part ? part : ctx_workspace(ctx, &wsf);
   hipStream_t st = stream_of(ctx);
   char keybuf[96];
   snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%ld", M, N, K, groups, wsf);
@@ -1207,19 +1177,23 @@ struct GemmDims {
   int M, N, K, groups;
 };
 
+// defer1 not null: the first problem's split-K partials go there and are
+// left unreduced (a later launch sums them); otherwise both problems'
+// partials share `ws` and each is reduced after the pair.
 template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA1, class LB1, class EP1, class LA2, class LB2,
           class EP2>
 inline void launch_pair_cfg(const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1, const GemmPlan& p1,
                             const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const GemmPlan& p2,
-                            float* ws, hipStream_t st) {
+                            float* ws, hipStream_t st, float* defer1) {
   const int gx1 = int(ceil_div(q1.M, BM)), gy1 = int(ceil_div(q1.N, BN));
   const int gx2 = int(ceil_div(q2.M, BM)), gy2 = int(ceil_div(q2.N, BN));
-  const long part1 = p1.splits > 1 ? (long(p1.splits) * q1.groups * q1.M * q1.N + 63) / 64 * 64 : 0;
-  const PairDims d1{q1.M, q1.N, q1.K, p1.kchunk, p1.splits, gx1, gy1, gx1 * gy1 * q1.groups * p1.splits, 0};
-  const PairDims d2{q2.M, q2.N, q2.K, p2.kchunk, p2.splits, gx2, gy2, gx2 * gy2 * q2.groups * p2.splits, part1};
+  const long part1 = p1.splits > 1 && !defer1 ? (long(p1.splits) * q1.groups * q1.M * q1.N + 63) / 64 * 64 : 0;
+  const PairDims d1{q1.M, q1.N, q1.K, p1.kchunk, p1.splits, gx1, gy1, gx1 * gy1 * q1.groups * p1.splits};
+  const PairDims d2{q2.M, q2.N, q2.K, p2.kchunk, p2.splits, gx2, gy2, gx2 * gy2 * q2.groups * p2.splits};
+  float* ws1 = defer1 ? defer1 : ws;
   hipLaunchKernelGGL((k_gemm_pair<BM, BN, WGM, WGN, WGK, TBK, LA1, LB1, EP1, LA2, LB2, EP2>),
                      dim3(unsigned(d1.blocks + d2.blocks)), dim3(64 * WGM * WGN * WGK), 0, st, la1, lb1, ep1, la2, lb2,
-                     ep2, ws, d1, d2);
+                     ep2, ws1, ws + part1, d1, d2);
   auto reduce = [&](const auto& ep, const GemmDims& q, const GemmPlan& p, float* w) {
     if (p.splits <= 1) return;
     unsigned blocks = unsigned(long(q.M) * q.N / 256 + 1);
@@ -1230,18 +1204,18 @@ inline void launch_pair_cfg(const LA1& la1, const LB1& lb1, const EP1& ep1, cons
     hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(blocks, unsigned(q.groups)), dim3(256), 0, st, w, ep, q.M, q.N,
                        p.splits, dn);
   };
-  reduce(ep1, q1, p1, ws);
+  if (!defer1) reduce(ep1, q1, p1, ws);
   reduce(ep2, q2, p2, ws + part1);
 }
 
 template <unsigned ALLOWED, class LA1, class LB1, class EP1, class LA2, class LB2, class EP2>
 inline void launch_pair(const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1, const GemmPlan& p1,
                         const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const GemmPlan& p2,
-                        float* ws, hipStream_t st) {
+                        float* ws, hipStream_t st, float* defer1 = nullptr) {
   dispatch_cfg<ALLOWED>(p1.cfg, [&](auto c) {
     using C = decltype(c);
     launch_pair_cfg<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws,
-                                                                  st);
+                                                                  st, defer1);
   });
 }
 
@@ -1250,10 +1224,14 @@ inline void launch_pair(const LA1& la1, const LB1& lb1, const EP1& ep1, const Ge
 // allowed tile shape, the cost model's split of each problem, and keeps the
 // fastest pair for the context (as run_gemm does for one GEMM).  The two
 // problems' split-K partials share the workspace below `ws_reserved`.
+// With `defer1` (room for defer1_floats), the first problem's partials go
+// there instead and are not reduced: a later consumer sums them, and
+// *plan1 receives the first problem's plan.
 template <unsigned ALLOWED, class LA1, class LB1, class EP1, class LA2, class LB2, class EP2>
 inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1,
                          const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const char* name,
-                         long ws_reserved = 0) {
+                         long ws_reserved = 0, float* defer1 = nullptr, long defer1_floats = 0,
+                         GemmPlan* plan1 = nullptr) {
   static_assert((ALLOWED & kCfgAll) != 0, "no tile shape allowed");
   for (const GemmDims* q : {&q1, &q2}) {
     if (q->M <= 0 || q->N <= 0 || q->groups <= 0 || q->groups > kMaxGroups || long(q->groups) * q->M * q->N >= (1L << 31))
@@ -1262,22 +1240,31 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
   long wsf = 0;
   float* ws = ctx_workspace(ctx, &wsf);
   const long half = (wsf - ws_reserved) / 2 / 64 * 64;
+  // each problem's room for partials: the workspace is shared unless the
+  // first problem's go to their own buffer
+  const long room1 = defer1 ? defer1_floats : half;
+  const long room2 = defer1 ? (wsf - ws_reserved) / 64 * 64 : half;
   hipStream_t st = stream_of(ctx);
-  char keybuf[160];
-  snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%d|%d|%d|%d|%ld", q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K,
-           q2.groups, half);
+  char keybuf[192];
+  if (defer1)
+    snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%d|%d|%d|%d|%ld|D%ld", q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N,
+             q2.K, q2.groups, room2, room1);
+  else
+    snprintf(keybuf, sizeof(keybuf), "|%d|%d|%d|%d|%d|%d|%d|%d|%ld", q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K,
+             q2.groups, half);
   const std::string key = std::string(__PRETTY_FUNCTION__) + keybuf;
   GemmPlan p1, p2;
-  if (gemm_forced(ALLOWED, q1.M, q1.N, q1.K, q1.groups, half, &p1) &&
-      gemm_forced(ALLOWED, q2.M, q2.N, q2.K, q2.groups, half, &p2)) {
-    launch_pair<ALLOWED>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws, st);
+  if (gemm_forced(ALLOWED, q1.M, q1.N, q1.K, q1.groups, room1, &p1) &&
+      gemm_forced(ALLOWED, q2.M, q2.N, q2.K, q2.groups, room2, &p2)) {
+    launch_pair<ALLOWED>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws, st, defer1);
+    if (plan1) *plan1 = p1;
     return check_launch(name);
   }
   const std::string key2 = key + "#2";
   const GemmPlan* h1 = ctx_plan_find(ctx, key);
   const GemmPlan* h2 = ctx_plan_find(ctx, key2);
-  if (h1 && h2 && h1->cfg == h2->cfg && plan_valid(*h1, q1.M, q1.N, q1.K, q1.groups, half, ALLOWED) &&
-      plan_valid(*h2, q2.M, q2.N, q2.K, q2.groups, half, ALLOWED)) {
+  if (h1 && h2 && h1->cfg == h2->cfg && plan_valid(*h1, q1.M, q1.N, q1.K, q1.groups, room1, ALLOWED) &&
+      plan_valid(*h2, q2.M, q2.N, q2.K, q2.groups, room2, ALLOWED)) {
     p1 = *h1;
     p2 = *h2;
   } else {
@@ -1287,8 +1274,8 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
     std::vector<std::pair<GemmPlan, GemmPlan>> cands;
     for (int c = 0; c < kNumCfg; ++c) {
       if (!(ALLOWED & cfg_bit(c))) continue;
-      const GemmPlan b1 = plan_gemm(q1.M, q1.N, q1.K, q1.groups, half, cfg_bit(c));
-      const GemmPlan b2 = plan_gemm(q2.M, q2.N, q2.K, q2.groups, half, cfg_bit(c));
+      const GemmPlan b1 = plan_gemm(q1.M, q1.N, q1.K, q1.groups, room1, cfg_bit(c));
+      const GemmPlan b2 = plan_gemm(q2.M, q2.N, q2.K, q2.groups, room2, cfg_bit(c));
       auto add = [&](const GemmPlan& a, const GemmPlan& b) {
         for (const auto& e : cands)
           if (e.first.cfg == a.cfg && e.first.splits == a.splits && e.second.splits == b.splits) return;
@@ -1297,8 +1284,8 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
       add(b1, b2);
       for (int sp : {2, 4, 8, 16}) {
         GemmPlan v;
-        if (plan_with_splits(c, q1.M, q1.N, q1.K, q1.groups, half, sp, &v)) add(v, b2);
-        if (plan_with_splits(c, q2.M, q2.N, q2.K, q2.groups, half, sp, &v)) add(b1, v);
+        if (plan_with_splits(c, q1.M, q1.N, q1.K, q1.groups, room1, sp, &v)) add(v, b2);
+        if (plan_with_splits(c, q2.M, q2.N, q2.K, q2.groups, room2, sp, &v)) add(b1, v);
       }
     }
     p1 = cands.front().first;
@@ -1313,15 +1300,18 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
       const EP2 t2 = ep2.tune_copy(sink + span1);
       float best_ms = 1e30f;
       for (const auto& c : cands) {
-        launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st);  // warm
-        const float ms = time_best_of(
-            e0, e1, st, [&] { launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st); });
+        launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st, defer1);  // warm
+        const float ms = time_best_of(e0, e1, st, [&] {
+          launch_pair<ALLOWED>(la1, lb1, t1, q1, c.first, la2, lb2, t2, q2, c.second, ws, st, defer1);
+        });
         if (ms < 0.f) break;
         if (gemm_tuning_log())
           fprintf(stderr, "[ttrl gemm tune pair] %dx%dx%d(G%d) + %dx%dx%d(G%d)  %dx%d tbk%d splits=%d,%d  %.2f us\n",
                   q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K, q2.groups, c.first.bm, c.first.bn, c.first.tbk,
                   c.first.splits, c.second.splits, ms * 1e3f / 3.f);
-        const float cost = ms + 3.f * kReduceLaunchMs * float(int(c.first.splits > 1) + int(c.second.splits > 1));
+        // a deferred first problem has no reduce launch to charge
+        const float cost =
+            ms + 3.f * kReduceLaunchMs * float(int(c.first.splits > 1 && !defer1) + int(c.second.splits > 1));
         if (cost < best_ms) {
           best_ms = cost;
           p1 = c.first;
@@ -1333,7 +1323,8 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
     ctx_plan_store(ctx, key, p1);
     ctx_plan_store(ctx, key2, p2);
   }
-  launch_pair<ALLOWED>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws, st);
+  launch_pair<ALLOWED>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws, st, defer1);
+  if (plan1) *plan1 = p1;
   return check_launch(name);
 }
 

@@ -81,7 +81,39 @@ class DqnTailDesc(C.Structure):
         ("discounts", C.c_void_p), ("is_weights", C.c_void_p), ("delta", C.c_float),
         ("loss", C.c_void_p), ("mean_q", C.c_void_p), ("td_abs", C.c_void_p), ("dq", C.c_void_p),
         ("next_actions", C.c_void_p), ("td_target", C.c_void_p), ("dh", C.c_void_p), ("dW2", C.c_void_p),
-        ("db2", C.c_void_p), ("beta_w", C.c_float),
+        ("db2", C.c_void_p), ("beta_w", C.c_float), ("loss_terms", C.c_void_p),
+    ]
+
+
+GRAD_NONE, GRAD_SPLITS, GRAD_OUTER = 0, 1, 2
+
+
+class GradSource(C.Structure):
+    """Mirror of ttrl_grad_source."""
+
+    _fields_ = [
+        ("kind", C.c_int), ("rows", C.c_int), ("cols", C.c_int), ("dw", C.c_void_p), ("db", C.c_void_p),
+        ("part", C.c_void_p), ("splits", C.c_int), ("scale", C.c_float), ("bias_scale", C.c_float),
+        ("u", C.c_void_p), ("v", C.c_void_p), ("batch", C.c_int),
+    ]
+
+
+class OrderedSum(C.Structure):
+    """Mirror of ttrl_ordered_sum."""
+
+    _fields_ = [("src", C.c_void_p), ("n", C.c_int), ("stride", C.c_int), ("scale", C.c_float),
+                ("dst", C.c_void_p)]
+
+
+class AdamSourcesDesc(C.Structure):
+    """Mirror of ttrl_adam_sources_desc."""
+
+    _fields_ = [
+        ("p", C.c_void_p), ("g", C.c_void_p), ("m_s", C.c_void_p), ("v_s", C.c_void_p), ("n", C.c_long),
+        ("step", C.c_void_p), ("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+        ("weight_decay", C.c_float), ("grad_sq", C.c_void_p), ("accumulate_grad_sq", C.c_int),
+        ("nsources", C.c_int), ("sources", C.POINTER(GradSource)), ("nsums", C.c_int),
+        ("sums", C.POINTER(OrderedSum)),
     ]
 
 
@@ -155,6 +187,10 @@ SIGNATURES = {
     "ttrl_conv2d_backward_weight": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, F], I),
     "ttrl_conv2d_backward_input": ([P, C.POINTER(ConvGeom), P, P, P, P, P, F, F], I),
     "ttrl_conv2d_backward": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, P, F, P, P, F], I),
+    "ttrl_conv2d_backward_deferred": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, P, P, P, F, I,
+                                       C.POINTER(GradSource)], I),
+    "ttrl_conv2d_backward_weight_deferred": ([P, C.POINTER(ConvGeom), P, F, P, P, P, P, I, C.POINTER(GradSource)], I),
+    "ttrl_grad_sources_materialize": ([P, I, C.POINTER(GradSource)], I),
     "ttrl_dqn_loss": ([P, I, I, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_dqn_tail": ([P, C.POINTER(DqnTailDesc)], I),
@@ -179,6 +215,8 @@ SIGNATURES = {
     "ttrl_adam_step_deferred": ([P, P, P, P, P, L, P, F, F, F, F, F, I], I),
     "ttrl_adam_multi": ([P, I, C.POINTER(AdamRange), P, P, L, F], I),
     "ttrl_adam_finish_slots": ([P, I, C.POINTER(AdamFinish)], I),
+    "ttrl_adam_step_sources": ([P, C.POINTER(AdamSourcesDesc)], I),
+    "ttrl_ordered_sums": ([P, I, C.POINTER(OrderedSum)], I),
     "ttrl_sum_squares": ([P, P, L, P, I], I),
     "ttrl_polyak": ([P, P, P, L, F], I),
     "ttrl_gae": ([P, I, I, P, P, P, P, P, C.c_double, C.c_double, P, P], I),

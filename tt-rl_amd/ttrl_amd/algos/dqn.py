@@ -197,14 +197,16 @@ def q_forward_multi(nets, inputs, tape_group: int | None = 0, *, skip_last: int 
 
 def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_n: int = 0, double: bool = True,
                 huber_delta: float = 1.0, prioritized: bool = False, grad_sq: bool = True,
-                metrics_out: dict | None = None) -> dict:
+                metrics_out: dict | None = None, defer: bool = False) -> dict:
     """One DQN update body: Huber loss against the n-step double-Q target,
     backward, metrics.  Reads only `inputs`; no host reads (capturable).
 
     The online forward on s (with tape), the online forward on s' and the
     target forward on s' (both constants of the step) run as one grouped
     launch per layer.  `metrics_out` may name the device arrays `loss`,
-    `mean_q` and `td_abs` are written to."""
+    `mean_q` and `td_abs` are written to.  defer=True leaves the Q head's
+    gradients, the loss and mean Q to the optimizer step that follows
+    (engine.pending); the caller's step must run before they are read."""
     (leaf,) = tuple(leaves)
     obs = inputs[leaf_key("obs", leaf)]
     next_obs = inputs[leaf_key("next_obs", leaf)]
@@ -218,7 +220,7 @@ def update_loss(online, target, inputs: dict, *, leaves, num_actions: int, mask_
         loss, extra, hs, qs = dqn_tail_td_loss(features, [t[0] for t in tails], [t[2] for t in tails],
                                                inputs["actions_onehot"], inputs["rewards"], inputs["dones"],
                                                inputs["discounts"], inputs["is_weights"] if prioritized else None,
-                                               huber_delta, out=metrics_out)
+                                               huber_delta, out=metrics_out, defer=defer)
         if layers_mod.RECORD is not None:  # the first layer's outputs, then the Q values, of every group
             layers_mod.RECORD.append(list(hs))
             layers_mod.RECORD.append(list(qs))
@@ -296,7 +298,8 @@ class DQNLearner:
     acting step either side of it (ttrl/algos/dqn/agent.py:89-119)."""
 
     def __init__(self, obs_spec, action_spec, device, *, cfg: DQNConfig = DQNConfig(), seed: int | None = None,
-                 online_state: dict | None = None, target_state: dict | None = None, n_envs: int = 1):
+                 online_state: dict | None = None, target_state: dict | None = None, n_envs: int = 1,
+                 defer_grads: bool = True):
         if action_spec.kind != "discrete":
             raise ValueError(f"DQN supports discrete actions only, got {action_spec.kind!r}")
         self.obs_spec = obs_spec
@@ -314,6 +317,14 @@ class DQNLearner:
         if target_state is not None:
             self.target.load_state_dict(target_state)
         self.optimizer = Adam(list(self.online.parameters()), lr=cfg.lr, eps=cfg.adam_eps)
+        # The update's weight-gradient reductions (convolution split-K sums,
+        # the Q head's outer product) and batch means are formed by the Adam
+        # launch that consumes them, one gradient bank per convolution.
+        self.defer_grads = bool(defer_grads)
+        if self.defer_grads:
+            convs = [m for m in getattr(getattr(self.online, "encoder", None), "layers", []) if isinstance(m, Conv2d)]
+            for bank, conv in enumerate(convs[:4]):
+                conv.defer_bank = bank
         # Every metric of an update in one device block, read back with one
         # copy: [loss, mean_q, grad_sq, -, td_abs[B]].
         B = cfg.batch_size
@@ -393,7 +404,7 @@ class DQNLearner:
         metrics = update_loss(self.online, self.target, inputs, leaves=(self.obs_spec.name,),
                               num_actions=self.num_actions, double=self.cfg.double,
                               huber_delta=self.cfg.huber_delta, prioritized=self.cfg.prioritized, grad_sq=False,
-                              metrics_out=self._metrics_out)
+                              metrics_out=self._metrics_out, defer=self.defer_grads)
         # Adam reduces sum(g^2) over the same gradients in its own launch.
         metrics["grad_sq"] = Tensor(self.optimizer.grad_sq)
         return metrics

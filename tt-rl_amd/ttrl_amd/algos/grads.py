@@ -6,6 +6,7 @@ import numpy as np
 
 from ttrl_amd.engine.autograd import Tensor
 from ttrl_amd.engine.ops import _kernels as K
+from ttrl_amd.engine.pending import settle
 from ttrl_amd.engine.tensor import arena_of, zeros
 
 __all__ = ["clip_grad_norm", "grad_norm", "grad_sq_device", "param_snapshot"]
@@ -13,6 +14,8 @@ __all__ = ["clip_grad_norm", "grad_norm", "grad_sq_device", "param_snapshot"]
 
 def grad_norm(params) -> float:
     """Global L2 norm (float64 on the host) over parameters holding a gradient."""
+    params = list(params)
+    settle(params)
     total = 0.0
     for p in params:
         if p.grad is None:
@@ -43,6 +46,7 @@ def grad_sq_device(params):
     Over a whole arena whose gradient slots hold every gradient this is one
     reduction of the flat gradient buffer."""
     params = list(params)
+    settle(params)
     have = [p for p in params if p.grad is not None]
     if not have:
         return None

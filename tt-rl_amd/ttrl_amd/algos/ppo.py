@@ -206,6 +206,8 @@ def clip_grad_norm(params, max_norm: float) -> float:
         raise ValueError("clip_grad_norm: the parameters must be exactly one ParamArena's tensors, in order")
     if any(p.grad is None for p in params):
         raise RuntimeError("clip_grad_norm: every parameter of the arena needs this step's gradient")
+    from ttrl_amd.engine.pending import settle
+    settle(params)
     norm = clip_grad_norm_device(arena.grad, max_norm)
     return float(norm.numpy()[0])
 

@@ -72,7 +72,7 @@ class Tensor:
     """A node in the autograd graph, backed by a `DeviceArray`."""
 
     __slots__ = ("data", "requires_grad", "grad", "_backward", "_parents", "_op", "_backward_done",
-                 "_grad_slot", "_grad_owned", "_arena", "_grad_masked", "__weakref__")
+                 "_grad_slot", "_grad_owned", "_arena", "_grad_masked", "_pending", "__weakref__")
 
     def __init__(self, data, requires_grad: bool = False, _parents=(), _op: str = ""):
         self.data = data
@@ -90,6 +90,9 @@ class Tensor:
         # epilogue, so this node's backward must not apply it again (it would
         # be harmless, but it costs a pass).
         self._grad_masked = False
+        # A gradient source (engine.pending) that will write `grad`: set
+        # while an earlier launch left this gradient unreduced.
+        self._pending = None
 
     # -- construction ------------------------------------------------------
 
@@ -130,6 +133,9 @@ class Tensor:
         from ttrl_amd.engine.ops import _kernels as K
 
         self._grad_masked = masked and (self.grad is None or self._grad_masked)
+        if self._pending is not None:
+            from ttrl_amd.engine.pending import settle
+            settle([self])
         if grad.shape != self.shape:
             grad = grad.reshape(self.shape)
         if self.grad is None:
@@ -154,6 +160,9 @@ class Tensor:
         beta is 0.0 for the first contribution (overwrite) and 1.0 after
         (accumulate).  The buffer is exclusively this tensor's.
         """
+        if self._pending is not None:
+            from ttrl_amd.engine.pending import settle
+            settle([self])
         if self.grad is None:
             buf = self._grad_slot if self._grad_slot is not None else DeviceArray(self.device, self.shape)
             self.grad = buf
@@ -172,6 +181,10 @@ class Tensor:
         self._grad_masked = masked and (beta == 0.0 or self._grad_masked)
 
     def zero_grad(self):
+        if self._pending is not None:
+            # a source writes all of its gradients together: zeroing one of
+            # them drops it as a whole
+            self._pending.release()
         self.grad = None
         self._grad_owned = False
         self._grad_masked = False

@@ -25,6 +25,7 @@ from ttrl_amd import _lib
 from ttrl_amd.engine.autograd import Tensor, is_grad_enabled, relu_mask
 from ttrl_amd.engine.nn import Module
 from ttrl_amd.engine.ops.fused import grad_targets
+from ttrl_amd.engine.pending import PendingGrad
 from ttrl_amd.engine.tensor import DeviceArray
 
 __all__ = ["Conv2d", "ConvGeometry", "ConvDoesNotFit", "conv_out_size"]
@@ -120,6 +121,10 @@ class Conv2d(Module):
         self.input_scale = float(input_scale)
         self.needs_input_grad = bool(needs_input_grad)
         self.input_layout = input_layout
+        # Gradient bank (0-3) of the device context: when set, a backward
+        # that writes the weight gradient fresh leaves its split-K sum to the
+        # optimizer step (engine.pending).
+        self.defer_bank = None
         if weight is None:
             bound = 1.0 / math.sqrt(in_channels * kernel * kernel)
             weight = np.random.uniform(-bound, bound, (out_channels, in_channels, kernel, kernel)).astype(np.float32)
@@ -262,6 +267,7 @@ class Conv2d(Module):
         x_data, w_data = x.data, weight.data
         scale = self.input_scale
         layer_has_dx = self.needs_input_grad
+        bank = self.defer_bank
 
         def _backward(grad):
             if x.requires_grad and not layer_has_dx:
@@ -273,6 +279,21 @@ class Conv2d(Module):
                 )
             mask = y.vp if relu and not out._grad_masked else None
             (dw, db), beta_w = grad_targets(weight, bias)
+            if dw is not None and bank is not None and beta_w == 0.0:
+                src = _lib.GradSource()
+                if x.requires_grad:
+                    (dx,), beta_x = grad_targets(x)
+                    xmask = relu_mask(x)
+                    dev.call("ttrl_conv2d_backward_deferred", C.byref(cg), x_data.vp, C.c_float(scale), grad.vp, mask,
+                             w_data.vp, dw.vp, None if db is None else db.vp, dx.vp,
+                             None if xmask is None else xmask.vp, C.c_float(beta_x), int(bank), C.byref(src))
+                    x._note_write(beta_x, xmask is not None)
+                else:
+                    dev.call("ttrl_conv2d_backward_weight_deferred", C.byref(cg), x_data.vp, C.c_float(scale),
+                             grad.vp, mask, dw.vp, None if db is None else db.vp, int(bank), C.byref(src))
+                if src.kind != _lib.GRAD_NONE:
+                    PendingGrad(src, (weight, bias if db is not None else None))
+                return
             if dw is not None and x.requires_grad:
                 # both gradients in one call: the two GEMMs share a launch
                 (dx,), beta_x = grad_targets(x)

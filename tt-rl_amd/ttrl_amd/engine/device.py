@@ -51,6 +51,8 @@ class Device:
         self._lock = threading.RLock()
         self.closed = False
         self._pool_stack = [0]
+        # ordered sums queued for the next optimizer step (engine.pending)
+        self.pending_sums: list = []
         plans = os.environ.get("TTRL_PLANS", "")
         if plans.lower() != "none":
             path = Path(plans) if plans else PLAN_FILE

@@ -16,6 +16,7 @@ import numpy as np
 
 from ttrl_amd import _lib
 from ttrl_amd.engine.autograd import Tensor, _detached, _needs, relu_mask
+from ttrl_amd.engine.pending import PendingGrad, add_sums
 from ttrl_amd.engine.tensor import DeviceArray
 
 __all__ = ["linear", "linear_node", "dqn_td_loss", "dqn_head_td_loss", "dqn_tail_td_loss", "grad_targets"]
@@ -226,7 +227,8 @@ def dqn_head_td_loss(features, heads, actions_onehot: Tensor, rewards: Tensor, d
 
 
 def dqn_tail_td_loss(features, fc1s, fc2s, actions_onehot: Tensor, rewards: Tensor, dones: Tensor,
-                     discounts: Tensor, is_weights: Tensor | None, delta: float, out: dict | None = None):
+                     discounts: Tensor, is_weights: Tensor | None, delta: float, out: dict | None = None,
+                     defer: bool = False):
     """A Q network's last two layers (Linear -> ReLU -> Linear) over 2 or 3
     feature sets, the DQN loss and the second layer's backward, as one GEMM
     and one kernel (ttrl_dqn_tail): features[0] = online(s) (taped),
@@ -238,7 +240,14 @@ def dqn_tail_td_loss(features, fc1s, fc2s, actions_onehot: Tensor, rewards: Tens
     weight and bias gradients are produced with the loss (they depend on the
     loss alone), so they are written into those parameters' gradients here;
     the loss node's backward hands the first layer's ReLU node its already
-    gated gradient.  The loss must be the root of the backward pass."""
+    gated gradient.  The loss must be the root of the backward pass.
+
+    defer=True leaves to the update's optimizer step what needs the whole
+    batch (engine.pending): the second layer's gradients become an
+    outer-product gradient source over h[0] and dq, and the loss and mean Q
+    ordered sums of the per-sample terms, so the kernel has no
+    cross-workgroup phase.  An optimizer step (or pending.settle and
+    settle_sums) must follow before they are read."""
     G = len(features)
     if G not in (2, 3) or len(fc1s) != G or len(fc2s) != G:
         raise ValueError(f"dqn_tail_td_loss: 2 or 3 feature sets and layer pairs, got {G}")
@@ -284,7 +293,20 @@ def dqn_tail_td_loss(features, fc1s, fc2s, actions_onehot: Tensor, rewards: Tens
     d.loss, d.mean_q, d.td_abs, d.dq = loss.ptr, mean_q.ptr, td_abs.ptr, dq.ptr
     d.next_actions, d.td_target = next_act.ptr, td_target.ptr
     d.dh, d.dW2, d.db2, d.beta_w = dh.ptr, dw2.ptr, _p(db2), beta_w
+    deferred = defer and beta_w == 0.0
+    if deferred:
+        terms = DeviceArray(dev, (B, 2))
+        d.dW2, d.db2, d.loss_terms = None, None, terms.ptr
     dev.call("ttrl_dqn_tail", C.byref(d))
+    if deferred:
+        src = _lib.GradSource(kind=_lib.GRAD_OUTER, rows=F, cols=A, dw=dw2.ptr, db=_p(db2), u=hs[0].ptr, v=dq.ptr,
+                              batch=B)
+        PendingGrad(src, (head.weight, head.bias if db2 is not None else None), keep=(hs[0], dq))
+        inv_b = float(np.float32(1.0) / np.float32(B))
+        sums = [_lib.OrderedSum(terms.ptr, B, 2, inv_b, loss.ptr)]
+        if mean_q is not None:
+            sums.append(_lib.OrderedSum(terms.ptr + 4, B, 2, inv_b, mean_q.ptr))
+        add_sums(dev, sums, keep=(terms,))
     h0 = linear_node(features[0], w1[0], fc1s[0].bias, hs[0], relu=True)
     metrics = {"mean_q": Tensor(mean_q), "td_abs": Tensor(td_abs), "td_target": Tensor(td_target),
                "next_actions": Tensor(next_act)}

@@ -8,6 +8,9 @@ One kernel updates a whole parameter arena (every tensor of a network built
 inside one `ParamArena`), reading the update count from a device counter so
 that a captured graph containing the step replays correctly for every t.
 The same launch reduces sum(g^2) into `grad_sq` (ttrl/algos/grads.py:46-60).
+Gradients an earlier launch left pending (engine.pending: split-K partials,
+outer products) are formed by the arena step itself as it reads them, and
+its finishing launch forms the ordered sums queued on the device.
 
 Several optimizers stepped in one update (SAC's critic, actor and
 temperature) can defer their finishes: `step_deferred` or one `adam_multi`
@@ -23,6 +26,7 @@ import math
 import numpy as np
 
 from ttrl_amd import _lib
+from ttrl_amd.engine.pending import MAX_SOURCES, MAX_SUMS, settle, settle_sums, take_sources, take_sums
 from ttrl_amd.engine.tensor import DeviceArray, MASTER_DTYPE, arena_of, zeros
 
 __all__ = ["Adam", "Optimizer", "adam_fused_scalars", "adam_multi", "finish_steps"]
@@ -43,8 +47,13 @@ class Optimizer:
         self.params = list(params)
 
     def zero_grad(self) -> None:
+        """Drops the gradients, and the work an abandoned update left
+        pending: its gradient sources and the device's queued ordered sums
+        (an update queues them and its own step consumes them)."""
         for p in self.params:
             p.zero_grad()
+        if self.params:
+            take_sums(self.params[0].device)
 
 
 class Adam(Optimizer):
@@ -118,12 +127,18 @@ class Adam(Optimizer):
         if self.arena is not None and all(have) and counts_in_sync:
             for p in self.params:
                 if p.grad is not p._grad_slot:
+                    settle([p])
                     p._grad_slot.copy_from(p.grad)
                     p.grad = p._grad_slot
                     p._grad_owned = True
             a = self.arena
-            dev.call("ttrl_adam_step", a.data.vp, a.grad.vp, self._m_flat.vp, self._v_flat.vp,
-                     C.c_long(a.numel), self._counter(len(self.params)), *args, self.grad_sq.vp, 0)
+            sources = take_sources(self.params)
+            sums = take_sums(dev)
+            if sources or sums:
+                self._step_sources(sources, sums)
+            else:
+                dev.call("ttrl_adam_step", a.data.vp, a.grad.vp, self._m_flat.vp, self._v_flat.vp,
+                         C.c_long(a.numel), self._counter(len(self.params)), *args, self.grad_sq.vp, 0)
             if not capturing:
                 self._arena_t += 1
                 self.steps = [s + 1 for s in self.steps]
@@ -133,6 +148,8 @@ class Adam(Optimizer):
                 "Adam.step inside a captured graph needs every parameter of one arena to hold a "
                 "gradient; step this optimizer outside the capture instead."
             )
+        settle(self.params)
+        settle_sums(dev)
         self._counters.upload(np.asarray(self.steps + [self._arena_t], np.int32))
         first = True
         for i, p in enumerate(self.params):
@@ -145,6 +162,27 @@ class Adam(Optimizer):
             self._step_one(i, p, g, args, accumulate=not first)
             first = False
             self.steps[i] += 1
+
+    def _step_sources(self, sources, sums) -> None:
+        """The arena step forming pending gradient sources as it reads the
+        gradients, its finishing launch also forming the queued ordered
+        sums (ttrl_adam_step_sources)."""
+        if len(sources) > MAX_SOURCES:
+            settle([t for p in sources[MAX_SOURCES:] for t in p.tensors])
+            sources = sources[:MAX_SOURCES]
+        if len(sums) > MAX_SUMS:
+            self.device.pending_sums.extend(sums[MAX_SUMS:])
+            settle_sums(self.device)
+            sums = sums[:MAX_SUMS]
+        a = self.arena
+        srcs = (_lib.GradSource * max(1, len(sources)))(*[p.source for p in sources])
+        osums = (_lib.OrderedSum * max(1, len(sums)))(*[s for s, _ in sums])
+        d = _lib.AdamSourcesDesc(a.data.ptr, a.grad.ptr, self._m_flat.ptr, self._v_flat.ptr, a.numel,
+                                 self._counter(len(self.params)).value, self.lr, self.b1, self.b2, self.eps,
+                                 self.weight_decay, self.grad_sq.ptr, 0, len(sources), srcs, len(sums), osums)
+        self.device.call("ttrl_adam_step_sources", C.byref(d))
+        for p in sources:
+            p.release()
 
     # -- deferred steps ------------------------------------------------------
 
@@ -161,6 +199,7 @@ class Adam(Optimizer):
             raise RuntimeError(f"Adam.{who}: parameters {missing} hold no gradient for this step")
         if any(st != self._arena_t for st in self.steps):
             raise RuntimeError(f"Adam.{who}: the parameters' update counts differ; use step()")
+        settle(self.params)
         for p in self.params:
             if p.grad is not p._grad_slot:
                 p._grad_slot.copy_from(p.grad)
@@ -203,6 +242,8 @@ class Adam(Optimizer):
         for p in self.params:
             if p.grad is None:
                 raise RuntimeError("Adam.arena_grads: every parameter needs this step's gradient")
+        settle(self.params)
+        for p in self.params:
             if p.grad is not p._grad_slot:
                 p._grad_slot.copy_from(p.grad)
                 p.grad = p._grad_slot

@@ -32,9 +32,9 @@ def tune_all(dev) -> None:
 
     image = ObsSpec.image((4, 84, 84))
     for batch in (32,):
-        for prioritized in (True, False):
+        for prioritized, defer in ((True, True), (False, True), (True, False)):
             cfg = DQNConfig(lr=6.25e-5, adam_eps=1.5e-4, batch_size=batch, prioritized=prioritized)
-            dqn = DQNLearner(image, ActionSpec.discrete(6), dev, cfg=cfg, seed=0, n_envs=8)
+            dqn = DQNLearner(image, ActionSpec.discrete(6), dev, cfg=cfg, seed=0, n_envs=8, defer_grads=defer)
             for k in range(2):
                 dqn.update(dqn_batch(k, batch=batch))
             rng = np.random.default_rng(0)
