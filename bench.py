@@ -289,15 +289,17 @@ def bench_rppo(dev, updates=3, mode="graph"):
 
 def dominant_kernel(dev, learner, reps=200):
     """The DQN update's longest entry point, ttrl_dqn_tail, at the update's
-    shapes on the learner's weights: the first linear layer 3136 -> 512 of the
-    three Q evaluations (online(s), online(s'), target(s')) as one split-K
-    GEMM launch, then one kernel for the split sums, the Q head 512 -> 6, the
-    double-DQN Huber loss and the second layer's backward.  Timed alone on
-    the library's stream with HIP events over `reps` calls.
+    shapes on the learner's weights and as the update calls it: the first
+    linear layer 3136 -> 512 of the three Q evaluations (online(s),
+    online(s'), target(s')) as one split-K GEMM launch, then one kernel for
+    the split sums, the Q head 512 -> 6, the double-DQN Huber row of every
+    sample and the gradient entering the first layer (the second layer's
+    gradients and the batch means are left to the Adam launch).  Timed alone
+    on the library's stream with HIP events over `reps` calls.
     Algorithmic work per call: 3 x 2 x 32 x 3136 x 512 FLOPs in the GEMM,
-    3 x 2 x 32 x 512 x 6 in the head, 2 x 32 x 512 x 6 each for dh and dW2;
-    HBM bytes: the three feature batches, the two distinct first-layer
-    weight sets (online, target) and biases, the three 32 x 512 outputs, dh."""
+    3 x 2 x 32 x 512 x 6 in the head, 2 x 32 x 512 x 6 for dh; HBM bytes:
+    the three feature batches, the two distinct first-layer weight sets
+    (online, target) and biases, the three 32 x 512 outputs, dh."""
     from ttrl_amd import _lib
     from ttrl_amd.algos.dqn import _lockstep_layers
     from ttrl_amd.engine.tensor import DeviceArray
@@ -322,7 +324,7 @@ def dominant_kernel(dev, learner, reps=200):
             arr((B, 1), np.full((B, 1), 0.99 ** 3)), arr((B, 1), rng.random((B, 1)))]
     outs = {n: DeviceArray(dev, shape) for n, shape in (("loss", (1, 1)), ("mean_q", (1, 1)), ("td_abs", (B, 1)),
                                                           ("dq", (B, A)), ("next", (B, 1)), ("y", (B, 1)),
-                                                          ("dh", (B, F)), ("dw2", (F, A)), ("db2", (1, A)))}
+                                                          ("dh", (B, F)), ("terms", (B, 2)))}
     d = _lib.DqnTailDesc()
     d.B, d.K, d.F, d.A, d.groups = B, K, F, A, 3
     for g, (fc1, _, fc2) in enumerate(sets):
@@ -332,7 +334,7 @@ def dominant_kernel(dev, learner, reps=200):
     d.delta = 1.0
     d.loss, d.mean_q, d.td_abs, d.dq = outs["loss"].ptr, outs["mean_q"].ptr, outs["td_abs"].ptr, outs["dq"].ptr
     d.next_actions, d.td_target, d.dh = outs["next"].ptr, outs["y"].ptr, outs["dh"].ptr
-    d.dW2, d.db2, d.beta_w = outs["dw2"].ptr, outs["db2"].ptr, 0.0
+    d.dW2, d.db2, d.beta_w, d.loss_terms = None, None, 0.0, outs["terms"].ptr
 
     def launch():
         dev.call("ttrl_dqn_tail", C.byref(d))
@@ -346,12 +348,12 @@ def dominant_kernel(dev, learner, reps=200):
         launch()
     dev.call("ttrl_timer_stop", C.byref(ms))
     sec = ms.value / 1e3 / reps
-    flops = 3 * 2.0 * B * K * F + 3 * 2.0 * B * F * A + 2 * 2.0 * B * F * A
+    flops = 3 * 2.0 * B * K * F + 3 * 2.0 * B * F * A + 2.0 * B * F * A
     algo_bytes = 4 * (3 * B * K + 2 * (K * F + F) + 3 * B * F + B * F)
     return {"name": "ttrl_dqn_tail: fc1 3 x (32x3136 @ 3136x512) split-K GEMM + k_dqn_tail (split sums, Q head "
-                    "512->6, double-DQN Huber loss, fc2 backward), batch 32",
+                    "512->6, double-DQN Huber rows, gradient into fc1), batch 32",
             "kernels": ["k_gemm<..., LdRowK, LdColK, EpStore> (tile and split from the plan table, partials left "
-                        "for the tail)", "k_dqn_tail<8>"],
+                        "for the tail)", "k_dqn_tail<8, SP> (SP: split partials per batch)"],
             "seconds": sec, "bytes": algo_bytes, "flops": flops}
 
 

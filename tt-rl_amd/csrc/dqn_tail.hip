@@ -114,11 +114,13 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
   __shared__ float qrow[3 * AP];
   __shared__ float dqrow[AP];
   __shared__ int last;
+  warm_kernargs<int(sizeof(TailArgs))>();
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int F = t.F, A = t.A, G = t.G, S = t.splits, B = t.B;
 
   // 0. the second layer's weights of this thread's first NPRE features in
-  // every set, in flight with the first layer's loads
+  // every set and its bias entry (threads g * AP + a), in flight with the
+  // first layer's loads
   float w2p[NPRE][3][AP];
 #pragma unroll
   for (int i = 0; i < NPRE; ++i) {
@@ -129,6 +131,14 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
 #pragma unroll
       for (int a = 0; a < AP; ++a) w2p[i][g][a] = w[min(a, A - 1)];
     }
+  }
+  float b2v = 0.f;
+  bool has_b2 = false;
+  {
+    const int g = min(tid / AP, 2), a = min(tid - g * AP, A - 1);
+    const float* b2 = g == 0 ? t.b2[0] : (g == 1 ? t.b2[1] : t.b2[2]);
+    has_b2 = b2 != nullptr;
+    if (tid < 3 * AP && has_b2) b2v = b2[a];
   }
   // 1. the first layer's outputs of sample b, every feature set: item
   // k = g * F + n, kTailItems items per thread per pass, every split of an
@@ -229,7 +239,7 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
     if (g < G && a < A) {
 #pragma unroll
       for (int w = 0; w < kTailThreads / 64; ++w) v += red[w][tid];
-      if (t.b2[g]) v += t.b2[g][a];
+      if (has_b2) v += b2v;
       t.q[g][long(b) * A + a] = v;
     }
     qrow[tid] = v;
@@ -470,14 +480,16 @@ int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* d) {
   t.partials = reinterpret_cast<float*>(words + kSyncCounters);
   t.loss_terms = d->loss_terms;
   const int ap = A <= 8 ? 8 : (A <= 16 ? 16 : 32);
-  const bool wide = t.splits > 8;  // up to kTailSplits partials per output in one batch
+  // partials per output loaded in one batch: 8, 12 or kTailSplits (16)
+  const int sp = t.splits <= 8 ? 8 : (t.splits <= 12 ? 12 : kTailSplits);
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(unsigned(B)), dim3(kTailThreads), 0, stream_of(ctx), t);
     return check_launch("ttrl_dqn_tail");
   };
-  if (ap == 8) return wide ? launch(k_dqn_tail<8, kTailSplits>) : launch(k_dqn_tail<8, 8>);
-  if (ap == 16) return wide ? launch(k_dqn_tail<16, kTailSplits>) : launch(k_dqn_tail<16, 8>);
-  return wide ? launch(k_dqn_tail<32, kTailSplits>) : launch(k_dqn_tail<32, 8>);
+  auto by_sp = [&](auto k8, auto k12, auto k16) { return sp == 8 ? launch(k8) : (sp == 12 ? launch(k12) : launch(k16)); };
+  if (ap == 8) return by_sp(k_dqn_tail<8, 8>, k_dqn_tail<8, 12>, k_dqn_tail<8, kTailSplits>);
+  if (ap == 16) return by_sp(k_dqn_tail<16, 8>, k_dqn_tail<16, 12>, k_dqn_tail<16, kTailSplits>);
+  return by_sp(k_dqn_tail<32, 8>, k_dqn_tail<32, 12>, k_dqn_tail<32, kTailSplits>);
 }
 
 }  // extern "C"

@@ -63,23 +63,24 @@ __device__ __forceinline__ void adam4(f32x4& pv, const f32x4& gv, f32x4& sv, f32
   }
 }
 
-// The update of float4s first, first + step, ... below end whose skip(i)
-// is false, g^2 added to gsq in that order.  The next float4's loads are in
-// flight while one is computed, and the first float4's are issued before
-// the step's scalars are formed (thread 0's double-precision powers), so
-// those latencies overlap.  Every thread of the workgroup calls it (the
-// scalars' barrier); alpha_t and eps_t receive the scalars.
-template <class Skip>
+// The update of float4s map(j), j = first, first + step, ... below end,
+// g^2 added to gsq in that order.  The next float4's loads are in flight
+// while one is computed, and the first float4's are issued before the
+// step's scalars are formed (thread 0's double-precision powers), so those
+// latencies overlap.  Every thread of the workgroup calls it (the scalars'
+// barrier); alpha_t and eps_t receive the scalars.
+template <class Map>
 __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ S,
                                           float* __restrict__ V, long first, long end, long step,
                                           const int* __restrict__ stepc, float lr, float b1, float b2, float eps,
-                                          float wd, float& gsq, float* alpha_t, float* eps_t, Skip skip) {
+                                          float wd, float& gsq, float* alpha_t, float* eps_t, Map map) {
   f32x4* P = reinterpret_cast<f32x4*>(p);
   const f32x4* G = reinterpret_cast<const f32x4*>(g);
   f32x4* Sv = reinterpret_cast<f32x4*>(S);
   f32x4* Vv = reinterpret_cast<f32x4*>(V);
-  long i = first;
-  bool have = i < end;
+  long j = first;
+  bool have = j < end;
+  long i = have ? map(j) : 0;
   f32x4 pv = {}, gv = {}, sv = {}, vv = {};
   if (have) {
     pv = P[i];
@@ -90,22 +91,22 @@ __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __
   adam_scalars(stepc, lr, b1, b2, eps, alpha_t, eps_t);
   const float at = *alpha_t, et = *eps_t;
   while (have) {
-    const long j = i + step;
-    const bool more = j < end;
+    const long jn = j + step;
+    const bool more = jn < end;
+    const long in = more ? map(jn) : 0;
     f32x4 pn = {}, gn = {}, sn = {}, vn = {};
     if (more) {
-      pn = P[j];
-      gn = G[j];
-      sn = Sv[j];
-      vn = Vv[j];
+      pn = P[in];
+      gn = G[in];
+      sn = Sv[in];
+      vn = Vv[in];
     }
-    if (!skip(i)) {
-      adam4(pv, gv, sv, vv, b1, b2, wd, et, at, gsq);
-      P[i] = pv;
-      Sv[i] = sv;
-      Vv[i] = vv;
-    }
-    i = j;
+    adam4(pv, gv, sv, vv, b1, b2, wd, et, at, gsq);
+    P[i] = pv;
+    Sv[i] = sv;
+    Vv[i] = vv;
+    j = jn;
+    i = in;
     have = more;
     pv = pn;
     gv = gn;
@@ -114,8 +115,8 @@ __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __
   }
 }
 
-struct NoSkip {
-  __device__ bool operator()(long) const { return false; }
+struct Identity {
+  __device__ long operator()(long j) const { return j; }
 };
 
 // Block `blk` of `nblk` of one Adam update: its grid-stride share of the
@@ -132,7 +133,7 @@ __device__ __forceinline__ void adam_block(float* __restrict__ p, const float* _
   const long n4 = n / 4;
   const long stride = long(nblk) * kOptThreads;
   adam_loop(p, g, S, V, blk * long(kOptThreads) + threadIdx.x, n4, stride, step, lr, b1, b2, eps, wd, gsq, &alpha_t,
-            &eps_t, NoSkip{});
+            &eps_t, Identity{});
   // Tail (n % 4) handled by block 0.
   if (blk == 0) {
     for (long i = n4 * 4 + threadIdx.x; i < n; i += kOptThreads) {
@@ -241,8 +242,9 @@ constexpr int kMaxGradSources = 8;
 constexpr int kMaxOrderedSums = 4;
 constexpr int kSplitBatch = 16;  // split partials of a float4 in flight together
 constexpr int kOuterBatch = 8;   // batch rows of an outer-product float4 in flight together (general path)
-constexpr int kOuterRows = 8;    // batch rows in flight together (staged path)
-constexpr int kOuterLds = 2048;  // v floats an outer-product source stages in LDS
+constexpr int kOuterLds = 2048;   // v floats an outer-product source stages in LDS
+constexpr int kOuterULds = 6144;  // u floats (the workgroup's slice of rows) it stages
+constexpr int kOuterChunk = 32;   // batch rows of u staged per memory round trip
 constexpr int kSumLds = 1024;    // terms of an ordered sum staged in LDS
 
 struct GradSrc {
@@ -317,19 +319,47 @@ __device__ __forceinline__ f32x4 source_grad(const GradSrc& s, int q, bool* bias
   return acc;
 }
 
-// True when an outer-product source's workgroups stage v ([batch][cols])
-// in LDS: then a float4 of the weight block spans at most two rows of u
-// (cols >= 4), both loaded for kOuterRows batch rows at a time.
-__device__ __forceinline__ bool outer_staged(const GradSrc& s) {
-  return s.kind == TTRL_GRAD_OUTER && s.cols >= 4 && s.batch * s.cols <= kOuterLds;
+// The rows of u an outer-product source's workgroup reads: its float4s
+// [qb0, qb0 + kOptThreads) cover weight elements from 4 qb0 on, rows
+// [r_lo, r_lo + R).  The workgroup stages that slice of u ([batch][R]) and
+// all of v ([batch][cols]) in LDS when they fit (R <= kOptThreads), one
+// memory round trip per kOuterChunk batch rows, and forms its float4s from
+// LDS; otherwise (staged false) each thread reads u and v itself.
+struct OuterSlice {
+  int r_lo, R;
+  bool staged;
+};
+__device__ __forceinline__ OuterSlice outer_slice(const GradSrc& s, int qb0) {
+  OuterSlice o{0, 0, false};
+  if (s.kind != TTRL_GRAD_OUTER) return o;
+  const int qw1 = min(qb0 + kOptThreads, s.nw4);
+  if (qw1 > qb0) {
+    o.r_lo = s.dc.div(4 * qb0);
+    o.R = s.dc.div(4 * qw1 - 1) - o.r_lo + 1;
+  }
+  o.staged = o.R <= kOptThreads && s.batch * o.R <= kOuterULds && s.batch * s.cols <= kOuterLds;
+  return o;
 }
-__device__ __forceinline__ void stage_outer(const GradSrc& s, float* vs) {
-  for (int i = threadIdx.x; i < s.batch * s.cols; i += kOptThreads) vs[i] = s.v[i];
+__device__ __forceinline__ void stage_outer(const GradSrc& s, const OuterSlice& o, float* us, float* vs) {
+  const int tid = threadIdx.x, nv = s.batch * s.cols;
+  const int rr = min(tid, max(o.R - 1, 0));
+  for (int b0 = 0; b0 < s.batch; b0 += kOuterChunk) {
+    float t[kOuterChunk];
+#pragma unroll
+    for (int i = 0; i < kOuterChunk; ++i) t[i] = s.u[long(min(b0 + i, s.batch - 1)) * s.rows + o.r_lo + rr];
+    const float vv = b0 == 0 && tid < nv ? s.v[tid] : 0.f;
+    if (b0 == 0 && tid < nv) vs[tid] = vv;
+#pragma unroll
+    for (int i = 0; i < kOuterChunk; ++i)
+      if (tid < o.R && b0 + i < s.batch) us[(b0 + i) * o.R + tid] = t[i];
+  }
+  for (int i = kOptThreads + tid; i < nv; i += kOptThreads) vs[i] = s.v[i];
   __syncthreads();
 }
 // source_grad of a staged outer-product source: the same sums in the same
-// order (b from zero, fmaf(u, v, acc); the bias adds v).
-__device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const float* vs, int q, bool* bias, int* qq) {
+// order (b from zero, fmaf(u, v, acc); the bias adds v), read from LDS.
+__device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const OuterSlice& o, const float* us,
+                                                   const float* vs, int q, bool* bias, int* qq) {
   *bias = q >= s.nw4;
   *qq = *bias ? q - s.nw4 : q;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -344,32 +374,16 @@ __device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const float
     for (int j = 0; j < 4; ++j) acc[j] = 4 * *qq + j < s.cols ? acc[j] : 0.f;
     return acc;
   }
-  const int e0 = 4 * *qq, r0 = s.dc.div(e0);
-  const int r1 = min(r0 + 1, s.rows - 1);
-  int c[4];
-  bool second[4];
+  int r[4], c[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int cj = e0 + j - r0 * s.cols;  // < 2 cols: the float4 spans rows r0 and r0 + 1 at most
-    second[j] = cj >= s.cols;
-    c[j] = second[j] ? cj - s.cols : cj;
+    const int e = 4 * *qq + j, rj = s.dc.div(e);
+    r[j] = rj - o.r_lo;
+    c[j] = e - rj * s.cols;
   }
-  for (int b0 = 0; b0 < s.batch; b0 += kOuterRows) {
-    float ua[kOuterRows], ub[kOuterRows];
+  for (int b = 0; b < s.batch; ++b)
 #pragma unroll
-    for (int i = 0; i < kOuterRows; ++i) {
-      const long bb = min(b0 + i, s.batch - 1);
-      ua[i] = s.u[bb * s.rows + r0];
-      ub[i] = s.u[bb * s.rows + r1];
-    }
-#pragma unroll
-    for (int i = 0; i < kOuterRows; ++i)
-      if (b0 + i < s.batch) {  // uniform
-        const float* vr = vs + (b0 + i) * s.cols;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] = fmaf(second[j] ? ub[i] : ua[i], vr[c[j]], acc[j]);
-      }
-  }
+    for (int j = 0; j < 4; ++j) acc[j] = fmaf(us[b * o.R + r[j]], vs[b * s.cols + c[j]], acc[j]);
   return acc;
 }
 
@@ -385,16 +399,16 @@ struct AdamSrcArgs {
   int nsrc;
   GradSrc src[kMaxGradSources];
   int plain0, plain_blocks;
-  long chunk4;  // float4s per plain workgroup (a contiguous chunk)
-  int nholes;   // the sources' float4 ranges [lo, hi), which plain workgroups skip
+  long plain4;  // float4s no source owns
+  int nholes;   // the sources' float4 ranges [lo, hi), ascending and disjoint
   long hole_lo[2 * kMaxGradSources], hole_hi[2 * kMaxGradSources];
 };
 
 // Blocks [0, plain0) form the sources' gradients (source k owns blocks
-// [block0, block0 + blocks)) and update their parameters; the rest update
-// contiguous chunks of chunk4 float4s, skipping the sources' ranges (a chunk
-// that meets none, the usual case, checks nothing per float4).  Block b's
-// partial sum of g^2 goes to partials[b].
+// [block0, block0 + blocks)) and update their parameters; the rest run the
+// grid-stride update over the float4s no source owns, numbered densely: j
+// maps to arena float4 j plus the lengths of the holes at or below it.
+// Block b's partial sum of g^2 goes to partials[b].
 __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_adam_src(AdamSrcArgs a) {
   __shared__ float red[kOptThreads / 64];
   warm_kernargs<int(sizeof(AdamSrcArgs))>();
@@ -411,11 +425,13 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
     for (int i = 1; i < kMaxGradSources; ++i)
       if (i < a.nsrc && blk >= a.src[i].block0) k = i;
     const GradSrc& s = a.src[k];
-    __shared__ float vs[kOuterLds];
-    const bool staged = outer_staged(s);  // uniform over the workgroup
+    __shared__ float us[kOuterULds], vs[kOuterLds];
+    const int qb0 = (blk - s.block0) * kOptThreads;
+    const OuterSlice o = outer_slice(s, qb0);  // uniform over the workgroup
+    const bool staged = o.staged && s.blocks * kOptThreads >= s.nw4 + s.nb4;  // one float4 per thread
     const int nq = s.nw4 + s.nb4;
     const int step = s.blocks * kOptThreads;
-    int q = (blk - s.block0) * kOptThreads + int(threadIdx.x);
+    int q = qb0 + int(threadIdx.x);
     // the first float4's parameters and moments in flight while the
     // gradient's operands are staged and the scalars formed
     auto where = [&](int qv) { return qv >= s.nw4 ? s.b4 + (qv - s.nw4) : s.w4 + qv; };
@@ -426,12 +442,12 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
       sv = Sv[i];
       vv = Vv[i];
     }
-    if (staged) stage_outer(s, vs);
+    if (staged) stage_outer(s, o, us, vs);
     adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
     for (bool first = true; q < nq; q += step, first = false) {
       bool bias;
       int qq;
-      const f32x4 gv = staged ? outer_grad_staged(s, vs, q, &bias, &qq) : source_grad(s, q, &bias, &qq);
+      const f32x4 gv = staged ? outer_grad_staged(s, o, us, vs, q, &bias, &qq) : source_grad(s, q, &bias, &qq);
       const long i = (bias ? s.b4 : s.w4) + qq;
       if (!first) {
         pv = P[i];
@@ -446,20 +462,15 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
     }
   } else {
     const long n4 = a.n / 4;
-    const long c0 = long(blk - a.plain0) * a.chunk4, c1 = min(n4, c0 + a.chunk4);
-    bool touch = false;  // uniform: does this chunk meet a source's range?
-    for (int h = 0; h < a.nholes; ++h) touch = touch || (a.hole_lo[h] < c1 && a.hole_hi[h] > c0);
-    if (!touch) {
-      adam_loop(a.p, a.g, a.S, a.V, c0 + threadIdx.x, c1, kOptThreads, a.step, a.lr, a.b1, a.b2, a.eps, a.wd, gsq,
-                &alpha_t, &eps_t, NoSkip{});
-    } else {
-      adam_loop(a.p, a.g, a.S, a.V, c0 + threadIdx.x, c1, kOptThreads, a.step, a.lr, a.b1, a.b2, a.eps, a.wd, gsq,
-                &alpha_t, &eps_t, [&](long i) {
-                  bool in = false;
-                  for (int h = 0; h < a.nholes; ++h) in = in || (i >= a.hole_lo[h] && i < a.hole_hi[h]);
-                  return in;
-                });
-    }
+    const long stride = long(a.plain_blocks) * kOptThreads;
+    adam_loop(a.p, a.g, a.S, a.V, long(blk - a.plain0) * kOptThreads + threadIdx.x, a.plain4, stride, a.step, a.lr,
+              a.b1, a.b2, a.eps, a.wd, gsq, &alpha_t, &eps_t, [&](long j) {
+                long i = j;
+#pragma unroll
+                for (int h = 0; h < 2 * kMaxGradSources; ++h)
+                  if (h < a.nholes && i >= a.hole_lo[h]) i += a.hole_hi[h] - a.hole_lo[h];
+                return i;
+              });
     // Tail (n % 4) handled by the first plain block; no source reaches it.
     if (blk == a.plain0) {
       for (long i = n4 * 4 + threadIdx.x; i < a.n; i += kOptThreads) {
@@ -489,14 +500,16 @@ __global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
   for (int i = 1; i < kMaxGradSources; ++i)
     if (i < a.nsrc && blk >= a.src[i].block0) k = i;
   const GradSrc& s = a.src[k];
-  __shared__ float vs[kOuterLds];
-  const bool staged = outer_staged(s);
-  if (staged) stage_outer(s, vs);
+  __shared__ float us[kOuterULds], vs[kOuterLds];
+  const int qb0 = (blk - s.block0) * kOptThreads;
+  const OuterSlice o = outer_slice(s, qb0);
   const int nq = s.nw4 + s.nb4;
-  for (int q = (blk - s.block0) * kOptThreads + int(threadIdx.x); q < nq; q += s.blocks * kOptThreads) {
+  const bool staged = o.staged && s.blocks * kOptThreads >= nq;
+  if (staged) stage_outer(s, o, us, vs);
+  for (int q = qb0 + int(threadIdx.x); q < nq; q += s.blocks * kOptThreads) {
     bool bias;
     int qq;
-    const f32x4 gv = staged ? outer_grad_staged(s, vs, q, &bias, &qq) : source_grad(s, q, &bias, &qq);
+    const f32x4 gv = staged ? outer_grad_staged(s, o, us, vs, q, &bias, &qq) : source_grad(s, q, &bias, &qq);
     if (!bias) {
       reinterpret_cast<f32x4*>(s.gw)[qq] = gv;
     } else {
@@ -762,16 +775,18 @@ int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* d) {
   // the plain part takes what the source workgroups leave of a launch's
   // kOptMaxBlocks, so the whole grid is resident at once
   a.plain_blocks = std::max(1, std::min(int(grid_for(d->n, 4)), kOptMaxBlocks - srcblocks));
-  const long n4 = d->n / 4;
-  a.chunk4 = std::max(1L, (n4 + a.plain_blocks - 1) / a.plain_blocks);
-  a.nholes = 0;
+  std::vector<std::pair<long, long>> holes;
   for (int k = 0; k < a.nsrc; ++k) {
-    a.hole_lo[a.nholes] = a.src[k].w4;
-    a.hole_hi[a.nholes++] = a.src[k].w4 + a.src[k].nw4;
-    if (a.src[k].nb4 > 0) {
-      a.hole_lo[a.nholes] = a.src[k].b4;
-      a.hole_hi[a.nholes++] = a.src[k].b4 + a.src[k].nb4;
-    }
+    holes.emplace_back(a.src[k].w4, a.src[k].w4 + a.src[k].nw4);
+    if (a.src[k].nb4 > 0) holes.emplace_back(a.src[k].b4, a.src[k].b4 + a.src[k].nb4);
+  }
+  std::sort(holes.begin(), holes.end());  // disjoint (make_sources checked)
+  a.nholes = int(holes.size());
+  a.plain4 = d->n / 4;
+  for (int h = 0; h < a.nholes; ++h) {
+    a.hole_lo[h] = holes[h].first;
+    a.hole_hi[h] = holes[h].second;
+    a.plain4 -= holes[h].second - holes[h].first;
   }
   const int blocks = a.plain0 + a.plain_blocks;
   long wsf = 0;

@@ -831,14 +831,17 @@ struct PairDims {
 // and input gradients): workgroups [0, d1.blocks) run the first, the rest
 // the second, so the two fill the device together instead of one after the
 // other.  LDS is the larger of the two problems' stages.  Each problem's
-// split-K partials go to its own buffer (ws1, ws2).
-template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA1, class LB1, class EP1, class LA2, class LB2,
-          class EP2>
+// split-K partials go to its own buffer (ws1, ws2).  The two share the tile
+// and the wavefront layout; their LDS stage depths (TBK1, TBK2) may differ,
+// so a short reduction (a weight gradient over a batch of 32) and a long
+// one (the input gradient through a wide layer) each get a stage to fit.
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK1, int TBK2, class LA1, class LB1, class EP1, class LA2,
+          class LB2, class EP2>
 __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm_pair(LA1 la1, LB1 lb1, EP1 ep1, LA2 la2, LB2 lb2,
                                                                     EP2 ep2, float* ws1, float* ws2, PairDims d1,
                                                                     PairDims d2) {
-  using S1 = TileShared<BM, BN, TBK, LA1, LB1>;
-  using S2 = TileShared<BM, BN, TBK, LA2, LB2>;
+  using S1 = TileShared<BM, BN, TBK1, LA1, LB1>;
+  using S2 = TileShared<BM, BN, TBK2, LA2, LB2>;
   constexpr int SIZE = S1::SIZE > S2::SIZE ? S1::SIZE : S2::SIZE;
   __shared__ __attribute__((aligned(16))) float lds[SIZE];
   warm_kernargs<int(sizeof(LA1) + sizeof(LB1) + sizeof(EP1) + sizeof(LA2) + sizeof(LB2) + sizeof(EP2) +
@@ -846,12 +849,12 @@ __global__ __launch_bounds__(64 * WGM * WGN * WGK) void k_gemm_pair(LA1 la1, LB1
   int b = blockIdx.x;
   if (b < d1.blocks) {
     const int bx = b % d1.gx, byz = b / d1.gx;
-    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la1, lb1, ep1, ws1, d1.M, d1.N, d1.K, d1.kchunk, d1.splits, bx,
+    gemm_tile<BM, BN, WGM, WGN, WGK, TBK1>(la1, lb1, ep1, ws1, d1.M, d1.N, d1.K, d1.kchunk, d1.splits, bx,
                                           byz % d1.gy, byz / d1.gy, lds, lds + S1::A);
   } else {
     b -= d1.blocks;
     const int bx = b % d2.gx, byz = b / d2.gx;
-    gemm_tile<BM, BN, WGM, WGN, WGK, TBK>(la2, lb2, ep2, ws2, d2.M, d2.N, d2.K, d2.kchunk, d2.splits, bx,
+    gemm_tile<BM, BN, WGM, WGN, WGK, TBK2>(la2, lb2, ep2, ws2, d2.M, d2.N, d2.K, d2.kchunk, d2.splits, bx,
                                           byz % d2.gy, byz / d2.gy, lds, lds + S2::A);
   }
 }
@@ -978,17 +981,26 @@ bool gemm_tuning_log();  // TTRL_GEMM_TUNE_LOG=1: print each tuned signature's c
 // tile shape wherever a call site allows it, bypassing the plan cache.
 bool gemm_forced(unsigned allowed, int M, int N, int K, int groups, long ws_floats, GemmPlan* out);
 
-template <int BM_, int BN_, int WGM_, int WGN_, int WGK_, int TBK_>
+template <int ID_, int BM_, int BN_, int WGM_, int WGN_, int WGK_, int TBK_>
 struct CfgTag {
-  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, WGK = WGK_, TBK = TBK_;
+  static constexpr int ID = ID_, BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, WGK = WGK_, TBK = TBK_;
 };
+
+// The tile shape with the same tile and wavefront layout and another LDS
+// stage depth (a pair may run its two problems at different depths), or -1.
+constexpr int twin_cfg(int c) {
+  return c == T32x32 ? T32x32S : c == T32x32S ? T32x32 : c == T64x64 ? T64x64S : c == T64x64S ? T64x64
+       : c == T128x64 ? T128x64S : c == T128x64S ? T128x64 : -1;
+}
+// True when a pair may run its problems with tile shapes c1 and c2.
+constexpr bool pair_cfgs_ok(int c1, int c2) { return c1 == c2 || twin_cfg(c1) == c2; }
 
 // Calls f(CfgTag<...>{}) for tile shape `cfg` if ALLOWED instantiates it.
 template <unsigned ALLOWED, class F>
 inline void dispatch_cfg(int cfg, F&& f) {
-#define TTRL_CFG(C, BM, BN, WGM, WGN, WGK, TBK)                                        \
-  case C:                                                                             \
-    if constexpr ((ALLOWED & cfg_bit(C)) != 0) f(CfgTag<BM, BN, WGM, WGN, WGK, TBK>{}); \
+#define TTRL_CFG(C, BM, BN, WGM, WGN, WGK, TBK)                                            \
+  case C:                                                                                 \
+    if constexpr ((ALLOWED & cfg_bit(C)) != 0) f(CfgTag<C, BM, BN, WGM, WGN, WGK, TBK>{}); \
     break;
   switch (cfg) {
     TTRL_CFG(T32x32, 32, 32, 2, 2, 1, 256)
@@ -1180,8 +1192,8 @@ struct GemmDims {
 // defer1 not null: the first problem's split-K partials go there and are
 // left unreduced (a later launch sums them); otherwise both problems'
 // partials share `ws` and each is reduced after the pair.
-template <int BM, int BN, int WGM, int WGN, int WGK, int TBK, class LA1, class LB1, class EP1, class LA2, class LB2,
-          class EP2>
+template <int BM, int BN, int WGM, int WGN, int WGK, int TBK1, int TBK2, class LA1, class LB1, class EP1, class LA2,
+          class LB2, class EP2>
 inline void launch_pair_cfg(const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1, const GemmPlan& p1,
                             const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const GemmPlan& p2,
                             float* ws, hipStream_t st, float* defer1) {
@@ -1191,7 +1203,7 @@ inline void launch_pair_cfg(const LA1& la1, const LB1& lb1, const EP1& ep1, cons
   const PairDims d1{q1.M, q1.N, q1.K, p1.kchunk, p1.splits, gx1, gy1, gx1 * gy1 * q1.groups * p1.splits};
   const PairDims d2{q2.M, q2.N, q2.K, p2.kchunk, p2.splits, gx2, gy2, gx2 * gy2 * q2.groups * p2.splits};
   float* ws1 = defer1 ? defer1 : ws;
-  hipLaunchKernelGGL((k_gemm_pair<BM, BN, WGM, WGN, WGK, TBK, LA1, LB1, EP1, LA2, LB2, EP2>),
+  hipLaunchKernelGGL((k_gemm_pair<BM, BN, WGM, WGN, WGK, TBK1, TBK2, LA1, LB1, EP1, LA2, LB2, EP2>),
                      dim3(unsigned(d1.blocks + d2.blocks)), dim3(64 * WGM * WGN * WGK), 0, st, la1, lb1, ep1, la2, lb2,
                      ep2, ws1, ws + part1, d1, d2);
   auto reduce = [&](const auto& ep, const GemmDims& q, const GemmPlan& p, float* w) {
@@ -1212,10 +1224,24 @@ template <unsigned ALLOWED, class LA1, class LB1, class EP1, class LA2, class LB
 inline void launch_pair(const LA1& la1, const LB1& lb1, const EP1& ep1, const GemmDims& q1, const GemmPlan& p1,
                         const LA2& la2, const LB2& lb2, const EP2& ep2, const GemmDims& q2, const GemmPlan& p2,
                         float* ws, hipStream_t st, float* defer1 = nullptr) {
-  dispatch_cfg<ALLOWED>(p1.cfg, [&](auto c) {
-    using C = decltype(c);
-    launch_pair_cfg<C::BM, C::BN, C::WGM, C::WGN, C::WGK, C::TBK>(la1, lb1, ep1, q1, p1, la2, lb2, ep2, q2, p2, ws,
-                                                                  st, defer1);
+  dispatch_cfg<ALLOWED>(p1.cfg, [&](auto c1) {
+    using C1 = decltype(c1);
+    if (p2.cfg == C1::ID) {
+      launch_pair_cfg<C1::BM, C1::BN, C1::WGM, C1::WGN, C1::WGK, C1::TBK, C1::TBK>(la1, lb1, ep1, q1, p1, la2, lb2,
+                                                                                    ep2, q2, p2, ws, st, defer1);
+      return;
+    }
+    constexpr int tw = twin_cfg(C1::ID);
+    if constexpr (tw >= 0 && (ALLOWED & cfg_bit(tw)) != 0) {
+      dispatch_cfg<cfg_bit(tw)>(p2.cfg, [&](auto c2) {
+        using C2 = decltype(c2);
+        static_assert(C2::BM == C1::BM && C2::BN == C1::BN && C2::WGM == C1::WGM && C2::WGN == C1::WGN &&
+                          C2::WGK == C1::WGK,
+                      "twin tile shapes share the tile and the wavefront layout");
+        launch_pair_cfg<C1::BM, C1::BN, C1::WGM, C1::WGN, C1::WGK, C1::TBK, C2::TBK>(la1, lb1, ep1, q1, p1, la2, lb2,
+                                                                                      ep2, q2, p2, ws, st, defer1);
+      });
+    }
   });
 }
 
@@ -1263,29 +1289,40 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
   const std::string key2 = key + "#2";
   const GemmPlan* h1 = ctx_plan_find(ctx, key);
   const GemmPlan* h2 = ctx_plan_find(ctx, key2);
-  if (h1 && h2 && h1->cfg == h2->cfg && plan_valid(*h1, q1.M, q1.N, q1.K, q1.groups, room1, ALLOWED) &&
+  if (h1 && h2 && pair_cfgs_ok(h1->cfg, h2->cfg) && plan_valid(*h1, q1.M, q1.N, q1.K, q1.groups, room1, ALLOWED) &&
       plan_valid(*h2, q2.M, q2.N, q2.K, q2.groups, room2, ALLOWED)) {
     p1 = *h1;
     p2 = *h2;
   } else {
     // Per tile shape: the cost model's split of each problem, then each
     // problem split 2 to 16 ways with the other at the model's split (the
-    // model prices a long K loop of a small problem below its latency).
+    // model prices a long K loop of a small problem below its latency);
+    // then the second problem at the twin stage depth, if allowed.
     std::vector<std::pair<GemmPlan, GemmPlan>> cands;
+    auto add = [&](const GemmPlan& a, const GemmPlan& b) {
+      for (const auto& e : cands)
+        if (e.first.cfg == a.cfg && e.second.cfg == b.cfg && e.first.splits == a.splits &&
+            e.second.splits == b.splits)
+          return;
+      cands.emplace_back(a, b);
+    };
     for (int c = 0; c < kNumCfg; ++c) {
       if (!(ALLOWED & cfg_bit(c))) continue;
       const GemmPlan b1 = plan_gemm(q1.M, q1.N, q1.K, q1.groups, room1, cfg_bit(c));
       const GemmPlan b2 = plan_gemm(q2.M, q2.N, q2.K, q2.groups, room2, cfg_bit(c));
-      auto add = [&](const GemmPlan& a, const GemmPlan& b) {
-        for (const auto& e : cands)
-          if (e.first.cfg == a.cfg && e.first.splits == a.splits && e.second.splits == b.splits) return;
-        cands.emplace_back(a, b);
-      };
       add(b1, b2);
       for (int sp : {2, 4, 8, 16}) {
         GemmPlan v;
         if (plan_with_splits(c, q1.M, q1.N, q1.K, q1.groups, room1, sp, &v)) add(v, b2);
         if (plan_with_splits(c, q2.M, q2.N, q2.K, q2.groups, room2, sp, &v)) add(b1, v);
+      }
+      const int t = twin_cfg(c);
+      if (t >= 0 && (ALLOWED & cfg_bit(t))) {
+        add(b1, plan_gemm(q2.M, q2.N, q2.K, q2.groups, room2, cfg_bit(t)));
+        for (int sp : {2, 4}) {
+          GemmPlan v;
+          if (plan_with_splits(t, q2.M, q2.N, q2.K, q2.groups, room2, sp, &v)) add(b1, v);
+        }
       }
     }
     p1 = cands.front().first;
@@ -1306,9 +1343,10 @@ inline int run_gemm_pair(ttrl_ctx* ctx, const LA1& la1, const LB1& lb1, const EP
         });
         if (ms < 0.f) break;
         if (gemm_tuning_log())
-          fprintf(stderr, "[ttrl gemm tune pair] %dx%dx%d(G%d) + %dx%dx%d(G%d)  %dx%d tbk%d splits=%d,%d  %.2f us\n",
+          fprintf(stderr,
+                  "[ttrl gemm tune pair] %dx%dx%d(G%d) + %dx%dx%d(G%d)  %dx%d tbk%d,%d splits=%d,%d  %.2f us\n",
                   q1.M, q1.N, q1.K, q1.groups, q2.M, q2.N, q2.K, q2.groups, c.first.bm, c.first.bn, c.first.tbk,
-                  c.first.splits, c.second.splits, ms * 1e3f / 3.f);
+                  c.second.tbk, c.first.splits, c.second.splits, ms * 1e3f / 3.f);
         // a deferred first problem has no reduce launch to charge
         const float cost =
             ms + 3.f * kReduceLaunchMs * float(int(c.first.splits > 1 && !defer1) + int(c.second.splits > 1));
