@@ -48,9 +48,13 @@ __device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float
 }
 
 // The update of four consecutive parameters with gradient gv; g^2 is added
-// to gsq element by element in order.
+// to gsq element by element in order.  Every product and sum is rounded on
+// its own (no contraction into FMAs), here and in the scalar tails, so every
+// kernel that steps a parameter gives the same bits however the compiler
+// schedules it.
 __device__ __forceinline__ void adam4(f32x4& pv, const f32x4& gv, f32x4& sv, f32x4& vv, float b1, float b2, float wd,
                                       float eps_t, float alpha_t, float& gsq) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const float graw = gv[q];
@@ -137,6 +141,7 @@ __device__ __forceinline__ void adam_block(float* __restrict__ p, const float* _
   // Tail (n % 4) handled by block 0.
   if (blk == 0) {
     for (long i = n4 * 4 + threadIdx.x; i < n; i += kOptThreads) {
+#pragma clang fp contract(off)
       const float graw = g[i];
       gsq += graw * graw;
       const float gg = wd != 0.f ? graw + wd * p[i] : graw;
@@ -474,6 +479,7 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
     // Tail (n % 4) handled by the first plain block; no source reaches it.
     if (blk == a.plain0) {
       for (long i = n4 * 4 + threadIdx.x; i < a.n; i += kOptThreads) {
+#pragma clang fp contract(off)
         const float graw = a.g[i];
         gsq += graw * graw;
         const float gg = a.wd != 0.f ? graw + a.wd * a.p[i] : graw;

@@ -252,6 +252,12 @@ def load(path: Path | str | None = None) -> C.CDLL:
             f"libttrl_hip.so is not built ({target} missing). Run __graft_entry__.build() or "
             f"`python -m ttrl_amd._build` with tt-rl_amd on sys.path; there is no host fallback."
         )
+    # Kernel arguments in device memory: every launch's first argument reads
+    # are then HBM reads rather than host-memory reads across the bus (about
+    # 1 us per update of the learners' 11 to 25 launches).  The HIP runtime
+    # reads this when it initialises, which happens at the library's first
+    # call; a value the caller set is kept.
+    os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
     dll = C.CDLL(str(target), mode=os.RTLD_LOCAL if hasattr(os, "RTLD_LOCAL") else 0)
     for name, (args, res) in SIGNATURES.items():
         fn = getattr(dll, name)
