@@ -5,11 +5,14 @@ a CPU baseline timed on this machine's host cores.
 
 One step = one full learner update (forward, backward, Adam; for SAC also
 the temperature step and the Polyak blend) replayed as one hipGraph, on a
-fresh synthetic batch: a ring of distinct batches is resident in HBM and each
-step first copies the next one into the graph's bound input block (one
-device copy), so no step re-reads the previous step's inputs and no host
-transfer is timed.  Weights are seeded He-uniform; data is synthetic
-(uint8 Atari-shaped frames, Hopper-shaped vectors).
+fresh synthetic batch: --ring distinct batches are resident in HBM, each in
+one of the learner's input slots (a bound input block with a graph captured
+against it), and update i reads slot i mod ring where it lies, so no step
+re-reads the previous step's inputs and neither a host transfer nor a device
+copy is timed.  `copy_in_each_step` times the same updates with a device copy
+of each batch into one bound block in front of every update, and `--mode
+eager` runs that form without graphs.  Weights are seeded He-uniform; data is
+synthetic (uint8 Atari-shaped frames, Hopper-shaped vectors).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints one JSON line.
@@ -60,6 +63,16 @@ def sac_update_flops(batch: int = 256) -> float:
     return 2.0 * batch * (critic_region + actor_region)
 
 
+def _fill_slots(dev, n, write, slot_block):
+    """Slot r's block holds batch r: written into the bound block (slot 0)
+    and copied into slot r; slot 0's own batch is written last."""
+    for r in range(n - 1, -1, -1):
+        write(r)
+        if r:
+            slot_block(r).copy_from(slot_block(0))
+    dev.synchronize()
+
+
 def _ring(dev, block, fill, n):
     from ttrl_amd.engine.tensor import DeviceArray
 
@@ -73,21 +86,35 @@ def _ring(dev, block, fill, n):
     return ring
 
 
-def _time_steps(dev, step, ring, block, steps, warmup):
+def _time_steps(dev, step, steps, warmup):
+    """step(i): update number i."""
     for i in range(warmup):
-        block.copy_from(ring[i % len(ring)])
-        step()
+        step(i)
     dev.synchronize()
     dev.call("ttrl_timer_start")
     t0 = time.perf_counter()
     for i in range(steps):
-        block.copy_from(ring[i % len(ring)])
-        step()
+        step(i)
     ms = C.c_float(0.0)
     dev.call("ttrl_timer_stop", C.byref(ms))
     dev.synchronize()
     wall = time.perf_counter() - t0
     return wall, ms.value / 1e3
+
+
+def _graph_legs(dev, steps, warmup, n, replay_slot, slot_block):
+    """(wall, gpu) of the headline loop: update i reads the resident batch
+    of slot i mod n where it lies; and of the loop with a device copy of
+    that batch into slot 0's block in front of every update."""
+    wall, gpu = _time_steps(dev, lambda i: replay_slot(i % n), steps, warmup)
+
+    def copied(i):
+        slot_block(0).copy_from(slot_block(1 + i % (n - 1)))
+        replay_slot(0)
+
+    cwall, cgpu = _time_steps(dev, copied, steps, warmup)
+    return wall, gpu, {"value": round(steps / cwall, 2), "ms_per_step": round(cwall / steps * 1e3, 5),
+                       "gpu_ms_per_step": cgpu / steps * 1e3}
 
 
 def bench_dqn(dev, steps, warmup, ring_n, mode="graph"):
@@ -100,12 +127,27 @@ def bench_dqn(dev, steps, warmup, ring_n, mode="graph"):
     learner.online.load_state_dict(he_uniform_qnet_state(learner.online, 1))
     learner.target.copy_from(learner.online)
     block = learner.inputs["_block"]
-    ring = _ring(dev, block, lambda r: (learner.load_batch(dqn_batch(1000 + r)), learner.step.flush_inputs()), ring_n)
-    learner.update()  # captures the graph and runs the first update
-    step = learner.step.replay if mode == "graph" else learner.step.run
-    wall, gpu = _time_steps(dev, step, ring, block, steps, warmup)
-    nodes = learner.step._trace.nodes if mode == "graph" else 0
-    return learner, wall, gpu, nodes
+
+    def write(r):
+        learner.load_batch(dqn_batch(1000 + r))
+        learner.step.flush_inputs()
+
+    if mode == "eager":
+        ring = _ring(dev, block, write, ring_n)
+        learner.update()
+
+        def step(i):
+            block.copy_from(ring[i % ring_n])
+            learner.step.run()
+
+        wall, gpu = _time_steps(dev, step, steps, warmup)
+        return learner, wall, gpu, 0, None
+    learner.step.enable_input_slots(ring_n)
+    slot_block = lambda k: learner.step.slot_inputs(k)["_block"]
+    _fill_slots(dev, ring_n, write, slot_block)
+    learner.update()  # captures one graph per input slot and runs the first update (slot 0)
+    wall, gpu, copied = _graph_legs(dev, steps, warmup, ring_n, learner.step.replay_slot, slot_block)
+    return learner, wall, gpu, learner.step._trace.nodes, copied
 
 
 def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
@@ -119,12 +161,27 @@ def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
     learner.nets.critics.load_state_dict(crit)
     learner.nets.targets.load_state_dict(crit)
     block = learner.batch.block
-    ring = _ring(dev, block, lambda r: (learner.batch.load_batch(sac_batch(2000 + r)), learner.batch.flush()), ring_n)
-    learner.update()  # eager first update
-    learner.update()  # captured graph, first replay
-    step = learner.replay if mode == "graph" else learner._run
-    wall, gpu = _time_steps(dev, step, ring, block, steps, warmup)
-    return learner, wall, gpu, (learner._graph.nodes if mode == "graph" else 0)
+
+    def write(r):
+        learner.batch.load_batch(sac_batch(2000 + r))
+        learner.batch.flush()
+
+    if mode == "eager":
+        ring = _ring(dev, block, write, ring_n)
+        learner.update()
+
+        def step(i):
+            block.copy_from(ring[i % ring_n])
+            learner._run()
+
+        wall, gpu = _time_steps(dev, step, steps, warmup)
+        return learner, wall, gpu, 0, None
+    learner.enable_input_slots(ring_n)
+    _fill_slots(dev, ring_n, write, learner.slot_block)
+    learner.update()  # eager first update (slot 0), then one graph captured per input slot
+    learner.update()  # first replay
+    wall, gpu, copied = _graph_legs(dev, steps, warmup, ring_n, learner.replay_slot, learner.slot_block)
+    return learner, wall, gpu, learner._graph.nodes, copied
 
 
 def ppo_step_flops(batch: int = 256, actions: int = 18) -> float:
@@ -542,7 +599,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--ring", type=int, default=32, help="distinct resident batches cycled through")
+    ap.add_argument("--ring", type=int, default=32,
+                    help="distinct resident batches cycled through (one input slot each in graph mode)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--act-steps", type=int, default=500, help="acting steps timed per lane count (0: skip)")
@@ -565,10 +623,10 @@ def main() -> int:
     from ttrl_amd.engine.device import acquire
 
     dev = acquire(0)
-    dqn, wall, gpu, nodes = bench_dqn(dev, args.steps, args.warmup, args.ring, args.mode)
+    dqn, wall, gpu, nodes, dqn_copied = bench_dqn(dev, args.steps, args.warmup, args.ring, args.mode)
     value = args.steps / wall
     flops = dqn_update_flops(32)
-    sac, swall, sgpu, snodes = bench_sac(dev, args.steps, args.warmup, args.ring, args.mode)
+    sac, swall, sgpu, snodes, sac_copied = bench_sac(dev, args.steps, args.warmup, args.ring, args.mode)
     sac_value = args.steps / swall
     sflops = sac_update_flops(256)
     dom = dominant_kernel(dev, dqn)
@@ -594,6 +652,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded uint8 frames, resident in HBM, fresh batch per step)",
+        "input_slots": args.ring if args.mode == "graph" else 1,
+        "copy_in_each_step": dqn_copied,
         "mode": args.mode,
         "config": {"workload": "DQN learner update: double DQN, n-step 3, PER weights, Nature-CNN 4x84x84 -> 6, "
                                "Huber 1, Adam lr 6.25e-5 eps 1.5e-4", "batch": 32, "graph_nodes": nodes},
@@ -601,7 +661,8 @@ def main() -> int:
                             "frac": flops * value / PEAK_FP32_MFMA, "gpu_ms_per_step": gpu / args.steps * 1e3},
         "sac": {"value": round(sac_value, 2), "unit": "SAC updates/s", "batch": 256,
                 "ms_per_step": round(swall / args.steps * 1e3, 5), "gpu_ms_per_step": sgpu / args.steps * 1e3,
-                "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA},
+                "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA,
+                "copy_in_each_step": sac_copied},
         "roofline": {"bound": "mfma", "kernel": dom["name"], "kernels": dom["kernels"], "achieved": achieved / 1e12,
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
                      "traffic": DQN_TAIL_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],

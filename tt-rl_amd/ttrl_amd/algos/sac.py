@@ -38,6 +38,7 @@ from ttrl_amd.engine.layers import Linear, ReLU
 from ttrl_amd.engine.ops import _kernels as K
 from ttrl_amd.engine.ops.fused import grad_targets, linear_node
 from ttrl_amd.engine.optim import Adam, adam_multi, finish_steps
+from ttrl_amd.engine.slots import InputSlots, check_slot_count, metric_ptrs
 from ttrl_amd.engine.step import InputBinder, MetricReader
 from ttrl_amd.engine.tensor import DeviceArray, ParamArena, bound_block
 from ttrl_amd.engine.trace import capture
@@ -521,6 +522,9 @@ class SACLearner:
         self._reader = MetricReader(device)
         self._graph = None
         self._graph_metrics = None
+        # input slots (enable_input_slots): slot k's graph reads _slot_batches[k]
+        self._slots = None
+        self._slot_batches: list = []
         self._pool = None
         self.update_count = 0
         self.n_envs = int(n_envs)
@@ -659,6 +663,51 @@ class SACLearner:
         metrics["actor_grad_sq"] = Tensor(self.actor_opt.grad_sq)
         return metrics
 
+    def enable_input_slots(self, n: int) -> None:
+        """n batch blocks of one layout (slot 0 is `batch.block`), one graph
+        captured against each at the first graph update (engine.slots);
+        `slot_block(k)` is slot k's block and `replay_slot(k)` runs the update
+        on it.  Graph mode, before the first update."""
+        if self.cfg.step_mode != "graph":
+            raise ValueError("SACLearner.enable_input_slots: input slots need step_mode='graph'")
+        if self._graph is not None or self._slots is not None:
+            raise RuntimeError("SACLearner.enable_input_slots: call it once, before the first update")
+        check_slot_count("SACLearner.enable_input_slots", n)
+        b = self.batch
+        self._slot_batches = [b] + [_BatchBuffers(self.device, b.B, self.obs_spec.size, self.action_spec.dim,
+                                                  self.cfg.prioritized) for _ in range(n - 1)]
+        self._slots = InputSlots(self.device, [x.block for x in self._slot_batches])
+
+    def slot_block(self, k: int) -> DeviceArray:
+        if self._slots is None:
+            raise RuntimeError("SACLearner.slot_block: call enable_input_slots() first")
+        return self._slot_batches[k].block
+
+    def _capture_slots(self) -> None:
+        """Slot k >= 1's graph: the same update over slot k's batch block."""
+        want = metric_ptrs(self._graph_metrics)
+        self._slots.graphs[0] = self._graph
+        first = self.batch
+        try:
+            for k, b in enumerate(self._slot_batches[1:], start=1):
+                self.batch = b
+                graph, metrics = capture(self.device, self._body)
+                self._slots.graphs[k] = graph
+                if metric_ptrs(metrics) != want:
+                    raise RuntimeError("SACLearner.enable_input_slots: a slot's graph writes its metrics elsewhere")
+        finally:
+            self.batch = first
+
+    def replay_slot(self, k: int) -> None:
+        """Launch the captured update on slot k's batch block without
+        reading metrics; they are read as after `replay()`."""
+        if self._slots is None:
+            raise RuntimeError("SACLearner.replay_slot: call enable_input_slots() before the first update")
+        if self._graph is None:
+            raise RuntimeError("SACLearner.replay_slot: update once in graph mode first (it captures)")
+        self._slots.launch(k)
+        self._replayed()
+
     def _run(self) -> dict:
         """One update; -> its metrics, read from the device."""
         binder = self.batch.binder
@@ -677,6 +726,8 @@ class SACLearner:
                 metrics = self._body()
                 dev.synchronize()
                 self._graph, self._graph_metrics = capture(dev, self._body)
+                if self._slots is not None:
+                    self._capture_slots()
             self._reader.bind(self._graph_metrics)
             return self._reader.read(metrics)
         span = self._reader.span
@@ -735,6 +786,12 @@ class SACLearner:
         self._acting.close()
         self.batch.close()
         self._reader.close()
+        slots, self._slots = self._slots, None
+        if slots is not None:
+            slots.close_extra()
+            for b in self._slot_batches[1:]:
+                b.close()
+            self._slot_batches = []
         if self._graph is not None:
             self._graph.close()
             self._graph = None

@@ -16,6 +16,10 @@ populates the step's private allocation pool so the capture pass reuses the
 same blocks, then the capture, then one replay so the call returns this
 step's metrics.  Buffers the graph touches come from that pool and stay
 reserved for the graph's lifetime.
+
+With input slots (`enable_input_slots`, engine.slots) the first call
+captures one graph per bound input block, and `replay_slot(k)` runs the
+update on the batch written into slot k's block.
 """
 
 from __future__ import annotations
@@ -27,6 +31,7 @@ import ctypes as C
 import numpy as np
 
 from ttrl_amd.engine.autograd import Tensor
+from ttrl_amd.engine.slots import InputSlots, check_slot_count, metric_ptrs, twin_inputs
 from ttrl_amd.engine.tensor import DeviceArray
 from ttrl_amd.engine.trace import capture
 
@@ -198,6 +203,42 @@ class TrainStep:
         self._trace_metrics: dict | None = None
         self._captured_grads: list = []
         self._pool = None
+        self._slots: InputSlots | None = None
+        self._slot_inputs: list = []
+        self._slot_grads: list = []
+
+    def enable_input_slots(self, n: int) -> None:
+        """n bound input blocks of the inputs' layout (slot 0 is
+        `inputs["_block"]`), one graph captured against each at the first
+        run (engine.slots); `slot_inputs(k)` are slot k's input tensors and
+        `replay_slot(k)` runs the update on them.  Graph mode, before the
+        first run; every metric must be written to fixed buffers."""
+        if self.mode != "graph":
+            raise ValueError("TrainStep.enable_input_slots: input slots need mode='graph'")
+        if self._trace is not None or self._slots is not None:
+            raise RuntimeError("TrainStep.enable_input_slots: call it once, before the first run (the capture)")
+        if not isinstance(self.inputs.get("_block"), DeviceArray):
+            raise ValueError("TrainStep.enable_input_slots: the inputs must be views of one bound block (`_block`)")
+        check_slot_count("TrainStep.enable_input_slots", n)
+        self._slot_inputs = [self.inputs] + [twin_inputs(self.device, self.inputs) for _ in range(n - 1)]
+        self._slots = InputSlots(self.device, [d["_block"] for d in self._slot_inputs])
+
+    def slot_inputs(self, k: int) -> dict:
+        """Slot k's input tensors (`_block`: its whole block)."""
+        if self._slots is None:
+            raise RuntimeError("TrainStep.slot_inputs: call enable_input_slots() first")
+        return self._slot_inputs[k]
+
+    def replay_slot(self, k: int) -> None:
+        """Launch the captured step on slot k's inputs without reading
+        metrics; they are read as after `replay()`."""
+        if self._slots is None:
+            raise RuntimeError("TrainStep.replay_slot: call enable_input_slots() before the first run")
+        if self._trace is None:
+            raise RuntimeError("TrainStep.replay_slot: run() once first (it captures every slot's graph)")
+        self._slots.launch(k)
+        self._captured_grads = self._slot_grads[k]
+        self._after_replay()
 
     def load_input(self, name: str, array) -> None:
         self._binder.load(name, array)
@@ -255,8 +296,8 @@ class TrainStep:
         self._after_replay()
         return self._reader._unpack(self._trace_metrics)
 
-    def _body(self, with_optimizer: bool):
-        metrics = self.step_fn(self.inputs)
+    def _body(self, with_optimizer: bool, inputs: dict | None = None):
+        metrics = self.step_fn(self.inputs if inputs is None else inputs)
         if with_optimizer and self.optimizer is not None:
             self.optimizer.step()
         return metrics
@@ -274,14 +315,35 @@ class TrainStep:
                 self.optimizer.zero_grad()
             dev.synchronize()
             self._trace, self._trace_metrics = capture(dev, lambda: self._body(in_graph))
-        if self.optimizer is not None:
-            self._captured_grads = [(p, p.grad) for p in self.optimizer.params]
+            self._captured_grads = self._grads_now()
+            if self._slots is not None:
+                self._capture_slots(in_graph)
+        self._rebind_grads()
         self._trace.replay(blocking=True)
         if self.optimizer is not None:
             if in_graph:
                 self.optimizer._replayed()
             else:
                 self.optimizer.step()
+
+    def _grads_now(self) -> list:
+        return [(p, p.grad) for p in self.optimizer.params] if self.optimizer is not None else []
+
+    def _capture_slots(self, in_graph: bool) -> None:
+        """Slot k >= 1's graph: the same update over slot k's inputs."""
+        dev = self.device
+        want = metric_ptrs(self._trace_metrics)
+        self._slots.graphs[0] = self._trace
+        self._slot_grads = [self._captured_grads]
+        for k, inputs in enumerate(self._slot_inputs[1:], start=1):
+            if self.optimizer is not None:
+                self.optimizer.zero_grad()
+            trace, metrics = capture(dev, lambda inputs=inputs: self._body(in_graph, inputs))
+            self._slots.graphs[k] = trace
+            self._slot_grads.append(self._grads_now())
+            if metric_ptrs(metrics) != want:
+                raise RuntimeError("TrainStep.enable_input_slots: the step's metrics are not written to the same "
+                                   "buffers by every slot's graph; give the step fixed metric outputs")
 
     def _rebind_grads(self) -> None:
         for param, grad in self._captured_grads:
@@ -291,7 +353,10 @@ class TrainStep:
         trace, self._trace = self._trace, None
         self._trace_metrics = None
         self._captured_grads = []
+        slots, self._slots = self._slots, None
         try:
+            if slots is not None:
+                slots.close_extra()
             if trace is not None:
                 trace.close()
         finally:
