@@ -294,3 +294,48 @@ def test_adam_step_with_sources_refuses_bad_sources(device):
                                 _lib.OrderedSum(t.ptr, 2, 1, 0.5, t.ptr + 8))
     assert lib.ttrl_ordered_sums(device.ctx, 2, dup) == _lib.TTRL_EINVAL
     assert b"same value" in lib.ttrl_last_error()
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(100, 128, 32), (48, 512, 5)])
+def test_wide_outer_source_formed_by_tiles(device, rows, cols, batch):
+    """An outer-product source too wide for one row band of v in LDS (a
+    linear layer's dW = x^T dZ, db = column sums of dZ) is formed by 16 x 64
+    tiles, the last row band ragged: the step forming it equals forming it
+    first and stepping after, bit for bit, and the formed gradient is x^T dZ
+    and the column sums to float32 accuracy."""
+    from ttrl_amd import _lib
+
+    rng = np.random.default_rng(rows + batch)
+    wn = rows * cols
+    n = wn + cols + 40
+    u = rng.standard_normal((batch, rows))
+    v = rng.standard_normal((batch, cols))
+    ud, vd = _up(device, u), _up(device, v)
+    p0, g0 = rng.standard_normal(n), rng.standard_normal(n)
+    s0, v0 = 0.1 * rng.standard_normal(n), rng.random(n)
+    hyper = (1e-3, 0.9, 0.999, 1e-8, 0.0)
+
+    def arena():
+        return {"p": _up(device, p0), "g": _up(device, g0), "S": _up(device, s0), "V": _up(device, v0),
+                "step": _up(device, np.array([1]), np.int32), "gsq": _empty(device, (1,))}
+
+    def source(a):
+        return (_lib.GradSource * 1)(_lib.GradSource(kind=_lib.GRAD_OUTER, rows=rows, cols=cols, dw=a["g"].ptr,
+                                                     db=a["g"].ptr + 4 * wn, u=ud.ptr, v=vd.ptr, batch=batch))
+
+    ref = arena()
+    device.call("ttrl_grad_sources_materialize", 1, source(ref))
+    g = ref["g"].numpy()
+    want_w = np.asarray(u, np.float32).astype(np.float64).T @ np.asarray(v, np.float32).astype(np.float64)
+    assert _rel(g[:wn], want_w.ravel()) < 1e-5
+    assert _rel(g[wn:wn + cols], np.asarray(v, np.float32).astype(np.float64).sum(0)) < 1e-5
+    assert np.array_equal(g[wn + cols:], np.asarray(g0[wn + cols:], np.float32))  # past the block: untouched
+    device.call("ttrl_adam_step", ref["p"].vp, ref["g"].vp, ref["S"].vp, ref["V"].vp, C.c_long(n), ref["step"].vp,
+                *(C.c_float(h) for h in hyper), ref["gsq"].vp, 0)
+    got = arena()
+    d = _lib.AdamSourcesDesc(got["p"].ptr, got["g"].ptr, got["S"].ptr, got["V"].ptr, n, got["step"].ptr, *hyper,
+                             got["gsq"].ptr, 0, 1, source(got), 0, None)
+    device.call("ttrl_adam_step_sources", C.byref(d))
+    for k in ("p", "g", "S", "V", "step"):
+        assert np.array_equal(got[k].numpy(), ref[k].numpy()), k
+    assert got["gsq"].numpy()[0] == pytest.approx(float(ref["gsq"].numpy()[0]), rel=1e-5)

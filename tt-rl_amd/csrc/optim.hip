@@ -251,6 +251,18 @@ constexpr int kOuterLds = 2048;   // v floats an outer-product source stages in 
 constexpr int kOuterULds = 6144;  // u floats (the workgroup's slice of rows) it stages
 constexpr int kOuterChunk = 32;   // batch rows of u staged per memory round trip
 constexpr int kSumLds = 1024;    // terms of an ordered sum staged in LDS
+// A wide outer-product source (cols a multiple of kTileCols, batch <=
+// kTileBatch) is formed by tiles: one workgroup per kTileRows x kTileCols
+// block of the weight, kTileOuts float4s per thread (tile rows tr and
+// tr + 16 of one float4 column), its slices of u and v staged in LDS, so
+// each workgroup reads [batch][32] of u and [batch][64] of v however wide
+// the layer is, and a layer of 3136 x 512 takes 784 workgroups (one wave of
+// the chip's resident workgroups with the rest of the step).
+constexpr int kTileRows = 32, kTileCols = 64, kTileBatch = 32;
+constexpr int kTileBand = kOptThreads / (kTileCols / 4);  // tile rows one pass of the workgroup covers
+constexpr int kTileOuts = kTileRows / kTileBand;
+static_assert(kTileRows % kTileBand == 0 && kTileOuts == 2, "a tile is two float4s per thread");
+static_assert(kTileBatch * kTileRows <= kOuterULds && kTileBatch * kTileCols <= kOuterLds, "a tile's slices fit");
 
 struct GradSrc {
   int kind, rows, cols, splits, batch;
@@ -265,6 +277,7 @@ struct GradSrc {
   const float* v;
   FDiv dc;         // division by cols
   int block0, blocks;
+  int tiled, ntc, ntiles;  // tiled outer product: tiles per row band, weight tiles (then the bias's blocks)
 };
 
 __device__ __forceinline__ f32x4 source_grad(const GradSrc& s, int q, bool* bias, int* qq) {
@@ -392,6 +405,79 @@ __device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const Outer
   return acc;
 }
 
+// A tile's slices in LDS: us[b][i] = u[b][r0 + i] (rows past the block
+// repeat its last row, never used), vs[b][j] = v[b][c0 + j].  Every load is
+// issued before the first store.
+__device__ __forceinline__ void stage_outer_tile(const GradSrc& s, int r0, int c0, float* us, float* vs) {
+  constexpr int NU = kTileBatch * kTileRows / kOptThreads, NV = kTileBatch * kTileCols / 4 / kOptThreads;
+  const int tid = threadIdx.x;
+  float u[NU];
+  f32x4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NU; ++k) {
+    const int e = tid + k * kOptThreads, b = e / kTileRows, i = e - b * kTileRows;
+    u[k] = b < s.batch ? s.u[long(b) * s.rows + min(r0 + i, s.rows - 1)] : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int e = tid + k * kOptThreads, b = e / (kTileCols / 4), j = e - b * (kTileCols / 4);
+    v[k] = b < s.batch ? *reinterpret_cast<const f32x4*>(s.v + long(b) * s.cols + c0 + 4 * j) : f32x4{};
+  }
+#pragma unroll
+  for (int k = 0; k < NU; ++k) us[tid + k * kOptThreads] = u[k];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) reinterpret_cast<f32x4*>(vs)[tid + k * kOptThreads] = v[k];
+  __syncthreads();
+}
+// The thread's kTileOuts float4s (tile rows tr + kTileBand * o, float4
+// column tc4): the same sums in the same order as source_grad (b from zero,
+// fmaf(u, v, acc)).
+__device__ __forceinline__ void outer_grad_tile(const GradSrc& s, const float* us, const float* vs, int tr, int tc4,
+                                                f32x4 (&acc)[kTileOuts]) {
+#pragma unroll
+  for (int o = 0; o < kTileOuts; ++o) acc[o] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < s.batch; ++b) {
+    const f32x4 v = reinterpret_cast<const f32x4*>(vs)[b * (kTileCols / 4) + tc4];
+#pragma unroll
+    for (int o = 0; o < kTileOuts; ++o) {
+      const float u = us[b * kTileRows + tr + kTileBand * o];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[o][j] = fmaf(u, v[j], acc[o][j]);
+    }
+  }
+}
+// Where workgroup t of a tiled source works: its tile (t < ntiles; the
+// thread's float4 q[o] of the weight, ok[o] false past the block's rows) or
+// a bias block (q[0] its bias float4, ok[0] inside the bias).
+struct TileSpot {
+  int r0, c0, tr, tc4;
+  int q[kTileOuts];
+  bool ok[kTileOuts];
+  bool weight;
+};
+__device__ __forceinline__ TileSpot tile_spot(const GradSrc& s, int t) {
+  const int tid = threadIdx.x;
+  TileSpot o{};
+  o.weight = t < s.ntiles;
+  o.tr = tid / (kTileCols / 4);
+  o.tc4 = tid % (kTileCols / 4);
+  if (o.weight) {
+    const int band = t / s.ntc;
+    o.r0 = band * kTileRows;
+    o.c0 = (t - band * s.ntc) * kTileCols;
+#pragma unroll
+    for (int k = 0; k < kTileOuts; ++k) {
+      const int row = o.r0 + o.tr + kTileBand * k;
+      o.ok[k] = row < s.rows;
+      o.q[k] = int((long(row) * s.cols + o.c0 + 4 * o.tc4) / 4);
+    }
+  } else {
+    o.q[0] = s.nw4 + (t - s.ntiles) * kOptThreads + tid;
+    o.ok[0] = o.q[0] < s.nw4 + s.nb4;
+  }
+  return o;
+}
+
 struct AdamSrcArgs {
   float* p;
   float* g;
@@ -431,6 +517,45 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
       if (i < a.nsrc && blk >= a.src[i].block0) k = i;
     const GradSrc& s = a.src[k];
     __shared__ float us[kOuterULds], vs[kOuterLds];
+    if (s.tiled) {
+      // a tile (kTileOuts float4s per thread, both slices staged) or a bias block
+      const TileSpot t = tile_spot(s, blk - s.block0);
+      const int nout = t.weight ? kTileOuts : 1;
+      long i[kTileOuts];
+      f32x4 pv[kTileOuts] = {}, sv[kTileOuts] = {}, vv[kTileOuts] = {};
+#pragma unroll
+      for (int o = 0; o < kTileOuts; ++o) {
+        i[o] = t.weight ? s.w4 + t.q[o] : s.b4 + (t.q[0] - s.nw4);
+        if (o < nout && t.ok[o]) {
+          pv[o] = P[i[o]];
+          sv[o] = Sv[i[o]];
+          vv[o] = Vv[i[o]];
+        }
+      }
+      if (t.weight) stage_outer_tile(s, t.r0, t.c0, us, vs);
+      adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+      f32x4 gv[kTileOuts];
+      if (t.weight) {
+        outer_grad_tile(s, us, vs, t.tr, t.tc4, gv);
+      } else if (t.ok[0]) {
+        bool bias;
+        int qq;
+        gv[0] = source_grad(s, t.q[0], &bias, &qq);
+      }
+#pragma unroll
+      for (int o = 0; o < kTileOuts; ++o) {
+        if (o < nout && t.ok[o]) {
+          Gd[i[o]] = gv[o];
+          adam4(pv[o], gv[o], sv[o], vv[o], a.b1, a.b2, a.wd, eps_t, alpha_t, gsq);
+          P[i[o]] = pv[o];
+          Sv[i[o]] = sv[o];
+          Vv[i[o]] = vv[o];
+        }
+      }
+      const float tot = block_sum<kOptThreads>(gsq, red);
+      if (threadIdx.x == 0) a.partials[blk] = tot;
+      return;
+    }
     const int qb0 = (blk - s.block0) * kOptThreads;
     const OuterSlice o = outer_slice(s, qb0);  // uniform over the workgroup
     const bool staged = o.staged && s.blocks * kOptThreads >= s.nw4 + s.nb4;  // one float4 per thread
@@ -507,6 +632,25 @@ __global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
     if (i < a.nsrc && blk >= a.src[i].block0) k = i;
   const GradSrc& s = a.src[k];
   __shared__ float us[kOuterULds], vs[kOuterLds];
+  if (s.tiled) {
+    const TileSpot t = tile_spot(s, blk - s.block0);
+    if (t.weight) {
+      stage_outer_tile(s, t.r0, t.c0, us, vs);
+      f32x4 gv[kTileOuts];
+      outer_grad_tile(s, us, vs, t.tr, t.tc4, gv);
+#pragma unroll
+      for (int o = 0; o < kTileOuts; ++o)
+        if (t.ok[o]) reinterpret_cast<f32x4*>(s.gw)[t.q[o]] = gv[o];
+    } else if (t.ok[0]) {
+      bool bias;
+      int qq;
+      const f32x4 gv = source_grad(s, t.q[0], &bias, &qq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (4 * qq + j < s.cols) s.gb[4 * qq + j] = gv[j];
+    }
+    return;
+  }
   const int qb0 = (blk - s.block0) * kOptThreads;
   const OuterSlice o = outer_slice(s, qb0);
   const int nq = s.nw4 + s.nb4;
@@ -715,9 +859,16 @@ int make_sources(int n, const ttrl_grad_source* srcs, const float* g, long gn, G
       d.u = s.u;
       d.v = s.v;
       d.batch = s.batch;
+      // wide enough that one row band of v would not fit in LDS: by tiles
+      d.tiled = s.cols % kTileCols == 0 && s.batch <= kTileBatch && aligned16(s.v) && s.batch * s.cols > kOuterLds;
+      if (d.tiled) {
+        d.ntc = s.cols / kTileCols;
+        d.ntiles = int(ceil_div(long(s.rows), kTileRows)) * d.ntc;
+      }
     }
     d.block0 = b;
-    d.blocks = int(ceil_div(long(d.nw4) + d.nb4, kOptThreads));
+    d.blocks = d.tiled ? d.ntiles + int(ceil_div(long(d.nb4), kOptThreads))
+                       : int(ceil_div(long(d.nw4) + d.nb4, kOptThreads));
     b += d.blocks;
     out[c++] = d;
   }
@@ -778,9 +929,6 @@ int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* d) {
   a.eps = d->eps;
   a.wd = d->weight_decay;
   a.plain0 = srcblocks;
-  // the plain part takes what the source workgroups leave of a launch's
-  // kOptMaxBlocks, so the whole grid is resident at once
-  a.plain_blocks = std::max(1, std::min(int(grid_for(d->n, 4)), kOptMaxBlocks - srcblocks));
   std::vector<std::pair<long, long>> holes;
   for (int k = 0; k < a.nsrc; ++k) {
     holes.emplace_back(a.src[k].w4, a.src[k].w4 + a.src[k].nw4);
@@ -794,6 +942,10 @@ int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* d) {
     a.hole_hi[h] = holes[h].second;
     a.plain4 -= holes[h].second - holes[h].first;
   }
+  // the plain part: a float4 per thread, within what the source workgroups
+  // leave of a launch's kOptMaxBlocks (so the whole grid is resident at
+  // once), and one workgroup at least (the tail of n % 4 and its g^2)
+  a.plain_blocks = std::max(1, std::min(int(grid_for(a.plain4 * 4, 4)), kOptMaxBlocks - srcblocks));
   const int blocks = a.plain0 + a.plain_blocks;
   long wsf = 0;
   a.partials = ctx_workspace(ctx, &wsf);

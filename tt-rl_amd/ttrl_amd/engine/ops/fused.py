@@ -69,8 +69,15 @@ def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None, *, relu: bool 
     return linear_node(x, weight, bias, y, relu=relu)
 
 
-def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, *, relu: bool) -> Tensor:
-    """The tape node of y = x @ W + b (+ReLU), with y computed elsewhere."""
+def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, *, relu: bool,
+                defer: bool = False) -> Tensor:
+    """The tape node of y = x @ W + b (+ReLU), with y computed elsewhere.
+
+    defer=True leaves the weight and bias gradients (dW = x^T dZ, db = the
+    column sums of dZ) to the optimizer step that follows, as an
+    outer-product source over the batch (engine.pending) whose operands are
+    x and dZ; the backward then computes only dX.  It applies when the
+    gradients are written fresh and dZ arrives already gated."""
     if not _needs(x, weight, bias):
         return _detached(y)
     M, K = (int(dim) for dim in x.shape)
@@ -85,6 +92,11 @@ def linear_node(x: Tensor, weight: Tensor, bias: Tensor | None, y: DeviceArray, 
         (dx,), beta_x = grad_targets(x)
         gate = relu and not out._grad_masked  # relu_bw still to apply to grad
         xmask = relu_mask(x) if dx is not None else None
+        if defer and dw is not None and beta_w == 0.0 and not gate and (bias is None or db is not None):
+            src = _lib.GradSource(kind=_lib.GRAD_OUTER, rows=K, cols=N, dw=dw.ptr, db=_p(db), u=x_data.ptr,
+                                  v=grad.ptr, batch=M)
+            PendingGrad(src, (weight, bias), keep=(x_data, grad))
+            dw = db = None
         if dw is None and db is not None:
             # Bias-only gradient: a column sum of dZ.
             from ttrl_amd.engine.ops import _kernels as Kk
@@ -307,7 +319,7 @@ def dqn_tail_td_loss(features, fc1s, fc2s, actions_onehot: Tensor, rewards: Tens
         if mean_q is not None:
             sums.append(_lib.OrderedSum(terms.ptr + 4, B, 2, inv_b, mean_q.ptr))
         add_sums(dev, sums, keep=(terms,))
-    h0 = linear_node(features[0], w1[0], fc1s[0].bias, hs[0], relu=True)
+    h0 = linear_node(features[0], w1[0], fc1s[0].bias, hs[0], relu=True, defer=deferred)
     metrics = {"mean_q": Tensor(mean_q), "td_abs": Tensor(td_abs), "td_target": Tensor(td_target),
                "next_actions": Tensor(next_act)}
     if not _needs(h0):
