@@ -37,11 +37,11 @@ for _p in (ROOT, ROOT / "tt-rl_amd"):
 import numpy as np  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12
-# HBM bytes per ttrl_dqn_tail call (fc1 GEMM + k_dqn_tail at batch 32): rocprofv3
-# FETCH_SIZE (11108.0 + 1172.4) KiB x 2.000 + WRITE_SIZE (1728.0 + 279.1) KiB x 1.000,
-# the factors being what the same counters read for a 256 MiB device-to-device
-# copy (131083.5 and 262144.0 KiB); profiles/dqn_tail_roofline_and_traffic.md.
-DQN_TAIL_TRAFFIC_BYTES = 27203426
+# HBM bytes per call of the DQN Adam step (k_adam_src + k_finish_sums at batch 32): rocprofv3
+# FETCH_SIZE (13402.1 + 5.2) KiB x 2.000 + WRITE_SIZE (26390.9 + 0.1) KiB x 1.000, medians over
+# 200 calls, the factors being what the same counters read for a 256 MiB device-to-device copy
+# (131083.5 and 262144.0 KiB); profiles/dqn_adam_step_roofline_and_traffic.md.
+ADAM_STEP_TRAFFIC_BYTES = 54479959
 PEAK_HBM = 8.0e12
 
 # Multiply-accumulates per sample of the Nature CNN at 4x84x84 (conv1..3, fc1, fc2).
@@ -345,56 +345,29 @@ def bench_rppo(dev, updates=3, mode="graph"):
 
 
 def dominant_kernel(dev, learner, reps=200):
-    """The DQN update's longest entry point, ttrl_dqn_tail, at the update's
-    shapes on the learner's weights and as the update calls it: the first
-    linear layer 3136 -> 512 of the three Q evaluations (online(s),
-    online(s'), target(s')) as one split-K GEMM launch, then one kernel for
-    the split sums, the Q head 512 -> 6, the double-DQN Huber row of every
-    sample and the gradient entering the first layer (the second layer's
-    gradients and the batch means are left to the Adam launch).  Timed alone
-    on the library's stream with HIP events over `reps` calls.
-    Algorithmic work per call: 3 x 2 x 32 x 3136 x 512 FLOPs in the GEMM,
-    3 x 2 x 32 x 512 x 6 in the head, 2 x 32 x 512 x 6 for dh; HBM bytes:
-    the three feature batches, the two distinct first-layer weight sets
-    (online, target) and biases, the three 32 x 512 outputs, dh."""
+    """The DQN update's longest launch, its Adam step, as the update calls it
+    (ttrl_adam_step_sources: k_adam_src over the 1,687,238-float parameter
+    arena, forming the gradients the update left pending as it reads them,
+    then k_finish_sums).  One forward and backward of the update's body run
+    on the bound batch (not captured) leave those sources pending: the three
+    convolutions' split-K partials and the two linear layers' outer products.
+    The step is then timed alone on the library's stream with HIP events over
+    `reps` calls, each forming the same gradients again and stepping.
+    Algorithmic HBM bytes per call: 28 per parameter (p, m, v read and
+    written, g read or, for a source, written) plus each source's operands
+    read once (split partials; an outer product's input and output gradient)."""
     from ttrl_amd import _lib
-    from ttrl_amd.algos.dqn import _lockstep_layers
-    from ttrl_amd.engine.tensor import DeviceArray
+    from ttrl_amd.engine.pending import take_sources, take_sums
 
-    B, K, F, A = 32, 3136, 512, 6
-    rng = np.random.default_rng(5)
-
-    def arr(shape, values=None):
-        a = DeviceArray(dev, shape)
-        a.upload((rng.standard_normal(shape) if values is None else values).astype(np.float32))
-        return a
-
-    online = _lockstep_layers([learner.online])[0][-3:]
-    target = _lockstep_layers([learner.target])[0][-3:]
-    sets = [online, online, target]
-    feats = [arr((B, K), np.maximum(rng.standard_normal((B, K)), 0.0)) for _ in range(3)]
-    hs = [DeviceArray(dev, (B, F)) for _ in range(3)]
-    qs = [DeviceArray(dev, (B, A)) for _ in range(3)]
-    onehot = np.zeros((B, A), np.float32)
-    onehot[np.arange(B), rng.integers(0, A, B)] = 1.0
-    keep = [arr((B, A), onehot), arr((B, 1)), arr((B, 1), (rng.random((B, 1)) < 0.1).astype(np.float32)),
-            arr((B, 1), np.full((B, 1), 0.99 ** 3)), arr((B, 1), rng.random((B, 1)))]
-    outs = {n: DeviceArray(dev, shape) for n, shape in (("loss", (1, 1)), ("mean_q", (1, 1)), ("td_abs", (B, 1)),
-                                                          ("dq", (B, A)), ("next", (B, 1)), ("y", (B, 1)),
-                                                          ("dh", (B, F)), ("terms", (B, 2)))}
-    d = _lib.DqnTailDesc()
-    d.B, d.K, d.F, d.A, d.groups = B, K, F, A, 3
-    for g, (fc1, _, fc2) in enumerate(sets):
-        d.x[g], d.W1[g], d.b1[g] = feats[g].ptr, fc1.weight.data.ptr, fc1.bias.data.ptr
-        d.h[g], d.W2[g], d.b2[g], d.q[g] = hs[g].ptr, fc2.weight.data.ptr, fc2.bias.data.ptr, qs[g].ptr
-    d.actions_onehot, d.rewards, d.dones, d.discounts, d.is_weights = (k.ptr for k in keep)
-    d.delta = 1.0
-    d.loss, d.mean_q, d.td_abs, d.dq = outs["loss"].ptr, outs["mean_q"].ptr, outs["td_abs"].ptr, outs["dq"].ptr
-    d.next_actions, d.td_target, d.dh = outs["next"].ptr, outs["y"].ptr, outs["dh"].ptr
-    d.dW2, d.db2, d.beta_w, d.loss_terms = None, None, 0.0, outs["terms"].ptr
+    opt = learner.optimizer
+    opt.zero_grad()
+    learner._step_fn(learner.inputs)
+    sources = take_sources(opt.params)
+    sums = take_sums(dev)
+    d, arrays = opt._sources_desc(sources, sums)
 
     def launch():
-        dev.call("ttrl_dqn_tail", C.byref(d))
+        dev.call("ttrl_adam_step_sources", C.byref(d))
 
     for _ in range(10):
         launch()
@@ -404,14 +377,25 @@ def dominant_kernel(dev, learner, reps=200):
     for _ in range(reps):
         launch()
     dev.call("ttrl_timer_stop", C.byref(ms))
+    dev.synchronize()
+    for p in sources:
+        p.release()
     sec = ms.value / 1e3 / reps
-    flops = 3 * 2.0 * B * K * F + 3 * 2.0 * B * F * A + 2.0 * B * F * A
-    algo_bytes = 4 * (3 * B * K + 2 * (K * F + F) + 3 * B * F + B * F)
-    return {"name": "ttrl_dqn_tail: fc1 3 x (32x3136 @ 3136x512) split-K GEMM + k_dqn_tail (split sums, Q head "
-                    "512->6, double-DQN Huber rows, gradient into fc1), batch 32",
-            "kernels": ["k_gemm<..., LdRowK, LdColK, EpStore> (tile and split from the plan table, partials left "
-                        "for the tail)", "k_dqn_tail<8, SP> (SP: split partials per batch)"],
-            "seconds": sec, "bytes": algo_bytes, "flops": flops}
+    operands = 0
+    for p in sources:
+        s = p.source
+        if s.kind == _lib.GRAD_SPLITS:
+            operands += 4 * s.splits * (s.rows + (1 if s.db else 0)) * s.cols
+        else:
+            operands += 4 * s.batch * (s.rows + s.cols)
+    n = opt.arena.numel
+    kinds = sorted(f"{p.source.rows}x{p.source.cols} {'split-K' if p.source.kind == _lib.GRAD_SPLITS else 'outer'}"
+                   for p in sources)
+    return {"name": f"ttrl_adam_step_sources: Adam over the {n:,}-float DQN arena forming {len(sources)} pending "
+                    f"gradients ({', '.join(kinds)}), batch 32",
+            "kernels": ["k_adam_src (one launch: sources' workgroups, then the plain float4s)",
+                        "k_finish_sums (update count, sum of g^2, loss and mean Q)"],
+            "seconds": sec, "bytes": 28 * n + operands, "flops": 0.0}
 
 
 def pcie_inclusive(dev, learner, n=100):
@@ -630,7 +614,7 @@ def main() -> int:
     sac_value = args.steps / swall
     sflops = sac_update_flops(256)
     dom = dominant_kernel(dev, dqn)
-    achieved = dom["flops"] / dom["seconds"]
+    achieved = dom["bytes"] / dom["seconds"]
     ppo = bench_ppo(dev, args.ppo_updates, args.mode) if args.ppo_updates > 0 else None
     rppo = bench_rppo(dev, max(1, args.ppo_updates // 2), args.mode) if args.ppo_updates > 0 else None
     replay = bench_replay(dev, args.replay_reps, not args.no_cpu_baseline) if args.replay_reps > 0 else None
@@ -663,10 +647,10 @@ def main() -> int:
                 "ms_per_step": round(swall / args.steps * 1e3, 5), "gpu_ms_per_step": sgpu / args.steps * 1e3,
                 "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA,
                 "copy_in_each_step": sac_copied},
-        "roofline": {"bound": "mfma", "kernel": dom["name"], "kernels": dom["kernels"], "achieved": achieved / 1e12,
-                     "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
-                     "traffic": DQN_TAIL_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],
-                     "hbm_frac": dom["bytes"] / dom["seconds"] / PEAK_HBM, "avg_us": dom["seconds"] * 1e6},
+        "roofline": {"bound": "hbm", "kernel": dom["name"], "kernels": dom["kernels"], "achieved": achieved / 1e9,
+                     "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved / PEAK_HBM,
+                     "traffic": ADAM_STEP_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],
+                     "avg_us": dom["seconds"] * 1e6},
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},

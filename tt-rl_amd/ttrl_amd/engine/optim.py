@@ -174,15 +174,21 @@ class Adam(Optimizer):
             self.device.pending_sums.extend(sums[MAX_SUMS:])
             settle_sums(self.device)
             sums = sums[:MAX_SUMS]
+        d, _arrays = self._sources_desc(sources, sums)
+        self.device.call("ttrl_adam_step_sources", C.byref(d))
+        for p in sources:
+            p.release()
+
+    def _sources_desc(self, sources, sums):
+        """-> (the AdamSourcesDesc of an arena step forming `sources` and the
+        ordered `sums`, the ctypes arrays it points to)."""
         a = self.arena
         srcs = (_lib.GradSource * max(1, len(sources)))(*[p.source for p in sources])
         osums = (_lib.OrderedSum * max(1, len(sums)))(*[s for s, _ in sums])
         d = _lib.AdamSourcesDesc(a.data.ptr, a.grad.ptr, self._m_flat.ptr, self._v_flat.ptr, a.numel,
                                  self._counter(len(self.params)).value, self.lr, self.b1, self.b2, self.eps,
                                  self.weight_decay, self.grad_sq.ptr, 0, len(sources), srcs, len(sums), osums)
-        self.device.call("ttrl_adam_step_sources", C.byref(d))
-        for p in sources:
-            p.release()
+        return d, (srcs, osums)
 
     # -- deferred steps ------------------------------------------------------
 
