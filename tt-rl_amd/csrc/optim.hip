@@ -30,7 +30,8 @@ constexpr int kOptMaxBlocks = 1024;
 float* ctx_workspace(ttrl_ctx* ctx, long* floats);
 
 // The step's fused scalars (alpha_t, eps_t) from the update count *step + 1,
-// computed once per workgroup.
+// computed once per workgroup by thread 0 (its loads issued before the call
+// stay in flight while it does).
 __device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float lr, float b1, float b2, float eps,
                                              float* alpha_t, float* eps_t) {
   __shared__ float sc[2];
@@ -405,28 +406,37 @@ __device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const Outer
   return acc;
 }
 
-// A tile's slices in LDS: us[b][i] = u[b][r0 + i] (rows past the block
-// repeat its last row, never used), vs[b][j] = v[b][c0 + j].  Every load is
-// issued before the first store.
-__device__ __forceinline__ void stage_outer_tile(const GradSrc& s, int r0, int c0, float* us, float* vs) {
+// A tile's slices: loaded into registers (issue_outer_tile), then written
+// to LDS (commit_outer_tile): us[b][i] = u[b][r0 + i] (rows past the block
+// repeat its last row, never used), vs[b][j] = v[b][c0 + j].  Work that does
+// not need them can run between the two while the loads are in flight.
+struct OuterTileLoads {
+  float u[kTileBatch * kTileRows / kOptThreads];
+  f32x4 v[kTileBatch * kTileCols / 4 / kOptThreads];
+};
+__device__ __forceinline__ OuterTileLoads issue_outer_tile(const GradSrc& s, int r0, int c0) {
   constexpr int NU = kTileBatch * kTileRows / kOptThreads, NV = kTileBatch * kTileCols / 4 / kOptThreads;
   const int tid = threadIdx.x;
-  float u[NU];
-  f32x4 v[NV];
+  OuterTileLoads l;
 #pragma unroll
   for (int k = 0; k < NU; ++k) {
     const int e = tid + k * kOptThreads, b = e / kTileRows, i = e - b * kTileRows;
-    u[k] = b < s.batch ? s.u[long(b) * s.rows + min(r0 + i, s.rows - 1)] : 0.f;
+    l.u[k] = b < s.batch ? s.u[long(b) * s.rows + min(r0 + i, s.rows - 1)] : 0.f;
   }
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int e = tid + k * kOptThreads, b = e / (kTileCols / 4), j = e - b * (kTileCols / 4);
-    v[k] = b < s.batch ? *reinterpret_cast<const f32x4*>(s.v + long(b) * s.cols + c0 + 4 * j) : f32x4{};
+    l.v[k] = b < s.batch ? *reinterpret_cast<const f32x4*>(s.v + long(b) * s.cols + c0 + 4 * j) : f32x4{};
   }
+  return l;
+}
+__device__ __forceinline__ void commit_outer_tile(const OuterTileLoads& l, float* us, float* vs) {
+  constexpr int NU = kTileBatch * kTileRows / kOptThreads, NV = kTileBatch * kTileCols / 4 / kOptThreads;
+  const int tid = threadIdx.x;
 #pragma unroll
-  for (int k = 0; k < NU; ++k) us[tid + k * kOptThreads] = u[k];
+  for (int k = 0; k < NU; ++k) us[tid + k * kOptThreads] = l.u[k];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) reinterpret_cast<f32x4*>(vs)[tid + k * kOptThreads] = v[k];
+  for (int k = 0; k < NV; ++k) reinterpret_cast<f32x4*>(vs)[tid + k * kOptThreads] = l.v[k];
   __syncthreads();
 }
 // The thread's kTileOuts float4s (tile rows tr + kTileBand * o, float4
@@ -521,6 +531,12 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
       // a tile (kTileOuts float4s per thread, both slices staged) or a bias block
       const TileSpot t = tile_spot(s, blk - s.block0);
       const int nout = t.weight ? kTileOuts : 1;
+      // the operand slices' loads first, the scalars formed while they are in
+      // flight, then the parameters' and moments' loads under the slices' LDS
+      // writes and the sums
+      OuterTileLoads tl;
+      if (t.weight) tl = issue_outer_tile(s, t.r0, t.c0);
+      adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
       long i[kTileOuts];
       f32x4 pv[kTileOuts] = {}, sv[kTileOuts] = {}, vv[kTileOuts] = {};
 #pragma unroll
@@ -532,8 +548,7 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
           vv[o] = Vv[i[o]];
         }
       }
-      if (t.weight) stage_outer_tile(s, t.r0, t.c0, us, vs);
-      adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+      if (t.weight) commit_outer_tile(tl, us, vs);
       f32x4 gv[kTileOuts];
       if (t.weight) {
         outer_grad_tile(s, us, vs, t.tr, t.tc4, gv);
@@ -635,7 +650,7 @@ __global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
   if (s.tiled) {
     const TileSpot t = tile_spot(s, blk - s.block0);
     if (t.weight) {
-      stage_outer_tile(s, t.r0, t.c0, us, vs);
+      commit_outer_tile(issue_outer_tile(s, t.r0, t.c0), us, vs);
       f32x4 gv[kTileOuts];
       outer_grad_tile(s, us, vs, t.tr, t.tc4, gv);
 #pragma unroll
