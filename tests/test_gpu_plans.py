@@ -87,3 +87,42 @@ def test_plan_table_text_round_trip_and_invalid_plans(device, monkeypatch):
         assert all(fixed[k] != "0 32 32 256 9 256" for k in used)
     finally:
         other.close()
+
+
+CHILD_UPDATES = r"""
+import sys
+sys.path[:0] = [{root!r}, {pkg!r}]
+from ttrl_amd.engine.device import acquire
+from tests._dqn_helpers import build_learner
+from tests._sac_helpers import build_sac
+from ttrl_amd.workloads import dqn_batch, sac_batch
+dev = acquire(0)
+dqn, _, _ = build_learner(dev, seed=1)
+dqn.update(dqn_batch(1))
+sac, _, _ = build_sac(dev, seed=1)
+sac.update(sac_batch(1))
+sac.update(sac_batch(2))
+dev.save_plans({plans!r})
+print("child done", flush=True)
+"""
+
+
+def test_the_learner_updates_find_every_plan_in_the_packaged_table(tmp_path):
+    """The DQN update at batch 32 and the SAC update at batch 256 (graph
+    mode, the learners' defaults) call no GEMM signature the packaged table
+    lacks: no process times candidates and picks plans of its own, so every
+    process sums split partials in the same order."""
+    packaged = ROOT / "tt-rl_amd" / "ttrl_amd" / "plans" / "gfx950.tsv"
+    plans = tmp_path / "after.tsv"
+    code = CHILD_UPDATES.format(root=str(ROOT), pkg=str(ROOT / "tt-rl_amd"), plans=str(plans))
+    env = {k: v for k, v in os.environ.items() if k != "TTRL_PLANS"}  # the packaged table
+    proc = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=240)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+
+    def entries(text):
+        return {line.split("\t", 1)[1]: line.split("\t", 1)[0] for line in text.splitlines() if "\t" in line}
+
+    before, after = entries(packaged.read_text()), entries(plans.read_text())
+    extra = sorted(set(after) - set(before))
+    assert not extra, "signatures missing from the packaged table:\n" + "\n".join(k[-120:] for k in extra)
+    assert all(after[k] == before[k] for k in after)
