@@ -362,6 +362,30 @@ int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* desc);
  * softplus correction (ttrl/algos/gaussian.py:55-117) minus log_det. */
 int ttrl_sac_sample(ttrl_ctx* ctx, int B, int d, const float* head, const float* noise, const float* centre,
                     const float* half_width, float log_det, float* action, float* logp, float* u_out);
+/* GaussianHead.forward (ttrl/nets/heads.py:65-93: mean and log_std Linear
+ * layers, log_std clamped to [lo, hi]) and the squashed sample above in one
+ * launch (the acting kernel of ttrl_gaussian_act), over rows of x
+ * ([rows][K]); W1, W2 are [K][d] with d <= 16, b1/b2 may be NULL.  Writes
+ * head [rows][2d] = [mean | log_std] and u, which the sample's backward
+ * takes, with action and logp. */
+typedef struct ttrl_sac_head_desc {
+  int rows, K, d;
+  const float* x;
+  const float* W1;
+  const float* b1;
+  const float* W2;
+  const float* b2;
+  float lo, hi;
+  const float* noise;
+  const float* centre;
+  const float* half_width;
+  float log_det;
+  float* head;
+  float* action;
+  float* logp;
+  float* u;
+} ttrl_sac_head_desc;
+int ttrl_sac_head_sample(ttrl_ctx* ctx, const ttrl_sac_head_desc* desc);
 /* Its backward to d_head ([B][2d]), given dL/daction (g_action0 + g_action1,
  * either may be NULL) and dL/dlogp per row; the log_std clamp passes
  * gradient strictly inside (log_std_min, log_std_max) (ttrl/engine/ops/select.py:26-29). */

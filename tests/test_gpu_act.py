@@ -113,6 +113,60 @@ def test_gaussian_act_kernel_matches_oracle(device, B, K, d, det):
         assert _rel(logp.numpy(), lp_ref) < 1e-5
 
 
+@pytest.mark.parametrize("rows,K,d", [(512, 256, 3), (37, 100, 1), (9, 128, 16)])
+def test_sac_head_sample_matches_oracle_and_acting_launch(device, rows, K, d):
+    """ttrl_sac_head_sample (the learner's policy head and sample) against
+    the float64 oracle at rel 1e-5, with the pre-squash u the sample's
+    backward takes; head, action and logp bit-identical to
+    ttrl_gaussian_act's, the same kernel."""
+    from oracle import gaussian
+    from ttrl_amd import _lib
+    from ttrl_amd.engine.tensor import DeviceArray, to_device
+
+    rng = np.random.default_rng(rows * 3 + K + d)
+    x = np.maximum(rng.standard_normal((rows, K)), 0).astype(np.float32)
+    Wm = (rng.standard_normal((K, d)) / np.sqrt(K)).astype(np.float32)
+    Ws = (rng.standard_normal((K, d)) / np.sqrt(K)).astype(np.float32)
+    bm = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    bs = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    lo, hi = -5.0, 1.0
+    bs[0] = 40.0  # log_std column 0 in the upper clamp
+    noise = rng.standard_normal((rows, d)).astype(np.float32)
+    centre = rng.uniform(-0.5, 0.5, d).astype(np.float32)
+    half = rng.uniform(0.5, 2.0, d).astype(np.float32)
+    log_det = float(np.sum(np.log(half.astype(np.float64))))
+    dv = {k: to_device(v, device) for k, v in dict(x=x, Wm=Wm, Ws=Ws, bm=bm, bs=bs, noise=noise, c=centre,
+                                                      hw=half).items()}
+    out = {k: DeviceArray(device, shape) for k, shape in (("head", (rows, 2 * d)), ("action", (rows, d)),
+                                                          ("logp", (rows,)), ("u", (rows, d)))}
+    desc = _lib.SacHeadDesc()
+    desc.rows, desc.K, desc.d = rows, K, d
+    desc.x, desc.W1, desc.b1, desc.W2, desc.b2 = (dv[k].ptr for k in ("x", "Wm", "bm", "Ws", "bs"))
+    desc.lo, desc.hi = lo, hi
+    desc.noise, desc.centre, desc.half_width, desc.log_det = dv["noise"].ptr, dv["c"].ptr, dv["hw"].ptr, log_det
+    desc.head, desc.action, desc.logp, desc.u = (out[k].ptr for k in ("head", "action", "logp", "u"))
+    device.call("ttrl_sac_head_sample", C.byref(desc))
+    x64 = x.astype(np.float64)
+    mean = x64 @ Wm.astype(np.float64) + bm
+    log_std = np.clip(x64 @ Ws.astype(np.float64) + bs, lo, hi)
+    a_ref, lp_ref, u_ref = gaussian.sample(mean, log_std, noise, centre, half, log_det)
+    got = {k: v.numpy() for k, v in out.items()}
+    assert _rel(got["head"][:, :d], mean) < 1e-5
+    assert _rel(got["head"][:, d:], log_std) < 1e-5
+    assert _rel(got["action"], a_ref) < 1e-5
+    assert _rel(got["logp"], lp_ref) < 1e-5
+    assert _rel(got["u"], u_ref) < 1e-5
+    act = {k: DeviceArray(device, out[k].shape) for k in ("head", "action", "logp")}
+    device.call("ttrl_gaussian_act", rows, K, d, dv["x"].ptr, dv["Wm"].ptr, dv["bm"].ptr, dv["Ws"].ptr,
+                dv["bs"].ptr, C.c_float(lo), C.c_float(hi), dv["noise"].ptr, dv["c"].ptr, dv["hw"].ptr,
+                C.c_float(log_det), 0, act["head"].ptr, act["action"].ptr, act["logp"].ptr)
+    for k in act:
+        assert np.array_equal(act[k].numpy(), got[k]), k
+    desc.d = 17
+    with pytest.raises(ValueError, match="at most 16 action dimensions"):
+        device.call("ttrl_sac_head_sample", C.byref(desc))
+
+
 @pytest.mark.parametrize("mode", ["graph", "eager"])
 def test_acting_net_matches_deploy_forward_and_full_width(device, mode):
     from oracle.nets import qnet_forward

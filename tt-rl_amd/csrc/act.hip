@@ -9,7 +9,9 @@
 //             (ttrl/nets/heads.py:65-93), then the tanh-squashed Gaussian
 //             action and its log-density at host-drawn noise, or tanh(mean)
 //             with logp 0 when deterministic (ttrl/algos/sac/policy.py:42-59,
-//             ttrl/algos/gaussian.py:106-167)
+//             ttrl/algos/gaussian.py:106-167); the learner's policy head
+//             takes the same launch with the pre-squash u kept for its
+//             backward (ttrl_sac_head_sample)
 //
 // One wavefront per lane row.  Lane l accumulates columns k = l, l+64, ... of
 // the row's dot products with every output column; the 64 partial sums of
@@ -26,6 +28,7 @@ namespace {
 constexpr int kActThreads = 256;  // four wavefronts, four lane rows per workgroup
 constexpr int kActRows = kActThreads / 64;
 constexpr int kActMaxN = 32;
+constexpr int kActDepth = 4;  // columns per lane whose loads are in flight together
 constexpr float kActLog2 = 0.69314718055994530942f;
 constexpr float kActLog2Pi = 1.83787706640934548356f;
 
@@ -49,6 +52,7 @@ struct ActArgs {
   float* head;    // squashed: [B][2 n1] = [mean | clamped log_std] or null
   float* action;  // squashed: [B][n1]
   float* logp;    // squashed: [B]
+  float* u;       // squashed: [B][n1] pre-squash sample, or null
 };
 
 __device__ __forceinline__ float softplus_act(float x) {
@@ -66,7 +70,41 @@ __global__ __launch_bounds__(kActThreads) void k_head_act(ActArgs a) {
   float acc[NP];
 #pragma unroll
   for (int n = 0; n < NP; ++n) acc[n] = 0.f;
-  for (int k = lane; k < a.K; k += 64) {
+  // The squashed sample's per-lane inputs (lane i < n1 owns action
+  // dimension i, its mean and log_std biases among them), loaded ahead of
+  // the dot products so their latency overlaps them.
+  const int own = lane < n1 ? lane : n1 - 1;
+  float noise_v = 0.f, half_v = 0.f, centre_v = 0.f, bias_mu = 0.f, bias_ls = 0.f;
+  if constexpr (MODE == ActMode::Squashed) {
+    if (!a.deterministic) noise_v = a.noise[long(b) * n1 + own];
+    half_v = a.half_width[own];
+    centre_v = a.centre[own];
+    if (a.b1) bias_mu = a.b1[own];
+    if (a.b2) bias_ls = a.b2[own];
+  }
+  // kActDepth columns per lane in flight at once: a round's loads are all
+  // issued before its products, so a row pays one memory latency per
+  // 64 * kActDepth columns; the columns past the last whole round follow
+  // one at a time.  Each lane sums its columns in ascending k.
+  int k0 = lane;
+  for (; k0 + 64 * (kActDepth - 1) < a.K; k0 += 64 * kActDepth) {
+    float x[kActDepth], w[kActDepth][NP];
+#pragma unroll
+    for (int r = 0; r < kActDepth; ++r) {
+      const int k = k0 + 64 * r;
+      x[r] = hb[k];
+      const float* w1 = a.W1 + long(k) * n1;
+      const float* w2 = a.W2 + long(k) * n2;
+#pragma unroll
+      for (int n = 0; n < NP; ++n) w[r][n] = n < n1 ? w1[n] : n < N ? w2[n - n1] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < kActDepth; ++r)
+#pragma unroll
+      for (int n = 0; n < NP; ++n)
+        if (n < N) acc[n] += x[r] * w[r][n];
+  }
+  for (int k = k0; k < a.K; k += 64) {
     const float x = hb[k];
     const float* w1 = a.W1 + long(k) * n1;
     const float* w2 = a.W2 + long(k) * n2;
@@ -81,13 +119,13 @@ __global__ __launch_bounds__(kActThreads) void k_head_act(ActArgs a) {
 #pragma unroll
     for (int n = 0; n < NP; ++n) acc[n] += __shfl_xor(acc[n], off);
   }
-  // Every lane now holds the same sums; add the bias.
-#pragma unroll
-  for (int n = 0; n < NP; ++n) {
-    if (n < n1) acc[n] += a.b1 ? a.b1[n] : 0.f;
-    else if (n < N) acc[n] += a.b2 ? a.b2[n - n1] : 0.f;
-  }
+  // Every lane now holds the same sums.
   if constexpr (MODE == ActMode::Greedy) {
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      if (n < n1) acc[n] += a.b1 ? a.b1[n] : 0.f;
+      else if (n < N) acc[n] += a.b2 ? a.b2[n - n1] : 0.f;
+    }
     float mine = 0.f;
 #pragma unroll
     for (int n = 0; n < NP; ++n) mine = lane == n ? acc[n] : mine;
@@ -112,6 +150,8 @@ __global__ __launch_bounds__(kActThreads) void k_head_act(ActArgs a) {
       mu = lane == n ? acc[n] : mu;
       lsr = lane + d == n ? acc[n] : lsr;
     }
+    mu += bias_mu;
+    lsr += bias_ls;
     float normal = 0.f, corr = 0.f;
     if (lane < d) {
       const float ls = fminf(fmaxf(lsr, a.lo), a.hi);
@@ -124,13 +164,14 @@ __global__ __launch_bounds__(kActThreads) void k_head_act(ActArgs a) {
         t = tanhf(mu);
       } else {
         const float sigma = expf(ls);
-        const float u = mu + sigma * a.noise[long(b) * d + lane];
+        const float u = mu + sigma * noise_v;
+        if (a.u) a.u[long(b) * d + lane] = u;
         const float z = (u - mu) / sigma;
         normal = (z * z) * -0.5f - ls;
         corr = ((kActLog2 - u) - softplus_act(u * -2.f)) * 2.f;
         t = tanhf(u);
       }
-      a.action[long(b) * d + lane] = t * a.half_width[lane] + a.centre[lane];
+      a.action[long(b) * d + lane] = t * half_v + centre_v;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -213,6 +254,40 @@ int ttrl_gaussian_act(ttrl_ctx* ctx, int B, int K, int d, const float* h, const 
   a.action = action;
   a.logp = logp;
   return launch_head_act<ActMode::Squashed>(ctx, a, 2 * d, "ttrl_gaussian_act");
+}
+
+int ttrl_sac_head_sample(ttrl_ctx* ctx, const ttrl_sac_head_desc* d) {
+  TTRL_REQUIRE(ctx && d, "ttrl_sac_head_sample: null argument");
+  TTRL_REQUIRE(d->x && d->W1 && d->W2 && d->noise && d->centre && d->half_width && d->head && d->action &&
+                   d->logp && d->u,
+               "ttrl_sac_head_sample: null buffer");
+  TTRL_REQUIRE(d->rows >= 0 && d->K > 0 && d->d > 0, "ttrl_sac_head_sample: bad extents (rows=%d, K=%d, d=%d)",
+               d->rows, d->K, d->d);
+  TTRL_REQUIRE(2 * d->d <= kActMaxN, "ttrl_sac_head_sample: at most %d action dimensions, got %d", kActMaxN / 2,
+               d->d);
+  TTRL_REQUIRE(d->lo < d->hi, "ttrl_sac_head_sample: log_std_min must be < log_std_max");
+  if (d->rows == 0) return TTRL_OK;
+  ActArgs a{};
+  a.B = d->rows;
+  a.K = d->K;
+  a.N = 2 * d->d;
+  a.n1 = d->d;
+  a.h = d->x;
+  a.W1 = d->W1;
+  a.b1 = d->b1;
+  a.W2 = d->W2;
+  a.b2 = d->b2;
+  a.lo = d->lo;
+  a.hi = d->hi;
+  a.noise = d->noise;
+  a.centre = d->centre;
+  a.half_width = d->half_width;
+  a.log_det = d->log_det;
+  a.head = d->head;
+  a.action = d->action;
+  a.logp = d->logp;
+  a.u = d->u;
+  return launch_head_act<ActMode::Squashed>(ctx, a, 2 * d->d, "ttrl_sac_head_sample");
 }
 
 }  // extern "C"

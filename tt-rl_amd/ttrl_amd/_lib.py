@@ -85,6 +85,17 @@ class DqnTailDesc(C.Structure):
     ]
 
 
+class SacHeadDesc(C.Structure):
+    """Mirror of ttrl_sac_head_desc."""
+
+    _fields_ = [
+        ("rows", C.c_int), ("K", C.c_int), ("d", C.c_int), ("x", C.c_void_p), ("W1", C.c_void_p),
+        ("b1", C.c_void_p), ("W2", C.c_void_p), ("b2", C.c_void_p), ("lo", C.c_float), ("hi", C.c_float),
+        ("noise", C.c_void_p), ("centre", C.c_void_p), ("half_width", C.c_void_p), ("log_det", C.c_float),
+        ("head", C.c_void_p), ("action", C.c_void_p), ("logp", C.c_void_p), ("u", C.c_void_p),
+    ]
+
+
 GRAD_NONE, GRAD_SPLITS, GRAD_OUTER = 0, 1, 2
 
 
@@ -195,6 +206,7 @@ SIGNATURES = {
     "ttrl_dqn_head": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, F, P, P, P, P, P, P], I),
     "ttrl_dqn_tail": ([P, C.POINTER(DqnTailDesc)], I),
     "ttrl_sac_sample": ([P, I, I, P, P, P, P, F, P, P, P], I),
+    "ttrl_sac_head_sample": ([P, C.POINTER(SacHeadDesc)], I),
     "ttrl_q_act": ([P, I, I, I, P, P, P, P, P], I),
     "ttrl_gru_step": ([P, I, I, P, P, P, P, P, P], I),
     "ttrl_gru_mask": ([P, I, I, P, P, P], I),

@@ -203,6 +203,16 @@ def squashed_sample_rows(head: Tensor, head_all: DeviceArray, noise_all: DeviceA
     dev = head_all.dev
     action_all = DeviceArray(dev, (rows, d))
     u = _sample_launch(head_all, noise_all, scale, action_all, logp_all.reshape((rows, 1)))
+    return sampled_rows_tape(head, action_all, logp_all, noise_all, u, scale, log_std_min, log_std_max)
+
+
+def sampled_rows_tape(head: Tensor, action_all: DeviceArray, logp_all: DeviceArray, noise_all: DeviceArray,
+                      u: DeviceArray, scale: ActionScale, log_std_min: float, log_std_max: float):
+    """The tape of a sample already taken over every row (action_all,
+    logp_all, the pre-squash u), over its first B rows (`head`'s).
+    -> as squashed_sample_rows."""
+    B = int(head.shape[0])
+    rows, d = (int(s) for s in action_all.shape)
     action = action_all.view(0, (B, d))
     logp = logp_all.view(0, (B, 1))
     rest = (action_all.view(B * d, (rows - B, d)), logp_all.view(B, (rows - B, 1)))

@@ -28,7 +28,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ttrl_amd import _lib
-from ttrl_amd.algos.gaussian import ActionScale, squashed_sample, squashed_sample_rows
+from ttrl_amd.algos.gaussian import ActionScale, sampled_rows_tape, squashed_sample, squashed_sample_rows
 from ttrl_amd.algos.state import TOWERS_SAC, assemble, from_reference_keys, to_reference_keys, validate
 from ttrl_amd.buffers.replay import PriorityConfig
 from ttrl_amd.nets.acting import ActingNet, SquashedDecision
@@ -43,7 +43,7 @@ from ttrl_amd.engine.step import InputBinder, MetricReader
 from ttrl_amd.engine.tensor import DeviceArray, ParamArena, bound_block
 from ttrl_amd.engine.trace import capture
 from ttrl_amd.nets.build import build_sac_nets
-from ttrl_amd.nets.heads import GaussianHead, packed_linear_pair_rows
+from ttrl_amd.nets.heads import GaussianHead, packed_linear_pair_rows, packed_tape
 
 __all__ = ["SACConfig", "SACLearner", "TwinQ", "sac_critic_loss", "sac_actor_losses"]
 
@@ -391,14 +391,11 @@ def _linear_relu_pairs(encoder):
     return [lin for lin, _ in pairs]
 
 
-def policy_rows(policy, obs_all: DeviceArray, B: int):
-    """The policy over every row of obs_all, one launch per layer, with the
-    tape over its first B rows (the actor's observations; the rest are the
-    soft target's next observations, constants of the update).
-    -> (packed head rows on the tape (B, 2d), packed head of every row)."""
-    head = policy.head
+def _encoder_rows(policy, obs_all: DeviceArray, B: int):
+    """The policy's encoder over every row of obs_all, one launch per layer,
+    the tape over its first B rows.  -> (tape node, output of every row)."""
     lins = _linear_relu_pairs(policy.encoder)
-    if not isinstance(head, GaussianHead) or lins is None:
+    if not isinstance(policy.head, GaussianHead) or lins is None:
         raise ValueError("policy_rows: needs an MLP encoder of Linear -> ReLU pairs and a GaussianHead")
     rows = int(obs_all.shape[0])
     dev = obs_all.dev
@@ -418,8 +415,59 @@ def policy_rows(policy, obs_all: DeviceArray, B: int):
             layers_mod.RECORD.append(y_all)
         x = linear_node(x, w, lin.bias, y_all.view(0, (B, N)), relu=True)
         x_all = y_all
+    return x, x_all
+
+
+def policy_rows(policy, obs_all: DeviceArray, B: int):
+    """The policy over every row of obs_all, one launch per layer, with the
+    tape over its first B rows (the actor's observations; the rest are the
+    soft target's next observations, constants of the update).
+    -> (packed head rows on the tape (B, 2d), packed head of every row)."""
+    head = policy.head
+    x, x_all = _encoder_rows(policy, obs_all, B)
     return packed_linear_pair_rows(head.heads["mean"], head.heads["log_std"], x, x_all,
                                    clamp=(head.log_std_min, head.log_std_max), op="gaussian_head")
+
+
+HEAD_SAMPLE_MAX_D = 16  # action dimensions ttrl_sac_head_sample takes
+
+
+def policy_sample_rows(policy, obs_all: DeviceArray, B: int, noise_all: DeviceArray, scale: ActionScale,
+                       logp_all: DeviceArray):
+    """policy_rows followed by squashed_sample_rows, the Gaussian head and the
+    sample in one launch (ttrl_sac_head_sample) where its shapes allow.
+    -> (action, logp) tensors of the first B rows and (action, logp) arrays
+    of the rest; `logp_all` receives every row's log-probability."""
+    head = policy.head
+    mean, log_std = head.heads["mean"], head.heads["log_std"]
+    x, x_all = _encoder_rows(policy, obs_all, B)
+    rows, K = (int(s) for s in x_all.shape)
+    d = head.action_dim
+    if d > HEAD_SAMPLE_MAX_D or mean.bias is None or log_std.bias is None:
+        h, h_all = packed_linear_pair_rows(mean, log_std, x, x_all, clamp=(head.log_std_min, head.log_std_max),
+                                           op="gaussian_head")
+        return squashed_sample_rows(h, h_all, noise_all, scale, logp_all, head.log_std_min, head.log_std_max)
+    if tuple(noise_all.shape) != (rows, d) or logp_all.numel != rows or rows <= B:
+        raise ValueError(f"policy_sample_rows: noise {noise_all.shape} and logp ({logp_all.numel}) must hold "
+                         f"{rows} rows of {d}, more than B = {B}")
+    if scale._centre is None:
+        raise ValueError("squashed_sample needs the device-resident bounds; construct ActionScale with a device")
+    dev = x_all.dev
+    head_all = DeviceArray(dev, (rows, 2 * d))
+    action_all = DeviceArray(dev, (rows, d))
+    u = DeviceArray(dev, (rows, d))
+    desc = _lib.SacHeadDesc()
+    desc.rows, desc.K, desc.d = rows, K, d
+    desc.x = x_all.ptr
+    desc.W1, desc.b1 = mean.weight.data.ptr, mean.bias.data.ptr
+    desc.W2, desc.b2 = log_std.weight.data.ptr, log_std.bias.data.ptr
+    desc.lo, desc.hi = head.log_std_min, head.log_std_max
+    desc.noise, desc.centre, desc.half_width = noise_all.ptr, scale._centre.data.ptr, scale._scale.data.ptr
+    desc.log_det = scale.log_det
+    desc.head, desc.action, desc.logp, desc.u = head_all.ptr, action_all.ptr, logp_all.ptr, u.ptr
+    dev.call("ttrl_sac_head_sample", C.byref(desc))
+    h = packed_tape(mean, log_std, x, head_all.view(0, (B, 2 * d)), "gaussian_head")
+    return sampled_rows_tape(h, action_all, logp_all, noise_all, u, scale, head.log_std_min, head.log_std_max)
 
 
 class _BatchBuffers:
@@ -594,9 +642,8 @@ class SACLearner:
         step leaves the policy unchanged, so the actor's forward can run with
         the soft target's.  -> (action, logp) on the tape, (a_next, logp_next)."""
         b = self.batch
-        head, head_all = policy_rows(self.nets.policy, b.obs_pair, b.B)
-        action, logp, (a_next, logp_next) = squashed_sample_rows(head, head_all, b.noise_pair, self.scale,
-                                                                 self._logp_all)
+        action, logp, (a_next, logp_next) = policy_sample_rows(self.nets.policy, b.obs_pair, b.B, b.noise_pair,
+                                                               self.scale, self._logp_all)
         return (action, logp), (a_next, Tensor(logp_next))
 
     def _critic_region(self, nxt=None) -> dict:

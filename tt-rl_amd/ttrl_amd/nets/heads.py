@@ -97,7 +97,7 @@ def _packed_launch(first: Linear, second: Linear, x: DeviceArray, clamp) -> Devi
     return y
 
 
-def _packed_tape(first: Linear, second: Linear, x: Tensor, y: DeviceArray, op: str) -> Tensor:
+def packed_tape(first: Linear, second: Linear, x: Tensor, y: DeviceArray, op: str) -> Tensor:
     """The tape node of a packed pair's rows: y (x's rows) computed elsewhere."""
     M, K = (int(d) for d in x.shape)
     n1 = first.out_features
@@ -140,7 +140,7 @@ def packed_linear_pair(first: Linear, second: Linear, x: Tensor, *, clamp=None, 
     """(B, n1 + n2) rows [x W1 + b1 | x W2 + b2] of two Linear layers over one
     input, from one launch; `clamp` = (lo, hi) clamps the second block in the
     epilogue.  Backward: both layers' dW and db and dx in one launch."""
-    return _packed_tape(first, second, x, _packed_launch(first, second, x.data, clamp), op)
+    return packed_tape(first, second, x, _packed_launch(first, second, x.data, clamp), op)
 
 
 def packed_linear_pair_rows(first: Linear, second: Linear, x: Tensor, x_all: DeviceArray, *, clamp=None,
@@ -152,4 +152,4 @@ def packed_linear_pair_rows(first: Linear, second: Linear, x: Tensor, x_all: Dev
         raise ValueError(f"{op}: x must view the leading rows of x_all")
     y_all = _packed_launch(first, second, x_all, clamp)
     N = int(y_all.shape[1])
-    return _packed_tape(first, second, x, y_all.view(0, (B, N)), op), y_all
+    return packed_tape(first, second, x, y_all.view(0, (B, N)), op), y_all
