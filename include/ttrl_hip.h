@@ -65,6 +65,11 @@ int ttrl_free(ttrl_ctx* ctx, void* ptr);
  * (ttrl/engine/tensor/transfer.py:11-51) and InputBinder.load
  * (ttrl/engine/step/inputs.py:28-85).  Both refuse to run during capture. */
 int ttrl_h2d(ttrl_ctx* ctx, void* dst, const void* host_src, size_t bytes);
+/* The same copy queued on the stream without waiting (InputBinder.load,
+ * ttrl/engine/step/inputs.py:28-85, as one input's part of a batch upload):
+ * host_src must lie inside one ttrl_host_alloc block and stay unchanged
+ * until the stream is next waited for (ttrl_sync, ttrl_h2d, ttrl_graph_step). */
+int ttrl_h2d_enqueue(ttrl_ctx* ctx, void* dst, const void* host_src, size_t bytes);
 int ttrl_d2h(ttrl_ctx* ctx, void* host_dst, const void* src, size_t bytes);
 /* Device copy on the stream; replaces copy_in_place (ttrl/engine/tensor/arena.py:32). */
 int ttrl_d2d(ttrl_ctx* ctx, void* dst, const void* src, size_t bytes);

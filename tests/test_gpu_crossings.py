@@ -1,9 +1,12 @@
 """Host<->device crossings of one learner update (the reference's crossing
-budget, tests/engine/test_crossing_budget.py:22-37): after the capture, an
-update from a host batch is one library call, ttrl_graph_step, which makes
-one host-to-device copy of the staged batch, replays the graph, makes one
-device-to-host copy of the packed metrics and waits once.  The metrics it
-returns equal a per-tensor read of the same device buffers."""
+budget, tests/engine/test_crossing_budget.py:22-37 and :71-92: one packed
+metrics download per update): after the capture, an update from a host
+batch queues the copy of each input of at least 256 KiB as soon as it is
+staged (ttrl_h2d_enqueue, no wait: DQN's obs and next_obs frames), then
+makes one ttrl_graph_step, which copies the rest of the staged batch in,
+replays the graph, makes one device-to-host copy of the packed metrics and
+waits once.  The metrics it returns equal a per-tensor read of the same
+device buffers."""
 
 from __future__ import annotations
 
@@ -36,7 +39,7 @@ class _Spy:
         del self.device.call
 
 
-def test_dqn_update_from_a_host_batch_is_one_call(device):
+def test_dqn_update_from_a_host_batch_is_one_step_call(device):
     from ttrl_amd.workloads import dqn_batch
 
     learner, _, _ = build_learner(device, seed=1)
@@ -45,7 +48,7 @@ def test_dqn_update_from_a_host_batch_is_one_call(device):
         for k in range(3):
             with _Spy(device) as spy:
                 m = learner.update(dqn_batch(11 + k))
-            assert spy.names == ["ttrl_graph_step"], spy.names
+            assert spy.names == ["ttrl_h2d_enqueue", "ttrl_h2d_enqueue", "ttrl_graph_step"], spy.names
             blk = learner._metric_block.numpy()
             assert m["loss"] == float(blk[0]) and m["mean_q"] == float(blk[1])
             assert m["grad_norm"] == float(np.sqrt(float(blk[2])))

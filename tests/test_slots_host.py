@@ -35,6 +35,7 @@ class _HostImage:
     def __init__(self, nbytes):
         self.buf = np.zeros(int(nbytes), np.uint8)
         self.nbytes = int(nbytes)
+        self.ptr = self.buf.ctypes.data
 
     def view(self, off, shape, dtype):
         n = int(np.prod(shape)) * np.dtype(dtype).itemsize
@@ -139,3 +140,39 @@ def test_train_step_slots_need_graph_mode_and_a_bound_block():
         bound.enable_input_slots(2)
     with pytest.raises(RuntimeError, match="run\\(\\) once first"):
         bound.replay_slot(1)
+
+
+def test_binder_queues_large_inputs_and_waits_before_restaging_them(monkeypatch):
+    """InputBinder.load: an input of at least QUEUE_MIN_BYTES is queued as
+    soon as it is staged (ttrl_h2d_enqueue) and leaves the pending ranges;
+    staging it again first waits for the stream; a flush or graph step that
+    waits clears that; small inputs stay pending for the one batch copy."""
+    from ttrl_amd.engine.step import InputBinder
+
+    dev = _Dev()
+    dev.capturing = False
+    dev.synchronize = lambda: dev.calls.append(("sync", ()))
+    inputs = _inputs(dev)
+    binder = InputBinder(dev, inputs)
+    monkeypatch.setattr(InputBinder, "QUEUE_MIN_BYTES", 16)  # obs: 16 bytes, rewards: 8
+    binder.load("obs", np.arange(16, dtype=np.uint8).reshape(2, 8))
+    assert [c[0] for c in dev.calls] == ["ttrl_h2d_enqueue"]
+    dst, src, n = (a.value for a in dev.calls[0][1])
+    assert (dst, src, n) == (inputs["_block"].ptr, binder.image.ptr, 16)
+    assert np.array_equal(binder.image.buf[:16], np.arange(16))
+    assert binder.pending() == []
+    binder.load("rewards", np.ones((2, 1), np.float32))
+    assert binder.pending() == [(256, 264)] and len(dev.calls) == 1
+    binder.load("obs", np.zeros((2, 8), np.uint8))  # its queued copy may still read the image
+    assert [c[0] for c in dev.calls] == ["ttrl_h2d_enqueue", "sync", "ttrl_h2d_enqueue"]
+    binder.flush()  # ttrl_h2d waits for the stream
+    assert dev.calls[-1][0] == "ttrl_h2d" and binder.pending() == []
+    binder.load("obs", np.ones((2, 8), np.uint8))
+    assert [c[0] for c in dev.calls[-2:]] == ["ttrl_h2d", "ttrl_h2d_enqueue"]
+    binder.synced()
+    binder.load("obs", np.ones((2, 8), np.uint8))
+    assert "sync" not in [c[0] for c in dev.calls[-2:]]
+    dev.capturing = True  # never queued during a capture
+    binder.synced()
+    binder.load("obs", np.ones((2, 8), np.uint8))
+    assert dev.calls[-1][0] == "ttrl_h2d_enqueue" and binder.pending() == [(0, 16)]

@@ -531,6 +531,21 @@ bool in_host_block(ttrl_ctx* ctx, const void* p, size_t bytes) {
 
 extern "C" {
 
+int ttrl_h2d_enqueue(ttrl_ctx* ctx, void* dst, const void* host_src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!host_src && bytes))
+    return set_error(TTRL_EINVAL, "ttrl_h2d_enqueue: null argument");
+  if (ctx->capturing)
+    return set_error(TTRL_ESTATE, "ttrl_h2d_enqueue: host-to-device writes are not allowed while a graph is being "
+                                  "captured; load inputs before the capture or between replays");
+  if (!bytes) return TTRL_OK;
+  // Only pinned blocks: the copy reads the host range after this returns.
+  if (!in_host_block(ctx, host_src, bytes))
+    return set_error(TTRL_EINVAL, "ttrl_h2d_enqueue: the source must lie inside one ttrl_host_alloc block");
+  const hipError_t e = hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (enqueued)");
+  return TTRL_OK;
+}
+
 int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_host, size_t in_bytes,
                     void* out_host, const void* out_dev, size_t out_bytes) {
   if (!ctx) return set_error(TTRL_EINVAL, "ttrl_graph_step: null ctx");

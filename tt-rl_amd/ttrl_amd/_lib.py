@@ -169,6 +169,7 @@ SIGNATURES = {
     "ttrl_alloc": ([P, SZ, C.POINTER(P)], I),
     "ttrl_free": ([P, P], I),
     "ttrl_h2d": ([P, P, P, SZ], I),
+    "ttrl_h2d_enqueue": ([P, P, P, SZ], I),
     "ttrl_d2h": ([P, P, P, SZ], I),
     "ttrl_d2d": ([P, P, P, SZ], I),
     "ttrl_fill_f32": ([P, P, F, L], I),

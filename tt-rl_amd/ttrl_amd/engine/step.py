@@ -50,9 +50,15 @@ class InputBinder:
     by `bound_block`) are staged in a pinned host image of that block:
     `load` writes into the image only, and `flush` sends every range loaded
     since the last flush, adjacent ranges coalesced, so a full batch is one
-    host-to-device copy.  Ranges not loaded are never sent, so device-side
-    writes into the block (a replay draw assembling a batch in place) are
-    not overwritten by stale host data.  Other inputs upload directly."""
+    host-to-device copy.  An input of at least QUEUE_MIN_BYTES is instead
+    queued on the stream as soon as it is staged (ttrl_h2d_enqueue), so its
+    copy overlaps the staging of the inputs after it; its part of the image
+    is not written again before the stream has been waited for.  Ranges not
+    loaded are never sent, so device-side writes into the block (a replay
+    draw assembling a batch in place) are not overwritten by stale host
+    data.  Other inputs upload directly."""
+
+    QUEUE_MIN_BYTES = 256 << 10
 
     def __init__(self, device, inputs: dict):
         self.device = device
@@ -62,6 +68,7 @@ class InputBinder:
         self._views: dict = {}
         self._ranges: dict = {}
         self._dirty: set = set()
+        self._queued: set = set()  # inputs whose queued copy may still read the image
         if self.block is not None and isinstance(self.block, DeviceArray):
             self.image = device.host_block(self.block.nbytes)
             for name, t in inputs.items():
@@ -81,8 +88,23 @@ class InputBinder:
         if view is None:
             t.data.upload(arr.astype(t.data.dtype, copy=False))
             return
+        if name in self._queued:
+            self.device.synchronize()
+            self._queued.clear()
         np.copyto(view, arr.reshape(view.shape), casting="unsafe")
-        self._dirty.add(name)
+        b, e = self._ranges[name]
+        if e - b >= self.QUEUE_MIN_BYTES and not self.device.capturing:
+            self.device.call("ttrl_h2d_enqueue", C.c_void_p(self.block.ptr + b), C.c_void_p(self.image.ptr + b),
+                             C.c_size_t(e - b))
+            self._queued.add(name)
+            self._dirty.discard(name)
+        else:
+            self._dirty.add(name)
+
+    def synced(self) -> None:
+        """The stream has been waited for since the last load: every queued
+        copy has finished reading the image."""
+        self._queued.clear()
 
     def pending(self) -> list:
         """[(begin, end)] byte ranges of the block loaded since the last
@@ -97,10 +119,13 @@ class InputBinder:
         return out
 
     def flush(self) -> None:
-        for b, e in self.pending():
+        spans = self.pending()
+        for b, e in spans:
             self.device.call("ttrl_h2d", C.c_void_p(self.block.ptr + b), C.c_void_p(self.image.ptr + b),
                              C.c_size_t(e - b))
         self._dirty.clear()
+        if spans:  # ttrl_h2d waits for the stream
+            self._queued.clear()
 
     def take_single_range(self):
         """The one pending range (begin, end) when at most one is pending
@@ -293,6 +318,7 @@ class TrainStep:
         ptr, n, _ = span
         self.device.call("ttrl_graph_step", self._trace._graph, C.c_void_p(blk.ptr + b), C.c_void_p(img.ptr + b),
                          C.c_size_t(e - b), C.c_void_p(self._reader.image.ptr), C.c_void_p(ptr), C.c_size_t(n))
+        self._binder.synced()  # ttrl_graph_step waits for the stream
         self._after_replay()
         return self._reader._unpack(self._trace_metrics)
 
