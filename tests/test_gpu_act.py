@@ -1,7 +1,8 @@
 """The acting step on the GPU against the float64 oracle.
 
-Kernels through the C-ABI: `ttrl_q_act` (Q head + first-index argmax) and
-`ttrl_gaussian_act` (Gaussian head + clamp + squashed sample).  Then the
+Kernels through the C-ABI: `ttrl_q_act` (Q head + first-index argmax),
+`ttrl_gaussian_act` (Gaussian head + clamp + squashed sample) and
+`ttrl_sac_head_sample` (the same launch in the SAC update, keeping u).  Then the
 acting network at lane counts below the width it was built for
 (ttrl/nets/acting.py:117-188, the cases of the reference's
 tests/hardware/test_acting_width.py), and the agents' `act`

@@ -396,7 +396,7 @@ def _encoder_rows(policy, obs_all: DeviceArray, B: int):
     the tape over its first B rows.  -> (tape node, output of every row)."""
     lins = _linear_relu_pairs(policy.encoder)
     if not isinstance(policy.head, GaussianHead) or lins is None:
-        raise ValueError("policy_rows: needs an MLP encoder of Linear -> ReLU pairs and a GaussianHead")
+        raise ValueError("the SAC policy path needs an MLP encoder of Linear -> ReLU pairs and a GaussianHead")
     rows = int(obs_all.shape[0])
     dev = obs_all.dev
     x_all = obs_all
@@ -418,24 +418,17 @@ def _encoder_rows(policy, obs_all: DeviceArray, B: int):
     return x, x_all
 
 
-def policy_rows(policy, obs_all: DeviceArray, B: int):
-    """The policy over every row of obs_all, one launch per layer, with the
-    tape over its first B rows (the actor's observations; the rest are the
-    soft target's next observations, constants of the update).
-    -> (packed head rows on the tape (B, 2d), packed head of every row)."""
-    head = policy.head
-    x, x_all = _encoder_rows(policy, obs_all, B)
-    return packed_linear_pair_rows(head.heads["mean"], head.heads["log_std"], x, x_all,
-                                   clamp=(head.log_std_min, head.log_std_max), op="gaussian_head")
-
-
 HEAD_SAMPLE_MAX_D = 16  # action dimensions ttrl_sac_head_sample takes
 
 
 def policy_sample_rows(policy, obs_all: DeviceArray, B: int, noise_all: DeviceArray, scale: ActionScale,
                        logp_all: DeviceArray):
-    """policy_rows followed by squashed_sample_rows, the Gaussian head and the
-    sample in one launch (ttrl_sac_head_sample) where its shapes allow.
+    """The policy over every row of obs_all, one launch per encoder layer,
+    then its Gaussian head and the squashed sample of every row in one launch
+    (ttrl_sac_head_sample; a packed head launch and squashed_sample_rows for
+    more than 16 action dimensions), the tape over the first B rows (the
+    actor's observations; the rest are the soft target's next observations,
+    constants of the update).
     -> (action, logp) tensors of the first B rows and (action, logp) arrays
     of the rest; `logp_all` receives every row's log-probability."""
     head = policy.head
