@@ -604,9 +604,9 @@ def main() -> int:
               "replicas would shard as independent learners with a periodic parameter all-reduce.",
               file=sys.stderr)
         return 2
-    from ttrl_amd.engine.device import acquire
+    from ttrl_amd.engine.device import open_device
 
-    dev = acquire(0)
+    dev = open_device(0)
     dqn, wall, gpu, nodes, dqn_copied = bench_dqn(dev, args.steps, args.warmup, args.ring, args.mode)
     value = args.steps / wall
     flops = dqn_update_flops(32)

@@ -40,6 +40,28 @@ typedef struct ttrl_graph ttrl_graph;
 const char* ttrl_last_error(void);
 int ttrl_version(void);
 int ttrl_device_count(int* out);
+
+/* What acquire() yields beside the device: the facts about it that the
+ * layers above may ask (replaces probe_profile, ttrl/engine/device/profile.py:79-97,
+ * whose grid and tile facts describe a Tenstorrent chip).  Reads the
+ * runtime's properties of visible device `device`; opens no context. */
+typedef struct ttrl_device_info {
+  char name[256];          /* marketing name, e.g. "AMD Instinct MI355X" */
+  char arch[64];           /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int compute_units;
+  int wavefront_size;
+  long lds_per_cu;         /* bytes of LDS per compute unit */
+  long lds_per_workgroup;  /* bytes one workgroup may allocate */
+  long l2_bytes;
+  long hbm_bytes;
+  int clock_khz;           /* peak engine clock */
+  int memory_clock_khz;
+  int memory_bus_bits;
+  int pci_bus_id;
+  int pci_device_id;
+  int pci_domain_id;
+} ttrl_device_info;
+int ttrl_device_query(int device, ttrl_device_info* out);
 /* Open a device and its stream; replaces acquire() (ttrl/engine/device/acquire.py:56). */
 int ttrl_init(int device, ttrl_ctx** out);
 /* Close; replaces the device close in ttrl/engine/device/acquire.py:56-140. */

@@ -48,3 +48,18 @@ def build_learner(device, *, seed=0, step_mode="graph", double=True, batch=32, d
               for k, v in online.items()}
     learner.target.load_state_dict(target)
     return learner, online, target
+
+
+def adam_moments(opt, module):
+    """Adam's stored S and V per parameter in state_dict layout (conv OIHW)."""
+    from ttrl_amd.engine.conv import Conv2d, master_to_oihw
+    from ttrl_amd.nets.acting import _walk_modules
+
+    convs = {id(m.weight): m for _, m in _walk_modules(module) if isinstance(m, Conv2d)}
+    S, V = [], []
+    for i, p in enumerate(opt.params):
+        m = convs.get(id(p))
+        for store, out in ((opt.m[i], S), (opt.v[i], V)):
+            a = store.numpy().astype(np.float64).reshape(p.shape)
+            out.append(master_to_oihw(a, m._oihw_shape, m.input_layout) if m is not None else a)
+    return S, V

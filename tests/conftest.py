@@ -22,11 +22,11 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def device():
-    from ttrl_amd.engine.device import acquire, device_count
+    from ttrl_amd.engine.device import device_count, open_device
 
     if device_count() < 1:
         pytest.fail("no GPU visible: -m gpu tests must run on a GPU box")
-    dev = acquire(0)
+    dev = open_device(0)
     yield dev
 
 

@@ -21,24 +21,11 @@ from dataclasses import replace
 import numpy as np
 import pytest
 
+from tests._dqn_helpers import adam_moments as _adam_moments
+
 pytestmark = pytest.mark.gpu
 
 SHAPE = (4, 36, 36)  # the Nature CNN's strides take 36 -> 8 -> 3 -> 1
-
-
-def _adam_moments(opt, module):
-    """Adam's stored S and V per parameter in state_dict layout (conv OIHW)."""
-    from ttrl_amd.engine.conv import Conv2d, master_to_oihw
-    from ttrl_amd.nets.acting import _walk_modules
-
-    convs = {id(m.weight): m for _, m in _walk_modules(module) if isinstance(m, Conv2d)}
-    S, V = [], []
-    for i, p in enumerate(opt.params):
-        m = convs.get(id(p))
-        for store, out in ((opt.m[i], S), (opt.v[i], V)):
-            a = store.numpy().astype(np.float64).reshape(p.shape)
-            out.append(master_to_oihw(a, m._oihw_shape, m.input_layout) if m is not None else a)
-    return S, V
 
 
 def _env_step(rng, L, pending, p_term=0.06, p_trunc=0.03):

@@ -114,3 +114,61 @@ def test_dqn_graph_and_eager_agree(device):
         assert a["loss"] == b["loss"]
     for k in res["graph"][1]:
         assert np.array_equal(res["graph"][1][k], res["eager"][1][k]), k
+
+
+def test_dqn_traced_fwd_bwd_with_deferred_gradients_tracks_the_oracle(device):
+    """The reference's trace mode (forward and backward captured, Adam
+    eager) with the weight-gradient reductions and batch means left to the
+    Adam launch: three updates, each checked against the float64 oracle from
+    the device's own parameters and Adam moments before it (loss, mean_q,
+    td_abs, grad_norm, every updated parameter at rel 1e-4), and the same
+    metrics and parameters as graph mode bit for bit.  The replays after the
+    first re-queue the captured backward's pending gradients, so each step
+    forms this update's gradients, not the capture's."""
+    from oracle.dqn import dqn_update
+    from oracle.nets import qnet_forward
+    from tests._dqn_helpers import adam_moments
+    from ttrl_amd.workloads import dqn_batch
+
+    from ttrl_amd.engine import layers
+
+    learner, _, _ = build_learner(device, seed=6, step_mode="traced_fwd_bwd", defer_grads=True)
+    graph, _, _ = build_learner(device, seed=6, step_mode="graph", defer_grads=True)
+    assert learner.defer_grads
+    outputs = None  # the captured forward's layer outputs, rewritten by every replay
+    try:
+        for k in range(3):
+            batch = dqn_batch(300 + k, batch=32)
+            p0 = learner.online.state_dict()
+            t0 = learner.target.state_dict()
+            S0, V0 = adam_moments(learner.optimizer, learner.online)
+            t_step = learner.optimizer.t + 1
+            layers.RECORD = []
+            try:
+                m = learner.update(batch)
+                if outputs is None:
+                    outputs = layers.RECORD[-5:]
+            finally:
+                layers.RECORD = None
+            recs = [[y.numpy() for y in ys] for ys in outputs]
+            gm = graph.update(batch)
+            for key in ("loss", "mean_q", "grad_norm"):
+                assert m[key] == gm[key], (k, key)
+            assert np.array_equal(m["td_abs"], gm["td_abs"]), k
+            onet, tnet = qnet_to_oracle(p0), qnet_to_oracle(t0)
+            _, acts = qnet_forward(onet, batch["obs"])
+            gates = {n: (recs[i][0] > 0).reshape(acts[i][1].shape)
+                     for i, n in enumerate(("conv0", "conv1", "conv2", "fc0"))}
+            ref = dqn_update(onet, tnet, batch, double=True, delta=1.0, lr=6.25e-5, eps=1.5e-4, gates=gates,
+                             device_next_actions=np.argmax(recs[4][1], 1), adam_state=(S0, V0), t=t_step)
+            for key in ("loss", "mean_q", "grad_norm"):
+                assert abs(m[key] - ref[key]) <= REL * abs(ref[key]), (k, key, m[key], ref[key])
+            assert _rel(m["td_abs"], ref["td_abs"]) < REL, k
+            new = learner.online.state_dict()
+            for (name, got), want in zip(new.items(), ref["new_params"]):
+                assert _rel(np.asarray(got).reshape(want.shape), want) < REL, (k, name)
+            for name, v in graph.online.state_dict().items():
+                assert np.array_equal(new[name], v), (k, name)
+    finally:
+        learner.close()
+        graph.close()

@@ -22,10 +22,10 @@ CHILD = r"""
 import sys
 import numpy as np
 sys.path[:0] = [{root!r}, {pkg!r}]
-from ttrl_amd.engine.device import acquire
+from ttrl_amd.engine.device import open_device
 from tests._dqn_helpers import build_learner
 from ttrl_amd.workloads import dqn_batch
-dev = acquire(0)
+dev = open_device(0)
 learner, _, _ = build_learner(dev, seed=7)
 for k in range(3):
     learner.update(dqn_batch(70 + k))
@@ -92,11 +92,11 @@ def test_plan_table_text_round_trip_and_invalid_plans(device, monkeypatch):
 CHILD_UPDATES = r"""
 import sys
 sys.path[:0] = [{root!r}, {pkg!r}]
-from ttrl_amd.engine.device import acquire
+from ttrl_amd.engine.device import open_device
 from tests._dqn_helpers import build_learner
 from tests._sac_helpers import build_sac
 from ttrl_amd.workloads import dqn_batch, sac_batch
-dev = acquire(0)
+dev = open_device(0)
 dqn, _, _ = build_learner(dev, seed=1)
 dqn.update(dqn_batch(1))
 sac, _, _ = build_sac(dev, seed=1)

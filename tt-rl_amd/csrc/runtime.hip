@@ -187,6 +187,34 @@ int ttrl_device_count(int* out) {
   return TTRL_OK;
 }
 
+int ttrl_device_query(int device, ttrl_device_info* out) {
+  if (!out) return set_error(TTRL_EINVAL, "ttrl_device_query: null out");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n)
+    return set_error(TTRL_EINVAL, "ttrl_device_query: device %d out of range (%d visible)", device, n);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_error(e, "hipGetDeviceProperties");
+  std::memset(out, 0, sizeof(*out));
+  std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
+  std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+  out->compute_units = prop.multiProcessorCount;
+  out->wavefront_size = prop.warpSize;
+  out->lds_per_cu = long(prop.maxSharedMemoryPerMultiProcessor);
+  out->lds_per_workgroup = long(prop.sharedMemPerBlock);
+  out->l2_bytes = long(prop.l2CacheSize);
+  out->hbm_bytes = long(prop.totalGlobalMem);
+  out->clock_khz = prop.clockRate;
+  out->memory_clock_khz = prop.memoryClockRate;
+  out->memory_bus_bits = prop.memoryBusWidth;
+  out->pci_bus_id = prop.pciBusID;
+  out->pci_device_id = prop.pciDeviceID;
+  out->pci_domain_id = prop.pciDomainID;
+  return TTRL_OK;
+}
+
 int ttrl_init(int device, ttrl_ctx** out) {
   if (!out) return set_error(TTRL_EINVAL, "ttrl_init: null out");
   int n = 0;

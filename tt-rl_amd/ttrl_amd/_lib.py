@@ -53,6 +53,17 @@ class LinearDesc(C.Structure):
     ]
 
 
+class DeviceInfo(C.Structure):
+    """Mirror of ttrl_device_info."""
+
+    _fields_ = [
+        ("name", C.c_char * 256), ("arch", C.c_char * 64), ("compute_units", C.c_int), ("wavefront_size", C.c_int),
+        ("lds_per_cu", C.c_long), ("lds_per_workgroup", C.c_long), ("l2_bytes", C.c_long), ("hbm_bytes", C.c_long),
+        ("clock_khz", C.c_int), ("memory_clock_khz", C.c_int), ("memory_bus_bits", C.c_int),
+        ("pci_bus_id", C.c_int), ("pci_device_id", C.c_int), ("pci_domain_id", C.c_int),
+    ]
+
+
 class AdamRange(C.Structure):
     """Mirror of ttrl_adam_range."""
 
@@ -158,6 +169,7 @@ SIGNATURES = {
     "ttrl_last_error": ([], C.c_char_p),
     "ttrl_version": ([], I),
     "ttrl_device_count": ([C.POINTER(I)], I),
+    "ttrl_device_query": ([I, C.POINTER(DeviceInfo)], I),
     "ttrl_init": ([I, C.POINTER(P)], I),
     "ttrl_shutdown": ([P], I),
     "ttrl_sync": ([P], I),

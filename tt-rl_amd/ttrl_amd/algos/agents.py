@@ -1,6 +1,9 @@
-"""DQN and SAC as agents (the Agent protocol of ttrl/algos/base.py:118-187):
-a learner, its GPU-resident replay, the update clock and the autoreset
-bookkeeping, behind act / observe / should_update / update.
+"""DQN, SAC and PPO as agents (the Agent protocol of ttrl/algos/base.py:118-187):
+a learner, its experience storage (GPU-resident replay; PPO's rollout), the
+update clock and the autoreset bookkeeping, behind act / observe /
+should_update / update.  Each constructor takes the keywords the
+reference's `build_agent` passes (cfg, n_envs, seed, profile) and the
+engine config.
 
 One gradient step (ttrl/algos/dqn/agent.py:183-214, ttrl/algos/sac/agent.py:218-238)
 stays on the device end to end: the replay draws the batch and assembles it
@@ -23,11 +26,13 @@ import numpy as np
 from ttrl_amd.algos.base import AutoresetTracker, Transition, leaf_array
 from ttrl_amd.algos.clock import UpdateClock
 from ttrl_amd.algos.dqn import DQNConfig, DQNLearner, leaf_key
+from ttrl_amd.algos.ppo import PPOConfig, PPOLearner
 from ttrl_amd.algos.sac import SACConfig, SACLearner
 from ttrl_amd.buffers.replay import ReplayBuffer, beta_at
+from ttrl_amd.engine.config import DEFAULT, EngineConfig, check_engine_config
 from ttrl_amd.engine.ops import _kernels as K
 
-__all__ = ["DQNAgent", "SACAgent"]
+__all__ = ["DQNAgent", "PPOAgent", "SACAgent"]
 
 
 class _OffPolicyAgent:
@@ -116,8 +121,10 @@ class DQNAgent(_OffPolicyAgent):
     (ttrl/algos/dqn/agent.py:38-253)."""
 
     def __init__(self, obs_spec, action_spec, device, *, cfg: DQNConfig = DQNConfig(), n_envs: int = 1,
-                 seed: int | None = None):
+                 seed: int | None = None, profile=None, engine: EngineConfig = DEFAULT):
         self.cfg = cfg
+        self.profile = profile
+        self.engine = check_engine_config(engine, "DQNAgent")
         self.learner = DQNLearner(obs_spec, action_spec, device, cfg=cfg, seed=seed, n_envs=n_envs)
         self._setup(obs_spec, action_spec, device, n_envs, seed)
         inp = self.learner.inputs
@@ -169,8 +176,10 @@ class SACAgent(_OffPolicyAgent):
     n-step replay (ttrl/algos/sac/agent.py:38-282)."""
 
     def __init__(self, obs_spec, action_spec, device, *, cfg: SACConfig = SACConfig(), n_envs: int = 1,
-                 seed: int | None = None):
+                 seed: int | None = None, profile=None, engine: EngineConfig = DEFAULT):
         self.cfg = cfg
+        self.profile = profile
+        self.engine = check_engine_config(engine, "SACAgent")
         self.learner = SACLearner(obs_spec, action_spec, device, cfg=cfg, seed=seed, n_envs=n_envs)
         self._setup(obs_spec, action_spec, device, n_envs, seed)
         b = self.learner.batch
@@ -216,3 +225,209 @@ class SACAgent(_OffPolicyAgent):
         keys = ("critic_loss", "actor_loss", "alpha_loss", "alpha", "entropy", "mean_q_target", "critic_grad_norm",
                 "actor_grad_norm")
         return {k: float(m[k]) for k in keys}
+
+
+class PPOAgent:
+    """Clipped PPO over a shared-trunk actor-critic with a categorical
+    policy (ttrl/algos/ppo/agent.py:40-238, ttrl/algos/ppo/learn.py:46-112).
+
+    `act` runs the captured acting forward at the lane count (log-softmax
+    of the logits and the value on the device) and draws each lane's action
+    on the host by the reference's inverse-CDF rule against one uniform per
+    lane (ttrl/algos/ppo/policy.py:37-62), recording the log-prob and value
+    for `observe`.  `observe` appends one vector step to the host rollout
+    (autoreset padding steps stored with valid 0); `should_update` is true
+    once the rollout holds n_steps steps; `update` bootstraps V of the last
+    next observation, then the learner uploads the rollout, runs GAE and
+    every epoch's minibatch steps on the device, and the rollout resets.
+    Feedforward policies only: a recurrent config is refused."""
+
+    def __init__(self, obs_spec, action_spec, device, *, cfg: PPOConfig = PPOConfig(), n_envs: int = 1,
+                 seed: int | None = None, profile=None, engine: EngineConfig = DEFAULT, boundaries=None):
+        from ttrl_amd.nets.acting import ActingNet, CategoricalValueDecision
+
+        if cfg.recurrent is not None:
+            raise ValueError("PPOAgent: a recurrent PPOConfig is not supported by the agent; drive "
+                             "RecurrentPPOLearner.update(rollout) with sequences of your own instead")
+        if boundaries is not None:
+            raise ValueError("PPOAgent: episode boundaries only matter to a recurrent policy, and this agent "
+                             "builds feedforward ones; pass boundaries=None")
+        if int(n_envs) < 1:
+            raise ValueError(f"PPOAgent: n_envs must be >= 1, got {n_envs}")
+        if cfg.minibatch_size > cfg.n_steps * int(n_envs):
+            raise ValueError(f"PPO: minibatch_size={cfg.minibatch_size} exceeds the {cfg.n_steps * int(n_envs)} "
+                             f"transitions one rollout collects (n_steps={cfg.n_steps} x n_envs={n_envs}), so no "
+                             f"minibatch could ever be drawn")
+        if int(n_envs) > cfg.minibatch_size:
+            raise ValueError(f"PPO: n_envs={n_envs} exceeds the network batch minibatch_size="
+                             f"{cfg.minibatch_size}; acting runs the network at the lane count")
+        self.cfg = cfg
+        self.profile = profile
+        self.engine = check_engine_config(engine, "PPOAgent")
+        self.obs_spec, self.action_spec, self.device = obs_spec, action_spec, device
+        self.n_envs = int(n_envs)
+        self.num_actions = int(action_spec.n)
+        self.learner = PPOLearner(obs_spec, action_spec, device, cfg=cfg, seed=seed)
+        self._acting = ActingNet(self.learner.net, obs_spec, device, width=cfg.minibatch_size, lanes=self.n_envs,
+                                 decision=CategoricalValueDecision(), mode="graph")
+        self._autoreset = AutoresetTracker(self.n_envs)
+        self._rng = np.random.default_rng(seed)
+        self._eval_rng = np.random.default_rng(seed).spawn(1)[0]
+        self._pending = None
+        self._last_next_obs = None
+        T, N = cfg.n_steps, self.n_envs
+        leaf = tuple(obs_spec.shape) if obs_spec.kind == "image" else (obs_spec.size,)
+        frames = np.uint8 if obs_spec.kind == "image" else np.float32
+        self._rollout = {"obs": np.zeros((T, N) + leaf, frames), "actions": np.zeros((T, N), np.int64),
+                         "logp": np.zeros((T, N), np.float32), "values": np.zeros((T, N), np.float32),
+                         "rewards": np.zeros((T, N), np.float32), "dones": np.zeros((T, N), np.float32),
+                         "valid": np.zeros((T, N), np.float32)}
+        self._t = 0
+
+    @property
+    def net(self):
+        return self.learner.net
+
+    @property
+    def optimizer(self):
+        return self.learner.optimizer
+
+    @property
+    def frame_count(self) -> int:
+        return self.learner.frame_count
+
+    @property
+    def update_count(self) -> int:
+        return self.learner.update_count
+
+    # -- acting --------------------------------------------------------------
+
+    def act(self, obs, *, deterministic: bool = False, episode_starts=None) -> np.ndarray:
+        """One action per lane; a stochastic step records its log-prob and
+        value for the `observe` that follows.  `episode_starts` belongs to
+        the acting contract of a policy with memory; this one has none."""
+        out = self._acting.decide(leaf_array(obs, self.obs_spec.name))
+        logp_all = out["logp"]
+        batch = logp_all.shape[0]
+        if deterministic:
+            actions = np.argmax(logp_all, axis=-1)
+        else:
+            probs = np.exp(logp_all)
+            probs = probs / probs.sum(axis=-1, keepdims=True)
+            cdf = np.cumsum(probs, axis=-1)
+            actions = (self._rng.random(batch)[:, None] > cdf).sum(axis=-1)
+            actions = np.clip(actions, 0, self.num_actions - 1)
+        actions = actions.astype(np.int64)
+        if not deterministic:
+            self._pending = {"action": actions, "logp": logp_all[np.arange(batch), actions].astype(np.float32),
+                             "value": out["value"].reshape(-1)[:batch].astype(np.float32)}
+        return actions
+
+    # -- observing -----------------------------------------------------------
+
+    def observe(self, transition: Transition) -> None:
+        """Append one vector step, padding steps included with valid 0
+        (ttrl/algos/ppo/agent.py:138-189)."""
+        if self._pending is None:
+            raise RuntimeError("PPO.observe: no act() preceded this transition. PPO records the log-prob and the "
+                               "value from the forward pass that chose the action, so every observe must follow "
+                               "the act that produced it; a deterministic act (evaluation) records nothing and "
+                               "must not be fed back.")
+        valid = self._autoreset.valid(transition)
+        pending, self._pending = self._pending, None
+        if pending["logp"].shape[0] != transition.n_envs:
+            raise ValueError(f"PPO.observe: the last act() produced {pending['logp'].shape[0]} actions but this "
+                             f"transition has {transition.n_envs} lanes")
+        if self._t >= self.cfg.n_steps:
+            raise RuntimeError(f"PPO.observe: the rollout already holds its {self.cfg.n_steps} steps; call "
+                               f"update() when should_update() says so")
+        t, r = self._t, self._rollout
+        r["obs"][t] = leaf_array(transition.obs, self.obs_spec.name)
+        r["actions"][t] = pending["action"]
+        r["logp"][t] = pending["logp"]
+        r["values"][t] = pending["value"]
+        r["rewards"][t] = np.asarray(transition.reward, np.float32)
+        r["dones"][t] = np.asarray(transition.terminated, np.float32)
+        r["valid"][t] = valid.astype(np.float32)
+        self._t += 1
+        self._last_next_obs = leaf_array(transition.next_obs, self.obs_spec.name)
+        self.learner.frame_count += transition.n_envs
+
+    def should_update(self, frame: int) -> bool:
+        """A full rollout: the trigger is how much this policy collected."""
+        return self._t >= self.cfg.n_steps
+
+    # -- learning ------------------------------------------------------------
+
+    def _last_values(self) -> np.ndarray:
+        """V(s) of the observation after the rollout's last stored step."""
+        out = self._acting.decide(self._last_next_obs)
+        return out["value"].reshape(-1)[:self.n_envs].astype(np.float32)
+
+    def update(self) -> dict:
+        if self._t < self.cfg.n_steps:
+            raise RuntimeError(f"PPO.update: the rollout holds fewer than its {self.cfg.n_steps} steps. Gate on "
+                               f"should_update, which reports when it is full.")
+        rollout = dict(self._rollout)
+        rollout["last_values"] = self._last_values()
+        metrics = self.learner.update(rollout)
+        self._t = 0
+        return metrics
+
+    def named_parameters(self):
+        """The whole actor-critic: on-policy learning keeps no lagged copy."""
+        return self.learner.net.named_parameters()
+
+    def parameters(self):
+        return self.learner.net.parameters()
+
+    # -- state -----------------------------------------------------------------
+
+    def _rollout_state(self) -> dict:
+        t = self._t
+        state = {"t": t, "acting_rng": self._rng.bit_generator.state,
+                 "last_next_obs": None if self._last_next_obs is None else np.array(self._last_next_obs)}
+        state.update({k: v[:t].copy() for k, v in self._rollout.items()})
+        return state
+
+    def state_dict(self, *, weights_only: bool = False) -> dict:
+        """The learner's tree (net, config, optimizer, counters, the
+        shuffle generator) plus the run state the agent holds: autoreset
+        phase and the half-collected rollout with the acting generator."""
+        state = self.learner.state_dict(weights_only=weights_only)
+        if not weights_only:
+            state["autoreset"] = self._autoreset.state_dict()
+            state["rollout"] = self._rollout_state()
+        return state
+
+    def load_state_dict(self, state: dict, *, weights_only: bool = False) -> None:
+        run = not (weights_only or state.get("weights_only", False))
+        if run:
+            missing = [k for k in ("autoreset", "rollout") if k not in state]
+            if missing:
+                raise ValueError(f"PPOAgent.load_state_dict: state is missing {missing}.")
+        self.learner.load_state_dict(state, weights_only=weights_only)
+        self._pending = None
+        if not run:
+            self._t = 0
+            return
+        self._autoreset.load_state_dict(state["autoreset"])
+        ro = state["rollout"]
+        t = int(ro["t"])
+        if not 0 <= t <= self.cfg.n_steps:
+            raise ValueError(f"PPOAgent.load_state_dict: the stored rollout holds {t} steps; this agent's "
+                             f"n_steps is {self.cfg.n_steps}")
+        for k, v in self._rollout.items():
+            arr = np.asarray(ro[k])
+            if arr.shape != (t,) + v.shape[1:]:
+                raise ValueError(f"PPOAgent.load_state_dict: stored rollout field {k!r} has shape {arr.shape}, "
+                                 f"expected {(t,) + v.shape[1:]}")
+            v[:t] = arr
+        self._t = t
+        self._rng.bit_generator.state = ro["acting_rng"]
+        last = ro.get("last_next_obs")
+        self._last_next_obs = None if last is None else np.asarray(last)
+
+    def close(self) -> None:
+        self._acting.close()
+        self.learner.close()

@@ -6,8 +6,12 @@ from __future__ import annotations
 import importlib
 from typing import Any
 
+from ttrl_amd.engine.config import DEFAULT, EngineConfig
+
 _LAZY = {
     "Device": "device", "acquire": "device", "device_count": "device", "NoDeviceAvailable": "device",
+    "DeviceProfile": "device", "open_device": "device", "purge_device_caches": "device",
+    "register_device_cache": "device", "survey": "device", "probe_profile": "device",
     "DeviceArray": "tensor", "MASTER_DTYPE": "tensor", "ParamArena": "tensor", "copy_in_place": "tensor",
     "copy_tensor_in_place": "tensor", "to_device": "tensor", "to_host": "tensor", "restore_in_place": "tensor",
     "Tensor": "autograd", "backward": "autograd", "no_grad": "autograd",
@@ -22,7 +26,7 @@ _LAZY = {
 
 _OPS = "ttrl_amd.engine.ops"
 
-__all__ = sorted(_LAZY) + [
+__all__ = ["DEFAULT", "EngineConfig", *sorted(_LAZY),
     "add", "div", "mul", "sub", "abs_", "exp", "log", "neg", "relu", "sigmoid", "sqrt", "square", "tanh",
     "clamp", "maximum", "minimum", "matmul", "argmax_dim_detached", "max_dim_detached", "mean_all", "mean_dim",
     "sum_all", "sum_dim", "concat", "reshape", "split", "apply_done_mask", "entropy", "gather_onehot", "huber",

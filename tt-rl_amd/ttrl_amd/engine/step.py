@@ -31,6 +31,8 @@ import ctypes as C
 import numpy as np
 
 from ttrl_amd.engine.autograd import Tensor
+from ttrl_amd.engine.config import DEFAULT, EngineConfig, check_engine_config
+from ttrl_amd.engine.pending import take_sources
 from ttrl_amd.engine.slots import InputSlots, check_slot_count, metric_ptrs, twin_inputs
 from ttrl_amd.engine.tensor import DeviceArray
 from ttrl_amd.engine.trace import capture
@@ -112,7 +114,10 @@ class InputBinder:
         spans = sorted(self._ranges[n] for n in self._dirty)
         out: list = []
         for b, e in spans:
-            if out and b <= out[-1][1] + 256:  # bound_block aligns inputs to 256 bytes
+            # bound_block starts every input on a 256-byte boundary: bridge
+            # only the alignment padding after the previous range, never an
+            # input that was not loaded
+            if out and b <= -(-out[-1][1] // 256) * 256:
                 out[-1] = (out[-1][0], max(out[-1][1], e))
             else:
                 out.append((b, e))
@@ -213,7 +218,8 @@ def read_metrics(metrics: dict | None) -> dict:
 
 
 class TrainStep:
-    def __init__(self, step_fn: StepFn, inputs: dict, device, *, optimizer=None, mode: str = "eager", cfg=None):
+    def __init__(self, step_fn: StepFn, inputs: dict, device, *, optimizer=None, mode: str = "eager",
+                 cfg: EngineConfig = DEFAULT):
         if mode not in MODES:
             raise ValueError(f"TrainStep mode must be one of {list(MODES)}, got {mode!r}")
         self.step_fn = step_fn
@@ -221,12 +227,19 @@ class TrainStep:
         self.device = device
         self.optimizer = optimizer
         self.mode = mode
-        self.cfg = cfg
+        # trace_blocking: a replay waits for the device before returning
+        # (ttrl/engine/step/core.py:87-91); the metric read-back waits anyway.
+        self.cfg = check_engine_config(cfg, "TrainStep")
         self._binder = InputBinder(device, inputs)
         self._reader = MetricReader(device)
         self._trace = None
         self._trace_metrics: dict | None = None
         self._captured_grads: list = []
+        # traced_fwd_bwd: the gradient sources and ordered sums the captured
+        # backward leaves for the eager optimizer step, re-queued after
+        # every replay (the replay refreshes their operands, not the host
+        # records the step consumes)
+        self._captured_pending: tuple = ((), ())
         self._pool = None
         self._slots: InputSlots | None = None
         self._slot_inputs: list = []
@@ -262,6 +275,9 @@ class TrainStep:
         if self._trace is None:
             raise RuntimeError("TrainStep.replay_slot: run() once first (it captures every slot's graph)")
         self._slots.launch(k)
+        if self.cfg.trace_blocking:
+            self.device.synchronize()
+            self._binder.synced()
         self._captured_grads = self._slot_grads[k]
         self._after_replay()
 
@@ -288,9 +304,12 @@ class TrainStep:
         return self._reader.read(metrics)
 
     def replay(self) -> None:
-        """Launch the captured step without reading metrics (benchmark loop)."""
+        """Launch the captured step without reading metrics (benchmark loop);
+        with `cfg.trace_blocking` it returns once the device has finished."""
         self._binder.flush()
-        self._trace.replay()
+        self._trace.replay(blocking=self.cfg.trace_blocking)
+        if self.cfg.trace_blocking:
+            self._binder.synced()
         self._after_replay()
 
     def _after_replay(self) -> None:
@@ -299,7 +318,21 @@ class TrainStep:
             if self.mode == "graph":
                 self.optimizer._replayed()
             else:
+                self._requeue_pending()
                 self.optimizer.step()
+
+    def _requeue_pending(self) -> None:
+        """Re-attach the captured backward's pending gradient sources to
+        their tensors and queue its ordered sums again, so the eager step
+        after this replay forms them from the operands the replay wrote."""
+        sources, sums = self._captured_pending
+        for pend in sources:
+            for t in pend.tensors:
+                t._pending = pend
+        queued = self.device.pending_sums
+        for item in sums:
+            if all(item is not q for q in queued):
+                queued.append(item)
 
     def _run_graph(self) -> dict:
         if self._trace is None:
@@ -311,6 +344,11 @@ class TrainStep:
         sent = self._binder.take_single_range() if (span is not None and self.mode == "graph") else None
         if sent is None:
             self.replay()
+            if not self._trace_metrics and not self.cfg.trace_blocking:
+                # nothing to read back orders the replay ahead of the caller's
+                # next host step (ttrl/engine/step/core.py:135-141)
+                self.device.synchronize()
+                self._binder.synced()
             return self._reader.read(self._trace_metrics)
         # One call: the loaded input range in, the replay, the metric span out, one wait.
         b, e = sent
@@ -342,6 +380,8 @@ class TrainStep:
             dev.synchronize()
             self._trace, self._trace_metrics = capture(dev, lambda: self._body(in_graph))
             self._captured_grads = self._grads_now()
+            if not in_graph and self.optimizer is not None:
+                self._captured_pending = (tuple(take_sources(self.optimizer.params)), tuple(dev.pending_sums))
             if self._slots is not None:
                 self._capture_slots(in_graph)
         self._rebind_grads()
@@ -379,6 +419,7 @@ class TrainStep:
         trace, self._trace = self._trace, None
         self._trace_metrics = None
         self._captured_grads = []
+        self._captured_pending = ((), ())
         slots, self._slots = self._slots, None
         try:
             if slots is not None:

@@ -32,7 +32,8 @@ from ttrl_amd.engine.nn import Module
 from ttrl_amd.engine.tensor import bound_block
 from ttrl_amd.engine.trace import capture
 
-__all__ = ["ActingNet", "GreedyDecision", "SquashedDecision", "check_encoder_layout", "net_at_batch"]
+__all__ = ["ActingNet", "CategoricalValueDecision", "GreedyDecision", "SquashedDecision", "check_encoder_layout",
+           "net_at_batch"]
 
 MODES = ("eager", "graph")
 
@@ -147,6 +148,42 @@ class SquashedDecision:
                  None if ls.bias is None else ls.bias.data.ptr, C.c_float(head.log_std_min),
                  C.c_float(head.log_std_max), ins["noise"].ptr, s._centre.data.ptr, s._scale.data.ptr,
                  C.c_float(s.log_det), int(deterministic), None, outs["action"].ptr, outs["logp"].ptr)
+
+
+class CategoricalValueDecision:
+    """A shared-trunk actor-critic's acting outputs: the log-softmax of the
+    policy logits and the critic's value, per lane, computed on the device
+    (the categorical draw is made on the host from these, as
+    ttrl/algos/ppo/policy.py:37-62 does, and the log-prob recorded for the
+    importance ratio is read from the same rows)."""
+
+    kind = "categorical"
+
+    def features(self, net, obs: Tensor) -> Tensor:
+        return net.encoders["actor"](obs)
+
+    def outputs(self, net, lanes: int):
+        A = net.heads["policy"].logits.out_features
+        return [("logp", np.zeros((lanes, A), np.float32)), ("value", np.zeros((lanes, 1), np.float32))]
+
+    def inputs(self, net, lanes: int):
+        return []
+
+    def launch(self, dev, net, features: Tensor, ins, outs, deterministic: bool) -> None:
+        from ttrl_amd.engine.ops import _kernels as K
+        from ttrl_amd.engine.ops.functional import log_softmax
+        from ttrl_amd.engine.tensor import DeviceArray
+        from ttrl_amd.nets.heads import policy_value_packed
+
+        L = int(features.shape[0])
+        A = outs["logp"].shape[1]
+        with no_grad():
+            head = policy_value_packed(net.heads["policy"], net.heads["value"], features).data
+            logits = DeviceArray(dev, (L, A))
+            K.copy_region(head, (0, 0), logits, (0, 0), (L, A))
+            logp = log_softmax(Tensor(logits), dim=-1).data
+        K.copy_region(logp, (0, 0), outs["logp"], (0, 0), (L, A))
+        K.copy_region(head, (0, A), outs["value"], (0, 0), (L, 1))
 
 
 def _q_layer(net):
@@ -278,8 +315,9 @@ class ActingNet:
     # -- the acting step -----------------------------------------------------
 
     def _body(self, w: _Width, deterministic: bool) -> None:
+        encode = getattr(self.decision, "features", None)
         with no_grad():
-            features = w.net.encoder(w.obs)
+            features = encode(w.net, w.obs) if encode is not None else w.net.encoder(w.obs)
         self.decision.launch(self.device, w.net, features, w.ins, w.outs, deterministic)
 
     def _graph(self, w: _Width, deterministic: bool):
@@ -297,7 +335,8 @@ class ActingNet:
 
     def decide(self, obs, *, noise=None, deterministic: bool = False) -> dict:
         """One acting step: {"actions", "q"} for a greedy decision,
-        {"action", "logp"} for a squashed one, as host arrays."""
+        {"action", "logp"} for a squashed one, {"logp" (lanes, A), "value"}
+        for a categorical one, as host arrays."""
         if self.decision is None:
             raise TypeError("ActingNet.decide needs a decision (GreedyDecision or SquashedDecision)")
         lanes, arr = self._lanes_of(obs)

@@ -65,9 +65,9 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--out", default=str(HERE / "gfx950.tsv"))
     args = ap.parse_args()
-    from ttrl_amd.engine.device import acquire
+    from ttrl_amd.engine.device import open_device
 
-    dev = acquire(0)
+    dev = open_device(0)
     tune_all(dev)
     dev.synchronize()
     dev.save_plans(args.out)
