@@ -316,8 +316,9 @@ def recurrent_ppo_step(params: dict, S: list, V: list, t: int, mb: dict, *, seq_
 
 
 def recurrent_ppo_update(params: dict, rollout: dict, *, rng, minibatch_size: int, epochs: int, seq_len: int,
-                         gamma: float = 0.99, lam: float = 0.95, **step_cfg) -> dict:
-    """-> dict(params, steps, batches): the whole recurrent update."""
+                         gamma: float = 0.99, lam: float = 0.95, batches_only: bool = False, **step_cfg) -> dict:
+    """-> dict(params, steps, batches): the whole recurrent update
+    (`batches_only`: the minibatches alone, no step taken)."""
     rewards = np.asarray(rollout["rewards"], np.float32)
     T, N = rewards.shape
     valid = rollout.get("valid")
@@ -338,8 +339,10 @@ def recurrent_ppo_update(params: dict, rollout: dict, *, rng, minibatch_size: in
     for t, (rows, h0_rows) in enumerate(sequence_minibatches(T, N, seq_len, minibatch_size, epochs, rng), start=1):
         mb = {k: v[rows] for k, v in flat.items()}
         mb["h0"] = hidden[h0_rows]
+        batches.append(mb)
+        if batches_only:
+            continue
         r = recurrent_ppo_step(params, S, V, t, mb, seq_len=seq_len, **step_cfg)
         params, S, V = r["params"], r["S"], r["V"]
         steps.append(r["metrics"])
-        batches.append(mb)
     return dict(params=params, steps=steps, batches=batches)

@@ -102,3 +102,37 @@ def test_ppo_policy_artifact_runs_on_the_device(device, tmp_path):
         if policy is not None:
             policy.close()
         learner.close()
+
+
+def test_dqn_acting_forward_at_32_lanes_matches_the_deploy_oracle(device, tmp_path):
+    """The batch-32 Q-network forward the benchmark times (the learner's
+    captured acting graph at 32 lanes over [32, 4, 84, 84] uint8 frames)
+    against the oracle's float64 restatement of the reference's numpy deploy
+    forward on the exported artifact (ttrl/deploy/artifact.py:188-252): Q at
+    rel 1e-4 and the argmax exact on every row whose top-two gap clears the
+    reference's decisive band of 1e-3 (tests/hardware/test_deploy_parity.py:281-292).
+    Replaying the graph back to back, as the benchmark does, leaves the same
+    Q rows."""
+    from oracle import deploy as odeploy
+
+    learner, _, _ = build_learner(device, seed=12)
+    try:
+        assert learner.cfg.batch_size == 32
+        art = _export(learner, tmp_path, "dqn32")
+        meta, arrays = odeploy.read(art)
+        frames = np.random.default_rng(21).integers(0, 256, (32, 4, 84, 84), dtype=np.uint8)
+        out = learner._acting.decide(frames)
+        rows = odeploy.head_rows(meta, arrays, frames)
+        assert out["q"].shape == (32, 6)
+        err = np.max(np.abs(out["q"].astype(np.float64) - rows)) / np.max(np.abs(rows))
+        assert err < 1e-4, err
+        top = np.sort(rows, 1)[:, -2:]
+        keep = (top[:, 1] - top[:, 0]) > 1e-3
+        assert keep.sum() >= 16
+        assert np.array_equal(out["actions"].astype(np.int64)[keep], np.argmax(rows, 1)[keep])
+        w = learner._acting._views[32]
+        w.graphs[False].replay_n(5)
+        device.synchronize()
+        assert np.array_equal(w.outs["q"].numpy(), out["q"])
+    finally:
+        learner.close()

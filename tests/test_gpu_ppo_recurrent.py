@@ -109,35 +109,55 @@ def test_recurrent_update_matches_oracle_small(device, mode):
         assert big.mean() < 0.01, (i, float(big.mean()))
 
 
-def test_recurrent_minibatch_steps_at_the_config_shape_step_by_step(device):
+@pytest.mark.parametrize("mode,epochs", [("eager", 1), ("graph", 4)])
+def test_recurrent_minibatch_steps_at_the_config_shape_step_by_step(device, mode, epochs):
     """16 envs x 128 steps, sequences of 32, hidden 512, minibatches of 512
-    rows (16 sequences), 18 actions; one epoch of four steps, each from the
-    device's own parameters and Adam moments."""
+    rows (16 sequences), 18 actions, each step from the device's own
+    parameters and Adam moments.  Eager: one epoch of four steps, each
+    recording its ReLU outputs as it runs.  Graph (the form the benchmark
+    times): the whole update, 4 epochs x 4 minibatches, as 16 replays of the
+    captured step, the ReLU outputs read after each replay from the buffers
+    the capture recorded."""
     from oracle.adam import fused_step
     from oracle.ppo import recurrent_ppo_step, recurrent_ppo_update
     from ttrl_amd.algos.ppo import PPOLearner
     from ttrl_amd.engine import layers as layers_mod
 
     T, N, L, Hd, mb, A, seed = 128, 16, 32, 512, 512, 18, 51
-    learner, cfg, state, rollout = _learner(device, T=T, N=N, L=L, Hd=Hd, mb=mb, epochs=1, mode="eager", A=A,
+    learner, cfg, state, rollout = _learner(device, T=T, N=N, L=L, Hd=Hd, mb=mb, epochs=epochs, mode=mode, A=A,
                                            seed=seed)
     try:
         steps = learner.load_rollout(rollout)
+        assert steps == 4 * epochs
         ref = recurrent_ppo_update(_params(state), rollout, rng=np.random.default_rng(seed), minibatch_size=mb,
-                                   epochs=1, seq_len=L, lr=cfg.lr, adam_eps=cfg.adam_eps,
-                                   max_grad_norm=cfg.max_grad_norm)
-        learner.begin_update()
+                                   epochs=epochs, seq_len=L, lr=cfg.lr, adam_eps=cfg.adam_eps,
+                                   max_grad_norm=cfg.max_grad_norm, batches_only=True)
+        captured = None
+        if mode == "graph":
+            layers_mod.RECORD = []
+            try:
+                learner.begin_update()  # warm-up pass, then the capture: the last four records are the graph's
+                captured = list(layers_mod.RECORD[-4:])
+            finally:
+                layers_mod.RECORD = None
+            assert learner._graph is not None
+        else:
+            learner.begin_update()
         opt = learner.optimizer
         for t in range(steps):
             p0 = _params(learner.net.state_dict())
             S0 = _flat(_params(_per_param(learner, lambda i, p: opt.m[i])))
             V0 = _flat(_params(_per_param(learner, lambda i, p: opt.v[i])))
-            layers_mod.RECORD = []
-            try:
+            if captured is not None:
                 learner.run_steps(1)
-                recs = [y.numpy() for y in layers_mod.RECORD[-4:]]
-            finally:
-                layers_mod.RECORD = None
+                recs = [y.numpy() for y in captured]
+            else:
+                layers_mod.RECORD = []
+                try:
+                    learner.run_steps(1)
+                    recs = [y.numpy() for y in layers_mod.RECORD[-4:]]
+                finally:
+                    layers_mod.RECORD = None
             shapes = [(mb, 20, 20, 32), (mb, 9, 9, 64), (mb, 7, 7, 64), (mb, 512)]
             gates = {n: y.reshape(sh) > 0 for n, y, sh in zip(("conv0", "conv1", "conv2", "fc0"), recs, shapes)}
             r = recurrent_ppo_step(p0, S0, V0, t + 1, ref["batches"][t], seq_len=L, lr=cfg.lr,
