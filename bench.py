@@ -37,12 +37,30 @@ for _p in (ROOT, ROOT / "tt-rl_amd"):
 import numpy as np  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12
-# HBM bytes per call of the DQN Adam step (k_adam_src + k_finish_sums at batch 32): rocprofv3
-# FETCH_SIZE (13402.1 + 5.2) KiB x 2.000 + WRITE_SIZE (26390.9 + 0.1) KiB x 1.000, medians over
-# 200 calls, the factors being what the same counters read for a 256 MiB device-to-device copy
-# (131083.5 and 262144.0 KiB); profiles/dqn_adam_step_roofline_and_traffic.md.
+# HBM bytes per call of the DQN Adam step at batch 32, from rocprofv3 FETCH_SIZE and WRITE_SIZE
+# passes over the step's kernel, each scaled by what the same counter reads for a 256 MiB
+# device-to-device copy (profiles/dqn_adam_step_roofline_and_traffic.md), and the SHA-256 of the
+# optimizer kernels' source the passes measured: a build from other source reports traffic null.
 ADAM_STEP_TRAFFIC_BYTES = 54479959
+ADAM_STEP_TRAFFIC_SOURCE = ""
+ADAM_STEP_SOURCES = ("tt-rl_amd/csrc/optim.hip", "tt-rl_amd/csrc/common.hpp")
 PEAK_HBM = 8.0e12
+
+
+def _source_digest(paths) -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in paths:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
+
+
+def adam_step_traffic():
+    """(bytes, digest now): the committed traffic figure when the kernel
+    source is the one it was measured on, else None."""
+    digest = _source_digest(ADAM_STEP_SOURCES)
+    return (ADAM_STEP_TRAFFIC_BYTES if digest == ADAM_STEP_TRAFFIC_SOURCE else None), digest
 
 # Multiply-accumulates per sample of the Nature CNN at 4x84x84 (conv1..3, fc1, fc2).
 NATURE_MACS = (20 * 20 * 32 * 4 * 64, 9 * 9 * 64 * 32 * 16, 7 * 7 * 64 * 64 * 9, 3136 * 512, 512 * 6)
@@ -102,19 +120,45 @@ def _time_steps(dev, step, steps, warmup):
     return wall, ms.value / 1e3
 
 
-def _graph_legs(dev, steps, warmup, n, replay_slot, slot_block):
+REPEATS = 5
+REPEAT_MIN_UPDATES = 1000
+
+
+def _spread(rates) -> dict:
+    r = sorted(rates)
+    return {"runs": len(r), "median": round(float(np.median(r)), 2), "min": round(r[0], 2), "max": round(r[-1], 2),
+            "values": [round(x, 2) for x in rates]}
+
+
+def _graph_legs(dev, steps, warmup, n, replay_slot, slot_block, run_slot):
     """(wall, gpu) of the headline loop: update i reads the resident batch
-    of slot i mod n where it lies; and of the loop with a device copy of
-    that batch into slot 0's block in front of every update."""
+    of slot i mod n where it lies; then, beside it:
+      repeats            the same loop REPEATS more times (at least
+                         REPEAT_MIN_UPDATES updates each): median and spread;
+      with_metric_read   update i as an agent that drew its batch on the
+                         device pays for it: slot i mod n's graph and the
+                         packed metric read-back in one call, one wait per
+                         update (ttrl_graph_step with no input bytes);
+      copy_in_each_step  a device copy of the batch into slot 0's block in
+                         front of every update."""
     wall, gpu = _time_steps(dev, lambda i: replay_slot(i % n), steps, warmup)
+    per = max(steps, REPEAT_MIN_UPDATES)
+    reps = [per / _time_steps(dev, lambda i: replay_slot(i % n), per, 0)[0] for _ in range(REPEATS)]
+    read = [per / _time_steps(dev, lambda i: run_slot(i % n), per, warmup if k == 0 else 0)[0]
+            for k in range(REPEATS)]
 
     def copied(i):
         slot_block(0).copy_from(slot_block(1 + i % (n - 1)))
         replay_slot(0)
 
     cwall, cgpu = _time_steps(dev, copied, steps, warmup)
-    return wall, gpu, {"value": round(steps / cwall, 2), "ms_per_step": round(cwall / steps * 1e3, 5),
-                       "gpu_ms_per_step": cgpu / steps * 1e3}
+    legs = {"repeats": dict(_spread(reps), updates_per_run=per),
+            "with_metric_read": dict(_spread(read), updates_per_run=per,
+                                     note="resident batch, graph replay and the packed metric read-back in one "
+                                          "call with one wait per update"),
+            "copy_in_each_step": {"value": round(steps / cwall, 2), "ms_per_step": round(cwall / steps * 1e3, 5),
+                                  "gpu_ms_per_step": cgpu / steps * 1e3}}
+    return wall, gpu, legs
 
 
 def bench_dqn(dev, steps, warmup, ring_n, mode="graph"):
@@ -146,8 +190,9 @@ def bench_dqn(dev, steps, warmup, ring_n, mode="graph"):
     slot_block = lambda k: learner.step.slot_inputs(k)["_block"]
     _fill_slots(dev, ring_n, write, slot_block)
     learner.update()  # captures one graph per input slot and runs the first update (slot 0)
-    wall, gpu, copied = _graph_legs(dev, steps, warmup, ring_n, learner.step.replay_slot, slot_block)
-    return learner, wall, gpu, learner.step._trace.nodes, copied
+    wall, gpu, legs = _graph_legs(dev, steps, warmup, ring_n, learner.step.replay_slot, slot_block,
+                                  learner.step.run_slot)
+    return learner, wall, gpu, learner.step._trace.nodes, legs
 
 
 def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
@@ -180,8 +225,9 @@ def bench_sac(dev, steps, warmup, ring_n, mode="graph"):
     _fill_slots(dev, ring_n, write, learner.slot_block)
     learner.update()  # eager first update (slot 0), then one graph captured per input slot
     learner.update()  # first replay
-    wall, gpu, copied = _graph_legs(dev, steps, warmup, ring_n, learner.replay_slot, learner.slot_block)
-    return learner, wall, gpu, learner._graph.nodes, copied
+    wall, gpu, legs = _graph_legs(dev, steps, warmup, ring_n, learner.replay_slot, learner.slot_block,
+                                  learner.run_slot)
+    return learner, wall, gpu, learner._graph.nodes, legs
 
 
 def ppo_step_flops(batch: int = 256, actions: int = 18) -> float:
@@ -346,16 +392,19 @@ def bench_rppo(dev, updates=3, mode="graph"):
 
 def dominant_kernel(dev, learner, reps=200):
     """The DQN update's longest launch, its Adam step, as the update calls it
-    (ttrl_adam_step_sources: k_adam_src over the 1,687,238-float parameter
-    arena, forming the gradients the update left pending as it reads them,
-    then k_finish_sums).  One forward and backward of the update's body run
-    on the bound batch (not captured) leave those sources pending: the three
+    (ttrl_adam_step_sources: k_adam_src over the 1,687,296-float parameter
+    arena, forming the gradients the update left pending as it reads them and
+    updating p, m and v with them without storing the gradients, then
+    k_finish_sums: the update count, sum of g^2, loss and mean Q).  One forward and backward of the update's body run on
+    the bound batch (not captured) leave those sources pending: the three
     convolutions' split-K partials and the two linear layers' outer products.
     The step is then timed alone on the library's stream with HIP events over
     `reps` calls, each forming the same gradients again and stepping.
-    Algorithmic HBM bytes per call: 28 per parameter (p, m, v read and
-    written, g read or, for a source, written) plus each source's operands
-    read once (split partials; an outer product's input and output gradient)."""
+    Algorithmic HBM bytes per call: 24 per parameter whose gradient is formed
+    in the step (p, m, v read and written), 28 per other parameter (g read
+    too), plus the outer products' inputs and output gradients read once;
+    the split-K partials of the convolutions' weight gradients are this
+    build's own intermediate, reported beside it, not counted."""
     from ttrl_amd import _lib
     from ttrl_amd.engine.pending import take_sources, take_sums
 
@@ -381,21 +430,24 @@ def dominant_kernel(dev, learner, reps=200):
     for p in sources:
         p.release()
     sec = ms.value / 1e3 / reps
-    operands = 0
+    outer, partials, formed = 0, 0, 0
     for p in sources:
         s = p.source
+        formed += s.rows * s.cols + (-(-s.cols // 4) * 4 if s.db else 0)
         if s.kind == _lib.GRAD_SPLITS:
-            operands += 4 * s.splits * (s.rows + (1 if s.db else 0)) * s.cols
+            partials += 4 * s.splits * (s.rows + (1 if s.db else 0)) * s.cols
         else:
-            operands += 4 * s.batch * (s.rows + s.cols)
+            outer += 4 * s.batch * (s.rows + s.cols)
     n = opt.arena.numel
     kinds = sorted(f"{p.source.rows}x{p.source.cols} {'split-K' if p.source.kind == _lib.GRAD_SPLITS else 'outer'}"
                    for p in sources)
     return {"name": f"ttrl_adam_step_sources: Adam over the {n:,}-float DQN arena forming {len(sources)} pending "
                     f"gradients ({', '.join(kinds)}), batch 32",
-            "kernels": ["k_adam_src (one launch: sources' workgroups, then the plain float4s)",
-                        "k_finish_sums (update count, sum of g^2, loss and mean Q)"],
-            "seconds": sec, "bytes": 28 * n + operands, "flops": 0.0}
+            "kernels": ["k_adam_src<false> (the sources' workgroups, then the plain float4s; the formed gradients "
+                        "are not stored)", "k_finish_sums (update count, sum of g^2, loss and mean Q)"],
+            "seconds": sec, "bytes": 24 * formed + 28 * (n - formed) + outer, "flops": 0.0,
+            "formed_params": formed, "outer_operand_bytes": outer, "split_partial_bytes": partials,
+            "store_formed_grads": bool(d.store_grads)}
 
 
 def pcie_inclusive(dev, learner, n=100):
@@ -607,14 +659,16 @@ def main() -> int:
     from ttrl_amd.engine.device import open_device
 
     dev = open_device(0)
-    dqn, wall, gpu, nodes, dqn_copied = bench_dqn(dev, args.steps, args.warmup, args.ring, args.mode)
+    dqn, wall, gpu, nodes, dqn_legs = bench_dqn(dev, args.steps, args.warmup, args.ring, args.mode)
     value = args.steps / wall
     flops = dqn_update_flops(32)
-    sac, swall, sgpu, snodes, sac_copied = bench_sac(dev, args.steps, args.warmup, args.ring, args.mode)
+    sac, swall, sgpu, snodes, sac_legs = bench_sac(dev, args.steps, args.warmup, args.ring, args.mode)
+    dqn_legs, sac_legs = dqn_legs or {}, sac_legs or {}
     sac_value = args.steps / swall
     sflops = sac_update_flops(256)
     dom = dominant_kernel(dev, dqn)
     achieved = dom["bytes"] / dom["seconds"]
+    traffic, digest = adam_step_traffic()
     ppo = bench_ppo(dev, args.ppo_updates, args.mode) if args.ppo_updates > 0 else None
     rppo = bench_rppo(dev, max(1, args.ppo_updates // 2), args.mode) if args.ppo_updates > 0 else None
     replay = bench_replay(dev, args.replay_reps, not args.no_cpu_baseline) if args.replay_reps > 0 else None
@@ -637,7 +691,9 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded uint8 frames, resident in HBM, fresh batch per step)",
         "input_slots": args.ring if args.mode == "graph" else 1,
-        "copy_in_each_step": dqn_copied,
+        "repeats": dqn_legs.get("repeats"),
+        "with_metric_read": dqn_legs.get("with_metric_read"),
+        "copy_in_each_step": dqn_legs.get("copy_in_each_step"),
         "mode": args.mode,
         "config": {"workload": "DQN learner update: double DQN, n-step 3, PER weights, Nature-CNN 4x84x84 -> 6, "
                                "Huber 1, Adam lr 6.25e-5 eps 1.5e-4", "batch": 32, "graph_nodes": nodes},
@@ -646,10 +702,12 @@ def main() -> int:
         "sac": {"value": round(sac_value, 2), "unit": "SAC updates/s", "batch": 256,
                 "ms_per_step": round(swall / args.steps * 1e3, 5), "gpu_ms_per_step": sgpu / args.steps * 1e3,
                 "graph_nodes": snodes, "flops_per_update": sflops, "roofline_frac": sflops * sac_value / PEAK_FP32_MFMA,
-                "copy_in_each_step": sac_copied},
+                "repeats": sac_legs.get("repeats"), "with_metric_read": sac_legs.get("with_metric_read"),
+                "copy_in_each_step": sac_legs.get("copy_in_each_step")},
         "roofline": {"bound": "hbm", "kernel": dom["name"], "kernels": dom["kernels"], "achieved": achieved / 1e9,
                      "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved / PEAK_HBM,
-                     "traffic": ADAM_STEP_TRAFFIC_BYTES, "algorithmic_bytes": dom["bytes"],
+                     "traffic": traffic, "traffic_source_sha256": digest, "algorithmic_bytes": dom["bytes"],
+                     "split_partial_bytes": dom["split_partial_bytes"], "formed_params": dom["formed_params"],
                      "avg_us": dom["seconds"] * 1e6},
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",

@@ -523,6 +523,9 @@ typedef struct ttrl_adam_sources_desc {
   const ttrl_grad_source* sources;
   int nsums;
   const ttrl_ordered_sum* sums;
+  int store_grads; /* 0: the formed gradients update the parameters but are not
+                      written into g (ttrl_grad_sources_materialize writes them
+                      from the same operands while those are unchanged) */
 } ttrl_adam_sources_desc;
 int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* desc);
 /* The ordered sums of ttrl_adam_step_sources without a step (up to 4). */

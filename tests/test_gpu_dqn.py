@@ -74,6 +74,9 @@ def test_dqn_update_matches_oracle(device, step_mode, defer):
     # every gradient tensor, each at rel 1e-4 of its own scale (the
     # reference checks every parameter gradient by name,
     # tests/hardware/test_algos_dqn_parity.py:147-152)
+    # the update forms the pending gradients inside its Adam launch without
+    # storing them; written on request from the same operands
+    learner.optimizer.materialize_grads()
     check_grads(grad_state(learner.online), ref["grads"], REL, "dqn")
     new = learner.online.state_dict()
     for (k, got), want in zip(new.items(), ref["new_params"]):

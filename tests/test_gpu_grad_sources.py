@@ -252,7 +252,7 @@ def test_adam_step_with_sources_matches_forming_then_stepping(device, n):
     sums = (_lib.OrderedSum * 2)(_lib.OrderedSum(terms.ptr, 32, 2, 0.5, got_sum.ptr),
                                  _lib.OrderedSum(terms.ptr + 4, 32, 2, 1.0, got_sum.ptr + 4))
     d = _lib.AdamSourcesDesc(got["p"].ptr, got["g"].ptr, got["S"].ptr, got["V"].ptr, n, got["step"].ptr, *hyper,
-                             got["gsq"].ptr, 0, 2, srcs2, 2, sums)
+                             got["gsq"].ptr, 0, 2, srcs2, 2, sums, store_grads=1)
     device.call("ttrl_adam_step_sources", C.byref(d))
     for k in ("p", "g", "S", "V", "step"):
         assert np.array_equal(got[k].numpy(), ref[k].numpy()), k
@@ -263,6 +263,46 @@ def test_adam_step_with_sources_matches_forming_then_stepping(device, n):
     for i in range(32):
         acc = np.float32(acc + t[i, 0])
     assert got_sum.numpy()[0] == np.float32(acc * np.float32(0.5))
+
+
+def test_adam_step_without_storing_the_formed_gradients(device):
+    """store_grads 0: the parameters, moments, count, sum of g^2 and ordered
+    sums are those of the storing step, bit for bit, the sources' gradient
+    ranges of g are left as they were, and materializing the same sources
+    afterwards writes the gradients the storing step would have, after two
+    steps in a row."""
+    from ttrl_amd import _lib
+
+    n = N
+    rng = np.random.default_rng(7)
+    p0, g0 = rng.standard_normal(n), rng.standard_normal(n)
+    g0[OUTER_B + 6:OUTER_B + 8] = 0.0
+    s0, v0 = 0.1 * rng.standard_normal(n), rng.random(n)
+    hyper = (1e-3, 0.9, 0.999, 1e-8, 0.0)
+    terms = _up(device, rng.standard_normal((32, 2)))
+    out = []
+    for store in (1, 0):
+        a = {"p": _up(device, p0), "g": _up(device, g0), "S": _up(device, s0), "V": _up(device, v0),
+             "step": _up(device, np.array([5]), np.int32), "gsq": _empty(device, (1,)), "sum": _empty(device, (1,))}
+        srcs, keep = _arena_sources(device, a["g"].ptr, np.random.default_rng(1))
+        sums = (_lib.OrderedSum * 1)(_lib.OrderedSum(terms.ptr, 32, 2, 0.5, a["sum"].ptr))
+        for _ in range(2):
+            d = _lib.AdamSourcesDesc(a["p"].ptr, a["g"].ptr, a["S"].ptr, a["V"].ptr, n, a["step"].ptr, *hyper,
+                                     a["gsq"].ptr, 0, 2, srcs, 1, sums, store_grads=store)
+            device.call("ttrl_adam_step_sources", C.byref(d))
+        host = {k: v.numpy() for k, v in a.items()}
+        if not store:
+            g = host["g"]
+            untouched = np.asarray(g0, np.float32)
+            for lo, hi in ((SPLIT_W, SPLIT_W + 40 * 32), (OUTER_W, OUTER_W + 64 * 6)):
+                assert np.array_equal(g[lo:hi], untouched[lo:hi])
+            device.call("ttrl_grad_sources_materialize", 2, srcs)
+            host["g"] = a["g"].numpy()
+        out.append((host, keep))
+    (ref, _), (got, _) = out
+    for k in ("p", "g", "S", "V", "step", "gsq", "sum"):
+        assert np.array_equal(got[k], ref[k]), k
+    assert int(got["step"][0]) == 7
 
 
 def test_adam_step_with_sources_refuses_bad_sources(device):
@@ -334,7 +374,7 @@ def test_wide_outer_source_formed_by_tiles(device, rows, cols, batch):
                 *(C.c_float(h) for h in hyper), ref["gsq"].vp, 0)
     got = arena()
     d = _lib.AdamSourcesDesc(got["p"].ptr, got["g"].ptr, got["S"].ptr, got["V"].ptr, n, got["step"].ptr, *hyper,
-                             got["gsq"].ptr, 0, 1, source(got), 0, None)
+                             got["gsq"].ptr, 0, 1, source(got), 0, None, store_grads=1)
     device.call("ttrl_adam_step_sources", C.byref(d))
     for k in ("p", "g", "S", "V", "step"):
         assert np.array_equal(got[k].numpy(), ref[k].numpy()), k

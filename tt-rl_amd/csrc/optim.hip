@@ -488,13 +488,62 @@ __device__ __forceinline__ TileSpot tile_spot(const GradSrc& s, int t) {
   return o;
 }
 
+// Ordered sums dst = scale * sum_{i<n} src[i*stride], one thread each.
+struct OrderedSums {
+  const float* src[kMaxOrderedSums];
+  int n[kMaxOrderedSums], stride[kMaxOrderedSums];
+  float scale[kMaxOrderedSums];
+  float* dst[kMaxOrderedSums];
+  int count;
+};
+// Every term of a sum of at most kSumLds terms is staged in LDS (one memory
+// round trip for all of them, overlapping the caller's own loads), then,
+// after a barrier of the caller's, one thread adds them in order.
+__device__ __forceinline__ void stage_sums(const OrderedSums& s, float (*terms)[kSumLds]) {
+#pragma unroll
+  for (int k = 0; k < kMaxOrderedSums; ++k)
+    if (k < s.count && s.n[k] <= kSumLds)
+      for (int i = threadIdx.x; i < s.n[k]; i += kOptThreads) terms[k][i] = s.src[k][long(i) * s.stride[k]];
+}
+__device__ __forceinline__ void ordered_sums(const OrderedSums& s, const float (*terms)[kSumLds]) {
+  const int k = int(threadIdx.x);
+  if (k >= s.count || k >= kMaxOrderedSums) return;
+  const float* src = s.src[k];
+  const int n = s.n[k], st = s.stride[k];
+  float t = 0.f;
+  if (n <= kSumLds) {
+    for (int i = 0; i < n; ++i) t += terms[k][i];  // in order: the same sum on every run
+  } else {
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) t += src[long(i) * st];
+  }
+  *s.dst[k] = t * s.scale[k];
+}
+
+// The finish of a step: the sum of the workgroups' partials of g^2 (each
+// thread a strided share, then the fixed-order block sum), the update count
+// advanced, the ordered sums formed.  `terms` stages the sums' terms.
+__device__ __forceinline__ void finish_step(const float* __restrict__ partials, int nparts, int* __restrict__ step,
+                                            float* __restrict__ out, int accumulate, const OrderedSums& sums,
+                                            float (*terms)[kSumLds], float* red) {
+  stage_sums(sums, terms);
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += partials[i];
+  const float tot = block_sum<kOptThreads>(s, red);
+  if (threadIdx.x == 0) {
+    if (out) *out = accumulate ? *out + tot : tot;
+    if (step) *step = *step + 1;
+  }
+  ordered_sums(sums, terms);
+}
+
 struct AdamSrcArgs {
   float* p;
   float* g;
   float* S;
   float* V;
   long n;
-  const int* step;
+  int* step;
   float lr, b1, b2, eps, wd;
   float* partials;
   int nsrc;
@@ -510,8 +559,11 @@ struct AdamSrcArgs {
 // grid-stride update over the float4s no source owns, numbered densely: j
 // maps to arena float4 j plus the lengths of the holes at or below it.
 // Block b's partial sum of g^2 goes to partials[b].
+// STORE: the sources' formed gradients are written into g as well.
+template <bool STORE>
 __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_adam_src(AdamSrcArgs a) {
   __shared__ float red[kOptThreads / 64];
+  __shared__ float us[kOuterULds], vs[kOuterLds];
   warm_kernargs<int(sizeof(AdamSrcArgs))>();
   const int blk = int(blockIdx.x);
   float alpha_t, eps_t;
@@ -526,7 +578,6 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
     for (int i = 1; i < kMaxGradSources; ++i)
       if (i < a.nsrc && blk >= a.src[i].block0) k = i;
     const GradSrc& s = a.src[k];
-    __shared__ float us[kOuterULds], vs[kOuterLds];
     if (s.tiled) {
       // a tile (kTileOuts float4s per thread, both slices staged) or a bias block
       const TileSpot t = tile_spot(s, blk - s.block0);
@@ -560,7 +611,7 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
       for (int o = 0; o < kTileOuts; ++o) {
         if (o < nout && t.ok[o]) {
-          Gd[i[o]] = gv[o];
+          if (STORE) Gd[i[o]] = gv[o];
           adam4(pv[o], gv[o], sv[o], vv[o], a.b1, a.b2, a.wd, eps_t, alpha_t, gsq);
           P[i[o]] = pv[o];
           Sv[i[o]] = sv[o];
@@ -599,7 +650,7 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
         sv = Sv[i];
         vv = Vv[i];
       }
-      Gd[i] = gv;
+      if (STORE) Gd[i] = gv;
       adam4(pv, gv, sv, vv, a.b1, a.b2, a.wd, eps_t, alpha_t, gsq);
       P[i] = pv;
       Sv[i] = sv;
@@ -685,55 +736,15 @@ __global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
   }
 }
 
-// Ordered sums dst = scale * sum_{i<n} src[i*stride], one thread each.
-struct OrderedSums {
-  const float* src[kMaxOrderedSums];
-  int n[kMaxOrderedSums], stride[kMaxOrderedSums];
-  float scale[kMaxOrderedSums];
-  float* dst[kMaxOrderedSums];
-  int count;
-};
-// Every term of a sum of at most kSumLds terms is staged in LDS (one memory
-// round trip for all of them, overlapping the caller's own loads), then,
-// after a barrier of the caller's, one thread adds them in order.
-__device__ __forceinline__ void stage_sums(const OrderedSums& s, float (*terms)[kSumLds]) {
-#pragma unroll
-  for (int k = 0; k < kMaxOrderedSums; ++k)
-    if (k < s.count && s.n[k] <= kSumLds)
-      for (int i = threadIdx.x; i < s.n[k]; i += kOptThreads) terms[k][i] = s.src[k][long(i) * s.stride[k]];
-}
-__device__ __forceinline__ void ordered_sums(const OrderedSums& s, const float (*terms)[kSumLds]) {
-  const int k = int(threadIdx.x);
-  if (k >= s.count || k >= kMaxOrderedSums) return;
-  const float* src = s.src[k];
-  const int n = s.n[k], st = s.stride[k];
-  float t = 0.f;
-  if (n <= kSumLds) {
-    for (int i = 0; i < n; ++i) t += terms[k][i];  // in order: the same sum on every run
-  } else {
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) t += src[long(i) * st];
-  }
-  *s.dst[k] = t * s.scale[k];
-}
-
-// k_finish, and the ordered sums, their terms staged while the partials
-// are read (block_sum's barriers order the staging before the sums).
+// The finish of a step as a launch of its own (ttrl_ordered_sums), the
+// sums' terms staged while the partials are read.
 __global__ __launch_bounds__(kOptThreads) void k_finish_sums(const float* __restrict__ partials, int nparts,
                                                              int* __restrict__ step, float* __restrict__ out,
                                                              int accumulate, OrderedSums sums) {
   __shared__ float red[kOptThreads / 64];
   __shared__ float terms[kMaxOrderedSums][kSumLds];
   warm_kernargs<int(sizeof(OrderedSums) + 40)>();
-  stage_sums(sums, terms);
-  float s = 0.f;
-  for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += partials[i];
-  const float tot = block_sum<kOptThreads>(s, red);
-  if (threadIdx.x == 0) {
-    if (out) *out = accumulate ? *out + tot : tot;
-    if (step) *step = *step + 1;
-  }
-  ordered_sums(sums, terms);
+  finish_step(partials, nparts, step, out, accumulate, sums, terms, red);
 }
 
 __global__ __launch_bounds__(kOptThreads) void k_sumsq(const float* __restrict__ x, long n,
@@ -966,7 +977,10 @@ int ttrl_adam_step_sources(ttrl_ctx* ctx, const ttrl_adam_sources_desc* d) {
   a.partials = ctx_workspace(ctx, &wsf);
   TTRL_REQUIRE(wsf >= long(blocks), "ttrl_adam_step_sources: workspace too small");
   hipStream_t st = stream_of(ctx);
-  hipLaunchKernelGGL(k_adam_src, dim3(unsigned(blocks)), dim3(kOptThreads), 0, st, a);
+  if (d->store_grads)
+    hipLaunchKernelGGL(k_adam_src<true>, dim3(unsigned(blocks)), dim3(kOptThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_adam_src<false>, dim3(unsigned(blocks)), dim3(kOptThreads), 0, st, a);
   hipLaunchKernelGGL(k_finish_sums, dim3(1), dim3(kOptThreads), 0, st, a.partials, blocks, d->step, d->grad_sq,
                      d->accumulate_grad_sq, sums);
   return check_launch("ttrl_adam_step_sources");

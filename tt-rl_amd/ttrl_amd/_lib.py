@@ -135,7 +135,7 @@ class AdamSourcesDesc(C.Structure):
         ("step", C.c_void_p), ("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
         ("weight_decay", C.c_float), ("grad_sq", C.c_void_p), ("accumulate_grad_sq", C.c_int),
         ("nsources", C.c_int), ("sources", C.POINTER(GradSource)), ("nsums", C.c_int),
-        ("sums", C.POINTER(OrderedSum)),
+        ("sums", C.POINTER(OrderedSum)), ("store_grads", C.c_int),
     ]
 
 

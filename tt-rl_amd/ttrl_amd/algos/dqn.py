@@ -319,8 +319,11 @@ class DQNLearner:
         self.optimizer = Adam(list(self.online.parameters()), lr=cfg.lr, eps=cfg.adam_eps)
         # The update's weight-gradient reductions (convolution split-K sums,
         # the Q head's outer product) and batch means are formed by the Adam
-        # launch that consumes them, one gradient bank per convolution.
+        # launch that consumes them, one gradient bank per convolution; the
+        # formed gradients update the parameters without a store nothing
+        # reads (optimizer.materialize_grads() writes them on request).
         self.defer_grads = bool(defer_grads)
+        self.optimizer.store_formed_grads = not self.defer_grads
         if self.defer_grads:
             convs = [m for m in getattr(getattr(self.online, "encoder", None), "layers", []) if isinstance(m, Conv2d)]
             for bank, conv in enumerate(convs[:4]):

@@ -748,6 +748,28 @@ class SACLearner:
         self._slots.launch(k)
         self._replayed()
 
+    def run_slot(self, k: int) -> dict:
+        """Slot k's update with its metrics read back: one ttrl_graph_step
+        replaying slot k's graph on the batch already in its block, the packed
+        metric block copied to the host, one wait; -> the metrics as
+        `update` returns them."""
+        if self._slots is None or self._graph is None:
+            raise RuntimeError("SACLearner.run_slot: enable_input_slots() and one graph update first")
+        if not 0 <= k < len(self._slot_batches):
+            raise IndexError(f"input slot {k} outside [0, {len(self._slot_batches)})")
+        span = self._reader.span
+        if span is None:
+            self.replay_slot(k)
+            out = self._reader.read(self._graph_metrics)
+        else:
+            ptr, n, _ = span
+            self.device.call("ttrl_graph_step", self._slots.graphs[k]._graph, None, None, C.c_size_t(0),
+                             C.c_void_p(self._reader.image.ptr), C.c_void_p(ptr), C.c_size_t(n))
+            self._replayed()
+            out = self._reader._unpack(self._graph_metrics)
+        self.update_count += 1
+        return self.summarize(out)
+
     def _run(self) -> dict:
         """One update; -> its metrics, read from the device."""
         binder = self.batch.binder

@@ -79,6 +79,12 @@ class Adam(Optimizer):
         self.b1, self.b2 = float(b1), float(b2)
         self.eps = float(eps)
         self.weight_decay = float(weight_decay)
+        # Whether a step that forms pending gradient sources also writes
+        # them into the gradient buffers.  Off, the parameters move the same
+        # and `materialize_grads()` writes the last step's formed gradients
+        # on request (from operands the next update overwrites).
+        self.store_formed_grads = True
+        self._formed: tuple = ()
         self.t = 0
         self.steps = [0] * len(self.params)
         dev = self.params[0].device
@@ -178,6 +184,21 @@ class Adam(Optimizer):
         self.device.call("ttrl_adam_step_sources", C.byref(d))
         for p in sources:
             p.release()
+        self._formed = () if self.store_formed_grads else tuple(sources)
+
+    def materialize_grads(self) -> None:
+        """Write the gradients the last step formed without storing them
+        (store_formed_grads False) into the parameters' gradient buffers,
+        with the step's own formulas and order, so they hold the same bits
+        a storing step writes.  Call it after the update and before the next
+        launch that reuses the operands (the next update on this device)."""
+        formed = self._formed
+        if not formed:
+            return
+        for i in range(0, len(formed), MAX_SOURCES):
+            chunk = formed[i:i + MAX_SOURCES]
+            arr = (_lib.GradSource * len(chunk))(*[p.source for p in chunk])
+            self.device.call("ttrl_grad_sources_materialize", len(chunk), arr)
 
     def _sources_desc(self, sources, sums):
         """-> (the AdamSourcesDesc of an arena step forming `sources` and the
@@ -187,7 +208,8 @@ class Adam(Optimizer):
         osums = (_lib.OrderedSum * max(1, len(sums)))(*[s for s, _ in sums])
         d = _lib.AdamSourcesDesc(a.data.ptr, a.grad.ptr, self._m_flat.ptr, self._v_flat.ptr, a.numel,
                                  self._counter(len(self.params)).value, self.lr, self.b1, self.b2, self.eps,
-                                 self.weight_decay, self.grad_sq.ptr, 0, len(sources), srcs, len(sums), osums)
+                                 self.weight_decay, self.grad_sq.ptr, 0, len(sources), srcs, len(sums), osums,
+                                 int(self.store_formed_grads))
         return d, (srcs, osums)
 
     # -- deferred steps ------------------------------------------------------

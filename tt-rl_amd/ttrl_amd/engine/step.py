@@ -281,6 +281,28 @@ class TrainStep:
         self._captured_grads = self._slot_grads[k]
         self._after_replay()
 
+    def run_slot(self, k: int) -> dict:
+        """Slot k's update with its metrics read back: one ttrl_graph_step
+        that replays slot k's graph on the batch already in slot k's block,
+        copies the packed metric span to the host and waits once."""
+        if self._slots is None:
+            raise RuntimeError("TrainStep.run_slot: call enable_input_slots() before the first run")
+        if self._trace is None:
+            raise RuntimeError("TrainStep.run_slot: run() once first (it captures every slot's graph)")
+        span = self._reader.span
+        if span is None:
+            self.replay_slot(k)
+            return self._reader.read(self._trace_metrics)
+        if not 0 <= k < len(self._slots.blocks):
+            raise IndexError(f"input slot {k} outside [0, {len(self._slots.blocks)})")
+        ptr, n, _ = span
+        self.device.call("ttrl_graph_step", self._slots.graphs[k]._graph, None, None, C.c_size_t(0),
+                         C.c_void_p(self._reader.image.ptr), C.c_void_p(ptr), C.c_size_t(n))
+        self._binder.synced()
+        self._captured_grads = self._slot_grads[k]
+        self._after_replay()
+        return self._reader._unpack(self._trace_metrics)
+
     def load_input(self, name: str, array) -> None:
         self._binder.load(name, array)
 
