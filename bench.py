@@ -327,6 +327,66 @@ def bench_replay(dev, reps=200, cpu=True):
     return out
 
 
+def bench_agent(dev, steps=300, capacity=1_000_000, lanes=8):
+    """DQN agent gradient steps at batch 32 over a 1M-transition prioritized
+    replay (8 lanes of uint8 4x84x84 frames, n-step 3, resident in HBM): each
+    step is the agent's own gradient step (ttrl/algos/dqn/agent.py:183-214):
+    the prioritized draw on the device assembled straight into the update's
+    bound inputs, the captured update with its packed metric read-back, and
+    the write-back of the batch's TD errors into the priority table from the
+    device.  Also times the draw alone (its call, which waits for the lane
+    sums, plus a stream wait for its kernels)."""
+    from ttrl_amd.algos.agents import DQNAgent
+    from ttrl_amd.algos.dqn import DQNConfig
+    from ttrl_amd.buffers import beta_at
+    from ttrl_amd.spaces import ActionSpec, ObsSpec
+    from ttrl_amd.workloads import he_uniform_qnet_state
+
+    cfg = DQNConfig(lr=6.25e-5, adam_eps=1.5e-4, batch_size=32, prioritized=True, buffer_capacity=capacity,
+                    train_freq=1, learning_starts=0)
+    agent = DQNAgent(ObsSpec.image((4, 84, 84)), ActionSpec.discrete(6), dev, cfg=cfg, n_envs=lanes, seed=0)
+    try:
+        agent.online.load_state_dict(he_uniform_qnet_state(agent.online, 1))
+        agent.target.copy_from(agent.online)
+        rng = np.random.default_rng(11)
+        per_call = 512
+        frames = rng.integers(0, 256, (per_call, lanes, 4, 84, 84), dtype=np.uint8)
+        buf = agent.buffer
+        t0 = time.perf_counter()
+        for _ in range(buf.per_lane_capacity // per_call + 1):
+            buf.add_steps(frames, rng.integers(0, 6, (per_call, lanes)),
+                          rng.choice(np.array([-1.0, 0.0, 1.0], np.float32), (per_call, lanes), p=[0.05, 0.9, 0.05]),
+                          np.zeros((per_call, lanes), bool))
+        cols = np.arange(buf.per_lane_capacity)
+        for lane in range(lanes):
+            for c0 in range(0, cols.size, 1024):
+                cc = cols[c0:c0 + 1024]
+                buf.update_priorities(np.full(cc.size, lane), cc, rng.exponential(1.0, cc.size))
+        dev.synchronize()
+        fill_s = time.perf_counter() - t0
+        for _ in range(20):
+            agent._gradient_step()
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            agent._gradient_step()
+        dev.synchronize()
+        step_s = (time.perf_counter() - t0) / steps
+        beta = beta_at(agent.priority, agent.learner.update_count)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            buf.sample(32, beta=beta, out=agent._out)
+        dev.synchronize()
+        draw_s = (time.perf_counter() - t0) / steps
+        return {"gradient_steps_per_s": round(1.0 / step_s, 1), "us_per_step": round(step_s * 1e6, 2),
+                "prioritized_draw_us": round(draw_s * 1e6, 2), "capacity": buf.capacity, "lanes": lanes,
+                "batch": 32, "fill_seconds": round(fill_s, 2),
+                "note": "DQNAgent._gradient_step: device prioritized draw into the bound inputs, captured update "
+                        "with the packed metric read-back, device PER write-back"}
+    finally:
+        agent.close()
+
+
 def cpu_replay_draw(capacity, lanes, batch, seconds=3.0):
     """The oracle's restatement of the reference's host prioritized draw
     (per-lane cumsum + searchsorted over float64 priorities) and n-step
@@ -642,6 +702,8 @@ def main() -> int:
     ap.add_argument("--act-steps", type=int, default=500, help="acting steps timed per lane count (0: skip)")
     ap.add_argument("--ppo-updates", type=int, default=5, help="PPO updates timed (0: skip)")
     ap.add_argument("--replay-reps", type=int, default=200, help="replay samples timed (0: skip)")
+    ap.add_argument("--agent-steps", type=int, default=300,
+                    help="DQN agent gradient steps timed over a 1M prioritized replay (0: skip)")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph",
                     help="eager dispatches every kernel from the host (for profilers that cannot trace graphs)")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
@@ -672,6 +734,7 @@ def main() -> int:
     ppo = bench_ppo(dev, args.ppo_updates, args.mode) if args.ppo_updates > 0 else None
     rppo = bench_rppo(dev, max(1, args.ppo_updates // 2), args.mode) if args.ppo_updates > 0 else None
     replay = bench_replay(dev, args.replay_reps, not args.no_cpu_baseline) if args.replay_reps > 0 else None
+    agent = bench_agent(dev, args.agent_steps) if args.agent_steps > 0 and args.mode == "graph" else None
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
@@ -715,6 +778,7 @@ def main() -> int:
         "ppo": ppo,
         "recurrent_ppo": rppo,
         "replay": replay,
+        "agent": agent,
         "act": act,
         "cpu_baseline": cpu,
     }

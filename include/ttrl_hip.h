@@ -124,6 +124,12 @@ int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_h
  * read_metrics (ttrl/engine/step/metrics.py:22-30). */
 int ttrl_host_alloc(ttrl_ctx* ctx, size_t bytes, void** out);
 int ttrl_host_free(ttrl_ctx* ctx, void* ptr);
+/* Pinned host memory that kernels read and write in place through *device
+ * (mapped, coherent: no copy, no staging), freed by ttrl_host_free(host) or
+ * at shutdown.  For the few words a host decision and a kernel exchange: a
+ * replay draw's run extents, lane sums and generator draws
+ * (ttrl/buffers/sampling.py:135-240 keeps them in host arrays). */
+int ttrl_host_alloc_mapped(ttrl_ctx* ctx, size_t bytes, void** host, void** device);
 int ttrl_graph_nodes(ttrl_graph* g, size_t* out);
 int ttrl_graph_destroy(ttrl_graph* g);
 
@@ -733,6 +739,41 @@ int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, con
                          int n_step, double gamma, void* obs_out, void* next_obs_out, float* actions_onehot,
                          int num_actions, int* actions_out, float* action_vec_out, float* rewards_out,
                          float* dones_out, float* discounts_out);
+/* One prioritized batch after the host's draws (ttrl/buffers/sampling.py:195-240,
+ * ttrl/buffers/replay.py:254-282): ttrl_replay_priority_pick (also copying
+ * the batch's lanes into lanes_out), then ttrl_replay_is_weights into
+ * weights_out, then ttrl_replay_assemble of the picked (lanes_out, cols_out),
+ * enqueued by one call.  lane, u, start, count and sums may be mapped host
+ * memory (ttrl_host_alloc_mapped); lanes_out and cols_out are device arrays a
+ * later priority update reads. */
+typedef struct ttrl_replay_draw {
+  int n;
+  const int* lane;
+  int* lanes_out;
+  const double* u;
+  const int* start;
+  const int* count;
+  int chunk, max_chunks;
+  const double* chunk_sums;
+  const double* sums;
+  long total_count;
+  double beta;
+  int* cols_out;
+  double* picked_weight;
+  float* weights_out;
+  int n_step;
+  double gamma;
+  void* obs_out;
+  void* next_obs_out;
+  float* actions_onehot;
+  int num_actions;
+  int* actions_out;
+  float* action_vec_out;
+  float* rewards_out;
+  float* dones_out;
+  float* discounts_out;
+} ttrl_replay_draw;
+int ttrl_replay_draw_batch(ttrl_ctx* ctx, const ttrl_replay_ring* ring, const ttrl_replay_draw* draw);
 /* weight[lane[b]][col[b]] = (|priorities[b]| + eps) ** alpha, the last of
  * duplicate columns winning, and *max_priority = max(*max_priority,
  * max |priorities|) (PrioritySampler.update, ttrl/buffers/sampling.py:168-193).

@@ -132,14 +132,27 @@ __global__ __launch_bounds__(kReplayThreads) void k_replay_chunk_sums(Ring r, co
   if (threadIdx.x == 0 && k < max_chunks) csum[long(l) * max_chunks + k] = red[0];
 }
 
-// sums[l] = the lane's chunk sums added in order.
+// sums[l] = the lane's chunk sums added in order, one wavefront per lane:
+// the wavefront stages up to kLaneSumBatch chunk sums in LDS with all its
+// loads in flight at once, then one thread adds them in chunk order (the
+// same additions in the same order as a sequential loop over the chunks).
+constexpr int kLaneSumBatch = 2048;
 __global__ __launch_bounds__(64) void k_replay_lane_sums(int lanes, int max_chunks, const double* __restrict__ csum,
                                                          double* __restrict__ sums) {
-  const int l = blockIdx.x * 64 + threadIdx.x;
-  if (l >= lanes) return;
+  __shared__ double stage[kLaneSumBatch];
+  const int l = blockIdx.x;
+  if (l >= lanes) return;  // uniform over the workgroup
+  const double* cs = csum + long(l) * max_chunks;
   double s = 0.0;
-  for (int k = 0; k < max_chunks; ++k) s += csum[long(l) * max_chunks + k];
-  sums[l] = s;
+  for (int k0 = 0; k0 < max_chunks; k0 += kLaneSumBatch) {
+    const int m = min(kLaneSumBatch, max_chunks - k0);
+    for (int i = threadIdx.x; i < m; i += 64) stage[i] = cs[k0 + i];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int i = 0; i < m; ++i) s += stage[i];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sums[l] = s;
 }
 
 // Wavefront inclusive prefix sum.
@@ -197,10 +210,12 @@ __global__ __launch_bounds__(kReplayThreads) void k_replay_pick(Ring r, int n, c
                                                                 int max_chunks, const double* __restrict__ csum,
                                                                 const double* __restrict__ sums,
                                                                 int* __restrict__ cols_out,
-                                                                double* __restrict__ w_out) {
+                                                                double* __restrict__ w_out,
+                                                                int* __restrict__ lanes_out) {
   const int b = blockIdx.x * (kReplayThreads / 64) + (threadIdx.x >> 6);
   if (b >= n) return;  // uniform per wavefront
   const int l = lane[b];
+  if (lanes_out && (threadIdx.x & 63) == 0) lanes_out[b] = l;
   if (l < 0 || l >= r.lanes) return;
   const int cnt = count[l], st = start[l];
   if (cnt <= 0) return;
@@ -393,8 +408,8 @@ int ttrl_replay_lane_sums(ttrl_ctx* ctx, const ttrl_replay_ring* ring, const int
                      stream_of(ctx), ring_of(ring), start, count, chunk, max_chunks, chunk_sums);
   rc = check_launch("ttrl_replay_lane_sums");
   if (rc) return rc;
-  hipLaunchKernelGGL(k_replay_lane_sums, dim3(unsigned((ring->lanes + 63) / 64)), dim3(64), 0, stream_of(ctx),
-                     ring->lanes, max_chunks, chunk_sums, sums);
+  hipLaunchKernelGGL(k_replay_lane_sums, dim3(unsigned(ring->lanes)), dim3(64), 0, stream_of(ctx), ring->lanes,
+                     max_chunks, chunk_sums, sums);
   return check_launch("ttrl_replay_lane_sums");
 }
 
@@ -410,7 +425,7 @@ int ttrl_replay_priority_pick(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n
   const int per_block = kReplayThreads / 64;
   hipLaunchKernelGGL(k_replay_pick, dim3(unsigned((n + per_block - 1) / per_block)), dim3(kReplayThreads), 0,
                      stream_of(ctx), ring_of(ring), n, lane, u, start, count, chunk, max_chunks, chunk_sums, sums,
-                     cols_out, picked_weight);
+                     cols_out, picked_weight, static_cast<int*>(nullptr));
   return check_launch("ttrl_replay_priority_pick");
 }
 
@@ -440,6 +455,29 @@ int ttrl_replay_assemble(ttrl_ctx* ctx, const ttrl_replay_ring* ring, int n, con
                      static_cast<unsigned char*>(next_obs_out), actions_onehot, num_actions, actions_out,
                      ring->action_vec ? action_vec_out : nullptr, rewards_out, dones_out, discounts_out);
   return check_launch("ttrl_replay_assemble");
+}
+
+int ttrl_replay_draw_batch(ttrl_ctx* ctx, const ttrl_replay_ring* ring, const ttrl_replay_draw* d) {
+  TTRL_REQUIRE(ctx && ring && d, "ttrl_replay_draw_batch: null argument");
+  int rc = check_ring(ring, "ttrl_replay_draw_batch");
+  if (rc) return rc;
+  TTRL_REQUIRE(ring->weight && d->lane && d->u && d->start && d->count && d->chunk_sums && d->sums && d->cols_out &&
+                   d->picked_weight && d->lanes_out,
+               "ttrl_replay_draw_batch: null argument");
+  TTRL_REQUIRE(d->chunk > 0 && d->max_chunks > 0, "ttrl_replay_draw_batch: bad chunking");
+  if (d->n <= 0) return TTRL_OK;
+  const int per_block = kReplayThreads / 64;
+  hipLaunchKernelGGL(k_replay_pick, dim3(unsigned((d->n + per_block - 1) / per_block)), dim3(kReplayThreads), 0,
+                     stream_of(ctx), ring_of(ring), d->n, d->lane, d->u, d->start, d->count, d->chunk, d->max_chunks,
+                     d->chunk_sums, d->sums, d->cols_out, d->picked_weight, d->lanes_out);
+  rc = check_launch("ttrl_replay_draw_batch");
+  if (rc) return rc;
+  rc = ttrl_replay_is_weights(ctx, d->n, d->picked_weight, d->sums, ring->lanes, d->total_count, d->beta,
+                              d->weights_out);
+  if (rc) return rc;
+  return ttrl_replay_assemble(ctx, ring, d->n, d->lanes_out, d->cols_out, d->n_step, d->gamma, d->obs_out,
+                              d->next_obs_out, d->actions_onehot, d->num_actions, d->actions_out, d->action_vec_out,
+                              d->rewards_out, d->dones_out, d->discounts_out);
 }
 
 }  // extern "C"

@@ -527,6 +527,24 @@ int ttrl_host_alloc(ttrl_ctx* ctx, size_t bytes, void** out) {
   return TTRL_OK;
 }
 
+int ttrl_host_alloc_mapped(ttrl_ctx* ctx, size_t bytes, void** host, void** device) {
+  if (!ctx || !host || !device) return set_error(TTRL_EINVAL, "ttrl_host_alloc_mapped: null argument");
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocMapped | hipHostMallocCoherent);
+  if (e != hipSuccess) return hip_error(e, "hipHostMalloc (ttrl_host_alloc_mapped)");
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, p, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return hip_error(e, "hipHostGetDevicePointer (ttrl_host_alloc_mapped)");
+  }
+  std::lock_guard<std::mutex> g(ctx->mu);
+  ctx->host_blocks[p] = bytes ? bytes : 1;
+  *host = p;
+  *device = d;
+  return TTRL_OK;
+}
+
 int ttrl_host_free(ttrl_ctx* ctx, void* ptr) {
   if (!ctx) return set_error(TTRL_EINVAL, "ttrl_host_free: null ctx");
   if (!ptr) return TTRL_OK;

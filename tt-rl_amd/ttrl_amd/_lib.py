@@ -151,6 +151,21 @@ class ReplayRing(C.Structure):
     ]
 
 
+class ReplayDraw(C.Structure):
+    """Mirror of ttrl_replay_draw."""
+
+    _fields_ = [
+        ("n", C.c_int), ("lane", C.c_void_p), ("lanes_out", C.c_void_p), ("u", C.c_void_p), ("start", C.c_void_p),
+        ("count", C.c_void_p),
+        ("chunk", C.c_int), ("max_chunks", C.c_int), ("chunk_sums", C.c_void_p), ("sums", C.c_void_p),
+        ("total_count", C.c_long), ("beta", C.c_double), ("cols_out", C.c_void_p), ("picked_weight", C.c_void_p),
+        ("weights_out", C.c_void_p), ("n_step", C.c_int), ("gamma", C.c_double), ("obs_out", C.c_void_p),
+        ("next_obs_out", C.c_void_p), ("actions_onehot", C.c_void_p), ("num_actions", C.c_int),
+        ("actions_out", C.c_void_p), ("action_vec_out", C.c_void_p), ("rewards_out", C.c_void_p),
+        ("dones_out", C.c_void_p), ("discounts_out", C.c_void_p),
+    ]
+
+
 class ConvGeom(C.Structure):
     """Mirror of ttrl_conv_geom."""
 
@@ -194,6 +209,7 @@ SIGNATURES = {
     "ttrl_graph_step": ([P, P, P, P, SZ, P, P, SZ], I),
     "ttrl_host_alloc": ([P, SZ, C.POINTER(P)], I),
     "ttrl_host_free": ([P, P], I),
+    "ttrl_host_alloc_mapped": ([P, SZ, C.POINTER(P), C.POINTER(P)], I),
     "ttrl_graph_nodes": ([P, C.POINTER(SZ)], I),
     "ttrl_graph_destroy": ([P], I),
     "ttrl_plans_export": ([P, C.c_char_p, SZ, C.POINTER(SZ)], I),
@@ -229,6 +245,7 @@ SIGNATURES = {
     "ttrl_replay_priority_pick": ([P, C.POINTER(ReplayRing), I, P, P, P, P, I, I, P, P, P, P], I),
     "ttrl_replay_is_weights": ([P, I, P, P, I, C.c_long, C.c_double, P], I),
     "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P, P], I),
+    "ttrl_replay_draw_batch": ([P, C.POINTER(ReplayRing), C.POINTER(ReplayDraw)], I),
     "ttrl_replay_update_priorities": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_replay_update_priorities_f64": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),

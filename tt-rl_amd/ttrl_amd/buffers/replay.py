@@ -89,6 +89,24 @@ class DeviceBatch:
         return out
 
 
+class _PriorityWords:
+    """One mapped host block of a prioritized draw: run starts and counts
+    (int32 per lane), lane sums (float64 per lane), the batch's lanes (int32)
+    and uniforms (float64), as numpy views and device addresses."""
+
+    def __init__(self, dev, lanes: int, max_batch: int):
+        layout, off = {}, 0
+        for name, n, dt in (("start", lanes, np.int32), ("count", lanes, np.int32), ("sums", lanes, np.float64),
+                            ("lanes", max_batch, np.int32), ("u", max_batch, np.float64)):
+            off = -(-off // 64) * 64
+            layout[name] = (off, n, dt)
+            off += n * np.dtype(dt).itemsize
+        self.block = dev.mapped_block(off)
+        for name, (o, n, dt) in layout.items():
+            setattr(self, name, self.block.view(o, (n,), dt))
+            setattr(self, "d_" + name, self.block.dptr + o)
+
+
 class ReplayBuffer:
     """Uniform or prioritized off-policy replay with n-step returns over
     `n_envs` lanes, resident in device memory."""
@@ -164,8 +182,17 @@ class ReplayBuffer:
         self._draw_host = np.zeros(self._draw.nbytes, np.uint8)
         if priority is not None:
             self._csum = DeviceArray(dev, (L * self._max_chunks,), np.float64)
-            self._sums = DeviceArray(dev, (L,), np.float64)
             self._picked = DeviceArray(dev, (self.max_batch,), np.float64)
+            # The words a prioritized draw exchanges between host and kernels
+            # (run extents, lane sums, the generator's lanes and uniforms), in
+            # two mapped host blocks used in turn: the kernels read and write
+            # them in place, and a draw never rewrites the block the previous
+            # draw's kernels may still read (each draw waits for its lane sums,
+            # which follow the previous draw's kernels on the stream).
+            self._pm = [_PriorityWords(dev, L, self.max_batch) for _ in range(2)]
+            self._pm_next = 0
+            self._lane_ids = np.arange(L, dtype=np.int32)
+            self._draw_cache: dict = {}
         self._last = None  # (n, device lanes, device cols) of the last draw
 
     # -- size ----------------------------------------------------------------
@@ -375,10 +402,6 @@ class ReplayBuffer:
         if total <= 0:
             raise ValueError(f"ReplayBuffer.sample: no lane holds a complete {self.n_step}-step window and its "
                              f"successor observation yet (size={self.size}); gate on num_sampleable")
-        dev = self.device
-        self._draw_put("start", start)
-        self._draw_put("count", count)
-        d = self._draw_in
         weights = None
         if self.priority is None:
             if beta is not None:
@@ -399,37 +422,75 @@ class ReplayBuffer:
             if beta is None:
                 raise ValueError("ReplayBuffer.sample: this buffer samples by priority, so the batch's "
                                  "importance-sampling weights need a beta (beta_at(cfg, update_count)).")
-            self._draw.upload(self._draw_host)
-            dev.call("ttrl_replay_lane_sums", C.byref(self._ring), d["start"].vp, d["count"].vp, PICK_CHUNK,
-                     self._max_chunks, self._csum.vp, self._sums.vp)
-            sums = self._sums.numpy()
-            if not np.all(np.isfinite(sums)):
-                # A non-finite TD error written by update_priorities_device
-                # (the host path refuses it on entry) poisons its lane's sum.
-                raise ValueError("ReplayBuffer.sample: a priority is NaN or infinite (written by a device "
-                                 "priority update since the last sample)")
-            if sums.sum() <= 0.0:
-                raise RuntimeError(f"replay: {total} transitions are sampleable but every priority in the "
-                                   f"sampleable runs is zero")
-            quota = self._rng.multinomial(batch_size, sums / sums.sum())
-            lanes, us = [], []
-            for lane, k in enumerate(int(v) for v in quota):
-                if k:
-                    lanes.append(np.full(k, lane, np.int64))
-                    us.append(self._rng.random(k))
-            lanes = np.concatenate(lanes)
-            self._draw_put("lanes", lanes)
-            self._draw_put("u", np.concatenate(us))
-            self._draw.upload(self._draw_host)
-            dev.call("ttrl_replay_priority_pick", C.byref(self._ring), batch_size, d["lanes"].vp, d["u"].vp,
-                     d["start"].vp, d["count"].vp, PICK_CHUNK, self._max_chunks, self._csum.vp, self._sums.vp,
-                     d["cols"].vp, self._picked.vp)
-            weights = (out or {}).get("weights") or DeviceArray(dev, (batch_size, 1))
-            dev.call("ttrl_replay_is_weights", batch_size, self._picked.vp, self._sums.vp, self.n_envs,
-                     C.c_long(total), C.c_double(beta), weights.vp)
+            return self._sample_prioritized(batch_size, start, count, total, beta, out)
         return self._assemble(batch_size, out, weights)
 
-    def _assemble(self, n: int, out: dict | None, weights) -> DeviceBatch:
+    def _sample_prioritized(self, n: int, start, count, total: int, beta: float, out) -> DeviceBatch:
+        """The lane sums computed into a mapped block and waited for, the
+        generator's draws in the reference's order (the multinomial lane
+        quota, then each lane's uniforms), then the pick, the IS weights and
+        the assembly enqueued by one call that reads the draws in place
+        (ttrl/buffers/sampling.py:195-240)."""
+        dev = self.device
+        w = self._pm[self._pm_next]
+        self._pm_next ^= 1
+        w.start[:] = start
+        w.count[:] = count
+        dev.call("ttrl_replay_lane_sums", C.byref(self._ring), C.c_void_p(w.d_start), C.c_void_p(w.d_count),
+                 PICK_CHUNK, self._max_chunks, self._csum.vp, C.c_void_p(w.d_sums))
+        dev.synchronize()
+        sums = w.sums.copy()
+        if not np.all(np.isfinite(sums)):
+            # A non-finite TD error written by update_priorities_device
+            # (the host path refuses it on entry) poisons its lane's sum.
+            raise ValueError("ReplayBuffer.sample: a priority is NaN or infinite (written by a device "
+                             "priority update since the last sample)")
+        if sums.sum() <= 0.0:
+            raise RuntimeError(f"replay: {total} transitions are sampleable but every priority in the "
+                               f"sampleable runs is zero")
+        quota = self._rng.multinomial(n, sums / sums.sum())
+        # each lane's uniforms in lane order: one call draws the same
+        # sequence as one call per lane
+        w.lanes[:n] = np.repeat(self._lane_ids, quota)
+        w.u[:n] = self._rng.random(n)
+        desc, batch = self._draw_desc(w, n, out)
+        desc.total_count = total
+        desc.beta = float(beta)
+        dev.call("ttrl_replay_draw_batch", C.byref(self._ring), C.byref(desc))
+        self._last = n
+        return batch
+
+    def _draw_desc(self, w, n: int, out):
+        """The draw call's arguments and the batch it returns, for mapped
+        block w, batch size n and the destinations `out` names, kept for the
+        next draw of the same shape into the same arrays."""
+        key = (id(w), n, None if not out else tuple((k, v.ptr) for k, v in out.items()))
+        hit = self._draw_cache.get(key)
+        if hit is not None:
+            return hit
+        dev = self.device
+        dst = self._outputs(n, out)
+        weights = (out or {}).get("weights") or DeviceArray(dev, (n, 1))
+        d = self._draw_in
+        desc = _lib.ReplayDraw(
+            n=n, lane=w.d_lanes, lanes_out=d["lanes"].ptr, u=w.d_u, start=w.d_start, count=w.d_count,
+            chunk=PICK_CHUNK, max_chunks=self._max_chunks, chunk_sums=self._csum.ptr, sums=w.d_sums,
+            total_count=0, beta=0.0, cols_out=d["cols"].ptr, picked_weight=self._picked.ptr,
+            weights_out=weights.ptr, n_step=self.n_step, gamma=self.gamma, obs_out=dst["obs"].ptr,
+            next_obs_out=dst["next_obs"].ptr, actions_onehot=None if dst["onehot"] is None else dst["onehot"].ptr,
+            num_actions=dst["A"], actions_out=None if self.action_dim else dst["actions"].ptr,
+            action_vec_out=dst["actions"].ptr if self.action_dim else None, rewards_out=dst["rewards"].ptr,
+            dones_out=dst["dones"].ptr, discounts_out=dst["discounts"].ptr)
+        batch = DeviceBatch(dst["obs"], dst["next_obs"], dst["actions"], dst["rewards"], dst["dones"],
+                            dst["discounts"], weights, d["lanes"].view(0, (n,)), d["cols"].view(0, (n,)),
+                            dst["onehot"])
+        if len(self._draw_cache) >= 16:
+            self._draw_cache.clear()
+        self._draw_cache[key] = (desc, batch)
+        return desc, batch
+
+    def _outputs(self, n: int, out: dict | None) -> dict:
+        """The batch's destination arrays: out's where given, else new."""
         dev, out = self.device, dict(out or {})
         A = int(self.action_spec.n) if not self.action_dim else 0
 
@@ -453,14 +514,21 @@ class ReplayBuffer:
                 onehot = dst("actions_onehot", (n, A))
             actions = DeviceArray(dev, (n,), np.int32)
         rewards, dones, discounts = (dst(k, (n, 1)) for k in ("rewards", "dones", "discounts"))
+        return {"obs": obs, "next_obs": nxt, "onehot": onehot, "A": A, "actions": actions, "rewards": rewards,
+                "dones": dones, "discounts": discounts}
+
+    def _assemble(self, n: int, out: dict | None, weights) -> DeviceBatch:
+        o = self._outputs(n, out)
         d = self._draw_in
-        dev.call("ttrl_replay_assemble", C.byref(self._ring), n, d["lanes"].vp, d["cols"].vp, self.n_step,
-                 C.c_double(self.gamma), obs.vp, nxt.vp, None if onehot is None else onehot.vp, A,
-                 None if self.action_dim else actions.vp, actions.vp if self.action_dim else None,
-                 rewards.vp, dones.vp, discounts.vp)
+        onehot, actions = o["onehot"], o["actions"]
+        self.device.call("ttrl_replay_assemble", C.byref(self._ring), n, d["lanes"].vp, d["cols"].vp, self.n_step,
+                         C.c_double(self.gamma), o["obs"].vp, o["next_obs"].vp,
+                         None if onehot is None else onehot.vp, o["A"], None if self.action_dim else actions.vp,
+                         actions.vp if self.action_dim else None, o["rewards"].vp, o["dones"].vp,
+                         o["discounts"].vp)
         self._last = n
-        return DeviceBatch(obs, nxt, actions, rewards, dones, discounts, weights, d["lanes"].view(0, (n,)),
-                           d["cols"].view(0, (n,)), onehot)
+        return DeviceBatch(o["obs"], o["next_obs"], actions, o["rewards"], o["dones"], o["discounts"], weights,
+                           d["lanes"].view(0, (n,)), d["cols"].view(0, (n,)), onehot)
 
     # -- priorities ----------------------------------------------------------
 

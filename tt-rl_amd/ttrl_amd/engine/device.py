@@ -133,6 +133,11 @@ class Device:
         """Pinned host memory owned by this context (see `HostBlock`)."""
         return HostBlock(self, nbytes)
 
+    def mapped_block(self, nbytes: int) -> "HostBlock":
+        """Pinned host memory kernels read and write in place (`dptr` is its
+        device address; see `HostBlock`)."""
+        return HostBlock(self, nbytes, mapped=True)
+
     def create_pool(self) -> int:
         pid = C.c_int(0)
         self.call("ttrl_pool_create", C.byref(pid))
@@ -182,16 +187,23 @@ class HostBlock:
 
     `array` is a uint8 numpy view of it.  Copies between it and device memory
     read and write it in place (no staging pass), which makes it the host
-    image of a bound input block or a metrics block.  The block owns the
-    memory: views of `array` must not outlive it."""
+    image of a bound input block or a metrics block.  A mapped block
+    (`Device.mapped_block`) is also read and written by kernels in place at
+    `dptr`.  The block owns the memory: views of `array` must not outlive it."""
 
-    def __init__(self, dev: Device, nbytes: int):
+    def __init__(self, dev: Device, nbytes: int, *, mapped: bool = False):
         import numpy as np
 
         self.dev = dev
         self.nbytes = max(1, int(nbytes))
         ptr = C.c_void_p()
-        dev.call("ttrl_host_alloc", C.c_size_t(self.nbytes), C.byref(ptr))
+        if mapped:
+            dptr = C.c_void_p()
+            dev.call("ttrl_host_alloc_mapped", C.c_size_t(self.nbytes), C.byref(ptr), C.byref(dptr))
+            self.dptr = int(dptr.value)
+        else:
+            dev.call("ttrl_host_alloc", C.c_size_t(self.nbytes), C.byref(ptr))
+            self.dptr = None
         self.ptr = int(ptr.value)
         self.array = np.frombuffer((C.c_uint8 * self.nbytes).from_address(self.ptr), dtype=np.uint8)
 
