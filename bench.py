@@ -41,8 +41,8 @@ PEAK_FP32_MFMA = 157.3e12
 # passes over the step's kernel, each scaled by what the same counter reads for a 256 MiB
 # device-to-device copy (profiles/dqn_adam_step_roofline_and_traffic.md), and the SHA-256 of the
 # optimizer kernels' source the passes measured: a build from other source reports traffic null.
-ADAM_STEP_TRAFFIC_BYTES = 54479959
-ADAM_STEP_TRAFFIC_SOURCE = ""
+ADAM_STEP_TRAFFIC_BYTES = 47718264
+ADAM_STEP_TRAFFIC_SOURCE = "85ddc6a4d4b27652c70bc9938985100d5dec4c1f4446abe2653c372d03b36c80"
 ADAM_STEP_SOURCES = ("tt-rl_amd/csrc/optim.hip", "tt-rl_amd/csrc/common.hpp")
 PEAK_HBM = 8.0e12
 
