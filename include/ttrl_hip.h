@@ -439,6 +439,66 @@ int ttrl_sac_actor_loss(ttrl_ctx* ctx, int B, const float* q, const float* logp,
                         float target_entropy, int learn_alpha, float* actor_loss, float* alpha_loss, float* dq,
                         float* g_logp, float* d_log_alpha);
 
+/* The SAC update (ttrl/algos/sac/agent.py:218-238 over ttrl/algos/sac/losses.py:25-94,
+ * ttrl/algos/gaussian.py:55-117, ttrl/algos/sac/policy.py:30-40 and the twin
+ * critics and policy of ttrl/nets/build.py) as eight stages, each one
+ * launch over blocks of 16 rows with each workgroup owning 64 of the H
+ * columns of the stage's H x H product (H a multiple of 64 up to 256, the
+ * first layer's inputs at most 64, at most 8 action dimensions, the batch B
+ * a multiple of 16 up to 1024):
+ *   0 policy over [obs; next_obs] to its Gaussian head's quarter partials;
+ *   1 the target critics on (next_obs, a' sampled) and the critics on (obs, actions);
+ *   2 soft target, twin-critic loss gradient, backward of both critics to layer 1;
+ *   3 the critics' weight and bias gradients (outer products over the batch)
+ *     into g_critic;
+ *   4 the (stepped) critics on (obs, a sampled);
+ *   5 actor loss gradient into the smaller critic of each row, backward to d/da;
+ *   6 the sample's backward, dh2, dh1; the actor, critic and temperature
+ *     losses and d alpha_loss / d log_alpha into g_log_alpha (learn_alpha);
+ *   7 the policy's weight and bias gradients into gP1 .. gbl.
+ * The caller steps the critics between stages 3 and 4 and the policy and
+ * temperature after stage 7.  critic[0..1] are the targets, critic[2..3] the
+ * trained critics; every weight is [in][out].  The activation buffers hold
+ * what later stages and the weight gradients read; logp receives the
+ * sample's log-density of all 2B rows (obs rows first). */
+typedef struct ttrl_sac_critic_params {
+  const float *W1, *b1, *W2, *b2, *w3, *b3;
+} ttrl_sac_critic_params;
+typedef struct ttrl_sac_fused_desc {
+  int B, O, A, H;
+  const float *P1, *p1, *P2, *p2, *Wm, *bm, *Wl, *bl;
+  float log_std_min, log_std_max;
+  const float *centre, *half_width;
+  float log_det;
+  ttrl_sac_critic_params critic[4];
+  const float *obs_pair;    /* [2B][O] obs rows, then next_obs rows */
+  const float *actions;     /* [B][A] */
+  const float *obs_actions; /* [B][O + A] */
+  const float *noise_pair;  /* [2B][A] */
+  const float *rewards, *dones, *discounts, *is_weights; /* [B]; is_weights may be NULL */
+  const float *log_alpha;
+  float target_entropy;
+  int learn_alpha;
+  float *h1, *h2;           /* [2B][H] */
+  float *headp;             /* [H/64][2B][2A] */
+  float *head, *act, *u;    /* [2B][2A], [2B][A], [2B][A] */
+  float *q1, *q2;           /* [4][B][H] */
+  float *qp;                /* [4][H/64][B] */
+  float *q1pi, *q2pi;       /* [2][B][H] */
+  float *qppi;              /* [2][H/64][B] */
+  float *dQ;                /* [2][B] */
+  float *dq2, *dq1;         /* [2][B][H] */
+  float *dap;               /* [2][H/64][B][A] */
+  float *dhead;             /* [B][2A] */
+  float *dh2, *dh1;         /* [B][H] */
+  float *terms;             /* [4][B] */
+  float *critic_loss, *alpha, *actor_loss, *alpha_loss, *q_target, *td_abs, *logp;
+  float *gP1, *gp1, *gP2, *gp2, *gWm, *gbm, *gWl, *gbl;
+  float *g_critic[2][6];    /* the trained critics' W1, b1, W2, b2, w3, b3 gradients */
+  float *g_log_alpha;
+} ttrl_sac_fused_desc;
+int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* desc);
+
 /* ----------------------------------------------------------- optimizer --- */
 
 /* One Adam update over a flat range (ttrl/engine/optim/adam.py:93-134 with

@@ -22,12 +22,12 @@ def sac_to_oracle(policy_state: dict, critics_state: dict, targets_state: dict, 
                      targets=[targ[:n], targ[n:]], log_alpha=float(log_alpha))
 
 
-def build_sac(device, *, seed=0, step_mode="graph", batch=256):
+def build_sac(device, *, seed=0, step_mode="graph", batch=256, fused=True, prioritized=False):
     from ttrl_amd.algos.sac import SACConfig, SACLearner
     from ttrl_amd.spaces import ActionSpec, ObsSpec
     from ttrl_amd.workloads import he_uniform_sac_state
 
-    cfg = SACConfig(batch_size=batch, step_mode=step_mode)
+    cfg = SACConfig(batch_size=batch, step_mode=step_mode, fused_update=fused, prioritized=prioritized)
     learner = SACLearner(ObsSpec.vector(11), ActionSpec.continuous(3), device, cfg=cfg, seed=seed)
     pol = he_uniform_sac_state(learner.nets.policy, seed + 10)
     crit = he_uniform_sac_state(learner.nets.critics, seed + 20)

@@ -353,3 +353,43 @@ def test_capture_abort_leaves_the_device_usable(device):
             assert np.array_equal(ops.sub(x, 1.0).numpy(), base - 1.0)  # eager work between replays
     finally:
         trace.close()
+
+
+def test_frees_during_capture_leave_the_capture_intact(device):
+    """A pinned host block or a released pool can be freed while a graph is
+    being captured (a garbage collector finalising an unrelated learner
+    does it from anywhere).  Releasing either waits for the stream, which a
+    capturing stream cannot do; the runtime holds those releases back until
+    the capture ends, so the capture succeeds and its graph replays
+    correctly, and both are released afterwards."""
+    from ttrl_amd.engine import ops
+    from ttrl_amd.engine.trace import capture
+
+    base = np.arange(6, dtype=np.float32).reshape(2, 3)
+    x = _t(device, base, grad=False)
+    ops.mul(x, 5.0)
+    block = device.host_block(4096)
+    mapped = device.mapped_block(4096)
+    pool = device.create_pool()
+    with device.use_pool(pool):
+        kept = device.alloc(1024)
+    device.synchronize()
+
+    def record():
+        y = ops.mul(x, 5.0)
+        block.close()
+        mapped.close()
+        device.release_pool(pool)  # retired: one block still live
+        device.free(kept)  # the last live block: the slabs go back after the capture
+        return ops.add(y, 1.0)
+
+    trace, z = capture(device, record)
+    assert device.pool_stats(pool) == (0, 0)  # released once the capture ended
+    try:
+        for _ in range(3):
+            trace.replay(blocking=True)
+            assert np.array_equal(z.numpy(), base * 5.0 + 1.0)
+    finally:
+        trace.close()
+    again = device.host_block(4096)  # the context still hands out pinned memory
+    again.close()

@@ -46,13 +46,16 @@ def _check_params(got_state: dict, ref_flat, grads, lr, label):
     return undecided
 
 
-@pytest.mark.parametrize("step_mode", ["graph", "eager"])
-def test_sac_update_matches_oracle(device, step_mode):
+@pytest.mark.parametrize("step_mode,fused", [("graph", True), ("eager", True), ("graph", False), ("eager", False)])
+def test_sac_update_matches_oracle(device, step_mode, fused):
+    """fused: the update as the library's eight fused stages
+    (ttrl_sac_fused_stage) rather than one launch per layer."""
     from oracle.sac import sac_update
     from ttrl_amd.engine import layers
     from ttrl_amd.workloads import sac_batch
 
-    learner, pol, crit = build_sac(device, seed=0, step_mode=step_mode)
+    learner, pol, crit = build_sac(device, seed=0, step_mode=step_mode, fused=fused)
+    assert (learner._fused is not None) == fused
     batch = sac_batch(7)
     P = sac_to_oracle(pol, crit, crit, 0.0)
     layers.RECORD = []

@@ -70,6 +70,10 @@ struct ttrl_ctx {
   size_t pinned_bytes = 0;
   // Pinned host blocks handed out by ttrl_host_alloc (base -> bytes).
   std::unordered_map<void*, size_t> host_blocks;
+  // Host blocks freed while the stream was capturing: releasing one waits for
+  // the stream, which a capturing stream cannot do, so they go back once the
+  // capture has ended (release_after_capture).
+  std::vector<void*> host_frees_after_capture;
 };
 
 struct ttrl_graph {
@@ -165,6 +169,28 @@ void pool_free_slabs(Pool& p) {
   p.cursor = nullptr;
   p.left = 0;
   p.reserved = 0;
+}
+
+// Releases held back while the stream captured a graph: host blocks freed in
+// the meantime and retired pools whose last block went back.  A free can
+// arrive during a capture from anywhere in the host program (a garbage
+// collector finalising an unrelated object), and the stream wait a release
+// needs would invalidate the capture.
+void release_after_capture(ttrl_ctx* ctx) {
+  std::lock_guard<std::mutex> g(ctx->mu);
+  bool pools_due = false;
+  for (auto& p : ctx->pools) pools_due |= p.retired && p.live == 0;
+  if (!pools_due && ctx->host_frees_after_capture.empty()) return;
+  (void)hipStreamSynchronize(ctx->stream);
+  for (auto& p : ctx->pools) {
+    if (p.retired && p.live == 0) {
+      pool_free_slabs(p);
+      p.retired = false;
+      p.in_use = false;
+    }
+  }
+  for (void* h : ctx->host_frees_after_capture) (void)hipHostFree(h);
+  ctx->host_frees_after_capture.clear();
 }
 
 }  // namespace
@@ -306,6 +332,7 @@ int ttrl_shutdown(ttrl_ctx* ctx) {
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
   if (ctx->pinned) (void)hipHostFree(ctx->pinned);
   for (auto& hb : ctx->host_blocks) (void)hipHostFree(hb.first);
+  for (void* h : ctx->host_frees_after_capture) (void)hipHostFree(h);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return TTRL_OK;
@@ -347,12 +374,12 @@ int ttrl_pool_release(ttrl_ctx* ctx, int pool) {
     return set_error(TTRL_EINVAL, "ttrl_pool_release: bad pool %d", pool);
   if (ctx->current_pool == pool) ctx->current_pool = 0;
   Pool& p = ctx->pools[pool];
-  if (p.live == 0) {
+  if (p.live == 0 && !ctx->capturing) {
     (void)hipStreamSynchronize(ctx->stream);
     pool_free_slabs(p);
     p.in_use = false;
   } else {
-    p.retired = true;  // slabs go back when the last live block is freed
+    p.retired = true;  // slabs go back when the last live block is freed, or after the capture
   }
   return TTRL_OK;
 }
@@ -414,7 +441,7 @@ int ttrl_free(ttrl_ctx* ctx, void* ptr) {
   Pool& p = ctx->pools[b.pool];
   p.live -= b.size;
   p.free_lists[b.size].push_back(static_cast<char*>(ptr));
-  if (p.retired && p.live == 0) {
+  if (p.retired && p.live == 0 && !ctx->capturing) {
     (void)hipStreamSynchronize(ctx->stream);
     pool_free_slabs(p);
     p.retired = false;
@@ -478,6 +505,7 @@ int ttrl_capture_end(ttrl_ctx* ctx, ttrl_graph** out) {
   ctx->capturing = false;
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+  release_after_capture(ctx);
   if (e != hipSuccess) {
     if (graph) (void)hipGraphDestroy(graph);
     return hip_error(e, "hipStreamEndCapture");
@@ -505,6 +533,7 @@ int ttrl_capture_abort(ttrl_ctx* ctx) {
   (void)hipStreamEndCapture(ctx->stream, &graph);
   if (graph) (void)hipGraphDestroy(graph);
   (void)hipGetLastError();
+  release_after_capture(ctx);
   return TTRL_OK;
 }
 
@@ -551,6 +580,11 @@ int ttrl_host_free(ttrl_ctx* ctx, void* ptr) {
   std::lock_guard<std::mutex> g(ctx->mu);
   auto it = ctx->host_blocks.find(ptr);
   if (it == ctx->host_blocks.end()) return set_error(TTRL_EINVAL, "ttrl_host_free: %p was not allocated here", ptr);
+  if (ctx->capturing) {
+    ctx->host_blocks.erase(it);
+    ctx->host_frees_after_capture.push_back(ptr);
+    return TTRL_OK;
+  }
   // A copy from or to the block may still be queued on the stream.
   (void)hipStreamSynchronize(ctx->stream);
   (void)hipHostFree(ptr);

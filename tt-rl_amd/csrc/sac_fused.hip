@@ -1,0 +1,693 @@
+// The SAC learner update as eight row-block launches (ttrl/algos/sac/agent.py:218-238,
+// ttrl/algos/sac/losses.py:25-94, ttrl/algos/gaussian.py:55-117, ttrl/algos/sac/policy.py:30-40).
+//
+// Every network here is Linear(in -> H) -> ReLU -> Linear(H -> H) -> ReLU ->
+// a narrow head, H a multiple of 64 up to 256.  A launch works on blocks of
+// 16 rows; each workgroup owns 64 of the H columns of the one wide (H x H)
+// product of its stage, so a block of rows is spread over H / 64
+// workgroups.  The narrow layers either side of the wide one are row-local
+// and run inside the same workgroup: the first layer (in <= 64) is formed
+// straight into the LDS operand of the wide product, and the head after it
+// (the Gaussian head's 2 x d columns, a critic's single column, the action
+// columns of a critic's input gradient) is left as one partial dot product
+// per 64-column quarter, summed in quarter order by the next stage.  The
+// per-row pieces in between (the squashed sample, the soft target, the
+// losses and their gradients, the sample's backward) are formed where a
+// stage needs them.
+//
+//   stage 0  policy over [obs; next_obs]: layer 1, layer 2 (H x H), head partials
+//   stage 1  the four critics of the critic region (targets on (s', a'), the
+//            critics on (s, a)): a' sampled from the head partials, layer 1,
+//            layer 2, Q partials
+//   stage 2  soft target, twin-critic loss and its gradient, dq2 = dQ w3 [q2 > 0],
+//            dq1 = dq2 W2^T [q1 > 0] for both critics
+//   stage 3  the critics' weight and bias gradients: batched outer products
+//            over the batch (W1: z^T dq1, W2: q1^T dq2, w3: q2^T dQ)
+//   stage 4  the two (just stepped) critics on (s, a): a sampled, layers 1-2, Q partials
+//   stage 5  actor loss terms, dQ to the smaller critic of each row, its
+//            backward to layer 1 and partial d/da
+//   stage 6  d/da summed, the sample's backward to the head, dh2, dh1 = dh2 P2^T [h1 > 0];
+//            workgroup 0 also forms the actor, temperature and critic losses and
+//            d alpha_loss / d log_alpha
+//   stage 7  the policy's weight and bias gradients (outer products)
+//
+// Products run on v_mfma_f32_16x16x4f32: a wavefront owns one 16 x 16 tile.
+// Lane l supplies, at step s of each 16-wide k block, A(row l % 16,
+// k = 4 (l / 16) + s) and B(k = 4 (l / 16) + s, col l % 16), a permutation
+// of the block both operands share, so a lane reads four consecutive k of
+// an A row (one 128-bit LDS read) and of a transposed B row (one 128-bit
+// global read).  Every sum runs in a fixed order, so replays are
+// bit-identical.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace ttrl {
+namespace {
+
+constexpr int kRows = 16;       // rows per workgroup
+constexpr int kQ = 64;          // columns of the wide product per workgroup
+constexpr int kThreads = 256;   // four wavefronts: four 16 x 16 tiles
+constexpr int kMaxH = 256;
+constexpr int kLda = kMaxH + 4;  // LDS row stride of the wide product's A operand
+constexpr int kMaxIn = 64;       // first-layer inputs
+constexpr int kMaxA = 8;         // action dimensions
+constexpr int kMaxB = 1024;      // batch rows (workgroup 0 of stage 6 stages four rows of terms)
+constexpr float kLog2f = 0.69314718055994530942f;
+constexpr float kLog2Pif = 1.83787706640934548356f;
+
+__device__ __forceinline__ float relu_s(float x) { return x > 0.f ? x : 0.f; }
+__device__ __forceinline__ float softplus_s(float x) { return relu_s(x) + logf(expf(-fabsf(x)) + 1.f); }
+// min(a, b) as a - relu(a - b): the gradient goes to b iff a > b (ttrl/engine/ops/select.py:39-47)
+__device__ __forceinline__ float min_relu_s(float a, float b) { return a - relu_s(a - b); }
+
+struct CriticP {
+  const float *W1, *b1, *W2, *b2, *w3, *b3;
+};
+
+struct FusedArgs {
+  int B, O, A, H, nq;
+  const float *P1, *p1, *P2, *p2, *Wm, *bm, *Wl, *bl;
+  float lo, hi;
+  const float *centre, *half;
+  float log_det;
+  CriticP cr[4];
+  const float *obs_pair, *actions, *obs_actions, *noise_pair;
+  const float *rewards, *dones, *discounts, *weights;
+  const float* log_alpha;
+  float target_entropy;
+  int learn_alpha;
+  float *h1, *h2, *headp, *head, *act, *u;
+  float *q1, *q2, *qp, *q1pi, *q2pi, *qppi;
+  float *dQ, *dq2, *dq1, *dap, *dhead, *dh2, *dh1, *terms;
+  float *critic_loss, *alpha, *actor_loss, *alpha_loss, *q_target, *td_abs, *logp;
+  float* g_log_alpha;
+};
+
+// acc(4 rows x 1 column per lane) = A[0:16][0:K] x B[0:K][col], A in LDS
+// (row stride kLda), B(k, n) = TRANS ? W[n * ldw + k] : W[k * ldw + n].
+// K is a multiple of 64.  Every B value of the product is loaded before the
+// first MFMA, so the product waits one memory round trip.
+template <bool TRANS>
+__device__ __forceinline__ f32x4 rows16_product(const float* At, int K, const float* __restrict__ W, int ldw,
+                                                int col) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 b[kMaxH / 16];
+#pragma unroll
+  for (int j = 0; j < kMaxH / 16; ++j) {
+    const int k = 16 * j + 4 * g;
+    if (16 * j < K) {  // uniform
+      if constexpr (TRANS) {
+        b[j] = *reinterpret_cast<const f32x4*>(W + long(col) * ldw + k);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) b[j][s] = W[long(k + s) * ldw + col];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxH / 16; ++j) {
+    if (16 * j < K) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(At + c * kLda + 16 * j + 4 * g);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b[j].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b[j].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b[j].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b[j].w, acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+// out[r][k] = relu(sum_j X[r][j] W[j][k] + b[k]) for the block's 16 rows and
+// k < H (thread t owns columns t, t + 256, ...); X in LDS (row stride
+// kMaxIn), W [J][H].  Also stored to gout[r][k] (row stride H) when given.
+__device__ __forceinline__ void first_layer(const float* X, int J, const float* __restrict__ W,
+                                            const float* __restrict__ b, int H, float* At, float* gout) {
+  for (int k = threadIdx.x; k < H; k += kThreads) {
+    float acc[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
+    for (int j = 0; j < J; ++j) {
+      const float w = W[long(j) * H + k];
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) acc[r] = fmaf(X[r * kMaxIn + j], w, acc[r]);
+    }
+    const float bk = b[k];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const float v = relu_s(acc[r] + bk);
+      At[r * kLda + k] = v;
+      if (gout) gout[long(r) * H + k] = v;
+    }
+  }
+}
+
+// The squashed sample of policy row `prow` (ttrl/algos/gaussian.py:106-167,
+// the stable log-density of ttrl/algos/sac/policy.py:30-40): the head summed
+// from its quarter partials plus bias, log_std clamped; writes the action
+// into xa[0:A] and, when `store`, the head, action, pre-squash u and log-prob.
+__device__ void sample_row(const FusedArgs& a, int prow, float* xa, bool store) {
+  const int A = a.A, A2 = 2 * a.A, rows = 2 * a.B;
+  float normal = 0.f, corr = 0.f;
+  for (int j = 0; j < A; ++j) {
+    float mu = 0.f, lsr = 0.f;
+    for (int q = 0; q < a.nq; ++q) {
+      mu += a.headp[(long(q) * rows + prow) * A2 + j];
+      lsr += a.headp[(long(q) * rows + prow) * A2 + A + j];
+    }
+    mu += a.bm[j];
+    lsr += a.bl[j];
+    const float ls = fminf(fmaxf(lsr, a.lo), a.hi);
+    const float sigma = expf(ls);
+    const float uu = mu + sigma * a.noise_pair[long(prow) * A + j];
+    const float z = (uu - mu) / sigma;
+    normal += (z * z) * -0.5f - ls;
+    corr += ((kLog2f - uu) - softplus_s(uu * -2.f)) * 2.f;
+    const float t = tanhf(uu);
+    const float act = t * a.half[j] + a.centre[j];
+    xa[j] = act;
+    if (store) {
+      a.head[long(prow) * A2 + j] = mu;
+      a.head[long(prow) * A2 + A + j] = ls;
+      a.act[long(prow) * A + j] = act;
+      a.u[long(prow) * A + j] = uu;
+    }
+  }
+  if (store) a.logp[prow] = ((normal - 0.5f * float(A) * kLog2Pif) - corr) - a.log_det;
+}
+
+// ------------------------------------------------------------ stage 0 ---
+// grid (2B / 16, nq): the policy over [obs; next_obs].
+__global__ __launch_bounds__(kThreads) void k_sac_policy_fwd(FusedArgs a) {
+  __shared__ float X[kRows * kMaxIn];
+  __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
+  __shared__ float Y[kRows * (kQ + 1)];
+  __shared__ float Wh[kQ * 2 * kMaxA];
+  const int r0 = blockIdx.x * kRows, q = blockIdx.y, t = threadIdx.x;
+  const int O = a.O, H = a.H, A2 = 2 * a.A, rows = 2 * a.B;
+  for (int i = t; i < kRows * O; i += kThreads) {
+    const int r = i / O, j = i - r * O;
+    X[r * kMaxIn + j] = a.obs_pair[long(r0 + r) * O + j];
+  }
+  for (int i = t; i < kQ * A2; i += kThreads) {
+    const int n = i / A2, j = i - n * A2, col = q * kQ + n;
+    Wh[n * A2 + j] = j < a.A ? a.Wm[long(col) * a.A + j] : a.Wl[long(col) * a.A + (j - a.A)];
+  }
+  __syncthreads();
+  first_layer(X, O, a.P1, a.p1, H, At, q == 0 ? a.h1 + long(r0) * H : nullptr);
+  __syncthreads();
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
+  const f32x4 acc = rows16_product<false>(At, H, a.P2, H, col);
+  const float bias = a.p2[col];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * g + i;
+    const float y = relu_s(acc[i] + bias);
+    a.h2[long(r0 + row) * H + col] = y;
+    Y[row * (kQ + 1) + w * 16 + c] = y;
+  }
+  __syncthreads();
+  if (t < kRows * A2) {
+    const int row = t / A2, j = t - row * A2;
+    float s = 0.f;
+    for (int n = 0; n < kQ; ++n) s = fmaf(Y[row * (kQ + 1) + n], Wh[n * A2 + j], s);
+    a.headp[(long(q) * rows + r0 + row) * A2 + j] = s;
+  }
+}
+
+// ------------------------------------------------------ stages 1 and 4 ---
+// grid (B / 16, nq, G).  REGION 0: the critic region's four groups (0, 1:
+// target critics on (next_obs, a' sampled here); 2, 3: the critics on
+// (obs, the batch's actions)).  REGION 1: the actor region's two groups (the
+// critics on (obs, a sampled here)).
+template <int REGION>
+__global__ __launch_bounds__(kThreads) void k_sac_critic_fwd(FusedArgs a) {
+  __shared__ float X[kRows * kMaxIn];
+  __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
+  __shared__ float Y[kRows * (kQ + 1)];
+  const int r0 = blockIdx.x * kRows, q = blockIdx.y, grp = blockIdx.z, t = threadIdx.x;
+  const int O = a.O, A = a.A, H = a.H, B = a.B;
+  const CriticP cp = REGION == 0 ? a.cr[grp] : a.cr[2 + grp];
+  const bool next = REGION == 0 && grp < 2;        // rows of next_obs
+  const bool sampled = REGION == 1 || grp < 2;      // actions sampled from the policy
+  const int prow0 = next ? B + r0 : r0;             // the rows' index among the policy's 2B rows
+  for (int i = t; i < kRows * O; i += kThreads) {
+    const int r = i / O, j = i - r * O;
+    X[r * kMaxIn + j] = a.obs_pair[long(prow0 + r) * O + j];
+  }
+  if (!sampled) {
+    for (int i = t; i < kRows * A; i += kThreads) {
+      const int r = i / A, j = i - r * A;
+      X[r * kMaxIn + O + j] = a.actions[long(r0 + r) * A + j];
+    }
+  } else if (t < kRows) {
+    // the first sampling group's first quarter stores the sample of its rows
+    sample_row(a, prow0 + t, X + t * kMaxIn + O, q == 0 && grp == 0);
+  }
+  __syncthreads();
+  float* q1 = REGION == 0 ? a.q1 : a.q1pi;
+  float* q2 = REGION == 0 ? a.q2 : a.q2pi;
+  float* qp = REGION == 0 ? a.qp : a.qppi;
+  first_layer(X, O + A, cp.W1, cp.b1, H, At, q == 0 ? q1 + (long(grp) * B + r0) * H : nullptr);
+  __syncthreads();
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
+  const f32x4 acc = rows16_product<false>(At, H, cp.W2, H, col);
+  const float bias = cp.b2[col];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * g + i;
+    const float y = relu_s(acc[i] + bias);
+    q2[(long(grp) * B + r0 + row) * H + col] = y;
+    Y[row * (kQ + 1) + w * 16 + c] = y;
+  }
+  __syncthreads();
+  if (t < kRows) {
+    float s = 0.f;
+    for (int n = 0; n < kQ; ++n) s = fmaf(Y[t * (kQ + 1) + n], cp.w3[q * kQ + n], s);
+    qp[(long(grp) * a.nq + q) * B + r0 + t] = s;
+  }
+}
+
+// Q of group grp, row r: its quarter partials in order, plus the bias.
+__device__ __forceinline__ float q_of(const float* qp, int nq, int B, int grp, int r, const float* b3) {
+  float s = 0.f;
+  for (int q = 0; q < nq; ++q) s += qp[(long(grp) * nq + q) * B + r];
+  return s + *b3;
+}
+
+// ------------------------------------------------------------ stage 2 ---
+// grid (B / 16, nq, 2): critic j's loss gradient and its backward to layer 1
+// (ttrl/algos/sac/losses.py:46-76).
+__global__ __launch_bounds__(kThreads) void k_sac_critic_bwd(FusedArgs a) {
+  __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
+  __shared__ float dqs[kRows];
+  const int rb = blockIdx.x, r0 = rb * kRows, q = blockIdx.y, j = blockIdx.z, t = threadIdx.x;
+  const int H = a.H, B = a.B, nq = a.nq;
+  const CriticP cp = a.cr[2 + j];
+  if (t < kRows) {
+    const int r = r0 + t;
+    const float invB = 1.f / float(B);
+    const float alpha = expf(*a.log_alpha);
+    const float qt0 = q_of(a.qp, nq, B, 0, r, a.cr[0].b3), qt1 = q_of(a.qp, nq, B, 1, r, a.cr[1].b3);
+    const float q0 = q_of(a.qp, nq, B, 2, r, a.cr[2].b3), q1v = q_of(a.qp, nq, B, 3, r, a.cr[3].b3);
+    const float soft = min_relu_s(qt0, qt1) - a.logp[B + r] * alpha;
+    const float y = a.rewards[r] + (soft * (1.f - a.dones[r])) * a.discounts[r];
+    const float e0 = q0 - y, e1 = q1v - y;
+    const float wgt = a.weights ? a.weights[r] : 1.f;
+    const float gs = wgt * (0.5f * invB) * 2.f;
+    const float dq = (j == 0 ? e0 : e1) * gs;
+    dqs[t] = dq;
+    if (q == 0) a.dQ[long(j) * B + r] = dq;
+    if (q == 0 && j == 0) {
+      a.q_target[r] = y;
+      if (a.td_abs) a.td_abs[r] = (fabsf(e0) + fabsf(e1)) * 0.5f;
+      a.terms[2L * B + r] = a.weights ? (e0 * e0) * wgt : e0 * e0;
+      a.terms[3L * B + r] = a.weights ? (e1 * e1) * wgt : e1 * e1;
+      if (r == 0) *a.alpha = alpha;
+    }
+  }
+  __syncthreads();
+  // dq2 = dQ w3 [q2 > 0], the wide product's operand (stored once for the weight gradients)
+  const float* q2 = a.q2 + (long(2 + j) * B + r0) * H;
+  float* dq2 = a.dq2 + (long(j) * B + r0) * H;
+  for (int i = t; i < kRows * H; i += kThreads) {
+    const int r = i / H, k = i - r * H;
+    const float v = q2[long(r) * H + k] > 0.f ? dqs[r] * cp.w3[k] : 0.f;
+    At[r * kLda + k] = v;
+    if (q == 0) dq2[long(r) * H + k] = v;
+  }
+  __syncthreads();
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
+  const f32x4 acc = rows16_product<true>(At, H, cp.W2, H, col);
+  const float* q1 = a.q1 + (long(2 + j) * B + r0) * H;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * g + i;
+    a.dq1[(long(j) * B + r0 + row) * H + col] = q1[long(row) * H + col] > 0.f ? acc[i] : 0.f;
+  }
+}
+
+// ------------------------------------------------------------ stage 5 ---
+// grid (B / 16, nq, 2): the actor loss's gradient into the smaller critic of
+// each row (ttrl/algos/sac/losses.py:79-94) and critic j's backward to the
+// action columns of its input, as quarter partials of d/da.
+__global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
+  __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
+  __shared__ float Y[kRows * (kQ + 1)];
+  __shared__ float dqs[kRows];
+  const int r0 = blockIdx.x * kRows, q = blockIdx.y, j = blockIdx.z, t = threadIdx.x;
+  const int H = a.H, B = a.B, nq = a.nq, O = a.O, A = a.A;
+  const CriticP cp = a.cr[2 + j];
+  if (t < kRows) {
+    const int r = r0 + t;
+    const float invB = 1.f / float(B);
+    const float q0 = q_of(a.qppi, nq, B, 0, r, a.cr[2].b3), q1v = q_of(a.qppi, nq, B, 1, r, a.cr[3].b3);
+    const bool second = q0 - q1v > 0.f;
+    dqs[t] = (j == (second ? 1 : 0)) ? -invB : 0.f;
+    if (q == 0 && j == 0) {
+      const float lp = a.logp[r];
+      const float alpha = expf(*a.log_alpha);
+      a.terms[r] = lp * alpha - min_relu_s(q0, q1v);
+      a.terms[long(B) + r] = lp + a.target_entropy;
+    }
+  }
+  __syncthreads();
+  const float* q2 = a.q2pi + (long(j) * B + r0) * H;
+  for (int i = t; i < kRows * H; i += kThreads) {
+    const int r = i / H, k = i - r * H;
+    At[r * kLda + k] = q2[long(r) * H + k] > 0.f ? dqs[r] * cp.w3[k] : 0.f;
+  }
+  __syncthreads();
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
+  const f32x4 acc = rows16_product<true>(At, H, cp.W2, H, col);
+  const float* q1 = a.q1pi + (long(j) * B + r0) * H;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * g + i;
+    Y[row * (kQ + 1) + w * 16 + c] = q1[long(row) * H + col] > 0.f ? acc[i] : 0.f;
+  }
+  __syncthreads();
+  if (t < kRows * A) {
+    const int row = t / A, aa = t - row * A;
+    const float* w1 = cp.W1 + long(O + aa) * H + q * kQ;
+    float s = 0.f;
+    for (int n = 0; n < kQ; ++n) s = fmaf(Y[row * (kQ + 1) + n], w1[n], s);
+    a.dap[((long(j) * nq + q) * B + r0 + row) * A + aa] = s;
+  }
+}
+
+// ------------------------------------------------------------ stage 6 ---
+// grid (B / 16, nq): d/da of every row, the sample's backward to the head
+// (the reparameterised path and the log-density's explicit terms), dh2 and
+// dh1.  Workgroup (0, 0) also forms the update's scalar losses and the
+// temperature's gradient from the terms stages 2 and 5 left.
+__global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
+  __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
+  __shared__ float DH[kRows * 2 * kMaxA];
+  __shared__ float T4[4 * kMaxB];
+  const int r0 = blockIdx.x * kRows, q = blockIdx.y, t = threadIdx.x;
+  const int H = a.H, B = a.B, nq = a.nq, A = a.A, A2 = 2 * a.A;
+  const float alpha = expf(*a.log_alpha);
+  const float invB = 1.f / float(B);
+  if (t < kRows * A) {
+    const int row = t / A, aa = t - row * A, r = r0 + row;
+    float ga = 0.f;
+    for (int j = 0; j < 2; ++j)
+      for (int qq = 0; qq < nq; ++qq) ga += a.dap[((long(j) * nq + qq) * B + r) * A + aa];
+    const float mu = a.head[long(r) * A2 + aa], ls = a.head[long(r) * A2 + A + aa];
+    const float sigma = expf(ls);
+    const float eps = a.noise_pair[long(r) * A + aa];
+    const float uu = a.u[long(r) * A + aa];
+    const float z = (uu - mu) / sigma;
+    const float th = tanhf(uu);
+    const float glp = alpha * invB;
+    const float gu = ga * a.half[aa] * (1.f - th * th) + glp * (2.f * th - z / sigma);
+    const float gmu = gu + glp * (z / sigma);
+    float gls = gu * (sigma * eps) + glp * (z * z - 1.f);
+    gls = (ls > a.lo && ls < a.hi) ? gls : 0.f;
+    DH[row * A2 + aa] = gmu;
+    DH[row * A2 + A + aa] = gls;
+    if (q == 0) {
+      a.dhead[long(r) * A2 + aa] = gmu;
+      a.dhead[long(r) * A2 + A + aa] = gls;
+    }
+  }
+  __syncthreads();
+  // dh2 = (dhead Wh^T) [h2 > 0]
+  for (int i = t; i < kRows * H; i += kThreads) {
+    const int r = i / H, k = i - r * H;
+    float s = 0.f;
+    for (int jj = 0; jj < A; ++jj) s = fmaf(DH[r * A2 + jj], a.Wm[long(k) * A + jj], s);
+    for (int jj = 0; jj < A; ++jj) s = fmaf(DH[r * A2 + A + jj], a.Wl[long(k) * A + jj], s);
+    const float v = a.h2[long(r0 + r) * H + k] > 0.f ? s : 0.f;
+    At[r * kLda + k] = v;
+    if (q == 0) a.dh2[long(r0 + r) * H + k] = v;
+  }
+  __syncthreads();
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
+  const f32x4 acc = rows16_product<true>(At, H, a.P2, H, col);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * g + i;
+    a.dh1[long(r0 + row) * H + col] = a.h1[long(r0 + row) * H + col] > 0.f ? acc[i] : 0.f;
+  }
+  if (blockIdx.x != 0 || q != 0) return;  // uniform
+  for (int i = t; i < 4 * B; i += kThreads) T4[i] = a.terms[i];
+  __syncthreads();
+  if (t == 0) {
+    float sa = 0.f, se = 0.f, s0 = 0.f, s1 = 0.f;
+    for (int i = 0; i < B; ++i) sa += T4[i];
+    for (int i = 0; i < B; ++i) se += T4[B + i];
+    for (int i = 0; i < B; ++i) s0 += T4[2 * B + i];
+    for (int i = 0; i < B; ++i) s1 += T4[3 * B + i];
+    *a.actor_loss = sa * invB;
+    *a.critic_loss = (s0 * invB + s1 * invB) * 0.5f;
+    if (a.learn_alpha) {
+      const float la = *a.log_alpha;
+      if (a.alpha_loss) *a.alpha_loss = (la * (se * invB)) * -1.f;
+      if (a.g_log_alpha) *a.g_log_alpha = (se * invB) * -1.f;
+    }
+  }
+}
+
+// --------------------------------------------------------- stages 3, 7 ---
+// Weight and bias gradients as outer products over the batch:
+// dw[m][n] = sum_b u[b][m] v[b][n], db[n] = sum_b v[b][n] (row M of the
+// tile grid, u taken as 1).  A workgroup owns 16 rows x 64 columns of one
+// problem, a wavefront one 16 x 16 tile.
+constexpr int kMaxOuter = 8;
+struct OuterProb {
+  const float* u;
+  int ldu, M;
+  const float* v;
+  int ldv, N;
+  float* dw;
+  float* db;
+  int tiles_n, wg0;
+};
+struct OuterArgs {
+  int nbatch, nprob;
+  OuterProb p[kMaxOuter];
+};
+
+__global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
+  const int wg = blockIdx.x;
+  int k = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxOuter; ++i)
+    if (i < a.nprob && wg >= a.p[i].wg0) k = i;
+  const OuterProb& p = a.p[k];
+  const int local = wg - p.wg0, tm = local / p.tiles_n, tn = local - tm * p.tiles_n;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
+  const int m = tm * kRows + c;                 // the A row this lane supplies
+  const int col = tn * kQ + w * 16 + c;         // the B column this lane supplies
+  const bool mrow = m < p.M, bias = m == p.M && p.db != nullptr, ncol = col < p.N;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < a.nbatch; kb += 128) {
+    float av[32], bv[32];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kk = kb + 16 * j + 4 * g + s;
+        const bool in = kk < a.nbatch;
+        av[4 * j + s] = in && mrow ? p.u[long(kk) * p.ldu + m] : (in && bias ? 1.f : 0.f);
+        bv[4 * j + s] = in && ncol ? p.v[long(kk) * p.ldv + col] : 0.f;
+      }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = tm * kRows + 4 * g + i;
+    const int n = tn * kQ + w * 16 + c;
+    if (n >= p.N) continue;
+    if (row < p.M) p.dw[long(row) * p.N + n] = acc[i];
+    else if (row == p.M && p.db) p.db[n] = acc[i];
+  }
+}
+
+bool aligned16(const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; }
+
+int add_outer(OuterArgs& o, int& wgs, const float* u, int ldu, int M, const float* v, int ldv, int N, float* dw,
+              float* db, const char* name) {
+  TTRL_REQUIRE(o.nprob < kMaxOuter, "%s: too many gradient products", name);
+  TTRL_REQUIRE(u && v && dw && M > 0 && N > 0 && ldu >= M && ldv >= N, "%s: bad gradient product", name);
+  OuterProb& p = o.p[o.nprob++];
+  p.u = u;
+  p.ldu = ldu;
+  p.M = M;
+  p.v = v;
+  p.ldv = ldv;
+  p.N = N;
+  p.dw = dw;
+  p.db = db;
+  p.tiles_n = int(ceil_div(N, kQ));
+  p.wg0 = wgs;
+  wgs += int(ceil_div(M + (db ? 1 : 0), kRows)) * p.tiles_n;
+  return TTRL_OK;
+}
+
+}  // namespace
+}  // namespace ttrl
+
+using namespace ttrl;
+
+extern "C" {
+
+int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d) {
+  TTRL_REQUIRE(ctx && d, "ttrl_sac_fused_stage: null argument");
+  const int B = d->B, O = d->O, A = d->A, H = d->H;
+  TTRL_REQUIRE(B > 0 && B % kRows == 0 && B <= kMaxB, "ttrl_sac_fused_stage: batch %d must be a multiple of %d, "
+               "at most %d", B, kRows, kMaxB);
+  TTRL_REQUIRE(H > 0 && H % kQ == 0 && H <= kMaxH, "ttrl_sac_fused_stage: hidden width %d must be a multiple of "
+               "%d, at most %d", H, kQ, kMaxH);
+  TTRL_REQUIRE(A > 0 && A <= kMaxA && O > 0 && O + A <= kMaxIn, "ttrl_sac_fused_stage: %d observation and %d "
+               "action dimensions (at most %d actions, %d together)", O, A, kMaxA, kMaxIn);
+  TTRL_REQUIRE(aligned16(d->P2) && aligned16(d->critic[2].W2) && aligned16(d->critic[3].W2),
+               "ttrl_sac_fused_stage: the H x H weights must be 16-byte aligned");
+  FusedArgs a{};
+  a.B = B;
+  a.O = O;
+  a.A = A;
+  a.H = H;
+  a.nq = H / kQ;
+  a.P1 = d->P1;
+  a.p1 = d->p1;
+  a.P2 = d->P2;
+  a.p2 = d->p2;
+  a.Wm = d->Wm;
+  a.bm = d->bm;
+  a.Wl = d->Wl;
+  a.bl = d->bl;
+  a.lo = d->log_std_min;
+  a.hi = d->log_std_max;
+  a.centre = d->centre;
+  a.half = d->half_width;
+  a.log_det = d->log_det;
+  for (int i = 0; i < 4; ++i) {
+    const ttrl_sac_critic_params& c = d->critic[i];
+    TTRL_REQUIRE(c.W1 && c.b1 && c.W2 && c.b2 && c.w3 && c.b3, "ttrl_sac_fused_stage: critic %d: null weight", i);
+    a.cr[i] = CriticP{c.W1, c.b1, c.W2, c.b2, c.w3, c.b3};
+  }
+  a.obs_pair = d->obs_pair;
+  a.actions = d->actions;
+  a.obs_actions = d->obs_actions;
+  a.noise_pair = d->noise_pair;
+  a.rewards = d->rewards;
+  a.dones = d->dones;
+  a.discounts = d->discounts;
+  a.weights = d->is_weights;
+  a.log_alpha = d->log_alpha;
+  a.target_entropy = d->target_entropy;
+  a.learn_alpha = d->learn_alpha;
+  a.h1 = d->h1;
+  a.h2 = d->h2;
+  a.headp = d->headp;
+  a.head = d->head;
+  a.act = d->act;
+  a.u = d->u;
+  a.q1 = d->q1;
+  a.q2 = d->q2;
+  a.qp = d->qp;
+  a.q1pi = d->q1pi;
+  a.q2pi = d->q2pi;
+  a.qppi = d->qppi;
+  a.dQ = d->dQ;
+  a.dq2 = d->dq2;
+  a.dq1 = d->dq1;
+  a.dap = d->dap;
+  a.dhead = d->dhead;
+  a.dh2 = d->dh2;
+  a.dh1 = d->dh1;
+  a.terms = d->terms;
+  a.critic_loss = d->critic_loss;
+  a.alpha = d->alpha;
+  a.actor_loss = d->actor_loss;
+  a.alpha_loss = d->alpha_loss;
+  a.q_target = d->q_target;
+  a.td_abs = d->td_abs;
+  a.logp = d->logp;
+  a.g_log_alpha = d->g_log_alpha;
+  const unsigned nq = unsigned(a.nq), rb = unsigned(B / kRows);
+  hipStream_t st = stream_of(ctx);
+  const char* name = "ttrl_sac_fused_stage";
+  switch (stage) {
+    case 0:
+      TTRL_REQUIRE(a.P1 && a.p1 && a.P2 && a.p2 && a.Wm && a.bm && a.Wl && a.bl && a.obs_pair && a.h1 && a.h2 &&
+                       a.headp,
+                   "%s: stage 0: null argument", name);
+      hipLaunchKernelGGL(k_sac_policy_fwd, dim3(2 * rb, nq), dim3(kThreads), 0, st, a);
+      break;
+    case 1:
+    case 4:
+      TTRL_REQUIRE(a.obs_pair && a.noise_pair && a.headp && a.head && a.act && a.u && a.logp && a.centre && a.half,
+                   "%s: stage %d: null argument", name, stage);
+      if (stage == 1) {
+        TTRL_REQUIRE(a.actions && a.q1 && a.q2 && a.qp, "%s: stage 1: null argument", name);
+        hipLaunchKernelGGL(k_sac_critic_fwd<0>, dim3(rb, nq, 4), dim3(kThreads), 0, st, a);
+      } else {
+        TTRL_REQUIRE(a.q1pi && a.q2pi && a.qppi, "%s: stage 4: null argument", name);
+        hipLaunchKernelGGL(k_sac_critic_fwd<1>, dim3(rb, nq, 2), dim3(kThreads), 0, st, a);
+      }
+      break;
+    case 2:
+      TTRL_REQUIRE(a.qp && a.q1 && a.q2 && a.logp && a.rewards && a.dones && a.discounts && a.log_alpha && a.dQ &&
+                       a.dq2 && a.dq1 && a.terms && a.q_target && a.alpha,
+                   "%s: stage 2: null argument", name);
+      hipLaunchKernelGGL(k_sac_critic_bwd, dim3(rb, nq, 2), dim3(kThreads), 0, st, a);
+      break;
+    case 5:
+      TTRL_REQUIRE(a.qppi && a.q1pi && a.q2pi && a.logp && a.log_alpha && a.dap && a.terms,
+                   "%s: stage 5: null argument", name);
+      hipLaunchKernelGGL(k_sac_actor_bwd, dim3(rb, nq, 2), dim3(kThreads), 0, st, a);
+      break;
+    case 6:
+      TTRL_REQUIRE(a.dap && a.head && a.noise_pair && a.u && a.h1 && a.h2 && a.dhead && a.dh2 && a.dh1 &&
+                       a.terms && a.log_alpha && a.actor_loss && a.critic_loss,
+                   "%s: stage 6: null argument", name);
+      hipLaunchKernelGGL(k_sac_policy_bwd, dim3(rb, nq), dim3(kThreads), 0, st, a);
+      break;
+    case 3:
+    case 7: {
+      OuterArgs o{};
+      o.nbatch = B;
+      int wgs = 0, rc = 0;
+      if (stage == 3) {
+        for (int j = 0; j < 2; ++j) {
+          float* const* gc = d->g_critic[j];
+          TTRL_REQUIRE(gc[0] && gc[1] && gc[2] && gc[3] && gc[4] && gc[5] && a.obs_actions,
+                       "%s: stage 3: null gradient", name);
+          rc = add_outer(o, wgs, a.obs_actions, O + A, O + A, a.dq1 + long(j) * B * H, H, H, gc[0], gc[1], name);
+          if (!rc)
+            rc = add_outer(o, wgs, a.q1 + long(2 + j) * B * H, H, H, a.dq2 + long(j) * B * H, H, H, gc[2], gc[3],
+                           name);
+          if (!rc) rc = add_outer(o, wgs, a.q2 + long(2 + j) * B * H, H, H, a.dQ + long(j) * B, 1, 1, gc[4], gc[5],
+                                  name);
+          if (rc) return rc;
+        }
+      } else {
+        TTRL_REQUIRE(d->gP1 && d->gp1 && d->gP2 && d->gp2 && d->gWm && d->gbm && d->gWl && d->gbl,
+                     "%s: stage 7: null gradient", name);
+        rc = add_outer(o, wgs, a.obs_pair, O, O, a.dh1, H, H, d->gP1, d->gp1, name);
+        if (!rc) rc = add_outer(o, wgs, a.h1, H, H, a.dh2, H, H, d->gP2, d->gp2, name);
+        if (!rc) rc = add_outer(o, wgs, a.h2, H, H, a.dhead, 2 * A, A, d->gWm, d->gbm, name);
+        if (!rc) rc = add_outer(o, wgs, a.h2, H, H, a.dhead + A, 2 * A, A, d->gWl, d->gbl, name);
+        if (rc) return rc;
+      }
+      hipLaunchKernelGGL(k_outer_grads, dim3(unsigned(wgs)), dim3(kThreads), 0, st, o);
+      break;
+    }
+    default:
+      return set_error(TTRL_EINVAL, "%s: stage %d outside [0, 7]", name, stage);
+  }
+  return check_launch(name);
+}
+
+}  // extern "C"

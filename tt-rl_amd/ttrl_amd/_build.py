@@ -21,7 +21,7 @@ OBJ_DIR = PKG_DIR.parent / "_build"
 LIB_PATH = LIB_DIR / "libttrl_hip.so"
 
 SOURCES = ("runtime.hip", "gemm.hip", "conv_fwd.hip", "conv_dw.hip", "conv_dx.hip", "conv_bwd.hip", "eltwise.hip",
-           "heads.hip", "dqn_tail.hip", "optim.hip", "ppo.hip", "act.hip", "rollout.hip", "replay.hip", "gru.hip")
+           "heads.hip", "dqn_tail.hip", "optim.hip", "ppo.hip", "act.hip", "rollout.hip", "replay.hip", "gru.hip", "sac_fused.hip")
 
 ARCH = "gfx950"
 

@@ -166,6 +166,32 @@ class ReplayDraw(C.Structure):
     ]
 
 
+class SacCriticParams(C.Structure):
+    """Mirror of ttrl_sac_critic_params."""
+
+    _fields_ = [(n, C.c_void_p) for n in ("W1", "b1", "W2", "b2", "w3", "b3")]
+
+
+SAC_FUSED_BUFFERS = ("h1", "h2", "headp", "head", "act", "u", "q1", "q2", "qp", "q1pi", "q2pi", "qppi", "dQ", "dq2",
+                     "dq1", "dap", "dhead", "dh2", "dh1", "terms")
+SAC_FUSED_METRICS = ("critic_loss", "alpha", "actor_loss", "alpha_loss", "q_target", "td_abs", "logp")
+SAC_FUSED_POLICY_GRADS = ("gP1", "gp1", "gP2", "gp2", "gWm", "gbm", "gWl", "gbl")
+
+
+class SacFusedDesc(C.Structure):
+    """Mirror of ttrl_sac_fused_desc."""
+
+    _fields_ = ([("B", C.c_int), ("O", C.c_int), ("A", C.c_int), ("H", C.c_int)]
+                + [(n, C.c_void_p) for n in ("P1", "p1", "P2", "p2", "Wm", "bm", "Wl", "bl")]
+                + [("log_std_min", C.c_float), ("log_std_max", C.c_float), ("centre", C.c_void_p),
+                   ("half_width", C.c_void_p), ("log_det", C.c_float), ("critic", SacCriticParams * 4)]
+                + [(n, C.c_void_p) for n in ("obs_pair", "actions", "obs_actions", "noise_pair", "rewards", "dones",
+                                             "discounts", "is_weights", "log_alpha")]
+                + [("target_entropy", C.c_float), ("learn_alpha", C.c_int)]
+                + [(n, C.c_void_p) for n in SAC_FUSED_BUFFERS + SAC_FUSED_METRICS + SAC_FUSED_POLICY_GRADS]
+                + [("g_critic", (C.c_void_p * 6) * 2), ("g_log_alpha", C.c_void_p)])
+
+
 class ConvGeom(C.Structure):
     """Mirror of ttrl_conv_geom."""
 
@@ -246,6 +272,7 @@ SIGNATURES = {
     "ttrl_replay_is_weights": ([P, I, P, P, I, C.c_long, C.c_double, P], I),
     "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P, P], I),
     "ttrl_replay_draw_batch": ([P, C.POINTER(ReplayRing), C.POINTER(ReplayDraw)], I),
+    "ttrl_sac_fused_stage": ([P, I, C.POINTER(SacFusedDesc)], I),
     "ttrl_replay_update_priorities": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_replay_update_priorities_f64": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),

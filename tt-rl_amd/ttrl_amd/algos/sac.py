@@ -62,6 +62,9 @@ class SACConfig:
     target_entropy: float | None = None
     prioritized: bool = False
     step_mode: str = "graph"
+    # the update as the library's fused stages when the networks have the
+    # standard shape (two hidden layers of one width); the per-layer path otherwise
+    fused_update: bool = True
     critic_hidden: tuple = (256, 256)
     policy_hidden: tuple = (256, 256)
     act_mode: str = "graph"
@@ -463,6 +466,155 @@ def policy_sample_rows(policy, obs_all: DeviceArray, B: int, noise_all: DeviceAr
     return sampled_rows_tape(h, action_all, logp_all, noise_all, u, scale, head.log_std_min, head.log_std_max)
 
 
+class _FusedUpdate:
+    """The update as the library's eight fused stages (ttrl_sac_fused_stage)
+    and the three optimizer launches, for the standard networks: a policy of
+    two Linear -> ReLU layers of width H with a Gaussian head, twin critics
+    (and targets) concat(s, a) -> H -> H -> 1, H a multiple of 64 up to 256,
+    a batch a multiple of 16.  The stages' activation buffers are allocated
+    once here; the weight and bias gradients are written into the arenas'
+    gradient slots, the temperature's into its slot, every metric into the
+    learner's metric block."""
+
+    def __init__(self, learner, H: int):
+        self.learner = learner
+        dev, B = learner.device, learner.cfg.batch_size
+        O, A = learner.obs_spec.size, learner.action_spec.dim
+        nq = H // 64
+        self.B, self.O, self.A, self.H = B, O, A, H
+        shapes = {"h1": (2 * B, H), "h2": (2 * B, H), "headp": (nq, 2 * B, 2 * A), "head": (2 * B, 2 * A),
+                  "act": (2 * B, A), "u": (2 * B, A), "q1": (4, B, H), "q2": (4, B, H), "qp": (4, nq, B),
+                  "q1pi": (2, B, H), "q2pi": (2, B, H), "qppi": (2, nq, B), "dQ": (2, B), "dq2": (2, B, H),
+                  "dq1": (2, B, H), "dap": (2, nq, B, A), "dhead": (B, 2 * A), "dh2": (B, H), "dh1": (B, H),
+                  "terms": (4, B)}
+        self.buf = {k: DeviceArray(dev, v) for k, v in shapes.items()}
+
+    @staticmethod
+    def width(learner):
+        """H when the learner's networks and batch fit the fused stages, else None."""
+        cfg = learner.cfg
+        if not cfg.fused_update or not learner._stacked:
+            return None
+        pol = learner.nets.policy
+        lins = _linear_relu_pairs(pol.encoder)
+        if lins is None or len(lins) != 2:
+            return None
+        H = lins[0].out_features
+        O, A, B = learner.obs_spec.size, learner.action_spec.dim, cfg.batch_size
+        if lins[0].in_features != O or lins[1].in_features != H or lins[1].out_features != H:
+            return None
+        if H % 64 or H > 256 or B % 16 or B > 1024 or A > 8 or O + A > 64:
+            return None
+        head = pol.head
+        for lin in (head.heads["mean"], head.heads["log_std"]):
+            if lin.in_features != H or lin.out_features != A or lin.bias is None:
+                return None
+        for twin in (learner.twin, learner.twin_targets):
+            for lins_c in twin.layers:
+                if len(lins_c) != 3:
+                    return None
+                l1, l2, l3 = lins_c
+                if (l1.in_features, l1.out_features, l2.in_features, l2.out_features, l3.in_features,
+                        l3.out_features) != (O + A, H, H, H, H, 1):
+                    return None
+                if any(x.bias is None for x in lins_c):
+                    return None
+        wide = [lins[1].weight] + [c[1].weight for c in learner.twin.layers]
+        if any(w.data.ptr % 16 for w in wide):
+            return None
+        return H
+
+    def _desc(self) -> "_lib.SacFusedDesc":
+        L = self.learner
+        b, cfg, buf = L.batch, L.cfg, self.buf
+        pol = L.nets.policy
+        p1, p2 = _linear_relu_pairs(pol.encoder)
+        head = pol.head
+        mean, log_std = head.heads["mean"], head.heads["log_std"]
+        d = _lib.SacFusedDesc()
+        d.B, d.O, d.A, d.H = self.B, self.O, self.A, self.H
+        d.P1, d.p1, d.P2, d.p2 = p1.weight.data.ptr, p1.bias.data.ptr, p2.weight.data.ptr, p2.bias.data.ptr
+        d.Wm, d.bm, d.Wl, d.bl = mean.weight.data.ptr, mean.bias.data.ptr, log_std.weight.data.ptr, \
+            log_std.bias.data.ptr
+        d.log_std_min, d.log_std_max = head.log_std_min, head.log_std_max
+        d.centre, d.half_width, d.log_det = L.scale._centre.data.ptr, L.scale._scale.data.ptr, L.scale.log_det
+        for i, lins_c in enumerate(list(L.twin_targets.layers) + list(L.twin.layers)):
+            l1, l2, l3 = lins_c
+            d.critic[i] = _lib.SacCriticParams(l1.weight.data.ptr, l1.bias.data.ptr, l2.weight.data.ptr,
+                                               l2.bias.data.ptr, l3.weight.data.ptr, l3.bias.data.ptr)
+        d.obs_pair, d.actions, d.obs_actions = b.obs_pair.ptr, b["actions"].data.ptr, b["obs_actions"].data.ptr
+        d.noise_pair = b.noise_pair.ptr
+        d.rewards, d.dones, d.discounts = b["rewards"].data.ptr, b["dones"].data.ptr, b["discounts"].data.ptr
+        d.is_weights = b["is_weights"].data.ptr if cfg.prioritized else None
+        d.log_alpha, d.target_entropy, d.learn_alpha = L.log_alpha.data.ptr, L.target_entropy, int(cfg.learn_alpha)
+        for name in _lib.SAC_FUSED_BUFFERS:
+            setattr(d, name, buf[name].ptr)
+        out = {"critic_loss": L._critic_out["loss"], "alpha": L._critic_out["alpha"],
+               "actor_loss": L._actor_out["actor_loss"], "alpha_loss": L._actor_out["alpha_loss"],
+               "q_target": L._critic_out["q_target"], "td_abs": L._critic_out["td_abs"], "logp": L._logp_all}
+        for name in _lib.SAC_FUSED_METRICS:
+            setattr(d, name, out[name].ptr)
+        grads = []
+        for lin in (p1, p2, mean, log_std):
+            grads += [lin.weight._grad_slot, lin.bias._grad_slot]
+        for name, g in zip(_lib.SAC_FUSED_POLICY_GRADS, grads):
+            setattr(d, name, g.ptr)
+        for j, lins_c in enumerate(L.twin.layers):
+            slots = [t._grad_slot for lin in lins_c for t in (lin.weight, lin.bias)]
+            for k, g in enumerate(slots):
+                d.g_critic[j][k] = g.ptr
+        d.g_log_alpha = L.log_alpha._grad_slot.ptr if cfg.learn_alpha else None
+        return d
+
+    def _stage(self, d, k: int) -> None:
+        self.learner.device.call("ttrl_sac_fused_stage", int(k), C.byref(d))
+
+    @staticmethod
+    def _written(params) -> None:
+        """Every parameter's gradient is in its slot (a stage wrote it)."""
+        for p in params:
+            p.grad, p._grad_owned, p._grad_masked = p._grad_slot, True, False
+
+    def body(self) -> dict:
+        L = self.learner
+        cfg, buf = L.cfg, self.buf
+        for opt in (L.critic_opt, L.actor_opt, L.alpha_opt):
+            opt.zero_grad()
+        d = self._desc()
+        B, H = self.B, self.H
+        rec = layers_mod.RECORD
+        self._stage(d, 0)
+        self._stage(d, 1)
+        if rec is not None:
+            rec += [buf["h1"], buf["h2"], buf["q1"], buf["q2"]]
+        self._stage(d, 2)
+        self._stage(d, 3)
+        self._written(L.critic_opt.params)
+        L.critic_opt.step_deferred(0)
+        self._stage(d, 4)
+        if rec is not None:
+            rec += [buf["q1pi"], buf["q2pi"]]
+        self._stage(d, 5)
+        self._stage(d, 6)
+        self._stage(d, 7)
+        self._written(L.actor_opt.params)
+        stepped = [(L.actor_opt, 1)]
+        if cfg.learn_alpha:
+            self._written([L.log_alpha])
+            stepped.append((L.alpha_opt, 2))
+        adam_multi(L.device, stepped, polyak=(L.nets.targets.arena.data, L.nets.critics.arena.data, cfg.tau))
+        finish_steps(L.device, [(L.critic_opt, 0)] + stepped)
+        metrics = {"critic_loss": Tensor(L._critic_out["loss"]), "alpha": Tensor(L._critic_out["alpha"]),
+                   "q_target": Tensor(L._critic_out["q_target"]), "actor_loss": Tensor(L._actor_out["actor_loss"]),
+                   "logp": Tensor(L._logp_out), "critic_grad_sq": Tensor(L.critic_opt.grad_sq),
+                   "actor_grad_sq": Tensor(L.actor_opt.grad_sq)}
+        if cfg.prioritized:
+            metrics["td_abs"] = Tensor(L._critic_out["td_abs"])
+        if cfg.learn_alpha:
+            metrics["alpha_loss"] = Tensor(L._actor_out["alpha_loss"])
+        return metrics
+
+
 class _BatchBuffers:
     """Bound device buffers of one SAC batch, back to back in one block
     (`block`), allocated once and written in place."""
@@ -574,6 +726,8 @@ class SACLearner:
         self.frame_count = 0
         self._rng = np.random.default_rng(seed)
         self._eval_rng = np.random.default_rng(seed).spawn(1)[0]
+        H = _FusedUpdate.width(self)
+        self._fused = None if H is None else _FusedUpdate(self, H)
 
     # -- state ---------------------------------------------------------------
 
@@ -678,6 +832,8 @@ class SACLearner:
         return out
 
     def _body(self) -> dict:
+        if self._fused is not None:
+            return self._fused.body()
         self.critic_opt.zero_grad()
         self.actor_opt.zero_grad()
         self.alpha_opt.zero_grad()

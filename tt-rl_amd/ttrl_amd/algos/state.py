@@ -90,7 +90,7 @@ def _config_diff(saved, current) -> str:
 
 
 # Fields that choose how an update is dispatched, not what it computes.
-_DISPATCH_ONLY = frozenset({"step_mode", "act_mode"})
+_DISPATCH_ONLY = frozenset({"step_mode", "act_mode", "fused_update"})
 
 
 def _plain(value):
