@@ -52,7 +52,7 @@ constexpr int kMaxH = 256;
 constexpr int kLda = kMaxH + 4;  // LDS row stride of the wide product's A operand
 constexpr int kMaxIn = 64;       // first-layer inputs
 constexpr int kMaxA = 8;         // action dimensions
-constexpr int kMaxB = 1024;      // batch rows (workgroup 0 of stage 6 stages four rows of terms)
+constexpr int kMaxB = 1024;      // batch rows accepted
 constexpr float kLog2f = 0.69314718055994530942f;
 constexpr float kLog2Pif = 1.83787706640934548356f;
 
@@ -120,27 +120,68 @@ __device__ __forceinline__ f32x4 rows16_product(const float* At, int K, const fl
 }
 
 // out[r][k] = relu(sum_j X[r][j] W[j][k] + b[k]) for the block's 16 rows and
-// k < H (thread t owns columns t, t + 256, ...); X in LDS (row stride
-// kMaxIn), W [J][H].  Also stored to gout[r][k] (row stride H) when given.
+// k < H (thread t owns column t, H <= the workgroup's 256 threads); X in LDS
+// (row stride kMaxIn), W [J][H].  Each 16-row chunk of W's column is loaded
+// before its products, so the layer waits one memory round trip per 16
+// inputs.  Also stored to gout[r][k] (row stride H) when given.
 __device__ __forceinline__ void first_layer(const float* X, int J, const float* __restrict__ W,
                                             const float* __restrict__ b, int H, float* At, float* gout) {
-  for (int k = threadIdx.x; k < H; k += kThreads) {
-    float acc[kRows];
+  const int k = threadIdx.x;
+  if (k >= H) return;
+  float acc[kRows];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
-    for (int j = 0; j < J; ++j) {
-      const float w = W[long(j) * H + k];
+  for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
+  for (int j0 = 0; j0 < J; j0 += 16) {
+    float w[16];
 #pragma unroll
-      for (int r = 0; r < kRows; ++r) acc[r] = fmaf(X[r * kMaxIn + j], w, acc[r]);
-    }
-    const float bk = b[k];
+    for (int jj = 0; jj < 16; ++jj) w[jj] = W[long(min(j0 + jj, J - 1)) * H + k];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      const float v = relu_s(acc[r] + bk);
-      At[r * kLda + k] = v;
-      if (gout) gout[long(r) * H + k] = v;
+    for (int jj = 0; jj < 16; ++jj) {
+      if (j0 + jj < J) {  // uniform
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) acc[r] = fmaf(X[r * kMaxIn + j0 + jj], w[jj], acc[r]);
+      }
     }
   }
+  const float bk = b[k];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const float v = relu_s(acc[r] + bk);
+    At[r * kLda + k] = v;
+    if (gout) gout[long(r) * H + k] = v;
+  }
+}
+
+// At[r][k] = gate[r][k] > 0 ? dq[r] * w[k] : 0 for the block's 16 rows
+// (thread t owns column t), the gated gradient into a critic's layer 2; also
+// stored to gout when given.  Every gate value is loaded before the first
+// store.
+__device__ __forceinline__ void gated_rows(const float* __restrict__ gate, const float* dq,
+                                           const float* __restrict__ w, int H, float* At, float* gout) {
+  const int k = threadIdx.x;
+  if (k >= H) return;
+  float gv[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) gv[r] = gate[long(r) * H + k];
+  const float wk = w[k];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const float v = gv[r] > 0.f ? dq[r] * wk : 0.f;
+    At[r * kLda + k] = v;
+    if (gout) gout[long(r) * H + k] = v;
+  }
+}
+
+// The sum of x[0:n] in a fixed order: lane l adds x[l], x[l + 64], ... in
+// turn, then the 64 lane sums are added pairwise over halving distances.
+// Every lane of the wavefront returns the sum.
+__device__ __forceinline__ float wave_sum_fixed(const float* x, int n) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.f;
+  for (int i = lane; i < n; i += 64) s += x[i];
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d, 64);
+  return s;
 }
 
 // The squashed sample of policy row `prow` (ttrl/algos/gaussian.py:106-167,
@@ -227,9 +268,11 @@ __global__ __launch_bounds__(kThreads) void k_sac_critic_fwd(FusedArgs a) {
   __shared__ float X[kRows * kMaxIn];
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
   __shared__ float Y[kRows * (kQ + 1)];
+  __shared__ float W3[kQ];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, grp = blockIdx.z, t = threadIdx.x;
   const int O = a.O, A = a.A, H = a.H, B = a.B;
   const CriticP cp = REGION == 0 ? a.cr[grp] : a.cr[2 + grp];
+  if (t < kQ) W3[t] = cp.w3[q * kQ + t];
   const bool next = REGION == 0 && grp < 2;        // rows of next_obs
   const bool sampled = REGION == 1 || grp < 2;      // actions sampled from the policy
   const int prow0 = next ? B + r0 : r0;             // the rows' index among the policy's 2B rows
@@ -266,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void k_sac_critic_fwd(FusedArgs a) {
   __syncthreads();
   if (t < kRows) {
     float s = 0.f;
-    for (int n = 0; n < kQ; ++n) s = fmaf(Y[t * (kQ + 1) + n], cp.w3[q * kQ + n], s);
+    for (int n = 0; n < kQ; ++n) s = fmaf(Y[t * (kQ + 1) + n], W3[n], s);
     qp[(long(grp) * a.nq + q) * B + r0 + t] = s;
   }
 }
@@ -311,24 +354,18 @@ __global__ __launch_bounds__(kThreads) void k_sac_critic_bwd(FusedArgs a) {
   }
   __syncthreads();
   // dq2 = dQ w3 [q2 > 0], the wide product's operand (stored once for the weight gradients)
-  const float* q2 = a.q2 + (long(2 + j) * B + r0) * H;
-  float* dq2 = a.dq2 + (long(j) * B + r0) * H;
-  for (int i = t; i < kRows * H; i += kThreads) {
-    const int r = i / H, k = i - r * H;
-    const float v = q2[long(r) * H + k] > 0.f ? dqs[r] * cp.w3[k] : 0.f;
-    At[r * kLda + k] = v;
-    if (q == 0) dq2[long(r) * H + k] = v;
-  }
+  gated_rows(a.q2 + (long(2 + j) * B + r0) * H, dqs, cp.w3, H, At,
+             q == 0 ? a.dq2 + (long(j) * B + r0) * H : nullptr);
   __syncthreads();
   const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
   const int col = q * kQ + w * 16 + c;
   const f32x4 acc = rows16_product<true>(At, H, cp.W2, H, col);
   const float* q1 = a.q1 + (long(2 + j) * B + r0) * H;
+  float gv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * g + i;
-    a.dq1[(long(j) * B + r0 + row) * H + col] = q1[long(row) * H + col] > 0.f ? acc[i] : 0.f;
-  }
+  for (int i = 0; i < 4; ++i) gv[i] = q1[long(4 * g + i) * H + col];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a.dq1[(long(j) * B + r0 + 4 * g + i) * H + col] = gv[i] > 0.f ? acc[i] : 0.f;
 }
 
 // ------------------------------------------------------------ stage 5 ---
@@ -338,10 +375,15 @@ __global__ __launch_bounds__(kThreads) void k_sac_critic_bwd(FusedArgs a) {
 __global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
   __shared__ float Y[kRows * (kQ + 1)];
+  __shared__ float W1a[kMaxA * kQ];
   __shared__ float dqs[kRows];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, j = blockIdx.z, t = threadIdx.x;
   const int H = a.H, B = a.B, nq = a.nq, O = a.O, A = a.A;
   const CriticP cp = a.cr[2 + j];
+  for (int i = t; i < A * kQ; i += kThreads) {  // the action rows of W1, this quarter's columns
+    const int aa = i / kQ, n = i - aa * kQ;
+    W1a[i] = cp.W1[long(O + aa) * H + q * kQ + n];
+  }
   if (t < kRows) {
     const int r = r0 + t;
     const float invB = 1.f / float(B);
@@ -356,11 +398,7 @@ __global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
     }
   }
   __syncthreads();
-  const float* q2 = a.q2pi + (long(j) * B + r0) * H;
-  for (int i = t; i < kRows * H; i += kThreads) {
-    const int r = i / H, k = i - r * H;
-    At[r * kLda + k] = q2[long(r) * H + k] > 0.f ? dqs[r] * cp.w3[k] : 0.f;
-  }
+  gated_rows(a.q2pi + (long(j) * B + r0) * H, dqs, cp.w3, H, At, nullptr);
   __syncthreads();
   const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
   const int col = q * kQ + w * 16 + c;
@@ -374,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
   __syncthreads();
   if (t < kRows * A) {
     const int row = t / A, aa = t - row * A;
-    const float* w1 = cp.W1 + long(O + aa) * H + q * kQ;
+    const float* w1 = W1a + aa * kQ;
     float s = 0.f;
     for (int n = 0; n < kQ; ++n) s = fmaf(Y[row * (kQ + 1) + n], w1[n], s);
     a.dap[((long(j) * nq + q) * B + r0 + row) * A + aa] = s;
@@ -382,18 +420,36 @@ __global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
 }
 
 // ------------------------------------------------------------ stage 6 ---
-// grid (B / 16, nq): d/da of every row, the sample's backward to the head
+// grid (B / 16 + 1, nq): d/da of every row, the sample's backward to the head
 // (the reparameterised path and the log-density's explicit terms), dh2 and
-// dh1.  Workgroup (0, 0) also forms the update's scalar losses and the
-// temperature's gradient from the terms stages 2 and 5 left.
+// dh1.  The extra row block's workgroup (B / 16, 0) forms the update's scalar
+// losses and the temperature's gradient from the terms stages 2 and 5 left;
+// the rest of that row block has nothing to do.
 __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
   __shared__ float DH[kRows * 2 * kMaxA];
-  __shared__ float T4[4 * kMaxB];
+  __shared__ float sums[4];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, t = threadIdx.x;
   const int H = a.H, B = a.B, nq = a.nq, A = a.A, A2 = 2 * a.A;
-  const float alpha = expf(*a.log_alpha);
   const float invB = 1.f / float(B);
+  if (r0 == B) {  // uniform: the loss sums
+    if (q != 0) return;
+    const int w = t >> 6;
+    const float s = wave_sum_fixed(a.terms + long(w) * B, B);
+    if ((t & 63) == 0) sums[w] = s;
+    __syncthreads();
+    if (t == 0) {
+      *a.actor_loss = sums[0] * invB;
+      *a.critic_loss = (sums[2] * invB + sums[3] * invB) * 0.5f;
+      if (a.learn_alpha) {
+        const float la = *a.log_alpha;
+        if (a.alpha_loss) *a.alpha_loss = (la * (sums[1] * invB)) * -1.f;
+        if (a.g_log_alpha) *a.g_log_alpha = (sums[1] * invB) * -1.f;
+      }
+    }
+    return;
+  }
+  const float alpha = expf(*a.log_alpha);
   if (t < kRows * A) {
     const int row = t / A, aa = t - row * A, r = r0 + row;
     float ga = 0.f;
@@ -418,42 +474,41 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
     }
   }
   __syncthreads();
-  // dh2 = (dhead Wh^T) [h2 > 0]
-  for (int i = t; i < kRows * H; i += kThreads) {
-    const int r = i / H, k = i - r * H;
-    float s = 0.f;
-    for (int jj = 0; jj < A; ++jj) s = fmaf(DH[r * A2 + jj], a.Wm[long(k) * A + jj], s);
-    for (int jj = 0; jj < A; ++jj) s = fmaf(DH[r * A2 + A + jj], a.Wl[long(k) * A + jj], s);
-    const float v = a.h2[long(r0 + r) * H + k] > 0.f ? s : 0.f;
-    At[r * kLda + k] = v;
-    if (q == 0) a.dh2[long(r0 + r) * H + k] = v;
+  // dh2 = (dhead Wh^T) [h2 > 0], thread t column t: its head weights and the
+  // block's h2 gates are loaded before the first store
+  if (t < H) {
+    const int k = t;
+    float wm[kMaxA], wl[kMaxA], hv[kRows];
+#pragma unroll
+    for (int jj = 0; jj < kMaxA; ++jj) {
+      wm[jj] = a.Wm[long(k) * A + min(jj, A - 1)];
+      wl[jj] = a.Wl[long(k) * A + min(jj, A - 1)];
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) hv[r] = a.h2[long(r0 + r) * H + k];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      float s = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < kMaxA; ++jj)
+        if (jj < A) s = fmaf(DH[r * A2 + jj], wm[jj], s);  // uniform
+#pragma unroll
+      for (int jj = 0; jj < kMaxA; ++jj)
+        if (jj < A) s = fmaf(DH[r * A2 + A + jj], wl[jj], s);
+      const float v = hv[r] > 0.f ? s : 0.f;
+      At[r * kLda + k] = v;
+      if (q == 0) a.dh2[long(r0 + r) * H + k] = v;
+    }
   }
   __syncthreads();
   const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
   const int col = q * kQ + w * 16 + c;
   const f32x4 acc = rows16_product<true>(At, H, a.P2, H, col);
+  float hv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * g + i;
-    a.dh1[long(r0 + row) * H + col] = a.h1[long(r0 + row) * H + col] > 0.f ? acc[i] : 0.f;
-  }
-  if (blockIdx.x != 0 || q != 0) return;  // uniform
-  for (int i = t; i < 4 * B; i += kThreads) T4[i] = a.terms[i];
-  __syncthreads();
-  if (t == 0) {
-    float sa = 0.f, se = 0.f, s0 = 0.f, s1 = 0.f;
-    for (int i = 0; i < B; ++i) sa += T4[i];
-    for (int i = 0; i < B; ++i) se += T4[B + i];
-    for (int i = 0; i < B; ++i) s0 += T4[2 * B + i];
-    for (int i = 0; i < B; ++i) s1 += T4[3 * B + i];
-    *a.actor_loss = sa * invB;
-    *a.critic_loss = (s0 * invB + s1 * invB) * 0.5f;
-    if (a.learn_alpha) {
-      const float la = *a.log_alpha;
-      if (a.alpha_loss) *a.alpha_loss = (la * (se * invB)) * -1.f;
-      if (a.g_log_alpha) *a.g_log_alpha = (se * invB) * -1.f;
-    }
-  }
+  for (int i = 0; i < 4; ++i) hv[i] = a.h1[long(r0 + 4 * g + i) * H + col];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a.dh1[long(r0 + 4 * g + i) * H + col] = hv[i] > 0.f ? acc[i] : 0.f;
 }
 
 // --------------------------------------------------------- stages 3, 7 ---
@@ -487,21 +542,31 @@ __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
   const int m = tm * kRows + c;                 // the A row this lane supplies
   const int col = tn * kQ + w * 16 + c;         // the B column this lane supplies
-  const bool mrow = m < p.M, bias = m == p.M && p.db != nullptr, ncol = col < p.N;
+  const bool mrow = m < p.M, ncol = col < p.N;
+  const float afill = (m == p.M && p.db != nullptr) ? 1.f : 0.f;  // the bias row
+  const int mc = min(m, p.M - 1), cc = min(col, p.N - 1);         // loads stay inside the operands
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int kb = 0; kb < a.nbatch; kb += 128) {
     float av[32], bv[32];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 8; ++j) {
+      const int kk0 = min(kb + 16 * j, a.nbatch - 16) + 4 * g;  // the batch is a multiple of 16
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int kk = kb + 16 * j + 4 * g + s;
-        const bool in = kk < a.nbatch;
-        av[4 * j + s] = in && mrow ? p.u[long(kk) * p.ldu + m] : (in && bias ? 1.f : 0.f);
-        bv[4 * j + s] = in && ncol ? p.v[long(kk) * p.ldv + col] : 0.f;
+        const float x = p.u[long(kk0 + s) * p.ldu + mc];
+        const float y = p.v[long(kk0 + s) * p.ldv + cc];
+        av[4 * j + s] = mrow ? x : afill;
+        bv[4 * j + s] = ncol ? y : 0.f;
       }
+    }
 #pragma unroll
-    for (int j = 0; j < 32; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc, 0, 0, 0);
+    for (int j = 0; j < 8; ++j) {
+      if (kb + 16 * j < a.nbatch) {  // uniform
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[4 * j + s], bv[4 * j + s], acc, 0, 0, 0);
+      }
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -652,7 +717,7 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
       TTRL_REQUIRE(a.dap && a.head && a.noise_pair && a.u && a.h1 && a.h2 && a.dhead && a.dh2 && a.dh1 &&
                        a.terms && a.log_alpha && a.actor_loss && a.critic_loss,
                    "%s: stage 6: null argument", name);
-      hipLaunchKernelGGL(k_sac_policy_bwd, dim3(rb, nq), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL(k_sac_policy_bwd, dim3(rb + 1, nq), dim3(kThreads), 0, st, a);
       break;
     case 3:
     case 7: {
