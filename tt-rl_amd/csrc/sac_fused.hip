@@ -39,6 +39,7 @@
 // global read).  Every sum runs in a fixed order, so replays are
 // bit-identical.
 #include "common.hpp"
+#include "tile_gemm.hpp"
 
 #include <cmath>
 
@@ -51,8 +52,11 @@ constexpr int kThreads = 256;   // four wavefronts: four 16 x 16 tiles
 constexpr int kMaxH = 256;
 constexpr int kLda = kMaxH + 4;  // LDS row stride of the wide product's A operand
 constexpr int kMaxIn = 64;       // first-layer inputs
+constexpr int kXs = kMaxIn + 4;  // LDS row stride of the first layer's input rows
 constexpr int kMaxA = 8;         // action dimensions
 constexpr int kMaxB = 1024;      // batch rows accepted
+constexpr int kTiles = kMaxH / 64;    // first-layer column tiles per wavefront
+constexpr int kBlocks = kMaxIn / 16;  // first-layer k blocks
 constexpr float kLog2f = 0.69314718055994530942f;
 constexpr float kLog2Pif = 1.83787706640934548356f;
 
@@ -60,6 +64,15 @@ __device__ __forceinline__ float relu_s(float x) { return x > 0.f ? x : 0.f; }
 __device__ __forceinline__ float softplus_s(float x) { return relu_s(x) + logf(expf(-fabsf(x)) + 1.f); }
 // min(a, b) as a - relu(a - b): the gradient goes to b iff a > b (ttrl/engine/ops/select.py:39-47)
 __device__ __forceinline__ float min_relu_s(float a, float b) { return a - relu_s(a - b); }
+
+// One float at byte voff + soff of a buffer resource (soff wave-uniform: it
+// rides in a scalar register, so the load needs no vector address math).
+__device__ __forceinline__ float ldb(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ f32x4 ldb4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
 
 struct CriticP {
   const float *W1, *b1, *W2, *b2, *w3, *b3;
@@ -84,86 +97,233 @@ struct FusedArgs {
   float* g_log_alpha;
 };
 
-// acc(4 rows x 1 column per lane) = A[0:16][0:K] x B[0:K][col], A in LDS
-// (row stride kLda), B(k, n) = TRANS ? W[n * ldw + k] : W[k * ldw + n].
-// K is a multiple of 64.  Every B value of the product is loaded before the
-// first MFMA, so the product waits one memory round trip.
+// Each stage issues every global load it needs before its first wait:
+// the loads of a workgroup then share one memory round trip, and what
+// follows runs from registers and LDS.  Loads are unconditional (indices
+// clamped into the operand, the value selected afterwards): a load inside
+// a branch taken by some lanes only is followed by a wait where the
+// branch joins.
+
+// The wide product's B operand for this lane's column `col`: b[j] holds
+// B(k, col) for k = 16 j + 4 (lane / 16) + s, s = 0..3, k < K (K a multiple
+// of 16).  TRANS: B(k, n) = W[n * ldw + k], one 16-byte load per j; else
+// B(k, n) = W[k * ldw + n], the row's offset in a scalar register.  W has
+// `rows` rows of ldw floats.
 template <bool TRANS>
-__device__ __forceinline__ f32x4 rows16_product(const float* At, int K, const float* __restrict__ W, int ldw,
-                                                int col) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  f32x4 b[kMaxH / 16];
+__device__ __forceinline__ void load_b(const float* W, int ldw, int rows, int K, int col, f32x4 (&b)[kMaxH / 16]) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const __amdgpu_buffer_rsrc_t res = make_res(W, uint32_t(rows) * uint32_t(ldw) * 4u);
 #pragma unroll
   for (int j = 0; j < kMaxH / 16; ++j) {
-    const int k = 16 * j + 4 * g;
     if (16 * j < K) {  // uniform
       if constexpr (TRANS) {
-        b[j] = *reinterpret_cast<const f32x4*>(W + long(col) * ldw + k);
+        b[j] = ldb4(res, (uint32_t(col) * uint32_t(ldw) + 4u * g) * 4u, 64u * j);
       } else {
+        const uint32_t base = (uint32_t(4 * g) * uint32_t(ldw) + col) * 4u;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) b[j][s] = W[long(k + s) * ldw + col];
+        for (int s = 0; s < 4; ++s) b[j][s] = ldb(res, base, uint32_t(16 * j + s) * uint32_t(ldw) * 4u);
       }
     }
   }
+}
+
+// acc(4 rows x 1 column per lane) = A[0:16][0:K] x B[0:K][col], A in LDS
+// (row stride kLda), B as load_b left it.
+__device__ __forceinline__ f32x4 rows16_mfma(const float* At, int K, const f32x4 (&b)[kMaxH / 16]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < kMaxH / 16; ++j) {
     if (16 * j < K) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(At + c * kLda + 16 * j + 4 * g);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b[j].x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b[j].y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b[j].z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b[j].w, acc, 0, 0, 0);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(At + c * kLda + 16 * j + 4 * g);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, b[j].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, b[j].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, b[j].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, b[j].w, acc, 0, 0, 0);
     }
   }
   return acc;
 }
 
-// out[r][k] = relu(sum_j X[r][j] W[j][k] + b[k]) for the block's 16 rows and
-// k < H (thread t owns column t, H <= the workgroup's 256 threads); X in LDS
-// (row stride kMaxIn), W [J][H].  Each 16-row chunk of W's column is loaded
-// before its products, so the layer waits one memory round trip per 16
-// inputs.  Also stored to gout[r][k] (row stride H) when given.
-__device__ __forceinline__ void first_layer(const float* X, int J, const float* __restrict__ W,
-                                            const float* __restrict__ b, int H, float* At, float* gout) {
-  const int k = threadIdx.x;
-  if (k >= H) return;
-  float acc[kRows];
+// The first layer's weights for this lane: wavefront w owns the 16-column
+// tiles w, w + 4, ... of W [J][H]; bw[i][kb][s] = W[16 kb + 4 (lane / 16) + s]
+// [16 (w + 4 i) + lane % 16] (zero past J, the buffer's end), bias[i] the
+// tile column's bias.
+struct FirstLayerW {
+  float bw[kTiles][kBlocks][4];
+  float bias[kTiles];
+};
+__device__ __forceinline__ void load_first(const float* W, const float* b, int J, int H, FirstLayerW& f) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
+  const __amdgpu_buffer_rsrc_t res = make_res(W, uint32_t(J) * uint32_t(H) * 4u);
+  const __amdgpu_buffer_rsrc_t rb = make_res(b, uint32_t(H) * 4u);
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
-  for (int j0 = 0; j0 < J; j0 += 16) {
-    float w[16];
+  for (int i = 0; i < kTiles; ++i) {
+    const uint32_t col = 16u * (w + 4 * i) + c;
+    f.bias[i] = 0.f;
+    if (64 * i < H) f.bias[i] = ldb(rb, col * 4u, 0);  // uniform
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) w[jj] = W[long(min(j0 + jj, J - 1)) * H + k];
+    for (int kb = 0; kb < kBlocks; ++kb)
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      if (j0 + jj < J) {  // uniform
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) acc[r] = fmaf(X[r * kMaxIn + j0 + jj], w[jj], acc[r]);
+      for (int s = 0; s < 4; ++s) {
+        f.bw[i][kb][s] = 0.f;
+        if (64 * i < H && 16 * kb < J)
+          f.bw[i][kb][s] = ldb(res, (uint32_t(4 * g) * uint32_t(H) + col) * 4u, uint32_t(16 * kb + s) * uint32_t(H) * 4u);
       }
-    }
-  }
-  const float bk = b[k];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const float v = relu_s(acc[r] + bk);
-    At[r * kLda + k] = v;
-    if (gout) gout[long(r) * H + k] = v;
   }
 }
 
-// At[r][k] = gate[r][k] > 0 ? dq[r] * w[k] : 0 for the block's 16 rows
-// (thread t owns column t), the gated gradient into a critic's layer 2; also
-// stored to gout when given.  Every gate value is loaded before the first
-// store.
-__device__ __forceinline__ void gated_rows(const float* __restrict__ gate, const float* dq,
-                                           const float* __restrict__ w, int H, float* At, float* gout) {
+// out[r][k] = relu(sum_j X[r][j] W[j][k] + b[k]) for the block's 16 rows and
+// every k < H on the matrix cores; X in LDS (row stride kXs, zero from J up
+// to the next multiple of 16).  Also stored to gout[r][k] (row stride H)
+// when given.
+__device__ __forceinline__ void first_layer(const float* X, int J, const FirstLayerW& f, int H, float* At,
+                                            float* gout) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
+  f32x4 xa[kBlocks];
+#pragma unroll
+  for (int kb = 0; kb < kBlocks; ++kb)
+    if (16 * kb < J) xa[kb] = *reinterpret_cast<const f32x4*>(X + c * kXs + 16 * kb + 4 * g);
+#pragma unroll
+  for (int i = 0; i < kTiles; ++i) {
+    if (64 * i >= H) break;  // uniform
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kBlocks; ++kb) {
+      if (16 * kb < J) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[kb].x, f.bw[i][kb][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[kb].y, f.bw[i][kb][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[kb].z, f.bw[i][kb][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[kb].w, f.bw[i][kb][3], acc, 0, 0, 0);
+      }
+    }
+    const int col = 16 * (w + 4 * i) + c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * g + r;
+      const float v = relu_s(acc[r] + f.bias[i]);
+      At[row * kLda + col] = v;
+      if (gout) gout[long(row) * H + col] = v;
+    }
+  }
+}
+
+// A block's first-layer input rows, gathered into registers (element
+// t + 256 m of the 16 x Jp slab, Jp = J rounded up to 16) and then written
+// to LDS: columns [0, O) from `obs` (row stride O), [O, O + A) from
+// `actions` (row stride A) unless those are sampled in the workgroup, and
+// zero up to Jp.
+struct InputRows {
+  float v[4];
+};
+template <bool ACTIONS>
+__device__ __forceinline__ void load_inputs(const float* obs, int O, const float* actions, int A, bool sampled,
+                                            InputRows& in) {
+  const int t = threadIdx.x, J = O + A, Jp = (J + 15) & ~15;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = t + kThreads * m, rr = i / Jp, j = i - rr * Jp, r = min(rr, kRows - 1);
+    const float ov = obs[long(r) * O + min(j, O - 1)];
+    float v = j < O ? ov : 0.f;
+    if constexpr (ACTIONS) {
+      const float av = actions[long(r) * A + min(max(j - O, 0), A - 1)];
+      v = (j >= O && j < J && !sampled) ? av : v;
+    }
+    in.v[m] = v;
+  }
+}
+__device__ __forceinline__ void store_inputs(const InputRows& in, int O, int A, bool sampled, float* X) {
+  const int t = threadIdx.x, J = O + A, Jp = (J + 15) & ~15;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = t + kThreads * m, r = i / Jp, j = i - r * Jp;
+    if (i < kRows * Jp && !(sampled && j >= O && j < J)) X[r * kXs + j] = in.v[m];
+  }
+}
+
+// The squashed sample of policy rows prow0 .. prow0 + 15
+// (ttrl/algos/gaussian.py:106-167, the stable log-density of
+// ttrl/algos/sac/policy.py:30-40), one thread per (row, action dimension).
+// sample_load gathers the head's quarter partials, biases, noise and
+// action scale; sample_rows sums the head, clamps log_std, writes the
+// action into X[row][O + j] and each dimension's two log-density terms into
+// parts[row][j], [kMaxA + j]; when `store`, also the head, action and
+// pre-squash u.  sample_logp adds the terms once the workgroup has
+// synchronised.
+struct SampleIn {
+  float mp[4], lp[4], eps, bm, bl, half, centre;
+};
+__device__ __forceinline__ void sample_load(const FusedArgs& a, int prow0, SampleIn& s) {
+  const int t = threadIdx.x, A = a.A, A2 = 2 * a.A, rows = 2 * a.B;
+  const int rr = t / A, j = t - rr * A, prow = prow0 + min(rr, kRows - 1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const long base = (long(min(q, a.nq - 1)) * rows + prow) * A2;
+    s.mp[q] = a.headp[base + j];
+    s.lp[q] = a.headp[base + A + j];
+  }
+  s.eps = a.noise_pair[long(prow) * A + j];
+  s.bm = a.bm[j];
+  s.bl = a.bl[j];
+  s.half = a.half[j];
+  s.centre = a.centre[j];
+}
+__device__ __forceinline__ void sample_rows(const FusedArgs& a, int prow0, const SampleIn& s, float* X, float* parts,
+                                            bool store) {
+  const int t = threadIdx.x, A = a.A, A2 = 2 * a.A, O = a.O;
+  if (t >= kRows * A) return;
+  const int row = t / A, j = t - row * A, prow = prow0 + row;
+  float mu = 0.f, lsr = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (q < a.nq) {  // uniform
+      mu += s.mp[q];
+      lsr += s.lp[q];
+    }
+  }
+  mu += s.bm;
+  lsr += s.bl;
+  const float ls = fminf(fmaxf(lsr, a.lo), a.hi);
+  const float sigma = expf(ls);
+  const float uu = mu + sigma * s.eps;
+  const float z = (uu - mu) / sigma;
+  parts[row * 2 * kMaxA + j] = (z * z) * -0.5f - ls;
+  parts[row * 2 * kMaxA + kMaxA + j] = ((kLog2f - uu) - softplus_s(uu * -2.f)) * 2.f;
+  const float act = tanhf(uu) * s.half + s.centre;
+  X[row * kXs + O + j] = act;
+  if (store) {
+    a.head[long(prow) * A2 + j] = mu;
+    a.head[long(prow) * A2 + A + j] = ls;
+    a.act[long(prow) * A + j] = act;
+    a.u[long(prow) * A + j] = uu;
+  }
+}
+__device__ __forceinline__ void sample_logp(const FusedArgs& a, int prow0, const float* parts) {
+  const int t = threadIdx.x;
+  if (t >= kRows) return;
+  float normal = 0.f, corr = 0.f;
+  for (int j = 0; j < a.A; ++j) {
+    normal += parts[t * 2 * kMaxA + j];
+    corr += parts[t * 2 * kMaxA + kMaxA + j];
+  }
+  a.logp[prow0 + t] = ((normal - 0.5f * float(a.A) * kLog2Pif) - corr) - a.log_det;
+}
+
+// The 16 gate values of this thread's column t (< H) of a [rows][H] block.
+__device__ __forceinline__ void load_gates(const float* src, int H, float (&gv)[kRows]) {
+  const int k = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t res = make_res(src, uint32_t(kRows) * uint32_t(H) * 4u);
+  const uint32_t kc = uint32_t(min(k, H - 1)) * 4u;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) gv[r] = ldb(res, kc, uint32_t(r) * uint32_t(H) * 4u);
+}
+
+// At[r][k] = gate[r][k] > 0 ? dq[r] * wk : 0 for the block's 16 rows,
+// thread t column t; also stored to gout when given.
+__device__ __forceinline__ void gated_rows(const float (&gv)[kRows], const float* dq, float wk, int H, float* At,
+                                           float* gout) {
   const int k = threadIdx.x;
   if (k >= H) return;
-  float gv[kRows];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) gv[r] = gate[long(r) * H + k];
-  const float wk = w[k];
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const float v = gv[r] > 0.f ? dq[r] * wk : 0.f;
@@ -184,64 +344,39 @@ __device__ __forceinline__ float wave_sum_fixed(const float* x, int n) {
   return s;
 }
 
-// The squashed sample of policy row `prow` (ttrl/algos/gaussian.py:106-167,
-// the stable log-density of ttrl/algos/sac/policy.py:30-40): the head summed
-// from its quarter partials plus bias, log_std clamped; writes the action
-// into xa[0:A] and, when `store`, the head, action, pre-squash u and log-prob.
-__device__ void sample_row(const FusedArgs& a, int prow, float* xa, bool store) {
-  const int A = a.A, A2 = 2 * a.A, rows = 2 * a.B;
-  float normal = 0.f, corr = 0.f;
-  for (int j = 0; j < A; ++j) {
-    float mu = 0.f, lsr = 0.f;
-    for (int q = 0; q < a.nq; ++q) {
-      mu += a.headp[(long(q) * rows + prow) * A2 + j];
-      lsr += a.headp[(long(q) * rows + prow) * A2 + A + j];
-    }
-    mu += a.bm[j];
-    lsr += a.bl[j];
-    const float ls = fminf(fmaxf(lsr, a.lo), a.hi);
-    const float sigma = expf(ls);
-    const float uu = mu + sigma * a.noise_pair[long(prow) * A + j];
-    const float z = (uu - mu) / sigma;
-    normal += (z * z) * -0.5f - ls;
-    corr += ((kLog2f - uu) - softplus_s(uu * -2.f)) * 2.f;
-    const float t = tanhf(uu);
-    const float act = t * a.half[j] + a.centre[j];
-    xa[j] = act;
-    if (store) {
-      a.head[long(prow) * A2 + j] = mu;
-      a.head[long(prow) * A2 + A + j] = ls;
-      a.act[long(prow) * A + j] = act;
-      a.u[long(prow) * A + j] = uu;
-    }
-  }
-  if (store) a.logp[prow] = ((normal - 0.5f * float(A) * kLog2Pif) - corr) - a.log_det;
-}
-
 // ------------------------------------------------------------ stage 0 ---
 // grid (2B / 16, nq): the policy over [obs; next_obs].
 __global__ __launch_bounds__(kThreads) void k_sac_policy_fwd(FusedArgs a) {
-  __shared__ float X[kRows * kMaxIn];
+  __shared__ __attribute__((aligned(16))) float X[kRows * kXs];
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
   __shared__ float Y[kRows * (kQ + 1)];
   __shared__ float Wh[kQ * 2 * kMaxA];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, t = threadIdx.x;
-  const int O = a.O, H = a.H, A2 = 2 * a.A, rows = 2 * a.B;
-  for (int i = t; i < kRows * O; i += kThreads) {
-    const int r = i / O, j = i - r * O;
-    X[r * kMaxIn + j] = a.obs_pair[long(r0 + r) * O + j];
-  }
-  for (int i = t; i < kQ * A2; i += kThreads) {
-    const int n = i / A2, j = i - n * A2, col = q * kQ + n;
-    Wh[n * A2 + j] = j < a.A ? a.Wm[long(col) * a.A + j] : a.Wl[long(col) * a.A + (j - a.A)];
-  }
-  __syncthreads();
-  first_layer(X, O, a.P1, a.p1, H, At, q == 0 ? a.h1 + long(r0) * H : nullptr);
-  __syncthreads();
+  const int O = a.O, H = a.H, A = a.A, A2 = 2 * a.A, rows = 2 * a.B;
   const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
   const int col = q * kQ + w * 16 + c;
-  const f32x4 acc = rows16_product<false>(At, H, a.P2, H, col);
+  InputRows in;
+  load_inputs<false>(a.obs_pair + long(r0) * O, O, nullptr, 0, false, in);
+  float wh[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = t + kThreads * m, n = min(i / A2, kQ - 1), j = i % A2, hc = q * kQ + n;
+    const float vm = a.Wm[long(hc) * A + min(j, A - 1)], vl = a.Wl[long(hc) * A + max(j - A, 0)];
+    wh[m] = j < A ? vm : vl;
+  }
+  FirstLayerW f1;
+  load_first(a.P1, a.p1, O, H, f1);
+  f32x4 b[kMaxH / 16];
+  load_b<false>(a.P2, H, H, H, col, b);
   const float bias = a.p2[col];
+  store_inputs(in, O, 0, false, X);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (t + kThreads * m < kQ * A2) Wh[t + kThreads * m] = wh[m];
+  __syncthreads();
+  first_layer(X, O, f1, H, At, q == 0 ? a.h1 + long(r0) * H : nullptr);
+  __syncthreads();
+  const f32x4 acc = rows16_mfma(At, H, b);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * g + i;
@@ -265,40 +400,41 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_fwd(FusedArgs a) {
 // critics on (obs, a sampled here)).
 template <int REGION>
 __global__ __launch_bounds__(kThreads) void k_sac_critic_fwd(FusedArgs a) {
-  __shared__ float X[kRows * kMaxIn];
+  __shared__ __attribute__((aligned(16))) float X[kRows * kXs];
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
   __shared__ float Y[kRows * (kQ + 1)];
   __shared__ float W3[kQ];
+  __shared__ float parts[kRows * 2 * kMaxA];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, grp = blockIdx.z, t = threadIdx.x;
   const int O = a.O, A = a.A, H = a.H, B = a.B;
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
   const CriticP cp = REGION == 0 ? a.cr[grp] : a.cr[2 + grp];
-  if (t < kQ) W3[t] = cp.w3[q * kQ + t];
   const bool next = REGION == 0 && grp < 2;        // rows of next_obs
   const bool sampled = REGION == 1 || grp < 2;      // actions sampled from the policy
   const int prow0 = next ? B + r0 : r0;             // the rows' index among the policy's 2B rows
-  for (int i = t; i < kRows * O; i += kThreads) {
-    const int r = i / O, j = i - r * O;
-    X[r * kMaxIn + j] = a.obs_pair[long(prow0 + r) * O + j];
-  }
-  if (!sampled) {
-    for (int i = t; i < kRows * A; i += kThreads) {
-      const int r = i / A, j = i - r * A;
-      X[r * kMaxIn + O + j] = a.actions[long(r0 + r) * A + j];
-    }
-  } else if (t < kRows) {
-    // the first sampling group's first quarter stores the sample of its rows
-    sample_row(a, prow0 + t, X + t * kMaxIn + O, q == 0 && grp == 0);
-  }
+  InputRows in;
+  load_inputs<true>(a.obs_pair + long(prow0) * O, O, a.actions + long(r0) * A, A, sampled, in);
+  SampleIn si;
+  sample_load(a, prow0, si);
+  const float w3 = cp.w3[q * kQ + min(t, kQ - 1)];
+  FirstLayerW f1;
+  load_first(cp.W1, cp.b1, O + A, H, f1);
+  f32x4 b[kMaxH / 16];
+  load_b<false>(cp.W2, H, H, H, col, b);
+  const float bias = cp.b2[col];
+  store_inputs(in, O, A, sampled, X);
+  if (t < kQ) W3[t] = w3;
+  // the first sampling group's first quarter stores the sample of its rows
+  if (sampled) sample_rows(a, prow0, si, X, parts, q == 0 && grp == 0);
   __syncthreads();
+  if (sampled && q == 0 && grp == 0) sample_logp(a, prow0, parts);
   float* q1 = REGION == 0 ? a.q1 : a.q1pi;
   float* q2 = REGION == 0 ? a.q2 : a.q2pi;
   float* qp = REGION == 0 ? a.qp : a.qppi;
-  first_layer(X, O + A, cp.W1, cp.b1, H, At, q == 0 ? q1 + (long(grp) * B + r0) * H : nullptr);
+  first_layer(X, O + A, f1, H, At, q == 0 ? q1 + (long(grp) * B + r0) * H : nullptr);
   __syncthreads();
-  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
-  const int col = q * kQ + w * 16 + c;
-  const f32x4 acc = rows16_product<false>(At, H, cp.W2, H, col);
-  const float bias = cp.b2[col];
+  const f32x4 acc = rows16_mfma(At, H, b);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * g + i;
@@ -314,58 +450,83 @@ __global__ __launch_bounds__(kThreads) void k_sac_critic_fwd(FusedArgs a) {
   }
 }
 
-// Q of group grp, row r: its quarter partials in order, plus the bias.
-__device__ __forceinline__ float q_of(const float* qp, int nq, int B, int grp, int r, const float* b3) {
+// ------------------------------------------------------------ stage 2 ---
+// The soft target and both critics' TD errors of one row
+// (ttrl/algos/sac/losses.py:46-76), from Q quarter partials in quarter order.
+struct CriticRow {
+  float qp[4][4], b3[4], logp, reward, done, discount, weight, log_alpha;
+};
+__device__ __forceinline__ void critic_row_load(const FusedArgs& a, int r, CriticRow& cr) {
+  const int B = a.B, nq = a.nq;
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cr.qp[gq][q] = a.qp[(long(gq) * nq + min(q, nq - 1)) * B + r];
+    cr.b3[gq] = *a.cr[gq].b3;
+  }
+  cr.logp = a.logp[B + r];
+  cr.reward = a.rewards[r];
+  cr.done = a.dones[r];
+  cr.discount = a.discounts[r];
+  const float wv = (a.weights ? a.weights : a.rewards)[r];
+  cr.weight = a.weights ? wv : 1.f;
+  cr.log_alpha = *a.log_alpha;
+}
+__device__ __forceinline__ float q_sum(const float (&qp)[4], int nq, float b3) {
   float s = 0.f;
-  for (int q = 0; q < nq; ++q) s += qp[(long(grp) * nq + q) * B + r];
-  return s + *b3;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (q < nq) s += qp[q];
+  return s + b3;
 }
 
-// ------------------------------------------------------------ stage 2 ---
-// grid (B / 16, nq, 2): critic j's loss gradient and its backward to layer 1
-// (ttrl/algos/sac/losses.py:46-76).
+// grid (B / 16, nq, 2): critic j's loss gradient and its backward to layer 1.
 __global__ __launch_bounds__(kThreads) void k_sac_critic_bwd(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
   __shared__ float dqs[kRows];
-  const int rb = blockIdx.x, r0 = rb * kRows, q = blockIdx.y, j = blockIdx.z, t = threadIdx.x;
+  const int r0 = blockIdx.x * kRows, q = blockIdx.y, j = blockIdx.z, t = threadIdx.x;
   const int H = a.H, B = a.B, nq = a.nq;
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
   const CriticP cp = a.cr[2 + j];
+  CriticRow cr;
+  critic_row_load(a, r0 + min(t, kRows - 1), cr);
+  float gv[kRows];
+  load_gates(a.q2 + (long(2 + j) * B + r0) * H, H, gv);
+  const float w3 = cp.w3[min(t, H - 1)];
+  f32x4 b[kMaxH / 16];
+  load_b<true>(cp.W2, H, H, H, col, b);
+  float g1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) g1[i] = a.q1[(long(2 + j) * B + r0 + 4 * g + i) * H + col];
   if (t < kRows) {
     const int r = r0 + t;
     const float invB = 1.f / float(B);
-    const float alpha = expf(*a.log_alpha);
-    const float qt0 = q_of(a.qp, nq, B, 0, r, a.cr[0].b3), qt1 = q_of(a.qp, nq, B, 1, r, a.cr[1].b3);
-    const float q0 = q_of(a.qp, nq, B, 2, r, a.cr[2].b3), q1v = q_of(a.qp, nq, B, 3, r, a.cr[3].b3);
-    const float soft = min_relu_s(qt0, qt1) - a.logp[B + r] * alpha;
-    const float y = a.rewards[r] + (soft * (1.f - a.dones[r])) * a.discounts[r];
+    const float alpha = expf(cr.log_alpha);
+    const float qt0 = q_sum(cr.qp[0], nq, cr.b3[0]), qt1 = q_sum(cr.qp[1], nq, cr.b3[1]);
+    const float q0 = q_sum(cr.qp[2], nq, cr.b3[2]), q1v = q_sum(cr.qp[3], nq, cr.b3[3]);
+    const float soft = min_relu_s(qt0, qt1) - cr.logp * alpha;
+    const float y = cr.reward + (soft * (1.f - cr.done)) * cr.discount;
     const float e0 = q0 - y, e1 = q1v - y;
-    const float wgt = a.weights ? a.weights[r] : 1.f;
-    const float gs = wgt * (0.5f * invB) * 2.f;
+    const float gs = cr.weight * (0.5f * invB) * 2.f;
     const float dq = (j == 0 ? e0 : e1) * gs;
     dqs[t] = dq;
     if (q == 0) a.dQ[long(j) * B + r] = dq;
     if (q == 0 && j == 0) {
       a.q_target[r] = y;
       if (a.td_abs) a.td_abs[r] = (fabsf(e0) + fabsf(e1)) * 0.5f;
-      a.terms[2L * B + r] = a.weights ? (e0 * e0) * wgt : e0 * e0;
-      a.terms[3L * B + r] = a.weights ? (e1 * e1) * wgt : e1 * e1;
+      a.terms[2L * B + r] = a.weights ? (e0 * e0) * cr.weight : e0 * e0;
+      a.terms[3L * B + r] = a.weights ? (e1 * e1) * cr.weight : e1 * e1;
       if (r == 0) *a.alpha = alpha;
     }
   }
   __syncthreads();
   // dq2 = dQ w3 [q2 > 0], the wide product's operand (stored once for the weight gradients)
-  gated_rows(a.q2 + (long(2 + j) * B + r0) * H, dqs, cp.w3, H, At,
-             q == 0 ? a.dq2 + (long(j) * B + r0) * H : nullptr);
+  gated_rows(gv, dqs, w3, H, At, q == 0 ? a.dq2 + (long(j) * B + r0) * H : nullptr);
   __syncthreads();
-  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
-  const int col = q * kQ + w * 16 + c;
-  const f32x4 acc = rows16_product<true>(At, H, cp.W2, H, col);
-  const float* q1 = a.q1 + (long(2 + j) * B + r0) * H;
-  float gv[4];
+  const f32x4 acc = rows16_mfma(At, H, b);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) gv[i] = q1[long(4 * g + i) * H + col];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a.dq1[(long(j) * B + r0 + 4 * g + i) * H + col] = gv[i] > 0.f ? acc[i] : 0.f;
+  for (int i = 0; i < 4; ++i) a.dq1[(long(j) * B + r0 + 4 * g + i) * H + col] = g1[i] > 0.f ? acc[i] : 0.f;
 }
 
 // ------------------------------------------------------------ stage 5 ---
@@ -379,42 +540,64 @@ __global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
   __shared__ float dqs[kRows];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, j = blockIdx.z, t = threadIdx.x;
   const int H = a.H, B = a.B, nq = a.nq, O = a.O, A = a.A;
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
   const CriticP cp = a.cr[2 + j];
-  for (int i = t; i < A * kQ; i += kThreads) {  // the action rows of W1, this quarter's columns
-    const int aa = i / kQ, n = i - aa * kQ;
-    W1a[i] = cp.W1[long(O + aa) * H + q * kQ + n];
+  float qa[2][4], b3[2];
+  {
+    const int r = r0 + min(t, kRows - 1);
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) qa[gq][qq] = a.qppi[(long(gq) * nq + min(qq, nq - 1)) * B + r];
+      b3[gq] = *a.cr[2 + gq].b3;
+    }
   }
+  const float lp = a.logp[r0 + min(t, kRows - 1)], la = *a.log_alpha;
+  float w1[2];  // the action rows of W1, this quarter's columns (A x kQ <= 512 values)
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int i = t + kThreads * m, aa = min(i / kQ, A - 1), n = i % kQ;
+    w1[m] = cp.W1[long(O + aa) * H + q * kQ + n];
+  }
+  float gv[kRows];
+  load_gates(a.q2pi + (long(j) * B + r0) * H, H, gv);
+  const float w3 = cp.w3[min(t, H - 1)];
+  f32x4 b[kMaxH / 16];
+  load_b<true>(cp.W2, H, H, H, col, b);
+  float g1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) g1[i] = a.q1pi[(long(j) * B + r0 + 4 * g + i) * H + col];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+    if (t + kThreads * m < A * kQ) W1a[t + kThreads * m] = w1[m];
   if (t < kRows) {
     const int r = r0 + t;
     const float invB = 1.f / float(B);
-    const float q0 = q_of(a.qppi, nq, B, 0, r, a.cr[2].b3), q1v = q_of(a.qppi, nq, B, 1, r, a.cr[3].b3);
+    const float q0 = q_sum(qa[0], nq, b3[0]), q1v = q_sum(qa[1], nq, b3[1]);
     const bool second = q0 - q1v > 0.f;
     dqs[t] = (j == (second ? 1 : 0)) ? -invB : 0.f;
     if (q == 0 && j == 0) {
-      const float lp = a.logp[r];
-      const float alpha = expf(*a.log_alpha);
+      const float alpha = expf(la);
       a.terms[r] = lp * alpha - min_relu_s(q0, q1v);
       a.terms[long(B) + r] = lp + a.target_entropy;
     }
   }
   __syncthreads();
-  gated_rows(a.q2pi + (long(j) * B + r0) * H, dqs, cp.w3, H, At, nullptr);
+  gated_rows(gv, dqs, w3, H, At, nullptr);
   __syncthreads();
-  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
-  const int col = q * kQ + w * 16 + c;
-  const f32x4 acc = rows16_product<true>(At, H, cp.W2, H, col);
-  const float* q1 = a.q1pi + (long(j) * B + r0) * H;
+  const f32x4 acc = rows16_mfma(At, H, b);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * g + i;
-    Y[row * (kQ + 1) + w * 16 + c] = q1[long(row) * H + col] > 0.f ? acc[i] : 0.f;
+    Y[row * (kQ + 1) + w * 16 + c] = g1[i] > 0.f ? acc[i] : 0.f;
   }
   __syncthreads();
   if (t < kRows * A) {
     const int row = t / A, aa = t - row * A;
-    const float* w1 = W1a + aa * kQ;
+    const float* w1r = W1a + aa * kQ;
     float s = 0.f;
-    for (int n = 0; n < kQ; ++n) s = fmaf(Y[row * (kQ + 1) + n], w1[n], s);
+    for (int n = 0; n < kQ; ++n) s = fmaf(Y[row * (kQ + 1) + n], w1r[n], s);
     a.dap[((long(j) * nq + q) * B + r0 + row) * A + aa] = s;
   }
 }
@@ -449,20 +632,46 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
     }
     return;
   }
-  const float alpha = expf(*a.log_alpha);
+  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
+  const int col = q * kQ + w * 16 + c;
+  // per (row, action dimension): the d/da partials, head, noise, u
+  float dp[2][4];
+  const int prr = min(t / A, kRows - 1), paa = t % A, pr = r0 + prr;
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) dp[jj][qq] = a.dap[((long(jj) * nq + min(qq, nq - 1)) * B + pr) * A + paa];
+  const float mu = a.head[long(pr) * A2 + paa], ls = a.head[long(pr) * A2 + A + paa];
+  const float eps = a.noise_pair[long(pr) * A + paa], uu = a.u[long(pr) * A + paa];
+  const float half = a.half[paa], la = *a.log_alpha;
+  // per column t: the head weights and the block's h2 gates
+  float wm[kMaxA], wl[kMaxA], hv[kRows];
+  const int k = min(t, H - 1);
+#pragma unroll
+  for (int jj = 0; jj < kMaxA; ++jj) {
+    wm[jj] = a.Wm[long(k) * A + min(jj, A - 1)];
+    wl[jj] = a.Wl[long(k) * A + min(jj, A - 1)];
+  }
+  load_gates(a.h2 + long(r0) * H, H, hv);
+  f32x4 b[kMaxH / 16];
+  load_b<true>(a.P2, H, H, H, col, b);
+  float g1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) g1[i] = a.h1[long(r0 + 4 * g + i) * H + col];
   if (t < kRows * A) {
     const int row = t / A, aa = t - row * A, r = r0 + row;
     float ga = 0.f;
-    for (int j = 0; j < 2; ++j)
-      for (int qq = 0; qq < nq; ++qq) ga += a.dap[((long(j) * nq + qq) * B + r) * A + aa];
-    const float mu = a.head[long(r) * A2 + aa], ls = a.head[long(r) * A2 + A + aa];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+        if (qq < nq) ga += dp[jj][qq];
+    const float alpha = expf(la);
     const float sigma = expf(ls);
-    const float eps = a.noise_pair[long(r) * A + aa];
-    const float uu = a.u[long(r) * A + aa];
     const float z = (uu - mu) / sigma;
     const float th = tanhf(uu);
     const float glp = alpha * invB;
-    const float gu = ga * a.half[aa] * (1.f - th * th) + glp * (2.f * th - z / sigma);
+    const float gu = ga * half * (1.f - th * th) + glp * (2.f * th - z / sigma);
     const float gmu = gu + glp * (z / sigma);
     float gls = gu * (sigma * eps) + glp * (z * z - 1.f);
     gls = (ls > a.lo && ls < a.hi) ? gls : 0.f;
@@ -474,18 +683,8 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
     }
   }
   __syncthreads();
-  // dh2 = (dhead Wh^T) [h2 > 0], thread t column t: its head weights and the
-  // block's h2 gates are loaded before the first store
+  // dh2 = (dhead Wh^T) [h2 > 0], thread t column t
   if (t < H) {
-    const int k = t;
-    float wm[kMaxA], wl[kMaxA], hv[kRows];
-#pragma unroll
-    for (int jj = 0; jj < kMaxA; ++jj) {
-      wm[jj] = a.Wm[long(k) * A + min(jj, A - 1)];
-      wl[jj] = a.Wl[long(k) * A + min(jj, A - 1)];
-    }
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) hv[r] = a.h2[long(r0 + r) * H + k];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
       float s = 0.f;
@@ -496,19 +695,14 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
       for (int jj = 0; jj < kMaxA; ++jj)
         if (jj < A) s = fmaf(DH[r * A2 + A + jj], wl[jj], s);
       const float v = hv[r] > 0.f ? s : 0.f;
-      At[r * kLda + k] = v;
-      if (q == 0) a.dh2[long(r0 + r) * H + k] = v;
+      At[r * kLda + t] = v;
+      if (q == 0) a.dh2[long(r0 + r) * H + t] = v;
     }
   }
   __syncthreads();
-  const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
-  const int col = q * kQ + w * 16 + c;
-  const f32x4 acc = rows16_product<true>(At, H, a.P2, H, col);
-  float hv[4];
+  const f32x4 acc = rows16_mfma(At, H, b);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hv[i] = a.h1[long(r0 + 4 * g + i) * H + col];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a.dh1[long(r0 + 4 * g + i) * H + col] = hv[i] > 0.f ? acc[i] : 0.f;
+  for (int i = 0; i < 4; ++i) a.dh1[long(r0 + 4 * g + i) * H + col] = g1[i] > 0.f ? acc[i] : 0.f;
 }
 
 // --------------------------------------------------------- stages 3, 7 ---
@@ -531,6 +725,38 @@ struct OuterArgs {
   OuterProb p[kMaxOuter];
 };
 
+// One 128-row chunk of the batch for this lane: av[4 j + s] = u[kk][m],
+// bv[4 j + s] = v[kk][col], kk = kb + 16 j + 4 (lane / 16) + s (rows past
+// the batch repeat its last 16; their products are skipped).
+struct OuterChunk {
+  float av[32], bv[32];
+};
+__device__ __forceinline__ void outer_load(__amdgpu_buffer_rsrc_t ru, uint32_t uoff, int ldu,
+                                           __amdgpu_buffer_rsrc_t rv, uint32_t voff, int ldv, int nbatch, int kb,
+                                           OuterChunk& ch) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k0 = min(kb + 16 * j, nbatch - 16);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ch.av[4 * j + s] = ldb(ru, uoff, uint32_t(k0 + s) * uint32_t(ldu) * 4u);
+      ch.bv[4 * j + s] = ldb(rv, voff, uint32_t(k0 + s) * uint32_t(ldv) * 4u);
+    }
+  }
+}
+__device__ __forceinline__ void outer_mfma(const OuterChunk& ch, bool mrow, float afill, bool ncol, int nbatch,
+                                           int kb, f32x4& acc) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (kb + 16 * j < nbatch) {  // uniform
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(mrow ? ch.av[4 * j + s] : afill, ncol ? ch.bv[4 * j + s] : 0.f,
+                                                   acc, 0, 0, 0);
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
   const int wg = blockIdx.x;
   int k = 0;
@@ -545,27 +771,21 @@ __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
   const bool mrow = m < p.M, ncol = col < p.N;
   const float afill = (m == p.M && p.db != nullptr) ? 1.f : 0.f;  // the bias row
   const int mc = min(m, p.M - 1), cc = min(col, p.N - 1);         // loads stay inside the operands
+  const int nb = a.nbatch;
+  const __amdgpu_buffer_rsrc_t ru = make_res(p.u, uint32_t(nb) * uint32_t(p.ldu) * 4u);
+  const __amdgpu_buffer_rsrc_t rv = make_res(p.v, uint32_t(nb) * uint32_t(p.ldv) * 4u);
+  const uint32_t uoff = (uint32_t(4 * g) * uint32_t(p.ldu) + mc) * 4u;
+  const uint32_t voff = (uint32_t(4 * g) * uint32_t(p.ldv) + cc) * 4u;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < a.nbatch; kb += 128) {
-    float av[32], bv[32];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kk0 = min(kb + 16 * j, a.nbatch - 16) + 4 * g;  // the batch is a multiple of 16
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float x = p.u[long(kk0 + s) * p.ldu + mc];
-        const float y = p.v[long(kk0 + s) * p.ldv + cc];
-        av[4 * j + s] = mrow ? x : afill;
-        bv[4 * j + s] = ncol ? y : 0.f;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (kb + 16 * j < a.nbatch) {  // uniform
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[4 * j + s], bv[4 * j + s], acc, 0, 0, 0);
-      }
+  // two chunks in flight: the next chunk's loads are issued before this one's products
+  OuterChunk c0, c1;
+  outer_load(ru, uoff, p.ldu, rv, voff, p.ldv, nb, 0, c0);
+  for (int kb = 0; kb < nb; kb += 256) {
+    if (kb + 128 < nb) outer_load(ru, uoff, p.ldu, rv, voff, p.ldv, nb, kb + 128, c1);
+    outer_mfma(c0, mrow, afill, ncol, nb, kb, acc);
+    if (kb + 128 < nb) {
+      if (kb + 256 < nb) outer_load(ru, uoff, p.ldu, rv, voff, p.ldv, nb, kb + 256, c0);
+      outer_mfma(c1, mrow, afill, ncol, nb, kb + 128, acc);
     }
   }
 #pragma unroll
@@ -692,10 +912,11 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
       break;
     case 1:
     case 4:
-      TTRL_REQUIRE(a.obs_pair && a.noise_pair && a.headp && a.head && a.act && a.u && a.logp && a.centre && a.half,
+      TTRL_REQUIRE(a.obs_pair && a.actions && a.noise_pair && a.headp && a.head && a.act && a.u && a.logp &&
+                       a.centre && a.half,
                    "%s: stage %d: null argument", name, stage);
       if (stage == 1) {
-        TTRL_REQUIRE(a.actions && a.q1 && a.q2 && a.qp, "%s: stage 1: null argument", name);
+        TTRL_REQUIRE(a.q1 && a.q2 && a.qp, "%s: stage 1: null argument", name);
         hipLaunchKernelGGL(k_sac_critic_fwd<0>, dim3(rb, nq, 4), dim3(kThreads), 0, st, a);
       } else {
         TTRL_REQUIRE(a.q1pi && a.q2pi && a.qppi, "%s: stage 4: null argument", name);
@@ -715,7 +936,7 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
       break;
     case 6:
       TTRL_REQUIRE(a.dap && a.head && a.noise_pair && a.u && a.h1 && a.h2 && a.dhead && a.dh2 && a.dh1 &&
-                       a.terms && a.log_alpha && a.actor_loss && a.critic_loss,
+                       a.terms && a.log_alpha && a.actor_loss && a.critic_loss && a.half && a.Wm && a.Wl && a.P2,
                    "%s: stage 6: null argument", name);
       hipLaunchKernelGGL(k_sac_policy_bwd, dim3(rb + 1, nq), dim3(kThreads), 0, st, a);
       break;
