@@ -53,6 +53,7 @@ constexpr int kMaxH = 256;
 constexpr int kLda = kMaxH + 4;  // LDS row stride of the wide product's A operand
 constexpr int kMaxIn = 64;       // first-layer inputs
 constexpr int kXs = kMaxIn + 4;  // LDS row stride of the first layer's input rows
+constexpr int kDhs = 20;         // LDS row stride of the policy head's gradient rows (2 x kMaxA <= 16 used)
 constexpr int kMaxA = 8;         // action dimensions
 constexpr int kMaxB = 1024;      // batch rows accepted
 constexpr int kTiles = kMaxH / 64;    // first-layer column tiles per wavefront
@@ -332,13 +333,19 @@ __device__ __forceinline__ void gated_rows(const float (&gv)[kRows], const float
   }
 }
 
-// The sum of x[0:n] in a fixed order: lane l adds x[l], x[l + 64], ... in
-// turn, then the 64 lane sums are added pairwise over halving distances.
+// The sum of x[0:n] (n <= kMaxB) in a fixed order: lane l adds x[l],
+// x[l + 64], ... in turn, then the 64 lane sums are added pairwise over
+// halving distances.
 // Every lane of the wavefront returns the sum.
 __device__ __forceinline__ float wave_sum_fixed(const float* x, int n) {
   const int lane = threadIdx.x & 63;
+  float v[kMaxB / 64];
+#pragma unroll
+  for (int i = 0; i < kMaxB / 64; ++i) v[i] = x[min(lane + 64 * i, n - 1)];
   float s = 0.f;
-  for (int i = lane; i < n; i += 64) s += x[i];
+#pragma unroll
+  for (int i = 0; i < kMaxB / 64; ++i)
+    if (lane + 64 * i < n) s += v[i];
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d, 64);
   return s;
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(kThreads) void k_sac_actor_bwd(FusedArgs a) {
 // the rest of that row block has nothing to do.
 __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
-  __shared__ float DH[kRows * 2 * kMaxA];
+  __shared__ __attribute__((aligned(16))) float DH[kRows * kDhs];  // dhead rows, zero from 2A to 16
   __shared__ float sums[4];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, t = threadIdx.x;
   const int H = a.H, B = a.B, nq = a.nq, A = a.A, A2 = 2 * a.A;
@@ -644,15 +651,22 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
   const float mu = a.head[long(pr) * A2 + paa], ls = a.head[long(pr) * A2 + A + paa];
   const float eps = a.noise_pair[long(pr) * A + paa], uu = a.u[long(pr) * A + paa];
   const float half = a.half[paa], la = *a.log_alpha;
-  // per column t: the head weights and the block's h2 gates
-  float wm[kMaxA], wl[kMaxA], hv[kRows];
-  const int k = min(t, H - 1);
+  // dh2 on the matrix cores: B(kk, n) = Wm[n][kk] (kk < A), Wl[n][kk - A]
+  // (A <= kk < 2A), zero to 16; wavefront w owns the column tiles w, w + 4, ...
+  // The h2 gates in the product's layout: rows 4 g + i of each tile column.
+  float wb[kTiles][4], hg[kTiles][4];
 #pragma unroll
-  for (int jj = 0; jj < kMaxA; ++jj) {
-    wm[jj] = a.Wm[long(k) * A + min(jj, A - 1)];
-    wl[jj] = a.Wl[long(k) * A + min(jj, A - 1)];
+  for (int i = 0; i < kTiles; ++i) {
+    const int n = min(16 * (w + 4 * i) + c, H - 1);
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int kk = 4 * g + s2;
+      const float vm = a.Wm[long(n) * A + min(kk, A - 1)];
+      const float vl = a.Wl[long(n) * A + min(max(kk - A, 0), A - 1)];
+      wb[i][s2] = kk < A ? vm : (kk < 2 * A ? vl : 0.f);
+      hg[i][s2] = a.h2[long(r0 + 4 * g + s2) * H + n];
+    }
   }
-  load_gates(a.h2 + long(r0) * H, H, hv);
   f32x4 b[kMaxH / 16];
   load_b<true>(a.P2, H, H, H, col, b);
   float g1[4];
@@ -675,28 +689,37 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
     const float gmu = gu + glp * (z / sigma);
     float gls = gu * (sigma * eps) + glp * (z * z - 1.f);
     gls = (ls > a.lo && ls < a.hi) ? gls : 0.f;
-    DH[row * A2 + aa] = gmu;
-    DH[row * A2 + A + aa] = gls;
+    DH[row * kDhs + aa] = gmu;
+    DH[row * kDhs + A + aa] = gls;
     if (q == 0) {
       a.dhead[long(r) * A2 + aa] = gmu;
       a.dhead[long(r) * A2 + A + aa] = gls;
     }
   }
+  {
+    const int zr = t >> 4, zc = t & 15;  // the zero columns of the dhead rows
+    if (zc >= A2) DH[zr * kDhs + zc] = 0.f;
+  }
   __syncthreads();
-  // dh2 = (dhead Wh^T) [h2 > 0], thread t column t
-  if (t < H) {
+  // dh2 = (dhead Wh^T) [h2 > 0]
+  {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(DH + c * kDhs + 4 * g);
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      float s = 0.f;
+    for (int i = 0; i < kTiles; ++i) {
+      if (64 * i >= H) break;  // uniform
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, wb[i][0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, wb[i][1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, wb[i][2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, wb[i][3], acc, 0, 0, 0);
+      const int n = 16 * (w + 4 * i) + c;
 #pragma unroll
-      for (int jj = 0; jj < kMaxA; ++jj)
-        if (jj < A) s = fmaf(DH[r * A2 + jj], wm[jj], s);  // uniform
-#pragma unroll
-      for (int jj = 0; jj < kMaxA; ++jj)
-        if (jj < A) s = fmaf(DH[r * A2 + A + jj], wl[jj], s);
-      const float v = hv[r] > 0.f ? s : 0.f;
-      At[r * kLda + t] = v;
-      if (q == 0) a.dh2[long(r0 + r) * H + t] = v;
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        const float v = hg[i][r] > 0.f ? acc[r] : 0.f;
+        At[row * kLda + n] = v;
+        if (q == 0) a.dh2[long(r0 + row) * H + n] = v;
+      }
     }
   }
   __syncthreads();
@@ -709,8 +732,15 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_bwd(FusedArgs a) {
 // Weight and bias gradients as outer products over the batch:
 // dw[m][n] = sum_b u[b][m] v[b][n], db[n] = sum_b v[b][n] (row M of the
 // tile grid, u taken as 1).  A workgroup owns 16 rows x 64 columns of one
-// problem, a wavefront one 16 x 16 tile.
+// problem, a wavefront one 16 x 16 tile.  The batch runs in chunks of 256
+// rows: the workgroup loads its u columns and v columns of a chunk with
+// coalesced loads (v 16 bytes at a time when its width allows), stages them
+// in LDS and reads the products' operands from there; the next chunk's
+// loads are issued before the current chunk's products.
 constexpr int kMaxOuter = 8;
+constexpr int kOC = 256;  // batch rows per chunk
+constexpr int kUs = 20;   // LDS row strides: lanes of one operand read fall in distinct banks
+constexpr int kVs = 68;
 struct OuterProb {
   const float* u;
   int ldu, M;
@@ -719,45 +749,16 @@ struct OuterProb {
   float* dw;
   float* db;
   int tiles_n, wg0;
+  int vec;  // v read 16 bytes at a time (N and ldv multiples of 4, v 16-byte aligned); else N <= 16
 };
 struct OuterArgs {
   int nbatch, nprob;
   OuterProb p[kMaxOuter];
 };
 
-// One 128-row chunk of the batch for this lane: av[4 j + s] = u[kk][m],
-// bv[4 j + s] = v[kk][col], kk = kb + 16 j + 4 (lane / 16) + s (rows past
-// the batch repeat its last 16; their products are skipped).
-struct OuterChunk {
-  float av[32], bv[32];
-};
-__device__ __forceinline__ void outer_load(__amdgpu_buffer_rsrc_t ru, uint32_t uoff, int ldu,
-                                           __amdgpu_buffer_rsrc_t rv, uint32_t voff, int ldv, int nbatch, int kb,
-                                           OuterChunk& ch) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int k0 = min(kb + 16 * j, nbatch - 16);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      ch.av[4 * j + s] = ldb(ru, uoff, uint32_t(k0 + s) * uint32_t(ldu) * 4u);
-      ch.bv[4 * j + s] = ldb(rv, voff, uint32_t(k0 + s) * uint32_t(ldv) * 4u);
-    }
-  }
-}
-__device__ __forceinline__ void outer_mfma(const OuterChunk& ch, bool mrow, float afill, bool ncol, int nbatch,
-                                           int kb, f32x4& acc) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (kb + 16 * j < nbatch) {  // uniform
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(mrow ? ch.av[4 * j + s] : afill, ncol ? ch.bv[4 * j + s] : 0.f,
-                                                   acc, 0, 0, 0);
-    }
-  }
-}
-
 __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
+  __shared__ float Us[kOC * kUs];
+  __shared__ __attribute__((aligned(16))) float Vs[kOC * kVs];
   const int wg = blockIdx.x;
   int k = 0;
 #pragma unroll
@@ -765,36 +766,63 @@ __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
     if (i < a.nprob && wg >= a.p[i].wg0) k = i;
   const OuterProb& p = a.p[k];
   const int local = wg - p.wg0, tm = local / p.tiles_n, tn = local - tm * p.tiles_n;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-  const int m = tm * kRows + c;                 // the A row this lane supplies
-  const int col = tn * kQ + w * 16 + c;         // the B column this lane supplies
-  const bool mrow = m < p.M, ncol = col < p.N;
-  const float afill = (m == p.M && p.db != nullptr) ? 1.f : 0.f;  // the bias row
-  const int mc = min(m, p.M - 1), cc = min(col, p.N - 1);         // loads stay inside the operands
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
   const int nb = a.nbatch;
-  const __amdgpu_buffer_rsrc_t ru = make_res(p.u, uint32_t(nb) * uint32_t(p.ldu) * 4u);
-  const __amdgpu_buffer_rsrc_t rv = make_res(p.v, uint32_t(nb) * uint32_t(p.ldv) * 4u);
-  const uint32_t uoff = (uint32_t(4 * g) * uint32_t(p.ldu) + mc) * 4u;
-  const uint32_t voff = (uint32_t(4 * g) * uint32_t(p.ldv) + cc) * 4u;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  // two chunks in flight: the next chunk's loads are issued before this one's products
-  OuterChunk c0, c1;
-  outer_load(ru, uoff, p.ldu, rv, voff, p.ldv, nb, 0, c0);
-  for (int kb = 0; kb < nb; kb += 256) {
-    if (kb + 128 < nb) outer_load(ru, uoff, p.ldu, rv, voff, p.ldv, nb, kb + 128, c1);
-    outer_mfma(c0, mrow, afill, ncol, nb, kb, acc);
-    if (kb + 128 < nb) {
-      if (kb + 256 < nb) outer_load(ru, uoff, p.ldu, rv, voff, p.ldv, nb, kb + 256, c0);
-      outer_mfma(c1, mrow, afill, ncol, nb, kb + 128, acc);
+  const bool vec = p.vec != 0;
+  // this thread's loads: rows (t / 16) + 16 i of the chunk; u column um, v columns vc (.. vc + 3)
+  const int lr = t >> 4, lc = t & 15;
+  const int um = min(tm * kRows + lc, p.M - 1);
+  const int vc = vec ? min(tn * kQ + 4 * lc, p.N - 4) : min(tn * kQ + lc, p.N - 1);
+  // this lane's operands: A row m, B column col
+  const int m = tm * kRows + c, col = tn * kQ + w * 16 + c;
+  const bool mrow = m < p.M;
+  const float afill = (m == p.M && p.db != nullptr) ? 1.f : 0.f;  // the bias row
+  const bool live = tn * kQ + w * 16 < p.N && (vec || w == 0);  // uniform: this wavefront's tile has columns
+  float uu[16];
+  f32x4 vv[16];
+  auto load = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const long kk = min(kb + lr + 16 * i, nb - 1);
+      uu[i] = p.u[kk * p.ldu + um];
+      if (vec) vv[i] = *reinterpret_cast<const f32x4*>(p.v + kk * p.ldv + vc);
+      else vv[i].x = p.v[kk * p.ldv + vc];
     }
+  };
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  load(0);
+  for (int kb = 0; kb < nb; kb += kOC) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = lr + 16 * i;
+      Us[r * kUs + lc] = uu[i];
+      if (vec) *reinterpret_cast<f32x4*>(Vs + r * kVs + 4 * lc) = vv[i];
+      else Vs[r * kVs + lc] = vv[i].x;
+    }
+    __syncthreads();
+    if (kb + kOC < nb) load(kb + kOC);
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < kOC / 16; ++j) {
+        if (kb + 16 * j < nb) {  // uniform
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) {
+            const int r = 16 * j + 4 * g + s2;
+            const float x = Us[r * kUs + c];
+            const float y = Vs[r * kVs + w * 16 + c];
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(mrow ? x : afill, y, acc, 0, 0, 0);
+          }
+        }
+      }
+    }
+    __syncthreads();
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = tm * kRows + 4 * g + i;
-    const int n = tn * kQ + w * 16 + c;
-    if (n >= p.N) continue;
-    if (row < p.M) p.dw[long(row) * p.N + n] = acc[i];
-    else if (row == p.M && p.db) p.db[n] = acc[i];
+    if (col >= p.N) continue;
+    if (row < p.M) p.dw[long(row) * p.N + col] = acc[i];
+    else if (row == p.M && p.db) p.db[col] = acc[i];
   }
 }
 
@@ -815,6 +843,9 @@ int add_outer(OuterArgs& o, int& wgs, const float* u, int ldu, int M, const floa
   p.db = db;
   p.tiles_n = int(ceil_div(N, kQ));
   p.wg0 = wgs;
+  p.vec = (N % 4 == 0 && ldv % 4 == 0 && aligned16(v)) ? 1 : 0;
+  TTRL_REQUIRE(p.vec || N <= 16, "%s: a gradient product of width %d must have a width and row stride that are "
+               "multiples of 4 and a 16-byte aligned operand", name, N);
   wgs += int(ceil_div(M + (db ? 1 : 0), kRows)) * p.tiles_n;
   return TTRL_OK;
 }
