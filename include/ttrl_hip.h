@@ -439,6 +439,18 @@ int ttrl_sac_actor_loss(ttrl_ctx* ctx, int B, const float* q, const float* logp,
                         float target_entropy, int learn_alpha, float* actor_loss, float* alpha_loss, float* dq,
                         float* g_logp, float* d_log_alpha);
 
+/* One deferred Adam step over a flat arena (the deferred steps under
+ * "optimizer" below run it; a fused SAC update applies it in its stages). */
+typedef struct ttrl_adam_range {
+  float* p;
+  const float* g;
+  float* m_s;
+  float* v_s;
+  long n;
+  const int* step;
+  float lr, beta1, beta2, eps, weight_decay;
+  int slot;
+} ttrl_adam_range;
 /* The SAC update (ttrl/algos/sac/agent.py:218-238 over ttrl/algos/sac/losses.py:25-94,
  * ttrl/algos/gaussian.py:55-117, ttrl/algos/sac/policy.py:30-40 and the twin
  * critics and policy of ttrl/nets/build.py) as eight stages, each one
@@ -496,8 +508,31 @@ typedef struct ttrl_sac_fused_desc {
   float *gP1, *gp1, *gP2, *gp2, *gWm, *gbm, *gWl, *gbl;
   float *g_critic[2][6];    /* the trained critics' W1, b1, W2, b2, w3, b3 gradients */
   float *g_log_alpha;
+  /* fuse_adam nonzero: the stages step the optimizers as they form the
+   * gradients, each element with ttrl_adam_step's arithmetic.  Stage 3 steps
+   * the critics' arena (critic_adam; g_critic lie inside its g) and then
+   * blends each stepped critic parameter into polyak_dst, the target
+   * critics' arena laid out like the critics' (dst = (1 - tau) dst + tau p,
+   * ttrl/algos/sac/targets.py:45-52); stage 7 steps the policy's arena
+   * (actor_adam; gP1 .. gbl inside its g) and, with learn_alpha, the
+   * temperature (alpha_adam; g_log_alpha inside its g).  Each range's
+   * partial sums of g^2 wait in its slot for ttrl_adam_finish_slots, with
+   * the counts ttrl_sac_fused_adam_parts gives.  Arena elements no stage
+   * forms a gradient for (the zero padding between tensors) are not
+   * stepped: with a zero gradient and zero moments a step leaves them as
+   * they are.  With fuse_adam zero the caller steps the optimizers after
+   * stages 3 and 7. */
+  int fuse_adam;
+  ttrl_adam_range critic_adam, actor_adam, alpha_adam;
+  float *polyak_dst;
+  float tau;
 } ttrl_sac_fused_desc;
 int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* desc);
+/* The number of partial sums of g^2 a fused stage leaves in its Adam
+ * range's slot: stage 3 (critic_adam) or 7 (actor_adam); the temperature's
+ * range leaves one.  No counterpart in the reference: the count a caller
+ * passes to ttrl_adam_finish_slots for these ranges. */
+int ttrl_sac_fused_adam_parts(const ttrl_sac_fused_desc* desc, int stage, int* parts);
 
 /* ----------------------------------------------------------- optimizer --- */
 
@@ -535,22 +570,13 @@ int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, fl
  * NULL) and *step incremented.  Each range gives the same bits as
  * ttrl_adam_step (ttrl/engine/optim/adam.py:93-134), grad_sq included.  A
  * slot must not be reused between its step and its finish. */
-typedef struct ttrl_adam_range {
-  float* p;
-  const float* g;
-  float* m_s;
-  float* v_s;
-  long n;
-  const int* step;
-  float lr, beta1, beta2, eps, weight_decay;
-  int slot;
-} ttrl_adam_range;
 typedef struct ttrl_adam_finish {
   int slot;
   long n;
   int* step;
   float* grad_sq;
   int accumulate;
+  int parts;  /* partial sums in the slot; 0: those of a deferred range of n parameters */
 } ttrl_adam_finish;
 int ttrl_adam_step_deferred(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n,
                             const int* step, float lr, float beta1, float beta2, float eps, float weight_decay,

@@ -13,6 +13,7 @@
 // kernel reads t_old and uses t = t_old + 1, and the finishing kernel (one
 // block, after every update block has run) stores t and the reduced
 // sum of squares.  All reductions are fixed-order.
+#include "adam_dev.hpp"
 #include "common.hpp"
 
 #include <algorithm>
@@ -29,42 +30,17 @@ constexpr int kOptMaxBlocks = 1024;
 
 float* ctx_workspace(ttrl_ctx* ctx, long* floats);
 
-// The step's fused scalars (alpha_t, eps_t) from the update count *step + 1,
-// computed once per workgroup by thread 0 (its loads issued before the call
-// stay in flight while it does).
-__device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float lr, float b1, float b2, float eps,
-                                             float* alpha_t, float* eps_t) {
-  __shared__ float sc[2];
-  if (threadIdx.x == 0) {
-    const int t = *step + 1;
-    const double bc1 = 1.0 - pow(double(b1), double(t));
-    const double bc2 = 1.0 - pow(double(b2), double(t));
-    const double c = sqrt((1.0 - double(b2)) / bc2);
-    sc[0] = float(double(lr) * (1.0 - double(b1)) / bc1 / c);
-    sc[1] = float(double(eps) / c);
-  }
-  __syncthreads();
-  *alpha_t = sc[0];
-  *eps_t = sc[1];
-}
-
-// The update of four consecutive parameters with gradient gv; g^2 is added
-// to gsq element by element in order.  Every product and sum is rounded on
-// its own (no contraction into FMAs), here and in the scalar tails, so every
-// kernel that steps a parameter gives the same bits however the compiler
-// schedules it.
+// The update of four consecutive parameters with gradient gv, element by
+// element in order (adam1); g^2 is added to gsq in that order.
 __device__ __forceinline__ void adam4(f32x4& pv, const f32x4& gv, f32x4& sv, f32x4& vv, float b1, float b2, float wd,
                                       float eps_t, float alpha_t, float& gsq) {
-#pragma clang fp contract(off)
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const float graw = gv[q];
-    gsq += graw * graw;
-    const float gg = wd != 0.f ? graw + wd * pv[q] : graw;
-    vv[q] = gg * gg + b2 * vv[q];
-    sv[q] = gg + b1 * sv[q];
-    const float upd = (sv[q] / (sqrtf(vv[q]) + eps_t)) * alpha_t;
-    pv[q] = pv[q] - upd;
+    float pq = pv[q], sq = sv[q], vq = vv[q];
+    adam1(pq, gv[q], sq, vq, b1, b2, wd, eps_t, alpha_t, gsq);
+    pv[q] = pq;
+    sv[q] = sq;
+    vv[q] = vq;
   }
 }
 
@@ -1109,7 +1085,9 @@ int ttrl_adam_finish_slots(ttrl_ctx* ctx, int n, const ttrl_adam_finish* f) {
                  f[i].slot, kAdamSlots);
     TTRL_REQUIRE(f[i].n > 0 && f[i].step, "ttrl_adam_finish_slots: finish %d: empty range or null step", i);
     fs.parts[i] = ctx_adam_partials(ctx) + long(f[i].slot) * kAdamSlotFloats;
-    fs.count[i] = int(grid_for(f[i].n, 4));
+    TTRL_REQUIRE(f[i].parts >= 0 && f[i].parts <= kAdamSlotFloats,
+                 "ttrl_adam_finish_slots: finish %d: %d partial sums outside [0, %d]", i, f[i].parts, kAdamSlotFloats);
+    fs.count[i] = f[i].parts > 0 ? f[i].parts : int(grid_for(f[i].n, 4));
     fs.step[i] = f[i].step;
     fs.out[i] = f[i].grad_sq;
     fs.accumulate[i] = f[i].accumulate;

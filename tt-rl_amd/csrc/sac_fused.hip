@@ -38,6 +38,7 @@
 // an A row (one 128-bit LDS read) and of a transposed B row (one 128-bit
 // global read).  Every sum runs in a fixed order, so replays are
 // bit-identical.
+#include "adam_dev.hpp"
 #include "common.hpp"
 #include "tile_gemm.hpp"
 
@@ -750,16 +751,56 @@ struct OuterProb {
   float* db;
   int tiles_n, wg0;
   int vec;  // v read 16 bytes at a time (N and ldv multiples of 4, v 16-byte aligned); else N <= 16
+  long offw, offb;  // with a fused Adam step: dw's and db's element offsets in the stepped arena
+};
+// A fused Adam step over one arena (the layout of ttrl_adam_range) and, when
+// target is given, the Polyak blend of each stepped element into it.
+struct OuterAdam {
+  float *p, *S, *V;
+  const int* step;
+  float lr, b1, b2, eps, wd;
+  float* partials;  // one sum of g^2 per workgroup
+  float* target;
+  float keep, tau;
 };
 struct OuterArgs {
   int nbatch, nprob;
   OuterProb p[kMaxOuter];
+  int adam_on;   // the products' workgroups step `adam`
+  OuterAdam adam;
+  int nwg;       // the products' workgroups; workgroup nwg (when alpha_on) steps the temperature
+  int alpha_on;
+  OuterAdam alpha;
+  long alpha_off;  // the temperature's element in its arena
+  const float* alpha_g;
 };
+
+// The temperature's Adam step (one element; the finish sums one partial).
+__device__ void alpha_step(const OuterArgs& a) {
+  const OuterAdam& q = a.alpha;
+  float at, et;
+  const long o = a.alpha_off;
+  const float pv0 = q.p[o], sv0 = q.S[o], vv0 = q.V[o], g = *a.alpha_g;
+  adam_scalars(q.step, q.lr, q.b1, q.b2, q.eps, &at, &et);
+  if (threadIdx.x == 0) {
+    float pv = pv0, sv = sv0, vv = vv0, gsq = 0.f;
+    adam1(pv, g, sv, vv, q.b1, q.b2, q.wd, et, at, gsq);
+    q.p[o] = pv;
+    q.S[o] = sv;
+    q.V[o] = vv;
+    q.partials[0] = gsq;
+  }
+}
 
 __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
   __shared__ float Us[kOC * kUs];
   __shared__ __attribute__((aligned(16))) float Vs[kOC * kVs];
+  __shared__ float red[kThreads / 64];
   const int wg = blockIdx.x;
+  if (a.alpha_on && wg == a.nwg) {  // uniform
+    alpha_step(a);
+    return;
+  }
   int k = 0;
 #pragma unroll
   for (int i = 1; i < kMaxOuter; ++i)
@@ -791,6 +832,25 @@ __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
   };
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   load(0);
+  // the stepped elements' parameters, moments and targets, in flight with the batch
+  const bool adam = a.adam_on != 0;
+  long eo[4];
+  bool ev[4];
+  float pp[4] = {}, ps[4] = {}, pvv[4] = {}, pt[4] = {};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = tm * kRows + 4 * g + i;
+    ev[i] = col < p.N && (row < p.M || (row == p.M && p.db));
+    eo[i] = !ev[i] ? 0 : (row < p.M ? p.offw + long(row) * p.N + col : p.offb + col);
+    if (adam) {
+      pp[i] = a.adam.p[eo[i]];
+      ps[i] = a.adam.S[eo[i]];
+      pvv[i] = a.adam.V[eo[i]];
+      if (a.adam.target) pt[i] = a.adam.target[eo[i]];
+    }
+  }
+  float at = 0.f, et = 0.f;
+  if (adam) adam_scalars(a.adam.step, a.adam.lr, a.adam.b1, a.adam.b2, a.adam.eps, &at, &et);
   for (int kb = 0; kb < nb; kb += kOC) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -817,12 +877,25 @@ __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
     }
     __syncthreads();
   }
+  float gsq = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = tm * kRows + 4 * g + i;
-    if (col >= p.N) continue;
+    if (!ev[i]) continue;
     if (row < p.M) p.dw[long(row) * p.N + col] = acc[i];
-    else if (row == p.M && p.db) p.db[col] = acc[i];
+    else p.db[col] = acc[i];
+    if (adam) {
+      float pv = pp[i], sv = ps[i], vv = pvv[i];
+      adam1(pv, acc[i], sv, vv, a.adam.b1, a.adam.b2, a.adam.wd, et, at, gsq);
+      a.adam.p[eo[i]] = pv;
+      a.adam.S[eo[i]] = sv;
+      a.adam.V[eo[i]] = vv;
+      if (a.adam.target) a.adam.target[eo[i]] = pt[i] * a.adam.keep + pv * a.adam.tau;
+    }
+  }
+  if (adam) {
+    const float tot = block_sum<kThreads>(gsq, red);
+    if (threadIdx.x == 0) a.adam.partials[wg] = tot;
   }
 }
 
@@ -846,7 +919,66 @@ int add_outer(OuterArgs& o, int& wgs, const float* u, int ldu, int M, const floa
   p.vec = (N % 4 == 0 && ldv % 4 == 0 && aligned16(v)) ? 1 : 0;
   TTRL_REQUIRE(p.vec || N <= 16, "%s: a gradient product of width %d must have a width and row stride that are "
                "multiples of 4 and a 16-byte aligned operand", name, N);
+  p.offw = p.offb = 0;
   wgs += int(ceil_div(M + (db ? 1 : 0), kRows)) * p.tiles_n;
+  return TTRL_OK;
+}
+
+// The gradient products of stage 3 (the trained critics' W1, b1, W2, b2,
+// w3, b3) or stage 7 (the policy's P1, p1, P2, p2, Wm, bm, Wl, bl).
+int outer_problems(const ttrl_sac_fused_desc* d, int stage, OuterArgs& o, int& wgs, const char* name) {
+  const int B = d->B, O = d->O, A = d->A, H = d->H;
+  o.nbatch = B;
+  wgs = 0;
+  int rc = 0;
+  if (stage == 3) {
+    for (int j = 0; j < 2; ++j) {
+      float* const* gc = d->g_critic[j];
+      TTRL_REQUIRE(gc[0] && gc[1] && gc[2] && gc[3] && gc[4] && gc[5] && d->obs_actions && d->dq1 && d->q1 &&
+                       d->dq2 && d->q2 && d->dQ,
+                   "%s: stage 3: null gradient or operand", name);
+      rc = add_outer(o, wgs, d->obs_actions, O + A, O + A, d->dq1 + long(j) * B * H, H, H, gc[0], gc[1], name);
+      if (!rc)
+        rc = add_outer(o, wgs, d->q1 + long(2 + j) * B * H, H, H, d->dq2 + long(j) * B * H, H, H, gc[2], gc[3], name);
+      if (!rc) rc = add_outer(o, wgs, d->q2 + long(2 + j) * B * H, H, H, d->dQ + long(j) * B, 1, 1, gc[4], gc[5], name);
+      if (rc) return rc;
+    }
+  } else {
+    TTRL_REQUIRE(d->gP1 && d->gp1 && d->gP2 && d->gp2 && d->gWm && d->gbm && d->gWl && d->gbl && d->obs_pair &&
+                     d->dh1 && d->h1 && d->dh2 && d->h2 && d->dhead,
+                 "%s: stage 7: null gradient or operand", name);
+    rc = add_outer(o, wgs, d->obs_pair, O, O, d->dh1, H, H, d->gP1, d->gp1, name);
+    if (!rc) rc = add_outer(o, wgs, d->h1, H, H, d->dh2, H, H, d->gP2, d->gp2, name);
+    if (!rc) rc = add_outer(o, wgs, d->h2, H, H, d->dhead, 2 * A, A, d->gWm, d->gbm, name);
+    if (!rc) rc = add_outer(o, wgs, d->h2, H, H, d->dhead + A, 2 * A, A, d->gWl, d->gbl, name);
+  }
+  return rc;
+}
+
+// A fused Adam step from its range: the hyperparameters checked as
+// ttrl_adam_step checks them, the partials in the range's context slot.
+int outer_adam(ttrl_ctx* ctx, const ttrl_adam_range& r, OuterAdam& q, const char* name, const char* which) {
+  TTRL_REQUIRE(r.p && r.g && r.m_s && r.v_s && r.step && r.n > 0, "%s: %s: null buffer or empty range", name, which);
+  TTRL_REQUIRE(r.lr > 0.f && r.beta1 >= 0.f && r.beta1 < 1.f && r.beta2 >= 0.f && r.beta2 < 1.f && r.eps > 0.f &&
+                   r.weight_decay >= 0.f,
+               "%s: %s: bad hyperparameters", name, which);
+  TTRL_REQUIRE(r.slot >= 0 && r.slot < kAdamSlots, "%s: %s: slot %d outside [0, %d)", name, which, r.slot,
+               kAdamSlots);
+  q = OuterAdam{r.p, r.m_s, r.v_s, r.step, r.lr, r.beta1, r.beta2, r.eps, r.weight_decay,
+                ctx_adam_partials(ctx) + long(r.slot) * kAdamSlotFloats, nullptr, 0.f, 0.f};
+  return TTRL_OK;
+}
+
+// Each product's dw and db as element offsets in the stepped arena [g, g + n).
+int outer_offsets(OuterArgs& o, const ttrl_adam_range& r, const char* name) {
+  for (int i = 0; i < o.nprob; ++i) {
+    OuterProb& p = o.p[i];
+    const long ow = long(p.dw - r.g), ob = p.db ? long(p.db - r.g) : 0;
+    TTRL_REQUIRE(ow >= 0 && ow + long(p.M) * p.N <= r.n && (!p.db || (ob >= 0 && ob + p.N <= r.n)),
+                 "%s: gradient product %d lies outside the stepped arena", name, i);
+    p.offw = ow;
+    p.offb = ob;
+  }
   return TTRL_OK;
 }
 
@@ -974,37 +1106,53 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
     case 3:
     case 7: {
       OuterArgs o{};
-      o.nbatch = B;
-      int wgs = 0, rc = 0;
-      if (stage == 3) {
-        for (int j = 0; j < 2; ++j) {
-          float* const* gc = d->g_critic[j];
-          TTRL_REQUIRE(gc[0] && gc[1] && gc[2] && gc[3] && gc[4] && gc[5] && a.obs_actions,
-                       "%s: stage 3: null gradient", name);
-          rc = add_outer(o, wgs, a.obs_actions, O + A, O + A, a.dq1 + long(j) * B * H, H, H, gc[0], gc[1], name);
-          if (!rc)
-            rc = add_outer(o, wgs, a.q1 + long(2 + j) * B * H, H, H, a.dq2 + long(j) * B * H, H, H, gc[2], gc[3],
-                           name);
-          if (!rc) rc = add_outer(o, wgs, a.q2 + long(2 + j) * B * H, H, H, a.dQ + long(j) * B, 1, 1, gc[4], gc[5],
-                                  name);
-          if (rc) return rc;
-        }
-      } else {
-        TTRL_REQUIRE(d->gP1 && d->gp1 && d->gP2 && d->gp2 && d->gWm && d->gbm && d->gWl && d->gbl,
-                     "%s: stage 7: null gradient", name);
-        rc = add_outer(o, wgs, a.obs_pair, O, O, a.dh1, H, H, d->gP1, d->gp1, name);
-        if (!rc) rc = add_outer(o, wgs, a.h1, H, H, a.dh2, H, H, d->gP2, d->gp2, name);
-        if (!rc) rc = add_outer(o, wgs, a.h2, H, H, a.dhead, 2 * A, A, d->gWm, d->gbm, name);
-        if (!rc) rc = add_outer(o, wgs, a.h2, H, H, a.dhead + A, 2 * A, A, d->gWl, d->gbl, name);
+      int wgs = 0;
+      int rc = outer_problems(d, stage, o, wgs, name);
+      if (rc) return rc;
+      o.nwg = wgs;
+      if (d->fuse_adam) {
+        const ttrl_adam_range& r = stage == 3 ? d->critic_adam : d->actor_adam;
+        rc = outer_adam(ctx, r, o.adam, name, stage == 3 ? "critic_adam" : "actor_adam");
+        if (!rc) rc = outer_offsets(o, r, name);
         if (rc) return rc;
+        TTRL_REQUIRE(wgs <= kAdamSlotFloats, "%s: %d partial sums exceed a slot", name, wgs);
+        o.adam_on = 1;
+        if (stage == 3) {
+          TTRL_REQUIRE(d->polyak_dst && d->tau >= 0.f && d->tau <= 1.f, "%s: stage 3: null Polyak target or tau "
+                       "outside [0, 1]", name);
+          o.adam.target = d->polyak_dst;
+          o.adam.keep = 1.f - d->tau;
+          o.adam.tau = d->tau;
+        } else if (d->learn_alpha) {
+          const ttrl_adam_range& ra = d->alpha_adam;
+          rc = outer_adam(ctx, ra, o.alpha, name, "alpha_adam");
+          if (rc) return rc;
+          TTRL_REQUIRE(ra.slot != r.slot, "%s: the temperature and the policy share slot %d", name, r.slot);
+          const long off = d->g_log_alpha ? long(d->g_log_alpha - ra.g) : -1;
+          TTRL_REQUIRE(off >= 0 && off < ra.n, "%s: g_log_alpha lies outside the temperature's arena", name);
+          o.alpha_on = 1;
+          o.alpha_off = off;
+          o.alpha_g = d->g_log_alpha;
+        }
       }
-      hipLaunchKernelGGL(k_outer_grads, dim3(unsigned(wgs)), dim3(kThreads), 0, st, o);
+      hipLaunchKernelGGL(k_outer_grads, dim3(unsigned(wgs + o.alpha_on)), dim3(kThreads), 0, st, o);
       break;
     }
     default:
       return set_error(TTRL_EINVAL, "%s: stage %d outside [0, 7]", name, stage);
   }
   return check_launch(name);
+}
+
+int ttrl_sac_fused_adam_parts(const ttrl_sac_fused_desc* d, int stage, int* parts) {
+  TTRL_REQUIRE(d && parts, "ttrl_sac_fused_adam_parts: null argument");
+  TTRL_REQUIRE(stage == 3 || stage == 7, "ttrl_sac_fused_adam_parts: stage %d steps no optimizer (3 or 7)", stage);
+  OuterArgs o{};
+  int wgs = 0;
+  const int rc = outer_problems(d, stage, o, wgs, "ttrl_sac_fused_adam_parts");
+  if (rc) return rc;
+  *parts = wgs;
+  return TTRL_OK;
 }
 
 }  // extern "C"

@@ -78,7 +78,7 @@ class AdamFinish(C.Structure):
     """Mirror of ttrl_adam_finish."""
 
     _fields_ = [("slot", C.c_int), ("n", C.c_long), ("step", C.c_void_p), ("grad_sq", C.c_void_p),
-                ("accumulate", C.c_int)]
+                ("accumulate", C.c_int), ("parts", C.c_int)]
 
 
 class DqnTailDesc(C.Structure):
@@ -189,7 +189,9 @@ class SacFusedDesc(C.Structure):
                                              "discounts", "is_weights", "log_alpha")]
                 + [("target_entropy", C.c_float), ("learn_alpha", C.c_int)]
                 + [(n, C.c_void_p) for n in SAC_FUSED_BUFFERS + SAC_FUSED_METRICS + SAC_FUSED_POLICY_GRADS]
-                + [("g_critic", (C.c_void_p * 6) * 2), ("g_log_alpha", C.c_void_p)])
+                + [("g_critic", (C.c_void_p * 6) * 2), ("g_log_alpha", C.c_void_p)]
+                + [("fuse_adam", C.c_int), ("critic_adam", AdamRange), ("actor_adam", AdamRange),
+                   ("alpha_adam", AdamRange), ("polyak_dst", C.c_void_p), ("tau", C.c_float)])
 
 
 class ConvGeom(C.Structure):
@@ -273,6 +275,7 @@ SIGNATURES = {
     "ttrl_replay_assemble": ([P, C.POINTER(ReplayRing), I, P, P, I, C.c_double, P, P, P, I, P, P, P, P, P], I),
     "ttrl_replay_draw_batch": ([P, C.POINTER(ReplayRing), C.POINTER(ReplayDraw)], I),
     "ttrl_sac_fused_stage": ([P, I, C.POINTER(SacFusedDesc)], I),
+    "ttrl_sac_fused_adam_parts": ([C.POINTER(SacFusedDesc), I, C.POINTER(I)], I),
     "ttrl_replay_update_priorities": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_replay_update_priorities_f64": ([P, C.POINTER(ReplayRing), I, P, P, P], I),
     "ttrl_gaussian_act": ([P, I, I, I, P, P, P, P, P, F, F, P, P, P, F, I, P, P, P], I),

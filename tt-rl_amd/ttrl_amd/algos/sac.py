@@ -488,6 +488,7 @@ class _FusedUpdate:
                   "dq1": (2, B, H), "dap": (2, nq, B, A), "dhead": (B, 2 * A), "dh2": (B, H), "dh1": (B, H),
                   "terms": (4, B)}
         self.buf = {k: DeviceArray(dev, v) for k, v in shapes.items()}
+        self._nparts: dict = {}
 
     @staticmethod
     def width(learner):
@@ -521,6 +522,10 @@ class _FusedUpdate:
                     return None
         wide = [lins[1].weight] + [c[1].weight for c in learner.twin.layers]
         if any(w.data.ptr % 16 for w in wide):
+            return None
+        # the Polyak blend runs element by element beside the critics' step
+        ca, ta = getattr(learner.nets.critics, "arena", None), getattr(learner.nets.targets, "arena", None)
+        if ca is None or ta is None or ca.numel != ta.numel or list(ca.offsets) != list(ta.offsets):
             return None
         return H
 
@@ -564,7 +569,23 @@ class _FusedUpdate:
             for k, g in enumerate(slots):
                 d.g_critic[j][k] = g.ptr
         d.g_log_alpha = L.log_alpha._grad_slot.ptr if cfg.learn_alpha else None
+        # the three Adam steps and the Polyak blend run inside stages 3 and 7
+        d.fuse_adam = 1
+        d.critic_adam = L.critic_opt.fused_range(0)
+        d.actor_adam = L.actor_opt.fused_range(1)
+        if cfg.learn_alpha:
+            d.alpha_adam = L.alpha_opt.fused_range(2)
+        d.polyak_dst, d.tau = L.nets.targets.arena.data.ptr, cfg.tau
         return d
+
+    def _parts(self, d, stage: int) -> int:
+        """The partial sums of g^2 stage 3 or 7 leaves for its optimizer's finish."""
+        if stage not in self._nparts:
+            n = C.c_int(0)
+            _lib.check(_lib.lib().ttrl_sac_fused_adam_parts(C.byref(d), int(stage), C.byref(n)),
+                       "ttrl_sac_fused_adam_parts")
+            self._nparts[stage] = int(n.value)
+        return self._nparts[stage]
 
     def _stage(self, d, k: int) -> None:
         self.learner.device.call("ttrl_sac_fused_stage", int(k), C.byref(d))
@@ -588,22 +609,20 @@ class _FusedUpdate:
         if rec is not None:
             rec += [buf["h1"], buf["h2"], buf["q1"], buf["q2"]]
         self._stage(d, 2)
-        self._stage(d, 3)
+        self._stage(d, 3)  # the critics' gradients, their Adam step and the Polyak blend
         self._written(L.critic_opt.params)
-        L.critic_opt.step_deferred(0)
         self._stage(d, 4)
         if rec is not None:
             rec += [buf["q1pi"], buf["q2pi"]]
         self._stage(d, 5)
         self._stage(d, 6)
-        self._stage(d, 7)
+        self._stage(d, 7)  # the policy's gradients and Adam step, and the temperature's
         self._written(L.actor_opt.params)
-        stepped = [(L.actor_opt, 1)]
+        stepped = [(L.critic_opt, 0, self._parts(d, 3)), (L.actor_opt, 1, self._parts(d, 7))]
         if cfg.learn_alpha:
             self._written([L.log_alpha])
-            stepped.append((L.alpha_opt, 2))
-        adam_multi(L.device, stepped, polyak=(L.nets.targets.arena.data, L.nets.critics.arena.data, cfg.tau))
-        finish_steps(L.device, [(L.critic_opt, 0)] + stepped)
+            stepped.append((L.alpha_opt, 2, 1))
+        finish_steps(L.device, stepped)
         metrics = {"critic_loss": Tensor(L._critic_out["loss"]), "alpha": Tensor(L._critic_out["alpha"]),
                    "q_target": Tensor(L._critic_out["q_target"]), "actor_loss": Tensor(L._actor_out["actor_loss"]),
                    "logp": Tensor(L._logp_out), "critic_grad_sq": Tensor(L.critic_opt.grad_sq),

@@ -251,9 +251,23 @@ class Adam(Optimizer):
                               self._counter(len(self.params)).value, self.lr, self.b1, self.b2, self.eps,
                               self.weight_decay, int(slot))
 
-    def _finish_desc(self, slot: int) -> "_lib.AdamFinish":
+    def fused_range(self, slot: int) -> "_lib.AdamRange":
+        """This arena's update as a range that a fused update stage applies
+        while it forms the gradients (it writes each gradient into the
+        arena's slot, then steps that element); finished by `finish_steps`
+        with the stage's partial count."""
+        if self.arena is None:
+            raise ValueError("Adam.fused_range: the parameters must be exactly one ParamArena's")
+        if any(st != self._arena_t for st in self.steps):
+            raise RuntimeError("Adam.fused_range: the parameters' update counts differ; use step()")
+        a = self.arena
+        return _lib.AdamRange(a.data.ptr, a.grad.ptr, self._m_flat.ptr, self._v_flat.ptr, a.numel,
+                              self._counter(len(self.params)).value, self.lr, self.b1, self.b2, self.eps,
+                              self.weight_decay, int(slot))
+
+    def _finish_desc(self, slot: int, parts: int = 0) -> "_lib.AdamFinish":
         return _lib.AdamFinish(int(slot), self.arena.numel, self._counter(len(self.params)).value,
-                               self.grad_sq.ptr, 0)
+                               self.grad_sq.ptr, 0, int(parts))
 
     def _finished(self) -> None:
         """Host counters after a finished step (a capture advances them at replay)."""
@@ -366,10 +380,12 @@ def adam_multi(device, ranges, polyak=None) -> None:
 
 
 def finish_steps(device, steps) -> None:
-    """Finishes deferred steps ([(optimizer, slot)]) in one launch: each
-    optimizer's sum(g^2) into its `grad_sq` and its update count stored."""
-    descs = [opt._finish_desc(slot) for opt, slot in steps]
+    """Finishes deferred steps ([(optimizer, slot)] or [(optimizer, slot,
+    parts)], parts the number of partial sums a fused stage left in the
+    slot) in one launch: each optimizer's sum(g^2) into its `grad_sq` and its
+    update count stored."""
+    descs = [step[0]._finish_desc(*step[1:]) for step in steps]
     arr = (_lib.AdamFinish * max(1, len(descs)))(*descs)
     device.call("ttrl_adam_finish_slots", len(descs), arr)
-    for opt, _ in steps:
-        opt._finished()
+    for step in steps:
+        step[0]._finished()
