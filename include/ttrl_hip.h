@@ -526,6 +526,7 @@ typedef struct ttrl_sac_fused_desc {
   ttrl_adam_range critic_adam, actor_adam, alpha_adam;
   float *polyak_dst;
   float tau;
+  float *adam_scalars;      /* [6] the three steps' fused scalars, formed by stage 0 for stages 3 and 7 */
 } ttrl_sac_fused_desc;
 int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* desc);
 /* The number of partial sums of g^2 a fused stage leaves in its Adam

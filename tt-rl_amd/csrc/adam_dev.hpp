@@ -11,21 +11,22 @@
 
 namespace ttrl {
 
-// The step's fused scalars (alpha_t, eps_t) from the update count *step + 1,
-// computed once per workgroup by thread 0 (its loads issued before the call
-// stay in flight while it does).  Every thread of the workgroup calls it
-// (a barrier).
+// The step's fused scalars (alpha_t, eps_t) at update count t.
+// adam_scalars forms them from the count *step + 1 once per workgroup, by
+// thread 0 (its loads issued before the call stay in flight while it does);
+// every thread of the workgroup calls it (a barrier).
+__device__ __forceinline__ void adam_scalars_at(int t, float lr, float b1, float b2, float eps, float& alpha_t,
+                                                float& eps_t) {
+  const double bc1 = 1.0 - pow(double(b1), double(t));
+  const double bc2 = 1.0 - pow(double(b2), double(t));
+  const double c = sqrt((1.0 - double(b2)) / bc2);
+  alpha_t = float(double(lr) * (1.0 - double(b1)) / bc1 / c);
+  eps_t = float(double(eps) / c);
+}
 __device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float lr, float b1, float b2, float eps,
                                              float* alpha_t, float* eps_t) {
   __shared__ float sc[2];
-  if (threadIdx.x == 0) {
-    const int t = *step + 1;
-    const double bc1 = 1.0 - pow(double(b1), double(t));
-    const double bc2 = 1.0 - pow(double(b2), double(t));
-    const double c = sqrt((1.0 - double(b2)) / bc2);
-    sc[0] = float(double(lr) * (1.0 - double(b1)) / bc1 / c);
-    sc[1] = float(double(eps) / c);
-  }
+  if (threadIdx.x == 0) adam_scalars_at(*step + 1, lr, b1, b2, eps, sc[0], sc[1]);
   __syncthreads();
   *alpha_t = sc[0];
   *eps_t = sc[1];

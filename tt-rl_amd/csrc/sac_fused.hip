@@ -97,6 +97,12 @@ struct FusedArgs {
   float *dQ, *dq2, *dq1, *dap, *dhead, *dh2, *dh1, *terms;
   float *critic_loss, *alpha, *actor_loss, *alpha_loss, *q_target, *td_abs, *logp;
   float* g_log_alpha;
+  // the fused Adam steps' counts and hyperparameters (critic, actor,
+  // temperature), whose scalars stage 0 forms into adam_sc
+  int nsc;
+  const int* sstep[3];
+  float slr[3], sb1[3], sb2[3], seps[3];
+  float* adam_sc;
 };
 
 // Each stage issues every global load it needs before its first wait:
@@ -353,7 +359,10 @@ __device__ __forceinline__ float wave_sum_fixed(const float* x, int n) {
 }
 
 // ------------------------------------------------------------ stage 0 ---
-// grid (2B / 16, nq): the policy over [obs; next_obs].
+// grid (2B / 16 (+ 1), nq): the policy over [obs; next_obs].  With fused
+// optimizer steps, workgroup (2B / 16, 0) forms their scalars (two
+// double-precision powers each, off the stages that use them); the rest of
+// that row block has nothing to do.
 __global__ __launch_bounds__(kThreads) void k_sac_policy_fwd(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) float X[kRows * kXs];
   __shared__ __attribute__((aligned(16))) float At[kRows * kLda];
@@ -361,6 +370,15 @@ __global__ __launch_bounds__(kThreads) void k_sac_policy_fwd(FusedArgs a) {
   __shared__ float Wh[kQ * 2 * kMaxA];
   const int r0 = blockIdx.x * kRows, q = blockIdx.y, t = threadIdx.x;
   const int O = a.O, H = a.H, A = a.A, A2 = 2 * a.A, rows = 2 * a.B;
+  if (r0 == rows) {  // uniform
+    if (q == 0 && t < a.nsc) {
+      float at, et;
+      adam_scalars_at(*a.sstep[t] + 1, a.slr[t], a.sb1[t], a.sb2[t], a.seps[t], at, et);
+      a.adam_sc[2 * t] = at;
+      a.adam_sc[2 * t + 1] = et;
+    }
+    return;
+  }
   const int lane = t & 63, w = t >> 6, g = lane >> 4, c = lane & 15;
   const int col = q * kQ + w * 16 + c;
   InputRows in;
@@ -757,7 +775,7 @@ struct OuterProb {
 // target is given, the Polyak blend of each stepped element into it.
 struct OuterAdam {
   float *p, *S, *V;
-  const int* step;
+  const float* sc;  // the step's fused scalars (alpha_t, eps_t), formed by stage 0
   float lr, b1, b2, eps, wd;
   float* partials;  // one sum of g^2 per workgroup
   float* target;
@@ -778,10 +796,8 @@ struct OuterArgs {
 // The temperature's Adam step (one element; the finish sums one partial).
 __device__ void alpha_step(const OuterArgs& a) {
   const OuterAdam& q = a.alpha;
-  float at, et;
   const long o = a.alpha_off;
-  const float pv0 = q.p[o], sv0 = q.S[o], vv0 = q.V[o], g = *a.alpha_g;
-  adam_scalars(q.step, q.lr, q.b1, q.b2, q.eps, &at, &et);
+  const float pv0 = q.p[o], sv0 = q.S[o], vv0 = q.V[o], g = *a.alpha_g, at = q.sc[0], et = q.sc[1];
   if (threadIdx.x == 0) {
     float pv = pv0, sv = sv0, vv = vv0, gsq = 0.f;
     adam1(pv, g, sv, vv, q.b1, q.b2, q.wd, et, at, gsq);
@@ -849,8 +865,7 @@ __global__ __launch_bounds__(kThreads) void k_outer_grads(OuterArgs a) {
       if (a.adam.target) pt[i] = a.adam.target[eo[i]];
     }
   }
-  float at = 0.f, et = 0.f;
-  if (adam) adam_scalars(a.adam.step, a.adam.lr, a.adam.b1, a.adam.b2, a.adam.eps, &at, &et);
+  const float at = adam ? a.adam.sc[0] : 0.f, et = adam ? a.adam.sc[1] : 0.f;
   for (int kb = 0; kb < nb; kb += kOC) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -964,7 +979,7 @@ int outer_adam(ttrl_ctx* ctx, const ttrl_adam_range& r, OuterAdam& q, const char
                "%s: %s: bad hyperparameters", name, which);
   TTRL_REQUIRE(r.slot >= 0 && r.slot < kAdamSlots, "%s: %s: slot %d outside [0, %d)", name, which, r.slot,
                kAdamSlots);
-  q = OuterAdam{r.p, r.m_s, r.v_s, r.step, r.lr, r.beta1, r.beta2, r.eps, r.weight_decay,
+  q = OuterAdam{r.p, r.m_s, r.v_s, nullptr, r.lr, r.beta1, r.beta2, r.eps, r.weight_decay,
                 ctx_adam_partials(ctx) + long(r.slot) * kAdamSlotFloats, nullptr, 0.f, 0.f};
   return TTRL_OK;
 }
@@ -1071,7 +1086,21 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
       TTRL_REQUIRE(a.P1 && a.p1 && a.P2 && a.p2 && a.Wm && a.bm && a.Wl && a.bl && a.obs_pair && a.h1 && a.h2 &&
                        a.headp,
                    "%s: stage 0: null argument", name);
-      hipLaunchKernelGGL(k_sac_policy_fwd, dim3(2 * rb, nq), dim3(kThreads), 0, st, a);
+      if (d->fuse_adam) {
+        const ttrl_adam_range* rs[3] = {&d->critic_adam, &d->actor_adam, &d->alpha_adam};
+        a.nsc = d->learn_alpha ? 3 : 2;
+        for (int i = 0; i < a.nsc; ++i) {
+          TTRL_REQUIRE(rs[i]->step, "%s: stage 0: a fused optimizer step without its update count", name);
+          a.sstep[i] = rs[i]->step;
+          a.slr[i] = rs[i]->lr;
+          a.sb1[i] = rs[i]->beta1;
+          a.sb2[i] = rs[i]->beta2;
+          a.seps[i] = rs[i]->eps;
+        }
+        TTRL_REQUIRE(d->adam_scalars, "%s: fused optimizer steps need adam_scalars", name);
+        a.adam_sc = d->adam_scalars;
+      }
+      hipLaunchKernelGGL(k_sac_policy_fwd, dim3(2 * rb + (a.nsc > 0 ? 1 : 0), nq), dim3(kThreads), 0, st, a);
       break;
     case 1:
     case 4:
@@ -1115,6 +1144,8 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
         rc = outer_adam(ctx, r, o.adam, name, stage == 3 ? "critic_adam" : "actor_adam");
         if (!rc) rc = outer_offsets(o, r, name);
         if (rc) return rc;
+        TTRL_REQUIRE(d->adam_scalars, "%s: fused optimizer steps need adam_scalars", name);
+        o.adam.sc = d->adam_scalars + (stage == 3 ? 0 : 2);
         TTRL_REQUIRE(wgs <= kAdamSlotFloats, "%s: %d partial sums exceed a slot", name, wgs);
         o.adam_on = 1;
         if (stage == 3) {
@@ -1127,6 +1158,7 @@ int ttrl_sac_fused_stage(ttrl_ctx* ctx, int stage, const ttrl_sac_fused_desc* d)
           const ttrl_adam_range& ra = d->alpha_adam;
           rc = outer_adam(ctx, ra, o.alpha, name, "alpha_adam");
           if (rc) return rc;
+          o.alpha.sc = d->adam_scalars + 4;
           TTRL_REQUIRE(ra.slot != r.slot, "%s: the temperature and the policy share slot %d", name, r.slot);
           const long off = d->g_log_alpha ? long(d->g_log_alpha - ra.g) : -1;
           TTRL_REQUIRE(off >= 0 && off < ra.n, "%s: g_log_alpha lies outside the temperature's arena", name);

@@ -191,7 +191,8 @@ class SacFusedDesc(C.Structure):
                 + [(n, C.c_void_p) for n in SAC_FUSED_BUFFERS + SAC_FUSED_METRICS + SAC_FUSED_POLICY_GRADS]
                 + [("g_critic", (C.c_void_p * 6) * 2), ("g_log_alpha", C.c_void_p)]
                 + [("fuse_adam", C.c_int), ("critic_adam", AdamRange), ("actor_adam", AdamRange),
-                   ("alpha_adam", AdamRange), ("polyak_dst", C.c_void_p), ("tau", C.c_float)])
+                   ("alpha_adam", AdamRange), ("polyak_dst", C.c_void_p), ("tau", C.c_float),
+                   ("adam_scalars", C.c_void_p)])
 
 
 class ConvGeom(C.Structure):

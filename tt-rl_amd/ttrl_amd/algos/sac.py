@@ -486,7 +486,7 @@ class _FusedUpdate:
                   "act": (2 * B, A), "u": (2 * B, A), "q1": (4, B, H), "q2": (4, B, H), "qp": (4, nq, B),
                   "q1pi": (2, B, H), "q2pi": (2, B, H), "qppi": (2, nq, B), "dQ": (2, B), "dq2": (2, B, H),
                   "dq1": (2, B, H), "dap": (2, nq, B, A), "dhead": (B, 2 * A), "dh2": (B, H), "dh1": (B, H),
-                  "terms": (4, B)}
+                  "terms": (4, B), "adam_scalars": (6,)}
         self.buf = {k: DeviceArray(dev, v) for k, v in shapes.items()}
         self._nparts: dict = {}
 
@@ -576,6 +576,7 @@ class _FusedUpdate:
         if cfg.learn_alpha:
             d.alpha_adam = L.alpha_opt.fused_range(2)
         d.polyak_dst, d.tau = L.nets.targets.arena.data.ptr, cfg.tau
+        d.adam_scalars = buf["adam_scalars"].ptr
         return d
 
     def _parts(self, d, stage: int) -> int:
