@@ -558,12 +558,10 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
       // a tile (kTileOuts float4s per thread, both slices staged) or a bias block
       const TileSpot t = tile_spot(s, blk - s.block0);
       const int nout = t.weight ? kTileOuts : 1;
-      // the operand slices' loads first, the scalars formed while they are in
-      // flight, then the parameters' and moments' loads under the slices' LDS
-      // writes and the sums
+      // the operand slices' loads first, then the parameters' and moments',
+      // all in flight while the scalars are formed
       OuterTileLoads tl;
       if (t.weight) tl = issue_outer_tile(s, t.r0, t.c0);
-      adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
       long i[kTileOuts];
       f32x4 pv[kTileOuts] = {}, sv[kTileOuts] = {}, vv[kTileOuts] = {};
 #pragma unroll
@@ -575,6 +573,7 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
           vv[o] = Vv[i[o]];
         }
       }
+      adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
       if (t.weight) commit_outer_tile(tl, us, vs);
       f32x4 gv[kTileOuts];
       if (t.weight) {
