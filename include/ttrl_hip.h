@@ -106,6 +106,15 @@ int ttrl_capture_end(ttrl_ctx* ctx, ttrl_graph** out);
 /* Leave capture after a failure (ttrl/engine/trace.py:39-53). */
 int ttrl_capture_abort(ttrl_ctx* ctx);
 int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g);
+/* No counterpart in the reference (its traces replay on the device's command
+ * queue): with on nonzero, every later replay of g (ttrl_graph_launch,
+ * ttrl_graph_launch_n, ttrl_graph_step) launches the graph's kernels one by
+ * one in dependency order on the context's stream, with the arguments they
+ * were captured with, instead of one graph launch.  Same kernels, same
+ * results; for a small graph replayed once per host step (an acting step),
+ * where a graph launch's fixed cost exceeds the launches.  TTRL_EINVAL for a
+ * graph with nodes other than kernels. */
+int ttrl_graph_set_direct(ttrl_graph* g, int on);
 int ttrl_graph_launch_n(ttrl_ctx* ctx, ttrl_graph* g, int n);
 /* One acting step as one host call: copy in_bytes of host memory into the
  * bound device block in_dev, replay g (skipped when NULL), copy out_bytes of

@@ -318,3 +318,56 @@ def test_sac_act_matches_oracle(device):
         assert _rel(out["logp"], lp_ref) < 1e-4
     finally:
         learner.close()
+
+
+def test_direct_replay_gives_the_graph_launch_bits(device):
+    """An acting step replayed as direct launches of its kernels
+    (ttrl_graph_set_direct, the ActingNet default) gives the same bits as
+    the same captured graph launched whole, for a greedy Nature-CNN step and
+    a squashed-Gaussian step; a graph with a node other than a kernel is
+    refused."""
+    from ttrl_amd.engine.tensor import DeviceArray
+    from ttrl_amd.engine.trace import capture
+    from ttrl_amd.nets.acting import ActingNet, GreedyDecision
+    from ttrl_amd.spaces import ObsSpec
+
+    learner, _, _ = build_learner(device, seed=6, batch=8)
+    acting = ActingNet(learner.online, ObsSpec.image((4, 84, 84)), device, width=8, lanes=3,
+                       decision=GreedyDecision())
+    try:
+        for lanes, seed in ((3, 11), (8, 12)):
+            frames = _frames(lanes, seed)
+            direct = acting.decide(frames)
+            w = acting._view(lanes)
+            for g in w.graphs.values():
+                g.set_direct(False)
+            whole = acting.decide(frames)
+            for g in w.graphs.values():
+                g.set_direct(True)
+            assert np.array_equal(direct["q"], whole["q"]) and np.array_equal(direct["actions"], whole["actions"])
+    finally:
+        acting.close()
+        learner.close()
+
+    sac, _, _ = build_sac(device, seed=9, batch=32)
+    try:
+        obs = np.random.default_rng(90).standard_normal((5, 11)).astype(np.float32)
+        noise = np.random.default_rng(91).standard_normal((5, 3))
+        direct = sac._acting.decide(obs, noise=noise)
+        w = sac._acting._view(5)
+        for g in w.graphs.values():
+            g.set_direct(False)
+        whole = sac._acting.decide(obs, noise=noise)
+        for k in direct:
+            assert np.array_equal(direct[k], whole[k]), k
+    finally:
+        sac.close()
+
+    a = DeviceArray(device, (64,))
+    b = DeviceArray(device, (64,))
+    trace, _ = capture(device, lambda: b.copy_from(a))  # a copy node, not a kernel
+    try:
+        with pytest.raises(ValueError, match="nodes other than kernels"):
+            trace.set_direct(True)
+    finally:
+        trace.close()

@@ -76,10 +76,23 @@ struct ttrl_ctx {
   std::vector<void*> host_frees_after_capture;
 };
 
+// One kernel node of a captured graph, as a direct launch.
+struct DirectLaunch {
+  const void* func;
+  dim3 grid, block;
+  unsigned shmem;
+  void** args;  // owned by the graph's node, valid while the graph lives
+};
+
 struct ttrl_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   size_t nodes = 0;
+  // The graph's kernels in dependency order, when every node is a kernel
+  // (ttrl_graph_set_direct replays them as individual launches).
+  std::vector<DirectLaunch> kernels;
+  bool direct_ok = false;
+  bool direct = false;
 };
 
 namespace ttrl {
@@ -121,7 +134,7 @@ void ctx_plan_store(ttrl_ctx* ctx, const std::string& key, const GemmPlan& p) { 
 
 float* ctx_tune_sink(ttrl_ctx* ctx, size_t bytes) {
   if (bytes > ctx->tune_bytes) {
-    if (ctx->tune_out) hipFree(ctx->tune_out);
+    if (ctx->tune_out) (void)hipFree(ctx->tune_out);
     ctx->tune_out = nullptr;
     ctx->tune_bytes = 0;
     if (hipMalloc(&ctx->tune_out, bytes) != hipSuccess) return nullptr;
@@ -490,6 +503,67 @@ int ttrl_d2d(ttrl_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 // --------------------------------------------------------------- graphs ---
 
+}  // extern "C"
+
+namespace {
+
+// Records g's kernel nodes in dependency order (Kahn's order over the
+// node dependencies); leaves g->direct_ok false when a node is not a kernel
+// or a query fails.
+void record_kernels(ttrl_graph* g) {
+  size_t n = 0;
+  if (hipGraphGetNodes(g->graph, nullptr, &n) != hipSuccess || n == 0) return;
+  std::vector<hipGraphNode_t> nodes(n);
+  if (hipGraphGetNodes(g->graph, nodes.data(), &n) != hipSuccess) return;
+  std::unordered_map<hipGraphNode_t, size_t> index;
+  for (size_t i = 0; i < n; ++i) index[nodes[i]] = i;
+  std::vector<int> pending(n, 0);
+  std::vector<std::vector<size_t>> next(n);
+  for (size_t i = 0; i < n; ++i) {
+    size_t nd = 0;
+    if (hipGraphNodeGetDependencies(nodes[i], nullptr, &nd) != hipSuccess) return;
+    std::vector<hipGraphNode_t> deps(nd);
+    if (nd && hipGraphNodeGetDependencies(nodes[i], deps.data(), &nd) != hipSuccess) return;
+    for (hipGraphNode_t d : deps) {
+      auto it = index.find(d);
+      if (it == index.end()) return;
+      next[it->second].push_back(i);
+      ++pending[i];
+    }
+  }
+  std::vector<size_t> order;
+  for (size_t i = 0; i < n; ++i)
+    if (pending[i] == 0) order.push_back(i);
+  for (size_t h = 0; h < order.size(); ++h)
+    for (size_t j : next[order[h]])
+      if (--pending[j] == 0) order.push_back(j);
+  if (order.size() != n) return;
+  std::vector<DirectLaunch> ks;
+  for (size_t i : order) {
+    hipGraphNodeType type;
+    if (hipGraphNodeGetType(nodes[i], &type) != hipSuccess || type != hipGraphNodeTypeKernel) return;
+    hipKernelNodeParams kp{};
+    if (hipGraphKernelNodeGetParams(nodes[i], &kp) != hipSuccess || kp.extra || !kp.func) return;
+    ks.push_back(DirectLaunch{kp.func, kp.gridDim, kp.blockDim, kp.sharedMemBytes, kp.kernelParams});
+  }
+  g->kernels = std::move(ks);
+  g->direct_ok = true;
+}
+
+// One replay of g on `stream`: the graph launch, or its kernels one by one.
+hipError_t replay(ttrl_graph* g, hipStream_t stream) {
+  if (!g->direct) return hipGraphLaunch(g->exec, stream);
+  for (const DirectLaunch& k : g->kernels) {
+    const hipError_t e = hipLaunchKernel(k.func, k.grid, k.block, k.args, k.shmem, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
 int ttrl_capture_begin(ttrl_ctx* ctx) {
   if (!ctx) return set_error(TTRL_EINVAL, "ttrl_capture_begin: null ctx");
   if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_capture_begin: already capturing");
@@ -521,6 +595,7 @@ int ttrl_capture_end(ttrl_ctx* ctx, ttrl_graph** out) {
   g->exec = exec;
   size_t n = 0;
   if (hipGraphGetNodes(graph, nullptr, &n) == hipSuccess) g->nodes = n;
+  record_kernels(g);
   *out = g;
   return TTRL_OK;
 }
@@ -540,8 +615,17 @@ int ttrl_capture_abort(ttrl_ctx* ctx) {
 int ttrl_graph_launch(ttrl_ctx* ctx, ttrl_graph* g) {
   if (!ctx || !g || !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_launch: null argument");
   if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_launch: the stream is capturing");
-  hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
-  if (e != hipSuccess) return hip_error(e, "hipGraphLaunch");
+  hipError_t e = replay(g, ctx->stream);
+  if (e != hipSuccess) return hip_error(e, g->direct ? "hipLaunchKernel (direct replay)" : "hipGraphLaunch");
+  return TTRL_OK;
+}
+
+int ttrl_graph_set_direct(ttrl_graph* g, int on) {
+  if (!g || !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_set_direct: null or destroyed graph");
+  if (on && !g->direct_ok)
+    return set_error(TTRL_EINVAL, "ttrl_graph_set_direct: the graph has nodes other than kernels (or none); "
+                                  "only a graph of kernels replays as direct launches");
+  g->direct = on != 0;
   return TTRL_OK;
 }
 
@@ -644,8 +728,8 @@ int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_h
       if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (graph step)");
     }
     if (g) {
-      e = hipGraphLaunch(g->exec, ctx->stream);
-      if (e != hipSuccess) return hip_error(e, "hipGraphLaunch (graph step)");
+      e = replay(g, ctx->stream);
+      if (e != hipSuccess) return hip_error(e, "replay (graph step)");
     }
     if (out_bytes) {
       e = hipMemcpyAsync(out_host, out_dev, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
@@ -674,8 +758,8 @@ int ttrl_graph_step(ttrl_ctx* ctx, ttrl_graph* g, void* in_dev, const void* in_h
     if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync H2D (graph step)");
   }
   if (g) {
-    e = hipGraphLaunch(g->exec, ctx->stream);
-    if (e != hipSuccess) return hip_error(e, "hipGraphLaunch (graph step)");
+    e = replay(g, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, "replay (graph step)");
   }
   if (out_bytes) {
     e = hipMemcpyAsync(ctx->pinned + out_at, out_dev, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
@@ -691,8 +775,8 @@ int ttrl_graph_launch_n(ttrl_ctx* ctx, ttrl_graph* g, int n) {
   if (!ctx || !g || !g->exec) return set_error(TTRL_EINVAL, "ttrl_graph_launch_n: null argument");
   if (ctx->capturing) return set_error(TTRL_ESTATE, "ttrl_graph_launch_n: the stream is capturing");
   for (int i = 0; i < n; ++i) {
-    hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
-    if (e != hipSuccess) return hip_error(e, "hipGraphLaunch");
+    hipError_t e = replay(g, ctx->stream);
+    if (e != hipSuccess) return hip_error(e, g->direct ? "hipLaunchKernel (direct replay)" : "hipGraphLaunch");
   }
   return TTRL_OK;
 }

@@ -50,6 +50,13 @@ class CapturedTrace:
         if blocking:
             self.device.synchronize()
 
+    def set_direct(self, on: bool = True) -> None:
+        """Replay the graph's kernels as individual launches (ttrl_graph_set_direct):
+        cheaper than one graph launch for a few kernels replayed once per host step."""
+        if self._graph is None:
+            raise RuntimeError("set_direct() on a closed CapturedTrace")
+        _lib.check(_lib.lib().ttrl_graph_set_direct(self._graph, int(bool(on))), "ttrl_graph_set_direct")
+
     def replay_n(self, n: int) -> None:
         if self._graph is None:
             raise RuntimeError("replay_n() on a closed CapturedTrace")

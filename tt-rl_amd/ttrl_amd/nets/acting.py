@@ -249,10 +249,15 @@ class ActingNet:
 
     `width` is the batch the net was built for and the widest call accepted.
     `decision` (GreedyDecision / SquashedDecision, or None) enables
-    `decide`; `mode` is "graph" (captured acting step) or "eager".
+    `decide`; `mode` is "graph" (captured acting step) or "eager".  With
+    `direct` (the default) a captured step replays its few kernels as
+    individual launches (`CapturedTrace.set_direct`): one step waits for its
+    result, and a graph launch's fixed cost exceeds the launches of a handful
+    of kernels.
     """
 
-    def __init__(self, net, obs_spec, device, *, width: int, lanes: int, decision=None, mode: str = "graph"):
+    def __init__(self, net, obs_spec, device, *, width: int, lanes: int, decision=None, mode: str = "graph",
+                 direct: bool = True):
         if mode not in MODES:
             raise ValueError(f"ActingNet mode must be one of {list(MODES)}, got {mode!r}")
         check_encoder_layout(net)
@@ -261,6 +266,7 @@ class ActingNet:
         self.width = int(width)
         self.decision = decision
         self.mode = mode
+        self.direct = bool(direct)
         self._net = net
         self._views: dict[int, _Width] = {}
         self._view(int(lanes))
@@ -330,6 +336,8 @@ class ActingNet:
                 self._body(w, deterministic)  # warm-up: tunes plans and fills the pool's free lists
                 dev.synchronize()
                 g, _ = capture(dev, lambda: self._body(w, deterministic))
+            if self.direct:
+                g.set_direct(True)
             w.graphs[deterministic] = g
         return g
 
