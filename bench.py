@@ -528,11 +528,13 @@ def pcie_inclusive(dev, learner, n=100):
 
 def bench_act(dev, dqn, sac, steps=500, lanes_dqn=(1, 8, 16, 32), lanes_sac=(1, 16, 256)):
     """Acting steps/s of the learners' acting networks: one step = host
-    observations (pageable numpy) -> device -> captured forward + fused
-    head-and-decision kernel -> actions back on the host (DQN: greedy
-    actions before the host epsilon draw; SAC: squashed-Gaussian actions at
+    observations (pageable numpy) staged into the step's mapped input block,
+    the captured forward + fused head-and-decision kernel launched directly,
+    the decisions read from its mapped output block (DQN: greedy actions
+    before the host epsilon draw; SAC: squashed-Gaussian actions at
     host-drawn noise).  At 32 lanes the DQN step is the batch-32 Q-network
-    forward of the deploy path, plus the upload and the action read."""
+    forward of the deploy path, plus the observations' staging and the
+    decisions' read."""
     out = {"dqn": [], "sac": []}
     rng = np.random.default_rng(17)
     for lanes in lanes_dqn:
@@ -545,15 +547,25 @@ def bench_act(dev, dqn, sac, steps=500, lanes_dqn=(1, 8, 16, 32), lanes_sac=(1, 
         dt = time.perf_counter() - t0
         out["dqn"].append({"lanes": lanes, "steps_per_s": round(steps / dt, 1), "us_per_step": round(dt / steps * 1e6, 2)})
     # Config 1 on the GPU: the batch-32 Q-network forward with its frames
-    # resident in HBM (the acting graph at 32 lanes replayed back to back,
-    # no host copies): forwards/s against the FP32 MFMA roofline.
-    fw = dqn._acting._views[32].graphs[False]
-    fw.replay_n(50)
-    dev.synchronize()
-    t0 = time.perf_counter()
-    fw.replay_n(steps * 4)
-    dev.synchronize()
-    dt = (time.perf_counter() - t0) / (steps * 4)
+    # resident in HBM (an acting graph at 32 lanes over device blocks,
+    # replayed back to back, no host copies): forwards/s against the FP32
+    # MFMA roofline.  The learner's own acting net keeps its blocks in mapped
+    # host memory, which a step reads once; replayed back to back it would
+    # read the frames over PCIe every time.
+    from ttrl_amd.nets.acting import ActingNet, GreedyDecision
+
+    resident = ActingNet(dqn.online, dqn.obs_spec, dev, width=32, lanes=32, decision=GreedyDecision(), mapped=False)
+    try:
+        resident.decide(rng.integers(0, 256, (32, 4, 84, 84), dtype=np.uint8))  # captures
+        fw = resident._views[32].graphs[False]
+        fw.replay_n(50)
+        dev.synchronize()
+        t0 = time.perf_counter()
+        fw.replay_n(steps * 4)
+        dev.synchronize()
+        dt = (time.perf_counter() - t0) / (steps * 4)
+    finally:
+        resident.close()
     flops = 2.0 * 32 * sum(NATURE_MACS)
     out["dqn_forward_bs32"] = {"forwards_per_s": round(1.0 / dt, 1), "us_per_forward": round(dt * 1e6, 2),
                                "flops": flops, "roofline_frac": flops / dt / PEAK_FP32_MFMA}

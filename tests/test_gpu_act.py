@@ -324,8 +324,10 @@ def test_direct_replay_gives_the_graph_launch_bits(device):
     """An acting step replayed as direct launches of its kernels
     (ttrl_graph_set_direct, the ActingNet default) gives the same bits as
     the same captured graph launched whole, for a greedy Nature-CNN step and
-    a squashed-Gaussian step; a graph with a node other than a kernel is
-    refused."""
+    a squashed-Gaussian step; so does a step whose input and output blocks
+    are device memory with copies either way, against the default's mapped
+    host blocks the kernels read and write in place; a graph with a node
+    other than a kernel is refused."""
     from ttrl_amd.engine.tensor import DeviceArray
     from ttrl_amd.engine.trace import capture
     from ttrl_amd.nets.acting import ActingNet, GreedyDecision
@@ -345,6 +347,15 @@ def test_direct_replay_gives_the_graph_launch_bits(device):
             for g in w.graphs.values():
                 g.set_direct(True)
             assert np.array_equal(direct["q"], whole["q"]) and np.array_equal(direct["actions"], whole["actions"])
+        copied = ActingNet(learner.online, ObsSpec.image((4, 84, 84)), device, width=8, lanes=3,
+                           decision=GreedyDecision(), direct=False, mapped=False)
+        try:
+            for lanes, seed in ((3, 13), (8, 14), (3, 15)):
+                frames = _frames(lanes, seed)
+                a, b = acting.decide(frames), copied.decide(frames)
+                assert np.array_equal(a["q"], b["q"]) and np.array_equal(a["actions"], b["actions"])
+        finally:
+            copied.close()
     finally:
         acting.close()
         learner.close()

@@ -60,8 +60,24 @@ class _Block:
         self.ptr = 0
 
 
+class _MappedBlock:
+    """Pinned host memory that kernels read and write in place, as a block of
+    DeviceArray views: kernels address it at `ptr` (its device address), the
+    host through `host.array` (a uint8 numpy view).  Frees itself with its
+    last view."""
+
+    __slots__ = ("dev", "ptr", "nbytes", "host", "__weakref__")
+
+    def __init__(self, dev: Device, nbytes: int):
+        self.dev = dev
+        self.host = dev.mapped_block(max(1, int(nbytes)))
+        self.nbytes = self.host.nbytes
+        self.ptr = self.host.dptr
+
+
 class DeviceArray:
-    """A dense, C-contiguous device array (a view into a `_Block`)."""
+    """A dense, C-contiguous device array (a view into a `_Block`, or into a
+    `_MappedBlock` of host memory)."""
 
     __slots__ = ("dev", "block", "offset", "shape", "dtype", "unit")
 
@@ -162,24 +178,31 @@ def zeros(dev: Device, shape, dtype=np.float32) -> DeviceArray:
     return out
 
 
-def bound_block(device: Device, specs):
+def bound_block(device: Device, specs, *, mapped: bool = False):
     """Input buffers laid out back to back in one allocation.
 
     `specs` is a sequence of (name, host_array); each buffer starts on a
     256-byte boundary.  Returns ({name: DeviceArray}, whole block as uint8),
-    so one device copy refreshes every input of a step.
+    so one device copy refreshes every input of a step.  With `mapped` the
+    block is pinned host memory that kernels read and write in place
+    (`_MappedBlock`; its host view is `whole.block.host.array`), so a step
+    needs no copy at all.
     """
     layout, offset = [], 0
     for name, arr in specs:
         arr = np.ascontiguousarray(arr)
         layout.append((name, arr, offset))
         offset += int(math.ceil(max(arr.nbytes, 1) / 256.0)) * 256
-    block = _Block(device, max(offset, 256))
-    whole = DeviceArray(device, (max(offset, 256),), np.uint8, block=block)
+    size = max(offset, 256)
+    block = _MappedBlock(device, size) if mapped else _Block(device, size)
+    whole = DeviceArray(device, (size,), np.uint8, block=block)
     out = {}
     for name, arr, off in layout:
         view = DeviceArray(device, arr.shape, arr.dtype, block=block, offset=off)
-        view.upload(arr)
+        if mapped:
+            block.host.array[off:off + arr.nbytes] = arr.reshape(-1).view(np.uint8)
+        else:
+            view.upload(arr)
         out[name] = view
     return out, whole
 

@@ -209,12 +209,20 @@ class _Width:
             host_obs = np.zeros((lanes, spec.size), np.float32)
         dec = acting.decision
         ins = [("obs", host_obs)] + (dec.inputs(self.net, lanes) if dec is not None else [])
-        self.ins, self.in_block = bound_block(dev, ins)
+        # mapped: the blocks are pinned host memory the kernels read and write
+        # in place, and in_host / out_host are their host views
+        self.mapped = acting.mapped
+        self.ins, self.in_block = bound_block(dev, ins, mapped=self.mapped)
         self.obs = Tensor(self.ins["obs"])
-        self.outs, self.out_block = (bound_block(dev, dec.outputs(self.net, lanes)) if dec is not None
-                                     else ({}, None))
-        self.in_host = np.zeros(self.in_block.nbytes, np.uint8)
-        self.out_host = np.zeros(self.out_block.nbytes if self.out_block is not None else 0, np.uint8)
+        self.outs, self.out_block = (bound_block(dev, dec.outputs(self.net, lanes), mapped=self.mapped)
+                                     if dec is not None else ({}, None))
+        if self.mapped:
+            self.in_host = self.in_block.block.host.array[:self.in_block.nbytes]
+            self.out_host = (self.out_block.block.host.array[:self.out_block.nbytes] if self.out_block is not None
+                             else np.zeros(0, np.uint8))
+        else:
+            self.in_host = np.zeros(self.in_block.nbytes, np.uint8)
+            self.out_host = np.zeros(self.out_block.nbytes if self.out_block is not None else 0, np.uint8)
         self.graphs: dict = {}
         self.pool = None
 
@@ -253,11 +261,13 @@ class ActingNet:
     `direct` (the default) a captured step replays its few kernels as
     individual launches (`CapturedTrace.set_direct`): one step waits for its
     result, and a graph launch's fixed cost exceeds the launches of a handful
-    of kernels.
+    of kernels.  With `mapped` (the default) the step's input and output
+    blocks are pinned host memory the kernels read and write in place, so a
+    step is the launches and one wait, with no copy either way.
     """
 
     def __init__(self, net, obs_spec, device, *, width: int, lanes: int, decision=None, mode: str = "graph",
-                 direct: bool = True):
+                 direct: bool = True, mapped: bool = True):
         if mode not in MODES:
             raise ValueError(f"ActingNet mode must be one of {list(MODES)}, got {mode!r}")
         check_encoder_layout(net)
@@ -267,6 +277,7 @@ class ActingNet:
         self.decision = decision
         self.mode = mode
         self.direct = bool(direct)
+        self.mapped = bool(mapped)
         self._net = net
         self._views: dict[int, _Width] = {}
         self._view(int(lanes))
@@ -361,7 +372,15 @@ class ActingNet:
         in_ptr, out_ptr = C.c_void_p(w.in_block.ptr), C.c_void_p(w.out_block.ptr)
         host_in = w.in_host.ctypes.data_as(C.c_void_p)
         host_out = w.out_host.ctypes.data_as(C.c_void_p)
-        if self.mode == "graph":
+        if w.mapped:
+            # the kernels read the staged inputs and write the outputs in place
+            if self.mode == "graph":
+                g = self._graph(w, bool(deterministic))
+                _lib.check(lib.ttrl_graph_step(dev.ctx, g._graph, None, None, 0, None, None, 0), "ttrl_graph_step")
+            else:
+                self._body(w, bool(deterministic))
+                dev.synchronize()
+        elif self.mode == "graph":
             g = self._graph(w, bool(deterministic))
             _lib.check(lib.ttrl_graph_step(dev.ctx, g._graph, in_ptr, host_in, w.in_host.nbytes, host_out,
                                            out_ptr, w.out_host.nbytes), "ttrl_graph_step")
