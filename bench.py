@@ -510,6 +510,52 @@ def dominant_kernel(dev, learner, reps=200):
             "store_formed_grads": bool(d.store_grads)}
 
 
+def achievable_peaks(dev, copy_mib=512, reps=10):
+    """The box's achievable rates beside the published peaks: a
+    device-to-device copy of `copy_mib` MiB (bytes read plus bytes written
+    per second, the median of `reps` copies timed one by one with the stream
+    timer) and the FP32 matrix rate of back-to-back v_mfma_f32_16x16x4f32
+    with no memory traffic (ttrl_mfma_rate, two 256-thread workgroups per
+    CU), the median of five launches."""
+    from ttrl_amd.engine.tensor import DeviceArray
+
+    n = copy_mib * (1 << 20) // 4
+    src, dst = DeviceArray(dev, (n,)), DeviceArray(dev, (n,))
+    src.fill(1.0)
+    dst.copy_from(src)
+    dev.synchronize()
+    ms = C.c_float(0.0)
+    copies = []
+    for _ in range(reps):
+        dev.call("ttrl_timer_start")
+        dst.copy_from(src)
+        dev.call("ttrl_timer_stop", C.byref(ms))
+        copies.append(2.0 * n * 4 / (ms.value / 1e3))
+    del src, dst
+    from ttrl_amd.engine.device import probe_profile
+
+    cus = int(probe_profile(dev).compute_units or 256)
+    wgs, iters = 2 * cus, 20000
+    out = DeviceArray(dev, (wgs * 256,))
+    flops = C.c_double(0.0)
+    dev.call("ttrl_mfma_rate", wgs, iters, out.vp, C.byref(flops))  # warm-up
+    dev.synchronize()
+    rates = []
+    for _ in range(5):
+        dev.call("ttrl_timer_start")
+        dev.call("ttrl_mfma_rate", wgs, iters, out.vp, C.byref(flops))
+        dev.call("ttrl_timer_stop", C.byref(ms))
+        rates.append(flops.value / (ms.value / 1e3))
+    dev.synchronize()
+    hbm, mfma = float(np.median(copies)), float(np.median(rates))
+    return {"hbm_copy_gbps": round(hbm / 1e9, 1), "hbm_published_gbps": PEAK_HBM / 1e9,
+            "hbm_frac_of_published": hbm / PEAK_HBM,
+            "mfma_fp32_tflops": round(mfma / 1e12, 2), "mfma_fp32_published_tflops": PEAK_FP32_MFMA / 1e12,
+            "mfma_frac_of_published": mfma / PEAK_FP32_MFMA,
+            "copy": f"{copy_mib} MiB device-to-device, {reps} copies",
+            "mfma": f"{wgs} workgroups x 256 threads x {iters} rounds of 8 independent v_mfma_f32_16x16x4f32"}
+
+
 def pcie_inclusive(dev, learner, n=100):
     """Updates/s when every update starts from a host batch (numpy arrays in
     pageable memory): the host-to-device copy of the batch is inside the loop."""
@@ -749,6 +795,7 @@ def main() -> int:
     agent = bench_agent(dev, args.agent_steps) if args.agent_steps > 0 and args.mode == "graph" else None
     host_rate = pcie_inclusive(dev, dqn) if args.mode == "graph" else None
     act = bench_act(dev, dqn, sac, args.act_steps) if args.act_steps > 0 and args.mode == "graph" else None
+    peaks = achievable_peaks(dev) if args.mode == "graph" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     if act is not None and cpu is not None:
         act["cpu_deploy_forward"] = [r for r in cpu["runs"] if r["workload"] == "deploy"]
@@ -783,7 +830,10 @@ def main() -> int:
                      "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved / PEAK_HBM,
                      "traffic": traffic, "traffic_source_sha256": digest, "algorithmic_bytes": dom["bytes"],
                      "split_partial_bytes": dom["split_partial_bytes"], "formed_params": dom["formed_params"],
-                     "avg_us": dom["seconds"] * 1e6},
+                     "avg_us": dom["seconds"] * 1e6,
+                     "achievable_peak": None if peaks is None else peaks["hbm_copy_gbps"],
+                     "frac_of_achievable": None if peaks is None else achieved / 1e9 / peaks["hbm_copy_gbps"]},
+        "achievable": peaks,
         "pcie_inclusive": None if host_rate is None else {
             "value": round(host_rate, 2), "unit": "DQN updates/s",
             "note": "each update loads a host numpy batch (pageable) through the learner's update(batch)"},

@@ -158,6 +158,13 @@ int ttrl_plans_import(ttrl_ctx* ctx, const char* text, int* count);
 /* Stream timer (events on the context's stream). */
 int ttrl_timer_start(ttrl_ctx* ctx);
 int ttrl_timer_stop(ttrl_ctx* ctx, float* ms);
+/* No counterpart in the reference (measurement only): `workgroups` x 256
+ * threads issuing `iters` rounds of eight independent
+ * v_mfma_f32_16x16x4f32 each, no memory traffic in the loop; each thread's
+ * sum goes to out[workgroups * 256]; *flops receives the launch's FP32
+ * matrix FLOPs.  Timed with the stream timer, it gives the achievable FP32
+ * MFMA rate beside the published peak. */
+int ttrl_mfma_rate(ttrl_ctx* ctx, int workgroups, int iters, float* out, double* flops);
 
 /* ------------------------------------------------------ dense layers --- */
 

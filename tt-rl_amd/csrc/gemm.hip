@@ -208,11 +208,39 @@ const float* relu_mask_into_workspace(ttrl_ctx* ctx, const float* src, const flo
   return dst;
 }
 
+// Back-to-back v_mfma_f32_16x16x4f32 on eight independent accumulators per
+// wavefront (no memory traffic inside the loop), for the achievable FP32
+// matrix rate; each lane's sum is stored so the work is kept.
+constexpr int kRateChains = 8;
+__global__ __launch_bounds__(256) void k_mfma_rate(int iters, float* __restrict__ out) {
+  f32x4 acc[kRateChains];
+#pragma unroll
+  for (int j = 0; j < kRateChains; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float a = float(threadIdx.x & 63) * (1.f / 64.f), b = 1.f / 1024.f;
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int j = 0; j < kRateChains; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[j], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRateChains; ++j) s += (acc[j][0] + acc[j][1]) + (acc[j][2] + acc[j][3]);
+  out[long(blockIdx.x) * blockDim.x + threadIdx.x] = s;
+}
+
 }  // namespace ttrl
 
 using namespace ttrl;
 
 extern "C" {
+
+int ttrl_mfma_rate(ttrl_ctx* ctx, int workgroups, int iters, float* out, double* flops) {
+  TTRL_REQUIRE(ctx && out && flops, "ttrl_mfma_rate: null argument");
+  TTRL_REQUIRE(workgroups > 0 && workgroups <= 65536 && iters > 0 && iters <= (1 << 24),
+               "ttrl_mfma_rate: %d workgroups of %d iterations outside [1, 65536] x [1, 2^24]", workgroups, iters);
+  hipLaunchKernelGGL(k_mfma_rate, dim3(unsigned(workgroups)), dim3(256), 0, stream_of(ctx), iters, out);
+  *flops = double(workgroups) * 4.0 * double(iters) * kRateChains * 2.0 * 16 * 16 * 4;
+  return check_launch("ttrl_mfma_rate");
+}
 
 int ttrl_matmul(ttrl_ctx* ctx, int M, int N, int K, const float* A, long lda, int ta, const float* B, long ldb,
                 int tb, float* C, long ldc, float alpha, float beta) {

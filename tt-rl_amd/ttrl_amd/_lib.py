@@ -235,6 +235,7 @@ SIGNATURES = {
     "ttrl_capture_abort": ([P], I),
     "ttrl_graph_launch": ([P, P], I),
     "ttrl_graph_set_direct": ([P, I], I),
+    "ttrl_mfma_rate": ([P, I, I, P, C.POINTER(C.c_double)], I),
     "ttrl_graph_launch_n": ([P, P, I], I),
     "ttrl_graph_step": ([P, P, P, P, SZ, P, P, SZ], I),
     "ttrl_host_alloc": ([P, SZ, C.POINTER(P)], I),
