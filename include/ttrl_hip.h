@@ -771,6 +771,26 @@ int ttrl_gru_mask(ttrl_ctx* ctx, int B, int H, const float* h, const float* done
 int ttrl_gru_step_backward(ttrl_ctx* ctx, int B, int H, const float* gi, const float* gh, const float* hin,
                            const float* dout, const float* dhin_next, const float* done_next, float* dgi, float* dgh,
                            float* dhin);
+/* ttrl_gru_step with its recurrent product in the same launch: gh = hin W_hh
+ * + b_hh (W_hh [H][3H], b_hh [3H]) is formed, written to gh and used for the
+ * cell (GRUCell.forward, ttrl/engine/recurrent.py:86-94).  H a multiple of
+ * 16 (<= 8192); hin and W_hh 16-byte aligned. */
+int ttrl_gru_step_fused(ttrl_ctx* ctx, int B, int H, const float* gi, const float* hin, const float* W_hh,
+                        const float* b_hh, float* gh, float* hout, const float* done_next, float* hin_next);
+/* One step of the GRU's reverse walk in one launch (the backward of
+ * ttrl/engine/recurrent.py:88-168 through step t): d hin_t = dhz + dgh
+ * W_hh^T, where dhz = z_t * dh_t is the direct part ttrl_gru_step_backward
+ * or the previous call left; written to dhin when given.  With gi_prev,
+ * also the cell backward of step t - 1 for dh_{t-1} = dout_prev + (1 - done)
+ * d hin_t (dout_prev, done [B] nullable; done is done_t): its gate gradients
+ * dgi_prev, dgh_prev and its direct part dhz_prev, the input of the next
+ * call.  gh_prev, hin_prev, dgi_prev, dgh_prev and dhz_prev come with
+ * gi_prev or not at all.  H a multiple of 16 (<= 8192); dgh and W_hh
+ * 16-byte aligned. */
+int ttrl_gru_step_backward_fused(ttrl_ctx* ctx, int B, int H, const float* dgh, const float* W_hh, const float* dhz,
+                                 float* dhin, const float* gi_prev, const float* gh_prev, const float* hin_prev,
+                                 const float* dout_prev, const float* done, float* dgi_prev, float* dgh_prev,
+                                 float* dhz_prev);
 
 /* ---- GPU-resident replay -------------------------------------------------- */
 

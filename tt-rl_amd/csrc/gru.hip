@@ -13,7 +13,21 @@
 // gi, gh and hin (the same expressions, so the same values) and writes the
 // gate gradients d gi, d gh for the batched weight-gradient GEMMs and the
 // direct part z * dh of d hin_t, to which a GEMM adds d gh W_hh^T.
+//
+// Fused steps (H a multiple of 16): the recurrent product and the cell
+// arithmetic of a timestep in one launch.  Forward, gh_t = hin_t W_hh + b_hh
+// and the cell; backward, d hin_t = z_t dh_t + d gh_t W_hh^T and then the
+// cell backward of step t - 1, whose dh_{t-1} = dout_{t-1} + (1 - done_t)
+// d hin_t needs only this workgroup's units.  A workgroup owns 16 hidden
+// units (the gate columns u, H + u, 2H + u of each) and 16 batch rows; its
+// kFw wavefronts split the product's reduction into groups of 16 (wavefront
+// w takes groups w, w + kFw, ...) and their 16 x 16 partial tiles are summed
+// in wavefront order through LDS, so every output has one fixed summation
+// order.  In group q a lane (column c = lane % 16, quarter g = lane / 16)
+// feeds k = 16q + 4g + j to MFMA j (j = 0..3): the operand that runs along
+// k in memory is one float4 per lane.
 #include "common.hpp"
+#include "tile_gemm.hpp"
 
 #include <cmath>
 
@@ -25,6 +39,33 @@ constexpr int kGruThreads = 256;
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 
 __device__ __forceinline__ float keep_f(const float* done, int b) { return done ? 1.f - done[b] : 1.f; }
+
+// h' = (1 - z) * n + z * h from the two projections' gate pre-activations.
+__device__ __forceinline__ float cell_forward(float xr, float xz, float xn, float hr, float hz, float hn, float h) {
+  const float r = sigmoid_f(xr + hr);
+  const float z = sigmoid_f(xz + hz);
+  const float c = tanhf(xn + r * hn);
+  return (1.f - z) * c + z * h;
+}
+
+// The cell's backward for dh = d h': the gate gradients (d gi = [r, z, n],
+// d gh = [r, z, hn]) and the direct part z * dh of d h.
+struct CellGrad {
+  float r, z, n, hn, hz;
+};
+__device__ __forceinline__ CellGrad cell_backward(float xr, float xz, float xn, float hr, float hz, float hn, float h,
+                                                  float dh) {
+  const float r = sigmoid_f(xr + hr);
+  const float z = sigmoid_f(xz + hz);
+  const float c = tanhf(xn + r * hn);
+  const float dc = dh * (1.f - z);
+  const float dz = dh * (h - c);
+  const float dcp = dc * (1.f - c * c);
+  const float dr = dcp * hn;
+  const float drp = dr * (r * (1.f - r));
+  const float dzp = dz * (z * (1.f - z));
+  return CellGrad{drp, dzp, dcp, dcp * r, dh * z};
+}
 
 __global__ __launch_bounds__(kGruThreads) void k_gru_mask(int B, int H, const float* __restrict__ h,
                                                           const float* __restrict__ done, float* __restrict__ out) {
@@ -45,11 +86,7 @@ __global__ __launch_bounds__(kGruThreads) void k_gru_step(int B, int H, const fl
     const int b = int(i / H), j = int(i - long(b) * H);
     const float* gib = gi + long(b) * 3 * H;
     const float* ghb = gh + long(b) * 3 * H;
-    const float r = sigmoid_f(gib[j] + ghb[j]);
-    const float z = sigmoid_f(gib[H + j] + ghb[H + j]);
-    const float c = tanhf(gib[2 * H + j] + r * ghb[2 * H + j]);
-    const float h = hin[i];
-    const float out = (1.f - z) * c + z * h;
+    const float out = cell_forward(gib[j], gib[H + j], gib[2 * H + j], ghb[j], ghb[H + j], ghb[2 * H + j], hin[i]);
     hout[i] = out;
     if (hin_next) hin_next[i] = out * keep_f(done_next, b);
   }
@@ -69,29 +106,204 @@ __global__ __launch_bounds__(kGruThreads) void k_gru_step_bwd(int B, int H, cons
     const int b = int(i / H), j = int(i - long(b) * H);
     const float* gib = gi + long(b) * 3 * H;
     const float* ghb = gh + long(b) * 3 * H;
-    const float r = sigmoid_f(gib[j] + ghb[j]);
-    const float z = sigmoid_f(gib[H + j] + ghb[H + j]);
-    const float hn = ghb[2 * H + j];
-    const float c = tanhf(gib[2 * H + j] + r * hn);
-    const float h = hin[i];
     float dh = dout ? dout[i] : 0.f;
     if (dhin_next) dh += keep_f(done_next, b) * dhin_next[i];
-    const float dc = dh * (1.f - z);
-    const float dz = dh * (h - c);
-    const float dcp = dc * (1.f - c * c);
-    const float dr = dcp * hn;
-    const float drp = dr * (r * (1.f - r));
-    const float dzp = dz * (z * (1.f - z));
+    const CellGrad d =
+        cell_backward(gib[j], gib[H + j], gib[2 * H + j], ghb[j], ghb[H + j], ghb[2 * H + j], hin[i], dh);
     float* dgib = dgi + long(b) * 3 * H;
     float* dghb = dgh + long(b) * 3 * H;
-    dgib[j] = drp;
-    dgib[H + j] = dzp;
-    dgib[2 * H + j] = dcp;
-    dghb[j] = drp;
-    dghb[H + j] = dzp;
-    dghb[2 * H + j] = dcp * r;
-    dhin[i] = dh * z;
+    dgib[j] = d.r;
+    dgib[H + j] = d.z;
+    dgib[2 * H + j] = d.n;
+    dghb[j] = d.r;
+    dghb[H + j] = d.z;
+    dghb[2 * H + j] = d.hn;
+    dhin[i] = d.hz;
   }
+}
+
+constexpr int kFw = 8;  // wavefronts of a fused-step workgroup
+constexpr int kFt = 64 * kFw;
+constexpr int kFwdChunk = 4;   // forward: groups in flight per wavefront (13 loads each)
+constexpr int kBwdChunk = 12;  // backward: groups in flight per wavefront (2 float4 loads each)
+
+__device__ __forceinline__ float ldb1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ f32x4 ldb4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ f32x4 mfma4(f32x4 a, f32x4 b, f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+}
+
+struct GruFwdArgs {
+  int B, H;
+  const float* gi;         // [B][3H]  x_t W_ih + b_ih
+  const float* hin;        // [B][H]   state entering the step
+  const float* W;          // [H][3H]  W_hh
+  const float* bias;       // [3H]     b_hh
+  float* gh;               // [B][3H]  out: hin W_hh + b_hh
+  float* hout;             // [B][H]   out: h_t
+  const float* done_next;  // [B] or null
+  float* hin_next;         // [B][H] or null: h_t * (1 - done_next)
+};
+
+__global__ __launch_bounds__(kFt) void k_gru_fwd_fused(GruFwdArgs a) {
+  __shared__ float part[kFw * 3 * 256];
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int B = a.B, H = a.H, G = 3 * H;
+  const int u0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
+  // The output element of threads 0..255 (row r0 + tid / 16, unit u0 + tid %
+  // 16); the other threads load the same operands and store nothing.  The
+  // loads are unconditional so that none of them waits before the product's.
+  const bool ep = tid < 256;  // whole wavefronts
+  const int er = r0 + ((tid >> 4) & 15), eu = u0 + (tid & 15), erc = min(er, B - 1);
+  const float* gib = a.gi + long(erc) * G;
+  const float xr = gib[eu], xz = gib[H + eu], xn = gib[2 * H + eu];
+  const float br = a.bias[eu], bz = a.bias[H + eu], bn = a.bias[2 * H + eu];
+  const float h = a.hin[long(erc) * H + eu];
+  const float dv = *(a.done_next ? a.done_next + erc : a.bias);
+  const float keep = a.done_next ? 1.f - dv : 1.f;
+  // A: hin[row c][16q + 4g + j] (one float4), B: W[16q + 4g + j][e H + u0 + c].
+  const __amdgpu_buffer_rsrc_t rA = make_res(a.hin, uint32_t(B) * uint32_t(H) * 4u);
+  const __amdgpu_buffer_rsrc_t rB = make_res(a.W, uint32_t(H) * uint32_t(G) * 4u);
+  const uint32_t va = (uint32_t(min(r0 + c, B - 1)) * uint32_t(H) + 4u * g) * 4u;
+  const uint32_t vb = (4u * g * uint32_t(G) + uint32_t(u0 + c)) * 4u;
+  const int nq = H >> 4;
+  f32x4 acc[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int q0 = wave; q0 < nq; q0 += kFwdChunk * kFw) {
+    f32x4 av[kFwdChunk], bv[kFwdChunk][3];
+#pragma unroll
+    for (int s = 0; s < kFwdChunk; ++s) {
+      const uint32_t q = uint32_t(min(q0 + s * kFw, nq - 1));
+      av[s] = ldb4(rA, va, 64u * q);
+#pragma unroll
+      for (int e = 0; e < 3; ++e) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[s][e][j] = ldb1(rB, vb, ((16u * q + j) * uint32_t(G) + e * uint32_t(H)) * 4u);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the chunk issues before the first product
+    // A group past the end (its loads re-read the last group) adds zeros:
+    // every product runs, so no load is deferred behind a branch.
+#pragma unroll
+    for (int s = 0; s < kFwdChunk; ++s) {
+      const f32x4 x = q0 + s * kFw < nq ? av[s] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 3; ++e) acc[e] = mfma4(x, bv[s][e], acc[e]);
+    }
+  }
+  // lane (c, g) holds rows 4g + i of column c
+#pragma unroll
+  for (int e = 0; e < 3; ++e) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[(wave * 3 + e) * 256 + (4 * g + i) * 16 + c] = acc[e][i];
+  }
+  __syncthreads();
+  if (!ep) return;
+  const int t = tid & 255;
+  float s3[3];
+#pragma unroll
+  for (int e = 0; e < 3; ++e) {
+    float v = part[e * 256 + t];
+#pragma unroll
+    for (int w = 1; w < kFw; ++w) v += part[(w * 3 + e) * 256 + t];
+    s3[e] = v;
+  }
+  const float hr = s3[0] + br, hz = s3[1] + bz, hn = s3[2] + bn;
+  if (er >= B) return;
+  const float out = cell_forward(xr, xz, xn, hr, hz, hn, h);
+  float* ghb = a.gh + long(er) * G;
+  ghb[eu] = hr;
+  ghb[H + eu] = hz;
+  ghb[2 * H + eu] = hn;
+  a.hout[long(er) * H + eu] = out;
+  if (a.hin_next) a.hin_next[long(er) * H + eu] = out * keep;
+}
+
+struct GruBwdArgs {
+  int B, H;
+  const float* dgh;  // [B][3H]  d gh_t
+  const float* W;    // [H][3H]  W_hh
+  const float* dhz;  // [B][H]   z_t * dh_t
+  float* dhin;       // [B][H] or null: out d hin_t = dhz + d gh_t W_hh^T
+  // the cell backward of step t - 1 (gi null: none)
+  const float *gi, *gh, *hin;  // step t - 1's [B][3H], [B][3H], [B][H]
+  const float* dout;           // [B][H] or null: d out_{t-1}
+  const float* done;           // [B] or null: done_t, the reset between the steps
+  float *dgi, *dgh_prev;       // [B][3H] out
+  float* dhz_prev;             // [B][H]  out: z_{t-1} * dh_{t-1}
+};
+
+__global__ __launch_bounds__(kFt) void k_gru_bwd_fused(GruBwdArgs a) {
+  __shared__ float part[kFw * 256];
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int B = a.B, H = a.H, G = 3 * H;
+  const int u0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
+  const bool ep = tid < 256;
+  const int er = r0 + ((tid >> 4) & 15), eu = u0 + (tid & 15), erc = min(er, B - 1);
+  const bool cell = a.gi != nullptr;
+  // Unconditional loads (see k_gru_fwd_fused); an absent operand reads a
+  // buffer of the same shape and is not used.
+  const long eh = long(erc) * H + eu;
+  const float dz0 = a.dhz[eh];
+  const float* gib = (cell ? a.gi : a.dgh) + long(erc) * G;
+  const float* ghb = (cell ? a.gh : a.dgh) + long(erc) * G;
+  const float xr = gib[eu], xz = gib[H + eu], xn = gib[2 * H + eu];
+  const float hr = ghb[eu], hz = ghb[H + eu], hn = ghb[2 * H + eu];
+  const float h = (cell ? a.hin : a.dhz)[eh];
+  const float ov = (a.dout ? a.dout : a.dhz)[eh];
+  const float dv = *(a.done ? a.done + erc : a.dhz);
+  const float dout = a.dout ? ov : 0.f;
+  const float keep = a.done ? 1.f - dv : 1.f;
+  // A: d gh[row c][16q + 4g + j], B: W[u0 + c][16q + 4g + j]; one float4 each.
+  const __amdgpu_buffer_rsrc_t rA = make_res(a.dgh, uint32_t(B) * uint32_t(G) * 4u);
+  const __amdgpu_buffer_rsrc_t rB = make_res(a.W, uint32_t(H) * uint32_t(G) * 4u);
+  const uint32_t va = (uint32_t(min(r0 + c, B - 1)) * uint32_t(G) + 4u * g) * 4u;
+  const uint32_t vb = (uint32_t(u0 + c) * uint32_t(G) + 4u * g) * 4u;
+  const int nq = G >> 4;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int q0 = wave; q0 < nq; q0 += kBwdChunk * kFw) {
+    f32x4 av[kBwdChunk], bv[kBwdChunk];
+#pragma unroll
+    for (int s = 0; s < kBwdChunk; ++s) {
+      const uint32_t q = uint32_t(min(q0 + s * kFw, nq - 1));
+      av[s] = ldb4(rA, va, 64u * q);
+      bv[s] = ldb4(rB, vb, 64u * q);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the chunk issues before the first product
+#pragma unroll
+    for (int s = 0; s < kBwdChunk; ++s) acc = mfma4(q0 + s * kFw < nq ? av[s] : f32x4{0.f, 0.f, 0.f, 0.f}, bv[s], acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[wave * 256 + (4 * g + i) * 16 + c] = acc[i];
+  __syncthreads();
+  if (!ep) return;
+  const int t = tid & 255;
+  float v = part[t];
+#pragma unroll
+  for (int w = 1; w < kFw; ++w) v += part[w * 256 + t];
+  const float dhin = v + dz0;
+  if (er >= B) return;
+  if (a.dhin) a.dhin[long(er) * H + eu] = dhin;
+  if (!cell) return;
+  const float dh = dout + keep * dhin;
+  const CellGrad d = cell_backward(xr, xz, xn, hr, hz, hn, h, dh);
+  float* dgib = a.dgi + long(er) * G;
+  float* dghb = a.dgh_prev + long(er) * G;
+  dgib[eu] = d.r;
+  dgib[H + eu] = d.z;
+  dgib[2 * H + eu] = d.n;
+  dghb[eu] = d.r;
+  dghb[H + eu] = d.z;
+  dghb[2 * H + eu] = d.hn;
+  a.dhz_prev[long(er) * H + eu] = d.hz;
 }
 
 unsigned grid_for(long n) {
@@ -134,6 +346,40 @@ int ttrl_gru_step_backward(ttrl_ctx* ctx, int B, int H, const float* gi, const f
   hipLaunchKernelGGL(k_gru_step_bwd, dim3(grid_for(long(B) * H)), dim3(kGruThreads), 0, stream_of(ctx), B, H, gi, gh,
                      hin, dout, dhin_next, done_next, dgi, dgh, dhin);
   return check_launch("ttrl_gru_step_backward");
+}
+
+int ttrl_gru_step_fused(ttrl_ctx* ctx, int B, int H, const float* gi, const float* hin, const float* W_hh,
+                        const float* b_hh, float* gh, float* hout, const float* done_next, float* hin_next) {
+  TTRL_REQUIRE(ctx && gi && hin && W_hh && b_hh && gh && hout, "ttrl_gru_step_fused: null argument");
+  TTRL_REQUIRE(B >= 0 && H > 0 && H % 16 == 0 && H <= 8192,
+               "ttrl_gru_step_fused: H must be a positive multiple of 16 up to 8192 (got B=%d, H=%d)", B, H);
+  TTRL_REQUIRE((reinterpret_cast<uintptr_t>(hin) | reinterpret_cast<uintptr_t>(W_hh)) % 16 == 0,
+               "ttrl_gru_step_fused: hin and W_hh must be 16-byte aligned");
+  if (B == 0) return TTRL_OK;
+  GruFwdArgs a{B, H, gi, hin, W_hh, b_hh, gh, hout, done_next, hin_next};
+  hipLaunchKernelGGL(k_gru_fwd_fused, dim3(unsigned(H / 16), ceil_div(B, 16)), dim3(kFt), 0, stream_of(ctx), a);
+  return check_launch("ttrl_gru_step_fused");
+}
+
+int ttrl_gru_step_backward_fused(ttrl_ctx* ctx, int B, int H, const float* dgh, const float* W_hh, const float* dhz,
+                                 float* dhin, const float* gi_prev, const float* gh_prev, const float* hin_prev,
+                                 const float* dout_prev, const float* done, float* dgi_prev, float* dgh_prev,
+                                 float* dhz_prev) {
+  TTRL_REQUIRE(ctx && dgh && W_hh && dhz, "ttrl_gru_step_backward_fused: null argument");
+  TTRL_REQUIRE(B >= 0 && H > 0 && H % 16 == 0 && H <= 8192,
+               "ttrl_gru_step_backward_fused: H must be a positive multiple of 16 up to 8192 (got B=%d, H=%d)", B,
+               H);
+  TTRL_REQUIRE((reinterpret_cast<uintptr_t>(dgh) | reinterpret_cast<uintptr_t>(W_hh)) % 16 == 0,
+               "ttrl_gru_step_backward_fused: dgh and W_hh must be 16-byte aligned");
+  const bool cell = gi_prev != nullptr;
+  TTRL_REQUIRE(cell ? (gh_prev && hin_prev && dgi_prev && dgh_prev && dhz_prev)
+                    : !(gh_prev || hin_prev || dout_prev || done || dgi_prev || dgh_prev || dhz_prev),
+               "ttrl_gru_step_backward_fused: the previous step's gi, gh, hin, dgi, dgh and dhz are given together");
+  TTRL_REQUIRE(cell || dhin, "ttrl_gru_step_backward_fused: nothing to write (dhin and gi_prev both NULL)");
+  if (B == 0) return TTRL_OK;
+  GruBwdArgs a{B, H, dgh, W_hh, dhz, dhin, gi_prev, gh_prev, hin_prev, dout_prev, done, dgi_prev, dgh_prev, dhz_prev};
+  hipLaunchKernelGGL(k_gru_bwd_fused, dim3(unsigned(H / 16), ceil_div(B, 16)), dim3(kFt), 0, stream_of(ctx), a);
+  return check_launch("ttrl_gru_step_backward_fused");
 }
 
 }  // extern "C"

@@ -271,6 +271,8 @@ SIGNATURES = {
     "ttrl_gru_step": ([P, I, I, P, P, P, P, P, P], I),
     "ttrl_gru_mask": ([P, I, I, P, P, P], I),
     "ttrl_gru_step_backward": ([P, I, I, P, P, P, P, P, P, P, P, P], I),
+    "ttrl_gru_step_fused": ([P, I, I, P, P, P, P, P, P, P, P], I),
+    "ttrl_gru_step_backward_fused": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
     "ttrl_replay_write": ([P, C.POINTER(ReplayRing), I, P, P, P, P, P, P, P, P, P, P], I),
     "ttrl_replay_lane_sums": ([P, C.POINTER(ReplayRing), P, P, I, I, P, P], I),
     "ttrl_replay_priority_pick": ([P, C.POINTER(ReplayRing), I, P, P, P, P, I, I, P, P, P, P], I),

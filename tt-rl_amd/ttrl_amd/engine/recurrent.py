@@ -127,26 +127,67 @@ def unroll(cell: GRUCell, x: Tensor, h0: Tensor, done: Tensor | None):
     def done_at(t):
         return None if dptr is None else C.c_void_p(dptr + 4 * t * B)
 
+    def at(arr, t, width):
+        return arr.view(t * B * width, (B, width))
+
+    W_hh = cell.weight_hh.data
+    # One launch per step when the fused kernels' layout holds (H a multiple
+    # of 16, float4-aligned operands), else a GEMM and a cell kernel per step.
+    fused = H % 16 == 0 and H <= 8192 and all(a.ptr % 16 == 0 for a in (HIN, W_hh))
     _linear(dev, X, cell.weight_ih, cell.bias_ih, GI, T * B, F, G)
     dev.call("ttrl_gru_mask", B, H, h0.data.vp, done_at(0), HIN.vp)
     for t in range(T):
-        gi, gh = GI.view(t * B * G, (B, G)), GH.view(t * B * G, (B, G))
-        hin = HIN.view(t * B * H, (B, H))
-        _linear(dev, hin, cell.weight_hh, cell.bias_hh, gh, B, H, G)
+        gi, gh, hin, out = at(GI, t, G), at(GH, t, G), at(HIN, t, H), at(OUT, t, H)
         last = t + 1 == T
-        dev.call("ttrl_gru_step", B, H, gi.vp, gh.vp, hin.vp, OUT.view(t * B * H, (B, H)).vp,
-                 None if last else done_at(t + 1), None if last else HIN.view((t + 1) * B * H, (B, H)).vp)
+        done_next = None if last else done_at(t + 1)
+        hin_next = None if last else at(HIN, t + 1, H).vp
+        if fused:
+            dev.call("ttrl_gru_step_fused", B, H, gi.vp, hin.vp, W_hh.vp, cell.bias_hh.data.vp, gh.vp, out.vp,
+                     done_next, hin_next)
+        else:
+            _linear(dev, hin, cell.weight_hh, cell.bias_hh, gh, B, H, G)
+            dev.call("ttrl_gru_step", B, H, gi.vp, gh.vp, hin.vp, out.vp, done_next, hin_next)
     params = (cell.weight_ih, cell.weight_hh, cell.bias_ih, cell.bias_hh)
     final_data = OUT.view((T - 1) * B * H, (B, H))
     if not _needs(x, h0, *params):
         return _detached(OUT), _detached(final_data)
     outputs = Tensor(OUT, True, (x, h0) + params, "gru_unroll")
 
+    def _backward_fused(grad: DeviceArray, DGI: DeviceArray, DGH: DeviceArray, need_h0: bool):
+        """The reverse walk with one launch per step: step s's launch forms
+        d hin_s and the cell backward of step s - 1; -> d hin_0 or None."""
+        DHZ = [DeviceArray(dev, (B, H)), DeviceArray(dev, (B, H))]
+        last = T - 1
+        dev.call("ttrl_gru_step_backward", B, H, at(GI, last, G).vp, at(GH, last, G).vp, at(HIN, last, H).vp,
+                 at(grad, last, H).vp, None, None, at(DGI, last, G).vp, at(DGH, last, G).vp, DHZ[last % 2].vp)
+        for s in range(last, 0, -1):
+            dev.call("ttrl_gru_step_backward_fused", B, H, at(DGH, s, G).vp, W_hh.vp, DHZ[s % 2].vp, None,
+                     at(GI, s - 1, G).vp, at(GH, s - 1, G).vp, at(HIN, s - 1, H).vp, at(grad, s - 1, H).vp,
+                     done_at(s), at(DGI, s - 1, G).vp, at(DGH, s - 1, G).vp, DHZ[(s - 1) % 2].vp)
+        if not need_h0:
+            return None
+        dhin0 = DeviceArray(dev, (B, H))
+        dev.call("ttrl_gru_step_backward_fused", B, H, at(DGH, 0, G).vp, W_hh.vp, DHZ[0].vp, dhin0.vp,
+                 None, None, None, None, None, None, None, None)
+        return dhin0
+
     def _backward(grad: DeviceArray):
         DGI = DeviceArray(dev, (T, B, G))
         DGH = DeviceArray(dev, (T, B, G))
-        DH = [DeviceArray(dev, (B, H)), DeviceArray(dev, (B, H))]
         need_h0 = h0.requires_grad
+        if fused:
+            dhin0 = _backward_fused(grad, DGI, DGH, need_h0)
+        else:
+            dhin0 = _backward_steps(grad, DGI, DGH, need_h0)
+        if need_h0:
+            dh0 = DeviceArray(dev, (B, H))
+            dev.call("ttrl_gru_mask", B, H, dhin0.vp, done_at(0), dh0.vp)
+            h0._accumulate(dh0)
+        _weight_grads(DGI, DGH)
+
+    def _backward_steps(grad: DeviceArray, DGI: DeviceArray, DGH: DeviceArray, need_h0: bool):
+        """The reverse walk with a cell-backward kernel and a GEMM per step."""
+        DH = [DeviceArray(dev, (B, H)), DeviceArray(dev, (B, H))]
         for t in range(T - 1, -1, -1):
             first = t == T - 1
             cur, nxt = DH[t % 2], DH[(t + 1) % 2]
@@ -159,10 +200,9 @@ def unroll(cell: GRUCell, x: Tensor, h0: Tensor, done: Tensor | None):
                 dev.call("ttrl_matmul", B, H, G, DGH.view(t * B * G, (B, G)).vp, C.c_long(G), 0,
                          cell.weight_hh.data.vp, C.c_long(G), 1, cur.vp, C.c_long(H), C.c_float(1.0),
                          C.c_float(1.0))
-        if need_h0:
-            dh0 = DeviceArray(dev, (B, H))
-            dev.call("ttrl_gru_mask", B, H, DH[0].vp, done_at(0), dh0.vp)
-            h0._accumulate(dh0)
+        return DH[0] if need_h0 else None
+
+    def _weight_grads(DGI: DeviceArray, DGH: DeviceArray):
         (dw_ih, dw_hh, db_ih, db_hh), beta_w = grad_targets(*params)
         (dx,), beta_x = grad_targets(x)
         xmask = relu_mask(x) if dx is not None else None
