@@ -18,14 +18,19 @@
 // arithmetic of a timestep in one launch.  Forward, gh_t = hin_t W_hh + b_hh
 // and the cell; backward, d hin_t = z_t dh_t + d gh_t W_hh^T and then the
 // cell backward of step t - 1, whose dh_{t-1} = dout_{t-1} + (1 - done_t)
-// d hin_t needs only this workgroup's units.  A workgroup owns 16 hidden
-// units (the gate columns u, H + u, 2H + u of each) and 16 batch rows; its
-// kFw wavefronts split the product's reduction into groups of 16 (wavefront
-// w takes groups w, w + kFw, ...) and their 16 x 16 partial tiles are summed
-// in wavefront order through LDS, so every output has one fixed summation
-// order.  In group q a lane (column c = lane % 16, quarter g = lane / 16)
-// feeds k = 16q + 4g + j to MFMA j (j = 0..3): the operand that runs along
-// k in memory is one float4 per lane.
+// d hin_t needs only this workgroup's units.  A workgroup owns 8 hidden
+// units (the gate columns u, H + u, 2H + u of each) and 8 batch rows, and
+// runs each 16 x 16 MFMA as two 8 x 8 products over different k: lanes of
+// column half h (c / 8) carry row or unit c % 8 at k offset 16 h, so the
+// diagonal blocks of the output hold the two k halves and every lane loads
+// distinct operands (an 8 x 8 tile puts half the bytes and MFMAs of a 16 x
+// 16 one on each CU, over twice the CUs).  Its kFw wavefronts split the
+// reduction into pair groups of 32 k (a contiguous run each, so a wavefront
+// reads whole cache lines of each operand row); in pair group p a lane
+// (c, quarter g = lane / 16) feeds k = 32p + 16h + 4g + j to MFMA j, the
+// operand that runs along k in memory as one float4.  The partial tiles are
+// summed in wavefront order through LDS, so every output has one fixed
+// summation order.
 #include "common.hpp"
 #include "tile_gemm.hpp"
 
@@ -124,8 +129,9 @@ __global__ __launch_bounds__(kGruThreads) void k_gru_step_bwd(int B, int H, cons
 
 constexpr int kFw = 8;  // wavefronts of a fused-step workgroup
 constexpr int kFt = 64 * kFw;
-constexpr int kFwdChunk = 4;   // forward: groups in flight per wavefront (13 loads each)
-constexpr int kBwdChunk = 12;  // backward: groups in flight per wavefront (2 float4 loads each)
+constexpr int kTile = 8;       // batch rows and hidden units of a workgroup
+constexpr int kFwdChunk = 2;   // forward: pair groups in flight per wavefront (13 loads each)
+constexpr int kBwdChunk = 6;   // backward: pair groups in flight per wavefront (2 float4 loads each)
 
 __device__ __forceinline__ float ldb1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
@@ -138,6 +144,26 @@ __device__ __forceinline__ f32x4 mfma4(f32x4 a, f32x4 b, f32x4 acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+}
+
+// The lane's place in the block-diagonal product: half h = c / 8 of the
+// 16 MFMA rows and columns, index cc = c % 8 in its 8 x 8 block; kh = the
+// lane's k offset in a pair group (16 h + 4 g), kmax = the reduction length.
+struct DiagLane {
+  int cc, h, g;
+  uint32_t kh;
+};
+__device__ __forceinline__ DiagLane diag_lane(int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  return DiagLane{c & 7, c >> 3, g, uint32_t(16 * (c >> 3) + 4 * g)};
+}
+
+// The pair groups [lo, hi) of this wavefront: a contiguous run, so it reads
+// whole cache lines of each operand row.
+__device__ __forceinline__ void wave_range(int wave, int np, int& lo, int& hi) {
+  const int per = (np + kFw - 1) / kFw;
+  lo = wave * per;
+  hi = min(np, lo + per);
 }
 
 struct GruFwdArgs {
@@ -154,51 +180,59 @@ struct GruFwdArgs {
 
 __global__ __launch_bounds__(kFt) void k_gru_fwd_fused(GruFwdArgs a) {
   __shared__ float part[kFw * 3 * 256];
-  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int B = a.B, H = a.H, G = 3 * H;
-  const int u0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
-  // The output element of threads 0..255 (row r0 + tid / 16, unit u0 + tid %
-  // 16); the other threads load the same operands and store nothing.  The
-  // loads are unconditional so that none of them waits before the product's.
-  const bool ep = tid < 256;  // whole wavefronts
-  const int er = r0 + ((tid >> 4) & 15), eu = u0 + (tid & 15), erc = min(er, B - 1);
+  const int u0 = blockIdx.x * kTile, r0 = blockIdx.y * kTile;
+  // The output element of threads 0..63 (row r0 + t / 8, unit u0 + t % 8);
+  // the other threads load the same operands and store nothing.  The loads
+  // are unconditional so that none of them waits before the product's.
+  const int t = tid & 63;
+  const bool ep = tid < 64;  // wavefront 0
+  const int er = r0 + t / kTile, eu = u0 + t % kTile, erc = min(er, B - 1);
   const float* gib = a.gi + long(erc) * G;
   const float xr = gib[eu], xz = gib[H + eu], xn = gib[2 * H + eu];
   const float br = a.bias[eu], bz = a.bias[H + eu], bn = a.bias[2 * H + eu];
   const float h = a.hin[long(erc) * H + eu];
   const float dv = *(a.done_next ? a.done_next + erc : a.bias);
   const float keep = a.done_next ? 1.f - dv : 1.f;
-  // A: hin[row c][16q + 4g + j] (one float4), B: W[16q + 4g + j][e H + u0 + c].
+  // A: hin[r0 + cc][k] (one float4), B: W[k][e H + u0 + cc], k = 32p + kh + j.
+  const DiagLane L = diag_lane(lane);
   const __amdgpu_buffer_rsrc_t rA = make_res(a.hin, uint32_t(B) * uint32_t(H) * 4u);
   const __amdgpu_buffer_rsrc_t rB = make_res(a.W, uint32_t(H) * uint32_t(G) * 4u);
-  const uint32_t va = (uint32_t(min(r0 + c, B - 1)) * uint32_t(H) + 4u * g) * 4u;
-  const uint32_t vb = (4u * g * uint32_t(G) + uint32_t(u0 + c)) * 4u;
-  const int nq = H >> 4;
+  const uint32_t va = uint32_t(min(r0 + L.cc, B - 1)) * uint32_t(H) * 4u;
+  const uint32_t vb = uint32_t(u0 + L.cc) * 4u;
+  const int np = (H + 31) >> 5;
+  int lo, hi;
+  wave_range(wave, np, lo, hi);
   f32x4 acc[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  for (int q0 = wave; q0 < nq; q0 += kFwdChunk * kFw) {
+  for (int p0 = lo; p0 < hi; p0 += kFwdChunk) {
     f32x4 av[kFwdChunk], bv[kFwdChunk][3];
+    bool in[kFwdChunk];
 #pragma unroll
     for (int s = 0; s < kFwdChunk; ++s) {
-      const uint32_t q = uint32_t(min(q0 + s * kFw, nq - 1));
-      av[s] = ldb4(rA, va, 64u * q);
+      // past the end of the run (re-reads its last group) or of k (H % 32 ==
+      // 16: re-reads the last 16 k): loaded, then zeroed below
+      const uint32_t k = 32u * uint32_t(min(p0 + s, hi - 1)) + L.kh;
+      in[s] = p0 + s < hi && k < uint32_t(H);
+      const uint32_t kc = min(k, uint32_t(H - 16) + 4u * L.g);
+      av[s] = ldb4(rA, va + kc * 4u, 0);
 #pragma unroll
       for (int e = 0; e < 3; ++e) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bv[s][e][j] = ldb1(rB, vb, ((16u * q + j) * uint32_t(G) + e * uint32_t(H)) * 4u);
+        for (int j = 0; j < 4; ++j) bv[s][e][j] = ldb1(rB, vb + ((kc + j) * uint32_t(G) + e * uint32_t(H)) * 4u, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the chunk issues before the first product
-    // A group past the end (its loads re-read the last group) adds zeros:
-    // every product runs, so no load is deferred behind a branch.
 #pragma unroll
     for (int s = 0; s < kFwdChunk; ++s) {
-      const f32x4 x = q0 + s * kFw < nq ? av[s] : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 x = in[s] ? av[s] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 3; ++e) acc[e] = mfma4(x, bv[s][e], acc[e]);
     }
   }
   // lane (c, g) holds rows 4g + i of column c
+  const int c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int e = 0; e < 3; ++e) {
 #pragma unroll
@@ -206,13 +240,14 @@ __global__ __launch_bounds__(kFt) void k_gru_fwd_fused(GruFwdArgs a) {
   }
   __syncthreads();
   if (!ep) return;
-  const int t = tid & 255;
+  // the element's two diagonal blocks (k halves), summed in wavefront order
+  const int o0 = (t / kTile) * 16 + t % kTile, o1 = o0 + 8 * 16 + 8;
   float s3[3];
 #pragma unroll
   for (int e = 0; e < 3; ++e) {
-    float v = part[e * 256 + t];
+    float v = part[e * 256 + o0] + part[e * 256 + o1];
 #pragma unroll
-    for (int w = 1; w < kFw; ++w) v += part[(w * 3 + e) * 256 + t];
+    for (int w = 1; w < kFw; ++w) v += part[(w * 3 + e) * 256 + o0] + part[(w * 3 + e) * 256 + o1];
     s3[e] = v;
   }
   const float hr = s3[0] + br, hz = s3[1] + bz, hn = s3[2] + bn;
@@ -242,12 +277,13 @@ struct GruBwdArgs {
 
 __global__ __launch_bounds__(kFt) void k_gru_bwd_fused(GruBwdArgs a) {
   __shared__ float part[kFw * 256];
-  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int B = a.B, H = a.H, G = 3 * H;
-  const int u0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
-  const bool ep = tid < 256;
-  const int er = r0 + ((tid >> 4) & 15), eu = u0 + (tid & 15), erc = min(er, B - 1);
+  const int u0 = blockIdx.x * kTile, r0 = blockIdx.y * kTile;
+  const int t = tid & 63;
+  const bool ep = tid < 64;
+  const int er = r0 + t / kTile, eu = u0 + t % kTile, erc = min(er, B - 1);
   const bool cell = a.gi != nullptr;
   // Unconditional loads (see k_gru_fwd_fused); an absent operand reads a
   // buffer of the same shape and is not used.
@@ -262,33 +298,40 @@ __global__ __launch_bounds__(kFt) void k_gru_bwd_fused(GruBwdArgs a) {
   const float dv = *(a.done ? a.done + erc : a.dhz);
   const float dout = a.dout ? ov : 0.f;
   const float keep = a.done ? 1.f - dv : 1.f;
-  // A: d gh[row c][16q + 4g + j], B: W[u0 + c][16q + 4g + j]; one float4 each.
+  // A: d gh[r0 + cc][k], B: W[u0 + cc][k], k = 32p + kh + j; one float4 each.
+  const DiagLane L = diag_lane(lane);
   const __amdgpu_buffer_rsrc_t rA = make_res(a.dgh, uint32_t(B) * uint32_t(G) * 4u);
   const __amdgpu_buffer_rsrc_t rB = make_res(a.W, uint32_t(H) * uint32_t(G) * 4u);
-  const uint32_t va = (uint32_t(min(r0 + c, B - 1)) * uint32_t(G) + 4u * g) * 4u;
-  const uint32_t vb = (uint32_t(u0 + c) * uint32_t(G) + 4u * g) * 4u;
-  const int nq = G >> 4;
+  const uint32_t va = uint32_t(min(r0 + L.cc, B - 1)) * uint32_t(G) * 4u;
+  const uint32_t vb = uint32_t(u0 + L.cc) * uint32_t(G) * 4u;
+  const int np = (G + 31) >> 5;
+  int lo, hi;
+  wave_range(wave, np, lo, hi);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int q0 = wave; q0 < nq; q0 += kBwdChunk * kFw) {
+  for (int p0 = lo; p0 < hi; p0 += kBwdChunk) {
     f32x4 av[kBwdChunk], bv[kBwdChunk];
+    bool in[kBwdChunk];
 #pragma unroll
     for (int s = 0; s < kBwdChunk; ++s) {
-      const uint32_t q = uint32_t(min(q0 + s * kFw, nq - 1));
-      av[s] = ldb4(rA, va, 64u * q);
-      bv[s] = ldb4(rB, vb, 64u * q);
+      const uint32_t k = 32u * uint32_t(min(p0 + s, hi - 1)) + L.kh;
+      in[s] = p0 + s < hi && k < uint32_t(G);
+      const uint32_t kc = min(k, uint32_t(G - 16) + 4u * L.g);
+      av[s] = ldb4(rA, va + kc * 4u, 0);
+      bv[s] = ldb4(rB, vb + kc * 4u, 0);
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the chunk issues before the first product
 #pragma unroll
-    for (int s = 0; s < kBwdChunk; ++s) acc = mfma4(q0 + s * kFw < nq ? av[s] : f32x4{0.f, 0.f, 0.f, 0.f}, bv[s], acc);
+    for (int s = 0; s < kBwdChunk; ++s) acc = mfma4(in[s] ? av[s] : f32x4{0.f, 0.f, 0.f, 0.f}, bv[s], acc);
   }
+  const int c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) part[wave * 256 + (4 * g + i) * 16 + c] = acc[i];
   __syncthreads();
   if (!ep) return;
-  const int t = tid & 255;
-  float v = part[t];
+  const int o0 = (t / kTile) * 16 + t % kTile, o1 = o0 + 8 * 16 + 8;
+  float v = part[o0] + part[o1];
 #pragma unroll
-  for (int w = 1; w < kFw; ++w) v += part[w * 256 + t];
+  for (int w = 1; w < kFw; ++w) v += part[w * 256 + o0] + part[w * 256 + o1];
   const float dhin = v + dz0;
   if (er >= B) return;
   if (a.dhin) a.dhin[long(er) * H + eu] = dhin;
@@ -357,7 +400,7 @@ int ttrl_gru_step_fused(ttrl_ctx* ctx, int B, int H, const float* gi, const floa
                "ttrl_gru_step_fused: hin and W_hh must be 16-byte aligned");
   if (B == 0) return TTRL_OK;
   GruFwdArgs a{B, H, gi, hin, W_hh, b_hh, gh, hout, done_next, hin_next};
-  hipLaunchKernelGGL(k_gru_fwd_fused, dim3(unsigned(H / 16), ceil_div(B, 16)), dim3(kFt), 0, stream_of(ctx), a);
+  hipLaunchKernelGGL(k_gru_fwd_fused, dim3(unsigned(H / kTile), ceil_div(B, kTile)), dim3(kFt), 0, stream_of(ctx), a);
   return check_launch("ttrl_gru_step_fused");
 }
 
@@ -378,7 +421,7 @@ int ttrl_gru_step_backward_fused(ttrl_ctx* ctx, int B, int H, const float* dgh, 
   TTRL_REQUIRE(cell || dhin, "ttrl_gru_step_backward_fused: nothing to write (dhin and gi_prev both NULL)");
   if (B == 0) return TTRL_OK;
   GruBwdArgs a{B, H, dgh, W_hh, dhz, dhin, gi_prev, gh_prev, hin_prev, dout_prev, done, dgi_prev, dgh_prev, dhz_prev};
-  hipLaunchKernelGGL(k_gru_bwd_fused, dim3(unsigned(H / 16), ceil_div(B, 16)), dim3(kFt), 0, stream_of(ctx), a);
+  hipLaunchKernelGGL(k_gru_bwd_fused, dim3(unsigned(H / kTile), ceil_div(B, kTile)), dim3(kFt), 0, stream_of(ctx), a);
   return check_launch("ttrl_gru_step_backward_fused");
 }
 
