@@ -280,9 +280,11 @@ int ttrl_conv2d_backward_input(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const 
                                const float* wt, float* dx, const float* xmask, float x_scale, float beta);
 /* Both gradients of one conv2d node's backward (ttrl/engine/conv/backward.py:33-78):
  * ttrl_conv2d_backward_weight(x, x_scale, dy, ymask, dwt, db, beta_w) and
- * ttrl_conv2d_backward_input(dy, ymask, wt, dx, xmask, x_scale, beta_x) with
- * the same results, the two GEMMs sharing one launch.  fp32 NHWC inputs only
- * (a uint8 frame input has no gradient); db may be NULL. */
+ * ttrl_conv2d_backward_input(dy, ymask, wt, dx, xmask, x_scale, beta_x), the
+ * two GEMMs sharing one launch or as two launches with their own tile shapes,
+ * whichever the context measured faster for the geometry on its first call
+ * outside capture (kept with the context's GEMM plans).  fp32 NHWC inputs
+ * only (a uint8 frame input has no gradient); db may be NULL. */
 int ttrl_conv2d_backward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale, const float* dy,
                          const float* ymask, const float* wt, float* dwt, float* db, float beta_w, float* dx,
                          const float* xmask, float beta_x);

@@ -107,3 +107,39 @@ def test_conv_each_tile(device, monkeypatch, cfg, splits, u8):
         assert _rel(master_to_oihw(dw2.numpy(), w.shape, layout), dw_ref) < 2e-5
         assert _rel(db2.numpy(), db_ref) < 2e-5
         assert _rel(dx2.numpy(), dx_ref) < 2e-5
+
+
+@pytest.mark.parametrize("B", [32, 256])
+def test_conv_backward_choice_gives_the_separate_gradients(device, B):
+    """ttrl_conv2d_backward runs the pair or two launches, whichever it
+    measured faster for the geometry; either way it gives the gradients of
+    ttrl_conv2d_backward_weight and ttrl_conv2d_backward_input (rel 1e-5: the
+    plans may sum in another order), with beta accumulation and the ReLU
+    gates, and files its choice with the context's plans."""
+    from ttrl_amd import _lib
+    from ttrl_amd.engine.tensor import DeviceArray
+
+    Cin, H, O, k, s = 32, 20, 64, 4, 2
+    OH = (H - k) // s + 1
+    g = _lib.ConvGeom(B, Cin, H, H, O, k, s, 0, _lib.LAYOUT_NHWC_F32)
+    rng = np.random.default_rng(B)
+    x = rng.standard_normal((B, H, H, Cin)).astype(np.float32)
+    dy = rng.standard_normal((B, OH, OH, O)).astype(np.float32)
+    ymask = rng.standard_normal((B, OH, OH, O)).astype(np.float32)
+    wt = (0.1 * rng.standard_normal((k * k * Cin, O))).astype(np.float32)
+    xd, dyd, md, wd = (_dev(device, a) for a in (x, dy, ymask, wt))
+    dw, db, dx = DeviceArray(device, wt.shape), DeviceArray(device, (O,)), DeviceArray(device, x.shape)
+    device.call("ttrl_conv2d_backward_weight", C.byref(g), xd.vp, C.c_float(1.0), dyd.vp, md.vp, dw.vp, db.vp,
+                C.c_float(0.0))
+    device.call("ttrl_conv2d_backward_input", C.byref(g), dyd.vp, md.vp, wd.vp, dx.vp, xd.vp, C.c_float(1.0),
+                C.c_float(0.0))
+    dw2, db2, dx2 = DeviceArray(device, wt.shape), DeviceArray(device, (O,)), DeviceArray(device, x.shape)
+    for t in (dw2, db2, dx2):
+        t.fill(0.5)
+    for rep in range(2):  # the first call chooses, the second runs the kept choice
+        device.call("ttrl_conv2d_backward", C.byref(g), xd.vp, C.c_float(1.0), dyd.vp, md.vp, wd.vp, dw2.vp, db2.vp,
+                    C.c_float(1.0), dx2.vp, xd.vp, C.c_float(1.0))
+    assert _rel(dw2.numpy() - 0.5, 2 * dw.numpy()) < 1e-5
+    assert _rel(db2.numpy() - 0.5, 2 * db.numpy()) < 1e-5
+    assert _rel(dx2.numpy() - 0.5, 2 * dx.numpy()) < 1e-5
+    assert f"ttrl_conv2d_backward:pair|" in device.export_plans()

@@ -1,7 +1,11 @@
 // A convolution layer's whole backward: weight (+ bias) gradient and input
 // gradient in one call.  The two GEMMs are independent given dZ, so the
 // weight gradient and the first launch of the input gradient (its first
-// four residue classes) run as one paired launch.
+// four residue classes) can run as one paired launch, which saves a launch
+// but makes both problems take one tile shape; at large batches the two as
+// separate launches, each with its own tile shape, are faster.  The plain
+// call times both once per geometry (outside capture, on scratch outputs)
+// and keeps the faster for the context.
 //   dW = sum over taps of X-slice^T dY  ttrl/engine/conv/backward.py:45-78
 //   dX = conv_transpose2d(dY, W)        ttrl/engine/conv/backward.py:33-42
 #include "conv.hpp"
@@ -32,6 +36,78 @@ int conv_backward_pair(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_s
                                  reserved);
   }
   return rc;
+}
+
+// The two gradients as separate launches, each GEMM with its own plan.
+template <int MODE>
+int conv_backward_split(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
+                        const float* wt, float* dwt, float* db, float beta_w, float* dx, const float* xmask,
+                        float beta_x, long reserved) {
+  constexpr unsigned kDw = MODE == kPatchGeneral ? kConvGeneralCfgs : kConvDwCfgs;
+  const ConvDwProblem<MODE> w = conv_dw_problem<MODE>(g, x, x_scale, dy, dwt, db, beta_w);
+  int rc = run_gemm<kDw>(ctx, w.la, w.lb, w.ep, w.q.M, w.q.N, w.q.K, 1, "ttrl_conv2d_backward", reserved);
+  for (int c0 = 0; c0 < g.S * g.S && rc == TTRL_OK; c0 += kMaxGroups) {
+    const ConvDxProblem d = conv_dx_problem(g, c0, dy, wt, dx, xmask, x_scale, beta_x);
+    rc = run_gemm<kConvDxCfgs>(ctx, d.la, d.lb, d.ep, d.q.M, d.q.N, d.q.K, d.q.groups, "ttrl_conv2d_backward",
+                               reserved);
+  }
+  return rc;
+}
+
+// Whether the paired launch is the faster way for this geometry.  Kept in
+// the context's plan table (cfg 1: pair, 0: separate), so it is exported and
+// imported with the GEMM plans and every later call, eager or captured, takes
+// the same path.  Without timing (under capture, or tuning off) a pair is
+// taken for at most 4096 output pixels, where the saved launch matters most.
+template <int MODE>
+bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
+                    const float* wt, const float* xmask, long reserved) {
+  char keybuf[192];
+  snprintf(keybuf, sizeof(keybuf), "ttrl_conv2d_backward:pair|%d|%d|%d|%d|%d|%d|%d|%d|%d|%d|%ld|%d", MODE, g.B, g.C,
+           g.H, g.W, g.O, g.KH, g.KW, g.S, g.P, reserved, xmask ? 1 : 0);
+  const std::string key(keybuf);
+  if (const GemmPlan* hit = ctx_plan_find(ctx, key)) return hit->cfg == 1;
+  bool pair = long(g.M) <= 4096;
+  hipEvent_t e0, e1;
+  if (!ctx_capturing(ctx) && gemm_tuning_enabled() && ctx_tune_events(ctx, &e0, &e1)) {
+    const size_t nw = size_t(g.KH) * g.KW * g.C * g.O, nx = size_t(g.B) * g.H * g.W * g.C;
+    float* out = nullptr;
+    if (hipMalloc(&out, (nw + size_t(g.O) + nx) * sizeof(float)) == hipSuccess) {
+      float *sw = out, *sb = out + nw, *sx = out + nw + g.O;
+      hipStream_t st = stream_of(ctx);
+      int rc = TTRL_OK;
+      auto paired = [&] {
+        if (rc == TTRL_OK) rc = conv_backward_pair<MODE>(ctx, g, x, x_scale, dy, wt, sw, sb, 0.f, sx, xmask, 0.f,
+                                                         reserved);
+      };
+      auto split = [&] {
+        if (rc == TTRL_OK) rc = conv_backward_split<MODE>(ctx, g, x, x_scale, dy, wt, sw, sb, 0.f, sx, xmask, 0.f,
+                                                          reserved);
+      };
+      paired();  // first runs: each GEMM's own plan is tuned here
+      split();
+      const float tp = rc == TTRL_OK ? time_best_of(e0, e1, st, paired) : -1.f;
+      const float ts = rc == TTRL_OK ? time_best_of(e0, e1, st, split) : -1.f;
+      if (tp > 0.f && ts > 0.f) pair = tp <= ts;
+      if (gemm_tuning_log())
+        fprintf(stderr, "[ttrl gemm tune] conv2d backward B=%d C=%d %dx%d O=%d k=%d s=%d: pair %.2f us, "
+                "separate %.2f us\n", g.B, g.C, g.H, g.W, g.O, g.KH, g.S, tp * 1e3f / 3.f, ts * 1e3f / 3.f);
+      (void)hipStreamSynchronize(st);
+      (void)hipFree(out);
+      (void)hipGetLastError();
+    }
+  }
+  ctx_plan_store(ctx, key, GemmPlan{pair ? 1 : 0, 0, 0, 0, 1, 0});
+  return pair;
+}
+
+template <int MODE>
+int conv_backward_chosen(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
+                         const float* wt, float* dwt, float* db, float beta_w, float* dx, const float* xmask,
+                         float beta_x, long reserved) {
+  if (pair_is_faster<MODE>(ctx, g, x, x_scale, dy, wt, xmask, reserved))
+    return conv_backward_pair<MODE>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved);
+  return conv_backward_split<MODE>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved);
 }
 
 }  // namespace
@@ -78,9 +154,10 @@ int ttrl_conv2d_backward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* 
     if (rc) return rc;
   }
   if (patch_mode(g, input_aligned(g, x)) == kPatchNhwcVec)
-    return conv_backward_pair<kPatchNhwcVec>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x,
+    return conv_backward_chosen<kPatchNhwcVec>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x,
+                                               reserved);
+  return conv_backward_chosen<kPatchGeneral>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x,
                                              reserved);
-  return conv_backward_pair<kPatchGeneral>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved);
 }
 
 }  // extern "C"
