@@ -67,9 +67,11 @@ def _minibatch(seed, B, A):
 
 
 @pytest.mark.parametrize("masked", [False, True])
-def test_ppo_loss_matches_oracle(device, masked):
+@pytest.mark.parametrize("B,A", [(256, 18), (300, 6), (1500, 32), (200, 40)])
+def test_ppo_loss_matches_oracle(device, masked, B, A):
+    """Up to 32 actions the rows sit in registers (several rows per thread
+    past 1024); more actions take the general kernel."""
     from ttrl_amd.engine.tensor import DeviceArray, to_device
-    B, A = 256, 18
     z, a, old_lp, adv, ret, old_v, v = _minibatch(11 + masked, B, A)
     w = (np.random.default_rng(2).random(B) > 0.3).astype(np.float32) if masked else None
     cfg = dict(clip_eps=0.1, value_clip_eps=0.1, value_coef=0.5, entropy_coef=0.01)

@@ -246,6 +246,196 @@ __global__ __launch_bounds__(kRedThreads) void k_ppo_loss(
   }
 }
 
+constexpr int kRedWaves = kRedThreads / 64;
+
+// Deterministic sums of NV values over the block: each wavefront folds its
+// lanes with xor shuffles and keeps lane 0's result, then the wavefront
+// partials are added in wavefront order.  Every thread gets the totals.
+template <int NV>
+__device__ inline void block_sums(float (&v)[NV], float* sh /* NV * kRedWaves */) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off, 64);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) sh[k * kRedWaves + wave] = v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float t = sh[k * kRedWaves];
+#pragma unroll
+    for (int w = 1; w < kRedWaves; ++w) t += sh[k * kRedWaves + w];
+    v[k] = t;
+  }
+  __syncthreads();
+}
+
+// One row's operands, the logits in registers (A <= AM).
+template <int AM>
+struct PpoRowIn {
+  float z[AM];
+  int a;
+  float w, olp, adv, v, ov, R;
+};
+
+template <int AM>
+__device__ __forceinline__ void ppo_row_load(const PpoCfg& cfg, const float* logits, const int* actions,
+                                             const float* old_logp, const float* adv, const float* returns,
+                                             const float* old_value, const float* value, const float* valid, int i,
+                                             PpoRowIn<AM>& r) {
+  const float* z = logits + long(i) * cfg.ldz;
+#pragma unroll
+  for (int j = 0; j < AM; ++j) r.z[j] = z[min(j, cfg.A - 1)];  // every load unconditional
+  r.a = actions[i];
+  const float wv = *(valid ? valid + i : old_logp + i);
+  r.w = valid ? wv : 1.f;
+  r.olp = old_logp[i];
+  r.adv = adv[i];
+  r.v = value[long(i) * cfg.ldv];
+  r.ov = old_value[i];
+  r.R = returns[i];
+}
+
+// The row's terms and gradients: the expressions of k_ppo_loss, in its order.
+template <int AM>
+__device__ __forceinline__ void ppo_row(const PpoCfg& cfg, const PpoRowIn<AM>& r, float inv, int i,
+                                        float* new_logp, float* dlogits, float* dvalue, float (&acc)[4]) {
+  const int A = cfg.A, a = r.a;
+  float mx = r.z[0];
+#pragma unroll
+  for (int j = 1; j < AM; ++j)
+    if (j < A) mx = fmaxf(mx, r.z[j]);
+  float se = 0.f;
+#pragma unroll
+  for (int j = 0; j < AM; ++j)
+    if (j < A) se += expf(r.z[j] - mx);
+  const bool act_in = a >= 0 && a < A;
+  float za = 0.f;  // z[a], selected without indexing the registers at run time
+#pragma unroll
+  for (int j = 0; j < AM; ++j)
+    if (j == a) za = r.z[j];
+  float* dz = dlogits + long(i) * cfg.ldz;
+  if (!(r.w > 0.f)) {
+    // an excluded slot: no loss term and no gradient (see k_ppo_loss)
+    const float lp = act_in ? (za - mx) - logf(se) : 0.f;
+    new_logp[i] = lp;
+    acc[3] += expm1f(lp) - lp;
+#pragma unroll
+    for (int j = 0; j < AM; ++j)
+      if (j < A) dz[j] = 0.f;
+    dvalue[long(i) * cfg.ldv] = 0.f;
+    return;
+  }
+  const float lse = logf(se);
+  const float lp = act_in ? (za - mx) - lse : 0.f;
+  float H = 0.f;
+#pragma unroll
+  for (int j = 0; j < AM; ++j) {
+    if (j < A) {
+      const float l = (r.z[j] - mx) - lse;
+      H -= expf(l) * l;
+    }
+  }
+  new_logp[i] = lp;
+  const float lr = lp - r.olp;
+  acc[3] += expm1f(lr) - lr;
+  const float ratio = expf(lr);
+  const float lo = 1.f - cfg.clip, hi = 1.f + cfg.clip;
+  const float rc = fminf(fmaxf(ratio, lo), hi);
+  const float Ad = r.adv;
+  const float u = ratio * Ad, c = rc * Ad;
+  const float surr = u - fmaxf(u - c, 0.f);
+  const bool take_u = !(u - c > 0.f);
+  const float dclamp = (ratio > lo && ratio < hi) ? 1.f : 0.f;
+  const float dsurr_dr = take_u ? Ad : dclamp * Ad;
+  const float dv = r.v - r.ov;
+  const float dvc = fminf(fmaxf(dv, -cfg.vclip), cfg.vclip);
+  const float eu = r.v - r.R, ec = (r.ov + dvc) - r.R;
+  const float qu = eu * eu, qc = ec * ec;
+  const bool take_c = qc - qu > 0.f;
+  const float vmax = take_c ? qc : qu;
+  const float dvclamp = (dv > -cfg.vclip && dv < cfg.vclip) ? 1.f : 0.f;
+  const float dq_dv = take_c ? 2.f * ec * dvclamp : 2.f * eu;
+  const float w = r.w;
+  acc[0] += surr * w;
+  acc[1] += vmax * w;
+  acc[2] += H * w;
+  const float gp = act_in ? -w * inv * dsurr_dr * ratio : 0.f;
+  const float ge = cfg.ecoef * w * inv;
+#pragma unroll
+  for (int j = 0; j < AM; ++j) {
+    if (j < A) {
+      const float l = (r.z[j] - mx) - lse;
+      const float p = expf(l);
+      dz[j] = gp * ((j == a ? 1.f : 0.f) - p) + ge * p * (l + H);
+    }
+  }
+  dvalue[long(i) * cfg.ldv] = cfg.vcoef * 0.5f * w * inv * dq_dv;
+}
+
+// k_ppo_loss with its latency cut for A <= AM: a thread's first row is
+// loaded before anything waits, the sums are two shuffle-and-LDS reductions
+// (the valid count, then the four loss sums together) instead of five
+// barrier trees.  Same per-row expressions; the block sums add in another
+// (fixed) order.
+template <int AM>
+__global__ __launch_bounds__(kRedThreads) void k_ppo_loss_rows(
+    PpoCfg cfg, const float* __restrict__ logits, const int* __restrict__ actions, const float* __restrict__ old_logp,
+    const float* __restrict__ adv, const float* __restrict__ returns, const float* __restrict__ old_value,
+    const float* __restrict__ value, const float* __restrict__ valid, float* __restrict__ out,
+    float* __restrict__ new_logp, float* __restrict__ dlogits, float* __restrict__ dvalue) {
+  __shared__ float sh[4 * kRedWaves];
+  const int B = cfg.B, tid = threadIdx.x;
+  PpoRowIn<AM> r0;
+  ppo_row_load<AM>(cfg, logits, actions, old_logp, adv, returns, old_value, value, valid, min(tid, B - 1), r0);
+  float wsum[1] = {tid < B ? r0.w : 0.f};
+  for (int i = tid + kRedThreads; i < B; i += kRedThreads) wsum[0] += valid ? valid[i] : 1.f;
+  block_sums<1>(wsum, sh);  // sum_all(valid)
+  const float inv = 1.f / wsum[0];
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // surrogate, value error, entropy, approximate KL
+  if (tid < B) ppo_row<AM>(cfg, r0, inv, tid, new_logp, dlogits, dvalue, acc);
+  for (int i = tid + kRedThreads; i < B; i += kRedThreads) {
+    PpoRowIn<AM> r;
+    ppo_row_load<AM>(cfg, logits, actions, old_logp, adv, returns, old_value, value, valid, i, r);
+    ppo_row<AM>(cfg, r, inv, i, new_logp, dlogits, dvalue, acc);
+  }
+  block_sums<4>(acc, sh);
+  if (tid == 0) {
+    const float pol = -acc[0] * inv;
+    const float val = 0.5f * acc[1] * inv;
+    const float ent = acc[2] * inv;
+    out[0] = (pol + val * cfg.vcoef) + ent * -cfg.ecoef;
+    out[1] = pol;
+    out[2] = val;
+    out[3] = ent;
+    if (cfg.kl) out[4] = acc[3] / float(B);
+  }
+}
+
+// The objective's launch: the register-row kernel for up to 32 actions.
+void launch_ppo_loss(hipStream_t st, const PpoCfg& cfg, const float* logits, const int* actions,
+                     const float* old_logp, const float* adv, const float* returns, const float* old_value,
+                     const float* value, const float* valid, float* out, float* new_logp, float* dlogits,
+                     float* dvalue) {
+  const dim3 g(1), b(kRedThreads);
+  if (cfg.A <= 8)
+    hipLaunchKernelGGL(k_ppo_loss_rows<8>, g, b, 0, st, cfg, logits, actions, old_logp, adv, returns, old_value,
+                       value, valid, out, new_logp, dlogits, dvalue);
+  else if (cfg.A <= 18)
+    hipLaunchKernelGGL(k_ppo_loss_rows<18>, g, b, 0, st, cfg, logits, actions, old_logp, adv, returns, old_value,
+                       value, valid, out, new_logp, dlogits, dvalue);
+  else if (cfg.A <= 32)
+    hipLaunchKernelGGL(k_ppo_loss_rows<32>, g, b, 0, st, cfg, logits, actions, old_logp, adv, returns, old_value,
+                       value, valid, out, new_logp, dlogits, dvalue);
+  else
+    hipLaunchKernelGGL(k_ppo_loss, g, b, 0, st, cfg, logits, actions, old_logp, adv, returns, old_value, value,
+                       valid, out, new_logp, dlogits, dvalue);
+}
+
 // g *= max_norm / (norm + 1e-6) when norm = sqrt(*sq) exceeds max_norm; the
 // norm before clipping is left in *norm_out.
 __global__ __launch_bounds__(256) void k_clip_scale(float* __restrict__ g, long n, const float* __restrict__ sq,
@@ -295,8 +485,8 @@ int ttrl_ppo_loss(ttrl_ctx* ctx, int B, int A, const float* logits, const int* a
   TTRL_REQUIRE(B > 0 && A > 0, "ttrl_ppo_loss: B and A must be positive (got %d, %d)", B, A);
   TTRL_REQUIRE(clip_eps > 0.f && value_clip_eps > 0.f, "ttrl_ppo_loss: clip ranges must be positive");
   PpoCfg cfg{B, A, clip_eps, value_clip_eps, value_coef, entropy_coef, A, 1, 0};
-  hipLaunchKernelGGL(k_ppo_loss, dim3(1), dim3(kRedThreads), 0, stream_of(ctx), cfg, logits, actions, old_logp,
-                     advantages, returns, old_values, values, valid, out4, new_logp, dlogits, dvalues);
+  launch_ppo_loss(stream_of(ctx), cfg, logits, actions, old_logp, advantages, returns, old_values, values, valid, out4,
+                  new_logp, dlogits, dvalues);
   return check_launch("ttrl_ppo_loss");
 }
 
@@ -310,8 +500,8 @@ int ttrl_ppo_loss_packed(ttrl_ctx* ctx, int B, int A, const float* head, const i
   TTRL_REQUIRE(B > 0 && A > 0, "ttrl_ppo_loss_packed: B and A must be positive (got %d, %d)", B, A);
   TTRL_REQUIRE(clip_eps > 0.f && value_clip_eps > 0.f, "ttrl_ppo_loss_packed: clip ranges must be positive");
   PpoCfg cfg{B, A, clip_eps, value_clip_eps, value_coef, entropy_coef, A + 1, A + 1, 1};
-  hipLaunchKernelGGL(k_ppo_loss, dim3(1), dim3(kRedThreads), 0, stream_of(ctx), cfg, head, actions, old_logp,
-                     advantages, returns, old_values, head + A, valid, out5, new_logp, dhead, dhead + A);
+  launch_ppo_loss(stream_of(ctx), cfg, head, actions, old_logp, advantages, returns, old_values, head + A, valid, out5,
+                  new_logp, dhead, dhead + A);
   return check_launch("ttrl_ppo_loss_packed");
 }
 
