@@ -562,6 +562,16 @@ int ttrl_sac_fused_adam_parts(const ttrl_sac_fused_desc* desc, int stage, int* p
  * (ttrl/algos/grads.py:46-60), added to its value when accumulate_grad_sq. */
 int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v_s, long n, int* step, float lr,
                    float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq);
+/* ttrl_clip_grad_norm then ttrl_adam_step (ttrl/algos/grads.py:13-43, then
+ * ttrl/engine/optim/adam.py:93-134) with one read of g: norm = sqrt(sum
+ * g^2); when norm > max_norm the step reads g * max_norm / (norm + 1e-6)
+ * and writes that clipped g back, as the clip leaves it, else it reads g.
+ * Same parameters, moments and gradient as the two calls.  *sq_out and
+ * *norm_out (nullable) receive sum g^2 and the norm before clipping;
+ * grad_sq as in ttrl_adam_step, over the clipped gradient. */
+int ttrl_adam_step_clipped(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
+                           float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                           int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out);
 /* ttrl_adam_step with the same kernels and results, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops): no context
  * and no allocation of any kind.  It enqueues on `stream` (a hipStream_t;

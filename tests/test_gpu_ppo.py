@@ -121,3 +121,36 @@ def test_clip_grad_norm_device(device, max_norm):
     ref, ref_norm = oppo.clip_grad_norm(g, max_norm)
     assert abs(norm.numpy()[0] - ref_norm) < 1e-5 * ref_norm
     assert _rel(gd.numpy(), ref) < 1e-6
+
+
+@pytest.mark.parametrize("n,max_norm", [(1_687_206, 0.5), (1_687_206, 1e6), (10_007, 0.05)])
+def test_clipped_adam_step_is_the_clip_then_the_step(device, n, max_norm):
+    """ttrl_adam_step_clipped against ttrl_clip_grad_norm followed by
+    ttrl_adam_step, bit for bit: parameters, moments, the gradient left in
+    place, the norm, the sum of squares and the update count, over two
+    steps (a ragged tail, clipping on and off)."""
+    from ttrl_amd.engine.tensor import DeviceArray, to_device
+
+    rng = np.random.default_rng(n)
+    p0 = rng.uniform(-1, 1, n).astype(np.float32)
+    g0 = rng.normal(0, 0.01, n).astype(np.float32)
+    runs = []
+    for fused in (False, True):
+        p, g = to_device(p0, device), to_device(g0, device)
+        S, V = DeviceArray(device, (n,)), DeviceArray(device, (n,))
+        S.fill(0.0)
+        V.fill(0.0)
+        step = to_device(np.zeros(1, np.int32), device, np.int32)
+        sq, norm, gsq = DeviceArray(device, (1,)), DeviceArray(device, (1,)), DeviceArray(device, (1,))
+        hyper = (C.c_float(2.5e-4), C.c_float(0.9), C.c_float(0.999), C.c_float(1e-5), C.c_float(0.0))
+        for _ in range(2):
+            if fused:
+                device.call("ttrl_adam_step_clipped", p.vp, g.vp, S.vp, V.vp, C.c_long(n), step.vp, *hyper, gsq.vp, 0,
+                            C.c_float(max_norm), sq.vp, norm.vp)
+            else:
+                device.call("ttrl_clip_grad_norm", g.vp, C.c_long(n), C.c_float(max_norm), sq.vp, norm.vp)
+                device.call("ttrl_adam_step", p.vp, g.vp, S.vp, V.vp, C.c_long(n), step.vp, *hyper, gsq.vp, 0)
+        runs.append([x.numpy() for x in (p, g, S, V, sq, norm, gsq)] + [step.numpy()])
+    for name, a, b in zip(("p", "g", "S", "V", "sq", "norm", "grad_sq", "step"), *runs):
+        assert np.array_equal(a, b), name
+    assert runs[1][-1][0] == 2

@@ -44,17 +44,25 @@ __device__ __forceinline__ void adam4(f32x4& pv, const f32x4& gv, f32x4& sv, f32
   }
 }
 
+// A gradient scale applied as the step reads g (NoScale: none).
+struct NoScale {
+  static constexpr bool kOn = false;
+  __device__ float operator()() const { return 1.f; }
+};
+
 // The update of float4s map(j), j = first, first + step, ... below end,
 // g^2 added to gsq in that order.  The next float4's loads are in flight
 // while one is computed, and the first float4's are issued before the
-// step's scalars are formed (thread 0's double-precision powers), so those
-// latencies overlap.  Every thread of the workgroup calls it (the scalars'
-// barrier); alpha_t and eps_t receive the scalars.
-template <class Map>
+// step's scalars are formed (thread 0's double-precision powers) and, with
+// a Scale, before the gradient scale is formed, so those latencies overlap.
+// Every thread of the workgroup calls it (the scalars' barrier); alpha_t and
+// eps_t receive the scalars, *gscale the gradient scale.
+template <class Map, class Scale = NoScale>
 __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ S,
                                           float* __restrict__ V, long first, long end, long step,
                                           const int* __restrict__ stepc, float lr, float b1, float b2, float eps,
-                                          float wd, float& gsq, float* alpha_t, float* eps_t, Map map) {
+                                          float wd, float& gsq, float* alpha_t, float* eps_t, Map map,
+                                          Scale scale = Scale{}, float* gscale = nullptr) {
   f32x4* P = reinterpret_cast<f32x4*>(p);
   const f32x4* G = reinterpret_cast<const f32x4*>(g);
   f32x4* Sv = reinterpret_cast<f32x4*>(S);
@@ -69,6 +77,9 @@ __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __
     sv = Sv[i];
     vv = Vv[i];
   }
+  float gs = 1.f;
+  if constexpr (Scale::kOn) gs = scale();
+  if (gscale) *gscale = gs;
   adam_scalars(stepc, lr, b1, b2, eps, alpha_t, eps_t);
   const float at = *alpha_t, et = *eps_t;
   while (have) {
@@ -81,6 +92,10 @@ __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __
       gn = G[in];
       sn = Sv[in];
       vn = Vv[in];
+    }
+    if constexpr (Scale::kOn) {
+      gv = gv * gs;
+      if (gs != 1.f) const_cast<f32x4*>(G)[i] = gv;  // the clipped gradient, as the clip leaves it
     }
     adam4(pv, gv, sv, vv, b1, b2, wd, et, at, gsq);
     P[i] = pv;
@@ -104,22 +119,28 @@ struct Identity {
 // range and its partial sum of g^2 into partials[blk].  The same code serves
 // a single-range launch and a range of a multi-range launch, so both give
 // the same bits.
+template <class Scale = NoScale>
 __device__ __forceinline__ void adam_block(float* __restrict__ p, const float* __restrict__ g,
                                            float* __restrict__ S, float* __restrict__ V, long n,
                                            const int* __restrict__ step, float lr, float b1, float b2, float eps,
-                                           float wd, float* __restrict__ partials, int blk, int nblk) {
+                                           float wd, float* __restrict__ partials, int blk, int nblk,
+                                           Scale scale = Scale{}) {
   __shared__ float red[kOptThreads / 64];
-  float alpha_t, eps_t;
+  float alpha_t, eps_t, gs;
   float gsq = 0.f;
   const long n4 = n / 4;
   const long stride = long(nblk) * kOptThreads;
   adam_loop(p, g, S, V, blk * long(kOptThreads) + threadIdx.x, n4, stride, step, lr, b1, b2, eps, wd, gsq, &alpha_t,
-            &eps_t, Identity{});
+            &eps_t, Identity{}, scale, &gs);
   // Tail (n % 4) handled by block 0.
   if (blk == 0) {
     for (long i = n4 * 4 + threadIdx.x; i < n; i += kOptThreads) {
 #pragma clang fp contract(off)
-      const float graw = g[i];
+      float graw = g[i];
+      if constexpr (Scale::kOn) {
+        graw *= gs;
+        if (gs != 1.f) const_cast<float*>(g)[i] = graw;
+      }
       gsq += graw * graw;
       const float gg = wd != 0.f ? graw + wd * p[i] : graw;
       V[i] = gg * gg + b2 * V[i];
@@ -136,6 +157,40 @@ __global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, con
                                                       const int* __restrict__ step, float lr, float b1, float b2,
                                                       float eps, float wd, float* __restrict__ partials) {
   adam_block(p, g, S, V, n, step, lr, b1, b2, eps, wd, partials, int(blockIdx.x), int(gridDim.x));
+}
+
+// The global-norm clip's scale (k_clip_scale's) from the sum of g^2 left as
+// partial sums: every workgroup adds them as k_finish does, so each forms
+// the same sum; workgroup 0 stores it and the norm.
+struct ClipScale {
+  static constexpr bool kOn = true;
+  const float* parts;
+  int nparts;
+  float max_norm;
+  float* sq_out;
+  float* norm_out;
+  __device__ float operator()() const {
+    __shared__ float red[kOptThreads / 64];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += parts[i];
+    const float sq = block_sum<kOptThreads>(s, red);
+    const double total = std::sqrt(double(sq));
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      if (sq_out) *sq_out = sq;
+      if (norm_out) *norm_out = float(total);
+    }
+    return total > double(max_norm) ? float(double(max_norm) / (total + 1e-6)) : 1.f;
+  }
+};
+
+// clip_grad_norm and the step in one pass over g: the step reads g times the
+// clip's scale and, when that is not 1, writes the clipped g back.
+__global__ __launch_bounds__(kOptThreads) void k_adam_clip(float* __restrict__ p, float* __restrict__ g,
+                                                           float* __restrict__ S, float* __restrict__ V, long n,
+                                                           const int* __restrict__ step, float lr, float b1,
+                                                           float b2, float eps, float wd,
+                                                           float* __restrict__ partials, ClipScale clip) {
+  adam_block(p, g, S, V, n, step, lr, b1, b2, eps, wd, partials, int(blockIdx.x), int(gridDim.x), clip);
 }
 
 // Up to kMultiRanges deferred Adam ranges and a Polyak blend in one launch:
@@ -998,6 +1053,29 @@ int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v
   hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
                      accumulate_grad_sq);
   return check_launch("ttrl_adam_step");
+}
+
+int ttrl_adam_step_clipped(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
+                           float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                           int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out) {
+  TTRL_REQUIRE(ctx, "ttrl_adam_step_clipped: null ctx");
+  int rc = check_adam_args(p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, "ttrl_adam_step_clipped");
+  if (rc) return rc;
+  TTRL_REQUIRE(max_norm > 0.f, "ttrl_adam_step_clipped: max_norm must be > 0, got %g", double(max_norm));
+  // the norm's partial sums as ttrl_sum_squares forms them, so every
+  // workgroup's sum is the one ttrl_clip_grad_norm forms
+  long wsf = 0;
+  float* ws = ctx_workspace(ctx, &wsf);
+  const unsigned blocks = grid_for(n, 4), sq_blocks = grid_for(n, 4);
+  TTRL_REQUIRE(wsf >= long(blocks) + sq_blocks, "ttrl_adam_step_clipped: workspace too small");
+  float* sq_parts = ws + blocks;
+  hipStream_t st = stream_of(ctx);
+  hipLaunchKernelGGL(k_sumsq, dim3(sq_blocks), dim3(kOptThreads), 0, st, g, n, sq_parts);
+  hipLaunchKernelGGL(k_adam_clip, dim3(blocks), dim3(kOptThreads), 0, st, p, g, m_s, v_s, n, step, lr, beta1, beta2,
+                     eps, weight_decay, ws, ClipScale{sq_parts, int(sq_blocks), max_norm, sq_out, norm_out});
+  hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
+                     accumulate_grad_sq);
+  return check_launch("ttrl_adam_step_clipped");
 }
 
 int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, float* v_s, long n, int* step,

@@ -395,10 +395,8 @@ class PPOLearner:
     def _step(self) -> None:
         dev = self.device
         self._forward_backward()
-        grad = self.optimizer.arena_grads()
-        dev.call("ttrl_clip_grad_norm", grad.vp, C.c_long(grad.numel), C.c_float(self.cfg.max_grad_norm),
-                 self._sq.vp, C.c_void_p(self._metrics.ptr + 4 * 5))
-        self.optimizer.step()
+        # clip_grad_norm and the Adam step with one read of the gradient
+        self.optimizer.step_clipped(self.cfg.max_grad_norm, self._sq.vp, C.c_void_p(self._metrics.ptr + 4 * 5))
         r = self._res
         dev.call("ttrl_step_end", self._counter.vp, self._metrics.vp, len(self.METRICS), r.ring.vp, r.slots)
 
