@@ -3,9 +3,10 @@
 // weight gradient and the first launch of the input gradient (its first
 // four residue classes) can run as one paired launch, which saves a launch
 // but makes both problems take one tile shape; at large batches the two as
-// separate launches, each with its own tile shape, are faster.  The plain
-// call times both once per geometry (outside capture, on scratch outputs)
-// and keeps the faster for the context.
+// separate launches, each with its own tile shape, are faster.  Both calls
+// (the plain one and the one that leaves the weight gradient's split-K
+// partials to the optimizer step) time the two ways once per geometry
+// (outside capture, on scratch outputs) and keep the faster for the context.
 //   dW = sum over taps of X-slice^T dY  ttrl/engine/conv/backward.py:45-78
 //   dX = conv_transpose2d(dY, W)        ttrl/engine/conv/backward.py:33-42
 #include "conv.hpp"
@@ -38,14 +39,23 @@ int conv_backward_pair(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_s
   return rc;
 }
 
-// The two gradients as separate launches, each GEMM with its own plan.
+// The two gradients as separate launches, each GEMM with its own plan; bank
+// as for conv_backward_pair.
 template <int MODE>
 int conv_backward_split(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
                         const float* wt, float* dwt, float* db, float beta_w, float* dx, const float* xmask,
-                        float beta_x, long reserved) {
+                        float beta_x, long reserved, float* bank = nullptr, ttrl_grad_source* out = nullptr) {
   constexpr unsigned kDw = MODE == kPatchGeneral ? kConvGeneralCfgs : kConvDwCfgs;
   const ConvDwProblem<MODE> w = conv_dw_problem<MODE>(g, x, x_scale, dy, dwt, db, beta_w);
-  int rc = run_gemm<kDw>(ctx, w.la, w.lb, w.ep, w.q.M, w.q.N, w.q.K, 1, "ttrl_conv2d_backward", reserved);
+  int rc = TTRL_OK;
+  if (bank) {
+    GemmPlan plan{};
+    rc = run_gemm_deferred<kDw>(ctx, w.la, w.lb, w.ep, w.q.M, w.q.N, w.q.K, 1, "ttrl_conv2d_backward_deferred",
+                                &plan, bank, kGradBankFloats);
+    if (rc == TTRL_OK) *out = conv_dw_source(g, x_scale, dwt, db, bank, plan);
+  } else {
+    rc = run_gemm<kDw>(ctx, w.la, w.lb, w.ep, w.q.M, w.q.N, w.q.K, 1, "ttrl_conv2d_backward", reserved);
+  }
   for (int c0 = 0; c0 < g.S * g.S && rc == TTRL_OK; c0 += kMaxGroups) {
     const ConvDxProblem d = conv_dx_problem(g, c0, dy, wt, dx, xmask, x_scale, beta_x);
     rc = run_gemm<kConvDxCfgs>(ctx, d.la, d.lb, d.ep, d.q.M, d.q.N, d.q.K, d.q.groups, "ttrl_conv2d_backward",
@@ -61,10 +71,10 @@ int conv_backward_split(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_
 // taken for at most 4096 output pixels, where the saved launch matters most.
 template <int MODE>
 bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
-                    const float* wt, const float* xmask, long reserved) {
+                    const float* wt, const float* xmask, long reserved, float* bank) {
   char keybuf[192];
-  snprintf(keybuf, sizeof(keybuf), "ttrl_conv2d_backward:pair|%d|%d|%d|%d|%d|%d|%d|%d|%d|%d|%ld|%d", MODE, g.B, g.C,
-           g.H, g.W, g.O, g.KH, g.KW, g.S, g.P, reserved, xmask ? 1 : 0);
+  snprintf(keybuf, sizeof(keybuf), "ttrl_conv2d_backward:pair|%d|%d|%d|%d|%d|%d|%d|%d|%d|%d|%ld|%d|%d", MODE, g.B,
+           g.C, g.H, g.W, g.O, g.KH, g.KW, g.S, g.P, reserved, xmask ? 1 : 0, bank ? 1 : 0);
   const std::string key(keybuf);
   if (const GemmPlan* hit = ctx_plan_find(ctx, key)) return hit->cfg == 1;
   bool pair = long(g.M) <= 4096;
@@ -76,13 +86,14 @@ bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scal
       float *sw = out, *sb = out + nw, *sx = out + nw + g.O;
       hipStream_t st = stream_of(ctx);
       int rc = TTRL_OK;
+      ttrl_grad_source src{};  // the deferred form's partials go to the bank the real call then overwrites
       auto paired = [&] {
         if (rc == TTRL_OK) rc = conv_backward_pair<MODE>(ctx, g, x, x_scale, dy, wt, sw, sb, 0.f, sx, xmask, 0.f,
-                                                         reserved);
+                                                         reserved, bank, &src);
       };
       auto split = [&] {
         if (rc == TTRL_OK) rc = conv_backward_split<MODE>(ctx, g, x, x_scale, dy, wt, sw, sb, 0.f, sx, xmask, 0.f,
-                                                          reserved);
+                                                          reserved, bank, &src);
       };
       paired();  // first runs: each GEMM's own plan is tuned here
       split();
@@ -104,10 +115,12 @@ bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scal
 template <int MODE>
 int conv_backward_chosen(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
                          const float* wt, float* dwt, float* db, float beta_w, float* dx, const float* xmask,
-                         float beta_x, long reserved) {
-  if (pair_is_faster<MODE>(ctx, g, x, x_scale, dy, wt, xmask, reserved))
-    return conv_backward_pair<MODE>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved);
-  return conv_backward_split<MODE>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved);
+                         float beta_x, long reserved, float* bank = nullptr, ttrl_grad_source* out = nullptr) {
+  if (pair_is_faster<MODE>(ctx, g, x, x_scale, dy, wt, xmask, reserved, bank))
+    return conv_backward_pair<MODE>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved, bank,
+                                    out);
+  return conv_backward_split<MODE>(ctx, g, x, x_scale, dy, wt, dwt, db, beta_w, dx, xmask, beta_x, reserved, bank,
+                                   out);
 }
 
 }  // namespace
@@ -134,10 +147,10 @@ int ttrl_conv2d_backward_deferred(ttrl_ctx* ctx, const ttrl_conv_geom* geom, con
   }
   float* b = ctx_grad_bank(ctx, bank);
   if (patch_mode(g, input_aligned(g, x)) == kPatchNhwcVec)
-    return conv_backward_pair<kPatchNhwcVec>(ctx, g, x, x_scale, dy, wt, dwt, db, 0.f, dx, xmask, beta_x, reserved, b,
-                                             out);
-  return conv_backward_pair<kPatchGeneral>(ctx, g, x, x_scale, dy, wt, dwt, db, 0.f, dx, xmask, beta_x, reserved, b,
-                                           out);
+    return conv_backward_chosen<kPatchNhwcVec>(ctx, g, x, x_scale, dy, wt, dwt, db, 0.f, dx, xmask, beta_x, reserved,
+                                               b, out);
+  return conv_backward_chosen<kPatchGeneral>(ctx, g, x, x_scale, dy, wt, dwt, db, 0.f, dx, xmask, beta_x, reserved,
+                                             b, out);
 }
 
 int ttrl_conv2d_backward(ttrl_ctx* ctx, const ttrl_conv_geom* geom, const void* x, float x_scale, const float* dy,

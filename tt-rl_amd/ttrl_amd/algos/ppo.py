@@ -340,6 +340,15 @@ class PPOLearner:
         self.net = self._build_net()
         self.params = list(self.net.parameters())
         self.optimizer = Adam(self.params, lr=cfg.lr, eps=cfg.adam_eps)
+        # Each convolution's weight-gradient split-K partials wait in a
+        # gradient bank of the device context; the step forms them all in one
+        # launch when it settles the gradients before the clip.
+        from ttrl_amd.engine.conv import Conv2d
+        from ttrl_amd.nets.acting import _walk_modules
+
+        convs = [m for _, m in _walk_modules(self.net) if isinstance(m, Conv2d)]
+        for bank, conv in enumerate(convs[:4]):
+            conv.defer_bank = bank
         self._rng = np.random.default_rng(seed)
         self.frame_count = 0
         self.update_count = 0
