@@ -13,8 +13,9 @@ namespace ttrl {
 
 // The step's fused scalars (alpha_t, eps_t) at update count t.
 // adam_scalars forms them from the count *step + 1 once per workgroup, by
-// thread 0 (its loads issued before the call stay in flight while it does);
-// every thread of the workgroup calls it (a barrier).
+// thread 0; every thread of the workgroup calls it (a barrier).  A wave's
+// loads complete in the order they were issued, so thread 0's wait for the
+// count also waits for every load issued before it.
 __device__ __forceinline__ void adam_scalars_at(int t, float lr, float b1, float b2, float eps, float& alpha_t,
                                                 float& eps_t) {
   const double bc1 = 1.0 - pow(double(b1), double(t));
@@ -23,13 +24,20 @@ __device__ __forceinline__ void adam_scalars_at(int t, float lr, float b1, float
   alpha_t = float(double(lr) * (1.0 - double(b1)) / bc1 / c);
   eps_t = float(double(eps) / c);
 }
-__device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float lr, float b1, float b2, float eps,
-                                             float* alpha_t, float* eps_t) {
+// adam_scalars_of takes the count the caller read (the same in every
+// thread); a caller that reads it before its other loads waits for no
+// later load when thread 0 uses it.
+__device__ __forceinline__ void adam_scalars_of(int step, float lr, float b1, float b2, float eps, float* alpha_t,
+                                                float* eps_t) {
   __shared__ float sc[2];
-  if (threadIdx.x == 0) adam_scalars_at(*step + 1, lr, b1, b2, eps, sc[0], sc[1]);
+  if (threadIdx.x == 0) adam_scalars_at(step + 1, lr, b1, b2, eps, sc[0], sc[1]);
   __syncthreads();
   *alpha_t = sc[0];
   *eps_t = sc[1];
+}
+__device__ __forceinline__ void adam_scalars(const int* __restrict__ step, float lr, float b1, float b2, float eps,
+                                             float* alpha_t, float* eps_t) {
+  adam_scalars_of(*step, lr, b1, b2, eps, alpha_t, eps_t);
 }
 
 // The update of one parameter p with gradient graw; graw^2 is added to gsq.

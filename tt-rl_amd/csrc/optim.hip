@@ -289,7 +289,10 @@ constexpr int kSumLds = 1024;    // terms of an ordered sum staged in LDS
 // tr + 16 of one float4 column), its slices of u and v staged in LDS, so
 // each workgroup reads [batch][32] of u and [batch][64] of v however wide
 // the layer is, and a layer of 3136 x 512 takes 784 workgroups (one wave of
-// the chip's resident workgroups with the rest of the step).
+// the chip's resident workgroups with the rest of the step).  The bias's
+// gradient (sum_b v[b][c]) is formed by the first row band's tiles, from
+// the rows of v they have staged: lanes 0 .. kTileCols/4 - 1 of wave 0 take
+// one float4 of the tile's columns each.
 constexpr int kTileRows = 32, kTileCols = 64, kTileBatch = 32;
 constexpr int kTileBand = kOptThreads / (kTileCols / 4);  // tile rows one pass of the workgroup covers
 constexpr int kTileOuts = kTileRows / kTileBand;
@@ -309,7 +312,7 @@ struct GradSrc {
   const float* v;
   FDiv dc;         // division by cols
   int block0, blocks;
-  int tiled, ntc, ntiles;  // tiled outer product: tiles per row band, weight tiles (then the bias's blocks)
+  int tiled, ntc, ntiles;  // tiled outer product: tiles per row band, tiles (the first band's also form the bias)
 };
 
 __device__ __forceinline__ f32x4 source_grad(const GradSrc& s, int q, bool* bias, int* qq) {
@@ -406,6 +409,34 @@ __device__ __forceinline__ void stage_outer(const GradSrc& s, const OuterSlice& 
   for (int i = kOptThreads + tid; i < nv; i += kOptThreads) vs[i] = s.v[i];
   __syncthreads();
 }
+// stage_outer in two halves when the batch is at most kOuterChunk rows:
+// issue_stage loads the thread's rows (every load unconditional: threads
+// past the slice repeat its last row or v's last element, and write
+// nothing), commit_stage writes them to LDS (with v past kOptThreads
+// elements) and waits for the workgroup.
+struct StageLoads {
+  float u[kOuterChunk];
+  float v;
+};
+__device__ __forceinline__ StageLoads issue_stage(const GradSrc& s, const OuterSlice& o) {
+  const int tid = threadIdx.x, nv = s.batch * s.cols;
+  const int rr = min(tid, max(o.R - 1, 0));
+  StageLoads l;
+#pragma unroll
+  for (int i = 0; i < kOuterChunk; ++i) l.u[i] = s.u[long(min(i, s.batch - 1)) * s.rows + o.r_lo + rr];
+  l.v = s.v[min(tid, nv - 1)];
+  return l;
+}
+__device__ __forceinline__ void commit_stage(const GradSrc& s, const OuterSlice& o, const StageLoads& l, float* us,
+                                             float* vs) {
+  const int tid = threadIdx.x, nv = s.batch * s.cols;
+  if (tid < nv) vs[tid] = l.v;
+#pragma unroll
+  for (int i = 0; i < kOuterChunk; ++i)
+    if (tid < o.R && i < s.batch) us[i * o.R + tid] = l.u[i];
+  for (int i = kOptThreads + tid; i < nv; i += kOptThreads) vs[i] = s.v[i];
+  __syncthreads();
+}
 // source_grad of a staged outer-product source: the same sums in the same
 // order (b from zero, fmaf(u, v, acc); the bias adds v), read from LDS.
 __device__ __forceinline__ f32x4 outer_grad_staged(const GradSrc& s, const OuterSlice& o, const float* us,
@@ -472,12 +503,17 @@ __device__ __forceinline__ void commit_outer_tile(const OuterTileLoads& l, float
 }
 // The thread's kTileOuts float4s (tile rows tr + kTileBand * o, float4
 // column tc4): the same sums in the same order as source_grad (b from zero,
-// fmaf(u, v, acc)).
-__device__ __forceinline__ void outer_grad_tile(const GradSrc& s, const float* us, const float* vs, int tr, int tc4,
+// fmaf(u, v, acc)).  The staged rows past the batch hold zeros, and adding
+// fmaf(0, 0, acc) = acc + 0 leaves acc's bits as they are (acc starts at +0
+// and a sum rounded to nearest is never -0 unless both terms are), so the
+// loop runs over all kTileBatch rows, unrolled by 8 (fully, its hoisted
+// reads would not fit the registers).
+__device__ __forceinline__ void outer_grad_tile(const float* us, const float* vs, int tr, int tc4,
                                                 f32x4 (&acc)[kTileOuts]) {
 #pragma unroll
   for (int o = 0; o < kTileOuts; ++o) acc[o] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int b = 0; b < s.batch; ++b) {
+#pragma unroll 8
+  for (int b = 0; b < kTileBatch; ++b) {
     const f32x4 v = reinterpret_cast<const f32x4*>(vs)[b * (kTileCols / 4) + tc4];
 #pragma unroll
     for (int o = 0; o < kTileOuts; ++o) {
@@ -487,35 +523,48 @@ __device__ __forceinline__ void outer_grad_tile(const GradSrc& s, const float* u
     }
   }
 }
-// Where workgroup t of a tiled source works: its tile (t < ntiles; the
-// thread's float4 q[o] of the weight, ok[o] false past the block's rows) or
-// a bias block (q[0] its bias float4, ok[0] inside the bias).
+// The bias float4 of the tile's float4 column tc4: sum_b v[b][c] in the
+// order source_grad adds it (b from zero; the zero rows past the batch, as
+// above, change nothing).
+__device__ __forceinline__ f32x4 outer_bias_tile(const float* vs, int tc4) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+  for (int b = 0; b < kTileBatch; ++b) {
+    const f32x4 v = reinterpret_cast<const f32x4*>(vs)[b * (kTileCols / 4) + tc4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = fmaf(1.f, v[j], acc[j]);
+  }
+  return acc;
+}
+// Where workgroup t of a tiled source works: its tile (the thread's float4
+// q[o] of the weight, ok[o] false past the block's rows) and, in the first
+// row band of a source with a bias, the bias: bias_wave for wave 0 (uniform
+// over the wave), bias_lane for its lanes that step bias float4 qb (the
+// tile's float4 column tc4 = tid; the other lanes' qb repeats the last).
 struct TileSpot {
   int r0, c0, tr, tc4;
   int q[kTileOuts];
   bool ok[kTileOuts];
-  bool weight;
+  bool bias_wave, bias_lane;
+  int qb;
 };
 __device__ __forceinline__ TileSpot tile_spot(const GradSrc& s, int t) {
   const int tid = threadIdx.x;
   TileSpot o{};
-  o.weight = t < s.ntiles;
   o.tr = tid / (kTileCols / 4);
   o.tc4 = tid % (kTileCols / 4);
-  if (o.weight) {
-    const int band = t / s.ntc;
-    o.r0 = band * kTileRows;
-    o.c0 = (t - band * s.ntc) * kTileCols;
+  const int band = t / s.ntc;
+  o.r0 = band * kTileRows;
+  o.c0 = (t - band * s.ntc) * kTileCols;
 #pragma unroll
-    for (int k = 0; k < kTileOuts; ++k) {
-      const int row = o.r0 + o.tr + kTileBand * k;
-      o.ok[k] = row < s.rows;
-      o.q[k] = int((long(row) * s.cols + o.c0 + 4 * o.tc4) / 4);
-    }
-  } else {
-    o.q[0] = s.nw4 + (t - s.ntiles) * kOptThreads + tid;
-    o.ok[0] = o.q[0] < s.nw4 + s.nb4;
+  for (int k = 0; k < kTileOuts; ++k) {
+    const int row = o.r0 + o.tr + kTileBand * k;
+    o.ok[k] = row < s.rows;
+    o.q[k] = int((long(row) * s.cols + o.c0 + 4 * o.tc4) / 4);
   }
+  o.bias_wave = band == 0 && s.nb4 > 0 && tid < 64;
+  o.bias_lane = o.bias_wave && tid < kTileCols / 4;
+  o.qb = o.c0 / 4 + min(tid, kTileCols / 4 - 1);
   return o;
 }
 
@@ -595,6 +644,12 @@ template <bool STORE>
 __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_adam_src(AdamSrcArgs a) {
   __shared__ float red[kOptThreads / 64];
   __shared__ float us[kOuterULds], vs[kOuterLds];
+  // the update count before any other load, through the scalar cache (one
+  // read per wavefront of one word every workgroup reads; no store of this
+  // launch reaches it): thread 0, forming the step's scalars from it, then
+  // waits for none of the vector loads
+  typedef __attribute__((address_space(1))) const int global_int;
+  const int stepc = *(global_int*)a.step;
   warm_kernargs<int(sizeof(AdamSrcArgs))>();
   const int blk = int(blockIdx.x);
   float alpha_t, eps_t;
@@ -610,43 +665,54 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
       if (i < a.nsrc && blk >= a.src[i].block0) k = i;
     const GradSrc& s = a.src[k];
     if (s.tiled) {
-      // a tile (kTileOuts float4s per thread, both slices staged) or a bias block
+      // a tile (kTileOuts float4s per thread, both slices staged), in the
+      // first row band with the bias's float4s of its columns
       const TileSpot t = tile_spot(s, blk - s.block0);
-      const int nout = t.weight ? kTileOuts : 1;
       // the operand slices' loads first, then the parameters' and moments',
-      // all in flight while the scalars are formed
-      OuterTileLoads tl;
-      if (t.weight) tl = issue_outer_tile(s, t.r0, t.c0);
+      // all in flight while the scalars are formed (unconditional, so that
+      // thread 0's wait for the count waits for none of them; a row past the
+      // block reads the block's first float4 and stores nothing)
+      const OuterTileLoads tl = issue_outer_tile(s, t.r0, t.c0);
       long i[kTileOuts];
-      f32x4 pv[kTileOuts] = {}, sv[kTileOuts] = {}, vv[kTileOuts] = {};
+      f32x4 pv[kTileOuts], sv[kTileOuts], vv[kTileOuts];
 #pragma unroll
       for (int o = 0; o < kTileOuts; ++o) {
-        i[o] = t.weight ? s.w4 + t.q[o] : s.b4 + (t.q[0] - s.nw4);
-        if (o < nout && t.ok[o]) {
-          pv[o] = P[i[o]];
-          sv[o] = Sv[i[o]];
-          vv[o] = Vv[i[o]];
-        }
+        i[o] = s.w4 + t.q[o];
+        const long il = t.ok[o] ? i[o] : s.w4;
+        pv[o] = P[il];
+        sv[o] = Sv[il];
+        vv[o] = Vv[il];
       }
-      adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
-      if (t.weight) commit_outer_tile(tl, us, vs);
+      // (left unset on waves that do not step the bias: a zero there would
+      // cost a copy that waits for the loads)
+      const long ib = s.b4 + t.qb;
+      f32x4 pb, sb, vb;
+      if (t.bias_wave) {
+        pb = P[ib];
+        sb = Sv[ib];
+        vb = Vv[ib];
+      }
+      adam_scalars_of(stepc, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+      commit_outer_tile(tl, us, vs);
       f32x4 gv[kTileOuts];
-      if (t.weight) {
-        outer_grad_tile(s, us, vs, t.tr, t.tc4, gv);
-      } else if (t.ok[0]) {
-        bool bias;
-        int qq;
-        gv[0] = source_grad(s, t.q[0], &bias, &qq);
-      }
+      outer_grad_tile(us, vs, t.tr, t.tc4, gv);
 #pragma unroll
       for (int o = 0; o < kTileOuts; ++o) {
-        if (o < nout && t.ok[o]) {
+        if (t.ok[o]) {
           if (STORE) Gd[i[o]] = gv[o];
           adam4(pv[o], gv[o], sv[o], vv[o], a.b1, a.b2, a.wd, eps_t, alpha_t, gsq);
           P[i[o]] = pv[o];
           Sv[i[o]] = sv[o];
           Vv[i[o]] = vv[o];
         }
+      }
+      if (t.bias_lane) {
+        const f32x4 gb = outer_bias_tile(vs, t.tc4);
+        if (STORE) Gd[ib] = gb;
+        adam4(pb, gb, sb, vb, a.b1, a.b2, a.wd, eps_t, alpha_t, gsq);
+        P[ib] = pb;
+        Sv[ib] = sb;
+        Vv[ib] = vb;
       }
       const float tot = block_sum<kOptThreads>(gsq, red);
       if (threadIdx.x == 0) a.partials[blk] = tot;
@@ -659,17 +725,28 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
     const int step = s.blocks * kOptThreads;
     int q = qb0 + int(threadIdx.x);
     // the first float4's parameters and moments in flight while the
-    // gradient's operands are staged and the scalars formed
+    // gradient's operands are staged and the scalars formed (unconditional,
+    // as in the tiles; a thread past the source reads its last float4)
     auto where = [&](int qv) { return qv >= s.nw4 ? s.b4 + (qv - s.nw4) : s.w4 + qv; };
-    f32x4 pv = {}, sv = {}, vv = {};
-    if (q < nq) {
-      const long i = where(q);
+    f32x4 pv, sv, vv;
+    {
+      const long i = where(min(q, nq - 1));
       pv = P[i];
       sv = Sv[i];
       vv = Vv[i];
     }
-    if (staged) stage_outer(s, o, us, vs);
-    adam_scalars(a.step, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+    // a staged slice of one chunk in flight too while thread 0 forms the
+    // scalars (the branches are uniform over the workgroup; a split-K
+    // source's partials are loaded after them: held across the scalars'
+    // arithmetic they would not fit the registers)
+    if (staged && s.batch <= kOuterChunk) {
+      const StageLoads sl = issue_stage(s, o);
+      adam_scalars_of(stepc, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+      commit_stage(s, o, sl, us, vs);
+    } else {
+      if (staged) stage_outer(s, o, us, vs);
+      adam_scalars_of(stepc, a.lr, a.b1, a.b2, a.eps, &alpha_t, &eps_t);
+    }
     for (bool first = true; q < nq; q += step, first = false) {
       bool bias;
       int qq;
@@ -730,21 +807,13 @@ __global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
   __shared__ float us[kOuterULds], vs[kOuterLds];
   if (s.tiled) {
     const TileSpot t = tile_spot(s, blk - s.block0);
-    if (t.weight) {
-      commit_outer_tile(issue_outer_tile(s, t.r0, t.c0), us, vs);
-      f32x4 gv[kTileOuts];
-      outer_grad_tile(s, us, vs, t.tr, t.tc4, gv);
+    commit_outer_tile(issue_outer_tile(s, t.r0, t.c0), us, vs);
+    f32x4 gv[kTileOuts];
+    outer_grad_tile(us, vs, t.tr, t.tc4, gv);
 #pragma unroll
-      for (int o = 0; o < kTileOuts; ++o)
-        if (t.ok[o]) reinterpret_cast<f32x4*>(s.gw)[t.q[o]] = gv[o];
-    } else if (t.ok[0]) {
-      bool bias;
-      int qq;
-      const f32x4 gv = source_grad(s, t.q[0], &bias, &qq);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (4 * qq + j < s.cols) s.gb[4 * qq + j] = gv[j];
-    }
+    for (int o = 0; o < kTileOuts; ++o)
+      if (t.ok[o]) reinterpret_cast<f32x4*>(s.gw)[t.q[o]] = gv[o];
+    if (t.bias_lane) reinterpret_cast<f32x4*>(s.gb)[t.qb] = outer_bias_tile(vs, t.tc4);
     return;
   }
   const int qb0 = (blk - s.block0) * kOptThreads;
@@ -923,8 +992,7 @@ int make_sources(int n, const ttrl_grad_source* srcs, const float* g, long gn, G
       }
     }
     d.block0 = b;
-    d.blocks = d.tiled ? d.ntiles + int(ceil_div(long(d.nb4), kOptThreads))
-                       : int(ceil_div(long(d.nw4) + d.nb4, kOptThreads));
+    d.blocks = d.tiled ? d.ntiles : int(ceil_div(long(d.nw4) + d.nb4, kOptThreads));
     b += d.blocks;
     out[c++] = d;
   }
