@@ -45,9 +45,13 @@ __device__ __forceinline__ void adam4(f32x4& pv, const f32x4& gv, f32x4& sv, f32
 }
 
 // A gradient scale applied as the step reads g (NoScale: none).
+// A step's gradient scale in two halves: issue() starts its loads, finish()
+// forms it from them (the step's scalars are formed in between).
 struct NoScale {
   static constexpr bool kOn = false;
-  __device__ float operator()() const { return 1.f; }
+  struct Loads {};
+  __device__ Loads issue() const { return {}; }
+  __device__ float finish(const Loads&) const { return 1.f; }
 };
 
 // The update of float4s map(j), j = first, first + step, ... below end,
@@ -63,6 +67,10 @@ __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __
                                           const int* __restrict__ stepc, float lr, float b1, float b2, float eps,
                                           float wd, float& gsq, float* alpha_t, float* eps_t, Map map,
                                           Scale scale = Scale{}, float* gscale = nullptr) {
+  // the update count first, through the scalar cache: thread 0's wait for
+  // it then waits for none of the first float4's loads, and the scalars'
+  // arithmetic runs while they are in flight
+  const int step_now = *(const __attribute__((address_space(1))) int*)stepc;
   f32x4* P = reinterpret_cast<f32x4*>(p);
   const f32x4* G = reinterpret_cast<const f32x4*>(g);
   f32x4* Sv = reinterpret_cast<f32x4*>(S);
@@ -77,10 +85,11 @@ __device__ __forceinline__ void adam_loop(float* __restrict__ p, const float* __
     sv = Sv[i];
     vv = Vv[i];
   }
+  const typename Scale::Loads sl = scale.issue();
+  adam_scalars_of(step_now, lr, b1, b2, eps, alpha_t, eps_t);
   float gs = 1.f;
-  if constexpr (Scale::kOn) gs = scale();
+  if constexpr (Scale::kOn) gs = scale.finish(sl);
   if (gscale) *gscale = gs;
-  adam_scalars(stepc, lr, b1, b2, eps, alpha_t, eps_t);
   const float at = *alpha_t, et = *eps_t;
   while (have) {
     const long jn = j + step;
@@ -162,6 +171,11 @@ __global__ __launch_bounds__(kOptThreads) void k_adam(float* __restrict__ p, con
 // The global-norm clip's scale (k_clip_scale's) from the sum of g^2 left as
 // partial sums: every workgroup adds them as k_finish does, so each forms
 // the same sum; workgroup 0 stores it and the norm.
+// The norm partials (nparts <= kOptMaxBlocks) are loaded kClipLoads to a
+// thread and summed in the order a loop over i = tid, tid + kOptThreads, ...
+// adds them.
+constexpr int kClipLoads = kOptMaxBlocks / kOptThreads;
+static_assert(kOptMaxBlocks % kOptThreads == 0, "whole loads per thread");
 struct ClipScale {
   static constexpr bool kOn = true;
   const float* parts;
@@ -169,10 +183,21 @@ struct ClipScale {
   float max_norm;
   float* sq_out;
   float* norm_out;
-  __device__ float operator()() const {
+  struct Loads {
+    float v[kClipLoads];
+  };
+  __device__ Loads issue() const {
+    Loads l;
+#pragma unroll
+    for (int k = 0; k < kClipLoads; ++k) l.v[k] = parts[min(int(threadIdx.x) + k * kOptThreads, nparts - 1)];
+    return l;
+  }
+  __device__ float finish(const Loads& l) const {
     __shared__ float red[kOptThreads / 64];
     float s = 0.f;
-    for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += parts[i];
+#pragma unroll
+    for (int k = 0; k < kClipLoads; ++k)
+      if (int(threadIdx.x) + k * kOptThreads < nparts) s += l.v[k];
     const float sq = block_sum<kOptThreads>(s, red);
     const double total = std::sqrt(double(sq));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
