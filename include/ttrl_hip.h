@@ -572,6 +572,15 @@ int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v
 int ttrl_adam_step_clipped(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
                            float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
                            int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out);
+/* ttrl_adam_step_clipped followed by ttrl_step_end(ctx, counter, metrics,
+ * n_metrics, ring, slots), the step end done by the step's finishing launch
+ * (one launch fewer; the same results as the two calls): the end of a
+ * replayed PPO minibatch step (ttrl/algos/ppo/learn.py:94-112).  metrics may
+ * hold the step's own norm_out. */
+int ttrl_adam_step_clipped_end(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
+                               float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                               int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out, int* counter,
+                               const float* metrics, int n_metrics, float* ring, int slots);
 /* ttrl_adam_step with the same kernels and results, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops): no context
  * and no allocation of any kind.  It enqueues on `stream` (a hipStream_t;

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import ppo as oppo
+from ttrl_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
@@ -154,3 +155,57 @@ def test_clipped_adam_step_is_the_clip_then_the_step(device, n, max_norm):
     for name, a, b in zip(("p", "g", "S", "V", "sq", "norm", "grad_sq", "step"), *runs):
         assert np.array_equal(a, b), name
     assert runs[1][-1][0] == 2
+
+
+def test_clipped_adam_step_with_the_step_end_is_the_two_calls(device):
+    """ttrl_adam_step_clipped_end against ttrl_adam_step_clipped followed by
+    ttrl_step_end, bit for bit: parameters, moments, gradient, norm, sums of
+    squares, update count, metric ring and step counter, over three steps
+    whose metrics hold the step's own norm (the PPO learner's layout) and
+    whose last one finds the ring full (the counter still advances)."""
+    from ttrl_amd.engine.tensor import DeviceArray, to_device
+
+    n, n_metrics, slots = 70001, 7, 2
+    rng = np.random.default_rng(3)
+    p0 = rng.uniform(-1, 1, n).astype(np.float32)
+    g0 = rng.normal(0, 0.01, n).astype(np.float32)
+    m0 = rng.normal(0, 1, n_metrics).astype(np.float32)
+    runs = []
+    for fused in (False, True):
+        p, g = to_device(p0, device), to_device(g0, device)
+        S, V = DeviceArray(device, (n,)), DeviceArray(device, (n,))
+        S.fill(0.0)
+        V.fill(0.0)
+        step = to_device(np.zeros(1, np.int32), device, np.int32)
+        counter = to_device(np.zeros(1, np.int32), device, np.int32)
+        metrics = to_device(m0, device)
+        ring = to_device(np.full((slots, n_metrics), -1.0, np.float32), device)
+        sq, gsq = DeviceArray(device, (1,)), DeviceArray(device, (1,))
+        norm = C.c_void_p(metrics.ptr + 4 * 5)
+        hyper = (C.c_float(2.5e-4), C.c_float(0.9), C.c_float(0.999), C.c_float(1e-5), C.c_float(0.0))
+        for k in range(3):
+            args = (p.vp, g.vp, S.vp, V.vp, C.c_long(n), step.vp, *hyper, gsq.vp, 0, C.c_float(0.5 if k else 1e-3),
+                    sq.vp, norm)
+            if fused:
+                device.call("ttrl_adam_step_clipped_end", *args, counter.vp, metrics.vp, n_metrics, ring.vp, slots)
+            else:
+                device.call("ttrl_adam_step_clipped", *args)
+                device.call("ttrl_step_end", counter.vp, metrics.vp, n_metrics, ring.vp, slots)
+        runs.append([x.numpy() for x in (p, g, S, V, sq, gsq, metrics, ring, step, counter)])
+    for name, a, b in zip(("p", "g", "S", "V", "sq", "grad_sq", "metrics", "ring", "step", "counter"), *runs):
+        assert np.array_equal(a, b), name
+    assert runs[1][-2][0] == 3 and runs[1][-1][0] == 3
+    assert not np.array_equal(runs[1][7][0], np.full(n_metrics, -1.0, np.float32))
+
+
+def test_clipped_adam_step_with_the_step_end_refuses_a_bad_ring(device):
+    from ttrl_amd.engine.tensor import DeviceArray
+
+    lib = _lib.lib()
+    x = DeviceArray(device, (8,))
+    i = DeviceArray(device, (1,))
+    hyper = (C.c_float(1e-3), C.c_float(0.9), C.c_float(0.999), C.c_float(1e-8), C.c_float(0.0))
+    base = (device.ctx, x.vp, x.vp, x.vp, x.vp, C.c_long(8), i.vp, *hyper, None, 0, C.c_float(1.0), None, None)
+    assert lib.ttrl_adam_step_clipped_end(*base, None, x.vp, 2, x.vp, 1) == _lib.TTRL_EINVAL
+    assert lib.ttrl_adam_step_clipped_end(*base, i.vp, None, 2, x.vp, 1) == _lib.TTRL_EINVAL
+    assert lib.ttrl_adam_step_clipped_end(*base, i.vp, x.vp, -1, x.vp, 1) == _lib.TTRL_EINVAL

@@ -293,6 +293,29 @@ __global__ __launch_bounds__(kOptThreads) void k_finish(const float* __restrict_
   }
 }
 
+// k_finish that also ends a replayed learner step: the metric ring's row
+// ring[c][0..n) = metrics when 0 <= c < slots, c = *counter, then
+// *counter = c + 1 (what ttrl_step_end does in a launch of its own).
+__global__ __launch_bounds__(kOptThreads) void k_finish_end(const float* __restrict__ partials, int nparts,
+                                                            int* __restrict__ step, float* __restrict__ out,
+                                                            int accumulate, int* __restrict__ counter,
+                                                            const float* __restrict__ metrics, int n,
+                                                            float* __restrict__ ring, int slots) {
+  __shared__ float red[kOptThreads / 64];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += kOptThreads) s += partials[i];
+  const float tot = block_sum<kOptThreads>(s, red);
+  const int c = *counter;
+  if (c >= 0 && c < slots)
+    for (int i = threadIdx.x; i < n; i += kOptThreads) ring[long(c) * n + i] = metrics[i];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (out) *out = accumulate ? *out + tot : tot;
+    if (step) *step = *step + 1;
+    *counter = c + 1;
+  }
+}
+
 // ----------------------------------------------------- gradient sources ---
 //
 // A source's gradient is formed a float4 at a time: float4 q < nw4 covers
@@ -1148,27 +1171,65 @@ int ttrl_adam_step(ttrl_ctx* ctx, float* p, const float* g, float* m_s, float* v
   return check_launch("ttrl_adam_step");
 }
 
-int ttrl_adam_step_clipped(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
-                           float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
-                           int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out) {
-  TTRL_REQUIRE(ctx, "ttrl_adam_step_clipped: null ctx");
-  int rc = check_adam_args(p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, "ttrl_adam_step_clipped");
+}  // extern "C"
+
+namespace {
+// The clipped step's launches; the finishing one also ends a learner step
+// when `end` names its metric ring (counter non-null).
+struct StepEnd {
+  int* counter;
+  const float* metrics;
+  int n;
+  float* ring;
+  int slots;
+};
+int adam_step_clipped(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step, float lr,
+                      float beta1, float beta2, float eps, float weight_decay, float* grad_sq, int accumulate_grad_sq,
+                      float max_norm, float* sq_out, float* norm_out, const StepEnd& end, const char* name) {
+  TTRL_REQUIRE(ctx, "%s: null ctx", name);
+  int rc = check_adam_args(p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, name);
   if (rc) return rc;
-  TTRL_REQUIRE(max_norm > 0.f, "ttrl_adam_step_clipped: max_norm must be > 0, got %g", double(max_norm));
+  TTRL_REQUIRE(max_norm > 0.f, "%s: max_norm must be > 0, got %g", name, double(max_norm));
   // the norm's partial sums as ttrl_sum_squares forms them, so every
   // workgroup's sum is the one ttrl_clip_grad_norm forms
   long wsf = 0;
   float* ws = ctx_workspace(ctx, &wsf);
   const unsigned blocks = grid_for(n, 4), sq_blocks = grid_for(n, 4);
-  TTRL_REQUIRE(wsf >= long(blocks) + sq_blocks, "ttrl_adam_step_clipped: workspace too small");
+  TTRL_REQUIRE(wsf >= long(blocks) + sq_blocks, "%s: workspace too small", name);
   float* sq_parts = ws + blocks;
   hipStream_t st = stream_of(ctx);
   hipLaunchKernelGGL(k_sumsq, dim3(sq_blocks), dim3(kOptThreads), 0, st, g, n, sq_parts);
   hipLaunchKernelGGL(k_adam_clip, dim3(blocks), dim3(kOptThreads), 0, st, p, g, m_s, v_s, n, step, lr, beta1, beta2,
                      eps, weight_decay, ws, ClipScale{sq_parts, int(sq_blocks), max_norm, sq_out, norm_out});
-  hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
-                     accumulate_grad_sq);
-  return check_launch("ttrl_adam_step_clipped");
+  if (end.counter)
+    hipLaunchKernelGGL(k_finish_end, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
+                       accumulate_grad_sq, end.counter, end.metrics, end.n, end.ring, end.slots);
+  else
+    hipLaunchKernelGGL(k_finish, dim3(1), dim3(kOptThreads), 0, st, ws, int(blocks), step, grad_sq,
+                       accumulate_grad_sq);
+  return check_launch(name);
+}
+}  // namespace
+
+extern "C" {
+
+int ttrl_adam_step_clipped(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
+                           float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                           int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out) {
+  return adam_step_clipped(ctx, p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, grad_sq,
+                           accumulate_grad_sq, max_norm, sq_out, norm_out, StepEnd{}, "ttrl_adam_step_clipped");
+}
+
+int ttrl_adam_step_clipped_end(ttrl_ctx* ctx, float* p, float* g, float* m_s, float* v_s, long n, int* step,
+                               float lr, float beta1, float beta2, float eps, float weight_decay, float* grad_sq,
+                               int accumulate_grad_sq, float max_norm, float* sq_out, float* norm_out, int* counter,
+                               const float* metrics, int n_metrics, float* ring, int slots) {
+  TTRL_REQUIRE(counter, "ttrl_adam_step_clipped_end: null counter");
+  TTRL_REQUIRE(n_metrics >= 0 && slots >= 0 && (n_metrics == 0 || (metrics && ring)),
+               "ttrl_adam_step_clipped_end: bad metric ring");
+  return adam_step_clipped(ctx, p, g, m_s, v_s, n, step, lr, beta1, beta2, eps, weight_decay, grad_sq,
+                           accumulate_grad_sq, max_norm, sq_out, norm_out,
+                           StepEnd{counter, metrics, n_metrics, ring, slots}, "ttrl_adam_step_clipped_end");
 }
 
 int ttrl_adam_step_static(void* stream, float* p, const float* g, float* m_s, float* v_s, long n, int* step,

@@ -289,6 +289,7 @@ SIGNATURES = {
     "ttrl_sac_actor_loss": ([P, I, P, P, P, F, I, P, P, P, P, P], I),
     "ttrl_adam_step": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
     "ttrl_adam_step_clipped": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I, F, P, P], I),
+    "ttrl_adam_step_clipped_end": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I, F, P, P, P, P, I, P, I], I),
     "ttrl_adam_step_static": ([P, P, P, P, P, L, P, F, F, F, F, F, P, I], I),
     "ttrl_adam_step_deferred": ([P, P, P, P, P, L, P, F, F, F, F, F, I], I),
     "ttrl_adam_multi": ([P, I, C.POINTER(AdamRange), P, P, L, F], I),

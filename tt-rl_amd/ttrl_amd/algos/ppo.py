@@ -402,12 +402,13 @@ class PPOLearner:
         loss.backward()
 
     def _step(self) -> None:
-        dev = self.device
         self._forward_backward()
-        # clip_grad_norm and the Adam step with one read of the gradient
-        self.optimizer.step_clipped(self.cfg.max_grad_norm, self._sq.vp, C.c_void_p(self._metrics.ptr + 4 * 5))
+        # clip_grad_norm and the Adam step with one read of the gradient, its
+        # finishing launch also ending the step (the metric ring's row, the
+        # step counter)
         r = self._res
-        dev.call("ttrl_step_end", self._counter.vp, self._metrics.vp, len(self.METRICS), r.ring.vp, r.slots)
+        self.optimizer.step_clipped(self.cfg.max_grad_norm, self._sq.vp, C.c_void_p(self._metrics.ptr + 4 * 5),
+                                    end=(self._counter.vp, self._metrics.vp, len(self.METRICS), r.ring.vp, r.slots))
 
     def _capture(self) -> None:
         dev = self.device

@@ -234,20 +234,27 @@ class Adam(Optimizer):
                 p.grad = p._grad_slot
                 p._grad_owned = True
 
-    def step_clipped(self, max_norm: float, sq_out, norm_out) -> None:
+    def step_clipped(self, max_norm: float, sq_out, norm_out, end=None) -> None:
         """clip_grad_norm over the arena's gradient, then step(), with one
         read of the gradient (ttrl_adam_step_clipped): the same parameters,
         moments and clipped gradient as ttrl_clip_grad_norm followed by the
         step.  sq_out and norm_out (device float pointers, nullable) receive
-        sum(g^2) and the norm before clipping."""
+        sum(g^2) and the norm before clipping.  end = (counter, metrics, n,
+        ring, slots) also ends a replayed learner step as ttrl_step_end does,
+        in the step's finishing launch (ttrl_adam_step_clipped_end)."""
         if not max_norm > 0:
             raise ValueError(f"clip_grad_norm: max_norm must be > 0, got {max_norm}")
         self._arena_ready("step_clipped")
         settle_sums(self.device)
         a = self.arena
-        self.device.call("ttrl_adam_step_clipped", a.data.vp, a.grad.vp, self._m_flat.vp, self._v_flat.vp,
-                         C.c_long(a.numel), self._counter(len(self.params)), *self._hyper(), self.grad_sq.vp, 0,
-                         C.c_float(max_norm), sq_out, norm_out)
+        args = (a.data.vp, a.grad.vp, self._m_flat.vp, self._v_flat.vp, C.c_long(a.numel),
+                self._counter(len(self.params)), *self._hyper(), self.grad_sq.vp, 0, C.c_float(max_norm), sq_out,
+                norm_out)
+        if end is None:
+            self.device.call("ttrl_adam_step_clipped", *args)
+        else:
+            counter, metrics, n, ring, slots = end
+            self.device.call("ttrl_adam_step_clipped_end", *args, counter, metrics, int(n), ring, int(slots))
         self._finished()
 
     def step_deferred(self, slot: int) -> None:
