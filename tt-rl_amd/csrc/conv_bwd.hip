@@ -65,10 +65,16 @@ int conv_backward_split(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_
 }
 
 // Whether the paired launch is the faster way for this geometry.  Kept in
-// the context's plan table (cfg 1: pair, 0: separate), so it is exported and
-// imported with the GEMM plans and every later call, eager or captured, takes
-// the same path.  Without timing (under capture, or tuning off) a pair is
-// taken for at most 4096 output pixels, where the saved launch matters most.
+// the context's plan table as {cfg 1: pair, 0: separate; 0, 0, 0, 1, 0}, so
+// it is exported and imported with the GEMM plans and every later call,
+// eager or captured, takes the same path; an entry of any other form (an
+// imported table's) is decided again and replaced.  Without timing (under
+// capture, or tuning off) a pair is taken for at most 4096 output pixels,
+// where the saved launch matters most.
+inline GemmPlan pair_choice(bool pair) { return GemmPlan{pair ? 1 : 0, 0, 0, 0, 1, 0}; }
+inline bool is_pair_choice(const GemmPlan& p) {
+  return (p.cfg == 0 || p.cfg == 1) && p.bm == 0 && p.bn == 0 && p.tbk == 0 && p.splits == 1 && p.kchunk == 0;
+}
 template <int MODE>
 bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scale, const float* dy,
                     const float* wt, const float* xmask, long reserved, float* bank) {
@@ -76,7 +82,8 @@ bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scal
   snprintf(keybuf, sizeof(keybuf), "ttrl_conv2d_backward:pair|%d|%d|%d|%d|%d|%d|%d|%d|%d|%d|%ld|%d|%d", MODE, g.B,
            g.C, g.H, g.W, g.O, g.KH, g.KW, g.S, g.P, reserved, xmask ? 1 : 0, bank ? 1 : 0);
   const std::string key(keybuf);
-  if (const GemmPlan* hit = ctx_plan_find(ctx, key)) return hit->cfg == 1;
+  if (const GemmPlan* hit = ctx_plan_find(ctx, key))
+    if (is_pair_choice(*hit)) return hit->cfg == 1;
   bool pair = long(g.M) <= 4096;
   hipEvent_t e0, e1;
   if (!ctx_capturing(ctx) && gemm_tuning_enabled() && ctx_tune_events(ctx, &e0, &e1)) {
@@ -108,7 +115,7 @@ bool pair_is_faster(ttrl_ctx* ctx, const ConvGeo& g, const void* x, float x_scal
       (void)hipGetLastError();
     }
   }
-  ctx_plan_store(ctx, key, GemmPlan{pair ? 1 : 0, 0, 0, 0, 1, 0});
+  ctx_plan_store(ctx, key, pair_choice(pair));
   return pair;
 }
 

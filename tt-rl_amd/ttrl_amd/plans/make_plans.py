@@ -4,9 +4,11 @@ Runs every learner workload of this package once on GPU 0 with no table
 loaded, so each GEMM signature is timed at its first call, then writes the
 context's table.  Every later process loads the table at device open and runs
 the same plans, so its split-K summation orders, and with them its bits,
-match.  Usage (on a gfx950 machine):
+match.  With --extend the packaged table is loaded first: only the signatures
+it lacks (a newer build's) are timed, and every packaged entry is kept.
+Usage (on a gfx950 machine):
 
-    python -m ttrl_amd.plans.make_plans [--out PATH]
+    python -m ttrl_amd.plans.make_plans [--extend] [--out PATH]
 """
 
 from __future__ import annotations
@@ -15,8 +17,6 @@ import argparse
 import os
 import sys
 from pathlib import Path
-
-os.environ["TTRL_PLANS"] = "none"  # tune from scratch
 
 HERE = Path(__file__).resolve().parent
 
@@ -64,7 +64,10 @@ def tune_all(dev) -> None:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--out", default=str(HERE / "gfx950.tsv"))
+    ap.add_argument("--extend", action="store_true", help="keep the packaged table, time only what it lacks")
     args = ap.parse_args()
+    # read when the device opens: the packaged table, or none (tune from scratch)
+    os.environ["TTRL_PLANS"] = str(HERE / "gfx950.tsv") if args.extend else "none"
     from ttrl_amd.engine.device import open_device
 
     dev = open_device(0)
