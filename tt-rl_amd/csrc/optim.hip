@@ -1039,10 +1039,20 @@ int make_sources(int n, const ttrl_grad_source* srcs, const float* g, long gn, G
         d.ntiles = int(ceil_div(long(s.rows), kTileRows)) * d.ntc;
       }
     }
-    d.block0 = b;
     d.blocks = d.tiled ? d.ntiles : int(ceil_div(long(d.nw4) + d.nb4, kOptThreads));
-    b += d.blocks;
     out[c++] = d;
+  }
+  // Workgroups are dispatched in block order and a launch's whole grid is
+  // resident at once, so a workgroup's loads queue behind those of the
+  // blocks before it.  The few workgroups of the staged outer products (a
+  // staging round trip, then the product) and of the split-K sources (a
+  // batch of partials per float4) are the longest chains: they take the
+  // first blocks, the many short tile chains the last.
+  auto chain = [](const GradSrc& s) { return s.kind == TTRL_GRAD_SPLITS ? 1 : s.tiled ? 2 : 0; };
+  std::stable_sort(out, out + c, [&](const GradSrc& x, const GradSrc& y) { return chain(x) < chain(y); });
+  for (int k = 0; k < c; ++k) {
+    out[k].block0 = b;
+    b += out[k].blocks;
   }
   std::sort(spans.begin(), spans.end());
   for (size_t i = 1; i < spans.size(); ++i)
