@@ -26,6 +26,7 @@
 #include "dqn_row.hpp"
 #include "tile_gemm.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace ttrl {
@@ -38,6 +39,15 @@ constexpr int kTailMaxB = kSyncPartials / 2;  // two partial sums per sample in 
 constexpr int kTailChunk = 32;                // samples per pass of the weight-gradient sum
 constexpr int kTailItems = 8;                 // first-layer outputs per thread per pass
 constexpr int kTailSplits = 16;               // split partials of an output loaded in one batch, at most
+// The vector path (F % 4 == 0, aligned buffers, G F A <= kTailW2Lds): the
+// split partials and biases read as float4s, kTailItems4 of them per thread
+// per pass, and every set's second-layer weights staged in LDS by
+// cooperative float4 loads, so that a thread's first round trip carries
+// about 30 loads (a wavefront keeps at most 63 in flight; the scalar path's
+// W2 rows and split partials are over 120 and take several trips).
+constexpr int kTailItems4 = 2;
+constexpr int kTailW2Lds = 3 * 512 * 8;
+constexpr int kTailW2Loads = (kTailW2Lds / 4 + kTailThreads - 1) / kTailThreads;
 static_assert(kSyncPartials + kTailChunk * kTailMaxA <= 3 * kTailMaxF, "the last workgroup's staging fits hs");
 
 constexpr unsigned kFc1Cfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64) | cfg_bit(T64x64) |
@@ -46,6 +56,8 @@ constexpr unsigned kFc1Cfgs = cfg_bit(T32x32) | cfg_bit(T64x32) | cfg_bit(T32x64
 struct TailArgs {
   int B, F, A, G, splits;  // splits 0: h holds the first layer's outputs already
   FDiv fdiv;               // division by F
+  int fa4;                 // float4s of one set's W2 (vector path)
+  FDiv fa4div;             // division by fa4
   const float* part;       // [G][splits][B][F]
   float* h[3];
   const float* b1[3];
@@ -106,10 +118,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int AP>
 constexpr int tail_prefetch() { return AP <= 16 ? 2 : 1; }
 
-template <int AP, int SP>
+template <int AP, int SP, bool V4>
 __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
-  constexpr int NPRE = tail_prefetch<AP>();
-  __shared__ float hs[3 * kTailMaxF];  // the sample's first-layer outputs; the last workgroup's staging
+  constexpr int NPRE = V4 ? 0 : tail_prefetch<AP>();
+  __shared__ __attribute__((aligned(16))) float hs[3 * kTailMaxF];  // the sample's first-layer outputs; the last workgroup's staging
+  __shared__ __attribute__((aligned(16))) float w2s[V4 ? kTailW2Lds : 1];  // vector path: W2 of every set, as stored
   __shared__ float red[kTailThreads / 64][3 * AP];
   __shared__ float qrow[3 * AP];
   __shared__ float dqrow[AP];
@@ -117,11 +130,27 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
   warm_kernargs<int(sizeof(TailArgs))>();
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int F = t.F, A = t.A, G = t.G, S = t.splits, B = t.B;
+  // a lane's feature set is its own: pointers picked by compares, not by a
+  // per-lane index into the argument arrays (a vector load of the pointer)
+  auto pick = [](int g, auto p0, auto p1, auto p2) { return g == 0 ? p0 : (g == 1 ? p1 : p2); };
+
+  // 0v. (vector path) every set's W2 in flight with the first layer's
+  // loads: float4 e of the sets' blocks laid end to end (threads past the
+  // last re-read it and store nothing)
+  f32x4 wv[V4 ? kTailW2Loads : 1];
+  const int nw4 = V4 ? G * t.fa4 : 0;
+  if constexpr (V4) {
+#pragma unroll
+    for (int i = 0; i < kTailW2Loads; ++i) {
+      const int e = min(tid + i * kTailThreads, nw4 - 1), g = t.fa4div.div(e);
+      wv[i] = reinterpret_cast<const f32x4*>(pick(g, t.W2[0], t.W2[1], t.W2[2]))[e - g * t.fa4];
+    }
+  }
 
   // 0. the second layer's weights of this thread's first NPRE features in
   // every set and its bias entry (threads g * AP + a), in flight with the
   // first layer's loads
-  float w2p[NPRE][3][AP];
+  float w2p[NPRE > 0 ? NPRE : 1][3][AP];
 #pragma unroll
   for (int i = 0; i < NPRE; ++i) {
     const int n = min(tid + i * kTailThreads, F - 1);
@@ -146,10 +175,52 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
   // re-reading it and not added)
   const int items = G * F;
   const long stride = long(B) * F;  // one split's partial tile
-  // a lane's feature set is its own: pointers picked by compares, not by a
-  // per-lane index into the argument arrays (a vector load of the pointer)
-  auto pick = [](int g, auto p0, auto p1, auto p2) { return g == 0 ? p0 : (g == 1 ? p1 : p2); };
-  for (int k0 = 0; k0 < items; k0 += kTailItems * kTailThreads) {
+  if constexpr (V4) {
+    // four consecutive outputs of one set per item (F % 4 == 0), the same
+    // sums in the same order per output
+    const int items4 = items / 4;
+    for (int k0 = 0; k0 < items4; k0 += kTailItems4 * kTailThreads) {
+      f32x4 v[kTailItems4][SP], bias[kTailItems4];
+#pragma unroll
+      for (int u = 0; u < kTailItems4; ++u) {
+        const int k = 4 * min(k0 + u * kTailThreads + tid, items4 - 1);  // a clamped lane's loads are dropped
+        const int g = t.fdiv.div(k), n = k - g * F;
+        const f32x4* p = reinterpret_cast<const f32x4*>(t.part + (long(g) * S * B + b) * F + n);
+#pragma unroll
+        for (int j = 0; j < SP; ++j) v[u][j] = p[(min(j, S - 1) * stride) / 4];
+        const float* bg = pick(g, t.b1[0], t.b1[1], t.b1[2]);
+        bias[u] = bg ? *reinterpret_cast<const f32x4*>(bg + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < kTailItems4; ++u) {
+        const int k4 = k0 + u * kTailThreads + tid;
+        if (k4 >= items4) break;
+        const int k = 4 * k4, g = t.fdiv.div(k), n = k - g * F;
+        f32x4 sum = {0.f, 0.f, 0.f, 0.f};  // split order from zero, as k_splitk_reduce sums
+#pragma unroll
+        for (int j = 0; j < SP; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sum[c] += j < S ? v[u][j][c] : 0.f;
+        const f32x4* p = reinterpret_cast<const f32x4*>(t.part + (long(g) * S * B + b) * F + n);
+        for (int j = SP; j < S; ++j) {
+          const f32x4 w = p[(j * stride) / 4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sum[c] += w[c];
+        }
+        f32x4 h;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) h[c] = relu_f(sum[c] + bias[u][c]);
+        *reinterpret_cast<f32x4*>(pick(g, t.h[0], t.h[1], t.h[2]) + long(b) * F + n) = h;
+        *reinterpret_cast<f32x4*>(hs + k) = h;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kTailW2Loads; ++i) {
+      const int e = tid + i * kTailThreads;
+      if (e < nw4) reinterpret_cast<f32x4*>(w2s)[e] = wv[i];
+    }
+  }
+  for (int k0 = 0; k0 < (V4 ? 0 : items); k0 += kTailItems * kTailThreads) {
     if (S == 0) {
       for (int u = 0; u < kTailItems; ++u) {
         const int k = k0 + u * kTailThreads + tid;
@@ -219,7 +290,7 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
     for (int g = 0; g < 3; ++g)
       if (g < G) {
         const float hv = hs[g * F + n];
-        const float* w = t.W2[g] + long(n) * A;
+        const float* w = V4 ? w2s + (g * F + n) * A : t.W2[g] + long(n) * A;
 #pragma unroll
         for (int a = 0; a < AP; ++a) acc[g][a] = fmaf(hv, w[min(a, A - 1)], acc[g][a]);
       }
@@ -281,7 +352,7 @@ __global__ __launch_bounds__(kTailThreads) void k_dqn_tail(TailArgs t) {
     }
   }
   for (int n = tid + NPRE * kTailThreads; n < F; n += kTailThreads) {
-    const float* w = t.W2[0] + long(n) * A;
+    const float* w = V4 ? w2s + n * A : t.W2[0] + long(n) * A;
     float s = 0.f;
 #pragma unroll
     for (int a = 0; a < AP; ++a) s = fmaf(dqr[a], w[min(a, A - 1)], s);
@@ -482,14 +553,26 @@ int ttrl_dqn_tail(ttrl_ctx* ctx, const ttrl_dqn_tail_desc* d) {
   const int ap = A <= 8 ? 8 : (A <= 16 ? 16 : 32);
   // partials per output loaded in one batch: 8, 12 or kTailSplits (16)
   const int sp = t.splits <= 8 ? 8 : (t.splits <= 12 ? 12 : kTailSplits);
+  // the vector path: split partials, biases, outputs and W2 as aligned
+  // float4s, every set's W2 within the LDS stage
+  bool v4 = t.splits > 0 && F % 4 == 0 && (F * A) % 4 == 0 && G * F * A <= kTailW2Lds && aligned16(t.part);
+  for (int g = 0; g < G; ++g)
+    v4 = v4 && aligned16(d->h[g]) && aligned16(d->W2[g]) && (!d->b1[g] || aligned16(d->b1[g]));
+  t.fa4 = F * A / 4;
+  t.fa4div.set(std::max(t.fa4, 1));
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(unsigned(B)), dim3(kTailThreads), 0, stream_of(ctx), t);
     return check_launch("ttrl_dqn_tail");
   };
   auto by_sp = [&](auto k8, auto k12, auto k16) { return sp == 8 ? launch(k8) : (sp == 12 ? launch(k12) : launch(k16)); };
-  if (ap == 8) return by_sp(k_dqn_tail<8, 8>, k_dqn_tail<8, 12>, k_dqn_tail<8, kTailSplits>);
-  if (ap == 16) return by_sp(k_dqn_tail<16, 8>, k_dqn_tail<16, 12>, k_dqn_tail<16, kTailSplits>);
-  return by_sp(k_dqn_tail<32, 8>, k_dqn_tail<32, 12>, k_dqn_tail<32, kTailSplits>);
+  if (v4) {
+    if (ap == 8) return by_sp(k_dqn_tail<8, 8, true>, k_dqn_tail<8, 12, true>, k_dqn_tail<8, kTailSplits, true>);
+    if (ap == 16) return by_sp(k_dqn_tail<16, 8, true>, k_dqn_tail<16, 12, true>, k_dqn_tail<16, kTailSplits, true>);
+    return by_sp(k_dqn_tail<32, 8, true>, k_dqn_tail<32, 12, true>, k_dqn_tail<32, kTailSplits, true>);
+  }
+  if (ap == 8) return by_sp(k_dqn_tail<8, 8, false>, k_dqn_tail<8, 12, false>, k_dqn_tail<8, kTailSplits, false>);
+  if (ap == 16) return by_sp(k_dqn_tail<16, 8, false>, k_dqn_tail<16, 12, false>, k_dqn_tail<16, kTailSplits, false>);
+  return by_sp(k_dqn_tail<32, 8, false>, k_dqn_tail<32, 12, false>, k_dqn_tail<32, kTailSplits, false>);
 }
 
 }  // extern "C"
