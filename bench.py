@@ -41,8 +41,8 @@ PEAK_FP32_MFMA = 157.3e12
 # passes over the step's kernel, each scaled by what the same counter reads for a 256 MiB
 # device-to-device copy (profiles/dqn_adam_step_roofline_and_traffic.md), and the SHA-256 of the
 # optimizer kernels' source the passes measured: a build from other source reports traffic null.
-ADAM_STEP_TRAFFIC_BYTES = 47657329
-ADAM_STEP_TRAFFIC_SOURCE = "8b5de4f82a8e6a8c15bd446a278e06569f52f57e827ac3f81960c420386d34a8"
+ADAM_STEP_TRAFFIC_BYTES = 45348659
+ADAM_STEP_TRAFFIC_SOURCE = "e4f92d8030583bd49af478ed7481ecc0f111f223e09826a20ed8628f63f7b3a4"
 ADAM_STEP_SOURCES = ("tt-rl_amd/csrc/optim.hip", "tt-rl_amd/csrc/common.hpp", "tt-rl_amd/csrc/adam_dev.hpp")
 PEAK_HBM = 8.0e12
 

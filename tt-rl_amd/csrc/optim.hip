@@ -589,6 +589,22 @@ __device__ __forceinline__ f32x4 outer_bias_tile(const float* vs, int tc4) {
 // row band of a source with a bias, the bias: bias_wave for wave 0 (uniform
 // over the wave), bias_lane for its lanes that step bias float4 qb (the
 // tile's float4 column tc4 = tid; the other lanes' qb repeats the last).
+// The tile that block blk of a tiled source's blocks [block0, block0 + T)
+// forms.  Workgroups go to the chip's eight XCDs in turn (block b to XCD
+// b % 8), each XCD with an L2 of its own, and the tiles of one row band
+// share their slice of u: the blocks of one XCD take a contiguous run of
+// tiles (XCD x the run after the blocks of XCDs 0 .. x-1), so a band's slice
+// is fetched into one L2, not eight.  A bijection onto [0, T).
+__device__ __forceinline__ int xcd_tile(int blk, int block0, int T) {
+  const int x = blk & 7;
+  int start = 0;
+#pragma unroll
+  for (int y = 0; y < 7; ++y)  // blocks of the range on XCD y: (T - offset of its first + 7) / 8
+    if (y < x) start += (T - ((y - block0) & 7) + 7) >> 3;
+  const int first = block0 + ((x - block0) & 7);
+  return start + ((blk - first) >> 3);
+}
+
 struct TileSpot {
   int r0, c0, tr, tc4;
   int q[kTileOuts];
@@ -715,7 +731,7 @@ __global__ __launch_bounds__(kOptThreads) __attribute__((amdgpu_waves_per_eu(4))
     if (s.tiled) {
       // a tile (kTileOuts float4s per thread, both slices staged), in the
       // first row band with the bias's float4s of its columns
-      const TileSpot t = tile_spot(s, blk - s.block0);
+      const TileSpot t = tile_spot(s, xcd_tile(blk, s.block0, s.blocks));
       // the operand slices' loads first, then the parameters' and moments',
       // all in flight while the scalars are formed (unconditional, so that
       // thread 0's wait for the count waits for none of them; a row past the
@@ -854,7 +870,7 @@ __global__ __launch_bounds__(kOptThreads) void k_sources_write(SrcSet a) {
   const GradSrc& s = a.src[k];
   __shared__ float us[kOuterULds], vs[kOuterLds];
   if (s.tiled) {
-    const TileSpot t = tile_spot(s, blk - s.block0);
+    const TileSpot t = tile_spot(s, xcd_tile(blk, s.block0, s.blocks));
     commit_outer_tile(issue_outer_tile(s, t.r0, t.c0), us, vs);
     f32x4 gv[kTileOuts];
     outer_grad_tile(us, vs, t.tr, t.tc4, gv);
