@@ -451,7 +451,9 @@ def bench_rppo(dev, updates=3, mode="graph"):
 
 
 def dominant_kernel(dev, learner, reps=200):
-    """The DQN update's longest launch, its Adam step, as the update calls it
+    """The DQN update's HBM-bound launch (its other launches are MFMA GEMMs or
+    latency-bound row kernels, reported per kernel with their MFMA fractions
+    beside the update's own FLOP rate), its Adam step, as the update calls it
     (ttrl_adam_step_sources: k_adam_src over the 1,687,296-float parameter
     arena, forming the gradients the update left pending as it reads them and
     updating p, m and v with them without storing the gradients, then
