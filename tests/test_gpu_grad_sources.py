@@ -200,6 +200,33 @@ def test_tail_with_deferred_head_gradients_and_means(device):
     assert lib.ttrl_dqn_tail(device.ctx, C.byref(d)) == _lib.TTRL_EINVAL
 
 
+def test_tail_vector_and_scalar_paths_agree_bitwise(device, monkeypatch):
+    """ttrl_dqn_tail reads the split partials, biases and W2 as float4s when
+    its first layer's GEMM split K, every buffer is 16-byte aligned and
+    F % 4 == 0, and element by element otherwise; both form the same sums in
+    the same order.  The DQN update's shape (K = 3136, the GEMM held at 7
+    splits), then the same inputs with the first-layer outputs one float off
+    alignment, which take the element path: every output carries the same
+    bits."""
+    B, K, F, A, G = 32, 3136, 512, 6, 3
+    monkeypatch.setenv("TTRL_GEMM_FORCE", "7:7")  # 32 x 32 tiles, two k-groups, 7 splits
+    desc, outputs = _tail_setup(device, np.random.default_rng(12), B=B, K=K, F=F, A=A, G=G)
+    vec = outputs()
+    device.call("ttrl_dqn_tail", C.byref(desc(vec)))
+    sca = outputs()
+    hbuf = [_empty(device, (B * F + 4,)) for _ in range(G)]
+    d = desc(sca)
+    for g in range(G):
+        d.h[g] = hbuf[g].ptr + 4  # 4 bytes past a 16-byte boundary
+    device.call("ttrl_dqn_tail", C.byref(d))
+    for k in ("loss", "mean_q", "td_abs", "dq", "dh", "dW2", "db2"):
+        assert np.array_equal(sca[k].numpy(), vec[k].numpy()), k
+    for g in range(G):
+        assert np.array_equal(hbuf[g].numpy()[1:1 + B * F].reshape(B, F), vec["h"][g].numpy()), g
+        assert np.array_equal(sca["q"][g].numpy(), vec["q"][g].numpy()), g
+    assert float(vec["loss"].numpy()[0]) > 0.0 and np.count_nonzero(vec["dh"].numpy()) > 0
+
+
 # An arena of N floats: a split-partials source (weight 40 x 32 + bias 32)
 # and an outer-product source (weight 64 x 6 + bias 6, padded to 8) inside it.
 N = 16_384
